@@ -1,0 +1,14 @@
+"""axk — MI355X (gfx950) kernels for the per-layer Qwen3.5 decode/prefill hot path of ax-dsl-kernels.
+
+Python host layer over libaxk.so (include/axk.h). Operator names and contracts mirror the reference's
+sgl_kernel_axera operator API; tensors are torch device tensors used only as memory and streams.
+"""
+from . import _lib
+from .gemm import bf16_gemm, fp8_gemm, mxfp4_dequant, mxfp4_gemm
+
+__all__ = ["bf16_gemm", "fp8_gemm", "mxfp4_dequant", "mxfp4_gemm", "load_library"]
+
+
+def load_library():
+    """Load libaxk.so (raises ImportError if it has not been built)."""
+    return _lib.load()

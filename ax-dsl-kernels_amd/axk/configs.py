@@ -1,0 +1,29 @@
+"""Seeded synthetic inputs for the BASELINE configs (CPU torch.Generator, fixed draw order).
+
+Each generator returns host tensors; callers move them to the device. Draw order is part of the
+contract (tests, smoke and bench all regenerate the same inputs from the seed).
+"""
+from __future__ import annotations
+
+import torch
+
+
+def pack_codes(codes: torch.Tensor) -> torch.Tensor:
+    """Logical E2M1 codes [..., K] -> packed u8 [..., K/2], even column in the low nibble."""
+    codes = codes.to(torch.uint8)
+    return (codes[..., 0::2] & 15) | ((codes[..., 1::2] & 15) << 4)
+
+
+def mxfp4_weight(n: int, k: int, g: torch.Generator, lo: int = 119, hi: int = 123, lead=()):
+    """Uniform random nibbles and E8M0 exponent bytes uniform in [lo, hi]: (codes [.., n, k/2], scales [.., n, k/32])."""
+    codes = torch.randint(0, 16, (*lead, n, k), generator=g, dtype=torch.uint8)
+    scales = torch.randint(lo, hi + 1, (*lead, n, k // 32), generator=g, dtype=torch.uint8)
+    return pack_codes(codes).contiguous(), scales.contiguous()
+
+
+def config0(seed: int = 0):
+    """Config 0: single MXFP4 linear, W N=4096 x K=4096, x bf16 [1, 4096] ~ N(0,1)."""
+    g = torch.Generator().manual_seed(seed)
+    codes, scales = mxfp4_weight(4096, 4096, g)
+    x = torch.randn(1, 4096, generator=g).to(torch.bfloat16)
+    return {"x": x, "w": codes, "s": scales}

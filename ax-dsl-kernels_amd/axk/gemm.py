@@ -1,0 +1,156 @@
+"""Runtime-weight linear operators (MXFP4 / FP8 E4M3 / bf16 weights) on gfx950.
+
+Mirrors the operator API of sgl_kernel_axera.gemm
+(models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/gemm.py): the same names, argument meaning and
+``ValueError`` contract checks (_prepare_bias_output 26-46, _normalize_scale 17-23). Every call goes
+through libaxk.so; there is no host fallback.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_OUT_DT = {torch.bfloat16: _lib.DT_BF16, torch.float32: _lib.DT_F32}
+
+
+def _as_u8(t: torch.Tensor, name: str) -> torch.Tensor:
+    """FP4 codes / E8M0 / E4M3 payloads travel as u8; accept torch's packed views of the same bytes."""
+    if t.dtype in (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn):
+        return t.view(torch.uint8)
+    raise ValueError(f"{name} must be uint8 (or a float4/float8 view of bytes), got {t.dtype}")
+
+
+def _prepare_bias_output(n, m, device, out_dtype, bias, output):
+    """As gemm.py:26-46: bias defaults to zeros and is rounded to out_dtype; output is [m, n]."""
+    if out_dtype not in _OUT_DT:
+        raise ValueError(f"out_dtype must be bfloat16 or float32, got {out_dtype}")
+    if bias is not None:
+        if tuple(bias.shape) != (n,):
+            raise ValueError(f"bias shape {tuple(bias.shape)} is incompatible with N={n}")
+        bias = bias.to(device=device, dtype=out_dtype).float().contiguous()
+    if output is None:
+        output = torch.empty((m, n), device=device, dtype=out_dtype)
+    elif tuple(output.shape) != (m, n):
+        raise ValueError(f"output shape {tuple(output.shape)} is incompatible with {(m, n)}")
+    elif output.dtype != out_dtype or not output.is_contiguous():
+        raise ValueError("output must be a contiguous tensor of out_dtype")
+    return bias, output
+
+
+def _normalize_scale(scale: torch.Tensor, size: int, name: str, device) -> torch.Tensor:
+    """As gemm.py:17-23: a scalar broadcasts, otherwise one fp32 scale per row / channel."""
+    scale = scale.reshape(-1)
+    if scale.numel() == 1:
+        return scale.to(device=device, dtype=torch.float32).expand(size).contiguous()
+    if scale.numel() != size:
+        raise ValueError(f"{name} shape {tuple(scale.shape)} is incompatible with size={size}")
+    return scale.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _check_a(a: torch.Tensor) -> tuple[int, int]:
+    if a.dim() != 2:
+        raise ValueError("a must be a 2D tensor")
+    if a.dtype != torch.bfloat16:
+        raise ValueError(f"a must be bfloat16, got {a.dtype}")
+    if a.stride(1) != 1:
+        raise ValueError("a must have unit stride along K")
+    return a.shape
+
+
+def mxfp4_dequant(b_fp4: torch.Tensor, b_scale: torch.Tensor) -> torch.Tensor:
+    """Exact fp32 dequantisation of packed E2M1 codes [N, K/2] and E8M0 scales [N, K/32]."""
+    codes, scales = _as_u8(b_fp4, "b_fp4").contiguous(), _as_u8(b_scale, "b_scale").contiguous()
+    _lib.require_device(codes, scales)
+    n, k = codes.shape[0], codes.shape[1] * 2
+    if tuple(scales.shape) != (n, k // 32):
+        raise ValueError(f"b_scale shape {tuple(scales.shape)} is incompatible with codes {tuple(codes.shape)}")
+    out = torch.empty((n, k), device=codes.device, dtype=torch.float32)
+    _lib.call("axk_mxfp4_dequant", codes.data_ptr(), scales.data_ptr(), out.data_ptr(), n, k, _lib.stream_of(out))
+    return out
+
+
+def mxfp4_gemm(
+    a: torch.Tensor,
+    b_fp4: torch.Tensor,
+    b_scale: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """MXFP4 GEMM: output = a @ dequant(b_fp4, b_scale).T + bias (gemm.py:626-641).
+
+    a       : (m, k) bf16 activation
+    b_fp4   : (n, k/2) packed E2M1 codes, low nibble = even column (u8 or float4_e2m1fn_x2 view)
+    b_scale : (n, k/32) E8M0 per-32 block scale (u8 or float8_e8m0fnu view)
+    """
+    m, k = _check_a(a)
+    codes, scales = _as_u8(b_fp4, "b_fp4"), _as_u8(b_scale, "b_scale")
+    n = codes.shape[0]
+    if codes.dim() != 2 or codes.shape[1] * 2 != k:
+        raise ValueError(f"b_fp4 shape {tuple(b_fp4.shape)} is incompatible with a having k={k}")
+    if tuple(scales.shape) != (n, k // 32):
+        raise ValueError(f"b_scale shape {tuple(b_scale.shape)} is incompatible with (n, k/32)={(n, k // 32)}")
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    codes, scales = codes.contiguous(), scales.contiguous()
+    _lib.require_device(a, codes, scales, output)
+    _lib.call(
+        "axk_mxfp4_gemm", a.data_ptr(), a.stride(0), codes.data_ptr(), scales.data_ptr(), _lib.ptr(bias),
+        output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output
+
+
+def fp8_gemm(
+    a: torch.Tensor,
+    b_fp8_t: torch.Tensor,
+    scale_a: Optional[torch.Tensor],
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """FP8 E4M3 weight linear with per-output-channel scales (gemm.py:119-181, 457-466).
+
+    output = (a * scale_a[:, None]) @ (b_fp8_t * scale_b[:, None]).T + bias, fp32 accumulation.
+    The activation is bf16 here (the hybrid decode group feeds bf16 hidden states).
+    """
+    m, k = _check_a(a)
+    w = _as_u8(b_fp8_t, "b_fp8_t")
+    if w.dim() != 2 or w.shape[1] != k:
+        raise ValueError(f"b_t must have shape [N, K], got {tuple(b_fp8_t.shape)} for K={k}")
+    n = w.shape[0]
+    sa = None if scale_a is None else _normalize_scale(scale_a, m, "scale_a", a.device)
+    sb = _normalize_scale(scale_b, n, "scale_b", a.device)
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    w = w.contiguous()
+    _lib.require_device(a, w, output)
+    _lib.call(
+        "axk_fp8_gemm", a.data_ptr(), a.stride(0), w.data_ptr(), _lib.ptr(sa), sb.data_ptr(), _lib.ptr(bias),
+        output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output
+
+
+def bf16_gemm(
+    a: torch.Tensor,
+    b_t: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Dense bf16 projection a[M,K] @ b_t[N,K].T + bias with fp32 accumulation (gemm.py:81-116, 469-476)."""
+    m, k = _check_a(a)
+    if b_t.dim() != 2 or b_t.shape[1] != k or b_t.dtype != torch.bfloat16:
+        raise ValueError(f"b_t must be bfloat16 [N, K], got {tuple(b_t.shape)} {b_t.dtype} for K={k}")
+    n = b_t.shape[0]
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    b_t = b_t.contiguous()
+    _lib.require_device(a, b_t, output)
+    _lib.call(
+        "axk_bf16_gemm", a.data_ptr(), a.stride(0), b_t.data_ptr(), _lib.ptr(bias), output.data_ptr(),
+        _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output

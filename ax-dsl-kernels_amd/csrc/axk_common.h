@@ -1,0 +1,120 @@
+// Device helpers shared by every axk kernel (gfx950 / CDNA4, wave64).
+//
+// Number formats on the boundary (all passed as raw bytes / bits):
+//   bf16  : uint16_t bit pattern, rounded from fp32 with round-to-nearest-even (torch's rule)
+//   E2M1  : 4-bit code s|e1 e0|m0, two per byte, LOW nibble = EVEN column
+//           (models/qwen35_35b_a3b/src/70b0fbc/q35_moe.py:46-63)
+//   E8M0  : one byte per 32 consecutive K values, value 2^(s-127) exactly as torch.exp2(s - 127):
+//           s = 0 -> 2^-127 (fp32 denormal), s = 255 -> +inf (q35_moe.py:60-63)
+//   E4M3  : OCP fp8 e4m3fn (no inf, 0x7f/0xff = NaN)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define AXK_DEV __device__ __forceinline__
+
+typedef __bf16 axk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 axk_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float axk_f32x4 __attribute__((ext_vector_type(4)));
+typedef float axk_f32x2 __attribute__((ext_vector_type(2)));
+
+AXK_DEV float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+AXK_DEV uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+AXK_DEV float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// E8M0 byte -> fp32 2^(s-127); bit-identical to torch.exp2(float(s) - 127).
+AXK_DEV float e8m0_to_f32(uint32_t s) {
+  return s == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+// E2M1 code (low 4 bits of c) -> exact fp32 value, code 8 -> -0.0.
+AXK_DEV float e2m1_to_f32(uint32_t c) {
+  const uint32_t m = c & 7u;
+  const uint32_t mag = m < 2u ? (m ? 0x3f000000u : 0u) : ((((m >> 1) + 126u) << 23) | ((m & 1u) << 22));
+  return __uint_as_float(mag | ((c & 8u) << 28));
+}
+
+// Eight consecutive bf16 values (16 bytes) as an MFMA operand.
+AXK_DEV axk_bf16x8 load_bf16x8(const uint16_t* p) {
+  return *reinterpret_cast<const axk_bf16x8*>(p);
+}
+
+AXK_DEV axk_bf16x8 zero_bf16x8() {
+  axk_bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (__bf16)0.0f;
+  return z;
+}
+
+// Eight E2M1 codes (one 32-bit word, low nibble first) -> eight bf16 scaled by `scale`
+// (a power of two), using gfx950's scaled FP4 conversion.
+AXK_DEV axk_bf16x8 fp4x8_to_bf16x8(uint32_t w, float scale) {
+  axk_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  axk_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  axk_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  axk_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  axk_bf16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
+// E4M3 (OCP) byte -> exact fp32, written from the format definition (bias 7, no inf).
+AXK_DEV float e4m3_to_f32(uint32_t b) {
+  const uint32_t s = (b & 0x80u) << 24;
+  const uint32_t e = (b >> 3) & 0xfu;
+  const uint32_t m = b & 7u;
+  if (e == 0xfu && m == 7u) return __uint_as_float(s | 0x7fc00000u);
+  if (e == 0u) {  // subnormal: m * 2^-9 (m == 0 keeps the sign of zero)
+    const float v = (float)m * 0.001953125f;
+    return s ? -v : v;
+  }
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// Four E4M3 bytes -> four bf16 (exact: E4M3 values fit bf16's 8-bit exponent and 7-bit mantissa).
+AXK_DEV void fp8x4_to_bf16(uint32_t w, __bf16* dst) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[i] = (__bf16)e4m3_to_f32((w >> (8 * i)) & 0xffu);
+}
+
+AXK_DEV axk_f32x4 mfma_bf16_16x16x32(axk_bf16x8 a, axk_bf16x8 b, axk_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Wave-wide reductions (wave64) through cross-lane shuffles.
+AXK_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+AXK_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+// Reduction inside aligned groups of `width` lanes (width a power of two <= 64).
+template <int W>
+AXK_DEV float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int W>
+AXK_DEV float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+AXK_DEV float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+AXK_DEV float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
+AXK_DEV float softplus_f32(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }

@@ -1,0 +1,176 @@
+"""Benchmark of the axk hot path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Prints ONE JSON line (rank 0) with the BASELINE metric for the chosen workload, the roofline of its
+dominant kernel and a CPU baseline (the oracle timed on the host cores over a bounded sample).
+Inputs are synthetic (seeded), resident in HBM before the timed region; weight / KV buffers rotate over
+>= 1 GiB of distinct copies so the 256 MB MALL cannot serve them.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ax-dsl-kernels_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 1 << 30
+METRIC = "µs/decode-layer + achieved HBM GB/s (% of 8 TB/s) for MXFP4 MoE + paged attn"
+
+
+def _cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 50) -> tuple[float, int]:
+    """Median seconds per call of fn over a bounded number of repetitions (~budget_s of CPU work)."""
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < max_reps and (len(times) < min_reps or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+class MxLinearWorkload:
+    """Config 0: one MXFP4 linear, W 4096 x 4096 (E2M1 + E8M0), x bf16 [1, 4096], bf16 out."""
+
+    name = "mxfp4_linear"
+    kernel = "mx_linear_kernel"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        c = configs.config0()
+        self.host = c
+        self.m, self.n, self.k = 1, 4096, 4096
+        # algorithmic bytes per launch: codes + scales + x + out
+        self.alg_bytes = self.n * self.k // 2 + self.n * self.k // 32 + 2 * self.m * self.k + 2 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        per_copy = self.n * self.k // 2 + self.n * self.k // 32
+        self.copies = max(2, -(-ROTATE_BYTES // per_copy))
+        w, s = c["w"].to(dev), c["s"].to(dev)
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.s = [s.clone() for _ in range(self.copies)]
+        self.x = c["x"].to(dev)
+        self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
+        self.config = {"workload": "config0: MXFP4 linear N=4096 K=4096 M=1", "rotating_copies": self.copies}
+        self.dtype = "mxfp4 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        j = i % self.copies
+        axk.mxfp4_gemm(self.x, self.w[j], self.s[j], output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import _c
+
+        x = self.host["x"].view(__import__("torch").int16).numpy().view("u2")
+        w, s = self.host["w"].numpy(), self.host["s"].numpy()
+        nt = _cpu_threads()
+        sec, reps = _time_cpu(lambda: _c.mxfp4_linear(x, w, s, nthreads=nt))
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config0 op (oracle/mx_codec.c, OpenMP), median of {reps} runs"}
+
+
+WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload}
+DEFAULT_WORKLOAD = MxLinearWorkload.name
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import axk
+
+    axk.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload](dev)
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+
+    # Capture exactly K steps in one HIP graph (removes host launch overhead from the measurement).
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(args.steps):
+                wl.step(i)
+    graph.replay()  # untimed replay: graph upload / first-run costs
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    ms_per_step = ms / args.steps
+    us = ms_per_step * 1e3
+
+    achieved = wl.alg_bytes / (ms_per_step * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(us, 3),
+        "unit": "µs/op",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.dtype,
+        "data": "synthetic (seeded generators in axk/configs.py)",
+        "config": wl.config,
+        "achieved_gbs": round(achieved, 1),
+        "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": wl.kernel,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "alg_bytes_per_launch": wl.alg_bytes,
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = wl.cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

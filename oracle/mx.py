@@ -1,0 +1,119 @@
+"""Oracle: MXFP4 / E8M0 / E4M3 codecs and the runtime-weight linear (CPU, test infrastructure only).
+
+Restates
+  * dequant_mxfp4            models/qwen35_35b_a3b/src/70b0fbc/q35_moe.py:60-63
+                             models/qwen38_27b/head/mx4_common.py:37-49
+  * quant_mxfp4 (ggml rule)  models/qwen38_27b/head/mx4_common.py:11-34 (== q35_moe.py:46-57 plus the
+                             0..254 clamp of the scale byte)
+  * pack_fp4_codes           models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:160-166
+  * MX linear golden         q35_moe.py:222-239 (torch fp32 matmul on exactly dequantised weights),
+                             sgl_kernel_axera/gemm.py:564-641 (a @ dequant(w).T + bias, fp32 acc)
+  * FP8 per-channel linear   sgl_kernel_axera/gemm.py:119-181
+Pinned by tests/test_oracle_mx.py: exhaustive 16 x 256 code/scale table against the closed form and
+torch's float8_e8m0fnu / exp2, E4M3 table against torch.float8_e4m3fn, the C restatement
+(oracle/mx_codec.c) against this module, quantiser brute force + round trip, and the linear
+against float64 dot products.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+GROUP = 32
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float32)
+FP4_LUT = np.concatenate([E2M1, -E2M1]).astype(np.float32)  # code -> value; code 8 -> -0.0
+
+
+def e8m0_to_f32(scales: np.ndarray) -> np.ndarray:
+    """2^(s - 127) in fp32, as torch.exp2(s.float() - 127) of q35_moe.py:63 (0 -> 2^-127, 255 -> inf)."""
+    s = np.asarray(scales).astype(np.int32)
+    with np.errstate(over="ignore"):
+        return np.ldexp(np.float32(1.0), s - 127).astype(np.float32)
+
+
+def pack_fp4_codes(codes: np.ndarray) -> np.ndarray:
+    """Logical codes [..., K] (0..15) -> packed [..., K/2] u8, even column in the low nibble."""
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    return (c[..., 0::2] & 15) | ((c[..., 1::2] & 15) << 4)
+
+
+def unpack_fp4_codes(packed: np.ndarray) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    return np.stack([p & 15, p >> 4], axis=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+
+
+def dequant_mxfp4(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """[N, K/2] u8 codes + [N, K/32] u8 E8M0 -> [N, K] fp32 (q35_moe.py:60-63)."""
+    code = unpack_fp4_codes(packed)
+    n, k = code.shape
+    mag = E2M1[code & 7]
+    v = mag * np.where(code >= 8, np.float32(-1.0), np.float32(1.0))
+    f = e8m0_to_f32(scales)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (v.reshape(n, k // GROUP, GROUP) * f[..., None]).reshape(n, k).astype(np.float32)
+
+
+def quant_mxfp4(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """ggml-axera's MXFP4 quantiser (mx4_common.py:11-34): e = floor(log2 amax) - 2 (0 if amax == 0),
+    scale byte clamp(e + 127, 0, 254), nearest E2M1 magnitude with ties to the lower code."""
+    w = np.asarray(w, dtype=np.float32)
+    n, k = w.shape
+    g = w.reshape(n, k // GROUP, GROUP)
+    amax = np.abs(g).max(-1)
+    with np.errstate(divide="ignore"):
+        e = np.where(amax > 0, np.floor(np.log2(np.maximum(amax, np.float32(1e-30)))) - 2, 0).astype(np.float32)
+    x = g / np.exp2(e)[..., None]
+    dist = np.abs(np.abs(x)[..., None] - E2M1)  # argmin returns the first minimum: ties go low
+    best = dist.argmin(-1).astype(np.uint8)
+    code = best | ((x < 0).astype(np.uint8) << 3)
+    packed = pack_fp4_codes(code.reshape(n, k))
+    scale = np.clip(e + 127, 0, 254).astype(np.uint8)
+    return packed, scale
+
+
+def e4m3_table() -> np.ndarray:
+    """All 256 OCP E4M3 (fn) values from the format definition: bias 7, subnormal m * 2^-9, 0x7f/0xff NaN."""
+    out = np.empty(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e, m = (b >> 3) & 15, b & 7
+        if e == 15 and m == 7:
+            out[b] = np.nan
+        elif e == 0:
+            out[b] = s * m * 2.0 ** -9
+        else:
+            out[b] = s * (1 + m / 8.0) * 2.0 ** (e - 7)
+    return out
+
+
+def bf16_round(x: np.ndarray | torch.Tensor) -> np.ndarray:
+    """fp32 -> bf16 (round to nearest even) -> fp32."""
+    t = torch.as_tensor(np.asarray(x, dtype=np.float32))
+    return t.to(torch.bfloat16).float().numpy()
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def mx_linear(a: torch.Tensor, packed: np.ndarray, scales: np.ndarray, bias=None) -> torch.Tensor:
+    """a[M,K] (bf16 / fp32 values) @ dequant(packed, scales).T (+ bias) in fp32: the reference golden
+    (q35_moe.py:234-238, gemm.py:564-598). Returns fp32; the caller rounds to its output dtype."""
+    w = torch.from_numpy(dequant_mxfp4(packed, scales))
+    out = a.float().cpu() @ w.T
+    if bias is not None:
+        out = out + bias.float().cpu()
+    return out
+
+
+def fp8_linear(a: torch.Tensor, w_fp8: np.ndarray, scale_a, scale_b, bias=None) -> torch.Tensor:
+    """(a * scale_a) @ (E4M3(w) * scale_b).T + bias in fp32 (gemm.py:123-153)."""
+    w = torch.from_numpy(e4m3_table()[np.asarray(w_fp8, dtype=np.uint8)])
+    w = w * torch.as_tensor(scale_b, dtype=torch.float32).reshape(-1, 1)
+    x = a.float().cpu()
+    if scale_a is not None:
+        x = x * torch.as_tensor(scale_a, dtype=torch.float32).reshape(-1, 1)
+    out = x @ w.T
+    if bias is not None:
+        out = out + bias.float().cpu()
+    return out

@@ -1,0 +1,69 @@
+"""The C-ABI library loads, exports every symbol include/axk.h declares, and rejects contract
+violations before touching the GPU (CPU only: no compute call is made)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import axk
+from axk import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_header_symbols_exported_and_bound():
+    lib = _lib.load()
+    declared = _lib.header_symbols()
+    assert declared, "no declarations parsed from include/axk.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/axk.h but not exported by libaxk.so"
+    # every declared function has a ctypes signature and vice versa
+    assert sorted(_lib.SIGNATURES) == declared
+
+
+def test_header_status_and_dtype_codes_match_python():
+    text = open(_lib.HEADER_PATH).read()
+    codes = {m[0]: int(m[1]) for m in re.findall(r"#define (AXK_E_[A-Z]+) (\d+)", text)}
+    assert {v: k for k, v in codes.items()} == _lib.STATUS_NAMES
+    dts = {m[0]: int(m[1]) for m in re.findall(r"#define AXK_DT_([A-Z0-9]+) (\d+)", text)}
+    # AX dtype codes of tools/manifest/onnx_io.py:18-29
+    assert dts == {"U8": 1, "F32": 3, "I32": 6, "BF16": 9, "F16": 10, "FP8E4M3": 11, "FP8E5M2": 12, "FP4": 15}
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert b"gfx950" in lib.axk_version()
+    for code in list(_lib.STATUS_NAMES) + [0]:
+        assert lib.axk_status_string(code)
+
+
+def test_contract_violations_return_before_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every check below fails first
+    # NULL codes
+    assert lib.axk_mxfp4_dequant(None, fake, fake, 4, 64, None) == 1
+    # k not a multiple of 32
+    assert lib.axk_mxfp4_dequant(fake, fake, fake, 4, 48, None) == 2
+    # misaligned activation
+    assert lib.axk_mxfp4_gemm(ctypes.c_void_p(0x1002), 64, fake, fake, None, fake, 9, 1, 16, 64, None) == 3
+    # bad output dtype
+    assert lib.axk_mxfp4_gemm(fake, 64, fake, fake, None, fake, 15, 1, 16, 64, None) == 4
+    # output overlapping the activation
+    assert lib.axk_mxfp4_gemm(fake, 64, ctypes.c_void_p(0x9000), fake, None, fake, 9, 1, 16, 64, None) == 5
+    # fp8 without its channel scales
+    assert lib.axk_fp8_gemm(fake, 64, fake, None, None, None, fake, 9, 1, 16, 64, None) == 1
+
+
+def test_python_layer_raises_value_error_on_contract():
+    import torch
+
+    a = torch.zeros(2, 64, dtype=torch.bfloat16)
+    w = torch.zeros(16, 16, dtype=torch.uint8)
+    s = torch.zeros(16, 2, dtype=torch.uint8)
+    with pytest.raises(ValueError):
+        axk.mxfp4_gemm(a, w, s)  # k/2 mismatch
+    with pytest.raises(ValueError):
+        axk.mxfp4_gemm(a.float(), torch.zeros(16, 32, dtype=torch.uint8), s)  # fp32 activation
+    with pytest.raises(ValueError):
+        axk.mxfp4_gemm(a, torch.zeros(16, 32, dtype=torch.uint8), torch.zeros(16, 3, dtype=torch.uint8))

@@ -1,0 +1,108 @@
+"""GPU parity of the MXFP4 codec and the MXFP4 / FP8 / bf16 runtime-weight linear against the oracle.
+
+Bar: dequantised values bit-exact; bf16 outputs within rel 2e-2 / abs 1e-2 of the fp32-accumulating
+golden (fp32 outputs: rel 1e-3 / abs 1e-3, the only difference being summation order).
+"""
+import numpy as np
+import pytest
+import torch
+
+import axk
+from axk import configs
+from oracle import mx
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = dict(rtol=2e-2, atol=1e-2)
+F32_TOL = dict(rtol=1e-3, atol=1e-3)
+
+
+def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return bool(np.all((np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+def test_dequant_exhaustive_table_bit_exact(dev):
+    codes = np.tile(np.arange(16, dtype=np.uint8), (256, 2))
+    packed = mx.pack_fp4_codes(codes)
+    scales = np.arange(256, dtype=np.uint8)[:, None]
+    got = axk.mxfp4_dequant(torch.from_numpy(packed).to(dev), torch.from_numpy(scales).to(dev)).cpu().numpy()
+    assert _bits_equal(got, mx.dequant_mxfp4(packed, scales))
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (37, 96), (4096, 4096)])
+def test_dequant_random_bit_exact(dev, n, k):
+    g = torch.Generator().manual_seed(n + k)
+    packed = torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.uint8)
+    scales = torch.randint(0, 256, (n, k // 32), generator=g, dtype=torch.uint8)
+    got = axk.mxfp4_dequant(packed.to(dev), scales.to(dev)).cpu().numpy()
+    assert _bits_equal(got, mx.dequant_mxfp4(packed.numpy(), scales.numpy()))
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 4096, 4096), (1, 16, 32), (1, 100, 96), (3, 2048, 512), (8, 1024, 2048), (16, 256, 4096),
+     (17, 300, 1024), (32, 512, 2048), (40, 64, 256)],
+)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_mxfp4_gemm_matches_oracle(dev, m, n, k, out_dtype):
+    g = torch.Generator().manual_seed(1000 * m + n + k)
+    packed, scales = configs.mxfp4_weight(n, k, g)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g) / 8
+    ref = mx.mx_linear(a, packed.numpy(), scales.numpy(), bias.to(out_dtype))
+    got = axk.mxfp4_gemm(a.to(dev), packed.to(dev), scales.to(dev), out_dtype=out_dtype, bias=bias.to(dev))
+    assert got.dtype == out_dtype and got.shape == (m, n)
+    tol = BF16_TOL if out_dtype == torch.bfloat16 else F32_TOL
+    torch.testing.assert_close(got.float().cpu(), ref.to(out_dtype).float(), **tol)
+
+
+def test_mxfp4_gemm_config0(dev):
+    c = configs.config0()
+    ref = mx.mx_linear(c["x"], c["w"].numpy(), c["s"].numpy()).to(torch.bfloat16)
+    got = axk.mxfp4_gemm(c["x"].to(dev), c["w"].to(dev), c["s"].to(dev))
+    torch.testing.assert_close(got.float().cpu(), ref.float(), **BF16_TOL)
+    # runtime weights: flipping every sign bit in place negates the output with the same launch
+    w = c["w"].to(dev)
+    w.bitwise_xor_(0x88)
+    neg = axk.mxfp4_gemm(c["x"].to(dev), w, c["s"].to(dev))
+    torch.testing.assert_close(neg.float().cpu(), -ref.float(), **BF16_TOL)
+
+
+def test_mxfp4_gemm_strided_activation_and_output_buffer(dev):
+    g = torch.Generator().manual_seed(7)
+    packed, scales = configs.mxfp4_weight(64, 128, g)
+    big = torch.randn(4, 256, generator=g).to(torch.bfloat16)
+    a = big[:, :128]  # row stride 256
+    out = torch.empty(4, 64, dtype=torch.float32, device=dev)
+    a_dev = big.to(dev)[:, :128]
+    assert a_dev.stride(0) == 256
+    res = axk.mxfp4_gemm(a_dev, packed.to(dev), scales.to(dev), out_dtype=torch.float32, output=out)
+    assert res is out
+    ref = mx.mx_linear(a, packed.numpy(), scales.numpy())
+    torch.testing.assert_close(out.cpu(), ref, **F32_TOL)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 4096), (8, 4096, 4096), (5, 96, 64), (32, 300, 512)])
+def test_fp8_gemm_matches_oracle(dev, m, n, k):
+    g = torch.Generator().manual_seed(m * n + k)
+    w = (torch.randn(n, k, generator=g) * 0.5).to(torch.float8_e4m3fn)
+    sb = torch.rand(n, generator=g) * 0.02 + 0.001
+    sa = torch.rand(m, generator=g) + 0.5
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    ref = mx.fp8_linear(a, w.view(torch.uint8).numpy(), sa, sb)
+    got = axk.fp8_gemm(a.to(dev), w.to(dev), sa.to(dev), sb.to(dev))
+    torch.testing.assert_close(got.float().cpu(), ref.to(torch.bfloat16).float(), **BF16_TOL)
+    got32 = axk.fp8_gemm(a.to(dev), w.to(dev), None, sb.to(dev), out_dtype=torch.float32)
+    ref32 = mx.fp8_linear(a, w.view(torch.uint8).numpy(), None, sb)
+    torch.testing.assert_close(got32.cpu(), ref32, **F32_TOL)
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 256, 2048), (1, 64, 32), (4096 // 64, 256, 2048)])
+def test_bf16_gemm_matches_oracle(dev, m, n, k):
+    g = torch.Generator().manual_seed(m + n + k)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    ref = a.float() @ w.float().T
+    got = axk.bf16_gemm(a.to(dev), w.to(dev), out_dtype=torch.float32)
+    torch.testing.assert_close(got.cpu(), ref, **F32_TOL)
