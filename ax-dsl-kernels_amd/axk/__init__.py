@@ -12,3 +12,15 @@ __all__ = ["bf16_gemm", "fp8_gemm", "mxfp4_dequant", "mxfp4_gemm", "load_library
 def load_library():
     """Load libaxk.so (raises ImportError if it has not been built)."""
     return _lib.load()
+
+from . import attention  # noqa: E402
+from .attention import (  # noqa: E402
+    paged_decode,
+    paged_decode_plan,
+    paged_decode_run,
+    paged_decode_workspace,
+    store_paged_kv,
+)
+
+__all__ += ["attention", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
+            "store_paged_kv"]

@@ -59,8 +59,19 @@ SIGNATURES: dict[str, list] = {
     "axk_mxfp4_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_fp8_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_bf16_gemm": [_vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "axk_paged_decode_workspace_size": [_i64, _i64, _i64, _i64],
+    "axk_paged_decode_plan": [_vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
+    "axk_paged_decode_run": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
+                             ctypes.c_size_t, _vp],
+    "axk_paged_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
+                         ctypes.c_size_t, _vp],
+    "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
 }
-_RESTYPES = {"axk_version": ctypes.c_char_p, "axk_status_string": ctypes.c_char_p}
+_RESTYPES = {
+    "axk_version": ctypes.c_char_p,
+    "axk_status_string": ctypes.c_char_p,
+    "axk_paged_decode_workspace_size": ctypes.c_size_t,
+}
 
 
 def header_symbols(path: str = HEADER_PATH) -> list[str]:

@@ -1,0 +1,126 @@
+"""Paged decode attention and the paged KV write on gfx950.
+
+Mirrors the paged-KV part of sgl_kernel_axera.attention.flash_attn
+(models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/flash_attn.py): cache
+[pages, 2, page_size, HKV, D] bf16, FlashInfer-style indptr / indices / last_page_len page tables
+(flash_attn.py:2549-2665) and store_paged_kv's cache_location = [page, offset] (53-84). Like the
+reference, the operator allocates nothing it is not asked to: pass ``workspace`` (see
+``paged_decode_workspace``) to keep calls allocation-free.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def paged_decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                           device) -> torch.Tensor:
+    """A byte buffer large enough for paged_decode with this configuration."""
+    n = _lib.load().axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim)
+    _check(n > 0, "invalid paged decode configuration")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def _check_decode(q, kv_cache, indptr, indices, last_page_len):
+    _check(q.dim() == 3 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, HQ, D]")
+    _check(kv_cache.dim() == 5 and kv_cache.dtype == torch.bfloat16 and kv_cache.is_contiguous(),
+           "kv_cache must be contiguous bf16 [pages, 2, page_size, HKV, D]")
+    b, hq, d = q.shape
+    p, two, page, hkv, d2 = kv_cache.shape
+    _check(two == 2 and d2 == d, f"kv_cache shape {tuple(kv_cache.shape)} does not match q {tuple(q.shape)}")
+    _check(hq % hkv == 0 and hq // hkv <= 16, f"num_qo_heads {hq} must be a multiple (<= 16x) of num_kv_heads {hkv}")
+    _check(d in (64, 128, 256), f"head_dim {d} not supported (64, 128, 256)")
+    _check(page % 32 == 0, f"page_size {page} must be a multiple of 32")
+    for name, t, n in (("indptr", indptr, b + 1), ("last_page_len", last_page_len, b)):
+        _check(t.dtype == torch.int32 and t.dim() == 1 and t.numel() == n and t.is_contiguous(),
+               f"{name} must be contiguous int32 [{n}]")
+    _check(indices.dtype == torch.int32 and indices.dim() == 1 and indices.is_contiguous(),
+           "indices must be contiguous int32 [nnz]")
+    return b, hq, hkv, d, page, p
+
+
+def paged_decode_plan(indptr: torch.Tensor, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                      workspace: torch.Tensor) -> None:
+    """Compute the split-KV partition for this page-table shape into ``workspace`` (once per decode step)."""
+    b = indptr.numel() - 1
+    _check(indptr.dtype == torch.int32 and indptr.dim() == 1 and b > 0, "indptr must be int32 [B+1]")
+    _lib.require_device(indptr, workspace)
+    _lib.call("axk_paged_decode_plan", indptr.data_ptr(), b, num_qo_heads, num_kv_heads, head_dim,
+              workspace.data_ptr(), workspace.numel(), _lib.stream_of(indptr))
+
+
+def paged_decode_run(q, kv_cache, indptr, indices, last_page_len, workspace, sm_scale=None, output=None):
+    """Decode attention with a plan already in ``workspace`` (see paged_decode_plan)."""
+    b, hq, hkv, d, page, p = _check_decode(q, kv_cache, indptr, indices, last_page_len)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    _lib.require_device(q, kv_cache, indptr, indices, last_page_len, output, workspace)
+    _lib.call(
+        "axk_paged_decode_run", q.data_ptr(), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
+        last_page_len.data_ptr(), output.data_ptr(), b, hq, hkv, d, page, p, float(sm_scale),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q),
+    )
+    return output
+
+
+def paged_decode(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    indptr: torch.Tensor,
+    indices: torch.Tensor,
+    last_page_len: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """One decode token per sequence attends all valid tokens of its pages.
+
+    q [B, HQ, D] bf16; kv_cache [P, 2, page, HKV, D] bf16; indptr [B+1], indices [nnz],
+    last_page_len [B] int32 (1..page; tokens in the last page). Returns bf16 [B, HQ, D].
+    """
+    b, hq, hkv, d, page, p = _check_decode(q, kv_cache, indptr, indices, last_page_len)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    if workspace is None:
+        workspace = paged_decode_workspace(b, hq, hkv, d, q.device)
+    _lib.require_device(q, kv_cache, indptr, indices, last_page_len, output, workspace)
+    _lib.call(
+        "axk_paged_decode", q.data_ptr(), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
+        last_page_len.data_ptr(), output.data_ptr(), b, hq, hkv, d, page, p, float(sm_scale),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q),
+    )
+    return output
+
+
+def store_paged_kv(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor, cache_location: torch.Tensor,
+                   status: Optional[torch.Tensor] = None) -> None:
+    """Write k[b], v[b] ([B, HKV, D] bf16) at cache_location[b] = (page, offset) in place (flash_attn.py:53-84)."""
+    _check(k.shape == v.shape and k.dim() == 3 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+           "k and v must be bf16 [B, HKV, D]")
+    _check(k.is_contiguous() and v.is_contiguous() and kv_cache.is_contiguous(), "tensors must be contiguous")
+    b, hkv, d = k.shape
+    p, two, page, hkv2, d2 = kv_cache.shape
+    _check(two == 2 and hkv2 == hkv and d2 == d, "kv_cache shape does not match k / v")
+    loc = cache_location.reshape(-1, 2) if cache_location.numel() == 2 * b else None
+    _check(loc is not None and cache_location.dtype == torch.int32 and loc.is_contiguous(),
+           "cache_location must be int32 [B, 2] = (page, offset)")
+    _lib.require_device(k, v, kv_cache, loc, status)
+    _lib.call(
+        "axk_paged_kv_write", k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(), loc.data_ptr(), b, hkv, d, page, p,
+        _lib.ptr(status), _lib.stream_of(k),
+    )

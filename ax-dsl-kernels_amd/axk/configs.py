@@ -27,3 +27,25 @@ def config0(seed: int = 0):
     codes, scales = mxfp4_weight(4096, 4096, g)
     x = torch.randn(1, 4096, generator=g).to(torch.bfloat16)
     return {"x": x, "w": codes, "s": scales}
+
+
+def paged_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator, extra_pages: int = 0):
+    """A paged KV pool holding sequences of the given lengths, pages placed by a random permutation."""
+    npages = [(L + page - 1) // page for L in lens]
+    pool = sum(npages) + extra_pages
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    indptr = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    indptr[1:] = torch.cumsum(torch.tensor(npages, dtype=torch.int32), 0)
+    indices = perm[: int(indptr[-1])].contiguous()
+    last = torch.tensor([L - page * (n - 1) if n else 0 for L, n in zip(lens, npages)], dtype=torch.int32)
+    q = torch.randn(len(lens), hq, d, generator=g).to(torch.bfloat16)
+    cache = torch.randn(pool, 2, page, hkv, d, generator=g).to(torch.bfloat16)
+    return {"q": q, "cache": cache, "indptr": indptr, "indices": indices, "last_page_len": last,
+            "lens": list(lens), "scale": d ** -0.5}
+
+
+def config1(seed: int = 0):
+    """Config 1: paged decode, batch 16, 16 q heads / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384]."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1024, 16385, (16,), generator=g).tolist()
+    return paged_case(lens, 16, 2, 256, 64, g)

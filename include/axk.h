@@ -96,6 +96,61 @@ int axk_fp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const flo
 int axk_bf16_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, const float* bias, void* out,
                   int out_dtype, int64_t m, int64_t n, int64_t k, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Paged flash-attention decode and the paged KV write
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes axk_paged_decode needs for this batch / head configuration (0 = invalid shape). */
+size_t axk_paged_decode_workspace_size(int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                                       int64_t head_dim);
+
+/* Split-KV work partition for axk_paged_decode_run, computed on the device from indptr into the
+ * workspace (pages per split, per-sequence item offsets; arrival counters zeroed). It depends only
+ * on the page-table shape, so one plan serves every attention layer of a decode step. */
+int axk_paged_decode_plan(const int32_t* indptr, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                          int64_t head_dim, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
+/* The decode attention itself, using the plan held in `workspace` (same batch / heads / indptr).
+ * One kernel launch; arguments as axk_paged_decode. */
+int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                         const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                         int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                         int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
+                         axk_stream_t stream);
+
+/* Decode attention of one query token per sequence over a paged KV cache (GQA, split-KV):
+ * axk_paged_decode_plan followed by axk_paged_decode_run.
+ * Replaces the page loop of sgl_kernel_axera.attention.flash_attn.paged_attention
+ * (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/flash_attn.py:1421-1596, page-id
+ * lookup 1478-1495, tail mask 87-104) and attention_split_qa of
+ * models/qwen38_27b/decode/q35_group.py:317-385 (split-KV + LSE merge).
+ *   q             bf16 [batch, num_qo_heads, head_dim]
+ *   kv_cache      bf16 [num_pages, 2, page_size, num_kv_heads, head_dim] (plane 0 = K, 1 = V)
+ *   indptr        i32  [batch + 1]   CSR offsets into indices
+ *   indices       i32  [indptr[batch]] physical page ids (each < num_pages)
+ *   last_page_len i32  [batch]        valid tokens in each sequence's last page (1..page_size)
+ *   out           bf16 [batch, num_qo_heads, head_dim]
+ * The query attends every valid cached token of its sequence (write the current token with
+ * axk_paged_kv_write first: the reference's "history + current token" merge is the same sum).
+ * A sequence with no pages yields zeros. head_dim in {64, 128, 256}; num_qo_heads / num_kv_heads
+ * <= 16; page_size a multiple of 32. Page ids outside [0, num_pages) are skipped, never read.
+ * workspace >= axk_paged_decode_workspace_size(...), 256-byte aligned. */
+int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                     const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                     int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                     int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
+                     axk_stream_t stream);
+
+/* Scatter the current token's K and V rows into the paged cache in place:
+ *   kv_cache[loc[b,0], 0, loc[b,1], :, :] = k[b]; kv_cache[loc[b,0], 1, loc[b,1], :, :] = v[b].
+ * Replaces store_paged_kv (flash_attn.py:53-84, cache_location = [page, offset]) and
+ * kv_write_paged (models/qwen38_27b/decode/q35_group.py:237-264). Every other cache byte is left
+ * untouched. k, v bf16 [batch, num_kv_heads, head_dim]; cache_location i32 [batch, 2].
+ * A location outside the pool is skipped and *status (if non-NULL, device i32) is set to 1. */
+int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* kv_cache, const int32_t* cache_location,
+                       int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                       int64_t num_pages, int32_t* status, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

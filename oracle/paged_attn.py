@@ -1,0 +1,68 @@
+"""Oracle: paged decode attention and the paged KV write (CPU, test infrastructure only).
+
+Restates
+  * the paged SDPA golden of models/qwen35_35b_a3b/sgl/tests/test_qwen35_runtime.py:73-84: gather the
+    history rows of the sequence's pages (cache[rows, 0/1].reshape(-1, HKV, D)[:L]) and run fp32
+    softmax(q K^T * scale) V with GQA (query head h uses KV head h // (HQ / HKV));
+  * the page-table semantics of sgl_kernel_axera/attention/flash_attn.py:1478-1495 (physical page =
+    indices[indptr[b] + logical page]) and the tail mask of 87-104 (tokens past the valid length of the
+    last page are excluded);
+  * store_paged_kv of flash_attn.py:53-84 (row = (page * 2 + plane) * page_size + offset).
+Pinned by tests/test_oracle_paged.py: torch SDPA (enable_gqa=True, the reference's golden call) on the
+same gathered rows, a brute-force per-token index computation of the gather, invariance under a
+consistent permutation of the page pool, and the one-page case against dense attention.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def seq_lens(indptr, last_page_len, page_size: int) -> list[int]:
+    ip = np.asarray(indptr)
+    lp = np.asarray(last_page_len)
+    out = []
+    for b in range(len(lp)):
+        n = int(ip[b + 1] - ip[b])
+        out.append(0 if n == 0 else (n - 1) * page_size + int(lp[b]))
+    return out
+
+
+def gather_kv(cache: torch.Tensor, indptr, indices, last_page_len, b: int):
+    """K, V rows [L, HKV, D] of sequence b, in token order (flash_attn.py:1478-1495)."""
+    page_size = cache.shape[2]
+    ip = np.asarray(indptr)
+    rows = torch.as_tensor(np.asarray(indices)[ip[b]:ip[b + 1]], dtype=torch.long)
+    L = seq_lens(indptr, last_page_len, page_size)[b]
+    k = cache[rows, 0].reshape(-1, cache.shape[3], cache.shape[4])[:L]
+    v = cache[rows, 1].reshape(-1, cache.shape[3], cache.shape[4])[:L]
+    return k, v
+
+
+def paged_decode(q: torch.Tensor, cache: torch.Tensor, indptr, indices, last_page_len, sm_scale: float) -> torch.Tensor:
+    """fp32 [B, HQ, D]; a sequence without tokens yields zeros."""
+    bsz, hq, d = q.shape
+    hkv = cache.shape[3]
+    grp = hq // hkv
+    out = torch.zeros(bsz, hq, d, dtype=torch.float32)
+    for b in range(bsz):
+        k, v = gather_kv(cache, indptr, indices, last_page_len, b)
+        if k.shape[0] == 0:
+            continue
+        kf = k.float().repeat_interleave(grp, dim=1)  # [L, HQ, D]
+        vf = v.float().repeat_interleave(grp, dim=1)
+        s = torch.einsum("hd,lhd->hl", q[b].float(), kf) * sm_scale
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.einsum("hl,lhd->hd", p, vf)
+    return out
+
+
+def store_paged_kv(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
+    """Returns a copy of cache with k[b] / v[b] written at (page, offset) = loc[b] (flash_attn.py:53-84)."""
+    c = cache.clone()
+    loc = np.asarray(loc).reshape(-1, 2)
+    for b in range(k.shape[0]):
+        page, off = int(loc[b, 0]), int(loc[b, 1])
+        c[page, 0, off] = k[b]
+        c[page, 1, off] = v[b]
+    return c

@@ -1,0 +1,136 @@
+"""GPU parity of paged decode attention and the paged KV write against the oracle.
+
+Bar: bf16 outputs within rel 2e-2 / abs 1e-2 of the fp32 golden; the KV write is byte-exact and leaves
+every other cache byte untouched; repeated launches are bitwise identical.
+"""
+import pytest
+import torch
+
+import axk
+from axk import attention, configs
+from oracle import paged_attn as pa
+
+pytestmark = pytest.mark.gpu
+TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def _run(c, dev, **kw):
+    out = attention.paged_decode(
+        c["q"].to(dev), c["cache"].to(dev), c["indptr"].to(dev), c["indices"].to(dev),
+        c["last_page_len"].to(dev), sm_scale=c["scale"], **kw,
+    )
+    return out.cpu()
+
+
+def _ref(c):
+    return pa.paged_decode(c["q"], c["cache"], c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+
+
+@pytest.mark.parametrize(
+    "lens,hq,hkv,d,page",
+    [
+        ([1], 1, 1, 64, 32),
+        ([31, 32, 33, 64, 65], 8, 2, 64, 32),
+        ([1, 100, 1000], 16, 2, 256, 64),
+        ([500, 7, 129], 4, 4, 128, 64),
+        ([300, 2000], 16, 1, 128, 256),
+        ([64, 0, 65], 8, 1, 256, 64),  # an empty sequence yields zeros
+        ([4096] * 3, 32, 4, 256, 64),
+    ],
+)
+def test_paged_decode_matches_oracle(dev, lens, hq, hkv, d, page):
+    g = torch.Generator().manual_seed(sum(lens) + hq + d)
+    c = configs.paged_case(lens, hq, hkv, d, page, g, extra_pages=2)
+    print(f"case lens={lens} hq={hq} hkv={hkv} d={d} page={page}", flush=True)
+    got = _run(c, dev)
+    ref = _ref(c)
+    torch.testing.assert_close(got.float(), ref.to(torch.bfloat16).float(), **TOL)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not got[b].any()
+
+
+def test_paged_decode_config1_and_determinism(dev):
+    c = configs.config1()
+    print(f"config1 lens={c['lens']}", flush=True)
+    ws = attention.paged_decode_workspace(16, 16, 2, 256, dev)
+    got = _run(c, dev, workspace=ws)
+    torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
+    again = _run(c, dev, workspace=ws)
+    assert torch.equal(got.view(torch.int16), again.view(torch.int16))
+
+
+def test_paged_decode_ignores_garbage_past_the_tail(dev):
+    g = torch.Generator().manual_seed(5)
+    c = configs.paged_case([70, 10], 8, 2, 64, 64, g)
+    clean = _run(c, dev)
+    # poison every slot past each sequence's valid length with NaN: masked slots must not leak
+    for b in range(len(c["lens"])):
+        last = int(c["indices"][int(c["indptr"][b + 1]) - 1])
+        c["cache"][last, :, int(c["last_page_len"][b]):] = float("nan")
+    poisoned = _run(c, dev)
+    assert torch.equal(clean.view(torch.int16), poisoned.view(torch.int16))
+
+
+def test_kv_write_then_decode(dev):
+    g = torch.Generator().manual_seed(11)
+    c = configs.paged_case([65, 128, 1], 8, 2, 128, 64, g, extra_pages=4)
+    cache = c["cache"].to(dev)
+    before = cache.clone()
+    # append one token to each sequence: (page, offset) of token L (a fresh page when L % 64 == 0)
+    loc, new_last, new_indices, new_indptr = [], [], [], [0]
+    used = set(c["indices"].tolist())
+    spare = [p for p in range(c["cache"].shape[0]) if p not in used]
+    for b, L in enumerate(c["lens"]):
+        pages = c["indices"][int(c["indptr"][b]):int(c["indptr"][b + 1])].tolist()
+        if L % 64 == 0:
+            pages.append(spare.pop())
+        loc.append([pages[-1], L % 64])
+        new_indices += pages
+        new_indptr.append(len(new_indices))
+        new_last.append(L % 64 + 1)
+    k = torch.randn(3, 2, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(3, 2, 128, generator=g).to(torch.bfloat16)
+    loc_t = torch.tensor(loc, dtype=torch.int32)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    attention.store_paged_kv(k.to(dev), v.to(dev), cache, loc_t.to(dev), status=status)
+    ref_cache = pa.store_paged_kv(before.cpu(), k, v, loc_t.numpy())
+    assert torch.equal(cache.cpu().view(torch.int16), ref_cache.view(torch.int16))
+    assert int(status.item()) == 0
+    c2 = dict(c, cache=cache.cpu(), indices=torch.tensor(new_indices, dtype=torch.int32),
+              indptr=torch.tensor(new_indptr, dtype=torch.int32), last_page_len=torch.tensor(new_last, dtype=torch.int32),
+              lens=[L + 1 for L in c["lens"]])
+    got = _run(c2, dev)
+    torch.testing.assert_close(got.float(), _ref(c2).to(torch.bfloat16).float(), **TOL)
+    # an out-of-pool location is skipped and flagged, the cache stays as it was
+    snap = cache.clone()
+    attention.store_paged_kv(k[:1].to(dev), v[:1].to(dev), cache,
+                             torch.tensor([[10_000, 0]], dtype=torch.int32, device=dev), status=status)
+    assert int(status.item()) == 1 and torch.equal(cache, snap)
+
+
+def test_contract_errors(dev):
+    c = configs.paged_case([10], 8, 2, 64, 32, torch.Generator().manual_seed(0))
+    with pytest.raises(ValueError):
+        attention.paged_decode(c["q"].to(dev), c["cache"].to(dev), c["indptr"].to(dev).long(), c["indices"].to(dev),
+                               c["last_page_len"].to(dev))
+    small = torch.empty(16, dtype=torch.uint8, device=dev)
+    with pytest.raises(axk._lib.AxkError):
+        attention.paged_decode(c["q"].to(dev), c["cache"].to(dev), c["indptr"].to(dev), c["indices"].to(dev),
+                               c["last_page_len"].to(dev), workspace=small)
+
+
+def test_plan_once_run_many(dev):
+    """One plan serves several runs (every attention layer of a step): the arrival counters reset."""
+    g = torch.Generator().manual_seed(21)
+    c = configs.paged_case([100, 3000, 64, 9000], 16, 2, 256, 64, g)
+    ws = attention.paged_decode_workspace(4, 16, 2, 256, dev)
+    args = [c[k].to(dev) for k in ("indptr", "indices", "last_page_len")]
+    cache = c["cache"].to(dev)
+    attention.paged_decode_plan(args[0], 16, 2, 256, ws)
+    for trial in range(3):
+        q = torch.randn(4, 16, 256, generator=g).to(torch.bfloat16)
+        print(f"run {trial}", flush=True)
+        got = attention.paged_decode_run(q.to(dev), cache, *args, workspace=ws, sm_scale=c["scale"]).cpu()
+        ref = pa.paged_decode(q, c["cache"], c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+        torch.testing.assert_close(got.float(), ref.to(torch.bfloat16).float(), **TOL)
