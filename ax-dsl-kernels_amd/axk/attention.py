@@ -48,14 +48,15 @@ def _check_decode(q, kv_cache, indptr, indices, last_page_len):
     return b, hq, hkv, d, page, p
 
 
-def paged_decode_plan(indptr: torch.Tensor, num_qo_heads: int, num_kv_heads: int, head_dim: int,
-                      workspace: torch.Tensor) -> None:
+def paged_decode_plan(indptr: torch.Tensor, last_page_len: torch.Tensor, num_qo_heads: int, num_kv_heads: int,
+                      head_dim: int, page_size: int, workspace: torch.Tensor) -> None:
     """Compute the split-KV partition for this page-table shape into ``workspace`` (once per decode step)."""
     b = indptr.numel() - 1
     _check(indptr.dtype == torch.int32 and indptr.dim() == 1 and b > 0, "indptr must be int32 [B+1]")
-    _lib.require_device(indptr, workspace)
-    _lib.call("axk_paged_decode_plan", indptr.data_ptr(), b, num_qo_heads, num_kv_heads, head_dim,
-              workspace.data_ptr(), workspace.numel(), _lib.stream_of(indptr))
+    _check(last_page_len.dtype == torch.int32 and last_page_len.numel() == b, "last_page_len must be int32 [B]")
+    _lib.require_device(indptr, last_page_len, workspace)
+    _lib.call("axk_paged_decode_plan", indptr.data_ptr(), last_page_len.data_ptr(), b, num_qo_heads, num_kv_heads,
+              head_dim, page_size, workspace.data_ptr(), workspace.numel(), _lib.stream_of(indptr))
 
 
 def paged_decode_run(q, kv_cache, indptr, indices, last_page_len, workspace, sm_scale=None, output=None):

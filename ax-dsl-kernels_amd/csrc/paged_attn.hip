@@ -5,19 +5,22 @@
 // indices[indptr[b] .. indptr[b+1]); the last one holds last_page_len[b] valid tokens (1..page_size),
 // every other page is full (flash_attn.py:1421-1596 page-id lookup, tail mask 87-104).
 //
-// Two kernels:
+// Three kernels:
 //  1. plan   — one wave: pages per split so that the number of (sequence, KV head, split) work items
-//              is about kTargetItems; prefix offsets of the items per sequence; zeroes the arrival
-//              counters. Depends only on the page-table shape, so one plan serves every attention layer
-//              of a decode step (no host sync, no memset: graph-capturable).
+//              is about kTargetItems, and one descriptor per item. Depends only on the page-table
+//              shape, so one plan serves every attention layer of a decode step (no host sync, no
+//              memset: graph-capturable).
 //  2. decode — one workgroup per work item. Each wave takes 32-token tiles of the item's pages:
 //              S^T = K Q^T on MFMA (K rows straight from HBM with 128-bit loads, Q in registers),
-//              online softmax in fp32 (exp2 domain), P (bf16) x V on MFMA with V staged through a
-//              padded LDS tile (the token-contiguous operand MFMA needs); the 4 waves merge their
-//              (m, l, O) in LDS. A sequence with one split writes its output directly; otherwise the
-//              item writes an fp32 partial and the last item of its (sequence, KV head) to arrive
-//              (atomic counter) merges all partials by log-sum-exp — the split-KV merge of
-//              models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:330-349 — and resets the counter.
+//              online softmax in fp32 (exp2 domain), P (bf16) x V on MFMA with V streamed HBM -> LDS
+//              by direct loads into a padded tile (the token-contiguous operand MFMA needs); the 4 waves
+//              merge their (m, l, O) in LDS. A sequence with one split writes its output directly;
+//              otherwise the item writes an fp32 partial (m, l, O).
+//  3. merge  — per (sequence, KV head) with more than one split: log-sum-exp merge of the partials,
+//              the split-KV merge of models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:330-349; zero
+//              output for sequences without pages. A separate launch on purpose: merging inside the
+//              decode kernel needs a device-scope release/acquire per workgroup, which on a multi-XCD
+//              part writes back and invalidates the whole L2 and serialises the kernel.
 #include "axk_common.h"
 #include "axk_host.h"
 
@@ -32,23 +35,30 @@ constexpr float kLog2e = 1.4426950408889634f;
 struct PlanHeader {
   int n_items;
   int pages_per_split;
-  int bad_page;  // set to 1 if a page id outside [0, num_pages) was met (page skipped)
-  int batch;     // batch / num_kv_heads the plan was made for (checked by the run kernel)
+  int bad_page;   // set to 1 if a page id outside [0, num_pages) was met (page skipped)
+  int batch;      // batch / num_kv_heads the plan was made for (checked by the run kernel)
   int hkv;
-  int pad[3];
+  int next_item;  // work queue of the persistent split kernel (zeroed by plan and by merge)
+  int pad[2];
+};
+
+// One work item: KV head kvh of sequence b, pages indices[ibeg .. ibeg + npg), split `split` of nsplit.
+struct ItemDesc {
+  int b, kvh, split, nsplit;
+  int ibeg, npg, last_valid, pad;  // last_valid: valid tokens in the item's last page
 };
 
 size_t ws_items_max(int64_t batch, int64_t hkv) { return (size_t)kTargetItems + (size_t)batch * hkv; }
 
-size_t ws_layout(int64_t batch, int64_t hkv, int64_t group, int64_t d, size_t* off_item, size_t* off_cnt,
+size_t ws_layout(int64_t batch, int64_t hkv, int64_t group, int64_t d, size_t* off_item, size_t* off_desc,
                  size_t* off_m, size_t* off_l, size_t* off_o) {
   const size_t maxi = ws_items_max(batch, hkv);
   size_t off = sizeof(PlanHeader);
   *off_item = off;
   off += sizeof(int) * (size_t)(batch + 1);
-  *off_cnt = off;
-  off += sizeof(int) * (size_t)(batch * hkv);
   off = (off + 255) & ~(size_t)255;
+  *off_desc = off;
+  off += sizeof(ItemDesc) * maxi;
   *off_m = off;
   off += sizeof(float) * maxi * group;
   *off_l = off;
@@ -59,103 +69,131 @@ size_t ws_layout(int64_t batch, int64_t hkv, int64_t group, int64_t d, size_t* o
   return off;
 }
 
-__global__ __launch_bounds__(64) void paged_plan_kernel(const int* __restrict__ indptr, int batch, int hkv,
-                                                        PlanHeader* __restrict__ hdr, int* __restrict__ item_off,
-                                                        int* __restrict__ counters) {
-  const int lane = threadIdx.x;
-  for (int i = lane; i < batch * hkv; i += 64) counters[i] = 0;
-  // total pages
-  int tot = 0;
-  for (int b = lane; b < batch; b += 64) tot += indptr[b + 1] - indptr[b];
+constexpr int kPlanLdsBatch = 4096;  // sequences whose item offsets the plan keeps in LDS
+
+__global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__ indptr,
+                                                         const int* __restrict__ last_page_len, int batch, int hkv,
+                                                         int page_size, PlanHeader* __restrict__ hdr,
+                                                         int* __restrict__ item_off, ItemDesc* __restrict__ descs) {
+  __shared__ int s_off[kPlanLdsBatch + 1];
+  __shared__ int s_pps, s_items;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int tpp = page_size / kTile;
+  if (tid < 64) {
+    int tot = 0;
+    for (int b = lane; b < batch; b += 64) tot += indptr[b + 1] - indptr[b];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
-  const long long work = (long long)tot * hkv;
-  int pps = (int)((work + kTargetItems - 1) / kTargetItems);
-  if (pps < 1) pps = 1;
-  // prefix sum of items per sequence, 64 sequences at a time
-  int base = 0;
-  for (int b0 = 0; b0 < batch; b0 += 64) {
-    const int b = b0 + lane;
-    int cnt = 0;
-    if (b < batch) {
-      const int np = indptr[b + 1] - indptr[b];
-      cnt = hkv * ((np + pps - 1) / pps);
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const long long work = (long long)tot * hkv;
+    int pps = (int)((work + kTargetItems - 1) / kTargetItems);
+    if (pps < 1) pps = 1;
+    // whole tiles per wave: make pages-per-split x tiles-per-page a multiple of the wave count
+    if (tpp < kWaves) {
+      const int mult = kWaves / tpp;
+      pps = (pps + mult - 1) / mult * mult;
     }
-    int incl = cnt;
+    // prefix sum of items per sequence, 64 sequences at a time
+    int base = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+      const int b = b0 + lane;
+      int cnt = 0;
+      if (b < batch) cnt = hkv * ((indptr[b + 1] - indptr[b] + pps - 1) / pps);
+      int incl = cnt;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int v = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += v;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += v;
+      }
+      if (b < batch) {
+        item_off[b] = base + incl - cnt;
+        if (b < kPlanLdsBatch) s_off[b] = base + incl - cnt;
+      }
+      base += __shfl(incl, 63, 64);
     }
-    if (b < batch) item_off[b] = base + incl - cnt;
-    base += __shfl(incl, 63, 64);
+    if (lane == 0) {
+      item_off[batch] = base;
+      if (batch <= kPlanLdsBatch) s_off[batch] = base;
+      s_pps = pps;
+      s_items = base;
+      hdr->n_items = base;
+      hdr->pages_per_split = pps;
+      hdr->bad_page = 0;
+      hdr->batch = batch;
+      hdr->hkv = hkv;
+      hdr->next_item = 0;
+    }
   }
-  if (lane == 0) {
-    item_off[batch] = base;
-    hdr->n_items = base;
-    hdr->pages_per_split = pps;
-    hdr->bad_page = 0;
-    hdr->batch = batch;
-    hdr->hkv = hkv;
+  __syncthreads();
+  const int pps = s_pps, n_items = s_items;
+  const int* offs = batch <= kPlanLdsBatch ? s_off : item_off;  // global copy: same values, written above
+  for (int it = tid; it < n_items; it += blockDim.x) {
+    int lo = 0, hi = batch - 1;  // the sequence whose item range holds `it`
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (offs[mid] <= it) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    const int pb = indptr[b], np = indptr[b + 1] - pb;
+    const int ns = (np + pps - 1) / pps;
+    const int local = it - offs[b];
+    const int kvh = local / ns, sp = local - kvh * ns;
+    ItemDesc d;
+    d.b = b;
+    d.kvh = kvh;
+    d.split = sp;
+    d.nsplit = ns;
+    d.ibeg = pb + sp * pps;
+    d.npg = min(pps, np - sp * pps);
+    d.last_valid = sp == ns - 1 ? last_page_len[b] : page_size;
+    d.pad = 0;
+    descs[it] = d;
   }
 }
 
 template <int D>
 struct PagedCfg {
-  static constexpr int KSTEPS = D / 32;         // MFMA k-steps over the head dim
-  static constexpr int DQ = D / 4;              // head-dim values per lane group
-  static constexpr int DT = D / 16;             // 16-wide d tiles of O
-  static constexpr int ROW = D * 2 + 16;        // LDS bytes per staged V row: 16-byte aligned rows, and
-                                                // the 4 lane groups reading rows 4g + i hit disjoint banks
-  static constexpr int VBYTES = kTile * ROW;    // one wave's V tile
-  static constexpr int CHUNKS = D / 8;          // 16-byte chunks per row
+  static constexpr int KSTEPS = D / 32;            // MFMA k-steps over the head dim
+  static constexpr int DT = D / 16;                // 16-wide d tiles of O
+  static constexpr int RPI = 512 / D;              // V rows per direct-to-LDS instruction (64 lanes x 16 B)
+  static constexpr int NINST = kTile / RPI;        // instructions per V tile
+  static constexpr int PAD = D == 256 ? 32 : 64;   // LDS bytes between instruction blocks: the 4 lane groups
+                                                   // reading rows 4g + i then hit disjoint banks
+  static constexpr int BLK = 1024 + PAD;
+  static constexpr int VBYTES = NINST * BLK;       // one wave's V tile
+  static AXK_DEV int row_off(int tok) { return (tok / RPI) * BLK + (tok % RPI) * (2 * D); }
 };
 
-template <int D>
-__global__ __launch_bounds__(256) void paged_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, const int* __restrict__ indptr,
-    const int* __restrict__ indices, const int* __restrict__ last_page_len, int batch, int hq, int hkv,
-    int page_size, int64_t num_pages, float sm_scale, PlanHeader* __restrict__ hdr,
-    const int* __restrict__ item_off, int* __restrict__ counters, float* __restrict__ part_m,
-    float* __restrict__ part_l, float* __restrict__ part_o, uint16_t* __restrict__ out) {
-  using C = PagedCfg<D>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int it = blockIdx.x;
-  const int n_items = hdr->n_items;
-  if (it >= n_items || hdr->batch != batch || hdr->hkv != hkv) return;
-  const int pps = hdr->pages_per_split;
-  const int group = hq / hkv;
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-  // item -> (b, kvh, split): binary search over the per-sequence item offsets
-  int lo = 0, hi = batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (item_off[mid] <= it) lo = mid; else hi = mid - 1;
-  }
-  const int b = lo;
-  const int nsplit = (item_off[b + 1] - item_off[b]) / hkv;
-  const int local = it - item_off[b];
-  const int kvh = local / nsplit, split = local - kvh * nsplit;
-  const int pbeg = indptr[b];
-  const int npages = indptr[b + 1] - pbeg;
-  const int lp0 = split * pps;
-  const int lp1 = min(npages, lp0 + pps);
-  const int last_valid = last_page_len[b];
+// Attention of one work item by the 4 waves of the workgroup.
+template <int D>
+__device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
+                                            const uint16_t* __restrict__ cache, const int* __restrict__ indices,
+                                            int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
+                                            PlanHeader* __restrict__ hdr, float* __restrict__ part_m,
+                                            float* __restrict__ part_l, float* __restrict__ part_o,
+                                            uint16_t* __restrict__ out, unsigned char* smem) {
+  using C = PagedCfg<D>;
+  const int group = hq / hkv;
+  const int b = desc.b, kvh = desc.kvh, nsplit = desc.nsplit;
   const int tpp = page_size / kTile;  // tiles per page
-  const int ntiles = (lp1 - lp0) * tpp;
+  const int ntiles = desc.npg * tpp;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const float c = sm_scale * kLog2e;
 
-  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = g*DQ + 8s .. +8.
+  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s.
   axk_bf16x8 qb[C::KSTEPS];
   {
     const bool hv = l16 < group;
-    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + g * C::DQ;
+    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 8 * g;
 #pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 8 * s) : zero_bf16x8();
+    for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
   }
+  // the item's page ids, 64 at a time: lane j holds page j of the current chunk
+  int chunk = 0;
+  int pid = lane < desc.npg ? indices[desc.ibeg + lane] : 0;
 
   axk_f32x4 o[C::DT];
 #pragma unroll
@@ -167,9 +205,14 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
   const int64_t plane_stride = (int64_t)page_size * row_stride;
 
   for (int ti = wave; ti < ntiles; ti += kWaves) {
-    const int lp = lp0 + ti / tpp, tp = ti - (ti / tpp) * tpp;
-    const int page = indices[pbeg + lp];
-    const int valid_in_page = (lp == npages - 1) ? last_valid : page_size;
+    const int lp = ti / tpp, tp = ti - lp * tpp;
+    if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids
+      chunk = lp >> 6;
+      const int j = (chunk << 6) + lane;
+      pid = j < desc.npg ? indices[desc.ibeg + j] : 0;
+    }
+    const int page = __shfl(pid, lp & 63, 64);
+    const int valid_in_page = (lp == desc.npg - 1) ? desc.last_valid : page_size;
     const int nvalid = min(kTile, valid_in_page - tp * kTile);
     if (nvalid <= 0) continue;
     if (page < 0 || page >= num_pages) {
@@ -179,25 +222,28 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     const uint16_t* kbase = cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + kvh * D;
     const uint16_t* vbase = kbase + plane_stride;
 
-    // K rows for the two 16-token halves (A operand): lane (token l16, group g), d = g*DQ + 8s.
+    // K rows for the two 16-token halves (A operand): lane (token l16, group g), d = 32s + 8g .. +8, so
+    // each row is read as 64-byte runs. Rows past nvalid re-read row 0 (finite) and are masked below.
     axk_bf16x8 ka[2][C::KSTEPS];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int tok = 16 * h + l16;
-      const bool ok = tok < nvalid;
-      const uint16_t* kp = kbase + (int64_t)tok * row_stride + g * C::DQ;
+      const uint16_t* kp = kbase + (int64_t)(tok < nvalid ? tok : 0) * row_stride + 8 * g;
 #pragma unroll
-      for (int s = 0; s < C::KSTEPS; ++s) ka[h][s] = ok ? load_bf16x8(kp + 8 * s) : zero_bf16x8();
+      for (int s = 0; s < C::KSTEPS; ++s) ka[h][s] = load_bf16x8(kp + 32 * s);
     }
-    // V tile -> LDS (row-major, padded); rows past nvalid are zero so masked P never meets garbage.
+    // V tile: HBM -> LDS directly (global_load_lds_dwordx4, no VGPRs). Instruction i writes rows
+    // RPI*i .. RPI*i + RPI - 1 contiguously at vt + i*BLK; lane l carries 16 bytes of row RPI*i + l / (D/8).
 #pragma unroll
-    for (int i = 0; i < (kTile * C::CHUNKS) / 64; ++i) {
-      const int qi = i * 64 + lane;
-      const int tok = qi / C::CHUNKS, ch = qi - tok * C::CHUNKS;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (tok < nvalid) v = *reinterpret_cast<const uint4*>(vbase + (int64_t)tok * row_stride + ch * 8);
-      *reinterpret_cast<uint4*>(vt + tok * C::ROW + ch * 16) = v;
+    for (int i = 0; i < C::NINST; ++i) {
+      const int tok = C::RPI * i + lane / (D / 8);
+      const uint16_t* src = vbase + (int64_t)(tok < nvalid ? tok : 0) * row_stride + (lane % (D / 8)) * 8;
+      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(vt + i * C::BLK), 16, 0, 0);
     }
+    // keep every load of the tile in flight before the first wait (no MFMA hoisted between them)
+    __builtin_amdgcn_sched_barrier(0);
+    // wait for the K loads only (issued first); the V tile keeps streaming during QK and softmax
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::NINST) : "memory");
 
     // S^T tiles: lane holds S[token 16h + 4g + r][head l16]
     axk_f32x4 st[2];
@@ -240,7 +286,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
 
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V tile landed in LDS
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
@@ -252,7 +298,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int tok = (i < 4) ? (4 * g + i) : (16 + 4 * g + i - 4);
-        vb[i] = *reinterpret_cast<const __bf16*>(col + tok * C::ROW);
+        vb[i] = *reinterpret_cast<const __bf16*>(col + C::row_off(tok));
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[t][r] *= ar[r];
@@ -328,30 +374,95 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     part_m[(int64_t)it * group + threadIdx.x] = sm_mm[threadIdx.x];
     part_l[(int64_t)it * group + threadIdx.x] = sm_mm[16 + threadIdx.x];
   }
-  // arrival: the last item of (b, kvh) merges every split of it
-  __threadfence();
-  __syncthreads();
-  int* ticket = reinterpret_cast<int*>(sm_mm + 32);
-  if (threadIdx.x == 0) *ticket = atomicAdd(&counters[b * hkv + kvh], 1);
-  __syncthreads();
-  if (*ticket != nsplit - 1) return;
-  __threadfence();
-  const int i0 = item_off[b] + kvh * nsplit;
-  for (int idx = threadIdx.x; idx < group * D; idx += blockDim.x) {
-    const int hh = idx / D, d = idx - hh * D;
-    float mm = -INFINITY;
-    for (int i = 0; i < nsplit; ++i) mm = fmaxf(mm, __builtin_nontemporal_load(&part_m[(int64_t)(i0 + i) * group + hh]));
-    float ll = 0.f, acc = 0.f;
-    for (int i = 0; i < nsplit; ++i) {
-      const float mi = __builtin_nontemporal_load(&part_m[(int64_t)(i0 + i) * group + hh]);
-      if (mi == -INFINITY) continue;
-      const float w = exp2f(mi - mm);
-      ll += __builtin_nontemporal_load(&part_l[(int64_t)(i0 + i) * group + hh]) * w;
-      acc += __builtin_nontemporal_load(&part_o[((int64_t)(i0 + i) * group + hh) * D + d]) * w;
-    }
-    out[out_base + idx] = (uint16_t)f32_to_bf16_bits(ll > 0.f ? acc / ll : 0.f);
+}
+
+// Persistent split kernel: a few workgroups per CU; each takes work items from the plan's queue until it
+// is empty (first item = blockIdx.x, then gridDim.x + ticket), so every CU stays busy to the end.
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, const int* __restrict__ indices, int batch,
+    int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, PlanHeader* __restrict__ hdr,
+    const ItemDesc* __restrict__ descs, float* __restrict__ part_m, float* __restrict__ part_l,
+    float* __restrict__ part_o, uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int s_next;
+  if (hdr->batch != batch || hdr->hkv != hkv) return;
+  const int n_items = hdr->n_items;
+  int it = blockIdx.x;
+  while (it < n_items) {
+    const ItemDesc desc = descs[it];
+    decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
+                   part_o, out, smem);
+    __syncthreads();  // LDS is reused by the next item
+    if (threadIdx.x == 0) s_next = gridDim.x + atomicAdd(&hdr->next_item, 1);
+    __syncthreads();
+    it = s_next;
   }
-  if (threadIdx.x == 0) counters[b * hkv + kvh] = 0;  // ready for another run with the same plan
+}
+
+// One wave per (sequence, query head): merge the item partials of a sequence with more than one split;
+// zero the output of a sequence without pages. Lane i holds split i's (m, l) (64 splits per pass); each
+// lane then accumulates D/64 output columns over all splits with independent loads.
+template <int D>
+__global__ __launch_bounds__(64) void paged_merge_kernel(const int* __restrict__ indptr,
+                                                         PlanHeader* __restrict__ hdr,
+                                                         const int* __restrict__ item_off, int batch, int hq,
+                                                         int hkv, const float* __restrict__ part_m,
+                                                         const float* __restrict__ part_l,
+                                                         const float* __restrict__ part_o,
+                                                         uint16_t* __restrict__ out) {
+  constexpr int V = D / 64;  // output columns per lane
+  const int b = blockIdx.x / hq, h = blockIdx.x - (blockIdx.x / hq) * hq;
+  const int lane = threadIdx.x;
+  if (hdr->batch != batch || hdr->hkv != hkv) return;
+  if (blockIdx.x == 0 && lane == 0) hdr->next_item = 0;  // the split kernel's queue, for the next run
+  const int group = hq / hkv, kvh = h / group, hh = h - kvh * group;
+  uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
+  if (indptr[b + 1] == indptr[b]) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) op[j] = 0;
+    return;
+  }
+  const int nsplit = (item_off[b + 1] - item_off[b]) / hkv;
+  if (nsplit <= 1) return;  // written by the decode kernel
+  const int i0 = item_off[b] + kvh * nsplit;
+  // online merge, 16 splits per pass: every load of a pass (m, l and this lane's O columns) is issued
+  // before any is used, so a pass costs one memory round trip
+  constexpr int P = 16;
+  float mm = -INFINITY, ll = 0.f, acc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) acc[j] = 0.f;
+  for (int c0 = 0; c0 < nsplit; c0 += P) {
+    float mi[P], li[P], oi[P][V];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      const int i = min(c0 + k, nsplit - 1);  // clamped: in-bounds, weight zeroed below
+      mi[k] = part_m[(int64_t)(i0 + i) * group + hh];
+      li[k] = part_l[(int64_t)(i0 + i) * group + hh];
+      const float* src = part_o + ((int64_t)(i0 + i) * group + hh) * D + lane * V;
+#pragma unroll
+      for (int j = 0; j < V; ++j) oi[k][j] = src[j];
+    }
+    float cm = mm;
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+      if (c0 + k < nsplit) cm = fmaxf(cm, mi[k]);
+    const float sc = mm == -INFINITY ? 0.f : exp2f(mm - cm);
+    ll *= sc;
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] *= sc;
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+      const float w = (c0 + k < nsplit && mi[k] != -INFINITY) ? exp2f(mi[k] - cm) : 0.f;
+      ll += w * li[k];
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] += w * oi[k][j];
+    }
+    mm = cm;
+  }
+  const float inv = ll > 0.f ? 1.0f / ll : 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
 }
 
 // cache[loc[b,0], 0, loc[b,1], kvh, :] = k[b, kvh, :]; plane 1 <- v (store_paged_kv, flash_attn.py:53-84).
@@ -382,26 +493,40 @@ __global__ __launch_bounds__(256) void paged_kv_write_kernel(const uint16_t* __r
 struct WsView {
   PlanHeader* hdr;
   int* item_off;
-  int* counters;
+  ItemDesc* descs;
   float *pm, *pl, *po;
 };
 
 WsView ws_view(void* ws, int batch, int hkv, int group, int d) {
-  size_t oi, oc, om, ol, oo;
-  ws_layout(batch, hkv, group, d, &oi, &oc, &om, &ol, &oo);
+  size_t oi, od, om, ol, oo;
+  ws_layout(batch, hkv, group, d, &oi, &od, &om, &ol, &oo);
   unsigned char* w = reinterpret_cast<unsigned char*>(ws);
-  return {reinterpret_cast<PlanHeader*>(w), reinterpret_cast<int*>(w + oi), reinterpret_cast<int*>(w + oc),
+  return {reinterpret_cast<PlanHeader*>(w), reinterpret_cast<int*>(w + oi), reinterpret_cast<ItemDesc*>(w + od),
           reinterpret_cast<float*>(w + om), reinterpret_cast<float*>(w + ol), reinterpret_cast<float*>(w + oo)};
 }
 
+constexpr int kBlocksPerCU = 2;  // resident split workgroups per CU (LDS-bound: 2 x 67 KiB)
+
+// Compute units of the current device (cached per device).
+int device_cu_count() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 template <int D>
-int launch_run(const uint16_t* q, const uint16_t* cache, const int* indptr, const int* indices,
-               const int* last_page_len, uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages,
-               float sm_scale, void* ws, hipStream_t st) {
+int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, const int* indices, uint16_t* out,
+                 int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, void* ws,
+                 hipStream_t st) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
   const size_t lds_v = (size_t)kWaves * PagedCfg<D>::VBYTES;
-  const size_t lds_m = sizeof(float) * (2 * kWaves * 16 + (size_t)kWaves * 16 * D + 32 + 4);
+  const size_t lds_m = sizeof(float) * (2 * kWaves * 16 + (size_t)kWaves * 16 * D + 36 + 32);
   const size_t lds = lds_v > lds_m ? lds_v : lds_m;
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
@@ -411,9 +536,18 @@ int launch_run(const uint16_t* q, const uint16_t* cache, const int* indptr, cons
     lds_raised = true;
   }
   const unsigned items = (unsigned)ws_items_max(batch, hkv);
-  hipLaunchKernelGGL((paged_decode_kernel<D>), dim3(items), dim3(64 * kWaves), lds, st, q, cache, indptr, indices,
-                     last_page_len, batch, hq, hkv, page_size, num_pages, sm_scale, v.hdr, v.item_off, v.counters,
-                     v.pm, v.pl, v.po, out);
+  const unsigned slots = (unsigned)(kBlocksPerCU * device_cu_count());
+  hipLaunchKernelGGL((paged_decode_kernel<D>), dim3(items < slots ? items : slots), dim3(64 * kWaves), lds, st, q,
+                     cache, indices, batch, hq, hkv, page_size, num_pages, sm_scale, v.hdr, v.descs, v.pm, v.pl, v.po,
+                     out);
+  return axk_launch_status();
+}
+
+template <int D>
+int launch_merge(const int* indptr, uint16_t* out, int batch, int hq, int hkv, void* ws, hipStream_t st) {
+  const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
+  hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)(batch * hq)), dim3(64), 0, st, indptr, v.hdr,
+                     v.item_off, batch, hq, hkv, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
 
@@ -433,26 +567,28 @@ extern "C" size_t axk_paged_decode_workspace_size(int64_t batch, int64_t num_qo_
   return ws_layout(batch, num_kv_heads, num_qo_heads / num_kv_heads, head_dim, &a, &b, &c, &d, &e);
 }
 
-extern "C" int axk_paged_decode_plan(const int32_t* indptr, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
-                                     int64_t head_dim, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
-  AXK_REQUIRE(indptr, AXK_E_NULL);
+extern "C" int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_page_len, int64_t batch,
+                                     int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                     void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(indptr && last_page_len, AXK_E_NULL);
   const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
+  AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096, AXK_E_SHAPE);
   const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
   const WsView v = ws_view(workspace, (int)batch, (int)num_kv_heads, (int)(num_qo_heads / num_kv_heads),
                            (int)head_dim);
-  hipLaunchKernelGGL(paged_plan_kernel, dim3(1), dim3(64), 0, axk_stream(stream), indptr, (int)batch,
-                     (int)num_kv_heads, v.hdr, v.item_off, v.counters);
+  hipLaunchKernelGGL(paged_plan_kernel, dim3(1), dim3(256), 0, axk_stream(stream), indptr, last_page_len, (int)batch,
+                     (int)num_kv_heads, (int)page_size, v.hdr, v.item_off, v.descs);
   return axk_launch_status();
 }
 
-extern "C" int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
-                                    const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
-                                    int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
-                                    int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
-                                    size_t workspace_bytes, axk_stream_t stream) {
-  AXK_REQUIRE(q && kv_cache && indptr && indices && last_page_len && out, AXK_E_NULL);
+extern "C" int axk_paged_decode_split(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                                      const int32_t* indices, uint16_t* out, int64_t batch, int64_t num_qo_heads,
+                                      int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                                      float sm_scale, void* workspace, size_t workspace_bytes,
+                                      axk_stream_t stream) {
+  AXK_REQUIRE(q && kv_cache && indptr && indices && out, AXK_E_NULL);
   const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096, AXK_E_SHAPE);
@@ -467,15 +603,42 @@ extern "C" int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache,
   const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
   switch (head_dim) {
     case 64:
-      return launch_run<64>(q, kv_cache, indptr, indices, last_page_len, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                            workspace, st);
+      return launch_split<64>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
     case 128:
-      return launch_run<128>(q, kv_cache, indptr, indices, last_page_len, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                             workspace, st);
+      return launch_split<128>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
     default:
-      return launch_run<256>(q, kv_cache, indptr, indices, last_page_len, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                             workspace, st);
+      return launch_split<256>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
   }
+}
+
+extern "C" int axk_paged_decode_merge(const int32_t* indptr, uint16_t* out, int64_t batch, int64_t num_qo_heads,
+                                      int64_t num_kv_heads, int64_t head_dim, void* workspace,
+                                      size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(indptr && out, AXK_E_NULL);
+  const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
+  if (rc != AXK_OK) return rc;
+  const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  hipStream_t st = axk_stream(stream);
+  const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads;
+  switch (head_dim) {
+    case 64: return launch_merge<64>(indptr, out, B, HQ, HKV, workspace, st);
+    case 128: return launch_merge<128>(indptr, out, B, HQ, HKV, workspace, st);
+    default: return launch_merge<256>(indptr, out, B, HQ, HKV, workspace, st);
+  }
+}
+
+extern "C" int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                                    const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
+                                    int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                    int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
+                                    size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(last_page_len, AXK_E_NULL);
+  int rc = axk_paged_decode_split(q, kv_cache, indptr, indices, out, batch, num_qo_heads, num_kv_heads, head_dim,
+                                  page_size, num_pages, sm_scale, workspace, workspace_bytes, stream);
+  if (rc != AXK_OK) return rc;
+  return axk_paged_decode_merge(indptr, out, batch, num_qo_heads, num_kv_heads, head_dim, workspace,
+                                workspace_bytes, stream);
 }
 
 extern "C" int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
@@ -486,8 +649,8 @@ extern "C" int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, con
   AXK_REQUIRE(q && kv_cache && indices && last_page_len && out, AXK_E_NULL);
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
   AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16), AXK_E_ALIGN);
-  const int rc = axk_paged_decode_plan(indptr, batch, num_qo_heads, num_kv_heads, head_dim, workspace,
-                                       workspace_bytes, stream);
+  const int rc = axk_paged_decode_plan(indptr, last_page_len, batch, num_qo_heads, num_kv_heads, head_dim,
+                                       page_size, workspace, workspace_bytes, stream);
   if (rc != AXK_OK) return rc;
   return axk_paged_decode_run(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads,
                               head_dim, page_size, num_pages, sm_scale, workspace, workspace_bytes, stream);

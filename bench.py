@@ -90,12 +90,13 @@ class MxLinearWorkload:
 class PagedDecodeWorkload:
     """Config 1: paged decode attention, batch 16, 16 q / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384].
 
-    One step = plan (split-KV partition from indptr) + run (the attention kernel). The roofline is the run
-    kernel's: algorithmic bytes = K and V rows of every valid token + q + out + page table.
+    One step = plan (split-KV partition) + split (the attention kernel) + merge (LSE merge of split partials).
+    The roofline is the split kernel's: algorithmic bytes = K and V rows of every valid token + q + out +
+    page table.
     """
 
     name = "paged_decode"
-    kernel = "paged_decode_kernel<256>"
+    kernel = "paged_decode_kernel<256>"  # launched by axk_paged_decode_split
     timing = "events"
 
     def __init__(self, dev):
@@ -123,12 +124,16 @@ class PagedDecodeWorkload:
         from axk import _lib
 
         lib = _lib.load()
-        self._plan = lambda: lib.axk_paged_decode_plan(self.indptr.data_ptr(), b, hq, hkv, d, self.ws.data_ptr(),
-                                                       self.ws.numel(), torch.cuda.current_stream().cuda_stream)
-        self._run = lambda cache: lib.axk_paged_decode_run(
+        self._plan = lambda: lib.axk_paged_decode_plan(self.indptr.data_ptr(), self.last.data_ptr(), b, hq, hkv, d,
+                                                       c["cache"].shape[2], self.ws.data_ptr(), self.ws.numel(),
+                                                       torch.cuda.current_stream().cuda_stream)
+        self._split = lambda cache: lib.axk_paged_decode_split(
             self.q.data_ptr(), cache.data_ptr(), self.indptr.data_ptr(), self.indices.data_ptr(),
-            self.last.data_ptr(), self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2], c["cache"].shape[0],
+            self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2], c["cache"].shape[0],
             c["scale"], self.ws.data_ptr(), self.ws.numel(), torch.cuda.current_stream().cuda_stream)
+        self._merge = lambda: lib.axk_paged_decode_merge(self.indptr.data_ptr(), self.out.data_ptr(), b, hq, hkv, d,
+                                                         self.ws.data_ptr(), self.ws.numel(),
+                                                         torch.cuda.current_stream().cuda_stream)
         self.config = {"workload": "config1: paged decode B=16 HQ=16 HKV=2 D=256 page=64 L~U[1024,16384]",
                        "sum_context": tot, "rotating_copies": self.copies}
         self.dtype = "bf16 (fp32 softmax / accumulation)"
@@ -137,11 +142,15 @@ class PagedDecodeWorkload:
         assert self._plan() == 0
 
     def main(self, i: int) -> None:
-        assert self._run(self.caches[i % self.copies]) == 0
+        assert self._split(self.caches[i % self.copies]) == 0
+
+    def post(self, i: int) -> None:
+        assert self._merge() == 0
 
     def step(self, i: int) -> None:
         self.pre(i)
         self.main(i)
+        self.post(i)
 
     def cpu_baseline(self) -> dict:
         import torch
@@ -218,6 +227,7 @@ def main() -> int:
             evs[i][0].record()
             wl.main(i)
             evs[i][1].record()
+            wl.post(i)
         end.record()
         torch.cuda.synchronize()
         ms_per_step = start.elapsed_time(end) / args.steps

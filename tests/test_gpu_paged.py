@@ -127,7 +127,7 @@ def test_plan_once_run_many(dev):
     ws = attention.paged_decode_workspace(4, 16, 2, 256, dev)
     args = [c[k].to(dev) for k in ("indptr", "indices", "last_page_len")]
     cache = c["cache"].to(dev)
-    attention.paged_decode_plan(args[0], 16, 2, 256, ws)
+    attention.paged_decode_plan(args[0], args[2], 16, 2, 256, 64, ws)
     for trial in range(3):
         q = torch.randn(4, 16, 256, generator=g).to(torch.bfloat16)
         print(f"run {trial}", flush=True)
