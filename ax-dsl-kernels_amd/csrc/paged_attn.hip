@@ -27,7 +27,8 @@
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kTile = 32;  // tokens per tile = one PV MFMA k-step
+constexpr int kTile = 16;  // tokens per tile = one 16x16x16 PV MFMA k-step
+constexpr int kNBuf = 3;   // LDS ring of tiles: two in flight while one is computed
 constexpr int kTargetItems = 1024;
 constexpr int kMaxGroup = 16;  // query heads per KV head (MFMA N tile)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -73,25 +74,23 @@ constexpr int kPlanLdsBatch = 4096;  // sequences whose item offsets the plan ke
 
 __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__ indptr,
                                                          const int* __restrict__ last_page_len, int batch, int hkv,
-                                                         int page_size, PlanHeader* __restrict__ hdr,
+                                                         int page_size, int slots, PlanHeader* __restrict__ hdr,
                                                          int* __restrict__ item_off, ItemDesc* __restrict__ descs) {
   __shared__ int s_off[kPlanLdsBatch + 1];
   __shared__ int s_pps, s_items;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int tpp = page_size / kTile;
   if (tid < 64) {
     int tot = 0;
     for (int b = lane; b < batch; b += 64) tot += indptr[b + 1] - indptr[b];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
     const long long work = (long long)tot * hkv;
-    int pps = (int)((work + kTargetItems - 1) / kTargetItems);
+    // one round of the persistent split kernel: at most `slots` items (each sequence may add one partial
+    // split per KV head on top of work / pps), and never more than the workspace holds
+    int target = min(slots, kTargetItems);
+    if (target - batch * hkv >= target / 2) target -= batch * hkv;
+    int pps = (int)((work + target - 1) / target);
     if (pps < 1) pps = 1;
-    // whole tiles per wave: make pages-per-split x tiles-per-page a multiple of the wave count
-    if (tpp < kWaves) {
-      const int mult = kWaves / tpp;
-      pps = (pps + mult - 1) / mult * mult;
-    }
     // prefix sum of items per sequence, 64 sequences at a time
     int base = 0;
     for (int b0 = 0; b0 < batch; b0 += 64) {
@@ -152,20 +151,50 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
 
 template <int D>
 struct PagedCfg {
-  static constexpr int KSTEPS = D / 32;            // MFMA k-steps over the head dim
-  static constexpr int DT = D / 16;                // 16-wide d tiles of O
-  static constexpr int RPI = 512 / D;              // V rows per direct-to-LDS instruction (64 lanes x 16 B)
-  static constexpr int NINST = kTile / RPI;        // instructions per V tile
-  static constexpr int PAD = D == 256 ? 32 : 64;   // LDS bytes between instruction blocks: the 4 lane groups
-                                                   // reading rows 4g + i then hit disjoint banks
+  static constexpr int KSTEPS = D / 32;       // 16x16x32 MFMA k-steps over the head dim (QK)
+  static constexpr int DW = D / kWaves;       // head-dim columns of O owned by one wave
+  static constexpr int DT = DW / 16;          // 16-wide O tiles per wave
+  static constexpr int RPI = 512 / D;         // rows per direct-to-LDS instruction (64 lanes x 16 B)
+  static constexpr int IPP = kTile / RPI;     // instructions per plane (K or V) of a tile
+  static constexpr int IPW = 2 * IPP / kWaves;  // instructions per wave per tile
+  static constexpr int PAD = D == 256 ? 32 : 64;  // bytes after each 1 KiB block (bank spread for V reads)
   static constexpr int BLK = 1024 + PAD;
-  static constexpr int VBYTES = NINST * BLK;       // one wave's V tile
+  static constexpr int PLANE = IPP * BLK;     // one plane of a tile in LDS
+  static constexpr int BUF = 2 * PLANE;       // one tile (K then V)
   static AXK_DEV int row_off(int tok) { return (tok / RPI) * BLK + (tok % RPI) * (2 * D); }
 };
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
+// LDS byte address of a __shared__ pointer (for M0).
+AXK_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
 
-// Attention of one work item by the 4 waves of the workgroup.
+// Direct HBM -> LDS load: lane l's 16 bytes at gptr land at lds_base + 16 l (lds_base wave-uniform).
+// Issued from asm on purpose: the compiler then counts none of these loads, so its own waits can only
+// over-wait, and the pipeline waits below (s_waitcnt vmcnt(n)) stay exactly as written. M0 is restored.
+AXK_DEV void lds_dma16(const void* gptr, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(gptr)
+      : "memory");
+}
+
+template <int N>
+AXK_DEV void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef short axk_i16x4 __attribute__((ext_vector_type(4)));
+
+// Attention of one work item. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
+// (each wave issues a quarter of its loads) into a ring of kNBuf buffers, two tiles ahead of the one being
+// computed. Every wave computes the full scores S^T = K Q^T of the tile (cheap on MFMA) and the online
+// softmax, then P x V for its own quarter of the head dim, so no cross-wave merge is needed.
 template <int D>
 __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
                                             const uint16_t* __restrict__ cache, const int* __restrict__ indices,
@@ -182,6 +211,13 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const float c = sm_scale * kLog2e;
+  const int64_t row_stride = (int64_t)hkv * D;  // elements between consecutive tokens
+  const int64_t plane_stride = (int64_t)page_size * row_stride;
+  const uint32_t lds0 = lds_addr(smem);
+
+  // the item's page ids, 64 at a time: lane j holds page j of the current chunk
+  int chunk = 0;
+  int pid = lane < desc.npg ? indices[desc.ibeg + lane] : 0;
 
   // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s.
   axk_bf16x8 qb[C::KSTEPS];
@@ -191,188 +227,136 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
   }
-  // the item's page ids, 64 at a time: lane j holds page j of the current chunk
-  int chunk = 0;
-  int pid = lane < desc.npg ? indices[desc.ibeg + lane] : 0;
-
-  axk_f32x4 o[C::DT];
+  // make the compiler take its waits for Q and the page ids here, before the asm loads it cannot count
+  asm volatile("" : "+v"(pid));
 #pragma unroll
-  for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g)
+  for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qb[s]));
 
-  unsigned char* vt = smem + wave * C::VBYTES;
-  const int64_t row_stride = (int64_t)hkv * D;          // elements between consecutive tokens
-  const int64_t plane_stride = (int64_t)page_size * row_stride;
-
-  for (int ti = wave; ti < ntiles; ti += kWaves) {
+  // tile ti -> valid tokens and K base; a tile past the sequence end or on a page outside the pool gets
+  // nvalid = 0 and an in-bounds base
+  auto locate = [&](int ti, int& nvalid) -> const uint16_t* {
     const int lp = ti / tpp, tp = ti - lp * tpp;
-    if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids
+    if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
       chunk = lp >> 6;
       const int j = (chunk << 6) + lane;
       pid = j < desc.npg ? indices[desc.ibeg + j] : 0;
+      asm volatile("" : "+v"(pid));  // the compiler's wait for this load stays inside this rare branch
     }
-    const int page = __shfl(pid, lp & 63, 64);
+    int page = __shfl(pid, lp & 63, 64);
     const int valid_in_page = (lp == desc.npg - 1) ? desc.last_valid : page_size;
-    const int nvalid = min(kTile, valid_in_page - tp * kTile);
-    if (nvalid <= 0) continue;
+    nvalid = min(kTile, valid_in_page - tp * kTile);
     if (page < 0 || page >= num_pages) {
-      if (lane == 0) hdr->bad_page = 1;
-      continue;
+      if (lane == 0 && nvalid > 0) hdr->bad_page = 1;
+      page = 0;
+      nvalid = 0;
     }
-    const uint16_t* kbase = cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + kvh * D;
-    const uint16_t* vbase = kbase + plane_stride;
+    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + kvh * D;
+  };
+  // this wave's share of tile ti's loads into ring buffer nb (rows past nvalid re-read row 0); returns the
+  // tile's valid token count
+  auto issue = [&](int ti, int nb) -> int {
+    int nvalid;
+    const uint16_t* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
+    const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
+#pragma unroll
+    for (int k = 0; k < C::IPW; ++k) {
+      const int j = wave * C::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
+      const int plane = j / C::IPP, blk = j - plane * C::IPP;
+      const int tok = blk * C::RPI + lane / (D / 8);
+      const uint16_t* src = kbase + plane * plane_stride + (int64_t)(tok < nrow ? tok : 0) * row_stride +
+                            (lane % (D / 8)) * 8;
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK));
+    }
+    return ti < ntiles ? nvalid : 0;
+  };
 
-    // K rows for the two 16-token halves (A operand): lane (token l16, group g), d = 32s + 8g .. +8, so
-    // each row is read as 64-byte runs. Rows past nvalid re-read row 0 (finite) and are masked below.
-    axk_bf16x8 ka[2][C::KSTEPS];
+  // O^T tiles: lane holds O[head l16][d = wave*DW + 16t + 4g + r] (same head layout as the softmax state)
+  axk_f32x4 o[C::DT];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int tok = 16 * h + l16;
-      const uint16_t* kp = kbase + (int64_t)(tok < nvalid ? tok : 0) * row_stride + 8 * g;
-#pragma unroll
-      for (int s = 0; s < C::KSTEPS; ++s) ka[h][s] = load_bf16x8(kp + 32 * s);
-    }
-    // V tile: HBM -> LDS directly (global_load_lds_dwordx4, no VGPRs). Instruction i writes rows
-    // RPI*i .. RPI*i + RPI - 1 contiguously at vt + i*BLK; lane l carries 16 bytes of row RPI*i + l / (D/8).
-#pragma unroll
-    for (int i = 0; i < C::NINST; ++i) {
-      const int tok = C::RPI * i + lane / (D / 8);
-      const uint16_t* src = vbase + (int64_t)(tok < nvalid ? tok : 0) * row_stride + (lane % (D / 8)) * 8;
-      __builtin_amdgcn_global_load_lds(src, (lds_ptr)(vt + i * C::BLK), 16, 0, 0);
-    }
-    // keep every load of the tile in flight before the first wait (no MFMA hoisted between them)
-    __builtin_amdgcn_sched_barrier(0);
-    // wait for the K loads only (issued first); the V tile keeps streaming during QK and softmax
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::NINST) : "memory");
+  for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g and over the waves)
 
-    // S^T tiles: lane holds S[token 16h + 4g + r][head l16]
-    axk_f32x4 st[2];
+  int nv0 = issue(0, 0);  // valid tokens of tiles ti, ti + 1, ti + 2
+  int nv1 = issue(1, 1);
+  for (int ti = 0; ti < ntiles; ++ti) {
+    const int nb = ti % kNBuf;
+    wait_vmcnt<C::IPW>();              // this wave's loads of tile ti have landed (tile ti + 1 may not)
+    __builtin_amdgcn_s_barrier();      // ... and every other wave's; all are done with tile ti - 1
+    const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);  // into the buffer of tile ti - 1
+    const int nvalid = nv0;
+    nv0 = nv1;
+    nv1 = nv2;
+    if (nvalid <= 0) continue;  // wave-uniform
+    const unsigned char* kt = smem + nb * C::BUF;
+    const unsigned char* vt = kt + C::PLANE;
+    // S^T (16 tokens x 16 heads): A = K rows (lane: token l16, d = 32s + 8g .. +8); lane holds
+    // S[token 4g + r][head l16]
+    axk_f32x4 st = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+    const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      st[h] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < C::KSTEPS; ++s) st[h] = mfma_bf16_16x16x32(ka[h][s], qb[s], st[h]);
-    }
+    for (int s = 0; s < C::KSTEPS; ++s)
+      st = mfma_bf16_16x16x32(*reinterpret_cast<const axk_bf16x8*>(krow + 64 * s), qb[s], st);
     float mx = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int tok = 16 * h + 4 * g + r;
-        const float sv = tok < nvalid ? st[h][r] * c : -INFINITY;
-        st[h][r] = sv;
-        mx = fmaxf(mx, sv);
-      }
+    for (int rr = 0; rr < 4; ++rr) {
+      const float sv = (4 * g + rr < nvalid) ? st[rr] * c : -INFINITY;
+      st[rr] = sv;
+      mx = fmaxf(mx, sv);
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
+    const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one valid token
     const float alpha = exp2f(m_run - m_new);
     float psum = 0.f;
-    axk_bf16x8 pa;
+    axk_i16x4 pb;  // B operand of O^T = V^T P^T: lane (head l16, group g) = P[head][tokens 4g .. 4g + 3]
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(st[h][r] - m_new);
-        psum += p;
-        pa[4 * h + r] = (__bf16)p;
-      }
+    for (int rr = 0; rr < 4; ++rr) {
+      const float p = (4 * g + rr < nvalid) ? exp2f(st[rr] - m_new) : 0.f;
+      psum += p;
+      pb[rr] = (short)f32_to_bf16_bits(p);
+    }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // O rows are heads 4g + r: fetch their alpha from lane (4g + r)
-    float ar[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * g + r, 64);
-
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // V tile landed in LDS
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // P x V: B operand lane (d = 16t + l16, group g) = V[token(8g + i)][d], token(8g+i) matching pa's order
 #pragma unroll
     for (int t = 0; t < C::DT; ++t) {
-      axk_bf16x8 vb;
-      const unsigned char* col = vt + (16 * t + l16) * 2;
+      // A operand V^T: lane (d = wave*DW + 16t + l16, group g) = V[tokens 4g .. 4g + 3][d]
+      const unsigned char* col = vt + (wave * C::DW + 16 * t + l16) * 2;
+      axk_i16x4 va;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int tok = (i < 4) ? (4 * g + i) : (16 + 4 * g + i - 4);
-        vb[i] = *reinterpret_cast<const __bf16*>(col + C::row_off(tok));
-      }
+      for (int rr = 0; rr < 4; ++rr) va[rr] = *reinterpret_cast<const short*>(col + C::row_off(4 * g + rr));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[t][r] *= ar[r];
-      o[t] = mfma_bf16_16x16x32(pa, vb, o[t]);
+      for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
   }
+  wait_vmcnt<0>();  // drain the two look-ahead tiles before the buffers are reused
+  __builtin_amdgcn_s_barrier();
 
-  // ---- merge the 4 waves' (m, l, O) in LDS, write the item partial ----
-  __syncthreads();
-  float* sm_m = reinterpret_cast<float*>(smem);           // [kWaves][16]
-  float* sm_l = sm_m + kWaves * 16;                       // [kWaves][16]
-  float* sm_o = sm_l + kWaves * 16;                       // [kWaves][16][D]
-  if (lane < 16) {
-    sm_m[wave * 16 + lane] = m_run;
-    sm_l[wave * 16 + lane] = l_run;
-  }
-  __syncthreads();
-  // each wave rescales its O rows (heads 4g + r) to the common max
-  float scale_r[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int hh = 4 * g + r;
-    float mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm_m[w * 16 + hh]);
-    const float mw = sm_m[wave * 16 + hh];
-    scale_r[r] = (mw == -INFINITY) ? 0.f : exp2f(mw - mm);
-  }
-#pragma unroll
-  for (int t = 0; t < C::DT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm_o[(wave * 16 + 4 * g + r) * D + 16 * t + l16] = o[t][r] * scale_r[r];
-  __syncthreads();
-  // merged (m, l) of this item for head hh
-  float* sm_mm = sm_o + kWaves * 16 * D;  // [16] item max, [16] item sum
-  if (threadIdx.x < 16) {
-    const int hh = threadIdx.x;
-    float mm = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm_m[w * 16 + hh]);
-    float ll = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = sm_m[w * 16 + hh];
-      if (mw != -INFINITY) ll += sm_l[w * 16 + hh] * exp2f(mw - mm);
-    }
-    sm_mm[hh] = mm;
-    sm_mm[16 + hh] = ll;
-  }
-  __syncthreads();
+  // every wave holds the same (m, l) for head l16 and O^T for its own columns
   const int64_t out_base = ((int64_t)b * hq + kvh * group) * D;
+  const bool hv = l16 < group;
   if (nsplit == 1) {  // the whole sequence in one item: normalise and store
-    for (int idx = threadIdx.x; idx < group * D; idx += blockDim.x) {
-      const int hh = idx / D, d = idx - hh * D;
-      float acc = 0.f;
+    const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) acc += sm_o[(w * 16 + hh) * D + d];
-      const float ll = sm_mm[16 + hh];
-      out[out_base + idx] = (uint16_t)f32_to_bf16_bits(ll > 0.f ? acc / ll : 0.f);
+    for (int t = 0; t < C::DT; ++t) {
+      if (!hv) continue;
+      uint2 w;
+      w.x = f32_to_bf16_bits(o[t][0] * inv) | (f32_to_bf16_bits(o[t][1] * inv) << 16);
+      w.y = f32_to_bf16_bits(o[t][2] * inv) | (f32_to_bf16_bits(o[t][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(out + out_base + (int64_t)l16 * D + wave * C::DW + 16 * t + 4 * g) = w;
     }
     return;
   }
-  for (int idx = threadIdx.x; idx < group * D; idx += blockDim.x) {
-    const int hh = idx / D, d = idx - hh * D;
-    float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) acc += sm_o[(w * 16 + hh) * D + d];
-    part_o[((int64_t)it * group + hh) * D + d] = acc;
-  }
-  if (threadIdx.x < group) {
-    part_m[(int64_t)it * group + threadIdx.x] = sm_mm[threadIdx.x];
-    part_l[(int64_t)it * group + threadIdx.x] = sm_mm[16 + threadIdx.x];
+  for (int t = 0; t < C::DT; ++t)
+    if (hv)
+      *reinterpret_cast<float4*>(part_o + ((int64_t)it * group + l16) * D + wave * C::DW + 16 * t + 4 * g) =
+          make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+  if (wave == 0 && lane < group) {
+    part_m[(int64_t)it * group + lane] = m_run;
+    part_l[(int64_t)it * group + lane] = l_run;
   }
 }
 
@@ -505,7 +489,7 @@ WsView ws_view(void* ws, int batch, int hkv, int group, int d) {
           reinterpret_cast<float*>(w + om), reinterpret_cast<float*>(w + ol), reinterpret_cast<float*>(w + oo)};
 }
 
-constexpr int kBlocksPerCU = 2;  // resident split workgroups per CU (LDS-bound: 2 x 67 KiB)
+constexpr int kBlocksPerCU = 3;  // resident split workgroups per CU (LDS-bound: 3 x 3 tiles x 16.5 KiB)
 
 // Compute units of the current device (cached per device).
 int device_cu_count() {
@@ -525,9 +509,7 @@ int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, co
                  hipStream_t st) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
-  const size_t lds_v = (size_t)kWaves * PagedCfg<D>::VBYTES;
-  const size_t lds_m = sizeof(float) * (2 * kWaves * 16 + (size_t)kWaves * 16 * D + 36 + 32);
-  const size_t lds = lds_v > lds_m ? lds_v : lds_m;
+  const size_t lds = (size_t)kNBuf * PagedCfg<D>::BUF;
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D>),
@@ -579,7 +561,7 @@ extern "C" int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_
   const WsView v = ws_view(workspace, (int)batch, (int)num_kv_heads, (int)(num_qo_heads / num_kv_heads),
                            (int)head_dim);
   hipLaunchKernelGGL(paged_plan_kernel, dim3(1), dim3(256), 0, axk_stream(stream), indptr, last_page_len, (int)batch,
-                     (int)num_kv_heads, (int)page_size, v.hdr, v.item_off, v.descs);
+                     (int)num_kv_heads, (int)page_size, kBlocksPerCU * device_cu_count(), v.hdr, v.item_off, v.descs);
   return axk_launch_status();
 }
 
