@@ -172,7 +172,8 @@ AXK_DEV uint32_t lds_addr(const void* p) {
 // Direct HBM -> LDS load: lane l's 16 bytes at gptr land at lds_base + 16 l (lds_base wave-uniform).
 // Issued from asm on purpose: the compiler then counts none of these loads, so its own waits can only
 // over-wait, and the pipeline waits below (s_waitcnt vmcnt(n)) stay exactly as written. M0 is restored.
-AXK_DEV void lds_dma16(const void* gptr, uint32_t lds_base) {
+AXK_DEV void lds_dma16(const void* gptr, uint32_t lds_base_any) {
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
   uint32_t save;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -232,8 +233,8 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 #pragma unroll
   for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qb[s]));
 
-  // tile ti -> valid tokens and K base; a tile past the sequence end or on a page outside the pool gets
-  // nvalid = 0 and an in-bounds base
+  // tile ti -> valid tokens and K base (both wave-uniform: scalar registers); a tile past the sequence end
+  // or on a page outside the pool gets nvalid = 0 and an in-bounds base
   auto locate = [&](int ti, int& nvalid) -> const uint16_t* {
     const int lp = ti / tpp, tp = ti - lp * tpp;
     if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
@@ -242,7 +243,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       pid = j < desc.npg ? indices[desc.ibeg + j] : 0;
       asm volatile("" : "+v"(pid));  // the compiler's wait for this load stays inside this rare branch
     }
-    int page = __shfl(pid, lp & 63, 64);
+    int page = __builtin_amdgcn_readfirstlane(__shfl(pid, lp & 63, 64));
     const int valid_in_page = (lp == desc.npg - 1) ? desc.last_valid : page_size;
     nvalid = min(kTile, valid_in_page - tp * kTile);
     if (page < 0 || page >= num_pages) {
@@ -252,6 +253,18 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     }
     return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + kvh * D;
   };
+  // per-lane element offsets of this wave's loads inside a tile (token row, plane, 16-byte chunk), and the
+  // same offsets clamped to row 0 for rows past nvalid
+  int lane_tok[C::IPW];
+  int64_t lane_off[C::IPW], lane_off0[C::IPW];
+#pragma unroll
+  for (int k = 0; k < C::IPW; ++k) {
+    const int j = wave * C::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
+    const int plane = j / C::IPP, blk = j - plane * C::IPP;
+    lane_tok[k] = blk * C::RPI + lane / (D / 8);
+    lane_off0[k] = plane * plane_stride + (lane % (D / 8)) * 8;
+    lane_off[k] = lane_off0[k] + (int64_t)lane_tok[k] * row_stride;
+  }
   // this wave's share of tile ti's loads into ring buffer nb (rows past nvalid re-read row 0); returns the
   // tile's valid token count
   auto issue = [&](int ti, int nb) -> int {
@@ -260,12 +273,10 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
 #pragma unroll
     for (int k = 0; k < C::IPW; ++k) {
-      const int j = wave * C::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
+      const int j = wave * C::IPW + k;
       const int plane = j / C::IPP, blk = j - plane * C::IPP;
-      const int tok = blk * C::RPI + lane / (D / 8);
-      const uint16_t* src = kbase + plane * plane_stride + (int64_t)(tok < nrow ? tok : 0) * row_stride +
-                            (lane % (D / 8)) * 8;
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK));
+      lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
+                lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK);
     }
     return ti < ntiles ? nvalid : 0;
   };
@@ -306,12 +317,14 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one valid token
-    const float alpha = exp2f(m_run - m_new);
+    // the running max rarely moves after the first tiles: rescale O only when it did (wave-uniform test)
+    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
     float psum = 0.f;
     axk_i16x4 pb;  // B operand of O^T = V^T P^T: lane (head l16, group g) = P[head][tokens 4g .. 4g + 3]
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const float p = (4 * g + rr < nvalid) ? exp2f(st[rr] - m_new) : 0.f;
+      const float p = (4 * g + rr < nvalid) ? __builtin_amdgcn_exp2f(st[rr] - m_new) : 0.f;
       psum += p;
       pb[rr] = (short)f32_to_bf16_bits(p);
     }
@@ -326,8 +339,10 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       axk_i16x4 va;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) va[rr] = *reinterpret_cast<const short*>(col + C::row_off(4 * g + rr));
+      if (moved) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+      }
       o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
     }
   }
