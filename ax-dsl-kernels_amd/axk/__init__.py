@@ -24,3 +24,8 @@ from .attention import (  # noqa: E402
 
 __all__ += ["attention", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
             "store_paged_kv"]
+
+from . import gdn  # noqa: E402
+from .gdn import gdn_recurrent  # noqa: E402
+
+__all__ += ["gdn", "gdn_recurrent"]

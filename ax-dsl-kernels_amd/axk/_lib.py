@@ -69,6 +69,7 @@ SIGNATURES: dict[str, list] = {
     "axk_paged_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                          ctypes.c_size_t, _vp],
     "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
+    "axk_gdn_recurrent": [_vp] * 10 + [_i64] * 6 + [_vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,

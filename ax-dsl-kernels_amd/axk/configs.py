@@ -49,3 +49,28 @@ def config1(seed: int = 0):
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(1024, 16385, (16,), generator=g).tolist()
     return paged_case(lens, 16, 2, 256, 64, g)
+
+
+def gdn_inputs(bsz: int, t: int, g: torch.Generator, nk: int = 16, nv: int = 32, d: int = 128,
+               state_std: float = 0.02):
+    """Config 2 distributions: q, k, v ~ N(0,1) (the kernel L2-normalises q and k); a, b ~ N(0,1) with
+    A_log = dt_bias = 0, so g = -softplus(a) and beta = sigmoid(b); state ~ N(0, state_std) (0: zero state)."""
+    q = torch.randn(bsz, t, nk, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(bsz, t, nk, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(bsz, t, nv, d, generator=g).to(torch.bfloat16)
+    a = torch.randn(bsz, t, nv, generator=g).to(torch.bfloat16)
+    b = torch.randn(bsz, t, nv, generator=g).to(torch.bfloat16)
+    a_log = torch.zeros(nv)
+    dt_bias = torch.zeros(nv)
+    state = (torch.randn(bsz, nv, d, d, generator=g) * state_std) if state_std else torch.zeros(bsz, nv, d, d)
+    return {"q": q, "k": k, "v": v, "a": a, "b": b, "a_log": a_log, "dt_bias": dt_bias, "state": state}
+
+
+def config2_decode(seed: int = 0):
+    """Config 2 decode: B = 32, one token, 32 value / 16 key heads, d = 128, state ~ N(0, 0.02)."""
+    return gdn_inputs(32, 1, torch.Generator().manual_seed(seed))
+
+
+def config2_prefill(seed: int = 0):
+    """Config 2 prefill: B = 1, T = 4096 from a zero state (chunk 64)."""
+    return gdn_inputs(1, 4096, torch.Generator().manual_seed(seed), state_std=0.0)

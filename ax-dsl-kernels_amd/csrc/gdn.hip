@@ -1,0 +1,161 @@
+// Gated DeltaNet (GDN) recurrent step for gfx950: gate, q/k L2 norm and the delta-rule state update.
+//
+// Per (sequence b, value head h), token by token (T >= 1; T = 1 is decode):
+//   q, k  <- L2-normalised key-head vectors (x / sqrt(sum x^2 + 1e-6)), q *= DK^-0.5
+//            (l2norm_lastdim, sgl_kernel_axera/attention/gdn.py:919-931; models/.../q35_step.py:164-169)
+//   g      = -exp(A_log[h]) * softplus(a + dt_bias[h]);  beta = sigmoid(b)          (gdn_gate, gdn.py:934-949)
+//   S     <- exp(g) S;  pred = k^T S;  err = beta (v - pred);  S <- S + k err^T;  o = q^T S
+//            (gdn_recurrent_step, gdn.py:952-989)
+// Value head h reads key head h / (NV / NK) (grouped GQA order, test_gdn_attn.py:268-277).
+// The state S [DK, DV] fp32 is the kernel's whole HBM traffic: a workgroup holds its 128 x 128 tile in
+// registers (64 floats per thread, float4 loads along DV) from one read to one write, across all T tokens.
+// Arithmetic is fp32 throughout (the reference rounds the state to bf16 for its two products; the
+// difference is well inside the bf16 output tolerance and is checked against both formulations).
+#include "axk_common.h"
+#include "axk_host.h"
+
+namespace {
+
+constexpr int kDK = 128, kDV = 128;
+constexpr int kThreads = 256;
+constexpr int kColGroups = kDV / 4;               // 32 threads across DV, 4 columns each
+constexpr int kRowGroups = kThreads / kColGroups; // 8 row groups
+constexpr int kRows = kDK / kRowGroups;           // 16 state rows per thread
+
+struct GdnArgs {
+  const uint16_t* q;   // [B, T, NK, DK] bf16
+  const uint16_t* k;   // [B, T, NK, DK] bf16
+  const uint16_t* v;   // [B, T, NV, DV] bf16
+  const uint16_t* a;   // [B, T, NV] bf16
+  const uint16_t* b;   // [B, T, NV] bf16
+  const float* a_log;  // [NV]
+  const float* dt_bias;  // [NV]
+  const float* state_in;  // [B, NV, DK, DV]
+  float* state_out;       // [B, NV, DK, DV] (may alias state_in)
+  uint16_t* out;          // [B, T, NV, DV] bf16
+  int B, T, NK, NV;
+};
+
+__global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
+  __shared__ float s_k[kDK], s_q[kDK];
+  __shared__ float s_red[kRowGroups / 2][kDV];  // per-wave partial column sums
+  __shared__ float s_vec[kDV];
+  __shared__ float s_norm[4];
+
+  const int bh = blockIdx.x;
+  const int b = bh / p.NV, h = bh - (bh / p.NV) * p.NV;
+  const int kh = h / (p.NV / p.NK);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cg = tid % kColGroups, rg = tid / kColGroups;
+  const int c0 = 4 * cg, r0 = kRows * rg;
+
+  // state tile in registers: rows r0 .. r0 + 15, columns c0 .. c0 + 3
+  const float* sin = p.state_in + ((int64_t)b * p.NV + h) * kDK * kDV;
+  float4 S[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) S[r] = *reinterpret_cast<const float4*>(sin + (r0 + r) * kDV + c0);
+
+  const float a_log = p.a_log[h], dt_bias = p.dt_bias[h];
+  const float qscale = rsqrtf((float)kDK);
+
+  for (int t = 0; t < p.T; ++t) {
+    const int64_t tok = (int64_t)b * p.T + t;
+    // ---- q / k L2 norm (threads 0..127 own one element of each) ----
+    float kx = 0.f, qx = 0.f;
+    if (tid < kDK) {
+      kx = bf16_bits_to_f32(p.k[(tok * p.NK + kh) * kDK + tid]);
+      qx = bf16_bits_to_f32(p.q[(tok * p.NK + kh) * kDK + tid]);
+    }
+    float ks = wave_sum(kx * kx), qs = wave_sum(qx * qx);
+    if (lane == 0 && wave < 2) {
+      s_norm[wave] = ks;
+      s_norm[2 + wave] = qs;
+    }
+    const int64_t vh = tok * p.NV + h;
+    const float a = bf16_bits_to_f32(p.a[vh]), bb = bf16_bits_to_f32(p.b[vh]);
+    const float4 vv = make_float4(bf16_bits_to_f32(p.v[vh * kDV + c0]), bf16_bits_to_f32(p.v[vh * kDV + c0 + 1]),
+                                  bf16_bits_to_f32(p.v[vh * kDV + c0 + 2]), bf16_bits_to_f32(p.v[vh * kDV + c0 + 3]));
+    __syncthreads();
+    if (tid < kDK) {
+      const float kn = sqrtf(s_norm[0] + s_norm[1] + 1e-6f), qn = sqrtf(s_norm[2] + s_norm[3] + 1e-6f);
+      s_k[tid] = kx / kn;
+      s_q[tid] = qx / qn * qscale;
+    }
+    // ---- gate ----
+    const float g = -__expf(a_log) * softplus_f32(a + dt_bias);
+    const float decay = __expf(g);
+    const float beta = sigmoid_f32(bb);
+    __syncthreads();
+
+    // ---- S <- decay S; pred = k^T S (column sums over this thread's rows, then over row groups) ----
+    float4 pr = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const float kr = s_k[r0 + r];
+      S[r].x *= decay; S[r].y *= decay; S[r].z *= decay; S[r].w *= decay;
+      pr.x += kr * S[r].x; pr.y += kr * S[r].y; pr.z += kr * S[r].z; pr.w += kr * S[r].w;
+    }
+    // the two row groups of a wave: lanes l and l ^ 32
+    pr.x += __shfl_xor(pr.x, 32, 64); pr.y += __shfl_xor(pr.y, 32, 64);
+    pr.z += __shfl_xor(pr.z, 32, 64); pr.w += __shfl_xor(pr.w, 32, 64);
+    if (lane < 32) *reinterpret_cast<float4*>(&s_red[wave][c0]) = pr;
+    __syncthreads();
+    if (tid < kDV) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRowGroups / 2; ++w) sum += s_red[w][tid];
+      s_vec[tid] = sum;
+    }
+    __syncthreads();
+    // ---- err = beta (v - pred); S += k err^T; o = q^T S ----
+    const float4 pd = *reinterpret_cast<const float4*>(&s_vec[c0]);
+    const float4 er = make_float4(beta * (vv.x - pd.x), beta * (vv.y - pd.y), beta * (vv.z - pd.z), beta * (vv.w - pd.w));
+    float4 ov = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const float kr = s_k[r0 + r], qr = s_q[r0 + r];
+      S[r].x += kr * er.x; S[r].y += kr * er.y; S[r].z += kr * er.z; S[r].w += kr * er.w;
+      ov.x += qr * S[r].x; ov.y += qr * S[r].y; ov.z += qr * S[r].z; ov.w += qr * S[r].w;
+    }
+    ov.x += __shfl_xor(ov.x, 32, 64); ov.y += __shfl_xor(ov.y, 32, 64);
+    ov.z += __shfl_xor(ov.z, 32, 64); ov.w += __shfl_xor(ov.w, 32, 64);
+    __syncthreads();  // s_red / s_vec reuse
+    if (lane < 32) *reinterpret_cast<float4*>(&s_red[wave][c0]) = ov;
+    __syncthreads();
+    if (tid < kDV) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRowGroups / 2; ++w) sum += s_red[w][tid];
+      p.out[vh * kDV + tid] = (uint16_t)f32_to_bf16_bits(sum);
+    }
+    __syncthreads();  // s_k / s_q / s_red reuse by the next token
+  }
+
+  float* sout = p.state_out + ((int64_t)b * p.NV + h) * kDK * kDV;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) *reinterpret_cast<float4*>(sout + (r0 + r) * kDV + c0) = S[r];
+}
+
+}  // namespace
+
+extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                 const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                                 float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                                 int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream) {
+  AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
+  AXK_REQUIRE(head_k_dim == kDK && head_v_dim == kDV, AXK_E_SHAPE);
+  AXK_REQUIRE(batch > 0 && tokens > 0 && num_k_heads > 0 && num_v_heads > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(num_v_heads % num_k_heads == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(batch * num_v_heads <= INT32_MAX && tokens <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(state_in, 16) && axk_aligned(state_out, 16), AXK_E_ALIGN);
+  const size_t sbytes = (size_t)batch * num_v_heads * kDK * kDV * 4;
+  // in place is allowed (each workgroup reads its whole tile before writing it); partial overlap is not
+  AXK_REQUIRE(state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
+  const size_t obytes = (size_t)batch * tokens * num_v_heads * kDV * 2;
+  AXK_REQUIRE(!axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
+  GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
+            (int)num_v_heads};
+  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0,
+                     axk_stream(stream), p);
+  return axk_launch_status();
+}

@@ -167,7 +167,57 @@ class PagedDecodeWorkload:
                 "sample": f"full config1 op (oracle/paged_attn.py, torch fp32 CPU), median of {reps} runs"}
 
 
-WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload}
+class GdnDecodeWorkload:
+    """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
+
+    name = "gdn_decode"
+    kernel = "gdn_recurrent_kernel"
+    timing = "graph"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        c = configs.config2_decode()
+        self.host = c
+        self.d = {k: v.to(dev) for k, v in c.items()}
+        st = c["state"]
+        # algorithmic bytes: state read + write, q, k, v, out, a, b
+        self.alg_bytes = 2 * st.numel() * 4 + 2 * (c["q"].numel() + c["k"].numel() + 2 * c["v"].numel()) + \
+            2 * (c["a"].numel() + c["b"].numel())
+        self.copies = max(2, -(-ROTATE_BYTES // (st.numel() * 4)))
+        self.states = [self.d["state"].clone() for _ in range(self.copies)]
+        self.out = torch.empty_like(self.d["v"])
+        self.config = {"workload": "config2a: GDN decode B=32 NV=32 NK=16 d=128 (state in place)",
+                       "rotating_copies": self.copies}
+        self.dtype = "fp32 state, bf16 io"
+
+    def step(self, i: int) -> None:
+        from axk import gdn
+
+        d = self.d
+        s = self.states[i % self.copies]
+        gdn.gdn_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["a_log"], d["dt_bias"], s, state_out=s,
+                          output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import gdn as ogdn
+
+        c = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: ogdn.gdn_fp32(c["q"], c["k"], c["v"], c["a"], c["b"], c["a_log"],
+                                                     c["dt_bias"], c["state"]), budget_s=10.0, min_reps=2,
+                              max_reps=20)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config2a step (oracle/gdn.py gdn_fp32, torch CPU), median of {reps} runs"}
+
+
+WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
+             GdnDecodeWorkload.name: GdnDecodeWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 

@@ -167,6 +167,27 @@ int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* kv_cache,
                        int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                        int64_t num_pages, int32_t* status, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Gated DeltaNet (GDN)
+ * ------------------------------------------------------------------------------------------- */
+
+/* GDN recurrence over `tokens` consecutive tokens (1 = decode), fused with the gate and the q/k L2 norm:
+ *   q, k <- x / sqrt(sum x^2 + 1e-6), q *= head_k_dim^-0.5; g = -exp(a_log) softplus(a + dt_bias);
+ *   beta = sigmoid(b); S <- exp(g) S; S <- S + k (beta (v - k^T S))^T; o = q^T S.
+ * Replaces gdn_gate + gdn_recurrent_step of
+ * models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/gdn.py:919-989 (l2norm 919-931, gate 934-949)
+ * with the golden of models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:259-296. Value head h uses key head
+ * h / (num_v_heads / num_k_heads).
+ *   q, k  bf16 [batch, tokens, num_k_heads, 128];  v bf16 [batch, tokens, num_v_heads, 128]
+ *   a, b  bf16 [batch, tokens, num_v_heads];        a_log, dt_bias f32 [num_v_heads]
+ *   state_in / state_out f32 [batch, num_v_heads, 128, 128] (state_out == state_in: in place)
+ *   out   bf16 [batch, tokens, num_v_heads, 128]
+ * head_k_dim = head_v_dim = 128. */
+int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                      const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                      float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                      int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
