@@ -29,3 +29,8 @@ from . import gdn  # noqa: E402
 from .gdn import gdn_recurrent  # noqa: E402
 
 __all__ += ["gdn", "gdn_recurrent"]
+
+from . import moe  # noqa: E402
+from .moe import moe_decode, moe_experts, moe_route, moe_workspace  # noqa: E402
+
+__all__ += ["moe", "moe_decode", "moe_experts", "moe_route", "moe_workspace"]

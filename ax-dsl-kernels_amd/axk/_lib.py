@@ -70,11 +70,16 @@ SIGNATURES: dict[str, list] = {
                          ctypes.c_size_t, _vp],
     "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "axk_gdn_recurrent": [_vp] * 10 + [_i64] * 6 + [_vp],
+    "axk_moe_workspace_size": [_i64] * 6,
+    "axk_moe_route": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "axk_moe_experts": [_vp] * 16 + [_i64] * 6 + [_vp, ctypes.c_size_t, _vp],
+    "axk_moe_decode": [_vp] * 18 + [_i64] * 6 + [_i32, _vp, ctypes.c_size_t, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,
     "axk_status_string": ctypes.c_char_p,
     "axk_paged_decode_workspace_size": ctypes.c_size_t,
+    "axk_moe_workspace_size": ctypes.c_size_t,
 }
 
 

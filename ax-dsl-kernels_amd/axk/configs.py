@@ -74,3 +74,29 @@ def config2_decode(seed: int = 0):
 def config2_prefill(seed: int = 0):
     """Config 2 prefill: B = 1, T = 4096 from a zero state (chunk 64)."""
     return gdn_inputs(1, 4096, torch.Generator().manual_seed(seed), state_std=0.0)
+
+
+def moe_weights(g: torch.Generator, hidden: int = 2048, experts: int = 256, inter: int = 512,
+                shared_inter: int = 512, router_std: float = 0.02):
+    """Config 3 weights: MXFP4 experts as config 0 (nibbles uniform, scale bytes 119..123), bf16 router and
+    shared-expert gate ~ N(0, router_std). Draw order: router, w_shg, shared gate / up / down, e_gw/e_gs,
+    e_dw/e_ds."""
+    w = {}
+    w["w_router"] = (torch.randn(experts, hidden, generator=g) * router_std).to(torch.bfloat16)
+    w["w_shg"] = (torch.randn(hidden, generator=g) * router_std).to(torch.bfloat16)
+    w["w_gate"], w["s_gate"] = mxfp4_weight(shared_inter, hidden, g)
+    w["w_up"], w["s_up"] = mxfp4_weight(shared_inter, hidden, g)
+    w["w_down"], w["s_down"] = mxfp4_weight(hidden, shared_inter, g)
+    w["e_gw"], w["e_gs"] = mxfp4_weight(2 * inter, hidden, g, lead=(experts,))
+    w["e_dw"], w["e_ds"] = mxfp4_weight(hidden, inter, g, lead=(experts,))
+    return w
+
+
+def config3(tokens: int = 32, seed: int = 0):
+    """Config 3: MoE layer, hidden 2048, 256 routed experts (inter 512) + 1 shared expert (inter 512), top-8,
+    activations ~ N(0,1) at `tokens` (32 = decode, 4096 = prefill); x_res ~ N(0,1) residual."""
+    g = torch.Generator().manual_seed(seed)
+    w = moe_weights(g)
+    h2 = torch.randn(tokens, 2048, generator=g).to(torch.bfloat16)
+    x_res = torch.randn(tokens, 2048, generator=g).to(torch.bfloat16)
+    return {"h2": h2, "x_res": x_res, "weights": w, "top_k": 8}

@@ -1,0 +1,479 @@
+// MoE layer with MXFP4 experts for gfx950: router top-K, shared expert with sigmoid gate, routed SwiGLU
+// experts, combine. Semantics of moe_full (models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:797-853):
+//   logits = h2 W_router^T (fp32); p = softmax(logits); top-K by value (ties: lower expert id), rw = p / sum p
+//   shared: act = bf16(silu(bf16(h2 Wg^T)) * bf16(h2 Wu^T)); sh = act Wd^T (fp32); gate = sigmoid(h2 . w_shg)
+//   base = x_res + gate * sh;  out = bf16(base + sum_k rw_k * down_k(silu(gate_k) * up_k))
+// The reference also rounds `base` to bf16 before the sum (the layer kernel's bf16 `out`); here it stays fp32
+// so the output is rounded once: a value within half an ulp of a bf16 midpoint would otherwise flip by one
+// ulp of |base| between any two summation orders.
+// Routed experts are planar MXFP4 tensors: gate-up e_gw [E, 2F, H/2] (gate rows, then up rows), e_gs
+// [E, 2F, H/32]; down e_dw [E, H, F/2], e_ds [E, H, F/32] (models/qwen35_35b_a3b/qwen35_35b_a3b.manifest.json).
+//
+// Kernels (decode sizes: tokens x top_k <= kMaxPairs):
+//   route   — one wave per token: softmax, top-K, renormalised weights
+//   group   — one workgroup: the (token, slot) pairs grouped by expert in (token, slot) order (deterministic
+//             counting sort: one thread per expert scans the pairs), and the list of active experts
+//   gateup  — one workgroup per (active expert or the shared expert, 16 intermediate rows): the gate and up
+//             tiles stream as MXFP4 over the expert's gathered tokens, SwiGLU in the epilogue
+//   down    — one workgroup per (expert, 64 hidden rows): act x Wd^T, scaled by the pair's routing weight
+//   combine — one workgroup per token: shared gate, residual, sum over the token's K experts in slot order
+// Every expert's weights are read once per call, whatever the number of its tokens.
+#include "axk_common.h"
+#include "axk_host.h"
+#include "axk_mx_tile.h"
+
+namespace {
+
+using axk::WF_MXFP4;
+
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 32;  // <= 64: lane k of the routing wave keeps selection k
+constexpr int kMaxPairs = 8192;
+constexpr int kMaxTokensPerChunk = 32;  // M rows per pass (2 MFMA tiles)
+
+struct MoeWs {
+  int* counts;      // [E]
+  int* offsets;     // [E + 1]
+  int* active_e;    // [E]
+  int* active_off;  // [E]
+  int* active_cnt;  // [E]
+  int* n_active;    // [1]
+  int* pair_pos;    // [P] sorted row of pair p = t * K + k
+  int* row_tok;     // [P] token of sorted row
+  float* row_w;     // [P] routing weight of sorted row
+  uint16_t* act;    // [P, F] bf16 routed activations (sorted rows)
+  uint16_t* act_sh; // [T, Fs] bf16 shared-expert activations
+  float* y;         // [P, H] fp32 routed outputs x routing weight
+  float* y_sh;      // [T, H] fp32 shared-expert output
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs, size_t* off) {
+  const int64_t P = T * K;
+  size_t o = 0;
+  const size_t sizes[13] = {(size_t)E * 4,     (size_t)(E + 1) * 4, (size_t)E * 4,      (size_t)E * 4,
+                            (size_t)E * 4,     4,                   (size_t)P * 4,      (size_t)P * 4,
+                            (size_t)P * 4,     (size_t)P * F * 2,   (size_t)T * Fs * 2, (size_t)P * H * 4,
+                            (size_t)T * H * 4};
+  for (int i = 0; i < 13; ++i) {
+    off[i] = o;
+    o = align256(o + sizes[i]);
+  }
+  return o;
+}
+
+MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs) {
+  size_t off[13];
+  moe_ws_layout(T, H, E, K, F, Fs, off);
+  unsigned char* b = reinterpret_cast<unsigned char*>(ws);
+  return {reinterpret_cast<int*>(b + off[0]),       reinterpret_cast<int*>(b + off[1]),
+          reinterpret_cast<int*>(b + off[2]),       reinterpret_cast<int*>(b + off[3]),
+          reinterpret_cast<int*>(b + off[4]),       reinterpret_cast<int*>(b + off[5]),
+          reinterpret_cast<int*>(b + off[6]),       reinterpret_cast<int*>(b + off[7]),
+          reinterpret_cast<float*>(b + off[8]),     reinterpret_cast<uint16_t*>(b + off[9]),
+          reinterpret_cast<uint16_t*>(b + off[10]), reinterpret_cast<float*>(b + off[11]),
+          reinterpret_cast<float*>(b + off[12])};
+}
+
+// ---------------------------------------------------------------------------------------------
+// route: one wave per token
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int K,
+                                                        int norm_topk, int32_t* __restrict__ ids,
+                                                        float* __restrict__ wts) {
+  constexpr int V = kMaxExperts / 64;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* lg = logits + (int64_t)t * E;
+  float x[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int e = i * 64 + lane;
+    x[i] = e < E ? lg[e] : -INFINITY;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < V; ++i) mx = fmaxf(mx, x[i]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum += (i * 64 + lane < E) ? __expf(x[i] - mx) : 0.f;
+  sum = wave_sum(sum);
+  const float inv = 1.0f / sum;
+  // top-K on the logits (the softmax is monotonic): descending value, ties to the lower expert id
+  unsigned taken = 0u;  // bit i: x[i] already selected
+  float myp = 0.f;       // lane k keeps the k-th selection
+  int myid = 0;
+  float psum = 0.f;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int e = i * 64 + lane;
+      if (e < E && !(taken >> i & 1u) && (x[i] > bv || (x[i] == bv && e < bi))) {
+        bv = x[i];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {  // butterfly: every lane ends with the same winner
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    const float p = __expf(bv - mx) * inv;
+    if (lane == k) {
+      myp = p;
+      myid = bi;
+    }
+    psum += p;
+  }
+  if (lane < K) {
+    ids[(int64_t)t * K + lane] = myid;
+    wts[(int64_t)t * K + lane] = norm_topk ? myp / psum : myp;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// group: one workgroup; pairs grouped by expert, stable in (token, slot) order
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restrict__ ids,
+                                                        const float* __restrict__ wts, int T, int E, int K,
+                                                        MoeWs w) {
+  __shared__ int s_ids[kMaxPairs];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts + 1];
+  __shared__ int s_act[kMaxExperts + 1];
+  const int P = T * K;
+  const int tid = threadIdx.x;
+  for (int p = tid; p < P; p += blockDim.x) s_ids[p] = ids[p];
+  for (int e = tid; e < E; e += blockDim.x) s_cnt[e] = 0;
+  __syncthreads();
+  // counts: one thread per expert scans the pairs (broadcast LDS reads; no atomics)
+  for (int e = tid; e < E; e += blockDim.x) {
+    int c = 0;
+    for (int p = 0; p < P; ++p) c += s_ids[p] == e;
+    s_cnt[e] = c;
+  }
+  __syncthreads();
+  // exclusive scans of counts and of (count > 0)
+  if (tid == 0) {
+    int run = 0, runa = 0;
+    for (int e = 0; e < E; ++e) {
+      s_off[e] = run;
+      s_act[e] = runa;
+      run += s_cnt[e];
+      runa += s_cnt[e] > 0;
+    }
+    s_off[E] = run;
+    s_act[E] = runa;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int c = s_cnt[e], o = s_off[e];
+    w.counts[e] = c;
+    w.offsets[e] = o;
+    if (c > 0) {
+      const int j = s_act[e];
+      w.active_e[j] = e;
+      w.active_off[j] = o;
+      w.active_cnt[j] = c;
+      int r = 0;
+      for (int p = 0; p < P; ++p)
+        if (s_ids[p] == e) {
+          const int pos = o + r++;
+          w.pair_pos[p] = pos;
+          w.row_tok[pos] = p / K;
+          w.row_w[pos] = wts[p];
+        }
+    }
+  }
+  if (tid == 0) {
+    w.offsets[E] = s_off[E];
+    *w.n_active = s_act[E];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// gate-up + SwiGLU: workgroup (slot, 16-row tile); slot < max_slots: routed (active expert), else shared
+// ---------------------------------------------------------------------------------------------
+struct GateUpArgs {
+  const uint16_t* h2;  // [T, H]
+  const uint8_t *e_gw, *e_gs;
+  const uint8_t *sg_w, *sg_s, *su_w, *su_s;  // shared gate / up (nullable: no shared expert)
+  int T, H, F, Fs, max_slots, ntile;
+  MoeWs w;
+};
+
+constexpr int kGuWaves = 4;
+
+__global__ __launch_bounds__(64 * kGuWaves) void moe_gateup_kernel(GateUpArgs a) {
+  __shared__ float red[kGuWaves][2][2][4][64];  // [wave][gate/up][M tile][r][lane]
+  const int slot = blockIdx.x / a.ntile, tile = blockIdx.x - (blockIdx.x / a.ntile) * a.ntile;
+  const bool shared = slot == a.max_slots;
+  int cnt, row0;
+  const uint8_t *gw, *gs, *uw, *us;
+  int Fo;  // intermediate size of this slot
+  int64_t e = 0;
+  if (shared) {
+    if (!a.sg_w) return;
+    cnt = a.T;
+    row0 = 0;
+    Fo = a.Fs;
+    gw = a.sg_w; gs = a.sg_s; uw = a.su_w; us = a.su_s;
+  } else {
+    if (slot >= *a.w.n_active) return;
+    e = a.w.active_e[slot];
+    cnt = a.w.active_cnt[slot];
+    row0 = a.w.active_off[slot];
+    Fo = a.F;
+    const int64_t rows = 2 * (int64_t)a.F;
+    gw = a.e_gw + e * rows * (a.H / 2);
+    gs = a.e_gs + e * rows * (a.H / 32);
+    uw = gw + (int64_t)a.F * (a.H / 2);
+    us = gs + (int64_t)a.F * (a.H / 32);
+  }
+  const int n0 = tile * 16;
+  if (n0 >= Fo) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15;
+  const int64_t n = n0 + nl;
+  const bool nvalid = n < Fo;
+  for (int m0 = 0; m0 < cnt; m0 += kMaxTokensPerChunk) {
+    const uint16_t* xrow[2];
+    bool mvalid[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int m = m0 + 16 * t + nl;
+      mvalid[t] = m < cnt;
+      const int tok = mvalid[t] ? (shared ? m : a.w.row_tok[row0 + m]) : 0;
+      xrow[t] = a.h2 + (int64_t)tok * a.H;
+    }
+    axk_f32x4 accg[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
+    axk_f32x4 accu[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
+    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, gw, gs, n, nvalid, a.H, wave, kGuWaves, accg);
+    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, uw, us, n, nvalid, a.H, wave, kGuWaves, accu);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        red[wave][0][t][r][lane] = accg[t][r];
+        red[wave][1][t][r][lane] = accu[t][r];
+      }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 2 * 256; idx += blockDim.x) {
+      const int t = idx >> 8, r = (idx >> 6) & 3, l = idx & 63;
+      float gsum = 0.f, usum = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kGuWaves; ++wv) {
+        gsum += red[wv][0][t][r][l];
+        usum += red[wv][1][t][r][l];
+      }
+      const int m = m0 + 16 * t + 4 * (l >> 4) + r;
+      const int nn = n0 + (l & 15);
+      if (m < cnt && nn < Fo) {
+        const float gv = round_bf16(gsum), uv = round_bf16(usum);  // projections rounded to bf16
+        const uint16_t act = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+        if (shared)
+          a.w.act_sh[(int64_t)m * a.Fs + nn] = act;
+        else
+          a.w.act[(int64_t)(row0 + m) * a.F + nn] = act;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// down: workgroup (slot, 64 hidden rows); wave w owns rows 16w .. 16w + 15 over the full K = F
+// ---------------------------------------------------------------------------------------------
+struct DownArgs {
+  const uint8_t *e_dw, *e_ds;
+  const uint8_t *sd_w, *sd_s;
+  int T, H, F, Fs, max_slots, ntile;
+  MoeWs w;
+};
+
+__global__ __launch_bounds__(256) void moe_down_kernel(DownArgs a) {
+  const int slot = blockIdx.x / a.ntile, tile = blockIdx.x - (blockIdx.x / a.ntile) * a.ntile;
+  const bool shared = slot == a.max_slots;
+  int cnt, row0, K;
+  const uint8_t *dw, *ds;
+  const uint16_t* act;
+  if (shared) {
+    if (!a.sd_w) return;
+    cnt = a.T;
+    row0 = 0;
+    K = a.Fs;
+    dw = a.sd_w; ds = a.sd_s;
+    act = a.w.act_sh;
+  } else {
+    if (slot >= *a.w.n_active) return;
+    const int64_t e = a.w.active_e[slot];
+    cnt = a.w.active_cnt[slot];
+    row0 = a.w.active_off[slot];
+    K = a.F;
+    dw = a.e_dw + e * (int64_t)a.H * (a.F / 2);
+    ds = a.e_ds + e * (int64_t)a.H * (a.F / 32);
+    act = a.w.act + (int64_t)row0 * a.F;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15;
+  const int n0 = tile * 64 + 16 * wave;
+  const int64_t n = n0 + nl;
+  const bool nvalid = n < a.H;
+  for (int m0 = 0; m0 < cnt; m0 += kMaxTokensPerChunk) {
+    const uint16_t* xrow[2];
+    bool mvalid[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int m = m0 + 16 * t + nl;
+      mvalid[t] = m < cnt;
+      xrow[t] = act + (int64_t)(mvalid[t] ? m : 0) * K;
+    }
+    axk_f32x4 acc[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
+    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, dw, ds, n, nvalid, K, 0, 1, acc);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * t + 4 * (lane >> 4) + r;
+        const int64_t nn = n0 + (lane & 15);
+        if (m < cnt && nn < a.H) {
+          if (shared)
+            a.w.y_sh[(int64_t)m * a.H + nn] = acc[t][r];
+          else
+            a.w.y[(int64_t)(row0 + m) * a.H + nn] = acc[t][r] * a.w.row_w[row0 + m];
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// combine: one workgroup per token
+// ---------------------------------------------------------------------------------------------
+struct CombineArgs {
+  const uint16_t* h2;     // [T, H]
+  const uint16_t* x_res;  // [T, H] or null
+  const uint16_t* w_shg;  // [H] or null (gate = 1)
+  int has_shared, T, H, K;
+  MoeWs w;
+  uint16_t* out;  // [T, H]
+};
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
+  __shared__ float s_part[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* hrow = a.h2 + (int64_t)t * a.H;
+  float gate = 1.0f;
+  if (a.has_shared && a.w_shg) {
+    float d = 0.f;
+    for (int i = tid; i < a.H; i += blockDim.x) d += bf16_bits_to_f32(hrow[i]) * bf16_bits_to_f32(a.w_shg[i]);
+    d = wave_sum(d);
+    if (lane == 0) s_part[wave] = d;
+    __syncthreads();
+    gate = sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]);
+  }
+  int pos[kMaxTopK];
+  for (int k = 0; k < a.K; ++k) pos[k] = a.w.pair_pos[(int64_t)t * a.K + k];
+  for (int i = tid; i < a.H; i += blockDim.x) {
+    float base = a.x_res ? bf16_bits_to_f32(a.x_res[(int64_t)t * a.H + i]) : 0.f;
+    if (a.has_shared) base += gate * a.w.y_sh[(int64_t)t * a.H + i];
+    float acc = base;
+    for (int k = 0; k < a.K; ++k) acc += a.w.y[(int64_t)pos[k] * a.H + i];
+    a.out[(int64_t)t * a.H + i] = (uint16_t)f32_to_bf16_bits(acc);
+  }
+}
+
+struct MoeDims {
+  int64_t T, H, E, K, F, Fs;
+};
+
+int check_dims(const MoeDims& d) {
+  AXK_REQUIRE(d.T > 0 && d.H > 0 && d.E > 0 && d.K > 0 && d.F > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(d.E <= kMaxExperts && d.K <= kMaxTopK && d.K <= d.E, AXK_E_SHAPE);
+  AXK_REQUIRE(d.T * d.K <= kMaxPairs, AXK_E_SHAPE);
+  AXK_REQUIRE(d.H % 64 == 0 && d.F % 32 == 0 && d.Fs % 32 == 0 && d.Fs >= 0, AXK_E_SHAPE);
+  AXK_REQUIRE(d.H <= INT32_MAX && d.F <= INT32_MAX, AXK_E_SHAPE);
+  return AXK_OK;
+}
+
+}  // namespace
+
+extern "C" size_t axk_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
+                                         int64_t inter, int64_t shared_inter) {
+  if (check_dims({tokens, hidden, num_experts, top_k, inter, shared_inter}) != AXK_OK) return 0;
+  size_t off[13];
+  return moe_ws_layout(tokens, hidden, num_experts, top_k, inter, shared_inter, off);
+}
+
+extern "C" int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk_weights, int64_t tokens,
+                             int64_t num_experts, int64_t top_k, int norm_topk_prob, axk_stream_t stream) {
+  AXK_REQUIRE(logits && topk_ids && topk_weights, AXK_E_NULL);
+  AXK_REQUIRE(tokens > 0 && num_experts > 0 && num_experts <= kMaxExperts, AXK_E_SHAPE);
+  AXK_REQUIRE(top_k > 0 && top_k <= kMaxTopK && top_k <= num_experts && tokens <= INT32_MAX, AXK_E_SHAPE);
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, axk_stream(stream), logits,
+                     (int)tokens, (int)num_experts, (int)top_k, norm_topk_prob, topk_ids, topk_weights);
+  return axk_launch_status();
+}
+
+extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg,
+                               const uint8_t* sh_gate_w, const uint8_t* sh_gate_s, const uint8_t* sh_up_w,
+                               const uint8_t* sh_up_s, const uint8_t* sh_down_w, const uint8_t* sh_down_s,
+                               const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds,
+                               const int32_t* topk_ids, const float* topk_weights, uint16_t* out, int64_t tokens,
+                               int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
+                               int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(h2 && e_gw && e_gs && e_dw && e_ds && topk_ids && topk_weights && out, AXK_E_NULL);
+  const bool has_shared = sh_gate_w != nullptr;
+  AXK_REQUIRE(!has_shared || (sh_gate_s && sh_up_w && sh_up_s && sh_down_w && sh_down_s), AXK_E_NULL);
+  const MoeDims d{tokens, hidden, num_experts, top_k, inter, has_shared ? shared_inter : 0};
+  const int rc = check_dims(d);
+  if (rc != AXK_OK) return rc;
+  AXK_REQUIRE(!has_shared || shared_inter > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(h2, 16) && axk_aligned(e_gw, 16) && axk_aligned(e_dw, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(!has_shared || (axk_aligned(sh_gate_w, 16) && axk_aligned(sh_up_w, 16) && axk_aligned(sh_down_w, 16)),
+              AXK_E_ALIGN);
+  const size_t need = axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, d.Fs);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const size_t obytes = (size_t)tokens * hidden * 2;
+  AXK_REQUIRE(!axk_overlap(out, obytes, h2, obytes) && !axk_overlap(out, obytes, workspace, workspace_bytes),
+              AXK_E_ALIAS);
+  hipStream_t st = axk_stream(stream);
+  const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, d.Fs);
+  const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, F = (int)inter, Fs = (int)d.Fs;
+  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
+  const int max_slots = E < T * K ? E : T * K;
+  const int fmax = F > Fs ? F : Fs;
+  GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, max_slots, (fmax + 15) / 16, w};
+  hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((max_slots + 1) * ga.ntile)), dim3(64 * kGuWaves), 0, st,
+                     ga);
+  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, (H + 63) / 64, w};
+  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((max_slots + 1) * da.ntile)), dim3(256), 0, st, da);
+  CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, st, ca);
+  return axk_launch_status();
+}
+
+extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router,
+                              const uint16_t* w_shg, const uint8_t* sh_gate_w, const uint8_t* sh_gate_s,
+                              const uint8_t* sh_up_w, const uint8_t* sh_up_s, const uint8_t* sh_down_w,
+                              const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
+                              const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
+                              int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden,
+                              int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
+                              int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(w_router && logits, AXK_E_NULL);
+  int rc = axk_bf16_gemm(h2, hidden, w_router, nullptr, logits, AXK_DT_F32, tokens, num_experts, hidden, stream);
+  if (rc != AXK_OK) return rc;
+  rc = axk_moe_route(logits, topk_ids, topk_weights, tokens, num_experts, top_k, norm_topk_prob, stream);
+  if (rc != AXK_OK) return rc;
+  return axk_moe_experts(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
+                         e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
+                         shared_inter, workspace, workspace_bytes, stream);
+}

@@ -15,69 +15,16 @@
 // gemm.py:119-181 (scaled GEMM), q35_mx_build.py:100-115 (proj_mx).
 #include "axk_common.h"
 #include "axk_host.h"
+#include "axk_mx_tile.h"
 
 namespace {
 
-enum WeightFmt { WF_MXFP4 = 0, WF_FP8 = 1, WF_BF16 = 2 };
-
-template <int F>
-struct WUnit;
-
-// MXFP4: codes [N, K/2] (low nibble = even k), E8M0 scales [N, K/32].
-template <>
-struct WUnit<WF_MXFP4> {
-  static constexpr int V = 32;
-  static constexpr int STEPS = 4;
-  static AXK_DEV uint4 load(const uint8_t* w, int64_t n, int64_t K, int64_t kb) {
-    return *reinterpret_cast<const uint4*>(w + n * (K >> 1) + (kb >> 1));
-  }
-  static AXK_DEV float scale(const uint8_t* s, int64_t n, int64_t K, int64_t kb) {
-    return e8m0_to_f32(s[n * (K >> 5) + (kb >> 5)]);
-  }
-  static AXK_DEV axk_bf16x8 conv(const uint4& q, int step, float sc) {
-    const uint32_t word = step == 0 ? q.x : step == 1 ? q.y : step == 2 ? q.z : q.w;
-    return fp4x8_to_bf16x8(word, sc);
-  }
-};
-
-// FP8 E4M3: [N, K] bytes; the per-channel scale is applied in the epilogue.
-template <>
-struct WUnit<WF_FP8> {
-  static constexpr int V = 16;
-  static constexpr int STEPS = 2;
-  static AXK_DEV uint4 load(const uint8_t* w, int64_t n, int64_t K, int64_t kb) {
-    return *reinterpret_cast<const uint4*>(w + n * K + kb);
-  }
-  static AXK_DEV float scale(const uint8_t*, int64_t, int64_t, int64_t) { return 1.0f; }
-  static AXK_DEV axk_bf16x8 conv(const uint4& q, int step, float) {
-    const uint32_t w0 = step == 0 ? q.x : q.z, w1 = step == 0 ? q.y : q.w;
-    axk_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
-    axk_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
-    axk_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
-    axk_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
-    axk_bf16x8 r;
-    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-    return r;
-  }
-};
-
-// bf16: [N, K] (uint16 bits).
-template <>
-struct WUnit<WF_BF16> {
-  static constexpr int V = 8;
-  static constexpr int STEPS = 1;
-  static AXK_DEV uint4 load(const uint8_t* w, int64_t n, int64_t K, int64_t kb) {
-    return *reinterpret_cast<const uint4*>(w + (n * K + kb) * 2);
-  }
-  static AXK_DEV float scale(const uint8_t*, int64_t, int64_t, int64_t) { return 1.0f; }
-  static AXK_DEV axk_bf16x8 conv(const uint4& q, int, float) {
-    return *reinterpret_cast<const axk_bf16x8*>(&q);
-  }
-};
+using axk::WF_BF16;
+using axk::WF_FP8;
+using axk::WF_MXFP4;
+using axk::WUnit;
 
 constexpr int kMaxWaves = 16;
-constexpr int kUnroll = 2;
 
 // One workgroup: output channels [16*blockIdx.x, +16) x rows [32*blockIdx.y... ) in MT tiles of 16.
 // Lane l: N column nl = l % 16, K group g = l / 16. Chunk c covers K [c*4V, (c+1)*4V); the lane's
@@ -90,12 +37,10 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
                                                           const float* __restrict__ col_scale,
                                                           const float* __restrict__ bias, void* __restrict__ out,
                                                           int out_f32, int M, int N, int64_t K) {
-  using U = WUnit<F>;
-  constexpr int CH = 4 * U::V;
   __shared__ float red[kMaxWaves * MT * 4 * 64];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
-  const int nl = lane & 15, g = lane >> 4;
+  const int nl = lane & 15;
   const int64_t n = (int64_t)blockIdx.x * 16 + nl;
   const int m0 = blockIdx.y * 16 * MT;
   const bool nvalid = n < N;
@@ -112,38 +57,7 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
   axk_f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int64_t NC = (K + CH - 1) / CH;
-  for (int64_t c0 = wave; c0 < NC; c0 += (int64_t)nwaves * kUnroll) {
-    uint4 q[kUnroll];
-    float sc[kUnroll];
-    int64_t kb[kUnroll];
-    bool kv[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t c = c0 + (int64_t)u * nwaves;
-      kb[u] = c * CH + g * U::V;
-      kv[u] = c < NC && kb[u] < K;
-      q[u] = make_uint4(0u, 0u, 0u, 0u);
-      sc[u] = 1.0f;
-      if (nvalid && kv[u]) {
-        q[u] = U::load(w, n, K, kb[u]);
-        sc[u] = U::scale(wscale, n, K, kb[u]);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-#pragma unroll
-      for (int s = 0; s < U::STEPS; ++s) {
-        const axk_bf16x8 b = U::conv(q[u], s, sc[u]);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const axk_bf16x8 a = (mvalid[t] && kv[u]) ? load_bf16x8(xrow[t] + kb[u] + 8 * s) : zero_bf16x8();
-          acc[t] = mfma_bf16_16x16x32(a, b, acc[t]);
-        }
-      }
-    }
-  }
+  axk::mx_tile_accum<F, MT>(xrow, mvalid, w, wscale, n, nvalid, K, wave, nwaves, acc);
 
 #pragma unroll
   for (int t = 0; t < MT; ++t)

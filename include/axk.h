@@ -188,6 +188,53 @@ int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
                       float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
                       int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * MoE with MXFP4 experts (router top-K, shared expert with sigmoid gate, routed SwiGLU experts)
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes for axk_moe_experts / axk_moe_decode (0 = unsupported shape: tokens x top_k <= 8192,
+ * num_experts <= 1024, top_k <= 32, hidden % 64 == 0, inter % 32 == 0). */
+size_t axk_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
+                              int64_t shared_inter);
+
+/* Router top-K on fp32 logits [tokens, num_experts]: p = softmax(logits); the top_k experts by logit
+ * (descending, ties to the lower expert id); weights = p / sum(p) when norm_topk_prob, else p.
+ * Replaces route() of models/qwen35_35b_a3b/src/70b0fbc/q35_moe.py:293-297 and the softmax / topk /
+ * renormalisation of q35_layer_mc.py:825-829 (tie rule: q35_layer_mc.py:1461-1466).
+ * topk_ids i32 [tokens, top_k]; topk_weights f32 [tokens, top_k]. */
+int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t num_experts,
+                  int64_t top_k, int norm_topk_prob, axk_stream_t stream);
+
+/* Experts half of the MoE layer for given routing (moe_full, q35_layer_mc.py:797-853; moe_pre +
+ * moe_experts_gu, q35_moe.py:96-137):
+ *   act_s = bf16(silu(bf16(h2 Wsg^T)) * bf16(h2 Wsu^T)); sh = act_s Wsd^T; gate = sigmoid(h2 . w_shg)
+ *   base = x_res + gate * sh;  out = bf16(base + sum_k w_k * down_e(bf16(silu(gate_e) * up_e)))
+ *   (fp32 throughout; the reference rounds base to bf16 first, a difference of at most one bf16 ulp of base)
+ *   h2, x_res (nullable) bf16 [tokens, hidden]; w_shg bf16 [hidden] (nullable: gate 1)
+ *   shared expert (sh_* all NULL: none): gate / up MXFP4 [shared_inter, hidden/2] + [.., hidden/32],
+ *     down [hidden, shared_inter/2] + [hidden, shared_inter/32]
+ *   e_gw u8 [E, 2*inter, hidden/2] (gate rows, then up rows), e_gs u8 [E, 2*inter, hidden/32],
+ *   e_dw u8 [E, hidden, inter/2], e_ds u8 [E, hidden, inter/32]
+ *   topk_ids i32 / topk_weights f32 [tokens, top_k]; out bf16 [tokens, hidden]. */
+int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg, const uint8_t* sh_gate_w,
+                    const uint8_t* sh_gate_s, const uint8_t* sh_up_w, const uint8_t* sh_up_s,
+                    const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
+                    const uint8_t* e_dw, const uint8_t* e_ds, const int32_t* topk_ids, const float* topk_weights,
+                    uint16_t* out, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
+                    int64_t inter, int64_t shared_inter, void* workspace, size_t workspace_bytes,
+                    axk_stream_t stream);
+
+/* The whole decode MoE layer: logits = h2 w_router^T (bf16 router [E, hidden], fp32 logits out), then
+ * axk_moe_route and axk_moe_experts. Outputs out, logits, topk_ids, topk_weights (the layer kernel's
+ * h2 / logits_out / topk_i / topk_v IO of q35_layer_mc.py:437-449). */
+int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router, const uint16_t* w_shg,
+                   const uint8_t* sh_gate_w, const uint8_t* sh_gate_s, const uint8_t* sh_up_w,
+                   const uint8_t* sh_up_s, const uint8_t* sh_down_w, const uint8_t* sh_down_s,
+                   const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds,
+                   uint16_t* out, float* logits, int32_t* topk_ids, float* topk_weights, int64_t tokens,
+                   int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
+                   int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

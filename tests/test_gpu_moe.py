@@ -1,0 +1,75 @@
+"""GPU parity of the MoE layer (router, top-K, shared + routed MXFP4 SwiGLU experts) against the oracle.
+
+Bar: top-K ids bit-exact against a stable descending sort of the kernel's own logits; routing weights and
+logits at fp32 tolerance; bf16 outputs within rel 2e-2 / abs 1e-2 of the oracle on the same routing.
+"""
+import pytest
+import torch
+
+from axk import configs, moe
+from oracle import moe as omoe
+
+pytestmark = pytest.mark.gpu
+TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def _dev_w(w, dev):
+    return {n: v.to(dev) for n, v in w.items()}
+
+
+def _check_layer(c, dev, norm=True):
+    h2, x, w, k = c["h2"], c["x_res"], c["weights"], c["top_k"]
+    out, logits, ids, wts = moe.moe_decode(h2.to(dev), _dev_w(w, dev), top_k=k,
+                                           x_res=None if x is None else x.to(dev), norm_topk_prob=norm)
+    out, logits, ids, wts = out.cpu(), logits.cpu(), ids.cpu(), wts.cpu()
+    ref_logits = h2.float() @ w["w_router"].float().T
+    torch.testing.assert_close(logits, ref_logits, rtol=1e-4, atol=1e-4)
+    sids, swts = omoe.route(logits, k, norm)  # the host rule on the kernel's own logits
+    assert torch.equal(ids, sids), "top-K ids differ from the stable sort of the kernel's logits"
+    torch.testing.assert_close(wts, swts, rtol=1e-5, atol=1e-6)
+    ref, *_ = omoe.moe_layer(h2, w, k, x_res=x, norm=norm, ids=ids, wts=wts, round_base=False)
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)
+    # the reference's rounding schedule (base rounded to bf16 first) differs by at most one ulp of |base|
+    # plus the same tolerance
+    ref_sched, *_ = omoe.moe_layer(h2, w, k, x_res=x, norm=norm, ids=ids, wts=wts, round_base=True)
+    slack = omoe.base_ulp(h2, w, x) + TOL["atol"] + TOL["rtol"] * ref_sched.float().abs()
+    assert ((out.float() - ref_sched.float()).abs() <= slack).all()
+    return out
+
+
+@pytest.mark.parametrize("t,h,e,f,fs,k", [(1, 64, 8, 32, 32, 2), (5, 256, 16, 64, 96, 4), (33, 128, 64, 32, 64, 8),
+                                          (7, 192, 40, 160, 0, 6)])
+def test_moe_small_shapes(dev, t, h, e, f, fs, k):
+    g = torch.Generator().manual_seed(t + h + e)
+    w = configs.moe_weights(g, hidden=h, experts=e, inter=f, shared_inter=max(fs, 32), router_std=0.5)
+    if fs == 0:  # no shared expert
+        for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down", "w_shg"):
+            w.pop(n)
+    c = {"h2": torch.randn(t, h, generator=g).to(torch.bfloat16), "x_res": torch.randn(t, h, generator=g).to(torch.bfloat16),
+         "weights": w, "top_k": k}
+    print(f"case t={t} h={h} e={e} f={f} fs={fs} k={k}", flush=True)
+    _check_layer(c, dev)
+
+
+def test_moe_config3_decode_and_determinism(dev):
+    c = configs.config3(32)
+    out = _check_layer(c, dev)
+    again, *_ = moe.moe_decode(c["h2"].to(dev), _dev_w(c["weights"], dev), top_k=8, x_res=c["x_res"].to(dev))
+    assert torch.equal(out.view(torch.int16), again.cpu().view(torch.int16))
+
+
+def test_moe_route_ties_and_experts_given_routing(dev):
+    logits = torch.zeros(3, 32)
+    logits[0, [5, 9, 30]] = 2.0
+    logits[1] = torch.arange(32).float() % 4  # many ties at the top
+    ids, wts = moe.moe_route(logits.to(dev), 6)
+    sids, swts = omoe.route(logits, 6)
+    assert torch.equal(ids.cpu(), sids)
+    torch.testing.assert_close(wts.cpu(), swts)
+    # experts with host-given routing (the reference's two-call path: host route(), experts kernel)
+    g = torch.Generator().manual_seed(4)
+    w = configs.moe_weights(g, hidden=128, experts=32, inter=64, shared_inter=64, router_std=0.5)
+    h2 = torch.randn(3, 128, generator=g).to(torch.bfloat16)
+    out = moe.moe_experts(h2.cuda(), _dev_w(w, dev), ids, wts).cpu()
+    ref, *_ = omoe.moe_layer(h2, w, 6, ids=ids.cpu(), wts=wts.cpu(), round_base=False)
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)
