@@ -112,4 +112,52 @@ __device__ __forceinline__ void mx_tile_accum(const uint16_t* const (&xrow)[MT],
   }
 }
 
+// Two weight tiles sharing the activations (the gate and up rows of a SwiGLU expert): every chunk's units of
+// both matrices are issued before any is used, so a lane keeps 2 x UNROLL 16-byte loads in flight.
+template <int F, int MT, int UNROLL>
+__device__ __forceinline__ void mx_tile_accum2(const uint16_t* const (&xrow)[MT], const bool (&mvalid)[MT],
+                                               const uint8_t* __restrict__ w1, const uint8_t* __restrict__ s1,
+                                               const uint8_t* __restrict__ w2, const uint8_t* __restrict__ s2,
+                                               int64_t n, bool nvalid, int64_t K, int64_t c_begin, int64_t c_step,
+                                               axk_f32x4 (&acc1)[MT], axk_f32x4 (&acc2)[MT]) {
+  using U = WUnit<F>;
+  constexpr int CH = 4 * U::V;
+  const int lane = threadIdx.x & 63, g = lane >> 4;
+  const int64_t NC = (K + CH - 1) / CH;
+  for (int64_t c0 = c_begin; c0 < NC; c0 += c_step * UNROLL) {
+    uint4 q1[UNROLL], q2[UNROLL];
+    float sc1[UNROLL], sc2[UNROLL];
+    int64_t kb[UNROLL];
+    bool kv[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int64_t c = c0 + (int64_t)u * c_step;
+      kb[u] = c * CH + g * U::V;
+      kv[u] = c < NC && kb[u] < K;
+      q1[u] = q2[u] = make_uint4(0u, 0u, 0u, 0u);
+      sc1[u] = sc2[u] = 1.0f;
+      if (nvalid && kv[u]) {
+        q1[u] = U::load(w1, n, K, kb[u]);
+        q2[u] = U::load(w2, n, K, kb[u]);
+        sc1[u] = U::scale(s1, n, K, kb[u]);
+        sc2[u] = U::scale(s2, n, K, kb[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+#pragma unroll
+      for (int s = 0; s < U::STEPS; ++s) {
+        const axk_bf16x8 b1 = U::conv(q1[u], s, sc1[u]);
+        const axk_bf16x8 b2 = U::conv(q2[u], s, sc2[u]);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const axk_bf16x8 a = (mvalid[t] && kv[u]) ? load_bf16x8(xrow[t] + kb[u] + 8 * s) : zero_bf16x8();
+          acc1[t] = mfma_bf16_16x16x32(a, b1, acc1[t]);
+          acc2[t] = mfma_bf16_16x16x32(a, b2, acc2[t]);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace axk

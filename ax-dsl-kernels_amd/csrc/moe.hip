@@ -29,6 +29,7 @@ using axk::WF_MXFP4;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;  // <= 64: lane k of the routing wave keeps selection k
 constexpr int kMaxPairs = 8192;
+constexpr int kMaskWords = 4;  // token bitmask words per expert in the grouping kernel: tokens <= 256
 constexpr int kMaxTokensPerChunk = 32;  // M rows per pass (2 MFMA tiles)
 
 struct MoeWs {
@@ -79,10 +80,10 @@ MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, in
 // ---------------------------------------------------------------------------------------------
 // route: one wave per token
 // ---------------------------------------------------------------------------------------------
+template <int V>  // expert logits per lane (num_experts <= 64 V)
 __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int K,
                                                         int norm_topk, int32_t* __restrict__ ids,
                                                         float* __restrict__ wts) {
-  constexpr int V = kMaxExperts / 64;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -144,60 +145,91 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------------------------
 // group: one workgroup; pairs grouped by expert, stable in (token, slot) order
 // ---------------------------------------------------------------------------------------------
+// Block-wide exclusive scan of one int per thread (256 threads); returns the exclusive prefix, *total the sum.
+__device__ __forceinline__ int block_exclusive_scan256(int v, int* s_tmp, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int x = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += x;
+  }
+  if (lane == 63) s_tmp[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += s_tmp[w];
+  *total = s_tmp[0] + s_tmp[1] + s_tmp[2] + s_tmp[3];
+  __syncthreads();
+  return base + incl - v;
+}
+
+// Expert e's tokens as a bitmask (a token's K experts are distinct, so a pair is (expert, token)): counts
+// are popcounts, and a pair's rank inside its expert is the popcount of the lower tokens' bits — the
+// grouping is stable in token order with no atomics on positions.
 __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restrict__ ids,
                                                         const float* __restrict__ wts, int T, int E, int K,
                                                         MoeWs w) {
-  __shared__ int s_ids[kMaxPairs];
-  __shared__ int s_cnt[kMaxExperts];
+  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
   __shared__ int s_off[kMaxExperts + 1];
-  __shared__ int s_act[kMaxExperts + 1];
-  const int P = T * K;
+  __shared__ int s_tmp[8];
+  const int P = T * K, W = (T + 63) / 64;
   const int tid = threadIdx.x;
-  for (int p = tid; p < P; p += blockDim.x) s_ids[p] = ids[p];
-  for (int e = tid; e < E; e += blockDim.x) s_cnt[e] = 0;
+  for (int i = tid; i < E * W; i += blockDim.x) s_mask[i] = 0ull;
   __syncthreads();
-  // counts: one thread per expert scans the pairs (broadcast LDS reads; no atomics)
-  for (int e = tid; e < E; e += blockDim.x) {
+  for (int p = tid; p < P; p += blockDim.x) {
+    const int e = ids[p], t = p / K;
+    if (e >= 0 && e < E) atomicOr(&s_mask[e * W + (t >> 6)], 1ull << (t & 63));
+  }
+  __syncthreads();
+  // expert e's count; 4 experts per thread (E <= 1024), then a block scan of the per-thread sums
+  constexpr int EPT = kMaxExperts / 256;
+  int cnt[EPT], sum = 0, nact = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
     int c = 0;
-    for (int p = 0; p < P; ++p) c += s_ids[p] == e;
-    s_cnt[e] = c;
+    if (e < E)
+      for (int i = 0; i < W; ++i) c += __popcll(s_mask[e * W + i]);
+    cnt[j] = c;
+    sum += c;
+    nact += c > 0;
   }
-  __syncthreads();
-  // exclusive scans of counts and of (count > 0)
-  if (tid == 0) {
-    int run = 0, runa = 0;
-    for (int e = 0; e < E; ++e) {
-      s_off[e] = run;
-      s_act[e] = runa;
-      run += s_cnt[e];
-      runa += s_cnt[e] > 0;
+  int tot, tota;
+  int off = block_exclusive_scan256(sum, s_tmp, &tot);
+  int aoff = block_exclusive_scan256(nact, s_tmp + 4, &tota);
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
+    if (e < E) {
+      s_off[e] = off;
+      w.counts[e] = cnt[j];
+      w.offsets[e] = off;
+      if (cnt[j] > 0) {
+        w.active_e[aoff] = e;
+        w.active_off[aoff] = off;
+        w.active_cnt[aoff] = cnt[j];
+        ++aoff;
+      }
     }
-    s_off[E] = run;
-    s_act[E] = runa;
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int c = s_cnt[e], o = s_off[e];
-    w.counts[e] = c;
-    w.offsets[e] = o;
-    if (c > 0) {
-      const int j = s_act[e];
-      w.active_e[j] = e;
-      w.active_off[j] = o;
-      w.active_cnt[j] = c;
-      int r = 0;
-      for (int p = 0; p < P; ++p)
-        if (s_ids[p] == e) {
-          const int pos = o + r++;
-          w.pair_pos[p] = pos;
-          w.row_tok[pos] = p / K;
-          w.row_w[pos] = wts[p];
-        }
-    }
+    off += cnt[j];
   }
   if (tid == 0) {
-    w.offsets[E] = s_off[E];
-    *w.n_active = s_act[E];
+    w.offsets[E] = tot;
+    *w.n_active = tota;
+  }
+  __syncthreads();
+  for (int p = tid; p < P; p += blockDim.x) {
+    const int e = ids[p], t = p / K;
+    if (e < 0 || e >= E) {  // an id outside [0, E) selects no expert: the combine skips the pair
+      w.pair_pos[p] = -1;
+      continue;
+    }
+    int rank = __popcll(s_mask[e * W + (t >> 6)] & ((1ull << (t & 63)) - 1ull));
+    for (int i = 0; i < (t >> 6); ++i) rank += __popcll(s_mask[e * W + i]);
+    const int pos = s_off[e] + rank;
+    w.pair_pos[p] = pos;
+    w.row_tok[pos] = t;
+    w.row_w[pos] = wts[p];
   }
 }
 
@@ -257,8 +289,7 @@ __global__ __launch_bounds__(64 * kGuWaves) void moe_gateup_kernel(GateUpArgs a)
     }
     axk_f32x4 accg[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
     axk_f32x4 accu[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
-    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, gw, gs, n, nvalid, a.H, wave, kGuWaves, accg);
-    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, uw, us, n, nvalid, a.H, wave, kGuWaves, accu);
+    axk::mx_tile_accum2<WF_MXFP4, 2, 4>(xrow, mvalid, gw, gs, uw, us, n, nvalid, a.H, wave, kGuWaves, accg, accu);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -337,7 +368,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(DownArgs a) {
       xrow[t] = act + (int64_t)(mvalid[t] ? m : 0) * K;
     }
     axk_f32x4 acc[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
-    axk::mx_tile_accum<WF_MXFP4, 2>(xrow, mvalid, dw, ds, n, nvalid, K, 0, 1, acc);
+    axk::mx_tile_accum<WF_MXFP4, 2, 4>(xrow, mvalid, dw, ds, n, nvalid, K, 0, 1, acc);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -371,7 +402,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint16_t* hrow = a.h2 + (int64_t)t * a.H;
   float gate = 1.0f;
-  if (a.has_shared && a.w_shg) {
+  if (a.has_shared && a.w_shg) {  // each column block recomputes the token's gate (H MACs)
     float d = 0.f;
     for (int i = tid; i < a.H; i += blockDim.x) d += bf16_bits_to_f32(hrow[i]) * bf16_bits_to_f32(a.w_shg[i]);
     d = wave_sum(d);
@@ -379,15 +410,19 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
     __syncthreads();
     gate = sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]);
   }
-  int pos[kMaxTopK];
-  for (int k = 0; k < a.K; ++k) pos[k] = a.w.pair_pos[(int64_t)t * a.K + k];
-  for (int i = tid; i < a.H; i += blockDim.x) {
-    float base = a.x_res ? bf16_bits_to_f32(a.x_res[(int64_t)t * a.H + i]) : 0.f;
-    if (a.has_shared) base += gate * a.w.y_sh[(int64_t)t * a.H + i];
-    float acc = base;
-    for (int k = 0; k < a.K; ++k) acc += a.w.y[(int64_t)pos[k] * a.H + i];
-    a.out[(int64_t)t * a.H + i] = (uint16_t)f32_to_bf16_bits(acc);
+  const int i = blockIdx.y * blockDim.x + tid;
+  if (i >= a.H) return;
+  float acc = a.x_res ? bf16_bits_to_f32(a.x_res[(int64_t)t * a.H + i]) : 0.f;
+  if (a.has_shared) acc += gate * a.w.y_sh[(int64_t)t * a.H + i];
+  float part[kMaxTopK];
+#pragma unroll 8
+  for (int k = 0; k < a.K; ++k) {
+    const int pos = a.w.pair_pos[(int64_t)t * a.K + k];
+    part[k] = pos >= 0 ? a.w.y[(int64_t)pos * a.H + i] : 0.f;
   }
+#pragma unroll 8
+  for (int k = 0; k < a.K; ++k) acc += part[k];
+  a.out[(int64_t)t * a.H + i] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
 struct MoeDims {
@@ -397,7 +432,7 @@ struct MoeDims {
 int check_dims(const MoeDims& d) {
   AXK_REQUIRE(d.T > 0 && d.H > 0 && d.E > 0 && d.K > 0 && d.F > 0, AXK_E_SHAPE);
   AXK_REQUIRE(d.E <= kMaxExperts && d.K <= kMaxTopK && d.K <= d.E, AXK_E_SHAPE);
-  AXK_REQUIRE(d.T * d.K <= kMaxPairs, AXK_E_SHAPE);
+  AXK_REQUIRE(d.T * d.K <= kMaxPairs && d.T <= 64 * kMaskWords, AXK_E_SHAPE);
   AXK_REQUIRE(d.H % 64 == 0 && d.F % 32 == 0 && d.Fs % 32 == 0 && d.Fs >= 0, AXK_E_SHAPE);
   AXK_REQUIRE(d.H <= INT32_MAX && d.F <= INT32_MAX, AXK_E_SHAPE);
   return AXK_OK;
@@ -417,8 +452,16 @@ extern "C" int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk
   AXK_REQUIRE(logits && topk_ids && topk_weights, AXK_E_NULL);
   AXK_REQUIRE(tokens > 0 && num_experts > 0 && num_experts <= kMaxExperts, AXK_E_SHAPE);
   AXK_REQUIRE(top_k > 0 && top_k <= kMaxTopK && top_k <= num_experts && tokens <= INT32_MAX, AXK_E_SHAPE);
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0, axk_stream(stream), logits,
-                     (int)tokens, (int)num_experts, (int)top_k, norm_topk_prob, topk_ids, topk_weights);
+  const dim3 grid((unsigned)((tokens + 3) / 4)), block(256);
+  const int T = (int)tokens, E = (int)num_experts, K = (int)top_k;
+  hipStream_t st = axk_stream(stream);
+  if (E <= 64)
+    hipLaunchKernelGGL(moe_route_kernel<1>, grid, block, 0, st, logits, T, E, K, norm_topk_prob, topk_ids, topk_weights);
+  else if (E <= 256)
+    hipLaunchKernelGGL(moe_route_kernel<4>, grid, block, 0, st, logits, T, E, K, norm_topk_prob, topk_ids, topk_weights);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<kMaxExperts / 64>, grid, block, 0, st, logits, T, E, K, norm_topk_prob,
+                       topk_ids, topk_weights);
   return axk_launch_status();
 }
 
@@ -456,7 +499,7 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, (H + 63) / 64, w};
   hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((max_slots + 1) * da.ntile)), dim3(256), 0, st, da);
   CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T), dim3(256), 0, st, ca);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)((H + 255) / 256)), dim3(256), 0, st, ca);
   return axk_launch_status();
 }
 

@@ -216,47 +216,84 @@ class GdnDecodeWorkload:
                 "sample": f"full config2a step (oracle/gdn.py gdn_fp32, torch CPU), median of {reps} runs"}
 
 
+class MoeDecodeWorkload:
+    """Config 3a: MoE layer decode, 32 tokens, hidden 2048, 256 MXFP4 experts (inter 512) + shared, top-8.
+
+    One step = router GEMV + top-K + grouping + gate-up/SwiGLU + down + combine (6 launches, one graph).
+    Algorithmic bytes: the weights of the experts actually routed (U distinct) + shared expert + router +
+    activations in/out."""
+
+    name = "moe_decode"
+    kernel = "moe step (router, route, group, gateup, down, combine)"
+    timing = "graph"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, moe
+
+        c = configs.config3(32)
+        self.host = c
+        w = c["weights"]
+        per_expert = sum(w[n][0].numel() for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+        shared = sum(w[n].numel() for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down"))
+        expert_bytes = per_expert * w["e_gw"].shape[0]
+        self.copies = max(2, -(-ROTATE_BYTES // expert_bytes))
+        wd = {n: v.to(dev) for n, v in w.items()}
+        self.wsets = [wd] + [{n: (v.clone() if n.startswith("e_") else v) for n, v in wd.items()}
+                             for _ in range(self.copies - 1)]
+        self.h2, self.x = c["h2"].to(dev), c["x_res"].to(dev)
+        self.out = torch.empty_like(self.h2)
+        self.ws = moe.moe_workspace(32, 2048, 256, 8, 512, 512, dev)
+        _, _, ids, _ = moe.moe_decode(self.h2, wd, top_k=8, x_res=self.x, output=self.out, workspace=self.ws)
+        self.active = int(torch.unique(ids).numel())
+        self.alg_bytes = self.active * per_expert + shared + w["w_router"].numel() * 2 + w["w_shg"].numel() * 2 + \
+            3 * self.h2.numel() * 2
+        self.config = {"workload": "config3a: MoE decode T=32 H=2048 E=256 F=512 top-8 + shared (MXFP4)",
+                       "distinct_experts": self.active, "rotating_copies": self.copies}
+        self.dtype = "mxfp4 weights x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        from axk import moe
+
+        moe.moe_decode(self.h2, self.wsets[i % self.copies], top_k=8, x_res=self.x, output=self.out,
+                       workspace=self.ws)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import moe as omoe
+
+        c = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: omoe.moe_layer(c["h2"], c["weights"], 8, x_res=c["x_res"]), budget_s=10.0,
+                              min_reps=1, max_reps=5)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config3a layer (oracle/moe.py, numpy dequant + torch CPU), median of {reps} runs"}
+
+
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
-             GdnDecodeWorkload.name: GdnDecodeWorkload}
+             GdnDecodeWorkload.name: GdnDecodeWorkload, MoeDecodeWorkload.name: MoeDecodeWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
-              file=sys.stderr)
-        return 2
-
+def measure(wl, steps: int, warmup: int) -> tuple[float, float]:
+    """(ms per step, ms per launch of the workload's roofline kernel) over exactly `steps` timed steps."""
     import torch
 
-    import axk
-
-    axk.load_library()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    wl = WORKLOADS[args.workload](dev)
     torch.cuda.synchronize()
-
-    for i in range(args.warmup):
+    for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
-
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if wl.timing == "graph":
-        # Capture exactly K steps in one HIP graph (removes host launch overhead from the measurement);
-        # the step is a single kernel, so the per-step time is that kernel's average launch duration.
+        # Capture exactly K steps in one HIP graph (removes host launch overhead from the measurement).
         graph = torch.cuda.CUDAGraph()
         stream = torch.cuda.Stream()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(graph, stream=stream):
-                for i in range(args.steps):
+                for i in range(steps):
                     wl.step(i)
         graph.replay()  # untimed replay: graph upload / first-run costs
         torch.cuda.synchronize()
@@ -265,29 +302,28 @@ def main() -> int:
             graph.replay()
         end.record(stream)
         torch.cuda.synchronize()
-        ms_per_step = start.elapsed_time(end) / args.steps
-        kernel_ms = ms_per_step
-    else:
-        # Eager steps on the current stream; HIP events bracket every launch of the dominant kernel.
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-        torch.cuda.synchronize()
-        start.record()
-        for i in range(args.steps):
-            wl.pre(i)
-            evs[i][0].record()
-            wl.main(i)
-            evs[i][1].record()
-            wl.post(i)
-        end.record()
-        torch.cuda.synchronize()
-        ms_per_step = start.elapsed_time(end) / args.steps
-        kernel_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
-    us = ms_per_step * 1e3
+        ms_per_step = start.elapsed_time(end) / steps
+        return ms_per_step, ms_per_step
+    # Eager steps on the current stream; HIP events bracket every launch of the dominant kernel.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        wl.pre(i)
+        evs[i][0].record()
+        wl.main(i)
+        evs[i][1].record()
+        wl.post(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, sum(a.elapsed_time(b) for a, b in evs) / steps
 
+
+def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
     achieved = wl.alg_bytes / (kernel_ms * 1e-3) / 1e9
-    line = {
+    return {
         "metric": METRIC,
-        "value": round(us, 3),
+        "value": round(ms_per_step * 1e3, 3),
         "unit": "µs/op",
         "n_gpus": 1,
         "steps": args.steps,
@@ -313,6 +349,47 @@ def main() -> int:
             "alg_bytes_per_launch": wl.alg_bytes,
         },
     }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-suite", action="store_true", help="measure only the headline workload")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    import axk
+
+    axk.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload](dev)
+    ms_per_step, kernel_ms = measure(wl, args.steps, args.warmup)
+    line = report_line(wl, args, ms_per_step, kernel_ms)
+    if not args.no_suite:
+        # the other hot-path workloads, measured in the same process (reported beside the headline line)
+        suite = {}
+        for name, cls in WORKLOADS.items():
+            if name == args.workload:
+                continue
+            other = cls(dev)
+            ms, kms = measure(other, max(20, args.steps // 4), min(args.warmup, 10))
+            gbs = other.alg_bytes / (kms * 1e-3) / 1e9
+            suite[name] = {"us_per_op": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3),
+                           "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                           "config": other.config["workload"]}
+            del other
+            torch.cuda.empty_cache()
+        line["suite"] = suite
     if not args.no_cpu:
         line["cpu_baseline"] = wl.cpu_baseline()
     print(json.dumps(line), flush=True)

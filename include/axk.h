@@ -192,8 +192,8 @@ int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
  * MoE with MXFP4 experts (router top-K, shared expert with sigmoid gate, routed SwiGLU experts)
  * ------------------------------------------------------------------------------------------- */
 
-/* Workspace bytes for axk_moe_experts / axk_moe_decode (0 = unsupported shape: tokens x top_k <= 8192,
- * num_experts <= 1024, top_k <= 32, hidden % 64 == 0, inter % 32 == 0). */
+/* Workspace bytes for axk_moe_experts / axk_moe_decode (0 = unsupported shape: tokens <= 256,
+ * tokens x top_k <= 8192, num_experts <= 1024, top_k <= 32, hidden % 64 == 0, inter % 32 == 0). */
 size_t axk_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
                               int64_t shared_inter);
 
@@ -215,7 +215,8 @@ int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk_weights, i
  *     down [hidden, shared_inter/2] + [hidden, shared_inter/32]
  *   e_gw u8 [E, 2*inter, hidden/2] (gate rows, then up rows), e_gs u8 [E, 2*inter, hidden/32],
  *   e_dw u8 [E, hidden, inter/2], e_ds u8 [E, hidden, inter/32]
- *   topk_ids i32 / topk_weights f32 [tokens, top_k]; out bf16 [tokens, hidden]. */
+ *   topk_ids i32 / topk_weights f32 [tokens, top_k]: a row holds distinct expert ids (as the router's
+ *     top-K does); an id outside [0, num_experts) selects nothing; out bf16 [tokens, hidden]. */
 int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg, const uint8_t* sh_gate_w,
                     const uint8_t* sh_gate_s, const uint8_t* sh_up_w, const uint8_t* sh_up_s,
                     const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,

@@ -67,3 +67,12 @@ def test_python_layer_raises_value_error_on_contract():
         axk.mxfp4_gemm(a.float(), torch.zeros(16, 32, dtype=torch.uint8), s)  # fp32 activation
     with pytest.raises(ValueError):
         axk.mxfp4_gemm(a, torch.zeros(16, 32, dtype=torch.uint8), torch.zeros(16, 3, dtype=torch.uint8))
+
+
+def test_moe_workspace_size_limits():
+    lib = _lib.load()
+    assert lib.axk_moe_workspace_size(256, 64, 8, 2, 32, 32) > 0
+    assert lib.axk_moe_workspace_size(257, 64, 8, 2, 32, 32) == 0  # tokens per call <= 256
+    assert lib.axk_moe_workspace_size(4, 64, 1025, 2, 32, 32) == 0  # experts <= 1024
+    assert lib.axk_moe_workspace_size(4, 64, 8, 33, 32, 32) == 0   # top_k <= 32
+    assert lib.axk_moe_workspace_size(4, 96, 8, 2, 32, 32) == 0     # hidden % 64

@@ -37,8 +37,12 @@ def _check_layer(c, dev, norm=True):
     return out
 
 
+# e spans the router's 64 / 256 / 1024-expert register layouts; t = 130 and 256 span several 64-token words
+# of the grouping bitmask (256 is the largest token count of one call)
 @pytest.mark.parametrize("t,h,e,f,fs,k", [(1, 64, 8, 32, 32, 2), (5, 256, 16, 64, 96, 4), (33, 128, 64, 32, 64, 8),
-                                          (7, 192, 40, 160, 0, 6)])
+                                          (7, 192, 40, 160, 0, 6), (3, 128, 200, 32, 32, 8),
+                                          (2, 64, 1000, 32, 0, 32), (130, 64, 16, 32, 32, 4),
+                                          (256, 64, 8, 32, 0, 2)])
 def test_moe_small_shapes(dev, t, h, e, f, fs, k):
     g = torch.Generator().manual_seed(t + h + e)
     w = configs.moe_weights(g, hidden=h, experts=e, inter=f, shared_inter=max(fs, 32), router_std=0.5)
@@ -73,3 +77,19 @@ def test_moe_route_ties_and_experts_given_routing(dev):
     out = moe.moe_experts(h2.cuda(), _dev_w(w, dev), ids, wts).cpu()
     ref, *_ = omoe.moe_layer(h2, w, 6, ids=ids.cpu(), wts=wts.cpu(), round_base=False)
     torch.testing.assert_close(out.float(), ref.float(), **TOL)
+
+
+def test_moe_experts_out_of_range_ids_select_nothing(dev):
+    g = torch.Generator().manual_seed(9)
+    w = configs.moe_weights(g, hidden=64, experts=8, inter=32, shared_inter=32, router_std=0.5)
+    h2 = torch.randn(4, 64, generator=g).to(torch.bfloat16)
+    ids = torch.tensor([[1, 2], [3, -1], [8, 0], [5, 6]], dtype=torch.int32)
+    wts = torch.rand(4, 2, generator=g)
+    out = moe.moe_experts(h2.to(dev), _dev_w(w, dev), ids.to(dev), wts.to(dev)).cpu()
+    # the reference computation with each invalid pair replaced by a zero-weight valid expert
+    ids_ref, wts_ref = ids.clone(), wts.clone()
+    ids_ref[1, 1], ids_ref[2, 0] = 7, 7
+    wts_ref[1, 1], wts_ref[2, 0] = 0.0, 0.0
+    ref, *_ = omoe.moe_layer(h2, w, 2, ids=ids_ref, wts=wts_ref, round_base=False)
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)
+
