@@ -42,12 +42,29 @@ def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 50)
     return statistics.median(times), len(times)
 
 
-class MxLinearWorkload:
+class Workload:
+    """A step is pre() + main() + post(); the roofline kernel is launched by main()."""
+
+    in_suite = True
+    traffic_profile = None  # profiles/ file holding the kernel's measured HBM bytes per launch
+
+    def pre(self, i: int) -> None:
+        pass
+
+    def main(self, i: int) -> None:
+        self.step(i)
+
+    def post(self, i: int) -> None:
+        pass
+
+
+class MxLinearWorkload(Workload):
     """Config 0: one MXFP4 linear, W 4096 x 4096 (E2M1 + E8M0), x bf16 [1, 4096], bf16 out."""
 
     name = "mxfp4_linear"
     kernel = "mx_linear_kernel"
     timing = "graph"
+    traffic_profile = "mxfp4_linear_config0_pmc.txt"
 
     def __init__(self, dev):
         import torch
@@ -87,7 +104,7 @@ class MxLinearWorkload:
                 "sample": f"full config0 op (oracle/mx_codec.c, OpenMP), median of {reps} runs"}
 
 
-class PagedDecodeWorkload:
+class PagedDecodeWorkload(Workload):
     """Config 1: paged decode attention, batch 16, 16 q / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384].
 
     One step = plan (split-KV partition) + split (the attention kernel) + merge (LSE merge of split partials).
@@ -98,6 +115,7 @@ class PagedDecodeWorkload:
     name = "paged_decode"
     kernel = "paged_decode_kernel<256>"  # launched by axk_paged_decode_split
     timing = "events"
+    traffic_profile = "paged_decode_config1_pmc.txt"
 
     def __init__(self, dev):
         import torch
@@ -167,12 +185,13 @@ class PagedDecodeWorkload:
                 "sample": f"full config1 op (oracle/paged_attn.py, torch fp32 CPU), median of {reps} runs"}
 
 
-class GdnDecodeWorkload:
+class GdnDecodeWorkload(Workload):
     """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
 
     name = "gdn_decode"
     kernel = "gdn_recurrent_kernel"
     timing = "graph"
+    traffic_profile = "gdn_decode_config2a_pmc.txt"
 
     def __init__(self, dev):
         import torch
@@ -216,7 +235,7 @@ class GdnDecodeWorkload:
                 "sample": f"full config2a step (oracle/gdn.py gdn_fp32, torch CPU), median of {reps} runs"}
 
 
-class MoeDecodeWorkload:
+class MoeDecodeWorkload(Workload):
     """Config 3a: MoE layer decode, 32 tokens, hidden 2048, 256 MXFP4 experts (inter 512) + shared, top-8.
 
     One step = router GEMV + top-K + grouping + gate-up/SwiGLU + down + combine (6 launches, one graph).
@@ -226,6 +245,7 @@ class MoeDecodeWorkload:
     name = "moe_decode"
     kernel = "moe step (router, route, group, gateup, down, combine)"
     timing = "graph"
+    traffic_profile = "moe_decode_config3a_pmc.txt"
 
     def __init__(self, dev):
         import torch
@@ -273,13 +293,41 @@ class MoeDecodeWorkload:
                 "sample": f"full config3a layer (oracle/moe.py, numpy dequant + torch CPU), median of {reps} runs"}
 
 
+class CopyCalibWorkload(Workload):
+    """A plain 256 MiB device-to-device copy: the known-size kernel that calibrates the FETCH_SIZE /
+    WRITE_SIZE counters (read 256 MiB, write 256 MiB per launch)."""
+
+    name = "copy_calib"
+    kernel = "__amd_rocclr_copyBuffer"
+    timing = "events"
+    in_suite = False
+
+    def __init__(self, dev):
+        import torch
+
+        self.n = 256 << 20
+        self.src = torch.randint(0, 255, (self.n,), dtype=torch.uint8, device=dev)
+        self.dst = torch.empty_like(self.src)
+        self.alg_bytes = 2 * self.n
+        self.config = {"workload": "copy calibration: 256 MiB device-to-device"}
+        self.dtype = "u8"
+
+    def step(self, i: int) -> None:
+        self.dst.copy_(self.src)
+
+    def cpu_baseline(self) -> dict:
+        return None
+
+
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
-             GdnDecodeWorkload.name: GdnDecodeWorkload, MoeDecodeWorkload.name: MoeDecodeWorkload}
+             GdnDecodeWorkload.name: GdnDecodeWorkload, MoeDecodeWorkload.name: MoeDecodeWorkload,
+             CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 
-def measure(wl, steps: int, warmup: int) -> tuple[float, float]:
-    """(ms per step, ms per launch of the workload's roofline kernel) over exactly `steps` timed steps."""
+def measure(wl, steps: int, warmup: int, eager: bool = False) -> tuple[float, float]:
+    """(ms per step, ms per launch of the workload's roofline kernel) over exactly `steps` timed steps.
+    eager: launch every step on the stream even where the workload is normally timed as one HIP graph."""
     import torch
 
     torch.cuda.synchronize()
@@ -287,7 +335,7 @@ def measure(wl, steps: int, warmup: int) -> tuple[float, float]:
         wl.step(i)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    if wl.timing == "graph":
+    if wl.timing == "graph" and not eager:
         # Capture exactly K steps in one HIP graph (removes host launch overhead from the measurement).
         graph = torch.cuda.CUDAGraph()
         stream = torch.cuda.Stream()
@@ -345,10 +393,26 @@ def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": read_traffic(wl),
             "alg_bytes_per_launch": wl.alg_bytes,
         },
     }
+
+
+def read_traffic(wl):
+    """HBM bytes per launch of the roofline kernel, from the committed PMC summary (FETCH_SIZE + WRITE_SIZE
+    per dispatch, scaled by the copy-kernel calibration factor), or None when no summary exists."""
+    if not wl.traffic_profile:
+        return None
+    path = os.path.join(ROOT, "profiles", wl.traffic_profile)
+    try:
+        with open(path, encoding="utf-8") as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(float(ln.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
 
 
 def main() -> int:
@@ -359,6 +423,7 @@ def main() -> int:
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-suite", action="store_true", help="measure only the headline workload")
+    ap.add_argument("--eager", action="store_true", help="no HIP graph capture (for counter collection)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -373,16 +438,16 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload](dev)
-    ms_per_step, kernel_ms = measure(wl, args.steps, args.warmup)
+    ms_per_step, kernel_ms = measure(wl, args.steps, args.warmup, args.eager)
     line = report_line(wl, args, ms_per_step, kernel_ms)
     if not args.no_suite:
         # the other hot-path workloads, measured in the same process (reported beside the headline line)
         suite = {}
         for name, cls in WORKLOADS.items():
-            if name == args.workload:
+            if name == args.workload or not cls.in_suite:
                 continue
             other = cls(dev)
-            ms, kms = measure(other, max(20, args.steps // 4), min(args.warmup, 10))
+            ms, kms = measure(other, max(20, args.steps // 4), min(args.warmup, 10), args.eager)
             gbs = other.alg_bytes / (kms * 1e-3) / 1e9
             suite[name] = {"us_per_op": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3),
                            "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -391,7 +456,9 @@ def main() -> int:
             torch.cuda.empty_cache()
         line["suite"] = suite
     if not args.no_cpu:
-        line["cpu_baseline"] = wl.cpu_baseline()
+        cpu = wl.cpu_baseline()
+        if cpu is not None:
+            line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0
 

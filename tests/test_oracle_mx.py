@@ -69,6 +69,21 @@ def test_pack_layout_matches_reference_bit_method():
     np.testing.assert_array_equal(mx.unpack_fp4_codes(ref), logical)
 
 
+def test_pack_and_decode_reference_kat():
+    # known-answer data of test_nvfp4_lm_head.py:19-30: source values and the codes the reference's quantiser
+    # assigns them (its rounding sends ties to the even code); packed low nibble = even column
+    source = [0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, 6, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5]
+    codes = np.array([0, 0, 2, 2, 4, 4, 6, 6, 7, 8, 10, 10, 12, 12, 14, 14], np.uint8)
+    expect_bytes = codes[::2] | (codes[1::2] << 4)
+    np.testing.assert_array_equal(mx.pack_fp4_codes(codes[None, :])[0], expect_bytes)
+    # decoding the KAT's bytes at scale 2^0 gives the E2M1 grid points the KAT names, and each one lies
+    # within half a grid step of its source value
+    dec = mx.dequant_mxfp4(np.concatenate([expect_bytes] * 2)[None, :], np.array([[127]], np.uint8))[0, :16]
+    np.testing.assert_array_equal(dec, np.array(REF_FP4_LUT, np.float32)[codes])
+    step = np.array([0.5 if abs(v) <= 2 else 1.0 if abs(v) <= 4 else 2.0 for v in source])
+    assert np.all(np.abs(dec - np.array(source)) <= step / 2)
+
+
 def test_c_oracle_matches_numpy_random():
     rng = np.random.default_rng(1)
     packed = rng.integers(0, 256, size=(33, 96), dtype=np.uint8)
