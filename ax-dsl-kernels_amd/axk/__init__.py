@@ -26,9 +26,9 @@ __all__ += ["attention", "paged_decode", "paged_decode_plan", "paged_decode_run"
             "store_paged_kv"]
 
 from . import gdn  # noqa: E402
-from .gdn import gdn_recurrent  # noqa: E402
+from .gdn import gdn_chunk_prefill, gdn_chunk_workspace, gdn_recurrent  # noqa: E402
 
-__all__ += ["gdn", "gdn_recurrent"]
+__all__ += ["gdn", "gdn_chunk_prefill", "gdn_chunk_workspace", "gdn_recurrent"]
 
 from . import moe  # noqa: E402
 from .moe import moe_decode, moe_experts, moe_route, moe_workspace  # noqa: E402

@@ -70,6 +70,8 @@ SIGNATURES: dict[str, list] = {
                          ctypes.c_size_t, _vp],
     "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "axk_gdn_recurrent": [_vp] * 10 + [_i64] * 6 + [_vp],
+    "axk_gdn_chunk_workspace_size": [_i64] * 7,
+    "axk_gdn_chunk_prefill": [_vp] * 10 + [_i64] * 7 + [_vp, ctypes.c_size_t, _vp],
     "axk_moe_workspace_size": [_i64] * 6,
     "axk_moe_route": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "axk_moe_experts": [_vp] * 16 + [_i64] * 6 + [_vp, ctypes.c_size_t, _vp],
@@ -80,6 +82,7 @@ _RESTYPES = {
     "axk_status_string": ctypes.c_char_p,
     "axk_paged_decode_workspace_size": ctypes.c_size_t,
     "axk_moe_workspace_size": ctypes.c_size_t,
+    "axk_gdn_chunk_workspace_size": ctypes.c_size_t,
 }
 
 

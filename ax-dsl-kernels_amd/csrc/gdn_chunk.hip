@@ -1,0 +1,594 @@
+// Gated DeltaNet chunked prefill (chunk-parallel WY form) for gfx950.
+//
+// Reference: gdn_stable_chunk (sgl_kernel_axera/attention/gdn.py:1122-1212) with the unit-lower solve of
+// inverse_unit_lower_recursive (gdn.py:1048-1119) and chunk_prefix_sum_fp32 (gdn.py:992-1009), driven chunk by
+// chunk as gdn_prefill_impl does (gdn.py:1628-1790) and as q35_prefill.gdn_chunked
+// (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:144-169).
+//
+// Per chunk of C = 64 tokens and value head, with the gate prefix G = cumsum(g) inside the chunk,
+// Gamma_t = exp(G_t) and decay_ij = exp(G_i - G_j) for i >= j:
+//   L = beta_i (k_i . k_j) decay_ij (i > j);   Tinv = (I + L)^-1          (fp32 solve, rounded to bf16)
+//   u = Tinv (beta v);   w = Tinv (beta Gamma k);   P = (q k^T) * decay   (bf16 MatMul operands and results)
+//   v_new = u - w S;   o = Gamma (q S) + P v_new;   S <- Gamma_last S + k^T (v_new * decay_last,:)
+// q and k are the L2-normalised head vectors (q also scaled by DK^-0.5), as in gdn_prefill_impl.
+//
+// Two launches:
+//   gdn_chunk_prep_kernel  one workgroup per (sequence, value head, chunk); every chunk in parallel. The
+//                          state-independent half: l2norm, gates, prefix, K K^T and Q K^T on MFMA, the
+//                          triangular solve (16 x 16 diagonal blocks by substitution, then two levels of block
+//                          products on fp32 MFMA), u and w on MFMA. Writes w, u, P, Gamma and the last decay
+//                          row to the workspace, and once per key head the normalised q and k^T.
+//   gdn_chunk_scan_kernel  one workgroup per (sequence, value head, 16-column slice of the state): the state's
+//                          columns evolve independently, so 8 workgroups carry one head's 128 x 128 fp32 state
+//                          through the chunks in order, held in MFMA accumulators, with each chunk's operands
+//                          loaded two chunks ahead.
+#include "axk_common.h"
+#include "axk_host.h"
+
+namespace {
+
+constexpr int kC = 64;    // chunk length
+constexpr int kD = 128;   // key / value head dim
+constexpr int kSlices = kD / 16;
+
+// Workspace: per (sequence, value head, chunk) w, u [C][D] bf16, P [C][C] bf16, Gamma and last-row decay
+// [C] fp32; per (sequence, key head, chunk) normalised q [C][D] bf16 and k^T [D][C] bf16.
+struct ChunkWs {
+  uint16_t* w;
+  uint16_t* u;
+  uint16_t* p;
+  float* gam;
+  float* dec;
+  uint16_t* qn;
+  uint16_t* kt;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t chunk_ws_layout(int64_t B, int64_t NK, int64_t NV, int64_t NC, size_t* off) {
+  const size_t vc = (size_t)(B * NV * NC), kc = (size_t)(B * NK * NC);
+  const size_t sizes[7] = {vc * kC * kD * 2, vc * kC * kD * 2, vc * kC * kC * 2, vc * kC * 4,
+                           vc * kC * 4,      kc * kC * kD * 2, kc * kD * kC * 2};
+  size_t o = 0;
+  for (int i = 0; i < 7; ++i) {
+    off[i] = o;
+    o = align256(o + sizes[i]);
+  }
+  return o;
+}
+
+ChunkWs chunk_ws(void* ws, int64_t B, int64_t NK, int64_t NV, int64_t NC) {
+  size_t off[7];
+  chunk_ws_layout(B, NK, NV, NC, off);
+  unsigned char* p = reinterpret_cast<unsigned char*>(ws);
+  return {reinterpret_cast<uint16_t*>(p + off[0]), reinterpret_cast<uint16_t*>(p + off[1]),
+          reinterpret_cast<uint16_t*>(p + off[2]), reinterpret_cast<float*>(p + off[3]),
+          reinterpret_cast<float*>(p + off[4]),    reinterpret_cast<uint16_t*>(p + off[5]),
+          reinterpret_cast<uint16_t*>(p + off[6])};
+}
+
+AXK_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+AXK_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+AXK_DEV uint32_t pack_bf16x2(float lo, float hi) { return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16); }
+
+AXK_DEV axk_f32x4 mfma_f32_16x16x4(float a, float b, axk_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------------------------
+// prep: the state-independent half of every chunk
+// ---------------------------------------------------------------------------------------------
+constexpr int kLdK = kD + 8;  // bf16 row stride of token-major [C][D] tiles in LDS
+constexpr int kLdT = kC + 8;  // bf16 row stride of [D][C] and [C][C] tiles
+constexpr int kLdL = kC + 4;  // fp32 row stride of [C][C] tiles
+constexpr int kLdX = 32 + 1;  // fp32 scratch of the solve's block products
+
+constexpr int kOffK = 0;                  // k (bf16 [C][LdK]); later u staging
+constexpr int kSzK = kC * kLdK * 2;
+constexpr int kOffQ = kOffK + kSzK;       // q (bf16 [C][LdK]); then (beta v)^T (bf16 [D][LdT]); later w staging
+constexpr int kSzQ = kD * kLdT * 2;
+constexpr int kOffL = kOffQ + kSzQ;       // L (fp32 [C][LdL]); then bf16 Tinv [C][LdT]
+constexpr int kSzL = kC * kLdL * 4;
+constexpr int kOffT = kOffL + kSzL;       // P staging (bf16 [C][LdT]); Tinv (fp32 [C][LdL]); (beta Gamma k)^T
+constexpr int kSzT = kD * kLdT * 2;
+constexpr int kOffX = kOffT + kSzT;       // fp32 [32][LdX]
+constexpr int kSzX = 32 * kLdX * 4;
+constexpr int kOffG = kOffX + kSzX;       // G, beta: fp32 [C] each
+constexpr int kPrepLds = kOffG + 2 * kC * 4;
+static_assert(kSzQ >= kC * kLdK * 2 && kSzT >= kC * kLdL * 4 && kSzL >= kC * kLdT * 2, "LDS carve");
+
+struct PrepArgs {
+  const uint16_t *q, *k, *v, *a, *b;
+  const float *a_log, *dt_bias;
+  ChunkWs ws;
+  int B, T, NK, NV, NC;
+};
+
+__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* sK = reinterpret_cast<uint16_t*>(smem + kOffK);
+  uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + kOffQ);
+  float* sL = reinterpret_cast<float*>(smem + kOffL);
+  float* sT = reinterpret_cast<float*>(smem + kOffT);
+  float* sX = reinterpret_cast<float*>(smem + kOffX);
+  float* sG = reinterpret_cast<float*>(smem + kOffG);
+  float* sBeta = sG + kC;
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int per_key = p.NV / p.NK, kh = h / per_key;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int t0 = c * kC;
+  const int n = min(kC, p.T - t0);
+  const int64_t vidx = ((int64_t)b * p.NV + h) * p.NC + c;   // (sequence, value head, chunk)
+  const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;  // (sequence, key head, chunk)
+
+  // ---- 1. q, k, v rows: thread = (token tt, 32-dim quarter qd); L2 norms over the 4 threads of a token ----
+  const int tt = tid >> 2, qd = tid & 3;
+  uint4 qr[4], kr[4], vr[4];
+  if (tt < n) {
+    const int64_t tok = (int64_t)b * p.T + t0 + tt;
+    const uint4* qp = reinterpret_cast<const uint4*>(p.q + (tok * p.NK + kh) * kD + 32 * qd);
+    const uint4* kp = reinterpret_cast<const uint4*>(p.k + (tok * p.NK + kh) * kD + 32 * qd);
+    const uint4* vp = reinterpret_cast<const uint4*>(p.v + (tok * p.NV + h) * kD + 32 * qd);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      qr[i] = qp[i];
+      kr[i] = kp[i];
+      vr[i] = vp[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qr[i] = kr[i] = vr[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  float qs = 0.f, ks = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t qw[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+    const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qs += bf16_lo(qw[j]) * bf16_lo(qw[j]) + bf16_hi(qw[j]) * bf16_hi(qw[j]);
+      ks += bf16_lo(kw[j]) * bf16_lo(kw[j]) + bf16_hi(kw[j]) * bf16_hi(kw[j]);
+    }
+  }
+  qs = group_sum<4>(qs);
+  ks = group_sum<4>(ks);
+  {
+    const float qn = sqrtf(qs + 1e-6f), kn = sqrtf(ks + 1e-6f);
+    const float qscale = 0.08838834764831845f;  // 128^-0.5
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t qw[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+      const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+      uint4 qo, ko;
+      uint32_t* qop = reinterpret_cast<uint32_t*>(&qo);
+      uint32_t* kop = reinterpret_cast<uint32_t*>(&ko);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // q: bf16(bf16(q / |q|) * DK^-0.5) (l2norm_lastdim, then the q scale; gdn.py:1631)
+        qop[j] = pack_bf16x2(round_bf16(bf16_lo(qw[j]) / qn) * qscale, round_bf16(bf16_hi(qw[j]) / qn) * qscale);
+        kop[j] = pack_bf16x2(bf16_lo(kw[j]) / kn, bf16_hi(kw[j]) / kn);
+      }
+      *reinterpret_cast<uint4*>(sQ + tt * kLdK + 32 * qd + 8 * i) = qo;
+      *reinterpret_cast<uint4*>(sK + tt * kLdK + 32 * qd + 8 * i) = ko;
+    }
+  }
+  // gates and the in-chunk prefix of g (wave 0, lane = token); padded tokens: g = 0, beta = 0
+  if (wave == 0) {
+    float g = 0.f, beta = 0.f;
+    if (lane < n) {
+      const int64_t vh = ((int64_t)b * p.T + t0 + lane) * p.NV + h;
+      const float x = bf16_bits_to_f32(p.a[vh]) + p.dt_bias[h];
+      const float sp = x > 20.f ? x : log1pf(expf(x));
+      g = -expf(p.a_log[h]) * sp;
+      beta = round_bf16(1.0f / (1.0f + expf(-bf16_bits_to_f32(p.b[vh]))));
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float x = __shfl_up(g, o, 64);
+      if (lane >= o) g += x;
+    }
+    sG[lane] = g;
+    sBeta[lane] = beta;
+  }
+  __syncthreads();
+
+  // ---- 2. normalised q and k^T of this key head (written once, by its first value head) ----
+  if (h % per_key == 0) {
+    uint16_t* qn_g = p.ws.qn + kidx * kC * kD;
+    uint16_t* kt_g = p.ws.kt + kidx * kD * kC;
+    for (int i = tid; i < kC * kD / 8; i += 256) {
+      const int row = i >> 4, c8 = i & 15;
+      *reinterpret_cast<uint4*>(qn_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sQ + row * kLdK + 8 * c8);
+    }
+    for (int i = tid; i < kD * kC / 8; i += 256) {
+      const int d = i >> 3, t8 = i & 7;
+      uint4 o;
+      uint32_t* op = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        op[e] = (uint32_t)sK[(8 * t8 + 2 * e) * kLdK + d] | ((uint32_t)sK[(8 * t8 + 2 * e + 1) * kLdK + d] << 16);
+      *reinterpret_cast<uint4*>(kt_g + d * kC + 8 * t8) = o;
+    }
+  }
+
+  // ---- 3. K K^T and Q K^T: wave w owns token rows 16w .. 16w + 15 ----
+  axk_f32x4 kk[4], qk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kk[j] = qk[j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < kD / 32; ++st) {
+    const int ko = 32 * st + 8 * g4;
+    const axk_bf16x8 ak = load_bf16x8(sK + (16 * wave + l16) * kLdK + ko);
+    const axk_bf16x8 aq = load_bf16x8(sQ + (16 * wave + l16) * kLdK + ko);
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const axk_bf16x8 bk = load_bf16x8(sK + (16 * jt + l16) * kLdK + ko);
+      kk[jt] = mfma_bf16_16x16x32(ak, bk, kk[jt]);
+      qk[jt] = mfma_bf16_16x16x32(aq, bk, qk[jt]);
+    }
+  }
+
+  // ---- 4. L (fp32, strictly lower), P = bf16((q k^T) * decay) staged for a coalesced write ----
+  uint16_t* sP = reinterpret_cast<uint16_t*>(sT);
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * g4 + r, j = 16 * jt + l16;
+      const float dij = i >= j ? expf(sG[i] - sG[j]) : 0.f;
+      sL[i * kLdL + j] = i > j ? kk[jt][r] * sBeta[i] * dij : 0.f;
+      sP[i * kLdT + j] = i >= j ? (uint16_t)f32_to_bf16_bits(qk[jt][r] * dij) : (uint16_t)0;
+    }
+  if (tid < kC) {
+    p.ws.gam[vidx * kC + tid] = expf(sG[tid]);
+    p.ws.dec[vidx * kC + tid] = expf(sG[kC - 1] - sG[tid]);  // padded tokens keep G: row of the last valid token
+  }
+  __syncthreads();
+  {
+    uint16_t* p_g = p.ws.p + vidx * kC * kC;
+    for (int i = tid; i < kC * kC / 8; i += 256) {
+      const int row = i >> 3, c8 = i & 7;
+      *reinterpret_cast<uint4*>(p_g + row * kC + 8 * c8) = *reinterpret_cast<const uint4*>(sP + row * kLdT + 8 * c8);
+    }
+  }
+  __syncthreads();
+
+  // ---- 5. Tinv = (I + L)^-1 ----
+  // 5a. the four 16 x 16 diagonal blocks by forward substitution (wave 0: lane = 16 * block + column);
+  //     the other waves zero the blocks above the diagonal
+  if (wave == 0) {
+    const int base = 16 * g4, col = l16;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = i == col ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc -= sL[(base + i) * kLdL + base + j] * t[j];
+      t[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sT[(base + i) * kLdL + base + col] = t[i];
+  } else {
+    for (int idx = tid - 64; idx < 6 * 256; idx += 192) {
+      const int pr = idx >> 8, e = idx & 255;  // block pairs (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+      const int rb = pr < 3 ? 0 : (pr < 5 ? 1 : 2);
+      const int cb = pr < 3 ? pr + 1 : (pr < 5 ? pr - 1 : 3);
+      sT[(16 * rb + (e >> 4)) * kLdL + 16 * cb + (e & 15)] = 0.f;
+    }
+  }
+  __syncthreads();
+  // 5b. 32 x 32 blocks: T21 = -T22 (L21 T11) with 16 x 16 parts (waves 0, 1: one 32-block each)
+  if (wave < 2) {
+    const int base = 32 * wave;
+    axk_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kq = 4 * st + g4;
+      x = mfma_f32_16x16x4(sL[(base + 16 + l16) * kLdL + base + kq], sT[(base + kq) * kLdL + base + l16], x);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sX[wave * 16 * 17 + (4 * g4 + r) * 17 + l16] = x[r];
+  }
+  __syncthreads();
+  if (wave < 2) {
+    const int base = 32 * wave;
+    axk_f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kq = 4 * st + g4;
+      y = mfma_f32_16x16x4(sT[(base + 16 + l16) * kLdL + base + 16 + kq], sX[wave * 16 * 17 + kq * 17 + l16], y);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sT[(base + 16 + 4 * g4 + r) * kLdL + base + l16] = -y[r];
+  }
+  __syncthreads();
+  // 5c. the 64 x 64 level: T21 = -T22 (L21 T11) with 32 x 32 parts (wave w: output tile (w / 2, w % 2))
+  {
+    const int rt = wave >> 1, ct = wave & 1;
+    axk_f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const int kq = 4 * st + g4;
+      x = mfma_f32_16x16x4(sL[(32 + 16 * rt + l16) * kLdL + kq], sT[kq * kLdL + 16 * ct + l16], x);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sX[(16 * rt + 4 * g4 + r) * kLdX + 16 * ct + l16] = x[r];
+    __syncthreads();
+    axk_f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const int kq = 4 * st + g4;
+      y = mfma_f32_16x16x4(sT[(32 + 16 * rt + l16) * kLdL + 32 + kq], sX[kq * kLdX + 16 * ct + l16], y);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sT[(32 + 16 * rt + 4 * g4 + r) * kLdL + 16 * ct + l16] = -y[r];
+  }
+  __syncthreads();
+
+  // ---- 6. bf16 operands: Tinv [C][LdT] (over L), (beta v)^T (over q), (beta Gamma k)^T (over fp32 Tinv) ----
+  uint16_t* sTb = reinterpret_cast<uint16_t*>(sL);
+  for (int i = tid; i < kC * kC; i += 256) {
+    const int r = i >> 6, cc = i & 63;
+    sTb[r * kLdT + cc] = (uint16_t)f32_to_bf16_bits(sT[r * kLdL + cc]);
+  }
+  __syncthreads();
+  uint16_t* sVB = sQ;
+  uint16_t* sKB = reinterpret_cast<uint16_t*>(sT);
+  {
+    const float beta = sBeta[tt], gm = expf(sG[tt]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = 32 * qd + 8 * i + 2 * j;
+        sVB[d * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_lo(vw[j]) * beta);
+        sVB[(d + 1) * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_hi(vw[j]) * beta);
+        sKB[d * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(sK[tt * kLdK + d]) * beta * gm);
+        sKB[(d + 1) * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(sK[tt * kLdK + d + 1]) * beta * gm);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 7. u = Tinv (beta v), w = Tinv (beta Gamma k): wave w owns token rows 16w .. 16w + 15 ----
+  axk_f32x4 ua[8], wa[8];
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) ua[ct] = wa[ct] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < kC / 32; ++st) {
+    const int ko = 32 * st + 8 * g4;
+    const axk_bf16x8 at = load_bf16x8(sTb + (16 * wave + l16) * kLdT + ko);
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      ua[ct] = mfma_bf16_16x16x32(at, load_bf16x8(sVB + (16 * ct + l16) * kLdT + ko), ua[ct]);
+      wa[ct] = mfma_bf16_16x16x32(at, load_bf16x8(sKB + (16 * ct + l16) * kLdT + ko), wa[ct]);
+    }
+  }
+  __syncthreads();
+
+  // ---- 8. stage u (over k) and w (over q), then coalesced writes ----
+  uint16_t* sU = sK;
+  uint16_t* sW = sQ;
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * g4 + r, d = 16 * ct + l16;
+      sU[i * kLdK + d] = (uint16_t)f32_to_bf16_bits(ua[ct][r]);
+      sW[i * kLdK + d] = (uint16_t)f32_to_bf16_bits(wa[ct][r]);
+    }
+  __syncthreads();
+  uint16_t* u_g = p.ws.u + vidx * kC * kD;
+  uint16_t* w_g = p.ws.w + vidx * kC * kD;
+  for (int i = tid; i < kC * kD / 8; i += 256) {
+    const int row = i >> 4, c8 = i & 15;
+    *reinterpret_cast<uint4*>(u_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sU + row * kLdK + 8 * c8);
+    *reinterpret_cast<uint4*>(w_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sW + row * kLdK + 8 * c8);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// scan: the state through the chunks, one 16-column slice per workgroup
+// ---------------------------------------------------------------------------------------------
+constexpr int kLdS = kD + 8;  // bf16 state slice in LDS, [16 columns][LdS] (8 consecutive rows per lane read)
+constexpr int kLdV = kC + 8;  // bf16 v_new and its decayed copy, [16 columns][LdV]
+
+struct ScanArgs {
+  const float* state_in;
+  float* state_out;
+  uint16_t* out;
+  ChunkWs ws;
+  int B, T, NK, NV, NC;
+};
+
+// One chunk's operands for one wave: rows 16w .. 16w + 15 of w, q and P; rows 32w .. 32w + 31 of k^T;
+// u, Gamma and last-row decay at the rows of the wave's output tile (16w + 4g + r).
+struct ScanOps {
+  axk_bf16x8 wf[4], qf[4], pf[2], kf[2][2];
+  uint32_t u[4];
+  float gm[4], dc[4], glast;
+};
+
+AXK_DEV void scan_load(ScanOps& s, const ScanArgs& p, int b, int bh, int kh, int c, int s0, int wave, int l16,
+                       int g4) {
+  const int64_t vidx = (int64_t)bh * p.NC + c;
+  const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;
+  const uint16_t* wg = p.ws.w + vidx * kC * kD + (16 * wave + l16) * kD + 8 * g4;
+  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (16 * wave + l16) * kD + 8 * g4;
+  const uint16_t* pg = p.ws.p + vidx * kC * kC + (16 * wave + l16) * kC + 8 * g4;
+  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (32 * wave + l16) * kC + 8 * g4;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    s.wf[st] = load_bf16x8(wg + 32 * st);
+    s.qf[st] = load_bf16x8(qg + 32 * st);
+  }
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    s.pf[st] = load_bf16x8(pg + 32 * st);
+    s.kf[0][st] = load_bf16x8(ktg + 32 * st);
+    s.kf[1][st] = load_bf16x8(ktg + 16 * kC + 32 * st);
+  }
+  const uint16_t* ug = p.ws.u + vidx * kC * kD + (16 * wave + 4 * g4) * kD + s0 + l16;
+  const float* gg = p.ws.gam + vidx * kC + 16 * wave + 4 * g4;
+  const float* dg = p.ws.dec + vidx * kC + 16 * wave + 4 * g4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    s.u[r] = ug[r * kD];
+    s.gm[r] = gg[r];
+    s.dc[r] = dg[r];
+  }
+  s.glast = p.ws.gam[vidx * kC + kC - 1];
+}
+
+__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
+  __shared__ __align__(16) uint16_t sS[16 * kLdS];
+  __shared__ __align__(16) uint16_t sV[16 * kLdV];
+  __shared__ __align__(16) uint16_t sXd[16 * kLdV];
+  const int nbh = p.B * p.NV;
+  const int slice = blockIdx.x / nbh, bh = blockIdx.x - slice * nbh;  // slices of a head share an XCD
+  const int b = bh / p.NV, h = bh - b * p.NV, kh = h / (p.NV / p.NK);
+  const int s0 = 16 * slice;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g4 = lane >> 4;
+
+  // state rows 32w + 16j + 4g + r, column s0 + l16, in two MFMA accumulator tiles
+  const float* sin = p.state_in + (int64_t)bh * kD * kD;
+  axk_f32x4 S[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[j][r] = sin[(32 * wave + 16 * j + 4 * g4 + r) * kD + s0 + l16];
+  auto put_state = [&]() {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<uint2*>(sS + l16 * kLdS + 32 * wave + 16 * j + 4 * g4) =
+          make_uint2(pack_bf16x2(S[j][0], S[j][1]), pack_bf16x2(S[j][2], S[j][3]));
+  };
+  put_state();
+  __syncthreads();
+
+  auto process = [&](const ScanOps& o, int c) {
+    // v_new = u - w S;  base = q S  (S as a bf16 operand, as the reference casts it)
+    axk_f32x4 vfs = {0.f, 0.f, 0.f, 0.f}, base = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const axk_bf16x8 sf = load_bf16x8(sS + l16 * kLdS + 32 * st + 8 * g4);
+      vfs = mfma_bf16_16x16x32(o.wf[st], sf, vfs);
+      base = mfma_bf16_16x16x32(o.qf[st], sf, base);
+    }
+    float vn[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vn[r] = bf16_bits_to_f32(o.u[r]) - vfs[r];
+    *reinterpret_cast<uint2*>(sV + l16 * kLdV + 16 * wave + 4 * g4) =
+        make_uint2(pack_bf16x2(vn[0], vn[1]), pack_bf16x2(vn[2], vn[3]));
+    *reinterpret_cast<uint2*>(sXd + l16 * kLdV + 16 * wave + 4 * g4) =
+        make_uint2(pack_bf16x2(vn[0] * o.dc[0], vn[1] * o.dc[1]), pack_bf16x2(vn[2] * o.dc[2], vn[3] * o.dc[3]));
+    __syncthreads();
+    // o = Gamma (q S) + P v_new
+    axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + l16 * kLdV + 32 * st + 8 * g4), acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = c * kC + 16 * wave + 4 * g4 + r;
+      if (t < p.T)
+        p.out[(((int64_t)b * p.T + t) * p.NV + h) * kD + s0 + l16] =
+            (uint16_t)f32_to_bf16_bits(base[r] * o.gm[r] + acc[r]);
+    }
+    // S <- Gamma_last S + k^T (v_new * decay_last)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[j][r] *= o.glast;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        S[j] = mfma_bf16_16x16x32(o.kf[j][st], load_bf16x8(sXd + l16 * kLdV + 32 * st + 8 * g4), S[j]);
+    }
+    put_state();
+    __syncthreads();
+  };
+
+  // three operand sets in rotation: chunk c + 2 is loaded while chunk c is processed
+  ScanOps o0, o1, o2;
+  scan_load(o0, p, b, bh, kh, 0, s0, wave, l16, g4);
+  if (p.NC > 1) scan_load(o1, p, b, bh, kh, 1, s0, wave, l16, g4);
+  for (int c = 0; c < p.NC; c += 3) {
+    if (c + 2 < p.NC) scan_load(o2, p, b, bh, kh, c + 2, s0, wave, l16, g4);
+    process(o0, c);
+    if (c + 1 >= p.NC) break;
+    if (c + 3 < p.NC) scan_load(o0, p, b, bh, kh, c + 3, s0, wave, l16, g4);
+    process(o1, c + 1);
+    if (c + 2 >= p.NC) break;
+    if (c + 4 < p.NC) scan_load(o1, p, b, bh, kh, c + 4, s0, wave, l16, g4);
+    process(o2, c + 2);
+  }
+
+  float* sout = p.state_out + (int64_t)bh * kD * kD;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sout[(32 * wave + 16 * j + 4 * g4 + r) * kD + s0 + l16] = S[j][r];
+}
+
+int check_chunk_dims(int64_t batch, int64_t tokens, int64_t nk, int64_t nv, int64_t dk, int64_t dv,
+                     int64_t chunk) {
+  AXK_REQUIRE(dk == kD && dv == kD && chunk == kC, AXK_E_SHAPE);
+  AXK_REQUIRE(batch > 0 && tokens > 0 && nk > 0 && nv > 0 && nv % nk == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(batch <= 65535 && nv <= 65535 && batch * nv * kSlices <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(tokens <= INT32_MAX - kC, AXK_E_SHAPE);
+  return AXK_OK;
+}
+
+}  // namespace
+
+extern "C" size_t axk_gdn_chunk_workspace_size(int64_t batch, int64_t tokens, int64_t num_k_heads,
+                                               int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim,
+                                               int64_t chunk_size) {
+  if (check_chunk_dims(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size) != AXK_OK)
+    return 0;
+  size_t off[7];
+  return chunk_ws_layout(batch, num_k_heads, num_v_heads, (tokens + kC - 1) / kC, off);
+}
+
+extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                     const uint16_t* b, const float* a_log, const float* dt_bias,
+                                     const float* state_in, float* state_out, uint16_t* out, int64_t batch,
+                                     int64_t tokens, int64_t num_k_heads, int64_t num_v_heads, int64_t head_k_dim,
+                                     int64_t head_v_dim, int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                                     axk_stream_t stream) {
+  AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
+  const int rc = check_chunk_dims(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size);
+  if (rc != AXK_OK) return rc;
+  AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(k, 16) && axk_aligned(v, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(axk_aligned(state_in, 16) && axk_aligned(state_out, 16), AXK_E_ALIGN);
+  const size_t need =
+      axk_gdn_chunk_workspace_size(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const size_t sbytes = (size_t)batch * num_v_heads * kD * kD * 4;
+  const size_t obytes = (size_t)batch * tokens * num_v_heads * kD * 2;
+  // in place is allowed (each workgroup reads its state slice before writing it); partial overlap is not
+  AXK_REQUIRE(state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
+  AXK_REQUIRE(!axk_overlap(out, obytes, state_out, sbytes) && !axk_overlap(out, obytes, workspace, need) &&
+                  !axk_overlap(state_out, sbytes, workspace, need),
+              AXK_E_ALIAS);
+  const int NC = (int)((tokens + kC - 1) / kC);
+  const ChunkWs ws = chunk_ws(workspace, batch, num_k_heads, num_v_heads, NC);
+  hipStream_t st = axk_stream(stream);
+  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gdn_chunk_prep_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrepLds) != hipSuccess)
+      return AXK_E_LAUNCH;
+    lds_raised = true;
+  }
+  PrepArgs pa{q, k, v, a, b, a_log, dt_bias, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC};
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((unsigned)NC, (unsigned)num_v_heads, (unsigned)batch), dim3(256),
+                     kPrepLds, st, pa);
+  int lrc = axk_launch_status();
+  if (lrc != AXK_OK) return lrc;
+  ScanArgs sa{state_in, state_out, out, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC};
+  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3((unsigned)(kSlices * batch * num_v_heads)), dim3(256), 0, st, sa);
+  return axk_launch_status();
+}

@@ -22,6 +22,7 @@ for _p in (ROOT, os.path.join(ROOT, "ax-dsl-kernels_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFS = 2500.0  # dense bf16 MFMA
 ROTATE_BYTES = 1 << 30
 METRIC = "µs/decode-layer + achieved HBM GB/s (% of 8 TB/s) for MXFP4 MoE + paged attn"
 
@@ -235,6 +236,60 @@ class GdnDecodeWorkload(Workload):
                 "sample": f"full config2a step (oracle/gdn.py gdn_fp32, torch CPU), median of {reps} runs"}
 
 
+class GdnPrefillWorkload(Workload):
+    """Config 2 prefill: GDN chunked prefill, B = 1, T = 4096, chunk 64, 32 value / 16 key heads, zero state.
+
+    One step = the chunk-parallel solve kernel + the state-scan kernel. Algorithmic bytes: q, k, v, a, b in,
+    output out, fp32 state in and out; algorithmic flops: the chunked form's products per (head, chunk)."""
+
+    name = "gdn_prefill"
+    kernel = "gdn chunk step (prep + scan)"
+    timing = "graph"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, gdn
+
+        c = configs.config2_prefill()
+        self.host = c
+        self.d = {k: v.to(dev) for k, v in c.items()}
+        b, t, nk, dk = c["q"].shape
+        nv = c["v"].shape[2]
+        st = c["state"]
+        self.alg_bytes = 2 * (c["q"].numel() + c["k"].numel() + 2 * c["v"].numel() + c["a"].numel() +
+                              c["b"].numel()) + 2 * st.numel() * 4
+        chunks = -(-t // 64)
+        per = 2 * 64 * 64 * dk * 5 + 2 * 64 * dk * dk * 3  # K K^T, Q K^T, u, w, P v_new; w S, q S, k^T X
+        self.alg_flops = b * nv * chunks * per
+        self.ws = gdn.gdn_chunk_workspace(b, t, nk, nv, dev)
+        self.state_out = torch.empty_like(self.d["state"])
+        self.out = torch.empty_like(self.d["v"])
+        self.config = {"workload": "config2b: GDN chunked prefill B=1 T=4096 C=64 NV=32 NK=16 d=128 (zero state)"}
+        self.dtype = "bf16 operands, fp32 accumulation / state"
+
+    def step(self, i: int) -> None:
+        from axk import gdn
+
+        d = self.d
+        gdn.gdn_chunk_prefill(d["q"], d["k"], d["v"], d["a"], d["b"], d["a_log"], d["dt_bias"], d["state"],
+                              state_out=self.state_out, output=self.out, workspace=self.ws)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import gdn as ogdn
+
+        c = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: ogdn.gdn_chunk(c["q"], c["k"], c["v"], c["a"], c["b"], c["a_log"],
+                                                      c["dt_bias"], c["state"], chunk=64, round_bf16=False),
+                              budget_s=10.0, min_reps=1, max_reps=5)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config2b prefill (oracle/gdn.py gdn_chunk fp32, torch CPU), median of {reps} runs"}
+
+
 class MoeDecodeWorkload(Workload):
     """Config 3a: MoE layer decode, 32 tokens, hidden 2048, 256 MXFP4 experts (inter 512) + shared, top-8.
 
@@ -320,7 +375,8 @@ class CopyCalibWorkload(Workload):
 
 
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
-             GdnDecodeWorkload.name: GdnDecodeWorkload, MoeDecodeWorkload.name: MoeDecodeWorkload,
+             GdnDecodeWorkload.name: GdnDecodeWorkload, GdnPrefillWorkload.name: GdnPrefillWorkload,
+             MoeDecodeWorkload.name: MoeDecodeWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
@@ -452,6 +508,9 @@ def main() -> int:
             suite[name] = {"us_per_op": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3),
                            "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                            "config": other.config["workload"]}
+            if getattr(other, "alg_flops", None) and other.name == "gdn_prefill":
+                tf = other.alg_flops / (kms * 1e-3) / 1e12
+                suite[name].update({"achieved_tflops": round(tf, 2), "bf16_mfma_frac": round(tf / BF16_PEAK_TFS, 4)})
             del other
             torch.cuda.empty_cache()
         line["suite"] = suite

@@ -188,6 +188,26 @@ int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, c
                       float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
                       int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream);
 
+/* Workspace bytes for axk_gdn_chunk_prefill (0 = unsupported shape). */
+size_t axk_gdn_chunk_workspace_size(int64_t batch, int64_t tokens, int64_t num_k_heads, int64_t num_v_heads,
+                                    int64_t head_k_dim, int64_t head_v_dim, int64_t chunk_size);
+
+/* GDN over `tokens` tokens in the chunked (WY / unit-lower solve) form: the same recurrence as
+ * axk_gdn_recurrent, computed chunk-parallel. Replaces gdn_stable_chunk + inverse_unit_lower_recursive +
+ * chunk_prefix_sum_fp32 (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/gdn.py:992-1212) as driven
+ * by gdn_prefill_impl (gdn.py:1628-1790) and q35_prefill.gdn_chunked
+ * (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:144-169). Rounding points as the reference: bf16 operands
+ * for every product (normalised q / k, beta, the inverse, u, w, q k^T * decay, the state, v_new), fp32
+ * accumulation and an fp32 state.
+ *   Tensors as axk_gdn_recurrent; chunk_size = 64; head dims 128. state_out == state_in: in place.
+ *   workspace >= axk_gdn_chunk_workspace_size(...), 256-byte aligned (per-chunk solve results; reused
+ *   freely between calls). */
+int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                          const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                          float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                          int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, int64_t chunk_size,
+                          void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * MoE with MXFP4 experts (router top-K, shared expert with sigmoid gate, routed SwiGLU experts)
  * ------------------------------------------------------------------------------------------- */

@@ -1,4 +1,5 @@
 """Pins the GDN oracle (CPU only)."""
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -64,3 +65,50 @@ def test_reference_golden_close_to_fp32():
     o32, s32 = gdn.gdn_fp32(q, k, v, a, b, a_log, dt_bias, s)
     torch.testing.assert_close(o_ref.float(), o32, rtol=2e-2, atol=1e-2)
     torch.testing.assert_close(s_ref, s32, rtol=2e-2, atol=1e-2)
+
+
+def test_chunk_fp32_matches_transformers_chunk_rule():
+    from transformers.models.qwen3_5.modeling_qwen3_5 import torch_chunk_gated_delta_rule
+
+    q, k, v, a, b, a_log, dt_bias, s = _case(B=2, T=150, NK=2, NV=4, D=32, seed=3)
+    g, beta = gdn.gates(a, b, a_log, dt_bias)
+    rep = v.shape[2] // q.shape[2]
+    for chunk in (16, 64):
+        out, st = gdn.gdn_chunk(q, k, v, a, b, a_log, dt_bias, s, chunk=chunk, round_bf16=False)
+        ref_out, ref_st = torch_chunk_gated_delta_rule(
+            q.float().repeat_interleave(rep, 2), k.float().repeat_interleave(rep, 2), v.float(), g, beta, chunk,
+            s.clone(), True, use_qk_l2norm_in_kernel=True)
+        torch.testing.assert_close(out, ref_out.float(), rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(st, ref_st.float(), rtol=1e-5, atol=1e-5)
+
+
+def test_chunked_equals_recurrent():
+    # the chunked form is an exact rewrite of the recurrence (q35_prefill.py:439-463 checks the same)
+    q, k, v, a, b, a_log, dt_bias, s = _case(B=1, T=97, NK=1, NV=2, D=32, seed=4)
+    out, st = gdn.gdn_chunk(q, k, v, a, b, a_log, dt_bias, s, chunk=32, round_bf16=False)
+    ref_out, ref_st = gdn.gdn_fp32(q, k, v, a, b, a_log, dt_bias, s)
+    torch.testing.assert_close(out, ref_out, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(st, ref_st, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("size,batch", [(1, 1), (2, 2), (17, 1), (32, 2), (64, 1), (256, 2)])
+def test_unit_lower_inverse_reference_cases(size, batch):
+    # the correlated strictly-lower matrices of test_gdn_attn.py:738-768, against a triangular solve
+    pos = torch.arange(size)
+    dist = pos[:, None] - pos[None, :]
+    neg = torch.tril(-0.96 * torch.exp(-0.012 * dist.float()), diagonal=-1)
+    if batch > 1:
+        neg = torch.stack((neg, neg * 0.7))
+    eye = torch.eye(size, dtype=torch.float64).expand(neg.shape)
+    expected = torch.linalg.solve_triangular(eye - neg.double(), eye, upper=False)
+    got = gdn.unit_lower_inverse(neg)
+    torch.testing.assert_close(got.double(), expected, rtol=2e-5, atol=2e-6)
+    torch.testing.assert_close((eye - neg.double()) @ got.double(), eye, rtol=0, atol=3e-6)
+
+
+def test_chunk_bf16_schedule_close_to_fp32():
+    q, k, v, a, b, a_log, dt_bias, s = _case(B=1, T=130, NK=2, NV=4, D=128, seed=5)
+    out, st = gdn.gdn_chunk(q, k, v, a, b, a_log, dt_bias, s, chunk=64, round_bf16=True)
+    ref_out, ref_st = gdn.gdn_fp32(q, k, v, a, b, a_log, dt_bias, s)
+    torch.testing.assert_close(out.float(), ref_out, rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(st, ref_st, rtol=5e-2, atol=3e-3)  # test_gdn_attn.py temporal tolerance
