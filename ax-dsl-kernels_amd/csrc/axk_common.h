@@ -20,12 +20,17 @@ typedef float axk_f32x2 __attribute__((ext_vector_type(2)));
 
 AXK_DEV float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+// fp32 -> bf16 bits, round to nearest even (gfx950's v_cvt_pk_bf16_f32); NaN stays a quiet NaN.
 AXK_DEV uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const __bf16 b = (__bf16)f;
+  return (uint32_t)__builtin_bit_cast(uint16_t, b);
+}
+
+// Two fp32 -> packed bf16 pair (low half = lo), one conversion instruction.
+AXK_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const axk_bf16x2 r = __builtin_convertvector((f2){lo, hi}, axk_bf16x2);
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 AXK_DEV float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }

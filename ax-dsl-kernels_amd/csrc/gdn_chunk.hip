@@ -31,8 +31,9 @@ constexpr int kC = 64;    // chunk length
 constexpr int kD = 128;   // key / value head dim
 constexpr int kSlices = kD / 16;
 
-// Workspace: per (sequence, value head, chunk) w, u [C][D] bf16, P [C][C] bf16, Gamma and last-row decay
-// [C] fp32; per (sequence, key head, chunk) normalised q [C][D] bf16 and k^T [D][C] bf16.
+// Workspace: per (sequence, value head, chunk) w [C][D] bf16, u in the scan's accumulator order
+// [D/16 slices][4 waves][64 lanes][4 rows] bf16, P [C][C] bf16, Gamma and last-row decay [C] fp32; per
+// (sequence, key head, chunk) normalised q [C][D] bf16 and k^T [D][C] bf16.
 struct ChunkWs {
   uint16_t* w;
   uint16_t* u;
@@ -69,7 +70,6 @@ ChunkWs chunk_ws(void* ws, int64_t B, int64_t NK, int64_t NV, int64_t NC) {
 
 AXK_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 AXK_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-AXK_DEV uint32_t pack_bf16x2(float lo, float hi) { return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16); }
 
 AXK_DEV axk_f32x4 mfma_f32_16x16x4(float a, float b, axk_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -83,7 +83,7 @@ constexpr int kLdT = kC + 8;  // bf16 row stride of [D][C] and [C][C] tiles
 constexpr int kLdL = kC + 4;  // fp32 row stride of [C][C] tiles
 constexpr int kLdX = 32 + 1;  // fp32 scratch of the solve's block products
 
-constexpr int kOffK = 0;                  // k (bf16 [C][LdK]); later u staging
+constexpr int kOffK = 0;                  // k (bf16 [C][LdK])
 constexpr int kSzK = kC * kLdK * 2;
 constexpr int kOffQ = kOffK + kSzK;       // q (bf16 [C][LdK]); then (beta v)^T (bf16 [D][LdT]); later w staging
 constexpr int kSzQ = kD * kLdT * 2;
@@ -369,23 +369,21 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   }
   __syncthreads();
 
-  // ---- 8. stage u (over k) and w (over q), then coalesced writes ----
-  uint16_t* sU = sK;
+  // ---- 8. u straight from the accumulators in the scan's order; w staged (over q) for row-major writes ----
+  uint16_t* u_g = p.ws.u + vidx * kC * kD;
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct)
+    *reinterpret_cast<uint2*>(u_g + ((ct * 4 + wave) * 64 + lane) * 4) =
+        make_uint2(pack_bf16x2(ua[ct][0], ua[ct][1]), pack_bf16x2(ua[ct][2], ua[ct][3]));
   uint16_t* sW = sQ;
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * wave + 4 * g4 + r, d = 16 * ct + l16;
-      sU[i * kLdK + d] = (uint16_t)f32_to_bf16_bits(ua[ct][r]);
-      sW[i * kLdK + d] = (uint16_t)f32_to_bf16_bits(wa[ct][r]);
-    }
+    for (int r = 0; r < 4; ++r) sW[(16 * wave + 4 * g4 + r) * kLdK + 16 * ct + l16] = (uint16_t)f32_to_bf16_bits(wa[ct][r]);
   __syncthreads();
-  uint16_t* u_g = p.ws.u + vidx * kC * kD;
   uint16_t* w_g = p.ws.w + vidx * kC * kD;
   for (int i = tid; i < kC * kD / 8; i += 256) {
     const int row = i >> 4, c8 = i & 15;
-    *reinterpret_cast<uint4*>(u_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sU + row * kLdK + 8 * c8);
     *reinterpret_cast<uint4*>(w_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sW + row * kLdK + 8 * c8);
   }
 }
@@ -408,8 +406,9 @@ struct ScanArgs {
 // u, Gamma and last-row decay at the rows of the wave's output tile (16w + 4g + r).
 struct ScanOps {
   axk_bf16x8 wf[4], qf[4], pf[2], kf[2][2];
-  uint32_t u[4];
-  float gm[4], dc[4], glast;
+  uint2 u;
+  float4 gm, dc;
+  float glast;
 };
 
 AXK_DEV void scan_load(ScanOps& s, const ScanArgs& p, int b, int bh, int kh, int c, int s0, int wave, int l16,
@@ -431,16 +430,13 @@ AXK_DEV void scan_load(ScanOps& s, const ScanArgs& p, int b, int bh, int kh, int
     s.kf[0][st] = load_bf16x8(ktg + 32 * st);
     s.kf[1][st] = load_bf16x8(ktg + 16 * kC + 32 * st);
   }
-  const uint16_t* ug = p.ws.u + vidx * kC * kD + (16 * wave + 4 * g4) * kD + s0 + l16;
-  const float* gg = p.ws.gam + vidx * kC + 16 * wave + 4 * g4;
-  const float* dg = p.ws.dec + vidx * kC + 16 * wave + 4 * g4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    s.u[r] = ug[r * kD];
-    s.gm[r] = gg[r];
-    s.dc[r] = dg[r];
-  }
-  s.glast = p.ws.gam[vidx * kC + kC - 1];
+  s.u = *reinterpret_cast<const uint2*>(p.ws.u + vidx * kC * kD + (((s0 >> 4) * 4 + wave) * 64 + 16 * g4 + l16) * 4);
+  s.gm = *reinterpret_cast<const float4*>(p.ws.gam + vidx * kC + 16 * wave + 4 * g4);
+  s.dc = *reinterpret_cast<const float4*>(p.ws.dec + vidx * kC + 16 * wave + 4 * g4);
+  // a per-lane load (an index the compiler cannot prove uniform): a scalar load here would be waited for at once
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  s.glast = p.ws.gam[vidx * kC + kC - 1 + z];
 }
 
 __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
@@ -479,23 +475,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
       base = mfma_bf16_16x16x32(o.qf[st], sf, base);
     }
     float vn[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vn[r] = bf16_bits_to_f32(o.u[r]) - vfs[r];
+    vn[0] = bf16_lo(o.u.x) - vfs[0];
+    vn[1] = bf16_hi(o.u.x) - vfs[1];
+    vn[2] = bf16_lo(o.u.y) - vfs[2];
+    vn[3] = bf16_hi(o.u.y) - vfs[3];
     *reinterpret_cast<uint2*>(sV + l16 * kLdV + 16 * wave + 4 * g4) =
         make_uint2(pack_bf16x2(vn[0], vn[1]), pack_bf16x2(vn[2], vn[3]));
     *reinterpret_cast<uint2*>(sXd + l16 * kLdV + 16 * wave + 4 * g4) =
-        make_uint2(pack_bf16x2(vn[0] * o.dc[0], vn[1] * o.dc[1]), pack_bf16x2(vn[2] * o.dc[2], vn[3] * o.dc[3]));
+        make_uint2(pack_bf16x2(vn[0] * o.dc.x, vn[1] * o.dc.y), pack_bf16x2(vn[2] * o.dc.z, vn[3] * o.dc.w));
     __syncthreads();
     // o = Gamma (q S) + P v_new
     axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + l16 * kLdV + 32 * st + 8 * g4), acc);
+    const float gmr[4] = {o.gm.x, o.gm.y, o.gm.z, o.gm.w};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = c * kC + 16 * wave + 4 * g4 + r;
       if (t < p.T)
         p.out[(((int64_t)b * p.T + t) * p.NV + h) * kD + s0 + l16] =
-            (uint16_t)f32_to_bf16_bits(base[r] * o.gm[r] + acc[r]);
+            (uint16_t)f32_to_bf16_bits(base[r] * gmr[r] + acc[r]);
     }
     // S <- Gamma_last S + k^T (v_new * decay_last)
 #pragma unroll
@@ -510,19 +509,20 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
     __syncthreads();
   };
 
-  // three operand sets in rotation: chunk c + 2 is loaded while chunk c is processed
+  // Three operand sets in rotation: chunk c + 2 is loaded while chunk c is processed. The loads are
+  // unconditional (past the end they repeat the last chunk, unused) so every path through the loop has the
+  // same loads in flight and the waits before each use stay two sets deep.
+  const int last = p.NC - 1;
   ScanOps o0, o1, o2;
   scan_load(o0, p, b, bh, kh, 0, s0, wave, l16, g4);
-  if (p.NC > 1) scan_load(o1, p, b, bh, kh, 1, s0, wave, l16, g4);
+  scan_load(o1, p, b, bh, kh, min(1, last), s0, wave, l16, g4);
   for (int c = 0; c < p.NC; c += 3) {
-    if (c + 2 < p.NC) scan_load(o2, p, b, bh, kh, c + 2, s0, wave, l16, g4);
+    scan_load(o2, p, b, bh, kh, min(c + 2, last), s0, wave, l16, g4);
     process(o0, c);
-    if (c + 1 >= p.NC) break;
-    if (c + 3 < p.NC) scan_load(o0, p, b, bh, kh, c + 3, s0, wave, l16, g4);
-    process(o1, c + 1);
-    if (c + 2 >= p.NC) break;
-    if (c + 4 < p.NC) scan_load(o1, p, b, bh, kh, c + 4, s0, wave, l16, g4);
-    process(o2, c + 2);
+    scan_load(o0, p, b, bh, kh, min(c + 3, last), s0, wave, l16, g4);
+    if (c + 1 < p.NC) process(o1, c + 1);
+    scan_load(o1, p, b, bh, kh, min(c + 4, last), s0, wave, l16, g4);
+    if (c + 2 < p.NC) process(o2, c + 2);
   }
 
   float* sout = p.state_out + (int64_t)bh * kD * kD;
