@@ -18,6 +18,15 @@
 //   down    — one workgroup per (expert, 64 hidden rows): act x Wd^T, scaled by the pair's routing weight
 //   combine — one workgroup per token: shared gate, residual, sum over the token's K experts in slot order
 // Every expert's weights are read once per call, whatever the number of its tokens.
+//
+// Prefill (tokens > kDecodeTokens; moe_slots_px + moe_combine of q35_moe_prefill.py:150-214):
+//   pcount / pscan / pscatter — the pairs grouped by expert in 256-token blocks (per-block bitmask counts, one
+//             scan of the (expert, block) bases, stable scatter), plus a tile list of kBM-row tiles per active
+//             expert and for the shared expert over all tokens
+//   ggemm   — a grouped GEMM on MFMA: workgroup = (tile, kBN output columns), A rows gathered by token and
+//             staged in LDS, MXFP4 B tiles staged in LDS and decoded into bf16 fragments; gate-up with the SwiGLU
+//             epilogue, then down with the routing-weight epilogue
+//   combine — as decode
 #include "axk_common.h"
 #include "axk_host.h"
 #include "axk_mx_tile.h"
@@ -31,6 +40,11 @@ constexpr int kMaxTopK = 32;  // <= 64: lane k of the routing wave keeps selecti
 constexpr int kMaxPairs = 8192;
 constexpr int kMaskWords = 4;  // token bitmask words per expert in the grouping kernel: tokens <= 256
 constexpr int kMaxTokensPerChunk = 32;  // M rows per pass (2 MFMA tiles)
+constexpr int kDecodeTokens = 64 * kMaskWords;  // above this the prefill path runs
+constexpr int64_t kMaxPrefillTokens = 1 << 16;
+constexpr int64_t kMaxPrefillPairs = 1 << 19;
+constexpr int kBlkTokens = 256;  // tokens per block of the prefill grouping
+constexpr int kBM = 64, kBN = 128, kBK = 64;  // prefill GEMM tile
 
 struct MoeWs {
   int* counts;      // [E]
@@ -46,18 +60,30 @@ struct MoeWs {
   uint16_t* act_sh; // [T, Fs] bf16 shared-expert activations
   float* y;         // [P, H] fp32 routed outputs x routing weight
   float* y_sh;      // [T, H] fp32 shared-expert output
+  int* blk;         // [NB, E] prefill: per-block expert counts, then per-block row bases
+  int4* tiles;      // [max tiles] prefill GEMM tiles: {expert (-1: shared), first row, rows, 0}
+  int* n_tiles;     // [1]
 };
+
+int64_t prefill_blocks(int64_t T) { return (T + kBlkTokens - 1) / kBlkTokens; }
+int64_t prefill_max_tiles(int64_t T, int64_t E, int64_t K) {
+  return (T * K + kBM - 1) / kBM + E + (T + kBM - 1) / kBM;
+}
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+constexpr int kWsParts = 16;
+
 size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs, size_t* off) {
   const int64_t P = T * K;
+  const bool prefill = T > kDecodeTokens;
+  const size_t nb = prefill ? (size_t)prefill_blocks(T) : 0, nt = prefill ? (size_t)prefill_max_tiles(T, E, K) : 0;
   size_t o = 0;
-  const size_t sizes[13] = {(size_t)E * 4,     (size_t)(E + 1) * 4, (size_t)E * 4,      (size_t)E * 4,
-                            (size_t)E * 4,     4,                   (size_t)P * 4,      (size_t)P * 4,
-                            (size_t)P * 4,     (size_t)P * F * 2,   (size_t)T * Fs * 2, (size_t)P * H * 4,
-                            (size_t)T * H * 4};
-  for (int i = 0; i < 13; ++i) {
+  const size_t sizes[kWsParts] = {(size_t)E * 4,     (size_t)(E + 1) * 4, (size_t)E * 4,      (size_t)E * 4,
+                                  (size_t)E * 4,     4,                   (size_t)P * 4,      (size_t)P * 4,
+                                  (size_t)P * 4,     (size_t)P * F * 2,   (size_t)T * Fs * 2, (size_t)P * H * 4,
+                                  (size_t)T * H * 4, nb * E * 4,          nt * 16,            4};
+  for (int i = 0; i < kWsParts; ++i) {
     off[i] = o;
     o = align256(o + sizes[i]);
   }
@@ -65,7 +91,7 @@ size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int6
 }
 
 MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs) {
-  size_t off[13];
+  size_t off[kWsParts];
   moe_ws_layout(T, H, E, K, F, Fs, off);
   unsigned char* b = reinterpret_cast<unsigned char*>(ws);
   return {reinterpret_cast<int*>(b + off[0]),       reinterpret_cast<int*>(b + off[1]),
@@ -74,7 +100,8 @@ MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, in
           reinterpret_cast<int*>(b + off[6]),       reinterpret_cast<int*>(b + off[7]),
           reinterpret_cast<float*>(b + off[8]),     reinterpret_cast<uint16_t*>(b + off[9]),
           reinterpret_cast<uint16_t*>(b + off[10]), reinterpret_cast<float*>(b + off[11]),
-          reinterpret_cast<float*>(b + off[12])};
+          reinterpret_cast<float*>(b + off[12]),    reinterpret_cast<int*>(b + off[13]),
+          reinterpret_cast<int4*>(b + off[14]),     reinterpret_cast<int*>(b + off[15])};
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -425,6 +452,286 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   a.out[(int64_t)t * a.H + i] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
+// ---------------------------------------------------------------------------------------------
+// prefill grouping: 256-token blocks
+// ---------------------------------------------------------------------------------------------
+// Per-expert token bitmasks of block `blk` in LDS (4 words per expert); pairs with an id outside [0, E) are
+// left out.
+__device__ void block_masks(const int32_t* __restrict__ ids, int T, int E, int K, int blk,
+                            unsigned long long* s_mask) {
+  const int t0 = blk * kBlkTokens, nt = min(kBlkTokens, T - t0);
+  for (int i = threadIdx.x; i < E * kMaskWords; i += blockDim.x) s_mask[i] = 0ull;
+  __syncthreads();
+  for (int p = threadIdx.x; p < nt * K; p += blockDim.x) {
+    const int t = p / K, e = ids[(int64_t)t0 * K + p];
+    if (e >= 0 && e < E) atomicOr(&s_mask[e * kMaskWords + (t >> 6)], 1ull << (t & 63));
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void moe_pcount_kernel(const int32_t* __restrict__ ids, int T, int E, int K,
+                                                         MoeWs w) {
+  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
+  block_masks(ids, T, E, K, blockIdx.x, s_mask);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kMaskWords; ++i) c += __popcll(s_mask[e * kMaskWords + i]);
+    w.blk[(int64_t)blockIdx.x * E + e] = c;
+  }
+}
+
+// One workgroup: expert totals, offsets and active list; per-(block, expert) row bases (in place of the
+// counts); the GEMM tile list (routed experts in expert order, then the shared expert's tiles).
+__global__ __launch_bounds__(256) void moe_pscan_kernel(int T, int E, int NB, int has_shared, MoeWs w) {
+  __shared__ int s_tmp[12];
+  constexpr int EPT = kMaxExperts / 256;
+  const int tid = threadIdx.x;
+  int cnt[EPT], sum = 0, nact = 0, ntile = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
+    int c = 0;
+    if (e < E)
+      for (int b = 0; b < NB; ++b) c += w.blk[(int64_t)b * E + e];
+    cnt[j] = c;
+    sum += c;
+    nact += c > 0;
+    ntile += (c + kBM - 1) / kBM;
+  }
+  int tot, tota, tott;
+  int off = block_exclusive_scan256(sum, s_tmp, &tot);
+  int aoff = block_exclusive_scan256(nact, s_tmp + 4, &tota);
+  int toff = block_exclusive_scan256(ntile, s_tmp + 8, &tott);
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid * EPT + j;
+    if (e < E) {
+      w.counts[e] = cnt[j];
+      w.offsets[e] = off;
+      int base = off;
+      for (int b = 0; b < NB; ++b) {
+        const int c = w.blk[(int64_t)b * E + e];
+        w.blk[(int64_t)b * E + e] = base;
+        base += c;
+      }
+      if (cnt[j] > 0) {
+        w.active_e[aoff] = e;
+        w.active_off[aoff] = off;
+        w.active_cnt[aoff] = cnt[j];
+        ++aoff;
+      }
+      for (int r = 0; r < cnt[j]; r += kBM) w.tiles[toff++] = make_int4(e, off + r, min(kBM, cnt[j] - r), 0);
+    }
+    off += cnt[j];
+  }
+  const int nsh = has_shared ? (T + kBM - 1) / kBM : 0;
+  for (int i = tid; i < nsh; i += blockDim.x) w.tiles[tott + i] = make_int4(-1, i * kBM, min(kBM, T - i * kBM), 0);
+  if (tid == 0) {
+    w.offsets[E] = tot;
+    *w.n_active = tota;
+    *w.n_tiles = tott + nsh;
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __restrict__ ids,
+                                                           const float* __restrict__ wts, int T, int E, int K,
+                                                           MoeWs w) {
+  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
+  const int blk = blockIdx.x, t0 = blk * kBlkTokens, nt = min(kBlkTokens, T - t0);
+  block_masks(ids, T, E, K, blk, s_mask);
+  for (int q = threadIdx.x; q < nt * K; q += blockDim.x) {
+    const int64_t p = (int64_t)t0 * K + q;
+    const int e = ids[p], t = q / K;
+    if (e < 0 || e >= E) {
+      w.pair_pos[p] = -1;
+      continue;
+    }
+    const unsigned long long* m = s_mask + e * kMaskWords;
+    int rank = __popcll(m[t >> 6] & ((1ull << (t & 63)) - 1ull));
+    for (int i = 0; i < (t >> 6); ++i) rank += __popcll(m[i]);
+    const int pos = w.blk[(int64_t)blk * E + e] + rank;
+    w.pair_pos[p] = pos;
+    w.row_tok[pos] = t0 + t;
+    w.row_w[pos] = wts[p];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// prefill grouped GEMM: workgroup (tile of kBM rows of one expert, kBN output columns), 4 waves as 2 x 2
+// ---------------------------------------------------------------------------------------------
+constexpr int kLdA = kBK + 8;  // bf16 elements per staged activation row
+constexpr int kLdB = 48;       // bytes per staged weight row of a K step (32 code bytes + pad)
+constexpr int kBufBytes = kBM * kLdA * 2 + kBN * kLdB + kBN * 2;
+
+struct GGemmArgs {
+  const uint16_t* a;     // gate-up: h2 [T, H]; down: act [P, F]
+  const uint16_t* a_sh;  // down: act_sh [T, Fs]
+  const uint8_t *w, *s;  // routed: gate-up e_gw / e_gs [E, 2F, H/2 | H/32]; down e_dw / e_ds [E, H, F/2 | F/32]
+  const uint8_t *w_sh, *s_sh, *u_sh, *us_sh;  // shared: gate-up gate and up [Fs, H/2]; down [H, Fs/2] (w_sh, s_sh)
+  int T, H, F, Fs;
+  MoeWs ws;
+};
+
+// MODE 0: gate-up + SwiGLU -> act (routed) / act_sh (shared); columns 64 n of gate and the same of up.
+// MODE 1: down -> y = acc * routing weight (routed) / y_sh (shared); 128 columns of H.
+template <int MODE>
+__global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
+  __shared__ __align__(16) unsigned char smem[2 * kBufBytes];
+  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
+  const int4 tl = g.ws.tiles[blockIdx.x];
+  const int e = tl.x, row0 = tl.y, rows = tl.z;
+  const bool shared = e < 0;
+  const int nt = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const int l16 = lane & 15, g4 = lane >> 4;
+
+  // shapes of this tile's GEMM
+  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);          // reduction length
+  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;          // output columns
+  const int col0 = MODE == 0 ? 64 * nt : kBN * nt;
+  if (col0 >= No) return;
+
+  // this thread's staged activation row and weight row
+  const int arow = tid >> 2, aq = tid & 3;           // 16 activation values of a 64-wide K step
+  const int brow = tid >> 1, bh = tid & 1;           // 32 codes (one E8M0 block) of a weight row
+  const uint16_t* asrc = nullptr;
+  if (arow < rows) {
+    if (MODE == 0) {
+      const int tok = shared ? row0 + arow : g.ws.row_tok[row0 + arow];
+      asrc = g.a + (int64_t)tok * g.H;
+    } else {
+      asrc = shared ? g.a_sh + (int64_t)(row0 + arow) * g.Fs : g.a + (int64_t)(row0 + arow) * g.F;
+    }
+  }
+  const uint8_t* bsrc = nullptr;
+  const uint8_t* ssrc = nullptr;
+  {
+    int wr;  // weight row in its matrix
+    const uint8_t *wb, *sb;
+    if (MODE == 0) {
+      const bool up = brow >= 64;
+      wr = col0 + (brow & 63);
+      if (shared) {
+        wb = up ? g.u_sh : g.w_sh;
+        sb = up ? g.us_sh : g.s_sh;
+      } else {
+        const int64_t rows2 = 2 * (int64_t)g.F;
+        wb = g.w + (int64_t)e * rows2 * (g.H / 2) + (up ? (int64_t)g.F * (g.H / 2) : 0);
+        sb = g.s + (int64_t)e * rows2 * (g.H / 32) + (up ? (int64_t)g.F * (g.H / 32) : 0);
+      }
+    } else {
+      wr = col0 + brow;
+      wb = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
+      sb = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
+    }
+    if (wr < No) {
+      bsrc = wb + (int64_t)wr * (Kd / 2);
+      ssrc = sb + (int64_t)wr * (Kd / 32);
+    }
+  }
+
+  // B rows of this wave's four 16-column tiles (gate-up: two gate tiles, then the same two of up)
+  int boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) boff[j] = MODE == 0 ? (j < 2 ? 32 * wn + 16 * j : 64 + 32 * wn + 16 * (j - 2)) : 64 * wn + 16 * j;
+
+  uint4 ra0, ra1, rb;
+  uint32_t rs;
+  auto load = [&](int k0) {
+    ra0 = ra1 = rb = make_uint4(0u, 0u, 0u, 0u);
+    rs = 127u;
+    if (asrc && k0 + 16 * aq < Kd) {
+      ra0 = *reinterpret_cast<const uint4*>(asrc + k0 + 16 * aq);
+      ra1 = *reinterpret_cast<const uint4*>(asrc + k0 + 16 * aq + 8);
+    }
+    if (bsrc && k0 + 32 * bh < Kd) {
+      rb = *reinterpret_cast<const uint4*>(bsrc + (k0 + 32 * bh) / 2);
+      rs = ssrc[(k0 + 32 * bh) / 32];
+    }
+  };
+  auto store = [&](int buf) {
+    unsigned char* base = smem + buf * kBufBytes;
+    uint16_t* sA = reinterpret_cast<uint16_t*>(base);
+    unsigned char* sB = base + kBM * kLdA * 2;
+    unsigned char* sS = sB + kBN * kLdB;
+    *reinterpret_cast<uint4*>(sA + arow * kLdA + 16 * aq) = ra0;
+    *reinterpret_cast<uint4*>(sA + arow * kLdA + 16 * aq + 8) = ra1;
+    *reinterpret_cast<uint4*>(sB + brow * kLdB + 16 * bh) = rb;
+    sS[brow * 2 + bh] = (unsigned char)rs;
+  };
+
+  axk_f32x4 acc[2][4];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = Kd / kBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ++ks) {
+    if (ks + 1 < nk) load((ks + 1) * kBK);
+    const unsigned char* base = smem + (ks & 1) * kBufBytes;
+    const uint16_t* sA = reinterpret_cast<const uint16_t*>(base);
+    const unsigned char* sB = base + kBM * kLdA * 2;
+    const unsigned char* sS = sB + kBN * kLdB;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      axk_bf16x8 af[2], bf[4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) af[mt] = load_bf16x8(sA + (32 * wm + 16 * mt + l16) * kLdA + 32 * kh + 8 * g4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = boff[j] + l16;
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(sB + r * kLdB + 16 * kh + 4 * g4);
+        bf[j] = fp4x8_to_bf16x8(word, e8m0_to_f32(sS[r * 2 + kh]));
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
+    }
+    if (ks + 1 < nk) store((ks + 1) & 1);
+    __syncthreads();
+  }
+
+  // epilogue: rows 32 wm + 16 mt + 4 g + r of the tile
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 32 * wm + 16 * mt + 4 * g4 + r;
+      if (row >= rows) continue;
+      const int64_t prow = row0 + row;
+      if (MODE == 0) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int col = col0 + 32 * wn + 16 * jj + l16;
+          if (col >= No) continue;
+          const float gv = round_bf16(acc[mt][jj][r]), uv = round_bf16(acc[mt][2 + jj][r]);
+          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+          if (shared)
+            g.ws.act_sh[prow * g.Fs + col] = a;
+          else
+            g.ws.act[prow * g.F + col] = a;
+        }
+      } else {
+        const float rw = shared ? 1.0f : g.ws.row_w[prow];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = col0 + 64 * wn + 16 * j + l16;
+          if (col >= No) continue;
+          if (shared)
+            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
+          else
+            g.ws.y[prow * g.H + col] = acc[mt][j][r] * rw;
+        }
+      }
+    }
+}
+
 struct MoeDims {
   int64_t T, H, E, K, F, Fs;
 };
@@ -432,8 +739,13 @@ struct MoeDims {
 int check_dims(const MoeDims& d) {
   AXK_REQUIRE(d.T > 0 && d.H > 0 && d.E > 0 && d.K > 0 && d.F > 0, AXK_E_SHAPE);
   AXK_REQUIRE(d.E <= kMaxExperts && d.K <= kMaxTopK && d.K <= d.E, AXK_E_SHAPE);
-  AXK_REQUIRE(d.T * d.K <= kMaxPairs && d.T <= 64 * kMaskWords, AXK_E_SHAPE);
-  AXK_REQUIRE(d.H % 64 == 0 && d.F % 32 == 0 && d.Fs % 32 == 0 && d.Fs >= 0, AXK_E_SHAPE);
+  if (d.T <= kDecodeTokens) {
+    AXK_REQUIRE(d.T * d.K <= kMaxPairs, AXK_E_SHAPE);
+    AXK_REQUIRE(d.H % 64 == 0 && d.F % 32 == 0 && d.Fs % 32 == 0 && d.Fs >= 0, AXK_E_SHAPE);
+  } else {  // prefill GEMM: whole 64-wide K steps and 64-column gate / up tiles
+    AXK_REQUIRE(d.T <= kMaxPrefillTokens && d.T * d.K <= kMaxPrefillPairs, AXK_E_SHAPE);
+    AXK_REQUIRE(d.H % 64 == 0 && d.F % 64 == 0 && d.Fs % 64 == 0 && d.Fs >= 0, AXK_E_SHAPE);
+  }
   AXK_REQUIRE(d.H <= INT32_MAX && d.F <= INT32_MAX, AXK_E_SHAPE);
   return AXK_OK;
 }
@@ -443,7 +755,7 @@ int check_dims(const MoeDims& d) {
 extern "C" size_t axk_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
                                          int64_t inter, int64_t shared_inter) {
   if (check_dims({tokens, hidden, num_experts, top_k, inter, shared_inter}) != AXK_OK) return 0;
-  size_t off[13];
+  size_t off[kWsParts];
   return moe_ws_layout(tokens, hidden, num_experts, top_k, inter, shared_inter, off);
 }
 
@@ -490,6 +802,21 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   hipStream_t st = axk_stream(stream);
   const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, d.Fs);
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, F = (int)inter, Fs = (int)d.Fs;
+  if (T > kDecodeTokens) {
+    const int NB = (int)prefill_blocks(T);
+    hipLaunchKernelGGL(moe_pcount_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, T, E, K, w);
+    hipLaunchKernelGGL(moe_pscan_kernel, dim3(1), dim3(256), 0, st, T, E, NB, has_shared ? 1 : 0, w);
+    hipLaunchKernelGGL(moe_pscatter_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
+    const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
+    const int fmax = F > Fs ? F : Fs;
+    GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, w};
+    hipLaunchKernelGGL(moe_ggemm_kernel<0>, dim3(tiles, (unsigned)(fmax / 64)), dim3(256), 0, st, gu);
+    GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, w};
+    hipLaunchKernelGGL(moe_ggemm_kernel<1>, dim3(tiles, (unsigned)((H + kBN - 1) / kBN)), dim3(256), 0, st, dn);
+    CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)((H + 255) / 256)), dim3(256), 0, st, ca);
+    return axk_launch_status();
+  }
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
   const int max_slots = E < T * K ? E : T * K;
   const int fmax = F > Fs ? F : Fs;

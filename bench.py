@@ -245,6 +245,7 @@ class GdnPrefillWorkload(Workload):
     name = "gdn_prefill"
     kernel = "gdn chunk step (prep + scan)"
     timing = "graph"
+    mfma = True
 
     def __init__(self, dev):
         import torch
@@ -374,9 +375,53 @@ class CopyCalibWorkload(Workload):
         return None
 
 
+class MoePrefillWorkload(Workload):
+    """Config 3b: MoE layer prefill, 4096 tokens, hidden 2048, 256 MXFP4 experts (inter 512) + shared, top-8.
+
+    One step = router GEMM + top-K + blocked grouping + grouped gate-up/SwiGLU and down GEMMs (MFMA, bf16
+    operands from in-register MXFP4 decode) + combine. Algorithmic bytes: every expert's weights (all are routed
+    at this size), shared expert, router, activations in / residual in / out; flops: router, routed and shared
+    experts."""
+
+    name = "moe_prefill"
+    kernel = "moe prefill step"
+    timing = "graph"
+    mfma = True
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, moe
+
+        t = 4096
+        c = configs.config3(t)
+        w = c["weights"]
+        e, two_f, hh = w["e_gw"].shape
+        hidden, inter = 2 * hh, two_f // 2
+        per_expert = sum(w[n][0].numel() for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+        shared = sum(w[n].numel() for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down"))
+        self.wd = {n: v.to(dev) for n, v in w.items()}
+        self.h2, self.x = c["h2"].to(dev), c["x_res"].to(dev)
+        self.out = torch.empty_like(self.h2)
+        self.ws = moe.moe_workspace(t, hidden, e, 8, inter, inter, dev)
+        self.alg_bytes = e * per_expert + shared + w["w_router"].numel() * 2 + 3 * t * hidden * 2
+        per_row = 2 * hidden * 2 * inter + 2 * inter * hidden  # gate-up + down of one (token, expert)
+        self.alg_flops = t * 8 * per_row + t * per_row + 2 * t * hidden * e
+        self.config = {"workload": "config3b: MoE prefill T=4096 H=2048 E=256 F=512 top-8 + shared (MXFP4)"}
+        self.dtype = "mxfp4 weights x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        from axk import moe
+
+        moe.moe_decode(self.h2, self.wd, top_k=8, x_res=self.x, output=self.out, workspace=self.ws)
+
+    def cpu_baseline(self) -> dict:
+        return None
+
+
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
              GdnDecodeWorkload.name: GdnDecodeWorkload, GdnPrefillWorkload.name: GdnPrefillWorkload,
-             MoeDecodeWorkload.name: MoeDecodeWorkload,
+             MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
@@ -508,7 +553,7 @@ def main() -> int:
             suite[name] = {"us_per_op": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3),
                            "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                            "config": other.config["workload"]}
-            if getattr(other, "alg_flops", None) and other.name == "gdn_prefill":
+            if getattr(other, "mfma", False):
                 tf = other.alg_flops / (kms * 1e-3) / 1e12
                 suite[name].update({"achieved_tflops": round(tf, 2), "bf16_mfma_frac": round(tf / BF16_PEAK_TFS, 4)})
             del other

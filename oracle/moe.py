@@ -8,9 +8,10 @@ Restates
                   gate = sigmoid(h2 . w_shg), base = bf16(x1 + gate * sh)
   * experts       q35_moe.py:96-113 (moe_experts_gu) and q35_layer_mc.py:830-853 (moe_full): gate-up rows
                   [gate | up] of one [2F, H] matrix, y = act Wd^T (fp32) * rw, out = bf16(base + sum_k y_k)
+  * moe_parts     base, routed sum and the bound on one-ulp flips of the bf16 activations (see its docstring)
 Pinned by tests/test_oracle_moe.py: torch.topk / stable sort agreement, a dense all-experts formulation
 (every token through every expert, masked by the routing) and closed-form special cases (one expert with
-weight 1, zero router).
+weight 1, zero router); the flip bound by flipping activations on purpose.
 """
 from __future__ import annotations
 
@@ -36,8 +37,9 @@ def _deq(codes, scales) -> torch.Tensor:
     return torch.from_numpy(mx.dequant_mxfp4(np.asarray(codes), np.asarray(scales)))
 
 
-def swiglu_expert(h: torch.Tensor, gw, gs, dw, ds, split: int | None = None, uw=None, us=None) -> torch.Tensor:
-    """h [n, H] bf16 -> fp32 [n, H]: gate/up projections rounded to bf16, act = bf16(silu(g) * u), act Wd^T."""
+def swiglu_act(h: torch.Tensor, gw, gs, split: int | None = None, uw=None, us=None) -> torch.Tensor:
+    """h [n, H] bf16 -> act [n, F] (bf16 values in fp32): gate/up projections rounded to bf16,
+    act = bf16(silu(g) * u)."""
     if uw is None:  # one [2F, H] gate-up matrix: gate rows first
         wgu = _deq(gw, gs)
         wg, wu = wgu[:split], wgu[split:]
@@ -45,8 +47,49 @@ def swiglu_expert(h: torch.Tensor, gw, gs, dw, ds, split: int | None = None, uw=
         wg, wu = _deq(gw, gs), _deq(uw, us)
     g = (h.float() @ wg.T).to(torch.bfloat16).float()
     u = (h.float() @ wu.T).to(torch.bfloat16).float()
-    act = (F.silu(g) * u).to(torch.bfloat16).float()
-    return act @ _deq(dw, ds).T
+    return (F.silu(g) * u).to(torch.bfloat16).float()
+
+
+def swiglu_expert(h: torch.Tensor, gw, gs, dw, ds, split: int | None = None, uw=None, us=None) -> torch.Tensor:
+    """h [n, H] bf16 -> fp32 [n, H]: act Wd^T."""
+    return swiglu_act(h, gw, gs, split, uw, us) @ _deq(dw, ds).T
+
+
+def ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """One bf16 ulp (7 stored mantissa bits) of |x|."""
+    return torch.exp2(torch.floor(torch.log2(x.abs().clamp_min(1e-30))) - 7)
+
+
+def moe_parts(h2, weights, ids, wts, x_res=None, flips: int = 2):
+    """(base, routed, slack), all fp32 [T, H]: base = x1 + gate * shared expert, routed = sum_k rw_k y_k, and
+    a bound on how far `flips` one-ulp changes of the bf16 activations of each (token, expert) row can move the
+    output. g, u and act are rounded to bf16 at the reference's points, but a value that lies within the fp32
+    accumulation error of a rounding midpoint goes either way depending on the summation order, so two correct
+    implementations may hold neighbouring bf16 values there; the slack charges every row `flips` times its
+    largest activation ulp against the largest |Wd| of each output column."""
+    w = weights
+    t, hidden = h2.shape
+    base = x_res.float() if x_res is not None else torch.zeros(t, hidden)
+    slack = torch.zeros(t, hidden)
+    if w.get("w_gate") is not None:
+        act = swiglu_act(h2, w["w_gate"], w["s_gate"], uw=w["w_up"], us=w["s_up"])
+        wd = _deq(w["w_down"], w["s_down"])
+        gate = torch.sigmoid(h2.float() @ w["w_shg"].float()) if w.get("w_shg") is not None else torch.ones(t)
+        base = base + gate[:, None] * (act @ wd.T)
+        slack += flips * (gate * ulp_bf16(act).amax(dim=1))[:, None] * wd.abs().amax(dim=1)[None, :]
+    e_gw, e_gs, e_dw, e_ds = (np.asarray(w[n]) for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+    inter = e_gw.shape[1] // 2
+    routed = torch.zeros(t, hidden)
+    ids_np = ids.numpy()
+    for e in np.unique(ids_np):
+        rows, slots = np.nonzero(ids_np == e)
+        act = swiglu_act(h2[rows], e_gw[e], e_gs[e], split=inter)
+        wd = _deq(e_dw[e], e_ds[e])
+        rw = wts[rows, slots][:, None]
+        r = torch.from_numpy(rows)
+        routed.index_add_(0, r, (act @ wd.T) * rw)
+        slack.index_add_(0, r, flips * rw * ulp_bf16(act).amax(dim=1)[:, None] * wd.abs().amax(dim=1)[None, :])
+    return base, routed, slack
 
 
 def moe_layer(h2, weights, top_k=8, x_res=None, norm=True, ids=None, wts=None, round_base=True):
@@ -57,24 +100,10 @@ def moe_layer(h2, weights, top_k=8, x_res=None, norm=True, ids=None, wts=None, r
     logits = h2.float() @ w["w_router"].float().T
     if ids is None:
         ids, wts = route(logits, top_k, norm)
-    t, hidden = h2.shape
-    e_gw, e_gs, e_dw, e_ds = (np.asarray(w[n]) for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
-    inter = e_gw.shape[1] // 2
-    base = x_res.float() if x_res is not None else torch.zeros(t, hidden)
-    if w.get("w_gate") is not None:
-        sh = swiglu_expert(h2, w["w_gate"], w["s_gate"], w["w_down"], w["s_down"], uw=w["w_up"], us=w["s_up"])
-        gate = torch.sigmoid(h2.float() @ w["w_shg"].float()) if w.get("w_shg") is not None else torch.ones(t)
-        base = base + gate[:, None] * sh
+    base, routed, _ = moe_parts(h2, w, ids, wts, x_res)
     if round_base:
         base = base.to(torch.bfloat16).float()
-    acc = base.clone()
-    ids_np = ids.numpy()
-    for e in np.unique(ids_np):
-        rows, slots = np.nonzero(ids_np == e)
-        y = swiglu_expert(h2[rows], e_gw[e], e_gs[e], e_dw[e], e_ds[e], split=inter)
-        y = y * wts[rows, slots][:, None]
-        acc.index_add_(0, torch.from_numpy(rows), y)
-    return acc.to(torch.bfloat16), logits, ids, wts
+    return (base + routed).to(torch.bfloat16), logits, ids, wts
 
 
 def base_ulp(h2, weights, x_res):
@@ -87,5 +116,4 @@ def base_ulp(h2, weights, x_res):
         sh = swiglu_expert(h2, w["w_gate"], w["s_gate"], w["w_down"], w["s_down"], uw=w["w_up"], us=w["s_up"])
         gate = torch.sigmoid(h2.float() @ w["w_shg"].float()) if w.get("w_shg") is not None else torch.ones(t)
         base = base + gate[:, None] * sh
-    e = torch.floor(torch.log2(base.abs().clamp_min(1e-30)))
-    return torch.exp2(e - 7)
+    return ulp_bf16(base)

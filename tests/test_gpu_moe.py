@@ -27,13 +27,18 @@ def _check_layer(c, dev, norm=True):
     sids, swts = omoe.route(logits, k, norm)  # the host rule on the kernel's own logits
     assert torch.equal(ids, sids), "top-K ids differ from the stable sort of the kernel's logits"
     torch.testing.assert_close(wts, swts, rtol=1e-5, atol=1e-6)
-    ref, *_ = omoe.moe_layer(h2, w, k, x_res=x, norm=norm, ids=ids, wts=wts, round_base=False)
-    torch.testing.assert_close(out.float(), ref.float(), **TOL)
-    # the reference's rounding schedule (base rounded to bf16 first) differs by at most one ulp of |base|
-    # plus the same tolerance
-    ref_sched, *_ = omoe.moe_layer(h2, w, k, x_res=x, norm=norm, ids=ids, wts=wts, round_base=True)
-    slack = omoe.base_ulp(h2, w, x) + TOL["atol"] + TOL["rtol"] * ref_sched.float().abs()
-    assert ((out.float() - ref_sched.float()).abs() <= slack).all()
+    base, routed, slack = omoe.moe_parts(h2, w, ids, wts, x)
+    ref = (base + routed).to(torch.bfloat16).float()  # base kept fp32, one final rounding (the kernel's schedule)
+    tol = TOL["atol"] + TOL["rtol"] * ref.abs()
+    d = (out.float() - ref).abs()
+    # Elementwise at the stated tolerance, except where a one-ulp flip of a bf16 activation (g, u, act are rounded
+    # at the reference's points; which way a value at a rounding midpoint goes depends on the fp32 summation
+    # order) moves an output that cancels to near zero: such elements are rare and stay inside the derived slack.
+    assert (d <= tol + slack).all(), f"max excess {(d - tol - slack).max().item()}"
+    assert (d > tol).float().mean().item() <= 1e-5, f"{int((d > tol).sum())} elements outside the plain tolerance"
+    # the reference's rounding schedule (base rounded to bf16 first) differs by at most one ulp of |base| more
+    sched = (base.to(torch.bfloat16).float() + routed).to(torch.bfloat16).float()
+    assert ((out.float() - sched).abs() <= omoe.ulp_bf16(base) + tol + slack).all()
     return out
 
 
@@ -93,3 +98,43 @@ def test_moe_experts_out_of_range_ids_select_nothing(dev):
     ref, *_ = omoe.moe_layer(h2, w, 2, ids=ids_ref, wts=wts_ref, round_base=False)
     torch.testing.assert_close(out.float(), ref.float(), **TOL)
 
+
+
+# the prefill path (tokens > 256: blocked grouping, tile list, grouped MFMA GEMMs)
+@pytest.mark.parametrize("t,h,e,f,fs,k", [(300, 128, 16, 64, 64, 4), (513, 256, 300, 64, 0, 8),
+                                          (1000, 256, 64, 128, 192, 8), (257, 64, 8, 64, 64, 2)])
+def test_moe_prefill_shapes(dev, t, h, e, f, fs, k):
+    g = torch.Generator().manual_seed(t + e)
+    w = configs.moe_weights(g, hidden=h, experts=e, inter=f, shared_inter=max(fs, 64), router_std=0.5)
+    if fs == 0:
+        for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down", "w_shg"):
+            w.pop(n)
+    c = {"h2": torch.randn(t, h, generator=g).to(torch.bfloat16), "x_res": torch.randn(t, h, generator=g).to(torch.bfloat16),
+         "weights": w, "top_k": k}
+    print(f"case t={t} h={h} e={e} f={f} fs={fs} k={k}", flush=True)
+    _check_layer(c, dev)
+
+
+def test_moe_prefill_config3b_and_determinism(dev):
+    c = configs.config3(4096)
+    out = _check_layer(c, dev)
+    again, *_ = moe.moe_decode(c["h2"].to(dev), _dev_w(c["weights"], dev), top_k=8, x_res=c["x_res"].to(dev))
+    assert torch.equal(out.view(torch.int16), again.cpu().view(torch.int16))
+
+
+def test_moe_prefill_out_of_range_ids(dev):
+    g = torch.Generator().manual_seed(21)
+    w = configs.moe_weights(g, hidden=64, experts=8, inter=64, shared_inter=64, router_std=0.5)
+    t = 400
+    h2 = torch.randn(t, 64, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(8, generator=g)[:2] for _ in range(t)]).to(torch.int32)
+    ids[5, 1], ids[300, 0] = -3, 8
+    wts = torch.rand(t, 2, generator=g)
+    out = moe.moe_experts(h2.to(dev), _dev_w(w, dev), ids.to(dev), wts.to(dev)).cpu()
+    ids_ref, wts_ref = ids.clone(), wts.clone()
+    for r, c_ in ((5, 1), (300, 0)):
+        other = int(ids[r, 1 - c_])
+        ids_ref[r, c_] = (other + 1) % 8
+        wts_ref[r, c_] = 0.0
+    ref, *_ = omoe.moe_layer(h2, w, 2, ids=ids_ref, wts=wts_ref, round_base=False)
+    torch.testing.assert_close(out.float(), ref.float(), **TOL)

@@ -65,3 +65,27 @@ def test_single_expert_weight_one_and_zero_router():
     y = moe.swiglu_expert(h2, e_gw, w["e_gs"][0].numpy(), w["e_dw"][0].numpy(), w["e_ds"][0].numpy(),
                           split=e_gw.shape[0] // 2)
     torch.testing.assert_close(out.float(), y.bfloat16().float(), rtol=1e-2, atol=1e-2)
+
+
+def test_flip_slack_bounds_flipped_activations():
+    # flip two activations of every (token, expert) row by one bf16 ulp, recompute the routed sum by hand: the
+    # change stays inside the slack moe_parts reports
+    h2, x, w, k = _small(seed=7, t=9, h=64, e=6, f=32, fs=32, k=3)
+    _, _, ids, wts = moe.moe_layer(h2, w, k, x_res=x)
+    base, routed, slack = moe.moe_parts(h2, w, ids, wts, x)
+    g = torch.Generator().manual_seed(3)
+    e_gw, e_gs, e_dw, e_ds = (w[n] for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+    inter = e_gw.shape[1] // 2
+    moved = torch.zeros_like(routed)
+    for t in range(h2.shape[0]):
+        for j in range(k):
+            e = int(ids[t, j])
+            act = moe.swiglu_act(h2[t:t + 1], e_gw[e], e_gs[e], split=inter)[0]
+            cols = torch.randperm(inter, generator=g)[:2]
+            sign = torch.where(torch.rand(2, generator=g) < 0.5, -1.0, 1.0)
+            act[cols] += sign * moe.ulp_bf16(act[cols])
+            wd = moe._deq(e_dw[e], e_ds[e])
+            moved[t] += wts[t, j] * (act @ wd.T)
+    diff = (moved - routed).abs()
+    assert diff.max() > 0
+    assert (diff <= slack + 1e-5).all()
