@@ -13,9 +13,10 @@
 //   route   — one wave per token: softmax, top-K, renormalised weights
 //   group   — one workgroup: the (token, slot) pairs grouped by expert in (token, slot) order (deterministic
 //             counting sort: one thread per expert scans the pairs), and the list of active experts
-//   gateup  — one workgroup per (active expert or the shared expert, 16 intermediate rows): the gate and up
-//             tiles stream as MXFP4 over the expert's gathered tokens, SwiGLU in the epilogue
-//   down    — one workgroup per (expert, 64 hidden rows): act x Wd^T, scaled by the pair's routing weight
+//   gateup  — one workgroup per (active expert or the shared expert, run of 16-row tiles): the expert's
+//             gathered token rows staged in LDS, each wave streaming its gate and up tiles as MXFP4 over the
+//             full K with the next batch of loads in flight; SwiGLU in the epilogue
+//   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the pair's routing weight
 //   combine — one workgroup per token: shared gate, residual, sum over the token's K experts in slot order
 // Every expert's weights are read once per call, whatever the number of its tokens.
 //
@@ -39,7 +40,7 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;  // <= 64: lane k of the routing wave keeps selection k
 constexpr int kMaxPairs = 8192;
 constexpr int kMaskWords = 4;  // token bitmask words per expert in the grouping kernel: tokens <= 256
-constexpr int kMaxTokensPerChunk = 32;  // M rows per pass (2 MFMA tiles)
+constexpr size_t kMaxStageLds = 160 * 1024;  // decode streaming: 16 staged activation rows of K + 8 bf16
 constexpr int kDecodeTokens = 64 * kMaskWords;  // above this the prefill path runs
 constexpr int64_t kMaxPrefillTokens = 1 << 16;
 constexpr int64_t kMaxPrefillPairs = 1 << 19;
@@ -244,6 +245,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
     w.offsets[E] = tot;
     *w.n_active = tota;
   }
+  for (int j = tota + tid; j < E; j += blockDim.x) w.active_cnt[j] = 0;  // streaming kernels exit on cnt 0
   __syncthreads();
   for (int p = tid; p < P; p += blockDim.x) {
     const int e = ids[p], t = p / K;
@@ -261,36 +263,94 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
 }
 
 // ---------------------------------------------------------------------------------------------
-// gate-up + SwiGLU: workgroup (slot, 16-row tile); slot < max_slots: routed (active expert), else shared
+// Decode expert streaming. A workgroup owns one slot (an active expert, or the shared expert) and a run of
+// 16-row weight tiles; the slot's gathered activation rows (16 per pass) are staged in LDS once, and every wave
+// then streams its own tiles over the full K with the next batch of 16-byte weight units in flight while the
+// current one feeds the MFMAs: no cross-wave reduction and no barrier inside the stream.
 // ---------------------------------------------------------------------------------------------
+#ifndef AXK_SW
+#define AXK_SW 4
+#endif
+constexpr int kStreamWaves = AXK_SW;
+#ifndef AXK_BC
+#define AXK_BC 2
+#endif
+#ifndef AXK_ROWS
+#define AXK_ROWS 16
+#endif
+constexpr int kBatchChunks = AXK_BC;  // 128-wide K chunks per streamed batch (each lane: one unit per chunk)
+constexpr int kStageRows = AXK_ROWS;  // activation rows staged per pass (MFMA rows past it are zero)
+#ifndef AXK_GU_TPW
+#define AXK_GU_TPW 2
+#endif
+#ifndef AXK_DN_TPW
+#define AXK_DN_TPW 4
+#endif
+constexpr int kGateUpTilesPerWave = AXK_GU_TPW;  // 16-row tiles each wave streams (gate-up / down)
+constexpr int kDownTilesPerWave = AXK_DN_TPW;
+
+// Stage activation rows [m0, m0 + kStageRows) of the slot into LDS as [kStageRows][K + 8] bf16 (rows past cnt
+// are skipped).
+template <bool GATHER>
+__device__ void stage_rows(uint16_t* sA, const uint16_t* __restrict__ src, const int* __restrict__ row_tok,
+                           int row0, int m0, int cnt, int K) {
+  const int ld = K + 8, units = K / 8;
+  const int rows = min(kStageRows, cnt - m0);
+  for (int i = threadIdx.x; i < rows * units; i += blockDim.x) {
+    const int r = i / units, u = i - r * units;
+    const int64_t srow = GATHER ? row_tok[row0 + m0 + r] : (int64_t)(row0 + m0 + r);
+    *reinterpret_cast<uint4*>(sA + r * ld + 8 * u) = *reinterpret_cast<const uint4*>(src + srow * K + 8 * u);
+  }
+}
+
+// A batch's E8M0 scales of one weight row when K % (128 kBatchChunks) == 0: kBatchChunks consecutive words,
+// word j holding chunk j's four lane-group scales (byte g).
+AXK_DEV void load_scale_words(uint32_t (&w)[kBatchChunks], const uint8_t* p) {
+  static_assert(kBatchChunks == 4 || kBatchChunks == 2, "batch of 2 or 4 chunks");
+  if constexpr (kBatchChunks == 4) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  }
+}
+
 struct GateUpArgs {
   const uint16_t* h2;  // [T, H]
   const uint8_t *e_gw, *e_gs;
   const uint8_t *sg_w, *sg_s, *su_w, *su_s;  // shared gate / up (nullable: no shared expert)
-  int T, H, F, Fs, max_slots, ntile;
+  int T, H, F, Fs, max_slots, ngrp, tpw;     // tpw: tiles per wave; ngrp: workgroups per slot
+  int nsp;                                   // grid slots of the shared expert (kStageRows tokens each)
   MoeWs w;
 };
 
-constexpr int kGuWaves = 4;
-
-__global__ __launch_bounds__(64 * kGuWaves) void moe_gateup_kernel(GateUpArgs a) {
-  __shared__ float red[kGuWaves][2][2][4][64];  // [wave][gate/up][M tile][r][lane]
-  const int slot = blockIdx.x / a.ntile, tile = blockIdx.x - (blockIdx.x / a.ntile) * a.ntile;
-  const bool shared = slot == a.max_slots;
-  int cnt, row0;
+// gate-up + SwiGLU: workgroup (slot, ngrp-th run of kStreamWaves * tpw tiles); wave w streams tiles
+// run + w + kStreamWaves i.
+// WIDE (K a multiple of the batch's 128 kBatchChunks values): a batch's E8M0 scales are 4 kBatchChunks
+// consecutive bytes of the row (chunks x lane groups), fetched with one load per matrix; otherwise one byte load
+// per unit.
+template <bool WIDE>
+__global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  // grid slots [0, nsp): the shared expert, kStageRows tokens each (first, so the shared rows start early);
+  // slot s >= nsp: active expert s - nsp
+  const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
+  const bool shared = gslot < a.nsp;
+  const int slot = gslot - a.nsp;
+  int cnt, row0, Fo, mbeg = 0;
   const uint8_t *gw, *gs, *uw, *us;
-  int Fo;  // intermediate size of this slot
-  int64_t e = 0;
   if (shared) {
-    if (!a.sg_w) return;
-    cnt = a.T;
+    mbeg = gslot * kStageRows;
+    cnt = min(a.T, mbeg + kStageRows);
     row0 = 0;
     Fo = a.Fs;
     gw = a.sg_w; gs = a.sg_s; uw = a.su_w; us = a.su_s;
   } else {
-    if (slot >= *a.w.n_active) return;
-    e = a.w.active_e[slot];
-    cnt = a.w.active_cnt[slot];
+    cnt = a.w.active_cnt[slot];  // 0 past the active list (written so by the grouping kernel)
+    if (cnt == 0) return;
+    const int64_t e = a.w.active_e[slot];
     row0 = a.w.active_off[slot];
     Fo = a.F;
     const int64_t rows = 2 * (int64_t)a.F;
@@ -299,116 +359,216 @@ __global__ __launch_bounds__(64 * kGuWaves) void moe_gateup_kernel(GateUpArgs a)
     uw = gw + (int64_t)a.F * (a.H / 2);
     us = gs + (int64_t)a.F * (a.H / 32);
   }
-  const int n0 = tile * 16;
-  if (n0 >= Fo) return;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15;
-  const int64_t n = n0 + nl;
-  const bool nvalid = n < Fo;
-  for (int m0 = 0; m0 < cnt; m0 += kMaxTokensPerChunk) {
-    const uint16_t* xrow[2];
-    bool mvalid[2];
+  const int ntiles = (Fo + 15) / 16;
+  const int tb = grp * kStreamWaves * a.tpw;
+  if (tb >= ntiles) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  const int H = a.H, ldA = H + 8;
+  const int nc = (H + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;  // chunks, batches per tile
+  // this wave's tiles: tb + wave + kStreamWaves i, i < nmine
+  const int nmine = max(0, min(a.tpw, (ntiles - tb - wave + kStreamWaves - 1) / kStreamWaves));
+  const int steps = nmine * nb;
+
+  struct Batch {
+    uint4 qg[kBatchChunks], qu[kBatchChunks];
+    uint32_t sg[kBatchChunks], su[kBatchChunks];
+  };
+  // Loads are unconditional, from addresses clamped into the weights (a row past Fo is never stored, a unit past
+  // K is zeroed where it is used): a branch around a load would make every later wait drain the queue.
+  auto load_batch = [&](Batch& bt, int step) {
+    const int i = step / nb, bi = step - i * nb;
+    const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)Fo - 1);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int m = m0 + 16 * t + nl;
-      mvalid[t] = m < cnt;
-      const int tok = mvalid[t] ? (shared ? m : a.w.row_tok[row0 + m]) : 0;
-      xrow[t] = a.h2 + (int64_t)tok * a.H;
-    }
-    axk_f32x4 accg[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
-    axk_f32x4 accu[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
-    axk::mx_tile_accum2<WF_MXFP4, 2, 4>(xrow, mvalid, gw, gs, uw, us, n, nvalid, a.H, wave, kGuWaves, accg, accu);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        red[wave][0][t][r][lane] = accg[t][r];
-        red[wave][1][t][r][lane] = accu[t][r];
-      }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 2 * 256; idx += blockDim.x) {
-      const int t = idx >> 8, r = (idx >> 6) & 3, l = idx & 63;
-      float gsum = 0.f, usum = 0.f;
-#pragma unroll
-      for (int wv = 0; wv < kGuWaves; ++wv) {
-        gsum += red[wv][0][t][r][l];
-        usum += red[wv][1][t][r][l];
-      }
-      const int m = m0 + 16 * t + 4 * (l >> 4) + r;
-      const int nn = n0 + (l & 15);
-      if (m < cnt && nn < Fo) {
-        const float gv = round_bf16(gsum), uv = round_bf16(usum);  // projections rounded to bf16
-        const uint16_t act = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
-        if (shared)
-          a.w.act_sh[(int64_t)m * a.Fs + nn] = act;
-        else
-          a.w.act[(int64_t)(row0 + m) * a.F + nn] = act;
+    for (int j = 0; j < kBatchChunks; ++j) {
+      const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
+      bt.qg[j] = *reinterpret_cast<const uint4*>(gw + n * (H / 2) + kb / 2);
+      bt.qu[j] = *reinterpret_cast<const uint4*>(uw + n * (H / 2) + kb / 2);
+      if (!WIDE) {
+        bt.sg[j] = gs[n * (H / 32) + kb / 32];
+        bt.su[j] = us[n * (H / 32) + kb / 32];
       }
     }
+    if (WIDE) {
+      load_scale_words(bt.sg, gs + n * (H / 32) + 4 * kBatchChunks * bi);
+      load_scale_words(bt.su, us + n * (H / 32) + 4 * kBatchChunks * bi);
+    }
+  };
+
+  for (int m0 = mbeg; m0 < cnt; m0 += kStageRows) {
+    axk_f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    auto proc = [&](const Batch& cur, int st) {
+      const int i = st / nb, bi = st - i * nb;
+#pragma unroll
+      for (int j = 0; j < kBatchChunks; ++j) {
+        const int c = bi * kBatchChunks + j;
+        if (c * 128 >= H) continue;  // whole chunk past K (uniform)
+        const int kb = c * 128 + 32 * g;
+        const bool kv = kb < H;      // this lane's unit (a chunk can straddle the end of K)
+        const int kc = kv ? kb : H - 32;
+        const uint32_t bg = WIDE ? (cur.sg[j] >> (8 * g)) & 0xffu : cur.sg[j];
+        const uint32_t bu = WIDE ? (cur.su[j] >> (8 * g)) & 0xffu : cur.su[j];
+        const float scg = kv ? e8m0_to_f32(bg) : 0.f, scu = kv ? e8m0_to_f32(bu) : 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const axk_bf16x8 af = (kv && nl < kStageRows) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8();
+          accg = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(cur.qg[j], s, scg), accg);
+          accu = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(cur.qu[j], s, scu), accu);
+        }
+      }
+      if (bi == nb - 1) {  // tile done: SwiGLU of rows m0 + 4 g + r, column tile * 16 + nl
+        const int col = (tb + wave + kStreamWaves * i) * 16 + nl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 4 * g + r;
+          if (4 * g + r < kStageRows && m < cnt && col < Fo) {
+            const float gv = round_bf16(accg[r]), uv = round_bf16(accu[r]);
+            const uint16_t act = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+            if (shared)
+              a.w.act_sh[(int64_t)m * a.Fs + col] = act;
+            else
+              a.w.act[(int64_t)(row0 + m) * a.F + col] = act;
+          }
+        }
+        accg = accu = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    // three batches in rotation: batch st + 2 is loaded while batch st is used; the first two are issued
+    // before the activation rows are staged, so they overlap the expert's metadata and row gathers
+    Batch b0, b1, b2;
+    const int last = max(steps - 1, 0);
+    __syncthreads();  // the previous pass's readers are done with sA
+    load_batch(b0, 0);
+    load_batch(b1, min(1, last));
+    if (shared)
+      stage_rows<false>(sA, a.h2, nullptr, 0, m0, cnt, H);
+    else
+      stage_rows<true>(sA, a.h2, a.w.row_tok, row0, m0, cnt, H);
     __syncthreads();
+    for (int st = 0; st < steps; st += 3) {
+      load_batch(b2, min(st + 2, last));
+      proc(b0, st);
+      load_batch(b0, min(st + 3, last));
+      if (st + 1 < steps) proc(b1, st + 1);
+      load_batch(b1, min(st + 4, last));
+      if (st + 2 < steps) proc(b2, st + 2);
+    }
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// down: workgroup (slot, 64 hidden rows); wave w owns rows 16w .. 16w + 15 over the full K = F
-// ---------------------------------------------------------------------------------------------
 struct DownArgs {
   const uint8_t *e_dw, *e_ds;
   const uint8_t *sd_w, *sd_s;
-  int T, H, F, Fs, max_slots, ntile;
+  int T, H, F, Fs, max_slots, ngrp, tpw, nsp;
   MoeWs w;
 };
 
-__global__ __launch_bounds__(256) void moe_down_kernel(DownArgs a) {
-  const int slot = blockIdx.x / a.ntile, tile = blockIdx.x - (blockIdx.x / a.ntile) * a.ntile;
-  const bool shared = slot == a.max_slots;
-  int cnt, row0, K;
+// down: workgroup (slot, run of kStreamWaves * tpw 16-row tiles of H); routed rows scaled by their routing weight.
+template <bool WIDE>
+__global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
+  const bool shared = gslot < a.nsp;
+  const int slot = gslot - a.nsp;
+  int cnt, row0, K, mbeg = 0;
   const uint8_t *dw, *ds;
   const uint16_t* act;
   if (shared) {
-    if (!a.sd_w) return;
-    cnt = a.T;
+    mbeg = gslot * kStageRows;
+    cnt = min(a.T, mbeg + kStageRows);
     row0 = 0;
     K = a.Fs;
     dw = a.sd_w; ds = a.sd_s;
     act = a.w.act_sh;
   } else {
-    if (slot >= *a.w.n_active) return;
-    const int64_t e = a.w.active_e[slot];
     cnt = a.w.active_cnt[slot];
+    if (cnt == 0) return;
+    const int64_t e = a.w.active_e[slot];
     row0 = a.w.active_off[slot];
     K = a.F;
     dw = a.e_dw + e * (int64_t)a.H * (a.F / 2);
     ds = a.e_ds + e * (int64_t)a.H * (a.F / 32);
-    act = a.w.act + (int64_t)row0 * a.F;
+    act = a.w.act;
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15;
-  const int n0 = tile * 64 + 16 * wave;
-  const int64_t n = n0 + nl;
-  const bool nvalid = n < a.H;
-  for (int m0 = 0; m0 < cnt; m0 += kMaxTokensPerChunk) {
-    const uint16_t* xrow[2];
-    bool mvalid[2];
+  const int ntiles = (a.H + 15) / 16;
+  const int tb = grp * kStreamWaves * a.tpw;
+  if (tb >= ntiles) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  const int ldA = K + 8;
+  const int nc = (K + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;
+  const int nmine = max(0, min(a.tpw, (ntiles - tb - wave + kStreamWaves - 1) / kStreamWaves));
+  const int steps = nmine * nb;
+
+  struct Batch {
+    uint4 q[kBatchChunks];
+    uint32_t s[kBatchChunks];
+  };
+  auto load_batch = [&](Batch& bt, int step) {  // unconditional, clamped (as in the gate-up kernel)
+    const int i = step / nb, bi = step - i * nb;
+    const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)a.H - 1);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int m = m0 + 16 * t + nl;
-      mvalid[t] = m < cnt;
-      xrow[t] = act + (int64_t)(mvalid[t] ? m : 0) * K;
+    for (int j = 0; j < kBatchChunks; ++j) {
+      const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
+      bt.q[j] = *reinterpret_cast<const uint4*>(dw + n * (K / 2) + kb / 2);
+      if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
     }
-    axk_f32x4 acc[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
-    axk::mx_tile_accum<WF_MXFP4, 2, 4>(xrow, mvalid, dw, ds, n, nvalid, K, 0, 1, acc);
+    if (WIDE) load_scale_words(bt.s, ds + n * (K / 32) + 4 * kBatchChunks * bi);
+  };
+
+  for (int m0 = mbeg; m0 < cnt; m0 += kStageRows) {
+    float rw[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 4 * g + r;
+      rw[r] = (!shared && m < cnt) ? a.w.row_w[row0 + m] : 1.0f;
+    }
+    axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto proc = [&](const Batch& cur, int st) {
+      const int i = st / nb, bi = st - i * nb;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * t + 4 * (lane >> 4) + r;
-        const int64_t nn = n0 + (lane & 15);
-        if (m < cnt && nn < a.H) {
-          if (shared)
-            a.w.y_sh[(int64_t)m * a.H + nn] = acc[t][r];
-          else
-            a.w.y[(int64_t)(row0 + m) * a.H + nn] = acc[t][r] * a.w.row_w[row0 + m];
-        }
+      for (int j = 0; j < kBatchChunks; ++j) {
+        const int c = bi * kBatchChunks + j;
+        if (c * 128 >= K) continue;
+        const int kb = c * 128 + 32 * g;
+        const bool kv = kb < K;
+        const int kc = kv ? kb : K - 32;
+        const uint32_t sb = WIDE ? (cur.s[j] >> (8 * g)) & 0xffu : cur.s[j];
+        const float sc = kv ? e8m0_to_f32(sb) : 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          acc = mfma_bf16_16x16x32((kv && nl < kStageRows) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8(),
+                                   axk::WUnit<WF_MXFP4>::conv(cur.q[j], s, sc), acc);
       }
+      if (bi == nb - 1) {
+        const int64_t col = (int64_t)(tb + wave + kStreamWaves * i) * 16 + nl;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 4 * g + r;
+          if (4 * g + r < kStageRows && m < cnt && col < a.H) {
+            if (shared)
+              a.w.y_sh[(int64_t)m * a.H + col] = acc[r];
+            else
+              a.w.y[(int64_t)(row0 + m) * a.H + col] = acc[r] * rw[r];
+          }
+        }
+        acc = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    Batch b0, b1, b2;
+    const int last = max(steps - 1, 0);
+    __syncthreads();
+    load_batch(b0, 0);
+    load_batch(b1, min(1, last));
+    stage_rows<false>(sA, act, nullptr, row0, m0, cnt, K);
+    __syncthreads();
+    for (int st = 0; st < steps; st += 3) {
+      load_batch(b2, min(st + 2, last));
+      proc(b0, st);
+      load_batch(b0, min(st + 3, last));
+      if (st + 1 < steps) proc(b1, st + 1);
+      load_batch(b1, min(st + 4, last));
+      if (st + 2 < steps) proc(b2, st + 2);
+    }
   }
 }
 
@@ -820,11 +980,39 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
   const int max_slots = E < T * K ? E : T * K;
   const int fmax = F > Fs ? F : Fs;
-  GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, max_slots, (fmax + 15) / 16, w};
-  hipLaunchKernelGGL(moe_gateup_kernel, dim3((unsigned)((max_slots + 1) * ga.ntile)), dim3(64 * kGuWaves), 0, st,
-                     ga);
-  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, (H + 63) / 64, w};
-  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)((max_slots + 1) * da.ntile)), dim3(256), 0, st, da);
+  // runs of 4 x tpw tiles per workgroup; activation rows staged in dynamic LDS (16 rows of K + 8)
+  const int gu_tpw = kGateUpTilesPerWave, dn_tpw = kDownTilesPerWave;
+  const int run_gu = kStreamWaves * gu_tpw, run_dn = kStreamWaves * dn_tpw;
+  const int gu_grp = ((fmax + 15) / 16 + run_gu - 1) / run_gu;
+  const int dn_grp = ((H + 15) / 16 + run_dn - 1) / run_dn;
+  const size_t gu_lds = (size_t)kStageRows * (H + 8) * 2, dn_lds = (size_t)kStageRows * (fmax + 8) * 2;
+  AXK_REQUIRE(gu_lds <= kMaxStageLds && dn_lds <= kMaxStageLds, AXK_E_SHAPE);
+  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  if (!lds_raised) {
+    const void* fns[4] = {reinterpret_cast<const void*>(&moe_gateup_kernel<false>),
+                          reinterpret_cast<const void*>(&moe_gateup_kernel<true>),
+                          reinterpret_cast<const void*>(&moe_down_kernel<false>),
+                          reinterpret_cast<const void*>(&moe_down_kernel<true>)};
+    for (const void* f : fns)
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
+        return AXK_E_LAUNCH;
+    lds_raised = true;
+  }
+  const int wide_k = 128 * kBatchChunks;
+  const bool gu_wide = H % wide_k == 0, dn_wide = F % wide_k == 0 && Fs % wide_k == 0;
+  const int nsp = has_shared ? (T + kStageRows - 1) / kStageRows : 0;
+  GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, max_slots, gu_grp, gu_tpw,
+                nsp, w};
+  const dim3 gu_grid((unsigned)((max_slots + nsp) * gu_grp)), dn_grid((unsigned)((max_slots + nsp) * dn_grp));
+  if (gu_wide)
+    hipLaunchKernelGGL(moe_gateup_kernel<true>, gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
+  else
+    hipLaunchKernelGGL(moe_gateup_kernel<false>, gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
+  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, dn_grp, dn_tpw, nsp, w};
+  if (dn_wide)
+    hipLaunchKernelGGL(moe_down_kernel<true>, dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
+  else
+    hipLaunchKernelGGL(moe_down_kernel<false>, dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)((H + 255) / 256)), dim3(256), 0, st, ca);
   return axk_launch_status();
