@@ -7,9 +7,10 @@
 //
 // Three kernels:
 //  1. plan   — one wave: pages per split so that the number of (sequence, KV head, split) work items
-//              is about kTargetItems, and one descriptor per item. Depends only on the page-table
-//              shape, so one plan serves every attention layer of a decode step (no host sync, no
-//              memset: graph-capturable).
+//              is about one per resident split workgroup, and one descriptor per item. Depends only on the
+//              page-table shape, so one plan serves every attention layer of a decode step (no host sync,
+//              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
+//              compute the same partition themselves from the page table and no plan launch is needed.
 //  2. decode — one workgroup per work item. Each wave takes 32-token tiles of the item's pages:
 //              S^T = K Q^T on MFMA (K rows straight from HBM with 128-bit loads, Q in registers),
 //              online softmax in fp32 (exp2 domain), P (bf16) x V on MFMA with V streamed HBM -> LDS
@@ -39,7 +40,7 @@ struct PlanHeader {
   int bad_page;   // set to 1 if a page id outside [0, num_pages) was met (page skipped)
   int batch;      // batch / num_kv_heads the plan was made for (checked by the run kernel)
   int hkv;
-  int next_item;  // work queue of the persistent split kernel (zeroed by plan and by merge)
+  int unused;
   int pad[2];
 };
 
@@ -77,11 +78,22 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
                                                          int page_size, int slots, PlanHeader* __restrict__ hdr,
                                                          int* __restrict__ item_off, ItemDesc* __restrict__ descs) {
   __shared__ int s_off[kPlanLdsBatch + 1];
+  __shared__ int s_ptr[kPlanLdsBatch + 1], s_last[kPlanLdsBatch];
   __shared__ int s_pps, s_items;
   const int tid = threadIdx.x, lane = tid & 63;
+  const bool cached = batch <= kPlanLdsBatch;  // page table shape held in LDS: one round of global loads
+  if (cached) {
+    for (int b = tid; b <= batch; b += blockDim.x) {
+      s_ptr[b] = indptr[b];
+      if (b < batch) s_last[b] = last_page_len[b];
+    }
+    __syncthreads();
+  }
+  const int* ptr = cached ? s_ptr : indptr;
+  const int* lastp = cached ? s_last : last_page_len;
   if (tid < 64) {
     int tot = 0;
-    for (int b = lane; b < batch; b += 64) tot += indptr[b + 1] - indptr[b];
+    for (int b = lane; b < batch; b += 64) tot += ptr[b + 1] - ptr[b];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
     const long long work = (long long)tot * hkv;
@@ -96,7 +108,7 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
     for (int b0 = 0; b0 < batch; b0 += 64) {
       const int b = b0 + lane;
       int cnt = 0;
-      if (b < batch) cnt = hkv * ((indptr[b + 1] - indptr[b] + pps - 1) / pps);
+      if (b < batch) cnt = hkv * ((ptr[b + 1] - ptr[b] + pps - 1) / pps);
       int incl = cnt;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -119,7 +131,6 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
       hdr->bad_page = 0;
       hdr->batch = batch;
       hdr->hkv = hkv;
-      hdr->next_item = 0;
     }
   }
   __syncthreads();
@@ -132,7 +143,7 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
       if (offs[mid] <= it) lo = mid; else hi = mid - 1;
     }
     const int b = lo;
-    const int pb = indptr[b], np = indptr[b + 1] - pb;
+    const int pb = ptr[b], np = ptr[b + 1] - pb;
     const int ns = (np + pps - 1) / pps;
     const int local = it - offs[b];
     const int kvh = local / ns, sp = local - kvh * ns;
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
     d.nsplit = ns;
     d.ibeg = pb + sp * pps;
     d.npg = min(pps, np - sp * pps);
-    d.last_valid = sp == ns - 1 ? last_page_len[b] : page_size;
+    d.last_valid = sp == ns - 1 ? lastp[b] : page_size;
     d.pad = 0;
     descs[it] = d;
   }
@@ -191,6 +202,66 @@ AXK_DEV void wait_vmcnt() {
 }
 
 typedef short axk_i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kLocalPlanBatch = 63;  // up to this many sequences the kernels derive the plan themselves
+
+// The plan's partition computed by one wave from the page table (batch <= kLocalPlanBatch: lane b holds
+// sequence b), with exactly the arithmetic of paged_plan_kernel: pages per split from the total work and the
+// slot count, items in (sequence, KV head, split) order.
+struct LocalPlan {
+  int p, np, last;  // lane b: first page index, pages, last page's valid tokens of sequence b
+  int off, ns;      // lane b: first item of sequence b, splits per KV head
+  int pps, n_items;
+};
+
+AXK_DEV LocalPlan local_plan(const int* __restrict__ indptr, const int* __restrict__ last_page_len, int batch,
+                             int hkv, int slots) {
+  const int lane = threadIdx.x & 63;
+  LocalPlan lp;
+  lp.p = indptr[min(lane, batch)];
+  lp.last = lane < batch ? last_page_len[lane] : 0;
+  const int pn = __shfl(lp.p, min(lane + 1, 63), 64);
+  lp.np = lane < batch ? pn - lp.p : 0;
+  int tot = lp.np;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+  const long long work = (long long)tot * hkv;
+  int target = min(slots, kTargetItems);
+  if (target - batch * hkv >= target / 2) target -= batch * hkv;
+  lp.pps = max(1, (int)((work + target - 1) / target));
+  lp.ns = (lp.np + lp.pps - 1) / lp.pps;
+  const int cnt = lane < batch ? hkv * lp.ns : 0;
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  lp.off = incl - cnt;
+  lp.n_items = __shfl(incl, 63, 64);
+  return lp;
+}
+
+// Descriptor of item `it` (< n_items) from the local plan (every lane gets the same values).
+AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_size) {
+  const int lane = threadIdx.x & 63;
+  ItemDesc d;
+  // the sequence: the last lane whose first item is <= it (item ranges are consecutive; a sequence without
+  // pages has an empty range and is never the last such lane for an item inside the plan)
+  const unsigned long long le = __builtin_amdgcn_ballot_w64(lane < batch && lp.off <= it);
+  const int b = 63 - __builtin_clzll(le);
+  const int pb = __shfl(lp.p, b, 64), npb = __shfl(lp.np, b, 64), ns = __shfl(lp.ns, b, 64);
+  const int local = it - __shfl(lp.off, b, 64);
+  d.b = b;
+  d.kvh = local / ns;
+  d.split = local - d.kvh * ns;
+  d.nsplit = ns;
+  d.ibeg = pb + d.split * lp.pps;
+  d.npg = min(lp.pps, npb - d.split * lp.pps);
+  d.last_valid = d.split == ns - 1 ? __shfl(lp.last, b, 64) : page_size;
+  d.pad = 0;
+  return d;
+}
 
 // Attention of one work item. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
 // (each wave issues a quarter of its loads) into a ring of kNBuf buffers, two tiles ahead of the one being
@@ -375,67 +446,93 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   }
 }
 
-// Persistent split kernel: a few workgroups per CU; each takes work items from the plan's queue until it
-// is empty (first item = blockIdx.x, then gridDim.x + ticket), so every CU stays busy to the end.
+// Persistent split kernel: a few workgroups per CU; workgroup w takes items w, w + gridDim.x, ... (the plan
+// sizes the items to about one per workgroup). With local != 0 the descriptors come from the page table
+// directly (local_plan), otherwise from the plan in the workspace.
 template <int D>
 __global__ __launch_bounds__(256) void paged_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, const int* __restrict__ indices, int batch,
-    int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, PlanHeader* __restrict__ hdr,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, const int* __restrict__ indptr,
+    const int* __restrict__ last_page_len, const int* __restrict__ indices, int batch, int hq, int hkv,
+    int page_size, int64_t num_pages, float sm_scale, int local, PlanHeader* __restrict__ hdr,
     const ItemDesc* __restrict__ descs, float* __restrict__ part_m, float* __restrict__ part_l,
     float* __restrict__ part_o, uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_next;
-  if (hdr->batch != batch || hdr->hkv != hkv) return;
-  const int n_items = hdr->n_items;
-  int it = blockIdx.x;
-  while (it < n_items) {
-    const ItemDesc desc = descs[it];
+  if (local) {
+    const LocalPlan lp = local_plan(indptr, last_page_len, batch, hkv, gridDim.x);
+    for (int it = blockIdx.x; it < lp.n_items; it += gridDim.x) {
+      const ItemDesc desc = local_item(lp, it, batch, page_size);
+      decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
+                     part_o, out, smem);
+      __syncthreads();  // LDS is reused by the next item
+    }
+    return;
+  }
+  // the header and the first descriptor are independent loads: one round trip (the descriptor slot exists
+  // whatever the plan holds, gridDim.x <= the workspace's item capacity)
+  const PlanHeader h = *hdr;
+  ItemDesc desc = descs[blockIdx.x];
+  if (h.batch != batch || h.hkv != hkv) return;
+  for (int it = blockIdx.x; it < h.n_items; it += gridDim.x) {
+    if (it != (int)blockIdx.x) desc = descs[it];
     decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
                    part_o, out, smem);
-    __syncthreads();  // LDS is reused by the next item
-    if (threadIdx.x == 0) s_next = gridDim.x + atomicAdd(&hdr->next_item, 1);
     __syncthreads();
-    it = s_next;
   }
 }
 
-// One wave per (sequence, query head): merge the item partials of a sequence with more than one split;
-// zero the output of a sequence without pages. Lane i holds split i's (m, l) (64 splits per pass); each
-// lane then accumulates D/64 output columns over all splits with independent loads.
+// One workgroup per (sequence, query head): log-sum-exp merge of the item partials of a sequence with more than
+// one split; zero output for a sequence without pages. Wave w merges splits w, w + 4, ... (16 per pass, every
+// load of a pass issued before any is used); the four running (m, l, O) are combined in LDS.
 template <int D>
-__global__ __launch_bounds__(64) void paged_merge_kernel(const int* __restrict__ indptr,
-                                                         PlanHeader* __restrict__ hdr,
-                                                         const int* __restrict__ item_off, int batch, int hq,
-                                                         int hkv, const float* __restrict__ part_m,
-                                                         const float* __restrict__ part_l,
-                                                         const float* __restrict__ part_o,
-                                                         uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict__ indptr,
+                                                          const int* __restrict__ last_page_len,
+                                                          PlanHeader* __restrict__ hdr,
+                                                          const int* __restrict__ item_off, int batch, int hq,
+                                                          int hkv, int slots, int local,
+                                                          const float* __restrict__ part_m,
+                                                          const float* __restrict__ part_l,
+                                                          const float* __restrict__ part_o,
+                                                          uint16_t* __restrict__ out) {
   constexpr int V = D / 64;  // output columns per lane
+  __shared__ float s_m[4], s_l[4];
+  __shared__ float s_acc[4][D];
   const int b = blockIdx.x / hq, h = blockIdx.x - (blockIdx.x / hq) * hq;
-  const int lane = threadIdx.x;
-  if (hdr->batch != batch || hdr->hkv != hkv) return;
-  if (blockIdx.x == 0 && lane == 0) hdr->next_item = 0;  // the split kernel's queue, for the next run
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int group = hq / hkv, kvh = h / group, hh = h - kvh * group;
+  int np, nsplit, i0;
+  if (local) {
+    const LocalPlan lp = local_plan(indptr, last_page_len, batch, hkv, slots);
+    np = __shfl(lp.np, b, 64);
+    nsplit = __shfl(lp.ns, b, 64);
+    i0 = __shfl(lp.off, b, 64) + kvh * nsplit;
+  } else {
+    // header, page range and item range: independent loads, one round trip
+    const int hb = hdr->batch, hk = hdr->hkv;
+    const int p0 = indptr[b], p1 = indptr[b + 1];
+    const int io0 = item_off[b], io1 = item_off[b + 1];
+    if (hb != batch || hk != hkv) return;
+    np = p1 - p0;
+    nsplit = (io1 - io0) / hkv;
+    i0 = io0 + kvh * nsplit;
+  }
   uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
-  if (indptr[b + 1] == indptr[b]) {
+  if (np == 0) {
+    if (wave == 0) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) op[j] = 0;
+      for (int j = 0; j < V; ++j) op[j] = 0;
+    }
     return;
   }
-  const int nsplit = (item_off[b + 1] - item_off[b]) / hkv;
   if (nsplit <= 1) return;  // written by the decode kernel
-  const int i0 = item_off[b] + kvh * nsplit;
-  // online merge, 16 splits per pass: every load of a pass (m, l and this lane's O columns) is issued
-  // before any is used, so a pass costs one memory round trip
   constexpr int P = 16;
   float mm = -INFINITY, ll = 0.f, acc[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) acc[j] = 0.f;
-  for (int c0 = 0; c0 < nsplit; c0 += P) {
+  for (int c0 = wave; c0 < nsplit; c0 += 4 * P) {
     float mi[P], li[P], oi[P][V];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      const int i = min(c0 + k, nsplit - 1);  // clamped: in-bounds, weight zeroed below
+      const int i = min(c0 + 4 * k, nsplit - 1);  // clamped: in-bounds, weight zeroed below
       mi[k] = part_m[(int64_t)(i0 + i) * group + hh];
       li[k] = part_l[(int64_t)(i0 + i) * group + hh];
       const float* src = part_o + ((int64_t)(i0 + i) * group + hh) * D + lane * V;
@@ -445,23 +542,44 @@ __global__ __launch_bounds__(64) void paged_merge_kernel(const int* __restrict__
     float cm = mm;
 #pragma unroll
     for (int k = 0; k < P; ++k)
-      if (c0 + k < nsplit) cm = fmaxf(cm, mi[k]);
+      if (c0 + 4 * k < nsplit) cm = fmaxf(cm, mi[k]);
     const float sc = mm == -INFINITY ? 0.f : exp2f(mm - cm);
     ll *= sc;
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] *= sc;
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      const float w = (c0 + k < nsplit && mi[k] != -INFINITY) ? exp2f(mi[k] - cm) : 0.f;
+      const float w = (c0 + 4 * k < nsplit && mi[k] != -INFINITY) ? exp2f(mi[k] - cm) : 0.f;
       ll += w * li[k];
 #pragma unroll
       for (int j = 0; j < V; ++j) acc[j] += w * oi[k][j];
     }
     mm = cm;
   }
-  const float inv = ll > 0.f ? 1.0f / ll : 0.f;
+  if (lane == 0) {
+    s_m[wave] = mm;
+    s_l[wave] = ll;
+  }
 #pragma unroll
-  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
+  for (int j = 0; j < V; ++j) s_acc[wave][lane * V + j] = acc[j];
+  __syncthreads();
+  if (wave != 0) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w]);
+  float L = 0.f, o[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) o[j] = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float f = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - M);  // a wave without splits holds -inf, 0
+    L += f * s_l[w];
+#pragma unroll
+    for (int j = 0; j < V; ++j) o[j] += f * s_acc[w][lane * V + j];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(o[j] * inv);
 }
 
 // cache[loc[b,0], 0, loc[b,1], kvh, :] = k[b, kvh, :]; plane 1 <- v (store_paged_kv, flash_attn.py:53-84).
@@ -518,10 +636,17 @@ int device_cu_count() {
   return cus[dev];
 }
 
+// Workgroups of the split kernel (also the slot count the local plan divides the work by).
+int split_grid(int batch, int hkv) {
+  const unsigned items = (unsigned)ws_items_max(batch, hkv);
+  const unsigned slots = (unsigned)(kBlocksPerCU * device_cu_count());
+  return (int)(items < slots ? items : slots);
+}
+
 template <int D>
-int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, const int* indices, uint16_t* out,
-                 int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, void* ws,
-                 hipStream_t st) {
+int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, const int* last, const int* indices,
+                 uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
+                 void* ws, hipStream_t st) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
   const size_t lds = (size_t)kNBuf * PagedCfg<D>::BUF;
@@ -532,19 +657,20 @@ int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, co
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
-  const unsigned items = (unsigned)ws_items_max(batch, hkv);
-  const unsigned slots = (unsigned)(kBlocksPerCU * device_cu_count());
-  hipLaunchKernelGGL((paged_decode_kernel<D>), dim3(items < slots ? items : slots), dim3(64 * kWaves), lds, st, q,
-                     cache, indices, batch, hq, hkv, page_size, num_pages, sm_scale, v.hdr, v.descs, v.pm, v.pl, v.po,
-                     out);
+  const int local = batch <= kLocalPlanBatch ? 1 : 0;
+  hipLaunchKernelGGL((paged_decode_kernel<D>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves), lds, st,
+                     q, cache, indptr, last, indices, batch, hq, hkv, page_size, num_pages, sm_scale, local, v.hdr,
+                     v.descs, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
 
 template <int D>
-int launch_merge(const int* indptr, uint16_t* out, int batch, int hq, int hkv, void* ws, hipStream_t st) {
+int launch_merge(const int* indptr, const int* last, uint16_t* out, int batch, int hq, int hkv, void* ws,
+                 hipStream_t st) {
   const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
-  hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)(batch * hq)), dim3(64), 0, st, indptr, v.hdr,
-                     v.item_off, batch, hq, hkv, v.pm, v.pl, v.po, out);
+  const int local = batch <= kLocalPlanBatch ? 1 : 0;
+  hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)(batch * hq)), dim3(256), 0, st, indptr, last, v.hdr,
+                     v.item_off, batch, hq, hkv, split_grid(batch, hkv), local, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
 
@@ -573,6 +699,7 @@ extern "C" int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096, AXK_E_SHAPE);
   const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  if (batch <= kLocalPlanBatch) return AXK_OK;  // the split and merge kernels derive the plan themselves
   const WsView v = ws_view(workspace, (int)batch, (int)num_kv_heads, (int)(num_qo_heads / num_kv_heads),
                            (int)head_dim);
   hipLaunchKernelGGL(paged_plan_kernel, dim3(1), dim3(256), 0, axk_stream(stream), indptr, last_page_len, (int)batch,
@@ -581,11 +708,11 @@ extern "C" int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_
 }
 
 extern "C" int axk_paged_decode_split(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
-                                      const int32_t* indices, uint16_t* out, int64_t batch, int64_t num_qo_heads,
-                                      int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
-                                      float sm_scale, void* workspace, size_t workspace_bytes,
-                                      axk_stream_t stream) {
-  AXK_REQUIRE(q && kv_cache && indptr && indices && out, AXK_E_NULL);
+                                      const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
+                                      int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                      int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
+                                      size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(q && kv_cache && indptr && indices && last_page_len && out, AXK_E_NULL);
   const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096, AXK_E_SHAPE);
@@ -600,18 +727,21 @@ extern "C" int axk_paged_decode_split(const uint16_t* q, const uint16_t* kv_cach
   const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
   switch (head_dim) {
     case 64:
-      return launch_split<64>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
+      return launch_split<64>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
+                                  workspace, st);
     case 128:
-      return launch_split<128>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
+      return launch_split<128>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
+                                  workspace, st);
     default:
-      return launch_split<256>(q, kv_cache, indptr, indices, out, B, HQ, HKV, PS, num_pages, sm_scale, workspace, st);
+      return launch_split<256>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
+                                  workspace, st);
   }
 }
 
-extern "C" int axk_paged_decode_merge(const int32_t* indptr, uint16_t* out, int64_t batch, int64_t num_qo_heads,
-                                      int64_t num_kv_heads, int64_t head_dim, void* workspace,
-                                      size_t workspace_bytes, axk_stream_t stream) {
-  AXK_REQUIRE(indptr && out, AXK_E_NULL);
+extern "C" int axk_paged_decode_merge(const int32_t* indptr, const int32_t* last_page_len, uint16_t* out,
+                                      int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                      void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(indptr && last_page_len && out, AXK_E_NULL);
   const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
   const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
@@ -619,9 +749,9 @@ extern "C" int axk_paged_decode_merge(const int32_t* indptr, uint16_t* out, int6
   hipStream_t st = axk_stream(stream);
   const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads;
   switch (head_dim) {
-    case 64: return launch_merge<64>(indptr, out, B, HQ, HKV, workspace, st);
-    case 128: return launch_merge<128>(indptr, out, B, HQ, HKV, workspace, st);
-    default: return launch_merge<256>(indptr, out, B, HQ, HKV, workspace, st);
+    case 64: return launch_merge<64>(indptr, last_page_len, out, B, HQ, HKV, workspace, st);
+    case 128: return launch_merge<128>(indptr, last_page_len, out, B, HQ, HKV, workspace, st);
+    default: return launch_merge<256>(indptr, last_page_len, out, B, HQ, HKV, workspace, st);
   }
 }
 
@@ -631,10 +761,11 @@ extern "C" int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache,
                                     int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
                                     size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(last_page_len, AXK_E_NULL);
-  int rc = axk_paged_decode_split(q, kv_cache, indptr, indices, out, batch, num_qo_heads, num_kv_heads, head_dim,
-                                  page_size, num_pages, sm_scale, workspace, workspace_bytes, stream);
+  int rc = axk_paged_decode_split(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads,
+                                  num_kv_heads, head_dim, page_size, num_pages, sm_scale, workspace, workspace_bytes,
+                                  stream);
   if (rc != AXK_OK) return rc;
-  return axk_paged_decode_merge(indptr, out, batch, num_qo_heads, num_kv_heads, head_dim, workspace,
+  return axk_paged_decode_merge(indptr, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim, workspace,
                                 workspace_bytes, stream);
 }
 

@@ -108,14 +108,16 @@ class MxLinearWorkload(Workload):
 class PagedDecodeWorkload(Workload):
     """Config 1: paged decode attention, batch 16, 16 q / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384].
 
-    One step = plan (split-KV partition) + split (the attention kernel) + merge (LSE merge of split partials).
+    One step = plan (split-KV partition) + split (the attention kernel) + merge (LSE merge of split partials),
+    captured with the other steps in one HIP graph (as a serving decode step is).
     The roofline is the split kernel's: algorithmic bytes = K and V rows of every valid token + q + out +
     page table.
     """
 
     name = "paged_decode"
     kernel = "paged_decode_kernel<256>"  # launched by axk_paged_decode_split
-    timing = "events"
+    timing = "graph"       # value: K steps (plan + split + merge) replayed as one HIP graph
+    kernel_events = True   # roofline: the split kernel timed alone with HIP events
     traffic_profile = "paged_decode_config1_pmc.txt"
 
     def __init__(self, dev):
@@ -148,11 +150,11 @@ class PagedDecodeWorkload(Workload):
                                                        torch.cuda.current_stream().cuda_stream)
         self._split = lambda cache: lib.axk_paged_decode_split(
             self.q.data_ptr(), cache.data_ptr(), self.indptr.data_ptr(), self.indices.data_ptr(),
-            self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2], c["cache"].shape[0],
+            self.last.data_ptr(), self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2], c["cache"].shape[0],
             c["scale"], self.ws.data_ptr(), self.ws.numel(), torch.cuda.current_stream().cuda_stream)
-        self._merge = lambda: lib.axk_paged_decode_merge(self.indptr.data_ptr(), self.out.data_ptr(), b, hq, hkv, d,
-                                                         self.ws.data_ptr(), self.ws.numel(),
-                                                         torch.cuda.current_stream().cuda_stream)
+        self._merge = lambda: lib.axk_paged_decode_merge(self.indptr.data_ptr(), self.last.data_ptr(),
+                                                         self.out.data_ptr(), b, hq, hkv, d, self.ws.data_ptr(),
+                                                         self.ws.numel(), torch.cuda.current_stream().cuda_stream)
         self.config = {"workload": "config1: paged decode B=16 HQ=16 HKV=2 D=256 page=64 L~U[1024,16384]",
                        "sum_context": tot, "rotating_copies": self.copies}
         self.dtype = "bf16 (fp32 softmax / accumulation)"
@@ -452,7 +454,11 @@ def measure(wl, steps: int, warmup: int, eager: bool = False) -> tuple[float, fl
         end.record(stream)
         torch.cuda.synchronize()
         ms_per_step = start.elapsed_time(end) / steps
-        return ms_per_step, ms_per_step
+        if not getattr(wl, "kernel_events", False):
+            return ms_per_step, ms_per_step
+        # the roofline kernel on its own: eager steps, HIP events around each launch of it on the current stream
+        _, kernel_ms = measure(wl, steps, 0, eager=True)
+        return ms_per_step, kernel_ms
     # Eager steps on the current stream; HIP events bracket every launch of the dominant kernel.
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()

@@ -105,9 +105,10 @@ size_t axk_paged_decode_workspace_size(int64_t batch, int64_t num_qo_heads, int6
                                        int64_t head_dim);
 
 /* Split-KV work partition for axk_paged_decode_run, computed on the device from indptr /
- * last_page_len into the workspace (pages per split, one descriptor per work item; arrival counters
- * zeroed). It depends only on the page-table shape, so one plan serves every attention layer of a
- * decode step. */
+ * last_page_len into the workspace (pages per split, one descriptor per work item). It depends only on
+ * the page-table shape, so one plan serves every attention layer of a decode step. Up to 63 sequences
+ * the run kernels derive the same partition from the page table themselves and this call launches
+ * nothing (it still validates its arguments). */
 int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_page_len, int64_t batch,
                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                           void* workspace, size_t workspace_bytes, axk_stream_t stream);
@@ -116,15 +117,16 @@ int axk_paged_decode_plan(const int32_t* indptr, const int32_t* last_page_len, i
  * sequence handled by a single item gets its final output; the others leave fp32 partials
  * (running max, sum, unnormalised O) in the workspace for axk_paged_decode_merge. */
 int axk_paged_decode_split(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
-                           const int32_t* indices, uint16_t* out, int64_t batch, int64_t num_qo_heads,
-                           int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
-                           float sm_scale, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                           const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                           int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
+                           axk_stream_t stream);
 
 /* Second half (one launch): log-sum-exp merge of the split partials, as the split-KV merge of
  * models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:330-349; zero output for empty sequences. */
-int axk_paged_decode_merge(const int32_t* indptr, uint16_t* out, int64_t batch, int64_t num_qo_heads,
-                           int64_t num_kv_heads, int64_t head_dim, void* workspace, size_t workspace_bytes,
-                           axk_stream_t stream);
+int axk_paged_decode_merge(const int32_t* indptr, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, void* workspace,
+                           size_t workspace_bytes, axk_stream_t stream);
 
 /* The decode attention itself, using the plan held in `workspace` (same batch / heads / indptr):
  * axk_paged_decode_split then axk_paged_decode_merge. Arguments as axk_paged_decode. */

@@ -36,6 +36,9 @@ def _ref(c):
         ([300, 2000], 16, 1, 128, 256),
         ([64, 0, 65], 8, 1, 256, 64),  # an empty sequence yields zeros
         ([4096] * 3, 32, 4, 256, 64),
+        # more than 63 sequences: the partition comes from the plan kernel instead of the run kernels
+        ([(37 * i) % 700 for i in range(100)], 8, 1, 128, 32),
+        ([1 + (53 * i) % 4000 for i in range(64)], 16, 2, 256, 64),
     ],
 )
 def test_paged_decode_matches_oracle(dev, lens, hq, hkv, d, page):
@@ -120,16 +123,19 @@ def test_contract_errors(dev):
                                c["last_page_len"].to(dev), workspace=small)
 
 
-def test_plan_once_run_many(dev):
-    """One plan serves several runs (every attention layer of a step): the arrival counters reset."""
+@pytest.mark.parametrize("lens", [[100, 3000, 64, 9000], [50 + 13 * i for i in range(70)]])
+def test_plan_once_run_many(dev, lens):
+    """One plan serves several runs (every attention layer of a step), with the run kernels deriving the
+    partition (4 sequences) or reading the plan kernel's (70 sequences)."""
     g = torch.Generator().manual_seed(21)
-    c = configs.paged_case([100, 3000, 64, 9000], 16, 2, 256, 64, g)
-    ws = attention.paged_decode_workspace(4, 16, 2, 256, dev)
+    bsz = len(lens)
+    c = configs.paged_case(lens, 16, 2, 256, 64, g)
+    ws = attention.paged_decode_workspace(bsz, 16, 2, 256, dev)
     args = [c[k].to(dev) for k in ("indptr", "indices", "last_page_len")]
     cache = c["cache"].to(dev)
     attention.paged_decode_plan(args[0], args[2], 16, 2, 256, 64, ws)
     for trial in range(3):
-        q = torch.randn(4, 16, 256, generator=g).to(torch.bfloat16)
+        q = torch.randn(bsz, 16, 256, generator=g).to(torch.bfloat16)
         print(f"run {trial}", flush=True)
         got = attention.paged_decode_run(q.to(dev), cache, *args, workspace=ws, sm_scale=c["scale"]).cpu()
         ref = pa.paged_decode(q, c["cache"], c["indptr"], c["indices"], c["last_page_len"], c["scale"])
