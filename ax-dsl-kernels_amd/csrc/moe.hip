@@ -17,7 +17,7 @@
 //             gathered token rows staged in LDS, each wave streaming its gate and up tiles as MXFP4 over the
 //             full K with the next batch of loads in flight; SwiGLU in the epilogue
 //   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the pair's routing weight
-//   combine — one workgroup per token: shared gate, residual, sum over the token's K experts in slot order
+//   combine — one workgroup per token: shared gate once, residual, sum over the token's K experts in slot order
 // Every expert's weights are read once per call, whatever the number of its tokens.
 //
 // Prefill (tokens > kDecodeTokens; moe_slots_px + moe_combine of q35_moe_prefill.py:150-214):
@@ -584,32 +584,52 @@ struct CombineArgs {
   uint16_t* out;  // [T, H]
 };
 
+// Workgroup (token, block of columns): the shared gate (the h2 . w_shg dot), then 4 columns per thread and pass:
+// base = x_res + gate * y_sh, + the K routed rows in slot order, one bf16 rounding. Few tokens: one block per
+// 1024 columns; many tokens: one block per token (the gate is then computed once per token).
 __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   __shared__ float s_part[4];
+  __shared__ int s_pos[kMaxTopK];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint16_t* hrow = a.h2 + (int64_t)t * a.H;
-  float gate = 1.0f;
-  if (a.has_shared && a.w_shg) {  // each column block recomputes the token's gate (H MACs)
+  if (tid < a.K) s_pos[tid] = a.w.pair_pos[(int64_t)t * a.K + tid];
+  const bool gated = a.has_shared && a.w_shg;
+  if (gated) {
+    const uint16_t* hrow = a.h2 + (int64_t)t * a.H;
     float d = 0.f;
-    for (int i = tid; i < a.H; i += blockDim.x) d += bf16_bits_to_f32(hrow[i]) * bf16_bits_to_f32(a.w_shg[i]);
+    for (int i = 8 * tid; i < a.H; i += 8 * blockDim.x) {
+      const uint4 hv = *reinterpret_cast<const uint4*>(hrow + i);
+      const uint4 wv = *reinterpret_cast<const uint4*>(a.w_shg + i);
+      const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        d += __uint_as_float(hw[j] << 16) * __uint_as_float(ww[j] << 16) +
+             __uint_as_float(hw[j] & 0xffff0000u) * __uint_as_float(ww[j] & 0xffff0000u);
+    }
     d = wave_sum(d);
     if (lane == 0) s_part[wave] = d;
-    __syncthreads();
-    gate = sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]);
   }
-  const int i = blockIdx.y * blockDim.x + tid;
-  if (i >= a.H) return;
-  float acc = a.x_res ? bf16_bits_to_f32(a.x_res[(int64_t)t * a.H + i]) : 0.f;
-  if (a.has_shared) acc += gate * a.w.y_sh[(int64_t)t * a.H + i];
-  float part[kMaxTopK];
-#pragma unroll 8
-  for (int k = 0; k < a.K; ++k) {
-    const int pos = a.w.pair_pos[(int64_t)t * a.K + k];
-    part[k] = pos >= 0 ? a.w.y[(int64_t)pos * a.H + i] : 0.f;
+  __syncthreads();
+  const float gate = gated ? sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]) : 1.0f;
+  const int64_t row = (int64_t)t * a.H;
+  for (int i = blockIdx.y * 4 * blockDim.x + 4 * tid; i < a.H; i += 4 * blockDim.x * gridDim.y) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.x_res) {
+      const uint2 xv = *reinterpret_cast<const uint2*>(a.x_res + row + i);
+      acc = make_float4(__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                        __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
+    }
+    if (a.has_shared) {
+      const float4 ys = *reinterpret_cast<const float4*>(a.w.y_sh + row + i);
+      acc.x += gate * ys.x; acc.y += gate * ys.y; acc.z += gate * ys.z; acc.w += gate * ys.w;
+    }
+    for (int k = 0; k < a.K; ++k) {
+      const int pos = s_pos[k];
+      if (pos < 0) continue;  // an id outside [0, E) selected nothing
+      const float4 yv = *reinterpret_cast<const float4*>(a.w.y + (int64_t)pos * a.H + i);
+      acc.x += yv.x; acc.y += yv.y; acc.z += yv.z; acc.w += yv.w;
+    }
+    *reinterpret_cast<uint2*>(a.out + row + i) = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
   }
-#pragma unroll 8
-  for (int k = 0; k < a.K; ++k) acc += part[k];
-  a.out[(int64_t)t * a.H + i] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -718,7 +738,7 @@ __global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __rest
 }
 
 // ---------------------------------------------------------------------------------------------
-// prefill grouped GEMM: workgroup (tile of kBM rows of one expert, kBN output columns), 4 waves as 2 x 2
+// prefill grouped GEMM: workgroup (tile of kBM rows of one expert, kBN output columns), 4 waves across N
 // ---------------------------------------------------------------------------------------------
 constexpr int kLdA = kBK + 8;  // bf16 elements per staged activation row
 constexpr int kLdB = 48;       // bytes per staged weight row of a K step (32 code bytes + pad)
@@ -735,6 +755,9 @@ struct GGemmArgs {
 
 // MODE 0: gate-up + SwiGLU -> act (routed) / act_sh (shared); columns 64 n of gate and the same of up.
 // MODE 1: down -> y = acc * routing weight (routed) / y_sh (shared); 128 columns of H.
+// Each K step (kBK) a thread loads 16 activation values and one 32-code E8M0 block of a weight row; the loads
+// run two K steps ahead (three register stages). Weights stay MXFP4 in LDS (small buffers keep several
+// workgroups per CU) and are decoded into bf16 fragments with the scaled converts.
 template <int MODE>
 __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   __shared__ __align__(16) unsigned char smem[2 * kBufBytes];
@@ -743,7 +766,7 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   const int e = tl.x, row0 = tl.y, rows = tl.z;
   const bool shared = e < 0;
   const int nt = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wm = wave >> 1, wn = wave & 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
 
   // shapes of this tile's GEMM
@@ -752,22 +775,23 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   const int col0 = MODE == 0 ? 64 * nt : kBN * nt;
   if (col0 >= No) return;
 
-  // this thread's staged activation row and weight row
-  const int arow = tid >> 2, aq = tid & 3;           // 16 activation values of a 64-wide K step
-  const int brow = tid >> 1, bh = tid & 1;           // 32 codes (one E8M0 block) of a weight row
-  const uint16_t* asrc = nullptr;
-  if (arow < rows) {
+  // this thread's staged activation row (16 values of a K step) and weight row (one 32-code block)
+  const int arow = tid >> 2, aq = tid & 3;
+  const int brow = tid >> 1, bh = tid & 1;
+  const uint16_t* asrc;
+  {
+    const int r = min(arow, rows - 1);  // rows past the tile re-read its last row (never stored)
     if (MODE == 0) {
-      const int tok = shared ? row0 + arow : g.ws.row_tok[row0 + arow];
+      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
       asrc = g.a + (int64_t)tok * g.H;
     } else {
-      asrc = shared ? g.a_sh + (int64_t)(row0 + arow) * g.Fs : g.a + (int64_t)(row0 + arow) * g.F;
+      asrc = shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F;
     }
   }
-  const uint8_t* bsrc = nullptr;
-  const uint8_t* ssrc = nullptr;
+  const uint8_t* bsrc;
+  const uint8_t* ssrc;
   {
-    int wr;  // weight row in its matrix
+    int wr;
     const uint8_t *wb, *sb;
     if (MODE == 0) {
       const bool up = brow >= 64;
@@ -785,103 +809,111 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
       wb = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
       sb = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
     }
-    if (wr < No) {
-      bsrc = wb + (int64_t)wr * (Kd / 2);
-      ssrc = sb + (int64_t)wr * (Kd / 32);
-    }
+    wr = min(wr, No - 1);  // columns past No re-read the last row (never stored)
+    bsrc = wb + (int64_t)wr * (Kd / 2);
+    ssrc = sb + (int64_t)wr * (Kd / 32);
   }
 
-  // B rows of this wave's four 16-column tiles (gate-up: two gate tiles, then the same two of up)
-  int boff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) boff[j] = MODE == 0 ? (j < 2 ? 32 * wn + 16 * j : 64 + 32 * wn + 16 * (j - 2)) : 64 * wn + 16 * j;
-
-  uint4 ra0, ra1, rb;
-  uint32_t rs;
-  auto load = [&](int k0) {
-    ra0 = ra1 = rb = make_uint4(0u, 0u, 0u, 0u);
-    rs = 127u;
-    if (asrc && k0 + 16 * aq < Kd) {
-      ra0 = *reinterpret_cast<const uint4*>(asrc + k0 + 16 * aq);
-      ra1 = *reinterpret_cast<const uint4*>(asrc + k0 + 16 * aq + 8);
-    }
-    if (bsrc && k0 + 32 * bh < Kd) {
-      rb = *reinterpret_cast<const uint4*>(bsrc + (k0 + 32 * bh) / 2);
-      rs = ssrc[(k0 + 32 * bh) / 32];
-    }
-  };
-  auto store = [&](int buf) {
-    unsigned char* base = smem + buf * kBufBytes;
-    uint16_t* sA = reinterpret_cast<uint16_t*>(base);
-    unsigned char* sB = base + kBM * kLdA * 2;
-    unsigned char* sS = sB + kBN * kLdB;
-    *reinterpret_cast<uint4*>(sA + arow * kLdA + 16 * aq) = ra0;
-    *reinterpret_cast<uint4*>(sA + arow * kLdA + 16 * aq + 8) = ra1;
-    *reinterpret_cast<uint4*>(sB + brow * kLdB + 16 * bh) = rb;
-    sS[brow * 2 + bh] = (unsigned char)rs;
-  };
-
-  axk_f32x4 acc[2][4];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  // Wave w owns all kBM rows and two 16-column tiles: gate-up, gate columns 16w .. and the same up columns
+  // (B rows 16w and 64 + 16w); down, columns 32w .. 32w + 31. Each B fragment is decoded once per wave.
+  const int boff[2] = {MODE == 0 ? 16 * wave : 32 * wave, MODE == 0 ? 64 + 16 * wave : 32 * wave + 16};
 
   const int nk = Kd / kBK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ++ks) {
-    if (ks + 1 < nk) load((ks + 1) * kBK);
-    const unsigned char* base = smem + (ks & 1) * kBufBytes;
+  // Three register stages, as plain variables (a stage passed around by reference would live in scratch).
+  // Loads are unconditional (K step clamped): every path keeps the same loads in flight.
+#define AXK_GG_LOAD(A0, A1, B, S, ks)                                          \
+  do {                                                                         \
+    const int k0_ = min((ks), nk - 1) * kBK;                                   \
+    A0 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq);                \
+    A1 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq + 8);            \
+    B = *reinterpret_cast<const uint4*>(bsrc + (k0_ + 32 * bh) / 2);           \
+    S = ssrc[(k0_ + 32 * bh) / 32];                                            \
+  } while (0)
+#define AXK_GG_STORE(A0, A1, B, S, buf)                                        \
+  do {                                                                         \
+    unsigned char* base_ = smem + (buf) * kBufBytes;                           \
+    uint16_t* sA_ = reinterpret_cast<uint16_t*>(base_);                        \
+    unsigned char* sB_ = base_ + kBM * kLdA * 2;                               \
+    *reinterpret_cast<uint4*>(sA_ + arow * kLdA + 16 * aq) = A0;               \
+    *reinterpret_cast<uint4*>(sA_ + arow * kLdA + 16 * aq + 8) = A1;           \
+    *reinterpret_cast<uint4*>(sB_ + brow * kLdB + 16 * bh) = B;                \
+    (sB_ + kBN * kLdB)[brow * 2 + bh] = (unsigned char)(S);                   \
+  } while (0)
+
+  axk_f32x4 acc[4][2];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf) {
+    const unsigned char* base = smem + buf * kBufBytes;
     const uint16_t* sA = reinterpret_cast<const uint16_t*>(base);
     const unsigned char* sB = base + kBM * kLdA * 2;
     const unsigned char* sS = sB + kBN * kLdB;
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      axk_bf16x8 af[2], bf[4];
+    for (int kh = 0; kh < kBK / 32; ++kh) {
+      axk_bf16x8 af[4], bf[2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) af[mt] = load_bf16x8(sA + (32 * wm + 16 * mt + l16) * kLdA + 32 * kh + 8 * g4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const int r = boff[j] + l16;
         const uint32_t word = *reinterpret_cast<const uint32_t*>(sB + r * kLdB + 16 * kh + 4 * g4);
         bf[j] = fp4x8_to_bf16x8(word, e8m0_to_f32(sS[r * 2 + kh]));
       }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(sA + (16 * mt + l16) * kLdA + 32 * kh + 8 * g4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
     }
-    if (ks + 1 < nk) store((ks + 1) & 1);
+  };
+
+  // K steps: stage ks + 2 is loaded while ks is computed; stage ks + 1 goes to LDS after it
+  uint4 a00, a10, b0, a01, a11, b1, a02, a12, b2;
+  uint32_t s0, s1, s2;
+  AXK_GG_LOAD(a00, a10, b0, s0, 0);
+  AXK_GG_LOAD(a01, a11, b1, s1, 1);
+  AXK_GG_STORE(a00, a10, b0, s0, 0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ks += 3) {  // one exit: steps past nk only move clamped data
+    AXK_GG_LOAD(a02, a12, b2, s2, ks + 2);
+    compute(ks & 1);
+    AXK_GG_STORE(a01, a11, b1, s1, (ks + 1) & 1);
+    __syncthreads();
+    AXK_GG_LOAD(a00, a10, b0, s0, ks + 3);
+    if (ks + 1 < nk) compute((ks + 1) & 1);
+    AXK_GG_STORE(a02, a12, b2, s2, ks & 1);
+    __syncthreads();
+    AXK_GG_LOAD(a01, a11, b1, s1, ks + 4);
+    if (ks + 2 < nk) compute(ks & 1);
+    AXK_GG_STORE(a00, a10, b0, s0, (ks + 1) & 1);
     __syncthreads();
   }
+#undef AXK_GG_LOAD
+#undef AXK_GG_STORE
 
-  // epilogue: rows 32 wm + 16 mt + 4 g + r of the tile
+  // epilogue: rows 16 mt + 4 g + r of the tile
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 32 * wm + 16 * mt + 4 * g4 + r;
+      const int row = 16 * mt + 4 * g4 + r;
       if (row >= rows) continue;
       const int64_t prow = row0 + row;
       if (MODE == 0) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int col = col0 + 32 * wn + 16 * jj + l16;
-          if (col >= No) continue;
-          const float gv = round_bf16(acc[mt][jj][r]), uv = round_bf16(acc[mt][2 + jj][r]);
-          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
-          if (shared)
-            g.ws.act_sh[prow * g.Fs + col] = a;
-          else
-            g.ws.act[prow * g.F + col] = a;
-        }
+        const int col = col0 + 16 * wave + l16;
+        if (col >= No) continue;
+        const float gv = round_bf16(acc[mt][0][r]), uv = round_bf16(acc[mt][1][r]);
+        const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+        if (shared)
+          g.ws.act_sh[prow * g.Fs + col] = a;
+        else
+          g.ws.act[prow * g.F + col] = a;
       } else {
         const float rw = shared ? 1.0f : g.ws.row_w[prow];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = col0 + 64 * wn + 16 * j + l16;
+        for (int j = 0; j < 2; ++j) {
+          const int col = col0 + 32 * wave + 16 * j + l16;
           if (col >= No) continue;
           if (shared)
             g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
@@ -974,7 +1006,8 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, w};
     hipLaunchKernelGGL(moe_ggemm_kernel<1>, dim3(tiles, (unsigned)((H + kBN - 1) / kBN)), dim3(256), 0, st, dn);
     CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)((H + 255) / 256)), dim3(256), 0, st, ca);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
+                       0, st, ca);
     return axk_launch_status();
   }
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
@@ -1014,7 +1047,8 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   else
     hipLaunchKernelGGL(moe_down_kernel<false>, dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)((H + 255) / 256)), dim3(256), 0, st, ca);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
+                       0, st, ca);
   return axk_launch_status();
 }
 
