@@ -91,33 +91,51 @@ AXK_DEV void fp8x4_to_bf16(uint32_t w, __bf16* dst) {
   for (int i = 0; i < 4; ++i) dst[i] = (__bf16)e4m3_to_f32((w >> (8 * i)) & 0xffu);
 }
 
+typedef unsigned int axk_u32x4 __attribute__((ext_vector_type(4)));
+
 AXK_DEV axk_f32x4 mfma_bf16_16x16x32(axk_bf16x8 a, axk_bf16x8 b, axk_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Wave-wide reductions (wave64) through cross-lane shuffles.
+// Wave-wide reductions (wave64) on DPP lane moves inside rows of 16 lanes, then two row broadcasts that leave
+// the total in lane 63, read back as a uniform value. Control codes (GFX9 DPP): quad_perm [1,0,3,2] = 0xB1,
+// [2,3,0,1] = 0x4E, row_half_mirror 0x141, row_mirror 0x140, row_bcast15 0x142 (rows 1 and 3 take lane 15 of
+// the row below), row_bcast31 0x143 (rows 2 and 3 take lane 31).
+template <int CTRL, int ROW_MASK = 0xF>
+AXK_DEV float dpp_move(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF,
+                                                               false));
+}
+AXK_DEV float lane63(float v) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63)); }
+// The sum of every lane's v (the same value in every lane).
 AXK_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  v += dpp_move<0xB1>(v, v);
+  v += dpp_move<0x4E>(v, v);
+  v += dpp_move<0x141>(v, v);
+  v += dpp_move<0x140>(v, v);
+  v += dpp_move<0x142, 0xA>(0.f, v);
+  v += dpp_move<0x143, 0xC>(0.f, v);
+  return lane63(v);
+}
+// Sum inside aligned groups of W lanes (W = 2, 4, 8 or 16), the same value in every lane of the group.
+template <int W>
+AXK_DEV float group_sum(float v) {
+  static_assert(W == 2 || W == 4 || W == 8 || W == 16, "group of 2..16 lanes");
+  v += dpp_move<0xB1>(v, v);
+  if constexpr (W >= 4) v += dpp_move<0x4E>(v, v);
+  if constexpr (W >= 8) v += dpp_move<0x141>(v, v);
+  if constexpr (W >= 16) v += dpp_move<0x140>(v, v);
   return v;
 }
 AXK_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-// Reduction inside aligned groups of `width` lanes (width a power of two <= 64).
-template <int W>
-AXK_DEV float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-template <int W>
-AXK_DEV float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_move<0xB1>(v, v));
+  v = fmaxf(v, dpp_move<0x4E>(v, v));
+  v = fmaxf(v, dpp_move<0x141>(v, v));
+  v = fmaxf(v, dpp_move<0x140>(v, v));
+  v = fmaxf(v, dpp_move<0x142, 0xA>(v, v));
+  v = fmaxf(v, dpp_move<0x143, 0xC>(v, v));
+  return lane63(v);
 }
 
 AXK_DEV float silu_f32(float x) { return x / (1.0f + __expf(-x)); }

@@ -18,10 +18,10 @@
 //                          triangular solve (16 x 16 diagonal blocks by substitution, then two levels of block
 //                          products on fp32 MFMA), u and w on MFMA. Writes w, u, P, Gamma and the last decay
 //                          row to the workspace, and once per key head the normalised q and k^T.
-//   gdn_chunk_scan_kernel  one workgroup per (sequence, value head, 16-column slice of the state): the state's
-//                          columns evolve independently, so 8 workgroups carry one head's 128 x 128 fp32 state
-//                          through the chunks in order, held in MFMA accumulators, with each chunk's operands
-//                          loaded two chunks ahead.
+//   gdn_chunk_scan_kernel  one workgroup per (sequence, value head, slice of kScanSW state columns): the state's
+//                          columns evolve independently, so 128 / kScanSW workgroups carry one head's 128 x 128
+//                          fp32 state through the chunks in order, held in MFMA accumulators, with each chunk's
+//                          operands loaded two chunks ahead.
 #include "axk_common.h"
 #include "axk_host.h"
 
@@ -29,7 +29,6 @@ namespace {
 
 constexpr int kC = 64;    // chunk length
 constexpr int kD = 128;   // key / value head dim
-constexpr int kSlices = kD / 16;
 
 // Workspace: per (sequence, value head, chunk) w [C][D] bf16, u in the scan's accumulator order
 // [D/16 slices][4 waves][64 lanes][4 rows] bf16, P [C][C] bf16, Gamma and last-row decay [C] fp32; per
@@ -391,8 +390,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 // ---------------------------------------------------------------------------------------------
 // scan: the state through the chunks, one 16-column slice per workgroup
 // ---------------------------------------------------------------------------------------------
-constexpr int kLdS = kD + 8;  // bf16 state slice in LDS, [16 columns][LdS] (8 consecutive rows per lane read)
-constexpr int kLdV = kC + 8;  // bf16 v_new and its decayed copy, [16 columns][LdV]
+constexpr int kLdS = kD + 8;  // bf16 state slice in LDS, [slice columns][LdS] (8 consecutive rows per lane read)
+constexpr int kLdV = kC + 8;  // bf16 v_new and its decayed copy, [slice columns][LdV]
+#ifndef AXK_GDN_SW
+#define AXK_GDN_SW 32
+#endif
+#ifndef AXK_GDN_NW
+#define AXK_GDN_NW 4
+#endif
+constexpr int kScanSW = AXK_GDN_SW;  // state columns per scan workgroup
+constexpr int kScanNW = AXK_GDN_NW;  // waves per scan workgroup
 
 struct ScanArgs {
   const float* state_in;
@@ -402,23 +409,35 @@ struct ScanArgs {
   int B, T, NK, NV, NC;
 };
 
-// One chunk's operands for one wave: rows 16w .. 16w + 15 of w, q and P; rows 32w .. 32w + 31 of k^T;
-// u, Gamma and last-row decay at the rows of the wave's output tile (16w + 4g + r).
+// Scan workgroup (sequence, value head, slice of SW state columns) with NW waves. Wave w: token tile
+// tt = w % 4 (rows 16 tt .. of w, q, P and of the outputs; state rows 32 tt .. 32 tt + 31) and CPW of the slice's
+// 16-column tiles (column group w / 4).
+template <int SW, int NW>
+struct ScanShape {
+  static constexpr int CT = SW / 16;   // column tiles in the slice
+  static constexpr int CG = NW / 4;    // column groups
+  static constexpr int CPW = CT / CG;  // column tiles per wave
+  static_assert(NW % 4 == 0 && CT % CG == 0 && CPW >= 1, "scan shape");
+};
+
+// One chunk's operands for one wave (plain members: the struct stays in registers).
+template <int CPW>
 struct ScanOps {
   axk_bf16x8 wf[4], qf[4], pf[2], kf[2][2];
-  uint2 u;
+  uint2 u[CPW];
   float4 gm, dc;
   float glast;
 };
 
-AXK_DEV void scan_load(ScanOps& s, const ScanArgs& p, int b, int bh, int kh, int c, int s0, int wave, int l16,
-                       int g4) {
+template <int CPW>
+AXK_DEV void scan_load(ScanOps<CPW>& s, const ScanArgs& p, int b, int bh, int kh, int c, int ct0, int tt, int l16,
+                       int g4, int lane) {
   const int64_t vidx = (int64_t)bh * p.NC + c;
   const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;
-  const uint16_t* wg = p.ws.w + vidx * kC * kD + (16 * wave + l16) * kD + 8 * g4;
-  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (16 * wave + l16) * kD + 8 * g4;
-  const uint16_t* pg = p.ws.p + vidx * kC * kC + (16 * wave + l16) * kC + 8 * g4;
-  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (32 * wave + l16) * kC + 8 * g4;
+  const uint16_t* wg = p.ws.w + vidx * kC * kD + (16 * tt + l16) * kD + 8 * g4;
+  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (16 * tt + l16) * kD + 8 * g4;
+  const uint16_t* pg = p.ws.p + vidx * kC * kC + (16 * tt + l16) * kC + 8 * g4;
+  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (32 * tt + l16) * kC + 8 * g4;
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     s.wf[st] = load_bf16x8(wg + 32 * st);
@@ -430,80 +449,110 @@ AXK_DEV void scan_load(ScanOps& s, const ScanArgs& p, int b, int bh, int kh, int
     s.kf[0][st] = load_bf16x8(ktg + 32 * st);
     s.kf[1][st] = load_bf16x8(ktg + 16 * kC + 32 * st);
   }
-  s.u = *reinterpret_cast<const uint2*>(p.ws.u + vidx * kC * kD + (((s0 >> 4) * 4 + wave) * 64 + 16 * g4 + l16) * 4);
-  s.gm = *reinterpret_cast<const float4*>(p.ws.gam + vidx * kC + 16 * wave + 4 * g4);
-  s.dc = *reinterpret_cast<const float4*>(p.ws.dec + vidx * kC + 16 * wave + 4 * g4);
+#pragma unroll
+  for (int j = 0; j < CPW; ++j)
+    s.u[j] = *reinterpret_cast<const uint2*>(p.ws.u + vidx * kC * kD + (((ct0 + j) * 4 + tt) * 64 + lane) * 4);
+  s.gm = *reinterpret_cast<const float4*>(p.ws.gam + vidx * kC + 16 * tt + 4 * g4);
+  s.dc = *reinterpret_cast<const float4*>(p.ws.dec + vidx * kC + 16 * tt + 4 * g4);
   // a per-lane load (an index the compiler cannot prove uniform): a scalar load here would be waited for at once
   int z = 0;
   asm volatile("" : "+v"(z));
   s.glast = p.ws.gam[vidx * kC + kC - 1 + z];
 }
 
-__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
-  __shared__ __align__(16) uint16_t sS[16 * kLdS];
-  __shared__ __align__(16) uint16_t sV[16 * kLdV];
-  __shared__ __align__(16) uint16_t sXd[16 * kLdV];
+template <int SW, int NW>
+__global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
+  using Sh = ScanShape<SW, NW>;
+  constexpr int CPW = Sh::CPW;
+  __shared__ __align__(16) uint16_t sS[SW * kLdS];
+  __shared__ __align__(16) uint16_t sV[SW * kLdV];
+  __shared__ __align__(16) uint16_t sXd[SW * kLdV];
   const int nbh = p.B * p.NV;
   const int slice = blockIdx.x / nbh, bh = blockIdx.x - slice * nbh;  // slices of a head share an XCD
   const int b = bh / p.NV, h = bh - b * p.NV, kh = h / (p.NV / p.NK);
-  const int s0 = 16 * slice;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g4 = lane >> 4;
+  const int tt = wave & 3;
+  const int ct_l = (wave >> 2) * CPW;         // first column tile of this wave inside the slice
+  const int ct0 = slice * Sh::CT + ct_l;      // ... inside the head (the u layout's column tile)
+  const int col0 = 16 * ct0;                  // first state / output column of the wave
 
-  // state rows 32w + 16j + 4g + r, column s0 + l16, in two MFMA accumulator tiles
+  // state rows 32 tt + 16 i + 4 g + r, columns col0 + 16 j + l16, in MFMA accumulator tiles
   const float* sin = p.state_in + (int64_t)bh * kD * kD;
-  axk_f32x4 S[2];
+  axk_f32x4 S[2][CPW];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[j][r] = sin[(32 * wave + 16 * j + 4 * g4 + r) * kD + s0 + l16];
+    for (int j = 0; j < CPW; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[i][j][r] = sin[(32 * tt + 16 * i + 4 * g4 + r) * kD + col0 + 16 * j + l16];
   auto put_state = [&]() {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<uint2*>(sS + l16 * kLdS + 32 * wave + 16 * j + 4 * g4) =
-          make_uint2(pack_bf16x2(S[j][0], S[j][1]), pack_bf16x2(S[j][2], S[j][3]));
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < CPW; ++j)
+        *reinterpret_cast<uint2*>(sS + (16 * (ct_l + j) + l16) * kLdS + 32 * tt + 16 * i + 4 * g4) =
+            make_uint2(pack_bf16x2(S[i][j][0], S[i][j][1]), pack_bf16x2(S[i][j][2], S[i][j][3]));
   };
   put_state();
   __syncthreads();
 
-  auto process = [&](const ScanOps& o, int c) {
+  auto process = [&](const ScanOps<CPW>& o, int c) {
     // v_new = u - w S;  base = q S  (S as a bf16 operand, as the reference casts it)
-    axk_f32x4 vfs = {0.f, 0.f, 0.f, 0.f}, base = {0.f, 0.f, 0.f, 0.f};
+    axk_f32x4 vfs[CPW], base[CPW];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const axk_bf16x8 sf = load_bf16x8(sS + l16 * kLdS + 32 * st + 8 * g4);
-      vfs = mfma_bf16_16x16x32(o.wf[st], sf, vfs);
-      base = mfma_bf16_16x16x32(o.qf[st], sf, base);
+    for (int j = 0; j < CPW; ++j) vfs[j] = base[j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        const axk_bf16x8 sf = load_bf16x8(sS + (16 * (ct_l + j) + l16) * kLdS + 32 * st + 8 * g4);
+        vfs[j] = mfma_bf16_16x16x32(o.wf[st], sf, vfs[j]);
+        base[j] = mfma_bf16_16x16x32(o.qf[st], sf, base[j]);
+      }
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      float vn[4];
+      vn[0] = bf16_lo(o.u[j].x) - vfs[j][0];
+      vn[1] = bf16_hi(o.u[j].x) - vfs[j][1];
+      vn[2] = bf16_lo(o.u[j].y) - vfs[j][2];
+      vn[3] = bf16_hi(o.u[j].y) - vfs[j][3];
+      const int lc = 16 * (ct_l + j) + l16;
+      *reinterpret_cast<uint2*>(sV + lc * kLdV + 16 * tt + 4 * g4) =
+          make_uint2(pack_bf16x2(vn[0], vn[1]), pack_bf16x2(vn[2], vn[3]));
+      *reinterpret_cast<uint2*>(sXd + lc * kLdV + 16 * tt + 4 * g4) =
+          make_uint2(pack_bf16x2(vn[0] * o.dc.x, vn[1] * o.dc.y), pack_bf16x2(vn[2] * o.dc.z, vn[3] * o.dc.w));
     }
-    float vn[4];
-    vn[0] = bf16_lo(o.u.x) - vfs[0];
-    vn[1] = bf16_hi(o.u.x) - vfs[1];
-    vn[2] = bf16_lo(o.u.y) - vfs[2];
-    vn[3] = bf16_hi(o.u.y) - vfs[3];
-    *reinterpret_cast<uint2*>(sV + l16 * kLdV + 16 * wave + 4 * g4) =
-        make_uint2(pack_bf16x2(vn[0], vn[1]), pack_bf16x2(vn[2], vn[3]));
-    *reinterpret_cast<uint2*>(sXd + l16 * kLdV + 16 * wave + 4 * g4) =
-        make_uint2(pack_bf16x2(vn[0] * o.dc.x, vn[1] * o.dc.y), pack_bf16x2(vn[2] * o.dc.z, vn[3] * o.dc.w));
     __syncthreads();
     // o = Gamma (q S) + P v_new
-    axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + l16 * kLdV + 32 * st + 8 * g4), acc);
     const float gmr[4] = {o.gm.x, o.gm.y, o.gm.z, o.gm.w};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = c * kC + 16 * wave + 4 * g4 + r;
-      if (t < p.T)
-        p.out[(((int64_t)b * p.T + t) * p.NV + h) * kD + s0 + l16] =
-            (uint16_t)f32_to_bf16_bits(base[r] * gmr[r] + acc[r]);
+    for (int j = 0; j < CPW; ++j) {
+      const int lc = 16 * (ct_l + j) + l16;
+      axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + lc * kLdV + 32 * st + 8 * g4), acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = c * kC + 16 * tt + 4 * g4 + r;
+        if (t < p.T)
+          p.out[(((int64_t)b * p.T + t) * p.NV + h) * kD + col0 + 16 * j + l16] =
+              (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
+      }
     }
     // S <- Gamma_last S + k^T (v_new * decay_last)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < CPW; ++j) {
+      const int lc = 16 * (ct_l + j) + l16;
+      axk_bf16x8 xf[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[j][r] *= o.glast;
+      for (int st = 0; st < 2; ++st) xf[st] = load_bf16x8(sXd + lc * kLdV + 32 * st + 8 * g4);
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
-        S[j] = mfma_bf16_16x16x32(o.kf[j][st], load_bf16x8(sXd + l16 * kLdV + 32 * st + 8 * g4), S[j]);
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[i][j][r] *= o.glast;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) S[i][j] = mfma_bf16_16x16x32(o.kf[i][st], xf[st], S[i][j]);
+      }
     }
     put_state();
     __syncthreads();
@@ -513,30 +562,32 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(ScanArgs p) {
   // unconditional (past the end they repeat the last chunk, unused) so every path through the loop has the
   // same loads in flight and the waits before each use stay two sets deep.
   const int last = p.NC - 1;
-  ScanOps o0, o1, o2;
-  scan_load(o0, p, b, bh, kh, 0, s0, wave, l16, g4);
-  scan_load(o1, p, b, bh, kh, min(1, last), s0, wave, l16, g4);
+  ScanOps<CPW> o0, o1, o2;
+  scan_load(o0, p, b, bh, kh, 0, ct0, tt, l16, g4, lane);
+  scan_load(o1, p, b, bh, kh, min(1, last), ct0, tt, l16, g4, lane);
   for (int c = 0; c < p.NC; c += 3) {
-    scan_load(o2, p, b, bh, kh, min(c + 2, last), s0, wave, l16, g4);
+    scan_load(o2, p, b, bh, kh, min(c + 2, last), ct0, tt, l16, g4, lane);
     process(o0, c);
-    scan_load(o0, p, b, bh, kh, min(c + 3, last), s0, wave, l16, g4);
+    scan_load(o0, p, b, bh, kh, min(c + 3, last), ct0, tt, l16, g4, lane);
     if (c + 1 < p.NC) process(o1, c + 1);
-    scan_load(o1, p, b, bh, kh, min(c + 4, last), s0, wave, l16, g4);
+    scan_load(o1, p, b, bh, kh, min(c + 4, last), ct0, tt, l16, g4, lane);
     if (c + 2 < p.NC) process(o2, c + 2);
   }
 
   float* sout = p.state_out + (int64_t)bh * kD * kD;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sout[(32 * wave + 16 * j + 4 * g4 + r) * kD + s0 + l16] = S[j][r];
+    for (int j = 0; j < CPW; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sout[(32 * tt + 16 * i + 4 * g4 + r) * kD + col0 + 16 * j + l16] = S[i][j][r];
 }
 
 int check_chunk_dims(int64_t batch, int64_t tokens, int64_t nk, int64_t nv, int64_t dk, int64_t dv,
                      int64_t chunk) {
   AXK_REQUIRE(dk == kD && dv == kD && chunk == kC, AXK_E_SHAPE);
   AXK_REQUIRE(batch > 0 && tokens > 0 && nk > 0 && nv > 0 && nv % nk == 0, AXK_E_SHAPE);
-  AXK_REQUIRE(batch <= 65535 && nv <= 65535 && batch * nv * kSlices <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(batch <= 65535 && nv <= 65535 && batch * nv * (kD / kScanSW) <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(tokens <= INT32_MAX - kC, AXK_E_SHAPE);
   return AXK_OK;
 }
@@ -589,6 +640,7 @@ extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const
   int lrc = axk_launch_status();
   if (lrc != AXK_OK) return lrc;
   ScanArgs sa{state_in, state_out, out, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC};
-  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3((unsigned)(kSlices * batch * num_v_heads)), dim3(256), 0, st, sa);
+  hipLaunchKernelGGL((gdn_chunk_scan_kernel<kScanSW, kScanNW>), dim3((unsigned)((kD / kScanSW) * batch * num_v_heads)),
+                     dim3(64 * kScanNW), 0, st, sa);
   return axk_launch_status();
 }

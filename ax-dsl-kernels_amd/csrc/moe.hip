@@ -50,20 +50,20 @@ constexpr int kBM = 64, kBN = 128, kBK = 64;  // prefill GEMM tile
 struct MoeWs {
   int* counts;      // [E]
   int* offsets;     // [E + 1]
-  int* active_e;    // [E]
-  int* active_off;  // [E]
-  int* active_cnt;  // [E]
+  int4* active;     // [E] active expert i: {rows, expert, first sorted row, 0}; rows 0 past the list
   int* n_active;    // [1]
   int* pair_pos;    // [P] sorted row of pair p = t * K + k
   int* row_tok;     // [P] token of sorted row
   float* row_w;     // [P] routing weight of sorted row
   uint16_t* act;    // [P, F] bf16 routed activations (sorted rows)
   uint16_t* act_sh; // [T, Fs] bf16 shared-expert activations
-  float* y;         // [P, H] fp32 routed outputs x routing weight
+  float* y;         // [P, H] fp32 routed outputs x routing weight, row t * K + k for pair (t, k)
   float* y_sh;      // [T, H] fp32 shared-expert output
   int* blk;         // [NB, E] prefill: per-block expert counts, then per-block row bases
   int4* tiles;      // [max tiles] prefill GEMM tiles: {expert (-1: shared), first row, rows, 0}
   int* n_tiles;     // [1]
+  int* row_pair;    // [P] pair t * K + k of sorted row (y is indexed by pair)
+  float* rpart;     // [S, T, E] decode router: partial logits of K slice s
 };
 
 int64_t prefill_blocks(int64_t T) { return (T + kBlkTokens - 1) / kBlkTokens; }
@@ -73,17 +73,25 @@ int64_t prefill_max_tiles(int64_t T, int64_t E, int64_t K) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Decode router: K slices reduced in fixed order by the routing kernel (8 steps of 32 per slice, 1..16 slices).
+constexpr int kMaxRouterSplits = 16;
+int router_splits(int64_t H) {
+  const int64_t s = (H / 32) / 8;
+  return (int)(s < 1 ? 1 : (s > kMaxRouterSplits ? kMaxRouterSplits : s));
+}
+
 constexpr int kWsParts = 16;
 
 size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs, size_t* off) {
   const int64_t P = T * K;
   const bool prefill = T > kDecodeTokens;
   const size_t nb = prefill ? (size_t)prefill_blocks(T) : 0, nt = prefill ? (size_t)prefill_max_tiles(T, E, K) : 0;
+  const size_t rp = prefill ? 0 : (size_t)router_splits(H) * T * E * 4;
   size_t o = 0;
-  const size_t sizes[kWsParts] = {(size_t)E * 4,     (size_t)(E + 1) * 4, (size_t)E * 4,      (size_t)E * 4,
-                                  (size_t)E * 4,     4,                   (size_t)P * 4,      (size_t)P * 4,
-                                  (size_t)P * 4,     (size_t)P * F * 2,   (size_t)T * Fs * 2, (size_t)P * H * 4,
-                                  (size_t)T * H * 4, nb * E * 4,          nt * 16,            4};
+  const size_t sizes[kWsParts] = {(size_t)E * 4,      (size_t)(E + 1) * 4, (size_t)E * 16,    4,
+                                  (size_t)P * 4,      (size_t)P * 4,       (size_t)P * 4,     (size_t)P * F * 2,
+                                  (size_t)T * Fs * 2, (size_t)P * H * 4,   (size_t)T * H * 4, nb * E * 4,
+                                  nt * 16,            4,                   (size_t)P * 4,     rp};
   for (int i = 0; i < kWsParts; ++i) {
     off[i] = o;
     o = align256(o + sizes[i]);
@@ -96,18 +104,68 @@ MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, in
   moe_ws_layout(T, H, E, K, F, Fs, off);
   unsigned char* b = reinterpret_cast<unsigned char*>(ws);
   return {reinterpret_cast<int*>(b + off[0]),       reinterpret_cast<int*>(b + off[1]),
-          reinterpret_cast<int*>(b + off[2]),       reinterpret_cast<int*>(b + off[3]),
+          reinterpret_cast<int4*>(b + off[2]),      reinterpret_cast<int*>(b + off[3]),
           reinterpret_cast<int*>(b + off[4]),       reinterpret_cast<int*>(b + off[5]),
-          reinterpret_cast<int*>(b + off[6]),       reinterpret_cast<int*>(b + off[7]),
-          reinterpret_cast<float*>(b + off[8]),     reinterpret_cast<uint16_t*>(b + off[9]),
-          reinterpret_cast<uint16_t*>(b + off[10]), reinterpret_cast<float*>(b + off[11]),
-          reinterpret_cast<float*>(b + off[12]),    reinterpret_cast<int*>(b + off[13]),
-          reinterpret_cast<int4*>(b + off[14]),     reinterpret_cast<int*>(b + off[15])};
+          reinterpret_cast<float*>(b + off[6]),     reinterpret_cast<uint16_t*>(b + off[7]),
+          reinterpret_cast<uint16_t*>(b + off[8]),  reinterpret_cast<float*>(b + off[9]),
+          reinterpret_cast<float*>(b + off[10]),    reinterpret_cast<int*>(b + off[11]),
+          reinterpret_cast<int4*>(b + off[12]),     reinterpret_cast<int*>(b + off[13]),
+          reinterpret_cast<int*>(b + off[14]),      reinterpret_cast<float*>(b + off[15])};
 }
 
 // ---------------------------------------------------------------------------------------------
 // route: one wave per token
 // ---------------------------------------------------------------------------------------------
+// Softmax and top-K of one token's logits, lane l holding experts l + 64 i (x[i] = -inf past E). Selection k is
+// the largest remaining logit (the softmax is monotonic), ties to the lower expert id: a DPP wave maximum, then
+// one ballot per register finds the lowest id holding it. Lane k keeps selection k.
+template <int V>
+AXK_DEV void route_select(const float (&x)[V], int lane, int E, int K, int norm_topk, int32_t* __restrict__ ids,
+                          float* __restrict__ wts) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < V; ++i) mx = fmaxf(mx, x[i]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) sum += (i * 64 + lane < E) ? __expf(x[i] - mx) : 0.f;
+  const float inv = 1.0f / wave_sum(sum);
+  unsigned taken = 0u;  // bit i: x[i] already selected
+  float myp = 0.f, psum = 0.f;
+  int myid = 0;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      if (i * 64 + lane < E && !(taken >> i & 1u)) bv = fmaxf(bv, x[i]);
+    const float m = wave_max(bv);
+    int id = -1;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const unsigned long long hit = __ballot(i * 64 + lane < E && !(taken >> i & 1u) && x[i] == m);
+      if (id < 0 && hit) id = i * 64 + __builtin_ctzll(hit);
+    }
+    if (id < 0) {  // no remaining logit compares equal (NaN): the lowest remaining id
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const unsigned long long left = __ballot(i * 64 + lane < E && !(taken >> i & 1u));
+        if (id < 0 && left) id = i * 64 + __builtin_ctzll(left);
+      }
+    }
+    if ((id & 63) == lane) taken |= 1u << (id >> 6);
+    const float p = __expf(m - mx) * inv;
+    if (lane == k) {
+      myp = p;
+      myid = id;
+    }
+    psum += p;
+  }
+  if (lane < K) {
+    ids[lane] = myid;
+    wts[lane] = norm_topk ? myp / psum : myp;
+  }
+}
+
 template <int V>  // expert logits per lane (num_experts <= 64 V)
 __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int K,
                                                         int norm_topk, int32_t* __restrict__ ids,
@@ -120,53 +178,77 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 #pragma unroll
   for (int i = 0; i < V; ++i) {
     const int e = i * 64 + lane;
-    x[i] = e < E ? lg[e] : -INFINITY;
+    const float v = lg[min(e, E - 1)];  // unconditional (clamped) loads
+    x[i] = e < E ? v : -INFINITY;
   }
-  float mx = -INFINITY;
+  route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+}
+
+// Decode routing from the router's partial logits: logit = sum of the S K-slice partials in slice order
+// (written out as the layer's logits), then route_select.
+template <int V>
+__global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part, int S, int T, int E,
+                                                             int K, int norm_topk, float* __restrict__ logits,
+                                                             int32_t* __restrict__ ids, float* __restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
+  float pv[kMaxRouterSplits][V];
 #pragma unroll
-  for (int i = 0; i < V; ++i) mx = fmaxf(mx, x[i]);
-  mx = wave_max(mx);
-  float sum = 0.f;
+  for (int sl = 0; sl < kMaxRouterSplits; ++sl)
 #pragma unroll
-  for (int i = 0; i < V; ++i) sum += (i * 64 + lane < E) ? __expf(x[i] - mx) : 0.f;
-  sum = wave_sum(sum);
-  const float inv = 1.0f / sum;
-  // top-K on the logits (the softmax is monotonic): descending value, ties to the lower expert id
-  unsigned taken = 0u;  // bit i: x[i] already selected
-  float myp = 0.f;       // lane k keeps the k-th selection
-  int myid = 0;
-  float psum = 0.f;
-  for (int k = 0; k < K; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    for (int i = 0; i < V; ++i)
+      pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
+  float x[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const int e = i * 64 + lane;
-      if (e < E && !(taken >> i & 1u) && (x[i] > bv || (x[i] == bv && e < bi))) {
-        bv = x[i];
-        bi = e;
-      }
-    }
+  for (int i = 0; i < V; ++i) {
+    float v = pv[0][i];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {  // butterfly: every lane ends with the same winner
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    const float p = __expf(bv - mx) * inv;
-    if (lane == k) {
-      myp = p;
-      myid = bi;
-    }
-    psum += p;
+    for (int sl = 1; sl < kMaxRouterSplits; ++sl)
+      if (sl < S) v += pv[sl][i];
+    x[i] = v;
   }
-  if (lane < K) {
-    ids[(int64_t)t * K + lane] = myid;
-    wts[(int64_t)t * K + lane] = norm_topk ? myp / psum : myp;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int e = i * 64 + lane;
+    if (e < E) logits[(int64_t)t * E + e] = x[i];
+    else x[i] = -INFINITY;
+  }
+  route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+}
+
+// Decode router GEMM, split over K: workgroup (16 experts, 16 tokens, K slice s); wave w multiplies the slice's
+// 32-wide K steps w, w + 4, ... on MFMA (h2 rows as A, router rows as B), the four waves are summed in LDS and
+// the partial logits written to part[s]. Rows past T or E are clamped for the loads and never stored.
+__global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h2,
+                                                         const uint16_t* __restrict__ wr, int T, int H, int E,
+                                                         int S, float* __restrict__ part) {
+  __shared__ float4 red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16, sl = blockIdx.z;
+  const int ns = H / 32, st0 = (int)((int64_t)sl * ns / S), st1 = (int)((int64_t)(sl + 1) * ns / S);
+  const uint16_t* arow = h2 + (int64_t)min(t0 + nl, T - 1) * H + 8 * g;
+  const uint16_t* brow = wr + (int64_t)min(e0 + nl, E - 1) * H + 8 * g;
+  axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = st0 + wave; i < st1; i += 8) {
+    const int j = min(i + 4, st1 - 1);
+    const axk_bf16x8 a0 = load_bf16x8(arow + 32 * i), b0 = load_bf16x8(brow + 32 * i);
+    const axk_bf16x8 a1 = load_bf16x8(arow + 32 * j), b1 = load_bf16x8(brow + 32 * j);
+    acc = mfma_bf16_16x16x32(a0, b0, acc);
+    if (i + 4 < st1) acc = mfma_bf16_16x16x32(a1, b1, acc);
+  }
+  red[wave][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __syncthreads();
+  if (wave != 0) return;
+  const float4 v0 = red[0][lane], v1 = red[1][lane], v2 = red[2][lane], v3 = red[3][lane];
+  const float v[4] = {((v0.x + v1.x) + v2.x) + v3.x, ((v0.y + v1.y) + v2.y) + v3.y, ((v0.z + v1.z) + v2.z) + v3.z,
+                      ((v0.w + v1.w) + v2.w) + v3.w};
+  const int e = e0 + nl;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * g + r;
+    if (t < T && e < E) part[((int64_t)sl * T + t) * E + e] = v[r];
   }
 }
 
@@ -233,9 +315,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
       w.counts[e] = cnt[j];
       w.offsets[e] = off;
       if (cnt[j] > 0) {
-        w.active_e[aoff] = e;
-        w.active_off[aoff] = off;
-        w.active_cnt[aoff] = cnt[j];
+        w.active[aoff] = make_int4(cnt[j], e, off, 0);
         ++aoff;
       }
     }
@@ -245,7 +325,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
     w.offsets[E] = tot;
     *w.n_active = tota;
   }
-  for (int j = tota + tid; j < E; j += blockDim.x) w.active_cnt[j] = 0;  // streaming kernels exit on cnt 0
+  for (int j = tota + tid; j < E; j += blockDim.x) w.active[j] = make_int4(0, 0, 0, 0);  // streaming kernels exit
   __syncthreads();
   for (int p = tid; p < P; p += blockDim.x) {
     const int e = ids[p], t = p / K;
@@ -259,6 +339,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
     w.pair_pos[p] = pos;
     w.row_tok[pos] = t;
     w.row_w[pos] = wts[p];
+    w.row_pair[pos] = p;
   }
 }
 
@@ -348,10 +429,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     Fo = a.Fs;
     gw = a.sg_w; gs = a.sg_s; uw = a.su_w; us = a.su_s;
   } else {
-    cnt = a.w.active_cnt[slot];  // 0 past the active list (written so by the grouping kernel)
+    int4 am = a.w.active[slot];  // one 16-byte record; rows 0 past the active list
+    asm volatile("" : "+s"(am.x), "+s"(am.y), "+s"(am.z));  // keep the record's loads together, before the exit
+    cnt = am.x;
     if (cnt == 0) return;
-    const int64_t e = a.w.active_e[slot];
-    row0 = a.w.active_off[slot];
+    const int64_t e = am.y;
+    row0 = am.z;
     Fo = a.F;
     const int64_t rows = 2 * (int64_t)a.F;
     gw = a.e_gw + e * rows * (a.H / 2);
@@ -481,10 +564,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     dw = a.sd_w; ds = a.sd_s;
     act = a.w.act_sh;
   } else {
-    cnt = a.w.active_cnt[slot];
+    int4 am = a.w.active[slot];
+    asm volatile("" : "+s"(am.x), "+s"(am.y), "+s"(am.z));
+    cnt = am.x;
     if (cnt == 0) return;
-    const int64_t e = a.w.active_e[slot];
-    row0 = a.w.active_off[slot];
+    const int64_t e = am.y;
+    row0 = am.z;
     K = a.F;
     dw = a.e_dw + e * (int64_t)a.H * (a.F / 2);
     ds = a.e_ds + e * (int64_t)a.H * (a.F / 32);
@@ -517,10 +602,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
 
   for (int m0 = mbeg; m0 < cnt; m0 += kStageRows) {
     float rw[4];
+    int pr[4];  // the rows' pair indices (y is indexed by pair)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + 4 * g + r;
       rw[r] = (!shared && m < cnt) ? a.w.row_w[row0 + m] : 1.0f;
+      pr[r] = (!shared && m < cnt) ? a.w.row_pair[row0 + m] : 0;
     }
     axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
@@ -548,7 +635,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
             if (shared)
               a.w.y_sh[(int64_t)m * a.H + col] = acc[r];
             else
-              a.w.y[(int64_t)(row0 + m) * a.H + col] = acc[r] * rw[r];
+              a.w.y[(int64_t)pr[r] * a.H + col] = acc[r] * rw[r];
           }
         }
         acc = axk_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -584,17 +671,40 @@ struct CombineArgs {
   uint16_t* out;  // [T, H]
 };
 
-// Workgroup (token, block of columns): the shared gate (the h2 . w_shg dot), then 4 columns per thread and pass:
-// base = x_res + gate * y_sh, + the K routed rows in slot order, one bf16 rounding. Few tokens: one block per
+// Workgroup (token, block of columns), 4 columns per thread and pass: base = x_res + gate * y_sh, + the K routed
+// rows in slot order (y is indexed by pair t K + k; a pair whose id is outside [0, E) selected nothing), one bf16
+// rounding. The first pass's loads are unconditional (clamped) and issued before the shared-gate dot
+// (h2 . w_shg, reduced across the workgroup), so both share one memory round trip. Few tokens: one block per
 // 1024 columns; many tokens: one block per token (the gate is then computed once per token).
 __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   __shared__ float s_part[4];
-  __shared__ int s_pos[kMaxTopK];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < a.K) s_pos[tid] = a.w.pair_pos[(int64_t)t * a.K + tid];
+  const int64_t row = (int64_t)t * a.H, pair0 = (int64_t)t * a.K;
+  auto gather = [&](int i, float4& acc, float4& ys) {
+    acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    ys = acc;
+    if (a.x_res) {
+      const uint2 xv = *reinterpret_cast<const uint2*>(a.x_res + row + i);
+      acc = make_float4(__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
+                        __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
+    }
+    if (a.has_shared) ys = *reinterpret_cast<const float4*>(a.w.y_sh + row + i);
+    for (int k = 0; k < a.K; ++k) {
+      const float4 yv = *reinterpret_cast<const float4*>(a.w.y + (pair0 + k) * a.H + i);
+      if (a.w.pair_pos[pair0 + k] < 0) continue;  // uniform: an id outside [0, E)
+      acc.x += yv.x; acc.y += yv.y; acc.z += yv.z; acc.w += yv.w;
+    }
+  };
+  auto finish = [&](int i, float4 acc, const float4& ys, float gate) {
+    acc.x += gate * ys.x; acc.y += gate * ys.y; acc.z += gate * ys.z; acc.w += gate * ys.w;
+    *reinterpret_cast<uint2*>(a.out + row + i) = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+  };
+  const int step = 4 * blockDim.x * gridDim.y, i0 = blockIdx.y * 4 * blockDim.x + 4 * tid;
+  float4 acc0, ys0;
+  gather(min(i0, a.H - 4), acc0, ys0);
   const bool gated = a.has_shared && a.w_shg;
   if (gated) {
-    const uint16_t* hrow = a.h2 + (int64_t)t * a.H;
+    const uint16_t* hrow = a.h2 + row;
     float d = 0.f;
     for (int i = 8 * tid; i < a.H; i += 8 * blockDim.x) {
       const uint4 hv = *reinterpret_cast<const uint4*>(hrow + i);
@@ -607,28 +717,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
     }
     d = wave_sum(d);
     if (lane == 0) s_part[wave] = d;
+    __syncthreads();
   }
-  __syncthreads();
   const float gate = gated ? sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]) : 1.0f;
-  const int64_t row = (int64_t)t * a.H;
-  for (int i = blockIdx.y * 4 * blockDim.x + 4 * tid; i < a.H; i += 4 * blockDim.x * gridDim.y) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (a.x_res) {
-      const uint2 xv = *reinterpret_cast<const uint2*>(a.x_res + row + i);
-      acc = make_float4(__uint_as_float(xv.x << 16), __uint_as_float(xv.x & 0xffff0000u),
-                        __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
-    }
-    if (a.has_shared) {
-      const float4 ys = *reinterpret_cast<const float4*>(a.w.y_sh + row + i);
-      acc.x += gate * ys.x; acc.y += gate * ys.y; acc.z += gate * ys.z; acc.w += gate * ys.w;
-    }
-    for (int k = 0; k < a.K; ++k) {
-      const int pos = s_pos[k];
-      if (pos < 0) continue;  // an id outside [0, E) selected nothing
-      const float4 yv = *reinterpret_cast<const float4*>(a.w.y + (int64_t)pos * a.H + i);
-      acc.x += yv.x; acc.y += yv.y; acc.z += yv.z; acc.w += yv.w;
-    }
-    *reinterpret_cast<uint2*>(a.out + row + i) = make_uint2(pack_bf16x2(acc.x, acc.y), pack_bf16x2(acc.z, acc.w));
+  if (i0 < a.H) finish(i0, acc0, ys0, gate);
+  for (int i = i0 + step; i < a.H; i += step) {
+    float4 acc, ys;
+    gather(i, acc, ys);
+    finish(i, acc, ys, gate);
   }
 }
 
@@ -696,9 +792,7 @@ __global__ __launch_bounds__(256) void moe_pscan_kernel(int T, int E, int NB, in
         base += c;
       }
       if (cnt[j] > 0) {
-        w.active_e[aoff] = e;
-        w.active_off[aoff] = off;
-        w.active_cnt[aoff] = cnt[j];
+        w.active[aoff] = make_int4(cnt[j], e, off, 0);
         ++aoff;
       }
       for (int r = 0; r < cnt[j]; r += kBM) w.tiles[toff++] = make_int4(e, off + r, min(kBM, cnt[j] - r), 0);
@@ -734,6 +828,7 @@ __global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __rest
     w.pair_pos[p] = pos;
     w.row_tok[pos] = t0 + t;
     w.row_w[pos] = wts[p];
+    w.row_pair[pos] = (int)p;
   }
 }
 
@@ -911,6 +1006,7 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
           g.ws.act[prow * g.F + col] = a;
       } else {
         const float rw = shared ? 1.0f : g.ws.row_w[prow];
+        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int col = col0 + 32 * wave + 16 * j + l16;
@@ -918,7 +1014,416 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
           if (shared)
             g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
           else
-            g.ws.y[prow * g.H + col] = acc[mt][j][r] * rw;
+            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// prefill grouped GEMM, wide tiles: workgroup (tile of kBM rows of one expert, 256 weight rows), wave w a 64 x 64
+// block of the output (four 16-row x four 16-column MFMA tiles): every A fragment feeds four MFMAs and every B
+// fragment four. MODE 0: weight rows = 128 gate + the same 128 up columns (SwiGLU pairs gate and up tiles in the
+// same lanes); MODE 1: 256 columns of H.
+// LDS per buffer: A [64 rows][72 bf16] (144-byte rows), B [256 rows][48 bytes] = 32 code bytes with the row's
+// 4-byte groups reordered (group g of k-half h at 8 g + 4 h, so one 64-bit read gives a lane both halves) and
+// the two E8M0 scale bytes at +32. Row strides of 36 and 12 banks keep the 16-lane phases of every read and
+// write on distinct banks.
+// ---------------------------------------------------------------------------------------------
+constexpr int kG2Rows = 256;                       // weight rows per workgroup
+constexpr int kG2LdA = kBK + 8;                    // bf16 per staged activation row
+constexpr int kG2LdB = 48;                         // bytes per staged weight row
+constexpr int kG2Buf = kBM * kG2LdA * 2 + kG2Rows * kG2LdB;
+constexpr int kG2Cols0 = kG2Rows / 2;              // gate-up: output (act) columns per workgroup
+constexpr int kG2Cols1 = kG2Rows;                  // down: output columns per workgroup
+
+template <int MODE>
+__global__ __launch_bounds__(256) void moe_ggemm2_kernel(GGemmArgs g) {
+  __shared__ __align__(16) unsigned char smem[2 * kG2Buf];
+  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
+  const int4 tl = g.ws.tiles[blockIdx.x];
+  const int e = tl.x, row0 = tl.y, rows = tl.z;
+  const bool shared = e < 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+
+  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);  // reduction length
+  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;  // output columns
+  const int col0 = blockIdx.y * (MODE == 0 ? kG2Cols0 : kG2Cols1);
+  if (col0 >= No) return;
+
+  // staging: thread t loads A row t % 64, k quarter t / 64 (16 values) and B row t (32 code bytes + 2 scales)
+  const int arow = tid & 63, aq = tid >> 6;
+  const uint16_t* asrc;
+  {
+    const int r = min(arow, rows - 1);  // rows past the tile re-read its last row (never stored)
+    if (MODE == 0) {
+      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
+      asrc = g.a + (int64_t)tok * g.H;
+    } else {
+      asrc = shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F;
+    }
+  }
+  const uint8_t* bsrc;
+  const uint8_t* ssrc;
+  {
+    int wr;
+    const uint8_t *wb, *sb;
+    if (MODE == 0) {
+      const bool up = tid >= kG2Cols0;
+      wr = col0 + (tid & (kG2Cols0 - 1));
+      if (shared) {
+        wb = up ? g.u_sh : g.w_sh;
+        sb = up ? g.us_sh : g.s_sh;
+      } else {
+        const int64_t rows2 = 2 * (int64_t)g.F;
+        wb = g.w + (int64_t)e * rows2 * (g.H / 2) + (up ? (int64_t)g.F * (g.H / 2) : 0);
+        sb = g.s + (int64_t)e * rows2 * (g.H / 32) + (up ? (int64_t)g.F * (g.H / 32) : 0);
+      }
+    } else {
+      wr = col0 + tid;
+      wb = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
+      sb = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
+    }
+    wr = min(wr, No - 1);  // columns past No re-read the last row (never stored)
+    bsrc = wb + (int64_t)wr * (Kd / 2);
+    ssrc = sb + (int64_t)wr * (Kd / 32);
+  }
+  // B rows of wave w's four column tiles j (16 rows each)
+  int brow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    brow[j] = MODE == 0 ? (j >> 1) * kG2Cols0 + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
+
+  const int nk = Kd / kBK;
+  // three register stages as plain variables; loads unconditional (K step clamped)
+#define AXK_G2_LOAD(A0, A1, B0, B1, S, ks)                                     \
+  do {                                                                         \
+    const int k0_ = min((ks), nk - 1) * kBK;                                   \
+    A0 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq);                \
+    A1 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq + 8);            \
+    B0 = *reinterpret_cast<const uint4*>(bsrc + k0_ / 2);                      \
+    B1 = *reinterpret_cast<const uint4*>(bsrc + k0_ / 2 + 16);                 \
+    S = *reinterpret_cast<const uint16_t*>(ssrc + k0_ / 32);                   \
+  } while (0)
+  // code dwords d0..d7 hold k 8i .. 8i + 7 (group i % 4 of k-half i / 4): stored as d0 d4 d1 d5 d2 d6 d3 d7
+#define AXK_G2_STORE(A0, A1, B0, B1, S, buf)                                   \
+  do {                                                                         \
+    unsigned char* base_ = smem + (buf) * kG2Buf;                              \
+    uint16_t* sA_ = reinterpret_cast<uint16_t*>(base_);                        \
+    unsigned char* sB_ = base_ + kBM * kG2LdA * 2 + tid * kG2LdB;              \
+    *reinterpret_cast<uint4*>(sA_ + arow * kG2LdA + 16 * aq) = A0;             \
+    *reinterpret_cast<uint4*>(sA_ + arow * kG2LdA + 16 * aq + 8) = A1;         \
+    *reinterpret_cast<uint4*>(sB_) = make_uint4(B0.x, B1.x, B0.y, B1.y);       \
+    *reinterpret_cast<uint4*>(sB_ + 16) = make_uint4(B0.z, B1.z, B0.w, B1.w);  \
+    *reinterpret_cast<uint16_t*>(sB_ + 32) = (uint16_t)(S);                    \
+  } while (0)
+
+  axk_f32x4 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+    const unsigned char* base = smem + buf * kG2Buf;
+    const uint16_t* sA = reinterpret_cast<const uint16_t*>(base);
+    const unsigned char* sB = base + kBM * kG2LdA * 2;
+    uint2 bw[4];
+    uint32_t sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned char* rp = sB + (brow[j] + l16) * kG2LdB;
+      bw[j] = *reinterpret_cast<const uint2*>(rp + 8 * g4);
+      sc[j] = *reinterpret_cast<const uint16_t*>(rp + 32);
+    }
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      axk_bf16x8 af[4], bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bf[j] = fp4x8_to_bf16x8(kh ? bw[j].y : bw[j].x, e8m0_to_f32((sc[j] >> (8 * kh)) & 0xffu));
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(sA + (16 * mt + l16) * kG2LdA + 32 * kh + 8 * g4);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
+    }
+  };
+
+  uint4 a00, a10, b00, b10, a01, a11, b01, b11, a02, a12, b02, b12;
+  uint32_t s0, s1, s2;
+  AXK_G2_LOAD(a00, a10, b00, b10, s0, 0);
+  AXK_G2_LOAD(a01, a11, b01, b11, s1, 1);
+  AXK_G2_STORE(a00, a10, b00, b10, s0, 0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ks += 3) {  // one exit: steps past nk only move clamped data
+    AXK_G2_LOAD(a02, a12, b02, b12, s2, ks + 2);
+    compute(ks & 1);
+    AXK_G2_STORE(a01, a11, b01, b11, s1, (ks + 1) & 1);
+    __syncthreads();
+    AXK_G2_LOAD(a00, a10, b00, b10, s0, ks + 3);
+    if (ks + 1 < nk) compute((ks + 1) & 1);
+    AXK_G2_STORE(a02, a12, b02, b12, s2, ks & 1);
+    __syncthreads();
+    AXK_G2_LOAD(a01, a11, b01, b11, s1, ks + 4);
+    if (ks + 2 < nk) compute(ks & 1);
+    AXK_G2_STORE(a00, a10, b00, b10, s0, (ks + 1) & 1);
+    __syncthreads();
+  }
+#undef AXK_G2_LOAD
+#undef AXK_G2_STORE
+
+  // epilogue: rows 16 mt + 4 g + r of the tile
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mt + 4 * g4 + r;
+      if (row >= rows) continue;
+      const int64_t prow = row0 + row;
+      if (MODE == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = col0 + 32 * wave + 16 * j + l16;
+          if (col >= No) continue;
+          const float gv = round_bf16(acc[mt][j][r]), uv = round_bf16(acc[mt][j + 2][r]);
+          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+          if (shared)
+            g.ws.act_sh[prow * g.Fs + col] = a;
+          else
+            g.ws.act[prow * g.F + col] = a;
+        }
+      } else {
+        const float rw = shared ? 1.0f : g.ws.row_w[prow];
+        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = col0 + 64 * wave + 16 * j + l16;
+          if (col >= No) continue;
+          if (shared)
+            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
+          else
+            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// prefill grouped GEMM, line-coalesced staging (the kernel launched): as moe_ggemm2_kernel for the MFMA work,
+// but every global load instruction covers whole 128-byte lines of few rows, which keeps the address path's
+// per-line work low: A per K step as 8 rows x 128 bytes per instruction; B for 4 K steps at once (128 code
+// bytes of a weight row = 256 k) as 8 rows x 128 bytes per instruction, held in registers for a whole super-step
+// and written to LDS at its start; the E8M0 scales of the whole reduction are staged once per workgroup.
+// LDS: A [2][64 rows][144 bytes]; B [256 rows][144 bytes] (one super-step); scales [256 rows][Kd/32 + 16].
+// ---------------------------------------------------------------------------------------------
+constexpr int kG3LdB = 144;  // bytes per staged weight row of a super-step (128 code bytes + pad)
+constexpr int kG3ABytes = kBM * kG2LdA * 2;
+size_t g3_lds_bytes(int Kd) { return 2 * (size_t)kG3ABytes + (size_t)kG2Rows * kG3LdB + (size_t)kG2Rows * (Kd / 32 + 16); }
+
+template <int MODE>
+__global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
+  const int4 tl = g.ws.tiles[blockIdx.x];
+  const int e = tl.x, row0 = tl.y, rows = tl.z;
+  const bool shared = e < 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+
+  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);  // reduction length
+  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;  // output columns
+  const int col0 = blockIdx.y * (MODE == 0 ? kG2Cols0 : kG2Cols1);
+  if (col0 >= No) return;
+  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  unsigned char* sB = smem + 2 * kG3ABytes;
+  unsigned char* sS = sB + kG2Rows * kG3LdB;
+  const int ldS = Kd / 32 + 16;
+
+  // A: thread t stages rows t / 8 and t / 8 + 32, 16-byte chunk t % 8 of the K step (one line per row)
+  const int ar = tid >> 3, ac = tid & 7;
+  const uint16_t* asrc[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = min(ar + 32 * h, rows - 1);  // rows past the tile re-read its last row (never stored)
+    if (MODE == 0) {
+      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
+      asrc[h] = g.a + (int64_t)tok * g.H + 8 * ac;
+    } else {
+      asrc[h] = (shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F) + 8 * ac;
+    }
+  }
+  // B: LDS row rho -> weight row (gate-up: rho < 128 gate column col0 + rho, else up column col0 + rho - 128;
+  // down: column col0 + rho), clamped to the last column (never stored)
+  const uint8_t *wgate, *wup, *sgate, *sup;
+  if (MODE == 0) {
+    if (shared) {
+      wgate = g.w_sh; wup = g.u_sh; sgate = g.s_sh; sup = g.us_sh;
+    } else {
+      const int64_t rows2 = 2 * (int64_t)g.F;
+      wgate = g.w + (int64_t)e * rows2 * (g.H / 2);
+      wup = wgate + (int64_t)g.F * (g.H / 2);
+      sgate = g.s + (int64_t)e * rows2 * (g.H / 32);
+      sup = sgate + (int64_t)g.F * (g.H / 32);
+    }
+  } else {
+    wgate = wup = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
+    sgate = sup = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
+  }
+  auto wrow = [&](int rho, bool scale) -> const uint8_t* {
+    const bool up = MODE == 0 && rho >= kG2Cols0;
+    const int c = min(col0 + (MODE == 0 ? (rho & (kG2Cols0 - 1)) : rho), No - 1);
+    return scale ? (up ? sup : sgate) + (int64_t)c * (Kd / 32) : (up ? wup : wgate) + (int64_t)c * (Kd / 2);
+  };
+  // B super-step loads: instruction i covers LDS rows 64 wave + 8 i .. + 7, lane -> row + lane / 8, chunk lane % 8
+  const int bsub = lane >> 3, bc = lane & 7;
+  const int nk = Kd / kBK, nsup = (nk + 3) / 4;
+  const int brow_bytes = Kd / 2;
+
+  // the E8M0 scales of the whole reduction: 16-byte units when the row length allows, else 2-byte units
+  {
+    const int sb = Kd / 32;
+    if (sb % 16 == 0 && (((uintptr_t)sgate | (uintptr_t)sup) & 15) == 0) {
+      const int u = sb / 16;
+      for (int idx = tid; idx < kG2Rows * u; idx += 256) {
+        const int rho = idx / u, q = idx - rho * u;
+        *reinterpret_cast<uint4*>(sS + rho * ldS + 16 * q) = *reinterpret_cast<const uint4*>(wrow(rho, true) + 16 * q);
+      }
+    } else {
+      const int u = sb / 2;
+      for (int idx = tid; idx < kG2Rows * u; idx += 256) {
+        const int rho = idx / u, q = idx - rho * u;
+        *reinterpret_cast<uint16_t*>(sS + rho * ldS + 2 * q) = *reinterpret_cast<const uint16_t*>(wrow(rho, true) + 2 * q);
+      }
+    }
+  }
+
+  int brow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    brow[j] = MODE == 0 ? (j >> 1) * kG2Cols0 + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
+
+#define AXK_G3_LOADA(A0, A1, ks)                                                   \
+  do {                                                                             \
+    const int k0_ = min((ks), nk - 1) * kBK;                                       \
+    A0 = *reinterpret_cast<const uint4*>(asrc[0] + k0_);                           \
+    A1 = *reinterpret_cast<const uint4*>(asrc[1] + k0_);                           \
+  } while (0)
+#define AXK_G3_STOREA(A0, A1, buf)                                                 \
+  do {                                                                             \
+    uint16_t* d_ = sA + (buf) * (kBM * kG2LdA) + ar * kG2LdA + 8 * ac;             \
+    *reinterpret_cast<uint4*>(d_) = A0;                                            \
+    *reinterpret_cast<uint4*>(d_ + 32 * kG2LdA) = A1;                              \
+  } while (0)
+  axk_u32x4 bq[8];  // a native vector type: an array of it stays in registers
+#define AXK_G3_LOADB(sup_)                                                         \
+  do {                                                                             \
+    const int off_ = min((sup_) * 128 + 16 * bc, brow_bytes - 16);                 \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                  \
+      bq[i] = *reinterpret_cast<const axk_u32x4*>(wrow(64 * wave + 8 * i + bsub, false) + off_); \
+  } while (0)
+#define AXK_G3_STOREB()                                                            \
+  do {                                                                             \
+    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                  \
+      *reinterpret_cast<axk_u32x4*>(sB + (64 * wave + 8 * i + bsub) * kG3LdB + 16 * bc) = bq[i]; \
+  } while (0)
+
+  axk_f32x4 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int ks) __attribute__((always_inline)) {
+    const uint16_t* a = sA + (ks & 1) * (kBM * kG2LdA);
+    const int q = ks & 3;
+    uint32_t sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = *reinterpret_cast<const uint16_t*>(sS + (brow[j] + l16) * ldS + 2 * ks);
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      axk_bf16x8 af[4], bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(sB + (brow[j] + l16) * kG3LdB + 32 * q + 16 * kh + 4 * g4);
+        bf[j] = fp4x8_to_bf16x8(w, e8m0_to_f32((sc[j] >> (8 * kh)) & 0xffu));
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(a + (16 * mt + l16) * kG2LdA + 32 * kh + 8 * g4);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
+    }
+  };
+
+  // prologue: A step 0 in LDS, steps 1 and 2 in registers; B super-step 0 in LDS, super-step 1 in registers
+  uint4 a00, a10, a01, a11, a02, a12, a03, a13;
+  AXK_G3_LOADA(a00, a10, 0);
+  AXK_G3_LOADB(0);
+  AXK_G3_LOADA(a01, a11, 1);
+  AXK_G3_LOADA(a02, a12, 2);
+  AXK_G3_STOREA(a00, a10, 0);
+  AXK_G3_STOREB();
+  AXK_G3_LOADB(1);
+  __syncthreads();
+  // K step ks: A step ks + 3 is loaded, ks computed from A buffer ks & 1 and B quarter ks & 3, A step ks + 1
+  // goes to LDS; at the end of a super-step the next one's B goes to LDS and the one after is loaded. Four A
+  // register sets rotate with the super-step, so every load is unconditional and every wait exact.
+#define AXK_G3_STEP(ks, AN0, AN1, AL0, AL1, LAST)                                  \
+  do {                                                                             \
+    AXK_G3_LOADA(AL0, AL1, (ks) + 3);                                              \
+    if ((ks) < nk) compute(ks);                                                    \
+    AXK_G3_STOREA(AN0, AN1, ((ks) + 1) & 1);                                       \
+    if (LAST) {                                                                    \
+      __syncthreads();                                                             \
+      AXK_G3_STOREB();                                                             \
+      AXK_G3_LOADB(((ks) >> 2) + 2);                                               \
+    }                                                                              \
+    __syncthreads();                                                               \
+  } while (0)
+  for (int ks = 0; ks < nk; ks += 4) {
+    AXK_G3_STEP(ks, a01, a11, a03, a13, false);
+    AXK_G3_STEP(ks + 1, a02, a12, a00, a10, false);
+    AXK_G3_STEP(ks + 2, a03, a13, a01, a11, false);
+    AXK_G3_STEP(ks + 3, a00, a10, a02, a12, true);
+  }
+#undef AXK_G3_STEP
+#undef AXK_G3_LOADA
+#undef AXK_G3_STOREA
+#undef AXK_G3_LOADB
+#undef AXK_G3_STOREB
+
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * mt + 4 * g4 + r;
+      if (row >= rows) continue;
+      const int64_t prow = row0 + row;
+      if (MODE == 0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int col = col0 + 32 * wave + 16 * j + l16;
+          if (col >= No) continue;
+          const float gv = round_bf16(acc[mt][j][r]), uv = round_bf16(acc[mt][j + 2][r]);
+          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+          if (shared)
+            g.ws.act_sh[prow * g.Fs + col] = a;
+          else
+            g.ws.act[prow * g.F + col] = a;
+        }
+      } else {
+        const float rw = shared ? 1.0f : g.ws.row_w[prow];
+        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = col0 + 64 * wave + 16 * j + l16;
+          if (col >= No) continue;
+          if (shared)
+            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
+          else
+            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
         }
       }
     }
@@ -937,6 +1442,7 @@ int check_dims(const MoeDims& d) {
   } else {  // prefill GEMM: whole 64-wide K steps and 64-column gate / up tiles
     AXK_REQUIRE(d.T <= kMaxPrefillTokens && d.T * d.K <= kMaxPrefillPairs, AXK_E_SHAPE);
     AXK_REQUIRE(d.H % 64 == 0 && d.F % 64 == 0 && d.Fs % 64 == 0 && d.Fs >= 0, AXK_E_SHAPE);
+    AXK_REQUIRE(d.H <= 8192 && d.F <= 8192 && d.Fs <= 8192, AXK_E_SHAPE);  // whole-K scales staged in LDS
   }
   AXK_REQUIRE(d.H <= INT32_MAX && d.F <= INT32_MAX, AXK_E_SHAPE);
   return AXK_OK;
@@ -1002,9 +1508,21 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
     const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
     const int fmax = F > Fs ? F : Fs;
     GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, w};
-    hipLaunchKernelGGL(moe_ggemm_kernel<0>, dim3(tiles, (unsigned)(fmax / 64)), dim3(256), 0, st, gu);
+    const size_t lds0 = g3_lds_bytes(H), lds1 = g3_lds_bytes(fmax);
+    static bool g3_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+    if (!g3_raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm3_kernel<0>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess ||
+          hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm3_kernel<1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
+        return AXK_E_LAUNCH;
+      g3_raised = true;
+    }
+    hipLaunchKernelGGL(moe_ggemm3_kernel<0>, dim3(tiles, (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0)), dim3(256),
+                       lds0, st, gu);
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, w};
-    hipLaunchKernelGGL(moe_ggemm_kernel<1>, dim3(tiles, (unsigned)((H + kBN - 1) / kBN)), dim3(256), 0, st, dn);
+    hipLaunchKernelGGL(moe_ggemm3_kernel<1>, dim3(tiles, (unsigned)((H + kG2Cols1 - 1) / kG2Cols1)), dim3(256),
+                       lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
                        0, st, ca);
@@ -1061,9 +1579,37 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
                               int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
                               int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(w_router && logits, AXK_E_NULL);
-  int rc = axk_bf16_gemm(h2, hidden, w_router, nullptr, logits, AXK_DT_F32, tokens, num_experts, hidden, stream);
-  if (rc != AXK_OK) return rc;
-  rc = axk_moe_route(logits, topk_ids, topk_weights, tokens, num_experts, top_k, norm_topk_prob, stream);
+  int rc;
+  if (tokens > kDecodeTokens) {
+    rc = axk_bf16_gemm(h2, hidden, w_router, nullptr, logits, AXK_DT_F32, tokens, num_experts, hidden, stream);
+    if (rc != AXK_OK) return rc;
+    rc = axk_moe_route(logits, topk_ids, topk_weights, tokens, num_experts, top_k, norm_topk_prob, stream);
+  } else {
+    // decode: the router as K-slice partials in the workspace, summed in slice order by the routing kernel
+    AXK_REQUIRE(h2 && topk_ids && topk_weights, AXK_E_NULL);
+    rc = check_dims({tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0});
+    if (rc != AXK_OK) return rc;
+    AXK_REQUIRE(axk_aligned(h2, 16) && axk_aligned(w_router, 16), AXK_E_ALIGN);
+    const size_t need =
+        axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
+    AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+    const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
+    const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, S = router_splits(hidden);
+    hipStream_t st = axk_stream(stream);
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
+                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
+    const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+    if (E <= 64)
+      hipLaunchKernelGGL(moe_route_part_kernel<1>, grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, logits,
+                         topk_ids, topk_weights);
+    else if (E <= 256)
+      hipLaunchKernelGGL(moe_route_part_kernel<4>, grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, logits,
+                         topk_ids, topk_weights);
+    else
+      hipLaunchKernelGGL(moe_route_part_kernel<kMaxExperts / 64>, grid, block, 0, st, w.rpart, S, T, E, K,
+                         norm_topk_prob, logits, topk_ids, topk_weights);
+    rc = axk_launch_status();
+  }
   if (rc != AXK_OK) return rc;
   return axk_moe_experts(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
                          e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,

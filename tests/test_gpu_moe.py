@@ -75,6 +75,15 @@ def test_moe_route_ties_and_experts_given_routing(dev):
     sids, swts = omoe.route(logits, 6)
     assert torch.equal(ids.cpu(), sids)
     torch.testing.assert_close(wts.cpu(), swts)
+    # ties in every register column of the 256- and 1024-expert layouts, and -inf logits (chosen last)
+    for e, k in [(200, 8), (1000, 32)]:
+        lg = (torch.arange(e) % 7).float().repeat(2, 1)
+        lg[1, ::3] = float("-inf")
+        ids, wts = moe.moe_route(lg.to(dev), k)
+        sids, swts = omoe.route(lg, k)
+        assert torch.equal(ids.cpu(), sids)
+        torch.testing.assert_close(wts.cpu(), swts)
+    ids, wts = moe.moe_route(logits.to(dev), 6)
     # experts with host-given routing (the reference's two-call path: host route(), experts kernel)
     g = torch.Generator().manual_seed(4)
     w = configs.moe_weights(g, hidden=128, experts=32, inter=64, shared_inter=64, router_std=0.5)
