@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 constexpr int kLdS = kD + 8;  // bf16 state slice in LDS, [slice columns][LdS] (8 consecutive rows per lane read)
 constexpr int kLdV = kC + 8;  // bf16 v_new and its decayed copy, [slice columns][LdV]
 #ifndef AXK_GDN_SW
-#define AXK_GDN_SW 32
+#define AXK_GDN_SW 16
 #endif
 #ifndef AXK_GDN_NW
 #define AXK_GDN_NW 4
