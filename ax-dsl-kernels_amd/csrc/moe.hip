@@ -75,6 +75,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Decode router: K slices reduced in fixed order by the routing kernel (8 steps of 32 per slice, 1..16 slices).
 constexpr int kMaxRouterSplits = 16;
+constexpr int kPrefillRouterSplits = 2;  // prefill router: K halves (two partial logits per token)
 int router_splits(int64_t H) {
   const int64_t s = (H / 32) / 8;
   return (int)(s < 1 ? 1 : (s > kMaxRouterSplits ? kMaxRouterSplits : s));
@@ -86,7 +87,7 @@ size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int6
   const int64_t P = T * K;
   const bool prefill = T > kDecodeTokens;
   const size_t nb = prefill ? (size_t)prefill_blocks(T) : 0, nt = prefill ? (size_t)prefill_max_tiles(T, E, K) : 0;
-  const size_t rp = prefill ? 0 : (size_t)router_splits(H) * T * E * 4;
+  const size_t rp = (size_t)(prefill ? kPrefillRouterSplits : router_splits(H)) * T * E * 4;
   size_t o = 0;
   const size_t sizes[kWsParts] = {(size_t)E * 4,      (size_t)(E + 1) * 4, (size_t)E * 16,    4,
                                   (size_t)P * 4,      (size_t)P * 4,       (size_t)P * 4,     (size_t)P * F * 2,
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 
 // Decode routing from the router's partial logits: logit = sum of the S K-slice partials in slice order
 // (written out as the layer's logits), then route_select.
-template <int V>
+template <int V, int MAXS>  // MAXS: bound on the number of partials
 __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part, int S, int T, int E,
                                                              int K, int norm_topk, float* __restrict__ logits,
                                                              int32_t* __restrict__ ids, float* __restrict__ wts) {
@@ -194,9 +195,9 @@ __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __rest
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
   // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
-  float pv[kMaxRouterSplits][V];
+  float pv[MAXS][V];
 #pragma unroll
-  for (int sl = 0; sl < kMaxRouterSplits; ++sl)
+  for (int sl = 0; sl < MAXS; ++sl)
 #pragma unroll
     for (int i = 0; i < V; ++i)
       pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __rest
   for (int i = 0; i < V; ++i) {
     float v = pv[0][i];
 #pragma unroll
-    for (int sl = 1; sl < kMaxRouterSplits; ++sl)
+    for (int sl = 1; sl < MAXS; ++sl)
       if (sl < S) v += pv[sl][i];
     x[i] = v;
   }
@@ -216,6 +217,92 @@ __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __rest
     else x[i] = -INFINITY;
   }
   route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+}
+
+// Prefill router GEMM: workgroup (64 tokens, 64 experts, K slice s), waves 2 x 2 with 32 x 32 each; both operands
+// staged in LDS per 64-wide K step from line-coalesced loads (8 lanes per 128-byte row segment), loaded two
+// steps ahead in register stages. Writes the slice's partial logits like the decode router.
+__global__ __launch_bounds__(256) void moe_router_tile_kernel(const uint16_t* __restrict__ h2,
+                                                              const uint16_t* __restrict__ wr, int T, int H, int E,
+                                                              int S, float* __restrict__ part) {
+  constexpr int kLd = 72;
+  __shared__ __align__(16) uint16_t sA[2][64 * kLd];
+  __shared__ __align__(16) uint16_t sB[2][64 * kLd];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64, sl = blockIdx.z;
+  const int nall = H / 64, kb = (int)((int64_t)sl * nall / S), nk = (int)((int64_t)(sl + 1) * nall / S) - kb;
+  const int r = tid >> 3, c = tid & 7;
+  const uint16_t* ap0 = h2 + (int64_t)min(t0 + r, T - 1) * H + 8 * c;
+  const uint16_t* ap1 = h2 + (int64_t)min(t0 + r + 32, T - 1) * H + 8 * c;
+  const uint16_t* bp0 = wr + (int64_t)min(e0 + r, E - 1) * H + 8 * c;
+  const uint16_t* bp1 = wr + (int64_t)min(e0 + r + 32, E - 1) * H + 8 * c;
+  const int wm = wave >> 1, wn = wave & 1;
+  if (nk <= 0) return;
+#define AXK_RT_LOAD(A0, A1, B0, B1, ks)                        \
+  do {                                                         \
+    const int k_ = (kb + min((ks), nk - 1)) * 64;              \
+    A0 = *reinterpret_cast<const uint4*>(ap0 + k_);            \
+    A1 = *reinterpret_cast<const uint4*>(ap1 + k_);            \
+    B0 = *reinterpret_cast<const uint4*>(bp0 + k_);            \
+    B1 = *reinterpret_cast<const uint4*>(bp1 + k_);            \
+  } while (0)
+#define AXK_RT_STORE(A0, A1, B0, B1, buf)                                  \
+  do {                                                                     \
+    *reinterpret_cast<uint4*>(&sA[buf][r * kLd + 8 * c]) = A0;             \
+    *reinterpret_cast<uint4*>(&sA[buf][(r + 32) * kLd + 8 * c]) = A1;      \
+    *reinterpret_cast<uint4*>(&sB[buf][r * kLd + 8 * c]) = B0;             \
+    *reinterpret_cast<uint4*>(&sB[buf][(r + 32) * kLd + 8 * c]) = B1;      \
+  } while (0)
+  axk_f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      axk_bf16x8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = load_bf16x8(&sA[buf][(32 * wm + 16 * i + l16) * kLd + 32 * kh + 8 * g4]);
+        bf[i] = load_bf16x8(&sB[buf][(32 * wn + 16 * i + l16) * kLd + 32 * kh + 8 * g4]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma_bf16_16x16x32(af[i], bf[j], acc[i][j]);
+    }
+  };
+  uint4 a00, a10, b00, b10, a01, a11, b01, b11, a02, a12, b02, b12;
+  AXK_RT_LOAD(a00, a10, b00, b10, 0);
+  AXK_RT_LOAD(a01, a11, b01, b11, 1);
+  AXK_RT_STORE(a00, a10, b00, b10, 0);
+  __syncthreads();
+  for (int ks = 0; ks < nk; ks += 3) {  // one exit; steps past nk only move clamped data
+    AXK_RT_LOAD(a02, a12, b02, b12, ks + 2);
+    compute(ks & 1);
+    AXK_RT_STORE(a01, a11, b01, b11, (ks + 1) & 1);
+    __syncthreads();
+    AXK_RT_LOAD(a00, a10, b00, b10, ks + 3);
+    if (ks + 1 < nk) compute((ks + 1) & 1);
+    AXK_RT_STORE(a02, a12, b02, b12, ks & 1);
+    __syncthreads();
+    AXK_RT_LOAD(a01, a11, b01, b11, ks + 4);
+    if (ks + 2 < nk) compute(ks & 1);
+    AXK_RT_STORE(a00, a10, b00, b10, (ks + 1) & 1);
+    __syncthreads();
+  }
+#undef AXK_RT_LOAD
+#undef AXK_RT_STORE
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int t = t0 + 32 * wm + 16 * i + 4 * g4 + q, e = e0 + 32 * wn + 16 * j + l16;
+        if (t < T && e < E) part[((int64_t)sl * T + t) * E + e] = acc[i][j][q];
+      }
 }
 
 // Decode router GEMM, split over K: workgroup (16 experts, 16 tokens, K slice s); wave w multiplies the slice's
@@ -763,34 +850,70 @@ __global__ __launch_bounds__(256) void moe_pscan_kernel(int T, int E, int NB, in
   __shared__ int s_tmp[12];
   constexpr int EPT = kMaxExperts / 256;
   const int tid = threadIdx.x;
+  // the per-block counts are read in chunks of kChunk blocks for all of the thread's experts at once (independent
+  // loads: one memory round trip per chunk, not one per block)
+  constexpr int kChunk = 8;
   int cnt[EPT], sum = 0, nact = 0, ntile = 0;
 #pragma unroll
+  for (int j = 0; j < EPT; ++j) cnt[j] = 0;
+  for (int b0 = 0; b0 < NB; b0 += kChunk) {
+    int v[EPT][kChunk];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        const int e = tid * EPT + j, b = b0 + i;
+        v[j][i] = (e < E && b < NB) ? w.blk[(int64_t)b * E + e] : 0;
+      }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) cnt[j] += v[j][i];
+  }
+#pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int e = tid * EPT + j;
-    int c = 0;
-    if (e < E)
-      for (int b = 0; b < NB; ++b) c += w.blk[(int64_t)b * E + e];
-    cnt[j] = c;
-    sum += c;
-    nact += c > 0;
-    ntile += (c + kBM - 1) / kBM;
+    sum += cnt[j];
+    nact += cnt[j] > 0;
+    ntile += (cnt[j] + kBM - 1) / kBM;
   }
   int tot, tota, tott;
   int off = block_exclusive_scan256(sum, s_tmp, &tot);
   int aoff = block_exclusive_scan256(nact, s_tmp + 4, &tota);
   int toff = block_exclusive_scan256(ntile, s_tmp + 8, &tott);
+  int base[EPT];
+  {
+    int o = off;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      base[j] = o;
+      o += cnt[j];
+    }
+  }
+  // per-(block, expert) row bases in place of the counts, chunk by chunk as above
+  for (int b0 = 0; b0 < NB; b0 += kChunk) {
+    int v[EPT][kChunk];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        const int e = tid * EPT + j, b = b0 + i;
+        v[j][i] = (e < E && b < NB) ? w.blk[(int64_t)b * E + e] : 0;
+      }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+#pragma unroll
+      for (int i = 0; i < kChunk; ++i) {
+        const int e = tid * EPT + j, b = b0 + i;
+        if (e < E && b < NB) w.blk[(int64_t)b * E + e] = base[j];
+        base[j] += v[j][i];
+      }
+  }
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
     const int e = tid * EPT + j;
     if (e < E) {
       w.counts[e] = cnt[j];
       w.offsets[e] = off;
-      int base = off;
-      for (int b = 0; b < NB; ++b) {
-        const int c = w.blk[(int64_t)b * E + e];
-        w.blk[(int64_t)b * E + e] = base;
-        base += c;
-      }
       if (cnt[j] > 0) {
         w.active[aoff] = make_int4(cnt[j], e, off, 0);
         ++aoff;
@@ -1580,12 +1703,8 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
                               int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(w_router && logits, AXK_E_NULL);
   int rc;
-  if (tokens > kDecodeTokens) {
-    rc = axk_bf16_gemm(h2, hidden, w_router, nullptr, logits, AXK_DT_F32, tokens, num_experts, hidden, stream);
-    if (rc != AXK_OK) return rc;
-    rc = axk_moe_route(logits, topk_ids, topk_weights, tokens, num_experts, top_k, norm_topk_prob, stream);
-  } else {
-    // decode: the router as K-slice partials in the workspace, summed in slice order by the routing kernel
+  {
+    // the router as K-slice partial logits in the workspace, summed in slice order by the routing kernel
     AXK_REQUIRE(h2 && topk_ids && topk_weights, AXK_E_NULL);
     rc = check_dims({tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0});
     if (rc != AXK_OK) return rc;
@@ -1594,20 +1713,30 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
         axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
     AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
     const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
-    const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, S = router_splits(hidden);
+    const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k;
+    const bool prefill = T > kDecodeTokens;
+    const int S = prefill ? (int)std::min<int64_t>(kPrefillRouterSplits, hidden / 64) : router_splits(hidden);
     hipStream_t st = axk_stream(stream);
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
-                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
-    const dim3 grid((unsigned)((T + 3) / 4)), block(256);
-    if (E <= 64)
-      hipLaunchKernelGGL(moe_route_part_kernel<1>, grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, logits,
-                         topk_ids, topk_weights);
-    else if (E <= 256)
-      hipLaunchKernelGGL(moe_route_part_kernel<4>, grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, logits,
-                         topk_ids, topk_weights);
+    if (prefill)
+      hipLaunchKernelGGL(moe_router_tile_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64), (unsigned)S),
+                         dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
     else
-      hipLaunchKernelGGL(moe_route_part_kernel<kMaxExperts / 64>, grid, block, 0, st, w.rpart, S, T, E, K,
-                         norm_topk_prob, logits, topk_ids, topk_weights);
+      hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
+                         dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
+    const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+#define AXK_ROUTE_PART(V, MS)                                                                                  \
+  hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob,  \
+                     logits, topk_ids, topk_weights)
+    if (prefill) {
+      if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
+      else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
+      else AXK_ROUTE_PART(kMaxExperts / 64, kPrefillRouterSplits);
+    } else {
+      if (E <= 64) AXK_ROUTE_PART(1, kMaxRouterSplits);
+      else if (E <= 256) AXK_ROUTE_PART(4, kMaxRouterSplits);
+      else AXK_ROUTE_PART(kMaxExperts / 64, kMaxRouterSplits);
+    }
+#undef AXK_ROUTE_PART
     rc = axk_launch_status();
   }
   if (rc != AXK_OK) return rc;
