@@ -197,18 +197,18 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   if (h % per_key == 0) {
     uint16_t* qn_g = p.ws.qn + kidx * kC * kD;
     uint16_t* kt_g = p.ws.kt + kidx * kD * kC;
-    for (int i = tid; i < kC * kD / 8; i += 256) {
-      const int row = i >> 4, c8 = i & 15;
-      *reinterpret_cast<uint4*>(qn_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sQ + row * kLdK + 8 * c8);
+    for (int i = tid; i < kC * kD / 8; i += 256) {  // fragment order: unit i of the destination
+      const int row = 16 * (i >> 8) + (i & 15), col = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+      *reinterpret_cast<uint4*>(qn_g + 8 * i) = *reinterpret_cast<const uint4*>(sQ + row * kLdK + col);
     }
-    for (int i = tid; i < kD * kC / 8; i += 256) {
-      const int d = i >> 3, t8 = i & 7;
+    for (int i = tid; i < kD * kC / 8; i += 256) {  // k^T [d][token] in fragment order
+      const int d = 16 * (i >> 7) + (i & 15), t8 = 4 * ((i >> 6) & 1) + ((i >> 4) & 3);
       uint4 o;
       uint32_t* op = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         op[e] = (uint32_t)sK[(8 * t8 + 2 * e) * kLdK + d] | ((uint32_t)sK[(8 * t8 + 2 * e + 1) * kLdK + d] << 16);
-      *reinterpret_cast<uint4*>(kt_g + d * kC + 8 * t8) = o;
+      *reinterpret_cast<uint4*>(kt_g + 8 * i) = o;
     }
   }
 
@@ -247,9 +247,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   __syncthreads();
   {
     uint16_t* p_g = p.ws.p + vidx * kC * kC;
-    for (int i = tid; i < kC * kC / 8; i += 256) {
-      const int row = i >> 3, c8 = i & 7;
-      *reinterpret_cast<uint4*>(p_g + row * kC + 8 * c8) = *reinterpret_cast<const uint4*>(sP + row * kLdT + 8 * c8);
+    for (int i = tid; i < kC * kC / 8; i += 256) {  // fragment order
+      const int row = 16 * (i >> 7) + (i & 15), col = 32 * ((i >> 6) & 1) + 8 * ((i >> 4) & 3);
+      *reinterpret_cast<uint4*>(p_g + 8 * i) = *reinterpret_cast<const uint4*>(sP + row * kLdT + col);
     }
   }
   __syncthreads();
@@ -381,9 +381,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
     for (int r = 0; r < 4; ++r) sW[(16 * wave + 4 * g4 + r) * kLdK + 16 * ct + l16] = (uint16_t)f32_to_bf16_bits(wa[ct][r]);
   __syncthreads();
   uint16_t* w_g = p.ws.w + vidx * kC * kD;
-  for (int i = tid; i < kC * kD / 8; i += 256) {
-    const int row = i >> 4, c8 = i & 15;
-    *reinterpret_cast<uint4*>(w_g + row * kD + 8 * c8) = *reinterpret_cast<const uint4*>(sW + row * kLdK + 8 * c8);
+  for (int i = tid; i < kC * kD / 8; i += 256) {  // fragment order
+    const int row = 16 * (i >> 8) + (i & 15), col = 32 * ((i >> 6) & 3) + 8 * ((i >> 4) & 3);
+    *reinterpret_cast<uint4*>(w_g + 8 * i) = *reinterpret_cast<const uint4*>(sW + row * kLdK + col);
   }
 }
 
@@ -434,20 +434,22 @@ AXK_DEV void scan_load(ScanOps<CPW>& s, const ScanArgs& p, int b, int bh, int kh
                        int g4, int lane) {
   const int64_t vidx = (int64_t)bh * p.NC + c;
   const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;
-  const uint16_t* wg = p.ws.w + vidx * kC * kD + (16 * tt + l16) * kD + 8 * g4;
-  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (16 * tt + l16) * kD + 8 * g4;
-  const uint16_t* pg = p.ws.p + vidx * kC * kC + (16 * tt + l16) * kC + 8 * g4;
-  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (32 * tt + l16) * kC + 8 * g4;
+  // operands stored in MFMA fragment order (16-row x 32-column fragments, 64 lanes x 16 bytes each): every load
+  // instruction reads 1 KiB contiguous
+  const uint16_t* wg = p.ws.w + vidx * kC * kD + (4 * tt * 64 + lane) * 8;    // fragments (tt, st), st < 4
+  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (4 * tt * 64 + lane) * 8;
+  const uint16_t* pg = p.ws.p + vidx * kC * kC + (2 * tt * 64 + lane) * 8;    // fragments (tt, st), st < 2
+  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (4 * tt * 64 + lane) * 8;  // fragments (2 tt + i, st), st < 2
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    s.wf[st] = load_bf16x8(wg + 32 * st);
-    s.qf[st] = load_bf16x8(qg + 32 * st);
+    s.wf[st] = load_bf16x8(wg + st * 512);
+    s.qf[st] = load_bf16x8(qg + st * 512);
   }
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
-    s.pf[st] = load_bf16x8(pg + 32 * st);
-    s.kf[0][st] = load_bf16x8(ktg + 32 * st);
-    s.kf[1][st] = load_bf16x8(ktg + 16 * kC + 32 * st);
+    s.pf[st] = load_bf16x8(pg + st * 512);
+    s.kf[0][st] = load_bf16x8(ktg + st * 512);
+    s.kf[1][st] = load_bf16x8(ktg + (2 + st) * 512);
   }
 #pragma unroll
   for (int j = 0; j < CPW; ++j)
