@@ -92,6 +92,14 @@ AXK_DEV void fp8x4_to_bf16(uint32_t w, __bf16* dst) {
 }
 
 typedef unsigned int axk_u32x4 __attribute__((ext_vector_type(4)));
+typedef short axk_s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: each lane gives the LDS address of 4 consecutive 16-bit values; in every group of 16 lanes,
+// lane i receives element i % 4 of the values of lanes i / 4, i / 4 + 4, i / 4 + 8 and i / 4 + 12 (one 64-bit
+// read per lane that transposes a 16 x 4 block of the group).
+AXK_DEV axk_s16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) axk_s16x4*)(p));
+}
 
 AXK_DEV axk_f32x4 mfma_bf16_16x16x32(axk_bf16x8 a, axk_bf16x8 b, axk_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -118,6 +126,28 @@ AXK_DEV float wave_sum(float v) {
   v += dpp_move<0x143, 0xC>(0.f, v);
   return lane63(v);
 }
+// Cross-row exchanges on VALU (gfx950 v_permlane16_swap / v_permlane32_swap, which swap the odd rows of 16 lanes
+// (upper 32 lanes) of the first operand with the even rows (lower 32 lanes) of the second): given v twice, the
+// pair holds the even-row (lower-half) value and the odd-row (upper-half) value of each row pair (half pair) in
+// every lane, hence v op v(l ^ 16) and v op v(l ^ 32) without the LDS pipe. The second copy of v is laundered
+// through an empty asm: with two operands it can prove equal, the compiler folds the swap away.
+AXK_DEV uint2 row_pair16(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("" : "+v"(b));
+  const auto p = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  return make_uint2(p[0], p[1]);
+}
+AXK_DEV uint2 half_pair32(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("" : "+v"(b));
+  const auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  return make_uint2(p[0], p[1]);
+}
+AXK_DEV float xor16_sum(float v) { const uint2 p = row_pair16(v); return __uint_as_float(p.x) + __uint_as_float(p.y); }
+AXK_DEV float xor32_sum(float v) { const uint2 p = half_pair32(v); return __uint_as_float(p.x) + __uint_as_float(p.y); }
+AXK_DEV float xor16_max(float v) { const uint2 p = row_pair16(v); return fmaxf(__uint_as_float(p.x), __uint_as_float(p.y)); }
+AXK_DEV float xor32_max(float v) { const uint2 p = half_pair32(v); return fmaxf(__uint_as_float(p.x), __uint_as_float(p.y)); }
+
 // Sum inside aligned groups of W lanes (W = 2, 4, 8 or 16), the same value in every lane of the group.
 template <int W>
 AXK_DEV float group_sum(float v) {

@@ -96,8 +96,8 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
       pr.x += kr * S[r].x; pr.y += kr * S[r].y; pr.z += kr * S[r].z; pr.w += kr * S[r].w;
     }
     // the two row groups of a wave: lanes l and l ^ 32
-    pr.x += __shfl_xor(pr.x, 32, 64); pr.y += __shfl_xor(pr.y, 32, 64);
-    pr.z += __shfl_xor(pr.z, 32, 64); pr.w += __shfl_xor(pr.w, 32, 64);
+    pr.x = xor32_sum(pr.x); pr.y = xor32_sum(pr.y);
+    pr.z = xor32_sum(pr.z); pr.w = xor32_sum(pr.w);
     if (lane < 32) *reinterpret_cast<float4*>(&s_red[wave][c0]) = pr;
     __syncthreads();
     if (tid < kDV) {
@@ -117,8 +117,8 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
       S[r].x += kr * er.x; S[r].y += kr * er.y; S[r].z += kr * er.z; S[r].w += kr * er.w;
       ov.x += qr * S[r].x; ov.y += qr * S[r].y; ov.z += qr * S[r].z; ov.w += qr * S[r].w;
     }
-    ov.x += __shfl_xor(ov.x, 32, 64); ov.y += __shfl_xor(ov.y, 32, 64);
-    ov.z += __shfl_xor(ov.z, 32, 64); ov.w += __shfl_xor(ov.w, 32, 64);
+    ov.x = xor32_sum(ov.x); ov.y = xor32_sum(ov.y);
+    ov.z = xor32_sum(ov.z); ov.w = xor32_sum(ov.w);
     __syncthreads();  // s_red / s_vec reuse
     if (lane < 32) *reinterpret_cast<float4*>(&s_red[wave][c0]) = ov;
     __syncthreads();

@@ -385,8 +385,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       st[rr] = sv;
       mx = fmaxf(mx, sv);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one valid token
     // the running max rarely moves after the first tiles: rescale O only when it did (wave-uniform test)
     const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
@@ -399,17 +398,15 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       psum += p;
       pb[rr] = (short)f32_to_bf16_bits(p);
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = xor32_sum(xor16_sum(psum));
     l_run = l_run * alpha + psum;
     m_run = m_new;
 #pragma unroll
     for (int t = 0; t < C::DT; ++t) {
-      // A operand V^T: lane (d = wave*DW + 16t + l16, group g) = V[tokens 4g .. 4g + 3][d]
-      const unsigned char* col = vt + (wave * C::DW + 16 * t + l16) * 2;
-      axk_i16x4 va;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) va[rr] = *reinterpret_cast<const short*>(col + C::row_off(4 * g + rr));
+      // A operand V^T: lane (d = wave*DW + 16t + l16, group g) = V[tokens 4g .. 4g + 3][d], by one transposing
+      // LDS read: in each 16-lane group, source lane 4j + a points at V[4g + j][16t' + 4a .. +3] and lane i
+      // receives element i % 4 of source lanes i / 4 + 4j, i.e. V[4g + j][16t' + i]
+      const axk_i16x4 va = lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (wave * C::DW + 16 * t + 4 * (l16 & 3)) * 2);
       if (moved) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
