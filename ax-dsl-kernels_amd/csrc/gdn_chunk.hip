@@ -333,21 +333,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
     sTb[r * kLdT + cc] = (uint16_t)f32_to_bf16_bits(sT[r * kLdL + cc]);
   }
   __syncthreads();
+  // beta v and beta Gamma k row-major [token][LdK] (16-byte writes); step 7 reads them transposed
   uint16_t* sVB = sQ;
   uint16_t* sKB = reinterpret_cast<uint16_t*>(sT);
   {
     const float beta = sBeta[tt], gm = expf(sG[tt]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+      const int d0 = 32 * qd + 8 * i;
+      const uint4 kq = *reinterpret_cast<const uint4*>(sK + tt * kLdK + d0);
+      const uint32_t vw[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w}, kw[4] = {kq.x, kq.y, kq.z, kq.w};
+      uint32_t vo[4], ko[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int d = 32 * qd + 8 * i + 2 * j;
-        sVB[d * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_lo(vw[j]) * beta);
-        sVB[(d + 1) * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_hi(vw[j]) * beta);
-        sKB[d * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(sK[tt * kLdK + d]) * beta * gm);
-        sKB[(d + 1) * kLdT + tt] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(sK[tt * kLdK + d + 1]) * beta * gm);
+        vo[j] = pack_bf16x2(bf16_lo(vw[j]) * beta, bf16_hi(vw[j]) * beta);
+        ko[j] = pack_bf16x2(bf16_lo(kw[j]) * beta * gm, bf16_hi(kw[j]) * beta * gm);
       }
+      *reinterpret_cast<uint4*>(sVB + tt * kLdK + d0) = make_uint4(vo[0], vo[1], vo[2], vo[3]);
+      *reinterpret_cast<uint4*>(sKB + tt * kLdK + d0) = make_uint4(ko[0], ko[1], ko[2], ko[3]);
     }
   }
   __syncthreads();
@@ -356,14 +359,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   axk_f32x4 ua[8], wa[8];
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct) ua[ct] = wa[ct] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  // B fragments (tokens 8 g .. 8 g + 7 of column 16 ct + l16) by two transposing reads: source lane 4 j + a of
+  // group g points at token 8 g + j (+ 4), columns 16 ct + 4 a .. + 3
+  auto bfrag = [&](const uint16_t* m, int tok, int col) __attribute__((always_inline)) -> axk_bf16x8 {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(m + tok * kLdK + col));
+    const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(m + (tok + 4) * kLdK + col));
+    return __builtin_bit_cast(axk_bf16x8, axk_u32x4{lo.x, lo.y, hi.x, hi.y});  // whole-register moves only
+  };
 #pragma unroll
   for (int st = 0; st < kC / 32; ++st) {
     const int ko = 32 * st + 8 * g4;
     const axk_bf16x8 at = load_bf16x8(sTb + (16 * wave + l16) * kLdT + ko);
+    const int tok = ko + (l16 >> 2);
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) {
-      ua[ct] = mfma_bf16_16x16x32(at, load_bf16x8(sVB + (16 * ct + l16) * kLdT + ko), ua[ct]);
-      wa[ct] = mfma_bf16_16x16x32(at, load_bf16x8(sKB + (16 * ct + l16) * kLdT + ko), wa[ct]);
+      const int col = 16 * ct + 4 * (l16 & 3);
+      ua[ct] = mfma_bf16_16x16x32(at, bfrag(sVB, tok, col), ua[ct]);
+      wa[ct] = mfma_bf16_16x16x32(at, bfrag(sKB, tok, col), wa[ct]);
     }
   }
   __syncthreads();
