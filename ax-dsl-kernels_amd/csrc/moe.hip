@@ -456,14 +456,19 @@ constexpr int kStageRows = AXK_ROWS;  // activation rows staged per pass (MFMA r
 #endif
 constexpr int kGateUpTilesPerWave = AXK_GU_TPW;  // 16-row tiles each wave streams (gate-up / down)
 constexpr int kDownTilesPerWave = AXK_DN_TPW;
+constexpr int kStageLd = 144;                       // bytes per staged 128-byte weight row segment (+16 pad)
+constexpr int kWaveStageBytes = 32 * kStageLd;      // a wave's LDS tile: gate and up, 16 rows each
+constexpr int kSmallRows = 8;                       // activation rows per pass of the staged kernels
+// byte offset of the wave tiles after the activation rows ([rows][K + 8] bf16), 16-byte aligned
+__host__ __device__ inline size_t stream_stage_off(int rows, int K) { return ((size_t)rows * (K + 8) * 2 + 15) & ~(size_t)15; }
 
 // Stage activation rows [m0, m0 + kStageRows) of the slot into LDS as [kStageRows][K + 8] bf16 (rows past cnt
 // are skipped).
-template <bool GATHER>
+template <bool GATHER, int ROWS>
 __device__ void stage_rows(uint16_t* sA, const uint16_t* __restrict__ src, const int* __restrict__ row_tok,
                            int row0, int m0, int cnt, int K) {
   const int ld = K + 8, units = K / 8;
-  const int rows = min(kStageRows, cnt - m0);
+  const int rows = min(ROWS, cnt - m0);
   for (int i = threadIdx.x; i < rows * units; i += blockDim.x) {
     const int r = i / units, u = i - r * units;
     const int64_t srow = GATHER ? row_tok[row0 + m0 + r] : (int64_t)(row0 + m0 + r);
@@ -498,10 +503,15 @@ struct GateUpArgs {
 // WIDE (K a multiple of the batch's 128 kBatchChunks values): a batch's E8M0 scales are 4 kBatchChunks
 // consecutive bytes of the row (chunks x lane groups), fetched with one load per matrix; otherwise one byte load
 // per unit.
-template <bool WIDE>
+// STAGE (with WIDE): each batch's weights are loaded as whole 128-byte row segments (8 rows per load instruction,
+// which keeps the address path's per-line work low), written to a wave-private LDS tile and read back in the
+// MFMA layout; ROWS activation rows per pass.
+template <bool WIDE, int ROWS, bool STAGE>
 __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArgs a) {
+  static_assert(!STAGE || WIDE, "staged weights need whole batches");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  unsigned char* sW = smem + stream_stage_off(ROWS, a.H) + (threadIdx.x >> 6) * kWaveStageBytes;
   // grid slots [0, nsp): the shared expert, kStageRows tokens each (first, so the shared rows start early);
   // slot s >= nsp: active expert s - nsp
   const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
@@ -510,8 +520,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
   int cnt, row0, Fo, mbeg = 0;
   const uint8_t *gw, *gs, *uw, *us;
   if (shared) {
-    mbeg = gslot * kStageRows;
-    cnt = min(a.T, mbeg + kStageRows);
+    mbeg = gslot * ROWS;
+    cnt = min(a.T, mbeg + ROWS);
     row0 = 0;
     Fo = a.Fs;
     gw = a.sg_w; gs = a.sg_s; uw = a.su_w; us = a.su_s;
@@ -539,23 +549,34 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
   const int nmine = max(0, min(a.tpw, (ntiles - tb - wave + kStreamWaves - 1) / kStreamWaves));
   const int steps = nmine * nb;
 
-  struct Batch {
-    uint4 qg[kBatchChunks], qu[kBatchChunks];
+  struct Batch {  // native vectors: arrays of them stay in registers
+    axk_u32x4 qg[kBatchChunks], qu[kBatchChunks];  // STAGE: [h] = rows 8 h + lane / 8, bytes 16 (lane % 8)
     uint32_t sg[kBatchChunks], su[kBatchChunks];
   };
+  static_assert(!STAGE || kBatchChunks == 2, "staged batches are 128-byte row segments");
   // Loads are unconditional, from addresses clamped into the weights (a row past Fo is never stored, a unit past
   // K is zeroed where it is used): a branch around a load would make every later wait drain the queue.
   auto load_batch = [&](Batch& bt, int step) {
     const int i = step / nb, bi = step - i * nb;
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)Fo - 1);
+    if (STAGE) {
 #pragma unroll
-    for (int j = 0; j < kBatchChunks; ++j) {
-      const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
-      bt.qg[j] = *reinterpret_cast<const uint4*>(gw + n * (H / 2) + kb / 2);
-      bt.qu[j] = *reinterpret_cast<const uint4*>(uw + n * (H / 2) + kb / 2);
-      if (!WIDE) {
-        bt.sg[j] = gs[n * (H / 32) + kb / 32];
-        bt.su[j] = us[n * (H / 32) + kb / 32];
+      for (int h = 0; h < 2; ++h) {
+        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + 8 * h + (lane >> 3), (int64_t)Fo - 1);
+        const int64_t off = (int64_t)bi * 128 + 16 * (lane & 7);
+        bt.qg[h] = *reinterpret_cast<const axk_u32x4*>(gw + r * (H / 2) + off);
+        bt.qu[h] = *reinterpret_cast<const axk_u32x4*>(uw + r * (H / 2) + off);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kBatchChunks; ++j) {
+        const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
+        bt.qg[j] = *reinterpret_cast<const axk_u32x4*>(gw + n * (H / 2) + kb / 2);
+        bt.qu[j] = *reinterpret_cast<const axk_u32x4*>(uw + n * (H / 2) + kb / 2);
+        if (!WIDE) {
+          bt.sg[j] = gs[n * (H / 32) + kb / 32];
+          bt.su[j] = us[n * (H / 32) + kb / 32];
+        }
       }
     }
     if (WIDE) {
@@ -564,10 +585,30 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     }
   };
 
-  for (int m0 = mbeg; m0 < cnt; m0 += kStageRows) {
+  for (int m0 = mbeg; m0 < cnt; m0 += ROWS) {
     axk_f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
       const int i = st / nb, bi = st - i * nb;
+      axk_u32x4 wg[kBatchChunks], wu[kBatchChunks];  // this lane's MFMA units of the batch
+      if (STAGE) {  // through the wave's LDS tile [gate, up][16 rows][kStageLd] (in-order LDS: no barrier)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int r = 8 * h + (lane >> 3);
+          *reinterpret_cast<axk_u32x4*>(sW + r * kStageLd + 16 * (lane & 7)) = cur.qg[h];
+          *reinterpret_cast<axk_u32x4*>(sW + (16 + r) * kStageLd + 16 * (lane & 7)) = cur.qu[h];
+        }
+#pragma unroll
+        for (int j = 0; j < kBatchChunks; ++j) {
+          wg[j] = *reinterpret_cast<const axk_u32x4*>(sW + nl * kStageLd + 64 * j + 16 * g);
+          wu[j] = *reinterpret_cast<const axk_u32x4*>(sW + (16 + nl) * kStageLd + 64 * j + 16 * g);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kBatchChunks; ++j) {
+          wg[j] = cur.qg[j];
+          wu[j] = cur.qu[j];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int c = bi * kBatchChunks + j;
@@ -580,9 +621,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
         const float scg = kv ? e8m0_to_f32(bg) : 0.f, scu = kv ? e8m0_to_f32(bu) : 0.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          const axk_bf16x8 af = (kv && nl < kStageRows) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8();
-          accg = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(cur.qg[j], s, scg), accg);
-          accu = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(cur.qu[j], s, scu), accu);
+          const axk_bf16x8 af = (kv && nl < ROWS) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8();
+          accg = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wg[j]), s, scg), accg);
+          accu = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wu[j]), s, scu), accu);
         }
       }
       if (bi == nb - 1) {  // tile done: SwiGLU of rows m0 + 4 g + r, column tile * 16 + nl
@@ -590,7 +631,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + 4 * g + r;
-          if (4 * g + r < kStageRows && m < cnt && col < Fo) {
+          if (4 * g + r < ROWS && m < cnt && col < Fo) {
             const float gv = round_bf16(accg[r]), uv = round_bf16(accu[r]);
             const uint16_t act = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
             if (shared)
@@ -610,9 +651,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     load_batch(b0, 0);
     load_batch(b1, min(1, last));
     if (shared)
-      stage_rows<false>(sA, a.h2, nullptr, 0, m0, cnt, H);
+      stage_rows<false, ROWS>(sA, a.h2, nullptr, 0, m0, cnt, H);
     else
-      stage_rows<true>(sA, a.h2, a.w.row_tok, row0, m0, cnt, H);
+      stage_rows<true, ROWS>(sA, a.h2, a.w.row_tok, row0, m0, cnt, H);
     __syncthreads();
     for (int st = 0; st < steps; st += 3) {
       load_batch(b2, min(st + 2, last));
@@ -633,10 +674,12 @@ struct DownArgs {
 };
 
 // down: workgroup (slot, run of kStreamWaves * tpw 16-row tiles of H); routed rows scaled by their routing weight.
-template <bool WIDE>
+template <bool WIDE, int ROWS, bool STAGE>
 __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a) {
+  static_assert(!STAGE || WIDE, "staged weights need whole batches");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  unsigned char* sW = smem + stream_stage_off(ROWS, a.Fs > a.F ? a.Fs : a.F) + (threadIdx.x >> 6) * kWaveStageBytes;
   const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
   const bool shared = gslot < a.nsp;
   const int slot = gslot - a.nsp;
@@ -644,8 +687,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
   const uint8_t *dw, *ds;
   const uint16_t* act;
   if (shared) {
-    mbeg = gslot * kStageRows;
-    cnt = min(a.T, mbeg + kStageRows);
+    mbeg = gslot * ROWS;
+    cnt = min(a.T, mbeg + ROWS);
     row0 = 0;
     K = a.Fs;
     dw = a.sd_w; ds = a.sd_s;
@@ -671,23 +714,31 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
   const int nmine = max(0, min(a.tpw, (ntiles - tb - wave + kStreamWaves - 1) / kStreamWaves));
   const int steps = nmine * nb;
 
-  struct Batch {
-    uint4 q[kBatchChunks];
+  struct Batch {  // native vectors: arrays of them stay in registers
+    axk_u32x4 q[kBatchChunks];  // STAGE: [h] = rows 8 h + lane / 8, bytes 16 (lane % 8) of the batch
     uint32_t s[kBatchChunks];
   };
   auto load_batch = [&](Batch& bt, int step) {  // unconditional, clamped (as in the gate-up kernel)
     const int i = step / nb, bi = step - i * nb;
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)a.H - 1);
+    if (STAGE) {
 #pragma unroll
-    for (int j = 0; j < kBatchChunks; ++j) {
-      const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
-      bt.q[j] = *reinterpret_cast<const uint4*>(dw + n * (K / 2) + kb / 2);
-      if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
+      for (int h = 0; h < 2; ++h) {
+        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + 8 * h + (lane >> 3), (int64_t)a.H - 1);
+        bt.q[h] = *reinterpret_cast<const axk_u32x4*>(dw + r * (K / 2) + (int64_t)bi * 128 + 16 * (lane & 7));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kBatchChunks; ++j) {
+        const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
+        bt.q[j] = *reinterpret_cast<const axk_u32x4*>(dw + n * (K / 2) + kb / 2);
+        if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
+      }
     }
     if (WIDE) load_scale_words(bt.s, ds + n * (K / 32) + 4 * kBatchChunks * bi);
   };
 
-  for (int m0 = mbeg; m0 < cnt; m0 += kStageRows) {
+  for (int m0 = mbeg; m0 < cnt; m0 += ROWS) {
     float rw[4];
     int pr[4];  // the rows' pair indices (y is indexed by pair)
 #pragma unroll
@@ -699,6 +750,18 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
       const int i = st / nb, bi = st - i * nb;
+      axk_u32x4 wq[kBatchChunks];
+      if (STAGE) {  // through the wave's LDS tile [16 rows][kStageLd] (in-order LDS: no barrier)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<axk_u32x4*>(sW + (8 * h + (lane >> 3)) * kStageLd + 16 * (lane & 7)) = cur.q[h];
+#pragma unroll
+        for (int j = 0; j < kBatchChunks; ++j)
+          wq[j] = *reinterpret_cast<const axk_u32x4*>(sW + nl * kStageLd + 64 * j + 16 * g);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kBatchChunks; ++j) wq[j] = cur.q[j];
+      }
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int c = bi * kBatchChunks + j;
@@ -710,15 +773,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
         const float sc = kv ? e8m0_to_f32(sb) : 0.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          acc = mfma_bf16_16x16x32((kv && nl < kStageRows) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8(),
-                                   axk::WUnit<WF_MXFP4>::conv(cur.q[j], s, sc), acc);
+          acc = mfma_bf16_16x16x32((kv && nl < ROWS) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8(),
+                                   axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wq[j]), s, sc), acc);
       }
       if (bi == nb - 1) {
         const int64_t col = (int64_t)(tb + wave + kStreamWaves * i) * 16 + nl;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + 4 * g + r;
-          if (4 * g + r < kStageRows && m < cnt && col < a.H) {
+          if (4 * g + r < ROWS && m < cnt && col < a.H) {
             if (shared)
               a.w.y_sh[(int64_t)m * a.H + col] = acc[r];
             else
@@ -733,7 +796,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     __syncthreads();
     load_batch(b0, 0);
     load_batch(b1, min(1, last));
-    stage_rows<false>(sA, act, nullptr, row0, m0, cnt, K);
+    stage_rows<false, ROWS>(sA, act, nullptr, row0, m0, cnt, K);
     __syncthreads();
     for (int st = 0; st < steps; st += 3) {
       load_batch(b2, min(st + 2, last));
@@ -1654,39 +1717,50 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
   const int max_slots = E < T * K ? E : T * K;
   const int fmax = F > Fs ? F : Fs;
-  // runs of 4 x tpw tiles per workgroup; activation rows staged in dynamic LDS (16 rows of K + 8)
+  // runs of 4 x tpw tiles per workgroup; activation rows staged in dynamic LDS ([rows][K + 8] bf16). Small batches
+  // (tokens <= 64, K a multiple of 256) take the staged-weight kernels with 8 activation rows per pass (their
+  // LDS tiles fit beside 8 rows, not 16); the others stream MFMA-layout units with 16 rows per pass.
   const int gu_tpw = kGateUpTilesPerWave, dn_tpw = kDownTilesPerWave;
   const int run_gu = kStreamWaves * gu_tpw, run_dn = kStreamWaves * dn_tpw;
   const int gu_grp = ((fmax + 15) / 16 + run_gu - 1) / run_gu;
   const int dn_grp = ((H + 15) / 16 + run_dn - 1) / run_dn;
-  const size_t gu_lds = (size_t)kStageRows * (H + 8) * 2, dn_lds = (size_t)kStageRows * (fmax + 8) * 2;
+  const int wide_k = 128 * kBatchChunks;
+  const bool gu_wide = H % wide_k == 0, dn_wide = F % wide_k == 0 && Fs % wide_k == 0;
+  const bool gu_stage = gu_wide && T <= 64, dn_stage = dn_wide && T <= 64;
+  const int gu_rows = gu_stage ? kSmallRows : kStageRows, dn_rows = dn_stage ? kSmallRows : kStageRows;
+  const size_t gu_lds = stream_stage_off(gu_rows, H) + (gu_stage ? kStreamWaves * kWaveStageBytes : 0);
+  const size_t dn_lds = stream_stage_off(dn_rows, fmax) + (dn_stage ? kStreamWaves * kWaveStageBytes : 0);
   AXK_REQUIRE(gu_lds <= kMaxStageLds && dn_lds <= kMaxStageLds, AXK_E_SHAPE);
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
-    const void* fns[4] = {reinterpret_cast<const void*>(&moe_gateup_kernel<false>),
-                          reinterpret_cast<const void*>(&moe_gateup_kernel<true>),
-                          reinterpret_cast<const void*>(&moe_down_kernel<false>),
-                          reinterpret_cast<const void*>(&moe_down_kernel<true>)};
+    const void* fns[6] = {reinterpret_cast<const void*>(&moe_gateup_kernel<false, kStageRows, false>),
+                          reinterpret_cast<const void*>(&moe_gateup_kernel<true, kStageRows, false>),
+                          reinterpret_cast<const void*>(&moe_gateup_kernel<true, kSmallRows, true>),
+                          reinterpret_cast<const void*>(&moe_down_kernel<false, kStageRows, false>),
+                          reinterpret_cast<const void*>(&moe_down_kernel<true, kStageRows, false>),
+                          reinterpret_cast<const void*>(&moe_down_kernel<true, kSmallRows, true>)};
     for (const void* f : fns)
       if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
         return AXK_E_LAUNCH;
     lds_raised = true;
   }
-  const int wide_k = 128 * kBatchChunks;
-  const bool gu_wide = H % wide_k == 0, dn_wide = F % wide_k == 0 && Fs % wide_k == 0;
-  const int nsp = has_shared ? (T + kStageRows - 1) / kStageRows : 0;
+  const int gu_nsp = has_shared ? (T + gu_rows - 1) / gu_rows : 0, dn_nsp = has_shared ? (T + dn_rows - 1) / dn_rows : 0;
   GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, max_slots, gu_grp, gu_tpw,
-                nsp, w};
-  const dim3 gu_grid((unsigned)((max_slots + nsp) * gu_grp)), dn_grid((unsigned)((max_slots + nsp) * dn_grp));
-  if (gu_wide)
-    hipLaunchKernelGGL(moe_gateup_kernel<true>, gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
+                gu_nsp, w};
+  const dim3 gu_grid((unsigned)((max_slots + gu_nsp) * gu_grp)), dn_grid((unsigned)((max_slots + dn_nsp) * dn_grp));
+  if (gu_stage)
+    hipLaunchKernelGGL((moe_gateup_kernel<true, kSmallRows, true>), gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
+  else if (gu_wide)
+    hipLaunchKernelGGL((moe_gateup_kernel<true, kStageRows, false>), gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
   else
-    hipLaunchKernelGGL(moe_gateup_kernel<false>, gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
-  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, dn_grp, dn_tpw, nsp, w};
-  if (dn_wide)
-    hipLaunchKernelGGL(moe_down_kernel<true>, dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
+    hipLaunchKernelGGL((moe_gateup_kernel<false, kStageRows, false>), gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
+  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, dn_grp, dn_tpw, dn_nsp, w};
+  if (dn_stage)
+    hipLaunchKernelGGL((moe_down_kernel<true, kSmallRows, true>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
+  else if (dn_wide)
+    hipLaunchKernelGGL((moe_down_kernel<true, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   else
-    hipLaunchKernelGGL(moe_down_kernel<false>, dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
+    hipLaunchKernelGGL((moe_down_kernel<false, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
                        0, st, ca);
@@ -1731,6 +1805,10 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
       if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
       else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
       else AXK_ROUTE_PART(kMaxExperts / 64, kPrefillRouterSplits);
+    } else if (S <= 8) {  // the partial loads are unrolled to the bound: keep it tight
+      if (E <= 64) AXK_ROUTE_PART(1, 8);
+      else if (E <= 256) AXK_ROUTE_PART(4, 8);
+      else AXK_ROUTE_PART(kMaxExperts / 64, 8);
     } else {
       if (E <= 64) AXK_ROUTE_PART(1, kMaxRouterSplits);
       else if (E <= 256) AXK_ROUTE_PART(4, kMaxRouterSplits);

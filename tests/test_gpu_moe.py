@@ -43,11 +43,14 @@ def _check_layer(c, dev, norm=True):
 
 
 # e spans the router's 64 / 256 / 1024-expert register layouts; t = 130 and 256 span several 64-token words
-# of the grouping bitmask (256 is the largest token count of one call)
+# of the grouping bitmask (256 is the largest token count of one call); the last three take the staged-weight
+# streaming kernels (t <= 64) or just miss them (t = 65)
 @pytest.mark.parametrize("t,h,e,f,fs,k", [(1, 64, 8, 32, 32, 2), (5, 256, 16, 64, 96, 4), (33, 128, 64, 32, 64, 8),
                                           (7, 192, 40, 160, 0, 6), (3, 128, 200, 32, 32, 8),
                                           (2, 64, 1000, 32, 0, 32), (130, 64, 16, 32, 32, 4),
-                                          (256, 64, 8, 32, 0, 2)])
+                                          (256, 64, 8, 32, 0, 2),
+                                          # K multiples of 256 with <= 64 tokens: the staged-weight streaming kernels
+                                          (20, 512, 32, 256, 256, 4), (64, 256, 64, 256, 0, 8), (65, 256, 16, 256, 256, 2)])
 def test_moe_small_shapes(dev, t, h, e, f, fs, k):
     g = torch.Generator().manual_seed(t + h + e)
     w = configs.moe_weights(g, hidden=h, experts=e, inter=f, shared_inter=max(fs, 32), router_std=0.5)
