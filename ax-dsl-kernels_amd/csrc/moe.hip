@@ -456,8 +456,10 @@ constexpr int kStageRows = AXK_ROWS;  // activation rows staged per pass (MFMA r
 #endif
 constexpr int kGateUpTilesPerWave = AXK_GU_TPW;  // 16-row tiles each wave streams (gate-up / down)
 constexpr int kDownTilesPerWave = AXK_DN_TPW;
-constexpr int kStageLd = 144;                       // bytes per staged 128-byte weight row segment (+16 pad)
+constexpr int kStageLd = 64 * kBatchChunks + 16;    // bytes per staged weight row segment of a batch (+16 pad)
 constexpr int kWaveStageBytes = 32 * kStageLd;      // a wave's LDS tile: gate and up, 16 rows each
+constexpr int kStageLpr = 4 * kBatchChunks;         // staged loads: lanes per row segment,
+constexpr int kStageRpi = 64 / kStageLpr;           // rows per load instruction (kBatchChunks instructions a tile)
 constexpr int kSmallRows = 8;                       // activation rows per pass of the staged kernels
 // byte offset of the wave tiles after the activation rows ([rows][K + 8] bf16), 16-byte aligned
 __host__ __device__ inline size_t stream_stage_off(int rows, int K) { return ((size_t)rows * (K + 8) * 2 + 15) & ~(size_t)15; }
@@ -503,9 +505,9 @@ struct GateUpArgs {
 // WIDE (K a multiple of the batch's 128 kBatchChunks values): a batch's E8M0 scales are 4 kBatchChunks
 // consecutive bytes of the row (chunks x lane groups), fetched with one load per matrix; otherwise one byte load
 // per unit.
-// STAGE (with WIDE): each batch's weights are loaded as whole 128-byte row segments (8 rows per load instruction,
-// which keeps the address path's per-line work low), written to a wave-private LDS tile and read back in the
-// MFMA layout; ROWS activation rows per pass.
+// STAGE (with WIDE): each batch's weights are loaded as whole row segments of 64 kBatchChunks bytes (16 / kBatchChunks
+// rows per load instruction, which keeps the address path's per-line work low), written to a wave-private LDS tile
+// and read back in the MFMA layout; ROWS activation rows per pass.
 template <bool WIDE, int ROWS, bool STAGE>
 __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArgs a) {
   static_assert(!STAGE || WIDE, "staged weights need whole batches");
@@ -550,10 +552,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
   const int steps = nmine * nb;
 
   struct Batch {  // native vectors: arrays of them stay in registers
-    axk_u32x4 qg[kBatchChunks], qu[kBatchChunks];  // STAGE: [h] = rows 8 h + lane / 8, bytes 16 (lane % 8)
+    axk_u32x4 qg[kBatchChunks], qu[kBatchChunks];  // STAGE: [h] = rows kStageRpi h + lane / kStageLpr
     uint32_t sg[kBatchChunks], su[kBatchChunks];
   };
-  static_assert(!STAGE || kBatchChunks == 2, "staged batches are 128-byte row segments");
   // Loads are unconditional, from addresses clamped into the weights (a row past Fo is never stored, a unit past
   // K is zeroed where it is used): a branch around a load would make every later wait drain the queue.
   auto load_batch = [&](Batch& bt, int step) {
@@ -561,9 +562,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)Fo - 1);
     if (STAGE) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + 8 * h + (lane >> 3), (int64_t)Fo - 1);
-        const int64_t off = (int64_t)bi * 128 + 16 * (lane & 7);
+      for (int h = 0; h < kBatchChunks; ++h) {
+        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
+                              (int64_t)Fo - 1);
+        const int64_t off = (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr);
         bt.qg[h] = *reinterpret_cast<const axk_u32x4*>(gw + r * (H / 2) + off);
         bt.qu[h] = *reinterpret_cast<const axk_u32x4*>(uw + r * (H / 2) + off);
       }
@@ -592,10 +594,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
       axk_u32x4 wg[kBatchChunks], wu[kBatchChunks];  // this lane's MFMA units of the batch
       if (STAGE) {  // through the wave's LDS tile [gate, up][16 rows][kStageLd] (in-order LDS: no barrier)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int r = 8 * h + (lane >> 3);
-          *reinterpret_cast<axk_u32x4*>(sW + r * kStageLd + 16 * (lane & 7)) = cur.qg[h];
-          *reinterpret_cast<axk_u32x4*>(sW + (16 + r) * kStageLd + 16 * (lane & 7)) = cur.qu[h];
+        for (int h = 0; h < kBatchChunks; ++h) {
+          const int r = kStageRpi * h + lane / kStageLpr;
+          *reinterpret_cast<axk_u32x4*>(sW + r * kStageLd + 16 * (lane % kStageLpr)) = cur.qg[h];
+          *reinterpret_cast<axk_u32x4*>(sW + (16 + r) * kStageLd + 16 * (lane % kStageLpr)) = cur.qu[h];
         }
 #pragma unroll
         for (int j = 0; j < kBatchChunks; ++j) {
@@ -715,7 +717,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
   const int steps = nmine * nb;
 
   struct Batch {  // native vectors: arrays of them stay in registers
-    axk_u32x4 q[kBatchChunks];  // STAGE: [h] = rows 8 h + lane / 8, bytes 16 (lane % 8) of the batch
+    axk_u32x4 q[kBatchChunks];  // STAGE: [h] = rows kStageRpi h + lane / kStageLpr of the batch
     uint32_t s[kBatchChunks];
   };
   auto load_batch = [&](Batch& bt, int step) {  // unconditional, clamped (as in the gate-up kernel)
@@ -723,9 +725,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)a.H - 1);
     if (STAGE) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + 8 * h + (lane >> 3), (int64_t)a.H - 1);
-        bt.q[h] = *reinterpret_cast<const axk_u32x4*>(dw + r * (K / 2) + (int64_t)bi * 128 + 16 * (lane & 7));
+      for (int h = 0; h < kBatchChunks; ++h) {
+        const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
+                              (int64_t)a.H - 1);
+        bt.q[h] = *reinterpret_cast<const axk_u32x4*>(dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) +
+                                                       16 * (lane % kStageLpr));
       }
     } else {
 #pragma unroll
@@ -753,8 +757,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
       axk_u32x4 wq[kBatchChunks];
       if (STAGE) {  // through the wave's LDS tile [16 rows][kStageLd] (in-order LDS: no barrier)
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          *reinterpret_cast<axk_u32x4*>(sW + (8 * h + (lane >> 3)) * kStageLd + 16 * (lane & 7)) = cur.q[h];
+        for (int h = 0; h < kBatchChunks; ++h)
+          *reinterpret_cast<axk_u32x4*>(sW + (kStageRpi * h + lane / kStageLpr) * kStageLd + 16 * (lane % kStageLpr)) =
+              cur.q[h];
 #pragma unroll
         for (int j = 0; j < kBatchChunks; ++j)
           wq[j] = *reinterpret_cast<const axk_u32x4*>(sW + nl * kStageLd + 64 * j + 16 * g);
