@@ -24,7 +24,7 @@
 //   pcount / pscan / pscatter — the pairs grouped by expert in 256-token blocks (per-block bitmask counts, one
 //             scan of the (expert, block) bases, stable scatter), plus a tile list of kBM-row tiles per active
 //             expert and for the shared expert over all tokens
-//   ggemm   — a grouped GEMM on MFMA: workgroup = (tile, kBN output columns), A rows gathered by token and
+//   ggemm   — a grouped GEMM on MFMA: workgroup = (tile, 256 weight rows), A rows gathered by token and
 //             staged in LDS, MXFP4 B tiles staged in LDS and decoded into bf16 fragments; gate-up with the SwiGLU
 //             epilogue, then down with the routing-weight epilogue
 //   combine — as decode
@@ -45,7 +45,7 @@ constexpr int kDecodeTokens = 64 * kMaskWords;  // above this the prefill path r
 constexpr int64_t kMaxPrefillTokens = 1 << 16;
 constexpr int64_t kMaxPrefillPairs = 1 << 19;
 constexpr int kBlkTokens = 256;  // tokens per block of the prefill grouping
-constexpr int kBM = 64, kBN = 128, kBK = 64;  // prefill GEMM tile
+constexpr int kBM = 64, kBK = 64;  // prefill GEMM tile rows, K step
 
 struct MoeWs {
   int* counts;      // [E]
@@ -1024,400 +1024,48 @@ __global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __rest
 }
 
 // ---------------------------------------------------------------------------------------------
-// prefill grouped GEMM: workgroup (tile of kBM rows of one expert, kBN output columns), 4 waves across N
+// prefill grouped GEMM: workgroup (tile of kBM rows of one expert, 256 weight rows), wave w a 64 x 64 block of
+// the output (four 16-row x four 16-column MFMA tiles: every A fragment feeds four MFMAs and every B fragment
+// four). MODE 0: weight rows = 128 gate + the same 128 up columns (SwiGLU pairs gate and up tiles in the same
+// lanes); MODE 1: 256 columns of H.
+// Every global load instruction covers whole 128-byte lines of few rows, which keeps the address path's
+// per-line work low: A per K step as 8 rows x 128 bytes per instruction; B for 4 K steps at once (128 code
+// bytes of a weight row = 256 k) as 8 rows x 128 bytes per instruction, held in registers for a whole
+// super-step and written to LDS at its start; the E8M0 scales of the whole reduction are staged once per
+// workgroup. Workgroups are mapped so that all tiles and column blocks of one expert run on one XCD: its
+// weights are fetched into that XCD's L2 once.
+// LDS: A [2][64 rows][144 bytes]; B [256 rows][144 bytes] (one super-step); scales [256 rows][Kd/32 + 16].
 // ---------------------------------------------------------------------------------------------
-constexpr int kLdA = kBK + 8;  // bf16 elements per staged activation row
-constexpr int kLdB = 48;       // bytes per staged weight row of a K step (32 code bytes + pad)
-constexpr int kBufBytes = kBM * kLdA * 2 + kBN * kLdB + kBN * 2;
-
 struct GGemmArgs {
   const uint16_t* a;     // gate-up: h2 [T, H]; down: act [P, F]
   const uint16_t* a_sh;  // down: act_sh [T, Fs]
   const uint8_t *w, *s;  // routed: gate-up e_gw / e_gs [E, 2F, H/2 | H/32]; down e_dw / e_ds [E, H, F/2 | F/32]
   const uint8_t *w_sh, *s_sh, *u_sh, *us_sh;  // shared: gate-up gate and up [Fs, H/2]; down [H, Fs/2] (w_sh, s_sh)
-  int T, H, F, Fs;
+  int T, H, F, Fs, Fmax;  // Fmax = max(F, Fs): sets the gate-up column-block count
   MoeWs ws;
 };
 
-// MODE 0: gate-up + SwiGLU -> act (routed) / act_sh (shared); columns 64 n of gate and the same of up.
-// MODE 1: down -> y = acc * routing weight (routed) / y_sh (shared); 128 columns of H.
-// Each K step (kBK) a thread loads 16 activation values and one 32-code E8M0 block of a weight row; the loads
-// run two K steps ahead (three register stages). Weights stay MXFP4 in LDS (small buffers keep several
-// workgroups per CU) and are decoded into bf16 fragments with the scaled converts.
-template <int MODE>
-__global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
-  __shared__ __align__(16) unsigned char smem[2 * kBufBytes];
-  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
-  const int4 tl = g.ws.tiles[blockIdx.x];
-  const int e = tl.x, row0 = tl.y, rows = tl.z;
-  const bool shared = e < 0;
-  const int nt = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, g4 = lane >> 4;
-
-  // shapes of this tile's GEMM
-  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);          // reduction length
-  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;          // output columns
-  const int col0 = MODE == 0 ? 64 * nt : kBN * nt;
-  if (col0 >= No) return;
-
-  // this thread's staged activation row (16 values of a K step) and weight row (one 32-code block)
-  const int arow = tid >> 2, aq = tid & 3;
-  const int brow = tid >> 1, bh = tid & 1;
-  const uint16_t* asrc;
-  {
-    const int r = min(arow, rows - 1);  // rows past the tile re-read its last row (never stored)
-    if (MODE == 0) {
-      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
-      asrc = g.a + (int64_t)tok * g.H;
-    } else {
-      asrc = shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F;
-    }
-  }
-  const uint8_t* bsrc;
-  const uint8_t* ssrc;
-  {
-    int wr;
-    const uint8_t *wb, *sb;
-    if (MODE == 0) {
-      const bool up = brow >= 64;
-      wr = col0 + (brow & 63);
-      if (shared) {
-        wb = up ? g.u_sh : g.w_sh;
-        sb = up ? g.us_sh : g.s_sh;
-      } else {
-        const int64_t rows2 = 2 * (int64_t)g.F;
-        wb = g.w + (int64_t)e * rows2 * (g.H / 2) + (up ? (int64_t)g.F * (g.H / 2) : 0);
-        sb = g.s + (int64_t)e * rows2 * (g.H / 32) + (up ? (int64_t)g.F * (g.H / 32) : 0);
-      }
-    } else {
-      wr = col0 + brow;
-      wb = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
-      sb = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
-    }
-    wr = min(wr, No - 1);  // columns past No re-read the last row (never stored)
-    bsrc = wb + (int64_t)wr * (Kd / 2);
-    ssrc = sb + (int64_t)wr * (Kd / 32);
-  }
-
-  // Wave w owns all kBM rows and two 16-column tiles: gate-up, gate columns 16w .. and the same up columns
-  // (B rows 16w and 64 + 16w); down, columns 32w .. 32w + 31. Each B fragment is decoded once per wave.
-  const int boff[2] = {MODE == 0 ? 16 * wave : 32 * wave, MODE == 0 ? 64 + 16 * wave : 32 * wave + 16};
-
-  const int nk = Kd / kBK;
-  // Three register stages, as plain variables (a stage passed around by reference would live in scratch).
-  // Loads are unconditional (K step clamped): every path keeps the same loads in flight.
-#define AXK_GG_LOAD(A0, A1, B, S, ks)                                          \
-  do {                                                                         \
-    const int k0_ = min((ks), nk - 1) * kBK;                                   \
-    A0 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq);                \
-    A1 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq + 8);            \
-    B = *reinterpret_cast<const uint4*>(bsrc + (k0_ + 32 * bh) / 2);           \
-    S = ssrc[(k0_ + 32 * bh) / 32];                                            \
-  } while (0)
-#define AXK_GG_STORE(A0, A1, B, S, buf)                                        \
-  do {                                                                         \
-    unsigned char* base_ = smem + (buf) * kBufBytes;                           \
-    uint16_t* sA_ = reinterpret_cast<uint16_t*>(base_);                        \
-    unsigned char* sB_ = base_ + kBM * kLdA * 2;                               \
-    *reinterpret_cast<uint4*>(sA_ + arow * kLdA + 16 * aq) = A0;               \
-    *reinterpret_cast<uint4*>(sA_ + arow * kLdA + 16 * aq + 8) = A1;           \
-    *reinterpret_cast<uint4*>(sB_ + brow * kLdB + 16 * bh) = B;                \
-    (sB_ + kBN * kLdB)[brow * 2 + bh] = (unsigned char)(S);                   \
-  } while (0)
-
-  axk_f32x4 acc[4][2];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int buf) {
-    const unsigned char* base = smem + buf * kBufBytes;
-    const uint16_t* sA = reinterpret_cast<const uint16_t*>(base);
-    const unsigned char* sB = base + kBM * kLdA * 2;
-    const unsigned char* sS = sB + kBN * kLdB;
-#pragma unroll
-    for (int kh = 0; kh < kBK / 32; ++kh) {
-      axk_bf16x8 af[4], bf[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = boff[j] + l16;
-        const uint32_t word = *reinterpret_cast<const uint32_t*>(sB + r * kLdB + 16 * kh + 4 * g4);
-        bf[j] = fp4x8_to_bf16x8(word, e8m0_to_f32(sS[r * 2 + kh]));
-      }
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(sA + (16 * mt + l16) * kLdA + 32 * kh + 8 * g4);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
-    }
-  };
-
-  // K steps: stage ks + 2 is loaded while ks is computed; stage ks + 1 goes to LDS after it
-  uint4 a00, a10, b0, a01, a11, b1, a02, a12, b2;
-  uint32_t s0, s1, s2;
-  AXK_GG_LOAD(a00, a10, b0, s0, 0);
-  AXK_GG_LOAD(a01, a11, b1, s1, 1);
-  AXK_GG_STORE(a00, a10, b0, s0, 0);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ks += 3) {  // one exit: steps past nk only move clamped data
-    AXK_GG_LOAD(a02, a12, b2, s2, ks + 2);
-    compute(ks & 1);
-    AXK_GG_STORE(a01, a11, b1, s1, (ks + 1) & 1);
-    __syncthreads();
-    AXK_GG_LOAD(a00, a10, b0, s0, ks + 3);
-    if (ks + 1 < nk) compute((ks + 1) & 1);
-    AXK_GG_STORE(a02, a12, b2, s2, ks & 1);
-    __syncthreads();
-    AXK_GG_LOAD(a01, a11, b1, s1, ks + 4);
-    if (ks + 2 < nk) compute(ks & 1);
-    AXK_GG_STORE(a00, a10, b0, s0, (ks + 1) & 1);
-    __syncthreads();
-  }
-#undef AXK_GG_LOAD
-#undef AXK_GG_STORE
-
-  // epilogue: rows 16 mt + 4 g + r of the tile
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mt + 4 * g4 + r;
-      if (row >= rows) continue;
-      const int64_t prow = row0 + row;
-      if (MODE == 0) {
-        const int col = col0 + 16 * wave + l16;
-        if (col >= No) continue;
-        const float gv = round_bf16(acc[mt][0][r]), uv = round_bf16(acc[mt][1][r]);
-        const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
-        if (shared)
-          g.ws.act_sh[prow * g.Fs + col] = a;
-        else
-          g.ws.act[prow * g.F + col] = a;
-      } else {
-        const float rw = shared ? 1.0f : g.ws.row_w[prow];
-        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = col0 + 32 * wave + 16 * j + l16;
-          if (col >= No) continue;
-          if (shared)
-            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
-          else
-            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
-        }
-      }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// prefill grouped GEMM, wide tiles: workgroup (tile of kBM rows of one expert, 256 weight rows), wave w a 64 x 64
-// block of the output (four 16-row x four 16-column MFMA tiles): every A fragment feeds four MFMAs and every B
-// fragment four. MODE 0: weight rows = 128 gate + the same 128 up columns (SwiGLU pairs gate and up tiles in the
-// same lanes); MODE 1: 256 columns of H.
-// LDS per buffer: A [64 rows][72 bf16] (144-byte rows), B [256 rows][48 bytes] = 32 code bytes with the row's
-// 4-byte groups reordered (group g of k-half h at 8 g + 4 h, so one 64-bit read gives a lane both halves) and
-// the two E8M0 scale bytes at +32. Row strides of 36 and 12 banks keep the 16-lane phases of every read and
-// write on distinct banks.
-// ---------------------------------------------------------------------------------------------
-constexpr int kG2Rows = 256;                       // weight rows per workgroup
-constexpr int kG2LdA = kBK + 8;                    // bf16 per staged activation row
-constexpr int kG2LdB = 48;                         // bytes per staged weight row
-constexpr int kG2Buf = kBM * kG2LdA * 2 + kG2Rows * kG2LdB;
-constexpr int kG2Cols0 = kG2Rows / 2;              // gate-up: output (act) columns per workgroup
-constexpr int kG2Cols1 = kG2Rows;                  // down: output columns per workgroup
-
-template <int MODE>
-__global__ __launch_bounds__(256) void moe_ggemm2_kernel(GGemmArgs g) {
-  __shared__ __align__(16) unsigned char smem[2 * kG2Buf];
-  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
-  const int4 tl = g.ws.tiles[blockIdx.x];
-  const int e = tl.x, row0 = tl.y, rows = tl.z;
-  const bool shared = e < 0;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, g4 = lane >> 4;
-
-  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);  // reduction length
-  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;  // output columns
-  const int col0 = blockIdx.y * (MODE == 0 ? kG2Cols0 : kG2Cols1);
-  if (col0 >= No) return;
-
-  // staging: thread t loads A row t % 64, k quarter t / 64 (16 values) and B row t (32 code bytes + 2 scales)
-  const int arow = tid & 63, aq = tid >> 6;
-  const uint16_t* asrc;
-  {
-    const int r = min(arow, rows - 1);  // rows past the tile re-read its last row (never stored)
-    if (MODE == 0) {
-      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
-      asrc = g.a + (int64_t)tok * g.H;
-    } else {
-      asrc = shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F;
-    }
-  }
-  const uint8_t* bsrc;
-  const uint8_t* ssrc;
-  {
-    int wr;
-    const uint8_t *wb, *sb;
-    if (MODE == 0) {
-      const bool up = tid >= kG2Cols0;
-      wr = col0 + (tid & (kG2Cols0 - 1));
-      if (shared) {
-        wb = up ? g.u_sh : g.w_sh;
-        sb = up ? g.us_sh : g.s_sh;
-      } else {
-        const int64_t rows2 = 2 * (int64_t)g.F;
-        wb = g.w + (int64_t)e * rows2 * (g.H / 2) + (up ? (int64_t)g.F * (g.H / 2) : 0);
-        sb = g.s + (int64_t)e * rows2 * (g.H / 32) + (up ? (int64_t)g.F * (g.H / 32) : 0);
-      }
-    } else {
-      wr = col0 + tid;
-      wb = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
-      sb = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
-    }
-    wr = min(wr, No - 1);  // columns past No re-read the last row (never stored)
-    bsrc = wb + (int64_t)wr * (Kd / 2);
-    ssrc = sb + (int64_t)wr * (Kd / 32);
-  }
-  // B rows of wave w's four column tiles j (16 rows each)
-  int brow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    brow[j] = MODE == 0 ? (j >> 1) * kG2Cols0 + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
-
-  const int nk = Kd / kBK;
-  // three register stages as plain variables; loads unconditional (K step clamped)
-#define AXK_G2_LOAD(A0, A1, B0, B1, S, ks)                                     \
-  do {                                                                         \
-    const int k0_ = min((ks), nk - 1) * kBK;                                   \
-    A0 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq);                \
-    A1 = *reinterpret_cast<const uint4*>(asrc + k0_ + 16 * aq + 8);            \
-    B0 = *reinterpret_cast<const uint4*>(bsrc + k0_ / 2);                      \
-    B1 = *reinterpret_cast<const uint4*>(bsrc + k0_ / 2 + 16);                 \
-    S = *reinterpret_cast<const uint16_t*>(ssrc + k0_ / 32);                   \
-  } while (0)
-  // code dwords d0..d7 hold k 8i .. 8i + 7 (group i % 4 of k-half i / 4): stored as d0 d4 d1 d5 d2 d6 d3 d7
-#define AXK_G2_STORE(A0, A1, B0, B1, S, buf)                                   \
-  do {                                                                         \
-    unsigned char* base_ = smem + (buf) * kG2Buf;                              \
-    uint16_t* sA_ = reinterpret_cast<uint16_t*>(base_);                        \
-    unsigned char* sB_ = base_ + kBM * kG2LdA * 2 + tid * kG2LdB;              \
-    *reinterpret_cast<uint4*>(sA_ + arow * kG2LdA + 16 * aq) = A0;             \
-    *reinterpret_cast<uint4*>(sA_ + arow * kG2LdA + 16 * aq + 8) = A1;         \
-    *reinterpret_cast<uint4*>(sB_) = make_uint4(B0.x, B1.x, B0.y, B1.y);       \
-    *reinterpret_cast<uint4*>(sB_ + 16) = make_uint4(B0.z, B1.z, B0.w, B1.w);  \
-    *reinterpret_cast<uint16_t*>(sB_ + 32) = (uint16_t)(S);                    \
-  } while (0)
-
-  axk_f32x4 acc[4][4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int buf) __attribute__((always_inline)) {
-    const unsigned char* base = smem + buf * kG2Buf;
-    const uint16_t* sA = reinterpret_cast<const uint16_t*>(base);
-    const unsigned char* sB = base + kBM * kG2LdA * 2;
-    uint2 bw[4];
-    uint32_t sc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const unsigned char* rp = sB + (brow[j] + l16) * kG2LdB;
-      bw[j] = *reinterpret_cast<const uint2*>(rp + 8 * g4);
-      sc[j] = *reinterpret_cast<const uint16_t*>(rp + 32);
-    }
-#pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      axk_bf16x8 af[4], bf[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = fp4x8_to_bf16x8(kh ? bw[j].y : bw[j].x, e8m0_to_f32((sc[j] >> (8 * kh)) & 0xffu));
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(sA + (16 * mt + l16) * kG2LdA + 32 * kh + 8 * g4);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
-    }
-  };
-
-  uint4 a00, a10, b00, b10, a01, a11, b01, b11, a02, a12, b02, b12;
-  uint32_t s0, s1, s2;
-  AXK_G2_LOAD(a00, a10, b00, b10, s0, 0);
-  AXK_G2_LOAD(a01, a11, b01, b11, s1, 1);
-  AXK_G2_STORE(a00, a10, b00, b10, s0, 0);
-  __syncthreads();
-  for (int ks = 0; ks < nk; ks += 3) {  // one exit: steps past nk only move clamped data
-    AXK_G2_LOAD(a02, a12, b02, b12, s2, ks + 2);
-    compute(ks & 1);
-    AXK_G2_STORE(a01, a11, b01, b11, s1, (ks + 1) & 1);
-    __syncthreads();
-    AXK_G2_LOAD(a00, a10, b00, b10, s0, ks + 3);
-    if (ks + 1 < nk) compute((ks + 1) & 1);
-    AXK_G2_STORE(a02, a12, b02, b12, s2, ks & 1);
-    __syncthreads();
-    AXK_G2_LOAD(a01, a11, b01, b11, s1, ks + 4);
-    if (ks + 2 < nk) compute(ks & 1);
-    AXK_G2_STORE(a00, a10, b00, b10, s0, (ks + 1) & 1);
-    __syncthreads();
-  }
-#undef AXK_G2_LOAD
-#undef AXK_G2_STORE
-
-  // epilogue: rows 16 mt + 4 g + r of the tile
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * mt + 4 * g4 + r;
-      if (row >= rows) continue;
-      const int64_t prow = row0 + row;
-      if (MODE == 0) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = col0 + 32 * wave + 16 * j + l16;
-          if (col >= No) continue;
-          const float gv = round_bf16(acc[mt][j][r]), uv = round_bf16(acc[mt][j + 2][r]);
-          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
-          if (shared)
-            g.ws.act_sh[prow * g.Fs + col] = a;
-          else
-            g.ws.act[prow * g.F + col] = a;
-        }
-      } else {
-        const float rw = shared ? 1.0f : g.ws.row_w[prow];
-        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = col0 + 64 * wave + 16 * j + l16;
-          if (col >= No) continue;
-          if (shared)
-            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
-          else
-            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
-        }
-      }
-    }
-}
-
-// ---------------------------------------------------------------------------------------------
-// prefill grouped GEMM, line-coalesced staging (the kernel launched): as moe_ggemm2_kernel for the MFMA work,
-// but every global load instruction covers whole 128-byte lines of few rows, which keeps the address path's
-// per-line work low: A per K step as 8 rows x 128 bytes per instruction; B for 4 K steps at once (128 code
-// bytes of a weight row = 256 k) as 8 rows x 128 bytes per instruction, held in registers for a whole super-step
-// and written to LDS at its start; the E8M0 scales of the whole reduction are staged once per workgroup.
-// LDS: A [2][64 rows][144 bytes]; B [256 rows][144 bytes] (one super-step); scales [256 rows][Kd/32 + 16].
-// ---------------------------------------------------------------------------------------------
-constexpr int kG3LdB = 144;  // bytes per staged weight row of a super-step (128 code bytes + pad)
+constexpr int kG2Rows = 256;          // weight rows per workgroup
+constexpr int kG2LdA = kBK + 8;       // bf16 per staged activation row
+constexpr int kG2Cols0 = kG2Rows / 2;  // gate-up: output (act) columns per workgroup
+constexpr int kG2Cols1 = kG2Rows;      // down: output columns per workgroup
+constexpr int kXcds = 8;              // MI355X: consecutive workgroups go round-robin over 8 XCDs
+constexpr int kG3LdB = 144;           // bytes per staged weight row of a super-step (128 code bytes + pad)
 constexpr int kG3ABytes = kBM * kG2LdA * 2;
 size_t g3_lds_bytes(int Kd) { return 2 * (size_t)kG3ABytes + (size_t)kG2Rows * kG3LdB + (size_t)kG2Rows * (Kd / 32 + 16); }
 
 template <int MODE>
 __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
-  if ((int)blockIdx.x >= *g.ws.n_tiles) return;
-  const int4 tl = g.ws.tiles[blockIdx.x];
+  // physical workgroup w runs on XCD w % 8: of the n_tiles x nblk (tile, column block) pairs, XCD x takes the
+  // contiguous run [x per, (x + 1) per) in order (tiles are in expert order), per = the pairs / 8 rounded up; the
+  // grid's surplus workgroups exit
+  const int nblk = MODE == 0 ? (g.Fmax + kG2Cols0 - 1) / kG2Cols0 : (g.H + kG2Cols1 - 1) / kG2Cols1;
+  const int total = *g.ws.n_tiles * nblk, per = (total + kXcds - 1) / kXcds;
+  const int k = blockIdx.x / kXcds, lid = (blockIdx.x % kXcds) * per + k;
+  if (k >= per || lid >= total) return;
+  const int tile = lid / nblk, cblk = lid - tile * nblk;
+  const int4 tl = g.ws.tiles[tile];
   const int e = tl.x, row0 = tl.y, rows = tl.z;
   const bool shared = e < 0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1425,7 +1073,7 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
 
   const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);  // reduction length
   const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;  // output columns
-  const int col0 = blockIdx.y * (MODE == 0 ? kG2Cols0 : kG2Cols1);
+  const int col0 = cblk * (MODE == 0 ? kG2Cols0 : kG2Cols1);
   if (col0 >= No) return;
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
   unsigned char* sB = smem + 2 * kG3ABytes;
@@ -1698,7 +1346,7 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
     hipLaunchKernelGGL(moe_pscatter_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
     const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
     const int fmax = F > Fs ? F : Fs;
-    GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, w};
+    GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, fmax, w};
     const size_t lds0 = g3_lds_bytes(H), lds1 = g3_lds_bytes(fmax);
     static bool g3_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
     if (!g3_raised) {
@@ -1709,11 +1357,11 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
         return AXK_E_LAUNCH;
       g3_raised = true;
     }
-    hipLaunchKernelGGL(moe_ggemm3_kernel<0>, dim3(tiles, (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0)), dim3(256),
-                       lds0, st, gu);
-    GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, w};
-    hipLaunchKernelGGL(moe_ggemm3_kernel<1>, dim3(tiles, (unsigned)((H + kG2Cols1 - 1) / kG2Cols1)), dim3(256),
-                       lds1, st, dn);
+    const unsigned nb0 = (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0), nb1 = (unsigned)((H + kG2Cols1 - 1) / kG2Cols1);
+    auto xgrid = [](unsigned n) { return dim3((n + kXcds - 1) / kXcds * kXcds); };  // whole rounds over the XCDs
+    hipLaunchKernelGGL(moe_ggemm3_kernel<0>, xgrid(tiles * nb0), dim3(256), lds0, st, gu);
+    GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
+    hipLaunchKernelGGL(moe_ggemm3_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
                        0, st, ca);
