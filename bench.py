@@ -248,6 +248,7 @@ class GdnPrefillWorkload(Workload):
     kernel = "gdn chunk step (prep + scan)"
     timing = "graph"
     mfma = True
+    traffic_profile = "gdn_prefill_config2b_pmc.txt"
 
     def __init__(self, dev):
         import torch
@@ -389,6 +390,7 @@ class MoePrefillWorkload(Workload):
     kernel = "moe prefill step"
     timing = "graph"
     mfma = True
+    traffic_profile = "moe_prefill_config3b_pmc.txt"
 
     def __init__(self, dev):
         import torch
