@@ -9,24 +9,33 @@
 // Routed experts are planar MXFP4 tensors: gate-up e_gw [E, 2F, H/2] (gate rows, then up rows), e_gs
 // [E, 2F, H/32]; down e_dw [E, H, F/2], e_ds [E, H, F/32] (models/qwen35_35b_a3b/qwen35_35b_a3b.manifest.json).
 //
-// Kernels (decode sizes: tokens x top_k <= kMaxPairs):
-//   route   — one wave per token: softmax, top-K, renormalised weights
-//   group   — one workgroup: the (token, slot) pairs grouped by expert in (token, slot) order (deterministic
-//             counting sort: one thread per expert scans the pairs), and the list of active experts
-//   gateup  — one workgroup per (active expert or the shared expert, run of 16-row tiles): the expert's
-//             gathered token rows staged in LDS, each wave streaming its gate and up tiles as MXFP4 over the
-//             full K with the next batch of loads in flight; SwiGLU in the epilogue
-//   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the pair's routing weight
-//   combine — one workgroup per token: shared gate once, residual, sum over the token's K experts in slot order
+// Router (axk_moe_decode; q35_layer_mc.py:820-829):
+//   router       — decode: split-K GEMV, workgroup = (16 experts, 16 tokens, K slice), partial logits per slice
+//   router_tile  — prefill: 64 x 64 MFMA tiles of tokens x experts over two K halves
+//   route_part   — one wave per token: the slice partials summed in fixed order into the logits, softmax,
+//                  top-K by ballot rounds (ties: lower id), renormalised weights
+//   route        — the same selection from caller logits (axk_moe_route)
+// Experts, decode (tokens <= kDecodeTokens, tokens x top_k <= kMaxPairs):
+//   group   — one workgroup: per-expert token bitmasks, the (token, slot) pairs ranked by popcount (stable,
+//             deterministic), the active-expert records {rows, expert, first sorted row}
+//   gateup  — workgroup = (active expert or the shared expert, run of 16-row weight tiles): each wave streams its
+//             MXFP4 gate and up rows over the full K. For small row counts the weights pass through a
+//             wave-private LDS tile in 128-byte row segments (whole cache lines per load) and are read back
+//             in the MFMA layout; SwiGLU in the epilogue
+//   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the routing weight, written
+//             to y by pair
+//   combine — workgroup = (token, columns): shared gate once, residual, sum over the token's K pairs in slot
+//             order, one bf16 rounding
 // Every expert's weights are read once per call, whatever the number of its tokens.
 //
 // Prefill (tokens > kDecodeTokens; moe_slots_px + moe_combine of q35_moe_prefill.py:150-214):
 //   pcount / pscan / pscatter — the pairs grouped by expert in 256-token blocks (per-block bitmask counts, one
 //             scan of the (expert, block) bases, stable scatter), plus a tile list of kBM-row tiles per active
 //             expert and for the shared expert over all tokens
-//   ggemm   — a grouped GEMM on MFMA: workgroup = (tile, 256 weight rows), A rows gathered by token and
-//             staged in LDS, MXFP4 B tiles staged in LDS and decoded into bf16 fragments; gate-up with the SwiGLU
-//             epilogue, then down with the routing-weight epilogue
+//   ggemm3  — a grouped GEMM on MFMA: workgroup = (tile, 256 weight rows), workgroups spread over the XCDs so
+//             that each XCD takes a contiguous run of the expert-ordered tiles; A rows gathered by token and
+//             B MXFP4 rows loaded as whole cache lines, both staged in LDS; per-wave 64 x 64 blocks; gate-up
+//             with the SwiGLU epilogue, then down with the routing-weight epilogue into fp32 y by pair
 //   combine — as decode
 #include "axk_common.h"
 #include "axk_host.h"
@@ -815,7 +824,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------
-// combine: one workgroup per token
+// combine
 // ---------------------------------------------------------------------------------------------
 struct CombineArgs {
   const uint16_t* h2;     // [T, H]

@@ -11,13 +11,14 @@
 //              page-table shape, so one plan serves every attention layer of a decode step (no host sync,
 //              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
 //              compute the same partition themselves from the page table and no plan launch is needed.
-//  2. decode — one workgroup per work item. Each wave takes 32-token tiles of the item's pages:
-//              S^T = K Q^T on MFMA (K rows straight from HBM with 128-bit loads, Q in registers),
-//              online softmax in fp32 (exp2 domain), P (bf16) x V on MFMA with V streamed HBM -> LDS
-//              by direct loads into a padded tile (the token-contiguous operand MFMA needs); the 4 waves
-//              merge their (m, l, O) in LDS. A sequence with one split writes its output directly;
-//              otherwise the item writes an fp32 partial (m, l, O).
-//  3. merge  — per (sequence, KV head) with more than one split: log-sum-exp merge of the partials,
+//  2. decode — persistent: a few workgroups per CU take the work items in turn. The 4 waves share every
+//              16-token K/V tile of the item's pages: the tile streams HBM -> LDS by direct loads into a
+//              3-deep ring (two tiles in flight while one is computed). Every wave computes the full scores
+//              S^T = K Q^T of the tile on MFMA (Q in registers) and the online softmax in fp32 (exp2 domain),
+//              then O^T += V^T P^T on MFMA for its own quarter of the head dim (V^T fragments by transposing
+//              LDS reads), so no cross-wave merge is needed. A sequence with one split writes its output
+//              directly; otherwise the item writes an fp32 partial (m, l, O).
+//  3. merge  — per (sequence, query head) of a sequence with more than one split: log-sum-exp merge of the partials,
 //              the split-KV merge of models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:330-349; zero
 //              output for sequences without pages. A separate launch on purpose: merging inside the
 //              decode kernel needs a device-scope release/acquire per workgroup, which on a multi-XCD

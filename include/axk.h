@@ -214,8 +214,10 @@ int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* 
  * MoE with MXFP4 experts (router top-K, shared expert with sigmoid gate, routed SwiGLU experts)
  * ------------------------------------------------------------------------------------------- */
 
-/* Workspace bytes for axk_moe_experts / axk_moe_decode (0 = unsupported shape: tokens <= 256,
- * tokens x top_k <= 8192, num_experts <= 1024, top_k <= 32, hidden % 64 == 0, inter % 32 == 0). */
+/* Workspace bytes for axk_moe_experts / axk_moe_decode (0 = unsupported shape). Always: num_experts <= 1024,
+ * top_k <= 32, top_k <= num_experts, hidden % 64 == 0. Decode (tokens <= 256): tokens x top_k <= 8192,
+ * inter and shared_inter % 32 == 0. Prefill (tokens > 256): tokens <= 65536, tokens x top_k <= 524288,
+ * inter and shared_inter % 64 == 0, hidden, inter, shared_inter <= 8192. */
 size_t axk_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
                               int64_t shared_inter);
 

@@ -43,7 +43,7 @@ def _check_layer(c, dev, norm=True):
 
 
 # e spans the router's 64 / 256 / 1024-expert register layouts; t = 130 and 256 span several 64-token words
-# of the grouping bitmask (256 is the largest token count of one call); the last three take the staged-weight
+# of the grouping bitmask (256 is the largest token count of the decode path); the last three take the staged-weight
 # streaming kernels (t <= 64) or just miss them (t = 65)
 @pytest.mark.parametrize("t,h,e,f,fs,k", [(1, 64, 8, 32, 32, 2), (5, 256, 16, 64, 96, 4), (33, 128, 64, 32, 64, 8),
                                           (7, 192, 40, 160, 0, 6), (3, 128, 200, 32, 32, 8),
