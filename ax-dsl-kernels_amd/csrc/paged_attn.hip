@@ -6,7 +6,7 @@
 // every other page is full (flash_attn.py:1421-1596 page-id lookup, tail mask 87-104).
 //
 // Three kernels:
-//  1. plan   — one wave: pages per split so that the number of (sequence, KV head, split) work items
+//  1. plan   — one wave: pages per split so that the number of (sequence, split, KV head) work items
 //              is about one per resident split workgroup, and one descriptor per item. Depends only on the
 //              page-table shape, so one plan serves every attention layer of a decode step (no host sync,
 //              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
     const int pb = ptr[b], np = ptr[b + 1] - pb;
     const int ns = (np + pps - 1) / pps;
     const int local = it - offs[b];
-    const int kvh = local / ns, sp = local - kvh * ns;
+    const int sp = local / hkv, kvh = local - sp * hkv;  // items in (split, KV head) order
     ItemDesc d;
     d.b = b;
     d.kvh = kvh;
@@ -208,17 +208,18 @@ constexpr int kLocalPlanBatch = 63;  // up to this many sequences the kernels de
 
 // The plan's partition computed by one wave from the page table (batch <= kLocalPlanBatch: lane b holds
 // sequence b), with exactly the arithmetic of paged_plan_kernel: pages per split from the total work and the
-// slot count, items in (sequence, KV head, split) order.
+// slot count, items in (sequence, split, KV head) order.
 struct LocalPlan {
   int p, np, last;  // lane b: first page index, pages, last page's valid tokens of sequence b
   int off, ns;      // lane b: first item of sequence b, splits per KV head
-  int pps, n_items;
+  int pps, n_items, hkv;
 };
 
 AXK_DEV LocalPlan local_plan(const int* __restrict__ indptr, const int* __restrict__ last_page_len, int batch,
                              int hkv, int slots) {
   const int lane = threadIdx.x & 63;
   LocalPlan lp;
+  lp.hkv = hkv;
   lp.p = indptr[min(lane, batch)];
   lp.last = lane < batch ? last_page_len[lane] : 0;
   const int pn = __shfl(lp.p, min(lane + 1, 63), 64);
@@ -254,8 +255,8 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
   const int pb = __shfl(lp.p, b, 64), npb = __shfl(lp.np, b, 64), ns = __shfl(lp.ns, b, 64);
   const int local = it - __shfl(lp.off, b, 64);
   d.b = b;
-  d.kvh = local / ns;
-  d.split = local - d.kvh * ns;
+  d.split = local / lp.hkv;
+  d.kvh = local - d.split * lp.hkv;
   d.nsplit = ns;
   d.ibeg = pb + d.split * lp.pps;
   d.npg = min(lp.pps, npb - d.split * lp.pps);
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
     const LocalPlan lp = local_plan(indptr, last_page_len, batch, hkv, slots);
     np = __shfl(lp.np, b, 64);
     nsplit = __shfl(lp.ns, b, 64);
-    i0 = __shfl(lp.off, b, 64) + kvh * nsplit;
+    i0 = __shfl(lp.off, b, 64) + kvh;
   } else {
     // header, page range and item range: independent loads, one round trip
     const int hb = hdr->batch, hk = hdr->hkv;
@@ -511,7 +512,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
     if (hb != batch || hk != hkv) return;
     np = p1 - p0;
     nsplit = (io1 - io0) / hkv;
-    i0 = io0 + kvh * nsplit;
+    i0 = io0 + kvh;
   }
   uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
   if (np == 0) {
@@ -530,7 +531,8 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
     float mi[P], li[P], oi[P][V];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      const int i = min(c0 + 4 * k, nsplit - 1);  // clamped: in-bounds, weight zeroed below
+      // item of split i: i0 + i hkv (items are in (split, KV head) order); clamped: in-bounds, weight zeroed below
+      const int i = min(c0 + 4 * k, nsplit - 1) * hkv;
       mi[k] = part_m[(int64_t)(i0 + i) * group + hh];
       li[k] = part_l[(int64_t)(i0 + i) * group + hh];
       const float* src = part_o + ((int64_t)(i0 + i) * group + hh) * D + lane * V;
