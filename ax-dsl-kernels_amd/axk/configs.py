@@ -100,3 +100,27 @@ def config3(tokens: int = 32, seed: int = 0):
     h2 = torch.randn(tokens, 2048, generator=g).to(torch.bfloat16)
     x_res = torch.randn(tokens, 2048, generator=g).to(torch.bfloat16)
     return {"h2": h2, "x_res": x_res, "weights": w, "top_k": 8}
+
+
+def config4_fp8_proj(seed: int = 0, n: int = 16384, k: int = 4096, m: int = 8):
+    """Config 4's largest FP8 projection (attention q + gate, [16384, 4096]) at the group's decode batch of 8:
+    weight = N(0, 0.5) rounded to E4M3 (u8 codes), per-output-channel scale_b ~ U(0.01, 0.03) f32,
+    x bf16 [m, k] ~ N(0,1). Draw order: weight, scale_b, x."""
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n, k, generator=g) * 0.5).to(torch.float8_e4m3fn).view(torch.uint8).contiguous()
+    scale_b = torch.rand(n, generator=g) * 0.02 + 0.01
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    return {"x": x, "w": w, "scale_b": scale_b}
+
+
+def config1_kv_write(seed: int = 0):
+    """The current token's K and V rows of config 1 (bf16 [16, 2, 256] ~ N(0,1)), written into the config-1
+    cache at each sequence's last page, offset last_page_len - 1 (in bounds of the pool)."""
+    c = config1(seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    b, hkv, d = c["q"].shape[0], c["cache"].shape[3], c["cache"].shape[4]
+    k = torch.randn(b, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(b, hkv, d, generator=g).to(torch.bfloat16)
+    ends = c["indptr"][1:].long() - 1
+    loc = torch.stack([c["indices"][ends], c["last_page_len"] - 1], dim=1).to(torch.int32).contiguous()
+    return {"cache": c["cache"], "k": k, "v": v, "loc": loc}

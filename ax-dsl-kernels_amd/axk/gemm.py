@@ -60,14 +60,21 @@ def _check_a(a: torch.Tensor) -> tuple[int, int]:
     return a.shape
 
 
-def mxfp4_dequant(b_fp4: torch.Tensor, b_scale: torch.Tensor) -> torch.Tensor:
-    """Exact fp32 dequantisation of packed E2M1 codes [N, K/2] and E8M0 scales [N, K/32]."""
+def mxfp4_dequant(b_fp4: torch.Tensor, b_scale: torch.Tensor, output: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Exact fp32 dequantisation of packed E2M1 codes [N, K/2] and E8M0 scales [N, K/32] (into `output` when
+    given: fp32 [N, K], contiguous)."""
     codes, scales = _as_u8(b_fp4, "b_fp4").contiguous(), _as_u8(b_scale, "b_scale").contiguous()
     _lib.require_device(codes, scales)
     n, k = codes.shape[0], codes.shape[1] * 2
     if tuple(scales.shape) != (n, k // 32):
         raise ValueError(f"b_scale shape {tuple(scales.shape)} is incompatible with codes {tuple(codes.shape)}")
-    out = torch.empty((n, k), device=codes.device, dtype=torch.float32)
+    if output is None:
+        out = torch.empty((n, k), device=codes.device, dtype=torch.float32)
+    else:
+        if output.dtype != torch.float32 or tuple(output.shape) != (n, k) or not output.is_contiguous():
+            raise ValueError(f"output must be contiguous float32 [{n}, {k}]")
+        _lib.require_device(output)
+        out = output
     _lib.call("axk_mxfp4_dequant", codes.data_ptr(), scales.data_ptr(), out.data_ptr(), n, k, _lib.stream_of(out))
     return out
 

@@ -420,13 +420,158 @@ class MoePrefillWorkload(Workload):
         moe.moe_decode(self.h2, self.wd, top_k=8, x_res=self.x, output=self.out, workspace=self.ws)
 
     def cpu_baseline(self) -> dict:
-        return None
+        import torch
+
+        from axk import configs
+        from oracle import moe as omoe
+
+        sample = 256  # tokens of the 4096 (same weights), scaled to the full step
+        c = configs.config3(4096)
+        h2, x = c["h2"][:sample], c["x_res"][:sample]
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: omoe.moe_layer(h2, c["weights"], 8, x_res=x), budget_s=10.0, min_reps=1,
+                              max_reps=5)
+        return {"value": sec * 1e6 * (4096 / sample), "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"{sample} of the 4096 config3b tokens (oracle/moe.py moe_layer, torch CPU), median of "
+                          f"{reps} runs, scaled x{4096 // sample} to the full step"}
+
+
+class MxDequantWorkload(Workload):
+    """Config 0's weight through the standalone codec: E2M1 codes + E8M0 scales -> exact fp32 [4096, 4096].
+
+    Algorithmic bytes: codes + scales read, fp32 values written."""
+
+    name = "mxfp4_dequant"
+    kernel = "mxfp4_dequant_kernel"
+    timing = "graph"
+    traffic_profile = "mxfp4_dequant_config0_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        c = configs.config0()
+        self.host = c
+        n, k = 4096, 4096
+        self.alg_bytes = n * k // 2 + n * k // 32 + 4 * n * k
+        per_copy = n * k // 2 + n * k // 32
+        self.copies = max(2, -(-ROTATE_BYTES // (per_copy + 4 * n * k)))
+        w, s = c["w"].to(dev), c["s"].to(dev)
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.s = [s.clone() for _ in range(self.copies)]
+        self.out = [torch.empty(n, k, dtype=torch.float32, device=dev) for _ in range(self.copies)]
+        self.config = {"workload": "config0 weight: MXFP4 dequant N=4096 K=4096 -> fp32", "rotating_copies": self.copies}
+        self.dtype = "u8 codes / E8M0 -> f32"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        j = i % self.copies
+        axk.mxfp4_dequant(self.w[j], self.s[j], output=self.out[j])
+
+    def cpu_baseline(self) -> dict:
+        from oracle import _c
+
+        w, s = self.host["w"].numpy(), self.host["s"].numpy()
+        sec, reps = _time_cpu(lambda: _c.mxfp4_dequant(w, s))
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": 1, "kind": "port",
+                "sample": f"full config0 weight (oracle/mx_codec.c, one thread), median of {reps} runs"}
+
+
+class Fp8LinearWorkload(Workload):
+    """Config 4's largest FP8 projection: E4M3 weight [16384, 4096] + f32 per-channel scale, x bf16 [8, 4096]
+    (the group's decode batch), bf16 out. Algorithmic bytes: weight + scales + x + out."""
+
+    name = "fp8_linear"
+    kernel = "mx_linear_kernel<FP8>"
+    timing = "graph"
+    traffic_profile = "fp8_linear_config4q_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        c = configs.config4_fp8_proj()
+        self.host = c
+        self.m, self.n, self.k = c["x"].shape[0], c["w"].shape[0], c["w"].shape[1]
+        self.alg_bytes = self.n * self.k + 4 * self.n + 2 * self.m * self.k + 2 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        self.copies = max(2, -(-ROTATE_BYTES // (self.n * self.k)))
+        w = c["w"].to(dev)
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.sb = c["scale_b"].to(dev)
+        self.x = c["x"].to(dev)
+        self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
+        self.config = {"workload": "config4 q projection: FP8 E4M3 linear N=16384 K=4096 M=8 (per-channel scale)",
+                       "rotating_copies": self.copies}
+        self.dtype = "fp8 e4m3 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        axk.fp8_gemm(self.x, self.w[i % self.copies], None, self.sb, output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import mx as omx
+
+        c = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        w = c["w"].numpy()
+        sec, reps = _time_cpu(lambda: omx.fp8_linear(c["x"], w, None, c["scale_b"]), budget_s=10.0, min_reps=2)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config4 q projection (oracle/mx.py fp8_linear, torch CPU), median of {reps} runs"}
+
+
+class KvWriteWorkload(Workload):
+    """Config 1's KV write: the current token's K and V rows (16 sequences x 2 KV heads x 256) scattered into the
+    paged cache in place. Algorithmic bytes: k, v and the locations read, the rows written."""
+
+    name = "kv_write"
+    kernel = "paged_kv_write_kernel"
+    timing = "graph"
+    traffic_profile = "kv_write_config1_pmc.txt"
+
+    def __init__(self, dev):
+        from axk import configs
+
+        c = configs.config1_kv_write()
+        self.host = c
+        b, hkv, d = c["k"].shape
+        self.alg_bytes = 2 * (2 * b * hkv * d * 2) + c["loc"].numel() * 4
+        self.cache = c["cache"].to(dev)
+        self.k, self.v, self.loc = c["k"].to(dev), c["v"].to(dev), c["loc"].to(dev)
+        self.config = {"workload": "config1 KV write: B=16 HKV=2 D=256 page=64, rows into the paged cache"}
+        self.dtype = "bf16 rows"
+
+    def step(self, i: int) -> None:
+        from axk import attention
+
+        attention.store_paged_kv(self.k, self.v, self.cache, self.loc)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import paged_attn as opa
+
+        c = self.host
+        cache = c["cache"].clone()
+        loc = c["loc"].numpy()
+        sec, reps = _time_cpu(lambda: opa.store_paged_kv_(cache, c["k"], c["v"], loc), budget_s=2.0, min_reps=20,
+                              max_reps=2000)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": 1, "kind": "port",
+                "sample": f"full config1 KV write into the config1 cache (oracle/paged_attn.py store_paged_kv_, in "
+                          f"place), median of {reps} runs"}
 
 
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
              GdnDecodeWorkload.name: GdnDecodeWorkload, GdnPrefillWorkload.name: GdnPrefillWorkload,
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
-             CopyCalibWorkload.name: CopyCalibWorkload}
+             MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
+             KvWriteWorkload.name: KvWriteWorkload, CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 
@@ -478,6 +623,15 @@ def measure(wl, steps: int, warmup: int, eager: bool = False) -> tuple[float, fl
 
 def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
     achieved = wl.alg_bytes / (kernel_ms * 1e-3) / 1e9
+    if getattr(wl, "mfma", False):  # MFMA-bound: the roofline is the dense bf16 rate
+        tf = wl.alg_flops / (kernel_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": wl.kernel, "achieved": round(tf, 2), "peak": BF16_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": read_traffic(wl),
+                "alg_flops_per_launch": wl.alg_flops, "alg_bytes_per_launch": wl.alg_bytes}
+    else:
+        roof = {"bound": "hbm", "kernel": wl.kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(wl),
+                "alg_bytes_per_launch": wl.alg_bytes}
     return {
         "metric": METRIC,
         "value": round(ms_per_step * 1e3, 3),
@@ -495,16 +649,7 @@ def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
         "kernel_us": round(kernel_ms * 1e3, 3),
         "achieved_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": wl.kernel,
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic(wl),
-            "alg_bytes_per_launch": wl.alg_bytes,
-        },
+        "roofline": roof,
     }
 
 

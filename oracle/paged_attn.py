@@ -57,12 +57,16 @@ def paged_decode(q: torch.Tensor, cache: torch.Tensor, indptr, indices, last_pag
     return out
 
 
-def store_paged_kv(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
-    """Returns a copy of cache with k[b] / v[b] written at (page, offset) = loc[b] (flash_attn.py:53-84)."""
-    c = cache.clone()
+def store_paged_kv_(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
+    """Writes k[b] / v[b] at (page, offset) = loc[b] of cache in place and returns it (flash_attn.py:53-84)."""
     loc = np.asarray(loc).reshape(-1, 2)
     for b in range(k.shape[0]):
         page, off = int(loc[b, 0]), int(loc[b, 1])
-        c[page, 0, off] = k[b]
-        c[page, 1, off] = v[b]
-    return c
+        cache[page, 0, off] = k[b]
+        cache[page, 1, off] = v[b]
+    return cache
+
+
+def store_paged_kv(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
+    """Returns a copy of cache with k[b] / v[b] written at (page, offset) = loc[b] (flash_attn.py:53-84)."""
+    return store_paged_kv_(cache.clone(), k, v, loc)

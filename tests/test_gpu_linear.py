@@ -98,6 +98,23 @@ def test_fp8_gemm_matches_oracle(dev, m, n, k):
     torch.testing.assert_close(got32.cpu(), ref32, **F32_TOL)
 
 
+def test_fp8_gemm_config4_q_projection(dev):
+    # the measured config-4 shape: E4M3 [16384, 4096] + per-channel scale, decode batch 8
+    c = configs.config4_fp8_proj()
+    ref = mx.fp8_linear(c["x"], c["w"].numpy(), None, c["scale_b"])
+    got = axk.fp8_gemm(c["x"].to(dev), c["w"].to(dev), None, c["scale_b"].to(dev))
+    torch.testing.assert_close(got.float().cpu(), ref.to(torch.bfloat16).float(), **BF16_TOL)
+
+
+def test_dequant_config0_into_output_buffer(dev):
+    # the measured codec workload: config 0's weight into a caller-owned fp32 buffer, bit-exact
+    c = configs.config0()
+    out = torch.full((4096, 4096), float("nan"), dtype=torch.float32, device=dev)
+    got = axk.mxfp4_dequant(c["w"].to(dev), c["s"].to(dev), output=out)
+    assert got.data_ptr() == out.data_ptr()
+    assert _bits_equal(out.cpu().numpy(), mx.dequant_mxfp4(c["w"].numpy(), c["s"].numpy()))
+
+
 @pytest.mark.parametrize("m,n,k", [(32, 256, 2048), (1, 64, 32), (4096 // 64, 256, 2048)])
 def test_bf16_gemm_matches_oracle(dev, m, n, k):
     g = torch.Generator().manual_seed(m + n + k)

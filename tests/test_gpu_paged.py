@@ -112,6 +112,15 @@ def test_kv_write_then_decode(dev):
     assert int(status.item()) == 1 and torch.equal(cache, snap)
 
 
+def test_kv_write_config1(dev):
+    # the measured KV write: config 1's current-token rows into its cache, byte-exact, nothing else touched
+    c = configs.config1_kv_write()
+    cache = c["cache"].to(dev)
+    attention.store_paged_kv(c["k"].to(dev), c["v"].to(dev), cache, c["loc"].to(dev))
+    ref = pa.store_paged_kv(c["cache"], c["k"], c["v"], c["loc"].numpy())
+    assert torch.equal(cache.cpu().view(torch.int16), ref.view(torch.int16))
+
+
 def test_contract_errors(dev):
     c = configs.paged_case([10], 8, 2, 64, 32, torch.Generator().manual_seed(0))
     with pytest.raises(ValueError):
