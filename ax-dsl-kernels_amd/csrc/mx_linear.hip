@@ -29,7 +29,9 @@ constexpr int kMaxWaves = 16;
 // One workgroup: output channels [16*blockIdx.x, +16) x rows [32*blockIdx.y... ) in MT tiles of 16.
 // Lane l: N column nl = l % 16, K group g = l / 16. Chunk c covers K [c*4V, (c+1)*4V); the lane's
 // unit inside it is [c*4V + g*V, +V). MFMA step s uses k = unit + 8s .. +8 for both operands.
-template <int F, int MT>
+// STAGE: the weights are read as whole 128-byte row segments through a wave-private LDS tile
+// (axk::mx_tile_accum_staged); wave w takes segments w, w + nwaves, ...
+template <int F, int MT, bool STAGE>
 __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           const uint8_t* __restrict__ w,
                                                           const uint8_t* __restrict__ wscale,
@@ -37,7 +39,10 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
                                                           const float* __restrict__ col_scale,
                                                           const float* __restrict__ bias, void* __restrict__ out,
                                                           int out_f32, int M, int N, int64_t K) {
-  __shared__ float red[kMaxWaves * MT * 4 * 64];
+  // the waves' staging tiles, then (after a barrier) the cross-wave partial sums
+  constexpr int kTileBytes = kMaxWaves * 16 * axk::kSegLd, kRedBytes = kMaxWaves * MT * 4 * 64 * 4;
+  __shared__ __align__(16) unsigned char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
+  float* red = reinterpret_cast<float*>(smem);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int nl = lane & 15;
@@ -57,7 +62,13 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
   axk_f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  axk::mx_tile_accum<F, MT>(xrow, mvalid, w, wscale, n, nvalid, K, wave, nwaves, acc);
+  if (STAGE) {
+    axk::mx_tile_accum_staged<F, MT>(xrow, mvalid, w, wscale, (int64_t)blockIdx.x * 16, N, K, wave, nwaves,
+                                     smem + wave * 16 * axk::kSegLd, acc);
+    __syncthreads();  // the staging tiles become the reduction buffer
+  } else {
+    axk::mx_tile_accum<F, MT>(xrow, mvalid, w, wscale, n, nvalid, K, wave, nwaves, acc);
+  }
 
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -83,32 +94,33 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
   }
 }
 
-// Exact E2M1 x E8M0 -> fp32, one 32-value block per thread.
+// Exact E2M1 x E8M0 -> fp32. Lane-consecutive quads of 4 values: a wave's stores cover contiguous 1 KiB
+// (64 lanes x 16 bytes) and its code loads contiguous 128 bytes. A thread converts kDqQuads quads, 64 quads
+// apart, with every load issued before the first store. Requires K % 32 == 0 (rows are whole quads).
+constexpr int kDqQuads = 4;
 __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __restrict__ codes,
                                                             const uint8_t* __restrict__ scales,
                                                             float* __restrict__ out, int64_t N, int64_t K) {
-  const int64_t nbk = K >> 5;
-  const int64_t total = N * nbk;
-  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < total; b += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = b / nbk, kb = b - n * nbk;
-    const uint4 q = *reinterpret_cast<const uint4*>(codes + n * (K >> 1) + kb * 16);
-    const float sc = e8m0_to_f32(scales[n * nbk + kb]);
-    float4* o = reinterpret_cast<float4*>(out + n * K + kb * 32);
-    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+  const int64_t qpr = K >> 2, total = N * qpr;  // quads per row, quads in all
+  const int lane = threadIdx.x & 63;
+  const int64_t wave_base = ((int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * (64 * kDqQuads);
+  const int64_t wave_step = (int64_t)gridDim.x * (blockDim.x >> 6) * (64 * kDqQuads);
+  for (int64_t q0 = wave_base + lane; q0 < total; q0 += wave_step) {
+    uint32_t c[kDqQuads];
+    float sc[kDqQuads];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t wd = words[i];
-      float4 lo, hi;
-      lo.x = e2m1_to_f32(wd) * sc;
-      lo.y = e2m1_to_f32(wd >> 4) * sc;
-      lo.z = e2m1_to_f32(wd >> 8) * sc;
-      lo.w = e2m1_to_f32(wd >> 12) * sc;
-      hi.x = e2m1_to_f32(wd >> 16) * sc;
-      hi.y = e2m1_to_f32(wd >> 20) * sc;
-      hi.z = e2m1_to_f32(wd >> 24) * sc;
-      hi.w = e2m1_to_f32(wd >> 28) * sc;
-      o[2 * i] = lo;
-      o[2 * i + 1] = hi;
+    for (int j = 0; j < kDqQuads; ++j) {
+      const int64_t q = min(q0 + 64 * j, total - 1);  // clamped: in bounds, never stored past total
+      const int64_t n = q / qpr, kq = (q - n * qpr) << 2;
+      c[j] = *reinterpret_cast<const uint16_t*>(codes + n * (K >> 1) + (kq >> 1));
+      sc[j] = e8m0_to_f32(scales[n * (K >> 5) + (kq >> 5)]);
+    }
+#pragma unroll
+    for (int j = 0; j < kDqQuads; ++j) {
+      const int64_t q = q0 + 64 * j;
+      if (q < total)
+        reinterpret_cast<float4*>(out)[q] = make_float4(e2m1_to_f32(c[j]) * sc[j], e2m1_to_f32(c[j] >> 4) * sc[j],
+                                                        e2m1_to_f32(c[j] >> 8) * sc[j], e2m1_to_f32(c[j] >> 12) * sc[j]);
     }
   }
 }
@@ -129,19 +141,26 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   const size_t a_bytes = (size_t)((m - 1) * lda + k) * 2;
   AXK_REQUIRE(!axk_overlap(out, out_bytes, a, a_bytes), AXK_E_ALIAS);
 
+  // staged weight loads when rows are whole 128-byte segments (and MXFP4 scale rows 8-byte aligned)
+  const int64_t rb = axk::row_bytes<F>(k);
+  const bool stage = rb % axk::kSegBytes == 0 && (F != WF_MXFP4 || axk_aligned(ws, 8));
   constexpr int CH = 4 * WUnit<F>::V;
-  const int64_t nc = (k + CH - 1) / CH;
+  const int64_t nc = stage ? rb / axk::kSegBytes : (k + CH - 1) / CH;  // K work units: segments or chunks
   const int waves = (int)(nc < kMaxWaves ? nc : kMaxWaves);
   const int mt = m <= 16 ? 1 : 2;
   dim3 grid((unsigned)((n + 15) / 16), (unsigned)((m + 16 * mt - 1) / (16 * mt)));
   dim3 block(64 * waves);
   const int of32 = out_dtype == AXK_DT_F32;
-  if (mt == 1)
-    hipLaunchKernelGGL((mx_linear_kernel<F, 1>), grid, block, 0, axk_stream(stream), a, lda, w, ws, row_scale,
-                       col_scale, bias, out, of32, (int)m, (int)n, k);
-  else
-    hipLaunchKernelGGL((mx_linear_kernel<F, 2>), grid, block, 0, axk_stream(stream), a, lda, w, ws, row_scale,
-                       col_scale, bias, out, of32, (int)m, (int)n, k);
+  hipStream_t st = axk_stream(stream);
+#define AXK_MX_LAUNCH(MT_, ST_)                                                                            \
+  hipLaunchKernelGGL((mx_linear_kernel<F, MT_, ST_>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, \
+                     bias, out, of32, (int)m, (int)n, k)
+  if (mt == 1) {
+    if (stage) AXK_MX_LAUNCH(1, true); else AXK_MX_LAUNCH(1, false);
+  } else {
+    if (stage) AXK_MX_LAUNCH(2, true); else AXK_MX_LAUNCH(2, false);
+  }
+#undef AXK_MX_LAUNCH
   return axk_launch_status();
 }
 
@@ -154,8 +173,8 @@ extern "C" int axk_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales, fl
   AXK_REQUIRE(axk_aligned(codes, 16) && axk_aligned(out, 16), AXK_E_ALIGN);
   if (n == 0) return AXK_OK;
   AXK_REQUIRE(!axk_overlap(out, (size_t)n * k * 4, codes, (size_t)n * k / 2), AXK_E_ALIAS);
-  const int64_t blocks = n * (k / 32);
-  int64_t grid = (blocks + 255) / 256;
+  const int64_t waves = (n * (k / 4) + 64 * kDqQuads - 1) / (64 * kDqQuads);
+  int64_t grid = (waves + 3) / 4;
   if (grid > 65536) grid = 65536;
   hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), codes, scales, out,
                      n, k);
