@@ -34,3 +34,7 @@ from . import moe  # noqa: E402
 from .moe import moe_decode, moe_experts, moe_route, moe_workspace  # noqa: E402
 
 __all__ += ["moe", "moe_decode", "moe_experts", "moe_route", "moe_workspace"]
+
+from . import glue  # noqa: E402
+
+__all__ += ["glue"]

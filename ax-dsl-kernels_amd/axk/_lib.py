@@ -76,6 +76,14 @@ SIGNATURES: dict[str, list] = {
     "axk_moe_route": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "axk_moe_experts": [_vp] * 16 + [_i64] * 6 + [_vp, ctypes.c_size_t, _vp],
     "axk_moe_decode": [_vp] * 18 + [_i64] * 6 + [_i32, _vp, ctypes.c_size_t, _vp],
+    "axk_rmsnorm": [_vp, _i64, _vp, _vp, _i64, _i64, _i64, ctypes.c_float, _vp],
+    "axk_add_rmsnorm": [_vp] * 5 + [_i64, _i64, ctypes.c_float, _vp],
+    "axk_gated_rmsnorm_silu": [_vp] * 4 + [_i64, _i64, ctypes.c_float, _vp],
+    "axk_causal_conv1d_silu": [_vp] * 5 + [_i64] * 4 + [_vp],
+    "axk_qk_norm_rope": [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp],
+    "axk_sigmoid_mul": [_vp, _vp, _i64, _vp, _i64, _i64, _vp],
+    "axk_silu_mul": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "axk_add": [_vp, _vp, _vp, _i64, _i64, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,

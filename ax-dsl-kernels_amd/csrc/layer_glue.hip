@@ -1,0 +1,292 @@
+// Per-layer glue of the Qwen3.5 hybrid decode layer for gfx950: RMSNorm (plain, fused with the residual add,
+// gated by silu(z)), the stateful causal depthwise conv1d + SiLU, q / k RMSNorm with partial NeoX RoPE, and the
+// elementwise gates. Semantics (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py):
+//   rmsnorm(x, w)  = x * rsqrt(mean(x^2) + eps) * w  in fp32, bf16 out; layer / q / k norms take w = 1 + weight
+//                    as the reference's runtime input (one_plus, q35_step.py:346-348)
+//   gdn core norm  = bf16(rmsnorm(core, norm_w)) * silu(z), fp32 activation, bf16 out (q35_step.py:179-181)
+//   conv1d + SiLU  = per channel sum over the kernel window of x_{t-j} w[c, j] (column 0 multiplies the current
+//                    token, gdn_args q35_step.py:365-368), accumulated tap by tap from the current token backwards
+//                    with a bf16 rounding after each tap, then silu in fp32 (the golden
+//                    causal_conv1d_silu_reference, models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:241-256);
+//                    the state holds the last kernel - 1 inputs, oldest first
+//   rope           = NeoX halves of the first `rot` channels: y_i = x_i cos_i - x_{i+h} sin_i,
+//                    y_{i+h} = x_{i+h} cos_i + x_i sin_i, h = rot / 2, on the bf16 normalised q / k
+//                    (attn_block q35_step.py:191-197; models/qwen38_27b/mtp/mtp_ref.py:176-187)
+//   sigmoid gate   = bf16(attn * sigmoid(gate)); MLP = bf16(silu(g) * u); residual = bf16(x + y)
+//                    (q35_step.py:136-139, 276-279)
+// All are bandwidth- or latency-bound row operations: one wave per row for the norms (4 rows per workgroup),
+// 16-byte vector loads and stores, fp32 arithmetic.
+#include "axk_common.h"
+#include "axk_host.h"
+
+namespace {
+
+constexpr int kRowsPerWg = 4;
+constexpr int kMaxConvKernel = 8;
+constexpr int kMaxRopeDim = 512;
+
+AXK_DEV void unpack8(const uint4& v, float (&f)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+AXK_DEV uint4 pack8(const float (&f)[8]) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
+}
+
+// MODE 0: out = rmsnorm(x) w.  MODE 1: s = bf16(x + y) -> sum_out, out = rmsnorm(s) w.
+// MODE 2: out = bf16(bf16(rmsnorm(x) w) * silu(z)).  One wave per row; lane c takes 8-element chunks c, c + 64, ...
+template <int MODE>
+__global__ __launch_bounds__(64 * kRowsPerWg) void rmsnorm_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                       const uint16_t* __restrict__ y,
+                                                                       const float* __restrict__ w,
+                                                                       const uint16_t* __restrict__ z,
+                                                                       uint16_t* sum_out, uint16_t* __restrict__ out,
+                                                                       int64_t ldo, int64_t rows, int n, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = n >> 3;
+  const uint16_t* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int c = lane; c < nch; c += 64) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(xr + 8 * c), f);
+    if (MODE == 1) {
+      float g[8];
+      unpack8(*reinterpret_cast<const uint4*>(y + row * n + 8 * c), g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = round_bf16(f[i] + g[i]);
+      *reinterpret_cast<uint4*>(sum_out + row * n + 8 * c) = pack8(f);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += f[i] * f[i];
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)n + eps);
+  // second pass: the row again (the sum as this lane wrote it)
+  const uint16_t* src = MODE == 1 ? sum_out + row * n : xr;
+  for (int c = lane; c < nch; c += 64) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(src + 8 * c), f);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * c), w1 = *reinterpret_cast<const float4*>(w + 8 * c + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = f[i] * inv * wv[i];
+    if (MODE == 2) {
+      float g[8];
+      unpack8(*reinterpret_cast<const uint4*>(z + row * n + 8 * c), g);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = round_bf16(f[i]) * silu_f32(g[i]);
+    }
+    *reinterpret_cast<uint4*>(out + row * ldo + 8 * c) = pack8(f);
+  }
+}
+
+// One thread per (sequence, channel): the window slides over the tokens; history in registers.
+__global__ __launch_bounds__(256) void conv1d_silu_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ w,
+                                                          const uint16_t* state_in, uint16_t* state_out,
+                                                          uint16_t* __restrict__ out, int B, int T, int C, int K) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * C) return;
+  const int b = (int)(i / C), c = (int)(i - (int64_t)b * C);
+  float wk[kMaxConvKernel], hist[kMaxConvKernel];  // hist[0 .. K-2]: the K - 1 previous inputs, oldest first
+#pragma unroll
+  for (int j = 0; j < kMaxConvKernel; ++j) {
+    wk[j] = j < K ? bf16_bits_to_f32(w[(int64_t)c * K + j]) : 0.f;
+    hist[j] = j < K - 1 ? bf16_bits_to_f32(state_in[((int64_t)b * (K - 1) + j) * C + c]) : 0.f;
+  }
+  for (int t = 0; t < T; ++t) {
+    const int64_t o = ((int64_t)b * T + t) * C + c;
+    const float xt = bf16_bits_to_f32(x[o]);
+    // tap j multiplies x_{t-j}: j = 0 the current token, then back through the history (a bf16 rounding per tap)
+    float acc = round_bf16(__fadd_rn(0.f, __fmul_rn(xt, wk[0])));
+#pragma unroll
+    for (int j = 1; j < kMaxConvKernel; ++j)
+      if (j < K) acc = round_bf16(__fadd_rn(acc, __fmul_rn(hist[K - 1 - j], wk[j])));
+    out[o] = (uint16_t)f32_to_bf16_bits(silu_f32(acc));
+#pragma unroll
+    for (int j = 0; j + 1 < kMaxConvKernel; ++j)
+      if (j + 1 < K - 1) hist[j] = hist[j + 1];
+    if (K > 1) hist[K - 2] = xt;
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxConvKernel; ++j)
+    if (j < K - 1) state_out[((int64_t)b * (K - 1) + j) * C + c] = (uint16_t)f32_to_bf16_bits(hist[j]);
+}
+
+// One wave per (sequence, head) row of D values: RMSNorm (bf16), then NeoX RoPE on the first rot channels
+// with the sequence's cos / sin. Lane l holds channels EPL l .. EPL l + EPL - 1; channel e pairs with e + rot / 2.
+template <int EPL>
+__global__ __launch_bounds__(64 * kRowsPerWg) void qk_norm_rope_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                       const float* __restrict__ w,
+                                                                       const uint16_t* __restrict__ cosv,
+                                                                       const uint16_t* __restrict__ sinv,
+                                                                       uint16_t* __restrict__ out, int64_t rows,
+                                                                       int heads, int rot, float eps) {
+  constexpr int D = 64 * EPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / heads;
+  float v[EPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    v[j] = bf16_bits_to_f32(x[row * ldx + EPL * lane + j]);
+    ss += v[j] * v[j];
+  }
+  const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) v[j] = round_bf16(v[j] * inv * w[EPL * lane + j]);
+  const int half = rot >> 1, lofs = half / EPL;  // partner lane offset (half % EPL == 0)
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = EPL * lane + j;
+    const bool low = e < half;
+    const int plane = low ? lane + lofs : lane - lofs;
+    const float pv = __shfl(v[j], (plane >= 0 && plane < 64) ? plane : lane, 64);
+    float r = v[j];
+    if (e < rot) {
+      const int ci = low ? e : e - half;
+      const float cs = bf16_bits_to_f32(cosv[b * half + ci]), sn = bf16_bits_to_f32(sinv[b * half + ci]);
+      r = low ? v[j] * cs - pv * sn : v[j] * cs + pv * sn;
+    }
+    out[row * D + e] = (uint16_t)f32_to_bf16_bits(r);
+  }
+}
+
+// Elementwise over rows x n (n % 8 == 0): OP 0 bf16(x * sigmoid(g)), OP 1 bf16(silu(x) * g), OP 2 bf16(x + g).
+// g rows are ldg elements apart (the attention gate sits inside the q projection's rows).
+template <int OP>
+__global__ __launch_bounds__(256) void eltwise_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ g,
+                                                      int64_t ldg, uint16_t* __restrict__ out, int64_t rows, int n) {
+  const int nch = n >> 3;
+  const int64_t total = rows * nch;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / nch, c = i - r * nch;
+    float a[8], b[8];
+    unpack8(*reinterpret_cast<const uint4*>(x + r * n + 8 * c), a);
+    unpack8(*reinterpret_cast<const uint4*>(g + r * ldg + 8 * c), b);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a[k] = OP == 0 ? a[k] * sigmoid_f32(b[k]) : (OP == 1 ? silu_f32(a[k]) * b[k] : a[k] + b[k]);
+    *reinterpret_cast<uint4*>(out + r * n + 8 * c) = pack8(a);
+  }
+}
+
+unsigned row_grid(int64_t rows) { return (unsigned)((rows + kRowsPerWg - 1) / kRowsPerWg); }
+
+unsigned elt_grid(int64_t work) {
+  const int64_t g = (work + 255) / 256;
+  return (unsigned)(g < 65536 ? (g > 0 ? g : 1) : 65536);
+}
+
+bool aligned16(const void* p) { return axk_aligned(p, 16); }
+
+}  // namespace
+
+extern "C" int axk_rmsnorm(const uint16_t* x, int64_t ldx, const float* w, uint16_t* out, int64_t ldo, int64_t rows,
+                           int64_t n, float eps, axk_stream_t stream) {
+  AXK_REQUIRE(x && w && out, AXK_E_NULL);
+  AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX && ldx >= n && ldo >= n, AXK_E_SHAPE);
+  AXK_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(out), AXK_E_ALIGN);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel<0>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, ldx,
+                     nullptr, w, nullptr, nullptr, out, ldo, rows, (int)n, eps);
+  return axk_launch_status();
+}
+
+extern "C" int axk_add_rmsnorm(const uint16_t* x, const uint16_t* y, const float* w, uint16_t* sum_out,
+                               uint16_t* norm_out, int64_t rows, int64_t n, float eps, axk_stream_t stream) {
+  AXK_REQUIRE(x && y && w && sum_out && norm_out, AXK_E_NULL);
+  AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(aligned16(x) && aligned16(y) && aligned16(w) && aligned16(sum_out) && aligned16(norm_out), AXK_E_ALIGN);
+  const size_t bytes = (size_t)rows * n * 2;
+  AXK_REQUIRE(!axk_overlap(norm_out, bytes, sum_out, bytes) && !axk_overlap(norm_out, bytes, x, bytes) &&
+                  !axk_overlap(norm_out, bytes, y, bytes),
+              AXK_E_ALIAS);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel<1>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, n, y,
+                     w, nullptr, sum_out, norm_out, n, rows, (int)n, eps);
+  return axk_launch_status();
+}
+
+extern "C" int axk_gated_rmsnorm_silu(const uint16_t* x, const float* w, const uint16_t* z, uint16_t* out,
+                                      int64_t rows, int64_t n, float eps, axk_stream_t stream) {
+  AXK_REQUIRE(x && w && z && out, AXK_E_NULL);
+  AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(aligned16(x) && aligned16(w) && aligned16(z) && aligned16(out), AXK_E_ALIGN);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel<2>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, n,
+                     nullptr, w, z, nullptr, out, n, rows, (int)n, eps);
+  return axk_launch_status();
+}
+
+extern "C" int axk_causal_conv1d_silu(const uint16_t* x, const uint16_t* w, const uint16_t* state_in,
+                                      uint16_t* state_out, uint16_t* out, int64_t batch, int64_t tokens,
+                                      int64_t channels, int64_t kernel, axk_stream_t stream) {
+  AXK_REQUIRE(x && w && out && (kernel == 1 || (state_in && state_out)), AXK_E_NULL);
+  AXK_REQUIRE(batch > 0 && tokens > 0 && channels > 0 && kernel >= 1 && kernel <= kMaxConvKernel, AXK_E_SHAPE);
+  AXK_REQUIRE(batch * channels <= INT32_MAX && tokens <= INT32_MAX, AXK_E_SHAPE);
+  const size_t sbytes = (size_t)batch * (kernel - 1) * channels * 2, obytes = (size_t)batch * tokens * channels * 2;
+  // in place state is allowed (each thread reads its history before writing it); the output may not overlap it
+  AXK_REQUIRE(kernel == 1 || state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
+  AXK_REQUIRE(kernel == 1 || !axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
+  const int64_t n = batch * channels;
+  hipLaunchKernelGGL(conv1d_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, axk_stream(stream), x, w,
+                     state_in, state_out, out, (int)batch, (int)tokens, (int)channels, (int)kernel);
+  return axk_launch_status();
+}
+
+extern "C" int axk_qk_norm_rope(const uint16_t* x, int64_t ldx, const float* w, const uint16_t* cos,
+                                const uint16_t* sin, uint16_t* out, int64_t batch, int64_t heads, int64_t head_dim,
+                                int64_t rot, float eps, axk_stream_t stream) {
+  AXK_REQUIRE(x && w && out && (rot == 0 || (cos && sin)), AXK_E_NULL);
+  AXK_REQUIRE(batch > 0 && heads > 0 && ldx >= head_dim, AXK_E_SHAPE);
+  AXK_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == kMaxRopeDim, AXK_E_SHAPE);
+  const int64_t epl = head_dim / 64;
+  AXK_REQUIRE(rot >= 0 && rot <= head_dim && rot % 2 == 0 && (rot / 2) % epl == 0, AXK_E_SHAPE);
+  const int64_t rows = batch * heads;
+  const size_t obytes = (size_t)rows * head_dim * 2;
+  AXK_REQUIRE(!axk_overlap(out, obytes, x, (size_t)((rows - 1) * ldx + head_dim) * 2), AXK_E_ALIAS);
+  hipStream_t st = axk_stream(stream);
+#define AXK_QKR(E)                                                                                                 \
+  hipLaunchKernelGGL(qk_norm_rope_kernel<E>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, st, x, ldx, w, cos, sin, \
+                     out, rows, (int)heads, (int)rot, eps)
+  if (epl == 1) AXK_QKR(1);
+  else if (epl == 2) AXK_QKR(2);
+  else if (epl == 4) AXK_QKR(4);
+  else AXK_QKR(8);
+#undef AXK_QKR
+  return axk_launch_status();
+}
+
+namespace {
+template <int OP>
+int launch_eltwise(const uint16_t* x, const uint16_t* g, int64_t ldg, uint16_t* out, int64_t rows, int64_t n,
+                   axk_stream_t stream) {
+  AXK_REQUIRE(x && g && out, AXK_E_NULL);
+  AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && ldg >= n && n <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(ldg % 8 == 0 && aligned16(x) && aligned16(g) && aligned16(out), AXK_E_ALIGN);
+  hipLaunchKernelGGL(eltwise_kernel<OP>, dim3(elt_grid(rows * (n / 8))), dim3(256), 0, axk_stream(stream), x, g, ldg,
+                     out, rows, (int)n);
+  return axk_launch_status();
+}
+}  // namespace
+
+extern "C" int axk_sigmoid_mul(const uint16_t* x, const uint16_t* gate, int64_t ldg, uint16_t* out, int64_t rows,
+                               int64_t n, axk_stream_t stream) {
+  return launch_eltwise<0>(x, gate, ldg, out, rows, n, stream);
+}
+
+extern "C" int axk_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t rows, int64_t n,
+                            axk_stream_t stream) {
+  return launch_eltwise<1>(g, u, n, out, rows, n, stream);
+}
+
+extern "C" int axk_add(const uint16_t* x, const uint16_t* y, uint16_t* out, int64_t rows, int64_t n,
+                       axk_stream_t stream) {
+  return launch_eltwise<2>(x, y, n, out, rows, n, stream);
+}

@@ -260,6 +260,64 @@ int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_
                    int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
                    int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Per-layer glue of the hybrid decode layer (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py gdn_layer 149-183,
+ * attn_block 186-280, mlp_block 118-142). bf16 tensors as uint16_t, fp32 arithmetic, one bf16 rounding per op.
+ * ------------------------------------------------------------------------------------------- */
+
+/* RMSNorm of `rows` rows of n values: out = x * rsqrt(mean(x^2) + eps) * w (w f32 [n]: the reference's runtime
+ * weight, 1 + weight for the layer / q / k norms, q35_step.py:346-348). Rows ldx / ldo elements apart.
+ * Replaces rmsnorm(...) of q35_step.py:151, 190-194, 138. n % 8 == 0; x, w, out 16-byte aligned. */
+int axk_rmsnorm(const uint16_t* x, int64_t ldx, const float* w, uint16_t* out, int64_t ldo, int64_t rows, int64_t n,
+                float eps, axk_stream_t stream);
+
+/* Residual add fused with the next RMSNorm: sum_out = bf16(x + y); norm_out = rmsnorm(sum_out, w).
+ * Replaces x1 = add(xt, proj(...)) followed by rmsnorm(x1, ln2) (q35_step.py:181 / 279 and 138).
+ * Contiguous [rows, n]; norm_out may not overlap the others. */
+int axk_add_rmsnorm(const uint16_t* x, const uint16_t* y, const float* w, uint16_t* sum_out, uint16_t* norm_out,
+                    int64_t rows, int64_t n, float eps, axk_stream_t stream);
+
+/* GDN output norm: out = bf16(bf16(rmsnorm(x) * w) * silu(z)), per head row of n values (w = norm_w f32 [n],
+ * not 1 + w). Replaces rmsnorm(core, norm_w) + silu_gate(normed, z) (q35_step.py:179-180). Contiguous
+ * [rows, n]. */
+int axk_gated_rmsnorm_silu(const uint16_t* x, const float* w, const uint16_t* z, uint16_t* out, int64_t rows,
+                           int64_t n, float eps, axk_stream_t stream);
+
+/* Stateful causal depthwise conv1d + SiLU over `tokens` tokens per sequence:
+ *   out[b, t, c] = silu(sum_j x[b, t - j, c] * w[c, j]), j = 0 .. kernel - 1 (column 0 multiplies the current
+ *   token, gdn_args q35_step.py:365-368), x[b, t - j] for t - j < 0 taken from state_in (oldest first);
+ *   accumulated from j = 0 upwards with a bf16 rounding after each tap, silu in fp32 (the golden
+ *   causal_conv1d_silu_reference, models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:241-256).
+ *   state_out = the last kernel - 1 inputs. Replaces stateful_runtime_causal_depthwise_conv1d_silu
+ *   (q35_step.py:156).
+ *   x, out bf16 [batch, tokens, channels]; w bf16 [channels, kernel]; state_in / state_out bf16
+ *   [batch, kernel - 1, channels] (state_out == state_in: in place). kernel <= 8. */
+int axk_causal_conv1d_silu(const uint16_t* x, const uint16_t* w, const uint16_t* state_in, uint16_t* state_out,
+                           uint16_t* out, int64_t batch, int64_t tokens, int64_t channels, int64_t kernel,
+                           axk_stream_t stream);
+
+/* q / k head norm and partial NeoX RoPE: per (sequence b, head) row of head_dim values (rows ldx elements apart),
+ * r = bf16(rmsnorm(x) * w); the first rot channels rotate by halves with cos / sin of sequence b:
+ * y_i = r_i cos_i - r_{i+h} sin_i, y_{i+h} = r_{i+h} cos_i + r_i sin_i (h = rot / 2); the rest pass through.
+ * Replaces rmsnorm(q, q_norm) / rmsnorm(k, k_norm) + rope(..., rotary_dim=ROT) (q35_step.py:192-197;
+ * models/qwen38_27b/mtp/mtp_ref.py:176-187).
+ *   x bf16 rows [batch * heads] x head_dim; w f32 [head_dim]; cos, sin bf16 [batch, rot / 2];
+ *   out bf16 [batch, heads, head_dim] contiguous. head_dim in {64, 128, 256, 512}; (rot / 2) % (head_dim / 64) == 0. */
+int axk_qk_norm_rope(const uint16_t* x, int64_t ldx, const float* w, const uint16_t* cos, const uint16_t* sin,
+                     uint16_t* out, int64_t batch, int64_t heads, int64_t head_dim, int64_t rot, float eps,
+                     axk_stream_t stream);
+
+/* out = bf16(x * sigmoid(gate)) over rows x n (gate rows ldg apart: the gate half of the q projection).
+ * Replaces sigmoid_mul(attn, gate) (q35_step.py:276-277). */
+int axk_sigmoid_mul(const uint16_t* x, const uint16_t* gate, int64_t ldg, uint16_t* out, int64_t rows, int64_t n,
+                    axk_stream_t stream);
+
+/* out = bf16(silu(g) * u): the MLP activation, silu_mul (q35_step.py:136-137). Contiguous [rows, n]. */
+int axk_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t rows, int64_t n, axk_stream_t stream);
+
+/* out = bf16(x + y): the residual add (q35_step.py:139). Contiguous [rows, n]. */
+int axk_add(const uint16_t* x, const uint16_t* y, uint16_t* out, int64_t rows, int64_t n, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

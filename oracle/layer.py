@@ -1,0 +1,87 @@
+"""Oracle: per-layer glue of the Qwen3.5 hybrid decode layer (CPU, test infrastructure only).
+
+Restates, with the reference's rounding points (bf16 tensors between ops, fp32 inside each op):
+  * rmsnorm            q35_step.py rmsnorm(x, w, eps) with w = 1 + weight for layer / q / k norms (one_plus,
+                       models/qwen35_35b_a3b/src/70b0fbc/q35_step.py:346-348); models/qwen38_27b/mtp/mtp_ref.py:172-174
+  * gated_rmsnorm_silu the GDN output norm, rmsnorm(core, norm_w) then silu_gate(normed, z) (q35_step.py:179-180)
+  * causal_conv1d_silu causal_conv1d_silu_reference (models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:241-256) in
+                       the kernel's weight layout (column 0 multiplies the current token, gdn_args q35_step.py:365-368)
+  * rope               NeoX halves of the first rot channels (models/qwen38_27b/mtp/mtp_ref.py:176-187), cos / sin
+                       given as bf16 (rope_cos_sin, q35_step.py:408-411)
+  * qk_norm_rope, sigmoid_mul, silu_mul, add: attn_block / mlp_block (q35_step.py:136-139, 191-197, 276-279)
+Pinned by tests/test_oracle_layer.py against transformers' Qwen3_5RMSNorm, Qwen3_5RMSNormGated and
+apply_rotary_pos_emb (third-party, installed), torch.nn.functional.conv1d, and closed forms.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def _bf(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16)
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """bf16(x * rsqrt(mean(x^2) + eps) * w) over the last dim, fp32 inside."""
+    xf = x.float()
+    return _bf(xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float())
+
+
+def add_rmsnorm(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, eps: float = 1e-6):
+    s = _bf(x.float() + y.float())
+    return s, rmsnorm(s, w, eps)
+
+
+def gated_rmsnorm_silu(x: torch.Tensor, w: torch.Tensor, z: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    normed = rmsnorm(x, w, eps)
+    return _bf(normed.float() * torch.nn.functional.silu(z.float()))
+
+
+def causal_conv1d_silu(x: torch.Tensor, w: torch.Tensor, state_in: torch.Tensor):
+    """x [B, T, C] bf16; w [C, K] bf16 (column j multiplies x_{t-j}); state [B, K-1, C] bf16 (oldest first).
+    Returns (out [B, T, C] bf16, state_out [B, K-1, C] bf16)."""
+    k = w.shape[1]
+    seq = torch.cat((state_in, x), dim=1)  # [B, K-1+T, C]
+    t = x.shape[1]
+    out = torch.zeros_like(x)
+    for j in range(k):  # the current token first, then back through the window (test_gdn_attn.py:249-253)
+        src = seq[:, k - 1 - j: k - 1 - j + t, :]
+        out = _bf(out.float() + src.float() * w[:, j].float().reshape(1, 1, -1))
+    state_out = seq[:, seq.shape[1] - (k - 1):, :] if k > 1 else seq[:, :0, :]
+    return _bf(torch.nn.functional.silu(out.float())), state_out.contiguous()
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, rot: int) -> torch.Tensor:
+    """x [B, heads, D] (bf16 values); cos, sin [B, rot/2]. fp32 rotation, bf16 out."""
+    half = rot // 2
+    xf = x.float()
+    y = xf.clone()
+    c, s = cos.float()[:, None, :], sin.float()[:, None, :]
+    x1, x2 = xf[..., :half], xf[..., half:rot]
+    y[..., :half] = x1 * c - x2 * s
+    y[..., half:rot] = x2 * c + x1 * s
+    return _bf(y)
+
+
+def qk_norm_rope(x: torch.Tensor, w: torch.Tensor, cos, sin, rot: int, eps: float = 1e-6) -> torch.Tensor:
+    r = rmsnorm(x, w, eps)
+    return rope(r, cos, sin, rot) if rot else r
+
+
+def rope_cos_sin(pos: torch.Tensor, rot: int, theta: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 cos / sin [B, rot/2] of each sequence's position (q35_step.py:408-411)."""
+    inv = 1.0 / (theta ** (torch.arange(0, rot, 2, dtype=torch.int64).float() / rot))
+    f = pos.float().reshape(-1, 1) * inv.reshape(1, -1)
+    return f.cos().bfloat16(), f.sin().bfloat16()
+
+
+def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    return _bf(x.float() * torch.sigmoid(gate.float()))
+
+
+def silu_mul(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    return _bf(torch.nn.functional.silu(g.float()) * u.float())
+
+
+def add(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    return _bf(x.float() + y.float())
