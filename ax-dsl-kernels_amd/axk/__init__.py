@@ -38,3 +38,7 @@ __all__ += ["moe", "moe_decode", "moe_experts", "moe_route", "moe_workspace"]
 from . import glue  # noqa: E402
 
 __all__ += ["glue"]
+
+from . import layer  # noqa: E402
+
+__all__ += ["layer"]

@@ -124,3 +124,79 @@ def config1_kv_write(seed: int = 0):
     ends = c["indptr"][1:].long() - 1
     loc = torch.stack([c["indices"][ends], c["last_page_len"] - 1], dim=1).to(torch.int32).contiguous()
     return {"cache": c["cache"], "k": k, "v": v, "loc": loc}
+
+
+def fp8_proj_weight(n: int, k: int, g: torch.Generator):
+    """FP8 E4M3 projection [n, k] (N(0, 0.5) rounded to E4M3) and per-output-channel scale ~ U(1, 3) / sqrt(k)."""
+    w = (torch.randn(n, k, generator=g) * 0.5).to(torch.float8_e4m3fn).view(torch.uint8).contiguous()
+    s = (torch.rand(n, generator=g) * 2 + 1) / (k ** 0.5)
+    return w, s
+
+
+def _norm_w(n: int, g: torch.Generator):
+    """A norm's run-time weight as the reference passes it: 1 + N(0, 0.1) (f32)."""
+    return 1.0 + 0.1 * torch.randn(n, generator=g)
+
+
+def mlp_weights(g: torch.Generator, hidden: int, inter: int) -> dict:
+    """The dense MXFP4 MLP of a layer: gate / up [inter, hidden], down [hidden, inter] (as config 0's draws)."""
+    w = {}
+    w["gate_w"], w["gate_s"] = mxfp4_weight(inter, hidden, g)
+    w["up_w"], w["up_s"] = mxfp4_weight(inter, hidden, g)
+    w["down_w"], w["down_s"] = mxfp4_weight(hidden, inter, g)
+    return w
+
+
+def gdn_layer_weights(g: torch.Generator, hidden: int, inter: int, nk: int, nv: int, conv_kernel: int = 4) -> dict:
+    """A GDN decode layer's weights (names of q35_step.py gdn_args): FP8 projections, bf16 conv taps, f32 norms
+    (ln1 / ln2 = 1 + N(0, 0.1); norm_w = 1 + N(0, 0.1)), A_log, dt_bias ~ N(0, 0.5), MXFP4 MLP."""
+    kd, vd = nk * 128, nv * 128
+    w = {"ln1": _norm_w(hidden, g)}
+    w["w_qkv"], w["s_qkv"] = fp8_proj_weight(2 * kd + vd, hidden, g)
+    w["w_z"], w["s_z"] = fp8_proj_weight(vd, hidden, g)
+    w["w_b"], w["s_b"] = fp8_proj_weight(nv, hidden, g)
+    w["w_a"], w["s_a"] = fp8_proj_weight(nv, hidden, g)
+    w["conv_w"] = (torch.randn(2 * kd + vd, conv_kernel, generator=g) * 0.5).to(torch.bfloat16)
+    w["a_log"] = torch.randn(nv, generator=g) * 0.5
+    w["dt_bias"] = torch.randn(nv, generator=g) * 0.5
+    w["norm_w"] = _norm_w(128, g)
+    w["w_out"], w["s_out"] = fp8_proj_weight(hidden, vd, g)
+    w["ln2"] = _norm_w(hidden, g)
+    w.update(mlp_weights(g, hidden, inter))
+    return w
+
+
+def attn_layer_weights(g: torch.Generator, hidden: int, inter: int, hq: int, hkv: int, d: int) -> dict:
+    """An attention decode layer's weights (names of q35_step.py attn_args): FP8 q (per head [q | gate]), k, v, o;
+    f32 norms 1 + N(0, 0.1); MXFP4 MLP."""
+    w = {"ln1": _norm_w(hidden, g)}
+    w["w_q"], w["s_q"] = fp8_proj_weight(hq * 2 * d, hidden, g)
+    w["w_k"], w["s_k"] = fp8_proj_weight(hkv * d, hidden, g)
+    w["w_v"], w["s_v"] = fp8_proj_weight(hkv * d, hidden, g)
+    w["q_norm"] = _norm_w(d, g)
+    w["k_norm"] = _norm_w(d, g)
+    w["w_o"], w["s_o"] = fp8_proj_weight(hidden, hq * d, g)
+    w["ln2"] = _norm_w(hidden, g)
+    w.update(mlp_weights(g, hidden, inter))
+    return w
+
+
+def append_token_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator):
+    """A paged cache holding sequences of `lens` tokens plus room for one more each: returns the paged case with
+    the page table already covering the new token (lens + 1), its cache locations (int32 [B, 2]) and positions."""
+    c = paged_case(lens, hq, hkv, d, page, g, extra_pages=len(lens))
+    used = set(c["indices"].tolist())
+    spare = [p for p in range(c["cache"].shape[0]) if p not in used]
+    loc, new_last, new_indices, new_indptr = [], [], [], [0]
+    for b, L in enumerate(lens):
+        pages = c["indices"][int(c["indptr"][b]):int(c["indptr"][b + 1])].tolist()
+        if L % page == 0:
+            pages.append(spare.pop())
+        loc.append([pages[-1], L % page])
+        new_indices += pages
+        new_indptr.append(len(new_indices))
+        new_last.append(L % page + 1)
+    c.update(indices=torch.tensor(new_indices, dtype=torch.int32), indptr=torch.tensor(new_indptr, dtype=torch.int32),
+             last_page_len=torch.tensor(new_last, dtype=torch.int32), lens=[L + 1 for L in lens],
+             loc=torch.tensor(loc, dtype=torch.int32), pos=torch.tensor(list(lens)))
+    return c

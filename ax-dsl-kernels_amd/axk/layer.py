@@ -1,0 +1,98 @@
+"""Hybrid decode layers (one token per sequence) over libaxk.so: the GDN layer and the attention layer of
+models/qwen35_35b_a3b/src/70b0fbc/q35_step.py (gdn_layer 149-183, attn_block 186-293), each with its MLP.
+
+Weights travel in dicts keyed by the reference's names (q35_step.py gdn_args / attn_args / mlp_args 361-406):
+projections FP8 E4M3 as (w_<name> u8 [N, K], s_<name> f32 [N]); the MLP MXFP4 as (gate_w, gate_s, up_w, up_s,
+down_w, down_s); norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is allocated once
+by the caller (layer_workspace) and reused; a layer call allocates nothing.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+GDN_WEIGHTS = ("ln1", "w_qkv", "s_qkv", "w_z", "s_z", "w_b", "s_b", "w_a", "s_a", "conv_w", "a_log", "dt_bias",
+               "norm_w", "w_out", "s_out", "ln2")
+ATTN_WEIGHTS = ("ln1", "w_q", "s_q", "w_k", "s_k", "w_v", "s_v", "q_norm", "k_norm", "w_o", "s_o", "ln2")
+MLP_WEIGHTS = ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _weights(w: dict, names) -> list:
+    missing = [n for n in names if n not in w]
+    _check(not missing, f"missing weights: {missing}")
+    for n in names:
+        _check(w[n].is_contiguous(), f"{n} must be contiguous")
+    return [w[n] for n in names]
+
+
+def gdn_workspace(batch: int, hidden: int, num_k_heads: int, num_v_heads: int, inter: int,
+                  device, head_dim: int = 128) -> torch.Tensor:
+    n = _lib.load().axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter)
+    _check(n > 0, "unsupported GDN layer shape")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def attn_workspace(batch: int, hidden: int, num_qo_heads: int, num_kv_heads: int, head_dim: int, inter: int,
+                   device) -> torch.Tensor:
+    n = _lib.load().axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter)
+    _check(n > 0, "unsupported attention layer shape")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: torch.Tensor,
+                     num_k_heads: int, num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
+                     conv_out: Optional[torch.Tensor] = None):
+    """x bf16 [B, hidden]; state f32 [B, NV, 128, 128]; conv state bf16 [B, K-1, 2 KD + VD].
+    Returns (out, state_out, conv_out); state_out / conv_out may be the inputs (in place)."""
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
+    b, h = x.shape
+    inter = w["gate_w"].shape[0]
+    kconv = w["conv_w"].shape[1]
+    ws = workspace if workspace is not None else gdn_workspace(b, h, num_k_heads, num_v_heads, inter, x.device)
+    o = torch.empty_like(x) if out is None else out
+    so = torch.empty_like(state_in) if state_out is None else state_out
+    co = torch.empty_like(conv_in) if conv_out is None else conv_out
+    args = _weights(w, GDN_WEIGHTS) + _weights(w, MLP_WEIGHTS)
+    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args)
+    ptrs = [t.data_ptr() for t in args]
+    # the C order: x, ln1 .. s_out, ln2, MLP, state_in, conv_in, out, state_out, conv_out
+    _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
+              so.data_ptr(), co.data_ptr(), b, h, num_k_heads, num_v_heads, 128, kconv, inter, eps, ws.data_ptr(),
+              ws.numel(), _lib.stream_of(x))
+    return o, so, co
+
+
+def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Tensor, kv_cache: torch.Tensor,
+                      indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
+                      cache_location: torch.Tensor, num_qo_heads: int, rot: int, eps: float = 1e-6,
+                      sm_scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x bf16 [B, hidden]; kv_cache bf16 [P, 2, page, HKV, D] written in place at cache_location (int32 [B, 2]);
+    the page table describes each sequence including the new token; cos, sin bf16 [B, rot/2]."""
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
+    b, h = x.shape
+    pages, two, page, hkv, d = kv_cache.shape
+    inter = w["gate_w"].shape[0]
+    ws = workspace if workspace is not None else attn_workspace(b, h, num_qo_heads, hkv, d, inter, x.device)
+    o = torch.empty_like(x) if out is None else out
+    scale = d ** -0.5 if sm_scale is None else sm_scale
+    wa = _weights(w, ATTN_WEIGHTS)
+    mlp = _weights(w, MLP_WEIGHTS)
+    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp)
+    (ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, w_o, s_o, ln2) = wa
+    _lib.call("axk_attn_layer_decode", x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(), w_k.data_ptr(),
+              s_k.data_ptr(), w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
+              _lib.ptr(cos), _lib.ptr(sin), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
+              last_page_len.data_ptr(), cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(),
+              *[t.data_ptr() for t in mlp], o.data_ptr(), b, h, num_qo_heads, hkv, d, rot, page, pages, inter, eps,
+              scale, ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    return o

@@ -34,6 +34,7 @@ struct GdnArgs {
   float* state_out;       // [B, NV, DK, DV] (may alias state_in)
   uint16_t* out;          // [B, T, NV, DV] bf16
   int B, T, NK, NV;
+  int64_t ldq, ldk, ldv, ldab;  // elements between consecutive (sequence, token) rows of q, k, v, a / b
 };
 
 __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
@@ -63,18 +64,19 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
     // ---- q / k L2 norm (threads 0..127 own one element of each) ----
     float kx = 0.f, qx = 0.f;
     if (tid < kDK) {
-      kx = bf16_bits_to_f32(p.k[(tok * p.NK + kh) * kDK + tid]);
-      qx = bf16_bits_to_f32(p.q[(tok * p.NK + kh) * kDK + tid]);
+      kx = bf16_bits_to_f32(p.k[tok * p.ldk + kh * kDK + tid]);
+      qx = bf16_bits_to_f32(p.q[tok * p.ldq + kh * kDK + tid]);
     }
     float ks = wave_sum(kx * kx), qs = wave_sum(qx * qx);
     if (lane == 0 && wave < 2) {
       s_norm[wave] = ks;
       s_norm[2 + wave] = qs;
     }
-    const int64_t vh = tok * p.NV + h;
-    const float a = bf16_bits_to_f32(p.a[vh]), bb = bf16_bits_to_f32(p.b[vh]);
-    const float4 vv = make_float4(bf16_bits_to_f32(p.v[vh * kDV + c0]), bf16_bits_to_f32(p.v[vh * kDV + c0 + 1]),
-                                  bf16_bits_to_f32(p.v[vh * kDV + c0 + 2]), bf16_bits_to_f32(p.v[vh * kDV + c0 + 3]));
+    const int64_t vh = tok * p.NV + h;  // output row
+    const float a = bf16_bits_to_f32(p.a[tok * p.ldab + h]), bb = bf16_bits_to_f32(p.b[tok * p.ldab + h]);
+    const uint16_t* vr = p.v + tok * p.ldv + h * kDV + c0;
+    const float4 vv = make_float4(bf16_bits_to_f32(vr[0]), bf16_bits_to_f32(vr[1]), bf16_bits_to_f32(vr[2]),
+                                  bf16_bits_to_f32(vr[3]));
     __syncthreads();
     if (tid < kDK) {
       const float kn = sqrtf(s_norm[0] + s_norm[1] + 1e-6f), qn = sqrtf(s_norm[2] + s_norm[3] + 1e-6f);
@@ -138,15 +140,17 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
 
 }  // namespace
 
-extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
-                                 const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
-                                 float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
-                                 int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream) {
+int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                              const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                              float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                              int64_t num_v_heads, const AxkGdnStrides& ld, hipStream_t stream) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
-  AXK_REQUIRE(head_k_dim == kDK && head_v_dim == kDV, AXK_E_SHAPE);
   AXK_REQUIRE(batch > 0 && tokens > 0 && num_k_heads > 0 && num_v_heads > 0, AXK_E_SHAPE);
   AXK_REQUIRE(num_v_heads % num_k_heads == 0, AXK_E_SHAPE);
   AXK_REQUIRE(batch * num_v_heads <= INT32_MAX && tokens <= INT32_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(ld.q >= num_k_heads * kDK && ld.k >= num_k_heads * kDK && ld.v >= num_v_heads * kDV &&
+                  ld.ab >= num_v_heads,
+              AXK_E_SHAPE);
   AXK_REQUIRE(axk_aligned(state_in, 16) && axk_aligned(state_out, 16), AXK_E_ALIGN);
   const size_t sbytes = (size_t)batch * num_v_heads * kDK * kDV * 4;
   // in place is allowed (each workgroup reads its whole tile before writing it); partial overlap is not
@@ -154,8 +158,17 @@ extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uin
   const size_t obytes = (size_t)batch * tokens * num_v_heads * kDV * 2;
   AXK_REQUIRE(!axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
   GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
-            (int)num_v_heads};
-  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0,
-                     axk_stream(stream), p);
+            (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab};
+  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
   return axk_launch_status();
+}
+
+extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                 const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                                 float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                                 int64_t num_v_heads, int64_t head_k_dim, int64_t head_v_dim, axk_stream_t stream) {
+  AXK_REQUIRE(head_k_dim == kDK && head_v_dim == kDV, AXK_E_SHAPE);
+  const AxkGdnStrides ld{num_k_heads * kDK, num_k_heads * kDK, num_v_heads * kDV, num_v_heads};
+  return axk_gdn_recurrent_strided(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens,
+                                   num_k_heads, num_v_heads, ld, axk_stream(stream));
 }

@@ -1,0 +1,208 @@
+// One hybrid decode layer per call, composed from the library's kernels on the caller's stream: the GDN layer
+// (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py gdn_layer 149-183) and the attention layer (attn_block 186-280),
+// each followed by the MLP block (mlp_block 118-142). Projections of the attention / GDN paths are FP8 E4M3 with
+// per-output-channel fp32 scales; the MLP is MXFP4 (the config of the hybrid decode group). Every intermediate is
+// a bf16 tensor in the caller's workspace, rounded where the reference rounds (each projection's output, each
+// glue op's output). No allocation, no host synchronisation: a layer is graph-capturable.
+#include "axk_host.h"
+
+namespace {
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Carves consecutive 256-byte aligned buffers out of a workspace (or, with base == nullptr, only sizes them).
+struct Carver {
+  unsigned char* base;
+  size_t off = 0;
+  template <typename T>
+  T* take(size_t count) {
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off = al256(off + count * sizeof(T));
+    return p;
+  }
+};
+
+struct MlpWeights {
+  const uint8_t *gate_w, *gate_s, *up_w, *up_s, *down_w, *down_s;
+};
+
+struct MlpBufs {
+  uint16_t *x1, *h2, *g, *u, *act, *d;
+};
+
+MlpBufs carve_mlp(Carver& c, int64_t B, int64_t H, int64_t F) {
+  MlpBufs m;
+  m.x1 = c.take<uint16_t>(B * H);
+  m.h2 = c.take<uint16_t>(B * H);
+  m.g = c.take<uint16_t>(B * F);
+  m.u = c.take<uint16_t>(B * F);
+  m.act = c.take<uint16_t>(B * F);
+  m.d = c.take<uint16_t>(B * H);
+  return m;
+}
+
+#define AXK_TRY(call)            \
+  do {                           \
+    const int rc_ = (call);      \
+    if (rc_ != AXK_OK) return rc_; \
+  } while (0)
+
+// x1 = x + y; h2 = rmsnorm(x1, ln2); out = x1 + down(silu(gate h2) * up h2)  (mlp_block, q35_step.py:118-142)
+int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const MlpWeights& w, uint16_t* out,
+                 const MlpBufs& m, int64_t B, int64_t H, int64_t F, float eps, axk_stream_t st) {
+  AXK_TRY(axk_add_rmsnorm(x, y, ln2, m.x1, m.h2, B, H, eps, st));
+  AXK_TRY(axk_mxfp4_gemm(m.h2, H, w.gate_w, w.gate_s, nullptr, m.g, AXK_DT_BF16, B, F, H, st));
+  AXK_TRY(axk_mxfp4_gemm(m.h2, H, w.up_w, w.up_s, nullptr, m.u, AXK_DT_BF16, B, F, H, st));
+  AXK_TRY(axk_silu_mul(m.g, m.u, m.act, B, F, st));
+  AXK_TRY(axk_mxfp4_gemm(m.act, F, w.down_w, w.down_s, nullptr, m.d, AXK_DT_BF16, B, H, F, st));
+  return axk_add(m.x1, m.d, out, B, H, st);
+}
+
+int fp8_proj(const uint16_t* a, int64_t lda, const uint8_t* w, const float* s, uint16_t* out, int64_t m, int64_t n,
+             int64_t k, axk_stream_t st) {
+  return axk_fp8_gemm(a, lda, w, nullptr, s, nullptr, out, AXK_DT_BF16, m, n, k, st);
+}
+
+struct GdnBufs {
+  uint16_t *h, *qkv, *z, *bb, *aa, *mixed, *core, *gated, *y;
+  MlpBufs mlp;
+};
+
+GdnBufs carve_gdn(Carver& c, int64_t B, int64_t H, int64_t NK, int64_t NV, int64_t DH, int64_t F) {
+  const int64_t KD = NK * DH, VD = NV * DH, C = 2 * KD + VD;
+  GdnBufs g;
+  g.h = c.take<uint16_t>(B * H);
+  g.qkv = c.take<uint16_t>(B * C);
+  g.z = c.take<uint16_t>(B * VD);
+  g.bb = c.take<uint16_t>(B * NV);
+  g.aa = c.take<uint16_t>(B * NV);
+  g.mixed = c.take<uint16_t>(B * C);
+  g.core = c.take<uint16_t>(B * VD);
+  g.gated = c.take<uint16_t>(B * VD);
+  g.y = c.take<uint16_t>(B * H);
+  g.mlp = carve_mlp(c, B, H, F);
+  return g;
+}
+
+struct AttnBufs {
+  uint16_t *h, *qg, *kk, *vv, *q, *k, *attn, *gated, *y;
+  void* pws;
+  size_t pws_bytes;
+  MlpBufs mlp;
+};
+
+AttnBufs carve_attn(Carver& c, int64_t B, int64_t H, int64_t HQ, int64_t HKV, int64_t D, int64_t F) {
+  AttnBufs a;
+  a.h = c.take<uint16_t>(B * H);
+  a.qg = c.take<uint16_t>(B * HQ * 2 * D);
+  a.kk = c.take<uint16_t>(B * HKV * D);
+  a.vv = c.take<uint16_t>(B * HKV * D);
+  a.q = c.take<uint16_t>(B * HQ * D);
+  a.k = c.take<uint16_t>(B * HKV * D);
+  a.attn = c.take<uint16_t>(B * HQ * D);
+  a.gated = c.take<uint16_t>(B * HQ * D);
+  a.y = c.take<uint16_t>(B * H);
+  a.pws_bytes = axk_paged_decode_workspace_size(B, HQ, HKV, D);
+  a.pws = c.take<unsigned char>(a.pws_bytes);
+  a.mlp = carve_mlp(c, B, H, F);
+  return a;
+}
+
+int check_common(int64_t B, int64_t H, int64_t F) {
+  AXK_REQUIRE(B > 0 && B <= 4096 && H > 0 && F > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(H % 256 == 0 && F % 256 == 0, AXK_E_SHAPE);  // whole MXFP4 / FP8 row segments
+  return AXK_OK;
+}
+
+}  // namespace
+
+extern "C" size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads,
+                                               int64_t num_v_heads, int64_t head_dim, int64_t inter) {
+  if (check_common(batch, hidden, inter) != AXK_OK || head_dim != 128 || num_k_heads <= 0 || num_v_heads <= 0 ||
+      num_v_heads % num_k_heads != 0)
+    return 0;
+  Carver c{nullptr};
+  carve_gdn(c, batch, hidden, num_k_heads, num_v_heads, head_dim, inter);
+  return c.off;
+}
+
+extern "C" int axk_gdn_layer_decode(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const float* s_qkv, const uint8_t* w_z,
+    const float* s_z, const uint8_t* w_b, const float* s_b, const uint8_t* w_a, const float* s_a,
+    const uint16_t* conv_w, const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out,
+    const float* s_out, const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
+    const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w, const uint8_t* mlp_down_s,
+    const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
+    int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel,
+    int64_t inter, float eps, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
+                  norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
+                  mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
+              AXK_E_NULL);
+  const size_t need = axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter);
+  AXK_REQUIRE(need > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const int64_t B = batch, H = hidden, NK = num_k_heads, NV = num_v_heads, DH = head_dim, F = inter;
+  const int64_t KD = NK * DH, VD = NV * DH, C = 2 * KD + VD;
+  Carver c{static_cast<unsigned char*>(workspace)};
+  const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
+  const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
+  AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
+  AXK_TRY(fp8_proj(g.h, H, w_qkv, s_qkv, g.qkv, B, C, H, stream));
+  AXK_TRY(fp8_proj(g.h, H, w_z, s_z, g.z, B, VD, H, stream));
+  AXK_TRY(fp8_proj(g.h, H, w_b, s_b, g.bb, B, NV, H, stream));
+  AXK_TRY(fp8_proj(g.h, H, w_a, s_a, g.aa, B, NV, H, stream));
+  AXK_TRY(axk_causal_conv1d_silu(g.qkv, conv_w, conv_in, conv_out, g.mixed, B, 1, C, conv_kernel, stream));
+  // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row
+  const AxkGdnStrides ld{C, C, C, NV};
+  AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
+                                    state_out, g.core, B, 1, NK, NV, ld, axk_stream(stream)));
+  AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, B * NV, DH, eps, stream));
+  AXK_TRY(fp8_proj(g.gated, VD, w_out, s_out, g.y, B, H, VD, stream));
+  return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
+}
+
+extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
+                                                int64_t num_kv_heads, int64_t head_dim, int64_t inter) {
+  if (check_common(batch, hidden, inter) != AXK_OK || axk_paged_decode_workspace_size(batch, num_qo_heads,
+                                                                                      num_kv_heads, head_dim) == 0)
+    return 0;
+  Carver c{nullptr};
+  carve_attn(c, batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+  return c.off;
+}
+
+extern "C" int axk_attn_layer_decode(
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const float* s_q, const uint8_t* w_k, const float* s_k,
+    const uint8_t* w_v, const float* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const float* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s, const uint8_t* mlp_up_w,
+    const uint8_t* mlp_up_s, const uint8_t* mlp_down_w, const uint8_t* mlp_down_s, uint16_t* out, int64_t batch,
+    int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
+    int64_t num_pages, int64_t inter, float eps, float sm_scale, void* workspace, size_t workspace_bytes,
+    axk_stream_t stream) {
+  AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
+                  indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
+                  mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
+              AXK_E_NULL);
+  const size_t need = axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+  AXK_REQUIRE(need > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const int64_t B = batch, H = hidden, HQ = num_qo_heads, HKV = num_kv_heads, D = head_dim, F = inter;
+  Carver c{static_cast<unsigned char*>(workspace)};
+  const AttnBufs a = carve_attn(c, B, H, HQ, HKV, D, F);
+  const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
+  AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
+  AXK_TRY(fp8_proj(a.h, H, w_q, s_q, a.qg, B, HQ * 2 * D, H, stream));  // per head [q | gate]
+  AXK_TRY(fp8_proj(a.h, H, w_k, s_k, a.kk, B, HKV * D, H, stream));
+  AXK_TRY(fp8_proj(a.h, H, w_v, s_v, a.vv, B, HKV * D, H, stream));
+  AXK_TRY(axk_qk_norm_rope(a.qg, 2 * D, q_norm, cos, sin, a.q, B, HQ, D, rot, eps, stream));
+  AXK_TRY(axk_qk_norm_rope(a.kk, D, k_norm, cos, sin, a.k, B, HKV, D, rot, eps, stream));
+  AXK_TRY(axk_paged_kv_write(a.k, a.vv, kv_cache, cache_location, B, HKV, D, page_size, num_pages, nullptr, stream));
+  AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
+                           num_pages, sm_scale, a.pws, a.pws_bytes, stream));
+  AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
+  AXK_TRY(fp8_proj(a.gated, HQ * D, w_o, s_o, a.y, B, H, HQ * D, stream));
+  return mlp_residual(x, a.y, ln2, mw, out, a.mlp, B, H, F, eps, stream);
+}

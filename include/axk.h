@@ -318,6 +318,61 @@ int axk_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t ro
 /* out = bf16(x + y): the residual add (q35_step.py:139). Contiguous [rows, n]. */
 int axk_add(const uint16_t* x, const uint16_t* y, uint16_t* out, int64_t rows, int64_t n, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Decode layers of the hybrid group (one token per sequence, `batch` sequences), composed from the kernels above
+ * on `stream`: projections FP8 E4M3 [N, K] + f32 per-output-channel scale, MLP MXFP4 (codes [N, K/2], E8M0
+ * [N, K/32]). Every intermediate lives in the caller's workspace (256-byte aligned, *_workspace_size bytes);
+ * nothing is allocated or synchronised, so a layer can be captured in a HIP graph. hidden, inter % 256 == 0.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes of axk_gdn_layer_decode (0 = unsupported shape; head_dim must be 128). */
+size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
+                                    int64_t head_dim, int64_t inter);
+
+/* The GDN layer, gdn_layer of models/qwen35_35b_a3b/src/70b0fbc/q35_step.py:149-183 (IO GDN_ORDER, :415-416):
+ *   h = rmsnorm(x, ln1); qkv, z, b, a = h W^T; mixed = conv1d_silu(qkv) (state conv_in -> conv_out);
+ *   core = GDN(q, k, v = mixed's channel ranges, a, b; state_in -> state_out);
+ *   x1 = x + (bf16(rmsnorm(core, norm_w)) * silu(z)) W_out^T; out = x1 + MLP(rmsnorm(x1, ln2)).
+ *   x, out bf16 [batch, hidden]; ln1, ln2 f32 [hidden] (1 + weight); w_qkv [2 KD + VD, hidden], w_z [VD, hidden],
+ *   w_b, w_a [num_v_heads, hidden], w_out [hidden, VD] (FP8, scales f32 [N]); conv_w bf16 [2 KD + VD, conv_kernel];
+ *   a_log, dt_bias f32 [num_v_heads]; norm_w f32 [head_dim]; MLP gate / up [inter, hidden], down [hidden, inter]
+ *   (MXFP4); state f32 [batch, num_v_heads, 128, 128] (in place allowed); conv state bf16
+ *   [batch, conv_kernel - 1, 2 KD + VD] (in place allowed). KD = num_k_heads * 128, VD = num_v_heads * 128. */
+int axk_gdn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const float* s_qkv,
+                         const uint8_t* w_z, const float* s_z, const uint8_t* w_b, const float* s_b,
+                         const uint8_t* w_a, const float* s_a, const uint16_t* conv_w, const float* a_log,
+                         const float* dt_bias, const float* norm_w, const uint8_t* w_out, const float* s_out,
+                         const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
+                         const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w,
+                         const uint8_t* mlp_down_s, const float* state_in, const uint16_t* conv_in, uint16_t* out,
+                         float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden, int64_t num_k_heads,
+                         int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+                         void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
+/* Workspace bytes of axk_attn_layer_decode (0 = unsupported shape). */
+size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
+                                     int64_t head_dim, int64_t inter);
+
+/* The attention layer, attn_block + mlp of q35_step.py:186-293 (IO ATTN_ORDER, :417-418) on the paged KV cache:
+ *   h = rmsnorm(x, ln1); [q | gate] = h W_q^T per head; q = rope(rmsnorm(q, q_norm)); k = rope(rmsnorm(h W_k^T,
+ *   k_norm)); v = h W_v^T; k, v written at cache_location; o = attention of q over each sequence's pages
+ *   (indptr / indices / last_page_len including the new token); x1 = x + (o * sigmoid(gate)) W_o^T;
+ *   out = x1 + MLP(rmsnorm(x1, ln2)).
+ *   w_q [2 D num_qo_heads, hidden], w_k, w_v [D num_kv_heads, hidden], w_o [hidden, D num_qo_heads] (FP8 + f32
+ *   scales); q_norm, k_norm f32 [D] (1 + weight); cos, sin bf16 [batch, rot / 2] (each sequence's position);
+ *   kv_cache and the page table as axk_paged_decode, cache_location as axk_paged_kv_write. */
+int axk_attn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_q, const float* s_q,
+                          const uint8_t* w_k, const float* s_k, const uint8_t* w_v, const float* s_v,
+                          const float* q_norm, const float* k_norm, const uint16_t* cos, const uint16_t* sin,
+                          uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                          const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o,
+                          const float* s_o, const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
+                          const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w,
+                          const uint8_t* mlp_down_s, uint16_t* out, int64_t batch, int64_t hidden,
+                          int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
+                          int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
+                          void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

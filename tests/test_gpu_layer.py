@@ -1,0 +1,100 @@
+"""GPU parity of whole hybrid decode layers (axk_gdn_layer_decode / axk_attn_layer_decode through the C-ABI)
+against the oracle composed of the per-op restatements.
+
+Bars:
+  * GDN layer output within the per-op bar rel 2e-2 / abs 1e-2 of the oracle;
+  * attention layer output within the reference's bar for fused (composed) layer outputs, rel 5e-2 / abs 0.0625
+    (models/qwen35_35b_a3b/sgl/tests/test_gdn_attn.py:354, 517, 537): the attention kernel multiplies P in bf16
+    (as the reference's own attention does) against an fp32 SDPA golden, and that difference passes through the
+    o projection, the residual, the RMSNorm and the MLP (each of those ops meets the per-op bar in its own test);
+  * the GDN state within the reference's temporal tolerance rel 5e-2 / abs 3e-3 (test_gdn_attn.py:711-712); the
+    conv state exact (it holds inputs); the KV rows written within the per-op bar, every other cache byte untouched.
+"""
+import pytest
+import torch
+
+from axk import configs, layer
+from oracle import layer as olayer
+
+pytestmark = pytest.mark.gpu
+TOL = dict(rtol=2e-2, atol=1e-2)
+FUSED_TOL = dict(rtol=5e-2, atol=0.0625)
+STATE_TOL = dict(rtol=5e-2, atol=3e-3)
+H, F = 256, 512
+
+
+def _dev(w, dev):
+    return {k: v.to(dev) for k, v in w.items()}
+
+
+def _gdn_case(seed, b=3, nk=2, nv=4):
+    g = torch.Generator().manual_seed(seed)
+    w = configs.gdn_layer_weights(g, H, F, nk, nv)
+    x = torch.randn(b, H, generator=g).bfloat16()
+    st = torch.randn(b, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(b, 3, 2 * nk * 128 + nv * 128, generator=g).bfloat16()
+    return w, x, st, cv
+
+
+@pytest.mark.parametrize("b,nk,nv", [(3, 2, 4), (1, 1, 2), (8, 2, 2)])
+def test_gdn_layer_decode(dev, b, nk, nv):
+    w, x, st, cv = _gdn_case(b + nk + nv, b, nk, nv)
+    out, so, co = layer.gdn_layer_decode(x.to(dev), _dev(w, dev), st.to(dev), cv.to(dev), nk, nv)
+    ro, rs, rc = olayer.gdn_layer_decode(x, w, st, cv, nk, nv)
+    torch.testing.assert_close(out.float().cpu(), ro.float(), **TOL)
+    torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
+    assert torch.equal(co.cpu(), rc)
+
+
+def test_gdn_layer_two_steps_in_place(dev):
+    w, x, st, cv = _gdn_case(11)
+    x2 = torch.randn(3, H, generator=torch.Generator().manual_seed(12)).bfloat16()
+    wd, sd, cd = _dev(w, dev), st.to(dev), cv.to(dev)
+    ws = layer.gdn_workspace(3, H, 2, 4, F, dev)
+    o1, _, _ = layer.gdn_layer_decode(x.to(dev), wd, sd, cd, 2, 4, workspace=ws, state_out=sd, conv_out=cd)
+    o2, _, _ = layer.gdn_layer_decode(x2.to(dev), wd, sd, cd, 2, 4, workspace=ws, state_out=sd, conv_out=cd)
+    r1, rs, rc = olayer.gdn_layer_decode(x, w, st, cv, 2, 4)
+    r2, rs, rc = olayer.gdn_layer_decode(x2, w, rs, rc, 2, 4)
+    torch.testing.assert_close(o1.float().cpu(), r1.float(), **TOL)
+    torch.testing.assert_close(o2.float().cpu(), r2.float(), **TOL)
+    torch.testing.assert_close(sd.cpu(), rs, **STATE_TOL)
+    assert torch.equal(cd.cpu(), rc)
+
+
+@pytest.mark.parametrize("lens,hq,hkv,rot", [([100, 64, 300], 4, 2, 64), ([1, 127], 8, 2, 64), ([640], 4, 4, 0)])
+def test_attn_layer_decode(dev, lens, hq, hkv, rot):
+    g = torch.Generator().manual_seed(len(lens) * 7 + hq)
+    d = 256
+    w = configs.attn_layer_weights(g, H, F, hq, hkv, d)
+    c = configs.append_token_case(lens, hq, hkv, d, 64, g)
+    x = torch.randn(len(lens), H, generator=g).bfloat16()
+    cos, sin = olayer.rope_cos_sin(c["pos"], max(rot, 2), 10_000_000.0)
+    cos, sin = cos[:, : rot // 2].contiguous(), sin[:, : rot // 2].contiguous()
+    cache = c["cache"].to(dev)
+    out = layer.attn_layer_decode(x.to(dev), _dev(w, dev), cos.to(dev), sin.to(dev), cache, c["indptr"].to(dev),
+                                  c["indices"].to(dev), c["last_page_len"].to(dev), c["loc"].to(dev), hq, rot)
+    ro, rcache = olayer.attn_layer_decode(x, w, cos, sin, c["cache"], c["indptr"], c["indices"], c["last_page_len"],
+                                          c["loc"], hq, rot)
+    torch.testing.assert_close(out.float().cpu(), ro.float(), **FUSED_TOL)
+    got = cache.cpu()
+    written = torch.zeros(got.shape[0], got.shape[2], dtype=torch.bool)
+    for p, o in c["loc"].tolist():
+        written[p, o] = True
+    torch.testing.assert_close(got.permute(0, 2, 1, 3, 4)[written].float(),
+                               rcache.permute(0, 2, 1, 3, 4)[written].float(), **TOL)
+    assert torch.equal(got.permute(0, 2, 1, 3, 4)[~written].view(torch.int16),
+                       c["cache"].permute(0, 2, 1, 3, 4)[~written].view(torch.int16))
+
+
+def test_layer_contract_errors(dev):
+    from axk import _lib
+
+    w, x, st, cv = _gdn_case(3)
+    wd = _dev(w, dev)
+    with pytest.raises(_lib.AxkError):  # workspace too small
+        layer.gdn_layer_decode(x.to(dev), wd, st.to(dev), cv.to(dev), 2, 4,
+                               workspace=torch.empty(256, dtype=torch.uint8, device=dev))
+    with pytest.raises(ValueError):
+        bad = dict(wd)
+        bad.pop("norm_w")
+        layer.gdn_layer_decode(x.to(dev), bad, st.to(dev), cv.to(dev), 2, 4)
