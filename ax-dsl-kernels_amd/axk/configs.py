@@ -200,3 +200,89 @@ def append_token_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Gener
              last_page_len=torch.tensor(new_last, dtype=torch.int32), lens=[L + 1 for L in lens],
              loc=torch.tensor(loc, dtype=torch.int32), pos=torch.tensor(list(lens)))
     return c
+
+
+# Config 4: the 16-layer hybrid decode group (GDN, GDN, GDN, attention) x 4 of BASELINE.json configs[4].
+CONFIG4 = dict(batch=8, ctx=131072, hidden=4096, inter=12288, hq=32, hkv=4, d=256, rot=64, nk=16, nv=32, conv=4,
+               page=64, theta=10_000_000.0, eps=1e-6, pattern="gggagggagggaggga")
+
+
+def config4_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None = None) -> dict:
+    """The group's weights, states, paged KV caches and page table, generated ON THE DEVICE by a seeded device
+    generator (about 20 GB: the KV of 4 attention layers at 131,072 tokens per sequence). Distributions as the
+    small-shape generators: FP8 projections N(0, 0.5) with scales U(1, 3) / sqrt(K), MXFP4 nibbles uniform with
+    exponent bytes 119..123, norms 1 + N(0, 0.1), KV ~ N(0, 1) bf16, GDN state ~ N(0, 0.02), x ~ N(0, 1).
+    Every sequence holds ctx tokens; the step's new token is position ctx (a fresh page per sequence)."""
+    c4 = dict(CONFIG4)
+    if ctx is not None:
+        c4["ctx"] = ctx
+    if batch is not None:
+        c4["batch"] = batch
+    b, h, f, d, hkv, page = c4["batch"], c4["hidden"], c4["inter"], c4["d"], c4["hkv"], c4["page"]
+    nk, nv, hq = c4["nk"], c4["nv"], c4["hq"]
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def fp8(n, k):
+        w = (torch.randn(n, k, generator=g, device=dev) * 0.5).to(torch.float8_e4m3fn).view(torch.uint8)
+        return w.contiguous(), (torch.rand(n, generator=g, device=dev) * 2 + 1) / (k ** 0.5)
+
+    def mx(n, k):
+        codes = torch.randint(0, 256, (n, k // 2), generator=g, device=dev, dtype=torch.uint8)
+        scales = torch.randint(119, 124, (n, k // 32), generator=g, device=dev, dtype=torch.uint8)
+        return codes, scales
+
+    def norm(n):
+        return 1.0 + 0.1 * torch.randn(n, generator=g, device=dev)
+
+    def mlp():
+        w = {}
+        w["gate_w"], w["gate_s"] = mx(f, h)
+        w["up_w"], w["up_s"] = mx(f, h)
+        w["down_w"], w["down_s"] = mx(h, f)
+        return w
+
+    kd, vd = nk * 128, nv * 128
+    pages_per_seq = c4["ctx"] // page + 1  # + the new token's page (ctx is a multiple of the page)
+    pool = b * pages_per_seq
+    perm = torch.randperm(pool, generator=g, device=dev).to(torch.int32)
+    indptr = (torch.arange(b + 1, device=dev, dtype=torch.int32) * pages_per_seq).contiguous()
+    last = torch.full((b,), c4["ctx"] % page + 1, dtype=torch.int32, device=dev)
+    loc = torch.stack([perm[indptr[1:].long() - 1], torch.full((b,), c4["ctx"] % page, dtype=torch.int32,
+                                                               device=dev)], 1).to(torch.int32).contiguous()
+    layers = []
+    for kind in c4["pattern"]:
+        if kind == "g":
+            w = {"ln1": norm(h)}
+            w["w_qkv"], w["s_qkv"] = fp8(2 * kd + vd, h)
+            w["w_z"], w["s_z"] = fp8(vd, h)
+            w["w_b"], w["s_b"] = fp8(nv, h)
+            w["w_a"], w["s_a"] = fp8(nv, h)
+            w["conv_w"] = (torch.randn(2 * kd + vd, c4["conv"], generator=g, device=dev) * 0.5).to(torch.bfloat16)
+            w["a_log"] = torch.randn(nv, generator=g, device=dev) * 0.5
+            w["dt_bias"] = torch.randn(nv, generator=g, device=dev) * 0.5
+            w["norm_w"] = norm(128)
+            w["w_out"], w["s_out"] = fp8(h, vd)
+            w["ln2"] = norm(h)
+            w.update(mlp())
+            st = torch.randn(b, nv, 128, 128, generator=g, device=dev) * 0.02
+            cv = torch.randn(b, c4["conv"] - 1, 2 * kd + vd, generator=g, device=dev).to(torch.bfloat16)
+            layers.append({"kind": "g", "w": w, "state": st, "conv": cv})
+        else:
+            w = {"ln1": norm(h)}
+            w["w_q"], w["s_q"] = fp8(hq * 2 * d, h)
+            w["w_k"], w["s_k"] = fp8(hkv * d, h)
+            w["w_v"], w["s_v"] = fp8(hkv * d, h)
+            w["q_norm"] = norm(d)
+            w["k_norm"] = norm(d)
+            w["w_o"], w["s_o"] = fp8(h, hq * d)
+            w["ln2"] = norm(h)
+            w.update(mlp())
+            cache = torch.randn(pool, 2, page, hkv, d, generator=g, device=dev, dtype=torch.bfloat16)
+            layers.append({"kind": "a", "w": w, "cache": cache})
+    inv = 1.0 / (c4["theta"] ** (torch.arange(0, c4["rot"], 2, dtype=torch.int64).float() / c4["rot"]))
+    fpos = float(c4["ctx"]) * inv
+    cos = fpos.cos().bfloat16().reshape(1, -1).repeat(b, 1).to(dev).contiguous()
+    sin = fpos.sin().bfloat16().reshape(1, -1).repeat(b, 1).to(dev).contiguous()
+    x = torch.randn(b, h, generator=g, device=dev).to(torch.bfloat16)
+    return {"cfg": c4, "layers": layers, "indptr": indptr, "indices": perm, "last_page_len": last, "loc": loc,
+            "cos": cos, "sin": sin, "x": x}
