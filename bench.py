@@ -578,6 +578,7 @@ class GroupDecodeWorkload(Workload):
     name = "group_decode"
     kernel = "hybrid decode group (16 layers)"
     timing = "graph"
+    traffic_profile = "group_decode_config4_pmc.txt"
 
     def __init__(self, dev):
         import torch
