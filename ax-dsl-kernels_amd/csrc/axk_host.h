@@ -36,3 +36,26 @@ __attribute__((visibility("hidden"))) int axk_gdn_recurrent_strided(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
     const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
     int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, hipStream_t stream);
+
+// Internal (not exported): one launch of up to AXK_MX_GROUP_MAX weight matrices that share the activations a
+// [m, k] (the projections of one decode layer). Matrix i: weights w [n, k] (FP8 bytes, or MXFP4 codes with E8M0
+// scales ws [n, k/32]), optional per-channel scale and bias, output out [m, n] with leading dimension ldo.
+// epi: AXK_MX_EPI_PLAIN; AXK_MX_EPI_SWIGLU (mats[0] gate, mats[1] up, one shape and one out:
+// out = bf16(silu(bf16 g) * bf16 u)); AXK_MX_EPI_RES (one matrix: out = bf16(res + bf16 y), res [m, n] with
+// leading dimension ldr). Rows must be whole 128-byte segments. Returns an AXK status.
+#define AXK_MX_GROUP_MAX 4
+enum { AXK_MX_EPI_PLAIN = 0, AXK_MX_EPI_SWIGLU = 1, AXK_MX_EPI_RES = 2 };
+enum { AXK_MX_MXFP4 = 0, AXK_MX_FP8 = 1 };
+struct AxkMxMat {
+  const uint8_t* w;
+  const uint8_t* ws;
+  const float* col_scale;
+  const float* bias;
+  void* out;
+  int64_t ldo;
+  int64_t n;
+};
+__attribute__((visibility("hidden"))) int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats,
+                                                       int count, int epi, const uint16_t* res, int64_t ldr,
+                                                       const float* row_scale, int out_dtype, int64_t m, int64_t k,
+                                                       hipStream_t stream);

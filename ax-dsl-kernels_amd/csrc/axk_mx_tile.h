@@ -112,67 +112,15 @@ __device__ __forceinline__ void mx_tile_accum(const uint16_t* const (&xrow)[MT],
   }
 }
 
-// Staged variant for rows whose byte length is a multiple of 128. Wave w takes the 128-byte row segments
-// d = d_begin, d_begin + d_step, ... (two chunks each) of its 16 weight rows n0 .. n0 + 15. A segment is loaded by
-// two instructions of 8 rows x 128 bytes (8 lanes per row: whole cache lines, which keeps the address path's
-// per-line work low), written to the wave's LDS tile [16 rows][kSegLd bytes] and read back in the MFMA layout
-// (lane (nl, g): unit g of each chunk), so the k mapping is the unstaged one. LDS is wave-private and in order:
-// no barrier. MXFP4 scales: the segment's eight E8M0 bytes of row nl as one 8-byte load (K % 256 == 0).
+// Staged loads (the linear kernels) read a tile's weights as 128-byte row segments, two instructions of 8 rows x
+// 128 bytes each (whole cache lines, which keeps the address path's per-line work low), through an LDS tile of
+// [16 rows][kSegLd bytes] (16 bytes of padding per row).
 constexpr int kSegBytes = 128;
 constexpr int kSegLd = kSegBytes + 16;
 
 template <int F>
 __host__ __device__ constexpr int64_t row_bytes(int64_t K) {
   return F == WF_MXFP4 ? K / 2 : (F == WF_FP8 ? K : 2 * K);
-}
-
-template <int F, int MT, int UNROLL = 2>
-__device__ __forceinline__ void mx_tile_accum_staged(const uint16_t* const (&xrow)[MT], const bool (&mvalid)[MT],
-                                                     const uint8_t* __restrict__ w, const uint8_t* __restrict__ wscale,
-                                                     int64_t n0, int64_t N, int64_t K, int64_t d_begin,
-                                                     int64_t d_step, unsigned char* tile, axk_f32x4 (&acc)[MT]) {
-  using U = WUnit<F>;
-  constexpr int CH = 4 * U::V;  // values per chunk (64 bytes of a row)
-  const int lane = threadIdx.x & 63, nl = lane & 15, g = lane >> 4, lr = lane >> 3, lc = lane & 7;
-  const int64_t rb = row_bytes<F>(K), ND = rb / kSegBytes;
-  // load lanes: instruction h reads row 8 h + lr, bytes 16 lc of the segment (rows past N re-read row N - 1)
-  const uint8_t* src[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) src[h] = w + (n0 + 8 * h + lr < N ? n0 + 8 * h + lr : N - 1) * rb + 16 * lc;
-  const uint8_t* srow = F == WF_MXFP4 ? wscale + (n0 + nl < N ? n0 + nl : N - 1) * (K / 32) : nullptr;
-  for (int64_t d0 = d_begin; d0 < ND; d0 += d_step * UNROLL) {
-    axk_u32x4 q[UNROLL][2];
-    uint2 sw[UNROLL];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {  // unconditional (clamped) loads: every wait stays exact
-      const int64_t d = d0 + u * d_step < ND ? d0 + u * d_step : ND - 1;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) q[u][h] = *reinterpret_cast<const axk_u32x4*>(src[h] + d * kSegBytes);
-      if (F == WF_MXFP4) sw[u] = *reinterpret_cast<const uint2*>(srow + 8 * d);
-    }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int64_t d = d0 + u * d_step;
-      if (d >= ND) break;  // uniform
-#pragma unroll
-      for (int h = 0; h < 2; ++h) *reinterpret_cast<axk_u32x4*>(tile + (8 * h + lr) * kSegLd + 16 * lc) = q[u][h];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint4 unit = __builtin_bit_cast(uint4, *reinterpret_cast<const axk_u32x4*>(tile + nl * kSegLd + 64 * j + 16 * g));
-        const int64_t kb = (2 * d + j) * CH + g * U::V;
-        const float sc = F == WF_MXFP4 ? e8m0_to_f32((((j ? sw[u].y : sw[u].x)) >> (8 * g)) & 0xffu) : 1.0f;
-#pragma unroll
-        for (int s = 0; s < U::STEPS; ++s) {
-          const axk_bf16x8 b = U::conv(unit, s, sc);
-#pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            const axk_bf16x8 a = mvalid[t] ? load_bf16x8(xrow[t] + kb + 8 * s) : zero_bf16x8();
-            acc[t] = mfma_bf16_16x16x32(a, b, acc[t]);
-          }
-        }
-      }
-    }
-  }
 }
 
 }  // namespace axk

@@ -3,7 +3,10 @@
 // each followed by the MLP block (mlp_block 118-142). Projections of the attention / GDN paths are FP8 E4M3 with
 // per-output-channel fp32 scales; the MLP is MXFP4 (the config of the hybrid decode group). Every intermediate is
 // a bf16 tensor in the caller's workspace, rounded where the reference rounds (each projection's output, each
-// glue op's output). No allocation, no host synchronisation: a layer is graph-capturable.
+// glue op's output). Projections that share an input run as one grouped launch (GDN: qkv | z | b | a; attention:
+// q | k | v); the MLP's gate and up projections run as one launch whose epilogue applies SwiGLU, and the down
+// projection's epilogue adds the residual (both round exactly where the separate ops round). No allocation, no
+// host synchronisation: a layer is graph-capturable.
 #include "axk_host.h"
 
 namespace {
@@ -27,17 +30,14 @@ struct MlpWeights {
 };
 
 struct MlpBufs {
-  uint16_t *x1, *h2, *g, *u, *act, *d;
+  uint16_t *x1, *h2, *act;
 };
 
 MlpBufs carve_mlp(Carver& c, int64_t B, int64_t H, int64_t F) {
   MlpBufs m;
   m.x1 = c.take<uint16_t>(B * H);
   m.h2 = c.take<uint16_t>(B * H);
-  m.g = c.take<uint16_t>(B * F);
-  m.u = c.take<uint16_t>(B * F);
   m.act = c.take<uint16_t>(B * F);
-  m.d = c.take<uint16_t>(B * H);
   return m;
 }
 
@@ -47,20 +47,29 @@ MlpBufs carve_mlp(Carver& c, int64_t B, int64_t H, int64_t F) {
     if (rc_ != AXK_OK) return rc_; \
   } while (0)
 
-// x1 = x + y; h2 = rmsnorm(x1, ln2); out = x1 + down(silu(gate h2) * up h2)  (mlp_block, q35_step.py:118-142)
+// x1 = x + y; h2 = rmsnorm(x1, ln2); out = x1 + down(silu(gate h2) * up h2)  (mlp_block, q35_step.py:118-142):
+// three launches (the norm, gate | up with SwiGLU, down with the residual add).
 int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const MlpWeights& w, uint16_t* out,
                  const MlpBufs& m, int64_t B, int64_t H, int64_t F, float eps, axk_stream_t st) {
   AXK_TRY(axk_add_rmsnorm(x, y, ln2, m.x1, m.h2, B, H, eps, st));
-  AXK_TRY(axk_mxfp4_gemm(m.h2, H, w.gate_w, w.gate_s, nullptr, m.g, AXK_DT_BF16, B, F, H, st));
-  AXK_TRY(axk_mxfp4_gemm(m.h2, H, w.up_w, w.up_s, nullptr, m.u, AXK_DT_BF16, B, F, H, st));
-  AXK_TRY(axk_silu_mul(m.g, m.u, m.act, B, F, st));
-  AXK_TRY(axk_mxfp4_gemm(m.act, F, w.down_w, w.down_s, nullptr, m.d, AXK_DT_BF16, B, H, F, st));
-  return axk_add(m.x1, m.d, out, B, H, st);
+  const AxkMxMat gate_up[2] = {{w.gate_w, w.gate_s, nullptr, nullptr, m.act, F, F},
+                               {w.up_w, w.up_s, nullptr, nullptr, m.act, F, F}};
+  AXK_TRY(axk_mx_group(AXK_MX_MXFP4, m.h2, H, gate_up, 2, AXK_MX_EPI_SWIGLU, nullptr, 0, nullptr, AXK_DT_BF16, B, H,
+                       axk_stream(st)));
+  const AxkMxMat down{w.down_w, w.down_s, nullptr, nullptr, out, H, H};
+  return axk_mx_group(AXK_MX_MXFP4, m.act, F, &down, 1, AXK_MX_EPI_RES, m.x1, H, nullptr, AXK_DT_BF16, B, F,
+                      axk_stream(st));
 }
 
-int fp8_proj(const uint16_t* a, int64_t lda, const uint8_t* w, const float* s, uint16_t* out, int64_t m, int64_t n,
-             int64_t k, axk_stream_t st) {
-  return axk_fp8_gemm(a, lda, w, nullptr, s, nullptr, out, AXK_DT_BF16, m, n, k, st);
+// FP8 projections of one input a [m, k] (bf16 outputs, per-channel scales) as one grouped launch.
+int fp8_projs(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int64_t m, int64_t k,
+              axk_stream_t st) {
+  return axk_mx_group(AXK_MX_FP8, a, lda, mats, count, AXK_MX_EPI_PLAIN, nullptr, 0, nullptr, AXK_DT_BF16, m, k,
+                      axk_stream(st));
+}
+
+AxkMxMat fp8_mat(const uint8_t* w, const float* s, uint16_t* out, int64_t n) {
+  return AxkMxMat{w, nullptr, s, nullptr, out, n, n};
 }
 
 struct GdnBufs {
@@ -148,17 +157,17 @@ extern "C" int axk_gdn_layer_decode(
   const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
   const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
   AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
-  AXK_TRY(fp8_proj(g.h, H, w_qkv, s_qkv, g.qkv, B, C, H, stream));
-  AXK_TRY(fp8_proj(g.h, H, w_z, s_z, g.z, B, VD, H, stream));
-  AXK_TRY(fp8_proj(g.h, H, w_b, s_b, g.bb, B, NV, H, stream));
-  AXK_TRY(fp8_proj(g.h, H, w_a, s_a, g.aa, B, NV, H, stream));
+  const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.qkv, C), fp8_mat(w_z, s_z, g.z, VD), fp8_mat(w_b, s_b, g.bb, NV),
+                            fp8_mat(w_a, s_a, g.aa, NV)};
+  AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream));
   AXK_TRY(axk_causal_conv1d_silu(g.qkv, conv_w, conv_in, conv_out, g.mixed, B, 1, C, conv_kernel, stream));
   // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row
   const AxkGdnStrides ld{C, C, C, NV};
   AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
                                     state_out, g.core, B, 1, NK, NV, ld, axk_stream(stream)));
   AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, B * NV, DH, eps, stream));
-  AXK_TRY(fp8_proj(g.gated, VD, w_out, s_out, g.y, B, H, VD, stream));
+  const AxkMxMat o = fp8_mat(w_out, s_out, g.y, H);
+  AXK_TRY(fp8_projs(g.gated, VD, &o, 1, B, VD, stream));
   return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
 }
 
@@ -194,15 +203,16 @@ extern "C" int axk_attn_layer_decode(
   const AttnBufs a = carve_attn(c, B, H, HQ, HKV, D, F);
   const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
   AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
-  AXK_TRY(fp8_proj(a.h, H, w_q, s_q, a.qg, B, HQ * 2 * D, H, stream));  // per head [q | gate]
-  AXK_TRY(fp8_proj(a.h, H, w_k, s_k, a.kk, B, HKV * D, H, stream));
-  AXK_TRY(fp8_proj(a.h, H, w_v, s_v, a.vv, B, HKV * D, H, stream));
+  const AxkMxMat proj[3] = {fp8_mat(w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
+                            fp8_mat(w_k, s_k, a.kk, HKV * D), fp8_mat(w_v, s_v, a.vv, HKV * D)};
+  AXK_TRY(fp8_projs(a.h, H, proj, 3, B, H, stream));
   AXK_TRY(axk_qk_norm_rope(a.qg, 2 * D, q_norm, cos, sin, a.q, B, HQ, D, rot, eps, stream));
   AXK_TRY(axk_qk_norm_rope(a.kk, D, k_norm, cos, sin, a.k, B, HKV, D, rot, eps, stream));
   AXK_TRY(axk_paged_kv_write(a.k, a.vv, kv_cache, cache_location, B, HKV, D, page_size, num_pages, nullptr, stream));
   AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
                            num_pages, sm_scale, a.pws, a.pws_bytes, stream));
   AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
-  AXK_TRY(fp8_proj(a.gated, HQ * D, w_o, s_o, a.y, B, H, HQ * D, stream));
+  const AxkMxMat o = fp8_mat(w_o, s_o, a.y, H);
+  AXK_TRY(fp8_projs(a.gated, HQ * D, &o, 1, B, HQ * D, stream));
   return mlp_residual(x, a.y, ln2, mw, out, a.mlp, B, H, F, eps, stream);
 }

@@ -2,17 +2,22 @@
 //
 // Decode-shaped projections (m <= 32 rows per launch tile) are pure weight streaming: every weight
 // byte is read once, so the kernel is bound by HBM bandwidth. The design:
-//   * a workgroup owns 16 output channels (one MFMA N tile) and splits K across its waves;
-//   * each lane streams one 16-byte weight unit per chunk with a single 128-bit load
-//     (MXFP4: 32 codes = exactly one E8M0 block; FP8: 16 values; bf16: 8 values), so the
-//     16 lanes of an N tile x 4 K-groups read 4 x 64 contiguous bytes per row;
+//   * a 16-row weight tile is one MFMA N tile; a workgroup holds NT tiles (one or two) and splits K across
+//     its waves in 128-byte row segments, so each activation fragment a wave loads feeds NT tiles;
+//   * a segment of a tile is read as two instructions of 8 rows x 128 bytes (whole cache lines), staged
+//     through a wave-private LDS tile and read back in the MFMA layout (rows whose byte length is not a
+//     multiple of 128 take an unstaged kernel that loads one 16-byte unit per lane);
 //   * the unit is dequantised in registers to bf16 (gfx950 scaled FP4/FP8 converts; exact, since
 //     E2M1 x 2^e and E4M3 values are representable in bf16) and fed to
 //     v_mfma_f32_16x16x32_bf16 with the activations as the A operand (fp32 accumulation);
 //   * per-wave partial tiles are summed through LDS and the epilogue applies row/column scales
 //     and bias, rounding once to the output dtype.
+// One launch may cover a group of up to four weight matrices that share the activations (the projections of
+// one decode layer): their tiles are laid end to end. Two fused epilogues serve the MLP: SwiGLU (a gate and an
+// up matrix of one shape, out = bf16(silu(bf16 g) * bf16 u)) and the residual add (out = bf16(res + bf16 y)),
+// each rounding exactly where the separate ops round.
 // Reference semantics: sgl_kernel_axera/gemm.py:564-641 (mx_gemm_kernel, mxfp4_gemm),
-// gemm.py:119-181 (scaled GEMM), q35_mx_build.py:100-115 (proj_mx).
+// gemm.py:119-181 (scaled GEMM), q35_mx_build.py:100-115 (proj_mx), q35_step.py:118-142 (mlp_block).
 #include "axk_common.h"
 #include "axk_host.h"
 #include "axk_mx_tile.h"
@@ -24,14 +29,16 @@ using axk::WF_FP8;
 using axk::WF_MXFP4;
 using axk::WUnit;
 
-constexpr int kMaxWaves = 16;
+constexpr int kMaxWaves = 16;  // unstaged kernel
+constexpr int kGroupWaves = 8;  // group kernel: waves per workgroup (at most)
+constexpr int kGroupMaxNT = 2;  // group kernel: N tiles per workgroup (at most)
 
-// One workgroup: output channels [16*blockIdx.x, +16) x rows [32*blockIdx.y... ) in MT tiles of 16.
-// Lane l: N column nl = l % 16, K group g = l / 16. Chunk c covers K [c*4V, (c+1)*4V); the lane's
-// unit inside it is [c*4V + g*V, +V). MFMA step s uses k = unit + 8s .. +8 for both operands.
-// STAGE: the weights are read as whole 128-byte row segments through a wave-private LDS tile
-// (axk::mx_tile_accum_staged); wave w takes segments w, w + nwaves, ...
-template <int F, int MT, bool STAGE>
+enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_RES = 2 };
+
+// Unstaged kernel, for rows whose byte length is not a multiple of 128. One workgroup: output channels
+// [16*blockIdx.x, +16) x rows [16*MT*blockIdx.y, ...) in MT tiles of 16. Lane l: N column nl = l % 16, K group
+// g = l / 16. Chunk c covers K [c*4V, (c+1)*4V); the lane's unit inside it is [c*4V + g*V, +V).
+template <int F, int MT>
 __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           const uint8_t* __restrict__ w,
                                                           const uint8_t* __restrict__ wscale,
@@ -39,10 +46,7 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
                                                           const float* __restrict__ col_scale,
                                                           const float* __restrict__ bias, void* __restrict__ out,
                                                           int out_f32, int M, int N, int64_t K) {
-  // the waves' staging tiles, then (after a barrier) the cross-wave partial sums
-  constexpr int kTileBytes = kMaxWaves * 16 * axk::kSegLd, kRedBytes = kMaxWaves * MT * 4 * 64 * 4;
-  __shared__ __align__(16) unsigned char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
-  float* red = reinterpret_cast<float*>(smem);
+  __shared__ __align__(16) float red[kMaxWaves * MT * 4 * 64];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
   const int nl = lane & 15;
@@ -62,13 +66,7 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
   axk_f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  if (STAGE) {
-    axk::mx_tile_accum_staged<F, MT>(xrow, mvalid, w, wscale, (int64_t)blockIdx.x * 16, N, K, wave, nwaves,
-                                     smem + wave * 16 * axk::kSegLd, acc);
-    __syncthreads();  // the staging tiles become the reduction buffer
-  } else {
-    axk::mx_tile_accum<F, MT>(xrow, mvalid, w, wscale, n, nvalid, K, wave, nwaves, acc);
-  }
+  axk::mx_tile_accum<F, MT>(xrow, mvalid, w, wscale, n, nvalid, K, wave, nwaves, acc);
 
 #pragma unroll
   for (int t = 0; t < MT; ++t)
@@ -91,6 +89,179 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
       else
         reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + nn] = (uint16_t)f32_to_bf16_bits(v);
     }
+  }
+}
+
+// A group of weight matrices sharing the activations. Matrix i owns the virtual 16-row tiles
+// [tile0[i], tile0[i + 1]); for EPI_SWIGLU matrix 0 is the gate and matrix 1 the up projection (one shape) and a
+// workgroup's tile slots alternate gate / up over the same channels.
+struct MxGroup {
+  const uint8_t* w[AXK_MX_GROUP_MAX];
+  const uint8_t* ws[AXK_MX_GROUP_MAX];
+  const float* col_scale[AXK_MX_GROUP_MAX];
+  const float* bias[AXK_MX_GROUP_MAX];
+  void* out[AXK_MX_GROUP_MAX];
+  int64_t ldo[AXK_MX_GROUP_MAX];
+  int n[AXK_MX_GROUP_MAX];
+  int tile0[AXK_MX_GROUP_MAX + 1];
+  int count;
+  const float* row_scale;
+  const uint16_t* res;  // EPI_RES: the residual [M, n] (leading dimension ldr)
+  int64_t ldr;
+  int out_f32;
+};
+
+// Matrix and local tile of workgroup slot t.
+template <int NT, int EPI>
+AXK_DEV void slot_tile(const MxGroup& g, int t, int& mi, int& lt, bool& valid) {
+  if (EPI == EPI_SWIGLU) {
+    mi = t & 1;
+    lt = (int)blockIdx.x * (NT / 2) + (t >> 1);
+    valid = lt < g.tile0[1];
+    if (!valid) lt = g.tile0[1] - 1;
+  } else {
+    int v = (int)blockIdx.x * NT + t;
+    valid = v < g.tile0[g.count];
+    if (!valid) v = g.tile0[g.count] - 1;
+    mi = 0;
+#pragma unroll
+    for (int i = 1; i < AXK_MX_GROUP_MAX; ++i) mi += (i < g.count && v >= g.tile0[i]) ? 1 : 0;
+    lt = v - g.tile0[mi];
+  }
+}
+
+// Staged group kernel: wave w takes the 128-byte row segments d = w, w + nwaves, ... of its NT tiles (rows of
+// whole segments; MXFP4 scale rows as 8-byte words). Segment d: the NT tiles' weights are loaded (two
+// instructions of 8 rows x 128 bytes per tile: rows past a matrix's end re-read its last row), then the MT
+// activation fragments, which every tile reuses; each tile goes through the wave's LDS tile into the MFMA layout
+// (lane (nl, g): 16-byte unit g of each 64-byte chunk), so the k mapping is the unstaged kernel's. LDS is
+// wave-private and in order: no barrier until the cross-wave sum.
+template <int F, int MT, int NT, int EPI>
+__global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                     const MxGroup g, int M, int64_t K) {
+  using U = axk::WUnit<F>;
+  constexpr int CH = 4 * U::V, SEGK = 2 * CH;  // values per 64-byte chunk, per 128-byte segment
+  constexpr int kTileBytes = kGroupWaves * NT * 16 * axk::kSegLd, kRedBytes = kGroupWaves * NT * MT * 4 * 64 * 4;
+  __shared__ __align__(16) unsigned char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
+  float* red = reinterpret_cast<float*>(smem);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int nl = lane & 15, kg = lane >> 4, lr = lane >> 3, lc = lane & 7;
+  const int m0 = blockIdx.y * 16 * MT;
+  const int64_t rb = axk::row_bytes<F>(K), ND = rb / axk::kSegBytes;
+  unsigned char* tile = smem + wave * NT * 16 * axk::kSegLd;
+
+  const uint16_t* xrow[MT];
+  bool mvalid[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = m0 + t * 16 + nl;
+    mvalid[t] = m < M;
+    xrow[t] = x + (int64_t)(mvalid[t] ? m : 0) * ldx;
+  }
+  const uint8_t* src[NT][2];
+  const uint8_t* srow[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int mi, lt;
+    bool valid;
+    slot_tile<NT, EPI>(g, t, mi, lt, valid);
+    const int64_t n0 = (int64_t)lt * 16, nmax = g.n[mi] - 1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r = n0 + 8 * h + lr;
+      src[t][h] = g.w[mi] + (r < nmax ? r : nmax) * rb + 16 * lc;
+    }
+    srow[t] = F == axk::WF_MXFP4 ? g.ws[mi] + (n0 + nl < nmax ? n0 + nl : nmax) * (K / 32) : nullptr;
+  }
+
+  axk_f32x4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int u = 0; u < MT; ++u) acc[t][u] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t d = wave; d < ND; d += nwaves) {
+    axk_u32x4 q[NT][2];
+    uint2 sw[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) q[t][h] = *reinterpret_cast<const axk_u32x4*>(src[t][h] + d * axk::kSegBytes);
+      if (F == axk::WF_MXFP4) sw[t] = *reinterpret_cast<const uint2*>(srow[t] + 8 * d);
+    }
+    axk_bf16x8 a[MT][2][U::STEPS];
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int s = 0; s < U::STEPS; ++s)
+          a[u][j][s] = mvalid[u] ? load_bf16x8(xrow[u] + d * SEGK + j * CH + kg * U::V + 8 * s) : zero_bf16x8();
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<axk_u32x4*>(tile + (t * 16 + 8 * h + lr) * axk::kSegLd + 16 * lc) = q[t][h];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint4 unit = __builtin_bit_cast(
+            uint4, *reinterpret_cast<const axk_u32x4*>(tile + (t * 16 + nl) * axk::kSegLd + 64 * j + 16 * kg));
+        const float sc =
+            F == axk::WF_MXFP4 ? e8m0_to_f32(((j ? sw[t].y : sw[t].x) >> (8 * kg)) & 0xffu) : 1.0f;
+#pragma unroll
+        for (int s = 0; s < U::STEPS; ++s) {
+          const axk_bf16x8 b = U::conv(unit, s, sc);
+#pragma unroll
+          for (int u = 0; u < MT; ++u) acc[t][u] = mfma_bf16_16x16x32(a[u][j][s], b, acc[t][u]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // the staging tiles become the reduction buffer
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[(((wave * NT + t) * MT + u) * 4 + r) * 64 + lane] = acc[t][u][r];
+  __syncthreads();
+
+  // element e of slot t, M tile u: row m0 + 16u + 4(l / 16) + r, channel 16 lt + l % 16
+  auto total = [&](int t, int u, int r, int l) {
+    float v = 0.f;
+    for (int wv = 0; wv < nwaves; ++wv) v += red[(((wv * NT + t) * MT + u) * 4 + r) * 64 + l];
+    return v;
+  };
+  constexpr int kOutSlots = EPI == EPI_SWIGLU ? NT / 2 : NT;
+  for (int idx = threadIdx.x; idx < kOutSlots * MT * 256; idx += blockDim.x) {
+    const int o = idx / (MT * 256), u = (idx >> 8) % MT, r = (idx >> 6) & 3, l = idx & 63;
+    const int m = m0 + u * 16 + 4 * (l >> 4) + r;
+    const int t = EPI == EPI_SWIGLU ? 2 * o : o;
+    int mi, lt;
+    bool valid;
+    slot_tile<NT, EPI>(g, t, mi, lt, valid);
+    const int64_t nn = (int64_t)lt * 16 + (l & 15);
+    if (!valid || m >= M || nn >= g.n[mi]) continue;
+    float v = total(t, u, r, l);
+    if (g.row_scale) v *= g.row_scale[m];
+    if (g.col_scale[mi]) v *= g.col_scale[mi][nn];
+    if (g.bias[mi]) v += g.bias[mi][nn];
+    if (EPI == EPI_SWIGLU) {
+      float up = total(t + 1, u, r, l);
+      if (g.row_scale) up *= g.row_scale[m];
+      if (g.col_scale[1]) up *= g.col_scale[1][nn];
+      if (g.bias[1]) up += g.bias[1][nn];
+      v = silu_f32(round_bf16(v)) * round_bf16(up);
+    } else if (EPI == EPI_RES) {
+      v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
+    }
+    if (g.out_f32)
+      reinterpret_cast<float*>(g.out[mi])[(int64_t)m * g.ldo[mi] + nn] = v;
+    else
+      reinterpret_cast<uint16_t*>(g.out[mi])[(int64_t)m * g.ldo[mi] + nn] = (uint16_t)f32_to_bf16_bits(v);
   }
 }
 
@@ -125,6 +296,83 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
   }
 }
 
+template <int F, int MT, int NT, int EPI>
+void launch_group(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, int64_t k, int64_t slots,
+                  hipStream_t st) {
+  const int64_t nd = axk::row_bytes<F>(k) / axk::kSegBytes;
+  const int waves = (int)(nd < kGroupWaves ? nd : kGroupWaves);
+  dim3 grid((unsigned)((slots + NT - 1) / NT), (unsigned)((m + 16 * MT - 1) / (16 * MT)));
+  hipLaunchKernelGGL((mx_group_kernel<F, MT, NT, EPI>), grid, dim3(64 * waves), 0, st, a, lda, g, (int)m, k);
+}
+
+template <int F, int EPI>
+int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, int64_t k, hipStream_t st) {
+  const int tiles = g.tile0[g.count];
+  const int64_t slots = EPI == EPI_SWIGLU ? 2 * (int64_t)g.tile0[1] : tiles;
+  // two tiles per workgroup when that still leaves >= 384 workgroups per M tile (a SwiGLU pair always)
+  const bool two = EPI == EPI_SWIGLU || tiles >= 768;
+  if (m <= 16) {
+    if (two) launch_group<F, 1, 2, EPI>(a, lda, g, m, k, slots, st);
+    else launch_group<F, 1, 1, EPI>(a, lda, g, m, k, slots, st);
+  } else {
+    if (two) launch_group<F, 2, 2, EPI>(a, lda, g, m, k, slots, st);
+    else launch_group<F, 2, 1, EPI>(a, lda, g, m, k, slots, st);
+  }
+  return axk_launch_status();
+}
+
+// Checks a group and launches it. Matrices need whole 128-byte row segments (and 8-byte aligned MXFP4 scale rows).
+template <int F>
+int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int epi, const uint16_t* res,
+             int64_t ldr, const float* row_scale, int out_dtype, int64_t m, int64_t k, hipStream_t st) {
+  AXK_REQUIRE(a && mats, AXK_E_NULL);
+  AXK_REQUIRE(count >= 1 && count <= AXK_MX_GROUP_MAX, AXK_E_SHAPE);
+  AXK_REQUIRE(epi == EPI_PLAIN || epi == EPI_SWIGLU || epi == EPI_RES, AXK_E_SHAPE);
+  AXK_REQUIRE(epi != EPI_SWIGLU || (count == 2 && mats[0].n == mats[1].n && mats[0].out == mats[1].out), AXK_E_SHAPE);
+  AXK_REQUIRE(epi != EPI_RES || (count == 1 && res), AXK_E_NULL);
+  AXK_REQUIRE(m >= 0 && k > 0 && m <= INT32_MAX && axk::row_bytes<F>(k) % axk::kSegBytes == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(lda >= k && lda % 8 == 0 && axk_aligned(a, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(out_dtype == AXK_DT_BF16 || out_dtype == AXK_DT_F32, AXK_E_DTYPE);
+  AXK_REQUIRE(epi == EPI_PLAIN || out_dtype == AXK_DT_BF16, AXK_E_DTYPE);
+  MxGroup g{};
+  g.count = count;
+  g.row_scale = row_scale;
+  g.res = res;
+  g.ldr = ldr;
+  g.out_f32 = out_dtype == AXK_DT_F32;
+  const size_t esz = out_dtype == AXK_DT_F32 ? 4 : 2;
+  const size_t a_bytes = m > 0 ? (size_t)((m - 1) * lda + k) * 2 : 0;
+  int64_t tiles = 0;
+  for (int i = 0; i < count; ++i) {
+    const AxkMxMat& p = mats[i];
+    AXK_REQUIRE(p.w && p.out && (F != axk::WF_MXFP4 || p.ws), AXK_E_NULL);
+    AXK_REQUIRE(p.n > 0 && p.n <= INT32_MAX && p.ldo >= p.n, AXK_E_SHAPE);
+    AXK_REQUIRE(axk_aligned(p.w, 16) && (F != axk::WF_MXFP4 || axk_aligned(p.ws, 8)), AXK_E_ALIGN);
+    const size_t o_bytes = m > 0 ? (size_t)((m - 1) * p.ldo + p.n) * esz : 0;
+    AXK_REQUIRE(!axk_overlap(p.out, o_bytes, a, a_bytes), AXK_E_ALIAS);
+    if (epi == EPI_RES) {  // in place (out == res, one leading dimension) or disjoint
+      AXK_REQUIRE(ldr >= p.n, AXK_E_SHAPE);
+      const size_t r_bytes = m > 0 ? (size_t)((m - 1) * ldr + p.n) * 2 : 0;
+      AXK_REQUIRE((p.out == res && p.ldo == ldr) || !axk_overlap(p.out, o_bytes, res, r_bytes), AXK_E_ALIAS);
+    }
+    g.w[i] = p.w;
+    g.ws[i] = p.ws;
+    g.col_scale[i] = p.col_scale;
+    g.bias[i] = p.bias;
+    g.out[i] = p.out;
+    g.ldo[i] = p.ldo;
+    g.n[i] = (int)p.n;
+    g.tile0[i] = (int)tiles;
+    tiles += (p.n + 15) / 16;
+  }
+  AXK_REQUIRE(tiles <= INT32_MAX / 16, AXK_E_SHAPE);
+  for (int i = count; i <= AXK_MX_GROUP_MAX; ++i) g.tile0[i] = (int)tiles;
+  if (m == 0) return AXK_OK;
+  if (epi == EPI_SWIGLU) return group_dispatch<F, EPI_SWIGLU>(a, lda, g, m, k, st);
+  if (epi == EPI_RES) return group_dispatch<F, EPI_RES>(a, lda, g, m, k, st);
+  return group_dispatch<F, EPI_PLAIN>(a, lda, g, m, k, st);
+}
+
 template <int F>
 int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_t* ws, const float* row_scale,
                   const float* col_scale, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
@@ -141,30 +389,38 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   const size_t a_bytes = (size_t)((m - 1) * lda + k) * 2;
   AXK_REQUIRE(!axk_overlap(out, out_bytes, a, a_bytes), AXK_E_ALIAS);
 
-  // staged weight loads when rows are whole 128-byte segments (and MXFP4 scale rows 8-byte aligned)
-  const int64_t rb = axk::row_bytes<F>(k);
-  const bool stage = rb % axk::kSegBytes == 0 && (F != WF_MXFP4 || axk_aligned(ws, 8));
+  hipStream_t st = axk_stream(stream);
+  // staged group kernel when rows are whole 128-byte segments (and MXFP4 scale rows 8-byte aligned)
+  if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 && (F != WF_MXFP4 || axk_aligned(ws, 8))) {
+    const AxkMxMat mat{w, ws, col_scale, bias, out, n, n};
+    return mx_group<F>(a, lda, &mat, 1, EPI_PLAIN, nullptr, 0, row_scale, out_dtype, m, k, st);
+  }
   constexpr int CH = 4 * WUnit<F>::V;
-  const int64_t nc = stage ? rb / axk::kSegBytes : (k + CH - 1) / CH;  // K work units: segments or chunks
+  const int64_t nc = (k + CH - 1) / CH;  // K chunks
   const int waves = (int)(nc < kMaxWaves ? nc : kMaxWaves);
   const int mt = m <= 16 ? 1 : 2;
   dim3 grid((unsigned)((n + 15) / 16), (unsigned)((m + 16 * mt - 1) / (16 * mt)));
   dim3 block(64 * waves);
   const int of32 = out_dtype == AXK_DT_F32;
-  hipStream_t st = axk_stream(stream);
-#define AXK_MX_LAUNCH(MT_, ST_)                                                                            \
-  hipLaunchKernelGGL((mx_linear_kernel<F, MT_, ST_>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, \
-                     bias, out, of32, (int)m, (int)n, k)
-  if (mt == 1) {
-    if (stage) AXK_MX_LAUNCH(1, true); else AXK_MX_LAUNCH(1, false);
-  } else {
-    if (stage) AXK_MX_LAUNCH(2, true); else AXK_MX_LAUNCH(2, false);
-  }
-#undef AXK_MX_LAUNCH
+  if (mt == 1)
+    hipLaunchKernelGGL((mx_linear_kernel<F, 1>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, out,
+                       of32, (int)m, (int)n, k);
+  else
+    hipLaunchKernelGGL((mx_linear_kernel<F, 2>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, out,
+                       of32, (int)m, (int)n, k);
   return axk_launch_status();
 }
 
 }  // namespace
+
+int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int epi,
+                 const uint16_t* res, int64_t ldr, const float* row_scale, int out_dtype, int64_t m, int64_t k,
+                 hipStream_t stream) {
+  if (fmt == AXK_MX_FP8) return mx_group<WF_FP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, stream);
+  if (fmt == AXK_MX_MXFP4)
+    return mx_group<WF_MXFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, stream);
+  return AXK_E_DTYPE;
+}
 
 extern "C" int axk_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales, float* out, int64_t n, int64_t k,
                                  axk_stream_t stream) {

@@ -63,7 +63,7 @@ class MxLinearWorkload(Workload):
     """Config 0: one MXFP4 linear, W 4096 x 4096 (E2M1 + E8M0), x bf16 [1, 4096], bf16 out."""
 
     name = "mxfp4_linear"
-    kernel = "mx_linear_kernel"
+    kernel = "mx_group_kernel"
     timing = "graph"
     traffic_profile = "mxfp4_linear_config0_pmc.txt"
 
@@ -485,7 +485,7 @@ class Fp8LinearWorkload(Workload):
     (the group's decode batch), bf16 out. Algorithmic bytes: weight + scales + x + out."""
 
     name = "fp8_linear"
-    kernel = "mx_linear_kernel<FP8>"
+    kernel = "mx_group_kernel<FP8>"
     timing = "graph"
     traffic_profile = "fp8_linear_config4q_pmc.txt"
 
