@@ -87,6 +87,63 @@ __global__ __launch_bounds__(64 * kRowsPerWg) void rmsnorm_rows_kernel(const uin
   }
 }
 
+// Register-resident variant for n <= 8192: TPR threads per row (64: a wave, 256: the workgroup), each holding CPT
+// 8-element chunks (c = rank + TPR i); every load of the row (x, y, z, w) is issued before the reduction, so a row
+// costs one memory round trip. Same rounding points as rmsnorm_rows_kernel.
+template <int MODE, int TPR, int CPT>
+__global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                          const uint16_t* __restrict__ y, const float* __restrict__ w,
+                                                          const uint16_t* __restrict__ z, uint16_t* sum_out,
+                                                          uint16_t* __restrict__ out, int64_t ldo, int64_t rows, int n,
+                                                          float eps) {
+  __shared__ float part[256 / 64];
+  const int rank = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  if (TPR == 64 && row >= rows) return;  // whole waves; TPR == 256 rows are always in range (grid = rows)
+  const int nch = n >> 3;
+  float f[CPT][8], wv[CPT][8], zv[CPT][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = rank + TPR * i;
+    if (c < nch) {
+      unpack8(*reinterpret_cast<const uint4*>(x + row * ldx + 8 * c), f[i]);
+      const float4 w0 = *reinterpret_cast<const float4*>(w + 8 * c), w1 = *reinterpret_cast<const float4*>(w + 8 * c + 4);
+      wv[i][0] = w0.x; wv[i][1] = w0.y; wv[i][2] = w0.z; wv[i][3] = w0.w;
+      wv[i][4] = w1.x; wv[i][5] = w1.y; wv[i][6] = w1.z; wv[i][7] = w1.w;
+      if (MODE == 1) {
+        float g[8];
+        unpack8(*reinterpret_cast<const uint4*>(y + row * n + 8 * c), g);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f[i][k] = round_bf16(f[i][k] + g[k]);
+        *reinterpret_cast<uint4*>(sum_out + row * n + 8 * c) = pack8(f[i]);
+      }
+      if (MODE == 2) unpack8(*reinterpret_cast<const uint4*>(z + row * n + 8 * c), zv[i]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss += f[i][k] * f[i][k];
+    }
+  }
+  ss = wave_sum(ss);
+  if (TPR == 256) {
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (part[0] + part[1]) + (part[2] + part[3]);
+  }
+  const float inv = rsqrtf(ss / (float)n + eps);
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = rank + TPR * i;
+    if (c < nch) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        f[i][k] = f[i][k] * inv * wv[i][k];
+        if (MODE == 2) f[i][k] = round_bf16(f[i][k]) * silu_f32(zv[i][k]);
+      }
+      *reinterpret_cast<uint4*>(out + row * ldo + 8 * c) = pack8(f[i]);
+    }
+  }
+}
+
 // One thread per (sequence, channel): the window slides over the tokens; history in registers.
 __global__ __launch_bounds__(256) void conv1d_silu_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
@@ -186,6 +243,26 @@ unsigned elt_grid(int64_t work) {
   return (unsigned)(g < 65536 ? (g > 0 ? g : 1) : 65536);
 }
 
+// Launches the register-resident kernel when the row fits (n <= 8192), else the looping one.
+template <int MODE>
+void launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* y, const float* w, const uint16_t* z,
+                    uint16_t* sum_out, uint16_t* out, int64_t ldo, int64_t rows, int n, float eps, hipStream_t st) {
+  const int nch = n >> 3;
+#define AXK_RMS(TPR, CPT)                                                                                          \
+  hipLaunchKernelGGL((rmsnorm_reg_kernel<MODE, TPR, CPT>), dim3((unsigned)((rows + 256 / TPR - 1) / (256 / TPR))), \
+                     dim3(256), 0, st, x, ldx, y, w, z, sum_out, out, ldo, rows, n, eps)
+  if (nch <= 64) AXK_RMS(64, 1);
+  else if (nch <= 128) AXK_RMS(64, 2);
+  else if (nch <= 256) AXK_RMS(256, 1);
+  else if (nch <= 512) AXK_RMS(256, 2);
+  else if (nch <= 768) AXK_RMS(256, 3);
+  else if (nch <= 1024) AXK_RMS(256, 4);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<MODE>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, st, x, ldx, y, w, z,
+                       sum_out, out, ldo, rows, n, eps);
+#undef AXK_RMS
+}
+
 bool aligned16(const void* p) { return axk_aligned(p, 16); }
 
 }  // namespace
@@ -195,8 +272,7 @@ extern "C" int axk_rmsnorm(const uint16_t* x, int64_t ldx, const float* w, uint1
   AXK_REQUIRE(x && w && out, AXK_E_NULL);
   AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX && ldx >= n && ldo >= n, AXK_E_SHAPE);
   AXK_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(out), AXK_E_ALIGN);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel<0>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, ldx,
-                     nullptr, w, nullptr, nullptr, out, ldo, rows, (int)n, eps);
+  launch_rmsnorm<0>(x, ldx, nullptr, w, nullptr, nullptr, out, ldo, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
 
@@ -209,8 +285,7 @@ extern "C" int axk_add_rmsnorm(const uint16_t* x, const uint16_t* y, const float
   AXK_REQUIRE(!axk_overlap(norm_out, bytes, sum_out, bytes) && !axk_overlap(norm_out, bytes, x, bytes) &&
                   !axk_overlap(norm_out, bytes, y, bytes),
               AXK_E_ALIAS);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel<1>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, n, y,
-                     w, nullptr, sum_out, norm_out, n, rows, (int)n, eps);
+  launch_rmsnorm<1>(x, n, y, w, nullptr, sum_out, norm_out, n, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
 
@@ -219,8 +294,7 @@ extern "C" int axk_gated_rmsnorm_silu(const uint16_t* x, const float* w, const u
   AXK_REQUIRE(x && w && z && out, AXK_E_NULL);
   AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(aligned16(x) && aligned16(w) && aligned16(z) && aligned16(out), AXK_E_ALIGN);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel<2>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, axk_stream(stream), x, n,
-                     nullptr, w, z, nullptr, out, n, rows, (int)n, eps);
+  launch_rmsnorm<2>(x, n, nullptr, w, z, nullptr, out, n, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
 

@@ -21,7 +21,8 @@ def _close(got, ref):
     torch.testing.assert_close(got.float().cpu(), ref.float(), **TOL)
 
 
-@pytest.mark.parametrize("rows,n", [(8, 4096), (3, 2048), (64, 128), (5, 8), (2, 8192)])
+@pytest.mark.parametrize("rows,n", [(8, 4096), (3, 2048), (64, 128), (5, 8), (2, 8192), (4, 6144), (3, 1032),
+                                    (2, 16384), (9, 1024)])
 def test_rmsnorm(dev, rows, n):
     g = _g(rows + n)
     x = torch.randn(rows, n, generator=g).bfloat16() * 3
@@ -40,11 +41,12 @@ def test_rmsnorm_strided_rows_and_output_buffer(dev):
     _close(got, layer.rmsnorm(qg[..., :256].reshape(24, 256), w))
 
 
-def test_add_rmsnorm(dev):
-    g = _g(2)
-    x = torch.randn(8, 4096, generator=g).bfloat16()
-    y = torch.randn(8, 4096, generator=g).bfloat16()
-    w = torch.rand(4096, generator=g) + 0.5
+@pytest.mark.parametrize("rows,n", [(8, 4096), (3, 512), (2, 16384)])
+def test_add_rmsnorm(dev, rows, n):
+    g = _g(2 + n)
+    x = torch.randn(rows, n, generator=g).bfloat16()
+    y = torch.randn(rows, n, generator=g).bfloat16()
+    w = torch.rand(n, generator=g) + 0.5
     s, n = glue.add_rmsnorm(x.to(dev), y.to(dev), w.to(dev))
     rs, rn = layer.add_rmsnorm(x, y, w)
     assert torch.equal(s.cpu().view(torch.int16), rs.view(torch.int16))
