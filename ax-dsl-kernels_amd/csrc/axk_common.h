@@ -169,5 +169,17 @@ AXK_DEV float wave_max(float v) {
 }
 
 AXK_DEV float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+
+// One token of the causal depthwise conv1d for one channel: taps wk[0 .. K-1] (wk[0] multiplies the current input
+// xt, wk[j] the input j tokens back), hist[0 .. K-2] the previous inputs, oldest first (K <= kMaxConvTaps). Each
+// tap's partial sum is rounded to bf16, as the reference accumulates in bf16; SiLU is applied by the caller.
+constexpr int kMaxConvTaps = 8;
+AXK_DEV float conv_taps(float xt, const float (&wk)[kMaxConvTaps], const float (&hist)[kMaxConvTaps], int K) {
+  float acc = round_bf16(__fadd_rn(0.f, __fmul_rn(xt, wk[0])));
+#pragma unroll
+  for (int j = 1; j < kMaxConvTaps; ++j)
+    if (j < K) acc = round_bf16(__fadd_rn(acc, __fmul_rn(hist[K - 1 - j], wk[j])));
+  return acc;
+}
 AXK_DEV float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
 AXK_DEV float softplus_f32(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }

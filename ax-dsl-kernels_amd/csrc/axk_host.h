@@ -29,13 +29,20 @@ static inline hipStream_t axk_stream(axk_stream_t s) { return reinterpret_cast<h
 // Internal (not exported): the GDN recurrence with row strides, in elements between consecutive (sequence, token)
 // rows, for q, k, v and a / b. axk_gdn_recurrent passes the contiguous strides; the decode layer reads q / k / v
 // straight out of the conv output. Returns an AXK status.
+// With gate (optional), out is the GDN output norm of each head's row: bf16(bf16(rmsnorm(o) * norm_w) * silu(z)),
+// z [batch, tokens, num_v_heads, 128] contiguous.
 struct AxkGdnStrides {
   int64_t q, k, v, ab;
+};
+struct AxkGdnGate {
+  const float* norm_w;
+  const uint16_t* z;
+  float eps;
 };
 __attribute__((visibility("hidden"))) int axk_gdn_recurrent_strided(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
     const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
-    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, hipStream_t stream);
+    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, hipStream_t stream);
 
 // Internal (not exported): one launch of up to AXK_MX_GROUP_MAX weight matrices that share the activations a
 // [m, k] (the projections of one decode layer). Matrix i: weights w [n, k] (FP8 bytes, or MXFP4 codes with E8M0
@@ -55,7 +62,26 @@ struct AxkMxMat {
   int64_t ldo;
   int64_t n;
 };
+// Optional conv epilogue on mats[0] (plain bf16): each row is one token of its sequence; the output is
+// silu(causal_conv1d) over the projection's bf16 output with taps w [n, kernel] (tap 0 = the current token) and
+// the state [m, kernel - 1, n] oldest first, advanced into state_out (which may be state_in).
+struct AxkConvEpi {
+  const uint16_t* w;
+  const uint16_t* state_in;
+  uint16_t* state_out;
+  int64_t kernel;
+};
 __attribute__((visibility("hidden"))) int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats,
                                                        int count, int epi, const uint16_t* res, int64_t ldr,
                                                        const float* row_scale, int out_dtype, int64_t m, int64_t k,
-                                                       hipStream_t stream);
+                                                       const AxkConvEpi* conv, hipStream_t stream);
+
+// Internal (not exported): the attention decode layer's q / k / v preparation in one launch. q heads of the
+// [q | gate] projection qg [B, HQ, 2 D] -> rmsnorm(q_norm) + NeoX RoPE -> q_out [B, HQ, D]; k [B, HKV, D] ->
+// rmsnorm(k_norm) + RoPE and v [B, HKV, D] as is -> the paged cache [P, 2, page, HKV, D] at cache_location [B, 2]
+// (page, slot); a location outside the cache writes nothing. Returns an AXK status.
+__attribute__((visibility("hidden"))) int axk_attn_qkv_prep(
+    const uint16_t* qg, const uint16_t* kk, const uint16_t* vv, const float* q_norm, const float* k_norm,
+    const uint16_t* cos, const uint16_t* sin, uint16_t* q_out, uint16_t* kv_cache, const int32_t* cache_location,
+    int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages,
+    float eps, hipStream_t stream);

@@ -11,6 +11,9 @@
 // registers (64 floats per thread, float4 loads along DV) from one read to one write, across all T tokens.
 // Arithmetic is fp32 throughout (the reference rounds the state to bf16 for its two products; the
 // difference is well inside the bf16 output tolerance and is checked against both formulations).
+// With GATE (the decode layer), the output row of each head goes through the GDN output norm before it is
+// stored: out = bf16(bf16(rmsnorm(bf16 o) * norm_w) * silu(z)) (q35_step.py:179-180), the same rounding points
+// as the separate gated-norm kernel.
 #include "axk_common.h"
 #include "axk_host.h"
 
@@ -35,10 +38,15 @@ struct GdnArgs {
   uint16_t* out;          // [B, T, NV, DV] bf16
   int B, T, NK, NV;
   int64_t ldq, ldk, ldv, ldab;  // elements between consecutive (sequence, token) rows of q, k, v, a / b
+  const float* norm_w;          // GATE: the output norm's weight [DV] and gate z [B, T, NV, DV]
+  const uint16_t* z;
+  float eps;
 };
 
+template <bool GATE>
 __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
   __shared__ float s_k[kDK], s_q[kDK];
+  __shared__ float s_gn[2];
   __shared__ float s_red[kRowGroups / 2][kDV];  // per-wave partial column sums
   __shared__ float s_vec[kDV];
   __shared__ float s_norm[4];
@@ -124,13 +132,30 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
     __syncthreads();  // s_red / s_vec reuse
     if (lane < 32) *reinterpret_cast<float4*>(&s_red[wave][c0]) = ov;
     __syncthreads();
-    if (tid < kDV) {
-      float sum = 0.f;
+    if (!GATE) {
+      if (tid < kDV) {
+        float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < kRowGroups / 2; ++w) sum += s_red[w][tid];
-      p.out[vh * kDV + tid] = (uint16_t)f32_to_bf16_bits(sum);
+        for (int w = 0; w < kRowGroups / 2; ++w) sum += s_red[w][tid];
+        p.out[vh * kDV + tid] = (uint16_t)f32_to_bf16_bits(sum);
+      }
+    } else {
+      float core = 0.f;  // the head's bf16 output, element tid (threads 0 .. 127: waves 0 and 1)
+      if (tid < kDV) {
+#pragma unroll
+        for (int w = 0; w < kRowGroups / 2; ++w) core += s_red[w][tid];
+        core = round_bf16(core);
+      }
+      const float ss = wave_sum(core * core);
+      if (lane == 0 && wave < 2) s_gn[wave] = ss;
+      __syncthreads();
+      if (tid < kDV) {
+        const float inv = rsqrtf((s_gn[0] + s_gn[1]) / (float)kDV + p.eps);
+        const float zz = bf16_bits_to_f32(p.z[vh * kDV + tid]);
+        p.out[vh * kDV + tid] = (uint16_t)f32_to_bf16_bits(round_bf16(core * inv * p.norm_w[tid]) * silu_f32(zz));
+      }
     }
-    __syncthreads();  // s_k / s_q / s_red reuse by the next token
+    __syncthreads();  // s_k / s_q / s_red / s_gn reuse by the next token
   }
 
   float* sout = p.state_out + ((int64_t)b * p.NV + h) * kDK * kDV;
@@ -143,8 +168,10 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
 int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
                               const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
                               float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
-                              int64_t num_v_heads, const AxkGdnStrides& ld, hipStream_t stream) {
+                              int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate,
+                              hipStream_t stream) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
+  AXK_REQUIRE(!gate || (gate->norm_w && gate->z), AXK_E_NULL);
   AXK_REQUIRE(batch > 0 && tokens > 0 && num_k_heads > 0 && num_v_heads > 0, AXK_E_SHAPE);
   AXK_REQUIRE(num_v_heads % num_k_heads == 0, AXK_E_SHAPE);
   AXK_REQUIRE(batch * num_v_heads <= INT32_MAX && tokens <= INT32_MAX, AXK_E_SHAPE);
@@ -158,8 +185,12 @@ int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16
   const size_t obytes = (size_t)batch * tokens * num_v_heads * kDV * 2;
   AXK_REQUIRE(!axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
   GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
-            (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab};
-  hipLaunchKernelGGL(gdn_recurrent_kernel, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
+            (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab, gate ? gate->norm_w : nullptr, gate ? gate->z : nullptr,
+            gate ? gate->eps : 0.f};
+  if (gate)
+    hipLaunchKernelGGL(gdn_recurrent_kernel<true>, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(gdn_recurrent_kernel<false>, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
   return axk_launch_status();
 }
 
@@ -170,5 +201,5 @@ extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uin
   AXK_REQUIRE(head_k_dim == kDK && head_v_dim == kDV, AXK_E_SHAPE);
   const AxkGdnStrides ld{num_k_heads * kDK, num_k_heads * kDK, num_v_heads * kDV, num_v_heads};
   return axk_gdn_recurrent_strided(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens,
-                                   num_k_heads, num_v_heads, ld, axk_stream(stream));
+                                   num_k_heads, num_v_heads, ld, nullptr, axk_stream(stream));
 }

@@ -3,10 +3,12 @@
 // each followed by the MLP block (mlp_block 118-142). Projections of the attention / GDN paths are FP8 E4M3 with
 // per-output-channel fp32 scales; the MLP is MXFP4 (the config of the hybrid decode group). Every intermediate is
 // a bf16 tensor in the caller's workspace, rounded where the reference rounds (each projection's output, each
-// glue op's output). Projections that share an input run as one grouped launch (GDN: qkv | z | b | a; attention:
-// q | k | v); the MLP's gate and up projections run as one launch whose epilogue applies SwiGLU, and the down
-// projection's epilogue adds the residual (both round exactly where the separate ops round). No allocation, no
-// host synchronisation: a layer is graph-capturable.
+// glue op's output). Projections that share an input run as one grouped launch (GDN: qkv | z | b | a, whose qkv
+// epilogue also runs the causal conv1d + SiLU; attention: q | k | v); the GDN kernel applies the gated output norm
+// to each head's row; one launch prepares q / k / v (norms, RoPE, the paged KV write); the MLP's gate and up
+// projections run as one launch whose epilogue applies SwiGLU, and the down projection's epilogue adds the
+// residual. Every fused step rounds exactly where the separate op rounds. No allocation, no host
+// synchronisation: a layer is graph-capturable.
 #include "axk_host.h"
 
 namespace {
@@ -55,17 +57,18 @@ int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const M
   const AxkMxMat gate_up[2] = {{w.gate_w, w.gate_s, nullptr, nullptr, m.act, F, F},
                                {w.up_w, w.up_s, nullptr, nullptr, m.act, F, F}};
   AXK_TRY(axk_mx_group(AXK_MX_MXFP4, m.h2, H, gate_up, 2, AXK_MX_EPI_SWIGLU, nullptr, 0, nullptr, AXK_DT_BF16, B, H,
-                       axk_stream(st)));
+                       nullptr, axk_stream(st)));
   const AxkMxMat down{w.down_w, w.down_s, nullptr, nullptr, out, H, H};
   return axk_mx_group(AXK_MX_MXFP4, m.act, F, &down, 1, AXK_MX_EPI_RES, m.x1, H, nullptr, AXK_DT_BF16, B, F,
-                      axk_stream(st));
+                      nullptr, axk_stream(st));
 }
 
-// FP8 projections of one input a [m, k] (bf16 outputs, per-channel scales) as one grouped launch.
+// FP8 projections of one input a [m, k] (bf16 outputs, per-channel scales) as one grouped launch; conv (optional)
+// runs the causal conv1d + SiLU on the first matrix's output.
 int fp8_projs(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int64_t m, int64_t k,
-              axk_stream_t st) {
+              axk_stream_t st, const AxkConvEpi* conv = nullptr) {
   return axk_mx_group(AXK_MX_FP8, a, lda, mats, count, AXK_MX_EPI_PLAIN, nullptr, 0, nullptr, AXK_DT_BF16, m, k,
-                      axk_stream(st));
+                      conv, axk_stream(st));
 }
 
 AxkMxMat fp8_mat(const uint8_t* w, const float* s, uint16_t* out, int64_t n) {
@@ -73,7 +76,7 @@ AxkMxMat fp8_mat(const uint8_t* w, const float* s, uint16_t* out, int64_t n) {
 }
 
 struct GdnBufs {
-  uint16_t *h, *qkv, *z, *bb, *aa, *mixed, *core, *gated, *y;
+  uint16_t *h, *z, *bb, *aa, *mixed, *gated, *y;
   MlpBufs mlp;
 };
 
@@ -81,12 +84,10 @@ GdnBufs carve_gdn(Carver& c, int64_t B, int64_t H, int64_t NK, int64_t NV, int64
   const int64_t KD = NK * DH, VD = NV * DH, C = 2 * KD + VD;
   GdnBufs g;
   g.h = c.take<uint16_t>(B * H);
-  g.qkv = c.take<uint16_t>(B * C);
   g.z = c.take<uint16_t>(B * VD);
   g.bb = c.take<uint16_t>(B * NV);
   g.aa = c.take<uint16_t>(B * NV);
   g.mixed = c.take<uint16_t>(B * C);
-  g.core = c.take<uint16_t>(B * VD);
   g.gated = c.take<uint16_t>(B * VD);
   g.y = c.take<uint16_t>(B * H);
   g.mlp = carve_mlp(c, B, H, F);
@@ -94,7 +95,7 @@ GdnBufs carve_gdn(Carver& c, int64_t B, int64_t H, int64_t NK, int64_t NV, int64
 }
 
 struct AttnBufs {
-  uint16_t *h, *qg, *kk, *vv, *q, *k, *attn, *gated, *y;
+  uint16_t *h, *qg, *kk, *vv, *q, *attn, *gated, *y;
   void* pws;
   size_t pws_bytes;
   MlpBufs mlp;
@@ -107,7 +108,6 @@ AttnBufs carve_attn(Carver& c, int64_t B, int64_t H, int64_t HQ, int64_t HKV, in
   a.kk = c.take<uint16_t>(B * HKV * D);
   a.vv = c.take<uint16_t>(B * HKV * D);
   a.q = c.take<uint16_t>(B * HQ * D);
-  a.k = c.take<uint16_t>(B * HKV * D);
   a.attn = c.take<uint16_t>(B * HQ * D);
   a.gated = c.take<uint16_t>(B * HQ * D);
   a.y = c.take<uint16_t>(B * H);
@@ -157,15 +157,17 @@ extern "C" int axk_gdn_layer_decode(
   const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
   const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
   AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
-  const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.qkv, C), fp8_mat(w_z, s_z, g.z, VD), fp8_mat(w_b, s_b, g.bb, NV),
+  // qkv | z | b | a, the qkv output through the causal conv1d + SiLU (mixed) as it is stored
+  const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.mixed, C), fp8_mat(w_z, s_z, g.z, VD), fp8_mat(w_b, s_b, g.bb, NV),
                             fp8_mat(w_a, s_a, g.aa, NV)};
-  AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream));
-  AXK_TRY(axk_causal_conv1d_silu(g.qkv, conv_w, conv_in, conv_out, g.mixed, B, 1, C, conv_kernel, stream));
-  // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row
+  const AxkConvEpi conv{conv_w, conv_in, conv_out, conv_kernel};
+  AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream, &conv));
+  // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row; each
+  // head's output row leaves through the gated output norm
   const AxkGdnStrides ld{C, C, C, NV};
+  const AxkGdnGate gate{norm_w, g.z, eps};
   AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
-                                    state_out, g.core, B, 1, NK, NV, ld, axk_stream(stream)));
-  AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, B * NV, DH, eps, stream));
+                                    state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
   const AxkMxMat o = fp8_mat(w_out, s_out, g.y, H);
   AXK_TRY(fp8_projs(g.gated, VD, &o, 1, B, VD, stream));
   return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
@@ -206,9 +208,8 @@ extern "C" int axk_attn_layer_decode(
   const AxkMxMat proj[3] = {fp8_mat(w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
                             fp8_mat(w_k, s_k, a.kk, HKV * D), fp8_mat(w_v, s_v, a.vv, HKV * D)};
   AXK_TRY(fp8_projs(a.h, H, proj, 3, B, H, stream));
-  AXK_TRY(axk_qk_norm_rope(a.qg, 2 * D, q_norm, cos, sin, a.q, B, HQ, D, rot, eps, stream));
-  AXK_TRY(axk_qk_norm_rope(a.kk, D, k_norm, cos, sin, a.k, B, HKV, D, rot, eps, stream));
-  AXK_TRY(axk_paged_kv_write(a.k, a.vv, kv_cache, cache_location, B, HKV, D, page_size, num_pages, nullptr, stream));
+  AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, B, HQ, HKV, D,
+                            rot, page_size, num_pages, eps, axk_stream(stream)));
   AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
                            num_pages, sm_scale, a.pws, a.pws_bytes, stream));
   AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));

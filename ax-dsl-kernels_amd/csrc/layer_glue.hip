@@ -22,7 +22,7 @@
 namespace {
 
 constexpr int kRowsPerWg = 4;
-constexpr int kMaxConvKernel = 8;
+constexpr int kMaxConvKernel = kMaxConvTaps;
 constexpr int kMaxRopeDim = 512;
 
 AXK_DEV void unpack8(const uint4& v, float (&f)[8]) {
@@ -162,11 +162,7 @@ __global__ __launch_bounds__(256) void conv1d_silu_kernel(const uint16_t* __rest
     const int64_t o = ((int64_t)b * T + t) * C + c;
     const float xt = bf16_bits_to_f32(x[o]);
     // tap j multiplies x_{t-j}: j = 0 the current token, then back through the history (a bf16 rounding per tap)
-    float acc = round_bf16(__fadd_rn(0.f, __fmul_rn(xt, wk[0])));
-#pragma unroll
-    for (int j = 1; j < kMaxConvKernel; ++j)
-      if (j < K) acc = round_bf16(__fadd_rn(acc, __fmul_rn(hist[K - 1 - j], wk[j])));
-    out[o] = (uint16_t)f32_to_bf16_bits(silu_f32(acc));
+    out[o] = (uint16_t)f32_to_bf16_bits(silu_f32(conv_taps(xt, wk, hist, K)));
 #pragma unroll
     for (int j = 0; j + 1 < kMaxConvKernel; ++j)
       if (j + 1 < K - 1) hist[j] = hist[j + 1];
@@ -177,30 +173,27 @@ __global__ __launch_bounds__(256) void conv1d_silu_kernel(const uint16_t* __rest
     if (j < K - 1) state_out[((int64_t)b * (K - 1) + j) * C + c] = (uint16_t)f32_to_bf16_bits(hist[j]);
 }
 
-// One wave per (sequence, head) row of D values: RMSNorm (bf16), then NeoX RoPE on the first rot channels
-// with the sequence's cos / sin. Lane l holds channels EPL l .. EPL l + EPL - 1; channel e pairs with e + rot / 2.
+// One wave, one row of D = 64 EPL values (lane l: channels EPL l .. EPL l + EPL - 1): RMSNorm to bf16, then NeoX
+// RoPE on the first rot channels with the row's cos / sin (channel e pairs with e + rot / 2); with norm == false
+// the row is copied. The wave must be whole (the norm and the rotation exchange values across lanes).
 template <int EPL>
-__global__ __launch_bounds__(64 * kRowsPerWg) void qk_norm_rope_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                       const float* __restrict__ w,
-                                                                       const uint16_t* __restrict__ cosv,
-                                                                       const uint16_t* __restrict__ sinv,
-                                                                       uint16_t* __restrict__ out, int64_t rows,
-                                                                       int heads, int rot, float eps) {
+AXK_DEV void norm_rope_row(const uint16_t* __restrict__ xr, const float* __restrict__ w,
+                           const uint16_t* __restrict__ cosr, const uint16_t* __restrict__ sinr, uint16_t* orow,
+                           int rot, float eps, bool norm) {
   constexpr int D = 64 * EPL;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t b = row / heads;
   float v[EPL];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    v[j] = bf16_bits_to_f32(x[row * ldx + EPL * lane + j]);
+    v[j] = bf16_bits_to_f32(xr[EPL * lane + j]);
     ss += v[j] * v[j];
   }
-  const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+  if (norm) {
+    const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) v[j] = round_bf16(v[j] * inv * w[EPL * lane + j]);
+    for (int j = 0; j < EPL; ++j) v[j] = round_bf16(v[j] * inv * w[EPL * lane + j]);
+  }
   const int half = rot >> 1, lofs = half / EPL;  // partner lane offset (half % EPL == 0)
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
@@ -209,13 +202,59 @@ __global__ __launch_bounds__(64 * kRowsPerWg) void qk_norm_rope_kernel(const uin
     const int plane = low ? lane + lofs : lane - lofs;
     const float pv = __shfl(v[j], (plane >= 0 && plane < 64) ? plane : lane, 64);
     float r = v[j];
-    if (e < rot) {
+    if (norm && e < rot) {
       const int ci = low ? e : e - half;
-      const float cs = bf16_bits_to_f32(cosv[b * half + ci]), sn = bf16_bits_to_f32(sinv[b * half + ci]);
+      const float cs = bf16_bits_to_f32(cosr[ci]), sn = bf16_bits_to_f32(sinr[ci]);
       r = low ? v[j] * cs - pv * sn : v[j] * cs + pv * sn;
     }
-    out[row * D + e] = (uint16_t)f32_to_bf16_bits(r);
+    orow[e] = (uint16_t)f32_to_bf16_bits(r);
   }
+}
+
+// One wave per (sequence, head) row: norm_rope_row over x rows ldx apart, into contiguous out rows.
+template <int EPL>
+__global__ __launch_bounds__(64 * kRowsPerWg) void qk_norm_rope_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                       const float* __restrict__ w,
+                                                                       const uint16_t* __restrict__ cosv,
+                                                                       const uint16_t* __restrict__ sinv,
+                                                                       uint16_t* __restrict__ out, int64_t rows,
+                                                                       int heads, int rot, float eps) {
+  constexpr int D = 64 * EPL;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / heads;
+  const int half = rot >> 1;
+  norm_rope_row<EPL>(x + row * ldx, w, cosv + b * half, sinv + b * half, out + row * D, rot, eps, true);
+}
+
+// The attention layer's q / k / v preparation in one launch, one wave per row of the rows b (HQ + 2 HKV) + r:
+// r < HQ: q head r of the [q | gate] projection rows (2D apart) -> norm (q_norm) + RoPE -> q_out [B, HQ, D];
+// HQ <= r < HQ + HKV: k head -> norm (k_norm) + RoPE -> the K plane of the paged cache at loc[b] = (page, slot);
+// the last HKV rows: v head -> the V plane (store_paged_kv; a location outside the cache writes nothing).
+template <int EPL>
+__global__ __launch_bounds__(64 * kRowsPerWg) void attn_prep_kernel(
+    const uint16_t* __restrict__ qg, const uint16_t* __restrict__ kk, const uint16_t* __restrict__ vv,
+    const float* __restrict__ q_norm, const float* __restrict__ k_norm, const uint16_t* __restrict__ cosv,
+    const uint16_t* __restrict__ sinv, uint16_t* __restrict__ q_out, uint16_t* __restrict__ cache,
+    const int* __restrict__ loc, int batch, int hq, int hkv, int rot, int page_size, int64_t num_pages, float eps) {
+  constexpr int D = 64 * EPL;
+  const int per = hq + 2 * hkv;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= (int64_t)batch * per) return;
+  const int b = (int)(row / per), r = (int)(row - (int64_t)b * per);
+  const int half = rot >> 1;
+  const uint16_t *cr = cosv + (int64_t)b * half, *sr = sinv + (int64_t)b * half;
+  if (r < hq) {
+    norm_rope_row<EPL>(qg + ((int64_t)b * hq + r) * 2 * D, q_norm, cr, sr, q_out + ((int64_t)b * hq + r) * D, rot,
+                       eps, true);
+    return;
+  }
+  const int plane = r >= hq + hkv, kvh = r - hq - plane * hkv;
+  const int page = loc[2 * b], off = loc[2 * b + 1];
+  if (page < 0 || page >= num_pages || off < 0 || off >= page_size) return;
+  uint16_t* dst = cache + ((((int64_t)page * 2 + plane) * page_size + off) * hkv + kvh) * D;
+  const uint16_t* src = (plane ? vv : kk) + ((int64_t)b * hkv + kvh) * D;
+  norm_rope_row<EPL>(src, k_norm, cr, sr, dst, rot, eps, !plane);
 }
 
 // Elementwise over rows x n (n % 8 == 0): OP 0 bf16(x * sigmoid(g)), OP 1 bf16(silu(x) * g), OP 2 bf16(x + g).
@@ -363,4 +402,29 @@ extern "C" int axk_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* out,
 extern "C" int axk_add(const uint16_t* x, const uint16_t* y, uint16_t* out, int64_t rows, int64_t n,
                        axk_stream_t stream) {
   return launch_eltwise<2>(x, y, n, out, rows, n, stream);
+}
+
+int axk_attn_qkv_prep(const uint16_t* qg, const uint16_t* kk, const uint16_t* vv, const float* q_norm,
+                      const float* k_norm, const uint16_t* cos, const uint16_t* sin, uint16_t* q_out,
+                      uint16_t* kv_cache, const int32_t* cache_location, int64_t batch, int64_t hq, int64_t hkv,
+                      int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages, float eps,
+                      hipStream_t stream) {
+  AXK_REQUIRE(qg && kk && vv && q_norm && k_norm && q_out && kv_cache && cache_location && (rot == 0 || (cos && sin)),
+              AXK_E_NULL);
+  AXK_REQUIRE(batch > 0 && hq > 0 && hkv > 0 && page_size > 0 && num_pages > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == kMaxRopeDim, AXK_E_SHAPE);
+  const int64_t epl = head_dim / 64;
+  AXK_REQUIRE(rot >= 0 && rot <= head_dim && rot % 2 == 0 && (rot / 2) % epl == 0, AXK_E_SHAPE);
+  const int64_t rows = batch * (hq + 2 * hkv);
+  AXK_REQUIRE(rows <= INT32_MAX, AXK_E_SHAPE);
+#define AXK_PREP(E)                                                                                             \
+  hipLaunchKernelGGL(attn_prep_kernel<E>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, stream, qg, kk, vv,  \
+                     q_norm, k_norm, cos, sin, q_out, kv_cache, cache_location, (int)batch, (int)hq, (int)hkv, \
+                     (int)rot, (int)page_size, num_pages, eps)
+  if (epl == 1) AXK_PREP(1);
+  else if (epl == 2) AXK_PREP(2);
+  else if (epl == 4) AXK_PREP(4);
+  else AXK_PREP(8);
+#undef AXK_PREP
+  return axk_launch_status();
 }

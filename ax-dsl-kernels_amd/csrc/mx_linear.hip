@@ -109,6 +109,12 @@ struct MxGroup {
   const uint16_t* res;  // EPI_RES: the residual [M, n] (leading dimension ldr)
   int64_t ldr;
   int out_f32;
+  // optional on matrix 0 (EPI_PLAIN): causal conv1d + SiLU over its bf16 output, one token per row, with the
+  // conv state [M, conv_k - 1, n[0]] (conv_out may be conv_in)
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  int conv_k;
 };
 
 // Matrix and local tile of workgroup slot t.
@@ -257,6 +263,21 @@ __global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16
       v = silu_f32(round_bf16(v)) * round_bf16(up);
     } else if (EPI == EPI_RES) {
       v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
+    } else if (g.conv_w && mi == 0) {  // the token enters the channel's conv window (q35_step.py:164)
+      const int kc = g.conv_k;
+      const int64_t C = g.n[0];
+      const float xt = round_bf16(v);
+      float wk[kMaxConvTaps], hist[kMaxConvTaps];
+#pragma unroll
+      for (int j = 0; j < kMaxConvTaps; ++j) {
+        wk[j] = j < kc ? bf16_bits_to_f32(g.conv_w[nn * kc + j]) : 0.f;
+        hist[j] = j < kc - 1 ? bf16_bits_to_f32(g.conv_in[((int64_t)m * (kc - 1) + j) * C + nn]) : 0.f;
+      }
+      v = silu_f32(conv_taps(xt, wk, hist, kc));
+#pragma unroll
+      for (int j = 0; j < kMaxConvTaps - 1; ++j)
+        if (j < kc - 1)
+          g.conv_out[((int64_t)m * (kc - 1) + j) * C + nn] = (uint16_t)f32_to_bf16_bits(j + 1 < kc - 1 ? hist[j + 1] : xt);
     }
     if (g.out_f32)
       reinterpret_cast<float*>(g.out[mi])[(int64_t)m * g.ldo[mi] + nn] = v;
@@ -324,7 +345,8 @@ int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, 
 // Checks a group and launches it. Matrices need whole 128-byte row segments (and 8-byte aligned MXFP4 scale rows).
 template <int F>
 int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int epi, const uint16_t* res,
-             int64_t ldr, const float* row_scale, int out_dtype, int64_t m, int64_t k, hipStream_t st) {
+             int64_t ldr, const float* row_scale, int out_dtype, int64_t m, int64_t k, const AxkConvEpi* conv,
+             hipStream_t st) {
   AXK_REQUIRE(a && mats, AXK_E_NULL);
   AXK_REQUIRE(count >= 1 && count <= AXK_MX_GROUP_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(epi == EPI_PLAIN || epi == EPI_SWIGLU || epi == EPI_RES, AXK_E_SHAPE);
@@ -334,8 +356,22 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   AXK_REQUIRE(lda >= k && lda % 8 == 0 && axk_aligned(a, 16), AXK_E_ALIGN);
   AXK_REQUIRE(out_dtype == AXK_DT_BF16 || out_dtype == AXK_DT_F32, AXK_E_DTYPE);
   AXK_REQUIRE(epi == EPI_PLAIN || out_dtype == AXK_DT_BF16, AXK_E_DTYPE);
+  if (conv) {  // the conv epilogue: matrix 0, plain bf16 outputs, one token per row
+    AXK_REQUIRE(conv->w && conv->state_in && conv->state_out, AXK_E_NULL);
+    AXK_REQUIRE(epi == EPI_PLAIN && out_dtype == AXK_DT_BF16 && conv->kernel >= 1 && conv->kernel <= kMaxConvTaps,
+                AXK_E_SHAPE);
+    const size_t sbytes = (size_t)m * (conv->kernel - 1) * mats[0].n * 2;
+    AXK_REQUIRE(conv->state_in == conv->state_out || !axk_overlap(conv->state_in, sbytes, conv->state_out, sbytes),
+                AXK_E_ALIAS);
+  }
   MxGroup g{};
   g.count = count;
+  if (conv) {
+    g.conv_w = conv->w;
+    g.conv_in = conv->state_in;
+    g.conv_out = conv->state_out;
+    g.conv_k = (int)conv->kernel;
+  }
   g.row_scale = row_scale;
   g.res = res;
   g.ldr = ldr;
@@ -393,7 +429,7 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   // staged group kernel when rows are whole 128-byte segments (and MXFP4 scale rows 8-byte aligned)
   if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 && (F != WF_MXFP4 || axk_aligned(ws, 8))) {
     const AxkMxMat mat{w, ws, col_scale, bias, out, n, n};
-    return mx_group<F>(a, lda, &mat, 1, EPI_PLAIN, nullptr, 0, row_scale, out_dtype, m, k, st);
+    return mx_group<F>(a, lda, &mat, 1, EPI_PLAIN, nullptr, 0, row_scale, out_dtype, m, k, nullptr, st);
   }
   constexpr int CH = 4 * WUnit<F>::V;
   const int64_t nc = (k + CH - 1) / CH;  // K chunks
@@ -415,10 +451,11 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
 
 int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int epi,
                  const uint16_t* res, int64_t ldr, const float* row_scale, int out_dtype, int64_t m, int64_t k,
-                 hipStream_t stream) {
-  if (fmt == AXK_MX_FP8) return mx_group<WF_FP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, stream);
+                 const AxkConvEpi* conv, hipStream_t stream) {
+  if (fmt == AXK_MX_FP8)
+    return mx_group<WF_FP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   if (fmt == AXK_MX_MXFP4)
-    return mx_group<WF_MXFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, stream);
+    return mx_group<WF_MXFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   return AXK_E_DTYPE;
 }
 
