@@ -193,7 +193,8 @@ __global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) q[t][h] = *reinterpret_cast<const axk_u32x4*>(src[t][h] + d * axk::kSegBytes);
+      for (int h = 0; h < 2; ++h)  // weights are read once: non-temporal
+        q[t][h] = __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(src[t][h] + d * axk::kSegBytes));
       if (F == axk::WF_MXFP4) sw[t] = *reinterpret_cast<const uint2*>(srow[t] + 8 * d);
     }
     axk_bf16x8 a[MT][2][U::STEPS];
