@@ -94,6 +94,11 @@ AXK_DEV void fp8x4_to_bf16(uint32_t w, __bf16* dst) {
 typedef unsigned int axk_u32x4 __attribute__((ext_vector_type(4)));
 typedef short axk_s16x4 __attribute__((ext_vector_type(4)));
 
+// Non-temporal 16-byte load and store (the nt cache policy) for streams touched once per launch: weights, the
+// recurrent state tile.
+AXK_DEV axk_u32x4 load_nt(const void* p) { return __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(p)); }
+AXK_DEV void store_nt(void* p, axk_u32x4 v) { __builtin_nontemporal_store(v, reinterpret_cast<axk_u32x4*>(p)); }
+
 // ds_read_b64_tr_b16: each lane gives the LDS address of 4 consecutive 16-bit values; in every group of 16 lanes,
 // lane i receives element i % 4 of the values of lanes i / 4, i / 4 + 4, i / 4 + 8 and i / 4 + 12 (one 64-bit
 // read per lane that transposes a 16 x 4 block of the group).

@@ -62,7 +62,10 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
   const float* sin = p.state_in + ((int64_t)b * p.NV + h) * kDK * kDV;
   float4 S[kRows];
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) S[r] = *reinterpret_cast<const float4*>(sin + (r0 + r) * kDV + c0);
+  for (int r = 0; r < kRows; ++r) {  // the tile is read once and written once: non-temporal
+    const axk_u32x4 u = load_nt(sin + (r0 + r) * kDV + c0);
+    S[r] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+  }
 
   const float a_log = p.a_log[h], dt_bias = p.dt_bias[h];
   const float qscale = rsqrtf((float)kDK);
@@ -160,7 +163,8 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
 
   float* sout = p.state_out + ((int64_t)b * p.NV + h) * kDK * kDV;
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) *reinterpret_cast<float4*>(sout + (r0 + r) * kDV + c0) = S[r];
+  for (int r = 0; r < kRows; ++r)
+    store_nt(sout + (r0 + r) * kDV + c0, axk_u32x4{__float_as_uint(S[r].x), __float_as_uint(S[r].y), __float_as_uint(S[r].z), __float_as_uint(S[r].w)});
 }
 
 }  // namespace

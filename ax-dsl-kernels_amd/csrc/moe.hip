@@ -575,15 +575,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)Fo - 1);
         const int64_t off = (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr);
-        bt.qg[h] = *reinterpret_cast<const axk_u32x4*>(gw + r * (H / 2) + off);
-        bt.qu[h] = *reinterpret_cast<const axk_u32x4*>(uw + r * (H / 2) + off);
+        bt.qg[h] = load_nt(gw + r * (H / 2) + off);  // expert weights: read once per step
+        bt.qu[h] = load_nt(uw + r * (H / 2) + off);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
-        bt.qg[j] = *reinterpret_cast<const axk_u32x4*>(gw + n * (H / 2) + kb / 2);
-        bt.qu[j] = *reinterpret_cast<const axk_u32x4*>(uw + n * (H / 2) + kb / 2);
+        bt.qg[j] = load_nt(gw + n * (H / 2) + kb / 2);
+        bt.qu[j] = load_nt(uw + n * (H / 2) + kb / 2);
         if (!WIDE) {
           bt.sg[j] = gs[n * (H / 32) + kb / 32];
           bt.su[j] = us[n * (H / 32) + kb / 32];
@@ -737,14 +737,13 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
       for (int h = 0; h < kBatchChunks; ++h) {
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)a.H - 1);
-        bt.q[h] = *reinterpret_cast<const axk_u32x4*>(dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) +
-                                                       16 * (lane % kStageLpr));
+        bt.q[h] = load_nt(dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr));
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
-        bt.q[j] = *reinterpret_cast<const axk_u32x4*>(dw + n * (K / 2) + kb / 2);
+        bt.q[j] = load_nt(dw + n * (K / 2) + kb / 2);
         if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
       }
     }
