@@ -289,7 +289,8 @@ __global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16
 
 // Exact E2M1 x E8M0 -> fp32. Lane-consecutive quads of 4 values: a wave's stores cover contiguous 1 KiB
 // (64 lanes x 16 bytes) and its code loads contiguous 128 bytes. A thread converts kDqQuads quads, 64 quads
-// apart, with every load issued before the first store. Requires K % 32 == 0 (rows are whole quads).
+// apart, with every load issued before the first store. Codes and output are streamed once (non-temporal).
+// Requires K % 32 == 0 (rows are whole quads).
 constexpr int kDqQuads = 4;
 __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __restrict__ codes,
                                                             const uint8_t* __restrict__ scales,
@@ -305,15 +306,16 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
     for (int j = 0; j < kDqQuads; ++j) {
       const int64_t q = min(q0 + 64 * j, total - 1);  // clamped: in bounds, never stored past total
       const int64_t n = q / qpr, kq = (q - n * qpr) << 2;
-      c[j] = *reinterpret_cast<const uint16_t*>(codes + n * (K >> 1) + (kq >> 1));
+      c[j] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(codes + n * (K >> 1) + (kq >> 1)));
       sc[j] = e8m0_to_f32(scales[n * (K >> 5) + (kq >> 5)]);
     }
 #pragma unroll
     for (int j = 0; j < kDqQuads; ++j) {
       const int64_t q = q0 + 64 * j;
       if (q < total)
-        reinterpret_cast<float4*>(out)[q] = make_float4(e2m1_to_f32(c[j]) * sc[j], e2m1_to_f32(c[j] >> 4) * sc[j],
-                                                        e2m1_to_f32(c[j] >> 8) * sc[j], e2m1_to_f32(c[j] >> 12) * sc[j]);
+        store_nt(out + 4 * q, axk_u32x4{__float_as_uint(e2m1_to_f32(c[j]) * sc[j]), __float_as_uint(e2m1_to_f32(c[j] >> 4) * sc[j]),
+                                        __float_as_uint(e2m1_to_f32(c[j] >> 8) * sc[j]),
+                                        __float_as_uint(e2m1_to_f32(c[j] >> 12) * sc[j])});
     }
   }
 }
