@@ -192,7 +192,7 @@ class GdnDecodeWorkload(Workload):
     """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
 
     name = "gdn_decode"
-    kernel = "gdn_recurrent_kernel"
+    kernel = "gdn_recurrent_kernel<false>"
     timing = "graph"
     traffic_profile = "gdn_decode_config2a_pmc.txt"
 
