@@ -8,7 +8,9 @@ Bars:
     (as the reference's own attention does) against an fp32 SDPA golden, and that difference passes through the
     o projection, the residual, the RMSNorm and the MLP (each of those ops meets the per-op bar in its own test);
   * the GDN state within the reference's temporal tolerance rel 5e-2 / abs 3e-3 (test_gdn_attn.py:711-712); the
-    conv state exact (it holds inputs); the KV rows written within the per-op bar, every other cache byte untouched.
+    conv state's shifted entries exact (moved inputs), its newest entry (this token's qkv projection output, a bf16
+    result of an fp32 sum) within the per-op bar; the KV rows written within the per-op bar, every other cache byte
+    untouched.
 """
 import pytest
 import torch
@@ -27,6 +29,12 @@ def _dev(w, dev):
     return {k: v.to(dev) for k, v in w.items()}
 
 
+def _check_conv(got, ref):
+    # [B, K-1, C]: entries 0 .. K-3 are the previous state shifted (exact); entry K-2 is the new token's projection
+    assert torch.equal(got[:, :-1].cpu(), ref[:, :-1])
+    torch.testing.assert_close(got[:, -1].float().cpu(), ref[:, -1].float(), **TOL)
+
+
 def _gdn_case(seed, b=3, nk=2, nv=4):
     g = torch.Generator().manual_seed(seed)
     w = configs.gdn_layer_weights(g, H, F, nk, nv)
@@ -36,14 +44,16 @@ def _gdn_case(seed, b=3, nk=2, nv=4):
     return w, x, st, cv
 
 
-@pytest.mark.parametrize("b,nk,nv", [(3, 2, 4), (1, 1, 2), (8, 2, 2)])
+# (2, 16, 32): config 4's heads, so the qkv | z | b | a projection group has 772 tiles and runs two tiles per
+# workgroup (with the conv epilogue); (20, 2, 4): more than 16 sequences, two 16-row M tiles per workgroup
+@pytest.mark.parametrize("b,nk,nv", [(3, 2, 4), (1, 1, 2), (8, 2, 2), (2, 16, 32), (20, 2, 4)])
 def test_gdn_layer_decode(dev, b, nk, nv):
     w, x, st, cv = _gdn_case(b + nk + nv, b, nk, nv)
     out, so, co = layer.gdn_layer_decode(x.to(dev), _dev(w, dev), st.to(dev), cv.to(dev), nk, nv)
     ro, rs, rc = olayer.gdn_layer_decode(x, w, st, cv, nk, nv)
     torch.testing.assert_close(out.float().cpu(), ro.float(), **TOL)
     torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
-    assert torch.equal(co.cpu(), rc)
+    _check_conv(co, rc)
 
 
 def test_gdn_layer_two_steps_in_place(dev):
@@ -58,10 +68,13 @@ def test_gdn_layer_two_steps_in_place(dev):
     torch.testing.assert_close(o1.float().cpu(), r1.float(), **TOL)
     torch.testing.assert_close(o2.float().cpu(), r2.float(), **TOL)
     torch.testing.assert_close(sd.cpu(), rs, **STATE_TOL)
-    assert torch.equal(cd.cpu(), rc)
+    _check_conv(cd, rc)
 
 
-@pytest.mark.parametrize("lens,hq,hkv,rot", [([100, 64, 300], 4, 2, 64), ([1, 127], 8, 2, 64), ([640], 4, 4, 0)])
+# hq = 32, hkv = 4: config 4's heads (the q | k | v group has 1152 tiles: two per workgroup); 20 sequences: two
+# 16-row M tiles per workgroup in every projection
+@pytest.mark.parametrize("lens,hq,hkv,rot", [([100, 64, 300], 4, 2, 64), ([1, 127], 8, 2, 64), ([640], 4, 4, 0),
+                                             ([70, 200], 32, 4, 64), ([17 + 9 * i for i in range(20)], 4, 2, 64)])
 def test_attn_layer_decode(dev, lens, hq, hkv, rot):
     g = torch.Generator().manual_seed(len(lens) * 7 + hq)
     d = 256
