@@ -624,7 +624,10 @@ WsView ws_view(void* ws, int batch, int hkv, int group, int d) {
           reinterpret_cast<float*>(w + om), reinterpret_cast<float*>(w + ol), reinterpret_cast<float*>(w + oo)};
 }
 
-constexpr int kBlocksPerCU = 3;  // resident split workgroups per CU (LDS-bound: 3 x 3 tiles x 16.5 KiB)
+// Split workgroups per CU (and the plan's slot count per CU). Two, not the three that LDS would allow: fewer,
+// larger items carry fewer per-item prologues and fp32 partials (measured, config 1: 55.7 us with three per CU,
+// 51.7 us with two, 73.8 us with one).
+constexpr int kBlocksPerCU = 2;
 
 // Compute units of the current device (cached per device).
 int device_cu_count() {
