@@ -29,6 +29,19 @@ def config0(seed: int = 0):
     return {"x": x, "w": codes, "s": scales}
 
 
+LM_HEAD = {"vocab": 248320, "hidden": 2048}  # mul_mat_mx4_n248320_k2048 (tools/manifest/mkmanifest.py:42)
+
+
+def lm_head_case(dev, seed: int = 0, n: int = LM_HEAD["vocab"], k: int = LM_HEAD["hidden"], m: int = 1):
+    """The MXFP4 LM head GEMV (decode): W [n, k] as config 0's weight (uniform nibbles, E8M0 bytes in 119..123),
+    x bf16 [m, k] ~ N(0,1), fp32 logits. Generated on `dev` (a 270 MB weight at the full vocabulary)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    codes = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8, device=dev)
+    scales = torch.randint(119, 124, (n, k // 32), generator=g, dtype=torch.uint8, device=dev)
+    x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+    return {"x": x, "w": pack_codes(codes).contiguous(), "s": scales.contiguous()}
+
+
 def paged_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator, extra_pages: int = 0):
     """A paged KV pool holding sequences of the given lengths, pages placed by a random permutation."""
     npages = [(L + page - 1) // page for L in lens]

@@ -142,12 +142,15 @@ AXK_DEV void slot_tile(const MxGroup& g, int t, int& mi, int& lt, bool& valid) {
 // activation fragments, which every tile reuses; each tile goes through the wave's LDS tile into the MFMA layout
 // (lane (nl, g): 16-byte unit g of each 64-byte chunk), so the k mapping is the unstaged kernel's. LDS is
 // wave-private and in order: no barrier until the cross-wave sum.
-template <int F, int MT, int NT, int EPI>
-__global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                     const MxGroup g, int M, int64_t K) {
+// Occupancy: the 4-wave form (four tiles) is held to at least 4 waves per SIMD, what its LDS allows; left to
+// itself the compiler spends enough registers to drop it to 3 (measured on the LM head: 59.5 against 44 us). The
+// 8-wave forms keep the compiler's choice (forcing more waves there spills).
+template <int F, int MT, int NT, int EPI, int WMAX = kGroupWaves>
+__global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX == 4 ? 4 : 1))) void mx_group_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const MxGroup g, int M, int64_t K) {
   using U = axk::WUnit<F>;
   constexpr int CH = 4 * U::V, SEGK = 2 * CH;  // values per 64-byte chunk, per 128-byte segment
-  constexpr int kTileBytes = kGroupWaves * NT * 16 * axk::kSegLd, kRedBytes = kGroupWaves * NT * MT * 4 * 64 * 4;
+  constexpr int kTileBytes = WMAX * NT * 16 * axk::kSegLd, kRedBytes = WMAX * NT * MT * 4 * 64 * 4;
   __shared__ __align__(16) unsigned char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
   float* red = reinterpret_cast<float*>(smem);
 
@@ -236,22 +239,17 @@ __global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16
       for (int r = 0; r < 4; ++r) red[(((wave * NT + t) * MT + u) * 4 + r) * 64 + lane] = acc[t][u][r];
   __syncthreads();
 
-  // element e of slot t, M tile u: row m0 + 16u + 4(l / 16) + r, channel 16 lt + l % 16
+  // element (u, r, l) of slot t: row m0 + 16u + 4(l / 16) + r, channel 16 lt + l % 16 of matrix mi
   auto total = [&](int t, int u, int r, int l) {
     float v = 0.f;
     for (int wv = 0; wv < nwaves; ++wv) v += red[(((wv * NT + t) * MT + u) * 4 + r) * 64 + l];
     return v;
   };
-  constexpr int kOutSlots = EPI == EPI_SWIGLU ? NT / 2 : NT;
-  for (int idx = threadIdx.x; idx < kOutSlots * MT * 256; idx += blockDim.x) {
-    const int o = idx / (MT * 256), u = (idx >> 8) % MT, r = (idx >> 6) & 3, l = idx & 63;
+  auto emit = [&](int t, int mi, int lt, int e) {
+    const int u = e >> 8, r = (e >> 6) & 3, l = e & 63;
     const int m = m0 + u * 16 + 4 * (l >> 4) + r;
-    const int t = EPI == EPI_SWIGLU ? 2 * o : o;
-    int mi, lt;
-    bool valid;
-    slot_tile<NT, EPI>(g, t, mi, lt, valid);
-    const int64_t nn = (int64_t)lt * 16 + (l & 15);
-    if (!valid || m >= M || nn >= g.n[mi]) continue;
+    const int64_t nn = (int64_t)lt * 16 + (l & 15), n_i = g.n[mi];
+    if (m >= M || nn >= n_i) return;
     float v = total(t, u, r, l);
     if (g.row_scale) v *= g.row_scale[m];
     if (g.col_scale[mi]) v *= g.col_scale[mi][nn];
@@ -266,24 +264,45 @@ __global__ __launch_bounds__(64 * kGroupWaves) void mx_group_kernel(const uint16
       v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
     } else if (g.conv_w && mi == 0) {  // the token enters the channel's conv window (q35_step.py:164)
       const int kc = g.conv_k;
-      const int64_t C = g.n[0];
       const float xt = round_bf16(v);
       float wk[kMaxConvTaps], hist[kMaxConvTaps];
 #pragma unroll
       for (int j = 0; j < kMaxConvTaps; ++j) {
         wk[j] = j < kc ? bf16_bits_to_f32(g.conv_w[nn * kc + j]) : 0.f;
-        hist[j] = j < kc - 1 ? bf16_bits_to_f32(g.conv_in[((int64_t)m * (kc - 1) + j) * C + nn]) : 0.f;
+        hist[j] = j < kc - 1 ? bf16_bits_to_f32(g.conv_in[((int64_t)m * (kc - 1) + j) * n_i + nn]) : 0.f;
       }
       v = silu_f32(conv_taps(xt, wk, hist, kc));
 #pragma unroll
       for (int j = 0; j < kMaxConvTaps - 1; ++j)
         if (j < kc - 1)
-          g.conv_out[((int64_t)m * (kc - 1) + j) * C + nn] = (uint16_t)f32_to_bf16_bits(j + 1 < kc - 1 ? hist[j + 1] : xt);
+          g.conv_out[((int64_t)m * (kc - 1) + j) * n_i + nn] = (uint16_t)f32_to_bf16_bits(j + 1 < kc - 1 ? hist[j + 1] : xt);
     }
     if (g.out_f32)
       reinterpret_cast<float*>(g.out[mi])[(int64_t)m * g.ldo[mi] + nn] = v;
     else
       reinterpret_cast<uint16_t*>(g.out[mi])[(int64_t)m * g.ldo[mi] + nn] = (uint16_t)f32_to_bf16_bits(v);
+  };
+  constexpr int kOutSlots = EPI == EPI_SWIGLU ? NT / 2 : NT;
+  if constexpr (WMAX == 4) {
+    // the four-tile form (short-lived workgroups): slots unrolled, each slot's matrix resolved once (measured on
+    // the LM head: 58.9 -> 52 us); the eight-wave forms keep the compact loop (smaller code, measured faster there)
+#pragma unroll
+    for (int o = 0; o < kOutSlots; ++o) {
+      const int t = EPI == EPI_SWIGLU ? 2 * o : o;
+      int mi, lt;
+      bool valid;
+      slot_tile<NT, EPI>(g, t, mi, lt, valid);
+      if (!valid) continue;  // uniform
+      for (int e = threadIdx.x; e < MT * 256; e += blockDim.x) emit(t, mi, lt, e);
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < kOutSlots * MT * 256; idx += blockDim.x) {
+      const int o = idx / (MT * 256), t = EPI == EPI_SWIGLU ? 2 * o : o;
+      int mi, lt;
+      bool valid;
+      slot_tile<NT, EPI>(g, t, mi, lt, valid);
+      if (valid) emit(t, mi, lt, idx - o * (MT * 256));
+    }
   }
 }
 
@@ -320,19 +339,27 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
   }
 }
 
-template <int F, int MT, int NT, int EPI>
+template <int F, int MT, int NT, int EPI, int WMAX = kGroupWaves>
 void launch_group(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, int64_t k, int64_t slots,
                   hipStream_t st) {
   const int64_t nd = axk::row_bytes<F>(k) / axk::kSegBytes;
-  const int waves = (int)(nd < kGroupWaves ? nd : kGroupWaves);
+  const int waves = (int)(nd < WMAX ? nd : WMAX);
   dim3 grid((unsigned)((slots + NT - 1) / NT), (unsigned)((m + 16 * MT - 1) / (16 * MT)));
-  hipLaunchKernelGGL((mx_group_kernel<F, MT, NT, EPI>), grid, dim3(64 * waves), 0, st, a, lda, g, (int)m, k);
+  hipLaunchKernelGGL((mx_group_kernel<F, MT, NT, EPI, WMAX>), grid, dim3(64 * waves), 0, st, a, lda, g, (int)m, k);
 }
 
 template <int F, int EPI>
 int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, int64_t k, hipStream_t st) {
   const int tiles = g.tile0[g.count];
   const int64_t slots = EPI == EPI_SWIGLU ? 2 * (int64_t)g.tile0[1] : tiles;
+  // short rows (<= 8 segments) of a very wide matrix (the LM head): four tiles and four waves per workgroup, so a
+  // wave streams two segments of four tiles (measured on 248320 x 2048 MXFP4: 60 -> 44 us against two tiles and
+  // eight waves)
+  const int64_t nd = axk::row_bytes<F>(k) / axk::kSegBytes;
+  if (EPI == EPI_PLAIN && m <= 16 && nd <= 8 && tiles >= 4096) {
+    launch_group<F, 1, 4, EPI, 4>(a, lda, g, m, k, slots, st);
+    return axk_launch_status();
+  }
   // two tiles per workgroup when that still leaves >= 384 workgroups per M tile (a SwiGLU pair always)
   const bool two = EPI == EPI_SWIGLU || tiles >= 768;
   if (m <= 16) {

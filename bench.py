@@ -105,6 +105,54 @@ class MxLinearWorkload(Workload):
                 "sample": f"full config0 op (oracle/mx_codec.c, OpenMP), median of {reps} runs"}
 
 
+class LmHeadWorkload(Workload):
+    """The MXFP4 LM head GEMV of decode (SURVEY next row): W [248320, 2048] (E2M1 + E8M0, config 0's encoding),
+    x bf16 [1, 2048], fp32 logits (mul_mat_mx4_n248320_k2048, q35_layer_mc.py:705-724)."""
+
+    name = "lm_head"
+    kernel = "mx_group_kernel<0, 1, 4, 0, 4>"
+    timing = "graph"
+    traffic_profile = "lm_head_vocab248320_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        self.m, self.n, self.k = 1, configs.LM_HEAD["vocab"], configs.LM_HEAD["hidden"]
+        per_copy = self.n * self.k // 2 + self.n * self.k // 32
+        # algorithmic bytes per launch: codes + scales + x + fp32 logits
+        self.alg_bytes = per_copy + 2 * self.m * self.k + 4 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        self.copies = max(2, -(-ROTATE_BYTES // per_copy))
+        c = [configs.lm_head_case(dev, seed=i) for i in range(self.copies)]
+        self.w, self.s, self.x = [ci["w"] for ci in c], [ci["s"] for ci in c], c[0]["x"]
+        self.out = torch.empty(self.m, self.n, dtype=torch.float32, device=dev)
+        self.config = {"workload": f"MXFP4 LM head GEMV N={self.n} K={self.k} M=1, fp32 logits",
+                       "rotating_copies": self.copies}
+        self.dtype = "mxfp4 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import torch
+
+        import axk
+
+        j = i % self.copies
+        axk.mxfp4_gemm(self.x, self.w[j], self.s[j], out_dtype=torch.float32, output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        from oracle import _c
+
+        rows = 16384  # a bounded sample of the vocabulary's rows, scaled to the whole head
+        x = self.x.cpu().view(__import__("torch").int16).numpy().view("u2")
+        w, s = self.w[0][:rows].cpu().numpy(), self.s[0][:rows].cpu().numpy()
+        nt = _cpu_threads()
+        sec, reps = _time_cpu(lambda: _c.mxfp4_linear(x, w, s, nthreads=nt))
+        return {"value": sec * 1e6 * self.n / rows, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"{rows} of the {self.n} rows (oracle/mx_codec.c, OpenMP), median of {reps} runs, "
+                          f"scaled by rows"}
+
+
 class PagedDecodeWorkload(Workload):
     """Config 1: paged decode attention, batch 16, 16 q / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384].
 
@@ -662,6 +710,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
+             LmHeadWorkload.name: LmHeadWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 

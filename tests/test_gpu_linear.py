@@ -123,3 +123,30 @@ def test_bf16_gemm_matches_oracle(dev, m, n, k):
     ref = a.float() @ w.float().T
     got = axk.bf16_gemm(a.to(dev), w.to(dev), out_dtype=torch.float32)
     torch.testing.assert_close(got.cpu(), ref, **F32_TOL)
+
+
+def test_lm_head_vocab_gemv(dev):
+    """The MXFP4 LM head at the full vocabulary (248320 x 2048, fp32 logits), M = 1 and the 4 rows of a
+    speculative verify: against an fp32 matmul on the GPU over the bit-exact dequantised weight (the oracle's
+    formula; the exhaustive codec tests pin the dequant), at the bf16-output bar."""
+    from axk import configs
+
+    c = configs.lm_head_case(dev, seed=3, m=4)
+    wf = axk.mxfp4_dequant(c["w"], c["s"])  # [N, K] fp32, exact
+    for m in (1, 4):
+        x = c["x"][:m].contiguous()
+        got = axk.mxfp4_gemm(x, c["w"], c["s"], out_dtype=torch.float32)
+        ref = (wf @ x.float().t().contiguous()).t()  # contiguous right operand
+        torch.testing.assert_close(got, ref, rtol=2e-2, atol=1e-2)
+    del wf
+
+
+def test_lm_head_rows_against_oracle(dev):
+    """A slice of LM-head rows (n not a multiple of the 16-row tile) against the CPU oracle, fp32 out."""
+    from axk import configs
+    from oracle import mx
+
+    c = configs.lm_head_case(dev, seed=4, n=3000, m=1)
+    got = axk.mxfp4_gemm(c["x"], c["w"], c["s"], out_dtype=torch.float32).cpu()
+    ref = mx.mx_linear(c["x"].cpu(), c["w"].cpu().numpy(), c["s"].cpu().numpy())
+    torch.testing.assert_close(got, ref.float(), rtol=2e-2, atol=1e-2)
