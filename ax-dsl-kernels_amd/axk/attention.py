@@ -30,10 +30,10 @@ def paged_decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, hea
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
-def _check_decode(q, kv_cache, indptr, indices, last_page_len):
+def _check_decode(q, kv_cache, indptr, indices, last_page_len, kv_dtype=torch.bfloat16):
     _check(q.dim() == 3 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [B, HQ, D]")
-    _check(kv_cache.dim() == 5 and kv_cache.dtype == torch.bfloat16 and kv_cache.is_contiguous(),
-           "kv_cache must be contiguous bf16 [pages, 2, page_size, HKV, D]")
+    _check(kv_cache.dim() == 5 and kv_cache.dtype == kv_dtype and kv_cache.is_contiguous(),
+           f"kv_cache must be contiguous {kv_dtype} [pages, 2, page_size, HKV, D]")
     b, hq, d = q.shape
     p, two, page, hkv, d2 = kv_cache.shape
     _check(two == 2 and d2 == d, f"kv_cache shape {tuple(kv_cache.shape)} does not match q {tuple(q.shape)}")
@@ -124,4 +124,68 @@ def store_paged_kv(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor, cac
     _lib.call(
         "axk_paged_kv_write", k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(), loc.data_ptr(), b, hkv, d, page, p,
         _lib.ptr(status), _lib.stream_of(k),
+    )
+
+
+def _check_kv_scale(kv_scale: float) -> None:
+    m, e = math.frexp(kv_scale)
+    _check(kv_scale > 0 and m == 0.5, f"kv_scale {kv_scale} must be a power of two")
+
+
+def paged_decode_fp8(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    indptr: torch.Tensor,
+    indices: torch.Tensor,
+    last_page_len: torch.Tensor,
+    kv_scale: float,
+    sm_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """paged_decode over an FP8 cache (q35_group.py:44-54, KV8=2): kv_cache u8 (or float8_e4m3fn) [P, 2, page, HKV,
+    D] holding e4m3(bf16(x * kv_scale)); attention reads stored / kv_scale. kv_scale: a power of two; D 128 or 256."""
+    if kv_cache.dtype == torch.float8_e4m3fn:
+        kv_cache = kv_cache.view(torch.uint8)
+    _check(kv_cache.dtype == torch.uint8, "kv_cache must be u8 / float8_e4m3fn")
+    b, hq, hkv, d, page, p = _check_decode(q, kv_cache, indptr, indices, last_page_len, kv_dtype=torch.uint8)
+    _check(d in (128, 256), f"head_dim {d} not supported with an FP8 cache (128, 256)")
+    _check_kv_scale(kv_scale)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    if workspace is None:
+        workspace = paged_decode_workspace(b, hq, hkv, d, q.device)
+    _lib.require_device(q, kv_cache, indptr, indices, last_page_len, output, workspace)
+    _lib.call(
+        "axk_paged_decode_fp8", q.data_ptr(), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
+        last_page_len.data_ptr(), output.data_ptr(), b, hq, hkv, d, page, p, float(sm_scale), float(kv_scale),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q),
+    )
+    return output
+
+
+def store_paged_kv_fp8(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor, cache_location: torch.Tensor,
+                       kv_scale: float, status: Optional[torch.Tensor] = None) -> None:
+    """store_paged_kv into an FP8 cache: the bytes at cache_location[b] become e4m3(bf16(x * kv_scale)) for
+    x = k[b] (plane 0) and v[b] (plane 1) (q35_group.py:244-247)."""
+    if kv_cache.dtype == torch.float8_e4m3fn:
+        kv_cache = kv_cache.view(torch.uint8)
+    _check(k.shape == v.shape and k.dim() == 3 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+           "k and v must be bf16 [B, HKV, D]")
+    _check(kv_cache.dtype == torch.uint8 and kv_cache.dim() == 5, "kv_cache must be u8 [P, 2, page, HKV, D]")
+    _check(k.is_contiguous() and v.is_contiguous() and kv_cache.is_contiguous(), "tensors must be contiguous")
+    _check_kv_scale(kv_scale)
+    b, hkv, d = k.shape
+    p, two, page, hkv2, d2 = kv_cache.shape
+    _check(two == 2 and hkv2 == hkv and d2 == d, "kv_cache shape does not match k / v")
+    loc = cache_location.reshape(-1, 2) if cache_location.numel() == 2 * b else None
+    _check(loc is not None and cache_location.dtype == torch.int32 and loc.is_contiguous(),
+           "cache_location must be int32 [B, 2] = (page, offset)")
+    _lib.require_device(k, v, kv_cache, loc, status)
+    _lib.call(
+        "axk_paged_kv_write_fp8", k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(), loc.data_ptr(), b, hkv, d, page,
+        p, float(kv_scale), _lib.ptr(status), _lib.stream_of(k),
     )

@@ -161,20 +161,47 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
   }
 }
 
-template <int D>
+// KB: bytes per cached K / V element (2: bf16; 1: FP8 E4M3 with a static scale, landed in LDS as stored and
+// converted to the bf16 layout before use).
+template <int D, int KB = 2>
 struct PagedCfg {
   static constexpr int KSTEPS = D / 32;       // 16x16x32 MFMA k-steps over the head dim (QK)
   static constexpr int DW = D / kWaves;       // head-dim columns of O owned by one wave
   static constexpr int DT = DW / 16;          // 16-wide O tiles per wave
-  static constexpr int RPI = 512 / D;         // rows per direct-to-LDS instruction (64 lanes x 16 B)
+  static constexpr int RB = D * KB;           // bytes per cached row of one KV head
+  static constexpr int RPI = 1024 / RB;       // rows per direct-to-LDS instruction (64 lanes x 16 B)
   static constexpr int IPP = kTile / RPI;     // instructions per plane (K or V) of a tile
   static constexpr int IPW = 2 * IPP / kWaves;  // instructions per wave per tile
-  static constexpr int PAD = D == 256 ? 32 : 64;  // bytes after each 1 KiB block (bank spread for V reads)
+  static_assert(IPW >= 1 && IPW * kWaves == 2 * IPP, "a tile's loads split evenly over the waves");
+  // bytes after each 1 KiB block (bank spread for the transposing V reads of the bf16 layout; FP8 landing slots are
+  // only read row-wise)
+  static constexpr int PAD = KB == 1 ? 0 : (D == 256 ? 32 : 64);
   static constexpr int BLK = 1024 + PAD;
   static constexpr int PLANE = IPP * BLK;     // one plane of a tile in LDS
   static constexpr int BUF = 2 * PLANE;       // one tile (K then V)
-  static AXK_DEV int row_off(int tok) { return (tok / RPI) * BLK + (tok % RPI) * (2 * D); }
+  static AXK_DEV int row_off(int tok) { return (tok / RPI) * BLK + (tok % RPI) * RB; }
 };
+
+// Software FP32 -> E4M3 (OCP e4m3fn) with round-to-nearest-even, as torch's float8_e4m3fn cast: |v| > 464
+// (rounding to 480, past the largest finite value 448) and NaN give NaN (0x7F with the sign), values under
+// 2^-6 round onto the subnormal grid m * 2^-9.
+AXK_DEV uint32_t f32_to_e4m3(float v) {
+  const uint32_t u = __float_as_uint(v), sgn = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+  const float av = __uint_as_float(a);
+  if (a > 0x7f800000u || av > 464.0f) return sgn | 0x7fu;
+  const int e = (int)(a >> 23) - 127;
+  if (e < -6) return sgn | (uint32_t)rintf(av * 512.0f);  // 0 .. 8 (8 = the smallest normal, code 0x08)
+  const uint32_t mant = a & 0x7fffffu;
+  uint32_t m3 = mant >> 20, ex = (uint32_t)(e + 7);
+  const uint32_t rb = (mant >> 19) & 1u, sticky = mant & 0x7ffffu;
+  if (rb && (sticky || (m3 & 1u))) {
+    if (++m3 == 8u) {
+      m3 = 0u;
+      ++ex;
+    }
+  }
+  return sgn | (ex << 3) | m3;
+}
 
 // LDS byte address of a __shared__ pointer (for M0).
 AXK_DEV uint32_t lds_addr(const void* p) {
@@ -271,14 +298,19 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
 // (each wave issues a quarter of its loads) into a ring of kNBuf buffers, two tiles ahead of the one being
 // computed. Every wave computes the full scores S^T = K Q^T of the tile (cheap on MFMA) and the online
 // softmax, then P x V for its own quarter of the head dim, so no cross-wave merge is needed.
-template <int D>
+// KB = 1 (FP8 cache): each landed tile is converted by the four waves (a quarter of its 1 KiB blocks each, scaled by
+// inv_scale, exact for a power-of-two scale) into a bf16 staging tile of the bf16 layout, behind one more barrier;
+// the compute below then reads the staging tile.
+template <int D, int KB>
 __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
-                                            const uint16_t* __restrict__ cache, const int* __restrict__ indices,
+                                            const unsigned char* __restrict__ cache, const int* __restrict__ indices,
                                             int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                                            PlanHeader* __restrict__ hdr, float* __restrict__ part_m,
-                                            float* __restrict__ part_l, float* __restrict__ part_o,
-                                            uint16_t* __restrict__ out, unsigned char* smem) {
-  using C = PagedCfg<D>;
+                                            float inv_scale, PlanHeader* __restrict__ hdr,
+                                            float* __restrict__ part_m, float* __restrict__ part_l,
+                                            float* __restrict__ part_o, uint16_t* __restrict__ out,
+                                            unsigned char* smem) {
+  using C = PagedCfg<D>;      // the compute layout (bf16)
+  using L = PagedCfg<D, KB>;  // the landing layout of the cached bytes
   const int group = hq / hkv;
   const int b = desc.b, kvh = desc.kvh, nsplit = desc.nsplit;
   const int tpp = page_size / kTile;  // tiles per page
@@ -287,7 +319,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const float c = sm_scale * kLog2e;
-  const int64_t row_stride = (int64_t)hkv * D;  // elements between consecutive tokens
+  const int64_t row_stride = (int64_t)hkv * D * KB;  // bytes between consecutive tokens
   const int64_t plane_stride = (int64_t)page_size * row_stride;
   const uint32_t lds0 = lds_addr(smem);
 
@@ -310,7 +342,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 
   // tile ti -> valid tokens and K base (both wave-uniform: scalar registers); a tile past the sequence end
   // or on a page outside the pool gets nvalid = 0 and an in-bounds base
-  auto locate = [&](int ti, int& nvalid) -> const uint16_t* {
+  auto locate = [&](int ti, int& nvalid) -> const unsigned char* {
     const int lp = ti / tpp, tp = ti - lp * tpp;
     if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
       chunk = lp >> 6;
@@ -326,32 +358,32 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       page = 0;
       nvalid = 0;
     }
-    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + kvh * D;
+    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * D * KB;
   };
   // per-lane element offsets of this wave's loads inside a tile (token row, plane, 16-byte chunk), and the
   // same offsets clamped to row 0 for rows past nvalid
-  int lane_tok[C::IPW];
-  int64_t lane_off[C::IPW], lane_off0[C::IPW];
+  int lane_tok[L::IPW];
+  int64_t lane_off[L::IPW], lane_off0[L::IPW];  // bytes
 #pragma unroll
-  for (int k = 0; k < C::IPW; ++k) {
-    const int j = wave * C::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
-    const int plane = j / C::IPP, blk = j - plane * C::IPP;
-    lane_tok[k] = blk * C::RPI + lane / (D / 8);
-    lane_off0[k] = plane * plane_stride + (lane % (D / 8)) * 8;
+  for (int k = 0; k < L::IPW; ++k) {
+    const int j = wave * L::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
+    const int plane = j / L::IPP, blk = j - plane * L::IPP;
+    lane_tok[k] = blk * L::RPI + lane / (L::RB / 16);
+    lane_off0[k] = plane * plane_stride + (lane % (L::RB / 16)) * 16;
     lane_off[k] = lane_off0[k] + (int64_t)lane_tok[k] * row_stride;
   }
   // this wave's share of tile ti's loads into ring buffer nb (rows past nvalid re-read row 0); returns the
   // tile's valid token count
   auto issue = [&](int ti, int nb) -> int {
     int nvalid;
-    const uint16_t* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
+    const unsigned char* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
     const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
 #pragma unroll
-    for (int k = 0; k < C::IPW; ++k) {
-      const int j = wave * C::IPW + k;
-      const int plane = j / C::IPP, blk = j - plane * C::IPP;
+    for (int k = 0; k < L::IPW; ++k) {
+      const int j = wave * L::IPW + k;
+      const int plane = j / L::IPP, blk = j - plane * L::IPP;
       lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
-                lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK);
+                lds0 + nb * L::BUF + plane * L::PLANE + blk * L::BLK);
     }
     return ti < ntiles ? nvalid : 0;
   };
@@ -362,18 +394,8 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g and over the waves)
 
-  int nv0 = issue(0, 0);  // valid tokens of tiles ti, ti + 1, ti + 2
-  int nv1 = issue(1, 1);
-  for (int ti = 0; ti < ntiles; ++ti) {
-    const int nb = ti % kNBuf;
-    wait_vmcnt<C::IPW>();              // this wave's loads of tile ti have landed (tile ti + 1 may not)
-    __builtin_amdgcn_s_barrier();      // ... and every other wave's; all are done with tile ti - 1
-    const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);  // into the buffer of tile ti - 1
-    const int nvalid = nv0;
-    nv0 = nv1;
-    nv1 = nv2;
-    if (nvalid <= 0) continue;  // wave-uniform
-    const unsigned char* kt = smem + nb * C::BUF;
+  // the math of one tile from its bf16 K / V in LDS (kt: K plane; V plane at kt + PLANE), nvalid > 0 tokens
+  auto tile_math = [&](const unsigned char* kt, int nvalid) {
     const unsigned char* vt = kt + C::PLANE;
     // S^T (16 tokens x 16 heads): A = K rows (lane: token l16, d = 32s + 8g .. +8); lane holds
     // S[token 4g + r][head l16]
@@ -417,6 +439,71 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       }
       o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
     }
+  };
+
+  if constexpr (KB == 2) {
+    int nv0 = issue(0, 0);  // valid tokens of tiles ti, ti + 1, ti + 2
+    int nv1 = issue(1, 1);
+    for (int ti = 0; ti < ntiles; ++ti) {
+      const int nb = ti % kNBuf;
+      wait_vmcnt<C::IPW>();              // this wave's loads of tile ti have landed (tile ti + 1 may not)
+      __builtin_amdgcn_s_barrier();      // ... and every other wave's; all are done with tile ti - 1
+      const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);  // into the buffer of tile ti - 1
+      const int nvalid = nv0;
+      nv0 = nv1;
+      nv1 = nv2;
+      if (nvalid > 0) tile_math(smem + nb * C::BUF, nvalid);  // uniform over the workgroup
+    }
+  } else {
+    // FP8: tiles land kAhead8 ahead in a ring of kAhead8 + 1 slots (an FP8 tile is half a bf16 one, so twice the
+    // look-ahead keeps as many bytes in flight), and two bf16 staging tiles. Iteration ti: wait for tile ti + 1, one
+    // fenced barrier (every wave's loads of ti + 1 landed, the conversion of ti done, the math of ti - 1 done), issue
+    // tile ti + kAhead8 into the slot of tile ti - 1, convert tile ti + 1 into the staging tile ti - 1 used, then
+    // the math of tile ti.
+    constexpr int kAhead8 = 4, kNBuf8 = kAhead8 + 1;
+    unsigned char* stage = smem + kNBuf8 * L::BUF;
+    auto convert = [&](int slot, unsigned char* dst_tile) {
+      // wave w converts 1 KiB blocks c = w, w + 4, ...: lane l's 16 stored bytes of row blk RPI + l / (RB / 16)
+#pragma unroll
+      for (int c = wave; c < 2 * L::IPP; c += kWaves) {
+        const int plane = c / L::IPP, blk = c - plane * L::IPP;
+        const int row = blk * L::RPI + lane / (L::RB / 16), col = (lane % (L::RB / 16)) * 16;
+        const axk_u32x4 f8 =
+            *reinterpret_cast<const axk_u32x4*>(smem + slot * L::BUF + plane * L::PLANE + blk * L::BLK + 16 * lane);
+        axk_u32x4 lo, hi;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t b0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(f8[w], inv_scale, false));
+          const uint32_t b1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(f8[w], inv_scale, true));
+          if (w < 2) {
+            lo[2 * w] = b0;
+            lo[2 * w + 1] = b1;
+          } else {
+            hi[2 * w - 4] = b0;
+            hi[2 * w - 3] = b1;
+          }
+        }
+        unsigned char* dst = dst_tile + plane * C::PLANE + C::row_off(row) + 2 * col;
+        *reinterpret_cast<axk_u32x4*>(dst) = lo;
+        *reinterpret_cast<axk_u32x4*>(dst + 16) = hi;
+      }
+    };
+    int nv[kAhead8];  // valid tokens of tiles ti .. ti + kAhead8 - 1 (nv[j]: tile ti + j)
+#pragma unroll
+    for (int j = 0; j < kAhead8; ++j) nv[j] = issue(j, j);
+    wait_vmcnt<(kAhead8 - 1) * L::IPW>();  // tile 0 has landed
+    __syncthreads();
+    if (nv[0] > 0) convert(0, stage);
+    for (int ti = 0; ti < ntiles; ++ti) {
+      wait_vmcnt<(kAhead8 - 2) * L::IPW>();  // tile ti + 1 has landed (later ones may not)
+      __syncthreads();  // a fence with the barrier: LDS written by other waves is read after it
+      const int nvn = issue(ti + kAhead8, (ti + kAhead8) % kNBuf8);  // into the slot of tile ti - 1 (converted)
+      if (nv[1] > 0) convert((ti + 1) % kNBuf8, stage + ((ti + 1) & 1) * C::BUF);
+      if (nv[0] > 0) tile_math(stage + (ti & 1) * C::BUF, nv[0]);
+#pragma unroll
+      for (int j = 0; j + 1 < kAhead8; ++j) nv[j] = nv[j + 1];
+      nv[kAhead8 - 1] = nvn;
+    }
   }
   wait_vmcnt<0>();  // drain the two look-ahead tiles before the buffers are reused
   __builtin_amdgcn_s_barrier();
@@ -450,11 +537,11 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 // Persistent split kernel: a few workgroups per CU; workgroup w takes items w, w + gridDim.x, ... (the plan
 // sizes the items to about one per workgroup). With local != 0 the descriptors come from the page table
 // directly (local_plan), otherwise from the plan in the workspace.
-template <int D>
+template <int D, int KB>
 __global__ __launch_bounds__(256) void paged_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, const int* __restrict__ indptr,
+    const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ indptr,
     const int* __restrict__ last_page_len, const int* __restrict__ indices, int batch, int hq, int hkv,
-    int page_size, int64_t num_pages, float sm_scale, int local, PlanHeader* __restrict__ hdr,
+    int page_size, int64_t num_pages, float sm_scale, float inv_scale, int local, PlanHeader* __restrict__ hdr,
     const ItemDesc* __restrict__ descs, float* __restrict__ part_m, float* __restrict__ part_l,
     float* __restrict__ part_o, uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -462,8 +549,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     const LocalPlan lp = local_plan(indptr, last_page_len, batch, hkv, gridDim.x);
     for (int it = blockIdx.x; it < lp.n_items; it += gridDim.x) {
       const ItemDesc desc = local_item(lp, it, batch, page_size);
-      decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
-                     part_o, out, smem);
+      decode_item<D, KB>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale, hdr,
+                         part_m, part_l, part_o, out, smem);
       __syncthreads();  // LDS is reused by the next item
     }
     return;
@@ -475,8 +562,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
   if (h.batch != batch || h.hkv != hkv) return;
   for (int it = blockIdx.x; it < h.n_items; it += gridDim.x) {
     if (it != (int)blockIdx.x) desc = descs[it];
-    decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
-                   part_o, out, smem);
+    decode_item<D, KB>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale, hdr,
+                       part_m, part_l, part_o, out, smem);
     __syncthreads();
   }
 }
@@ -609,6 +696,40 @@ __global__ __launch_bounds__(256) void paged_kv_write_kernel(const uint16_t* __r
   }
 }
 
+// The FP8 cache's KV write: cache[loc[b,0], plane, loc[b,1], kvh, :] = e4m3(bf16(x * scale)) for x = k (plane 0)
+// and v (plane 1) (q35_group.py:244-247, KV8=2). One thread per 8 elements.
+__global__ __launch_bounds__(256) void paged_kv_write_fp8_kernel(const uint16_t* __restrict__ k,
+                                                                 const uint16_t* __restrict__ v,
+                                                                 unsigned char* __restrict__ cache,
+                                                                 const int* __restrict__ loc, int batch, int hkv,
+                                                                 int d, int page_size, int64_t num_pages, float scale,
+                                                                 int* __restrict__ status) {
+  const int row_chunks = hkv * d / 8;
+  const int64_t total = (int64_t)batch * row_chunks;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int plane = i >= total;
+    const int64_t j = plane ? i - total : i;
+    const int b = (int)(j / row_chunks), ch = (int)(j - (int64_t)b * row_chunks);
+    const int page = loc[2 * b], off = loc[2 * b + 1];
+    if (page < 0 || page >= num_pages || off < 0 || off >= page_size) {
+      if (status) *status = 1;
+      continue;
+    }
+    const uint4 src = *reinterpret_cast<const uint4*>((plane ? v : k) + (int64_t)b * hkv * d + ch * 8);
+    const uint32_t w[4] = {src.x, src.y, src.z, src.w};
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = __uint_as_float(e & 1 ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+      const uint32_t c = f32_to_e4m3(round_bf16(x * scale));
+      if (e < 4) lo |= c << (8 * e); else hi |= c << (8 * (e - 4));
+    }
+    unsigned char* dst = cache + (((int64_t)page * 2 + plane) * page_size + off) * (int64_t)hkv * d + ch * 8;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  }
+}
+
 struct WsView {
   PlanHeader* hdr;
   int* item_off;
@@ -648,24 +769,25 @@ int split_grid(int batch, int hkv) {
   return (int)(items < slots ? items : slots);
 }
 
-template <int D>
-int launch_split(const uint16_t* q, const uint16_t* cache, const int* indptr, const int* last, const int* indices,
+template <int D, int KB = 2>
+int launch_split(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
                  uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                 void* ws, hipStream_t st) {
+                 void* ws, hipStream_t st, float inv_scale = 1.0f) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
-  const size_t lds = (size_t)kNBuf * PagedCfg<D>::BUF;
+  // the ring of landed tiles; an FP8 cache: a ring of 5 landing slots (kNBuf8) and two bf16 staging tiles
+  const size_t lds = KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF : (size_t)kNBuf * PagedCfg<D>::BUF;
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, KB>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
-  hipLaunchKernelGGL((paged_decode_kernel<D>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves), lds, st,
-                     q, cache, indptr, last, indices, batch, hq, hkv, page_size, num_pages, sm_scale, local, v.hdr,
-                     v.descs, v.pm, v.pl, v.po, out);
+  hipLaunchKernelGGL((paged_decode_kernel<D, KB>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves), lds,
+                     st, q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv, page_size,
+                     num_pages, sm_scale, inv_scale, local, v.hdr, v.descs, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
 
@@ -803,5 +925,64 @@ extern "C" int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t
   if (grid > 4096) grid = 4096;
   hipLaunchKernelGGL(paged_kv_write_kernel, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v, kv_cache,
                      cache_location, (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, status);
+  return axk_launch_status();
+}
+
+// ---- FP8 KV cache (E4M3 with one static power-of-two scale: the stored value is e4m3(bf16(x * kv_scale)), the
+// attended value stored / kv_scale, exact in bf16). q35_group.py:44-54, 244-247 (KV8=2).
+namespace {
+int check_kv_scale(float s) {
+  int e = 0;
+  const float m = frexpf(s, &e);
+  return s > 0.f && m == 0.5f && e >= -125 && e <= 126 ? AXK_OK : AXK_E_SHAPE;  // a power of two
+}
+}  // namespace
+
+extern "C" int axk_paged_decode_fp8(const uint16_t* q, const uint8_t* kv_cache, const int32_t* indptr,
+                                    const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
+                                    int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                    int64_t page_size, int64_t num_pages, float sm_scale, float kv_scale,
+                                    void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(q && kv_cache && indptr && indices && last_page_len && out, AXK_E_NULL);
+  int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
+  if (rc != AXK_OK) return rc;
+  AXK_REQUIRE(head_dim == 128 || head_dim == 256, AXK_E_SHAPE);  // whole 1 KiB load blocks split over the waves
+  AXK_REQUIRE(check_kv_scale(kv_scale) == AXK_OK, AXK_E_SHAPE);
+  AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16), AXK_E_ALIGN);
+  const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const size_t qbytes = (size_t)batch * num_qo_heads * head_dim * 2;
+  AXK_REQUIRE(!axk_overlap(out, qbytes, q, qbytes), AXK_E_ALIAS);
+  AXK_REQUIRE(!axk_overlap(out, qbytes, workspace, workspace_bytes), AXK_E_ALIAS);
+  rc = axk_paged_decode_plan(indptr, last_page_len, batch, num_qo_heads, num_kv_heads, head_dim, page_size, workspace,
+                             workspace_bytes, stream);
+  if (rc != AXK_OK) return rc;
+  hipStream_t st = axk_stream(stream);
+  const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
+  rc = head_dim == 128 ? launch_split<128, 1>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS,
+                                              num_pages, sm_scale, workspace, st, 1.0f / kv_scale)
+                       : launch_split<256, 1>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS,
+                                              num_pages, sm_scale, workspace, st, 1.0f / kv_scale);
+  if (rc != AXK_OK) return rc;
+  return axk_paged_decode_merge(indptr, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim, workspace,
+                                workspace_bytes, stream);
+}
+
+extern "C" int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint8_t* kv_cache,
+                                      const int32_t* cache_location, int64_t batch, int64_t num_kv_heads,
+                                      int64_t head_dim, int64_t page_size, int64_t num_pages, float kv_scale,
+                                      int32_t* status, axk_stream_t stream) {
+  AXK_REQUIRE(k && v && kv_cache && cache_location, AXK_E_NULL);
+  AXK_REQUIRE(batch >= 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(page_size > 0 && num_pages > 0 && check_kv_scale(kv_scale) == AXK_OK, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(k, 16) && axk_aligned(v, 16) && axk_aligned(kv_cache, 8), AXK_E_ALIGN);
+  if (batch == 0) return AXK_OK;
+  const int64_t chunks = 2 * batch * num_kv_heads * head_dim / 8;
+  int64_t grid = (chunks + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  hipLaunchKernelGGL(paged_kv_write_fp8_kernel, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v, kv_cache,
+                     cache_location, (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, kv_scale,
+                     status);
   return axk_launch_status();
 }

@@ -236,6 +236,67 @@ class PagedDecodeWorkload(Workload):
                 "sample": f"full config1 op (oracle/paged_attn.py, torch fp32 CPU), median of {reps} runs"}
 
 
+class PagedDecodeFp8Workload(Workload):
+    """Config 1's attention over an FP8 E4M3 cache (SURVEY next row: KV8 = 2, q35_group.py:44-54): the same
+    sequences, pages and queries, the cache stored as e4m3(bf16(x * 8)). One step = axk_paged_decode_fp8 (plan +
+    split + merge); the roofline is the whole op's (so it includes the merge): K and V bytes of every valid token
+    (half of bf16's) + q + out + page table."""
+
+    name = "paged_decode_fp8kv"
+    kernel = "paged_decode_kernel<256, 1> (+ merge)"
+    timing = "graph"
+    traffic_profile = None
+    KV_SCALE = 8.0
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import attention, configs
+        from oracle import paged_attn
+
+        c = configs.config1()
+        self.host = c
+        tot = sum(c["lens"])
+        b, hq, d = c["q"].shape
+        pool, _, page, hkv, _ = c["cache"].shape
+        npages = int(c["indptr"][-1])
+        self.alg_bytes = tot * 2 * hkv * d + 2 * b * hq * d * 2 + 4 * (npages + 2 * b + 1)
+        self.alg_flops = 4 * tot * hq * d
+        codes = paged_attn.quant_kv_fp8(c["cache"], self.KV_SCALE).to(dev)
+        self.copies = max(2, -(-ROTATE_BYTES // codes.numel()))
+        self.caches = [codes] + [codes.clone() for _ in range(self.copies - 1)]
+        self.q = c["q"].to(dev)
+        self.indptr, self.indices, self.last = (c[k].to(dev) for k in ("indptr", "indices", "last_page_len"))
+        self.out = torch.empty_like(self.q)
+        self.ws = attention.paged_decode_workspace(b, hq, hkv, d, dev)
+        self.scale = c["scale"]
+        self.config = {"workload": "config1 over an FP8 E4M3 KV cache (kv_scale 8): B=16 HQ=16 HKV=2 D=256 page=64",
+                       "sum_context": tot, "rotating_copies": self.copies}
+        self.dtype = "fp8 e4m3 KV -> bf16 (fp32 softmax / accumulation)"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        axk.paged_decode_fp8(self.q, self.caches[i % self.copies], self.indptr, self.indices, self.last,
+                             self.KV_SCALE, sm_scale=self.scale, output=self.out, workspace=self.ws)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import paged_attn
+
+        c = self.host
+        deq = paged_attn.dequant_kv_fp8(paged_attn.quant_kv_fp8(c["cache"], self.KV_SCALE), self.KV_SCALE)
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: paged_attn.paged_decode(c["q"], deq, c["indptr"], c["indices"],
+                                                              c["last_page_len"], c["scale"]), budget_s=10.0,
+                              min_reps=2, max_reps=10)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config1 op on the dequantised FP8 cache (oracle/paged_attn.py, torch fp32 CPU), "
+                          f"median of {reps} runs"}
+
+
 class GdnDecodeWorkload(Workload):
     """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
 
@@ -710,7 +771,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
-             LmHeadWorkload.name: LmHeadWorkload,
+             LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 

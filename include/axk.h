@@ -169,6 +169,25 @@ int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t* kv_cache,
                        int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                        int64_t num_pages, int32_t* status, axk_stream_t stream);
 
+/* FP8 KV cache (models/qwen38_27b/decode/q35_group.py:44-54, KV8=2): K and V stored as OCP E4M3 bytes of
+ * bf16(x * kv_scale) with one static power-of-two kv_scale (the reference's KV8_SCALE, 8 for the 27B); attention
+ * reads stored / kv_scale, exact in bf16. Same page table, shapes and result as axk_paged_decode, with
+ * kv_cache u8 [num_pages, 2, page_size, num_kv_heads, head_dim] (half the bytes); head_dim 128 or 256.
+ * Same workspace (axk_paged_decode_workspace_size). */
+int axk_paged_decode_fp8(const uint16_t* q, const uint8_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                         const int32_t* last_page_len, uint16_t* out, int64_t batch, int64_t num_qo_heads,
+                         int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                         float sm_scale, float kv_scale, void* workspace, size_t workspace_bytes,
+                         axk_stream_t stream);
+
+/* The FP8 cache's KV write (kv_write_paged with KV8=2, q35_group.py:244-247): the cache bytes at the token's
+ * (page, slot) become e4m3(bf16(k * kv_scale)) and e4m3(bf16(v * kv_scale)), rounded to nearest even as torch's
+ * float8_e4m3fn cast (a magnitude past 464 becomes NaN); every other byte is left untouched. Arguments as
+ * axk_paged_kv_write. */
+int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint8_t* kv_cache, const int32_t* cache_location,
+                           int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                           int64_t num_pages, float kv_scale, int32_t* status, axk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Gated DeltaNet (GDN)
  * ------------------------------------------------------------------------------------------- */

@@ -70,3 +70,15 @@ def store_paged_kv_(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) 
 def store_paged_kv(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
     """Returns a copy of cache with k[b] / v[b] written at (page, offset) = loc[b] (flash_attn.py:53-84)."""
     return store_paged_kv_(cache.clone(), k, v, loc)
+
+
+def quant_kv_fp8(x: torch.Tensor, kv_scale: float) -> torch.Tensor:
+    """The FP8 cache's stored bytes: e4m3(bf16(x * kv_scale)) as u8 (kv_write_paged with KV8=2,
+    models/qwen38_27b/decode/q35_group.py:244-247: a bf16 multiply, then the cast to fp8_e4m3)."""
+    return (x.float() * kv_scale).to(torch.bfloat16).float().to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def dequant_kv_fp8(codes: torch.Tensor, kv_scale: float) -> torch.Tensor:
+    """The values attention reads from an FP8 cache: stored / kv_scale (q35_group.py:48-51: K through a constant
+    E8M0 scale of 1 / KV8_SCALE, V with the probabilities carrying it), exact in bf16 for a power-of-two scale."""
+    return (codes.view(torch.float8_e4m3fn).float() / kv_scale).to(torch.bfloat16)

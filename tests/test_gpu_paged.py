@@ -149,3 +149,63 @@ def test_plan_once_run_many(dev, lens):
         got = attention.paged_decode_run(q.to(dev), cache, *args, workspace=ws, sm_scale=c["scale"]).cpu()
         ref = pa.paged_decode(q, c["cache"], c["indptr"], c["indices"], c["last_page_len"], c["scale"])
         torch.testing.assert_close(got.float(), ref.to(torch.bfloat16).float(), **TOL)
+
+
+# ---- FP8 KV cache (q35_group.py:44-54, KV8=2): stored e4m3(bf16(x * S)), attended stored / S ----
+KV_SCALE = 8.0
+
+
+def _fp8_case(c):
+    """c's cache quantised the reference's way, and the bf16 values attention reads from it."""
+    codes = pa.quant_kv_fp8(c["cache"], KV_SCALE)
+    return codes, pa.dequant_kv_fp8(codes, KV_SCALE)
+
+
+@pytest.mark.parametrize(
+    "lens,hq,hkv,d,page",
+    [
+        ([1, 100, 1000], 16, 2, 256, 64),
+        ([500, 7, 129], 4, 4, 128, 64),
+        ([64, 0, 65], 8, 1, 256, 64),  # an empty sequence yields zeros
+        ([300, 2000], 16, 1, 128, 256),
+        ([(37 * i) % 700 for i in range(70)], 8, 1, 128, 32),  # the plan kernel's partition
+    ],
+)
+def test_paged_decode_fp8(dev, lens, hq, hkv, d, page):
+    g = torch.Generator().manual_seed(sum(lens) + hq + d)
+    c = configs.paged_case(lens, hq, hkv, d, page, g)
+    codes, deq = _fp8_case(c)
+    got = axk.paged_decode_fp8(c["q"].to(dev), codes.to(dev), c["indptr"].to(dev), c["indices"].to(dev),
+                               c["last_page_len"].to(dev), KV_SCALE, sm_scale=c["scale"]).cpu()
+    ref = pa.paged_decode(c["q"], deq, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)
+
+
+def test_paged_decode_fp8_config1(dev):
+    c = configs.config1()
+    codes, deq = _fp8_case(c)
+    got = axk.paged_decode_fp8(c["q"].to(dev), codes.to(dev), c["indptr"].to(dev), c["indices"].to(dev),
+                               c["last_page_len"].to(dev), KV_SCALE, sm_scale=c["scale"]).cpu()
+    ref = pa.paged_decode(c["q"], deq, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)
+
+
+def test_kv_write_fp8_bytes(dev):
+    """The written bytes equal the reference quantisation (e4m3 of bf16(x * S), round to nearest even; past 464
+    after scaling -> NaN), every other byte untouched; includes values at and around the E4M3 ties and limits."""
+    g = torch.Generator().manual_seed(5)
+    b, hkv, d, page, pages = 6, 2, 128, 32, 9
+    k = (torch.randn(b, hkv, d, generator=g) * 4).bfloat16()
+    v = (torch.randn(b, hkv, d, generator=g) * 4).bfloat16()
+    special = torch.tensor([58.0, 57.0, -58.5, 60.0, -61.0, 0.0, -0.0, 2.0 ** -12, 2.0 ** -13, 3 * 2.0 ** -13,
+                            0.1, -0.3, 55.5, 56.0])  # x 8: 464 (tie to 448), 456, -468, 480 (NaN), ...
+    k[0, 0, : special.numel()] = special.bfloat16()
+    cache = torch.randint(0, 256, (pages, 2, page, hkv, d), generator=g, dtype=torch.uint8)
+    loc = torch.tensor([[1, 0], [1, 31], [4, 7], [0, 0], [8, 16], [5, 3]], dtype=torch.int32)
+    got = cache.to(dev)
+    axk.store_paged_kv_fp8(k.to(dev), v.to(dev), got, loc.to(dev), KV_SCALE)
+    ref = cache.clone()
+    for i, (p, o) in enumerate(loc.tolist()):
+        ref[p, 0, o] = pa.quant_kv_fp8(k[i], KV_SCALE)
+        ref[p, 1, o] = pa.quant_kv_fp8(v[i], KV_SCALE)
+    assert torch.equal(got.cpu(), ref)

@@ -76,3 +76,24 @@ def test_store_paged_kv_row_math():
             assert torch.equal(flat[row], src[b])
     diff = (out != c["cache"]).reshape(out.shape[0], 2, 32, -1).any(-1)
     assert int(diff.sum()) <= 4
+
+
+
+def test_fp8_kv_codec_pinned():
+    """The FP8 cache codec against an independent E4M3 decode (OCP e4m3fn: bias 7, no infinities, S.1111.111 = NaN)
+    and the round trip of every finite code through bf16(x * S) with S = 8; past 464 after scaling -> NaN."""
+    import math
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    vals = pa.dequant_kv_fp8(codes, 8.0).float()
+    for c in range(256):
+        s, e, m = c >> 7, (c >> 3) & 15, c & 7
+        if e == 15 and m == 7:
+            assert math.isnan(vals[c])
+            continue
+        mag = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        assert vals[c].item() == (-mag if s else mag) / 8.0, c
+    finite = ~torch.isnan(vals)
+    assert torch.equal(pa.quant_kv_fp8(vals[finite].bfloat16(), 8.0), codes[finite])
+    big = pa.quant_kv_fp8(torch.tensor([60.0, -61.0, 58.0]).bfloat16(), 8.0)  # 480 -> NaN; 464 ties to 448
+    assert big.tolist() == [0x7F, 0xFF, 0x7E]
