@@ -163,7 +163,7 @@ class PagedDecodeWorkload(Workload):
     """
 
     name = "paged_decode"
-    kernel = "paged_decode_kernel<256>"  # launched by axk_paged_decode_split
+    kernel = "paged_decode_kernel<256, 2>"  # launched by axk_paged_decode_split
     timing = "graph"       # value: K steps (plan + split + merge) replayed as one HIP graph
     kernel_events = True   # roofline: the split kernel timed alone with HIP events
     traffic_profile = "paged_decode_config1_pmc.txt"
@@ -245,7 +245,7 @@ class PagedDecodeFp8Workload(Workload):
     name = "paged_decode_fp8kv"
     kernel = "paged_decode_kernel<256, 1> (+ merge)"
     timing = "graph"
-    traffic_profile = None
+    traffic_profile = "paged_decode_fp8kv_config1_pmc.txt"  # every kernel of the op, summed
     KV_SCALE = 8.0
 
     def __init__(self, dev):
