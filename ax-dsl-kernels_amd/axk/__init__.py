@@ -22,10 +22,12 @@ from .attention import (  # noqa: E402
     store_paged_kv,
     paged_decode_fp8,
     store_paged_kv_fp8,
+    paged_prefill,
 )
 
 __all__ += ["attention", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
-            "store_paged_kv", "paged_decode_fp8", "store_paged_kv_fp8"]
+            "store_paged_kv", "paged_decode_fp8", "store_paged_kv_fp8",
+            "paged_prefill"]
 
 from . import gdn  # noqa: E402
 from .gdn import gdn_chunk_prefill, gdn_chunk_workspace, gdn_recurrent  # noqa: E402

@@ -189,3 +189,53 @@ def store_paged_kv_fp8(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor,
         "axk_paged_kv_write_fp8", k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(), loc.data_ptr(), b, hkv, d, page,
         p, float(kv_scale), _lib.ptr(status), _lib.stream_of(k),
     )
+
+
+def paged_prefill(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    qo_indptr: torch.Tensor,
+    indptr: torch.Tensor,
+    indices: torch.Tensor,
+    last_page_len: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
+    status: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal attention of several new tokens per sequence over the paged cache (prefill chunks, speculative verify):
+    q bf16 [T, HQ, D] holds sequence b's new tokens in rows qo_indptr[b] .. qo_indptr[b + 1]; their K / V are already
+    in the cache as the sequence's last tokens, so new token t of a sequence of kv_len cached tokens sees positions
+    0 .. kv_len - qlen + t (flash_attn.py:471-611, q35_prefill.py:264-336). Returns bf16 [T, HQ, D]. A page id
+    outside the pool or a query range outside q sets status (device int32 [1], if given) to 1."""
+    _check(q.dim() == 3 and q.dtype == torch.bfloat16 and q.is_contiguous(), "q must be contiguous bf16 [T, HQ, D]")
+    _check(kv_cache.dim() == 5 and kv_cache.dtype == torch.bfloat16 and kv_cache.is_contiguous(),
+           "kv_cache must be contiguous bf16 [pages, 2, page_size, HKV, D]")
+    t, hq, d = q.shape
+    p, two, page, hkv, d2 = kv_cache.shape
+    _check(two == 2 and d2 == d, f"kv_cache shape {tuple(kv_cache.shape)} does not match q {tuple(q.shape)}")
+    _check(hq % hkv == 0, f"num_qo_heads {hq} must be a multiple of num_kv_heads {hkv}")
+    _check(d in (64, 128, 256), f"head_dim {d} not supported (64, 128, 256)")
+    _check(page % 16 == 0, f"page_size {page} must be a multiple of 16")
+    b = qo_indptr.numel() - 1
+    _check(b > 0, "qo_indptr must hold B + 1 offsets")
+    for name, x, n in (("qo_indptr", qo_indptr, b + 1), ("indptr", indptr, b + 1), ("last_page_len", last_page_len, b)):
+        _check(x.dtype == torch.int32 and x.dim() == 1 and x.numel() == n and x.is_contiguous(),
+               f"{name} must be contiguous int32 [{n}]")
+    _check(indices.dtype == torch.int32 and indices.dim() == 1 and indices.is_contiguous(),
+           "indices must be contiguous int32 [nnz]")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    tensors = [q, kv_cache, qo_indptr, indptr, indices, last_page_len, output]
+    if status is not None:
+        _check(status.dtype == torch.int32 and status.numel() >= 1, "status must be int32 [1]")
+        tensors.append(status)
+    _lib.require_device(*tensors)
+    _lib.call(
+        "axk_paged_prefill", q.data_ptr(), kv_cache.data_ptr(), qo_indptr.data_ptr(), indptr.data_ptr(),
+        indices.data_ptr(), last_page_len.data_ptr(), output.data_ptr(), b, t, hq, hkv, d, page, p, float(sm_scale),
+        _lib.ptr(status), _lib.stream_of(q),
+    )
+    return output

@@ -57,6 +57,18 @@ def paged_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator, e
             "lens": list(lens), "scale": d ** -0.5}
 
 
+def prefill_case(qlens, kv_lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator, extra_pages: int = 0):
+    """paged_case over kv_lens plus q bf16 [sum(qlens), HQ, D] and qo_indptr: sequence b's qlens[b] new tokens are
+    the last of its kv_lens[b] cached tokens."""
+    c = paged_case(kv_lens, hq, hkv, d, page, g, extra_pages)
+    c["q"] = torch.randn(sum(qlens), hq, d, generator=g).to(torch.bfloat16)
+    qo = torch.zeros(len(qlens) + 1, dtype=torch.int32)
+    qo[1:] = torch.cumsum(torch.tensor(qlens, dtype=torch.int32), 0)
+    c["qo_indptr"] = qo
+    c["qlens"] = list(qlens)
+    return c
+
+
 def config1(seed: int = 0):
     """Config 1: paged decode, batch 16, 16 q heads / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384]."""
     g = torch.Generator().manual_seed(seed)

@@ -730,6 +730,242 @@ __global__ __launch_bounds__(256) void paged_kv_write_fp8_kernel(const uint16_t*
   }
 }
 
+// ---- Multi-token (prefill / verify) attention over the paged cache, causal ----
+// The qlen new tokens of sequence b are the last qlen of its kv_len cached tokens (they are written before the call),
+// so token t sits at position kv_len - qlen + t and sees cached tokens 0 .. that position (the causal bias of the
+// current block, flash_attn.py:484-486; q35_prefill.py:264-300 masks the block the same way). The query rows of one
+// (sequence, KV head) are r = t * G + h for the G query heads h of the KV head: a workgroup takes 128 consecutive
+// rows (4 waves x 2 blocks of 16) and streams the K / V tiles its rows can see, up to its last row's position,
+// through the decode kernel's 3-deep direct-to-LDS ring. Each wave computes S^T = K Q^T for its 32 rows (every
+// K fragment feeds two MFMAs) and O^T += V^T P^T over the whole head dim (every V^T fragment feeds two).
+constexpr int kPfRowsPerWave = 32;
+constexpr int kPfRows = kWaves * kPfRowsPerWave;
+
+template <int D>
+__global__ __launch_bounds__(256) void paged_prefill_kernel(
+    const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ qo_indptr,
+    const int* __restrict__ indptr, const int* __restrict__ last_page_len, const int* __restrict__ indices,
+    int batch, int total_q, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
+    int* __restrict__ status, uint16_t* __restrict__ out) {
+  using C = PagedCfg<D>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int group = hq / hkv, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+
+  // this workgroup's (sequence, row block): the blocks of each sequence in turn, its last (longest) block first.
+  // Every wave derives the same answer; the grid is an upper bound and surplus workgroups return.
+  int b = -1, blk = 0;
+  for (int c0 = 0, base = 0; c0 < batch && b < 0; c0 += 64) {
+    const int sq = c0 + lane;
+    const int qlen_l = sq < batch ? qo_indptr[sq + 1] - qo_indptr[sq] : 0;
+    const int nb = qlen_l > 0 ? (qlen_l * group + kPfRows - 1) / kPfRows : 0;
+    int incl = nb;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += v;
+    }
+    const int excl = base + incl - nb;
+    const int want = blockIdx.x;
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(nb > 0 && want >= excl && want < excl + nb);
+    if (hit) {
+      const int hl = __builtin_ctzll(hit);
+      b = c0 + hl;
+      blk = __shfl(nb, hl, 64) - 1 - (want - __shfl(excl, hl, 64));
+    }
+    base += __shfl(incl, 63, 64);
+  }
+  if (b < 0) return;
+  const int q0 = qo_indptr[b], qlen = qo_indptr[b + 1] - q0;
+  if (q0 < 0 || q0 + qlen > total_q) {  // a query range outside q: nothing is read or written
+    if (status && threadIdx.x == 0) *status = 1;
+    return;
+  }
+  const int pb = indptr[b], npg = max(indptr[b + 1] - pb, 0);
+  const int last = min(max(npg > 0 ? last_page_len[b] : 0, 0), page_size);
+  const int kv_len = npg > 0 ? (npg - 1) * page_size + last : 0;
+  const int tpp = page_size / kTile;
+  const int r_first = blk * kPfRows, r_last = min(r_first + kPfRows, qlen * group) - 1;
+  const int base_pos = kv_len - qlen;  // position of new token 0 (negative if the cache lacks the new tokens)
+  const int kv_end = min(kv_len, max(0, base_pos + r_last / group + 1));
+  const int ntiles = min((kv_end + kTile - 1) / kTile, npg * tpp);
+  const float c = sm_scale * kLog2e;
+  const int64_t row_stride = (int64_t)hkv * D * 2, plane_stride = (int64_t)page_size * row_stride;
+  const uint32_t lds0 = lds_addr(smem);
+
+  // rows of this wave: block i holds row r_first + 32 wave + 16 i + l16 (replicated over g)
+  int pos[2];
+  int64_t qoff[2];
+  axk_bf16x8 qb[2][C::KSTEPS];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = r_first + kPfRowsPerWave * wave + 16 * i + l16;
+    const bool valid = r <= r_last;
+    const int t = valid ? r / group : 0, h = valid ? r - t * group : 0;
+    pos[i] = valid ? base_pos + t : -1;
+    qoff[i] = ((int64_t)(q0 + t) * hq + kvh * group + h) * D;
+    const uint16_t* qp = q + qoff[i] + 8 * g;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) qb[i][s] = valid ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
+  }
+  int chunk = 0;
+  int pid = lane < npg ? indices[pb + lane] : 0;
+  asm volatile("" : "+v"(pid));
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qb[i][s]));
+
+  auto locate = [&](int ti, int& nvalid) -> const unsigned char* {
+    const int lp = ti / tpp, tp = ti - lp * tpp;
+    if ((lp >> 6) != chunk) {
+      chunk = lp >> 6;
+      const int j = (chunk << 6) + lane;
+      pid = j < npg ? indices[pb + j] : 0;
+      asm volatile("" : "+v"(pid));
+    }
+    int page = __builtin_amdgcn_readfirstlane(__shfl(pid, lp & 63, 64));
+    const int valid_in_page = (lp == npg - 1) ? last : page_size;
+    nvalid = min(kTile, valid_in_page - tp * kTile);
+    if (page < 0 || page >= num_pages) {
+      if (status && lane == 0 && nvalid > 0) *status = 1;
+      page = 0;
+      nvalid = 0;
+    }
+    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * D * 2;
+  };
+  int lane_tok[C::IPW];
+  int64_t lane_off[C::IPW], lane_off0[C::IPW];
+#pragma unroll
+  for (int k = 0; k < C::IPW; ++k) {
+    const int j = wave * C::IPW + k;
+    const int plane = j / C::IPP, blk2 = j - plane * C::IPP;
+    lane_tok[k] = blk2 * C::RPI + lane / (C::RB / 16);
+    lane_off0[k] = plane * plane_stride + (lane % (C::RB / 16)) * 16;
+    lane_off[k] = lane_off0[k] + (int64_t)lane_tok[k] * row_stride;
+  }
+  auto issue = [&](int ti, int nb) -> int {
+    int nvalid;
+    const unsigned char* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
+    const int nrow = nvalid > 0 ? nvalid : 1;
+#pragma unroll
+    for (int k = 0; k < C::IPW; ++k) {
+      const int j = wave * C::IPW + k;
+      const int plane = j / C::IPP, blk2 = j - plane * C::IPP;
+      lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
+                lds0 + nb * C::BUF + plane * C::PLANE + blk2 * C::BLK);
+    }
+    return ti < ntiles ? nvalid : 0;
+  };
+
+  constexpr int DT = D / 16;
+  axk_f32x4 o[2][DT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[i][t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  auto tile_math = [&](const unsigned char* kt, int ti, int nvalid) {
+    const unsigned char* vt = kt + C::PLANE;
+    axk_f32x4 st[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
+    const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) {
+      const axk_bf16x8 ka = *reinterpret_cast<const axk_bf16x8*>(krow + 64 * s);
+      st[0] = mfma_bf16_16x16x32(ka, qb[0][s], st[0]);
+      st[1] = mfma_bf16_16x16x32(ka, qb[1][s], st[1]);
+    }
+    const int tok0 = ti * kTile + 4 * g;
+    axk_i16x4 pbv[2];
+    float alpha[2];
+    bool moved = false;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const bool ok = 4 * g + rr < nvalid && tok0 + rr <= pos[i];
+        const float sv = ok ? st[i][rr] * c : -INFINITY;
+        st[i][rr] = sv;
+        mx = fmaxf(mx, sv);
+      }
+      mx = xor32_max(xor16_max(mx));
+      const float m_new = fmaxf(m_run[i], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a row that has seen nothing yet stays at zero
+      moved |= __builtin_amdgcn_ballot_w64(m_new > m_run[i]) != 0;
+      alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+      float psum = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float pv = st[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[i][rr] - m_use);
+        psum += pv;
+        pbv[i][rr] = (short)f32_to_bf16_bits(pv);
+      }
+      psum = xor32_sum(xor16_sum(psum));
+      l_run[i] = l_run[i] * alpha[i] + psum;
+      m_run[i] = m_new;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const axk_i16x4 va = lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (16 * t + 4 * (l16 & 3)) * 2);
+      if (moved) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          o[0][t][rr] *= alpha[0];
+          o[1][t][rr] *= alpha[1];
+        }
+      }
+      o[0][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[0], o[0][t], 0, 0, 0);
+      o[1][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[1], o[1][t], 0, 0, 0);
+    }
+  };
+
+  if (ntiles > 0) {
+    int nv0 = issue(0, 0);
+    int nv1 = issue(1, 1);
+    for (int ti = 0; ti < ntiles; ++ti) {
+      const int nb = ti % kNBuf;
+      wait_vmcnt<C::IPW>();
+      __builtin_amdgcn_s_barrier();
+      const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);
+      const int nvalid = nv0;
+      nv0 = nv1;
+      nv1 = nv2;
+      if (nvalid > 0) tile_math(smem + nb * C::BUF, ti, nvalid);
+    }
+    wait_vmcnt<0>();
+  }
+
+  // lane (row l16 of block i, g) holds O[row][d = 16 t + 4 g .. + 3]
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = r_first + kPfRowsPerWave * wave + 16 * i + l16;
+    if (r > r_last) continue;
+    const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      uint2 w;
+      w.x = f32_to_bf16_bits(o[i][t][0] * inv) | (f32_to_bf16_bits(o[i][t][1] * inv) << 16);
+      w.y = f32_to_bf16_bits(o[i][t][2] * inv) | (f32_to_bf16_bits(o[i][t][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(out + qoff[i] + 16 * t + 4 * g) = w;
+    }
+  }
+}
+
+template <int D>
+int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, const int* indptr, const int* last,
+                   const int* indices, uint16_t* out, int batch, int total_q, int hq, int hkv, int page_size,
+                   int64_t num_pages, float sm_scale, int* status, hipStream_t st) {
+  const int64_t rows = (int64_t)total_q * (hq / hkv);
+  const int64_t grid = (rows + kPfRows - 1) / kPfRows + batch;  // >= the sum over sequences of their row blocks
+  hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid, (unsigned)hkv), dim3(64 * kWaves),
+                     (size_t)kNBuf * PagedCfg<D>::BUF, st, q, static_cast<const unsigned char*>(cache), qo_indptr,
+                     indptr, last, indices, batch, total_q, hq, hkv, page_size, num_pages, sm_scale, status, out);
+  return axk_launch_status();
+}
+
 struct WsView {
   PlanHeader* hdr;
   int* item_off;
@@ -985,4 +1221,38 @@ extern "C" int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint
                      cache_location, (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, kv_scale,
                      status);
   return axk_launch_status();
+}
+
+// Prefill / speculative-verify attention: the qo_indptr[b + 1] - qo_indptr[b] new tokens of each sequence (rows of q,
+// already written into the cache as the sequence's last tokens) attend causally over its paged history and
+// themselves. flash_attn.py:471-611 (paged_flash_attention: history pages, then the causal current block),
+// q35_prefill.py:264-336 (the G x P-row block attention per KV head).
+extern "C" int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr,
+                                 const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                                 uint16_t* out, int64_t batch, int64_t total_q, int64_t num_qo_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                                 float sm_scale, int32_t* status, axk_stream_t stream) {
+  AXK_REQUIRE(q && kv_cache && qo_indptr && indptr && indices && last_page_len && out, AXK_E_NULL);
+  AXK_REQUIRE(batch > 0 && batch <= (1 << 20) && total_q >= 0 && total_q <= (1 << 24), AXK_E_SHAPE);
+  AXK_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(num_kv_heads <= 65535 && total_q * num_qo_heads <= ((int64_t)1 << 31) / 256, AXK_E_SHAPE);
+  AXK_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, AXK_E_SHAPE);
+  AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16) && axk_aligned(out, 8), AXK_E_ALIGN);
+  if (total_q == 0) return AXK_OK;
+  const size_t qbytes = (size_t)total_q * num_qo_heads * head_dim * 2;
+  AXK_REQUIRE(!axk_overlap(out, qbytes, q, qbytes), AXK_E_ALIAS);
+  hipStream_t st = axk_stream(stream);
+  const int B = (int)batch, T = (int)total_q, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
+  switch (head_dim) {
+    case 64:
+      return launch_prefill<64>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
+                                num_pages, sm_scale, status, st);
+    case 128:
+      return launch_prefill<128>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
+                                 num_pages, sm_scale, status, st);
+    default:
+      return launch_prefill<256>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
+                                 num_pages, sm_scale, status, st);
+  }
 }

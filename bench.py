@@ -297,6 +297,59 @@ class PagedDecodeFp8Workload(Workload):
                           f"median of {reps} runs"}
 
 
+class PagedPrefillWorkload(Workload):
+    """Prefill attention (SURVEY next row: G x P-row causal block attention, q35_prefill.py:264-336; flash_attn.py:
+    471-611): one sequence's 4096-token chunk over an empty history in the paged cache, config 1's attention shape
+    (HQ 16 / HKV 2, D 256, page 64). One step = axk_paged_prefill (one launch). MFMA-bound: the flops of the visible
+    (query, key) pairs only, 4 D HQ sum_t (t + 1) (QK^T and PV), against dense bf16."""
+
+    name = "paged_prefill"
+    kernel = "paged_prefill_kernel<256>"
+    timing = "graph"
+    mfma = True
+    traffic_profile = None
+    T = 4096
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        g = torch.Generator().manual_seed(0)
+        c = configs.prefill_case([self.T], [self.T], 16, 2, 256, 64, g)
+        self.host = c
+        self.d = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in c.items()}
+        hq, d = 16, 256
+        self.alg_flops = 4 * d * hq * (self.T * (self.T + 1) // 2)
+        self.alg_bytes = 2 * c["q"].numel() * 2 + c["cache"].numel() * 2 + 4 * (c["indices"].numel() + 4)
+        self.out = torch.empty_like(self.d["q"])
+        self.config = {"workload": "prefill chunk: B=1, T=4096 new tokens, empty history, HQ=16 HKV=2 D=256 page=64, "
+                                   "causal"}
+        self.dtype = "bf16 (fp32 softmax / accumulation)"
+
+    def step(self, i: int) -> None:
+        from axk import attention
+
+        d = self.d
+        attention.paged_prefill(d["q"], d["cache"], d["qo_indptr"], d["indptr"], d["indices"], d["last_page_len"],
+                                sm_scale=self.host["scale"], output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import paged_attn
+
+        c = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: paged_attn.paged_prefill(c["q"], c["cache"], c["qo_indptr"], c["indptr"],
+                                                               c["indices"], c["last_page_len"], c["scale"]),
+                              budget_s=10.0, min_reps=1, max_reps=5)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"the full 4096-token chunk (oracle/paged_attn.py paged_prefill, torch fp32 CPU), "
+                          f"median of {reps} runs"}
+
+
 class GdnDecodeWorkload(Workload):
     """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
 
@@ -772,6 +825,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
              LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
+             PagedPrefillWorkload.name: PagedPrefillWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 

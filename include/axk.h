@@ -188,6 +188,19 @@ int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint8_t* kv_cac
                            int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                            int64_t num_pages, float kv_scale, int32_t* status, axk_stream_t stream);
 
+/* Prefill / speculative-verify attention over the paged cache, causal (the history pages and the current block of
+ * sgl_kernel_axera/attention/flash_attn.py:471-611 paged_flash_attention, flash_attn.py:1044 flash_attn_with_kvcache;
+ * the G x P-row block attention of models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:264-336). Sequence b's new tokens
+ * are rows qo_indptr[b] .. qo_indptr[b + 1] of q bf16 [total_q, num_qo_heads, head_dim]; their K / V are already in
+ * the cache (axk_paged_kv_write) as the sequence's last tokens, so new token t of a sequence with kv_len cached tokens
+ * attends positions 0 .. kv_len - qlen + t. Same cache layout and page table as axk_paged_decode; head_dim 64, 128 or
+ * 256; page_size a multiple of 16. out bf16 like q. No workspace. A page id outside the pool (page skipped) or a
+ * query range outside q (sequence skipped) sets *status (if non-NULL, device i32) to 1. */
+int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr, const int32_t* indptr,
+                      const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                      int64_t total_q, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                      int64_t page_size, int64_t num_pages, float sm_scale, int32_t* status, axk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Gated DeltaNet (GDN)
  * ------------------------------------------------------------------------------------------- */

@@ -57,6 +57,34 @@ def paged_decode(q: torch.Tensor, cache: torch.Tensor, indptr, indices, last_pag
     return out
 
 
+def paged_prefill(q: torch.Tensor, cache: torch.Tensor, qo_indptr, indptr, indices, last_page_len,
+                  sm_scale: float) -> torch.Tensor:
+    """fp32 [T, HQ, D]: the new tokens of sequence b (rows qo_indptr[b] .. qo_indptr[b+1] of q) are its last qlen
+    cached tokens; token t attends cached positions 0 .. L - qlen + t (the causal current block over the history,
+    flash_attn.py:484-486; q35_prefill.py:264-300 builds the same additive mask). A row that sees nothing yields 0."""
+    t_all, hq, d = q.shape
+    hkv = cache.shape[3]
+    grp = hq // hkv
+    qi = np.asarray(qo_indptr)
+    out = torch.zeros(t_all, hq, d, dtype=torch.float32)
+    for b in range(len(qi) - 1):
+        q0, qlen = int(qi[b]), int(qi[b + 1] - qi[b])
+        if qlen <= 0:
+            continue
+        k, v = gather_kv(cache, indptr, indices, last_page_len, b)
+        L = k.shape[0]
+        kf = k.float().repeat_interleave(grp, dim=1).permute(1, 0, 2)  # [HQ, L, D]
+        vf = v.float().repeat_interleave(grp, dim=1).permute(1, 0, 2)
+        qf = q[q0:q0 + qlen].float().permute(1, 0, 2)  # [HQ, qlen, D]
+        s = torch.matmul(qf, kf.transpose(1, 2)) * sm_scale  # [HQ, qlen, L]
+        pos = torch.arange(qlen).reshape(-1, 1) + (L - qlen)
+        s = s.masked_fill(torch.arange(L).reshape(1, -1) > pos, float("-inf"))
+        seen = (pos >= 0).reshape(1, -1, 1) & (L > 0)
+        p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0) * seen
+        out[q0:q0 + qlen] = torch.matmul(p, vf).permute(1, 0, 2)
+    return out
+
+
 def store_paged_kv_(cache: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc) -> torch.Tensor:
     """Writes k[b] / v[b] at (page, offset) = loc[b] of cache in place and returns it (flash_attn.py:53-84)."""
     loc = np.asarray(loc).reshape(-1, 2)

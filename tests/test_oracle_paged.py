@@ -97,3 +97,75 @@ def test_fp8_kv_codec_pinned():
     assert torch.equal(pa.quant_kv_fp8(vals[finite].bfloat16(), 8.0), codes[finite])
     big = pa.quant_kv_fp8(torch.tensor([60.0, -61.0, 58.0]).bfloat16(), 8.0)  # 480 -> NaN; 464 ties to 448
     assert big.tolist() == [0x7F, 0xFF, 0x7E]
+
+
+def _pcase(seed, qlens, kv_lens, hq=8, hkv=2, d=64, page=32):
+    g = torch.Generator().manual_seed(seed)
+    return configs.prefill_case(qlens, kv_lens, hq, hkv, d, page, g, extra_pages=3)
+
+
+def _prefill(c):
+    return pa.paged_prefill(c["q"], c["cache"], c["qo_indptr"], c["indptr"], c["indices"], c["last_page_len"],
+                            c["scale"])
+
+
+def test_prefill_matches_sdpa_lower_right_causal():
+    # torch's own bottom-right-aligned causal bias (the new tokens are the last of the sequence) with GQA
+    from torch.nn.attention.bias import causal_lower_right
+
+    c = _pcase(11, [5, 40, 1, 33], [5, 100, 70, 33])
+    got = _prefill(c)
+    for b, (ql, L) in enumerate(zip(c["qlens"], c["lens"])):
+        k, v = pa.gather_kv(c["cache"], c["indptr"], c["indices"], c["last_page_len"], b)
+        q0 = int(c["qo_indptr"][b])
+        ref = F.scaled_dot_product_attention(
+            c["q"][q0:q0 + ql].float().permute(1, 0, 2)[None], k.float().permute(1, 0, 2)[None],
+            v.float().permute(1, 0, 2)[None], attn_mask=causal_lower_right(ql, L), enable_gqa=True, scale=c["scale"],
+        )[0].permute(1, 0, 2)
+        torch.testing.assert_close(got[q0:q0 + ql], ref, rtol=1e-5, atol=1e-5)
+
+
+def test_prefill_brute_force_small():
+    # per (token, head): softmax over positions 0 .. L - qlen + t by explicit loops
+    c = _pcase(12, [3, 2], [4, 2], hq=4, hkv=2, d=8, page=16)
+    got = _prefill(c)
+    for b, (ql, L) in enumerate(zip(c["qlens"], c["lens"])):
+        k, v = pa.gather_kv(c["cache"], c["indptr"], c["indices"], c["last_page_len"], b)
+        q0 = int(c["qo_indptr"][b])
+        for t in range(ql):
+            for h in range(4):
+                kvh = h // 2
+                scores = [float((c["q"][q0 + t, h].float() * k[j, kvh].float()).sum()) * c["scale"]
+                          for j in range(L - ql + t + 1)]
+                m = max(scores)
+                w = [np.exp(s - m) for s in scores]
+                o = sum(wj * v[j, kvh].double() for j, wj in enumerate(w)) / sum(w)
+                torch.testing.assert_close(got[q0 + t, h].double(), o, rtol=1e-5, atol=1e-6)
+
+
+def test_prefill_one_token_equals_decode_and_causality():
+    c = _pcase(13, [1, 1, 1], [1, 65, 200])
+    got = _prefill(c)
+    dec = pa.paged_decode(c["q"], c["cache"], c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+    torch.testing.assert_close(got, dec, rtol=1e-6, atol=1e-6)
+    # future rows do not matter: rewriting the cache past token t's position leaves row t unchanged
+    c = _pcase(14, [30], [90])
+    base = _prefill(c)
+    k, _ = pa.gather_kv(c["cache"], c["indptr"], c["indices"], c["last_page_len"], 0)
+    page = c["cache"].shape[2]
+    pos = 90 - 30 + 9  # token 9 of the block
+    for j in range(pos + 1, 90):
+        pg = int(c["indices"][j // page])
+        c["cache"][pg, :, j % page] = 100.0
+    after = _prefill(c)
+    torch.testing.assert_close(after[:10], base[:10], rtol=0, atol=0)
+    assert not torch.allclose(after[10:], base[10:])
+
+
+def test_prefill_empty_and_short_cache():
+    # a sequence without new tokens contributes no rows; rows before the cache start see nothing (zeros)
+    c = _pcase(15, [0, 4, 6], [10, 4, 3])
+    got = _prefill(c)
+    assert got.shape == (10, 8, 64)
+    assert not got[4:7].any()  # sequence 2: qlen 6 > 3 cached tokens, its first 3 rows see nothing
+    assert got[7:].abs().sum() > 0
