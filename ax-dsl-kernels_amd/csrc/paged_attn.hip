@@ -735,21 +735,38 @@ __global__ __launch_bounds__(256) void paged_kv_write_fp8_kernel(const uint16_t*
 // so token t sits at position kv_len - qlen + t and sees cached tokens 0 .. that position (the causal bias of the
 // current block, flash_attn.py:484-486; q35_prefill.py:264-300 masks the block the same way). The query rows of one
 // (sequence, KV head) are r = t * G + h for the G query heads h of the KV head: a workgroup takes 128 consecutive
-// rows (4 waves x 2 blocks of 16) and streams the K / V tiles its rows can see, up to its last row's position,
-// through the decode kernel's 3-deep direct-to-LDS ring. Each wave computes S^T = K Q^T for its 32 rows (every
-// K fragment feeds two MFMAs) and O^T += V^T P^T over the whole head dim (every V^T fragment feeds two).
-constexpr int kPfRowsPerWave = 32;
-constexpr int kPfRows = kWaves * kPfRowsPerWave;
+// rows (8 waves x 16) and streams the K / V tiles its rows can see, up to its last row's position, through a
+// direct-to-LDS ring (the decode kernel's tile layout, loads issued by the first 4 waves). Each wave computes
+// S^T = K Q^T for its 16 rows and O^T += V^T P^T over the whole head dim. 16 rows per wave keep Q and O in
+// 100 VGPRs (two waves per SIMD); 32 rows per wave overflowed the VGPRs and the compiler moved O between AGPRs and
+// VGPRs on every tile (measured: 700 VALU instructions per tile, 608 us for the 4096-token chunk).
+constexpr int kPfWaves = 8;
+constexpr int kPfRowsPerWave = 16;
+constexpr int kPfNI = kPfRowsPerWave / 16;  // 16-row MFMA blocks per wave
+constexpr int kPfRows = kPfWaves * kPfRowsPerWave;
+constexpr int kPfAhead = 4;  // tiles in flight while one is computed (the K / V stream from L2 / MALL is latency bound)
+constexpr int kPfBuf = kPfAhead + 1;
 
 template <int D>
-__global__ __launch_bounds__(256) void paged_prefill_kernel(
+__global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ qo_indptr,
     const int* __restrict__ indptr, const int* __restrict__ last_page_len, const int* __restrict__ indices,
-    int batch, int total_q, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
+    int batch, int total_q, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, int xcd_per_head,
     int* __restrict__ status, uint16_t* __restrict__ out) {
   using C = PagedCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int group = hq / hkv, kvh = blockIdx.y;
+  const int group = hq / hkv;
+  // KV head and block index: consecutive workgroups go to the 8 XCDs in turn, so with xcd_per_head > 0 the blocks of
+  // one KV head run on xcd_per_head XCDs only and its K / V stay in their L2s
+  int kvh, want;
+  if (xcd_per_head > 0) {
+    const int x = blockIdx.x & 7, sl = blockIdx.x >> 3;
+    kvh = x / xcd_per_head;
+    want = sl * xcd_per_head + (x - kvh * xcd_per_head);
+  } else {
+    kvh = blockIdx.x % hkv;
+    want = blockIdx.x / hkv;
+  }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
 
@@ -767,7 +784,6 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
       if (lane >= o) incl += v;
     }
     const int excl = base + incl - nb;
-    const int want = blockIdx.x;
     const unsigned long long hit = __builtin_amdgcn_ballot_w64(nb > 0 && want >= excl && want < excl + nb);
     if (hit) {
       const int hl = __builtin_ctzll(hit);
@@ -794,12 +810,12 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
   const int64_t row_stride = (int64_t)hkv * D * 2, plane_stride = (int64_t)page_size * row_stride;
   const uint32_t lds0 = lds_addr(smem);
 
-  // rows of this wave: block i holds row r_first + 32 wave + 16 i + l16 (replicated over g)
-  int pos[2];
-  int64_t qoff[2];
-  axk_bf16x8 qb[2][C::KSTEPS];
+  // rows of this wave: block i holds row r_first + kPfRowsPerWave wave + 16 i + l16 (replicated over g)
+  int pos[kPfNI];
+  int64_t qoff[kPfNI];
+  axk_bf16x8 qb[kPfNI][C::KSTEPS];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kPfNI; ++i) {
     const int r = r_first + kPfRowsPerWave * wave + 16 * i + l16;
     const bool valid = r <= r_last;
     const int t = valid ? r / group : 0, h = valid ? r - t * group : 0;
@@ -813,7 +829,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
   int pid = lane < npg ? indices[pb + lane] : 0;
   asm volatile("" : "+v"(pid));
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kPfNI; ++i)
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qb[i][s]));
 
@@ -849,6 +865,7 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
     int nvalid;
     const unsigned char* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
     const int nrow = nvalid > 0 ? nvalid : 1;
+    if (wave < kWaves)  // wave-uniform: the first four waves load the tile
 #pragma unroll
     for (int k = 0; k < C::IPW; ++k) {
       const int j = wave * C::IPW + k;
@@ -860,29 +877,34 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
   };
 
   constexpr int DT = D / 16;
-  axk_f32x4 o[2][DT];
+  axk_f32x4 o[kPfNI][DT];
+  float m_run[kPfNI], l_run[kPfNI];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kPfNI; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[i][t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  }
 
   auto tile_math = [&](const unsigned char* kt, int ti, int nvalid) {
     const unsigned char* vt = kt + C::PLANE;
-    axk_f32x4 st[2] = {axk_f32x4{0.f, 0.f, 0.f, 0.f}, axk_f32x4{0.f, 0.f, 0.f, 0.f}};
+    axk_f32x4 st[kPfNI];
+#pragma unroll
+    for (int i = 0; i < kPfNI; ++i) st[i] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
     const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) {
       const axk_bf16x8 ka = *reinterpret_cast<const axk_bf16x8*>(krow + 64 * s);
-      st[0] = mfma_bf16_16x16x32(ka, qb[0][s], st[0]);
-      st[1] = mfma_bf16_16x16x32(ka, qb[1][s], st[1]);
+#pragma unroll
+      for (int i = 0; i < kPfNI; ++i) st[i] = mfma_bf16_16x16x32(ka, qb[i][s], st[i]);
     }
     const int tok0 = ti * kTile + 4 * g;
-    axk_i16x4 pbv[2];
-    float alpha[2];
+    axk_i16x4 pbv[kPfNI];
+    float alpha[kPfNI];
     bool moved = false;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kPfNI; ++i) {
       float mx = -INFINITY;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -910,37 +932,37 @@ __global__ __launch_bounds__(256) void paged_prefill_kernel(
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const axk_i16x4 va = lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (16 * t + 4 * (l16 & 3)) * 2);
-      if (moved) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          o[0][t][rr] *= alpha[0];
-          o[1][t][rr] *= alpha[1];
+      for (int i = 0; i < kPfNI; ++i) {
+        if (moved) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) o[i][t][rr] *= alpha[i];
         }
+        o[i][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[i], o[i][t], 0, 0, 0);
       }
-      o[0][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[0], o[0][t], 0, 0, 0);
-      o[1][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[1], o[1][t], 0, 0, 0);
     }
   };
 
   if (ntiles > 0) {
-    int nv0 = issue(0, 0);
-    int nv1 = issue(1, 1);
+    int nv[kPfAhead];  // valid tokens of tiles ti .. ti + kPfAhead - 1
+#pragma unroll
+    for (int j = 0; j < kPfAhead; ++j) nv[j] = issue(j, j);
     for (int ti = 0; ti < ntiles; ++ti) {
-      const int nb = ti % kNBuf;
-      wait_vmcnt<C::IPW>();
-      __builtin_amdgcn_s_barrier();
-      const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);
-      const int nvalid = nv0;
-      nv0 = nv1;
-      nv1 = nv2;
-      if (nvalid > 0) tile_math(smem + nb * C::BUF, ti, nvalid);
+      wait_vmcnt<(kPfAhead - 1) * C::IPW>();  // this wave's loads of tile ti have landed
+      __builtin_amdgcn_s_barrier();            // ... and every wave's; all are done with tile ti - 1
+      const int nvn = issue(ti + kPfAhead, (ti + kPfAhead) % kPfBuf);  // into the buffer of tile ti - 1
+      const int nvalid = nv[0];
+#pragma unroll
+      for (int j = 0; j + 1 < kPfAhead; ++j) nv[j] = nv[j + 1];
+      nv[kPfAhead - 1] = nvn;
+      if (nvalid > 0) tile_math(smem + (ti % kPfBuf) * C::BUF, ti, nvalid);
     }
     wait_vmcnt<0>();
   }
 
   // lane (row l16 of block i, g) holds O[row][d = 16 t + 4 g .. + 3]
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < kPfNI; ++i) {
     const int r = r_first + kPfRowsPerWave * wave + 16 * i + l16;
     if (r > r_last) continue;
     const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
@@ -959,10 +981,21 @@ int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, c
                    const int* indices, uint16_t* out, int batch, int total_q, int hq, int hkv, int page_size,
                    int64_t num_pages, float sm_scale, int* status, hipStream_t st) {
   const int64_t rows = (int64_t)total_q * (hq / hkv);
-  const int64_t grid = (rows + kPfRows - 1) / kPfRows + batch;  // >= the sum over sequences of their row blocks
-  hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid, (unsigned)hkv), dim3(64 * kWaves),
-                     (size_t)kNBuf * PagedCfg<D>::BUF, st, q, static_cast<const unsigned char*>(cache), qo_indptr,
-                     indptr, last, indices, batch, total_q, hq, hkv, page_size, num_pages, sm_scale, status, out);
+  const int64_t nblk = (rows + kPfRows - 1) / kPfRows + batch;  // >= the sum over sequences of their row blocks
+  const int xph = hkv <= 8 && 8 % hkv == 0 ? 8 / hkv : 0;      // XCDs per KV head
+  const int64_t grid = xph ? 8 * ((nblk + xph - 1) / xph) : nblk * hkv;
+  if (grid > 0x7fffffff) return AXK_E_SHAPE;
+  const size_t lds = (size_t)kPfBuf * PagedCfg<D>::BUF;
+  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+      return AXK_E_LAUNCH;
+    lds_raised = true;
+  }
+  hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid), dim3(64 * kPfWaves), lds, st, q,
+                     static_cast<const unsigned char*>(cache), qo_indptr, indptr, last, indices, batch, total_q, hq,
+                     hkv, page_size, num_pages, sm_scale, xph, status, out);
   return axk_launch_status();
 }
 
@@ -1235,7 +1268,7 @@ extern "C" int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, co
   AXK_REQUIRE(q && kv_cache && qo_indptr && indptr && indices && last_page_len && out, AXK_E_NULL);
   AXK_REQUIRE(batch > 0 && batch <= (1 << 20) && total_q >= 0 && total_q <= (1 << 24), AXK_E_SHAPE);
   AXK_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0, AXK_E_SHAPE);
-  AXK_REQUIRE(num_kv_heads <= 65535 && total_q * num_qo_heads <= ((int64_t)1 << 31) / 256, AXK_E_SHAPE);
+  AXK_REQUIRE(num_kv_heads <= 4096 && total_q * num_qo_heads <= ((int64_t)1 << 31) / 256, AXK_E_SHAPE);
   AXK_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, AXK_E_SHAPE);
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
   AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16) && axk_aligned(out, 8), AXK_E_ALIGN);
