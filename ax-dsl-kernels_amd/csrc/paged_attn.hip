@@ -740,12 +740,13 @@ __global__ __launch_bounds__(256) void paged_kv_write_fp8_kernel(const uint16_t*
 // S^T = K Q^T for its 16 rows and O^T += V^T P^T over the whole head dim. 16 rows per wave keep Q and O in
 // 100 VGPRs (two waves per SIMD); 32 rows per wave overflowed the VGPRs and the compiler moved O between AGPRs and
 // VGPRs on every tile (measured: 700 VALU instructions per tile, 608 us for the 4096-token chunk).
+typedef short axk_s16x8 __attribute__((ext_vector_type(8)));
 constexpr int kPfWaves = 8;
 constexpr int kPfRowsPerWave = 16;
 constexpr int kPfNI = kPfRowsPerWave / 16;  // 16-row MFMA blocks per wave
 constexpr int kPfRows = kPfWaves * kPfRowsPerWave;
-constexpr int kPfAhead = 4;  // tiles in flight while one is computed (the K / V stream from L2 / MALL is latency bound)
-constexpr int kPfBuf = kPfAhead + 1;
+constexpr int kPfAhead = 4;  // tiles in flight while two are computed (even: tiles are taken in pairs)
+constexpr int kPfBuf = kPfAhead + 2;
 
 template <int D>
 __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
@@ -887,20 +888,29 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
     for (int t = 0; t < DT; ++t) o[i][t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  auto tile_math = [&](const unsigned char* kt, int ti, int nvalid) {
-    const unsigned char* vt = kt + C::PLANE;
-    axk_f32x4 st[kPfNI];
+  // the math of tiles ti and ti + 1 (K planes ka, kb; V planes PLANE after them; na, nb valid tokens). The 32 tokens
+  // are one k-step of the 16x16x32 PV MFMA: k = 8 g + j is token 4 g + j of tile ti for j < 4 and token 4 g + j - 4
+  // of tile ti + 1 otherwise, in both operands (P^T from the two score tiles, V^T from one transposing read of each).
+  // The softmax reference max is raised only when a row's scores pass it by more than kPfSlack (log2 units), so
+  // p <= 2^kPfSlack and O is rescaled only on those rare tiles.
+  constexpr float kPfSlack = 8.0f;
+  auto pair_math = [&](const unsigned char* ka, const unsigned char* kb, int ti, int na, int nb) {
+    axk_f32x4 sa[kPfNI], sb[kPfNI];
 #pragma unroll
-    for (int i = 0; i < kPfNI; ++i) st[i] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-    const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
+    for (int i = 0; i < kPfNI; ++i) sa[i] = sb[i] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+    const int roff = C::row_off(l16) + 16 * g;
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) {
-      const axk_bf16x8 ka = *reinterpret_cast<const axk_bf16x8*>(krow + 64 * s);
+      const axk_bf16x8 fa = *reinterpret_cast<const axk_bf16x8*>(ka + roff + 64 * s);
+      const axk_bf16x8 fb = *reinterpret_cast<const axk_bf16x8*>(kb + roff + 64 * s);
 #pragma unroll
-      for (int i = 0; i < kPfNI; ++i) st[i] = mfma_bf16_16x16x32(ka, qb[i][s], st[i]);
+      for (int i = 0; i < kPfNI; ++i) {
+        sa[i] = mfma_bf16_16x16x32(fa, qb[i][s], sa[i]);
+        sb[i] = mfma_bf16_16x16x32(fb, qb[i][s], sb[i]);
+      }
     }
     const int tok0 = ti * kTile + 4 * g;
-    axk_i16x4 pbv[kPfNI];
+    axk_bf16x8 pb8[kPfNI];
     float alpha[kPfNI];
     bool moved = false;
 #pragma unroll
@@ -908,54 +918,65 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       float mx = -INFINITY;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const bool ok = 4 * g + rr < nvalid && tok0 + rr <= pos[i];
-        const float sv = ok ? st[i][rr] * c : -INFINITY;
-        st[i][rr] = sv;
-        mx = fmaxf(mx, sv);
+        const float va = (4 * g + rr < na && tok0 + rr <= pos[i]) ? sa[i][rr] * c : -INFINITY;
+        const float vb = (4 * g + rr < nb && tok0 + kTile + rr <= pos[i]) ? sb[i][rr] * c : -INFINITY;
+        sa[i][rr] = va;
+        sb[i][rr] = vb;
+        mx = fmaxf(mx, fmaxf(va, vb));
       }
       mx = xor32_max(xor16_max(mx));
-      const float m_new = fmaxf(m_run[i], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a row that has seen nothing yet stays at zero
-      moved |= __builtin_amdgcn_ballot_w64(m_new > m_run[i]) != 0;
-      alpha[i] = __builtin_amdgcn_exp2f(m_run[i] - m_use);
+      const bool raise = mx > m_run[i] + kPfSlack;  // -inf + slack stays -inf: a row's first visible score raises
+      moved |= __builtin_amdgcn_ballot_w64(raise) != 0;
+      alpha[i] = raise ? __builtin_amdgcn_exp2f(m_run[i] - mx) : 1.0f;
+      if (raise) m_run[i] = mx;
+      const float m_use = m_run[i] == -INFINITY ? 0.f : m_run[i];  // a row that has seen nothing stays at zero
+      axk_s16x8 pbits;
       float psum = 0.f;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const float pv = st[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[i][rr] - m_use);
-        psum += pv;
-        pbv[i][rr] = (short)f32_to_bf16_bits(pv);
+        const float pa = sa[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sa[i][rr] - m_use);
+        const float pbv = sb[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sb[i][rr] - m_use);
+        psum += pa + pbv;
+        pbits[rr] = (short)f32_to_bf16_bits(pa);
+        pbits[4 + rr] = (short)f32_to_bf16_bits(pbv);
       }
+      pb8[i] = __builtin_bit_cast(axk_bf16x8, pbits);
       psum = xor32_sum(xor16_sum(psum));
       l_run[i] = l_run[i] * alpha[i] + psum;
-      m_run[i] = m_new;
     }
+    const int voff = C::PLANE + C::row_off(4 * g + (l16 >> 2)) + 8 * (l16 & 3);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-      const axk_i16x4 va = lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (16 * t + 4 * (l16 & 3)) * 2);
+      const axk_s16x4 va = lds_read_tr16(ka + voff + 32 * t);
+      const axk_s16x4 vb = lds_read_tr16(kb + voff + 32 * t);
+      const axk_bf16x8 v8 = __builtin_bit_cast(axk_bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int i = 0; i < kPfNI; ++i) {
         if (moved) {
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) o[i][t][rr] *= alpha[i];
         }
-        o[i][t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pbv[i], o[i][t], 0, 0, 0);
+        o[i][t] = mfma_bf16_16x16x32(v8, pb8[i], o[i][t]);
       }
     }
   };
 
   if (ntiles > 0) {
+    // tiles land kPfAhead ahead in a ring of kPfBuf = kPfAhead + 2; an iteration computes two
     int nv[kPfAhead];  // valid tokens of tiles ti .. ti + kPfAhead - 1
 #pragma unroll
     for (int j = 0; j < kPfAhead; ++j) nv[j] = issue(j, j);
-    for (int ti = 0; ti < ntiles; ++ti) {
-      wait_vmcnt<(kPfAhead - 1) * C::IPW>();  // this wave's loads of tile ti have landed
-      __builtin_amdgcn_s_barrier();            // ... and every wave's; all are done with tile ti - 1
-      const int nvn = issue(ti + kPfAhead, (ti + kPfAhead) % kPfBuf);  // into the buffer of tile ti - 1
-      const int nvalid = nv[0];
+    for (int ti = 0; ti < ntiles; ti += 2) {
+      wait_vmcnt<(kPfAhead - 2) * C::IPW>();  // this wave's loads of tiles ti, ti + 1 have landed
+      __builtin_amdgcn_s_barrier();            // ... and every wave's; all are done with tiles ti - 2, ti - 1
+      const int n0 = issue(ti + kPfAhead, (ti + kPfAhead) % kPfBuf);  // into the buffers of tiles ti - 2, ti - 1
+      const int n1 = issue(ti + kPfAhead + 1, (ti + kPfAhead + 1) % kPfBuf);
+      const int na = nv[0], nb = nv[1];
 #pragma unroll
-      for (int j = 0; j + 1 < kPfAhead; ++j) nv[j] = nv[j + 1];
-      nv[kPfAhead - 1] = nvn;
-      if (nvalid > 0) tile_math(smem + (ti % kPfBuf) * C::BUF, ti, nvalid);
+      for (int j = 0; j + 2 < kPfAhead; ++j) nv[j] = nv[j + 2];
+      nv[kPfAhead - 2] = n0;
+      nv[kPfAhead - 1] = n1;
+      if (na + nb > 0) pair_math(smem + (ti % kPfBuf) * C::BUF, smem + ((ti + 1) % kPfBuf) * C::BUF, ti, na, nb);
     }
     wait_vmcnt<0>();
   }
