@@ -929,13 +929,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       moved |= __builtin_amdgcn_ballot_w64(raise) != 0;
       alpha[i] = raise ? __builtin_amdgcn_exp2f(m_run[i] - mx) : 1.0f;
       if (raise) m_run[i] = mx;
-      const float m_use = m_run[i] == -INFINITY ? 0.f : m_run[i];  // a row that has seen nothing stays at zero
+      // a row that has seen nothing stays at zero: its scores are all -inf and exp2(-inf) = 0
+      const float m_use = m_run[i] == -INFINITY ? 0.f : m_run[i];
       axk_s16x8 pbits;
       float psum = 0.f;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const float pa = sa[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sa[i][rr] - m_use);
-        const float pbv = sb[i][rr] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sb[i][rr] - m_use);
+        const float pa = __builtin_amdgcn_exp2f(sa[i][rr] - m_use);
+        const float pbv = __builtin_amdgcn_exp2f(sb[i][rr] - m_use);
         psum += pa + pbv;
         pbits[rr] = (short)f32_to_bf16_bits(pa);
         pbits[4 + rr] = (short)f32_to_bf16_bits(pbv);
@@ -944,6 +945,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       psum = xor32_sum(xor16_sum(psum));
       l_run[i] = l_run[i] * alpha[i] + psum;
     }
+    if (moved) {  // wave-uniform and rare: a branch, not a select per accumulator
+#pragma unroll
+      for (int i = 0; i < kPfNI; ++i)
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) o[i][t][rr] *= alpha[i];
+    }
     const int voff = C::PLANE + C::row_off(4 * g + (l16 >> 2)) + 8 * (l16 & 3);
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -951,13 +960,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       const axk_s16x4 vb = lds_read_tr16(kb + voff + 32 * t);
       const axk_bf16x8 v8 = __builtin_bit_cast(axk_bf16x8, __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-      for (int i = 0; i < kPfNI; ++i) {
-        if (moved) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) o[i][t][rr] *= alpha[i];
-        }
-        o[i][t] = mfma_bf16_16x16x32(v8, pb8[i], o[i][t]);
-      }
+      for (int i = 0; i < kPfNI; ++i) o[i][t] = mfma_bf16_16x16x32(v8, pb8[i], o[i][t]);
     }
   };
 
@@ -976,7 +979,9 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       for (int j = 0; j + 2 < kPfAhead; ++j) nv[j] = nv[j + 2];
       nv[kPfAhead - 2] = n0;
       nv[kPfAhead - 1] = n1;
-      if (na + nb > 0) pair_math(smem + (ti % kPfBuf) * C::BUF, smem + ((ti + 1) % kPfBuf) * C::BUF, ti, na, nb);
+      unsigned char* ka = smem + (ti % kPfBuf) * C::BUF;
+      unsigned char* kb = smem + ((ti + 1) % kPfBuf) * C::BUF;
+      if (na + nb > 0) pair_math(ka, kb, ti, na, nb);
     }
     wait_vmcnt<0>();
   }
