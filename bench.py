@@ -307,7 +307,7 @@ class PagedPrefillWorkload(Workload):
     kernel = "paged_prefill_kernel<256>"
     timing = "graph"
     mfma = True
-    traffic_profile = None
+    traffic_profile = "paged_prefill_chunk4096_pmc.txt"
     T = 4096
 
     def __init__(self, dev):
