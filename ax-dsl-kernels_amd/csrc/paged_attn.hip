@@ -894,7 +894,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
   // The softmax reference max is raised only when a row's scores pass it by more than kPfSlack (log2 units), so
   // p <= 2^kPfSlack and O is rescaled only on those rare tiles.
   constexpr float kPfSlack = 8.0f;
-  auto pair_math = [&](const unsigned char* ka, const unsigned char* kb, int ti, int na, int nb) {
+  // the lowest position among this wave's rows (-1 if it holds an invalid row): a pair of full tiles wholly at or
+  // before it needs no mask (every wave-uniform)
+  int pos_lo = pos[0];
+#pragma unroll
+  for (int i = 1; i < kPfNI; ++i) pos_lo = min(pos_lo, pos[i]);
+#pragma unroll
+  for (int o2 = 1; o2 < 16; o2 <<= 1) pos_lo = min(pos_lo, __shfl_xor(pos_lo, o2, 64));
+  auto pair_math = [&](const unsigned char* ka, const unsigned char* kb, int ti, int na, int nb, bool full) {
     axk_f32x4 sa[kPfNI], sb[kPfNI];
 #pragma unroll
     for (int i = 0; i < kPfNI; ++i) sa[i] = sb[i] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
@@ -915,15 +922,25 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
     bool moved = false;
 #pragma unroll
     for (int i = 0; i < kPfNI; ++i) {
-      float mx = -INFINITY;
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const float va = (4 * g + rr < na && tok0 + rr <= pos[i]) ? sa[i][rr] * c : -INFINITY;
-        const float vb = (4 * g + rr < nb && tok0 + kTile + rr <= pos[i]) ? sb[i][rr] * c : -INFINITY;
-        sa[i][rr] = va;
-        sb[i][rr] = vb;
-        mx = fmaxf(mx, fmaxf(va, vb));
+        sa[i][rr] *= c;
+        sb[i][rr] *= c;
       }
+      if (!full) {
+        // token tok0 + rr of tile ti is visible iff rr <= la (inside the tile's valid rows and at or before the
+        // row's position); tile ti + 1 likewise with lb
+        const int la = min(pos[i], ti * kTile + na - 1) - tok0;
+        const int lb = min(pos[i], ti * kTile + kTile + nb - 1) - tok0 - kTile;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          if (rr > la) sa[i][rr] = -INFINITY;
+          if (rr > lb) sb[i][rr] = -INFINITY;
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) mx = fmaxf(mx, fmaxf(sa[i][rr], sb[i][rr]));
       mx = xor32_max(xor16_max(mx));
       const bool raise = mx > m_run[i] + kPfSlack;  // -inf + slack stays -inf: a row's first visible score raises
       moved |= __builtin_amdgcn_ballot_w64(raise) != 0;
@@ -981,7 +998,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       nv[kPfAhead - 1] = n1;
       unsigned char* ka = smem + (ti % kPfBuf) * C::BUF;
       unsigned char* kb = smem + ((ti + 1) % kPfBuf) * C::BUF;
-      if (na + nb > 0) pair_math(ka, kb, ti, na, nb);
+      const bool full = na == kTile && nb == kTile && ti * kTile + 2 * kTile - 1 <= pos_lo;
+      if (na + nb > 0) pair_math(ka, kb, ti, na, nb, full);
     }
     wait_vmcnt<0>();
   }
