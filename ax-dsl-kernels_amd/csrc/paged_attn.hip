@@ -842,7 +842,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
       pid = j < npg ? indices[pb + j] : 0;
       asm volatile("" : "+v"(pid));
     }
-    int page = __builtin_amdgcn_readfirstlane(__shfl(pid, lp & 63, 64));
+    int page = __builtin_amdgcn_readlane(pid, lp & 63);  // lp is wave-uniform: a lane read, no LDS round trip
     const int valid_in_page = (lp == npg - 1) ? last : page_size;
     nvalid = min(kTile, valid_in_page - tp * kTile);
     if (page < 0 || page >= num_pages) {
