@@ -10,15 +10,16 @@ Restates, with the reference's rounding points (bf16 tensors between ops, fp32 i
                        given as bf16 (rope_cos_sin, q35_step.py:408-411)
   * qk_norm_rope, sigmoid_mul, silu_mul, add: attn_block / mlp_block (q35_step.py:136-139, 191-197, 276-279)
 Pinned by tests/test_oracle_layer.py against transformers' Qwen3_5RMSNorm, Qwen3_5RMSNormGated and
-apply_rotary_pos_emb (third-party, installed), torch.nn.functional.conv1d, and closed forms.
+apply_rotary_pos_emb (third-party, installed), torch.nn.functional.conv1d, and closed forms; the whole decode
+layers (gdn_layer_decode, attn_layer_decode) token by token against transformers' Qwen3_5DecoderLayer run over
+the same tokens in fp32 (oracle.rounding.fp32() switches the bf16 points off), and the bf16 schedule within
+tolerance of that fp32 composition.
 """
 from __future__ import annotations
 
 import torch
 
-
-def _bf(x: torch.Tensor) -> torch.Tensor:
-    return x.to(torch.bfloat16)
+from .rounding import bf as _bf
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -72,7 +73,7 @@ def rope_cos_sin(pos: torch.Tensor, rot: int, theta: float) -> tuple[torch.Tenso
     """bf16 cos / sin [B, rot/2] of each sequence's position (q35_step.py:408-411)."""
     inv = 1.0 / (theta ** (torch.arange(0, rot, 2, dtype=torch.int64).float() / rot))
     f = pos.float().reshape(-1, 1) * inv.reshape(1, -1)
-    return f.cos().bfloat16(), f.sin().bfloat16()
+    return _bf(f.cos()), _bf(f.sin())
 
 
 def sigmoid_mul(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
@@ -94,7 +95,7 @@ def add(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
 def _fp8(a: torch.Tensor, w: dict, name: str) -> torch.Tensor:
     from oracle import mx
 
-    return mx.fp8_linear(a, w["w_" + name].numpy(), None, w["s_" + name]).to(torch.bfloat16)
+    return _bf(mx.fp8_linear(a, w["w_" + name].numpy(), None, w["s_" + name]))
 
 
 def mlp_residual(x: torch.Tensor, y: torch.Tensor, w: dict, eps: float) -> torch.Tensor:
@@ -102,9 +103,9 @@ def mlp_residual(x: torch.Tensor, y: torch.Tensor, w: dict, eps: float) -> torch
     from oracle import mx
 
     x1, h2 = add_rmsnorm(x, y, w["ln2"], eps)
-    g = mx.mx_linear(h2, w["gate_w"].numpy(), w["gate_s"].numpy()).to(torch.bfloat16)
-    u = mx.mx_linear(h2, w["up_w"].numpy(), w["up_s"].numpy()).to(torch.bfloat16)
-    d = mx.mx_linear(silu_mul(g, u), w["down_w"].numpy(), w["down_s"].numpy()).to(torch.bfloat16)
+    g = _bf(mx.mx_linear(h2, w["gate_w"].numpy(), w["gate_s"].numpy()))
+    u = _bf(mx.mx_linear(h2, w["up_w"].numpy(), w["up_s"].numpy()))
+    d = _bf(mx.mx_linear(silu_mul(g, u), w["down_w"].numpy(), w["down_s"].numpy()))
     return add(x1, d)
 
 
@@ -122,7 +123,7 @@ def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_head
     k = m[:, kd:2 * kd].reshape(b, 1, num_k_heads, 128)
     v = m[:, 2 * kd:].reshape(b, 1, num_v_heads, 128)
     core, state_out = gdn.gdn_fp32(q, k, v, aa[:, None], bb[:, None], w["a_log"], w["dt_bias"], state_in)
-    core = core.to(torch.bfloat16).reshape(b * num_v_heads, 128)
+    core = _bf(core).reshape(b * num_v_heads, 128)
     gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(b * num_v_heads, 128), eps).reshape(b, vd)
     return mlp_residual(x, _fp8(gated, w, "out"), w, eps), state_out, conv_out
 
@@ -143,6 +144,6 @@ def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
     q = qk_norm_rope(qg[..., :d], w["q_norm"], cos, sin, rot, eps)
     k = qk_norm_rope(kk, w["k_norm"], cos, sin, rot, eps)
     cache2 = paged_attn.store_paged_kv(cache, k, vv, cache_location.numpy())
-    attn = paged_attn.paged_decode(q, cache2, indptr, indices, last_page_len, scale).to(torch.bfloat16)
+    attn = _bf(paged_attn.paged_decode(q, cache2, indptr, indices, last_page_len, scale))
     gated = sigmoid_mul(attn, qg[..., d:]).reshape(b, num_qo_heads * d)
     return mlp_residual(x, _fp8(gated, w, "o"), w, eps), cache2

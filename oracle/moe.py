@@ -9,7 +9,10 @@ Restates
   * experts       q35_moe.py:96-113 (moe_experts_gu) and q35_layer_mc.py:830-853 (moe_full): gate-up rows
                   [gate | up] of one [2F, H] matrix, y = act Wd^T (fp32) * rw, out = bf16(base + sum_k y_k)
   * moe_parts     base, routed sum and the bound on one-ulp flips of the bf16 activations (see its docstring)
-Pinned by tests/test_oracle_moe.py: torch.topk / stable sort agreement, a dense all-experts formulation
+Pinned by tests/test_oracle_moe.py: against transformers' Qwen3_5MoeSparseMoeBlock (third-party, installed; the
+reference's own oracle family, q35_moe.py:300-312) holding the exactly dequantised weights: router ids and
+weights equal, and the layer equal at fp32 tolerance with the bf16 points switched off (oracle.rounding.fp32());
+the bf16 schedule within tolerance of that; torch.topk / stable sort agreement, a dense all-experts formulation
 (every token through every expert, masked by the routing) and closed-form special cases (one expert with
 weight 1, zero router); the flip bound by flipping activations on purpose.
 """
@@ -20,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from . import mx
+from .rounding import bf as _bf
 
 
 def route(logits: torch.Tensor, top_k: int, norm: bool = True):
@@ -45,9 +49,9 @@ def swiglu_act(h: torch.Tensor, gw, gs, split: int | None = None, uw=None, us=No
         wg, wu = wgu[:split], wgu[split:]
     else:
         wg, wu = _deq(gw, gs), _deq(uw, us)
-    g = (h.float() @ wg.T).to(torch.bfloat16).float()
-    u = (h.float() @ wu.T).to(torch.bfloat16).float()
-    return (F.silu(g) * u).to(torch.bfloat16).float()
+    g = _bf(h.float() @ wg.T).float()
+    u = _bf(h.float() @ wu.T).float()
+    return _bf(F.silu(g) * u).float()
 
 
 def swiglu_expert(h: torch.Tensor, gw, gs, dw, ds, split: int | None = None, uw=None, us=None) -> torch.Tensor:
@@ -102,8 +106,8 @@ def moe_layer(h2, weights, top_k=8, x_res=None, norm=True, ids=None, wts=None, r
         ids, wts = route(logits, top_k, norm)
     base, routed, _ = moe_parts(h2, w, ids, wts, x_res)
     if round_base:
-        base = base.to(torch.bfloat16).float()
-    return (base + routed).to(torch.bfloat16), logits, ids, wts
+        base = _bf(base).float()
+    return _bf(base + routed), logits, ids, wts
 
 
 def base_ulp(h2, weights, x_res):

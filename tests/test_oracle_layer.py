@@ -3,7 +3,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle import layer
+from oracle import layer, rounding
 
 
 def _g(seed):
@@ -107,3 +107,161 @@ def test_elementwise_gates_special_values():
     s, n = layer.add_rmsnorm(x, x, torch.ones(4))
     assert torch.equal(s, (2 * x.float()).bfloat16())
     assert torch.equal(n, layer.rmsnorm(s, torch.ones(4)))
+
+
+# ---------------------------------------------------------------------------------------------
+# Whole decode layers against transformers' Qwen3_5DecoderLayer (fp32, the dequantised weights)
+# ---------------------------------------------------------------------------------------------
+def _deq_fp8(w, s):
+    from oracle import mx
+
+    return torch.from_numpy(mx.e4m3_table()[w.numpy()]) * s.float()[:, None]
+
+
+def _deq_mx(c, s):
+    from oracle import mx
+
+    return torch.from_numpy(mx.dequant_mxfp4(c.numpy(), s.numpy()))
+
+
+def _hf_layer(kind, w, hidden, inter, **kw):
+    """transformers' Qwen3_5DecoderLayer (fp32, eager attention) holding the layer's dequantised weights. The
+    kernel contract passes norm weights as 1 + weight (q35_step.py:346-348); transformers adds the 1 itself."""
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5DecoderLayer
+
+    cfg = Qwen3_5TextConfig(hidden_size=hidden, intermediate_size=inter, num_hidden_layers=1, hidden_act="silu",
+                            layer_types=[kind], rms_norm_eps=1e-6, **kw)
+    cfg._attn_implementation = "eager"
+    m = Qwen3_5DecoderLayer(cfg, 0).float().eval()
+    with torch.no_grad():
+        m.input_layernorm.weight.copy_(w["ln1"] - 1)
+        m.post_attention_layernorm.weight.copy_(w["ln2"] - 1)
+        m.mlp.gate_proj.weight.copy_(_deq_mx(w["gate_w"], w["gate_s"]))
+        m.mlp.up_proj.weight.copy_(_deq_mx(w["up_w"], w["up_s"]))
+        m.mlp.down_proj.weight.copy_(_deq_mx(w["down_w"], w["down_s"]))
+        if kind == "linear_attention":
+            la = m.linear_attn
+            la.in_proj_qkv.weight.copy_(_deq_fp8(w["w_qkv"], w["s_qkv"]))
+            la.in_proj_z.weight.copy_(_deq_fp8(w["w_z"], w["s_z"]))
+            la.in_proj_b.weight.copy_(_deq_fp8(w["w_b"], w["s_b"]))
+            la.in_proj_a.weight.copy_(_deq_fp8(w["w_a"], w["s_a"]))
+            # column 0 of conv_w multiplies the current token; torch's last tap does
+            la.conv1d.weight.copy_(w["conv_w"].float().flip(-1)[:, None, :])
+            la.A_log.copy_(w["a_log"])
+            la.dt_bias.copy_(w["dt_bias"])
+            la.norm.weight.copy_(w["norm_w"])
+            la.out_proj.weight.copy_(_deq_fp8(w["w_out"], w["s_out"]))
+        else:
+            sa = m.self_attn
+            sa.q_proj.weight.copy_(_deq_fp8(w["w_q"], w["s_q"]))
+            sa.k_proj.weight.copy_(_deq_fp8(w["w_k"], w["s_k"]))
+            sa.v_proj.weight.copy_(_deq_fp8(w["w_v"], w["s_v"]))
+            sa.o_proj.weight.copy_(_deq_fp8(w["w_o"], w["s_o"]))
+            sa.q_norm.weight.copy_(w["q_norm"] - 1)
+            sa.k_norm.weight.copy_(w["k_norm"] - 1)
+    return m, cfg
+
+
+def _gdn_decode_tokens(x, w, nk, nv, conv_k=4):
+    """The oracle's decode layer applied token by token from zero GDN and conv states."""
+    b, t, _ = x.shape
+    c = (2 * nk + nv) * 128
+    st = torch.zeros(b, nv, 128, 128)
+    cv = torch.zeros(b, conv_k - 1, c, dtype=x.dtype)
+    outs = []
+    for i in range(t):
+        o, st, cv = layer.gdn_layer_decode(x[:, i], w, st, cv, nk, nv)
+        outs.append(o.float())
+    return torch.stack(outs, 1), st
+
+
+@pytest.mark.parametrize("b,t,nk,nv", [(2, 5, 1, 2), (1, 9, 2, 4)])
+def test_gdn_layer_decode_matches_transformers_decoder_layer(b, t, nk, nv):
+    """q35_step.py gdn_layer (149-183) + mlp_block (118-142) decoded token by token == transformers'
+    linear-attention decoder layer over the same tokens (its conv over the window and its chunked delta rule:
+    an independent formulation). Pins projection roles (qkv | z | b | a), the conv tap order, the q / k / v
+    split and the grouped key heads, the gates, the output norm gated by silu(z), and both residuals."""
+    from axk import configs
+
+    hidden, inter = 128, 64
+    w = configs.gdn_layer_weights(_g(40 + t), hidden, inter, nk, nv)
+    m, _ = _hf_layer("linear_attention", w, hidden, inter, linear_num_key_heads=nk, linear_num_value_heads=nv,
+                     linear_key_head_dim=128, linear_value_head_dim=128, linear_conv_kernel_dim=4)
+    x = torch.randn(b, t, hidden, generator=_g(41 + t))
+    dummy = torch.zeros(b, t, 64)
+    with torch.no_grad():
+        ref = m(x, position_embeddings=(dummy, dummy))
+    with rounding.fp32():
+        got, _ = _gdn_decode_tokens(x, w, nk, nv)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+    # the reference's bf16 points keep the composed layer within the fused-layer bar (test_gdn_attn.py:354)
+    got_bf, _ = _gdn_decode_tokens(x.bfloat16(), w, nk, nv)
+    torch.testing.assert_close(got_bf, ref, rtol=5e-2, atol=0.0625)
+    # slips that the pin must catch: z gate off, conv taps in torch order, value heads paired with the other key head
+    for name, bad_w in (("z", dict(w, w_z=torch.zeros_like(w["w_z"]))),
+                        ("conv", dict(w, conv_w=w["conv_w"].flip(-1).contiguous()))):
+        with rounding.fp32():
+            bad, _ = _gdn_decode_tokens(x, bad_w, nk, nv)
+        assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3), name
+
+
+def _attn_decode_tokens(x, w, hq, hkv, d, rot, theta, page, g):
+    """The oracle's attention decode layer, token by token, over a paged cache that grows by one token per step
+    (pages drawn from a shuffled pool, the new token's page appended when it starts)."""
+    from oracle import paged_attn  # noqa: F401  (the layer oracle calls it)
+
+    b, t, _ = x.shape
+    pages_per_seq = -(-t // page)
+    pool = torch.randperm(b * pages_per_seq + 3, generator=g).to(torch.int32)
+    cache = torch.randn(pool.numel() + 1, 2, page, hkv, d, generator=g)  # garbage beyond the written rows
+    cache = cache.to(x.dtype)
+    inv = 1.0 / (theta ** (torch.arange(0, rot, 2, dtype=torch.int64).float() / rot))
+    outs = []
+    for i in range(t):
+        npg = i // page + 1
+        indices = torch.cat([pool[s * pages_per_seq: s * pages_per_seq + npg] for s in range(b)])
+        indptr = torch.arange(0, b * npg + 1, npg, dtype=torch.int32)
+        lpl = torch.full((b,), i % page + 1, dtype=torch.int32)
+        loc = torch.tensor([[int(pool[s * pages_per_seq + npg - 1]), i % page] for s in range(b)], dtype=torch.int32)
+        f = torch.full((b, 1), float(i)) * inv[None, :]
+        cos, sin = rounding.bf(f.cos()), rounding.bf(f.sin())
+        o, cache = layer.attn_layer_decode(x[:, i], w, cos, sin, cache, indptr, indices, lpl, loc, hq, rot)
+        outs.append(o.float())
+    return torch.stack(outs, 1)
+
+
+@pytest.mark.parametrize("b,t,hq,hkv,page", [(2, 7, 4, 2, 4), (1, 11, 6, 2, 8)])
+def test_attn_layer_decode_matches_transformers_decoder_layer(b, t, hq, hkv, page):
+    """q35_step.py attn_block (186-293) + mlp_block decoded token by token over the paged cache == transformers'
+    full-attention decoder layer with a causal mask over the same tokens. Pins the per-head [q | gate] split of
+    the q projection, the (1 + w) q / k norms, partial NeoX RoPE (64 of 256 channels) at each position, GQA
+    grouping, the sigmoid output gate, the paged KV write / read and both residuals."""
+    from axk import configs
+
+    hidden, inter, d, rot, theta = 128, 64, 256, 64, 10_000_000.0
+    w = configs.attn_layer_weights(_g(50 + t), hidden, inter, hq, hkv, d)
+    m, cfg = _hf_layer("full_attention", w, hidden, inter, num_attention_heads=hq, num_key_value_heads=hkv,
+                       head_dim=d, rope_parameters={"rope_type": "default", "rope_theta": theta,
+                                                    "partial_rotary_factor": rot / d})
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    x = torch.randn(b, t, hidden, generator=_g(51 + t))
+    pos = torch.arange(t)[None].expand(b, t)
+    cos, sin = Qwen3_5TextRotaryEmbedding(cfg)(x, pos)
+    mask = torch.full((t, t), float("-inf")).triu(1)[None, None].expand(b, 1, t, t)
+    with torch.no_grad():
+        ref = m(x, position_embeddings=(cos, sin), attention_mask=mask)
+    with rounding.fp32():
+        got = _attn_decode_tokens(x, w, hq, hkv, d, rot, theta, page, _g(52))
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+    got_bf = _attn_decode_tokens(x.bfloat16(), w, hq, hkv, d, rot, theta, page, _g(52))
+    torch.testing.assert_close(got_bf, ref, rtol=5e-2, atol=0.0625)
+    # slips the pin must catch: [gate | q] instead of [q | gate], RoPE on the wrong channels (no rotation)
+    q = w["w_q"].reshape(hq, 2, d, hidden)
+    for name, bad_w, bad_rot in (("gate order", dict(w, w_q=q.flip(1).reshape(hq * 2 * d, hidden),
+                                                     s_q=w["s_q"].reshape(hq, 2, d).flip(1).reshape(-1)), rot),
+                                 ("no rope", w, 0)):
+        with rounding.fp32():
+            bad = _attn_decode_tokens(x, bad_w, hq, hkv, d, bad_rot, theta, page, _g(52))
+        assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3), name

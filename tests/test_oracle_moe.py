@@ -1,9 +1,10 @@
 """Pins the MoE oracle (CPU only)."""
 import numpy as np
+import pytest
 import torch
 
 from axk import configs
-from oracle import moe, mx
+from oracle import moe, mx, rounding
 
 
 def _small(seed=0, t=6, h=64, e=8, f=32, fs=32, k=3):
@@ -89,3 +90,76 @@ def test_flip_slack_bounds_flipped_activations():
     diff = (moved - routed).abs()
     assert diff.max() > 0
     assert (diff <= slack + 1e-5).all()
+
+
+def _hf_moe_block(w, top_k):
+    """transformers' Qwen3_5MoeSparseMoeBlock (fp32, eager experts) holding the exactly dequantised weights."""
+    from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
+    from transformers.models.qwen3_5_moe.modeling_qwen3_5_moe import Qwen3_5MoeSparseMoeBlock
+
+    e, two_f, h = w["e_gw"].shape[0], w["e_gw"].shape[1], w["w_router"].shape[1]
+    cfg = Qwen3_5MoeTextConfig(hidden_size=h, num_experts=e, moe_intermediate_size=two_f // 2,
+                               shared_expert_intermediate_size=w["w_gate"].shape[0], num_experts_per_tok=top_k,
+                               num_hidden_layers=1, layer_types=["full_attention"], hidden_act="silu")
+    cfg._experts_implementation = "eager"
+    blk = Qwen3_5MoeSparseMoeBlock(cfg).float().eval()
+
+    def deq(c, s):
+        return torch.from_numpy(mx.dequant_mxfp4(np.asarray(c), np.asarray(s)))
+
+    with torch.no_grad():
+        blk.gate.weight.copy_(w["w_router"].float())
+        blk.experts.gate_up_proj.copy_(torch.stack([deq(w["e_gw"][j], w["e_gs"][j]) for j in range(e)]))
+        blk.experts.down_proj.copy_(torch.stack([deq(w["e_dw"][j], w["e_ds"][j]) for j in range(e)]))
+        blk.shared_expert.gate_proj.weight.copy_(deq(w["w_gate"], w["s_gate"]))
+        blk.shared_expert.up_proj.weight.copy_(deq(w["w_up"], w["s_up"]))
+        blk.shared_expert.down_proj.weight.copy_(deq(w["w_down"], w["s_down"]))
+        blk.shared_expert_gate.weight.copy_(w["w_shg"].float().reshape(1, -1))
+    return blk
+
+
+@pytest.mark.parametrize("seed,t,h,e,f,fs,k", [(0, 6, 64, 8, 32, 32, 3), (4, 17, 128, 16, 64, 96, 8),
+                                                (5, 3, 64, 32, 32, 64, 4)])
+def test_moe_layer_matches_transformers_sparse_moe_block(seed, t, h, e, f, fs, k):
+    """The reference's own oracle family (q35_moe.py:300-312): transformers' Qwen3_5MoeSparseMoeBlock with the
+    dequantised MXFP4 experts, shared expert and sigmoid gate. Pins the router (softmax -> top-K -> renormalise),
+    the [gate | up] split of the gate-up matrix, silu(gate) * up, the sigmoid-gated shared expert and the sum."""
+    h2, x, w, _ = _small(seed=seed, t=t, h=h, e=e, f=f, fs=fs, k=k)
+    blk = _hf_moe_block(w, k)
+    with torch.no_grad():
+        ref = blk(h2.float()[None])[0]
+        _, hf_w, hf_ids = blk.gate(h2.float())
+    logits = h2.float() @ w["w_router"].float().T
+    ids, wts = moe.route(logits, k)
+    assert torch.equal(ids.long(), hf_ids)
+    torch.testing.assert_close(wts, hf_w, rtol=1e-6, atol=1e-7)
+    with rounding.fp32():
+        out, *_ = moe.moe_layer(h2, w, k, x_res=x, ids=ids, wts=wts, round_base=False)
+    assert out.dtype == torch.float32
+    torch.testing.assert_close(out, x.float() + ref, rtol=1e-5, atol=1e-5)
+    # the bf16 rounding points (q35_moe.py:96-137) stay within the north-star bar of the fp32 composition
+    out_bf, *_ = moe.moe_layer(h2, w, k, x_res=x, ids=ids, wts=wts)
+    torch.testing.assert_close(out_bf.float(), x.float() + ref, rtol=2e-2, atol=1e-2)
+
+
+def test_transformers_pin_detects_plausible_slips():
+    """Each slip a restatement could make moves the output far outside the fp32 bar of the pin above."""
+    h2, x, w, k = _small(seed=9, t=8, h=64, e=8, f=32, fs=32, k=3)
+    blk = _hf_moe_block(w, k)
+    with torch.no_grad():
+        ref = x.float() + blk(h2.float()[None])[0]
+    ids, wts = moe.route(h2.float() @ w["w_router"].float().T, k)
+
+    def run(wd, **kw):
+        with rounding.fp32():
+            return moe.moe_layer(h2, wd, k, x_res=x, ids=ids, wts=wts, round_base=False)[0]
+
+    f = w["e_gw"].shape[1] // 2
+    swapped = dict(w, e_gw=torch.cat([w["e_gw"][:, f:], w["e_gw"][:, :f]], 1),
+                   e_gs=torch.cat([w["e_gs"][:, f:], w["e_gs"][:, :f]], 1))
+    no_gate = {n: v for n, v in w.items() if n != "w_shg"}  # shared expert ungated
+    for bad in (run(swapped), run(no_gate)):
+        assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3)
+    with rounding.fp32():
+        unnorm = moe.moe_layer(h2, w, k, x_res=x, norm=False, round_base=False)[0]  # weights not renormalised
+    assert not torch.allclose(unnorm, ref, rtol=1e-3, atol=1e-3)
