@@ -15,6 +15,7 @@ def load_library():
 
 from . import attention  # noqa: E402
 from .attention import (  # noqa: E402
+    paged_attention_decode,
     paged_decode,
     paged_decode_plan,
     paged_decode_run,
@@ -25,7 +26,7 @@ from .attention import (  # noqa: E402
     paged_prefill,
 )
 
-__all__ += ["attention", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
+__all__ += ["attention", "paged_attention_decode", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
             "store_paged_kv", "paged_decode_fp8", "store_paged_kv_fp8",
             "paged_prefill"]
 

@@ -63,11 +63,12 @@ SIGNATURES: dict[str, list] = {
     "axk_paged_decode_plan": [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "axk_paged_decode_split": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                                _vp, ctypes.c_size_t, _vp],
-    "axk_paged_decode_merge": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
+    "axk_paged_decode_merge": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "axk_paged_decode_run": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                              ctypes.c_size_t, _vp],
     "axk_paged_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                          ctypes.c_size_t, _vp],
+    "axk_paged_attention_decode": [_vp] * 9 + [_i64] * 6 + [ctypes.c_float, _vp, _vp, ctypes.c_size_t, _vp],
     "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "axk_paged_decode_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                              ctypes.c_float, _vp, ctypes.c_size_t, _vp],

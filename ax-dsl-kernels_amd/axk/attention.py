@@ -39,7 +39,7 @@ def _check_decode(q, kv_cache, indptr, indices, last_page_len, kv_dtype=torch.bf
     _check(two == 2 and d2 == d, f"kv_cache shape {tuple(kv_cache.shape)} does not match q {tuple(q.shape)}")
     _check(hq % hkv == 0 and hq // hkv <= 16, f"num_qo_heads {hq} must be a multiple (<= 16x) of num_kv_heads {hkv}")
     _check(d in (64, 128, 256), f"head_dim {d} not supported (64, 128, 256)")
-    _check(page % 32 == 0, f"page_size {page} must be a multiple of 32")
+    _check(page % 16 == 0 and page <= 4096, f"page_size {page} must be a multiple of 16, at most 4096")
     for name, t, n in (("indptr", indptr, b + 1), ("last_page_len", last_page_len, b)):
         _check(t.dtype == torch.int32 and t.dim() == 1 and t.numel() == n and t.is_contiguous(),
                f"{name} must be contiguous int32 [{n}]")
@@ -104,6 +104,47 @@ def paged_decode(
         "axk_paged_decode", q.data_ptr(), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
         last_page_len.data_ptr(), output.data_ptr(), b, hq, hkv, d, page, p, float(sm_scale),
         workspace.data_ptr(), workspace.numel(), _lib.stream_of(q),
+    )
+    return output
+
+
+def paged_attention_decode(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    kv_cache: torch.Tensor,
+    indptr: torch.Tensor,
+    indices: torch.Tensor,
+    last_page_len: torch.Tensor,
+    cache_location: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    status: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Decode attention in the sgl operator's page-table convention (flash_attn.py:2335-2357, 1421-1596): writes the
+    current token's k, v ([B, HKV, D] bf16) at cache_location[b] = (page, offset), then q attends the history
+    ((pages - 1) * page_size + last_page_len[b] tokens, last_page_len counting history only, 0 .. page - 1) plus the
+    current token. The page list already holds the current token's page. Returns bf16 [B, HQ, D]."""
+    b, hq, hkv, d, page, p = _check_decode(q, kv_cache, indptr, indices, last_page_len)
+    _check(k.shape == (b, hkv, d) and v.shape == k.shape and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+           and k.is_contiguous() and v.is_contiguous(), f"k and v must be contiguous bf16 [{b}, {hkv}, {d}]")
+    loc = cache_location.reshape(-1, 2) if cache_location.numel() == 2 * b else None
+    _check(loc is not None and cache_location.dtype == torch.int32 and loc.is_contiguous(),
+           "cache_location must be int32 [B, 2] = (page, offset)")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    if workspace is None:
+        workspace = paged_decode_workspace(b, hq, hkv, d, q.device)
+    _lib.require_device(q, k, v, kv_cache, indptr, indices, last_page_len, loc, output, workspace, status)
+    _lib.call(
+        "axk_paged_attention_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(),
+        indptr.data_ptr(), indices.data_ptr(), last_page_len.data_ptr(), loc.data_ptr(), output.data_ptr(), b, hq,
+        hkv, d, page, p, float(sm_scale), _lib.ptr(status), workspace.data_ptr(), workspace.numel(),
+        _lib.stream_of(q),
     )
     return output
 

@@ -1,5 +1,23 @@
 // Library identification and status text for the axk C-ABI.
+#include <pthread.h>
+
 #include "axk_host.h"
+
+namespace {
+pthread_key_t g_validate_key;
+pthread_once_t g_validate_once = PTHREAD_ONCE_INIT;
+void make_validate_key() { pthread_key_create(&g_validate_key, nullptr); }
+}  // namespace
+
+int axk_validate_only() {
+  pthread_once(&g_validate_once, make_validate_key);
+  return (int)(intptr_t)pthread_getspecific(g_validate_key);
+}
+
+void axk_validate_add(int delta) {
+  const int v = axk_validate_only() + delta;
+  pthread_setspecific(g_validate_key, reinterpret_cast<void*>((intptr_t)v));
+}
 
 extern "C" const char* axk_version(void) { return "axk 0.1.0 gfx950"; }
 

@@ -26,6 +26,23 @@ static inline bool axk_overlap(const void* a, size_t na, const void* b, size_t n
 
 static inline hipStream_t axk_stream(axk_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Validate-only mode of the calling thread: while it is set, entry points run every argument check and return
+// AXK_OK just before their first launch. The composed layer entry points run their whole call sequence once this way
+// before running it for real, so a contract error in a late sub-call is returned before an early one has advanced a
+// state, a conv state or the KV cache (a nonzero status means nothing was enqueued). Kept in a POSIX thread key.
+__attribute__((visibility("hidden"))) int axk_validate_only();
+__attribute__((visibility("hidden"))) void axk_validate_add(int delta);
+struct AxkValidateScope {
+  AxkValidateScope() { axk_validate_add(1); }
+  ~AxkValidateScope() { axk_validate_add(-1); }
+  AxkValidateScope(const AxkValidateScope&) = delete;
+  AxkValidateScope& operator=(const AxkValidateScope&) = delete;
+};
+#define AXK_LAUNCH_GATE()                    \
+  do {                                       \
+    if (axk_validate_only()) return AXK_OK; \
+  } while (0)
+
 // Internal (not exported): the GDN recurrence with row strides, in elements between consecutive (sequence, token)
 // rows, for q, k, v and a / b. axk_gdn_recurrent passes the contiguous strides; the decode layer reads q / k / v
 // straight out of the conv output. Returns an AXK status.
@@ -45,14 +62,15 @@ __attribute__((visibility("hidden"))) int axk_gdn_recurrent_strided(
     int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, hipStream_t stream);
 
 // Internal (not exported): one launch of up to AXK_MX_GROUP_MAX weight matrices that share the activations a
-// [m, k] (the projections of one decode layer). Matrix i: weights w [n, k] (FP8 bytes, or MXFP4 codes with E8M0
-// scales ws [n, k/32]), optional per-channel scale and bias, output out [m, n] with leading dimension ldo.
+// [m, k] (the projections of one decode layer). Matrix i: weights w [n, k] (FP8 bytes with a per-channel scale, or
+// MXFP4 codes / MXFP8 E4M3 bytes with E8M0 scales ws [n, k/32]), optional per-channel scale and bias, output
+// out [m, n] with leading dimension ldo.
 // epi: AXK_MX_EPI_PLAIN; AXK_MX_EPI_SWIGLU (mats[0] gate, mats[1] up, one shape and one out:
 // out = bf16(silu(bf16 g) * bf16 u)); AXK_MX_EPI_RES (one matrix: out = bf16(res + bf16 y), res [m, n] with
 // leading dimension ldr). Rows must be whole 128-byte segments. Returns an AXK status.
 #define AXK_MX_GROUP_MAX 4
 enum { AXK_MX_EPI_PLAIN = 0, AXK_MX_EPI_SWIGLU = 1, AXK_MX_EPI_RES = 2 };
-enum { AXK_MX_MXFP4 = 0, AXK_MX_FP8 = 1 };
+enum { AXK_MX_MXFP4 = 0, AXK_MX_FP8 = 1, AXK_MX_MXFP8 = 2 };
 struct AxkMxMat {
   const uint8_t* w;
   const uint8_t* ws;

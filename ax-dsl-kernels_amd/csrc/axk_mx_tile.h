@@ -9,7 +9,10 @@
 
 namespace axk {
 
-enum WeightFmt { WF_MXFP4 = 0, WF_FP8 = 1, WF_BF16 = 2 };
+enum WeightFmt { WF_MXFP4 = 0, WF_FP8 = 1, WF_BF16 = 2, WF_MXFP8 = 3, WF_MXBF8 = 4 };
+
+// Formats whose E8M0 scales (one per 32 values along K, [N, K/32]) are applied inside the unit decode.
+__host__ __device__ constexpr bool is_mx(int F) { return F == WF_MXFP4 || F == WF_MXFP8 || F == WF_MXBF8; }
 
 template <int F>
 struct WUnit;
@@ -52,6 +55,38 @@ struct WUnit<WF_FP8> {
     return r;
   }
 };
+
+// MXFP8: OCP FP8 codes [N, K] bytes, E4M3 (WF_MXFP8) or E5M2 (WF_MXBF8), with E8M0 scales [N, K/32]; a 16-byte unit
+// is half a scale block. gfx950's scaled converts multiply by the block scale on the way to bf16 (exact while the
+// scaled value is a bf16 normal).
+template <int F>
+struct WUnitMx8 {
+  static constexpr int V = 16;
+  static constexpr int STEPS = 2;
+  static AXK_DEV uint4 load(const uint8_t* w, int64_t n, int64_t K, int64_t kb) {
+    return *reinterpret_cast<const uint4*>(w + n * K + kb);
+  }
+  static AXK_DEV float scale(const uint8_t* s, int64_t n, int64_t K, int64_t kb) {
+    return e8m0_to_f32(s[n * (K >> 5) + (kb >> 5)]);
+  }
+  template <bool HI>
+  static AXK_DEV axk_bf16x2 cvt(uint32_t w, float sc) {
+    if constexpr (F == WF_MXBF8) return __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, sc, HI);
+    else return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, sc, HI);
+  }
+  static AXK_DEV axk_bf16x8 conv(const uint4& q, int step, float sc) {
+    const uint32_t w0 = step == 0 ? q.x : q.z, w1 = step == 0 ? q.y : q.w;
+    const axk_bf16x2 p0 = cvt<false>(w0, sc), p1 = cvt<true>(w0, sc), p2 = cvt<false>(w1, sc), p3 = cvt<true>(w1, sc);
+    axk_bf16x8 r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+  }
+};
+template <>
+struct WUnit<WF_MXFP8> : WUnitMx8<WF_MXFP8> {};
+template <>
+struct WUnit<WF_MXBF8> : WUnitMx8<WF_MXBF8> {};
 
 // bf16: [N, K] (uint16 bits).
 template <>
@@ -120,7 +155,7 @@ constexpr int kSegLd = kSegBytes + 16;
 
 template <int F>
 __host__ __device__ constexpr int64_t row_bytes(int64_t K) {
-  return F == WF_MXFP4 ? K / 2 : (F == WF_FP8 ? K : 2 * K);
+  return F == WF_MXFP4 ? K / 2 : (F == WF_BF16 ? 2 * K : K);
 }
 
 }  // namespace axk

@@ -191,6 +191,7 @@ int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16
   GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
             (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab, gate ? gate->norm_w : nullptr, gate ? gate->z : nullptr,
             gate ? gate->eps : 0.f};
+  AXK_LAUNCH_GATE();
   if (gate)
     hipLaunchKernelGGL(gdn_recurrent_kernel<true>, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
   else

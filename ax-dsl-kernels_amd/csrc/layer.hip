@@ -156,21 +156,28 @@ extern "C" int axk_gdn_layer_decode(
   Carver c{static_cast<unsigned char*>(workspace)};
   const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
   const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
-  AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
-  // qkv | z | b | a, the qkv output through the causal conv1d + SiLU (mixed) as it is stored
-  const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.mixed, C), fp8_mat(w_z, s_z, g.z, VD), fp8_mat(w_b, s_b, g.bb, NV),
-                            fp8_mat(w_a, s_a, g.aa, NV)};
-  const AxkConvEpi conv{conv_w, conv_in, conv_out, conv_kernel};
-  AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream, &conv));
-  // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row; each
-  // head's output row leaves through the gated output norm
-  const AxkGdnStrides ld{C, C, C, NV};
-  const AxkGdnGate gate{norm_w, g.z, eps};
-  AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
-                                    state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
-  const AxkMxMat o = fp8_mat(w_out, s_out, g.y, H);
-  AXK_TRY(fp8_projs(g.gated, VD, &o, 1, B, VD, stream));
-  return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
+  auto body = [&]() -> int {
+    AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
+    // qkv | z | b | a, the qkv output through the causal conv1d + SiLU (mixed) as it is stored
+    const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.mixed, C), fp8_mat(w_z, s_z, g.z, VD),
+                              fp8_mat(w_b, s_b, g.bb, NV), fp8_mat(w_a, s_a, g.aa, NV)};
+    const AxkConvEpi conv{conv_w, conv_in, conv_out, conv_kernel};
+    AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream, &conv));
+    // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row; each
+    // head's output row leaves through the gated output norm
+    const AxkGdnStrides ld{C, C, C, NV};
+    const AxkGdnGate gate{norm_w, g.z, eps};
+    AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
+                                      state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
+    const AxkMxMat o = fp8_mat(w_out, s_out, g.y, H);
+    AXK_TRY(fp8_projs(g.gated, VD, &o, 1, B, VD, stream));
+    return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
+  };
+  {
+    const AxkValidateScope check_only;  // every sub-call's checks before the first launch
+    AXK_TRY(body());
+  }
+  return body();
 }
 
 extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
@@ -204,16 +211,23 @@ extern "C" int axk_attn_layer_decode(
   Carver c{static_cast<unsigned char*>(workspace)};
   const AttnBufs a = carve_attn(c, B, H, HQ, HKV, D, F);
   const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
-  AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
-  const AxkMxMat proj[3] = {fp8_mat(w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
-                            fp8_mat(w_k, s_k, a.kk, HKV * D), fp8_mat(w_v, s_v, a.vv, HKV * D)};
-  AXK_TRY(fp8_projs(a.h, H, proj, 3, B, H, stream));
-  AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, B, HQ, HKV, D,
-                            rot, page_size, num_pages, eps, axk_stream(stream)));
-  AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
-                           num_pages, sm_scale, a.pws, a.pws_bytes, stream));
-  AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
-  const AxkMxMat o = fp8_mat(w_o, s_o, a.y, H);
-  AXK_TRY(fp8_projs(a.gated, HQ * D, &o, 1, B, HQ * D, stream));
-  return mlp_residual(x, a.y, ln2, mw, out, a.mlp, B, H, F, eps, stream);
+  auto body = [&]() -> int {
+    AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
+    const AxkMxMat proj[3] = {fp8_mat(w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
+                              fp8_mat(w_k, s_k, a.kk, HKV * D), fp8_mat(w_v, s_v, a.vv, HKV * D)};
+    AXK_TRY(fp8_projs(a.h, H, proj, 3, B, H, stream));
+    AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, B, HQ, HKV,
+                              D, rot, page_size, num_pages, eps, axk_stream(stream)));
+    AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
+                             num_pages, sm_scale, a.pws, a.pws_bytes, stream));
+    AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
+    const AxkMxMat o = fp8_mat(w_o, s_o, a.y, H);
+    AXK_TRY(fp8_projs(a.gated, HQ * D, &o, 1, B, HQ * D, stream));
+    return mlp_residual(x, a.y, ln2, mw, out, a.mlp, B, H, F, eps, stream);
+  };
+  {
+    const AxkValidateScope check_only;  // every sub-call's checks before the first launch
+    AXK_TRY(body());
+  }
+  return body();
 }

@@ -311,6 +311,7 @@ extern "C" int axk_rmsnorm(const uint16_t* x, int64_t ldx, const float* w, uint1
   AXK_REQUIRE(x && w && out, AXK_E_NULL);
   AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX && ldx >= n && ldo >= n, AXK_E_SHAPE);
   AXK_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(out), AXK_E_ALIGN);
+  AXK_LAUNCH_GATE();
   launch_rmsnorm<0>(x, ldx, nullptr, w, nullptr, nullptr, out, ldo, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
@@ -324,6 +325,7 @@ extern "C" int axk_add_rmsnorm(const uint16_t* x, const uint16_t* y, const float
   AXK_REQUIRE(!axk_overlap(norm_out, bytes, sum_out, bytes) && !axk_overlap(norm_out, bytes, x, bytes) &&
                   !axk_overlap(norm_out, bytes, y, bytes),
               AXK_E_ALIAS);
+  AXK_LAUNCH_GATE();
   launch_rmsnorm<1>(x, n, y, w, nullptr, sum_out, norm_out, n, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
@@ -333,6 +335,7 @@ extern "C" int axk_gated_rmsnorm_silu(const uint16_t* x, const float* w, const u
   AXK_REQUIRE(x && w && z && out, AXK_E_NULL);
   AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && n <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(aligned16(x) && aligned16(w) && aligned16(z) && aligned16(out), AXK_E_ALIGN);
+  AXK_LAUNCH_GATE();
   launch_rmsnorm<2>(x, n, nullptr, w, z, nullptr, out, n, rows, (int)n, eps, axk_stream(stream));
   return axk_launch_status();
 }
@@ -383,6 +386,7 @@ int launch_eltwise(const uint16_t* x, const uint16_t* g, int64_t ldg, uint16_t* 
   AXK_REQUIRE(x && g && out, AXK_E_NULL);
   AXK_REQUIRE(rows > 0 && n > 0 && n % 8 == 0 && ldg >= n && n <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(ldg % 8 == 0 && aligned16(x) && aligned16(g) && aligned16(out), AXK_E_ALIGN);
+  AXK_LAUNCH_GATE();
   hipLaunchKernelGGL(eltwise_kernel<OP>, dim3(elt_grid(rows * (n / 8))), dim3(256), 0, axk_stream(stream), x, g, ldg,
                      out, rows, (int)n);
   return axk_launch_status();
@@ -417,6 +421,7 @@ int axk_attn_qkv_prep(const uint16_t* qg, const uint16_t* kk, const uint16_t* vv
   AXK_REQUIRE(rot >= 0 && rot <= head_dim && rot % 2 == 0 && (rot / 2) % epl == 0, AXK_E_SHAPE);
   const int64_t rows = batch * (hq + 2 * hkv);
   AXK_REQUIRE(rows <= INT32_MAX, AXK_E_SHAPE);
+  AXK_LAUNCH_GATE();
 #define AXK_PREP(E)                                                                                             \
   hipLaunchKernelGGL(attn_prep_kernel<E>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, stream, qg, kk, vv,  \
                      q_norm, k_norm, cos, sin, q_out, kv_cache, cache_location, (int)batch, (int)hq, (int)hkv, \

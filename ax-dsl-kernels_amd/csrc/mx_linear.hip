@@ -181,7 +181,7 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
       const int64_t r = n0 + 8 * h + lr;
       src[t][h] = g.w[mi] + (r < nmax ? r : nmax) * rb + 16 * lc;
     }
-    srow[t] = F == axk::WF_MXFP4 ? g.ws[mi] + (n0 + nl < nmax ? n0 + nl : nmax) * (K / 32) : nullptr;
+    srow[t] = axk::is_mx(F) ? g.ws[mi] + (n0 + nl < nmax ? n0 + nl : nmax) * (K / 32) : nullptr;
   }
 
   axk_f32x4 acc[NT][MT];
@@ -192,13 +192,14 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
 
   for (int64_t d = wave; d < ND; d += nwaves) {
     axk_u32x4 q[NT][2];
-    uint2 sw[NT];
+    uint2 sw[NT];  // the segment's E8M0 scales: 8 bytes (MXFP4: 256 values) or 4 (MXFP8: 128 values)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)  // weights are read once: non-temporal
         q[t][h] = __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(src[t][h] + d * axk::kSegBytes));
       if (F == axk::WF_MXFP4) sw[t] = *reinterpret_cast<const uint2*>(srow[t] + 8 * d);
+      if (F == axk::WF_MXFP8 || F == axk::WF_MXBF8) sw[t].x = *reinterpret_cast<const uint32_t*>(srow[t] + 4 * d);
     }
     axk_bf16x8 a[MT][2][U::STEPS];
 #pragma unroll
@@ -219,8 +220,10 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
       for (int j = 0; j < 2; ++j) {
         const uint4 unit = __builtin_bit_cast(
             uint4, *reinterpret_cast<const axk_u32x4*>(tile + (t * 16 + nl) * axk::kSegLd + 64 * j + 16 * kg));
-        const float sc =
-            F == axk::WF_MXFP4 ? e8m0_to_f32(((j ? sw[t].y : sw[t].x) >> (8 * kg)) & 0xffu) : 1.0f;
+        // unit (j, kg) of the segment: values 64 j + V kg .. + V, in scale block (64 j + V kg) / 32
+        const float sc = F == axk::WF_MXFP4 ? e8m0_to_f32(((j ? sw[t].y : sw[t].x) >> (8 * kg)) & 0xffu)
+                         : axk::is_mx(F)    ? e8m0_to_f32((sw[t].x >> (8 * (2 * j + (kg >> 1)))) & 0xffu)
+                                            : 1.0f;
 #pragma unroll
         for (int s = 0; s < U::STEPS; ++s) {
           const axk_bf16x8 b = U::conv(unit, s, sc);
@@ -411,9 +414,10 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) {
     const AxkMxMat& p = mats[i];
-    AXK_REQUIRE(p.w && p.out && (F != axk::WF_MXFP4 || p.ws), AXK_E_NULL);
+    AXK_REQUIRE(p.w && p.out && (!axk::is_mx(F) || p.ws), AXK_E_NULL);
     AXK_REQUIRE(p.n > 0 && p.n <= INT32_MAX && p.ldo >= p.n, AXK_E_SHAPE);
-    AXK_REQUIRE(axk_aligned(p.w, 16) && (F != axk::WF_MXFP4 || axk_aligned(p.ws, 8)), AXK_E_ALIGN);
+    AXK_REQUIRE(axk_aligned(p.w, 16) && (!axk::is_mx(F) || axk_aligned(p.ws, F == axk::WF_MXFP4 ? 8 : 4)),
+                AXK_E_ALIGN);
     const size_t o_bytes = m > 0 ? (size_t)((m - 1) * p.ldo + p.n) * esz : 0;
     AXK_REQUIRE(!axk_overlap(p.out, o_bytes, a, a_bytes), AXK_E_ALIAS);
     if (epi == EPI_RES) {  // in place (out == res, one leading dimension) or disjoint
@@ -434,6 +438,7 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   AXK_REQUIRE(tiles <= INT32_MAX / 16, AXK_E_SHAPE);
   for (int i = count; i <= AXK_MX_GROUP_MAX; ++i) g.tile0[i] = (int)tiles;
   if (m == 0) return AXK_OK;
+  AXK_LAUNCH_GATE();
   if (epi == EPI_SWIGLU) return group_dispatch<F, EPI_SWIGLU>(a, lda, g, m, k, st);
   if (epi == EPI_RES) return group_dispatch<F, EPI_RES>(a, lda, g, m, k, st);
   return group_dispatch<F, EPI_PLAIN>(a, lda, g, m, k, st);
@@ -444,7 +449,7 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
                   const float* col_scale, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
                   int64_t k, axk_stream_t stream) {
   AXK_REQUIRE(a && w && out, AXK_E_NULL);
-  AXK_REQUIRE(F != WF_MXFP4 || ws, AXK_E_NULL);
+  AXK_REQUIRE(!axk::is_mx(F) || ws, AXK_E_NULL);
   AXK_REQUIRE(m >= 0 && n >= 0 && k > 0 && k % 32 == 0, AXK_E_SHAPE);
   AXK_REQUIRE(m <= INT32_MAX && n <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(lda >= k && lda % 8 == 0, AXK_E_ALIGN);
@@ -456,8 +461,9 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   AXK_REQUIRE(!axk_overlap(out, out_bytes, a, a_bytes), AXK_E_ALIAS);
 
   hipStream_t st = axk_stream(stream);
-  // staged group kernel when rows are whole 128-byte segments (and MXFP4 scale rows 8-byte aligned)
-  if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 && (F != WF_MXFP4 || axk_aligned(ws, 8))) {
+  // staged group kernel when rows are whole 128-byte segments (and scale rows 8-byte (MXFP4) / 4-byte (MXFP8)
+  // aligned)
+  if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 && (!axk::is_mx(F) || axk_aligned(ws, F == WF_MXFP4 ? 8 : 4))) {
     const AxkMxMat mat{w, ws, col_scale, bias, out, n, n};
     return mx_group<F>(a, lda, &mat, 1, EPI_PLAIN, nullptr, 0, row_scale, out_dtype, m, k, nullptr, st);
   }
@@ -486,6 +492,8 @@ int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, 
     return mx_group<WF_FP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   if (fmt == AXK_MX_MXFP4)
     return mx_group<WF_MXFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
+  if (fmt == AXK_MX_MXFP8)
+    return mx_group<axk::WF_MXFP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   return AXK_E_DTYPE;
 }
 
@@ -515,6 +523,18 @@ extern "C" int axk_fp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8
                             int64_t k, axk_stream_t stream) {
   AXK_REQUIRE(scale_b, AXK_E_NULL);
   return launch_linear<WF_FP8>(a, lda, b_fp8, nullptr, scale_a, scale_b, bias, out, out_dtype, m, n, k, stream);
+}
+
+extern "C" int axk_mxfp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const uint8_t* b_scale,
+                              int fp8_dtype, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
+                              int64_t k, axk_stream_t stream) {
+  if (fp8_dtype == AXK_DT_FP8E4M3)
+    return launch_linear<axk::WF_MXFP8>(a, lda, b_fp8, b_scale, nullptr, nullptr, bias, out, out_dtype, m, n, k,
+                                        stream);
+  if (fp8_dtype == AXK_DT_FP8E5M2)
+    return launch_linear<axk::WF_MXBF8>(a, lda, b_fp8, b_scale, nullptr, nullptr, bias, out, out_dtype, m, n, k,
+                                        stream);
+  return AXK_E_DTYPE;
 }
 
 extern "C" int axk_bf16_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, const float* bias, void* out,

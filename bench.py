@@ -28,7 +28,40 @@ METRIC = "µs/decode-layer + achieved HBM GB/s (% of 8 TB/s) for MXFP4 MoE + pag
 
 
 def _cpu_threads() -> int:
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads the CPU baseline uses: the CPUs this process may run on, at most 16 (the GPU box's CPU share)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
+
+
+def cpu_machine() -> dict:
+    """The host the CPU baseline ran on: CPU model, logical CPUs, physical cores and the CPUs this process may use."""
+    model, phys = None, set()
+    cur = {}
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for ln in f:
+                if ":" not in ln:
+                    if "core id" in cur:
+                        phys.add((cur.get("physical id", "0"), cur["core id"]))
+                    cur = {}
+                    continue
+                k, v = (x.strip() for x in ln.split(":", 1))
+                cur[k] = v
+                if k == "model name" and model is None:
+                    model = v
+        if "core id" in cur:
+            phys.add((cur.get("physical id", "0"), cur["core id"]))
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "physical_cores": len(phys) or None,
+            "cpus_available": affinity}
 
 
 def _time_cpu(fn, budget_s: float = 10.0, min_reps: int = 3, max_reps: int = 50) -> tuple[float, int]:
@@ -163,9 +196,8 @@ class PagedDecodeWorkload(Workload):
     """
 
     name = "paged_decode"
-    kernel = "paged_decode_kernel<256, 2>"  # launched by axk_paged_decode_split
+    kernel = "paged_decode_sk_kernel<256>"  # launched by axk_paged_decode_split
     timing = "graph"       # value: K steps (plan + split + merge) replayed as one HIP graph
-    kernel_events = True   # roofline: the split kernel timed alone with HIP events
     traffic_profile = "paged_decode_config1_pmc.txt"
 
     def __init__(self, dev):
@@ -201,8 +233,9 @@ class PagedDecodeWorkload(Workload):
             self.last.data_ptr(), self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2], c["cache"].shape[0],
             c["scale"], self.ws.data_ptr(), self.ws.numel(), torch.cuda.current_stream().cuda_stream)
         self._merge = lambda: lib.axk_paged_decode_merge(self.indptr.data_ptr(), self.last.data_ptr(),
-                                                         self.out.data_ptr(), b, hq, hkv, d, self.ws.data_ptr(),
-                                                         self.ws.numel(), torch.cuda.current_stream().cuda_stream)
+                                                         self.out.data_ptr(), b, hq, hkv, d, c["cache"].shape[2],
+                                                         self.ws.data_ptr(), self.ws.numel(),
+                                                         torch.cuda.current_stream().cuda_stream)
         self.config = {"workload": "config1: paged decode B=16 HQ=16 HKV=2 D=256 page=64 L~U[1024,16384]",
                        "sum_context": tot, "rotating_copies": self.copies}
         self.dtype = "bf16 (fp32 softmax / accumulation)"
@@ -220,6 +253,10 @@ class PagedDecodeWorkload(Workload):
         self.pre(i)
         self.main(i)
         self.post(i)
+
+    def roofline_step(self, i: int) -> None:
+        """The split kernel alone (the plan and the merge are other launches)."""
+        self.main(i)
 
     def cpu_baseline(self) -> dict:
         import torch
@@ -830,6 +867,38 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 
+WARM_GPU_MS = 200.0  # untimed graph replays before the timed one: the clocks settle after the first launches
+
+
+def _graph_ms(fn, steps: int) -> float:
+    """ms per call of fn over exactly `steps` calls captured as one HIP graph; the graph is replayed untimed (upload,
+    clocks) for about WARM_GPU_MS first, then one replay is timed with HIP events on the graph's own stream."""
+    import torch
+
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                fn(i)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    spent = 0.0
+    for _ in range(50):
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        spent += (time.perf_counter() - t0) * 1e3
+        if spent >= WARM_GPU_MS:
+            break
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        graph.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def measure(wl, steps: int, warmup: int, eager: bool = False) -> tuple[float, float]:
     """(ms per step, ms per launch of the workload's roofline kernel) over exactly `steps` timed steps.
     eager: launch every step on the stream even where the workload is normally timed as one HIP graph."""
@@ -841,26 +910,13 @@ def measure(wl, steps: int, warmup: int, eager: bool = False) -> tuple[float, fl
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     if wl.timing == "graph" and not eager:
-        # Capture exactly K steps in one HIP graph (removes host launch overhead from the measurement).
-        graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream()
-        with torch.cuda.stream(stream):
-            with torch.cuda.graph(graph, stream=stream):
-                for i in range(steps):
-                    wl.step(i)
-        graph.replay()  # untimed replay: graph upload / first-run costs
-        torch.cuda.synchronize()
-        start.record(stream)
-        with torch.cuda.stream(stream):
-            graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms_per_step = start.elapsed_time(end) / steps
-        if not getattr(wl, "kernel_events", False):
+        # exactly K steps in one HIP graph (no host launch overhead in the measurement)
+        ms_per_step = _graph_ms(wl.step, steps)
+        roof = getattr(wl, "roofline_step", None)
+        if roof is None:
             return ms_per_step, ms_per_step
-        # the roofline kernel on its own: eager steps, HIP events around each launch of it on the current stream
-        _, kernel_ms = measure(wl, steps, 0, eager=True)
-        return ms_per_step, kernel_ms
+        # the roofline kernel on its own: K launches of it (over the same rotating inputs) as one HIP graph
+        return ms_per_step, _graph_ms(roof, steps)
     # Eager steps on the current stream; HIP events bracket every launch of the dominant kernel.
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
@@ -973,6 +1029,7 @@ def main() -> int:
     if not args.no_cpu:
         cpu = wl.cpu_baseline()
         if cpu is not None:
+            cpu.update(cpu_machine())
             line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0

@@ -125,8 +125,8 @@ int axk_paged_decode_split(const uint16_t* q, const uint16_t* kv_cache, const in
 /* Second half (one launch): log-sum-exp merge of the split partials, as the split-KV merge of
  * models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:330-349; zero output for empty sequences. */
 int axk_paged_decode_merge(const int32_t* indptr, const int32_t* last_page_len, uint16_t* out, int64_t batch,
-                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, void* workspace,
-                           size_t workspace_bytes, axk_stream_t stream);
+                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                           void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 /* The decode attention itself, using the plan held in `workspace` (same batch / heads / indptr):
  * axk_paged_decode_split then axk_paged_decode_merge. Arguments as axk_paged_decode. */
@@ -151,13 +151,29 @@ int axk_paged_decode_run(const uint16_t* q, const uint16_t* kv_cache, const int3
  * The query attends every valid cached token of its sequence (write the current token with
  * axk_paged_kv_write first: the reference's "history + current token" merge is the same sum).
  * A sequence with no pages yields zeros. head_dim in {64, 128, 256}; num_qo_heads / num_kv_heads
- * <= 16; page_size a multiple of 32. Page ids outside [0, num_pages) are skipped, never read.
+ * <= 16; page_size a multiple of 16, at most 4096. Page ids outside [0, num_pages) are skipped, never read.
  * workspace >= axk_paged_decode_workspace_size(...), 256-byte aligned. */
 int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
                      const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
                      int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                      int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
                      axk_stream_t stream);
+
+/* The sgl decode operator's page-table convention (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/
+ * flash_attn.py:2335-2357 and 1421-1596; its test models/qwen35_35b_a3b/sgl/tests/test_qwen35_runtime.py:96-118):
+ * last_page_len counts the HISTORY tokens on each sequence's last page (0 .. page_size - 1, so the cached length is
+ * (pages - 1) * page_size + last_page_len and may be 0), the page list already holds the page the current token goes
+ * to, and cache_location[b] = (page, offset) is that token's slot (offset == last_page_len[b]). The current token's
+ * k, v bf16 [batch, num_kv_heads, head_dim] are written there first (as axk_paged_kv_write; a location outside the
+ * pool is skipped and sets *status), then q attends the history plus the current token, the same sum as the
+ * reference's history loop merged with the current token's score. Every sequence holds at least one page. Other
+ * arguments and the workspace as axk_paged_decode. */
+int axk_paged_attention_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kv_cache,
+                               const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                               const int32_t* cache_location, uint16_t* out, int64_t batch, int64_t num_qo_heads,
+                               int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                               float sm_scale, int32_t* status, void* workspace, size_t workspace_bytes,
+                               axk_stream_t stream);
 
 /* Scatter the current token's K and V rows into the paged cache in place:
  *   kv_cache[loc[b,0], 0, loc[b,1], :, :] = k[b]; kv_cache[loc[b,0], 1, loc[b,1], :, :] = v[b].

@@ -5,6 +5,7 @@ import os
 import re
 
 import pytest
+import torch
 
 import axk
 from axk import _lib
@@ -72,7 +73,35 @@ def test_python_layer_raises_value_error_on_contract():
 def test_moe_workspace_size_limits():
     lib = _lib.load()
     assert lib.axk_moe_workspace_size(256, 64, 8, 2, 32, 32) > 0
-    assert lib.axk_moe_workspace_size(257, 64, 8, 2, 32, 32) == 0  # tokens per call <= 256
+    # above 256 tokens the prefill path needs inter and shared_inter % 64 == 0 (32 passes only the decode path)
+    assert lib.axk_moe_workspace_size(257, 64, 8, 2, 32, 32) == 0
+    assert lib.axk_moe_workspace_size(257, 64, 8, 2, 64, 64) > 0
     assert lib.axk_moe_workspace_size(4, 64, 1025, 2, 32, 32) == 0  # experts <= 1024
     assert lib.axk_moe_workspace_size(4, 64, 8, 33, 32, 32) == 0   # top_k <= 32
     assert lib.axk_moe_workspace_size(4, 96, 8, 2, 32, 32) == 0     # hidden % 64
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="drives entry points with host pointers: only on a GPU-less host")
+def test_entry_points_reach_the_launch_on_a_gpu_less_host():
+    """Every host-side step of an entry point (argument checks, the layers' validate-only pass, workspace carving)
+    runs on a host without a GPU and ends at the launch with AXK_E_LAUNCH, never a crash."""
+    import ctypes
+
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(1 << 24)
+    base = (ctypes.addressof(buf) + 4095) // 4096 * 4096
+    p = [base + 65536 * i for i in range(200)]
+    launch = 7  # AXK_E_LAUNCH
+    assert lib.axk_rmsnorm(p[0], 64, p[1], p[2], 64, 1, 64, 1e-6, None) == launch
+    ws = lib.axk_paged_decode_workspace_size(2, 8, 2, 128)
+    assert lib.axk_paged_decode(p[0], p[1], p[2], p[3], p[4], p[5], 2, 8, 2, 128, 32, 4, 0.1, p[100], ws,
+                                None) == launch
+    assert lib.axk_paged_attention_decode(p[0], p[6], p[7], p[1], p[2], p[3], p[4], p[8], p[5], 2, 8, 2, 128, 32, 4,
+                                          0.1, None, p[100], ws, None) == launch
+    gws = lib.axk_gdn_layer_workspace_size(1, 256, 1, 2, 128, 256)
+    args = [p[10 + i] for i in range(28)]
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, p[150], gws, None) == launch
+    # a late contract error (misaligned w_out, argument 15) is found by the validate pass before any launch
+    bad = list(args)
+    bad[14] += 1
+    assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, p[150], gws, None) == 3

@@ -111,3 +111,36 @@ def test_layer_contract_errors(dev):
         bad = dict(wd)
         bad.pop("norm_w")
         layer.gdn_layer_decode(x.to(dev), bad, st.to(dev), cv.to(dev), 2, 4)
+
+
+def test_layer_late_contract_error_enqueues_nothing(dev):
+    """A contract error in a late sub-call (the GDN out projection's weight misaligned; a page size the paged decode
+    rejects) returns its status before anything is launched: the recurrent state, the conv state and the KV cache
+    are unchanged, so a caller's retry cannot advance them twice."""
+    from axk import _lib
+
+    w, x, st, cv = _gdn_case(21)
+    wd = _dev(w, dev)
+    raw = torch.zeros(wd["w_out"].numel() + 16, dtype=torch.uint8, device=dev)
+    raw[1:1 + wd["w_out"].numel()] = wd["w_out"].reshape(-1)
+    wd["w_out"] = raw[1:1 + wd["w_out"].numel()].view(wd["w_out"].shape)  # one byte off a 16-byte boundary
+    sd, cd = st.to(dev), cv.to(dev)
+    with pytest.raises(_lib.AxkError) as e:
+        layer.gdn_layer_decode(x.to(dev), wd, sd, cd, 2, 4, state_out=sd, conv_out=cd)
+    assert e.value.status == 3  # AXK_E_ALIGN
+    torch.cuda.synchronize()
+    assert torch.equal(sd.cpu(), st) and torch.equal(cd.cpu(), cv)
+
+    g = torch.Generator().manual_seed(22)
+    hq, hkv, d, page = 4, 2, 256, 24  # 24-token pages: the q / k / v preparation accepts them, the decode does not
+    wa = configs.attn_layer_weights(g, H, F, hq, hkv, d)
+    c = configs.append_token_case([30, 50], hq, hkv, d, page, g)
+    xa = torch.randn(2, H, generator=g).bfloat16()
+    cos, sin = olayer.rope_cos_sin(c["pos"], 64, 10_000_000.0)
+    cache = c["cache"].to(dev)
+    with pytest.raises(_lib.AxkError) as e:
+        layer.attn_layer_decode(xa.to(dev), _dev(wa, dev), cos.to(dev), sin.to(dev), cache, c["indptr"].to(dev),
+                                c["indices"].to(dev), c["last_page_len"].to(dev), c["loc"].to(dev), hq, 64)
+    assert e.value.status == 2  # AXK_E_SHAPE
+    torch.cuda.synchronize()
+    assert torch.equal(cache.cpu().view(torch.int16), c["cache"].view(torch.int16))

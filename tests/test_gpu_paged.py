@@ -209,3 +209,91 @@ def test_kv_write_fp8_bytes(dev):
         ref[p, 0, o] = pa.quant_kv_fp8(k[i], KV_SCALE)
         ref[p, 1, o] = pa.quant_kv_fp8(v[i], KV_SCALE)
     assert torch.equal(got.cpu(), ref)
+
+
+# ---- the stream-K partition's edge cases (batch <= 63): many segments per workgroup, fewer tiles than workgroups,
+# tails that are not whole tiles, page-id chunks of 256 pages crossed inside a sequence, odd KV-head counts ----
+@pytest.mark.parametrize(
+    "lens,hq,hkv,d,page",
+    [
+        ([1, 2, 3, 5, 8, 13, 21, 34, 55], 8, 2, 128, 16),   # fewer tiles than workgroups, every tail partial
+        ([17] * 63, 4, 1, 64, 16),                            # 63 sequences, units < workgroups
+        ([5000, 4097, 16], 12, 3, 128, 16),                  # 313 pages of 16 tokens: two chunk crossings
+        ([9000, 1, 0, 700], 16, 1, 256, 32),                 # empty sequence between others
+        ([16 * i + 1 for i in range(40)], 32, 16, 64, 16),   # 16 KV heads, many short pairs per workgroup
+        ([100000], 16, 2, 256, 64),                          # one long sequence over every workgroup
+    ],
+)
+def test_paged_decode_stream_k_partition(dev, lens, hq, hkv, d, page):
+    g = torch.Generator().manual_seed(len(lens) * 7 + hkv)
+    c = configs.paged_case(lens, hq, hkv, d, page, g, extra_pages=1)
+    print(f"case lens={lens[:6]}.. hq={hq} hkv={hkv} d={d} page={page}", flush=True)
+    got = _run(c, dev)
+    torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not got[b].any()
+
+
+# ---- the sgl decode convention (flash_attn.py:2335-2357): last_page_len counts history only, may be 0 ----
+def _sgl_reference_case(history, g, hq=8, hkv=2, d=256, page=256):
+    """The metadata of the reference's own runtime test (test_qwen35_runtime.py:96-118): a 32-page pool of 256-token
+    pages, page list [7, 2, 11], page_count = history // 256 + 1, last_page_len = history % 256 and the current token
+    at cache_location = [rows[-1], history % 256]."""
+    cache = (torch.randn(32, 2, page, hkv, d, generator=g) * 0.05).bfloat16()
+    indices = torch.tensor([7, 2, 11] + [0] * 29, dtype=torch.int32)
+    page_count = history // page + 1
+    rows = indices[:page_count].long()
+    q = torch.randn(1, hq, d, generator=g).bfloat16()
+    k = torch.randn(1, hkv, d, generator=g).bfloat16()
+    v = torch.randn(1, hkv, d, generator=g).bfloat16()
+    return dict(cache=cache, indices=indices, rows=rows, q=q, k=k, v=v,
+                indptr=torch.tensor([0, page_count], dtype=torch.int32),
+                last=torch.tensor([history % page], dtype=torch.int32),
+                loc=torch.tensor([[int(rows[-1]), history % page]], dtype=torch.int32))
+
+
+@pytest.mark.parametrize("history", [0, 1, 255, 256, 514])
+def test_paged_attention_decode_sgl_convention(dev, history):
+    g = torch.Generator().manual_seed(history)
+    c = _sgl_reference_case(history, g)
+    hkv, d = c["k"].shape[1], c["k"].shape[2]
+    print(f"sgl history={history}", flush=True)
+    cache = c["cache"].to(dev)
+    got = attention.paged_attention_decode(c["q"].to(dev), c["k"].to(dev), c["v"].to(dev), cache,
+                                           c["indptr"].to(dev), c["indices"].to(dev), c["last"].to(dev),
+                                           c["loc"].to(dev)).cpu()
+    # the reference's golden: SDPA over the gathered history plus the current token (test_qwen35_runtime.py:73-84)
+    hk = c["cache"][c["rows"], 0].reshape(-1, hkv, d)[:history]
+    hv = c["cache"][c["rows"], 1].reshape(-1, hkv, d)[:history]
+    kk = torch.cat((hk, c["k"]), 0).float().transpose(0, 1)[None]
+    vv = torch.cat((hv, c["v"]), 0).float().transpose(0, 1)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(c["q"].float()[:, :, None, :], kk, vv, enable_gqa=True)
+    torch.testing.assert_close(got.float(), ref[:, :, 0, :].bfloat16().float(), **TOL)
+    # the current token's rows written, every other cache byte untouched
+    want = c["cache"].clone()
+    want[c["rows"][-1], 0, history % 256] = c["k"][0]
+    want[c["rows"][-1], 1, history % 256] = c["v"][0]
+    assert torch.equal(cache.cpu().view(torch.int16), want.view(torch.int16))
+
+
+def test_paged_attention_decode_sgl_convention_matches_paged_decode(dev):
+    """History-only last_page_len (+ the written current token) == axk_paged_decode with last_page_len + 1, for a
+    batch that takes the stream-K split (16) and one that takes the plan kernel's items (70)."""
+    for bsz in (16, 70):
+        g = torch.Generator().manual_seed(bsz)
+        hist = [int(x) for x in torch.randint(0, 3000, (bsz,), generator=g)]
+        hist[0] = 0
+        hist[1] = 64
+        c = configs.append_token_case(hist, 8, 2, 128, 64, g)
+        k = torch.randn(bsz, 2, 128, generator=g).bfloat16()
+        v = torch.randn(bsz, 2, 128, generator=g).bfloat16()
+        hist_last = (c["last_page_len"] - 1).to(torch.int32)
+        print(f"sgl batch={bsz}", flush=True)
+        cache = c["cache"].to(dev)
+        got = attention.paged_attention_decode(c["q"].to(dev), k.to(dev), v.to(dev), cache, c["indptr"].to(dev),
+                                               c["indices"].to(dev), hist_last.to(dev), c["loc"].to(dev)).cpu()
+        ref_cache = pa.store_paged_kv(c["cache"], k, v, c["loc"].numpy())
+        ref = pa.paged_decode(c["q"], ref_cache, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+        torch.testing.assert_close(got.float(), ref.to(torch.bfloat16).float(), **TOL)
+        assert torch.equal(cache.cpu().view(torch.int16), ref_cache.view(torch.int16))

@@ -39,6 +39,9 @@ def _ref(c):
         ([64, 65, 1], [64, 700, 5], 4, 4, 64, 16),             # group 1
         ([100], [150], 24, 2, 128, 128),                       # group 12: rows straddle tokens
         ([9, 6], [9, 3], 8, 1, 64, 32),                        # a query longer than the cache: early rows see nothing
+        ([64], [5000], 8, 2, 128, 16),                         # 313 pages: the page ids reload past 64 pages
+        ([40, 7], [90, 700], 12, 3, 128, 32),                  # 3 KV heads: no whole number of XCDs per head
+        ([33], [333], 32, 16, 64, 16),                         # 16 KV heads: the per-head XCD mapping is off
     ],
 )
 def test_paged_prefill_matches_oracle(dev, qlens, kv_lens, hq, hkv, d, page):
