@@ -27,6 +27,7 @@ STATUS_NAMES = {
     7: "AXK_E_LAUNCH",
     8: "AXK_E_ROLE",
     9: "AXK_E_BUFFER",
+    10: "AXK_E_SCRATCH",
 }
 DT_U8, DT_F32, DT_I32, DT_BF16, DT_F16, DT_FP8E4M3, DT_FP8E5M2, DT_FP4 = 1, 3, 6, 9, 10, 11, 12, 15
 
@@ -69,6 +70,7 @@ SIGNATURES: dict[str, list] = {
     "axk_paged_decode": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp,
                          ctypes.c_size_t, _vp],
     "axk_paged_attention_decode": [_vp] * 9 + [_i64] * 6 + [ctypes.c_float, _vp, _vp, ctypes.c_size_t, _vp],
+    "axk_paged_decode_noalloc": [_vp] * 6 + [_i64] * 6 + [ctypes.c_float, _vp],
     "axk_paged_kv_write": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "axk_paged_decode_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                              ctypes.c_float, _vp, ctypes.c_size_t, _vp],

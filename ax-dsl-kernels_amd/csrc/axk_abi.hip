@@ -33,6 +33,7 @@ extern "C" const char* axk_status_string(int status) {
     case AXK_E_LAUNCH: return "HIP launch failed";
     case AXK_E_ROLE: return "unknown role";
     case AXK_E_BUFFER: return "host output buffer too small";
+    case AXK_E_SCRATCH: return "request exceeds the library's static scratch";
     default: return "unknown status";
   }
 }

@@ -23,6 +23,8 @@
 //              output for sequences without pages. A separate launch on purpose: merging inside the
 //              decode kernel needs a device-scope release/acquire per workgroup, which on a multi-XCD
 //              part writes back and invalidates the whole L2 and serialises the kernel.
+#include <mutex>
+
 #include "axk_common.h"
 #include "axk_host.h"
 
@@ -1809,6 +1811,44 @@ extern "C" int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, con
                                 axk_stream_t stream) {
   return decode_all(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim,
                     page_size, num_pages, sm_scale, 0, workspace, workspace_bytes, axk_stream(stream));
+}
+
+// ---- No-allocation variant: the workspace is a static device array of the library ----
+namespace {
+// The split partials of axk_paged_decode_noalloc. Host code never uses this name as an address: each device's copy
+// is resolved once with hipGetSymbolAddress (scratch_ptr) and only that pointer is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[AXK_PAGED_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {nullptr};
+
+// This device's copy of `scratch` (the current device), or nullptr if its address cannot be resolved.
+void* scratch_ptr() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
+}
+}  // namespace
+
+extern "C" int axk_paged_decode_noalloc(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                                        const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
+                                        int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                        int64_t page_size, int64_t num_pages, float sm_scale, axk_stream_t stream) {
+  const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
+  if (rc != AXK_OK) return rc;
+  const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
+  AXK_REQUIRE(need <= AXK_PAGED_NOALLOC_SCRATCH_BYTES, AXK_E_SCRATCH);
+  void* ws = scratch_ptr();
+  AXK_REQUIRE(ws, AXK_E_LAUNCH);
+  return decode_all(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim,
+                    page_size, num_pages, sm_scale, 0, ws, AXK_PAGED_NOALLOC_SCRATCH_BYTES, axk_stream(stream));
 }
 
 extern "C" int axk_paged_attention_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kv_cache,

@@ -41,6 +41,7 @@ typedef void* axk_stream_t; /* hipStream_t */
 #define AXK_E_LAUNCH 7    /* the HIP runtime rejected the launch */
 #define AXK_E_ROLE 8      /* unknown role name in an IO-table query */
 #define AXK_E_BUFFER 9    /* a host-side output buffer is too small */
+#define AXK_E_SCRATCH 10  /* the call needs more than the library's static scratch (no-allocation entry points) */
 
 /* AX dtype codes used on the boundary (tools/manifest/onnx_io.py:18-29) */
 #define AXK_DT_U8 1
@@ -158,6 +159,19 @@ int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, const int32_t*
                      int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                      int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
                      axk_stream_t stream);
+
+/* axk_paged_decode without a workspace argument, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The split partials live in
+ * a static device array of the library (AXK_PAGED_NOALLOC_SCRATCH_BYTES, held by each GPU the library runs on until the
+ * process ends); nothing is allocated or freed. A configuration whose axk_paged_decode_workspace_size exceeds it is
+ * rejected with AXK_E_SCRATCH before anything is launched. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, or host threads) race and must be serialised by the caller. Other arguments
+ * and the result as axk_paged_decode. */
+#define AXK_PAGED_NOALLOC_SCRATCH_BYTES (24u << 20)
+int axk_paged_decode_noalloc(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
+                             const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                             int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                             int64_t num_pages, float sm_scale, axk_stream_t stream);
 
 /* The sgl decode operator's page-table convention (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/attention/
  * flash_attn.py:2335-2357 and 1421-1596; its test models/qwen35_35b_a3b/sgl/tests/test_qwen35_runtime.py:96-118):
