@@ -4,9 +4,9 @@ Python host layer over libaxk.so (include/axk.h). Operator names and contracts m
 sgl_kernel_axera operator API; tensors are torch device tensors used only as memory and streams.
 """
 from . import _lib
-from .gemm import bf16_gemm, fp8_gemm, mxfp4_dequant, mxfp4_gemm
+from .gemm import bf16_gemm, fp8_gemm, mxfp4_dequant, mxfp4_gemm, mxfp8_gemm
 
-__all__ = ["bf16_gemm", "fp8_gemm", "mxfp4_dequant", "mxfp4_gemm", "load_library"]
+__all__ = ["bf16_gemm", "fp8_gemm", "mxfp4_dequant", "mxfp4_gemm", "mxfp8_gemm", "load_library"]
 
 
 def load_library():

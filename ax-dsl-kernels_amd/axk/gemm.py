@@ -18,7 +18,7 @@ _OUT_DT = {torch.bfloat16: _lib.DT_BF16, torch.float32: _lib.DT_F32}
 
 def _as_u8(t: torch.Tensor, name: str) -> torch.Tensor:
     """FP4 codes / E8M0 / E4M3 payloads travel as u8; accept torch's packed views of the same bytes."""
-    if t.dtype in (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn):
+    if t.dtype in (torch.uint8, torch.float4_e2m1fn_x2, torch.float8_e8m0fnu, torch.float8_e4m3fn, torch.float8_e5m2):
         return t.view(torch.uint8)
     raise ValueError(f"{name} must be uint8 (or a float4/float8 view of bytes), got {t.dtype}")
 
@@ -136,6 +136,53 @@ def fp8_gemm(
     _lib.require_device(a, w, output)
     _lib.call(
         "axk_fp8_gemm", a.data_ptr(), a.stride(0), w.data_ptr(), _lib.ptr(sa), sb.data_ptr(), _lib.ptr(bias),
+        output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output
+
+
+_FP8_DT = {"e4m3": _lib.DT_FP8E4M3, "e5m2": _lib.DT_FP8E5M2}
+
+
+def mxfp8_gemm(
+    a: torch.Tensor,
+    b_fp8: torch.Tensor,
+    b_scale: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+    fmt: Optional[str] = None,
+) -> torch.Tensor:
+    """MXFP8 GEMM: output = a @ dequant(b_fp8, b_scale).T + bias (gemm.py:644-659).
+
+    a       : (m, k) bf16 activation
+    b_fp8   : (n, k) MXFP8 weight, fp8_e4m3 or fp8_e5m2 (a float8 view, or u8 with fmt = "e4m3" / "e5m2")
+    b_scale : (n, k//32) E8M0 per-32 block scale (u8 or float8_e8m0fnu view)
+    """
+    m, k = _check_a(a)
+    if fmt is None:
+        if b_fp8.dtype == torch.float8_e4m3fn:
+            fmt = "e4m3"
+        elif b_fp8.dtype == torch.float8_e5m2:
+            fmt = "e5m2"
+        else:
+            raise ValueError("b_fp8 must be a float8_e4m3fn / float8_e5m2 tensor, or u8 with fmt given")
+    if fmt not in _FP8_DT:
+        raise ValueError(f"fmt must be 'e4m3' or 'e5m2', got {fmt}")
+    if b_fp8.dtype not in (torch.uint8, torch.float8_e4m3fn, torch.float8_e5m2):
+        raise ValueError(f"b_fp8 must be uint8 or a float8 view, got {b_fp8.dtype}")
+    w = b_fp8.view(torch.uint8)
+    scales = _as_u8(b_scale, "b_scale")
+    if w.dim() != 2 or w.shape[1] != k:
+        raise ValueError(f"b_fp8 shape {tuple(b_fp8.shape)} is incompatible with a having k={k}")
+    n = w.shape[0]
+    if tuple(scales.shape) != (n, k // 32):
+        raise ValueError(f"b_scale shape {tuple(b_scale.shape)} is incompatible with (n, k/32)={(n, k // 32)}")
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    w, scales = w.contiguous(), scales.contiguous()
+    _lib.require_device(a, w, scales, output)
+    _lib.call(
+        "axk_mxfp8_gemm", a.data_ptr(), a.stride(0), w.data_ptr(), scales.data_ptr(), _FP8_DT[fmt], _lib.ptr(bias),
         output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
     )
     return output

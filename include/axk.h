@@ -91,6 +91,19 @@ int axk_fp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const flo
                  const float* scale_b, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
                  int64_t k, axk_stream_t stream);
 
+/* MXFP8 GEMM: output = a @ dequant(b_fp8, b_scale).T + bias, fp32 accumulation, where
+ * dequant(w)[n, k] = FP8(b_fp8[n, k]) * 2^(b_scale[n, k / 32] - 127). Replaces sgl_kernel_axera.gemm.mxfp8_gemm
+ * (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/gemm.py:644-659) and the MXFP8 projections of
+ * models/qwen35_35b_a3b/src/70b0fbc/q35_mx_build.py:60-72 (quant_mxfp8 / dequant).
+ *   a        bf16 [m, k] (row stride lda elements, lda % 8 == 0)
+ *   b_fp8    u8   [n, k]: OCP FP8 codes, E4M3 (fp8_dtype == AXK_DT_FP8E4M3) or E5M2 (AXK_DT_FP8E5M2)
+ *   b_scale  u8   [n, k/32] E8M0
+ *   bias f32 [n] or NULL; out bf16 / f32 [m, n]; k % 32 == 0; a, b_fp8 16-byte aligned.
+ * Each weight is decoded to bf16 in registers by gfx950's scaled converts, exactly while code * 2^(s-127) is a bf16
+ * normal (every finite code at scale bytes 10 .. 246 for E4M3, 17 .. 239 for E5M2). */
+int axk_mxfp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const uint8_t* b_scale, int fp8_dtype,
+                   const float* bias, void* out, int out_dtype, int64_t m, int64_t n, int64_t k, axk_stream_t stream);
+
 /* Dense bf16-weight linear (router logits and other small bf16 projections):
  * output = a @ b.T + bias, fp32 accumulation. Replaces sgl_kernel_axera.gemm.fp16_gemm / bf16_gemm
  * (gemm.py:81-116, 469-476). a bf16 [m, k]; b bf16 [n, k]; k % 32 == 0. */

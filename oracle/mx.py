@@ -9,9 +9,14 @@ Restates
   * MX linear golden         q35_moe.py:222-239 (torch fp32 matmul on exactly dequantised weights),
                              sgl_kernel_axera/gemm.py:564-641 (a @ dequant(w).T + bias, fp32 acc)
   * FP8 per-channel linear   sgl_kernel_axera/gemm.py:119-181
+  * quant_mxfp8 / dequant    models/qwen35_35b_a3b/src/70b0fbc/q35_mx_build.py:60-72 (E4M3 codes, one E8M0 per 32
+                             along K, e = ceil(log2(amax / 448)) so nothing saturates); E5M2 codes as the other
+                             MXFP8 element type sgl's mxfp8_gemm accepts (gemm.py:644-659)
 Pinned by tests/test_oracle_mx.py: exhaustive 16 x 256 code/scale table against the closed form and
-torch's float8_e8m0fnu / exp2, E4M3 table against torch.float8_e4m3fn, the C restatement
-(oracle/mx_codec.c) against this module, quantiser brute force + round trip, and the linear
+torch's float8_e8m0fnu / exp2, E4M3 and E5M2 tables against torch.float8_e4m3fn / float8_e5m2, the
+MXFP8 dequant against a float64 bit-field decode for every (code, scale) pair, the MXFP8 quantiser's
+scale rule and nearest-code choice against a brute-force search over all 256 codes, the C restatement
+(oracle/mx_codec.c) against this module, quantiser brute force + round trip, and the linears
 against float64 dot products.
 """
 from __future__ import annotations
@@ -83,6 +88,62 @@ def e4m3_table() -> np.ndarray:
             out[b] = s * m * 2.0 ** -9
         else:
             out[b] = s * (1 + m / 8.0) * 2.0 ** (e - 7)
+    return out
+
+
+def e5m2_table() -> np.ndarray:
+    """All 256 OCP E5M2 values from the format definition: bias 15, subnormal m * 2^-16, exponent 31 = inf / NaN."""
+    out = np.empty(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e, m = (b >> 2) & 31, b & 3
+        if e == 31:
+            out[b] = s * np.inf if m == 0 else np.nan
+        elif e == 0:
+            out[b] = s * m * 2.0 ** -16
+        else:
+            out[b] = s * (1 + m / 4.0) * 2.0 ** (e - 15)
+    return out
+
+
+FP8_MAX = {"e4m3": 448.0, "e5m2": 57344.0}
+
+
+def fp8_table(fmt: str) -> np.ndarray:
+    return e4m3_table() if fmt == "e4m3" else e5m2_table()
+
+
+def quant_mxfp8(w, fmt: str = "e4m3") -> tuple[np.ndarray, np.ndarray]:
+    """[N, K] -> (codes u8 [N, K], E8M0 scales u8 [N, K/32]) as q35_mx_build.py:60-66: per block of 32 along K,
+    amax clamped to >= 2^-126, e = clamp(ceil(log2(amax / FP8_MAX)), -127, 127), codes = FP8(w / 2^e) rounded to
+    nearest even by torch's float8 cast, scale byte e + 127."""
+    t = torch.as_tensor(np.asarray(w, dtype=np.float32))
+    n, k = t.shape
+    g = t.reshape(n, k // GROUP, GROUP)
+    amax = g.abs().amax(-1, keepdim=True).clamp_min(2.0 ** -126)
+    e = torch.ceil(torch.log2(amax / FP8_MAX[fmt])).clamp(-127, 127)
+    dt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+    codes = (g / torch.exp2(e)).to(dt).reshape(n, k).view(torch.uint8)
+    scale = (e.squeeze(-1) + 127).to(torch.uint8)
+    return codes.numpy(), scale.numpy()
+
+
+def dequant_mxfp8(codes: np.ndarray, scales: np.ndarray, fmt: str = "e4m3") -> np.ndarray:
+    """u8 FP8 codes [N, K] + u8 E8M0 [N, K/32] -> fp32 [N, K] (q35_mx_build.py:69-72)."""
+    c = np.asarray(codes, dtype=np.uint8)
+    n, k = c.shape
+    v = fp8_table(fmt)[c]
+    f = e8m0_to_f32(scales)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (v.reshape(n, k // GROUP, GROUP) * f[..., None]).reshape(n, k).astype(np.float32)
+
+
+def mxfp8_linear(a: torch.Tensor, codes: np.ndarray, scales: np.ndarray, fmt: str = "e4m3", bias=None):
+    """a[M, K] @ dequant_mxfp8(codes, scales).T (+ bias) in fp32 (sgl mxfp8_gemm, gemm.py:644-659)."""
+    w = torch.from_numpy(dequant_mxfp8(codes, scales, fmt))
+    out = a.float().cpu() @ w.T
+    if bias is not None:
+        out = out + bias.float().cpu()
     return out
 
 

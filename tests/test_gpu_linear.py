@@ -150,3 +150,73 @@ def test_lm_head_rows_against_oracle(dev):
     got = axk.mxfp4_gemm(c["x"], c["w"], c["s"], out_dtype=torch.float32).cpu()
     ref = mx.mx_linear(c["x"].cpu(), c["w"].cpu().numpy(), c["s"].cpu().numpy())
     torch.testing.assert_close(got, ref.float(), rtol=2e-2, atol=1e-2)
+
+
+# ---- MXFP8 (E4M3 / E5M2 codes + E8M0 per 32 along K): sgl mxfp8_gemm (gemm.py:644-659), q35_mx_build.py:60-72 ----
+def _mxfp8_weight(n, k, g, fmt, lo=119, hi=124):
+    """Finite FP8 codes (uniform over the non-NaN / non-inf bytes) and scale bytes uniform in lo .. hi - 1."""
+    table = mx.fp8_table(fmt)
+    finite = np.flatnonzero(np.isfinite(table)).astype(np.uint8)
+    codes = finite[torch.randint(0, finite.size, (n, k), generator=g).numpy()]
+    scales = torch.randint(lo, hi, (n, k // 32), generator=g, dtype=torch.uint8).numpy()
+    return codes, scales
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_mxfp8_decode_bit_exact_through_identity(dev, fmt):
+    """out = I @ dequant(W)^T = dequant(W)^T exactly (each output is one product, fp32 out): every finite code at
+    every scale byte of the bf16-normal range goes through the in-register scaled convert unchanged. A zero weight
+    comes out as +0 whatever its sign (1 * -0 + 0 * others rounds to +0 in any linear), so zeros compare by value."""
+    table = mx.fp8_table(fmt)
+    finite = np.flatnonzero(np.isfinite(table)).astype(np.uint8)
+    k = 256
+    codes = np.resize(finite, (64, k)).astype(np.uint8)
+    codes = np.roll(codes, 7, axis=1)
+    lo = 10 if fmt == "e4m3" else 17  # the smallest subnormal code times 2^(lo - 127) is a bf16 normal
+    scales = (lo + (np.arange(64 * k // 32).reshape(64, k // 32) * 29) % (239 - lo)).astype(np.uint8)
+    eye = torch.eye(k, dtype=torch.bfloat16)
+    got = axk.mxfp8_gemm(eye.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev),
+                         out_dtype=torch.float32, fmt=fmt).cpu().numpy()
+    want = mx.dequant_mxfp8(codes, scales, fmt).T
+    zero = want == 0
+    assert (got[zero] == 0).all()
+    assert _bits_equal(got[~zero], want[~zero])
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(1, 16, 32), (1, 100, 96), (3, 2048, 512), (8, 1024, 2048), (17, 300, 1024), (32, 512, 2048), (40, 64, 256)],
+)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_mxfp8_gemm_matches_oracle(dev, fmt, m, n, k, out_dtype):
+    g = torch.Generator().manual_seed(7000 * m + n + k)
+    codes, scales = _mxfp8_weight(n, k, g, fmt)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g) / 8
+    ref = mx.mxfp8_linear(a, codes, scales, fmt, bias.to(out_dtype))
+    got = axk.mxfp8_gemm(a.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev),
+                         out_dtype=out_dtype, bias=bias.to(dev), fmt=fmt)
+    if out_dtype == torch.bfloat16:
+        torch.testing.assert_close(got.float().cpu(), ref.to(out_dtype).float(), **BF16_TOL)
+    else:
+        # fp32 out: the two fp32 summation orders may differ by a few ulps of the largest partial sums, which with
+        # E5M2 codes over their whole range (weights up to ~3600) can exceed a flat 1e-3 on a cancelling sum; bound
+        # each element by its terms' magnitude: 1e-3 + 2^-20 * sum_k |a_k w_k|
+        w = torch.from_numpy(mx.dequant_mxfp8(codes, scales, fmt))
+        mag = a.float().abs() @ w.abs().T
+        err = (got.float().cpu() - ref).abs()
+        assert (err <= 1e-3 + 1e-3 * ref.abs() + mag * 2.0 ** -20).all(), float((err - mag * 2.0 ** -20).max())
+
+
+@pytest.mark.parametrize("n,k", [(16384, 4096), (1024, 4096), (4096, 8192), (8192, 4096)])
+def test_mxfp8_config4_projections(dev, n, k):
+    """Config 4's attention / GDN projection shapes (q, k / v, o, GDN qkv) with MXFP8 weights from the reference's
+    own quantiser rule (quant_mxfp8 of an N(0, 0.02) weight), 8 decode rows."""
+    g = torch.Generator().manual_seed(n + k)
+    w = (torch.randn(n, k, generator=g) * 0.02).numpy()
+    codes, scales = mx.quant_mxfp8(w)
+    a = torch.randn(8, k, generator=g).to(torch.bfloat16)
+    got = axk.mxfp8_gemm(a.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev), fmt="e4m3")
+    ref = mx.mxfp8_linear(a, codes, scales, "e4m3")
+    torch.testing.assert_close(got.float().cpu(), ref.to(torch.bfloat16).float(), **BF16_TOL)

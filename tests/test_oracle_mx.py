@@ -148,3 +148,78 @@ def test_bf16_round_is_rne(shape):
     u = x.view(np.uint32).astype(np.uint64)
     rne = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16).astype(np.uint32).view(np.float32)
     np.testing.assert_array_equal(mx.bf16_round(x), rne)
+
+
+# ---- MXFP8 (q35_mx_build.py:60-72; sgl mxfp8_gemm, gemm.py:644-659) ----
+def _fp8_closed_form(b: int, fmt: str) -> float:
+    """float64 decode of one FP8 byte from its bit fields (independent of the oracle's table loop)."""
+    ebits, mbits, bias = (4, 3, 7) if fmt == "e4m3" else (5, 2, 15)
+    s = -1.0 if b >> 7 else 1.0
+    e, m = (b >> mbits) & ((1 << ebits) - 1), b & ((1 << mbits) - 1)
+    if fmt == "e4m3" and e == 15 and m == 7:
+        return float("nan")
+    if fmt == "e5m2" and e == 31:
+        return s * float("inf") if m == 0 else float("nan")
+    if e == 0:
+        return s * m * 2.0 ** (1 - bias - mbits)
+    return s * (1.0 + m / 2.0 ** mbits) * 2.0 ** (e - bias)
+
+
+@pytest.mark.parametrize("fmt,dt", [("e4m3", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2)])
+def test_fp8_tables_against_torch_and_bit_fields(fmt, dt):
+    t = mx.fp8_table(fmt)
+    ref = torch.arange(256, dtype=torch.uint8).view(dt).float().numpy()
+    cf = np.array([_fp8_closed_form(b, fmt) for b in range(256)], dtype=np.float64)
+    assert np.array_equal(np.isnan(t), np.isnan(ref)) and np.array_equal(np.isnan(t), np.isnan(cf))
+    ok = ~np.isnan(t)
+    assert np.array_equal(t[ok], ref[ok]) and np.array_equal(t[ok].astype(np.float64), cf[ok])
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_dequant_mxfp8_every_code_and_scale(fmt):
+    # rows: one per scale byte 0..254; columns: the 256 codes in 8 blocks of 32
+    codes = np.tile(np.arange(256, dtype=np.uint8), (255, 1))
+    scales = np.repeat(np.arange(255, dtype=np.uint8)[:, None], 8, axis=1)
+    got = mx.dequant_mxfp8(codes, scales, fmt).astype(np.float64)
+    cf = np.array([_fp8_closed_form(b, fmt) for b in range(256)])
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = cf[None, :] * np.ldexp(1.0, np.arange(255)[:, None] - 127)
+    with np.errstate(over="ignore"):
+        want32 = want.astype(np.float32).astype(np.float64)  # the fp32 result of the exact product
+    both_nan = np.isnan(got) & np.isnan(want32)
+    assert np.array_equal(got[~both_nan], want32[~both_nan])
+
+
+def test_quant_mxfp8_scale_rule_and_nearest_code():
+    g = torch.Generator().manual_seed(4)
+    w = (torch.randn(6, 256, generator=g) * torch.logspace(-6, 6, 6)[:, None]).numpy()
+    w[0, :32] = 0.0  # an all-zero block: amax clamps to 2^-126
+    codes, scales = mx.quant_mxfp8(w)
+    e = scales.astype(np.int32) - 127
+    amax = np.abs(w.reshape(6, 8, 32)).max(-1)
+    # the chosen exponent is the smallest with amax / 2^e <= 448 (nothing saturates, no NaN codes)
+    nz = amax > 0
+    assert (amax[nz] / np.ldexp(1.0, e[nz]) <= 448.0).all()
+    assert (amax[nz] / np.ldexp(1.0, e[nz] - 1) > 448.0).all()
+    table = mx.e4m3_table()
+    assert not np.isnan(table[codes]).any()
+    # every code is a nearest E4M3 value of w / 2^e (brute force over the 254 finite codes)
+    x = (w.reshape(6, 8, 32) / np.ldexp(1.0, e)[..., None]).reshape(6, 256)
+    fin = table[~np.isnan(table)]
+    best = np.abs(x[..., None] - fin[None, None, :]).min(-1)
+    assert np.allclose(np.abs(x - table[codes]), best, rtol=0, atol=0)
+    # round trip within half an E4M3 step (3 mantissa bits) of each element's block scale
+    back = mx.dequant_mxfp8(codes, scales)
+    step = np.ldexp(1.0, e).repeat(32, axis=1) * 2.0 ** -9  # coarsest step below the subnormal boundary
+    assert (np.abs(back - w) <= np.maximum(np.abs(w) * 2.0 ** -4, step)).all()
+
+
+def test_mxfp8_linear_against_float64():
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(48, 128, generator=g).numpy()
+    for fmt in ("e4m3", "e5m2"):
+        codes, scales = mx.quant_mxfp8(w, fmt)
+        a = torch.randn(3, 128, generator=g).bfloat16()
+        got = mx.mxfp8_linear(a, codes, scales, fmt)
+        ref = a.double() @ torch.from_numpy(mx.dequant_mxfp8(codes, scales, fmt)).double().T
+        torch.testing.assert_close(got.double(), ref, rtol=1e-6, atol=1e-6)
