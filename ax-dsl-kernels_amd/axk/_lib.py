@@ -93,9 +93,10 @@ SIGNATURES: dict[str, list] = {
     "axk_silu_mul": [_vp, _vp, _vp, _i64, _i64, _vp],
     "axk_add": [_vp, _vp, _vp, _i64, _i64, _vp],
     "axk_gdn_layer_workspace_size": [_i64] * 6,
-    "axk_gdn_layer_decode": [_vp] * 28 + [_i64] * 7 + [ctypes.c_float, _vp, ctypes.c_size_t, _vp],
+    "axk_gdn_layer_decode": [_vp] * 28 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
     "axk_attn_layer_workspace_size": [_i64] * 6,
-    "axk_attn_layer_decode": [_vp] * 27 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _vp, ctypes.c_size_t, _vp],
+    "axk_attn_layer_decode": [_vp] * 27 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
+                              ctypes.c_size_t, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,

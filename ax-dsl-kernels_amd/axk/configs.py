@@ -158,51 +158,67 @@ def fp8_proj_weight(n: int, k: int, g: torch.Generator):
     return w, s
 
 
+def proj_weight(fmt: str, n: int, k: int, g: torch.Generator):
+    """A weight [n, k] in format fmt with its scales: "fp8" as fp8_proj_weight; "mxfp4" as mxfp4_weight (config 0's
+    draws); "mxfp8" E4M3 codes of N(0, 3^2) (torch's float8_e4m3fn cast) with E8M0 scale bytes uniform in 119..123,
+    the same weight RMS (about 0.05) as the MXFP4 draws."""
+    if fmt == "fp8":
+        return fp8_proj_weight(n, k, g)
+    if fmt == "mxfp4":
+        return mxfp4_weight(n, k, g)
+    codes = (torch.randn(n, k, generator=g) * 3).to(torch.float8_e4m3fn).view(torch.uint8).contiguous()
+    return codes, torch.randint(119, 124, (n, k // 32), generator=g, dtype=torch.uint8)
+
+
 def _norm_w(n: int, g: torch.Generator):
     """A norm's run-time weight as the reference passes it: 1 + N(0, 0.1) (f32)."""
     return 1.0 + 0.1 * torch.randn(n, generator=g)
 
 
-def mlp_weights(g: torch.Generator, hidden: int, inter: int) -> dict:
-    """The dense MXFP4 MLP of a layer: gate / up [inter, hidden], down [hidden, inter] (as config 0's draws)."""
+def mlp_weights(g: torch.Generator, hidden: int, inter: int, fmt: str = "mxfp4") -> dict:
+    """The dense MLP of a layer: gate / up [inter, hidden], down [hidden, inter] (MXFP4 by default, as config 0's
+    draws)."""
     w = {}
-    w["gate_w"], w["gate_s"] = mxfp4_weight(inter, hidden, g)
-    w["up_w"], w["up_s"] = mxfp4_weight(inter, hidden, g)
-    w["down_w"], w["down_s"] = mxfp4_weight(hidden, inter, g)
+    w["w_gate"], w["s_gate"] = proj_weight(fmt, inter, hidden, g)
+    w["w_up"], w["s_up"] = proj_weight(fmt, inter, hidden, g)
+    w["w_down"], w["s_down"] = proj_weight(fmt, hidden, inter, g)
     return w
 
 
-def gdn_layer_weights(g: torch.Generator, hidden: int, inter: int, nk: int, nv: int, conv_kernel: int = 4) -> dict:
-    """A GDN decode layer's weights (names of q35_step.py gdn_args): FP8 projections, bf16 conv taps, f32 norms
-    (ln1 / ln2 = 1 + N(0, 0.1); norm_w = 1 + N(0, 0.1)), A_log, dt_bias ~ N(0, 0.5), MXFP4 MLP."""
+def gdn_layer_weights(g: torch.Generator, hidden: int, inter: int, nk: int, nv: int, conv_kernel: int = 4,
+                      proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4") -> dict:
+    """A GDN decode layer's weights (names of q35_step.py gdn_args): projections in proj_fmt (FP8 by default), bf16
+    conv taps, f32 norms (ln1 / ln2 = 1 + N(0, 0.1); norm_w = 1 + N(0, 0.1)), A_log, dt_bias ~ N(0, 0.5), the MLP in
+    mlp_fmt (MXFP4 by default)."""
     kd, vd = nk * 128, nv * 128
     w = {"ln1": _norm_w(hidden, g)}
-    w["w_qkv"], w["s_qkv"] = fp8_proj_weight(2 * kd + vd, hidden, g)
-    w["w_z"], w["s_z"] = fp8_proj_weight(vd, hidden, g)
-    w["w_b"], w["s_b"] = fp8_proj_weight(nv, hidden, g)
-    w["w_a"], w["s_a"] = fp8_proj_weight(nv, hidden, g)
+    w["w_qkv"], w["s_qkv"] = proj_weight(proj_fmt, 2 * kd + vd, hidden, g)
+    w["w_z"], w["s_z"] = proj_weight(proj_fmt, vd, hidden, g)
+    w["w_b"], w["s_b"] = proj_weight(proj_fmt, nv, hidden, g)
+    w["w_a"], w["s_a"] = proj_weight(proj_fmt, nv, hidden, g)
     w["conv_w"] = (torch.randn(2 * kd + vd, conv_kernel, generator=g) * 0.5).to(torch.bfloat16)
     w["a_log"] = torch.randn(nv, generator=g) * 0.5
     w["dt_bias"] = torch.randn(nv, generator=g) * 0.5
     w["norm_w"] = _norm_w(128, g)
-    w["w_out"], w["s_out"] = fp8_proj_weight(hidden, vd, g)
+    w["w_out"], w["s_out"] = proj_weight(proj_fmt, hidden, vd, g)
     w["ln2"] = _norm_w(hidden, g)
-    w.update(mlp_weights(g, hidden, inter))
+    w.update(mlp_weights(g, hidden, inter, mlp_fmt))
     return w
 
 
-def attn_layer_weights(g: torch.Generator, hidden: int, inter: int, hq: int, hkv: int, d: int) -> dict:
-    """An attention decode layer's weights (names of q35_step.py attn_args): FP8 q (per head [q | gate]), k, v, o;
-    f32 norms 1 + N(0, 0.1); MXFP4 MLP."""
+def attn_layer_weights(g: torch.Generator, hidden: int, inter: int, hq: int, hkv: int, d: int,
+                       proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4") -> dict:
+    """An attention decode layer's weights (names of q35_step.py attn_args): q (per head [q | gate]), k, v, o in
+    proj_fmt (FP8 by default); f32 norms 1 + N(0, 0.1); the MLP in mlp_fmt (MXFP4 by default)."""
     w = {"ln1": _norm_w(hidden, g)}
-    w["w_q"], w["s_q"] = fp8_proj_weight(hq * 2 * d, hidden, g)
-    w["w_k"], w["s_k"] = fp8_proj_weight(hkv * d, hidden, g)
-    w["w_v"], w["s_v"] = fp8_proj_weight(hkv * d, hidden, g)
+    w["w_q"], w["s_q"] = proj_weight(proj_fmt, hq * 2 * d, hidden, g)
+    w["w_k"], w["s_k"] = proj_weight(proj_fmt, hkv * d, hidden, g)
+    w["w_v"], w["s_v"] = proj_weight(proj_fmt, hkv * d, hidden, g)
     w["q_norm"] = _norm_w(d, g)
     w["k_norm"] = _norm_w(d, g)
-    w["w_o"], w["s_o"] = fp8_proj_weight(hidden, hq * d, g)
+    w["w_o"], w["s_o"] = proj_weight(proj_fmt, hidden, hq * d, g)
     w["ln2"] = _norm_w(hidden, g)
-    w.update(mlp_weights(g, hidden, inter))
+    w.update(mlp_weights(g, hidden, inter, mlp_fmt))
     return w
 
 
@@ -261,9 +277,9 @@ def config4_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None 
 
     def mlp():
         w = {}
-        w["gate_w"], w["gate_s"] = mx(f, h)
-        w["up_w"], w["up_s"] = mx(f, h)
-        w["down_w"], w["down_s"] = mx(h, f)
+        w["w_gate"], w["s_gate"] = mx(f, h)
+        w["w_up"], w["s_up"] = mx(f, h)
+        w["w_down"], w["s_down"] = mx(h, f)
         return w
 
     kd, vd = nk * 128, nv * 128

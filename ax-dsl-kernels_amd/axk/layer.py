@@ -1,10 +1,14 @@
 """Hybrid decode layers (one token per sequence) over libaxk.so: the GDN layer and the attention layer of
 models/qwen35_35b_a3b/src/70b0fbc/q35_step.py (gdn_layer 149-183, attn_block 186-293), each with its MLP.
 
-Weights travel in dicts keyed by the reference's names (q35_step.py gdn_args / attn_args / mlp_args 361-406):
-projections FP8 E4M3 as (w_<name> u8 [N, K], s_<name> f32 [N]); the MLP MXFP4 as (gate_w, gate_s, up_w, up_s,
-down_w, down_s); norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is allocated once
-by the caller (layer_workspace) and reused; a layer call allocates nothing.
+Weights travel in dicts keyed by the reference's names (q35_step.py gdn_args / attn_args / mlp_args 361-406, the
+manifest params of tools/manifest/mkmanifest.py:23-35): each projection and MLP weight as w_<name> with its scales
+s_<name>, in the format given by proj_fmt / mlp_fmt:
+  "fp8"   (w u8 E4M3 [N, K], s f32 [N] per output channel)  - config 4's projections (sgl gemm.py:119-181)
+  "mxfp8" (w u8 E4M3 [N, K], s u8 E8M0 [N, K/32])            - the 35B manifest (q35_mx_build.py:60-72)
+  "mxfp4" (w u8 E2M1 pairs [N, K/2], s u8 E8M0 [N, K/32])    - the 9B / 27B manifests and config 4's MLP
+norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is allocated once by the caller
+(layer_workspace) and reused; a layer call allocates nothing.
 """
 from __future__ import annotations
 
@@ -17,7 +21,8 @@ from . import _lib
 GDN_WEIGHTS = ("ln1", "w_qkv", "s_qkv", "w_z", "s_z", "w_b", "s_b", "w_a", "s_a", "conv_w", "a_log", "dt_bias",
                "norm_w", "w_out", "s_out", "ln2")
 ATTN_WEIGHTS = ("ln1", "w_q", "s_q", "w_k", "s_k", "w_v", "s_v", "q_norm", "k_norm", "w_o", "s_o", "ln2")
-MLP_WEIGHTS = ("gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s")
+MLP_WEIGHTS = ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down")
+WFMT = {"fp8": 0, "mxfp8": 1, "mxfp4": 2}  # AXK_WFMT_FP8_CHANNEL, AXK_WFMT_MXFP8, AXK_WFMT_MXFP4
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -47,15 +52,20 @@ def attn_workspace(batch: int, hidden: int, num_qo_heads: int, num_kv_heads: int
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
+def _fmt(name: str) -> int:
+    _check(name in WFMT, f"weight format must be one of {sorted(WFMT)}, got {name!r}")
+    return WFMT[name]
+
+
 def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: torch.Tensor,
                      num_k_heads: int, num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                      out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
-                     conv_out: Optional[torch.Tensor] = None):
+                     conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
     """x bf16 [B, hidden]; state f32 [B, NV, 128, 128]; conv state bf16 [B, K-1, 2 KD + VD].
     Returns (out, state_out, conv_out); state_out / conv_out may be the inputs (in place)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
     b, h = x.shape
-    inter = w["gate_w"].shape[0]
+    inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
     ws = workspace if workspace is not None else gdn_workspace(b, h, num_k_heads, num_v_heads, inter, x.device)
     o = torch.empty_like(x) if out is None else out
@@ -66,8 +76,8 @@ def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     ptrs = [t.data_ptr() for t in args]
     # the C order: x, ln1 .. s_out, ln2, MLP, state_in, conv_in, out, state_out, conv_out
     _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
-              so.data_ptr(), co.data_ptr(), b, h, num_k_heads, num_v_heads, 128, kconv, inter, eps, ws.data_ptr(),
-              ws.numel(), _lib.stream_of(x))
+              so.data_ptr(), co.data_ptr(), b, h, num_k_heads, num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt),
+              _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
     return o, so, co
 
 
@@ -75,13 +85,13 @@ def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
                       indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
                       cache_location: torch.Tensor, num_qo_heads: int, rot: int, eps: float = 1e-6,
                       sm_scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
-                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4") -> torch.Tensor:
     """x bf16 [B, hidden]; kv_cache bf16 [P, 2, page, HKV, D] written in place at cache_location (int32 [B, 2]);
     the page table describes each sequence including the new token; cos, sin bf16 [B, rot/2]."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
     b, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
-    inter = w["gate_w"].shape[0]
+    inter = w["w_gate"].shape[0]
     ws = workspace if workspace is not None else attn_workspace(b, h, num_qo_heads, hkv, d, inter, x.device)
     o = torch.empty_like(x) if out is None else out
     scale = d ** -0.5 if sm_scale is None else sm_scale
@@ -94,5 +104,5 @@ def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
               _lib.ptr(cos), _lib.ptr(sin), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
               last_page_len.data_ptr(), cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(),
               *[t.data_ptr() for t in mlp], o.data_ptr(), b, h, num_qo_heads, hkv, d, rot, page, pages, inter, eps,
-              scale, ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+              scale, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
     return o

@@ -1,7 +1,8 @@
 // One hybrid decode layer per call, composed from the library's kernels on the caller's stream: the GDN layer
 // (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py gdn_layer 149-183) and the attention layer (attn_block 186-280),
-// each followed by the MLP block (mlp_block 118-142). Projections of the attention / GDN paths are FP8 E4M3 with
-// per-output-channel fp32 scales; the MLP is MXFP4 (the config of the hybrid decode group). Every intermediate is
+// each followed by the MLP block (mlp_block 118-142). The projections of the attention / GDN paths and the MLP each take
+// a weight format (AXK_WFMT_*): FP8 E4M3 with per-output-channel fp32 scales (the config of the hybrid decode group),
+// MXFP8 (the 35B manifest's layer weights) or MXFP4 (the 9B / 27B manifests' and the group's MLP). Every intermediate is
 // a bf16 tensor in the caller's workspace, rounded where the reference rounds (each projection's output, each
 // glue op's output). Projections that share an input run as one grouped launch (GDN: qkv | z | b | a, whose qkv
 // epilogue also runs the causal conv1d + SiLU; attention: q | k | v); the GDN kernel applies the gated output norm
@@ -28,8 +29,25 @@ struct Carver {
 };
 
 struct MlpWeights {
-  const uint8_t *gate_w, *gate_s, *up_w, *up_s, *down_w, *down_s;
+  const uint8_t *gate_w, *up_w, *down_w;
+  const void *gate_s, *up_s, *down_s;
 };
+
+// The grouped kernel's format of a weight format code (AXK_WFMT_*), or -1.
+int mx_fmt_of(int wfmt) {
+  switch (wfmt) {
+    case AXK_WFMT_FP8_CHANNEL: return AXK_MX_FP8;
+    case AXK_WFMT_MXFP8: return AXK_MX_MXFP8;
+    case AXK_WFMT_MXFP4: return AXK_MX_MXFP4;
+    default: return -1;
+  }
+}
+
+// One projection of the group: per-channel f32 scales [N] (FP8) or E8M0 block scales [N, K/32] (MX formats).
+AxkMxMat proj_mat(int wfmt, const uint8_t* w, const void* s, void* out, int64_t n) {
+  if (wfmt == AXK_WFMT_FP8_CHANNEL) return AxkMxMat{w, nullptr, static_cast<const float*>(s), nullptr, out, n, n};
+  return AxkMxMat{w, static_cast<const uint8_t*>(s), nullptr, nullptr, out, n, n};
+}
 
 struct MlpBufs {
   uint16_t *x1, *h2, *act;
@@ -50,29 +68,24 @@ MlpBufs carve_mlp(Carver& c, int64_t B, int64_t H, int64_t F) {
   } while (0)
 
 // x1 = x + y; h2 = rmsnorm(x1, ln2); out = x1 + down(silu(gate h2) * up h2)  (mlp_block, q35_step.py:118-142):
-// three launches (the norm, gate | up with SwiGLU, down with the residual add).
-int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const MlpWeights& w, uint16_t* out,
+// three launches (the norm, gate | up with SwiGLU, down with the residual add). wfmt: the MLP weights' format.
+int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const MlpWeights& w, int wfmt, uint16_t* out,
                  const MlpBufs& m, int64_t B, int64_t H, int64_t F, float eps, axk_stream_t st) {
   AXK_TRY(axk_add_rmsnorm(x, y, ln2, m.x1, m.h2, B, H, eps, st));
-  const AxkMxMat gate_up[2] = {{w.gate_w, w.gate_s, nullptr, nullptr, m.act, F, F},
-                               {w.up_w, w.up_s, nullptr, nullptr, m.act, F, F}};
-  AXK_TRY(axk_mx_group(AXK_MX_MXFP4, m.h2, H, gate_up, 2, AXK_MX_EPI_SWIGLU, nullptr, 0, nullptr, AXK_DT_BF16, B, H,
-                       nullptr, axk_stream(st)));
-  const AxkMxMat down{w.down_w, w.down_s, nullptr, nullptr, out, H, H};
-  return axk_mx_group(AXK_MX_MXFP4, m.act, F, &down, 1, AXK_MX_EPI_RES, m.x1, H, nullptr, AXK_DT_BF16, B, F,
+  const AxkMxMat gate_up[2] = {proj_mat(wfmt, w.gate_w, w.gate_s, m.act, F), proj_mat(wfmt, w.up_w, w.up_s, m.act, F)};
+  AXK_TRY(axk_mx_group(mx_fmt_of(wfmt), m.h2, H, gate_up, 2, AXK_MX_EPI_SWIGLU, nullptr, 0, nullptr, AXK_DT_BF16, B,
+                       H, nullptr, axk_stream(st)));
+  const AxkMxMat down = proj_mat(wfmt, w.down_w, w.down_s, out, H);
+  return axk_mx_group(mx_fmt_of(wfmt), m.act, F, &down, 1, AXK_MX_EPI_RES, m.x1, H, nullptr, AXK_DT_BF16, B, F,
                       nullptr, axk_stream(st));
 }
 
-// FP8 projections of one input a [m, k] (bf16 outputs, per-channel scales) as one grouped launch; conv (optional)
+// Projections of one input a [m, k] in weight format wfmt (bf16 outputs) as one grouped launch; conv (optional)
 // runs the causal conv1d + SiLU on the first matrix's output.
-int fp8_projs(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int64_t m, int64_t k,
-              axk_stream_t st, const AxkConvEpi* conv = nullptr) {
-  return axk_mx_group(AXK_MX_FP8, a, lda, mats, count, AXK_MX_EPI_PLAIN, nullptr, 0, nullptr, AXK_DT_BF16, m, k,
+int projs(int wfmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int64_t m, int64_t k,
+          axk_stream_t st, const AxkConvEpi* conv = nullptr) {
+  return axk_mx_group(mx_fmt_of(wfmt), a, lda, mats, count, AXK_MX_EPI_PLAIN, nullptr, 0, nullptr, AXK_DT_BF16, m, k,
                       conv, axk_stream(st));
-}
-
-AxkMxMat fp8_mat(const uint8_t* w, const float* s, uint16_t* out, int64_t n) {
-  return AxkMxMat{w, nullptr, s, nullptr, out, n, n};
 }
 
 struct GdnBufs {
@@ -136,18 +149,19 @@ extern "C" size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, in
 }
 
 extern "C" int axk_gdn_layer_decode(
-    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const float* s_qkv, const uint8_t* w_z,
-    const float* s_z, const uint8_t* w_b, const float* s_b, const uint8_t* w_a, const float* s_a,
-    const uint16_t* conv_w, const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out,
-    const float* s_out, const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
-    const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w, const uint8_t* mlp_down_s,
-    const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
-    int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel,
-    int64_t inter, float eps, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
+    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
+    int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+    int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
                   mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
               AXK_E_NULL);
+  AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
   const size_t need = axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
@@ -155,23 +169,23 @@ extern "C" int axk_gdn_layer_decode(
   const int64_t KD = NK * DH, VD = NV * DH, C = 2 * KD + VD;
   Carver c{static_cast<unsigned char*>(workspace)};
   const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
-  const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
+  const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
     // qkv | z | b | a, the qkv output through the causal conv1d + SiLU (mixed) as it is stored
-    const AxkMxMat proj[4] = {fp8_mat(w_qkv, s_qkv, g.mixed, C), fp8_mat(w_z, s_z, g.z, VD),
-                              fp8_mat(w_b, s_b, g.bb, NV), fp8_mat(w_a, s_a, g.aa, NV)};
+    const AxkMxMat proj[4] = {proj_mat(proj_fmt, w_qkv, s_qkv, g.mixed, C), proj_mat(proj_fmt, w_z, s_z, g.z, VD),
+                              proj_mat(proj_fmt, w_b, s_b, g.bb, NV), proj_mat(proj_fmt, w_a, s_a, g.aa, NV)};
     const AxkConvEpi conv{conv_w, conv_in, conv_out, conv_kernel};
-    AXK_TRY(fp8_projs(g.h, H, proj, 4, B, H, stream, &conv));
+    AXK_TRY(projs(proj_fmt, g.h, H, proj, 4, B, H, stream, &conv));
     // q, k, v are the conv output's channel ranges [0, KD), [KD, 2 KD), [2 KD, C) of each sequence's row; each
     // head's output row leaves through the gated output norm
     const AxkGdnStrides ld{C, C, C, NV};
     const AxkGdnGate gate{norm_w, g.z, eps};
     AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
                                       state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
-    const AxkMxMat o = fp8_mat(w_out, s_out, g.y, H);
-    AXK_TRY(fp8_projs(g.gated, VD, &o, 1, B, VD, stream));
-    return mlp_residual(x, g.y, ln2, mw, out, g.mlp, B, H, F, eps, stream);
+    const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
+    AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, B, VD, stream));
+    return mlp_residual(x, g.y, ln2, mw, mlp_fmt, out, g.mlp, B, H, F, eps, stream);
   };
   {
     const AxkValidateScope check_only;  // every sub-call's checks before the first launch
@@ -191,39 +205,40 @@ extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, i
 }
 
 extern "C" int axk_attn_layer_decode(
-    const uint16_t* x, const float* ln1, const uint8_t* w_q, const float* s_q, const uint8_t* w_k, const float* s_k,
-    const uint8_t* w_v, const float* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
+    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
     const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
-    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const float* s_o,
-    const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s, const uint8_t* mlp_up_w,
-    const uint8_t* mlp_up_s, const uint8_t* mlp_down_w, const uint8_t* mlp_down_s, uint16_t* out, int64_t batch,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, uint16_t* out, int64_t batch,
     int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
-    int64_t num_pages, int64_t inter, float eps, float sm_scale, void* workspace, size_t workspace_bytes,
-    axk_stream_t stream) {
+    int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
+    size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
                   indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
                   mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
               AXK_E_NULL);
+  AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
   const size_t need = axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
   const int64_t B = batch, H = hidden, HQ = num_qo_heads, HKV = num_kv_heads, D = head_dim, F = inter;
   Carver c{static_cast<unsigned char*>(workspace)};
   const AttnBufs a = carve_attn(c, B, H, HQ, HKV, D, F);
-  const MlpWeights mw{mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s};
+  const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
-    const AxkMxMat proj[3] = {fp8_mat(w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
-                              fp8_mat(w_k, s_k, a.kk, HKV * D), fp8_mat(w_v, s_v, a.vv, HKV * D)};
-    AXK_TRY(fp8_projs(a.h, H, proj, 3, B, H, stream));
+    const AxkMxMat proj[3] = {proj_mat(proj_fmt, w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
+                              proj_mat(proj_fmt, w_k, s_k, a.kk, HKV * D), proj_mat(proj_fmt, w_v, s_v, a.vv, HKV * D)};
+    AXK_TRY(projs(proj_fmt, a.h, H, proj, 3, B, H, stream));
     AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, B, HQ, HKV,
                               D, rot, page_size, num_pages, eps, axk_stream(stream)));
     AXK_TRY(axk_paged_decode(a.q, kv_cache, indptr, indices, last_page_len, a.attn, B, HQ, HKV, D, page_size,
                              num_pages, sm_scale, a.pws, a.pws_bytes, stream));
     AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
-    const AxkMxMat o = fp8_mat(w_o, s_o, a.y, H);
-    AXK_TRY(fp8_projs(a.gated, HQ * D, &o, 1, B, HQ * D, stream));
-    return mlp_residual(x, a.y, ln2, mw, out, a.mlp, B, H, F, eps, stream);
+    const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
+    AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, B, HQ * D, stream));
+    return mlp_residual(x, a.y, ln2, mw, mlp_fmt, out, a.mlp, B, H, F, eps, stream);
   };
   {
     const AxkValidateScope check_only;  // every sub-call's checks before the first launch

@@ -53,6 +53,14 @@ typedef void* axk_stream_t; /* hipStream_t */
 #define AXK_DT_FP8E5M2 12
 #define AXK_DT_FP4 15
 
+/* Weight formats of the decode layers' projections and MLP (proj_fmt / mlp_fmt):
+ *   AXK_WFMT_FP8_CHANNEL  E4M3 bytes [N, K] + f32 per-output-channel scale [N]   (sgl gemm.py:119-181)
+ *   AXK_WFMT_MXFP8        E4M3 bytes [N, K] + E8M0 bytes [N, K/32]              (q35_mx_build.py:60-72; the 35B manifest)
+ *   AXK_WFMT_MXFP4        E2M1 pairs [N, K/2] + E8M0 bytes [N, K/32]            (q35_moe.py:46-63; the 9B / 27B manifests) */
+#define AXK_WFMT_FP8_CHANNEL 0
+#define AXK_WFMT_MXFP8 1
+#define AXK_WFMT_MXFP4 2
+
 /* Library identification and error text. */
 const char* axk_version(void);
 const char* axk_status_string(int status);
@@ -395,9 +403,12 @@ int axk_add(const uint16_t* x, const uint16_t* y, uint16_t* out, int64_t rows, i
 
 /* ---------------------------------------------------------------------------------------------
  * Decode layers of the hybrid group (one token per sequence, `batch` sequences), composed from the kernels above
- * on `stream`: projections FP8 E4M3 [N, K] + f32 per-output-channel scale, MLP MXFP4 (codes [N, K/2], E8M0
- * [N, K/32]). Every intermediate lives in the caller's workspace (256-byte aligned, *_workspace_size bytes);
- * nothing is allocated or synchronised, so a layer can be captured in a HIP graph. hidden, inter % 256 == 0.
+ * on `stream`. The attention / GDN projections are in weight format proj_fmt and the MLP in mlp_fmt (AXK_WFMT_*):
+ * each weight w_<x> with its scales s_<x> (f32 [N] for AXK_WFMT_FP8_CHANNEL, E8M0 bytes [N, K/32] for the MX formats,
+ * hence `const void*`). Every intermediate lives in the caller's workspace (256-byte aligned, *_workspace_size bytes);
+ * nothing is allocated or synchronised, so a layer can be captured in a HIP graph. hidden, inter % 256 == 0; every
+ * projection's K a whole number of 128-byte weight rows. All checks run before the first launch: a nonzero status
+ * means no state, conv state or cache byte changed.
  * ------------------------------------------------------------------------------------------- */
 
 /* Workspace bytes of axk_gdn_layer_decode (0 = unsupported shape; head_dim must be 128). */
@@ -413,16 +424,16 @@ size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k
  *   a_log, dt_bias f32 [num_v_heads]; norm_w f32 [head_dim]; MLP gate / up [inter, hidden], down [hidden, inter]
  *   (MXFP4); state f32 [batch, num_v_heads, 128, 128] (in place allowed); conv state bf16
  *   [batch, conv_kernel - 1, 2 KD + VD] (in place allowed). KD = num_k_heads * 128, VD = num_v_heads * 128. */
-int axk_gdn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const float* s_qkv,
-                         const uint8_t* w_z, const float* s_z, const uint8_t* w_b, const float* s_b,
-                         const uint8_t* w_a, const float* s_a, const uint16_t* conv_w, const float* a_log,
-                         const float* dt_bias, const float* norm_w, const uint8_t* w_out, const float* s_out,
-                         const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
-                         const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w,
-                         const uint8_t* mlp_down_s, const float* state_in, const uint16_t* conv_in, uint16_t* out,
+int axk_gdn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
+                         const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b,
+                         const uint8_t* w_a, const void* s_a, const uint16_t* conv_w, const float* a_log,
+                         const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+                         const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                         const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                         const void* mlp_down_s, const float* state_in, const uint16_t* conv_in, uint16_t* out,
                          float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden, int64_t num_k_heads,
                          int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
-                         void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                         int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 /* Workspace bytes of axk_attn_layer_decode (0 = unsupported shape). */
 size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
@@ -436,17 +447,17 @@ size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_
  *   w_q [2 D num_qo_heads, hidden], w_k, w_v [D num_kv_heads, hidden], w_o [hidden, D num_qo_heads] (FP8 + f32
  *   scales); q_norm, k_norm f32 [D] (1 + weight); cos, sin bf16 [batch, rot / 2] (each sequence's position);
  *   kv_cache and the page table as axk_paged_decode, cache_location as axk_paged_kv_write. */
-int axk_attn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_q, const float* s_q,
-                          const uint8_t* w_k, const float* s_k, const uint8_t* w_v, const float* s_v,
+int axk_attn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q,
+                          const uint8_t* w_k, const void* s_k, const uint8_t* w_v, const void* s_v,
                           const float* q_norm, const float* k_norm, const uint16_t* cos, const uint16_t* sin,
                           uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
                           const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o,
-                          const float* s_o, const float* ln2, const uint8_t* mlp_gate_w, const uint8_t* mlp_gate_s,
-                          const uint8_t* mlp_up_w, const uint8_t* mlp_up_s, const uint8_t* mlp_down_w,
-                          const uint8_t* mlp_down_s, uint16_t* out, int64_t batch, int64_t hidden,
+                          const void* s_o, const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                          const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                          const void* mlp_down_s, uint16_t* out, int64_t batch, int64_t hidden,
                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
                           int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
-                          void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                          int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 #ifdef __cplusplus
 }

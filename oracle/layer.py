@@ -92,31 +92,39 @@ def add(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
 # Whole decode layers, composed from the restatements above and the other oracles
 # (gdn_layer q35_step.py:149-183, attn_block 186-293, mlp_block 118-142)
 # ---------------------------------------------------------------------------------------------
-def _fp8(a: torch.Tensor, w: dict, name: str) -> torch.Tensor:
+def proj(a: torch.Tensor, w: dict, name: str, fmt: str = "fp8") -> torch.Tensor:
+    """bf16(a @ W_name^T) in fp32 for the weight w_<name> / s_<name> in format fmt: "fp8" (E4M3 with a per-channel
+    scale, gemm.py:119-181), "mxfp8" (E4M3 + E8M0 per 32, q35_mx_build.py:60-72) or "mxfp4" (q35_moe.py:46-63)."""
     from oracle import mx
 
-    return _bf(mx.fp8_linear(a, w["w_" + name].numpy(), None, w["s_" + name]))
+    wt, s = w["w_" + name], w["s_" + name]
+    if fmt == "fp8":
+        y = mx.fp8_linear(a, wt.numpy(), None, s)
+    elif fmt == "mxfp8":
+        y = mx.mxfp8_linear(a, wt.numpy(), s.numpy(), "e4m3")
+    else:
+        y = mx.mx_linear(a, wt.numpy(), s.numpy())
+    return _bf(y)
 
 
-def mlp_residual(x: torch.Tensor, y: torch.Tensor, w: dict, eps: float) -> torch.Tensor:
+def mlp_residual(x: torch.Tensor, y: torch.Tensor, w: dict, eps: float, fmt: str = "mxfp4") -> torch.Tensor:
     """x1 = bf16(x + y); out = bf16(x1 + down(bf16(silu(gate h2) * up h2))), h2 = rmsnorm(x1, ln2)."""
-    from oracle import mx
-
     x1, h2 = add_rmsnorm(x, y, w["ln2"], eps)
-    g = _bf(mx.mx_linear(h2, w["gate_w"].numpy(), w["gate_s"].numpy()))
-    u = _bf(mx.mx_linear(h2, w["up_w"].numpy(), w["up_s"].numpy()))
-    d = _bf(mx.mx_linear(silu_mul(g, u), w["down_w"].numpy(), w["down_s"].numpy()))
+    g = proj(h2, w, "gate", fmt)
+    u = proj(h2, w, "up", fmt)
+    d = proj(silu_mul(g, u), w, "down", fmt)
     return add(x1, d)
 
 
-def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6):
+def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
     """One token per sequence. Returns (out bf16 [B, H], state_out f32, conv_out bf16)."""
     from oracle import gdn
 
     b = x.shape[0]
     kd, vd = num_k_heads * 128, num_v_heads * 128
     h = rmsnorm(x, w["ln1"], eps)
-    qkv, z, bb, aa = (_fp8(h, w, n) for n in ("qkv", "z", "b", "a"))
+    qkv, z, bb, aa = (proj(h, w, n, proj_fmt) for n in ("qkv", "z", "b", "a"))
     mixed, conv_out = causal_conv1d_silu(qkv[:, None, :], w["conv_w"], conv_in)
     m = mixed[:, 0]
     q = m[:, :kd].reshape(b, 1, num_k_heads, 128)
@@ -125,11 +133,12 @@ def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_head
     core, state_out = gdn.gdn_fp32(q, k, v, aa[:, None], bb[:, None], w["a_log"], w["dt_bias"], state_in)
     core = _bf(core).reshape(b * num_v_heads, 128)
     gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(b * num_v_heads, 128), eps).reshape(b, vd)
-    return mlp_residual(x, _fp8(gated, w, "out"), w, eps), state_out, conv_out
+    return mlp_residual(x, proj(gated, w, "out", proj_fmt), w, eps, mlp_fmt), state_out, conv_out
 
 
 def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_len, cache_location,
-                      num_qo_heads: int, rot: int, eps: float = 1e-6, sm_scale=None):
+                      num_qo_heads: int, rot: int, eps: float = 1e-6, sm_scale=None, proj_fmt: str = "fp8",
+                      mlp_fmt: str = "mxfp4"):
     """One token per sequence over the paged cache (the page table includes the new token).
     Returns (out bf16 [B, H], the cache with the new K / V rows written)."""
     from oracle import paged_attn
@@ -138,12 +147,12 @@ def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
     hkv, d = cache.shape[3], cache.shape[4]
     scale = d ** -0.5 if sm_scale is None else sm_scale
     h = rmsnorm(x, w["ln1"], eps)
-    qg = _fp8(h, w, "q").reshape(b, num_qo_heads, 2 * d)
-    kk = _fp8(h, w, "k").reshape(b, hkv, d)
-    vv = _fp8(h, w, "v").reshape(b, hkv, d)
+    qg = proj(h, w, "q", proj_fmt).reshape(b, num_qo_heads, 2 * d)
+    kk = proj(h, w, "k", proj_fmt).reshape(b, hkv, d)
+    vv = proj(h, w, "v", proj_fmt).reshape(b, hkv, d)
     q = qk_norm_rope(qg[..., :d], w["q_norm"], cos, sin, rot, eps)
     k = qk_norm_rope(kk, w["k_norm"], cos, sin, rot, eps)
     cache2 = paged_attn.store_paged_kv(cache, k, vv, cache_location.numpy())
     attn = _bf(paged_attn.paged_decode(q, cache2, indptr, indices, last_page_len, scale))
     gated = sigmoid_mul(attn, qg[..., d:]).reshape(b, num_qo_heads * d)
-    return mlp_residual(x, _fp8(gated, w, "o"), w, eps), cache2
+    return mlp_residual(x, proj(gated, w, "o", proj_fmt), w, eps, mlp_fmt), cache2

@@ -100,8 +100,10 @@ def test_entry_points_reach_the_launch_on_a_gpu_less_host():
                                           0.1, None, p[100], ws, None) == launch
     gws = lib.axk_gdn_layer_workspace_size(1, 256, 1, 2, 128, 256)
     args = [p[10 + i] for i in range(28)]
-    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, p[150], gws, None) == launch
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], gws, None) == launch
     # a late contract error (misaligned w_out, argument 15) is found by the validate pass before any launch
     bad = list(args)
     bad[14] += 1
-    assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, p[150], gws, None) == 3
+    assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], gws, None) == 3
+    # an unknown weight format is refused before anything else
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 7, 2, p[150], gws, None) == 4

@@ -144,3 +144,40 @@ def test_layer_late_contract_error_enqueues_nothing(dev):
     assert e.value.status == 2  # AXK_E_SHAPE
     torch.cuda.synchronize()
     assert torch.equal(cache.cpu().view(torch.int16), c["cache"].view(torch.int16))
+
+
+# ---- the manifests' weight formats: MXFP8 layer weights (the 35B manifest, q35_mx_build.py:60-72) and MXFP4 layer
+# weights (the 9B / 27B manifests), for the projections and the MLP ----
+@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4"), ("mxfp8", "mxfp4")])
+def test_gdn_layer_decode_weight_formats(dev, proj_fmt, mlp_fmt):
+    b, nk, nv = 3, 2, 4
+    g = torch.Generator().manual_seed(31)
+    w = configs.gdn_layer_weights(g, H, F, nk, nv, proj_fmt=proj_fmt, mlp_fmt=mlp_fmt)
+    x = torch.randn(b, H, generator=g).bfloat16()
+    st = torch.randn(b, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(b, 3, 2 * nk * 128 + nv * 128, generator=g).bfloat16()
+    print(f"gdn layer proj={proj_fmt} mlp={mlp_fmt}", flush=True)
+    out, so, co = layer.gdn_layer_decode(x.to(dev), _dev(w, dev), st.to(dev), cv.to(dev), nk, nv, proj_fmt=proj_fmt,
+                                         mlp_fmt=mlp_fmt)
+    ro, rs, rc = olayer.gdn_layer_decode(x, w, st, cv, nk, nv, proj_fmt=proj_fmt, mlp_fmt=mlp_fmt)
+    torch.testing.assert_close(out.float().cpu(), ro.float(), **TOL)
+    torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
+    _check_conv(co, rc)
+
+
+@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4")])
+def test_attn_layer_decode_weight_formats(dev, proj_fmt, mlp_fmt):
+    lens, hq, hkv, rot, d = [100, 64, 300], 4, 2, 64, 256
+    g = torch.Generator().manual_seed(37)
+    w = configs.attn_layer_weights(g, H, F, hq, hkv, d, proj_fmt=proj_fmt, mlp_fmt=mlp_fmt)
+    c = configs.append_token_case(lens, hq, hkv, d, 64, g)
+    x = torch.randn(len(lens), H, generator=g).bfloat16()
+    cos, sin = olayer.rope_cos_sin(c["pos"], rot, 10_000_000.0)
+    cache = c["cache"].to(dev)
+    print(f"attn layer proj={proj_fmt} mlp={mlp_fmt}", flush=True)
+    out = layer.attn_layer_decode(x.to(dev), _dev(w, dev), cos.to(dev), sin.to(dev), cache, c["indptr"].to(dev),
+                                  c["indices"].to(dev), c["last_page_len"].to(dev), c["loc"].to(dev), hq, rot,
+                                  proj_fmt=proj_fmt, mlp_fmt=mlp_fmt)
+    ro, _ = olayer.attn_layer_decode(x, w, cos, sin, c["cache"], c["indptr"], c["indices"], c["last_page_len"],
+                                     c["loc"], hq, rot, proj_fmt=proj_fmt, mlp_fmt=mlp_fmt)
+    torch.testing.assert_close(out.float().cpu(), ro.float(), **FUSED_TOL)

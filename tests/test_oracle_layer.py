@@ -137,9 +137,9 @@ def _hf_layer(kind, w, hidden, inter, **kw):
     with torch.no_grad():
         m.input_layernorm.weight.copy_(w["ln1"] - 1)
         m.post_attention_layernorm.weight.copy_(w["ln2"] - 1)
-        m.mlp.gate_proj.weight.copy_(_deq_mx(w["gate_w"], w["gate_s"]))
-        m.mlp.up_proj.weight.copy_(_deq_mx(w["up_w"], w["up_s"]))
-        m.mlp.down_proj.weight.copy_(_deq_mx(w["down_w"], w["down_s"]))
+        m.mlp.gate_proj.weight.copy_(_deq_mx(w["w_gate"], w["s_gate"]))
+        m.mlp.up_proj.weight.copy_(_deq_mx(w["w_up"], w["s_up"]))
+        m.mlp.down_proj.weight.copy_(_deq_mx(w["w_down"], w["s_down"]))
         if kind == "linear_attention":
             la = m.linear_attn
             la.in_proj_qkv.weight.copy_(_deq_fp8(w["w_qkv"], w["s_qkv"]))
