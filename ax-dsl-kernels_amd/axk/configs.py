@@ -252,7 +252,9 @@ def config4_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None 
     """The group's weights, states, paged KV caches and page table, generated ON THE DEVICE by a seeded device
     generator (about 20 GB: the KV of 4 attention layers at 131,072 tokens per sequence). Distributions as the
     small-shape generators: FP8 projections N(0, 0.5) with scales U(1, 3) / sqrt(K), MXFP4 nibbles uniform with
-    exponent bytes 119..123, norms 1 + N(0, 0.1), KV ~ N(0, 1) bf16, GDN state ~ N(0, 0.02), x ~ N(0, 1).
+    exponent bytes 116..120 (weight RMS about 0.012, near 1 / sqrt(K), which keeps the MLP's outputs O(1) at
+    K = 4096 and 12288 as the FP8 scales do for the projections), norms 1 + N(0, 0.1), KV ~ N(0, 1) bf16, GDN state ~ N(0, 0.02),
+    x ~ N(0, 1).
     Every sequence holds ctx tokens; the step's new token is position ctx (a fresh page per sequence)."""
     c4 = dict(CONFIG4)
     if ctx is not None:
@@ -269,7 +271,7 @@ def config4_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None 
 
     def mx(n, k):
         codes = torch.randint(0, 256, (n, k // 2), generator=g, device=dev, dtype=torch.uint8)
-        scales = torch.randint(119, 124, (n, k // 32), generator=g, device=dev, dtype=torch.uint8)
+        scales = torch.randint(116, 121, (n, k // 32), generator=g, device=dev, dtype=torch.uint8)
         return codes, scales
 
     def norm(n):
