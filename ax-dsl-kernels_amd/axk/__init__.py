@@ -47,3 +47,8 @@ __all__ += ["glue"]
 from . import layer  # noqa: E402
 
 __all__ += ["layer"]
+
+from . import manifest  # noqa: E402
+from .manifest import Manifest, io_table  # noqa: E402
+
+__all__ += ["manifest", "Manifest", "io_table"]

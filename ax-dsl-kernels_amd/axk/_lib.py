@@ -56,6 +56,7 @@ _vp, _i64, _i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 SIGNATURES: dict[str, list] = {
     "axk_version": [],
     "axk_status_string": [_i32],
+    "axk_io_table": [ctypes.c_char_p, _vp, _i32, _vp, _i32, _vp],
     "axk_mxfp4_dequant": [_vp, _vp, _vp, _i64, _i64, _vp],
     "axk_mxfp4_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_fp8_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],

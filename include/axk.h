@@ -66,6 +66,47 @@ const char* axk_version(void);
 const char* axk_status_string(int status);
 
 /* ---------------------------------------------------------------------------------------------
+ * IO tables: the named IO of each role libaxk serves, as the AX engine reports a kernel's IO (AX_ENGINE_GetIOInfo's
+ * {pName, nSize, eDataType, pShape, nShapeSize}, dumped by tools/board/iojson.c:23-34 as [name, bytes, dtype, shape])
+ * and as manifest.json records it (tools/manifest/mkmanifest.py:183-199, 296-311). Names, dtype codes (AXK_DT_*, the
+ * board's codes of tools/manifest/onnx_io.py:18-29) and byte counts are the reference's, so a host can check its
+ * buffers name -> bytes the way models/qwen35_35b_a3b/sgl/scripts/check_adapter_abi.py:20-56 does.
+ * ------------------------------------------------------------------------------------------- */
+
+#define AXK_IO_NAME_MAX 48
+#define AXK_IO_RANK_MAX 6
+typedef struct {
+  char name[AXK_IO_NAME_MAX]; /* NUL-terminated */
+  int64_t bytes;              /* storage bytes (E2M1: two values per byte) */
+  int32_t dtype;              /* AXK_DT_* */
+  int32_t output;             /* 0: input, 1: output */
+  int32_t rank;
+  int64_t shape[AXK_IO_RANK_MAX]; /* logical elements (E2M1: values, as the board reports them) */
+} axk_io_entry;
+
+/* Fills entries[0 .. *count) with the IO of `role` at the dimensions dims[0 .. ndims), inputs first, in the
+ * reference's order; a dimension left out takes its default (in brackets). Roles and their dims:
+ *   "lm_head"     n, k [, m = 1]          mul_mat_mx4_n<n>_k<k>: x bf16 [m, k]; w E2M1 [n, k]; s E8M0 [n, k/32] ->
+ *                                         out f32 [m, n] (axk_mx_gemm with f32 output)
+ *   "layer.gdn"   hidden, num_k_heads, num_v_heads, inter [, conv_kernel = 4, proj_fmt = AXK_WFMT_MXFP4,
+ *                 mlp_fmt = AXK_WFMT_MXFP4, num_experts = 0, batch = 1]
+ *                 x, the layer's parameters in the manifest's order (params.gdn: ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b,
+ *                 w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out, s_out, ln2, w_gate .. s_down, and with num_experts
+ *                 the MoE layer's w_router, w_shg), state_in, conv_in -> out, state_out, conv_out (axk_gdn_layer_decode;
+ *                 the MoE half through axk_moe_decode)
+ *   "layer.attn"  hidden, num_qo_heads, num_kv_heads, head_dim, inter [, proj_fmt = AXK_WFMT_MXFP4,
+ *                 mlp_fmt = AXK_WFMT_MXFP4, num_experts = 0, batch = 1, rot = 64, page_size = 256, num_pages = 1]
+ *                 x, the parameters (params.attn: ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, w_o, s_o, ln2,
+ *                 the MLP, and with num_experts w_router, w_shg), cos, sin, the paged cache and page table -> out,
+ *                 kv_cache (in place) (axk_attn_layer_decode)
+ *   "experts"     num_experts, hidden, inter   e_gw, e_gs, e_dw, e_ds (params.experts; axk_moe_experts)
+ * Weight w_<x> / s_<x> by format: FP8_CHANNEL E4M3 [N, K] + f32 [N]; MXFP8 E4M3 [N, K] + E8M0 [N, K/32]; MXFP4
+ * E2M1 [N, K] + E8M0 [N, K/32]. Returns AXK_E_ROLE for an unknown role, AXK_E_SHAPE for missing or invalid dims,
+ * AXK_E_BUFFER when more than `capacity` entries are needed (*count is then the number needed). Host only: makes no
+ * HIP call. */
+int axk_io_table(const char* role, const int64_t* dims, int ndims, axk_io_entry* entries, int capacity, int* count);
+
+/* ---------------------------------------------------------------------------------------------
  * MXFP4 codec and MX / FP8 runtime-weight linear
  * ------------------------------------------------------------------------------------------- */
 
