@@ -154,7 +154,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   qs = group_sum<4>(qs);
   ks = group_sum<4>(ks);
   {
-    const float qn = sqrtf(qs + 1e-6f), kn = sqrtf(ks + 1e-6f);
+    // one reciprocal per row instead of a division per element (x * (1 / n) is within an fp32 ulp of x / n)
+    const float rq = 1.0f / sqrtf(qs + 1e-6f), rk = 1.0f / sqrtf(ks + 1e-6f);
     const float qscale = 0.08838834764831845f;  // 128^-0.5
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -166,8 +167,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // q: bf16(bf16(q / |q|) * DK^-0.5) (l2norm_lastdim, then the q scale; gdn.py:1631)
-        qop[j] = pack_bf16x2(round_bf16(bf16_lo(qw[j]) / qn) * qscale, round_bf16(bf16_hi(qw[j]) / qn) * qscale);
-        kop[j] = pack_bf16x2(bf16_lo(kw[j]) / kn, bf16_hi(kw[j]) / kn);
+        qop[j] = pack_bf16x2(round_bf16(bf16_lo(qw[j]) * rq) * qscale, round_bf16(bf16_hi(qw[j]) * rq) * qscale);
+        kop[j] = pack_bf16x2(bf16_lo(kw[j]) * rk, bf16_hi(kw[j]) * rk);
       }
       *reinterpret_cast<uint4*>(sQ + tt * kLdK + 32 * qd + 8 * i) = qo;
       *reinterpret_cast<uint4*>(sK + tt * kLdK + 32 * qd + 8 * i) = ko;
@@ -236,13 +237,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * wave + 4 * g4 + r, j = 16 * jt + l16;
-      const float dij = i >= j ? expf(sG[i] - sG[j]) : 0.f;
+      const float dij = i >= j ? __expf(sG[i] - sG[j]) : 0.f;  // hardware exp2: ~1e-6 relative, far below bf16
       sL[i * kLdL + j] = i > j ? kk[jt][r] * sBeta[i] * dij : 0.f;
       sP[i * kLdT + j] = i >= j ? (uint16_t)f32_to_bf16_bits(qk[jt][r] * dij) : (uint16_t)0;
     }
   if (tid < kC) {
-    p.ws.gam[vidx * kC + tid] = expf(sG[tid]);
-    p.ws.dec[vidx * kC + tid] = expf(sG[kC - 1] - sG[tid]);  // padded tokens keep G: row of the last valid token
+    p.ws.gam[vidx * kC + tid] = __expf(sG[tid]);
+    p.ws.dec[vidx * kC + tid] = __expf(sG[kC - 1] - sG[tid]);  // padded tokens keep G: row of the last valid token
   }
   __syncthreads();
   {
@@ -337,7 +338,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   uint16_t* sVB = sQ;
   uint16_t* sKB = reinterpret_cast<uint16_t*>(sT);
   {
-    const float beta = sBeta[tt], gm = expf(sG[tt]);
+    const float beta = sBeta[tt], gm = __expf(sG[tt]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int d0 = 32 * qd + 8 * i;
