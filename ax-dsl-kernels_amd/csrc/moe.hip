@@ -66,7 +66,8 @@ struct MoeWs {
   float* row_w;     // [P] routing weight of sorted row
   uint16_t* act;    // [P, F] bf16 routed activations (sorted rows)
   uint16_t* act_sh; // [T, Fs] bf16 shared-expert activations
-  float* y;         // [P, H] fp32 routed outputs x routing weight, row t * K + k for pair (t, k)
+  float* y;         // [P, H] routed outputs x routing weight, row t * K + k for pair (t, k): fp32 (decode) or
+                    // bf16 (prefill: the first P H bf16 of the buffer)
   float* y_sh;      // [T, H] fp32 shared-expert output
   int* blk;         // [NB, E] prefill: per-block expert counts, then per-block row bases
   int4* tiles;      // [max tiles] prefill GEMM tiles: {expert (-1: shared), first row, rows, 0}
@@ -839,6 +840,8 @@ struct CombineArgs {
 // rounding. The first pass's loads are unconditional (clamped) and issued before the shared-gate dot
 // (h2 . w_shg, reduced across the workgroup), so both share one memory round trip. Few tokens: one block per
 // 1024 columns; many tokens: one block per token (the gate is then computed once per token).
+// YB: the routed rows are bf16 (the prefill path's slot outputs), else fp32.
+template <bool YB>
 __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   __shared__ float s_part[4];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -853,7 +856,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
     }
     if (a.has_shared) ys = *reinterpret_cast<const float4*>(a.w.y_sh + row + i);
     for (int k = 0; k < a.K; ++k) {
-      const float4 yv = *reinterpret_cast<const float4*>(a.w.y + (pair0 + k) * a.H + i);
+      float4 yv;
+      if constexpr (YB) {
+        const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.w.y) + (pair0 + k) * a.H + i);
+        yv = make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u), __uint_as_float(b.y << 16),
+                         __uint_as_float(b.y & 0xffff0000u));
+      } else {
+        yv = *reinterpret_cast<const float4*>(a.w.y + (pair0 + k) * a.H + i);
+      }
       if (a.w.pair_pos[pair0 + k] < 0) continue;  // uniform: an id outside [0, E)
       acc.x += yv.x; acc.y += yv.y; acc.z += yv.z; acc.w += yv.w;
     }
@@ -1267,10 +1277,12 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
         for (int j = 0; j < 4; ++j) {
           const int col = col0 + 64 * wave + 16 * j + l16;
           if (col >= No) continue;
+          // a routed slot is stored as bf16(rw * y), as the reference's delivered slot kernels store it
+          // (qwen35moe_slots*_bo: SLOT_OUT=bf16, q35_moe_prefill.py:41, 100, 165) and its combine reads it
           if (shared)
             g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
           else
-            g.ws.y[ypair * g.H + col] = acc[mt][j][r] * rw;
+            reinterpret_cast<uint16_t*>(g.ws.y)[ypair * g.H + col] = (uint16_t)f32_to_bf16_bits(acc[mt][j][r] * rw);
         }
       }
     }
@@ -1371,8 +1383,8 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
     hipLaunchKernelGGL(moe_ggemm3_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
-                       0, st, ca);
+    hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
+                       dim3(256), 0, st, ca);
     return axk_launch_status();
   }
   hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
@@ -1423,8 +1435,8 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   else
     hipLaunchKernelGGL((moe_down_kernel<false, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)), dim3(256),
-                       0, st, ca);
+  hipLaunchKernelGGL(moe_combine_kernel<false>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
+                     dim3(256), 0, st, ca);
   return axk_launch_status();
 }
 

@@ -64,13 +64,17 @@ def ulp_bf16(x: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(x.abs().clamp_min(1e-30))) - 7)
 
 
-def moe_parts(h2, weights, ids, wts, x_res=None, flips: int = 2):
+def moe_parts(h2, weights, ids, wts, x_res=None, flips: int = 2, slot_bf16: bool = False):
     """(base, routed, slack), all fp32 [T, H]: base = x1 + gate * shared expert, routed = sum_k rw_k y_k, and
     a bound on how far `flips` one-ulp changes of the bf16 activations of each (token, expert) row can move the
     output. g, u and act are rounded to bf16 at the reference's points, but a value that lies within the fp32
     accumulation error of a rounding midpoint goes either way depending on the summation order, so two correct
     implementations may hold neighbouring bf16 values there; the slack charges every row `flips` times its
-    largest activation ulp against the largest |Wd| of each output column."""
+    largest activation ulp against the largest |Wd| of each output column.
+    slot_bf16: each routed slot is bf16(rw_k y_k) before the fp32 sum, as the reference's delivered prefill slot
+    kernels store it (qwen35moe_slots*_bo, SLOT_OUT=bf16: q35_moe_prefill.py:41, 100, 165; the combine's bf16 sout,
+    moe_combine 196-213); the slack then also takes one ulp of each slot (its rounding, like the activations', can
+    go either way between two summation orders)."""
     w = weights
     t, hidden = h2.shape
     base = x_res.float() if x_res is not None else torch.zeros(t, hidden)
@@ -91,20 +95,24 @@ def moe_parts(h2, weights, ids, wts, x_res=None, flips: int = 2):
         wd = _deq(e_dw[e], e_ds[e])
         rw = wts[rows, slots][:, None]
         r = torch.from_numpy(rows)
-        routed.index_add_(0, r, (act @ wd.T) * rw)
+        y = (act @ wd.T) * rw
+        if slot_bf16:
+            y = _bf(y).float()
+            slack.index_add_(0, r, ulp_bf16(y))
+        routed.index_add_(0, r, y)
         slack.index_add_(0, r, flips * rw * ulp_bf16(act).amax(dim=1)[:, None] * wd.abs().amax(dim=1)[None, :])
     return base, routed, slack
 
 
-def moe_layer(h2, weights, top_k=8, x_res=None, norm=True, ids=None, wts=None, round_base=True):
+def moe_layer(h2, weights, top_k=8, x_res=None, norm=True, ids=None, wts=None, round_base=True, slot_bf16=False):
     """Returns (out bf16 [T, H], logits f32 [T, E], ids i32 [T, K], weights f32 [T, K]).
     round_base: round base = x1 + gate * sh to bf16 before the expert sum, as the reference's layer kernel
-    stores it (q35_layer_mc.py:845-846); False keeps it fp32 (a single final rounding)."""
+    stores it (q35_layer_mc.py:845-846); False keeps it fp32 (a single final rounding). slot_bf16: as moe_parts."""
     w = weights
     logits = h2.float() @ w["w_router"].float().T
     if ids is None:
         ids, wts = route(logits, top_k, norm)
-    base, routed, _ = moe_parts(h2, w, ids, wts, x_res)
+    base, routed, _ = moe_parts(h2, w, ids, wts, x_res, slot_bf16=slot_bf16)
     if round_base:
         base = _bf(base).float()
     return _bf(base + routed), logits, ids, wts

@@ -1,7 +1,9 @@
 """GPU parity of the MoE layer (router, top-K, shared + routed MXFP4 SwiGLU experts) against the oracle.
 
 Bar: top-K ids bit-exact against a stable descending sort of the kernel's own logits; routing weights and
-logits at fp32 tolerance; bf16 outputs within rel 2e-2 / abs 1e-2 of the oracle on the same routing.
+logits at fp32 tolerance; bf16 outputs within rel 2e-2 / abs 1e-2 of the oracle on the same routing. The prefill
+path (tokens > 256) is checked against the reference's delivered prefill schedule, each routed slot rounded to
+bf16 before the slot-order sum (q35_moe_prefill.py:41, 100, 165, 196-213); decode against fp32 slots.
 """
 import pytest
 import torch
@@ -27,7 +29,8 @@ def _check_layer(c, dev, norm=True):
     sids, swts = omoe.route(logits, k, norm)  # the host rule on the kernel's own logits
     assert torch.equal(ids, sids), "top-K ids differ from the stable sort of the kernel's logits"
     torch.testing.assert_close(wts, swts, rtol=1e-5, atol=1e-6)
-    base, routed, slack = omoe.moe_parts(h2, w, ids, wts, x)
+    prefill = h2.shape[0] > 256
+    base, routed, slack = omoe.moe_parts(h2, w, ids, wts, x, slot_bf16=prefill)
     ref = (base + routed).to(torch.bfloat16).float()  # base kept fp32, one final rounding (the kernel's schedule)
     tol = TOL["atol"] + TOL["rtol"] * ref.abs()
     d = (out.float() - ref).abs()
@@ -35,7 +38,10 @@ def _check_layer(c, dev, norm=True):
     # at the reference's points; which way a value at a rounding midpoint goes depends on the fp32 summation
     # order) moves an output that cancels to near zero: such elements are rare and stay inside the derived slack.
     assert (d <= tol + slack).all(), f"max excess {(d - tol - slack).max().item()}"
-    assert (d > tol).float().mean().item() <= 1e-5, f"{int((d > tol).sum())} elements outside the plain tolerance"
+    # The prefill schedule rounds each of the K routed slots to bf16 as well: K more order-dependent roundings per
+    # element, so more of the (rare, slack-bounded) flips reach the plain bar (config 3b: about 1.6e-5 of elements)
+    frac = 5e-5 if prefill else 1e-5
+    assert (d > tol).float().mean().item() <= frac, f"{int((d > tol).sum())} elements outside the plain tolerance"
     # the reference's rounding schedule (base rounded to bf16 first) differs by at most one ulp of |base| more
     sched = (base.to(torch.bfloat16).float() + routed).to(torch.bfloat16).float()
     assert ((out.float() - sched).abs() <= omoe.ulp_bf16(base) + tol + slack).all()
@@ -148,5 +154,5 @@ def test_moe_prefill_out_of_range_ids(dev):
         other = int(ids[r, 1 - c_])
         ids_ref[r, c_] = (other + 1) % 8
         wts_ref[r, c_] = 0.0
-    ref, *_ = omoe.moe_layer(h2, w, 2, ids=ids_ref, wts=wts_ref, round_base=False)
+    ref, *_ = omoe.moe_layer(h2, w, 2, ids=ids_ref, wts=wts_ref, round_base=False, slot_bf16=True)
     torch.testing.assert_close(out.float(), ref.float(), **TOL)

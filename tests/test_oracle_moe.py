@@ -92,6 +92,38 @@ def test_flip_slack_bounds_flipped_activations():
     assert (diff <= slack + 1e-5).all()
 
 
+def test_bf16_slots_schedule():
+    """The prefill schedule (each routed slot bf16(rw y) before the fp32 sum): with every slot exactly
+    representable in bf16 (dyadic routing weights on an expert whose outputs are bf16 values) it equals the fp32
+    schedule; in general each slot moves by at most half a bf16 ulp of itself, and the reported slack covers that
+    rounding on top of the activation flips."""
+    h2, x, w, k = _small(seed=11, t=12, h=64, e=4, f=32, fs=32, k=2)
+    _, _, ids, wts = moe.moe_layer(h2, w, k, x_res=x)
+    base, r32, s32 = moe.moe_parts(h2, w, ids, wts, x)
+    _, r16, s16 = moe.moe_parts(h2, w, ids, wts, x, slot_bf16=True)
+    assert not torch.equal(r16, r32)
+    # bound: |sum bf16(y_k) - sum y_k| <= sum_k ulp(y_k) / 2 <= the added slack
+    assert ((r16 - r32).abs() <= (s16 - s32) / 2 + 1e-6).all()
+    assert (s16 >= s32).all()
+    # exactness: an expert whose down weight has one 1.0 per row (so each output is one bf16 activation) and dyadic
+    # routing weights make every slot exact in bf16: both schedules agree bit for bit
+    ids2 = torch.tensor([[1, 2]], dtype=torch.int32).repeat(h2.shape[0], 1)
+    wts2 = torch.tensor([[0.5, 0.25]]).repeat(h2.shape[0], 1)
+    w2 = dict(w)
+    dw, ds = w["e_dw"].clone(), w["e_ds"].clone()
+    hid, f2 = dw.shape[1], dw.shape[2] * 2
+    for e in (1, 2):
+        dw[e] = 0
+        ds[e] = 127
+        for r in range(hid):
+            col = (3 * r + e) % f2
+            dw[e, r, col // 2] = 2 if col % 2 == 0 else 2 << 4  # E2M1 code 2 = 1.0
+    w2["e_dw"], w2["e_ds"] = dw, ds
+    _, b32, _ = moe.moe_parts(h2, w2, ids2, wts2, x)
+    _, b16, _ = moe.moe_parts(h2, w2, ids2, wts2, x, slot_bf16=True)
+    assert torch.equal(b32, b16) and b32.abs().max() > 0
+
+
 def _hf_moe_block(w, top_k):
     """transformers' Qwen3_5MoeSparseMoeBlock (fp32, eager experts) holding the exactly dequantised weights."""
     from transformers.models.qwen3_5_moe.configuration_qwen3_5_moe import Qwen3_5MoeTextConfig
