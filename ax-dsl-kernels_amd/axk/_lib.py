@@ -96,6 +96,11 @@ SIGNATURES: dict[str, list] = {
     "axk_gdn_layer_workspace_size": [_i64] * 6,
     "axk_gdn_layer_decode": [_vp] * 28 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
     "axk_attn_layer_workspace_size": [_i64] * 6,
+    "axk_gdn_layer_verify_workspace_size": [_i64] * 7,
+    "axk_attn_layer_verify_workspace_size": [_i64] * 7,
+    "axk_gdn_layer_verify": [_vp] * 30 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_attn_layer_verify": [_vp] * 27 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
+                              ctypes.c_size_t, _vp],
     "axk_attn_layer_decode": [_vp] * 27 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                               ctypes.c_size_t, _vp],
 }
@@ -107,6 +112,8 @@ _RESTYPES = {
     "axk_gdn_chunk_workspace_size": ctypes.c_size_t,
     "axk_gdn_layer_workspace_size": ctypes.c_size_t,
     "axk_attn_layer_workspace_size": ctypes.c_size_t,
+    "axk_gdn_layer_verify_workspace_size": ctypes.c_size_t,
+    "axk_attn_layer_verify_workspace_size": ctypes.c_size_t,
 }
 
 

@@ -243,6 +243,34 @@ def append_token_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Gener
     return c
 
 
+def verify_rows_case(lens, rows: int, hq: int, hkv: int, d: int, page: int, g: torch.Generator):
+    """A paged cache holding sequences of `lens` tokens plus room for `rows` more each (a speculative draft): the page
+    table already covers the new rows (lens + rows tokens), cache locations int32 [B, rows, 2] and positions
+    [B, rows] of the new rows."""
+    c = paged_case(lens, hq, hkv, d, page, g, extra_pages=len(lens) * ((rows + page - 1) // page + 1))
+    used = set(c["indices"].tolist())
+    spare = [p for p in range(c["cache"].shape[0]) if p not in used]
+    loc, new_last, new_indices, new_indptr, pos = [], [], [], [0], []
+    for b, L in enumerate(lens):
+        pages = c["indices"][int(c["indptr"][b]):int(c["indptr"][b + 1])].tolist()
+        rl = []
+        for r in range(rows):
+            tok = L + r
+            if tok // page >= len(pages):
+                pages.append(spare.pop())
+            rl.append([pages[tok // page], tok % page])
+        loc.append(rl)
+        pos.append([L + r for r in range(rows)])
+        new_indices += pages
+        new_indptr.append(len(new_indices))
+        n = L + rows
+        new_last.append(n - (len(pages) - 1) * page)
+    c.update(indices=torch.tensor(new_indices, dtype=torch.int32), indptr=torch.tensor(new_indptr, dtype=torch.int32),
+             last_page_len=torch.tensor(new_last, dtype=torch.int32), lens=[L + rows for L in lens],
+             loc=torch.tensor(loc, dtype=torch.int32), pos=torch.tensor(pos))
+    return c
+
+
 # Config 4: the 16-layer hybrid decode group (GDN, GDN, GDN, attention) x 4 of BASELINE.json configs[4].
 CONFIG4 = dict(batch=8, ctx=131072, hidden=4096, inter=12288, hq=32, hkv=4, d=256, rot=64, nk=16, nv=32, conv=4,
                page=64, theta=10_000_000.0, eps=1e-6, pattern="gggagggagggaggga")

@@ -45,7 +45,8 @@ struct AxkValidateScope {
 
 // Internal (not exported): the GDN recurrence with row strides, in elements between consecutive (sequence, token)
 // rows, for q, k, v and a / b. axk_gdn_recurrent passes the contiguous strides; the decode layer reads q / k / v
-// straight out of the conv output. Returns an AXK status.
+// straight out of the conv output. state_snap (optional): the fp32 state after token t, [batch, NV, DK, DV] at
+// state_snap + t * snap_ld elements. Returns an AXK status.
 // With gate (optional), out is the GDN output norm of each head's row: bf16(bf16(rmsnorm(o) * norm_w) * silu(z)),
 // z [batch, tokens, num_v_heads, 128] contiguous.
 struct AxkGdnStrides {
@@ -59,7 +60,21 @@ struct AxkGdnGate {
 __attribute__((visibility("hidden"))) int axk_gdn_recurrent_strided(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
     const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
-    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, hipStream_t stream);
+    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, hipStream_t stream,
+    float* state_snap = nullptr, int64_t snap_ld = 0);
+
+// Internal (not exported): the conv state after each of a sequence's `tokens` new rows (speculative verification's
+// per-row snapshots): snapshot t holds the last kernel - 1 inputs of [state_in | x rows 0 .. t] (oldest first), written
+// at snap + t * snap_ld elements as [batch, kernel - 1, channels]. x bf16 [batch, tokens, channels] (the raw
+// projection rows the conv consumes), state_in bf16 [batch, kernel - 1, channels]. Returns an AXK status.
+__attribute__((visibility("hidden"))) int axk_conv_snapshots(const uint16_t* x, const uint16_t* state_in,
+                                                             uint16_t* snap, int64_t snap_ld, int64_t batch,
+                                                             int64_t tokens, int64_t channels, int64_t kernel,
+                                                             hipStream_t stream);
+
+// Internal (not exported): out[i] = i * step for i = 0 .. n (n + 1 values), int32 (a uniform row index, e.g. the
+// qo_indptr of `step` query rows per sequence). Returns an AXK status.
+__attribute__((visibility("hidden"))) int axk_fill_iota_i32(int32_t* out, int64_t n, int64_t step, hipStream_t stream);
 
 // Internal (not exported): one launch of up to AXK_MX_GROUP_MAX weight matrices that share the activations a
 // [m, k] (the projections of one decode layer). Matrix i: weights w [n, k] (FP8 bytes with a per-channel scale, or

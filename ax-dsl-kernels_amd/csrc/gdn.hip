@@ -41,6 +41,8 @@ struct GdnArgs {
   const float* norm_w;          // GATE: the output norm's weight [DV] and gate z [B, T, NV, DV]
   const uint16_t* z;
   float eps;
+  float* snap;                  // optional: the state after token t at snap + t * snap_ld, [B, NV, DK, DV] each
+  int64_t snap_ld;
 };
 
 template <bool GATE>
@@ -158,6 +160,13 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
         p.out[vh * kDV + tid] = (uint16_t)f32_to_bf16_bits(round_bf16(core * inv * p.norm_w[tid]) * silu_f32(zz));
       }
     }
+    if (p.snap) {  // the state after this token (speculative verification's per-row snapshots)
+      float* sn = p.snap + t * p.snap_ld + ((int64_t)b * p.NV + h) * kDK * kDV;
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+        store_nt(sn + (r0 + r) * kDV + c0, axk_u32x4{__float_as_uint(S[r].x), __float_as_uint(S[r].y),
+                                                     __float_as_uint(S[r].z), __float_as_uint(S[r].w)});
+    }
     __syncthreads();  // s_k / s_q / s_red / s_gn reuse by the next token
   }
 
@@ -173,7 +182,7 @@ int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16
                               const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
                               float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
                               int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate,
-                              hipStream_t stream) {
+                              hipStream_t stream, float* state_snap, int64_t snap_ld) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
   AXK_REQUIRE(!gate || (gate->norm_w && gate->z), AXK_E_NULL);
   AXK_REQUIRE(batch > 0 && tokens > 0 && num_k_heads > 0 && num_v_heads > 0, AXK_E_SHAPE);
@@ -188,9 +197,17 @@ int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16
   AXK_REQUIRE(state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
   const size_t obytes = (size_t)batch * tokens * num_v_heads * kDV * 2;
   AXK_REQUIRE(!axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
+  if (state_snap) {  // snapshot t: [B, NV, DK, DV] at state_snap + t * snap_ld, none overlapping the states
+    const int64_t per = batch * num_v_heads * kDK * kDV;
+    AXK_REQUIRE(snap_ld >= per && axk_aligned(state_snap, 16) && snap_ld % 4 == 0, AXK_E_SHAPE);
+    const size_t nbytes = (size_t)((tokens - 1) * snap_ld + per) * 4;
+    AXK_REQUIRE(!axk_overlap(state_snap, nbytes, state_in, sbytes) && !axk_overlap(state_snap, nbytes, state_out, sbytes) &&
+                    !axk_overlap(state_snap, nbytes, out, obytes),
+                AXK_E_ALIAS);
+  }
   GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
             (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab, gate ? gate->norm_w : nullptr, gate ? gate->z : nullptr,
-            gate ? gate->eps : 0.f};
+            gate ? gate->eps : 0.f, state_snap, snap_ld};
   AXK_LAUNCH_GATE();
   if (gate)
     hipLaunchKernelGGL(gdn_recurrent_kernel<true>, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);

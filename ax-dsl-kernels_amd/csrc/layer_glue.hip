@@ -351,8 +351,60 @@ extern "C" int axk_causal_conv1d_silu(const uint16_t* x, const uint16_t* w, cons
   AXK_REQUIRE(kernel == 1 || state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
   AXK_REQUIRE(kernel == 1 || !axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
   const int64_t n = batch * channels;
+  AXK_LAUNCH_GATE();
   hipLaunchKernelGGL(conv1d_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, axk_stream(stream), x, w,
                      state_in, state_out, out, (int)batch, (int)tokens, (int)channels, (int)kernel);
+  return axk_launch_status();
+}
+
+namespace {
+// Thread = (snapshot t, sequence b, row i, 8 channels).
+__global__ __launch_bounds__(256) void conv_snapshots_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ state_in,
+                                                             uint16_t* __restrict__ snap, int64_t snap_ld, int B, int T,
+                                                             int C, int K) {
+  const int c8 = C / 8;
+  const int64_t n = (int64_t)T * B * (K - 1) * c8;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int cc = (int)(e % c8);
+    int64_t r = e / c8;
+    const int i = (int)(r % (K - 1));
+    r /= K - 1;
+    const int b = (int)(r % B), t = (int)(r / B);
+    const int src = t + 1 + i;  // row of [state_in (K - 1 rows) | x rows]
+    const uint16_t* from = src < K - 1 ? state_in + ((int64_t)b * (K - 1) + src) * C
+                                       : x + ((int64_t)b * T + (src - (K - 1))) * C;
+    *reinterpret_cast<uint4*>(snap + t * snap_ld + ((int64_t)b * (K - 1) + i) * C + 8 * cc) =
+        *reinterpret_cast<const uint4*>(from + 8 * cc);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_iota_kernel(int32_t* out, int n, int step) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i <= n) out[i] = i * step;
+}
+}  // namespace
+
+int axk_conv_snapshots(const uint16_t* x, const uint16_t* state_in, uint16_t* snap, int64_t snap_ld, int64_t batch,
+                       int64_t tokens, int64_t channels, int64_t kernel, hipStream_t stream) {
+  AXK_REQUIRE(x && state_in && snap, AXK_E_NULL);
+  AXK_REQUIRE(batch > 0 && tokens > 0 && kernel >= 2 && kernel <= kMaxConvKernel && channels % 8 == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(snap_ld >= batch * (kernel - 1) * channels && snap_ld % 8 == 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(x, 16) && axk_aligned(state_in, 16) && axk_aligned(snap, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(batch * tokens <= INT32_MAX, AXK_E_SHAPE);
+  const int64_t n = tokens * batch * (kernel - 1) * (channels / 8);
+  const int64_t grid = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+  AXK_LAUNCH_GATE();
+  hipLaunchKernelGGL(conv_snapshots_kernel, dim3((unsigned)grid), dim3(256), 0, stream, x, state_in, snap, snap_ld,
+                     (int)batch, (int)tokens, (int)channels, (int)kernel);
+  return axk_launch_status();
+}
+
+int axk_fill_iota_i32(int32_t* out, int64_t n, int64_t step, hipStream_t stream) {
+  AXK_REQUIRE(out, AXK_E_NULL);
+  AXK_REQUIRE(n >= 0 && n < INT32_MAX && step >= 0 && n * step <= INT32_MAX, AXK_E_SHAPE);
+  AXK_LAUNCH_GATE();
+  hipLaunchKernelGGL(fill_iota_kernel, dim3((unsigned)(n / 256 + 1)), dim3(256), 0, stream, out, (int)n, (int)step);
   return axk_launch_status();
 }
 
@@ -368,6 +420,7 @@ extern "C" int axk_qk_norm_rope(const uint16_t* x, int64_t ldx, const float* w, 
   const size_t obytes = (size_t)rows * head_dim * 2;
   AXK_REQUIRE(!axk_overlap(out, obytes, x, (size_t)((rows - 1) * ldx + head_dim) * 2), AXK_E_ALIAS);
   hipStream_t st = axk_stream(stream);
+  AXK_LAUNCH_GATE();
 #define AXK_QKR(E)                                                                                                 \
   hipLaunchKernelGGL(qk_norm_rope_kernel<E>, dim3(row_grid(rows)), dim3(64 * kRowsPerWg), 0, st, x, ldx, w, cos, sin, \
                      out, rows, (int)heads, (int)rot, eps)

@@ -1531,6 +1531,7 @@ int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, c
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
+  AXK_LAUNCH_GATE();
   hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid), dim3(64 * kPfWaves), lds, st, q,
                      static_cast<const unsigned char*>(cache), qo_indptr, indptr, last, indices, batch, total_q, hq,
                      hkv, page_size, num_pages, sm_scale, xph, status, out);
@@ -1866,6 +1867,7 @@ extern "C" int axk_paged_attention_decode(const uint16_t* q, const uint16_t* k, 
   hipStream_t st = axk_stream(stream);
   const int64_t chunks = 2 * batch * num_kv_heads * head_dim / 8;
   const int64_t grid = chunks / 256 + 1 < 4096 ? chunks / 256 + 1 : 4096;
+  AXK_LAUNCH_GATE();
   hipLaunchKernelGGL(paged_kv_write_kernel, dim3((unsigned)grid), dim3(256), 0, st, k, v, kv_cache, cache_location,
                      (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, status);
   if ((rc = axk_launch_status()) != AXK_OK) return rc;
@@ -1885,6 +1887,7 @@ extern "C" int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t
   const int64_t chunks = 2 * batch * num_kv_heads * head_dim / 8;
   int64_t grid = (chunks + 255) / 256;
   if (grid > 4096) grid = 4096;
+  AXK_LAUNCH_GATE();
   hipLaunchKernelGGL(paged_kv_write_kernel, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v, kv_cache,
                      cache_location, (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, status);
   return axk_launch_status();

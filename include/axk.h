@@ -500,6 +500,53 @@ int axk_attn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_
                           int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
                           int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Speculative verification: the decode layers over `tokens` (1 .. 16) consecutive new rows per sequence in one call,
+ * the decode.verify role of models/qwen38_27b/README.md:11 (verify/verify_group_m4.py:1-9: a draft of up to 3 tokens
+ * after the last cell checked in one pass; every projection shared by the rows, so each weight is read once; the row
+ * recurrences in order). Row t of sequence b is row b * tokens + t of x / out bf16 [batch * tokens, hidden]. The
+ * result equals `tokens` successive decode-layer calls, one row each. Arguments otherwise as the decode layers.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes of axk_gdn_layer_verify / axk_attn_layer_verify (0 = unsupported shape; batch * tokens <= 4096). */
+size_t axk_gdn_layer_verify_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                                           int64_t num_v_heads, int64_t head_dim, int64_t inter);
+size_t axk_attn_layer_verify_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_qo_heads,
+                                            int64_t num_kv_heads, int64_t head_dim, int64_t inter);
+
+/* The GDN layer over the rows of each sequence in order (verify_group_m4.py gdn_rows 147-243). state_out / conv_out:
+ * after the last row (may be the inputs: in place). Per-row snapshots (each optional, NULL = none), the verify
+ * group's ssnap / cqsnap / cksnap / cvsnap: state_snap f32 [tokens, batch, NV, 128, 128] = the state after row t,
+ * conv_snap bf16 [tokens, batch, conv_kernel - 1, 2 KD + VD] = the conv state after row t (oldest first; the q / k / v
+ * channel ranges of the reference's three conv states). conv_kernel >= 2. */
+int axk_gdn_layer_verify(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
+                         const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b, const uint8_t* w_a,
+                         const void* s_a, const uint16_t* conv_w, const float* a_log, const float* dt_bias,
+                         const float* norm_w, const uint8_t* w_out, const void* s_out, const float* ln2,
+                         const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+                         const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s,
+                         const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out,
+                         uint16_t* conv_out, float* state_snap, uint16_t* conv_snap, int64_t batch, int64_t tokens,
+                         int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
+                         int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, void* workspace,
+                         size_t workspace_bytes, axk_stream_t stream);
+
+/* The attention layer over the rows (verify_group_m4.py attn_rows 226-300): every row's K / V is written at its
+ * cache_location (i32 [batch * tokens, 2]), then row t attends its sequence's history and rows 0 .. t (the page table
+ * covers all the new rows; they are the sequence's last `tokens` tokens). cos, sin bf16 [batch * tokens, rot / 2]:
+ * each row's position. page_size a multiple of 16; head_dim 64, 128 or 256. */
+int axk_attn_layer_verify(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k,
+                          const void* s_k, const uint8_t* w_v, const void* s_v, const float* q_norm,
+                          const float* k_norm, const uint16_t* cos, const uint16_t* sin, uint16_t* kv_cache,
+                          const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                          const int32_t* cache_location, const uint8_t* w_o, const void* s_o, const float* ln2,
+                          const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+                          const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, uint16_t* out,
+                          int64_t batch, int64_t tokens, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
+                          int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages, int64_t inter,
+                          float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
+                          size_t workspace_bytes, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

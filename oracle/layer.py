@@ -156,3 +156,51 @@ def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
     attn = _bf(paged_attn.paged_decode(q, cache2, indptr, indices, last_page_len, scale))
     gated = sigmoid_mul(attn, qg[..., d:]).reshape(b, num_qo_heads * d)
     return mlp_residual(x, proj(gated, w, "o", proj_fmt), w, eps, mlp_fmt), cache2
+
+
+# ---------------------------------------------------------------------------------------------
+# Speculative verification (models/qwen38_27b/verify/verify_group_m4.py:1-9): T rows per sequence through a layer in
+# one call is, by definition, T decode steps one row each; the per-row snapshots are the states after each step.
+# ---------------------------------------------------------------------------------------------
+def gdn_layer_verify(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+    """x bf16 [B, T, H]. Returns (out [B, T, H], state_out, conv_out, state_snaps [T, ...], conv_snaps [T, ...])."""
+    outs, snaps, csnaps = [], [], []
+    st, cv = state_in, conv_in
+    for t in range(x.shape[1]):
+        o, st, cv = gdn_layer_decode(x[:, t], w, st, cv, num_k_heads, num_v_heads, eps, proj_fmt, mlp_fmt)
+        outs.append(o)
+        snaps.append(st)
+        csnaps.append(cv)
+    return torch.stack(outs, 1), st, cv, torch.stack(snaps), torch.stack(csnaps)
+
+
+def attn_layer_verify(x, w: dict, cos, sin, cache, indptr, indices, last_page_len, cache_location,
+                      num_qo_heads: int, rot: int, eps: float = 1e-6, sm_scale=None, proj_fmt: str = "fp8",
+                      mlp_fmt: str = "mxfp4"):
+    """x bf16 [B, T, H]; the page table (indptr / indices / last_page_len) covers each sequence's history and its T
+    new rows; cache_location [B, T, 2]; cos, sin [B, T, rot / 2]. Row t runs as a decode step over the table's
+    prefix of length history + t + 1. Returns (out [B, T, H], the cache with every new row written)."""
+    import numpy as np
+
+    from oracle import paged_attn
+
+    b, t_rows = x.shape[:2]
+    page = cache.shape[2]
+    ip = np.asarray(indptr)
+    idx = np.asarray(indices)
+    full = paged_attn.seq_lens(indptr, last_page_len, page)
+    outs = []
+    for t in range(t_rows):
+        ptr, ind, last = [0], [], []
+        for s in range(b):
+            n_tok = full[s] - (t_rows - 1 - t)
+            pages = (n_tok + page - 1) // page
+            ind += idx[ip[s]:ip[s] + pages].tolist()
+            ptr.append(len(ind))
+            last.append(n_tok - (pages - 1) * page)
+        o, cache = attn_layer_decode(x[:, t], w, cos[:, t], sin[:, t], cache, torch.tensor(ptr, dtype=torch.int32),
+                                     torch.tensor(ind, dtype=torch.int32), torch.tensor(last, dtype=torch.int32),
+                                     cache_location[:, t], num_qo_heads, rot, eps, sm_scale, proj_fmt, mlp_fmt)
+        outs.append(o)
+    return torch.stack(outs, 1), cache

@@ -265,3 +265,33 @@ def test_attn_layer_decode_matches_transformers_decoder_layer(b, t, hq, hkv, pag
         with rounding.fp32():
             bad = _attn_decode_tokens(x, bad_w, hq, hkv, d, bad_rot, theta, page, _g(52))
         assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3), name
+
+
+def test_attn_verify_oracle_is_causal_and_one_row_is_a_decode_step():
+    """attn_layer_verify's per-row page-table prefixes: row t sees the history and rows 0 .. t only (changing later
+    rows leaves it unchanged, changing an earlier row moves it), and a single row is exactly one decode step."""
+    from axk import configs
+
+    g = torch.Generator().manual_seed(4)
+    hq, hkv, d, page, H, F = 4, 2, 64, 16, 128, 128
+    w = configs.attn_layer_weights(g, H, F, hq, hkv, d)
+    c = configs.verify_rows_case([20, 15], 3, hq, hkv, d, page, g)  # the second sequence's rows cross a page
+    x = torch.randn(2, 3, H, generator=g).bfloat16()
+    cos, sin = layer.rope_cos_sin(c["pos"].reshape(-1), 32, 10_000_000.0)
+    cos, sin = cos.reshape(2, 3, -1), sin.reshape(2, 3, -1)
+    args = (c["indptr"], c["indices"], c["last_page_len"], c["loc"], hq, 32)
+    out, _ = layer.attn_layer_verify(x, w, cos, sin, c["cache"], *args)
+    x2 = x.clone()
+    x2[:, 2] = torch.randn(2, H, generator=g).bfloat16()
+    out2, _ = layer.attn_layer_verify(x2, w, cos, sin, c["cache"], *args)
+    assert torch.equal(out[:, :2], out2[:, :2]) and not torch.equal(out[:, 2], out2[:, 2])
+    x3 = x.clone()
+    x3[:, 0] = torch.randn(2, H, generator=g).bfloat16()
+    out3, _ = layer.attn_layer_verify(x3, w, cos, sin, c["cache"], *args)
+    assert not torch.equal(out[:, 1], out3[:, 1])  # row 1 attends row 0's K / V
+    c1 = configs.verify_rows_case([20, 15], 1, hq, hkv, d, page, torch.Generator().manual_seed(4))
+    one, _ = layer.attn_layer_verify(x[:, :1], w, cos[:, :1], sin[:, :1], c1["cache"], c1["indptr"], c1["indices"],
+                                     c1["last_page_len"], c1["loc"], hq, 32)
+    dec, _ = layer.attn_layer_decode(x[:, 0], w, cos[:, 0], sin[:, 0], c1["cache"], c1["indptr"], c1["indices"],
+                                     c1["last_page_len"], c1["loc"][:, 0], hq, 32)
+    assert torch.equal(one[:, 0], dec)
