@@ -60,7 +60,7 @@ struct MoeWs {
   int* counts;      // [E]
   int* offsets;     // [E + 1]
   int4* active;     // [E] active expert i: {rows, expert, first sorted row, 0}; rows 0 past the list
-  int* n_active;    // [1]
+  int* n_active;    // [2]: the active experts; [1] the decode routing's finished-workgroup count
   int* pair_pos;    // [P] sorted row of pair p = t * K + k
   int* row_tok;     // [P] token of sorted row
   float* row_w;     // [P] routing weight of sorted row
@@ -99,7 +99,7 @@ size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int6
   const size_t nb = prefill ? (size_t)prefill_blocks(T) : 0, nt = prefill ? (size_t)prefill_max_tiles(T, E, K) : 0;
   const size_t rp = (size_t)(prefill ? kPrefillRouterSplits : router_splits(H)) * T * E * 4;
   size_t o = 0;
-  const size_t sizes[kWsParts] = {(size_t)E * 4,      (size_t)(E + 1) * 4, (size_t)E * 16,    4,
+  const size_t sizes[kWsParts] = {(size_t)E * 4,      (size_t)(E + 1) * 4, (size_t)E * 16,    8,
                                   (size_t)P * 4,      (size_t)P * 4,       (size_t)P * 4,     (size_t)P * F * 2,
                                   (size_t)T * Fs * 2, (size_t)P * H * 4,   (size_t)T * H * 4, nb * E * 4,
                                   nt * 16,            4,                   (size_t)P * 4,     rp};
@@ -195,38 +195,60 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
   route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
 }
 
+// The decode grouping (below, beside moe_group_kernel).
+template <bool COH = false>
+AXK_DEV void group_body(const int32_t* ids, const float* wts, int T, int E, int K, const MoeWs& w,
+                        unsigned long long* s_mask, int* s_off, int* s_tmp);
+
 // Decode routing from the router's partial logits: logit = sum of the S K-slice partials in slice order
-// (written out as the layer's logits), then route_select.
-template <int V, int MAXS>  // MAXS: bound on the number of partials
+// (written out as the layer's logits), then route_select. GROUP (decode): the last workgroup to finish also groups
+// the pairs (moe_group_kernel's work), counted on `done`, which the router kernel zeroed earlier on the stream.
+template <int V, int MAXS, bool GROUP = false>  // MAXS: bound on the number of partials
 __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part, int S, int T, int E,
                                                              int K, int norm_topk, float* __restrict__ logits,
-                                                             int32_t* __restrict__ ids, float* __restrict__ wts) {
+                                                             int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                             MoeWs w, int* done) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-  // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
-  float pv[MAXS][V];
+  if (t < T) {
+    // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
+    float pv[MAXS][V];
 #pragma unroll
-  for (int sl = 0; sl < MAXS; ++sl)
+    for (int sl = 0; sl < MAXS; ++sl)
 #pragma unroll
-    for (int i = 0; i < V; ++i)
-      pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
-  float x[V];
+      for (int i = 0; i < V; ++i)
+        pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
+    float x[V];
 #pragma unroll
-  for (int i = 0; i < V; ++i) {
-    float v = pv[0][i];
+    for (int i = 0; i < V; ++i) {
+      float v = pv[0][i];
 #pragma unroll
-    for (int sl = 1; sl < MAXS; ++sl)
-      if (sl < S) v += pv[sl][i];
-    x[i] = v;
+      for (int sl = 1; sl < MAXS; ++sl)
+        if (sl < S) v += pv[sl][i];
+      x[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const int e = i * 64 + lane;
+      if (e < E) logits[(int64_t)t * E + e] = x[i];
+      else x[i] = -INFINITY;
+    }
+    route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
   }
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    const int e = i * 64 + lane;
-    if (e < E) logits[(int64_t)t * E + e] = x[i];
-    else x[i] = -INFINITY;
+  if constexpr (GROUP) {
+    __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
+    __shared__ int s_off[kMaxExperts + 1];
+    __shared__ int s_tmp[8];
+    __shared__ int s_last;
+    __threadfence();  // this workgroup's selections visible device-wide before it counts itself done
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(done, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (s_last) {
+      __threadfence();
+      group_body<true>(ids, wts, T, E, K, w, s_mask, s_off, s_tmp);
+    }
   }
-  route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
 }
 
 // Prefill router GEMM: workgroup (64 tokens, 64 experts, K slice s), waves 2 x 2 with 32 x 32 each; both operands
@@ -320,8 +342,10 @@ __global__ __launch_bounds__(256) void moe_router_tile_kernel(const uint16_t* __
 // the partial logits written to part[s]. Rows past T or E are clamped for the loads and never stored.
 __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h2,
                                                          const uint16_t* __restrict__ wr, int T, int H, int E,
-                                                         int S, float* __restrict__ part) {
+                                                         int S, float* __restrict__ part, int* done) {
   __shared__ float4 red[4][64];
+  // the routing kernel's finished-workgroup count, zeroed here (the router runs before it on the stream)
+  if (done && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *done = 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
   const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16, sl = blockIdx.z;
   const int ns = H / 32, st0 = (int)((int64_t)sl * ns / S), st1 = (int)((int64_t)(sl + 1) * ns / S);
@@ -361,10 +385,10 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int* s_tmp, int* t
     const int x = __shfl_up(incl, o, 64);
     if (lane >= o) incl += x;
   }
-  if (lane == 63) s_tmp[wave] = incl;
+  if (lane == 63 && wave < 4) s_tmp[wave] = incl;  // wider workgroups: only threads 0 .. 255 take part
   __syncthreads();
   int base = 0;
-  for (int w = 0; w < wave; ++w) base += s_tmp[w];
+  for (int w = 0; w < wave && w < 4; ++w) base += s_tmp[w];
   *total = s_tmp[0] + s_tmp[1] + s_tmp[2] + s_tmp[3];
   __syncthreads();
   return base + incl - v;
@@ -373,20 +397,32 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int* s_tmp, int* t
 // Expert e's tokens as a bitmask (a token's K experts are distinct, so a pair is (expert, token)): counts
 // are popcounts, and a pair's rank inside its expert is the popcount of the lower tokens' bits — the
 // grouping is stable in token order with no atomics on positions.
-__global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restrict__ ids,
-                                                        const float* __restrict__ wts, int T, int E, int K,
-                                                        MoeWs w) {
-  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
-  __shared__ int s_off[kMaxExperts + 1];
-  __shared__ int s_tmp[8];
+// The grouping, for every thread of the workgroup (its barriers are unconditional); threads 0 .. 255 do the work.
+// COH: ids / wts were written by other workgroups of the same launch: read them at device scope (past this CU's L1).
+template <bool COH>
+AXK_DEV int load_id(const int32_t* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+template <bool COH>
+AXK_DEV float load_wt(const float* p) {
+  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *p;
+}
+template <bool COH>
+AXK_DEV void group_body(const int32_t* ids, const float* wts, int T, int E, int K, const MoeWs& w,
+                        unsigned long long* s_mask, int* s_off, int* s_tmp) {
   const int P = T * K, W = (T + 63) / 64;
   const int tid = threadIdx.x;
-  for (int i = tid; i < E * W; i += blockDim.x) s_mask[i] = 0ull;
+  const bool on = tid < 256;
+  if (on)
+    for (int i = tid; i < E * W; i += 256) s_mask[i] = 0ull;
   __syncthreads();
-  for (int p = tid; p < P; p += blockDim.x) {
-    const int e = ids[p], t = p / K;
-    if (e >= 0 && e < E) atomicOr(&s_mask[e * W + (t >> 6)], 1ull << (t & 63));
-  }
+  if (on)
+    for (int p = tid; p < P; p += 256) {
+      const int e = load_id<COH>(ids + p), t = p / K;
+      if (e >= 0 && e < E) atomicOr(&s_mask[e * W + (t >> 6)], 1ull << (t & 63));
+    }
   __syncthreads();
   // expert e's count; 4 experts per thread (E <= 1024), then a block scan of the per-thread sums
   constexpr int EPT = kMaxExperts / 256;
@@ -395,7 +431,7 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
   for (int j = 0; j < EPT; ++j) {
     const int e = tid * EPT + j;
     int c = 0;
-    if (e < E)
+    if (on && e < E)
       for (int i = 0; i < W; ++i) c += __popcll(s_mask[e * W + i]);
     cnt[j] = c;
     sum += c;
@@ -404,41 +440,54 @@ __global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restric
   int tot, tota;
   int off = block_exclusive_scan256(sum, s_tmp, &tot);
   int aoff = block_exclusive_scan256(nact, s_tmp + 4, &tota);
+  if (on) {
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid * EPT + j;
-    if (e < E) {
-      s_off[e] = off;
-      w.counts[e] = cnt[j];
-      w.offsets[e] = off;
-      if (cnt[j] > 0) {
-        w.active[aoff] = make_int4(cnt[j], e, off, 0);
-        ++aoff;
+    for (int j = 0; j < EPT; ++j) {
+      const int e = tid * EPT + j;
+      if (e < E) {
+        s_off[e] = off;
+        w.counts[e] = cnt[j];
+        w.offsets[e] = off;
+        if (cnt[j] > 0) {
+          w.active[aoff] = make_int4(cnt[j], e, off, 0);
+          ++aoff;
+        }
       }
+      off += cnt[j];
     }
-    off += cnt[j];
+    if (tid == 0) {
+      w.offsets[E] = tot;
+      *w.n_active = tota;
+    }
+    for (int j = tota + tid; j < E; j += 256) w.active[j] = make_int4(0, 0, 0, 0);  // streaming kernels exit
   }
-  if (tid == 0) {
-    w.offsets[E] = tot;
-    *w.n_active = tota;
-  }
-  for (int j = tota + tid; j < E; j += blockDim.x) w.active[j] = make_int4(0, 0, 0, 0);  // streaming kernels exit
   __syncthreads();
-  for (int p = tid; p < P; p += blockDim.x) {
-    const int e = ids[p], t = p / K;
-    if (e < 0 || e >= E) {  // an id outside [0, E) selects no expert: the combine skips the pair
-      w.pair_pos[p] = -1;
-      continue;
+  if (on)
+    for (int p = tid; p < P; p += 256) {
+      const int e = load_id<COH>(ids + p), t = p / K;
+      if (e < 0 || e >= E) {  // an id outside [0, E) selects no expert: the combine skips the pair
+        w.pair_pos[p] = -1;
+        continue;
+      }
+      int rank = __popcll(s_mask[e * W + (t >> 6)] & ((1ull << (t & 63)) - 1ull));
+      for (int i = 0; i < (t >> 6); ++i) rank += __popcll(s_mask[e * W + i]);
+      const int pos = s_off[e] + rank;
+      w.pair_pos[p] = pos;
+      w.row_tok[pos] = t;
+      w.row_w[pos] = load_wt<COH>(wts + p);
+      w.row_pair[pos] = p;
     }
-    int rank = __popcll(s_mask[e * W + (t >> 6)] & ((1ull << (t & 63)) - 1ull));
-    for (int i = 0; i < (t >> 6); ++i) rank += __popcll(s_mask[e * W + i]);
-    const int pos = s_off[e] + rank;
-    w.pair_pos[p] = pos;
-    w.row_tok[pos] = t;
-    w.row_w[pos] = wts[p];
-    w.row_pair[pos] = p;
-  }
 }
+
+__global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restrict__ ids,
+                                                        const float* __restrict__ wts, int T, int E, int K,
+                                                        MoeWs w) {
+  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
+  __shared__ int s_off[kMaxExperts + 1];
+  __shared__ int s_tmp[8];
+  group_body(ids, wts, T, E, K, w, s_mask, s_off, s_tmp);
+}
+
 
 // ---------------------------------------------------------------------------------------------
 // Decode expert streaming. A workgroup owns one slot (an active expert, or the shared expert) and a run of
@@ -1334,13 +1383,16 @@ extern "C" int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk
   return axk_launch_status();
 }
 
-extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg,
-                               const uint8_t* sh_gate_w, const uint8_t* sh_gate_s, const uint8_t* sh_up_w,
-                               const uint8_t* sh_up_s, const uint8_t* sh_down_w, const uint8_t* sh_down_s,
-                               const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds,
-                               const int32_t* topk_ids, const float* topk_weights, uint16_t* out, int64_t tokens,
-                               int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
-                               int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+namespace {
+// The experts half. grouped: the decode grouping already ran (in the routing launch's last workgroup); check_only: run the
+// contract checks and return before any launch.
+int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg, const uint8_t* sh_gate_w,
+                     const uint8_t* sh_gate_s, const uint8_t* sh_up_w, const uint8_t* sh_up_s,
+                     const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
+                     const uint8_t* e_dw, const uint8_t* e_ds, const int32_t* topk_ids, const float* topk_weights,
+                     uint16_t* out, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
+                     int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream, bool grouped,
+                     bool check_only) {
   AXK_REQUIRE(h2 && e_gw && e_gs && e_dw && e_ds && topk_ids && topk_weights && out, AXK_E_NULL);
   const bool has_shared = sh_gate_w != nullptr;
   AXK_REQUIRE(!has_shared || (sh_gate_s && sh_up_w && sh_up_s && sh_down_w && sh_down_s), AXK_E_NULL);
@@ -1356,6 +1408,7 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
   const size_t obytes = (size_t)tokens * hidden * 2;
   AXK_REQUIRE(!axk_overlap(out, obytes, h2, obytes) && !axk_overlap(out, obytes, workspace, workspace_bytes),
               AXK_E_ALIAS);
+  if (check_only) return AXK_OK;
   hipStream_t st = axk_stream(stream);
   const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, d.Fs);
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, F = (int)inter, Fs = (int)d.Fs;
@@ -1387,7 +1440,7 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
                        dim3(256), 0, st, ca);
     return axk_launch_status();
   }
-  hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
+  if (!grouped) hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
   const int max_slots = E < T * K ? E : T * K;
   const int fmax = F > Fs ? F : Fs;
   // runs of 4 x tpw tiles per workgroup; activation rows staged in dynamic LDS ([rows][K + 8] bf16). Small batches
@@ -1439,6 +1492,19 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
                      dim3(256), 0, st, ca);
   return axk_launch_status();
 }
+}  // namespace
+
+extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg,
+                               const uint8_t* sh_gate_w, const uint8_t* sh_gate_s, const uint8_t* sh_up_w,
+                               const uint8_t* sh_up_s, const uint8_t* sh_down_w, const uint8_t* sh_down_s,
+                               const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds,
+                               const int32_t* topk_ids, const float* topk_weights, uint16_t* out, int64_t tokens,
+                               int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
+                               int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  return moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
+                          e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
+                          shared_inter, workspace, workspace_bytes, stream, false, false);
+}
 
 extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router,
                               const uint16_t* w_shg, const uint8_t* sh_gate_w, const uint8_t* sh_gate_s,
@@ -1449,49 +1515,57 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
                               int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
                               int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(w_router && logits, AXK_E_NULL);
-  int rc;
-  {
-    // the router as K-slice partial logits in the workspace, summed in slice order by the routing kernel
-    AXK_REQUIRE(h2 && topk_ids && topk_weights, AXK_E_NULL);
-    rc = check_dims({tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0});
-    if (rc != AXK_OK) return rc;
-    AXK_REQUIRE(axk_aligned(h2, 16) && axk_aligned(w_router, 16), AXK_E_ALIGN);
-    const size_t need =
-        axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
-    AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
-    const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
-    const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k;
-    const bool prefill = T > kDecodeTokens;
-    const int S = prefill ? (int)std::min<int64_t>(kPrefillRouterSplits, hidden / 64) : router_splits(hidden);
-    hipStream_t st = axk_stream(stream);
-    if (prefill)
-      hipLaunchKernelGGL(moe_router_tile_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64), (unsigned)S),
-                         dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
-    else
-      hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
-                         dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
-    const dim3 grid((unsigned)((T + 3) / 4)), block(256);
-#define AXK_ROUTE_PART(V, MS)                                                                                  \
-  hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob,  \
-                     logits, topk_ids, topk_weights)
-    if (prefill) {
-      if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
-      else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
-      else AXK_ROUTE_PART(kMaxExperts / 64, kPrefillRouterSplits);
-    } else if (S <= 8) {  // the partial loads are unrolled to the bound: keep it tight
-      if (E <= 64) AXK_ROUTE_PART(1, 8);
-      else if (E <= 256) AXK_ROUTE_PART(4, 8);
-      else AXK_ROUTE_PART(kMaxExperts / 64, 8);
-    } else {
-      if (E <= 64) AXK_ROUTE_PART(1, kMaxRouterSplits);
-      else if (E <= 256) AXK_ROUTE_PART(4, kMaxRouterSplits);
-      else AXK_ROUTE_PART(kMaxExperts / 64, kMaxRouterSplits);
-    }
-#undef AXK_ROUTE_PART
-    rc = axk_launch_status();
-  }
+  AXK_REQUIRE(h2 && topk_ids && topk_weights, AXK_E_NULL);
+  int rc = check_dims({tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0});
   if (rc != AXK_OK) return rc;
-  return axk_moe_experts(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
-                         e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
-                         shared_inter, workspace, workspace_bytes, stream);
+  AXK_REQUIRE(axk_aligned(h2, 16) && axk_aligned(w_router, 16), AXK_E_ALIGN);
+  const size_t need = axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  // the experts half's checks before anything is launched (a nonzero status means nothing was enqueued)
+  rc = moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
+                        e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
+                        shared_inter, workspace, workspace_bytes, stream, false, true);
+  if (rc != AXK_OK) return rc;
+  const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
+  const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k;
+  const bool prefill = T > kDecodeTokens;
+  const bool grouped = !prefill;  // decode: the routing launch also groups the pairs
+  const int S = prefill ? (int)std::min<int64_t>(kPrefillRouterSplits, hidden / 64) : router_splits(hidden);
+  hipStream_t st = axk_stream(stream);
+  // the router as K-slice partial logits in the workspace, summed in slice order by the routing kernel
+  if (prefill)
+    hipLaunchKernelGGL(moe_router_tile_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64), (unsigned)S),
+                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
+  else
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
+                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart, w.n_active + 1);
+  const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+#define AXK_ROUTE_PART(V, MS)                                                                                   \
+  do {                                                                                                          \
+    if (grouped)                                                                                                \
+      hipLaunchKernelGGL((moe_route_part_kernel<V, MS, true>), grid, block, 0, st, w.rpart, S, T, E, K,        \
+                         norm_topk_prob, logits, topk_ids, topk_weights, w, w.n_active + 1);                    \
+    else                                                                                                        \
+      hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, \
+                         logits, topk_ids, topk_weights, w, nullptr);                                          \
+  } while (0)
+  if (prefill) {
+    if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
+    else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
+    else AXK_ROUTE_PART(kMaxExperts / 64, kPrefillRouterSplits);
+  } else if (S <= 8) {  // the partial loads are unrolled to the bound: keep it tight
+    if (E <= 64) AXK_ROUTE_PART(1, 8);
+    else if (E <= 256) AXK_ROUTE_PART(4, 8);
+    else AXK_ROUTE_PART(kMaxExperts / 64, 8);
+  } else {
+    if (E <= 64) AXK_ROUTE_PART(1, kMaxRouterSplits);
+    else if (E <= 256) AXK_ROUTE_PART(4, kMaxRouterSplits);
+    else AXK_ROUTE_PART(kMaxExperts / 64, kMaxRouterSplits);
+  }
+#undef AXK_ROUTE_PART
+  rc = axk_launch_status();
+  if (rc != AXK_OK) return rc;
+  return moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
+                          e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
+                          shared_inter, workspace, workspace_bytes, stream, grouped, false);
 }
