@@ -35,10 +35,9 @@ AXK_DEV uint32_t pack_bf16x2(float lo, float hi) {
 
 AXK_DEV float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
-// E8M0 byte -> fp32 2^(s-127); bit-identical to torch.exp2(float(s) - 127).
-AXK_DEV float e8m0_to_f32(uint32_t s) {
-  return s == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
-}
+// E8M0 byte -> fp32 2^(s-127); bit-identical to torch.exp2(float(s) - 127): s << 23 is the value's bits for s >= 1
+// (s = 255: +inf), and for s = 0 the subnormal 2^-127 (0x00400000) is the larger of the two (a max, not a select).
+AXK_DEV float e8m0_to_f32(uint32_t s) { return __uint_as_float(max(s << 23, 0x00400000u)); }
 
 // E2M1 code (low 4 bits of c) -> exact fp32 value, code 8 -> -0.0.
 AXK_DEV float e2m1_to_f32(uint32_t c) {
