@@ -5,12 +5,14 @@
 // indices[indptr[b] .. indptr[b+1]); the last one holds last_page_len[b] valid tokens (1..page_size),
 // every other page is full (flash_attn.py:1421-1596 page-id lookup, tail mask 87-104).
 //
-// Three kernels:
+// Up to kLocalPlanBatch sequences over a bf16 cache the split is stream-K (paged_decode_sk_kernel: every workgroup
+// streams the same number of 16-token tiles, its range crossing (sequence, KV head) pairs) and its own merge follows
+// (paged_merge_sk_kernel). Above that, and for the FP8 cache, three kernels partition by items:
 //  1. plan   — one wave: pages per split so that the number of (sequence, split, KV head) work items
 //              is about one per resident split workgroup, and one descriptor per item. Depends only on the
 //              page-table shape, so one plan serves every attention layer of a decode step (no host sync,
-//              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
-//              compute the same partition themselves from the page table and no plan launch is needed.
+//              no memset: graph-capturable). Up to kLocalPlanBatch sequences (the FP8 cache) the split and
+//              merge kernels compute the same partition themselves and no plan launch is needed.
 //  2. decode — persistent: a few workgroups per CU take the work items in turn. The 4 waves share every
 //              16-token K/V tile of the item's pages: the tile streams HBM -> LDS by direct loads into a
 //              3-deep ring (two tiles in flight while one is computed). Every wave computes the full scores
