@@ -615,8 +615,14 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     uint32_t sg[kBatchChunks], su[kBatchChunks];
   };
   // Loads are unconditional, from addresses clamped into the weights (a row past Fo is never stored, a unit past
-  // K is zeroed where it is used): a branch around a load would make every later wait drain the queue.
+  // K is zeroed where it is used): a branch around a load would make every later wait drain the queue. Steps past
+  // the wave's last (the look-ahead at the end of its stream) load the first 16 bytes of h2, already in L2 from the
+  // row staging, instead of repeating the last weight batch: those non-temporal re-reads missed L2 and came from
+  // HBM again.
+  const uint8_t* idle = reinterpret_cast<const uint8_t*>(a.h2);
   auto load_batch = [&](Batch& bt, int step) {
+    const bool past = step >= steps;  // wave-uniform
+    step = min(step, max(steps - 1, 0));
     const int i = step / nb, bi = step - i * nb;
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)Fo - 1);
     if (STAGE) {
@@ -625,15 +631,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)Fo - 1);
         const int64_t off = (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr);
-        bt.qg[h] = load_nt(gw + r * (H / 2) + off);  // expert weights: read once per step
-        bt.qu[h] = load_nt(uw + r * (H / 2) + off);
+        bt.qg[h] = load_nt(past ? idle : gw + r * (H / 2) + off);  // expert weights: read once per step
+        bt.qu[h] = load_nt(past ? idle : uw + r * (H / 2) + off);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
-        bt.qg[j] = load_nt(gw + n * (H / 2) + kb / 2);
-        bt.qu[j] = load_nt(uw + n * (H / 2) + kb / 2);
+        bt.qg[j] = load_nt(past ? idle : gw + n * (H / 2) + kb / 2);
+        bt.qu[j] = load_nt(past ? idle : uw + n * (H / 2) + kb / 2);
         if (!WIDE) {
           bt.sg[j] = gs[n * (H / 32) + kb / 32];
           bt.su[j] = us[n * (H / 32) + kb / 32];
@@ -707,21 +713,20 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     // three batches in rotation: batch st + 2 is loaded while batch st is used; the first two are issued
     // before the activation rows are staged, so they overlap the expert's metadata and row gathers
     Batch b0, b1, b2;
-    const int last = max(steps - 1, 0);
     __syncthreads();  // the previous pass's readers are done with sA
     load_batch(b0, 0);
-    load_batch(b1, min(1, last));
+    load_batch(b1, 1);
     if (shared)
       stage_rows<false, ROWS>(sA, a.h2, nullptr, 0, m0, cnt, H);
     else
       stage_rows<true, ROWS>(sA, a.h2, a.w.row_tok, row0, m0, cnt, H);
     __syncthreads();
     for (int st = 0; st < steps; st += 3) {
-      load_batch(b2, min(st + 2, last));
+      load_batch(b2, st + 2);
       proc(b0, st);
-      load_batch(b0, min(st + 3, last));
+      load_batch(b0, st + 3);
       if (st + 1 < steps) proc(b1, st + 1);
-      load_batch(b1, min(st + 4, last));
+      load_batch(b1, st + 4);
       if (st + 2 < steps) proc(b2, st + 2);
     }
   }
@@ -779,7 +784,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     axk_u32x4 q[kBatchChunks];  // STAGE: [h] = rows kStageRpi h + lane / kStageLpr of the batch
     uint32_t s[kBatchChunks];
   };
-  auto load_batch = [&](Batch& bt, int step) {  // unconditional, clamped (as in the gate-up kernel)
+  // unconditional, clamped, and past the wave's last step from the slot's first activation bytes (as in the
+  // gate-up kernel)
+  const uint8_t* idle = reinterpret_cast<const uint8_t*>(act);
+  auto load_batch = [&](Batch& bt, int step) {
+    const bool past = step >= steps;  // wave-uniform
+    step = min(step, max(steps - 1, 0));
     const int i = step / nb, bi = step - i * nb;
     const int64_t n = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + nl, (int64_t)a.H - 1);
     if (STAGE) {
@@ -787,13 +797,13 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
       for (int h = 0; h < kBatchChunks; ++h) {
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)a.H - 1);
-        bt.q[h] = load_nt(dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr));
+        bt.q[h] = load_nt(past ? idle : dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr));
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
-        bt.q[j] = load_nt(dw + n * (K / 2) + kb / 2);
+        bt.q[j] = load_nt(past ? idle : dw + n * (K / 2) + kb / 2);
         if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
       }
     }
@@ -855,18 +865,17 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
       }
     };
     Batch b0, b1, b2;
-    const int last = max(steps - 1, 0);
     __syncthreads();
     load_batch(b0, 0);
-    load_batch(b1, min(1, last));
+    load_batch(b1, 1);
     stage_rows<false, ROWS>(sA, act, nullptr, row0, m0, cnt, K);
     __syncthreads();
     for (int st = 0; st < steps; st += 3) {
-      load_batch(b2, min(st + 2, last));
+      load_batch(b2, st + 2);
       proc(b0, st);
-      load_batch(b0, min(st + 3, last));
+      load_batch(b0, st + 3);
       if (st + 1 < steps) proc(b1, st + 1);
-      load_batch(b1, min(st + 4, last));
+      load_batch(b1, st + 4);
       if (st + 2 < steps) proc(b2, st + 2);
     }
   }
