@@ -105,6 +105,46 @@ AXK_DEV axk_s16x4 lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) axk_s16x4*)(p));
 }
 
+// LDS byte address of a __shared__ pointer (for M0).
+AXK_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Direct global -> LDS loads: lane l's 16 bytes at gptr land at lds_base + 16 l (lds_base wave-uniform).
+// Issued from asm on purpose: the compiler then counts none of these loads, so its own waits can only over-wait,
+// and pipeline waits (wait_vmcnt<n>) stay exactly as written. M0 is restored.
+// lds_dma16: non-temporal, for bytes read once per launch (they should not displace cached lines);
+// lds_dma16_cached: the default policy, for tiles other workgroups re-read through L2.
+AXK_DEV void lds_dma16(const void* gptr, uint32_t lds_base_any) {
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(gptr)
+      : "memory");
+}
+AXK_DEV void lds_dma16_cached(const void* gptr, uint32_t lds_base_any) {
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(gptr)
+      : "memory");
+}
+
+template <int N>
+AXK_DEV void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 AXK_DEV axk_f32x4 mfma_bf16_16x16x32(axk_bf16x8 a, axk_bf16x8 b, axk_f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

@@ -32,10 +32,10 @@
 //   pcount / pscan / pscatter — the pairs grouped by expert in 256-token blocks (per-block bitmask counts, one
 //             scan of the (expert, block) bases, stable scatter), plus a tile list of kBM-row tiles per active
 //             expert and for the shared expert over all tokens
-//   ggemm3  — a grouped GEMM on MFMA: workgroup = (tile, 256 weight rows), workgroups spread over the XCDs so
+//   ggemm   — a grouped GEMM on MFMA: workgroup = (tile, 256 weight rows), workgroups spread over the XCDs so
 //             that each XCD takes a contiguous run of the expert-ordered tiles; A rows gathered by token and
-//             B MXFP4 rows loaded as whole cache lines, both staged in LDS; per-wave 64 x 64 blocks; gate-up
-//             with the SwiGLU epilogue, then down with the routing-weight epilogue into fp32 y by pair
+//             B MXFP4 rows land in an LDS ring by direct loads; per-wave 64 x 64 blocks; gate-up with the
+//             SwiGLU epilogue, then down with the routing-weight epilogue into bf16 y by pair
 //   combine — as decode
 #include "axk_common.h"
 #include "axk_host.h"
@@ -1104,13 +1104,13 @@ __global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __rest
 // the output (four 16-row x four 16-column MFMA tiles: every A fragment feeds four MFMAs and every B fragment
 // four). MODE 0: weight rows = 128 gate + the same 128 up columns (SwiGLU pairs gate and up tiles in the same
 // lanes); MODE 1: 256 columns of H.
-// Every global load instruction covers whole 128-byte lines of few rows, which keeps the address path's
-// per-line work low: A per K step as 8 rows x 128 bytes per instruction; B for 4 K steps at once (128 code
-// bytes of a weight row = 256 k) as 8 rows x 128 bytes per instruction, held in registers for a whole
-// super-step and written to LDS at its start; the E8M0 scales of the whole reduction are staged once per
-// workgroup. Workgroups are mapped so that all tiles and column blocks of one expert run on one XCD: its
-// weights are fetched into that XCD's L2 once.
-// LDS: A [2][64 rows][144 bytes]; B [256 rows][144 bytes] (one super-step); scales [256 rows][Kd/32 + 16].
+// The A rows (gathered by token) and the packed weights of each 64-wide K step land in LDS by direct loads (no
+// register staging) into a ring of kGStages steps, two steps ahead, with one barrier per step; the E8M0 scales of
+// the whole reduction are staged once per workgroup. A stage holds A [64 rows][128 B] with the 16-byte chunk c of
+// row r at position c ^ (r & 7), and B [256 weight rows][32 B] with the 16-byte half h of row r at position
+// h ^ ((r >> 3) & 1): the fragment reads of either are then free of bank conflicts. Workgroups are mapped so that
+// all tiles and column blocks of one expert run on one XCD: its weights are fetched into that XCD's L2 once.
+// LDS: kGStages x (A 8 KiB + B 8 KiB); scales [256 rows][Kd/32 + 16].
 // ---------------------------------------------------------------------------------------------
 struct GGemmArgs {
   const uint16_t* a;     // gate-up: h2 [T, H]; down: act [P, F]
@@ -1122,20 +1122,18 @@ struct GGemmArgs {
 };
 
 constexpr int kG2Rows = 256;          // weight rows per workgroup
-constexpr int kG2LdA = kBK + 8;       // bf16 per staged activation row
 constexpr int kG2Cols0 = kG2Rows / 2;  // gate-up: output (act) columns per workgroup
 constexpr int kG2Cols1 = kG2Rows;      // down: output columns per workgroup
 constexpr int kXcds = 8;              // MI355X: consecutive workgroups go round-robin over 8 XCDs
-constexpr int kG3LdB = 144;           // bytes per staged weight row of a super-step (128 code bytes + pad)
-constexpr int kG3ABytes = kBM * kG2LdA * 2;
-size_t g3_lds_bytes(int Kd) { return 2 * (size_t)kG3ABytes + (size_t)kG2Rows * kG3LdB + (size_t)kG2Rows * (Kd / 32 + 16); }
+constexpr int kGStages = 3;
+constexpr int kGAStage = kBM * kBK * 2;      // 8 KiB
+constexpr int kGBStage = kG2Rows * kBK / 2;  // 8 KiB
+constexpr int kGStage = kGAStage + kGBStage;
+size_t gemm_lds_bytes(int Kd) { return (size_t)kGStages * kGStage + (size_t)kG2Rows * (Kd / 32 + 16); }
 
 template <int MODE>
-__global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
+__global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
-  // physical workgroup w runs on XCD w % 8: of the n_tiles x nblk (tile, column block) pairs, XCD x takes the
-  // contiguous run [x per, (x + 1) per) in order (tiles are in expert order), per = the pairs / 8 rounded up; the
-  // grid's surplus workgroups exit
   const int nblk = MODE == 0 ? (g.Fmax + kG2Cols0 - 1) / kG2Cols0 : (g.H + kG2Cols1 - 1) / kG2Cols1;
   const int total = *g.ws.n_tiles * nblk, per = (total + kXcds - 1) / kXcds;
   const int k = blockIdx.x / kXcds, lid = (blockIdx.x % kXcds) * per + k;
@@ -1147,30 +1145,15 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
 
-  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);  // reduction length
-  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;  // output columns
+  const int Kd = MODE == 0 ? g.H : (shared ? g.Fs : g.F);
+  const int No = MODE == 0 ? (shared ? g.Fs : g.F) : g.H;
   const int col0 = cblk * (MODE == 0 ? kG2Cols0 : kG2Cols1);
   if (col0 >= No) return;
-  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
-  unsigned char* sB = smem + 2 * kG3ABytes;
-  unsigned char* sS = sB + kG2Rows * kG3LdB;
+  const uint32_t lds0 = lds_addr(smem);
+  unsigned char* sS = smem + kGStages * kGStage;
   const int ldS = Kd / 32 + 16;
+  const int nk = Kd / kBK;
 
-  // A: thread t stages rows t / 8 and t / 8 + 32, 16-byte chunk t % 8 of the K step (one line per row)
-  const int ar = tid >> 3, ac = tid & 7;
-  const uint16_t* asrc[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = min(ar + 32 * h, rows - 1);  // rows past the tile re-read its last row (never stored)
-    if (MODE == 0) {
-      const int tok = shared ? row0 + r : g.ws.row_tok[row0 + r];
-      asrc[h] = g.a + (int64_t)tok * g.H + 8 * ac;
-    } else {
-      asrc[h] = (shared ? g.a_sh + (int64_t)(row0 + r) * g.Fs : g.a + (int64_t)(row0 + r) * g.F) + 8 * ac;
-    }
-  }
-  // B: LDS row rho -> weight row (gate-up: rho < 128 gate column col0 + rho, else up column col0 + rho - 128;
-  // down: column col0 + rho), clamped to the last column (never stored)
   const uint8_t *wgate, *wup, *sgate, *sup;
   if (MODE == 0) {
     if (shared) {
@@ -1186,17 +1169,48 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
     wgate = wup = shared ? g.w_sh : g.w + (int64_t)e * g.H * (g.F / 2);
     sgate = sup = shared ? g.s_sh : g.s + (int64_t)e * g.H * (g.F / 32);
   }
+  // LDS weight row rho -> weight row (gate-up: rho < 128 gate column col0 + rho, else up column col0 + rho - 128;
+  // down: column col0 + rho), clamped to the last column (never stored)
   auto wrow = [&](int rho, bool scale) -> const uint8_t* {
     const bool up = MODE == 0 && rho >= kG2Cols0;
     const int c = min(col0 + (MODE == 0 ? (rho & (kG2Cols0 - 1)) : rho), No - 1);
     return scale ? (up ? sup : sgate) + (int64_t)c * (Kd / 32) : (up ? wup : wgate) + (int64_t)c * (Kd / 2);
   };
-  // B super-step loads: instruction i covers LDS rows 64 wave + 8 i .. + 7, lane -> row + lane / 8, chunk lane % 8
-  const int bsub = lane >> 3, bc = lane & 7;
-  const int nk = Kd / kBK, nsup = (nk + 3) / 4;
-  const int brow_bytes = Kd / 2;
 
-  // the E8M0 scales of the whole reduction: 16-byte units when the row length allows, else 2-byte units
+  // per-lane sources of this wave's two A and two B load instructions of a step (instruction i = 2 wave + h):
+  // A: row 8 i + lane / 8 (rows past the tile re-read its last row, never stored), chunk (lane % 8) ^ (row & 7);
+  // B: weight row 32 i + lane / 2, half (lane % 2) ^ ((row >> 3) & 1)
+  const uint16_t* asrc[2];
+  const uint8_t* bsrc[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = 2 * wave + h;
+    const int r = 8 * i + (lane >> 3), rr = min(r, rows - 1), ch = (lane & 7) ^ (r & 7);
+    if (MODE == 0) {
+      const int tok = shared ? row0 + rr : g.ws.row_tok[row0 + rr];
+      asrc[h] = g.a + (int64_t)tok * g.H + 8 * ch;
+    } else {
+      asrc[h] = (shared ? g.a_sh + (int64_t)(row0 + rr) * g.Fs : g.a + (int64_t)(row0 + rr) * g.F) + 8 * ch;
+    }
+    const int rho = 32 * i + (lane >> 1);
+    bsrc[h] = wrow(rho, false) + 16 * ((lane & 1) ^ ((rho >> 3) & 1));
+  }
+  // step ks into ring slot buf; past the last step the last one is loaded again (in bounds, unused), so every
+  // iteration waits on the same count
+  auto issue = [&](int ks, int buf) {
+    const int kk = min(ks, nk - 1);
+    const uint32_t base = lds0 + buf * kGStage;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      lds_dma16_cached(asrc[h] + kk * kBK, base + (2 * wave + h) * 1024);
+      lds_dma16_cached(bsrc[h] + kk * (kBK / 2), base + kGAStage + (2 * wave + h) * 1024);
+    }
+  };
+  issue(0, 0);
+  issue(1, 1);
+
+  // the E8M0 scales of the whole reduction (while the first steps load): 16-byte units when the row length
+  // allows, else 2-byte units
   {
     const int sb = Kd / 32;
     if (sb % 16 == 0 && (((uintptr_t)sgate | (uintptr_t)sup) & 15) == 0) {
@@ -1219,95 +1233,50 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
   for (int j = 0; j < 4; ++j)
     brow[j] = MODE == 0 ? (j >> 1) * kG2Cols0 + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
 
-#define AXK_G3_LOADA(A0, A1, ks)                                                   \
-  do {                                                                             \
-    const int k0_ = min((ks), nk - 1) * kBK;                                       \
-    A0 = *reinterpret_cast<const uint4*>(asrc[0] + k0_);                           \
-    A1 = *reinterpret_cast<const uint4*>(asrc[1] + k0_);                           \
-  } while (0)
-#define AXK_G3_STOREA(A0, A1, buf)                                                 \
-  do {                                                                             \
-    uint16_t* d_ = sA + (buf) * (kBM * kG2LdA) + ar * kG2LdA + 8 * ac;             \
-    *reinterpret_cast<uint4*>(d_) = A0;                                            \
-    *reinterpret_cast<uint4*>(d_ + 32 * kG2LdA) = A1;                              \
-  } while (0)
-  axk_u32x4 bq[8];  // a native vector type: an array of it stays in registers
-#define AXK_G3_LOADB(sup_)                                                         \
-  do {                                                                             \
-    const int off_ = min((sup_) * 128 + 16 * bc, brow_bytes - 16);                 \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                  \
-      bq[i] = *reinterpret_cast<const axk_u32x4*>(wrow(64 * wave + 8 * i + bsub, false) + off_); \
-  } while (0)
-#define AXK_G3_STOREB()                                                            \
-  do {                                                                             \
-    _Pragma("unroll") for (int i = 0; i < 8; ++i)                                  \
-      *reinterpret_cast<axk_u32x4*>(sB + (64 * wave + 8 * i + bsub) * kG3LdB + 16 * bc) = bq[i]; \
-  } while (0)
-
   axk_f32x4 acc[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int ks) __attribute__((always_inline)) {
-    const uint16_t* a = sA + (ks & 1) * (kBM * kG2LdA);
-    const int q = ks & 3;
-    uint32_t sc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sc[j] = *reinterpret_cast<const uint16_t*>(sS + (brow[j] + l16) * ldS + 2 * ks);
+
+  // step ks from ring slot BUF (a constant: the loop is unrolled over the ring, so every LDS offset is immediate)
+  auto step = [&](int ks, auto buf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
+    wait_vmcnt<4>();  // this wave's loads of step ks have landed (step ks + 1's four may not have)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of step ks - 1 are done
+    __builtin_amdgcn_s_barrier();  // every wave's step-ks loads landed; every wave is done with step ks - 1
+    asm volatile("" ::: "memory");
+    issue(ks + 2, (BUF + 2) % kGStages);  // into the slot of step ks - 1
+    const unsigned char* sa = smem + BUF * kGStage;
+    const unsigned char* sb = sa + kGAStage;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
       axk_bf16x8 af[4], bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(sB + (brow[j] + l16) * kG3LdB + 32 * q + 16 * kh + 4 * g4);
-        bf[j] = fp4x8_to_bf16x8(w, e8m0_to_f32((sc[j] >> (8 * kh)) & 0xffu));
+        const int r = brow[j] + l16;
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(sb + r * 32 + 16 * (kh ^ ((r >> 3) & 1)) + 4 * g4);
+        const uint32_t sbyte = sS[r * ldS + 2 * ks + kh];  // one E8M0 byte: two VALU to an fp32 scale
+        bf[j] = fp4x8_to_bf16x8(w, e8m0_to_f32(sbyte));
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) af[mt] = load_bf16x8(a + (16 * mt + l16) * kG2LdA + 32 * kh + 8 * g4);
+      for (int mt = 0; mt < 4; ++mt) {
+        const int r = 16 * mt + l16;
+        af[mt] = *reinterpret_cast<const axk_bf16x8*>(sa + r * 128 + 16 * ((4 * kh + g4) ^ (r & 7)));
+      }
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
     }
   };
-
-  // prologue: A step 0 in LDS, steps 1 and 2 in registers; B super-step 0 in LDS, super-step 1 in registers
-  uint4 a00, a10, a01, a11, a02, a12, a03, a13;
-  AXK_G3_LOADA(a00, a10, 0);
-  AXK_G3_LOADB(0);
-  AXK_G3_LOADA(a01, a11, 1);
-  AXK_G3_LOADA(a02, a12, 2);
-  AXK_G3_STOREA(a00, a10, 0);
-  AXK_G3_STOREB();
-  AXK_G3_LOADB(1);
-  __syncthreads();
-  // K step ks: A step ks + 3 is loaded, ks computed from A buffer ks & 1 and B quarter ks & 3, A step ks + 1
-  // goes to LDS; at the end of a super-step the next one's B goes to LDS and the one after is loaded. Four A
-  // register sets rotate with the super-step, so every load is unconditional and every wait exact.
-#define AXK_G3_STEP(ks, AN0, AN1, AL0, AL1, LAST)                                  \
-  do {                                                                             \
-    AXK_G3_LOADA(AL0, AL1, (ks) + 3);                                              \
-    if ((ks) < nk) compute(ks);                                                    \
-    AXK_G3_STOREA(AN0, AN1, ((ks) + 1) & 1);                                       \
-    if (LAST) {                                                                    \
-      __syncthreads();                                                             \
-      AXK_G3_STOREB();                                                             \
-      AXK_G3_LOADB(((ks) >> 2) + 2);                                               \
-    }                                                                              \
-    __syncthreads();                                                               \
-  } while (0)
-  for (int ks = 0; ks < nk; ks += 4) {
-    AXK_G3_STEP(ks, a01, a11, a03, a13, false);
-    AXK_G3_STEP(ks + 1, a02, a12, a00, a10, false);
-    AXK_G3_STEP(ks + 2, a03, a13, a01, a11, false);
-    AXK_G3_STEP(ks + 3, a00, a10, a02, a12, true);
+  static_assert(kGStages == 3, "the K loop is unrolled over three ring slots");
+  for (int ks = 0; ks < nk; ks += 3) {
+    step(ks, std::integral_constant<int, 0>{});
+    if (ks + 1 < nk) step(ks + 1, std::integral_constant<int, 1>{});
+    if (ks + 2 < nk) step(ks + 2, std::integral_constant<int, 2>{});
   }
-#undef AXK_G3_STEP
-#undef AXK_G3_LOADA
-#undef AXK_G3_STOREA
-#undef AXK_G3_LOADB
-#undef AXK_G3_STOREB
+  wait_vmcnt<0>();  // the look-ahead loads land before the workgroup's LDS is released
 
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -1322,7 +1291,7 @@ __global__ __launch_bounds__(256) void moe_ggemm3_kernel(GGemmArgs g) {
           const int col = col0 + 32 * wave + 16 * j + l16;
           if (col >= No) continue;
           const float gv = round_bf16(acc[mt][j][r]), uv = round_bf16(acc[mt][j + 2][r]);
-          const uint16_t a = (uint16_t)f32_to_bf16_bits(silu_f32(gv) * uv);
+          const uint16_t a = (uint16_t)f32_to_bf16_bits(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
           if (shared)
             g.ws.act_sh[prow * g.Fs + col] = a;
           else
@@ -1429,21 +1398,21 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
     const int fmax = F > Fs ? F : Fs;
     GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, fmax, w};
-    const size_t lds0 = g3_lds_bytes(H), lds1 = g3_lds_bytes(fmax);
-    static bool g3_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-    if (!g3_raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm3_kernel<0>),
+    const size_t lds0 = gemm_lds_bytes(H), lds1 = gemm_lds_bytes(fmax);
+    static bool gemm_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+    if (!gemm_raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm_kernel<0>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess ||
-          hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm3_kernel<1>),
+          hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm_kernel<1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
         return AXK_E_LAUNCH;
-      g3_raised = true;
+      gemm_raised = true;
     }
     const unsigned nb0 = (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0), nb1 = (unsigned)((H + kG2Cols1 - 1) / kG2Cols1);
     auto xgrid = [](unsigned n) { return dim3((n + kXcds - 1) / kXcds * kXcds); };  // whole rounds over the XCDs
-    hipLaunchKernelGGL(moe_ggemm3_kernel<0>, xgrid(tiles * nb0), dim3(256), lds0, st, gu);
+    hipLaunchKernelGGL(moe_ggemm_kernel<0>, xgrid(tiles * nb0), dim3(256), lds0, st, gu);
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
-    hipLaunchKernelGGL(moe_ggemm3_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
+    hipLaunchKernelGGL(moe_ggemm_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
     hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
                        dim3(256), 0, st, ca);

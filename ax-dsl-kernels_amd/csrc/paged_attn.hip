@@ -208,34 +208,6 @@ AXK_DEV uint32_t f32_to_e4m3(float v) {
   return sgn | (ex << 3) | m3;
 }
 
-// LDS byte address of a __shared__ pointer (for M0).
-AXK_DEV uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// Direct HBM -> LDS load: lane l's 16 bytes at gptr land at lds_base + 16 l (lds_base wave-uniform).
-// Issued from asm on purpose: the compiler then counts none of these loads, so its own waits can only
-// over-wait, and the pipeline waits below (s_waitcnt vmcnt(n)) stay exactly as written. M0 is restored.
-// Non-temporal (nt): every K / V byte is read once per launch, so the loads should not displace cached lines
-// (measured: 62.1 -> 55.9 us for the config-1 split kernel, 5.0 -> 5.6 TB/s).
-AXK_DEV void lds_dma16(const void* gptr, uint32_t lds_base_any) {
-  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
-  uint32_t save;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off nt\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(save)
-      : "s"(lds_base), "v"(gptr)
-      : "memory");
-}
-
-template <int N>
-AXK_DEV void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 typedef short axk_i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLocalPlanBatch = 63;  // up to this many sequences the kernels derive the plan themselves
