@@ -103,6 +103,11 @@ SIGNATURES: dict[str, list] = {
                               ctypes.c_size_t, _vp],
     "axk_attn_layer_decode": [_vp] * 27 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                               ctypes.c_size_t, _vp],
+    "axk_gdn_layer_moe_workspace_size": [_i64] * 6 + [_vp],
+    "axk_attn_layer_moe_workspace_size": [_i64] * 6 + [_vp],
+    "axk_gdn_layer_decode_moe": [_vp] * 29 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_attn_layer_decode_moe": [_vp] * 28 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
+                                  ctypes.c_size_t, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,
@@ -114,7 +119,19 @@ _RESTYPES = {
     "axk_attn_layer_workspace_size": ctypes.c_size_t,
     "axk_gdn_layer_verify_workspace_size": ctypes.c_size_t,
     "axk_attn_layer_verify_workspace_size": ctypes.c_size_t,
+    "axk_gdn_layer_moe_workspace_size": ctypes.c_size_t,
+    "axk_attn_layer_moe_workspace_size": ctypes.c_size_t,
 }
+
+
+class MoeBlock(ctypes.Structure):
+    """axk_moe_block of include/axk.h: the MoE block of the MoE decode layers (device pointers and sizes)."""
+
+    _fields_ = [("w_router", ctypes.c_void_p), ("w_shg", ctypes.c_void_p), ("e_gw", ctypes.c_void_p),
+                ("e_gs", ctypes.c_void_p), ("e_dw", ctypes.c_void_p), ("e_ds", ctypes.c_void_p),
+                ("num_experts", ctypes.c_int64), ("top_k", ctypes.c_int64), ("expert_inter", ctypes.c_int64),
+                ("norm_topk_prob", ctypes.c_int32), ("reserved", ctypes.c_int32), ("logits", ctypes.c_void_p),
+                ("topk_ids", ctypes.c_void_p), ("topk_weights", ctypes.c_void_p)]
 
 
 def header_symbols(path: str = HEADER_PATH) -> list[str]:

@@ -117,6 +117,19 @@ def moe_weights(g: torch.Generator, hidden: int = 2048, experts: int = 256, inte
     return w
 
 
+def moe_block(g: torch.Generator, hidden: int, experts: int = 256, inter: int = 512, top_k: int = 8,
+              router_std: float = 0.02) -> dict:
+    """The MoE block of a MoE decode layer beside the layer's MLP weights (its shared expert): bf16 router and
+    shared-expert gate ~ N(0, router_std), MXFP4 routed experts as config 3 (nibbles uniform, scale bytes 119..123),
+    top_k. Draw order: router, w_shg, e_gw/e_gs, e_dw/e_ds."""
+    w = {"w_router": (torch.randn(experts, hidden, generator=g) * router_std).to(torch.bfloat16),
+         "w_shg": (torch.randn(hidden, generator=g) * router_std).to(torch.bfloat16)}
+    w["e_gw"], w["e_gs"] = mxfp4_weight(2 * inter, hidden, g, lead=(experts,))
+    w["e_dw"], w["e_ds"] = mxfp4_weight(hidden, inter, g, lead=(experts,))
+    w["top_k"] = top_k
+    return w
+
+
 def config3(tokens: int = 32, seed: int = 0):
     """Config 3: MoE layer, hidden 2048, 256 routed experts (inter 512) + 1 shared expert (inter 512), top-8,
     activations ~ N(0,1) at `tokens` (32 = decode, 4096 = prefill); x_res ~ N(0,1) residual."""

@@ -12,6 +12,7 @@ norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -38,16 +39,66 @@ def _weights(w: dict, names) -> list:
     return [w[n] for n in names]
 
 
+MOE_WEIGHTS = ("w_router", "e_gw", "e_gs", "e_dw", "e_ds")
+
+
+def moe_block(moe: dict) -> _lib.MoeBlock:
+    """The axk_moe_block of a MoE block (moe_full, q35_layer_mc.py:797-853) given as a dict: w_router bf16 [E, H],
+    w_shg bf16 [H] (optional: the shared expert's sigmoid gate), the routed experts e_gw / e_gs [E, 2 F, H/2 | H/32]
+    and e_dw / e_ds [E, H, F/2 | F/32] (MXFP4, the manifest's planar layout), top_k, norm_topk_prob (default True),
+    and optional routing outputs logits f32 [B, E], topk_ids int32 [B, K], topk_weights f32 [B, K].
+    The shared expert is the layer's MLP weights (w_gate .. s_down) in mlp_fmt."""
+    _weights(moe, MOE_WEIGHTS)
+    shg = moe.get("w_shg")
+    _check(shg is None or shg.is_contiguous(), "w_shg must be contiguous")
+    e, two_f = moe["e_gw"].shape[0], moe["e_gw"].shape[1]
+    _check("top_k" in moe, "the MoE block needs top_k")
+    m = _lib.MoeBlock()
+    m.w_router, m.e_gw, m.e_gs, m.e_dw, m.e_ds = (moe[n].data_ptr() for n in MOE_WEIGHTS)
+    m.w_shg = _lib.ptr(shg)
+    m.num_experts, m.top_k, m.expert_inter = e, int(moe["top_k"]), two_f // 2
+    m.norm_topk_prob = 1 if moe.get("norm_topk_prob", True) else 0
+    for n, dt, cols in (("logits", torch.float32, e), ("topk_ids", torch.int32, m.top_k),
+                        ("topk_weights", torch.float32, m.top_k)):
+        t = moe.get(n)
+        _check(t is None or (t.dtype == dt and t.dim() == 2 and t.shape[1] == cols and t.is_contiguous()),
+               f"{n} must be contiguous {dt} [B, {cols}]")
+        setattr(m, n, _lib.ptr(t))
+    return m
+
+
+def _moe_tensors(moe: Optional[dict]) -> list:
+    """The MoE block's tensors (for the device check)."""
+    if moe is None:
+        return []
+    return [moe[n] for n in MOE_WEIGHTS] + [moe[n] for n in ("w_shg", "logits", "topk_ids", "topk_weights")
+                                            if moe.get(n) is not None]
+
+
 def gdn_workspace(batch: int, hidden: int, num_k_heads: int, num_v_heads: int, inter: int,
-                  device, head_dim: int = 128) -> torch.Tensor:
-    n = _lib.load().axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter)
+                  device, head_dim: int = 128, moe: Optional[dict] = None) -> torch.Tensor:
+    """The workspace of gdn_layer_decode (with moe: of its MoE form)."""
+    lib = _lib.load()
+    if moe is None:
+        n = lib.axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter)
+    else:
+        m = moe_block(moe)
+        n = lib.axk_gdn_layer_moe_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter,
+                                                 ctypes.addressof(m))
     _check(n > 0, "unsupported GDN layer shape")
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def attn_workspace(batch: int, hidden: int, num_qo_heads: int, num_kv_heads: int, head_dim: int, inter: int,
-                   device) -> torch.Tensor:
-    n = _lib.load().axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter)
+                   device, moe: Optional[dict] = None) -> torch.Tensor:
+    """The workspace of attn_layer_decode (with moe: of its MoE form)."""
+    lib = _lib.load()
+    if moe is None:
+        n = lib.axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter)
+    else:
+        m = moe_block(moe)
+        n = lib.axk_attn_layer_moe_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter,
+                                                  ctypes.addressof(m))
     _check(n > 0, "unsupported attention layer shape")
     return torch.empty(n, dtype=torch.uint8, device=device)
 
@@ -60,24 +111,34 @@ def _fmt(name: str) -> int:
 def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: torch.Tensor,
                      num_k_heads: int, num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                      out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
-                     conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+                     conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
+                     moe: Optional[dict] = None):
     """x bf16 [B, hidden]; state f32 [B, NV, 128, 128]; conv state bf16 [B, K-1, 2 KD + VD].
-    Returns (out, state_out, conv_out); state_out / conv_out may be the inputs (in place)."""
+    Returns (out, state_out, conv_out); state_out / conv_out may be the inputs (in place).
+    moe (optional, see moe_block): the MLP is the MoE block, whose shared expert is the MLP weights
+    (gdn_layer_full_mx, q35_layer_mc.py:855-866)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
     b, h = x.shape
     inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
-    ws = workspace if workspace is not None else gdn_workspace(b, h, num_k_heads, num_v_heads, inter, x.device)
+    ws = workspace if workspace is not None else gdn_workspace(b, h, num_k_heads, num_v_heads, inter, x.device,
+                                                               moe=moe)
     o = torch.empty_like(x) if out is None else out
     so = torch.empty_like(state_in) if state_out is None else state_out
     co = torch.empty_like(conv_in) if conv_out is None else conv_out
     args = _weights(w, GDN_WEIGHTS) + _weights(w, MLP_WEIGHTS)
-    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args)
+    extra = _moe_tensors(moe)
+    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args, *extra)
     ptrs = [t.data_ptr() for t in args]
-    # the C order: x, ln1 .. s_out, ln2, MLP, state_in, conv_in, out, state_out, conv_out
-    _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
-              so.data_ptr(), co.data_ptr(), b, h, num_k_heads, num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt),
-              _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    tail = (state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(), so.data_ptr(), co.data_ptr(), b, h, num_k_heads,
+            num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(),
+            _lib.stream_of(x))
+    # the C order: x, ln1 .. s_out, ln2, MLP, [moe], state_in, conv_in, out, state_out, conv_out
+    if moe is None:
+        _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, *tail)
+    else:
+        m = moe_block(moe)
+        _lib.call("axk_gdn_layer_decode_moe", x.data_ptr(), *ptrs, ctypes.addressof(m), *tail)
     return o, so, co
 
 
@@ -85,26 +146,35 @@ def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
                       indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
                       cache_location: torch.Tensor, num_qo_heads: int, rot: int, eps: float = 1e-6,
                       sm_scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
-                      out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4") -> torch.Tensor:
+                      out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
+                      moe: Optional[dict] = None) -> torch.Tensor:
     """x bf16 [B, hidden]; kv_cache bf16 [P, 2, page, HKV, D] written in place at cache_location (int32 [B, 2]);
-    the page table describes each sequence including the new token; cos, sin bf16 [B, rot/2]."""
+    the page table describes each sequence including the new token; cos, sin bf16 [B, rot/2].
+    moe (optional, see moe_block): the MLP is the MoE block (attn_layer_full_mx, q35_layer_mc.py:867-880)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
     b, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
     inter = w["w_gate"].shape[0]
-    ws = workspace if workspace is not None else attn_workspace(b, h, num_qo_heads, hkv, d, inter, x.device)
+    ws = workspace if workspace is not None else attn_workspace(b, h, num_qo_heads, hkv, d, inter, x.device, moe=moe)
     o = torch.empty_like(x) if out is None else out
     scale = d ** -0.5 if sm_scale is None else sm_scale
     wa = _weights(w, ATTN_WEIGHTS)
     mlp = _weights(w, MLP_WEIGHTS)
-    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp)
+    extra = _moe_tensors(moe)
+    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp,
+                        *extra)
     (ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, w_o, s_o, ln2) = wa
-    _lib.call("axk_attn_layer_decode", x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(), w_k.data_ptr(),
-              s_k.data_ptr(), w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
-              _lib.ptr(cos), _lib.ptr(sin), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
-              last_page_len.data_ptr(), cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(),
-              *[t.data_ptr() for t in mlp], o.data_ptr(), b, h, num_qo_heads, hkv, d, rot, page, pages, inter, eps,
-              scale, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    head = (x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(), w_k.data_ptr(), s_k.data_ptr(),
+            w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(), _lib.ptr(cos), _lib.ptr(sin),
+            kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(), last_page_len.data_ptr(),
+            cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(), *[t.data_ptr() for t in mlp])
+    tail = (o.data_ptr(), b, h, num_qo_heads, hkv, d, rot, page, pages, inter, eps, scale, _fmt(proj_fmt),
+            _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    if moe is None:
+        _lib.call("axk_attn_layer_decode", *head, *tail)
+    else:
+        m = moe_block(moe)
+        _lib.call("axk_attn_layer_decode_moe", *head, ctypes.addressof(m), *tail)
     return o
 
 

@@ -118,3 +118,13 @@ __attribute__((visibility("hidden"))) int axk_attn_qkv_prep(
     const uint16_t* cos, const uint16_t* sin, uint16_t* q_out, uint16_t* kv_cache, const int32_t* cache_location,
     int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages,
     float eps, hipStream_t stream);
+
+// Internal (not exported): axk_moe_decode with the shared expert computed by the caller: y_sh [tokens, hidden] fp32
+// is its down projection (any weight format), gated by sigmoid(h2 . w_shg) in the combine as the library's own
+// shared expert is; the routed experts and routing as axk_moe_decode. Size the workspace with
+// axk_moe_workspace_size(..., shared_inter = 0). Returns an AXK status; a nonzero one means nothing was launched.
+__attribute__((visibility("hidden"))) int axk_moe_decode_shared_given(
+    const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router, const uint16_t* w_shg, const float* y_sh,
+    const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
+    int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
+    int64_t inter, int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream);

@@ -80,6 +80,56 @@ int mlp_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const M
                       nullptr, axk_stream(st));
 }
 
+// The MoE block's buffers beside the dense MLP's (whose act holds the shared expert's activations).
+struct MoeBufs {
+  float* y_sh;     // [B, H] the shared expert's fp32 output
+  float* logits;   // [B, E]
+  int32_t* ids;    // [B, K]
+  float* wts;      // [B, K]
+  void* mws;       // the routed experts' workspace
+  size_t mws_bytes;
+};
+
+// Shapes the MoE block takes beside the layer's (0 when unsupported).
+size_t moe_ws_bytes(int64_t B, int64_t H, const axk_moe_block& m) {
+  if (m.num_experts <= 0 || m.top_k <= 0 || m.expert_inter <= 0) return 0;
+  return axk_moe_workspace_size(B, H, m.num_experts, m.top_k, m.expert_inter, 0);
+}
+
+MoeBufs carve_moe(Carver& c, int64_t B, int64_t H, const axk_moe_block& m) {
+  MoeBufs e;
+  e.y_sh = c.take<float>(B * H);
+  e.logits = c.take<float>(B * m.num_experts);
+  e.ids = c.take<int32_t>(B * m.top_k);
+  e.wts = c.take<float>(B * m.top_k);
+  if (c.base) {  // the caller's routing outputs where given
+    if (m.logits) e.logits = m.logits;
+    if (m.topk_ids) e.ids = m.topk_ids;
+    if (m.topk_weights) e.wts = m.topk_weights;
+  }
+  e.mws_bytes = moe_ws_bytes(B, H, m);
+  e.mws = c.take<unsigned char>(e.mws_bytes);
+  return e;
+}
+
+// moe_full (q35_layer_mc.py:797-853) after the layer's first half: x1 = x + y; h2 = rmsnorm(x1, ln2); the shared
+// expert (the layer's MLP weights in wfmt: gate | up with SwiGLU, then down into fp32 y_sh); the router, top-K and
+// the routed MXFP4 experts, whose combine writes out = x1 + sigmoid(h2 . w_shg) y_sh + the routed sum.
+int moe_residual(const uint16_t* x, const uint16_t* y, const float* ln2, const MlpWeights& w, int wfmt,
+                 const axk_moe_block& m, uint16_t* out, const MlpBufs& mb, const MoeBufs& eb, int64_t B, int64_t H,
+                 int64_t F, float eps, axk_stream_t st) {
+  AXK_TRY(axk_add_rmsnorm(x, y, ln2, mb.x1, mb.h2, B, H, eps, st));
+  const AxkMxMat gate_up[2] = {proj_mat(wfmt, w.gate_w, w.gate_s, mb.act, F), proj_mat(wfmt, w.up_w, w.up_s, mb.act, F)};
+  AXK_TRY(axk_mx_group(mx_fmt_of(wfmt), mb.h2, H, gate_up, 2, AXK_MX_EPI_SWIGLU, nullptr, 0, nullptr, AXK_DT_BF16, B,
+                       H, nullptr, axk_stream(st)));
+  const AxkMxMat down = proj_mat(wfmt, w.down_w, w.down_s, eb.y_sh, H);
+  AXK_TRY(axk_mx_group(mx_fmt_of(wfmt), mb.act, F, &down, 1, AXK_MX_EPI_PLAIN, nullptr, 0, nullptr, AXK_DT_F32, B, F,
+                       nullptr, axk_stream(st)));
+  return axk_moe_decode_shared_given(mb.h2, mb.x1, m.w_router, m.w_shg, eb.y_sh, m.e_gw, m.e_gs, m.e_dw, m.e_ds, out,
+                                     eb.logits, eb.ids, eb.wts, B, H, m.num_experts, m.top_k, m.expert_inter,
+                                     m.norm_topk_prob, eb.mws, eb.mws_bytes, st);
+}
+
 // Projections of one input a [m, k] in weight format wfmt (bf16 outputs) as one grouped launch; conv (optional)
 // runs the causal conv1d + SiLU on the first matrix's output.
 int projs(int wfmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int64_t m, int64_t k,
@@ -138,37 +188,41 @@ int check_common(int64_t B, int64_t H, int64_t F) {
 
 }  // namespace
 
-extern "C" size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads,
-                                               int64_t num_v_heads, int64_t head_dim, int64_t inter) {
-  if (check_common(batch, hidden, inter) != AXK_OK || head_dim != 128 || num_k_heads <= 0 || num_v_heads <= 0 ||
-      num_v_heads % num_k_heads != 0)
-    return 0;
+namespace {
+
+// Workspace of a GDN decode layer, with the MoE block's buffers after the layer's when moe is given.
+size_t gdn_ws_bytes(int64_t B, int64_t H, int64_t NK, int64_t NV, int64_t DH, int64_t F, const axk_moe_block* moe) {
+  if (check_common(B, H, F) != AXK_OK || DH != 128 || NK <= 0 || NV <= 0 || NV % NK != 0) return 0;
+  if (moe && moe_ws_bytes(B, H, *moe) == 0) return 0;
   Carver c{nullptr};
-  carve_gdn(c, batch, hidden, num_k_heads, num_v_heads, head_dim, inter);
+  carve_gdn(c, B, H, NK, NV, DH, F);
+  if (moe) carve_moe(c, B, H, *moe);
   return c.off;
 }
 
-extern "C" int axk_gdn_layer_decode(
-    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
-    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
-    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
-    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
-    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
-    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
-    int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
-    int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+int gdn_layer_impl(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z,
+                   const void* s_z, const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a,
+                   const uint16_t* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                   const uint8_t* w_out, const void* s_out, const float* ln2, const uint8_t* mlp_gate_w,
+                   const void* mlp_gate_s, const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                   const void* mlp_down_s, const axk_moe_block* moe, const float* state_in, const uint16_t* conv_in,
+                   uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
+                   int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
+                   float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes,
+                   axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
                   mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
               AXK_E_NULL);
   AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
-  const size_t need = axk_gdn_layer_workspace_size(batch, hidden, num_k_heads, num_v_heads, head_dim, inter);
+  const size_t need = gdn_ws_bytes(batch, hidden, num_k_heads, num_v_heads, head_dim, inter, moe);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
   const int64_t B = batch, H = hidden, NK = num_k_heads, NV = num_v_heads, DH = head_dim, F = inter;
   const int64_t KD = NK * DH, VD = NV * DH, C = 2 * KD + VD;
   Carver c{static_cast<unsigned char*>(workspace)};
   const GdnBufs g = carve_gdn(c, B, H, NK, NV, DH, F);
+  const MoeBufs eb = moe ? carve_moe(c, B, H, *moe) : MoeBufs{};
   const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, B, H, eps, stream));
@@ -185,6 +239,7 @@ extern "C" int axk_gdn_layer_decode(
                                       state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
     const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
     AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, B, VD, stream));
+    if (moe) return moe_residual(x, g.y, ln2, mw, mlp_fmt, *moe, out, g.mlp, eb, B, H, F, eps, stream);
     return mlp_residual(x, g.y, ln2, mw, mlp_fmt, out, g.mlp, B, H, F, eps, stream);
   };
   {
@@ -194,37 +249,38 @@ extern "C" int axk_gdn_layer_decode(
   return body();
 }
 
-extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
-                                                int64_t num_kv_heads, int64_t head_dim, int64_t inter) {
-  if (check_common(batch, hidden, inter) != AXK_OK || axk_paged_decode_workspace_size(batch, num_qo_heads,
-                                                                                      num_kv_heads, head_dim) == 0)
-    return 0;
+// Workspace of an attention decode layer, with the MoE block's buffers after the layer's when moe is given.
+size_t attn_ws_bytes(int64_t B, int64_t H, int64_t HQ, int64_t HKV, int64_t D, int64_t F, const axk_moe_block* moe) {
+  if (check_common(B, H, F) != AXK_OK || axk_paged_decode_workspace_size(B, HQ, HKV, D) == 0) return 0;
+  if (moe && moe_ws_bytes(B, H, *moe) == 0) return 0;
   Carver c{nullptr};
-  carve_attn(c, batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+  carve_attn(c, B, H, HQ, HKV, D, F);
+  if (moe) carve_moe(c, B, H, *moe);
   return c.off;
 }
 
-extern "C" int axk_attn_layer_decode(
-    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
-    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
-    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
-    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
-    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
-    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, uint16_t* out, int64_t batch,
-    int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
-    int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
-    size_t workspace_bytes, axk_stream_t stream) {
+int attn_layer_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k,
+                    const void* s_k, const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm,
+                    const uint16_t* cos, const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr,
+                    const int32_t* indices, const int32_t* last_page_len, const int32_t* cache_location,
+                    const uint8_t* w_o, const void* s_o, const float* ln2, const uint8_t* mlp_gate_w,
+                    const void* mlp_gate_s, const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                    const void* mlp_down_s, const axk_moe_block* moe, uint16_t* out, int64_t batch, int64_t hidden,
+                    int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
+                    int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt,
+                    void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
                   indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
                   mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
               AXK_E_NULL);
   AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
-  const size_t need = axk_attn_layer_workspace_size(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+  const size_t need = attn_ws_bytes(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter, moe);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
   const int64_t B = batch, H = hidden, HQ = num_qo_heads, HKV = num_kv_heads, D = head_dim, F = inter;
   Carver c{static_cast<unsigned char*>(workspace)};
   const AttnBufs a = carve_attn(c, B, H, HQ, HKV, D, F);
+  const MoeBufs eb = moe ? carve_moe(c, B, H, *moe) : MoeBufs{};
   const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, B, H, eps, stream));
@@ -238,6 +294,7 @@ extern "C" int axk_attn_layer_decode(
     AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, B * HQ, D, stream));
     const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
     AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, B, HQ * D, stream));
+    if (moe) return moe_residual(x, a.y, ln2, mw, mlp_fmt, *moe, out, a.mlp, eb, B, H, F, eps, stream);
     return mlp_residual(x, a.y, ln2, mw, mlp_fmt, out, a.mlp, B, H, F, eps, stream);
   };
   {
@@ -245,6 +302,97 @@ extern "C" int axk_attn_layer_decode(
     AXK_TRY(body());
   }
   return body();
+}
+
+}  // namespace
+
+extern "C" size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads,
+                                               int64_t num_v_heads, int64_t head_dim, int64_t inter) {
+  return gdn_ws_bytes(batch, hidden, num_k_heads, num_v_heads, head_dim, inter, nullptr);
+}
+
+extern "C" int axk_gdn_layer_decode(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
+    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
+    int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+    int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  return gdn_layer_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
+                        s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, nullptr,
+                        state_in, conv_in, out, state_out, conv_out, batch, hidden, num_k_heads, num_v_heads,
+                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t axk_gdn_layer_moe_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads,
+                                                   int64_t num_v_heads, int64_t head_dim, int64_t inter,
+                                                   const axk_moe_block* moe) {
+  return moe ? gdn_ws_bytes(batch, hidden, num_k_heads, num_v_heads, head_dim, inter, moe) : 0;
+}
+
+extern "C" int axk_gdn_layer_decode_moe(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
+    const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
+    int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel,
+    int64_t inter, float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes,
+    axk_stream_t stream) {
+  AXK_REQUIRE(moe, AXK_E_NULL);
+  return gdn_layer_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
+                        s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, moe,
+                        state_in, conv_in, out, state_out, conv_out, batch, hidden, num_k_heads, num_v_heads,
+                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
+                                                int64_t num_kv_heads, int64_t head_dim, int64_t inter) {
+  return attn_ws_bytes(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter, nullptr);
+}
+
+extern "C" int axk_attn_layer_decode(
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
+    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, uint16_t* out, int64_t batch,
+    int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
+    int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
+    size_t workspace_bytes, axk_stream_t stream) {
+  return attn_layer_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
+                         last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
+                         mlp_down_w, mlp_down_s, nullptr, out, batch, hidden, num_qo_heads, num_kv_heads, head_dim,
+                         rot, page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace,
+                         workspace_bytes, stream);
+}
+
+extern "C" size_t axk_attn_layer_moe_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
+                                                    int64_t num_kv_heads, int64_t head_dim, int64_t inter,
+                                                    const axk_moe_block* moe) {
+  return moe ? attn_ws_bytes(batch, hidden, num_qo_heads, num_kv_heads, head_dim, inter, moe) : 0;
+}
+
+extern "C" int axk_attn_layer_decode_moe(
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
+    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
+    uint16_t* out, int64_t batch, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t rot, int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt,
+    int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(moe, AXK_E_NULL);
+  return attn_layer_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
+                         last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
+                         mlp_down_w, mlp_down_s, moe, out, batch, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
+                         page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace, workspace_bytes,
+                         stream);
 }
 
 // ---------------------------------------------------------------------------------------------

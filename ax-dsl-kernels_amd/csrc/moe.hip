@@ -1363,17 +1363,22 @@ extern "C" int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk
 
 namespace {
 // The experts half. grouped: the decode grouping already ran (in the routing launch's last workgroup); check_only: run the
-// contract checks and return before any launch.
+// contract checks and return before any launch. y_sh_given (optional, with no MXFP4 shared expert): the shared
+// expert's fp32 output [T, H], computed by the caller; the combine gates and adds it as its own.
 int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg, const uint8_t* sh_gate_w,
                      const uint8_t* sh_gate_s, const uint8_t* sh_up_w, const uint8_t* sh_up_s,
                      const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
                      const uint8_t* e_dw, const uint8_t* e_ds, const int32_t* topk_ids, const float* topk_weights,
                      uint16_t* out, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
                      int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream, bool grouped,
-                     bool check_only) {
+                     bool check_only, const float* y_sh_given = nullptr) {
   AXK_REQUIRE(h2 && e_gw && e_gs && e_dw && e_ds && topk_ids && topk_weights && out, AXK_E_NULL);
   const bool has_shared = sh_gate_w != nullptr;
   AXK_REQUIRE(!has_shared || (sh_gate_s && sh_up_w && sh_up_s && sh_down_w && sh_down_s), AXK_E_NULL);
+  AXK_REQUIRE(!(has_shared && y_sh_given), AXK_E_NULL);  // one shared expert or the other
+  AXK_REQUIRE(!y_sh_given || axk_aligned(y_sh_given, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(!y_sh_given || !axk_overlap(y_sh_given, (size_t)tokens * hidden * 4, out, (size_t)tokens * hidden * 2),
+              AXK_E_ALIAS);
   const MoeDims d{tokens, hidden, num_experts, top_k, inter, has_shared ? shared_inter : 0};
   const int rc = check_dims(d);
   if (rc != AXK_OK) return rc;
@@ -1388,7 +1393,9 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
               AXK_E_ALIAS);
   if (check_only) return AXK_OK;
   hipStream_t st = axk_stream(stream);
-  const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, d.Fs);
+  MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, d.Fs);
+  if (y_sh_given) w.y_sh = const_cast<float*>(y_sh_given);  // read only (by the combine)
+  const int combine_shared = (has_shared || y_sh_given) ? 1 : 0;
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, F = (int)inter, Fs = (int)d.Fs;
   if (T > kDecodeTokens) {
     const int NB = (int)prefill_blocks(T);
@@ -1413,7 +1420,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     hipLaunchKernelGGL(moe_ggemm_kernel<0>, xgrid(tiles * nb0), dim3(256), lds0, st, gu);
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
     hipLaunchKernelGGL(moe_ggemm_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
-    CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
+    CombineArgs ca{h2, x_res, w_shg, combine_shared, T, H, K, w, out};
     hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
                        dim3(256), 0, st, ca);
     return axk_launch_status();
@@ -1465,7 +1472,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     hipLaunchKernelGGL((moe_down_kernel<true, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   else
     hipLaunchKernelGGL((moe_down_kernel<false, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
-  CombineArgs ca{h2, x_res, w_shg, has_shared ? 1 : 0, T, H, K, w, out};
+  CombineArgs ca{h2, x_res, w_shg, combine_shared, T, H, K, w, out};
   hipLaunchKernelGGL(moe_combine_kernel<false>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
                      dim3(256), 0, st, ca);
   return axk_launch_status();
@@ -1484,14 +1491,14 @@ extern "C" int axk_moe_experts(const uint16_t* h2, const uint16_t* x_res, const 
                           shared_inter, workspace, workspace_bytes, stream, false, false);
 }
 
-extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router,
-                              const uint16_t* w_shg, const uint8_t* sh_gate_w, const uint8_t* sh_gate_s,
-                              const uint8_t* sh_up_w, const uint8_t* sh_up_s, const uint8_t* sh_down_w,
-                              const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
-                              const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
-                              int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden,
-                              int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
-                              int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+namespace {
+int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router, const uint16_t* w_shg,
+                    const uint8_t* sh_gate_w, const uint8_t* sh_gate_s, const uint8_t* sh_up_w, const uint8_t* sh_up_s,
+                    const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
+                    const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits, int32_t* topk_ids,
+                    float* topk_weights, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
+                    int64_t inter, int64_t shared_inter, int norm_topk_prob, void* workspace, size_t workspace_bytes,
+                    axk_stream_t stream, const float* y_sh_given) {
   AXK_REQUIRE(w_router && logits, AXK_E_NULL);
   AXK_REQUIRE(h2 && topk_ids && topk_weights, AXK_E_NULL);
   int rc = check_dims({tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0});
@@ -1502,8 +1509,9 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
   // the experts half's checks before anything is launched (a nonzero status means nothing was enqueued)
   rc = moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
                         e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
-                        shared_inter, workspace, workspace_bytes, stream, false, true);
+                        shared_inter, workspace, workspace_bytes, stream, false, true, y_sh_given);
   if (rc != AXK_OK) return rc;
+  AXK_LAUNCH_GATE();
   const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k;
   const bool prefill = T > kDecodeTokens;
@@ -1545,5 +1553,31 @@ extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const u
   if (rc != AXK_OK) return rc;
   return moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
                           e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
-                          shared_inter, workspace, workspace_bytes, stream, grouped, false);
+                          shared_inter, workspace, workspace_bytes, stream, grouped, false, y_sh_given);
+}
+}  // namespace
+
+extern "C" int axk_moe_decode(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router,
+                              const uint16_t* w_shg, const uint8_t* sh_gate_w, const uint8_t* sh_gate_s,
+                              const uint8_t* sh_up_w, const uint8_t* sh_up_s, const uint8_t* sh_down_w,
+                              const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
+                              const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
+                              int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden,
+                              int64_t num_experts, int64_t top_k, int64_t inter, int64_t shared_inter,
+                              int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  return moe_decode_impl(h2, x_res, w_router, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s,
+                         e_gw, e_gs, e_dw, e_ds, out, logits, topk_ids, topk_weights, tokens, hidden, num_experts,
+                         top_k, inter, shared_inter, norm_topk_prob, workspace, workspace_bytes, stream, nullptr);
+}
+
+int axk_moe_decode_shared_given(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_router,
+                                const uint16_t* w_shg, const float* y_sh, const uint8_t* e_gw, const uint8_t* e_gs,
+                                const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
+                                int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden,
+                                int64_t num_experts, int64_t top_k, int64_t inter, int norm_topk_prob,
+                                void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(y_sh, AXK_E_NULL);
+  return moe_decode_impl(h2, x_res, w_router, w_shg, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, e_gw, e_gs,
+                         e_dw, e_ds, out, logits, topk_ids, topk_weights, tokens, hidden, num_experts, top_k, inter, 0,
+                         norm_topk_prob, workspace, workspace_bytes, stream, y_sh);
 }

@@ -501,6 +501,72 @@ int axk_attn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_
                           int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * MoE decode layers: the decode layers above with the MLP replaced by the 35B's MoE block, moe_full of
+ * models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:797-853 (inside gdn_layer_full_mx / attn_layer_full_mx, :855-880):
+ *   x1 = x + y (y: the attention / GDN half's output projection); h2 = rmsnorm(x1, ln2);
+ *   sh = bf16(silu(bf16(h2 gate^T)) * bf16(h2 up^T)) down^T in fp32: the shared expert, the layer's MLP weights
+ *        mlp_gate / mlp_up [inter, hidden], mlp_down [hidden, inter] in mlp_fmt (MXFP8 in the 35B manifest);
+ *   logits = h2 w_router^T (fp32); the top_k experts by logit (ties: the lower id) weighted by their softmax
+ *        probabilities, renormalised over the selection when norm_topk_prob;
+ *   out = bf16(x1 + sigmoid(h2 . w_shg) sh + sum_k weight_k bf16(silu(g_k) u_k) down_k^T), the routed experts in
+ *        MXFP4 as axk_moe_decode takes them (the manifest's planar e_gw / e_gs / e_dw / e_ds).
+ * The reference rounds x1 + gate * sh to bf16 before adding the routed sum; here it stays fp32 up to the one final
+ * rounding (at most one bf16 ulp of that sum apart). Decode routes (batch <= 256) run the decode experts; larger
+ * batches the grouped prefill GEMMs. Other arguments, checks and workspace rules as the decode layers.
+ * ------------------------------------------------------------------------------------------- */
+typedef struct axk_moe_block {
+  const uint16_t* w_router; /* bf16 [num_experts, hidden] */
+  const uint16_t* w_shg;    /* bf16 [hidden]: the shared expert's sigmoid gate; null = gate 1 */
+  const uint8_t* e_gw;      /* MXFP4 codes [num_experts, 2 expert_inter, hidden / 2] (gate rows, then up rows) */
+  const uint8_t* e_gs;      /* E8M0 [num_experts, 2 expert_inter, hidden / 32] */
+  const uint8_t* e_dw;      /* MXFP4 codes [num_experts, hidden, expert_inter / 2] */
+  const uint8_t* e_ds;      /* E8M0 [num_experts, hidden, expert_inter / 32] */
+  int64_t num_experts;
+  int64_t top_k;
+  int64_t expert_inter;
+  int32_t norm_topk_prob;
+  int32_t reserved; /* 0 */
+  /* optional outputs (null: kept in the workspace), as the reference's MoE layer kernel stores logits_out / topk
+   * (q35_layer_mc.py:435-449): */
+  float* logits;        /* f32 [batch, num_experts] */
+  int32_t* topk_ids;    /* i32 [batch, top_k], the experts by descending logit */
+  float* topk_weights;  /* f32 [batch, top_k], their routing weights */
+} axk_moe_block;
+
+/* Workspace bytes of axk_gdn_layer_decode_moe / axk_attn_layer_decode_moe (0 = unsupported shape). */
+size_t axk_gdn_layer_moe_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
+                                        int64_t head_dim, int64_t inter, const axk_moe_block* moe);
+size_t axk_attn_layer_moe_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
+                                         int64_t head_dim, int64_t inter, const axk_moe_block* moe);
+
+/* gdn_layer_full_mx (q35_layer_mc.py:855-866): axk_gdn_layer_decode with the MoE block as its MLP. */
+int axk_gdn_layer_decode_moe(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
+                             const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b,
+                             const uint8_t* w_a, const void* s_a, const uint16_t* conv_w, const float* a_log,
+                             const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+                             const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                             const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                             const void* mlp_down_s, const axk_moe_block* moe, const float* state_in,
+                             const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
+                             int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
+                             int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps, int proj_fmt,
+                             int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
+/* attn_layer_full_mx (q35_layer_mc.py:867-880): axk_attn_layer_decode with the MoE block as its MLP. */
+int axk_attn_layer_decode_moe(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q,
+                              const uint8_t* w_k, const void* s_k, const uint8_t* w_v, const void* s_v,
+                              const float* q_norm, const float* k_norm, const uint16_t* cos, const uint16_t* sin,
+                              uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                              const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o,
+                              const void* s_o, const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                              const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                              const void* mlp_down_s, const axk_moe_block* moe, uint16_t* out, int64_t batch,
+                              int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                              int64_t rot, int64_t page_size, int64_t num_pages, int64_t inter, float eps,
+                              float sm_scale, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes,
+                              axk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Speculative verification: the decode layers over `tokens` (1 .. 16) consecutive new rows per sequence in one call,
  * the decode.verify role of models/qwen38_27b/README.md:11 (verify/verify_group_m4.py:1-9: a draft of up to 3 tokens
  * after the last cell checked in one pass; every projection shared by the rows, so each weight is read once; the row

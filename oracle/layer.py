@@ -116,9 +116,55 @@ def mlp_residual(x: torch.Tensor, y: torch.Tensor, w: dict, eps: float, fmt: str
     return add(x1, d)
 
 
+def dequant_weight(w: dict, name: str, fmt: str) -> torch.Tensor:
+    """The fp32 weight w_<name> [N, K] of format fmt, exactly dequantised (as proj multiplies it)."""
+    from oracle import mx
+
+    wt, s = w["w_" + name].numpy(), w["s_" + name]
+    if fmt == "fp8":
+        return torch.from_numpy(mx.e4m3_table()[wt]) * s.float().reshape(-1, 1)
+    if fmt == "mxfp8":
+        return torch.from_numpy(mx.dequant_mxfp8(wt, s.numpy(), "e4m3"))
+    return torch.from_numpy(mx.dequant_mxfp4(wt, s.numpy()))
+
+
+def moe_block_parts(x, y, w: dict, moe: dict, eps: float = 1e-6, fmt: str = "mxfp8", ids=None, wts=None,
+                    flips: int = 2):
+    """moe_full (models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:797-853) after the layer's first half:
+    x1 = bf16(x + y), h2 = rmsnorm(x1, ln2); the shared expert sh = bf16(silu(bf16 h2 Wg^T) * bf16 h2 Wu^T) Wd^T in
+    fp32, its weights the layer's MLP (w_gate .. s_down) in fmt; logits = h2 w_router^T; the routing (ids, wts)
+    given or the top-K of the logits (oracle.moe.route); base = x1 + sigmoid(h2 . w_shg) sh; the routed MXFP4 experts
+    as oracle.moe.moe_parts (fp32 slots). Returns (base, routed, slack, logits, ids, wts), fp32; slack bounds
+    `flips` one-ulp changes of each bf16 activation row, the shared expert's included (oracle.moe.moe_parts)."""
+    from oracle import moe as omoe
+
+    x1, h2 = add_rmsnorm(x, y, w["ln2"], eps)
+    logits = h2.float() @ moe["w_router"].float().T
+    if ids is None:
+        ids, wts = omoe.route(logits, int(moe["top_k"]), moe.get("norm_topk_prob", True))
+    act = silu_mul(proj(h2, w, "gate", fmt), proj(h2, w, "up", fmt)).float()
+    wd = dequant_weight(w, "down", fmt)
+    sh = act @ wd.T
+    shg = moe.get("w_shg")
+    gate = torch.sigmoid(h2.float() @ shg.float()) if shg is not None else torch.ones(x.shape[0])
+    routed_w = {n: moe[n] for n in ("e_gw", "e_gs", "e_dw", "e_ds")}
+    base0, routed, slack = omoe.moe_parts(h2, routed_w, ids, wts, x1, flips=flips)
+    base = base0 + gate[:, None] * sh
+    slack = slack + flips * (gate * omoe.ulp_bf16(act).amax(dim=1))[:, None] * wd.abs().amax(dim=1)[None, :]
+    return base, routed, slack, logits, ids, wts
+
+
 def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
                      proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
     """One token per sequence. Returns (out bf16 [B, H], state_out f32, conv_out bf16)."""
+    y, state_out, conv_out = gdn_layer_half(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt)
+    return mlp_residual(x, y, w, eps, mlp_fmt), state_out, conv_out
+
+
+def gdn_layer_half(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                   proj_fmt: str = "fp8"):
+    """The GDN layer up to its output projection y (bf16, before the residual and the MLP / MoE block).
+    Returns (y, state_out, conv_out)."""
     from oracle import gdn
 
     b = x.shape[0]
@@ -133,7 +179,7 @@ def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_head
     core, state_out = gdn.gdn_fp32(q, k, v, aa[:, None], bb[:, None], w["a_log"], w["dt_bias"], state_in)
     core = _bf(core).reshape(b * num_v_heads, 128)
     gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(b * num_v_heads, 128), eps).reshape(b, vd)
-    return mlp_residual(x, proj(gated, w, "out", proj_fmt), w, eps, mlp_fmt), state_out, conv_out
+    return proj(gated, w, "out", proj_fmt), state_out, conv_out
 
 
 def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_len, cache_location,
@@ -141,6 +187,15 @@ def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
                       mlp_fmt: str = "mxfp4"):
     """One token per sequence over the paged cache (the page table includes the new token).
     Returns (out bf16 [B, H], the cache with the new K / V rows written)."""
+    y, cache2 = attn_layer_half(x, w, cos, sin, cache, indptr, indices, last_page_len, cache_location, num_qo_heads,
+                                rot, eps, sm_scale, proj_fmt)
+    return mlp_residual(x, y, w, eps, mlp_fmt), cache2
+
+
+def attn_layer_half(x, w: dict, cos, sin, cache, indptr, indices, last_page_len, cache_location,
+                    num_qo_heads: int, rot: int, eps: float = 1e-6, sm_scale=None, proj_fmt: str = "fp8"):
+    """The attention layer up to its output projection y (bf16, before the residual and the MLP / MoE block).
+    Returns (y, the cache with the new K / V rows written)."""
     from oracle import paged_attn
 
     b = x.shape[0]
@@ -155,7 +210,7 @@ def attn_layer_decode(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
     cache2 = paged_attn.store_paged_kv(cache, k, vv, cache_location.numpy())
     attn = _bf(paged_attn.paged_decode(q, cache2, indptr, indices, last_page_len, scale))
     gated = sigmoid_mul(attn, qg[..., d:]).reshape(b, num_qo_heads * d)
-    return mlp_residual(x, proj(gated, w, "o", proj_fmt), w, eps, mlp_fmt), cache2
+    return proj(gated, w, "o", proj_fmt), cache2
 
 
 # ---------------------------------------------------------------------------------------------

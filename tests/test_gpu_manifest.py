@@ -77,3 +77,34 @@ def test_bound_9b_attention_layer_runs_like_loose_tensors(dev):
         outs.append((o, cache))
     assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
     assert torch.equal(outs[0][1].view(torch.int16), outs[1][1].view(torch.int16))
+
+
+def test_bound_35b_moe_layer_runs_like_loose_tensors(dev):
+    """The 35B group's GDN layer as the reference binds it, MoE block included (the router and shared gate from its
+    packs, the routed experts e_gw<j> .. as their own IO): axk_gdn_layer_decode_moe on the bound tensors equals the
+    call on the same weights as loose tensors, bit for bit."""
+    m = mf.Manifest.load(os.path.join(HERE, "qwen35_35b_a3b.manifest.json"))
+    g = torch.Generator().manual_seed(35)
+    h, f = 2048, 512
+    w = configs.gdn_layer_weights(g, h, f, 16, 32, proj_fmt="mxfp8", mlp_fmt="mxfp8")
+    blk = configs.moe_block(g, h, 256, 512, 8)
+    w["w_router"], w["w_shg"] = blk["w_router"], blk["w_shg"]
+    wd = {n: t.to(dev) for n, t in w.items()}
+    b, bufs = _bound(m, "decode.group", 1, wd, dev)
+    for n in mf.EXPERT_IO:
+        bufs[f"{n}1"].copy_(blk[n].reshape(-1).to(dev))
+    print(f"{m.model} layer 1: {b.kind} {b.proj_fmt}/{b.mlp_fmt}", flush=True)
+    names = ("w_router", "w_shg") + mf.EXPERT_IO
+    bound = dict({n: b.weights[n] for n in names}, top_k=8)
+    loose = dict({n: (blk[n] if n in mf.EXPERT_IO else w[n]).to(dev) for n in names}, top_k=8)
+    x = torch.randn(2, h, generator=g).bfloat16().to(dev)
+    st = (torch.randn(2, 32, 128, 128, generator=g) * 0.02).to(dev)
+    cv = torch.randn(2, 3, 8192, generator=g).bfloat16().to(dev)
+    outs = []
+    for weights, moe in ((wd, loose), (b.weights, bound)):
+        o = layer.gdn_layer_decode(x, weights, st.clone(), cv.clone(), 16, 32, proj_fmt=b.proj_fmt,
+                                   mlp_fmt=b.mlp_fmt, moe=moe)
+        torch.cuda.synchronize()
+        outs.append(o)
+    for r, t in zip(*outs):
+        assert torch.equal(r.view(torch.uint8), t.view(torch.uint8))

@@ -295,3 +295,64 @@ def test_attn_verify_oracle_is_causal_and_one_row_is_a_decode_step():
     dec, _ = layer.attn_layer_decode(x[:, 0], w, cos[:, 0], sin[:, 0], c1["cache"], c1["indptr"], c1["indices"],
                                      c1["last_page_len"], c1["loc"][:, 0], hq, 32)
     assert torch.equal(one[:, 0], dec)
+
+
+# ---- the MoE block of the MoE decode layers (moe_full, q35_layer_mc.py:797-853) ----
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp8", "mxfp4"])
+def test_dequant_weight_is_what_proj_multiplies(fmt):
+    """dequant_weight(w, name, fmt) is the weight proj() multiplies (the shared expert's down projection uses it
+    unrounded)."""
+    from axk import configs
+
+    g = _g(40)
+    w = configs.mlp_weights(g, 64, 96, fmt)
+    a = torch.randn(5, 96, generator=g).bfloat16()
+    ref = layer.proj(a, w, "down", fmt).float()
+    got = (a.float() @ layer.dequant_weight(w, "down", fmt).T).bfloat16().float()
+    torch.testing.assert_close(got, ref, rtol=1e-6, atol=1e-6)
+
+
+def _moe_case(seed, fmt="mxfp4"):
+    from axk import configs
+
+    g = _g(seed)
+    h, f, e, fe, k, b = 64, 96, 8, 32, 3, 5
+    w = configs.mlp_weights(g, h, f, fmt)
+    w["ln2"] = 1.0 + 0.1 * torch.randn(h, generator=g)
+    blk = configs.moe_block(g, h, e, fe, k, router_std=0.2)
+    x = torch.randn(b, h, generator=g).bfloat16()
+    y = torch.randn(b, h, generator=g).bfloat16()
+    return w, blk, x, y
+
+
+def test_moe_block_with_an_mxfp4_shared_expert_equals_the_moe_oracle():
+    """With the shared expert in MXFP4 the block is oracle.moe.moe_layer (pinned against transformers'
+    Qwen3_5MoeSparseMoeBlock) on h2 = rmsnorm(x1, ln2) with x1 as the residual: the same routing, and the same
+    output with base kept fp32."""
+    from oracle import moe as omoe
+
+    w, blk, x, y = _moe_case(41)
+    base, routed, slack, logits, ids, wts = layer.moe_block_parts(x, y, w, blk, fmt="mxfp4")
+    x1, h2 = layer.add_rmsnorm(x, y, w["ln2"])
+    mw = dict(blk, **{n: w[n] for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down")})
+    ref, rlogits, rids, rwts = omoe.moe_layer(h2, mw, top_k=blk["top_k"], x_res=x1, round_base=False)
+    assert torch.equal(ids, rids)
+    torch.testing.assert_close(wts, rwts, rtol=0, atol=0)
+    torch.testing.assert_close(logits, rlogits, rtol=0, atol=0)
+    torch.testing.assert_close((base + routed).bfloat16().float(), ref.float(), rtol=1e-6, atol=1e-6)
+    assert (slack > 0).all()
+
+
+def test_moe_block_pin_detects_plausible_slips():
+    """The comparison above fails for a gate / up swap in the shared expert and for a dropped shared gate."""
+    from oracle import moe as omoe
+
+    w, blk, x, y = _moe_case(42)
+    x1, h2 = layer.add_rmsnorm(x, y, w["ln2"])
+    mw = dict(blk, **{n: w[n] for n in ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down")})
+    ref = omoe.moe_layer(h2, mw, top_k=blk["top_k"], x_res=x1, round_base=False)[0].float()
+    swapped = dict(w, w_gate=w["w_up"], s_gate=w["s_up"], w_up=w["w_gate"], s_up=w["s_gate"])
+    base, routed, *_ = layer.moe_block_parts(x, y, swapped, blk, fmt="mxfp4")
+    assert not torch.allclose((base + routed).bfloat16().float(), ref, rtol=2e-2, atol=1e-2)
+    base, routed, *_ = layer.moe_block_parts(x, y, w, dict(blk, w_shg=None), fmt="mxfp4")
+    assert not torch.allclose((base + routed).bfloat16().float(), ref, rtol=2e-2, atol=1e-2)
