@@ -551,6 +551,88 @@ class MoeDecodeWorkload(Workload):
                 "sample": f"full config3a layer (oracle/moe.py, numpy dequant + torch CPU), median of {reps} runs"}
 
 
+class MoeLayerDecodeWorkload(Workload):
+    """The 35B's MoE decode layer (gdn_layer_full_mx, q35_layer_mc.py:855-866): a GDN layer (16 key / 32 value heads,
+    hidden 2048, MXFP8 projections) whose MLP is the MoE block (shared expert MXFP8 inter 512, 256 MXFP4 experts of
+    512, top-8), 32 sequences as config 3a, state and conv state in place.
+
+    One step = the layer's 7 launches before the MLP, the shared expert's two, and config 3a's routed path, one graph.
+    Algorithmic bytes: every weight of the layer and the shared expert, the router, the routed experts actually
+    used (U distinct), the fp32 state read and written, the conv state, activations in and out."""
+
+    name = "moe_layer_decode"
+    kernel = "35B MoE decode layer (GDN half + shared expert + routed experts)"
+    timing = "graph"
+    traffic_profile = "moe_layer_decode_b32_pmc.txt"  # every kernel of the step, summed
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, layer
+
+        self.b, self.h, self.nk, self.nv = 32, 2048, 16, 32
+        g = torch.Generator().manual_seed(0)
+        w = configs.gdn_layer_weights(g, self.h, 512, self.nk, self.nv, proj_fmt="mxfp8", mlp_fmt="mxfp8")
+        blk = configs.moe_block(g, self.h, 256, 512, 8)
+        x = torch.randn(self.b, self.h, generator=g).bfloat16()
+        st = torch.randn(self.b, self.nv, 128, 128, generator=g) * 0.02
+        cv = torch.randn(self.b, 3, 2 * self.nk * 128 + self.nv * 128, generator=g).bfloat16()
+        self.host = (w, blk, x, st, cv)
+        per_expert = sum(blk[n][0].numel() for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+        layer_bytes = sum(v.numel() * v.element_size() for v in w.values())
+        set_bytes = layer_bytes + per_expert * 256
+        self.copies = max(2, -(-ROTATE_BYTES // set_bytes))
+        wd = {n: v.to(dev) for n, v in w.items()}
+        bd = {n: (v.to(dev) if torch.is_tensor(v) else v) for n, v in blk.items()}
+        self.wsets = [(wd, bd)] + [({n: v.clone() for n, v in wd.items()},
+                                    {n: (v.clone() if torch.is_tensor(v) else v) for n, v in bd.items()})
+                                   for _ in range(self.copies - 1)]
+        self.scopies = max(2, -(-ROTATE_BYTES // (st.numel() * 4)))
+        self.states = [st.to(dev) for _ in range(self.scopies)]
+        self.convs = [cv.to(dev) for _ in range(self.scopies)]
+        self.x = x.to(dev)
+        self.out = torch.empty_like(self.x)
+        self.ws = layer.gdn_workspace(self.b, self.h, self.nk, self.nv, 512, dev, moe=bd)
+        ids = torch.empty(self.b, 8, dtype=torch.int32, device=dev)
+        layer.gdn_layer_decode(self.x, wd, self.states[0].clone(), self.convs[0].clone(), self.nk, self.nv,
+                               workspace=self.ws, proj_fmt="mxfp8", mlp_fmt="mxfp8",
+                               moe=dict(bd, topk_ids=ids))
+        self.active = int(torch.unique(ids).numel())
+        self.alg_bytes = layer_bytes + blk["w_router"].numel() * 2 + blk["w_shg"].numel() * 2 + \
+            self.active * per_expert + 2 * st.numel() * 4 + 2 * cv.numel() * 2 + 2 * x.numel() * 2
+        self.config = {"workload": "35B MoE decode layer: GDN (16/32 heads, H=2048, MXFP8) + MoE (shared MXFP8 "
+                                   "F=512, 256 MXFP4 experts F=512, top-8), B=32",
+                       "distinct_experts": self.active, "rotating_copies": self.copies}
+        self.dtype = "mxfp8 / mxfp4 weights x bf16 -> fp32 acc, fp32 state"
+
+    def step(self, i: int) -> None:
+        from axk import layer
+
+        wd, bd = self.wsets[i % self.copies]
+        s, c = self.states[i % self.scopies], self.convs[i % self.scopies]
+        layer.gdn_layer_decode(self.x, wd, s, c, self.nk, self.nv, workspace=self.ws, out=self.out, state_out=s,
+                               conv_out=c, proj_fmt="mxfp8", mlp_fmt="mxfp8", moe=bd)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import layer as olayer
+
+        w, blk, x, st, cv = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        n = 4  # a bounded sample: 4 of the 32 sequences, scaled by sequences
+
+        def run():
+            y, _, _ = olayer.gdn_layer_half(x[:n], w, st[:n], cv[:n], self.nk, self.nv, proj_fmt="mxfp8")
+            return olayer.moe_block_parts(x[:n], y, w, blk, fmt="mxfp8")
+
+        sec, reps = _time_cpu(run, budget_s=10.0, min_reps=1, max_reps=3)
+        return {"value": sec * self.b / n * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"oracle/layer.py on {n} of the {self.b} sequences (GDN half + MoE block), scaled by "
+                          f"sequences, median of {reps} runs"}
+
+
 class CopyCalibWorkload(Workload):
     """A plain 256 MiB device-to-device copy: the known-size kernel that calibrates the FETCH_SIZE /
     WRITE_SIZE counters (read 256 MiB, write 256 MiB per launch)."""
@@ -862,7 +944,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
              LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
-             PagedPrefillWorkload.name: PagedPrefillWorkload,
+             PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
