@@ -375,6 +375,275 @@ int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, 
   return axk_launch_status();
 }
 
+// ---------------------------------------------------------------------------------------------
+// The large-M path (prefill): a dense GEMM per matrix (or per gate / up pair) with an LDS pipeline. Workgroup = 64
+// activation rows x 256 weight rows (EPI_SWIGLU: 128 gate + the same 128 up channels), wave w a 64 x 64 block of
+// four by four MFMA tiles (every A fragment feeds four MFMAs, every B fragment four). The activation rows and the
+// weight rows of each 64-wide K step land in a ring of kDgStages LDS slots by direct loads two steps ahead, one
+// barrier per step: A [64 rows][128 B] with 16-byte chunk c of row r at position c ^ (r & 7); B [256 rows][RB bytes]
+// (RB = 32 for MXFP4, 64 for the 8-bit formats) with 16-byte chunk c of row r at c ^ ((r >> 3) & 1) (MXFP4) or
+// c ^ ((r >> 2) & 3) (8-bit): the fragment reads are free of bank conflicts. E8M0 scales of the whole reduction are
+// staged in LDS once; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
+// kernel's. Consecutive workgroups go round-robin over the 8 XCDs, so each XCD takes a contiguous run of the
+// column-block-major tile order: a column block's weights are fetched into one XCD's L2 for all its row blocks.
+// ---------------------------------------------------------------------------------------------
+constexpr int kDgBM = 64, kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8;
+constexpr int64_t kDgMinRows = 128;  // below this the group kernel (weights streamed once per 16 / 32 rows) is faster
+constexpr int kDgAStage = kDgBM * kDgBK * 2;  // 8 KiB
+template <int F>
+constexpr int dg_row_bytes() { return F == WF_MXFP4 ? kDgBK / 2 : kDgBK; }  // weight bytes per row and step
+template <int F>
+constexpr int dg_stage() { return kDgAStage + kDgBN * dg_row_bytes<F>(); }
+template <int F>
+size_t dg_lds_bytes(int64_t k) {
+  return (size_t)kDgStages * dg_stage<F>() + (axk::is_mx(F) ? (size_t)kDgBN * (k / 32 + 16) : 0);
+}
+
+struct DgArgs {
+  const uint16_t* a;
+  int64_t lda;
+  const uint8_t* w[2];      // the matrix (EPI_SWIGLU: gate, up)
+  const uint8_t* ws[2];     // E8M0 scales [n, k/32] (MX formats)
+  const float* col_scale[2];
+  const float* bias[2];
+  void* out;
+  int64_t ldo;
+  const float* row_scale;
+  const uint16_t* res;  // EPI_RES
+  int64_t ldr;
+  int out_f32;
+  int m, n, k;
+};
+
+template <int F>
+AXK_DEV axk_bf16x8 dg_decode(const unsigned char* row, int kh, int g4, int r, float sc) {
+  if constexpr (F == WF_MXFP4) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 16 * (kh ^ ((r >> 3) & 1)) + 4 * g4);
+    return fp4x8_to_bf16x8(w, sc);
+  } else {
+    // 8 bytes (k = 32 kh + 8 g4 ..) of the 64-byte row: chunk 2 kh + g4 / 2, half g4 % 2
+    const int c = (2 * kh + (g4 >> 1)) ^ ((r >> 2) & 3);
+    const uint2 w = *reinterpret_cast<const uint2*>(row + 16 * c + 8 * (g4 & 1));
+    const uint4 q = make_uint4(w.x, w.y, 0u, 0u);
+    return axk::WUnit<F>::conv(q, 0, sc);
+  }
+}
+
+template <int F, int EPI>
+__global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int RB = dg_row_bytes<F>(), STAGE = dg_stage<F>();
+  constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;  // output channels per workgroup
+  const int nb = (g.n + COLS - 1) / COLS, mb = (g.m + kDgBM - 1) / kDgBM;
+  const int total = nb * mb, per = (total + kDgXcds - 1) / kDgXcds;
+  const int q = blockIdx.x / kDgXcds, lid = (blockIdx.x % kDgXcds) * per + q;
+  if (q >= per || lid >= total) return;
+  const int cb = lid / mb, rbk = lid - cb * mb;  // column-block-major
+  const int col0 = cb * COLS, m0 = rbk * kDgBM;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
+  const int K = g.k, nk = K / kDgBK;
+  const uint32_t lds0 = lds_addr(smem);
+  unsigned char* sS = smem + kDgStages * STAGE;
+  const int ldS = K / 32 + 16;
+
+  // LDS weight row rho -> weight row (SwiGLU: rho < 128 the gate channel col0 + rho, else the up channel col0 + rho -
+  // 128), clamped to the last channel (never stored)
+  auto wrow = [&](int rho, bool scale) -> const uint8_t* {
+    const int mi = EPI == EPI_SWIGLU && rho >= COLS ? 1 : 0;
+    const int c = min(col0 + (EPI == EPI_SWIGLU ? (rho & (COLS - 1)) : rho), g.n - 1);
+    return scale ? g.ws[mi] + (int64_t)c * (K / 32) : g.w[mi] + (int64_t)c * axk::row_bytes<F>(K);
+  };
+  // per-lane sources of this wave's direct loads of a step: A instructions i = 2 wave + h (rows 8 i + lane / 8,
+  // chunk (lane % 8) ^ (row & 7)); B instructions (RB == 32: 2 per wave, 32 rows each; RB == 64: 4 per wave,
+  // 16 rows each)
+  constexpr int BI = kDgBN * RB / 1024 / 4;  // B instructions per wave and step
+  const uint16_t* asrc[2];
+  const uint8_t* bsrc[BI];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = 2 * wave + h;
+    const int r = 8 * i + (lane >> 3), rr = min(m0 + r, g.m - 1), ch = (lane & 7) ^ (r & 7);
+    asrc[h] = g.a + (int64_t)rr * g.lda + 8 * ch;
+  }
+#pragma unroll
+  for (int h = 0; h < BI; ++h) {
+    const int i = BI * wave + h;
+    if constexpr (RB == 32) {
+      const int rho = 32 * i + (lane >> 1);
+      bsrc[h] = wrow(rho, false) + 16 * ((lane & 1) ^ ((rho >> 3) & 1));
+    } else {
+      const int rho = 16 * i + (lane >> 2);
+      bsrc[h] = wrow(rho, false) + 16 * ((lane & 3) ^ ((rho >> 2) & 3));
+    }
+  }
+  // step ks into ring slot buf (past the last step the last one again: in bounds, unused), so every iteration
+  // waits on the same count
+  auto issue = [&](int ks, int buf) {
+    const int kk = min(ks, nk - 1);
+    const uint32_t base = lds0 + buf * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lds_dma16_cached(asrc[h] + kk * kDgBK, base + (2 * wave + h) * 1024);
+#pragma unroll
+    for (int h = 0; h < BI; ++h) lds_dma16_cached(bsrc[h] + kk * RB, base + kDgAStage + (BI * wave + h) * 1024);
+  };
+  issue(0, 0);
+  issue(1, 1);
+  if constexpr (axk::is_mx(F)) {  // the E8M0 scales of the whole reduction (while the first steps load)
+    const int sb = K / 32;
+    if (sb % 16 == 0 && (((uintptr_t)g.ws[0] | (uintptr_t)g.ws[1]) & 15) == 0) {
+      const int u = sb / 16;
+      for (int idx = tid; idx < kDgBN * u; idx += 256) {
+        const int rho = idx / u, qq = idx - rho * u;
+        *reinterpret_cast<uint4*>(sS + rho * ldS + 16 * qq) = *reinterpret_cast<const uint4*>(wrow(rho, true) + 16 * qq);
+      }
+    } else {
+      for (int idx = tid; idx < kDgBN * sb; idx += 256) {
+        const int rho = idx / sb, qq = idx - rho * sb;
+        sS[rho * ldS + qq] = wrow(rho, true)[qq];
+      }
+    }
+  }
+  int brow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    brow[j] = EPI == EPI_SWIGLU ? (j >> 1) * COLS + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
+  axk_f32x4 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](int ks, auto buf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
+    wait_vmcnt<2 + BI>();  // this wave's loads of step ks have landed (step ks + 1's may not have)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of step ks - 1 are done
+    __builtin_amdgcn_s_barrier();  // every wave's step-ks loads landed; every wave is done with step ks - 1
+    asm volatile("" ::: "memory");
+    issue(ks + 2, (BUF + 2) % kDgStages);  // into the slot of step ks - 1
+    const unsigned char* sa = smem + BUF * STAGE;
+    const unsigned char* sb = sa + kDgAStage;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      axk_bf16x8 af[4], bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = brow[j] + l16;
+        const float sc = axk::is_mx(F) ? e8m0_to_f32(sS[r * ldS + 2 * ks + kh]) : 1.0f;
+        bf[j] = dg_decode<F>(sb + r * RB, kh, g4, r, sc);
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int r = 16 * mt + l16;
+        af[mt] = *reinterpret_cast<const axk_bf16x8*>(sa + r * 128 + 16 * ((4 * kh + g4) ^ (r & 7)));
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
+    }
+  };
+  static_assert(kDgStages == 3, "the K loop is unrolled over three ring slots");
+  for (int ks = 0; ks < nk; ks += 3) {
+    step(ks, std::integral_constant<int, 0>{});
+    if (ks + 1 < nk) step(ks + 1, std::integral_constant<int, 1>{});
+    if (ks + 2 < nk) step(ks + 2, std::integral_constant<int, 2>{});
+  }
+  wait_vmcnt<0>();  // the look-ahead loads land before the workgroup's LDS is released
+
+  // element (mt, r) of tile j: row m0 + 16 mt + 4 g4 + r, weight row brow[j] + l16 (the group kernel's epilogue)
+  auto fin = [&](int mi, int nn, int m, float v) {
+    if (g.row_scale) v *= g.row_scale[m];
+    if (g.col_scale[mi]) v *= g.col_scale[mi][nn];
+    if (g.bias[mi]) v += g.bias[mi][nn];
+    return v;
+  };
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 16 * mt + 4 * g4 + r;
+      if (m >= g.m) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int nn = col0 + 32 * wave + 16 * j + l16;
+          if (nn >= g.n) continue;
+          const float gv = fin(0, nn, m, acc[mt][j][r]), uv = fin(1, nn, m, acc[mt][j + 2][r]);
+          reinterpret_cast<uint16_t*>(g.out)[(int64_t)m * g.ldo + nn] =
+              (uint16_t)f32_to_bf16_bits(silu_f32(round_bf16(gv)) * round_bf16(uv));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nn = col0 + 64 * wave + 16 * j + l16;
+          if (nn >= g.n) continue;
+          float v = fin(0, nn, m, acc[mt][j][r]);
+          if constexpr (EPI == EPI_RES) v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
+          if (g.out_f32)
+            reinterpret_cast<float*>(g.out)[(int64_t)m * g.ldo + nn] = v;
+          else
+            reinterpret_cast<uint16_t*>(g.out)[(int64_t)m * g.ldo + nn] = (uint16_t)f32_to_bf16_bits(v);
+        }
+      }
+    }
+}
+
+// Launches the dense GEMM for a checked group (one launch per matrix; EPI_SWIGLU one for the pair). False when the
+// shape does not take it (then the group kernel runs).
+template <int F>
+bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv) {
+  if constexpr (F == axk::WF_BF16) {
+    return false;
+  } else {
+    return conv == nullptr && m >= kDgMinRows && k % kDgBK == 0 && dg_lds_bytes<F>(k) <= 160 * 1024;
+  }
+}
+
+template <int F, int EPI>
+int dg_launch(const DgArgs& d, hipStream_t st) {
+  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  if (!lds_raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mx_gemm_kernel<F, EPI>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return AXK_E_LAUNCH;
+    lds_raised = true;
+  }
+  constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;
+  const int64_t tiles = ((int64_t)d.n + COLS - 1) / COLS * (((int64_t)d.m + kDgBM - 1) / kDgBM);
+  const int64_t grid = (tiles + kDgXcds - 1) / kDgXcds * kDgXcds;  // whole rounds over the XCDs
+  AXK_REQUIRE(grid <= INT32_MAX, AXK_E_SHAPE);
+  hipLaunchKernelGGL((mx_gemm_kernel<F, EPI>), dim3((unsigned)grid), dim3(256), dg_lds_bytes<F>(d.k), st, d);
+  return axk_launch_status();
+}
+
+template <int F>
+int dg_group(const uint16_t* a, int64_t lda, const MxGroup& g, int epi, int64_t m, int64_t k, hipStream_t st) {
+  auto args = [&](int i0, int i1) {
+    DgArgs d{};
+    d.a = a;
+    d.lda = lda;
+    d.w[0] = g.w[i0], d.w[1] = g.w[i1];
+    d.ws[0] = g.ws[i0], d.ws[1] = g.ws[i1];
+    d.col_scale[0] = g.col_scale[i0], d.col_scale[1] = g.col_scale[i1];
+    d.bias[0] = g.bias[i0], d.bias[1] = g.bias[i1];
+    d.out = g.out[i0];
+    d.ldo = g.ldo[i0];
+    d.row_scale = g.row_scale;
+    d.res = g.res;
+    d.ldr = g.ldr;
+    d.out_f32 = g.out_f32;
+    d.m = (int)m, d.n = g.n[i0], d.k = (int)k;
+    return d;
+  };
+  if (epi == EPI_SWIGLU) return dg_launch<F, EPI_SWIGLU>(args(0, 1), st);
+  if (epi == EPI_RES) return dg_launch<F, EPI_RES>(args(0, 0), st);
+  for (int i = 0; i < g.count; ++i) {
+    const int rc = dg_launch<F, EPI_PLAIN>(args(i, i), st);
+    if (rc != AXK_OK) return rc;
+  }
+  return AXK_OK;
+}
+
 // Checks a group and launches it. Matrices need whole 128-byte row segments (and 8-byte aligned MXFP4 scale rows).
 template <int F>
 int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, int epi, const uint16_t* res,
@@ -439,6 +708,7 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   for (int i = count; i <= AXK_MX_GROUP_MAX; ++i) g.tile0[i] = (int)tiles;
   if (m == 0) return AXK_OK;
   AXK_LAUNCH_GATE();
+  if (dg_fits<F>(m, k, conv)) return dg_group<F>(a, lda, g, epi, m, k, st);
   if (epi == EPI_SWIGLU) return group_dispatch<F, EPI_SWIGLU>(a, lda, g, m, k, st);
   if (epi == EPI_RES) return group_dispatch<F, EPI_RES>(a, lda, g, m, k, st);
   return group_dispatch<F, EPI_PLAIN>(a, lda, g, m, k, st);
