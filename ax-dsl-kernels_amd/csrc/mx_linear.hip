@@ -384,10 +384,10 @@ int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, 
 // (RB = 32 for MXFP4, 64 for the 8-bit formats) with 16-byte chunk c of row r at c ^ ((r >> 3) & 1) (MXFP4) or
 // c ^ ((r >> 2) & 3) (8-bit): the fragment reads are free of bank conflicts. E8M0 scales of the whole reduction are
 // staged in LDS once; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
-// kernel's. Consecutive workgroups go round-robin over the 8 XCDs, so each XCD takes a contiguous run of the
-// column-block-major tile order: a column block's weights are fetched into one XCD's L2 for all its row blocks.
+// kernel's. Consecutive workgroups go round-robin over the 8 XCDs, so each XCD takes a contiguous run of the tile
+// order, which walks groups of 8 row blocks across all column blocks: an XCD's L2 keeps its activation rows.
 // ---------------------------------------------------------------------------------------------
-constexpr int kDgBM = 64, kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8;
+constexpr int kDgBM = 64, kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8, kDgGroupRows = 8;
 constexpr int64_t kDgMinRows = 128;  // below this the group kernel (weights streamed once per 16 / 32 rows) is faster
 constexpr int kDgAStage = kDgBM * kDgBK * 2;  // 8 KiB
 template <int F>
@@ -438,7 +438,11 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   const int total = nb * mb, per = (total + kDgXcds - 1) / kDgXcds;
   const int q = blockIdx.x / kDgXcds, lid = (blockIdx.x % kDgXcds) * per + q;
   if (q >= per || lid >= total) return;
-  const int cb = lid / mb, rbk = lid - cb * mb;  // column-block-major
+  // groups of kDgGroupRows row blocks, column blocks inner: an XCD's run of tiles (and the 64 it runs at once) covers
+  // a few row blocks across the column blocks, so its L2 keeps those activation rows for every column block
+  const int gfirst = (lid / (kDgGroupRows * nb)) * kDgGroupRows, gsize = min(mb - gfirst, kDgGroupRows);
+  const int inner = lid - gfirst * nb;
+  const int rbk = gfirst + inner % gsize, cb = inner / gsize;
   const int col0 = cb * COLS, m0 = rbk * kDgBM;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
   const int K = g.k, nk = K / kDgBK;

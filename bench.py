@@ -138,6 +138,62 @@ class MxLinearWorkload(Workload):
                 "sample": f"full config0 op (oracle/mx_codec.c, OpenMP), median of {reps} runs"}
 
 
+class MxLinearPrefillWorkload(Workload):
+    """Config 0's MXFP4 weight (4096 x 4096) at prefill rows: x bf16 [4096, 4096], bf16 out: the dense GEMM path of
+    axk_mxfp4_gemm (m >= 128). MFMA-bound: 2 M N K flops against dense bf16 (the weights are decoded exactly to bf16
+    in registers, the activations are bf16)."""
+
+    name = "mxfp4_linear_prefill"
+    kernel = "mx_gemm_kernel<0, 0>"
+    timing = "graph"
+    mfma = True
+    traffic_profile = "mxfp4_linear_prefill_m4096_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        c = configs.config0()
+        g = torch.Generator().manual_seed(1)
+        self.m, self.n, self.k = 4096, 4096, 4096
+        self.host = (torch.randn(self.m, self.k, generator=g).to(torch.bfloat16), c["w"], c["s"])
+        self.alg_bytes = self.n * self.k // 2 + self.n * self.k // 32 + 2 * self.m * self.k + 2 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        w, s = c["w"].to(dev), c["s"].to(dev)
+        # the activations (32 MiB) and outputs rotate with the weights so the MALL serves no repeated bytes
+        per_copy = self.alg_bytes
+        self.copies = max(2, -(-ROTATE_BYTES // per_copy))
+        self.x = [self.host[0].to(dev) for _ in range(self.copies)]
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.s = [s.clone() for _ in range(self.copies)]
+        self.out = [torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev) for _ in range(self.copies)]
+        self.config = {"workload": "MXFP4 linear N=4096 K=4096 at M=4096 prefill rows (config 0's weight)",
+                       "rotating_copies": self.copies}
+        self.dtype = "mxfp4 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        j = i % self.copies
+        axk.mxfp4_gemm(self.x[j], self.w[j], self.s[j], output=self.out[j])
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import _c
+
+        x, w, s = self.host
+        rows = 64  # a bounded sample of the 4096 rows, scaled by rows
+        xs = x[:rows].contiguous().view(torch.int16).numpy().view("u2")
+        nt = _cpu_threads()
+        sec, reps = _time_cpu(lambda: _c.mxfp4_linear(xs, w.numpy(), s.numpy(), nthreads=nt), budget_s=10.0,
+                              min_reps=1, max_reps=5)
+        return {"value": sec * self.m / rows * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"{rows} of the {self.m} rows (oracle/mx_codec.c, OpenMP), scaled by rows, median of "
+                          f"{reps} runs"}
+
+
 class LmHeadWorkload(Workload):
     """The MXFP4 LM head GEMV of decode (SURVEY next row): W [248320, 2048] (E2M1 + E8M0, config 0's encoding),
     x bf16 [1, 2048], fp32 logits (mul_mat_mx4_n248320_k2048, q35_layer_mc.py:705-724)."""
@@ -945,6 +1001,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
              LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
+             MxLinearPrefillWorkload.name: MxLinearPrefillWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
