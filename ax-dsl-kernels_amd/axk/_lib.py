@@ -108,6 +108,11 @@ SIGNATURES: dict[str, list] = {
     "axk_gdn_layer_decode_moe": [_vp] * 29 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
     "axk_attn_layer_decode_moe": [_vp] * 28 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                                   ctypes.c_size_t, _vp],
+    "axk_gdn_layer_prefill_workspace_size": [_i64] * 7,
+    "axk_attn_layer_prefill_workspace_size": [_i64] * 7,
+    "axk_gdn_layer_prefill": [_vp] * 28 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_attn_layer_prefill": [_vp] * 27 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
+                               ctypes.c_size_t, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,
@@ -121,6 +126,8 @@ _RESTYPES = {
     "axk_attn_layer_verify_workspace_size": ctypes.c_size_t,
     "axk_gdn_layer_moe_workspace_size": ctypes.c_size_t,
     "axk_attn_layer_moe_workspace_size": ctypes.c_size_t,
+    "axk_gdn_layer_prefill_workspace_size": ctypes.c_size_t,
+    "axk_attn_layer_prefill_workspace_size": ctypes.c_size_t,
 }
 
 

@@ -256,3 +256,77 @@ def attn_layer_verify(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
               *[t_.data_ptr() for t_ in mlp], o.data_ptr(), b, t, h, num_qo_heads, hkv, d, rot, page, pages, inter,
               eps, scale, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
     return o
+
+
+# ---- prefill: T new tokens per sequence through one layer call (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:
+# gdn_layer_prefill 57-141, attn_layer_prefill 172-336) ----
+def gdn_prefill_workspace(batch: int, tokens: int, hidden: int, num_k_heads: int, num_v_heads: int, inter: int,
+                          device, head_dim: int = 128) -> torch.Tensor:
+    n = _lib.load().axk_gdn_layer_prefill_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim,
+                                                         inter)
+    _check(n > 0, "unsupported GDN prefill shape")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def attn_prefill_workspace(batch: int, tokens: int, hidden: int, num_qo_heads: int, num_kv_heads: int,
+                           head_dim: int, inter: int, device) -> torch.Tensor:
+    n = _lib.load().axk_attn_layer_prefill_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                                                          head_dim, inter)
+    _check(n > 0, "unsupported attention prefill shape")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def gdn_layer_prefill(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: torch.Tensor, num_k_heads: int,
+                      num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
+                      conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+    """x bf16 [B, T, hidden]: T new tokens per sequence. state f32 [B, NV, 128, 128]; conv state bf16
+    [B, K-1, 2 KD + VD]. Returns (out [B, T, hidden], state_out, conv_out) after the last token."""
+    _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    b, t, h = x.shape
+    inter = w["w_gate"].shape[0]
+    kconv = w["conv_w"].shape[1]
+    ws = workspace if workspace is not None else gdn_prefill_workspace(b, t, h, num_k_heads, num_v_heads, inter,
+                                                                       x.device)
+    o = torch.empty_like(x) if out is None else out
+    so = torch.empty_like(state_in) if state_out is None else state_out
+    co = torch.empty_like(conv_in) if conv_out is None else conv_out
+    args = _weights(w, GDN_WEIGHTS) + _weights(w, MLP_WEIGHTS)
+    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args)
+    ptrs = [t_.data_ptr() for t_ in args]
+    _lib.call("axk_gdn_layer_prefill", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
+              so.data_ptr(), co.data_ptr(), b, t, h, num_k_heads, num_v_heads, 128, kconv, inter, eps,
+              _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    return o, so, co
+
+
+def attn_layer_prefill(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Tensor, kv_cache: torch.Tensor,
+                       indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
+                       cache_location: torch.Tensor, num_qo_heads: int, rot: int, eps: float = 1e-6,
+                       sm_scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
+                       out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8",
+                       mlp_fmt: str = "mxfp4") -> torch.Tensor:
+    """x bf16 [B, T, hidden]; the page table covers each sequence's history and its T new tokens; cache_location
+    int32 [B, T, 2] (page, slot) of each new token; cos, sin bf16 [B, T, rot / 2]. kv_cache bf16
+    [P, 2, page, HKV, D] is written in place. Returns out bf16 [B, T, hidden]."""
+    _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    b, t, h = x.shape
+    pages, two, page, hkv, d = kv_cache.shape
+    inter = w["w_gate"].shape[0]
+    _check(cache_location.dtype == torch.int32 and cache_location.numel() == 2 * b * t and
+           cache_location.is_contiguous(), "cache_location must be contiguous int32 [B, T, 2]")
+    ws = workspace if workspace is not None else attn_prefill_workspace(b, t, h, num_qo_heads, hkv, d, inter,
+                                                                        x.device)
+    o = torch.empty_like(x) if out is None else out
+    scale = d ** -0.5 if sm_scale is None else sm_scale
+    wa = _weights(w, ATTN_WEIGHTS)
+    mlp = _weights(w, MLP_WEIGHTS)
+    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp)
+    (ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, w_o, s_o, ln2) = wa
+    _lib.call("axk_attn_layer_prefill", x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(),
+              w_k.data_ptr(), s_k.data_ptr(), w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
+              _lib.ptr(cos), _lib.ptr(sin), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
+              last_page_len.data_ptr(), cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(),
+              *[t_.data_ptr() for t_ in mlp], o.data_ptr(), b, t, h, num_qo_heads, hkv, d, rot, page, pages, inter,
+              eps, scale, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    return o

@@ -128,3 +128,12 @@ __attribute__((visibility("hidden"))) int axk_moe_decode_shared_given(
     const uint8_t* e_gw, const uint8_t* e_gs, const uint8_t* e_dw, const uint8_t* e_ds, uint16_t* out, float* logits,
     int32_t* topk_ids, float* topk_weights, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k,
     int64_t inter, int norm_topk_prob, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
+// Internal (not exported): axk_gdn_chunk_prefill (chunk 64, head dims 128) with q, k, v read at row strides ldq, ldk,
+// ldv (elements between consecutive (sequence, token) rows; the heads of a row contiguous), so the prefill layer
+// reads them straight out of the conv output. Returns an AXK status.
+__attribute__((visibility("hidden"))) int axk_gdn_chunk_prefill_strided(
+    const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
+    const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
+    int64_t num_k_heads, int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, void* workspace,
+    size_t workspace_bytes, axk_stream_t stream);

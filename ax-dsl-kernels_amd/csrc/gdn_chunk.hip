@@ -101,6 +101,7 @@ struct PrepArgs {
   const float *a_log, *dt_bias;
   ChunkWs ws;
   int B, T, NK, NV, NC;
+  int64_t ldq, ldk, ldv;  // elements between consecutive (sequence, token) rows of q, k, v
 };
 
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
@@ -127,9 +128,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   uint4 qr[4], kr[4], vr[4];
   if (tt < n) {
     const int64_t tok = (int64_t)b * p.T + t0 + tt;
-    const uint4* qp = reinterpret_cast<const uint4*>(p.q + (tok * p.NK + kh) * kD + 32 * qd);
-    const uint4* kp = reinterpret_cast<const uint4*>(p.k + (tok * p.NK + kh) * kD + 32 * qd);
-    const uint4* vp = reinterpret_cast<const uint4*>(p.v + (tok * p.NV + h) * kD + 32 * qd);
+    const uint4* qp = reinterpret_cast<const uint4*>(p.q + tok * p.ldq + kh * kD + 32 * qd);
+    const uint4* kp = reinterpret_cast<const uint4*>(p.k + tok * p.ldk + kh * kD + 32 * qd);
+    const uint4* vp = reinterpret_cast<const uint4*>(p.v + tok * p.ldv + h * kD + 32 * qd);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       qr[i] = qp[i];
@@ -619,16 +620,18 @@ extern "C" size_t axk_gdn_chunk_workspace_size(int64_t batch, int64_t tokens, in
   return chunk_ws_layout(batch, num_k_heads, num_v_heads, (tokens + kC - 1) / kC, off);
 }
 
-extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
-                                     const uint16_t* b, const float* a_log, const float* dt_bias,
-                                     const float* state_in, float* state_out, uint16_t* out, int64_t batch,
-                                     int64_t tokens, int64_t num_k_heads, int64_t num_v_heads, int64_t head_k_dim,
-                                     int64_t head_v_dim, int64_t chunk_size, void* workspace, size_t workspace_bytes,
-                                     axk_stream_t stream) {
+namespace {
+int chunk_prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b,
+                       const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
+                       uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads, int64_t num_v_heads,
+                       int64_t head_k_dim, int64_t head_v_dim, int64_t chunk_size, int64_t ldq, int64_t ldk,
+                       int64_t ldv, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
   const int rc = check_chunk_dims(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size);
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(k, 16) && axk_aligned(v, 16), AXK_E_ALIGN);
+  AXK_REQUIRE(ldq >= num_k_heads * kD && ldk >= num_k_heads * kD && ldv >= num_v_heads * kD, AXK_E_SHAPE);
+  AXK_REQUIRE(ldq % 8 == 0 && ldk % 8 == 0 && ldv % 8 == 0, AXK_E_ALIGN);
   AXK_REQUIRE(axk_aligned(state_in, 16) && axk_aligned(state_out, 16), AXK_E_ALIGN);
   const size_t need =
       axk_gdn_chunk_workspace_size(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size);
@@ -642,6 +645,7 @@ extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const
               AXK_E_ALIAS);
   const int NC = (int)((tokens + kC - 1) / kC);
   const ChunkWs ws = chunk_ws(workspace, batch, num_k_heads, num_v_heads, NC);
+  AXK_LAUNCH_GATE();
   hipStream_t st = axk_stream(stream);
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once
   if (!lds_raised) {
@@ -650,7 +654,8 @@ extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
-  PrepArgs pa{q, k, v, a, b, a_log, dt_bias, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC};
+  PrepArgs pa{q, k, v, a, b, a_log, dt_bias, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC,
+              ldq, ldk, ldv};
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((unsigned)NC, (unsigned)num_v_heads, (unsigned)batch), dim3(256),
                      kPrepLds, st, pa);
   int lrc = axk_launch_status();
@@ -659,4 +664,25 @@ extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const
   hipLaunchKernelGGL((gdn_chunk_scan_kernel<kScanSW, kScanNW>), dim3((unsigned)((kD / kScanSW) * batch * num_v_heads)),
                      dim3(64 * kScanNW), 0, st, sa);
   return axk_launch_status();
+}
+}  // namespace
+
+extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                     const uint16_t* b, const float* a_log, const float* dt_bias,
+                                     const float* state_in, float* state_out, uint16_t* out, int64_t batch,
+                                     int64_t tokens, int64_t num_k_heads, int64_t num_v_heads, int64_t head_k_dim,
+                                     int64_t head_v_dim, int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                                     axk_stream_t stream) {
+  return chunk_prefill_impl(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens, num_k_heads,
+                            num_v_heads, head_k_dim, head_v_dim, chunk_size, num_k_heads * kD, num_k_heads * kD,
+                            num_v_heads * kD, workspace, workspace_bytes, stream);
+}
+
+int axk_gdn_chunk_prefill_strided(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                                  const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
+                                  float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
+                                  int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, void* workspace,
+                                  size_t workspace_bytes, axk_stream_t stream) {
+  return chunk_prefill_impl(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens, num_k_heads,
+                            num_v_heads, kD, kD, kC, ldq, ldk, ldv, workspace, workspace_bytes, stream);
 }

@@ -454,6 +454,68 @@ int check_verify(int64_t B, int64_t T, int64_t H, int64_t F) {
   return check_common(B * T, H, F);
 }
 
+// Prefill: up to kMaxPrefillTokens new tokens per sequence, kMaxPrefillRows rows per call.
+constexpr int64_t kMaxPrefillTokens = 1 << 16, kMaxPrefillRows = 1 << 17;
+int check_prefill(int64_t B, int64_t T, int64_t H, int64_t F) {
+  AXK_REQUIRE(T >= 1 && T <= kMaxPrefillTokens && B > 0 && B <= kMaxPrefillRows / T, AXK_E_SHAPE);
+  AXK_REQUIRE(H > 0 && F > 0 && H % 256 == 0 && F % 256 == 0, AXK_E_SHAPE);
+  return AXK_OK;
+}
+
+size_t attn_rows_ws(int64_t B, int64_t T, int64_t H, int64_t HQ, int64_t HKV, int64_t D, int64_t F) {
+  if (HQ <= 0 || HKV <= 0 || HQ % HKV != 0 || !(D == 64 || D == 128 || D == 256)) return 0;
+  Carver c{nullptr};
+  carve_attn_verify(c, B, B * T, H, HQ, HKV, D, F);
+  return c.off;
+}
+
+// The attention layer over T new rows per sequence (verify and prefill): every projection over the B T rows; each
+// row's K / V into the cache at its own location; causal attention of the rows over the history and the rows up to
+// themselves (the T rows are the last T tokens of the sequence's page table); the output gate, o projection and MLP.
+int attn_rows_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k,
+                   const void* s_k, const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm,
+                   const uint16_t* cos, const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr,
+                   const int32_t* indices, const int32_t* last_page_len, const int32_t* cache_location,
+                   const uint8_t* w_o, const void* s_o, const float* ln2, const uint8_t* mlp_gate_w,
+                   const void* mlp_gate_s, const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                   const void* mlp_down_s, uint16_t* out, int64_t batch, int64_t tokens, int64_t hidden,
+                   int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
+                   int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt,
+                   void* workspace, size_t workspace_bytes, axk_stream_t stream, size_t need) {
+  AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
+                  indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
+                  mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
+              AXK_E_NULL);
+  AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
+  AXK_REQUIRE(need > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const int64_t B = batch, T = tokens, R = B * T, H = hidden, HQ = num_qo_heads, HKV = num_kv_heads, D = head_dim,
+                F = inter;
+  Carver c{static_cast<unsigned char*>(workspace)};
+  const AttnVerifyBufs a = carve_attn_verify(c, B, R, H, HQ, HKV, D, F);
+  const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
+  auto body = [&]() -> int {
+    AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, R, H, eps, stream));
+    const AxkMxMat proj[3] = {proj_mat(proj_fmt, w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
+                              proj_mat(proj_fmt, w_k, s_k, a.kk, HKV * D), proj_mat(proj_fmt, w_v, s_v, a.vv, HKV * D)};
+    AXK_TRY(projs(proj_fmt, a.h, H, proj, 3, R, H, stream));
+    AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, R, HQ, HKV,
+                              D, rot, page_size, num_pages, eps, axk_stream(stream)));
+    AXK_TRY(axk_fill_iota_i32(a.qo_indptr, B, T, axk_stream(stream)));
+    AXK_TRY(axk_paged_prefill(a.q, kv_cache, a.qo_indptr, indptr, indices, last_page_len, a.attn, B, R, HQ, HKV, D,
+                              page_size, num_pages, sm_scale, nullptr, stream));
+    AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, R * HQ, D, stream));
+    const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
+    AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, R, HQ * D, stream));
+    return mlp_residual(x, a.y, ln2, mw, mlp_fmt, out, a.mlp, R, H, F, eps, stream);
+  };
+  {
+    const AxkValidateScope check_only;  // every sub-call's checks before the first launch
+    AXK_TRY(body());
+  }
+  return body();
+}
+
 }  // namespace
 
 extern "C" size_t axk_gdn_layer_verify_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
@@ -524,12 +586,8 @@ extern "C" int axk_gdn_layer_verify(
 extern "C" size_t axk_attn_layer_verify_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
                                                        int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
                                                        int64_t inter) {
-  if (check_verify(batch, tokens, hidden, inter) != AXK_OK || num_qo_heads <= 0 || num_kv_heads <= 0 ||
-      num_qo_heads % num_kv_heads != 0 || !(head_dim == 64 || head_dim == 128 || head_dim == 256))
-    return 0;
-  Carver c{nullptr};
-  carve_attn_verify(c, batch, batch * tokens, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
-  return c.off;
+  if (check_verify(batch, tokens, hidden, inter) != AXK_OK) return 0;
+  return attn_rows_ws(batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
 }
 
 extern "C" int axk_attn_layer_verify(
@@ -542,40 +600,131 @@ extern "C" int axk_attn_layer_verify(
     int64_t tokens, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
     int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt,
     void* workspace, size_t workspace_bytes, axk_stream_t stream) {
-  AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
-                  indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
-                  mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
-              AXK_E_NULL);
-  AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
   const size_t need = axk_attn_layer_verify_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
                                                            head_dim, inter);
+  return attn_rows_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
+                        last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
+                        mlp_down_w, mlp_down_s, out, batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
+                        page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace, workspace_bytes,
+                        stream, need);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Prefill: T new tokens per sequence through a layer in one call (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py
+// gdn_layer_prefill 57-141 and attn_layer_prefill 172-336): every projection and the MLP as B T-row matrix products
+// (the dense GEMM path from 128 rows), the GDN conv over the T tokens with its state, the delta rule in the chunked
+// form (axk_gdn_chunk_prefill: chunk-parallel solves, then the state through the chunks); the attention layer as
+// the verify layer's rows. Row t of sequence b is x row b T + t.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+struct GdnPrefillBufs {
+  uint16_t *h, *qkv, *z, *bb, *aa, *mixed, *core, *gated, *y;
+  void* cws;
+  size_t cws_bytes;
+  MlpBufs mlp;
+};
+
+GdnPrefillBufs carve_gdn_prefill(Carver& c, int64_t B, int64_t T, int64_t H, int64_t NK, int64_t NV, int64_t F) {
+  const int64_t R = B * T, KD = NK * 128, VD = NV * 128, C = 2 * KD + VD;
+  GdnPrefillBufs g;
+  g.h = c.take<uint16_t>(R * H);
+  g.qkv = c.take<uint16_t>(R * C);
+  g.z = c.take<uint16_t>(R * VD);
+  g.bb = c.take<uint16_t>(R * NV);
+  g.aa = c.take<uint16_t>(R * NV);
+  g.mixed = c.take<uint16_t>(R * C);
+  g.core = c.take<uint16_t>(R * VD);
+  g.gated = c.take<uint16_t>(R * VD);
+  g.y = c.take<uint16_t>(R * H);
+  g.cws_bytes = axk_gdn_chunk_workspace_size(B, T, NK, NV, 128, 128, 64);
+  g.cws = c.take<unsigned char>(g.cws_bytes);
+  g.mlp = carve_mlp(c, R, H, F);
+  return g;
+}
+
+}  // namespace
+
+extern "C" size_t axk_gdn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
+                                                       int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
+                                                       int64_t inter) {
+  if (check_prefill(batch, tokens, hidden, inter) != AXK_OK || head_dim != 128 || num_k_heads <= 0 ||
+      num_v_heads <= 0 || num_v_heads % num_k_heads != 0 ||
+      axk_gdn_chunk_workspace_size(batch, tokens, num_k_heads, num_v_heads, 128, 128, 64) == 0)
+    return 0;
+  Carver c{nullptr};
+  carve_gdn_prefill(c, batch, tokens, hidden, num_k_heads, num_v_heads, inter);
+  return c.off;
+}
+
+extern "C" int axk_gdn_layer_prefill(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
+    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t tokens,
+    int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
+    float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
+                  norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
+                  mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
+              AXK_E_NULL);
+  AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
+  const size_t need = axk_gdn_layer_prefill_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim,
+                                                           inter);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
-  const int64_t B = batch, T = tokens, R = B * T, H = hidden, HQ = num_qo_heads, HKV = num_kv_heads, D = head_dim,
-                F = inter;
+  const int64_t B = batch, T = tokens, R = B * T, H = hidden, NK = num_k_heads, NV = num_v_heads, F = inter;
+  const int64_t KD = NK * 128, VD = NV * 128, C = 2 * KD + VD;
   Carver c{static_cast<unsigned char*>(workspace)};
-  const AttnVerifyBufs a = carve_attn_verify(c, B, R, H, HQ, HKV, D, F);
+  const GdnPrefillBufs g = carve_gdn_prefill(c, B, T, H, NK, NV, F);
   const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
-    AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, R, H, eps, stream));
-    const AxkMxMat proj[3] = {proj_mat(proj_fmt, w_q, s_q, a.qg, HQ * 2 * D),  // per head [q | gate]
-                              proj_mat(proj_fmt, w_k, s_k, a.kk, HKV * D), proj_mat(proj_fmt, w_v, s_v, a.vv, HKV * D)};
-    AXK_TRY(projs(proj_fmt, a.h, H, proj, 3, R, H, stream));
-    // every row's K / V into the cache at its own location, then each row attends the history and the rows up to
-    // itself (the T rows are the last T tokens of the sequence's page table)
-    AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, R, HQ, HKV,
-                              D, rot, page_size, num_pages, eps, axk_stream(stream)));
-    AXK_TRY(axk_fill_iota_i32(a.qo_indptr, B, T, axk_stream(stream)));
-    AXK_TRY(axk_paged_prefill(a.q, kv_cache, a.qo_indptr, indptr, indices, last_page_len, a.attn, B, R, HQ, HKV, D,
-                              page_size, num_pages, sm_scale, nullptr, stream));
-    AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, R * HQ, D, stream));
-    const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
-    AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, R, HQ * D, stream));
-    return mlp_residual(x, a.y, ln2, mw, mlp_fmt, out, a.mlp, R, H, F, eps, stream);
+    AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, R, H, eps, stream));
+    const AxkMxMat proj[4] = {proj_mat(proj_fmt, w_qkv, s_qkv, g.qkv, C), proj_mat(proj_fmt, w_z, s_z, g.z, VD),
+                              proj_mat(proj_fmt, w_b, s_b, g.bb, NV), proj_mat(proj_fmt, w_a, s_a, g.aa, NV)};
+    AXK_TRY(projs(proj_fmt, g.h, H, proj, 4, R, H, stream));
+    // the causal conv1d + SiLU over each sequence's T tokens, from and into the conv state
+    AXK_TRY(axk_causal_conv1d_silu(g.qkv, conv_w, conv_in, conv_out, g.mixed, B, T, C, conv_kernel, stream));
+    // the delta rule over the chunks, q / k / v the channel ranges of the conv output's rows
+    AXK_TRY(axk_gdn_chunk_prefill_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias,
+                                          state_in, state_out, g.core, B, T, NK, NV, C, C, C, g.cws, g.cws_bytes,
+                                          stream));
+    AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, R * NV, 128, eps, stream));
+    const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
+    AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, R, VD, stream));
+    return mlp_residual(x, g.y, ln2, mw, mlp_fmt, out, g.mlp, R, H, F, eps, stream);
   };
   {
     const AxkValidateScope check_only;  // every sub-call's checks before the first launch
     AXK_TRY(body());
   }
   return body();
+}
+
+extern "C" size_t axk_attn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
+                                                        int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                                                        int64_t inter) {
+  if (check_prefill(batch, tokens, hidden, inter) != AXK_OK) return 0;
+  return attn_rows_ws(batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+}
+
+extern "C" int axk_attn_layer_prefill(
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
+    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, uint16_t* out, int64_t batch,
+    int64_t tokens, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
+    int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt,
+    void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  const size_t need = axk_attn_layer_prefill_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                                                            head_dim, inter);
+  return attn_rows_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
+                        last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
+                        mlp_down_w, mlp_down_s, out, batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
+                        page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace, workspace_bytes,
+                        stream, need);
 }

@@ -613,6 +613,50 @@ int axk_attn_layer_verify(const uint16_t* x, const float* ln1, const uint8_t* w_
                           float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
                           size_t workspace_bytes, axk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Prefill: `tokens` (1 .. 65536) new tokens per sequence through a layer in one call, batch * tokens <= 131072
+ * (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py: gdn_layer_prefill 57-141, attn_layer_prefill 172-336). Row t of
+ * sequence b is row b * tokens + t of x / out bf16 [batch * tokens, hidden]. Every projection and the MLP are
+ * matrix products over the batch * tokens rows; the recurrences run over each sequence's tokens in order. No
+ * per-row snapshots (the verify layers keep those). Arguments otherwise as the verify layers.
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes of axk_gdn_layer_prefill / axk_attn_layer_prefill (0 = unsupported shape). */
+size_t axk_gdn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                                            int64_t num_v_heads, int64_t head_dim, int64_t inter);
+size_t axk_attn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_qo_heads,
+                                             int64_t num_kv_heads, int64_t head_dim, int64_t inter);
+
+/* The GDN layer over each sequence's tokens (q35_prefill.py gdn_layer_prefill 57-141): the causal conv over the
+ * tokens from conv_in, the delta rule in the chunked form (64-token chunks, as axk_gdn_chunk_prefill) from state_in.
+ * state_out f32 [batch, NV, 128, 128] / conv_out bf16 [batch, conv_kernel - 1, 2 KD + VD]: after the last token (may
+ * be the inputs: in place). head_dim 128. */
+int axk_gdn_layer_prefill(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
+                          const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b, const uint8_t* w_a,
+                          const void* s_a, const uint16_t* conv_w, const float* a_log, const float* dt_bias,
+                          const float* norm_w, const uint8_t* w_out, const void* s_out, const float* ln2,
+                          const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+                          const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s,
+                          const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out,
+                          uint16_t* conv_out, int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                          int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+                          int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
+/* The attention layer over each sequence's tokens (q35_prefill.py attn_layer_prefill 172-336): every token's K / V
+ * is written at its cache_location (i32 [batch * tokens, 2]), then token t attends its sequence's history and tokens
+ * 0 .. t (the page table covers the history and all the new tokens). cos, sin bf16 [batch * tokens, rot / 2]. */
+int axk_attn_layer_prefill(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q,
+                           const uint8_t* w_k, const void* s_k, const uint8_t* w_v, const void* s_v,
+                           const float* q_norm, const float* k_norm, const uint16_t* cos, const uint16_t* sin,
+                           uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                           const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o,
+                           const void* s_o, const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                           const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                           const void* mlp_down_s, uint16_t* out, int64_t batch, int64_t tokens, int64_t hidden,
+                           int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
+                           int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
+                           int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@ from __future__ import annotations
 import torch
 
 from .rounding import bf as _bf
+from .rounding import rounding
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -259,3 +260,49 @@ def attn_layer_verify(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
                                      cache_location[:, t], num_qo_heads, rot, eps, sm_scale, proj_fmt, mlp_fmt)
         outs.append(o)
     return torch.stack(outs, 1), cache
+
+
+# ---------------------------------------------------------------------------------------------
+# Prefill (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py): T new tokens per sequence through a layer; the
+# projections and the MLP row by row as in decode, the GDN conv over the T tokens and the delta rule in the chunked
+# form the reference's prefill uses (gdn_chunked, q35_prefill.py:144-169).
+# ---------------------------------------------------------------------------------------------
+def gdn_layer_prefill(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                      proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64):
+    """gdn_layer_prefill, q35_prefill.py:57-141: x bf16 [B, T, H]. rmsnorm and the qkv / z / b / a projections over
+    the B T rows (69-74), the causal conv1d + SiLU over each sequence's tokens from its conv state (75-101), the
+    chunked delta rule from state_in (gdn.gdn_chunk with the reference's bf16 rounding points, none when the layer's
+    points are switched off; 103-109, gdn_chunked 144-169), the gated norm (125-138), the output projection and the
+    MLP (139-140). Returns (out [B, T, H], state_out, conv_out)."""
+    return gdn_layer_prefill_parts(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt, mlp_fmt,
+                                   chunk)[:3]
+
+
+def gdn_layer_prefill_parts(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                            proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64, flips: int = 2):
+    """gdn_layer_prefill and a bound on how far `flips` one-ulp changes of each row's bf16 gated output (the input of
+    the output projection, rmsnorm(core) * silu(z), whose magnitude the gate can raise well above the core's) move
+    the layer output: per row, flips times the row's largest gated ulp against the largest |W_out| of each output
+    column, the model of oracle.moe.moe_parts. Returns (out, state_out, conv_out, slack fp32 [B, T, H])."""
+    from oracle import gdn
+    from oracle import moe as omoe
+
+    b, t, hd = x.shape
+    r = b * t
+    kd, vd = num_k_heads * 128, num_v_heads * 128
+    xr = x.reshape(r, hd)
+    h = rmsnorm(xr, w["ln1"], eps)
+    qkv, z, bb, aa = (proj(h, w, n, proj_fmt) for n in ("qkv", "z", "b", "a"))
+    mixed, conv_out = causal_conv1d_silu(qkv.reshape(b, t, -1), w["conv_w"], conv_in)
+    q = mixed[..., :kd].reshape(b, t, num_k_heads, 128)
+    k = mixed[..., kd:2 * kd].reshape(b, t, num_k_heads, 128)
+    v = mixed[..., 2 * kd:].reshape(b, t, num_v_heads, 128)
+    core, state_out = gdn.gdn_chunk(q, k, v, aa.reshape(b, t, num_v_heads), bb.reshape(b, t, num_v_heads),
+                                    w["a_log"], w["dt_bias"], state_in, chunk=chunk, round_bf16=rounding())
+    core = _bf(core).reshape(r * num_v_heads, 128)
+    gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(r * num_v_heads, 128), eps).reshape(r, vd)
+    y = proj(gated, w, "out", proj_fmt)
+    out = mlp_residual(xr, y, w, eps, mlp_fmt).reshape(b, t, hd)
+    wo = dequant_weight(w, "out", proj_fmt)
+    slack = flips * omoe.ulp_bf16(gated.float()).amax(dim=1)[:, None] * wo.abs().amax(dim=1)[None, :]
+    return out, state_out, conv_out, slack.reshape(b, t, hd)

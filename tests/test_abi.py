@@ -82,6 +82,22 @@ def test_moe_workspace_size_limits():
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="drives entry points with host pointers: only on a GPU-less host")
+def test_prefill_layer_workspace_limits():
+    lib = _lib.load()
+    assert lib.axk_gdn_layer_prefill_workspace_size(2, 100, 256, 2, 4, 128, 512) > 0
+    assert lib.axk_gdn_layer_prefill_workspace_size(1, 1 << 16, 256, 2, 4, 128, 512) > 0
+    assert lib.axk_gdn_layer_prefill_workspace_size(1, (1 << 16) + 1, 256, 2, 4, 128, 512) == 0  # tokens <= 65536
+    assert lib.axk_gdn_layer_prefill_workspace_size(3, 1 << 16, 256, 2, 4, 128, 512) == 0  # rows <= 131072
+    assert lib.axk_gdn_layer_prefill_workspace_size(2, 100, 256, 2, 4, 64, 512) == 0  # head_dim 128
+    assert lib.axk_gdn_layer_prefill_workspace_size(2, 100, 256, 2, 3, 128, 512) == 0  # NV % NK
+    assert lib.axk_attn_layer_prefill_workspace_size(2, 100, 256, 4, 2, 256, 512) > 0
+    assert lib.axk_attn_layer_prefill_workspace_size(2, 100, 256, 4, 2, 96, 512) == 0  # head_dim 64 / 128 / 256
+    assert lib.axk_attn_layer_prefill_workspace_size(2, 100, 256, 5, 2, 256, 512) == 0  # HQ % HKV
+    # the attention prefill's workspace is the verify layer's at the same rows
+    assert (lib.axk_attn_layer_prefill_workspace_size(4, 16, 256, 4, 2, 256, 512) ==
+            lib.axk_attn_layer_verify_workspace_size(4, 16, 256, 4, 2, 256, 512))
+
+
 def test_entry_points_reach_the_launch_on_a_gpu_less_host():
     """Every host-side step of an entry point (argument checks, the layers' validate-only pass, workspace carving)
     runs on a host without a GPU and ends at the launch with AXK_E_LAUNCH, never a crash."""
@@ -107,3 +123,9 @@ def test_entry_points_reach_the_launch_on_a_gpu_less_host():
     assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], gws, None) == 3
     # an unknown weight format is refused before anything else
     assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 7, 2, p[150], gws, None) == 4
+    # the prefill layer: 20 tokens of one sequence; a late misaligned w_out found before the conv / state launches
+    pws = lib.axk_gdn_layer_prefill_workspace_size(1, 20, 256, 1, 2, 128, 256)
+    assert 0 < pws < 65536 * 48
+    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws, None) == launch
+    assert lib.axk_gdn_layer_prefill(*bad, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws, None) == 3
+    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws - 1, None) == 6

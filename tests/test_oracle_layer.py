@@ -297,6 +297,29 @@ def test_attn_verify_oracle_is_causal_and_one_row_is_a_decode_step():
     assert torch.equal(one[:, 0], dec)
 
 
+@pytest.mark.parametrize("t,chunk", [(7, 64), (20, 8), (21, 4)])
+def test_gdn_prefill_oracle_equals_decode_steps(t, chunk):
+    """gdn_layer_prefill (the chunked delta rule over T tokens, conv over the tokens) equals T decode steps of the
+    layer (the recurrent form, pinned to transformers' decoder layer) in fp32 arithmetic, for one chunk and for
+    several chunks with a ragged last one; and the bf16 schedule stays within the fused bar of it."""
+    from axk import configs
+
+    g = torch.Generator().manual_seed(t)
+    w = configs.gdn_layer_weights(g, 128, 128, 1, 2)
+    x = torch.randn(2, t, 128, generator=g).bfloat16()
+    st = torch.randn(2, 2, 128, 128, generator=g) * 0.02
+    cv = torch.randn(2, 3, 512, generator=g).bfloat16()
+    with rounding.fp32():
+        po, ps, pc = layer.gdn_layer_prefill(x, w, st, cv, 1, 2, chunk=chunk)
+        ro, rs, rc, _, _ = layer.gdn_layer_verify(x, w, st, cv, 1, 2)
+    torch.testing.assert_close(po.float(), ro.float(), rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(ps, rs, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(pc, rc, rtol=1e-5, atol=1e-6)  # fp32 products over B T rows vs B rows
+    bo, bs, _ = layer.gdn_layer_prefill(x, w, st, cv, 1, 2, chunk=chunk)
+    torch.testing.assert_close(bo.float(), ro.float(), rtol=5e-2, atol=0.0625)
+    torch.testing.assert_close(bs, rs, rtol=5e-2, atol=3e-3)
+
+
 # ---- the MoE block of the MoE decode layers (moe_full, q35_layer_mc.py:797-853) ----
 @pytest.mark.parametrize("fmt", ["fp8", "mxfp8", "mxfp4"])
 def test_dequant_weight_is_what_proj_multiplies(fmt):
