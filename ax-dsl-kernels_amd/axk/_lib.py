@@ -94,23 +94,27 @@ SIGNATURES: dict[str, list] = {
     "axk_silu_mul": [_vp, _vp, _vp, _i64, _i64, _vp],
     "axk_add": [_vp, _vp, _vp, _i64, _i64, _vp],
     "axk_gdn_layer_workspace_size": [_i64] * 6,
-    "axk_gdn_layer_decode": [_vp] * 28 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_gdn_layer_decode": [_vp] * 28 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _i32, _vp, ctypes.c_size_t,
+                             _vp],
     "axk_attn_layer_workspace_size": [_i64] * 6,
     "axk_gdn_layer_verify_workspace_size": [_i64] * 7,
     "axk_attn_layer_verify_workspace_size": [_i64] * 7,
-    "axk_gdn_layer_verify": [_vp] * 30 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_gdn_layer_verify": [_vp] * 30 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _i32, _vp, ctypes.c_size_t,
+                             _vp],
     "axk_attn_layer_verify": [_vp] * 27 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                               ctypes.c_size_t, _vp],
     "axk_attn_layer_decode": [_vp] * 27 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                               ctypes.c_size_t, _vp],
     "axk_gdn_layer_moe_workspace_size": [_i64] * 6 + [_vp],
     "axk_attn_layer_moe_workspace_size": [_i64] * 6 + [_vp],
-    "axk_gdn_layer_decode_moe": [_vp] * 29 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_gdn_layer_decode_moe": [_vp] * 29 + [_i64] * 7 + [ctypes.c_float, _i32, _i32, _i32, _vp,
+                                 ctypes.c_size_t, _vp],
     "axk_attn_layer_decode_moe": [_vp] * 28 + [_i64] * 9 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                                   ctypes.c_size_t, _vp],
     "axk_gdn_layer_prefill_workspace_size": [_i64] * 7,
     "axk_attn_layer_prefill_workspace_size": [_i64] * 7,
-    "axk_gdn_layer_prefill": [_vp] * 28 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _vp, ctypes.c_size_t, _vp],
+    "axk_gdn_layer_prefill": [_vp] * 28 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _i32, _vp, ctypes.c_size_t,
+                              _vp],
     "axk_attn_layer_prefill": [_vp] * 27 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                                ctypes.c_size_t, _vp],
 }

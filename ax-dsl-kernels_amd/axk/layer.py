@@ -9,6 +9,10 @@ s_<name>, in the format given by proj_fmt / mlp_fmt:
   "mxfp4" (w u8 E2M1 pairs [N, K/2], s u8 E8M0 [N, K/32])    - the 9B / 27B manifests and config 4's MLP
 norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is allocated once by the caller
 (layer_workspace) and reused; a layer call allocates nothing.
+
+GDN value-head order (v_order, q35_step.py:82-85): "tiled" (value head vh reads key head vh % NK; the order the
+reference's layer kernels are built with by default, its exported weights permuted to it by v_tiled, 351-358) or
+"grouped" (vh / (NV / NK), the checkpoint's). tile_value_heads converts a grouped weight dict to the tiled order.
 """
 from __future__ import annotations
 
@@ -24,6 +28,52 @@ GDN_WEIGHTS = ("ln1", "w_qkv", "s_qkv", "w_z", "s_z", "w_b", "s_b", "w_a", "s_a"
 ATTN_WEIGHTS = ("ln1", "w_q", "s_q", "w_k", "s_k", "w_v", "s_v", "q_norm", "k_norm", "w_o", "s_o", "ln2")
 MLP_WEIGHTS = ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down")
 WFMT = {"fp8": 0, "mxfp8": 1, "mxfp4": 2}  # AXK_WFMT_FP8_CHANNEL, AXK_WFMT_MXFP8, AXK_WFMT_MXFP4
+VORDER = {"grouped": 0, "tiled": 1}  # AXK_VORDER_GROUPED, AXK_VORDER_TILED
+
+
+def _vorder(name: str) -> int:
+    _check(name in VORDER, f"v_order must be one of {sorted(VORDER)}, got {name!r}")
+    return VORDER[name]
+
+
+def v_tiled(t: torch.Tensor, dim: int, num_k_heads: int, num_v_heads: int, unit: int) -> torch.Tensor:
+    """The value heads along `dim` (each `unit` entries wide) from the grouped order to the tiled one: entry
+    (vo, kh) of the result is entry (kh, vo) of t (q35_step.py v_tiled 351-358)."""
+    if num_v_heads == num_k_heads:
+        return t
+    sh = list(t.shape)
+    _check(sh[dim] == num_v_heads * unit, f"dim {dim} of {sh} is not {num_v_heads} heads of {unit}")
+    t = t.reshape(sh[:dim] + [num_k_heads, num_v_heads // num_k_heads, unit] + sh[dim + 1:]).transpose(dim, dim + 1)
+    return t.contiguous().reshape(sh)
+
+
+def tile_value_heads(w: dict, num_k_heads: int, num_v_heads: int, proj_fmt: str = "fp8") -> dict:
+    """A GDN layer's weight dict in the grouped value-head order -> the tiled one (the reference's gdn_args,
+    q35_step.py:361-377): the v rows of w_qkv / conv_w, the rows of w_z, w_b, w_a and their scales, a_log, dt_bias,
+    and the input columns of w_out (with its MX scale columns). Other entries are passed through. States of that
+    layer convert with v_tiled (the recurrent state along dim 1, unit 1; the conv state's v channels, unit 128)."""
+    nk, nv = num_k_heads, num_v_heads
+    kd = 2 * nk * 128
+    out = dict(w)
+
+    def rows(name, unit, start=0):
+        t = w[name]
+        out[name] = torch.cat((t[:start], v_tiled(t[start:], 0, nk, nv, unit))) if start else v_tiled(t, 0, nk, nv,
+                                                                                                      unit)
+
+    rows("w_qkv", 128, kd)
+    rows("conv_w", 128, kd)
+    rows("w_z", 128)
+    rows("w_b", 1)
+    rows("w_a", 1)
+    rows("a_log", 1)
+    rows("dt_bias", 1)
+    for name, unit, start in (("s_qkv", 128, kd), ("s_z", 128, 0), ("s_b", 1, 0), ("s_a", 1, 0)):
+        rows(name, unit, start)  # per-row scales: f32 [N] or E8M0 [N, K/32], rows as their weight's
+    out["w_out"] = v_tiled(w["w_out"], 1, nk, nv, 64 if proj_fmt == "mxfp4" else 128)
+    if proj_fmt != "fp8":  # E8M0 [H, VD / 32]: 4 scale columns per value head
+        out["s_out"] = v_tiled(w["s_out"], 1, nk, nv, 4)
+    return out
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -112,7 +162,7 @@ def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
                      num_k_heads: int, num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                      out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
                      conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
-                     moe: Optional[dict] = None):
+                     moe: Optional[dict] = None, v_order: str = "tiled"):
     """x bf16 [B, hidden]; state f32 [B, NV, 128, 128]; conv state bf16 [B, K-1, 2 KD + VD].
     Returns (out, state_out, conv_out); state_out / conv_out may be the inputs (in place).
     moe (optional, see moe_block): the MLP is the MoE block, whose shared expert is the MLP weights
@@ -131,8 +181,8 @@ def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args, *extra)
     ptrs = [t.data_ptr() for t in args]
     tail = (state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(), so.data_ptr(), co.data_ptr(), b, h, num_k_heads,
-            num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(),
-            _lib.stream_of(x))
+            num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), _vorder(v_order), ws.data_ptr(),
+            ws.numel(), _lib.stream_of(x))
     # the C order: x, ln1 .. s_out, ln2, MLP, [moe], state_in, conv_in, out, state_out, conv_out
     if moe is None:
         _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, *tail)
@@ -200,7 +250,8 @@ def gdn_layer_verify(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
                      num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                      out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
                      conv_out: Optional[torch.Tensor] = None, state_snap: Optional[torch.Tensor] = None,
-                     conv_snap: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+                     conv_snap: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
+                     v_order: str = "tiled"):
     """x bf16 [B, T, hidden]: T new rows per sequence. state f32 [B, NV, 128, 128]; conv state bf16
     [B, K-1, 2 KD + VD]. Returns (out [B, T, hidden], state_out, conv_out) after the last row; the optional
     snapshots state_snap f32 [T, B, NV, 128, 128] and conv_snap bf16 [T, B, K-1, C] receive the states after
@@ -223,8 +274,8 @@ def gdn_layer_verify(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     ptrs = [t_.data_ptr() for t_ in args]
     _lib.call("axk_gdn_layer_verify", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
               so.data_ptr(), co.data_ptr(), _lib.ptr(state_snap), _lib.ptr(conv_snap), b, t, h, num_k_heads,
-              num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(),
-              _lib.stream_of(x))
+              num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), _vorder(v_order), ws.data_ptr(),
+              ws.numel(), _lib.stream_of(x))
     return o, so, co
 
 
@@ -279,7 +330,8 @@ def attn_prefill_workspace(batch: int, tokens: int, hidden: int, num_qo_heads: i
 def gdn_layer_prefill(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: torch.Tensor, num_k_heads: int,
                       num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                       out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
-                      conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+                      conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
+                      v_order: str = "tiled"):
     """x bf16 [B, T, hidden]: T new tokens per sequence. state f32 [B, NV, 128, 128]; conv state bf16
     [B, K-1, 2 KD + VD]. Returns (out [B, T, hidden], state_out, conv_out) after the last token."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
@@ -296,7 +348,7 @@ def gdn_layer_prefill(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in:
     ptrs = [t_.data_ptr() for t_ in args]
     _lib.call("axk_gdn_layer_prefill", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
               so.data_ptr(), co.data_ptr(), b, t, h, num_k_heads, num_v_heads, 128, kconv, inter, eps,
-              _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+              _fmt(proj_fmt), _fmt(mlp_fmt), _vorder(v_order), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
     return o, so, co
 
 

@@ -48,7 +48,8 @@ struct AxkValidateScope {
 // straight out of the conv output. state_snap (optional): the fp32 state after token t, [batch, NV, DK, DV] at
 // state_snap + t * snap_ld elements. Returns an AXK status.
 // With gate (optional), out is the GDN output norm of each head's row: bf16(bf16(rmsnorm(o) * norm_w) * silu(z)),
-// z [batch, tokens, num_v_heads, 128] contiguous.
+// z [batch, tokens, num_v_heads, 128] contiguous. v_order: AXK_VORDER_GROUPED or AXK_VORDER_TILED (which key head
+// each value head reads).
 struct AxkGdnStrides {
   int64_t q, k, v, ab;
 };
@@ -60,8 +61,8 @@ struct AxkGdnGate {
 __attribute__((visibility("hidden"))) int axk_gdn_recurrent_strided(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
     const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
-    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, hipStream_t stream,
-    float* state_snap = nullptr, int64_t snap_ld = 0);
+    int64_t num_k_heads, int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, int v_order,
+    hipStream_t stream, float* state_snap = nullptr, int64_t snap_ld = 0);
 
 // Internal (not exported): the conv state after each of a sequence's `tokens` new rows (speculative verification's
 // per-row snapshots): snapshot t holds the last kernel - 1 inputs of [state_in | x rows 0 .. t] (oldest first), written
@@ -131,9 +132,9 @@ __attribute__((visibility("hidden"))) int axk_moe_decode_shared_given(
 
 // Internal (not exported): axk_gdn_chunk_prefill (chunk 64, head dims 128) with q, k, v read at row strides ldq, ldk,
 // ldv (elements between consecutive (sequence, token) rows; the heads of a row contiguous), so the prefill layer
-// reads them straight out of the conv output. Returns an AXK status.
+// reads them straight out of the conv output, and the value-head order v_order (AXK_VORDER_*). Returns an AXK status.
 __attribute__((visibility("hidden"))) int axk_gdn_chunk_prefill_strided(
     const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a, const uint16_t* b, const float* a_log,
     const float* dt_bias, const float* state_in, float* state_out, uint16_t* out, int64_t batch, int64_t tokens,
-    int64_t num_k_heads, int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, void* workspace,
+    int64_t num_k_heads, int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, int v_order, void* workspace,
     size_t workspace_bytes, axk_stream_t stream);

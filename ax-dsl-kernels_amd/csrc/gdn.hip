@@ -6,7 +6,9 @@
 //   g      = -exp(A_log[h]) * softplus(a + dt_bias[h]);  beta = sigmoid(b)          (gdn_gate, gdn.py:934-949)
 //   S     <- exp(g) S;  pred = k^T S;  err = beta (v - pred);  S <- S + k err^T;  o = q^T S
 //            (gdn_recurrent_step, gdn.py:952-989)
-// Value head h reads key head h / (NV / NK) (grouped GQA order, test_gdn_attn.py:268-277).
+// Value head h reads key head (h / kdiv) % NK: kdiv = NV / NK in the grouped order (h / (NV / NK), the operators'
+// order, test_gdn_attn.py:268-277), kdiv = 1 in the tiled order (h % NK, the layer kernels' default order,
+// models/qwen35_35b_a3b/src/70b0fbc/q35_step.py:82-85, 171).
 // The state S [DK, DV] fp32 is the kernel's whole HBM traffic: a workgroup holds its 128 x 128 tile in
 // registers (64 floats per thread, float4 loads along DV) from one read to one write, across all T tokens.
 // Arithmetic is fp32 throughout (the reference rounds the state to bf16 for its two products; the
@@ -43,6 +45,7 @@ struct GdnArgs {
   float eps;
   float* snap;                  // optional: the state after token t at snap + t * snap_ld, [B, NV, DK, DV] each
   int64_t snap_ld;
+  int kdiv;                     // value head h reads key head (h / kdiv) % NK
 };
 
 template <bool GATE>
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
 
   const int bh = blockIdx.x;
   const int b = bh / p.NV, h = bh - (bh / p.NV) * p.NV;
-  const int kh = h / (p.NV / p.NK);
+  const int kh = (h / p.kdiv) % p.NK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cg = tid % kColGroups, rg = tid / kColGroups;
   const int c0 = 4 * cg, r0 = kRows * rg;
@@ -181,9 +184,10 @@ __global__ __launch_bounds__(kThreads) void gdn_recurrent_kernel(GdnArgs p) {
 int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
                               const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
                               float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
-                              int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate,
+                              int64_t num_v_heads, const AxkGdnStrides& ld, const AxkGdnGate* gate, int v_order,
                               hipStream_t stream, float* state_snap, int64_t snap_ld) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
+  AXK_REQUIRE(v_order == AXK_VORDER_GROUPED || v_order == AXK_VORDER_TILED, AXK_E_SHAPE);
   AXK_REQUIRE(!gate || (gate->norm_w && gate->z), AXK_E_NULL);
   AXK_REQUIRE(batch > 0 && tokens > 0 && num_k_heads > 0 && num_v_heads > 0, AXK_E_SHAPE);
   AXK_REQUIRE(num_v_heads % num_k_heads == 0, AXK_E_SHAPE);
@@ -207,7 +211,8 @@ int axk_gdn_recurrent_strided(const uint16_t* q, const uint16_t* k, const uint16
   }
   GdnArgs p{q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, (int)batch, (int)tokens, (int)num_k_heads,
             (int)num_v_heads, ld.q, ld.k, ld.v, ld.ab, gate ? gate->norm_w : nullptr, gate ? gate->z : nullptr,
-            gate ? gate->eps : 0.f, state_snap, snap_ld};
+            gate ? gate->eps : 0.f, state_snap, snap_ld,
+            v_order == AXK_VORDER_TILED ? 1 : (int)(num_v_heads / num_k_heads)};
   AXK_LAUNCH_GATE();
   if (gate)
     hipLaunchKernelGGL(gdn_recurrent_kernel<true>, dim3((unsigned)(batch * num_v_heads)), dim3(kThreads), 0, stream, p);
@@ -223,5 +228,5 @@ extern "C" int axk_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uin
   AXK_REQUIRE(head_k_dim == kDK && head_v_dim == kDV, AXK_E_SHAPE);
   const AxkGdnStrides ld{num_k_heads * kDK, num_k_heads * kDK, num_v_heads * kDV, num_v_heads};
   return axk_gdn_recurrent_strided(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens,
-                                   num_k_heads, num_v_heads, ld, nullptr, axk_stream(stream));
+                                   num_k_heads, num_v_heads, ld, nullptr, AXK_VORDER_GROUPED, axk_stream(stream));
 }

@@ -102,6 +102,7 @@ struct PrepArgs {
   ChunkWs ws;
   int B, T, NK, NV, NC;
   int64_t ldq, ldk, ldv;  // elements between consecutive (sequence, token) rows of q, k, v
+  int kdiv;               // value head h reads key head (h / kdiv) % NK: NV / NK grouped, 1 tiled
 };
 
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   float* sBeta = sG + kC;
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int per_key = p.NV / p.NK, kh = h / per_key;
+  const int kh = (h / p.kdiv) % p.NK;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int t0 = c * kC;
@@ -195,8 +196,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   }
   __syncthreads();
 
-  // ---- 2. normalised q and k^T of this key head (written once, by its first value head) ----
-  if (h % per_key == 0) {
+  // ---- 2. normalised q and k^T of this key head (written once, by its first value head, kh * kdiv) ----
+  if (h == kh * p.kdiv) {
     uint16_t* qn_g = p.ws.qn + kidx * kC * kD;
     uint16_t* kt_g = p.ws.kt + kidx * kD * kC;
     for (int i = tid; i < kC * kD / 8; i += 256) {  // fragment order: unit i of the destination
@@ -422,6 +423,7 @@ struct ScanArgs {
   uint16_t* out;
   ChunkWs ws;
   int B, T, NK, NV, NC;
+  int kdiv;  // value head h reads key head (h / kdiv) % NK
 };
 
 // Scan workgroup (sequence, value head, slice of SW state columns) with NW waves. Wave w: token tile
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
   __shared__ __align__(16) uint16_t sXd[SW * kLdV];
   const int nbh = p.B * p.NV;
   const int slice = blockIdx.x / nbh, bh = blockIdx.x - slice * nbh;  // slices of a head share an XCD
-  const int b = bh / p.NV, h = bh - b * p.NV, kh = h / (p.NV / p.NK);
+  const int b = bh / p.NV, h = bh - b * p.NV, kh = (h / p.kdiv) % p.NK;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, g4 = lane >> 4;
   const int tt = wave & 3;
   const int ct_l = (wave >> 2) * CPW;         // first column tile of this wave inside the slice
@@ -625,8 +627,9 @@ int chunk_prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v, 
                        const float* a_log, const float* dt_bias, const float* state_in, float* state_out,
                        uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads, int64_t num_v_heads,
                        int64_t head_k_dim, int64_t head_v_dim, int64_t chunk_size, int64_t ldq, int64_t ldk,
-                       int64_t ldv, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+                       int64_t ldv, int v_order, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(q && k && v && a && b && a_log && dt_bias && state_in && state_out && out, AXK_E_NULL);
+  AXK_REQUIRE(v_order == AXK_VORDER_GROUPED || v_order == AXK_VORDER_TILED, AXK_E_SHAPE);
   const int rc = check_chunk_dims(batch, tokens, num_k_heads, num_v_heads, head_k_dim, head_v_dim, chunk_size);
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(k, 16) && axk_aligned(v, 16), AXK_E_ALIGN);
@@ -654,13 +657,14 @@ int chunk_prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v, 
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
+  const int kdiv = v_order == AXK_VORDER_TILED ? 1 : (int)(num_v_heads / num_k_heads);
   PrepArgs pa{q, k, v, a, b, a_log, dt_bias, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC,
-              ldq, ldk, ldv};
+              ldq, ldk, ldv, kdiv};
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3((unsigned)NC, (unsigned)num_v_heads, (unsigned)batch), dim3(256),
                      kPrepLds, st, pa);
   int lrc = axk_launch_status();
   if (lrc != AXK_OK) return lrc;
-  ScanArgs sa{state_in, state_out, out, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC};
+  ScanArgs sa{state_in, state_out, out, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC, kdiv};
   hipLaunchKernelGGL((gdn_chunk_scan_kernel<kScanSW, kScanNW>), dim3((unsigned)((kD / kScanSW) * batch * num_v_heads)),
                      dim3(64 * kScanNW), 0, st, sa);
   return axk_launch_status();
@@ -675,14 +679,14 @@ extern "C" int axk_gdn_chunk_prefill(const uint16_t* q, const uint16_t* k, const
                                      axk_stream_t stream) {
   return chunk_prefill_impl(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens, num_k_heads,
                             num_v_heads, head_k_dim, head_v_dim, chunk_size, num_k_heads * kD, num_k_heads * kD,
-                            num_v_heads * kD, workspace, workspace_bytes, stream);
+                            num_v_heads * kD, AXK_VORDER_GROUPED, workspace, workspace_bytes, stream);
 }
 
 int axk_gdn_chunk_prefill_strided(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
                                   const uint16_t* b, const float* a_log, const float* dt_bias, const float* state_in,
                                   float* state_out, uint16_t* out, int64_t batch, int64_t tokens, int64_t num_k_heads,
-                                  int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, void* workspace,
-                                  size_t workspace_bytes, axk_stream_t stream) {
+                                  int64_t num_v_heads, int64_t ldq, int64_t ldk, int64_t ldv, int v_order,
+                                  void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   return chunk_prefill_impl(q, k, v, a, b, a_log, dt_bias, state_in, state_out, out, batch, tokens, num_k_heads,
-                            num_v_heads, kD, kD, kC, ldq, ldk, ldv, workspace, workspace_bytes, stream);
+                            num_v_heads, kD, kD, kC, ldq, ldk, ldv, v_order, workspace, workspace_bytes, stream);
 }

@@ -208,7 +208,7 @@ int gdn_layer_impl(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, co
                    const void* mlp_down_s, const axk_moe_block* moe, const float* state_in, const uint16_t* conv_in,
                    uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
                    int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
-                   float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes,
+                   float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
                    axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
@@ -236,7 +236,7 @@ int gdn_layer_impl(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, co
     const AxkGdnStrides ld{C, C, C, NV};
     const AxkGdnGate gate{norm_w, g.z, eps};
     AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
-                                      state_out, g.gated, B, 1, NK, NV, ld, &gate, axk_stream(stream)));
+                                      state_out, g.gated, B, 1, NK, NV, ld, &gate, v_order, axk_stream(stream)));
     const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
     AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, B, VD, stream));
     if (moe) return moe_residual(x, g.y, ln2, mw, mlp_fmt, *moe, out, g.mlp, eb, B, H, F, eps, stream);
@@ -319,11 +319,12 @@ extern "C" int axk_gdn_layer_decode(
     const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
     const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden,
     int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
-    int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+    int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   return gdn_layer_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
                         s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, nullptr,
                         state_in, conv_in, out, state_out, conv_out, batch, hidden, num_k_heads, num_v_heads,
-                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, workspace, workspace_bytes, stream);
+                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, v_order, workspace, workspace_bytes,
+                        stream);
 }
 
 extern "C" size_t axk_gdn_layer_moe_workspace_size(int64_t batch, int64_t hidden, int64_t num_k_heads,
@@ -340,13 +341,14 @@ extern "C" int axk_gdn_layer_decode_moe(
     const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
     const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
     int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel,
-    int64_t inter, float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes,
+    int64_t inter, float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
     axk_stream_t stream) {
   AXK_REQUIRE(moe, AXK_E_NULL);
   return gdn_layer_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
                         s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, moe,
                         state_in, conv_in, out, state_out, conv_out, batch, hidden, num_k_heads, num_v_heads,
-                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, workspace, workspace_bytes, stream);
+                        head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, v_order, workspace, workspace_bytes,
+                        stream);
 }
 
 extern "C" size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads,
@@ -537,8 +539,8 @@ extern "C" int axk_gdn_layer_verify(
     const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
     const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, float* state_snap,
     uint16_t* conv_snap, int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
-    int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, void* workspace,
-    size_t workspace_bytes, axk_stream_t stream) {
+    int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, int v_order,
+    void* workspace, size_t workspace_bytes, axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
                   mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
@@ -570,8 +572,8 @@ extern "C" int axk_gdn_layer_verify(
     const AxkGdnStrides ld{C, C, C, NV};
     const AxkGdnGate gate{norm_w, g.z, eps};
     AXK_TRY(axk_gdn_recurrent_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias, state_in,
-                                      state_out, g.gated, B, T, NK, NV, ld, &gate, axk_stream(stream), state_snap,
-                                      B * NV * DH * DH));
+                                      state_out, g.gated, B, T, NK, NV, ld, &gate, v_order, axk_stream(stream),
+                                      state_snap, B * NV * DH * DH));
     const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
     AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, R, VD, stream));
     return mlp_residual(x, g.y, ln2, mw, mlp_fmt, out, g.mlp, R, H, F, eps, stream);
@@ -665,7 +667,8 @@ extern "C" int axk_gdn_layer_prefill(
     const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
     const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t tokens,
     int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
-    float eps, int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+    float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+    axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
                   mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
@@ -689,8 +692,8 @@ extern "C" int axk_gdn_layer_prefill(
     AXK_TRY(axk_causal_conv1d_silu(g.qkv, conv_w, conv_in, conv_out, g.mixed, B, T, C, conv_kernel, stream));
     // the delta rule over the chunks, q / k / v the channel ranges of the conv output's rows
     AXK_TRY(axk_gdn_chunk_prefill_strided(g.mixed, g.mixed + KD, g.mixed + 2 * KD, g.aa, g.bb, a_log, dt_bias,
-                                          state_in, state_out, g.core, B, T, NK, NV, C, C, C, g.cws, g.cws_bytes,
-                                          stream));
+                                          state_in, state_out, g.core, B, T, NK, NV, C, C, C, v_order, g.cws,
+                                          g.cws_bytes, stream));
     AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, R * NV, 128, eps, stream));
     const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
     AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, R, VD, stream));

@@ -61,6 +61,12 @@ typedef void* axk_stream_t; /* hipStream_t */
 #define AXK_WFMT_MXFP8 1
 #define AXK_WFMT_MXFP4 2
 
+/* Value-head order of the GDN layers when num_v_heads > num_k_heads: which key head value head vh reads
+ * (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py:82-85; the weights of the value heads, w_qkv's v rows, conv_w's
+ * v rows, w_z, w_b, w_a, a_log, dt_bias, w_out's columns and the state, are in the same order). */
+#define AXK_VORDER_GROUPED 0 /* vh / (NV / NK): the checkpoint's order, the GDN operators' */
+#define AXK_VORDER_TILED 1   /* vh % NK: the order the reference's layer kernels are built with by default */
+
 /* Library identification and error text. */
 const char* axk_version(void);
 const char* axk_status_string(int status);
@@ -464,7 +470,9 @@ size_t axk_gdn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_k
  *   w_b, w_a [num_v_heads, hidden], w_out [hidden, VD] (FP8, scales f32 [N]); conv_w bf16 [2 KD + VD, conv_kernel];
  *   a_log, dt_bias f32 [num_v_heads]; norm_w f32 [head_dim]; MLP gate / up [inter, hidden], down [hidden, inter]
  *   (MXFP4); state f32 [batch, num_v_heads, 128, 128] (in place allowed); conv state bf16
- *   [batch, conv_kernel - 1, 2 KD + VD] (in place allowed). KD = num_k_heads * 128, VD = num_v_heads * 128. */
+ *   [batch, conv_kernel - 1, 2 KD + VD] (in place allowed). KD = num_k_heads * 128, VD = num_v_heads * 128.
+ *   v_order: AXK_VORDER_TILED for weights exported in the reference's default layer order, AXK_VORDER_GROUPED for
+ *   the checkpoint's (the same for every GDN layer entry). */
 int axk_gdn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
                          const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b,
                          const uint8_t* w_a, const void* s_a, const uint16_t* conv_w, const float* a_log,
@@ -474,7 +482,8 @@ int axk_gdn_layer_decode(const uint16_t* x, const float* ln1, const uint8_t* w_q
                          const void* mlp_down_s, const float* state_in, const uint16_t* conv_in, uint16_t* out,
                          float* state_out, uint16_t* conv_out, int64_t batch, int64_t hidden, int64_t num_k_heads,
                          int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
-                         int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                         int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+                         axk_stream_t stream);
 
 /* Workspace bytes of axk_attn_layer_decode (0 = unsupported shape). */
 size_t axk_attn_layer_workspace_size(int64_t batch, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
@@ -550,7 +559,7 @@ int axk_gdn_layer_decode_moe(const uint16_t* x, const float* ln1, const uint8_t*
                              const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
                              int64_t batch, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
                              int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps, int proj_fmt,
-                             int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                             int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 /* attn_layer_full_mx (q35_layer_mc.py:867-880): axk_attn_layer_decode with the MoE block as its MLP. */
 int axk_attn_layer_decode_moe(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q,
@@ -594,8 +603,8 @@ int axk_gdn_layer_verify(const uint16_t* x, const float* ln1, const uint8_t* w_q
                          const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out,
                          uint16_t* conv_out, float* state_snap, uint16_t* conv_snap, int64_t batch, int64_t tokens,
                          int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
-                         int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, void* workspace,
-                         size_t workspace_bytes, axk_stream_t stream);
+                         int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, int v_order,
+                         void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
 /* The attention layer over the rows (verify_group_m4.py attn_rows 226-300): every row's K / V is written at its
  * cache_location (i32 [batch * tokens, 2]), then row t attends its sequence's history and rows 0 .. t (the page table
@@ -640,7 +649,8 @@ int axk_gdn_layer_prefill(const uint16_t* x, const float* ln1, const uint8_t* w_
                           const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out,
                           uint16_t* conv_out, int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
                           int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
-                          int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
+                          int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+                          axk_stream_t stream);
 
 /* The attention layer over each sequence's tokens (q35_prefill.py attn_layer_prefill 172-336): every token's K / V
  * is written at its cache_location (i32 [batch * tokens, 2]), then token t attends its sequence's history and tokens

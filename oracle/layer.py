@@ -155,15 +155,28 @@ def moe_block_parts(x, y, w: dict, moe: dict, eps: float = 1e-6, fmt: str = "mxf
     return base, routed, slack, logits, ids, wts
 
 
+def value_head_keys(x, num_v_heads: int, v_order: str):
+    """q or k [B, T, NK, D] -> [B, T, NV, D]: the key head each value head reads. "grouped": value head vh reads key
+    head vh / (NV / NK) (the checkpoint's order and the GDN operators', test_gdn_attn.py:268-277); "tiled": vh % NK,
+    the order the reference's layer kernels are built with by default (models/qwen35_35b_a3b/src/70b0fbc/
+    q35_step.py:82-85 VORDER; 171: vh = vo * NK + kh)."""
+    rep = num_v_heads // x.shape[2]
+    if v_order == "grouped":
+        return x.repeat_interleave(rep, dim=2)
+    assert v_order == "tiled", v_order
+    return x.repeat(1, 1, rep, 1)
+
+
 def gdn_layer_decode(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
-                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", v_order: str = "tiled"):
     """One token per sequence. Returns (out bf16 [B, H], state_out f32, conv_out bf16)."""
-    y, state_out, conv_out = gdn_layer_half(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt)
+    y, state_out, conv_out = gdn_layer_half(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt,
+                                            v_order)
     return mlp_residual(x, y, w, eps, mlp_fmt), state_out, conv_out
 
 
 def gdn_layer_half(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
-                   proj_fmt: str = "fp8"):
+                   proj_fmt: str = "fp8", v_order: str = "tiled"):
     """The GDN layer up to its output projection y (bf16, before the residual and the MLP / MoE block).
     Returns (y, state_out, conv_out)."""
     from oracle import gdn
@@ -177,6 +190,7 @@ def gdn_layer_half(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads:
     q = m[:, :kd].reshape(b, 1, num_k_heads, 128)
     k = m[:, kd:2 * kd].reshape(b, 1, num_k_heads, 128)
     v = m[:, 2 * kd:].reshape(b, 1, num_v_heads, 128)
+    q, k = value_head_keys(q, num_v_heads, v_order), value_head_keys(k, num_v_heads, v_order)
     core, state_out = gdn.gdn_fp32(q, k, v, aa[:, None], bb[:, None], w["a_log"], w["dt_bias"], state_in)
     core = _bf(core).reshape(b * num_v_heads, 128)
     gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(b * num_v_heads, 128), eps).reshape(b, vd)
@@ -219,12 +233,12 @@ def attn_layer_half(x, w: dict, cos, sin, cache, indptr, indices, last_page_len,
 # one call is, by definition, T decode steps one row each; the per-row snapshots are the states after each step.
 # ---------------------------------------------------------------------------------------------
 def gdn_layer_verify(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
-                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4"):
+                     proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", v_order: str = "tiled"):
     """x bf16 [B, T, H]. Returns (out [B, T, H], state_out, conv_out, state_snaps [T, ...], conv_snaps [T, ...])."""
     outs, snaps, csnaps = [], [], []
     st, cv = state_in, conv_in
     for t in range(x.shape[1]):
-        o, st, cv = gdn_layer_decode(x[:, t], w, st, cv, num_k_heads, num_v_heads, eps, proj_fmt, mlp_fmt)
+        o, st, cv = gdn_layer_decode(x[:, t], w, st, cv, num_k_heads, num_v_heads, eps, proj_fmt, mlp_fmt, v_order)
         outs.append(o)
         snaps.append(st)
         csnaps.append(cv)
@@ -268,18 +282,19 @@ def attn_layer_verify(x, w: dict, cos, sin, cache, indptr, indices, last_page_le
 # form the reference's prefill uses (gdn_chunked, q35_prefill.py:144-169).
 # ---------------------------------------------------------------------------------------------
 def gdn_layer_prefill(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
-                      proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64):
+                      proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64, v_order: str = "tiled"):
     """gdn_layer_prefill, q35_prefill.py:57-141: x bf16 [B, T, H]. rmsnorm and the qkv / z / b / a projections over
     the B T rows (69-74), the causal conv1d + SiLU over each sequence's tokens from its conv state (75-101), the
     chunked delta rule from state_in (gdn.gdn_chunk with the reference's bf16 rounding points, none when the layer's
     points are switched off; 103-109, gdn_chunked 144-169), the gated norm (125-138), the output projection and the
     MLP (139-140). Returns (out [B, T, H], state_out, conv_out)."""
     return gdn_layer_prefill_parts(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt, mlp_fmt,
-                                   chunk)[:3]
+                                   chunk, v_order=v_order)[:3]
 
 
 def gdn_layer_prefill_parts(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
-                            proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64, flips: int = 2):
+                            proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64, flips: int = 2,
+                            v_order: str = "tiled"):
     """gdn_layer_prefill and a bound on how far `flips` one-ulp changes of each row's bf16 gated output (the input of
     the output projection, rmsnorm(core) * silu(z), whose magnitude the gate can raise well above the core's) move
     the layer output: per row, flips times the row's largest gated ulp against the largest |W_out| of each output
@@ -297,6 +312,7 @@ def gdn_layer_prefill_parts(x, w: dict, state_in, conv_in, num_k_heads: int, num
     q = mixed[..., :kd].reshape(b, t, num_k_heads, 128)
     k = mixed[..., kd:2 * kd].reshape(b, t, num_k_heads, 128)
     v = mixed[..., 2 * kd:].reshape(b, t, num_v_heads, 128)
+    q, k = value_head_keys(q, num_v_heads, v_order), value_head_keys(k, num_v_heads, v_order)
     core, state_out = gdn.gdn_chunk(q, k, v, aa.reshape(b, t, num_v_heads), bb.reshape(b, t, num_v_heads),
                                     w["a_log"], w["dt_bias"], state_in, chunk=chunk, round_bf16=rounding())
     core = _bf(core).reshape(r * num_v_heads, 128)

@@ -116,16 +116,18 @@ def test_entry_points_reach_the_launch_on_a_gpu_less_host():
                                           0.1, None, p[100], ws, None) == launch
     gws = lib.axk_gdn_layer_workspace_size(1, 256, 1, 2, 128, 256)
     args = [p[10 + i] for i in range(28)]
-    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], gws, None) == launch
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], gws, None) == launch
     # a late contract error (misaligned w_out, argument 15) is found by the validate pass before any launch
     bad = list(args)
     bad[14] += 1
-    assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], gws, None) == 3
+    assert lib.axk_gdn_layer_decode(*bad, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], gws, None) == 3
     # an unknown weight format is refused before anything else
-    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 7, 2, p[150], gws, None) == 4
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 7, 2, 1, p[150], gws, None) == 4
+    # an unknown value-head order is refused before any launch
+    assert lib.axk_gdn_layer_decode(*args, 1, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 2, p[150], gws, None) == 2
     # the prefill layer: 20 tokens of one sequence; a late misaligned w_out found before the conv / state launches
     pws = lib.axk_gdn_layer_prefill_workspace_size(1, 20, 256, 1, 2, 128, 256)
     assert 0 < pws < 65536 * 48
-    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws, None) == launch
-    assert lib.axk_gdn_layer_prefill(*bad, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws, None) == 3
-    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, p[150], pws - 1, None) == 6
+    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws, None) == launch
+    assert lib.axk_gdn_layer_prefill(*bad, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws, None) == 3
+    assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws - 1, None) == 6

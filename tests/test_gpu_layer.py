@@ -56,6 +56,53 @@ def test_gdn_layer_decode(dev, b, nk, nv):
     _check_conv(co, rc)
 
 
+@pytest.mark.parametrize("entry", ["decode", "verify", "prefill"])
+def test_gdn_layers_value_head_orders(dev, entry):
+    """Both value-head orders against the oracle (grouped: value head vh reads key head vh / (NV / NK); tiled, the
+    reference layers' default: vh % NK), and the tiled order on weights converted by tile_value_heads computes the
+    grouped layer: the state and conv state bit-identical up to the value-head permutation (each head's arithmetic
+    is the same), the output within the per-op bar (the output projection sums the heads in another order)."""
+    nk, nv, b, t = 2, 6, 3, {"decode": 1, "verify": 3, "prefill": 70}[entry]
+    g = torch.Generator().manual_seed(606 + t)
+    w = configs.gdn_layer_weights(g, H, F, nk, nv)
+    x = torch.randn(b, t, H, generator=g).bfloat16()
+    st = torch.randn(b, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(b, 3, (2 * nk + nv) * 128, generator=g).bfloat16()
+    kd = 2 * nk * 128
+    wt = layer.tile_value_heads(w, nk, nv)
+    stt = layer.v_tiled(st, 1, nk, nv, 1)
+    cvt = torch.cat((cv[..., :kd], layer.v_tiled(cv[..., kd:], 2, nk, nv, 128)), -1)
+    print(f"gdn v_order {entry} t={t}", flush=True)
+
+    def run(weights, s0, c0, order):
+        wd = _dev(weights, dev)
+        if entry == "decode":
+            o, so, co = layer.gdn_layer_decode(x[:, 0].contiguous().to(dev), wd, s0.to(dev), c0.to(dev), nk, nv,
+                                               v_order=order)
+            return o[:, None], so, co
+        fn = layer.gdn_layer_verify if entry == "verify" else layer.gdn_layer_prefill
+        return fn(x.to(dev), wd, s0.to(dev), c0.to(dev), nk, nv, v_order=order)
+
+    def oracle(order):
+        if entry == "prefill":
+            return olayer.gdn_layer_prefill(x, w, st, cv, nk, nv, v_order=order)
+        r = olayer.gdn_layer_verify(x, w, st, cv, nk, nv, v_order=order)
+        return r[0], r[1], r[2]
+
+    res = {}
+    for order in ("grouped", "tiled"):
+        out, so, co = res[order] = run(w, st, cv, order)
+        ro, rs, rc = oracle(order)
+        torch.testing.assert_close(out.float().cpu(), ro.float(), **FUSED_TOL)
+        torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
+    assert not torch.allclose(res["grouped"][1], res["tiled"][1])  # the orders pair other heads
+    out_t, so_t, co_t = run(wt, stt, cvt, "tiled")
+    out_g, so_g, co_g = res["grouped"]
+    assert torch.equal(so_t, layer.v_tiled(so_g, 1, nk, nv, 1))
+    assert torch.equal(co_t, torch.cat((co_g[..., :kd], layer.v_tiled(co_g[..., kd:], 2, nk, nv, 128)), -1))
+    torch.testing.assert_close(out_t.float(), out_g.float(), **TOL)
+
+
 def test_gdn_layer_two_steps_in_place(dev):
     w, x, st, cv = _gdn_case(11)
     x2 = torch.randn(3, H, generator=torch.Generator().manual_seed(12)).bfloat16()

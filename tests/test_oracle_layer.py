@@ -163,15 +163,16 @@ def _hf_layer(kind, w, hidden, inter, **kw):
     return m, cfg
 
 
-def _gdn_decode_tokens(x, w, nk, nv, conv_k=4):
-    """The oracle's decode layer applied token by token from zero GDN and conv states."""
+def _gdn_decode_tokens(x, w, nk, nv, conv_k=4, v_order="grouped"):
+    """The oracle's decode layer applied token by token from zero GDN and conv states (in the checkpoint's value-head
+    order by default, the order transformers' layer reads its weights in)."""
     b, t, _ = x.shape
     c = (2 * nk + nv) * 128
     st = torch.zeros(b, nv, 128, 128)
     cv = torch.zeros(b, conv_k - 1, c, dtype=x.dtype)
     outs = []
     for i in range(t):
-        o, st, cv = layer.gdn_layer_decode(x[:, i], w, st, cv, nk, nv)
+        o, st, cv = layer.gdn_layer_decode(x[:, i], w, st, cv, nk, nv, v_order=v_order)
         outs.append(o.float())
     return torch.stack(outs, 1), st
 
@@ -204,6 +205,10 @@ def test_gdn_layer_decode_matches_transformers_decoder_layer(b, t, nk, nv):
         with rounding.fp32():
             bad, _ = _gdn_decode_tokens(x, bad_w, nk, nv)
         assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3), name
+    if nv > 1 and nk > 1:  # the tiled pairing on checkpoint-order weights
+        with rounding.fp32():
+            bad, _ = _gdn_decode_tokens(x, w, nk, nv, v_order="tiled")
+        assert not torch.allclose(bad, ref, rtol=1e-3, atol=1e-3), "v_order"
 
 
 def _attn_decode_tokens(x, w, hq, hkv, d, rot, theta, page, g):
@@ -318,6 +323,56 @@ def test_gdn_prefill_oracle_equals_decode_steps(t, chunk):
     bo, bs, _ = layer.gdn_layer_prefill(x, w, st, cv, 1, 2, chunk=chunk)
     torch.testing.assert_close(bo.float(), ro.float(), rtol=5e-2, atol=0.0625)
     torch.testing.assert_close(bs, rs, rtol=5e-2, atol=3e-3)
+
+
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp8", "mxfp4"])
+def test_tiled_value_heads_on_tiled_weights_equal_the_grouped_layer(fmt):
+    """The tiled value-head order (q35_step.py:82-85, the reference's layer default) on weights converted as its
+    loader converts them (axk.layer.tile_value_heads, q35_step.py v_tiled 351-358) computes the grouped layer on the
+    checkpoint's weights: the same outputs (the output projection sums the value heads in another order) and the
+    same states with their value heads permuted; decode and chunked prefill."""
+    from axk import configs
+    from axk.layer import tile_value_heads, v_tiled
+
+    nk, nv, h = 2, 6, 128
+    g = torch.Generator().manual_seed(31)
+    w = configs.gdn_layer_weights(g, h, 128, nk, nv, proj_fmt=fmt)
+    wt = tile_value_heads(w, nk, nv, fmt)
+    x = torch.randn(2, 5, h, generator=g).bfloat16()
+    st = torch.randn(2, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(2, 3, (2 * nk + nv) * 128, generator=g).bfloat16()
+    kd = 2 * nk * 128
+    cvt = torch.cat((cv[..., :kd], v_tiled(cv[..., kd:], 2, nk, nv, 128)), -1)
+    stt = v_tiled(st, 1, nk, nv, 1)
+    with rounding.fp32():
+        o_g, s_g, c_g = layer.gdn_layer_decode(x[:, 0], w, st, cv, nk, nv, proj_fmt=fmt, v_order="grouped")
+        o_t, s_t, c_t = layer.gdn_layer_decode(x[:, 0], wt, stt, cvt, nk, nv, proj_fmt=fmt, v_order="tiled")
+        p_g, ps_g, _ = layer.gdn_layer_prefill(x, w, st, cv, nk, nv, proj_fmt=fmt, chunk=2, v_order="grouped")
+        p_t, ps_t, _ = layer.gdn_layer_prefill(x, wt, stt, cvt, nk, nv, proj_fmt=fmt, chunk=2, v_order="tiled")
+    torch.testing.assert_close(o_t, o_g, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(s_t, v_tiled(s_g, 1, nk, nv, 1), rtol=1e-6, atol=1e-7)
+    torch.testing.assert_close(c_t, torch.cat((c_g[..., :kd], v_tiled(c_g[..., kd:], 2, nk, nv, 128)), -1),
+                               rtol=1e-6, atol=1e-7)
+    torch.testing.assert_close(p_t, p_g, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ps_t, v_tiled(ps_g, 1, nk, nv, 1), rtol=1e-6, atol=1e-7)
+    # and the orders differ: the tiled pairing on the checkpoint's weights is another layer
+    with rounding.fp32():
+        o_x, _, _ = layer.gdn_layer_decode(x[:, 0], w, st, cv, nk, nv, proj_fmt=fmt, v_order="tiled")
+    assert not torch.allclose(o_x, o_g, rtol=1e-3, atol=1e-3)
+
+
+def test_v_tiled_is_the_reference_permutation():
+    """v_tiled: value head (vo, kh) of the result is head (kh, vo) of the input, i.e. tiled head vh = vo * NK + kh
+    holds grouped head kh * (NV / NK) + vo (q35_step.py:171); identity for NV == NK."""
+    from axk.layer import v_tiled
+
+    nk, nv = 3, 12
+    t = torch.arange(nv * 2).reshape(nv * 2, 1)
+    r = v_tiled(t, 0, nk, nv, 2).reshape(nv, 2)
+    for vh in range(nv):
+        vo, kh = divmod(vh, nk)
+        assert r[vh, 0] == 2 * (kh * (nv // nk) + vo)
+    assert torch.equal(v_tiled(t[:6], 0, 3, 3, 2), t[:6])
 
 
 # ---- the MoE block of the MoE decode layers (moe_full, q35_layer_mc.py:797-853) ----
