@@ -144,7 +144,87 @@ __global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const uint16_t* __rest
   }
 }
 
-// One thread per (sequence, channel): the window slides over the tokens; history in registers.
+// Thread = (sequence b, 8 channels, a tile of kConvTile tokens): the K - 1 inputs before the tile (conv-state rows or
+// x rows) and the tile's rows loaded into registers up front, then the tile's tokens in order; 16-byte loads and
+// stores along the channels. The conv state after the last token (the last K - 1 rows of [state_in | x]) is written
+// by one thread per (sequence, channels): with one tile, from its registers at the end; with more (then T > K - 1
+// and those rows are all x rows), by the tile-0 thread, the only one that reads state_in, after its own reads, so
+// an in-place state is read before it is overwritten.
+constexpr int kConvTile = 8;
+template <int K>
+__global__ __launch_bounds__(256) void conv1d_silu_tiled_kernel(const uint16_t* __restrict__ x,
+                                                                const uint16_t* __restrict__ w,
+                                                                const uint16_t* state_in, uint16_t* state_out,
+                                                                uint16_t* __restrict__ out, int B, int T, int C) {
+  const int c8 = C / 8, tiles = (T + kConvTile - 1) / kConvTile;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)B * tiles * c8) return;
+  const int cg = (int)(i % c8);
+  const int64_t rest = i / c8;
+  const int tile = (int)(rest % tiles), b = (int)(rest / tiles);
+  const int c0 = 8 * cg, t0 = tile * kConvTile, t1 = min(T, t0 + kConvTile);
+  float wk[8][kMaxConvKernel], hist[8][kMaxConvKernel];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+#pragma unroll
+    for (int j = 0; j < kMaxConvKernel; ++j) {
+      wk[q][j] = j < K ? bf16_bits_to_f32(w[(int64_t)(c0 + q) * K + j]) : 0.f;
+      hist[q][j] = 0.f;
+    }
+#pragma unroll
+  for (int j = 0; j < kMaxConvKernel; ++j) {  // input rows t0 - (K - 1) .. t0 - 1, oldest first
+    if (j < K - 1) {
+      const int r = t0 - (K - 1) + j;
+      const uint16_t* src = r < 0 ? state_in + ((int64_t)b * (K - 1) + (K - 1) + r) * C
+                                  : x + ((int64_t)b * T + r) * C;
+      float f[8];
+      unpack8(*reinterpret_cast<const uint4*>(src + c0), f);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) hist[q][j] = f[q];
+    }
+  }
+  uint4 rows[kConvTile];  // the tile's input rows, all loads in flight together
+#pragma unroll
+  for (int u = 0; u < kConvTile; ++u)
+    if (t0 + u < t1) rows[u] = *reinterpret_cast<const uint4*>(x + ((int64_t)b * T + t0 + u) * C + c0);
+#pragma unroll
+  for (int u = 0; u < kConvTile; ++u) {
+    if (t0 + u < t1) {
+      const int64_t o = ((int64_t)b * T + t0 + u) * C + c0;
+      float xt[8], y[8];
+      unpack8(rows[u], xt);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        // tap j multiplies x_{t-j}: j = 0 the current token, then back through the history (a bf16 rounding per tap)
+        y[q] = silu_f32(conv_taps(xt[q], wk[q], hist[q], K));
+#pragma unroll
+        for (int j = 0; j + 1 < kMaxConvKernel; ++j)
+          if (j + 1 < K - 1) hist[q][j] = hist[q][j + 1];
+        if (K > 1) hist[q][K - 2] = xt[q];
+      }
+      *reinterpret_cast<uint4*>(out + o) = pack8(y);
+    }
+  }
+  if (K > 1 && tiles == 1) {
+#pragma unroll
+    for (int j = 0; j < kMaxConvKernel; ++j)
+      if (j < K - 1) {
+        float f[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) f[q] = hist[q][j];
+        *reinterpret_cast<uint4*>(state_out + ((int64_t)b * (K - 1) + j) * C + c0) = pack8(f);
+      }
+  } else if (K > 1 && tile == 0) {
+#pragma unroll
+    for (int j = 0; j < kMaxConvKernel; ++j)
+      if (j < K - 1)
+        *reinterpret_cast<uint4*>(state_out + ((int64_t)b * (K - 1) + j) * C + c0) =
+            *reinterpret_cast<const uint4*>(x + ((int64_t)b * T + T - (K - 1) + j) * C + c0);
+  }
+}
+
+// One thread per (sequence, channel): the window slides over the tokens; history in registers (channel counts that
+// are not a multiple of 8, or rows not 16-byte aligned).
 __global__ __launch_bounds__(256) void conv1d_silu_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const uint16_t* state_in, uint16_t* state_out,
@@ -350,10 +430,28 @@ extern "C" int axk_causal_conv1d_silu(const uint16_t* x, const uint16_t* w, cons
   // in place state is allowed (each thread reads its history before writing it); the output may not overlap it
   AXK_REQUIRE(kernel == 1 || state_in == state_out || !axk_overlap(state_in, sbytes, state_out, sbytes), AXK_E_ALIAS);
   AXK_REQUIRE(kernel == 1 || !axk_overlap(out, obytes, state_out, sbytes), AXK_E_ALIAS);
-  const int64_t n = batch * channels;
   AXK_LAUNCH_GATE();
-  hipLaunchKernelGGL(conv1d_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, axk_stream(stream), x, w,
-                     state_in, state_out, out, (int)batch, (int)tokens, (int)channels, (int)kernel);
+  if (channels % 8 == 0 && aligned16(x) && aligned16(out) &&
+      (kernel == 1 || (aligned16(state_in) && aligned16(state_out)))) {
+    const int64_t n = batch * ((tokens + kConvTile - 1) / kConvTile) * (channels / 8);
+    const dim3 grid((unsigned)((n + 255) / 256));
+    const hipStream_t st = axk_stream(stream);
+    const int Bi = (int)batch, Ti = (int)tokens, Ci = (int)channels;
+    switch (kernel) {  // the tap count is a template argument: every register index is then constant
+#define AXK_CONV_CASE(KK)                                                                                          \
+  case KK:                                                                                                         \
+    hipLaunchKernelGGL(conv1d_silu_tiled_kernel<KK>, grid, dim3(256), 0, st, x, w, state_in, state_out, out, Bi, Ti, \
+                       Ci);                                                                                        \
+    break;
+      AXK_CONV_CASE(1) AXK_CONV_CASE(2) AXK_CONV_CASE(3) AXK_CONV_CASE(4)
+      AXK_CONV_CASE(5) AXK_CONV_CASE(6) AXK_CONV_CASE(7) AXK_CONV_CASE(8)
+#undef AXK_CONV_CASE
+    }
+  } else {
+    const int64_t n = batch * channels;
+    hipLaunchKernelGGL(conv1d_silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, axk_stream(stream), x,
+                       w, state_in, state_out, out, (int)batch, (int)tokens, (int)channels, (int)kernel);
+  }
   return axk_launch_status();
 }
 

@@ -61,7 +61,10 @@ def test_gated_rmsnorm_silu(dev):
     _close(glue.gated_rmsnorm_silu(x.to(dev), w.to(dev), z.to(dev)), layer.gated_rmsnorm_silu(x, w, z))
 
 
-@pytest.mark.parametrize("b,t,c,k", [(8, 1, 8192, 4), (2, 5, 200, 4), (1, 3, 64, 2), (3, 2, 16, 1)])
+# one token; a channel count that is not a multiple of 8 (the per-channel kernel); fewer tokens than K - 1; several
+# 32-token tiles with a one-token tail; eight taps; config 2b's conv width at prefill length
+@pytest.mark.parametrize("b,t,c,k", [(8, 1, 8192, 4), (2, 5, 200, 4), (1, 3, 64, 2), (3, 2, 16, 1), (2, 2, 64, 4),
+                                     (2, 33, 256, 4), (3, 100, 136, 8), (1, 4096, 8192, 4)])
 def test_causal_conv1d_silu(dev, b, t, c, k):
     g = _g(b * 10 + t)
     x = torch.randn(b, t, c, generator=g).bfloat16()
@@ -71,6 +74,20 @@ def test_causal_conv1d_silu(dev, b, t, c, k):
     ro, rs = layer.causal_conv1d_silu(x, w, st)
     _close(out, ro)
     assert torch.equal(so.cpu(), rs)
+
+
+def test_causal_conv1d_in_place_state_over_many_tiles(dev):
+    """An in-place conv state with several token tiles: the tile that reads the state is the one that rewrites it."""
+    g = _g(5)
+    x = torch.randn(2, 150, 256, generator=g).bfloat16()
+    w = (torch.randn(256, 4, generator=g) * 0.5).bfloat16()
+    st = torch.randn(2, 3, 256, generator=g).bfloat16()
+    ref_out, ref_st = layer.causal_conv1d_silu(x, w, st)
+    sd = st.to(dev)
+    o1, _ = glue.causal_conv1d_silu(x[:, :100].contiguous().to(dev), w.to(dev), sd, state_out=sd)
+    o2, _ = glue.causal_conv1d_silu(x[:, 100:].contiguous().to(dev), w.to(dev), sd, state_out=sd)
+    _close(torch.cat((o1, o2), 1), ref_out)
+    assert torch.equal(sd.cpu(), ref_st)
 
 
 def test_causal_conv1d_in_place_state_and_continuation(dev):
