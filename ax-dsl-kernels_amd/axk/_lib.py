@@ -117,6 +117,12 @@ SIGNATURES: dict[str, list] = {
                               _vp],
     "axk_attn_layer_prefill": [_vp] * 27 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
                                ctypes.c_size_t, _vp],
+    "axk_gdn_layer_prefill_moe_workspace_size": [_i64] * 7 + [_vp],
+    "axk_attn_layer_prefill_moe_workspace_size": [_i64] * 7 + [_vp],
+    "axk_gdn_layer_prefill_moe": [_vp] * 29 + [_i64] * 8 + [ctypes.c_float, _i32, _i32, _i32, _vp,
+                                  ctypes.c_size_t, _vp],
+    "axk_attn_layer_prefill_moe": [_vp] * 28 + [_i64] * 10 + [ctypes.c_float, ctypes.c_float, _i32, _i32, _vp,
+                                   ctypes.c_size_t, _vp],
 }
 _RESTYPES = {
     "axk_version": ctypes.c_char_p,
@@ -132,6 +138,8 @@ _RESTYPES = {
     "axk_attn_layer_moe_workspace_size": ctypes.c_size_t,
     "axk_gdn_layer_prefill_workspace_size": ctypes.c_size_t,
     "axk_attn_layer_prefill_workspace_size": ctypes.c_size_t,
+    "axk_gdn_layer_prefill_moe_workspace_size": ctypes.c_size_t,
+    "axk_attn_layer_prefill_moe_workspace_size": ctypes.c_size_t,
 }
 
 

@@ -92,12 +92,12 @@ def _weights(w: dict, names) -> list:
 MOE_WEIGHTS = ("w_router", "e_gw", "e_gs", "e_dw", "e_ds")
 
 
-def moe_block(moe: dict) -> _lib.MoeBlock:
+def moe_block(moe: dict, rows: Optional[int] = None) -> _lib.MoeBlock:
     """The axk_moe_block of a MoE block (moe_full, q35_layer_mc.py:797-853) given as a dict: w_router bf16 [E, H],
     w_shg bf16 [H] (optional: the shared expert's sigmoid gate), the routed experts e_gw / e_gs [E, 2 F, H/2 | H/32]
     and e_dw / e_ds [E, H, F/2 | F/32] (MXFP4, the manifest's planar layout), top_k, norm_topk_prob (default True),
-    and optional routing outputs logits f32 [B, E], topk_ids int32 [B, K], topk_weights f32 [B, K].
-    The shared expert is the layer's MLP weights (w_gate .. s_down) in mlp_fmt."""
+    and optional routing outputs logits f32 [B, E], topk_ids int32 [B, K], topk_weights f32 [B, K] (B = rows when
+    given: the layer's token rows). The shared expert is the layer's MLP weights (w_gate .. s_down) in mlp_fmt."""
     _weights(moe, MOE_WEIGHTS)
     shg = moe.get("w_shg")
     _check(shg is None or shg.is_contiguous(), "w_shg must be contiguous")
@@ -111,8 +111,9 @@ def moe_block(moe: dict) -> _lib.MoeBlock:
     for n, dt, cols in (("logits", torch.float32, e), ("topk_ids", torch.int32, m.top_k),
                         ("topk_weights", torch.float32, m.top_k)):
         t = moe.get(n)
-        _check(t is None or (t.dtype == dt and t.dim() == 2 and t.shape[1] == cols and t.is_contiguous()),
-               f"{n} must be contiguous {dt} [B, {cols}]")
+        _check(t is None or (t.dtype == dt and t.dim() == 2 and t.shape[1] == cols and t.is_contiguous() and
+                             (rows is None or t.shape[0] == rows)),
+               f"{n} must be contiguous {dt} [{'B' if rows is None else rows}, {cols}]")
         setattr(m, n, _lib.ptr(t))
     return m
 
@@ -187,7 +188,7 @@ def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     if moe is None:
         _lib.call("axk_gdn_layer_decode", x.data_ptr(), *ptrs, *tail)
     else:
-        m = moe_block(moe)
+        m = moe_block(moe, b)
         _lib.call("axk_gdn_layer_decode_moe", x.data_ptr(), *ptrs, ctypes.addressof(m), *tail)
     return o, so, co
 
@@ -223,7 +224,7 @@ def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
     if moe is None:
         _lib.call("axk_attn_layer_decode", *head, *tail)
     else:
-        m = moe_block(moe)
+        m = moe_block(moe, b)
         _lib.call("axk_attn_layer_decode_moe", *head, ctypes.addressof(m), *tail)
     return o
 
@@ -312,17 +313,30 @@ def attn_layer_verify(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
 # ---- prefill: T new tokens per sequence through one layer call (models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:
 # gdn_layer_prefill 57-141, attn_layer_prefill 172-336) ----
 def gdn_prefill_workspace(batch: int, tokens: int, hidden: int, num_k_heads: int, num_v_heads: int, inter: int,
-                          device, head_dim: int = 128) -> torch.Tensor:
-    n = _lib.load().axk_gdn_layer_prefill_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim,
-                                                         inter)
+                          device, head_dim: int = 128, moe: Optional[dict] = None) -> torch.Tensor:
+    """The workspace of gdn_layer_prefill (with moe: of its MoE form)."""
+    lib = _lib.load()
+    if moe is None:
+        n = lib.axk_gdn_layer_prefill_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim, inter)
+    else:
+        m = moe_block(moe)
+        n = lib.axk_gdn_layer_prefill_moe_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim,
+                                                         inter, ctypes.addressof(m))
     _check(n > 0, "unsupported GDN prefill shape")
     return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def attn_prefill_workspace(batch: int, tokens: int, hidden: int, num_qo_heads: int, num_kv_heads: int,
-                           head_dim: int, inter: int, device) -> torch.Tensor:
-    n = _lib.load().axk_attn_layer_prefill_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
-                                                          head_dim, inter)
+                           head_dim: int, inter: int, device, moe: Optional[dict] = None) -> torch.Tensor:
+    """The workspace of attn_layer_prefill (with moe: of its MoE form)."""
+    lib = _lib.load()
+    if moe is None:
+        n = lib.axk_attn_layer_prefill_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim,
+                                                      inter)
+    else:
+        m = moe_block(moe)
+        n = lib.axk_attn_layer_prefill_moe_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                                                          head_dim, inter, ctypes.addressof(m))
     _check(n > 0, "unsupported attention prefill shape")
     return torch.empty(n, dtype=torch.uint8, device=device)
 
@@ -331,24 +345,31 @@ def gdn_layer_prefill(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in:
                       num_v_heads: int, eps: float = 1e-6, workspace: Optional[torch.Tensor] = None,
                       out: Optional[torch.Tensor] = None, state_out: Optional[torch.Tensor] = None,
                       conv_out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
-                      v_order: str = "tiled"):
+                      v_order: str = "tiled", moe: Optional[dict] = None):
     """x bf16 [B, T, hidden]: T new tokens per sequence. state f32 [B, NV, 128, 128]; conv state bf16
-    [B, K-1, 2 KD + VD]. Returns (out [B, T, hidden], state_out, conv_out) after the last token."""
+    [B, K-1, 2 KD + VD]. Returns (out [B, T, hidden], state_out, conv_out) after the last token. moe (optional, see
+    moe_block; routing outputs [B T, ...]): the MLP is the MoE block (qwen35moe_gdn_prefill,
+    q35_moe_prefill.py:47-52)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
     b, t, h = x.shape
     inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
     ws = workspace if workspace is not None else gdn_prefill_workspace(b, t, h, num_k_heads, num_v_heads, inter,
-                                                                       x.device)
+                                                                       x.device, moe=moe)
     o = torch.empty_like(x) if out is None else out
     so = torch.empty_like(state_in) if state_out is None else state_out
     co = torch.empty_like(conv_in) if conv_out is None else conv_out
     args = _weights(w, GDN_WEIGHTS) + _weights(w, MLP_WEIGHTS)
-    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args)
+    _lib.require_device(x, ws, o, so, co, state_in, conv_in, *args, *_moe_tensors(moe))
     ptrs = [t_.data_ptr() for t_ in args]
-    _lib.call("axk_gdn_layer_prefill", x.data_ptr(), *ptrs, state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(),
-              so.data_ptr(), co.data_ptr(), b, t, h, num_k_heads, num_v_heads, 128, kconv, inter, eps,
-              _fmt(proj_fmt), _fmt(mlp_fmt), _vorder(v_order), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    tail = (state_in.data_ptr(), conv_in.data_ptr(), o.data_ptr(), so.data_ptr(), co.data_ptr(), b, t, h,
+            num_k_heads, num_v_heads, 128, kconv, inter, eps, _fmt(proj_fmt), _fmt(mlp_fmt), _vorder(v_order),
+            ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    if moe is None:
+        _lib.call("axk_gdn_layer_prefill", x.data_ptr(), *ptrs, *tail)
+    else:
+        m = moe_block(moe, b * t)
+        _lib.call("axk_gdn_layer_prefill_moe", x.data_ptr(), *ptrs, ctypes.addressof(m), *tail)
     return o, so, co
 
 
@@ -356,11 +377,12 @@ def attn_layer_prefill(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.T
                        indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
                        cache_location: torch.Tensor, num_qo_heads: int, rot: int, eps: float = 1e-6,
                        sm_scale: Optional[float] = None, workspace: Optional[torch.Tensor] = None,
-                       out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8",
-                       mlp_fmt: str = "mxfp4") -> torch.Tensor:
+                       out: Optional[torch.Tensor] = None, proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4",
+                       moe: Optional[dict] = None) -> torch.Tensor:
     """x bf16 [B, T, hidden]; the page table covers each sequence's history and its T new tokens; cache_location
     int32 [B, T, 2] (page, slot) of each new token; cos, sin bf16 [B, T, rot / 2]. kv_cache bf16
-    [P, 2, page, HKV, D] is written in place. Returns out bf16 [B, T, hidden]."""
+    [P, 2, page, HKV, D] is written in place. Returns out bf16 [B, T, hidden]. moe (optional): the MLP is the MoE
+    block (qwen35moe_attn_prefill, q35_moe_prefill.py:55-60)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
     b, t, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
@@ -368,17 +390,23 @@ def attn_layer_prefill(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.T
     _check(cache_location.dtype == torch.int32 and cache_location.numel() == 2 * b * t and
            cache_location.is_contiguous(), "cache_location must be contiguous int32 [B, T, 2]")
     ws = workspace if workspace is not None else attn_prefill_workspace(b, t, h, num_qo_heads, hkv, d, inter,
-                                                                        x.device)
+                                                                        x.device, moe=moe)
     o = torch.empty_like(x) if out is None else out
     scale = d ** -0.5 if sm_scale is None else sm_scale
     wa = _weights(w, ATTN_WEIGHTS)
     mlp = _weights(w, MLP_WEIGHTS)
-    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp)
+    _lib.require_device(x, ws, o, kv_cache, indptr, indices, last_page_len, cache_location, cos, sin, *wa, *mlp,
+                        *_moe_tensors(moe))
     (ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, w_o, s_o, ln2) = wa
-    _lib.call("axk_attn_layer_prefill", x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(),
-              w_k.data_ptr(), s_k.data_ptr(), w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(),
-              _lib.ptr(cos), _lib.ptr(sin), kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(),
-              last_page_len.data_ptr(), cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(),
-              *[t_.data_ptr() for t_ in mlp], o.data_ptr(), b, t, h, num_qo_heads, hkv, d, rot, page, pages, inter,
-              eps, scale, _fmt(proj_fmt), _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    head = (x.data_ptr(), ln1.data_ptr(), w_q.data_ptr(), s_q.data_ptr(), w_k.data_ptr(), s_k.data_ptr(),
+            w_v.data_ptr(), s_v.data_ptr(), q_norm.data_ptr(), k_norm.data_ptr(), _lib.ptr(cos), _lib.ptr(sin),
+            kv_cache.data_ptr(), indptr.data_ptr(), indices.data_ptr(), last_page_len.data_ptr(),
+            cache_location.data_ptr(), w_o.data_ptr(), s_o.data_ptr(), ln2.data_ptr(), *[t_.data_ptr() for t_ in mlp])
+    tail = (o.data_ptr(), b, t, h, num_qo_heads, hkv, d, rot, page, pages, inter, eps, scale, _fmt(proj_fmt),
+            _fmt(mlp_fmt), ws.data_ptr(), ws.numel(), _lib.stream_of(x))
+    if moe is None:
+        _lib.call("axk_attn_layer_prefill", *head, *tail)
+    else:
+        m = moe_block(moe, b * t)
+        _lib.call("axk_attn_layer_prefill_moe", *head, ctypes.addressof(m), *tail)
     return o

@@ -464,10 +464,13 @@ int check_prefill(int64_t B, int64_t T, int64_t H, int64_t F) {
   return AXK_OK;
 }
 
-size_t attn_rows_ws(int64_t B, int64_t T, int64_t H, int64_t HQ, int64_t HKV, int64_t D, int64_t F) {
+size_t attn_rows_ws(int64_t B, int64_t T, int64_t H, int64_t HQ, int64_t HKV, int64_t D, int64_t F,
+                    const axk_moe_block* moe = nullptr) {
   if (HQ <= 0 || HKV <= 0 || HQ % HKV != 0 || !(D == 64 || D == 128 || D == 256)) return 0;
+  if (moe && moe_ws_bytes(B * T, H, *moe) == 0) return 0;
   Carver c{nullptr};
   carve_attn_verify(c, B, B * T, H, HQ, HKV, D, F);
+  if (moe) carve_moe(c, B * T, H, *moe);
   return c.off;
 }
 
@@ -480,10 +483,10 @@ int attn_rows_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, cons
                    const int32_t* indices, const int32_t* last_page_len, const int32_t* cache_location,
                    const uint8_t* w_o, const void* s_o, const float* ln2, const uint8_t* mlp_gate_w,
                    const void* mlp_gate_s, const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
-                   const void* mlp_down_s, uint16_t* out, int64_t batch, int64_t tokens, int64_t hidden,
-                   int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot, int64_t page_size,
-                   int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt, int mlp_fmt,
-                   void* workspace, size_t workspace_bytes, axk_stream_t stream, size_t need) {
+                   const void* mlp_down_s, const axk_moe_block* moe, uint16_t* out, int64_t batch, int64_t tokens,
+                   int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t rot,
+                   int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale, int proj_fmt,
+                   int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream, size_t need) {
   AXK_REQUIRE(x && ln1 && w_q && s_q && w_k && s_k && w_v && s_v && q_norm && k_norm && kv_cache && indptr &&
                   indices && last_page_len && cache_location && w_o && s_o && ln2 && mlp_gate_w && mlp_gate_s &&
                   mlp_up_w && mlp_up_s && mlp_down_w && mlp_down_s && out && (rot == 0 || (cos && sin)),
@@ -495,6 +498,7 @@ int attn_rows_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, cons
                 F = inter;
   Carver c{static_cast<unsigned char*>(workspace)};
   const AttnVerifyBufs a = carve_attn_verify(c, B, R, H, HQ, HKV, D, F);
+  const MoeBufs eb = moe ? carve_moe(c, R, H, *moe) : MoeBufs{};
   const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, a.h, H, R, H, eps, stream));
@@ -509,6 +513,7 @@ int attn_rows_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, cons
     AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, R * HQ, D, stream));
     const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
     AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, R, HQ * D, stream));
+    if (moe) return moe_residual(x, a.y, ln2, mw, mlp_fmt, *moe, out, a.mlp, eb, R, H, F, eps, stream);
     return mlp_residual(x, a.y, ln2, mw, mlp_fmt, out, a.mlp, R, H, F, eps, stream);
   };
   {
@@ -606,7 +611,7 @@ extern "C" int axk_attn_layer_verify(
                                                            head_dim, inter);
   return attn_rows_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
                         last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
-                        mlp_down_w, mlp_down_s, out, batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
+                        mlp_down_w, mlp_down_s, nullptr, out, batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
                         page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace, workspace_bytes,
                         stream, need);
 }
@@ -645,43 +650,44 @@ GdnPrefillBufs carve_gdn_prefill(Carver& c, int64_t B, int64_t T, int64_t H, int
   return g;
 }
 
-}  // namespace
-
-extern "C" size_t axk_gdn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
-                                                       int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
-                                                       int64_t inter) {
+size_t gdn_prefill_ws(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads,
+                      int64_t head_dim, int64_t inter, const axk_moe_block* moe) {
   if (check_prefill(batch, tokens, hidden, inter) != AXK_OK || head_dim != 128 || num_k_heads <= 0 ||
       num_v_heads <= 0 || num_v_heads % num_k_heads != 0 ||
       axk_gdn_chunk_workspace_size(batch, tokens, num_k_heads, num_v_heads, 128, 128, 64) == 0)
     return 0;
+  if (moe && moe_ws_bytes(batch * tokens, hidden, *moe) == 0) return 0;
   Carver c{nullptr};
   carve_gdn_prefill(c, batch, tokens, hidden, num_k_heads, num_v_heads, inter);
+  if (moe) carve_moe(c, batch * tokens, hidden, *moe);
   return c.off;
 }
 
-extern "C" int axk_gdn_layer_prefill(
-    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
-    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
-    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
-    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
-    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
-    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t tokens,
-    int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
-    float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
-    axk_stream_t stream) {
+int gdn_prefill_impl(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z,
+                     const void* s_z, const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a,
+                     const uint16_t* conv_w, const float* a_log, const float* dt_bias, const float* norm_w,
+                     const uint8_t* w_out, const void* s_out, const float* ln2, const uint8_t* mlp_gate_w,
+                     const void* mlp_gate_s, const uint8_t* mlp_up_w, const void* mlp_up_s,
+                     const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
+                     const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out,
+                     uint16_t* conv_out, int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                     int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+                     int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+                     axk_stream_t stream) {
   AXK_REQUIRE(x && ln1 && w_qkv && s_qkv && w_z && s_z && w_b && s_b && w_a && s_a && conv_w && a_log && dt_bias &&
                   norm_w && w_out && s_out && ln2 && mlp_gate_w && mlp_gate_s && mlp_up_w && mlp_up_s &&
                   mlp_down_w && mlp_down_s && state_in && conv_in && out && state_out && conv_out,
               AXK_E_NULL);
   AXK_REQUIRE(mx_fmt_of(proj_fmt) >= 0 && mx_fmt_of(mlp_fmt) >= 0, AXK_E_DTYPE);
-  const size_t need = axk_gdn_layer_prefill_workspace_size(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim,
-                                                           inter);
+  const size_t need =
+      gdn_prefill_ws(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim, inter, moe);
   AXK_REQUIRE(need > 0, AXK_E_SHAPE);
   AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
   const int64_t B = batch, T = tokens, R = B * T, H = hidden, NK = num_k_heads, NV = num_v_heads, F = inter;
   const int64_t KD = NK * 128, VD = NV * 128, C = 2 * KD + VD;
   Carver c{static_cast<unsigned char*>(workspace)};
   const GdnPrefillBufs g = carve_gdn_prefill(c, B, T, H, NK, NV, F);
+  const MoeBufs eb = moe ? carve_moe(c, R, H, *moe) : MoeBufs{};
   const MlpWeights mw{mlp_gate_w, mlp_up_w, mlp_down_w, mlp_gate_s, mlp_up_s, mlp_down_s};
   auto body = [&]() -> int {
     AXK_TRY(axk_rmsnorm(x, H, ln1, g.h, H, R, H, eps, stream));
@@ -697,6 +703,7 @@ extern "C" int axk_gdn_layer_prefill(
     AXK_TRY(axk_gated_rmsnorm_silu(g.core, norm_w, g.z, g.gated, R * NV, 128, eps, stream));
     const AxkMxMat o = proj_mat(proj_fmt, w_out, s_out, g.y, H);
     AXK_TRY(projs(proj_fmt, g.gated, VD, &o, 1, R, VD, stream));
+    if (moe) return moe_residual(x, g.y, ln2, mw, mlp_fmt, *moe, out, g.mlp, eb, R, H, F, eps, stream);
     return mlp_residual(x, g.y, ln2, mw, mlp_fmt, out, g.mlp, R, H, F, eps, stream);
   };
   {
@@ -706,11 +713,69 @@ extern "C" int axk_gdn_layer_prefill(
   return body();
 }
 
+}  // namespace
+
+extern "C" size_t axk_gdn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
+                                                       int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
+                                                       int64_t inter) {
+  return gdn_prefill_ws(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim, inter, nullptr);
+}
+
+extern "C" size_t axk_gdn_layer_prefill_moe_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
+                                                           int64_t num_k_heads, int64_t num_v_heads,
+                                                           int64_t head_dim, int64_t inter,
+                                                           const axk_moe_block* moe) {
+  return moe ? gdn_prefill_ws(batch, tokens, hidden, num_k_heads, num_v_heads, head_dim, inter, moe) : 0;
+}
+
+extern "C" int axk_gdn_layer_prefill(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const float* state_in,
+    const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out, int64_t batch, int64_t tokens,
+    int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter,
+    float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+    axk_stream_t stream) {
+  return gdn_prefill_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
+                          s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, nullptr,
+                          state_in, conv_in, out, state_out, conv_out, batch, tokens, hidden, num_k_heads,
+                          num_v_heads, head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, v_order, workspace,
+                          workspace_bytes, stream);
+}
+
+extern "C" int axk_gdn_layer_prefill_moe(
+    const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv, const uint8_t* w_z, const void* s_z,
+    const uint8_t* w_b, const void* s_b, const uint8_t* w_a, const void* s_a, const uint16_t* conv_w,
+    const float* a_log, const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
+    const float* state_in, const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
+    int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads, int64_t num_v_heads, int64_t head_dim,
+    int64_t conv_kernel, int64_t inter, float eps, int proj_fmt, int mlp_fmt, int v_order, void* workspace,
+    size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(moe, AXK_E_NULL);
+  return gdn_prefill_impl(x, ln1, w_qkv, s_qkv, w_z, s_z, w_b, s_b, w_a, s_a, conv_w, a_log, dt_bias, norm_w, w_out,
+                          s_out, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s, mlp_down_w, mlp_down_s, moe,
+                          state_in, conv_in, out, state_out, conv_out, batch, tokens, hidden, num_k_heads,
+                          num_v_heads, head_dim, conv_kernel, inter, eps, proj_fmt, mlp_fmt, v_order, workspace,
+                          workspace_bytes, stream);
+}
+
 extern "C" size_t axk_attn_layer_prefill_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
                                                         int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
                                                         int64_t inter) {
   if (check_prefill(batch, tokens, hidden, inter) != AXK_OK) return 0;
   return attn_rows_ws(batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, inter);
+}
+
+extern "C" size_t axk_attn_layer_prefill_moe_workspace_size(int64_t batch, int64_t tokens, int64_t hidden,
+                                                            int64_t num_qo_heads, int64_t num_kv_heads,
+                                                            int64_t head_dim, int64_t inter,
+                                                            const axk_moe_block* moe) {
+  if (!moe || check_prefill(batch, tokens, hidden, inter) != AXK_OK) return 0;
+  return attn_rows_ws(batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, inter, moe);
 }
 
 extern "C" int axk_attn_layer_prefill(
@@ -727,7 +792,27 @@ extern "C" int axk_attn_layer_prefill(
                                                             head_dim, inter);
   return attn_rows_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
                         last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
-                        mlp_down_w, mlp_down_s, out, batch, tokens, hidden, num_qo_heads, num_kv_heads, head_dim, rot,
-                        page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace, workspace_bytes,
-                        stream, need);
+                        mlp_down_w, mlp_down_s, nullptr, out, batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                        head_dim, rot, page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace,
+                        workspace_bytes, stream, need);
+}
+
+extern "C" int axk_attn_layer_prefill_moe(
+    const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q, const uint8_t* w_k, const void* s_k,
+    const uint8_t* w_v, const void* s_v, const float* q_norm, const float* k_norm, const uint16_t* cos,
+    const uint16_t* sin, uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+    const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o, const void* s_o,
+    const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s, const uint8_t* mlp_up_w,
+    const void* mlp_up_s, const uint8_t* mlp_down_w, const void* mlp_down_s, const axk_moe_block* moe,
+    uint16_t* out, int64_t batch, int64_t tokens, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
+    int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(moe, AXK_E_NULL);
+  const size_t need = axk_attn_layer_prefill_moe_workspace_size(batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                                                                head_dim, inter, moe);
+  return attn_rows_impl(x, ln1, w_q, s_q, w_k, s_k, w_v, s_v, q_norm, k_norm, cos, sin, kv_cache, indptr, indices,
+                        last_page_len, cache_location, w_o, s_o, ln2, mlp_gate_w, mlp_gate_s, mlp_up_w, mlp_up_s,
+                        mlp_down_w, mlp_down_s, moe, out, batch, tokens, hidden, num_qo_heads, num_kv_heads,
+                        head_dim, rot, page_size, num_pages, inter, eps, sm_scale, proj_fmt, mlp_fmt, workspace,
+                        workspace_bytes, stream, need);
 }

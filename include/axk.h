@@ -667,6 +667,43 @@ int axk_attn_layer_prefill(const uint16_t* x, const float* ln1, const uint8_t* w
                            int64_t page_size, int64_t num_pages, int64_t inter, float eps, float sm_scale,
                            int proj_fmt, int mlp_fmt, void* workspace, size_t workspace_bytes, axk_stream_t stream);
 
+/* The 35B's MoE prefill layers (models/qwen35_35b_a3b/src/70b0fbc/q35_moe_prefill.py: qwen35moe_gdn_prefill /
+ * qwen35moe_attn_prefill 47-77, the layer up to its MLP then moe_pre on the P rows, q35_moe.py:123-137; the routed
+ * experts of the P tokens grouped by expert and combined, moe_slots_px / moe_combine 150-214): the prefill layers
+ * with the MoE block of axk_gdn_layer_decode_moe as their MLP, over the batch * tokens rows (more than 256 rows take
+ * the grouped prefill expert GEMMs, whose per-(token, slot) outputs are bf16 as the reference's slot kernels store
+ * them). moe's optional routing outputs are [batch * tokens, ...]. Arguments otherwise as the prefill layers. */
+size_t axk_gdn_layer_prefill_moe_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                                                int64_t num_v_heads, int64_t head_dim, int64_t inter,
+                                                const axk_moe_block* moe);
+size_t axk_attn_layer_prefill_moe_workspace_size(int64_t batch, int64_t tokens, int64_t hidden, int64_t num_qo_heads,
+                                                 int64_t num_kv_heads, int64_t head_dim, int64_t inter,
+                                                 const axk_moe_block* moe);
+int axk_gdn_layer_prefill_moe(const uint16_t* x, const float* ln1, const uint8_t* w_qkv, const void* s_qkv,
+                              const uint8_t* w_z, const void* s_z, const uint8_t* w_b, const void* s_b,
+                              const uint8_t* w_a, const void* s_a, const uint16_t* conv_w, const float* a_log,
+                              const float* dt_bias, const float* norm_w, const uint8_t* w_out, const void* s_out,
+                              const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                              const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                              const void* mlp_down_s, const axk_moe_block* moe, const float* state_in,
+                              const uint16_t* conv_in, uint16_t* out, float* state_out, uint16_t* conv_out,
+                              int64_t batch, int64_t tokens, int64_t hidden, int64_t num_k_heads,
+                              int64_t num_v_heads, int64_t head_dim, int64_t conv_kernel, int64_t inter, float eps,
+                              int proj_fmt, int mlp_fmt, int v_order, void* workspace, size_t workspace_bytes,
+                              axk_stream_t stream);
+int axk_attn_layer_prefill_moe(const uint16_t* x, const float* ln1, const uint8_t* w_q, const void* s_q,
+                               const uint8_t* w_k, const void* s_k, const uint8_t* w_v, const void* s_v,
+                               const float* q_norm, const float* k_norm, const uint16_t* cos, const uint16_t* sin,
+                               uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                               const int32_t* last_page_len, const int32_t* cache_location, const uint8_t* w_o,
+                               const void* s_o, const float* ln2, const uint8_t* mlp_gate_w, const void* mlp_gate_s,
+                               const uint8_t* mlp_up_w, const void* mlp_up_s, const uint8_t* mlp_down_w,
+                               const void* mlp_down_s, const axk_moe_block* moe, uint16_t* out, int64_t batch,
+                               int64_t tokens, int64_t hidden, int64_t num_qo_heads, int64_t num_kv_heads,
+                               int64_t head_dim, int64_t rot, int64_t page_size, int64_t num_pages, int64_t inter,
+                               float eps, float sm_scale, int proj_fmt, int mlp_fmt, void* workspace,
+                               size_t workspace_bytes, axk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -130,13 +130,14 @@ def dequant_weight(w: dict, name: str, fmt: str) -> torch.Tensor:
 
 
 def moe_block_parts(x, y, w: dict, moe: dict, eps: float = 1e-6, fmt: str = "mxfp8", ids=None, wts=None,
-                    flips: int = 2):
+                    flips: int = 2, slot_bf16: bool = False):
     """moe_full (models/qwen35_35b_a3b/src/70b0fbc/q35_layer_mc.py:797-853) after the layer's first half:
     x1 = bf16(x + y), h2 = rmsnorm(x1, ln2); the shared expert sh = bf16(silu(bf16 h2 Wg^T) * bf16 h2 Wu^T) Wd^T in
     fp32, its weights the layer's MLP (w_gate .. s_down) in fmt; logits = h2 w_router^T; the routing (ids, wts)
     given or the top-K of the logits (oracle.moe.route); base = x1 + sigmoid(h2 . w_shg) sh; the routed MXFP4 experts
-    as oracle.moe.moe_parts (fp32 slots). Returns (base, routed, slack, logits, ids, wts), fp32; slack bounds
-    `flips` one-ulp changes of each bf16 activation row, the shared expert's included (oracle.moe.moe_parts)."""
+    as oracle.moe.moe_parts (fp32 slots; slot_bf16: bf16 slots, the prefill form). Returns (base, routed, slack,
+    logits, ids, wts), fp32; slack bounds `flips` one-ulp changes of each bf16 activation row, the shared expert's
+    included (oracle.moe.moe_parts)."""
     from oracle import moe as omoe
 
     x1, h2 = add_rmsnorm(x, y, w["ln2"], eps)
@@ -149,7 +150,7 @@ def moe_block_parts(x, y, w: dict, moe: dict, eps: float = 1e-6, fmt: str = "mxf
     shg = moe.get("w_shg")
     gate = torch.sigmoid(h2.float() @ shg.float()) if shg is not None else torch.ones(x.shape[0])
     routed_w = {n: moe[n] for n in ("e_gw", "e_gs", "e_dw", "e_ds")}
-    base0, routed, slack = omoe.moe_parts(h2, routed_w, ids, wts, x1, flips=flips)
+    base0, routed, slack = omoe.moe_parts(h2, routed_w, ids, wts, x1, flips=flips, slot_bf16=slot_bf16)
     base = base0 + gate[:, None] * sh
     slack = slack + flips * (gate * omoe.ulp_bf16(act).amax(dim=1))[:, None] * wd.abs().amax(dim=1)[None, :]
     return base, routed, slack, logits, ids, wts
@@ -295,10 +296,22 @@ def gdn_layer_prefill(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_hea
 def gdn_layer_prefill_parts(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
                             proj_fmt: str = "fp8", mlp_fmt: str = "mxfp4", chunk: int = 64, flips: int = 2,
                             v_order: str = "tiled"):
-    """gdn_layer_prefill and a bound on how far `flips` one-ulp changes of each row's bf16 gated output (the input of
-    the output projection, rmsnorm(core) * silu(z), whose magnitude the gate can raise well above the core's) move
-    the layer output: per row, flips times the row's largest gated ulp against the largest |W_out| of each output
-    column, the model of oracle.moe.moe_parts. Returns (out, state_out, conv_out, slack fp32 [B, T, H])."""
+    """gdn_layer_prefill and the slack of gdn_prefill_half. Returns (out, state_out, conv_out, slack fp32
+    [B, T, H])."""
+    b, t, hd = x.shape
+    y, state_out, conv_out, slack = gdn_prefill_half(x, w, state_in, conv_in, num_k_heads, num_v_heads, eps, proj_fmt,
+                                                     chunk, flips, v_order)
+    out = mlp_residual(x.reshape(b * t, hd), y, w, eps, mlp_fmt).reshape(b, t, hd)
+    return out, state_out, conv_out, slack.reshape(b, t, hd)
+
+
+def gdn_prefill_half(x, w: dict, state_in, conv_in, num_k_heads: int, num_v_heads: int, eps: float = 1e-6,
+                     proj_fmt: str = "fp8", chunk: int = 64, flips: int = 2, v_order: str = "tiled"):
+    """The GDN prefill layer up to its output projection (q35_prefill.py:69-139 before the residual), over the B T
+    rows, and a bound on how far `flips` one-ulp changes of each row's bf16 gated output (the input of the output
+    projection, rmsnorm(core) * silu(z), whose magnitude the gate can raise well above the core's) move y: per row,
+    flips times the row's largest gated ulp against the largest |W_out| of each output column, the model of
+    oracle.moe.moe_parts. Returns (y bf16 [B T, H], state_out, conv_out, slack fp32 [B T, H])."""
     from oracle import gdn
     from oracle import moe as omoe
 
@@ -318,7 +331,36 @@ def gdn_layer_prefill_parts(x, w: dict, state_in, conv_in, num_k_heads: int, num
     core = _bf(core).reshape(r * num_v_heads, 128)
     gated = gated_rmsnorm_silu(core, w["norm_w"], z.reshape(r * num_v_heads, 128), eps).reshape(r, vd)
     y = proj(gated, w, "out", proj_fmt)
-    out = mlp_residual(xr, y, w, eps, mlp_fmt).reshape(b, t, hd)
     wo = dequant_weight(w, "out", proj_fmt)
     slack = flips * omoe.ulp_bf16(gated.float()).amax(dim=1)[:, None] * wo.abs().amax(dim=1)[None, :]
-    return out, state_out, conv_out, slack.reshape(b, t, hd)
+    return y, state_out, conv_out, slack
+
+
+def attn_rows_half(x, w: dict, cos, sin, cache, indptr, indices, last_page_len, cache_location, num_qo_heads: int,
+                   rot: int, eps: float = 1e-6, sm_scale=None, proj_fmt: str = "fp8"):
+    """The attention layer over T new rows per sequence up to its output projection: row t as a decode step over
+    the page table's prefix of history + t + 1 tokens (as attn_layer_verify). Returns (y bf16 [B T, H], the cache
+    with every new row written)."""
+    import numpy as np
+
+    from oracle import paged_attn
+
+    b, t_rows = x.shape[:2]
+    page = cache.shape[2]
+    ip = np.asarray(indptr)
+    idx = np.asarray(indices)
+    full = paged_attn.seq_lens(indptr, last_page_len, page)
+    ys = []
+    for t in range(t_rows):
+        ptr, ind, last = [0], [], []
+        for s_ in range(b):
+            n_tok = full[s_] - (t_rows - 1 - t)
+            pages = (n_tok + page - 1) // page
+            ind += idx[ip[s_]:ip[s_] + pages].tolist()
+            ptr.append(len(ind))
+            last.append(n_tok - (pages - 1) * page)
+        y, cache = attn_layer_half(x[:, t], w, cos[:, t], sin[:, t], cache, torch.tensor(ptr, dtype=torch.int32),
+                                   torch.tensor(ind, dtype=torch.int32), torch.tensor(last, dtype=torch.int32),
+                                   cache_location[:, t], num_qo_heads, rot, eps, sm_scale, proj_fmt)
+        ys.append(y)
+    return torch.stack(ys, 1).reshape(b * t_rows, -1), cache

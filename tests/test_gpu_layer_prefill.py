@@ -172,3 +172,81 @@ def test_prefill_contract_errors_enqueue_nothing(dev):
     assert e.value.status == 3  # AXK_E_ALIGN, found by the validate pass before the conv / state launches
     torch.cuda.synchronize()
     assert torch.equal(sd.cpu(), st) and torch.equal(cd.cpu(), cv)
+
+
+# ---- the MoE prefill layers (qwen35moe_gdn_prefill / qwen35moe_attn_prefill, q35_moe_prefill.py:47-77) ----
+def _routing_outputs(rows, blk, dev):
+    e, k = blk["w_router"].shape[0], blk["top_k"]
+    return dict(logits=torch.empty(rows, e, device=dev), topk_ids=torch.empty(rows, k, dtype=torch.int32, device=dev),
+                topk_weights=torch.empty(rows, k, device=dev))
+
+
+def _check_moe(out, r, x, y, w, blk, fmt, extra_slack):
+    """out [B, T, H]; r the kernel's routing outputs over the B T rows; y [B T, H] the oracle's first half; more
+    than 256 rows take the grouped prefill experts, whose slots are bf16 (oracle slot_bf16)."""
+    from oracle import moe as omoe
+
+    rows = y.shape[0]
+    logits, ids, wts = r["logits"].cpu(), r["topk_ids"].cpu(), r["topk_weights"].cpu()
+    sids, swts = omoe.route(logits, blk["top_k"], True)
+    assert torch.equal(ids, sids), "top-K ids differ from the stable sort of the kernel's logits"
+    torch.testing.assert_close(wts, swts, rtol=1e-5, atol=1e-6)
+    base, routed, slack, ref_logits, _, _ = olayer.moe_block_parts(x.reshape(rows, -1), y, w, blk, fmt=fmt,
+                                                                   ids=ids.long(), wts=wts, slot_bf16=rows > 256)
+    torch.testing.assert_close(logits, ref_logits, **TOL)
+    ref = (base + routed).bfloat16().float()
+    d = (out.reshape(rows, -1).float().cpu() - ref).abs()
+    tol = FUSED_TOL["atol"] + FUSED_TOL["rtol"] * ref.abs()
+    assert (d <= tol + slack + extra_slack).all(), f"max excess {(d - tol - slack - extra_slack).max().item()}"
+
+
+def _dev_any(w, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in w.items()}
+
+
+# 40 rows (the decode experts), 300 rows (the grouped prefill experts with bf16 slots), the 35B's widths
+@pytest.mark.parametrize("b,t,h,nk,nv,e,fe,k,fmt", [(2, 20, 256, 2, 4, 16, 256, 4, "mxfp8"),
+                                                    (2, 150, 256, 2, 4, 40, 256, 8, "mxfp4"),
+                                                    (1, 300, 2048, 16, 32, 256, 512, 8, "mxfp8")])
+def test_gdn_layer_prefill_moe(dev, b, t, h, nk, nv, e, fe, k, fmt):
+    g = torch.Generator().manual_seed(b * t + e)
+    print(f"gdn prefill moe b={b} t={t} h={h} e={e} {fmt}", flush=True)
+    w = configs.gdn_layer_weights(g, h, 256, nk, nv, proj_fmt="mxfp8", mlp_fmt=fmt)
+    blk = configs.moe_block(g, h, e, fe, k)
+    x = torch.randn(b, t, h, generator=g).bfloat16()
+    st = torch.randn(b, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(b, 3, (2 * nk + nv) * 128, generator=g).bfloat16()
+    r = _routing_outputs(b * t, blk, dev)
+    out, so, co = layer.gdn_layer_prefill(x.to(dev), _dev(w, dev), st.to(dev), cv.to(dev), nk, nv, proj_fmt="mxfp8",
+                                          mlp_fmt=fmt, moe=dict(_dev_any(blk, dev), **r))
+    y, rs, rc, yslack = olayer.gdn_prefill_half(x, w, st, cv, nk, nv, proj_fmt="mxfp8")
+    _check_moe(out, r, x, y, w, blk, fmt, yslack)
+    torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
+    _conv_close(co, rc, 3)
+
+
+def test_attn_layer_prefill_moe(dev):
+    """140 new tokens for each of 2 sequences (280 rows: the grouped prefill experts) over histories of 100 and 5."""
+    g = torch.Generator().manual_seed(280)
+    hq, hkv, rows = 4, 2, 140
+    w = configs.attn_layer_weights(g, H, 256, hq, hkv, 256, proj_fmt="mxfp8", mlp_fmt="mxfp8")
+    blk = configs.moe_block(g, H, 16, 256, 4)
+    c = configs.verify_rows_case([100, 5], rows, hq, hkv, 256, 64, g)
+    x = torch.randn(2, rows, H, generator=g).bfloat16()
+    cos, sin = olayer.rope_cos_sin(c["pos"].reshape(-1), 64, 10_000_000.0)
+    cos, sin = cos.reshape(2, rows, -1).contiguous(), sin.reshape(2, rows, -1).contiguous()
+    r = _routing_outputs(2 * rows, blk, dev)
+    cache = c["cache"].to(dev)
+    out = layer.attn_layer_prefill(x.to(dev), _dev(w, dev), cos.to(dev), sin.to(dev), cache, c["indptr"].to(dev),
+                                   c["indices"].to(dev), c["last_page_len"].to(dev), c["loc"].to(dev), hq, 64,
+                                   proj_fmt="mxfp8", mlp_fmt="mxfp8", moe=dict(_dev_any(blk, dev), **r))
+    y, rcache = olayer.attn_rows_half(x, w, cos, sin, c["cache"], c["indptr"], c["indices"], c["last_page_len"],
+                                      c["loc"], hq, 64, proj_fmt="mxfp8")
+    _check_moe(out, r, x, y, w, blk, "mxfp8", 0.0)
+    got = cache.cpu()
+    written = torch.zeros(got.shape[0], got.shape[2], dtype=torch.bool)
+    for p, o in c["loc"].reshape(-1, 2).tolist():
+        written[p, o] = True
+    torch.testing.assert_close(got.permute(0, 2, 1, 3, 4)[written].float(),
+                               rcache.permute(0, 2, 1, 3, 4)[written].float(), **TOL)
+

@@ -375,6 +375,24 @@ def test_v_tiled_is_the_reference_permutation():
     assert torch.equal(v_tiled(t[:6], 0, 3, 3, 2), t[:6])
 
 
+def test_attn_rows_half_is_the_verify_layer_before_its_mlp():
+    """attn_rows_half (the MoE prefill layer's first half) then the MLP residual is attn_layer_verify, exactly."""
+    from axk import configs
+
+    g = torch.Generator().manual_seed(8)
+    hq, hkv, d, page, H, F = 4, 2, 64, 16, 128, 128
+    w = configs.attn_layer_weights(g, H, F, hq, hkv, d)
+    c = configs.verify_rows_case([20, 15], 3, hq, hkv, d, page, g)
+    x = torch.randn(2, 3, H, generator=g).bfloat16()
+    cos, sin = layer.rope_cos_sin(c["pos"].reshape(-1), 32, 10_000_000.0)
+    cos, sin = cos.reshape(2, 3, -1), sin.reshape(2, 3, -1)
+    args = (c["indptr"], c["indices"], c["last_page_len"], c["loc"], hq, 32)
+    out, cache = layer.attn_layer_verify(x, w, cos, sin, c["cache"], *args)
+    y, cache2 = layer.attn_rows_half(x, w, cos, sin, c["cache"], *args)
+    assert torch.equal(layer.mlp_residual(x.reshape(6, H), y, w, 1e-6).reshape(2, 3, H), out)
+    assert torch.equal(cache, cache2)
+
+
 # ---- the MoE block of the MoE decode layers (moe_full, q35_layer_mc.py:797-853) ----
 @pytest.mark.parametrize("fmt", ["fp8", "mxfp8", "mxfp4"])
 def test_dequant_weight_is_what_proj_multiplies(fmt):
