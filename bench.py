@@ -689,6 +689,82 @@ class MoeLayerDecodeWorkload(Workload):
                           f"sequences, median of {reps} runs"}
 
 
+class MoeLayerPrefillWorkload(Workload):
+    """The 35B's MoE prefill layer (qwen35moe_gdn_prefill, q35_moe_prefill.py:47-52, then its routed experts and
+    combine 150-214): a prompt chunk of 4096 tokens through a GDN layer (16 key / 32 value heads, hidden 2048, MXFP8
+    projections) whose MLP is the MoE block (shared expert MXFP8 inter 512, 256 MXFP4 experts of 512, top-8), state
+    and conv state in place.
+
+    One step = the layer's launches (rmsnorm, the qkv | z | b | a GEMMs, conv, chunk prep + scan, gated norm, the
+    output GEMM), the shared expert's two GEMMs and config 3b's routed path, one graph. Algorithmic flops: every
+    projection, the shared and routed experts, the router and the chunked delta rule's products; bytes: the weights
+    (every expert is routed at this size), the state read and written, activations in and out."""
+
+    name = "moe_layer_prefill"
+    kernel = "35B MoE prefill layer (GDN prefill + shared expert + grouped routed experts)"
+    timing = "graph"
+    mfma = True
+    traffic_profile = "moe_layer_prefill_t4096_pmc.txt"  # every kernel of the step, summed
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, layer
+
+        self.t, self.h, self.nk, self.nv, e, fe, k = 4096, 2048, 16, 32, 256, 512, 8
+        g = torch.Generator().manual_seed(0)
+        w = configs.gdn_layer_weights(g, self.h, 512, self.nk, self.nv, proj_fmt="mxfp8", mlp_fmt="mxfp8")
+        blk = configs.moe_block(g, self.h, e, fe, k)
+        x = torch.randn(1, self.t, self.h, generator=g).bfloat16()
+        st = torch.randn(1, self.nv, 128, 128, generator=g) * 0.02
+        cv = torch.randn(1, 3, 2 * self.nk * 128 + self.nv * 128, generator=g).bfloat16()
+        self.host = (w, blk, x, st, cv)
+        self.wd = {n: v.to(dev) for n, v in w.items()}
+        self.bd = {n: (v.to(dev) if torch.is_tensor(v) else v) for n, v in blk.items()}
+        self.x, self.st, self.cv = x.to(dev), st.to(dev), cv.to(dev)
+        self.out = torch.empty_like(self.x)
+        self.ws = layer.gdn_prefill_workspace(1, self.t, self.h, self.nk, self.nv, 512, dev, moe=self.bd)
+        per_expert = sum(blk[n][0].numel() for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+        layer_bytes = sum(v.numel() * v.element_size() for v in w.values())
+        r, hh, kd, vd = self.t, self.h, self.nk * 128, self.nv * 128
+        c = 2 * kd + vd
+        self.alg_bytes = layer_bytes + blk["w_router"].numel() * 2 + blk["w_shg"].numel() * 2 + e * per_expert + \
+            2 * st.numel() * 4 + 2 * cv.numel() * 2 + 2 * x.numel() * 2
+        proj = 2 * r * hh * (c + vd + 2 * self.nv) + 2 * r * vd * hh
+        shared = 2 * r * hh * 2 * 512 + 2 * r * 512 * hh
+        routed = r * k * (2 * hh * 2 * fe + 2 * fe * hh)
+        chunk = self.nv * (-(-r // 64)) * (2 * 64 * 64 * 128 * 5 + 2 * 64 * 128 * 128 * 3)
+        self.alg_flops = proj + shared + routed + 2 * r * hh * e + chunk
+        self.config = {"workload": "35B MoE prefill layer: GDN (16/32 heads, H=2048, MXFP8) + MoE (shared MXFP8 "
+                                   "F=512, 256 MXFP4 experts F=512, top-8), B=1, T=4096"}
+        self.dtype = "mxfp8 / mxfp4 weights x bf16 -> fp32 acc, fp32 state"
+
+    def step(self, i: int) -> None:
+        from axk import layer
+
+        layer.gdn_layer_prefill(self.x, self.wd, self.st, self.cv, self.nk, self.nv, workspace=self.ws, out=self.out,
+                                state_out=self.st, conv_out=self.cv, proj_fmt="mxfp8", mlp_fmt="mxfp8", moe=self.bd)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import layer as olayer
+
+        w, blk, x, st, cv = self.host
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        n = 128  # a bounded sample: the first 128 tokens, scaled by tokens
+
+        def run():
+            y, _, _, _ = olayer.gdn_prefill_half(x[:, :n], w, st, cv, self.nk, self.nv, proj_fmt="mxfp8")
+            return olayer.moe_block_parts(x[0, :n], y, w, blk, fmt="mxfp8")
+
+        sec, reps = _time_cpu(run, budget_s=10.0, min_reps=1, max_reps=3)
+        return {"value": sec * self.t / n * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"oracle/layer.py on the first {n} of the {self.t} tokens (GDN prefill half + MoE block), "
+                          f"scaled by tokens, median of {reps} runs"}
+
+
 class CopyCalibWorkload(Workload):
     """A plain 256 MiB device-to-device copy: the known-size kernel that calibrates the FETCH_SIZE /
     WRITE_SIZE counters (read 256 MiB, write 256 MiB per launch)."""
@@ -1001,7 +1077,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
              LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
-             MxLinearPrefillWorkload.name: MxLinearPrefillWorkload,
+             MxLinearPrefillWorkload.name: MxLinearPrefillWorkload, MoeLayerPrefillWorkload.name: MoeLayerPrefillWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
