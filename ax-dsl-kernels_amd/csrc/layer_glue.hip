@@ -87,9 +87,9 @@ __global__ __launch_bounds__(64 * kRowsPerWg) void rmsnorm_rows_kernel(const uin
   }
 }
 
-// Register-resident variant for n <= 8192: TPR threads per row (64: a wave, 256: the workgroup), each holding CPT
-// 8-element chunks (c = rank + TPR i); every load of the row (x, y, z, w) is issued before the reduction, so a row
-// costs one memory round trip. Same rounding points as rmsnorm_rows_kernel.
+// Register-resident variant for n <= 8192: TPR threads per row (16 or 32: a lane group of a wave, 64: a wave, 256: the
+// workgroup), each holding CPT 8-element chunks (c = rank + TPR i); every load of the row (x, y, z, w) is issued
+// before the reduction, so a row costs one memory round trip. Same rounding points as rmsnorm_rows_kernel.
 template <int MODE, int TPR, int CPT>
 __global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                           const uint16_t* __restrict__ y, const float* __restrict__ w,
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const uint16_t* __rest
   __shared__ float part[256 / 64];
   const int rank = threadIdx.x % TPR;
   const int64_t row = (int64_t)blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
-  if (TPR == 64 && row >= rows) return;  // whole waves; TPR == 256 rows are always in range (grid = rows)
+  if (TPR <= 64 && row >= rows) return;  // whole lane groups; TPR == 256 rows are always in range (grid = rows)
   const int nch = n >> 3;
   float f[CPT][8], wv[CPT][8], zv[CPT][8];
   float ss = 0.f;
@@ -123,7 +123,12 @@ __global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const uint16_t* __rest
       for (int k = 0; k < 8; ++k) ss += f[i][k] * f[i][k];
     }
   }
-  ss = wave_sum(ss);
+  if constexpr (TPR < 64) {  // the row's lane group (aligned, whole: it returned or stayed together)
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  } else {
+    ss = wave_sum(ss);
+  }
   if (TPR == 256) {
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();
@@ -370,7 +375,9 @@ void launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* y, const flo
 #define AXK_RMS(TPR, CPT)                                                                                          \
   hipLaunchKernelGGL((rmsnorm_reg_kernel<MODE, TPR, CPT>), dim3((unsigned)((rows + 256 / TPR - 1) / (256 / TPR))), \
                      dim3(256), 0, st, x, ldx, y, w, z, sum_out, out, ldo, rows, n, eps)
-  if (nch <= 64) AXK_RMS(64, 1);
+  if (nch <= 16) AXK_RMS(16, 1);  // a head's row (128 values): 4 rows per wave
+  else if (nch <= 32) AXK_RMS(32, 1);
+  else if (nch <= 64) AXK_RMS(64, 1);
   else if (nch <= 128) AXK_RMS(64, 2);
   else if (nch <= 256) AXK_RMS(256, 1);
   else if (nch <= 512) AXK_RMS(256, 2);

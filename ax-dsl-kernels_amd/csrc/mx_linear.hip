@@ -402,17 +402,20 @@ size_t dg_lds_bytes(int64_t k) {
 struct DgArgs {
   const uint16_t* a;
   int64_t lda;
-  const uint8_t* w[2];      // the matrix (EPI_SWIGLU: gate, up)
-  const uint8_t* ws[2];     // E8M0 scales [n, k/32] (MX formats)
-  const float* col_scale[2];
-  const float* bias[2];
-  void* out;
-  int64_t ldo;
+  const uint8_t* w[AXK_MX_GROUP_MAX];   // EPI_PLAIN: the group's matrices; EPI_SWIGLU: gate, up; EPI_RES: one
+  const uint8_t* ws[AXK_MX_GROUP_MAX];  // E8M0 scales [n, k/32] (MX formats)
+  const float* col_scale[AXK_MX_GROUP_MAX];
+  const float* bias[AXK_MX_GROUP_MAX];
+  void* out[AXK_MX_GROUP_MAX];
+  int64_t ldo[AXK_MX_GROUP_MAX];
+  int n[AXK_MX_GROUP_MAX];
+  int cb0[AXK_MX_GROUP_MAX + 1];  // EPI_PLAIN: first column block of each matrix (cb0[count] = all of them)
+  int count;
   const float* row_scale;
   const uint16_t* res;  // EPI_RES
   int64_t ldr;
   int out_f32;
-  int m, n, k;
+  int m, k;
 };
 
 template <int F>
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int RB = dg_row_bytes<F>(), STAGE = dg_stage<F>();
   constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;  // output channels per workgroup
-  const int nb = (g.n + COLS - 1) / COLS, mb = (g.m + kDgBM - 1) / kDgBM;
+  const int nb = EPI == EPI_PLAIN ? g.cb0[g.count] : (g.n[0] + COLS - 1) / COLS, mb = (g.m + kDgBM - 1) / kDgBM;
   const int total = nb * mb, per = (total + kDgXcds - 1) / kDgXcds;
   const int q = blockIdx.x / kDgXcds, lid = (blockIdx.x % kDgXcds) * per + q;
   if (q >= per || lid >= total) return;
@@ -443,7 +446,11 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   const int gfirst = (lid / (kDgGroupRows * nb)) * kDgGroupRows, gsize = min(mb - gfirst, kDgGroupRows);
   const int inner = lid - gfirst * nb;
   const int rbk = gfirst + inner % gsize, cb = inner / gsize;
-  const int col0 = cb * COLS, m0 = rbk * kDgBM;
+  int mat = 0;  // EPI_PLAIN: the matrix whose column blocks hold cb (workgroup-uniform)
+  if constexpr (EPI == EPI_PLAIN)
+    while (mat + 1 < g.count && cb >= g.cb0[mat + 1]) ++mat;
+  const int N = g.n[mat];
+  const int col0 = (cb - (EPI == EPI_PLAIN ? g.cb0[mat] : 0)) * COLS, m0 = rbk * kDgBM;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
   const int K = g.k, nk = K / kDgBK;
   const uint32_t lds0 = lds_addr(smem);
@@ -453,8 +460,8 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   // LDS weight row rho -> weight row (SwiGLU: rho < 128 the gate channel col0 + rho, else the up channel col0 + rho -
   // 128), clamped to the last channel (never stored)
   auto wrow = [&](int rho, bool scale) -> const uint8_t* {
-    const int mi = EPI == EPI_SWIGLU && rho >= COLS ? 1 : 0;
-    const int c = min(col0 + (EPI == EPI_SWIGLU ? (rho & (COLS - 1)) : rho), g.n - 1);
+    const int mi = EPI == EPI_SWIGLU ? (rho >= COLS ? 1 : 0) : mat;
+    const int c = min(col0 + (EPI == EPI_SWIGLU ? (rho & (COLS - 1)) : rho), N - 1);
     return scale ? g.ws[mi] + (int64_t)c * (K / 32) : g.w[mi] + (int64_t)c * axk::row_bytes<F>(K);
   };
   // per-lane sources of this wave's direct loads of a step: A instructions i = 2 wave + h (rows 8 i + lane / 8,
@@ -494,7 +501,8 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   issue(1, 1);
   if constexpr (axk::is_mx(F)) {  // the E8M0 scales of the whole reduction (while the first steps load)
     const int sb = K / 32;
-    if (sb % 16 == 0 && (((uintptr_t)g.ws[0] | (uintptr_t)g.ws[1]) & 15) == 0) {
+    const uintptr_t wsa = EPI == EPI_SWIGLU ? ((uintptr_t)g.ws[0] | (uintptr_t)g.ws[1]) : (uintptr_t)g.ws[mat];
+    if (sb % 16 == 0 && (wsa & 15) == 0) {
       const int u = sb / 16;
       for (int idx = tid; idx < kDgBN * u; idx += 256) {
         const int rho = idx / u, qq = idx - rho * u;
@@ -571,29 +579,29 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int nn = col0 + 32 * wave + 16 * j + l16;
-          if (nn >= g.n) continue;
+          if (nn >= N) continue;
           const float gv = fin(0, nn, m, acc[mt][j][r]), uv = fin(1, nn, m, acc[mt][j + 2][r]);
-          reinterpret_cast<uint16_t*>(g.out)[(int64_t)m * g.ldo + nn] =
+          reinterpret_cast<uint16_t*>(g.out[0])[(int64_t)m * g.ldo[0] + nn] =
               (uint16_t)f32_to_bf16_bits(silu_f32(round_bf16(gv)) * round_bf16(uv));
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int nn = col0 + 64 * wave + 16 * j + l16;
-          if (nn >= g.n) continue;
-          float v = fin(0, nn, m, acc[mt][j][r]);
+          if (nn >= N) continue;
+          float v = fin(mat, nn, m, acc[mt][j][r]);
           if constexpr (EPI == EPI_RES) v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
           if (g.out_f32)
-            reinterpret_cast<float*>(g.out)[(int64_t)m * g.ldo + nn] = v;
+            reinterpret_cast<float*>(g.out[mat])[(int64_t)m * g.ldo[mat] + nn] = v;
           else
-            reinterpret_cast<uint16_t*>(g.out)[(int64_t)m * g.ldo + nn] = (uint16_t)f32_to_bf16_bits(v);
+            reinterpret_cast<uint16_t*>(g.out[mat])[(int64_t)m * g.ldo[mat] + nn] = (uint16_t)f32_to_bf16_bits(v);
         }
       }
     }
 }
 
-// Launches the dense GEMM for a checked group (one launch per matrix; EPI_SWIGLU one for the pair). False when the
-// shape does not take it (then the group kernel runs).
+// The dense GEMM for a checked group: one launch for all of its matrices (their column blocks end to end; EPI_SWIGLU
+// the gate / up pair). dg_fits is false when the shape does not take it (then the group kernel runs).
 template <int F>
 bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv) {
   if constexpr (F == axk::WF_BF16) {
@@ -613,7 +621,8 @@ int dg_launch(const DgArgs& d, hipStream_t st) {
     lds_raised = true;
   }
   constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;
-  const int64_t tiles = ((int64_t)d.n + COLS - 1) / COLS * (((int64_t)d.m + kDgBM - 1) / kDgBM);
+  const int64_t nb = EPI == EPI_PLAIN ? d.cb0[d.count] : ((int64_t)d.n[0] + COLS - 1) / COLS;
+  const int64_t tiles = nb * (((int64_t)d.m + kDgBM - 1) / kDgBM);
   const int64_t grid = (tiles + kDgXcds - 1) / kDgXcds * kDgXcds;  // whole rounds over the XCDs
   AXK_REQUIRE(grid <= INT32_MAX, AXK_E_SHAPE);
   hipLaunchKernelGGL((mx_gemm_kernel<F, EPI>), dim3((unsigned)grid), dim3(256), dg_lds_bytes<F>(d.k), st, d);
@@ -622,30 +631,24 @@ int dg_launch(const DgArgs& d, hipStream_t st) {
 
 template <int F>
 int dg_group(const uint16_t* a, int64_t lda, const MxGroup& g, int epi, int64_t m, int64_t k, hipStream_t st) {
-  auto args = [&](int i0, int i1) {
-    DgArgs d{};
-    d.a = a;
-    d.lda = lda;
-    d.w[0] = g.w[i0], d.w[1] = g.w[i1];
-    d.ws[0] = g.ws[i0], d.ws[1] = g.ws[i1];
-    d.col_scale[0] = g.col_scale[i0], d.col_scale[1] = g.col_scale[i1];
-    d.bias[0] = g.bias[i0], d.bias[1] = g.bias[i1];
-    d.out = g.out[i0];
-    d.ldo = g.ldo[i0];
-    d.row_scale = g.row_scale;
-    d.res = g.res;
-    d.ldr = g.ldr;
-    d.out_f32 = g.out_f32;
-    d.m = (int)m, d.n = g.n[i0], d.k = (int)k;
-    return d;
-  };
-  if (epi == EPI_SWIGLU) return dg_launch<F, EPI_SWIGLU>(args(0, 1), st);
-  if (epi == EPI_RES) return dg_launch<F, EPI_RES>(args(0, 0), st);
+  DgArgs d{};
+  d.a = a;
+  d.lda = lda;
+  d.count = g.count;
+  d.cb0[0] = 0;
   for (int i = 0; i < g.count; ++i) {
-    const int rc = dg_launch<F, EPI_PLAIN>(args(i, i), st);
-    if (rc != AXK_OK) return rc;
+    d.w[i] = g.w[i], d.ws[i] = g.ws[i], d.col_scale[i] = g.col_scale[i], d.bias[i] = g.bias[i];
+    d.out[i] = g.out[i], d.ldo[i] = g.ldo[i], d.n[i] = g.n[i];
+    d.cb0[i + 1] = d.cb0[i] + (g.n[i] + kDgBN - 1) / kDgBN;
   }
-  return AXK_OK;
+  d.row_scale = g.row_scale;
+  d.res = g.res;
+  d.ldr = g.ldr;
+  d.out_f32 = g.out_f32;
+  d.m = (int)m, d.k = (int)k;
+  if (epi == EPI_SWIGLU) return dg_launch<F, EPI_SWIGLU>(d, st);
+  if (epi == EPI_RES) return dg_launch<F, EPI_RES>(d, st);
+  return dg_launch<F, EPI_PLAIN>(d, st);  // every matrix of the group in one launch
 }
 
 // Checks a group and launches it. Matrices need whole 128-byte row segments (and 8-byte aligned MXFP4 scale rows).

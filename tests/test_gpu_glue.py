@@ -21,8 +21,10 @@ def _close(got, ref):
     torch.testing.assert_close(got.float().cpu(), ref.float(), **TOL)
 
 
+# rows of 16-lane groups (n <= 128: a partial last workgroup at 5 and 33 rows), 32-lane groups (136, 256), waves,
+# workgroups and the looping kernel (n > 8192)
 @pytest.mark.parametrize("rows,n", [(8, 4096), (3, 2048), (64, 128), (5, 8), (2, 8192), (4, 6144), (3, 1032),
-                                    (2, 16384), (9, 1024)])
+                                    (2, 16384), (9, 1024), (5, 128), (33, 128), (7, 256), (3, 136)])
 def test_rmsnorm(dev, rows, n):
     g = _g(rows + n)
     x = torch.randn(rows, n, generator=g).bfloat16() * 3
@@ -53,10 +55,11 @@ def test_add_rmsnorm(dev, rows, n):
     _close(n, rn)
 
 
-def test_gated_rmsnorm_silu(dev):
+@pytest.mark.parametrize("rows", [8 * 32, 13, 4096 * 32])
+def test_gated_rmsnorm_silu(dev, rows):
     g = _g(3)
-    x = torch.randn(8 * 32, 128, generator=g).bfloat16()
-    z = torch.randn(8 * 32, 128, generator=g).bfloat16()
+    x = torch.randn(rows, 128, generator=g).bfloat16()
+    z = torch.randn(rows, 128, generator=g).bfloat16()
     w = torch.rand(128, generator=g) + 0.5
     _close(glue.gated_rmsnorm_silu(x.to(dev), w.to(dev), z.to(dev)), layer.gated_rmsnorm_silu(x, w, z))
 
