@@ -140,6 +140,20 @@ AXK_DEV void lds_dma16_cached(const void* gptr, uint32_t lds_base_any) {
       : "memory");
 }
 
+// As lds_dma16_cached for 4 bytes a lane: lane l's dword at gptr (4-byte aligned) lands at lds_base + 4 l.
+AXK_DEV void lds_dma4_cached(const void* gptr, uint32_t lds_base_any) {
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(gptr)
+      : "memory");
+}
+
 template <int N>
 AXK_DEV void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

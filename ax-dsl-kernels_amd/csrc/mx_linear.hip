@@ -382,8 +382,9 @@ int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, 
 // weight rows of each 64-wide K step land in a ring of kDgStages LDS slots by direct loads two steps ahead, one
 // barrier per step: A [64 rows][128 B] with 16-byte chunk c of row r at position c ^ (r & 7); B [256 rows][RB bytes]
 // (RB = 32 for MXFP4, 64 for the 8-bit formats) with 16-byte chunk c of row r at c ^ ((r >> 3) & 1) (MXFP4) or
-// c ^ ((r >> 2) & 3) (8-bit): the fragment reads are free of bank conflicts. E8M0 scales of the whole reduction are
-// staged in LDS once; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
+// c ^ ((r >> 2) & 3) (8-bit): the fragment reads are free of bank conflicts. The E8M0 bytes of each step come with
+// the step's direct loads (one dword per weight row), so LDS holds only the ring (49.5 / 73.5 KiB) and two or three
+// workgroups share a CU; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
 // kernel's. Consecutive workgroups go round-robin over the 8 XCDs, so each XCD takes a contiguous run of the tile
 // order, which walks groups of 8 row blocks across all column blocks: an XCD's L2 keeps its activation rows.
 // ---------------------------------------------------------------------------------------------
@@ -392,11 +393,12 @@ constexpr int64_t kDgMinRows = 128;  // below this the group kernel (weights str
 constexpr int kDgAStage = kDgBM * kDgBK * 2;  // 8 KiB
 template <int F>
 constexpr int dg_row_bytes() { return F == WF_MXFP4 ? kDgBK / 2 : kDgBK; }  // weight bytes per row and step
+constexpr int kDgSStage = kDgBN * 4;  // MX formats: one scale dword per weight row and step
 template <int F>
-constexpr int dg_stage() { return kDgAStage + kDgBN * dg_row_bytes<F>(); }
+constexpr int dg_stage() { return kDgAStage + kDgBN * dg_row_bytes<F>() + (axk::is_mx(F) ? kDgSStage : 0); }
 template <int F>
-size_t dg_lds_bytes(int64_t k) {
-  return (size_t)kDgStages * dg_stage<F>() + (axk::is_mx(F) ? (size_t)kDgBN * (k / 32 + 16) : 0);
+size_t dg_lds_bytes(int64_t) {
+  return (size_t)kDgStages * dg_stage<F>();
 }
 
 struct DgArgs {
@@ -454,8 +456,6 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
   const int K = g.k, nk = K / kDgBK;
   const uint32_t lds0 = lds_addr(smem);
-  unsigned char* sS = smem + kDgStages * STAGE;
-  const int ldS = K / 32 + 16;
 
   // LDS weight row rho -> weight row (SwiGLU: rho < 128 the gate channel col0 + rho, else the up channel col0 + rho -
   // 128), clamped to the last channel (never stored)
@@ -487,38 +487,30 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
       bsrc[h] = wrow(rho, false) + 16 * ((lane & 3) ^ ((rho >> 2) & 3));
     }
   }
-  // step ks into ring slot buf (past the last step the last one again: in bounds, unused), so every iteration
-  // waits on the same count
-  auto issue = [&](int ks, int buf) {
-    const int kk = min(ks, nk - 1);
-    const uint32_t base = lds0 + buf * STAGE;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) lds_dma16_cached(asrc[h] + kk * kDgBK, base + (2 * wave + h) * 1024);
-#pragma unroll
-    for (int h = 0; h < BI; ++h) lds_dma16_cached(bsrc[h] + kk * RB, base + kDgAStage + (BI * wave + h) * 1024);
-  };
-  issue(0, 0);
-  issue(1, 1);
-  if constexpr (axk::is_mx(F)) {  // the E8M0 scales of the whole reduction (while the first steps load)
-    const int sb = K / 32;
-    const uintptr_t wsa = EPI == EPI_SWIGLU ? ((uintptr_t)g.ws[0] | (uintptr_t)g.ws[1]) : (uintptr_t)g.ws[mat];
-    if (sb % 16 == 0 && (wsa & 15) == 0) {
-      const int u = sb / 16;
-      for (int idx = tid; idx < kDgBN * u; idx += 256) {
-        const int rho = idx / u, qq = idx - rho * u;
-        *reinterpret_cast<uint4*>(sS + rho * ldS + 16 * qq) = *reinterpret_cast<const uint4*>(wrow(rho, true) + 16 * qq);
-      }
-    } else {
-      for (int idx = tid; idx < kDgBN * sb; idx += 256) {
-        const int rho = idx / sb, qq = idx - rho * sb;
-        sS[rho * ldS + qq] = wrow(rho, true)[qq];
-      }
-    }
-  }
   int brow[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     brow[j] = EPI == EPI_SWIGLU ? (j >> 1) * COLS + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
+  // the E8M0 bytes of a step (MX formats) join the direct loads: wave w loads the aligned dword holding blocks
+  // 4 (ks / 2) .. + 3 of weight rows 64 w + lane into the slot's scale table [256 rows][4 B], so no whole-K scale
+  // table takes LDS (which then fits several workgroups a CU) and the loop has no load the compiler waits on
+  const uint8_t* ssrc = axk::is_mx(F) ? wrow(64 * wave + lane, true) : nullptr;
+  // step ks into ring slot BUF (past the last step the last one again: in bounds, unused), so every iteration
+  // waits on the same count
+  auto issue = [&](int ks, auto buf_c) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(buf_c)::value;
+    const int kk = min(ks, nk - 1);
+    const uint32_t base = lds0 + BUF * STAGE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lds_dma16_cached(asrc[h] + kk * kDgBK, base + (2 * wave + h) * 1024);
+#pragma unroll
+    for (int h = 0; h < BI; ++h) lds_dma16_cached(bsrc[h] + kk * RB, base + kDgAStage + (BI * wave + h) * 1024);
+    if constexpr (axk::is_mx(F))
+      lds_dma4_cached(ssrc + 4 * (kk >> 1), base + kDgAStage + kDgBN * RB + 256 * wave);
+  };
+  constexpr int LPS = 2 + BI + (axk::is_mx(F) ? 1 : 0);  // vector-memory instructions per step
+  issue(0, std::integral_constant<int, 0>{});
+  issue(1, std::integral_constant<int, 1>{});
   axk_f32x4 acc[4][4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
@@ -527,11 +519,11 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
 
   auto step = [&](int ks, auto buf_c) __attribute__((always_inline)) {
     constexpr int BUF = decltype(buf_c)::value;
-    wait_vmcnt<2 + BI>();  // this wave's loads of step ks have landed (step ks + 1's may not have)
+    wait_vmcnt<LPS>();  // this wave's loads of step ks have landed (step ks + 1's may not have)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of step ks - 1 are done
     __builtin_amdgcn_s_barrier();  // every wave's step-ks loads landed; every wave is done with step ks - 1
     asm volatile("" ::: "memory");
-    issue(ks + 2, (BUF + 2) % kDgStages);  // into the slot of step ks - 1
+    issue(ks + 2, std::integral_constant<int, (BUF + 2) % kDgStages>{});  // into the slot of step ks - 1
     const unsigned char* sa = smem + BUF * STAGE;
     const unsigned char* sb = sa + kDgAStage;
 #pragma unroll
@@ -540,7 +532,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = brow[j] + l16;
-        const float sc = axk::is_mx(F) ? e8m0_to_f32(sS[r * ldS + 2 * ks + kh]) : 1.0f;
+        const float sc = axk::is_mx(F) ? e8m0_to_f32(sb[kDgBN * RB + 4 * r + 2 * (ks & 1) + kh]) : 1.0f;
         bf[j] = dg_decode<F>(sb + r * RB, kh, g4, r, sc);
       }
 #pragma unroll
@@ -602,12 +594,20 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
 
 // The dense GEMM for a checked group: one launch for all of its matrices (their column blocks end to end; EPI_SWIGLU
 // the gate / up pair). dg_fits is false when the shape does not take it (then the group kernel runs).
+// MX formats load each step's E8M0 bytes as 4-byte aligned dwords of the scale rows: K a multiple of 128 (whole
+// dwords per row) and 4-byte aligned scale matrices.
 template <int F>
-bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv) {
+bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv, const MxGroup& g) {
   if constexpr (F == axk::WF_BF16) {
     return false;
   } else {
-    return conv == nullptr && m >= kDgMinRows && k % kDgBK == 0 && dg_lds_bytes<F>(k) <= 160 * 1024;
+    if (conv != nullptr || m < kDgMinRows || k % kDgBK != 0 || dg_lds_bytes<F>(k) > 160 * 1024) return false;
+    if constexpr (axk::is_mx(F)) {
+      if (k % 128 != 0) return false;
+      for (int i = 0; i < g.count; ++i)
+        if (!axk_aligned(g.ws[i], 4)) return false;
+    }
+    return true;
   }
 }
 
@@ -715,7 +715,7 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   for (int i = count; i <= AXK_MX_GROUP_MAX; ++i) g.tile0[i] = (int)tiles;
   if (m == 0) return AXK_OK;
   AXK_LAUNCH_GATE();
-  if (dg_fits<F>(m, k, conv)) return dg_group<F>(a, lda, g, epi, m, k, st);
+  if (dg_fits<F>(m, k, conv, g)) return dg_group<F>(a, lda, g, epi, m, k, st);
   if (epi == EPI_SWIGLU) return group_dispatch<F, EPI_SWIGLU>(a, lda, g, m, k, st);
   if (epi == EPI_RES) return group_dispatch<F, EPI_RES>(a, lda, g, m, k, st);
   return group_dispatch<F, EPI_PLAIN>(a, lda, g, m, k, st);
