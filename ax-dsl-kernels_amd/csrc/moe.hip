@@ -1110,7 +1110,9 @@ __global__ __launch_bounds__(256) void moe_pscatter_kernel(const int32_t* __rest
 // row r at position c ^ (r & 7), and B [256 weight rows][32 B] with the 16-byte half h of row r at position
 // h ^ ((r >> 3) & 1): the fragment reads of either are then free of bank conflicts. Workgroups are mapped so that
 // all tiles and column blocks of one expert run on one XCD: its weights are fetched into that XCD's L2 once.
-// LDS: kGStages x (A 8 KiB + B 8 KiB); scales [256 rows][Kd/32 + 16].
+// SDMA (reductions of whole 128-element scale dwords, 4-byte aligned scales): each step's E8M0 bytes come with the
+// step's direct loads, one dword per weight row, LDS kGStages x (A 8 KiB + B 8 KiB + 1 KiB), so three workgroups
+// share a CU; otherwise the scales of the whole reduction are staged once, LDS kGStages x 16 KiB + [256][Kd/32 + 16].
 // ---------------------------------------------------------------------------------------------
 struct GGemmArgs {
   const uint16_t* a;     // gate-up: h2 [T, H]; down: act [P, F]
@@ -1129,10 +1131,14 @@ constexpr int kGStages = 3;
 constexpr int kGAStage = kBM * kBK * 2;      // 8 KiB
 constexpr int kGBStage = kG2Rows * kBK / 2;  // 8 KiB
 constexpr int kGStage = kGAStage + kGBStage;
-size_t gemm_lds_bytes(int Kd) { return (size_t)kGStages * kGStage + (size_t)kG2Rows * (Kd / 32 + 16); }
+constexpr int kGSStage = kG2Rows * 4;  // SDMA: one scale dword per weight row and step
+size_t gemm_lds_bytes(int Kd, bool sdma) {
+  return sdma ? (size_t)kGStages * (kGStage + kGSStage) : (size_t)kGStages * kGStage + (size_t)kG2Rows * (Kd / 32 + 16);
+}
 
-template <int MODE>
+template <int MODE, bool SDMA>
 __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
+  constexpr int STAGE = kGStage + (SDMA ? kGSStage : 0);
   extern __shared__ __align__(16) unsigned char smem[];
   const int nblk = MODE == 0 ? (g.Fmax + kG2Cols0 - 1) / kG2Cols0 : (g.H + kG2Cols1 - 1) / kG2Cols1;
   const int total = *g.ws.n_tiles * nblk, per = (total + kXcds - 1) / kXcds;
@@ -1150,7 +1156,7 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   const int col0 = cblk * (MODE == 0 ? kG2Cols0 : kG2Cols1);
   if (col0 >= No) return;
   const uint32_t lds0 = lds_addr(smem);
-  unsigned char* sS = smem + kGStages * kGStage;
+  unsigned char* sS = smem + kGStages * STAGE;  // whole-reduction scales (not SDMA)
   const int ldS = Kd / 32 + 16;
   const int nk = Kd / kBK;
 
@@ -1195,23 +1201,26 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
     const int rho = 32 * i + (lane >> 1);
     bsrc[h] = wrow(rho, false) + 16 * ((lane & 1) ^ ((rho >> 3) & 1));
   }
+  // SDMA: wave w loads the aligned dword holding blocks 4 (ks / 2) .. + 3 of weight rows 64 w + lane
+  const uint8_t* ssrc = SDMA ? wrow(64 * wave + lane, true) : nullptr;
   // step ks into ring slot buf; past the last step the last one is loaded again (in bounds, unused), so every
   // iteration waits on the same count
   auto issue = [&](int ks, int buf) {
     const int kk = min(ks, nk - 1);
-    const uint32_t base = lds0 + buf * kGStage;
+    const uint32_t base = lds0 + buf * STAGE;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       lds_dma16_cached(asrc[h] + kk * kBK, base + (2 * wave + h) * 1024);
       lds_dma16_cached(bsrc[h] + kk * (kBK / 2), base + kGAStage + (2 * wave + h) * 1024);
     }
+    if constexpr (SDMA) lds_dma4_cached(ssrc + 4 * (kk >> 1), base + kGStage + 256 * wave);
   };
   issue(0, 0);
   issue(1, 1);
 
   // the E8M0 scales of the whole reduction (while the first steps load): 16-byte units when the row length
   // allows, else 2-byte units
-  {
+  if constexpr (!SDMA) {
     const int sb = Kd / 32;
     if (sb % 16 == 0 && (((uintptr_t)sgate | (uintptr_t)sup) & 15) == 0) {
       const int u = sb / 16;
@@ -1242,12 +1251,12 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   // step ks from ring slot BUF (a constant: the loop is unrolled over the ring, so every LDS offset is immediate)
   auto step = [&](int ks, auto buf_c) __attribute__((always_inline)) {
     constexpr int BUF = decltype(buf_c)::value;
-    wait_vmcnt<4>();  // this wave's loads of step ks have landed (step ks + 1's four may not have)
+    wait_vmcnt<SDMA ? 5 : 4>();  // this wave's loads of step ks have landed (step ks + 1's may not have)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of step ks - 1 are done
     __builtin_amdgcn_s_barrier();  // every wave's step-ks loads landed; every wave is done with step ks - 1
     asm volatile("" ::: "memory");
     issue(ks + 2, (BUF + 2) % kGStages);  // into the slot of step ks - 1
-    const unsigned char* sa = smem + BUF * kGStage;
+    const unsigned char* sa = smem + BUF * STAGE;
     const unsigned char* sb = sa + kGAStage;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -1256,7 +1265,8 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
       for (int j = 0; j < 4; ++j) {
         const int r = brow[j] + l16;
         const uint32_t w = *reinterpret_cast<const uint32_t*>(sb + r * 32 + 16 * (kh ^ ((r >> 3) & 1)) + 4 * g4);
-        const uint32_t sbyte = sS[r * ldS + 2 * ks + kh];  // one E8M0 byte: two VALU to an fp32 scale
+        // one E8M0 byte: two VALU to an fp32 scale
+        const uint32_t sbyte = SDMA ? sb[kGBStage + 4 * r + 2 * (ks & 1) + kh] : sS[r * ldS + 2 * ks + kh];
         bf[j] = fp4x8_to_bf16x8(w, e8m0_to_f32(sbyte));
       }
 #pragma unroll
@@ -1405,21 +1415,33 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
     const int fmax = F > Fs ? F : Fs;
     GGemmArgs gu{h2, nullptr, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, fmax, w};
-    const size_t lds0 = gemm_lds_bytes(H), lds1 = gemm_lds_bytes(fmax);
+    // per-step scale dwords (SDMA) where every scale row of the reduction is whole, aligned dwords
+    auto a4 = [](const void* p) { return p == nullptr || axk_aligned(p, 4); };
+    const bool sdma0 = H % 128 == 0 && a4(e_gs) && a4(sh_gate_s) && a4(sh_up_s);
+    const bool sdma1 = F % 128 == 0 && Fs % 128 == 0 && a4(e_ds) && a4(sh_down_s);
+    const size_t lds0 = gemm_lds_bytes(H, sdma0), lds1 = gemm_lds_bytes(fmax, sdma1);
     static bool gemm_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
     if (!gemm_raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm_kernel<0>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess ||
-          hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_ggemm_kernel<1>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
-        return AXK_E_LAUNCH;
+      const void* fns[4] = {reinterpret_cast<const void*>(&moe_ggemm_kernel<0, false>),
+                            reinterpret_cast<const void*>(&moe_ggemm_kernel<1, false>),
+                            reinterpret_cast<const void*>(&moe_ggemm_kernel<0, true>),
+                            reinterpret_cast<const void*>(&moe_ggemm_kernel<1, true>)};
+      for (const void* f : fns)
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
+          return AXK_E_LAUNCH;
       gemm_raised = true;
     }
     const unsigned nb0 = (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0), nb1 = (unsigned)((H + kG2Cols1 - 1) / kG2Cols1);
     auto xgrid = [](unsigned n) { return dim3((n + kXcds - 1) / kXcds * kXcds); };  // whole rounds over the XCDs
-    hipLaunchKernelGGL(moe_ggemm_kernel<0>, xgrid(tiles * nb0), dim3(256), lds0, st, gu);
+    if (sdma0)
+      hipLaunchKernelGGL((moe_ggemm_kernel<0, true>), xgrid(tiles * nb0), dim3(256), lds0, st, gu);
+    else
+      hipLaunchKernelGGL((moe_ggemm_kernel<0, false>), xgrid(tiles * nb0), dim3(256), lds0, st, gu);
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
-    hipLaunchKernelGGL(moe_ggemm_kernel<1>, xgrid(tiles * nb1), dim3(256), lds1, st, dn);
+    if (sdma1)
+      hipLaunchKernelGGL((moe_ggemm_kernel<1, true>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
+    else
+      hipLaunchKernelGGL((moe_ggemm_kernel<1, false>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, combine_shared, T, H, K, w, out};
     hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
                        dim3(256), 0, st, ca);
