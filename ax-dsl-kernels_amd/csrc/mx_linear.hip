@@ -376,26 +376,36 @@ int group_dispatch(const uint16_t* a, int64_t lda, const MxGroup& g, int64_t m, 
 }
 
 // ---------------------------------------------------------------------------------------------
-// The large-M path (prefill): a dense GEMM per matrix (or per gate / up pair) with an LDS pipeline. Workgroup = 64
-// activation rows x 256 weight rows (EPI_SWIGLU: 128 gate + the same 128 up channels), wave w a 64 x 64 block of
-// four by four MFMA tiles (every A fragment feeds four MFMAs, every B fragment four). The activation rows and the
+// The large-M path (prefill): a dense GEMM over the matrices of a group (or a gate / up pair) with an LDS pipeline.
+// Workgroup = BM activation rows (dg_bm: 128 for MXFP4, 64 for the 8-bit formats) x 256 weight rows (EPI_SWIGLU: 128
+// gate + the same 128 up channels), wave w a BM x 64 block of BM / 16 by four MFMA tiles (every A fragment feeds
+// four MFMAs, every decoded B fragment BM / 16). The activation rows and the
 // weight rows of each 64-wide K step land in a ring of kDgStages LDS slots by direct loads two steps ahead, one
-// barrier per step: A [64 rows][128 B] with 16-byte chunk c of row r at position c ^ (r & 7); B [256 rows][RB bytes]
+// barrier per step: A [BM rows][128 B] with 16-byte chunk c of row r at position c ^ (r & 7); B [256 rows][RB bytes]
 // (RB = 32 for MXFP4, 64 for the 8-bit formats) with 16-byte chunk c of row r at c ^ ((r >> 3) & 1) (MXFP4) or
 // c ^ ((r >> 2) & 3) (8-bit): the fragment reads are free of bank conflicts. The E8M0 bytes of each step come with
-// the step's direct loads (one dword per weight row), so LDS holds only the ring (49.5 / 73.5 KiB) and two or three
-// workgroups share a CU; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
+// the step's direct loads (one dword per weight row), so LDS holds only the ring (75 KiB for MXFP4, 73.5 KiB for the
+// 8-bit formats) and two workgroups share a CU; FP8 per-channel scales, biases, row scales and the SwiGLU / residual epilogues as the group
 // kernel's. Consecutive workgroups go round-robin over the 8 XCDs, so each XCD takes a contiguous run of the tile
 // order, which walks groups of 8 row blocks across all column blocks: an XCD's L2 keeps its activation rows.
 // ---------------------------------------------------------------------------------------------
-constexpr int kDgBM = 64, kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8, kDgGroupRows = 8;
+constexpr int kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8, kDgGroupRows = 8;
+// activation rows per workgroup: 128 for MXFP4 (each decoded weight fragment feeds eight MFMAs; a 75 KiB ring, two
+// workgroups a CU), 64 for the 8-bit formats (whose 64-byte weight rows would make a 128-row ring 99 KiB: one a CU)
+template <int F>
+constexpr int dg_bm() { return F == WF_MXFP4 ? 128 : 64; }
+template <int F>
+constexpr int dg_mt() { return dg_bm<F>() / 16; }  // 16-row MFMA tiles per wave (a wave spans every row of the tile)
+template <int F>
+constexpr int dg_ai() { return dg_bm<F>() * kDgBK * 2 / 1024 / 4; }  // A direct-load instructions per wave and step
+template <int F>
+constexpr int dg_astage() { return dg_bm<F>() * kDgBK * 2; }
 constexpr int64_t kDgMinRows = 128;  // below this the group kernel (weights streamed once per 16 / 32 rows) is faster
-constexpr int kDgAStage = kDgBM * kDgBK * 2;  // 8 KiB
 template <int F>
 constexpr int dg_row_bytes() { return F == WF_MXFP4 ? kDgBK / 2 : kDgBK; }  // weight bytes per row and step
 constexpr int kDgSStage = kDgBN * 4;  // MX formats: one scale dword per weight row and step
 template <int F>
-constexpr int dg_stage() { return kDgAStage + kDgBN * dg_row_bytes<F>() + (axk::is_mx(F) ? kDgSStage : 0); }
+constexpr int dg_stage() { return dg_astage<F>() + kDgBN * dg_row_bytes<F>() + (axk::is_mx(F) ? kDgSStage : 0); }
 template <int F>
 size_t dg_lds_bytes(int64_t) {
   return (size_t)kDgStages * dg_stage<F>();
@@ -435,9 +445,10 @@ AXK_DEV axk_bf16x8 dg_decode(const unsigned char* row, int kh, int g4, int r, fl
 }
 
 template <int F, int EPI>
-__global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
+__global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int RB = dg_row_bytes<F>(), STAGE = dg_stage<F>();
+  constexpr int kDgBM = dg_bm<F>(), kDgMT = dg_mt<F>(), kDgAI = dg_ai<F>(), kDgAStage = dg_astage<F>();
   constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;  // output channels per workgroup
   const int nb = EPI == EPI_PLAIN ? g.cb0[g.count] : (g.n[0] + COLS - 1) / COLS, mb = (g.m + kDgBM - 1) / kDgBM;
   const int total = nb * mb, per = (total + kDgXcds - 1) / kDgXcds;
@@ -464,15 +475,16 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
     const int c = min(col0 + (EPI == EPI_SWIGLU ? (rho & (COLS - 1)) : rho), N - 1);
     return scale ? g.ws[mi] + (int64_t)c * (K / 32) : g.w[mi] + (int64_t)c * axk::row_bytes<F>(K);
   };
-  // per-lane sources of this wave's direct loads of a step: A instructions i = 2 wave + h (rows 8 i + lane / 8,
+  // per-lane sources of this wave's direct loads of a step: A instructions i = kDgAI wave + h (rows 8 i + lane / 8,
   // chunk (lane % 8) ^ (row & 7)); B instructions (RB == 32: 2 per wave, 32 rows each; RB == 64: 4 per wave,
   // 16 rows each)
   constexpr int BI = kDgBN * RB / 1024 / 4;  // B instructions per wave and step
-  const uint16_t* asrc[2];
+  static_assert(kDgAI * 4 * 1024 == kDgAStage && BI * 4 * 1024 == kDgBN * RB, "the direct loads cover the stage");
+  const uint16_t* asrc[kDgAI];
   const uint8_t* bsrc[BI];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int i = 2 * wave + h;
+  for (int h = 0; h < kDgAI; ++h) {
+    const int i = kDgAI * wave + h;
     const int r = 8 * i + (lane >> 3), rr = min(m0 + r, g.m - 1), ch = (lane & 7) ^ (r & 7);
     asrc[h] = g.a + (int64_t)rr * g.lda + 8 * ch;
   }
@@ -502,18 +514,18 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
     const int kk = min(ks, nk - 1);
     const uint32_t base = lds0 + BUF * STAGE;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) lds_dma16_cached(asrc[h] + kk * kDgBK, base + (2 * wave + h) * 1024);
+    for (int h = 0; h < kDgAI; ++h) lds_dma16_cached(asrc[h] + kk * kDgBK, base + (kDgAI * wave + h) * 1024);
 #pragma unroll
     for (int h = 0; h < BI; ++h) lds_dma16_cached(bsrc[h] + kk * RB, base + kDgAStage + (BI * wave + h) * 1024);
     if constexpr (axk::is_mx(F))
       lds_dma4_cached(ssrc + 4 * (kk >> 1), base + kDgAStage + kDgBN * RB + 256 * wave);
   };
-  constexpr int LPS = 2 + BI + (axk::is_mx(F) ? 1 : 0);  // vector-memory instructions per step
+  constexpr int LPS = kDgAI + BI + (axk::is_mx(F) ? 1 : 0);  // vector-memory instructions per step
   issue(0, std::integral_constant<int, 0>{});
   issue(1, std::integral_constant<int, 1>{});
-  axk_f32x4 acc[4][4];
+  axk_f32x4 acc[kDgMT][4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kDgMT; ++mt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -528,7 +540,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
     const unsigned char* sb = sa + kDgAStage;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
-      axk_bf16x8 af[4], bf[4];
+      axk_bf16x8 af[kDgMT], bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = brow[j] + l16;
@@ -536,12 +548,12 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
         bf[j] = dg_decode<F>(sb + r * RB, kh, g4, r, sc);
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < kDgMT; ++mt) {
         const int r = 16 * mt + l16;
         af[mt] = *reinterpret_cast<const axk_bf16x8*>(sa + r * 128 + 16 * ((4 * kh + g4) ^ (r & 7)));
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < kDgMT; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
     }
@@ -562,7 +574,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(DgArgs g) {
     return v;
   };
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kDgMT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m0 + 16 * mt + 4 * g4 + r;
@@ -622,7 +634,7 @@ int dg_launch(const DgArgs& d, hipStream_t st) {
   }
   constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;
   const int64_t nb = EPI == EPI_PLAIN ? d.cb0[d.count] : ((int64_t)d.n[0] + COLS - 1) / COLS;
-  const int64_t tiles = nb * (((int64_t)d.m + kDgBM - 1) / kDgBM);
+  const int64_t tiles = nb * (((int64_t)d.m + dg_bm<F>() - 1) / dg_bm<F>());
   const int64_t grid = (tiles + kDgXcds - 1) / kDgXcds * kDgXcds;  // whole rounds over the XCDs
   AXK_REQUIRE(grid <= INT32_MAX, AXK_E_SHAPE);
   hipLaunchKernelGGL((mx_gemm_kernel<F, EPI>), dim3((unsigned)grid), dim3(256), dg_lds_bytes<F>(d.k), st, d);
