@@ -446,17 +446,20 @@ struct ScanOps {
   float glast;
 };
 
+// A wave's operand pointers at chunk 0 (operands stored in MFMA fragment order, 16-row x 32-column fragments of 64
+// lanes x 16 bytes: every load instruction reads 1 KiB contiguous); chunk c adds c times the per-chunk stride.
+struct ScanBase {
+  const uint16_t *w, *q, *p, *kt, *u;
+  const float *gam, *dec, *glast;
+};
+
 template <int CPW>
-AXK_DEV void scan_load(ScanOps<CPW>& s, const ScanArgs& p, int b, int bh, int kh, int c, int ct0, int tt, int l16,
-                       int g4, int lane) {
-  const int64_t vidx = (int64_t)bh * p.NC + c;
-  const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;
-  // operands stored in MFMA fragment order (16-row x 32-column fragments, 64 lanes x 16 bytes each): every load
-  // instruction reads 1 KiB contiguous
-  const uint16_t* wg = p.ws.w + vidx * kC * kD + (4 * tt * 64 + lane) * 8;    // fragments (tt, st), st < 4
-  const uint16_t* qg = p.ws.qn + kidx * kC * kD + (4 * tt * 64 + lane) * 8;
-  const uint16_t* pg = p.ws.p + vidx * kC * kC + (2 * tt * 64 + lane) * 8;    // fragments (tt, st), st < 2
-  const uint16_t* ktg = p.ws.kt + kidx * kD * kC + (4 * tt * 64 + lane) * 8;  // fragments (2 tt + i, st), st < 2
+AXK_DEV void scan_load(ScanOps<CPW>& s, const ScanBase& sb, int c) {
+  const int64_t cc = c;
+  const uint16_t* wg = sb.w + cc * (kC * kD);    // fragments (tt, st), st < 4
+  const uint16_t* qg = sb.q + cc * (kC * kD);
+  const uint16_t* pg = sb.p + cc * (kC * kC);    // fragments (tt, st), st < 2
+  const uint16_t* ktg = sb.kt + cc * (kD * kC);  // fragments (2 tt + i, st), st < 2
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
     s.wf[st] = load_bf16x8(wg + st * 512);
@@ -469,14 +472,13 @@ AXK_DEV void scan_load(ScanOps<CPW>& s, const ScanArgs& p, int b, int bh, int kh
     s.kf[1][st] = load_bf16x8(ktg + (2 + st) * 512);
   }
 #pragma unroll
-  for (int j = 0; j < CPW; ++j)
-    s.u[j] = *reinterpret_cast<const uint2*>(p.ws.u + vidx * kC * kD + (((ct0 + j) * 4 + tt) * 64 + lane) * 4);
-  s.gm = *reinterpret_cast<const float4*>(p.ws.gam + vidx * kC + 16 * tt + 4 * g4);
-  s.dc = *reinterpret_cast<const float4*>(p.ws.dec + vidx * kC + 16 * tt + 4 * g4);
+  for (int j = 0; j < CPW; ++j) s.u[j] = *reinterpret_cast<const uint2*>(sb.u + cc * (kC * kD) + j * (4 * 64 * 4));
+  s.gm = *reinterpret_cast<const float4*>(sb.gam + cc * kC);
+  s.dc = *reinterpret_cast<const float4*>(sb.dec + cc * kC);
   // a per-lane load (an index the compiler cannot prove uniform): a scalar load here would be waited for at once
   int z = 0;
   asm volatile("" : "+v"(z));
-  s.glast = p.ws.gam[vidx * kC + kC - 1 + z];
+  s.glast = sb.glast[cc * kC + z];
 }
 
 template <int SW, int NW>
@@ -494,6 +496,19 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
   const int ct_l = (wave >> 2) * CPW;         // first column tile of this wave inside the slice
   const int ct0 = slice * Sh::CT + ct_l;      // ... inside the head (the u layout's column tile)
   const int col0 = 16 * ct0;                  // first state / output column of the wave
+  const int64_t vbase = (int64_t)bh * p.NC, kbase = ((int64_t)b * p.NK + kh) * p.NC;  // chunk 0's indices
+  ScanBase sbase;
+  sbase.w = p.ws.w + vbase * kC * kD + (4 * tt * 64 + lane) * 8;
+  sbase.q = p.ws.qn + kbase * kC * kD + (4 * tt * 64 + lane) * 8;
+  sbase.p = p.ws.p + vbase * kC * kC + (2 * tt * 64 + lane) * 8;
+  sbase.kt = p.ws.kt + kbase * kD * kC + (4 * tt * 64 + lane) * 8;
+  sbase.u = p.ws.u + vbase * kC * kD + ((ct0 * 4 + tt) * 64 + lane) * 4;
+  sbase.gam = p.ws.gam + vbase * kC + 16 * tt + 4 * g4;
+  sbase.dec = p.ws.dec + vbase * kC + 16 * tt + 4 * g4;
+  sbase.glast = p.ws.gam + vbase * kC + kC - 1;
+  // the wave's output column of token row 0; token t at + t * ostride
+  uint16_t* obase = p.out + ((int64_t)b * p.T * p.NV + h) * kD + col0 + l16;
+  const int64_t ostride = (int64_t)p.NV * kD;
 
   // state rows 32 tt + 16 i + 4 g + r, columns col0 + 16 j + l16, in MFMA accumulator tiles
   const float* sin = p.state_in + (int64_t)bh * kD * kD;
@@ -550,12 +565,15 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
       axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + lc * kLdV + 32 * st + 8 * g4), acc);
+      const int t0 = c * kC + 16 * tt + 4 * g4;
+      uint16_t* orow = obase + t0 * ostride + 16 * j;
+      if (c * kC + kC <= p.T) {  // a whole chunk (every one but possibly the last): no per-row test
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = c * kC + 16 * tt + 4 * g4 + r;
-        if (t < p.T)
-          p.out[(((int64_t)b * p.T + t) * p.NV + h) * kD + col0 + 16 * j + l16] =
-              (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
+        for (int r = 0; r < 4; ++r) orow[r * ostride] = (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (t0 + r < p.T) orow[r * ostride] = (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
       }
     }
     // S <- Gamma_last S + k^T (v_new * decay_last)
@@ -582,14 +600,14 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
   // same loads in flight and the waits before each use stay two sets deep.
   const int last = p.NC - 1;
   ScanOps<CPW> o0, o1, o2;
-  scan_load(o0, p, b, bh, kh, 0, ct0, tt, l16, g4, lane);
-  scan_load(o1, p, b, bh, kh, min(1, last), ct0, tt, l16, g4, lane);
+  scan_load(o0, sbase, 0);
+  scan_load(o1, sbase, min(1, last));
   for (int c = 0; c < p.NC; c += 3) {
-    scan_load(o2, p, b, bh, kh, min(c + 2, last), ct0, tt, l16, g4, lane);
+    scan_load(o2, sbase, min(c + 2, last));
     process(o0, c);
-    scan_load(o0, p, b, bh, kh, min(c + 3, last), ct0, tt, l16, g4, lane);
+    scan_load(o0, sbase, min(c + 3, last));
     if (c + 1 < p.NC) process(o1, c + 1);
-    scan_load(o1, p, b, bh, kh, min(c + 4, last), ct0, tt, l16, g4, lane);
+    scan_load(o1, sbase, min(c + 4, last));
     if (c + 2 < p.NC) process(o2, c + 2);
   }
 
