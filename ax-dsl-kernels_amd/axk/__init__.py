@@ -23,11 +23,13 @@ from .attention import (  # noqa: E402
     store_paged_kv,
     paged_decode_fp8,
     store_paged_kv_fp8,
+    paged_decode_i8,
+    store_paged_kv_i8,
     paged_prefill,
 )
 
 __all__ += ["attention", "paged_attention_decode", "paged_decode", "paged_decode_plan", "paged_decode_run", "paged_decode_workspace",
-            "store_paged_kv", "paged_decode_fp8", "store_paged_kv_fp8",
+            "store_paged_kv", "paged_decode_fp8", "store_paged_kv_fp8", "paged_decode_i8", "store_paged_kv_i8",
             "paged_prefill"]
 
 from . import gdn  # noqa: E402

@@ -77,6 +77,8 @@ SIGNATURES: dict[str, list] = {
     "axk_paged_decode_fp8": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
                              ctypes.c_float, _vp, ctypes.c_size_t, _vp],
     "axk_paged_kv_write_fp8": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp],
+    "axk_paged_kv_write_i8": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
+    "axk_paged_decode_i8": [_vp] * 7 + [_i64] * 6 + [ctypes.c_float, _vp, ctypes.c_size_t, _vp],
     "axk_paged_prefill": [_vp] * 7 + [_i64] * 7 + [ctypes.c_float, _vp, _vp],
     "axk_gdn_recurrent": [_vp] * 10 + [_i64] * 6 + [_vp],
     "axk_gdn_chunk_workspace_size": [_i64] * 7,

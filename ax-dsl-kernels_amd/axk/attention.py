@@ -232,6 +232,64 @@ def store_paged_kv_fp8(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor,
     )
 
 
+def paged_decode_i8(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    kv_scales: torch.Tensor,
+    indptr: torch.Tensor,
+    indices: torch.Tensor,
+    last_page_len: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    output: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """paged_decode over an INT8 cache (q35_group.py:44-47, 208-221, KV8=1): kv_cache int8 [P, 2, page, HKV, D],
+    kv_scales bf16 [P, 2, page, HKV]; attention reads bf16(q * s). D 128 or 256, HKV <= 16."""
+    b, hq, hkv, d, page, p = _check_decode(q, kv_cache, indptr, indices, last_page_len, kv_dtype=torch.int8)
+    _check(d in (128, 256) and hkv <= 16, f"head_dim {d} / num_kv_heads {hkv} not supported with an INT8 cache")
+    _check(kv_scales.dtype == torch.bfloat16 and tuple(kv_scales.shape) == (p, 2, page, hkv) and
+           kv_scales.is_contiguous(), "kv_scales must be contiguous bf16 [P, 2, page, HKV]")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(d)
+    if output is None:
+        output = torch.empty_like(q)
+    _check(output.shape == q.shape and output.dtype == q.dtype and output.is_contiguous(), "bad output tensor")
+    if workspace is None:
+        workspace = paged_decode_workspace(b, hq, hkv, d, q.device)
+    _lib.require_device(q, kv_cache, kv_scales, indptr, indices, last_page_len, output, workspace)
+    _lib.call(
+        "axk_paged_decode_i8", q.data_ptr(), kv_cache.data_ptr(), kv_scales.data_ptr(), indptr.data_ptr(),
+        indices.data_ptr(), last_page_len.data_ptr(), output.data_ptr(), b, hq, hkv, d, page, p, float(sm_scale),
+        workspace.data_ptr(), workspace.numel(), _lib.stream_of(q),
+    )
+    return output
+
+
+def store_paged_kv_i8(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor, kv_scales: torch.Tensor,
+                      cache_location: torch.Tensor, status: Optional[torch.Tensor] = None) -> None:
+    """store_paged_kv into an INT8 cache (kv_write_paged with kvs, q35_group.py:250-255): each row and head of k[b]
+    (plane 0) and v[b] (plane 1) quantized as kv_quant_row (197-205) into kv_cache at cache_location[b], its scale
+    into kv_scales."""
+    _check(k.shape == v.shape and k.dim() == 3 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16,
+           "k and v must be bf16 [B, HKV, D]")
+    _check(kv_cache.dtype == torch.int8 and kv_cache.dim() == 5, "kv_cache must be int8 [P, 2, page, HKV, D]")
+    _check(k.is_contiguous() and v.is_contiguous() and kv_cache.is_contiguous() and kv_scales.is_contiguous(),
+           "tensors must be contiguous")
+    b, hkv, d = k.shape
+    p, two, page, hkv2, d2 = kv_cache.shape
+    _check(two == 2 and hkv2 == hkv and d2 == d and d in (128, 256), "kv_cache shape does not match k / v")
+    _check(kv_scales.dtype == torch.bfloat16 and tuple(kv_scales.shape) == (p, 2, page, hkv),
+           "kv_scales must be bf16 [P, 2, page, HKV]")
+    loc = cache_location.reshape(-1, 2) if cache_location.numel() == 2 * b else None
+    _check(loc is not None and cache_location.dtype == torch.int32 and loc.is_contiguous(),
+           "cache_location must be int32 [B, 2] = (page, offset)")
+    _lib.require_device(k, v, kv_cache, kv_scales, loc, status)
+    _lib.call(
+        "axk_paged_kv_write_i8", k.data_ptr(), v.data_ptr(), kv_cache.data_ptr(), kv_scales.data_ptr(),
+        loc.data_ptr(), b, hkv, d, page, p, _lib.ptr(status), _lib.stream_of(k),
+    )
+
+
 def paged_prefill(
     q: torch.Tensor,
     kv_cache: torch.Tensor,

@@ -278,11 +278,15 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
 // KB = 1 (FP8 cache): each landed tile is converted by the four waves (a quarter of its 1 KiB blocks each, scaled by
 // inv_scale, exact for a power-of-two scale) into a bf16 staging tile of the bf16 layout, behind one more barrier;
 // the compute below then reads the staging tile.
-template <int D, int KB>
+// QM = 1 (INT8 cache, KB = 1): each row and KV head carries a bf16 scale in kv_scales [pages, 2, page, hkv]; a
+// tile's scales (16 rows x hkv per plane, contiguous) land with the tile as one dword load per wave (256 dwords: up
+// to 16 KV heads), and the conversion writes bf16(q * s) (q35_group.py kv_page 208-221).
+template <int D, int KB, int QM = 0>
 __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
                                             const unsigned char* __restrict__ cache, const int* __restrict__ indices,
                                             int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                                            float inv_scale, PlanHeader* __restrict__ hdr,
+                                            float inv_scale, const unsigned char* __restrict__ kv_scales,
+                                            PlanHeader* __restrict__ hdr,
                                             float* __restrict__ part_m, float* __restrict__ part_l,
                                             float* __restrict__ part_o, uint16_t* __restrict__ out,
                                             unsigned char* smem) {
@@ -299,6 +303,8 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int64_t row_stride = (int64_t)hkv * D * KB;  // bytes between consecutive tokens
   const int64_t plane_stride = (int64_t)page_size * row_stride;
   const uint32_t lds0 = lds_addr(smem);
+  // QM: the scale ring (kAhead8 + 1 slots of 1 KiB) after the landing ring and the two bf16 staging tiles
+  constexpr int scale_lds = 5 * L::BUF + 2 * C::BUF;
 
   // the item's page ids, 64 at a time: lane j holds page j of the current chunk
   int chunk = 0;
@@ -319,6 +325,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 
   // tile ti -> valid tokens and K base (both wave-uniform: scalar registers); a tile past the sequence end
   // or on a page outside the pool gets nvalid = 0 and an in-bounds base
+  const unsigned char* tile_scales = kv_scales;  // QM: the scales of the tile located last, plane 0
   auto locate = [&](int ti, int& nvalid) -> const unsigned char* {
     const int lp = ti / tpp, tp = ti - lp * tpp;
     if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
@@ -335,8 +342,14 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       page = 0;
       nvalid = 0;
     }
+    if constexpr (QM == 1)
+      tile_scales = kv_scales + ((int64_t)page * 2 * page_size + tp * kTile) * hkv * 2;
     return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * D * KB;
   };
+  // QM: this lane's dword of a tile's scale spans (plane 0 dwords 0 .. 8 hkv - 1, then plane 1; past them dword 0
+  // again, landing in the unused tail of the 1 KiB scale slot)
+  const int sdw = wave * 64 + lane, sspan = 8 * hkv;
+  const int64_t s_off = sdw < 2 * sspan ? (sdw >= sspan ? (int64_t)page_size * hkv * 2 + 4 * (sdw - sspan) : 4 * sdw) : 0;
   // per-lane element offsets of this wave's loads inside a tile (token row, plane, 16-byte chunk), and the
   // same offsets clamped to row 0 for rows past nvalid
   int lane_tok[L::IPW];
@@ -362,6 +375,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
                 lds0 + nb * L::BUF + plane * L::PLANE + blk * L::BLK);
     }
+    if constexpr (QM == 1) lds_dma4_cached(tile_scales + s_off, lds0 + scale_lds + nb * 1024 + wave * 256);
     return ti < ntiles ? nvalid : 0;
   };
 
@@ -438,6 +452,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     // tile ti + kAhead8 into the slot of tile ti - 1, convert tile ti + 1 into the staging tile ti - 1 used, then
     // the math of tile ti.
     constexpr int kAhead8 = 4, kNBuf8 = kAhead8 + 1;
+    constexpr int IPWQ = L::IPW + (QM == 1 ? 1 : 0);  // this wave's loads of a tile
     unsigned char* stage = smem + kNBuf8 * L::BUF;
     auto convert = [&](int slot, unsigned char* dst_tile) {
       // wave w converts 1 KiB blocks c = w, w + 4, ...: lane l's 16 stored bytes of row blk RPI + l / (RB / 16)
@@ -448,6 +463,26 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
         const axk_u32x4 f8 =
             *reinterpret_cast<const axk_u32x4*>(smem + slot * L::BUF + plane * L::PLANE + blk * L::BLK + 16 * lane);
         axk_u32x4 lo, hi;
+        if constexpr (QM == 1) {  // int8 codes of row `row`: bf16(q * s), s its row's scale for this KV head
+          const uint16_t sbits = *reinterpret_cast<const uint16_t*>(smem + scale_lds + slot * 1024 +
+                                                                    plane * 32 * hkv + (row * hkv + kvh) * 2);
+          const float sc = bf16_bits_to_f32(sbits), off = -128.0f * sc;
+          // q = (byte ^ 0x80) - 128 through the unsigned byte conversion; (u - 128) s = fma(u, s, -128 s) is exact
+          // (q s has at most 16 significant bits), so the bf16 rounding below sees fp32(q s)
+          uint32_t o16[8];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t u = f8[w] ^ 0x80808080u;
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb) {
+              const float x0 = __builtin_fmaf((float)((u >> (16 * hb)) & 0xffu), sc, off);
+              const float x1 = __builtin_fmaf((float)((u >> (16 * hb + 8)) & 0xffu), sc, off);
+              o16[2 * w + hb] = f32_to_bf16_bits(x0) | (f32_to_bf16_bits(x1) << 16);
+            }
+          }
+          lo = axk_u32x4{o16[0], o16[1], o16[2], o16[3]};
+          hi = axk_u32x4{o16[4], o16[5], o16[6], o16[7]};
+        } else {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           const uint32_t b0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(f8[w], inv_scale, false));
@@ -460,6 +495,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
             hi[2 * w - 3] = b1;
           }
         }
+        }
         unsigned char* dst = dst_tile + plane * C::PLANE + C::row_off(row) + 2 * col;
         *reinterpret_cast<axk_u32x4*>(dst) = lo;
         *reinterpret_cast<axk_u32x4*>(dst + 16) = hi;
@@ -468,11 +504,11 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     int nv[kAhead8];  // valid tokens of tiles ti .. ti + kAhead8 - 1 (nv[j]: tile ti + j)
 #pragma unroll
     for (int j = 0; j < kAhead8; ++j) nv[j] = issue(j, j);
-    wait_vmcnt<(kAhead8 - 1) * L::IPW>();  // tile 0 has landed
+    wait_vmcnt<(kAhead8 - 1) * IPWQ>();  // tile 0 has landed
     __syncthreads();
     if (nv[0] > 0) convert(0, stage);
     for (int ti = 0; ti < ntiles; ++ti) {
-      wait_vmcnt<(kAhead8 - 2) * L::IPW>();  // tile ti + 1 has landed (later ones may not)
+      wait_vmcnt<(kAhead8 - 2) * IPWQ>();  // tile ti + 1 has landed (later ones may not)
       __syncthreads();  // a fence with the barrier: LDS written by other waves is read after it
       const int nvn = issue(ti + kAhead8, (ti + kAhead8) % kNBuf8);  // into the slot of tile ti - 1 (converted)
       if (nv[1] > 0) convert((ti + 1) % kNBuf8, stage + ((ti + 1) & 1) * C::BUF);
@@ -514,11 +550,12 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 // Persistent split kernel: a few workgroups per CU; workgroup w takes items w, w + gridDim.x, ... (the plan
 // sizes the items to about one per workgroup). With local != 0 the descriptors come from the page table
 // directly (local_plan), otherwise from the plan in the workspace.
-template <int D, int KB>
+template <int D, int KB, int QM = 0>
 __global__ __launch_bounds__(256) void paged_decode_kernel(
     const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ indptr,
     const int* __restrict__ last_page_len, const int* __restrict__ indices, int batch, int hq, int hkv,
-    int page_size, int64_t num_pages, float sm_scale, float inv_scale, int local, int bias,
+    int page_size, int64_t num_pages, float sm_scale, float inv_scale, const unsigned char* __restrict__ kv_scales,
+    int local, int bias,
     PlanHeader* __restrict__ hdr, const ItemDesc* __restrict__ descs, float* __restrict__ part_m,
     float* __restrict__ part_l, float* __restrict__ part_o, uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -526,7 +563,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     const LocalPlan lp = local_plan(indptr, last_page_len, bias, batch, hkv, gridDim.x);
     for (int it = blockIdx.x; it < lp.n_items; it += gridDim.x) {
       const ItemDesc desc = local_item(lp, it, batch, page_size);
-      decode_item<D, KB>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale, hdr,
+      decode_item<D, KB, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
+                             kv_scales, hdr,
                          part_m, part_l, part_o, out, smem);
       __syncthreads();  // LDS is reused by the next item
     }
@@ -539,7 +577,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
   if (h.batch != batch || h.hkv != hkv) return;
   for (int it = blockIdx.x; it < h.n_items; it += gridDim.x) {
     if (it != (int)blockIdx.x) desc = descs[it];
-    decode_item<D, KB>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale, hdr,
+    decode_item<D, KB, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
+                           kv_scales, hdr,
                        part_m, part_l, part_o, out, smem);
     __syncthreads();
   }
@@ -1581,28 +1620,30 @@ int launch_split_sk(const uint16_t* q, const void* cache, const int* indptr, con
   return axk_launch_status();
 }
 
-template <int D, int KB = 2>
+template <int D, int KB = 2, int QM = 0>
 int launch_split(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
                  uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                 void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0) {
+                 void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr) {
   if (use_sk(batch, KB))
     return launch_split_sk<D>(q, cache, indptr, last, indices, out, batch, hq, hkv, page_size, num_pages, sm_scale,
                               bias, ws, st);
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
   // the ring of landed tiles; an FP8 cache: a ring of 5 landing slots (kNBuf8) and two bf16 staging tiles
-  const size_t lds = KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF : (size_t)kNBuf * PagedCfg<D>::BUF;
+  const size_t lds = KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF + (QM == 1 ? 5 * 1024 : 0)
+                              : (size_t)kNBuf * PagedCfg<D>::BUF;
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, KB>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, KB, QM>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
       return AXK_E_LAUNCH;
     lds_raised = true;
   }
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
-  hipLaunchKernelGGL((paged_decode_kernel<D, KB>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves), lds,
-                     st, q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv, page_size,
-                     num_pages, sm_scale, inv_scale, local, bias, v.hdr, v.descs, v.pm, v.pl, v.po, out);
+  hipLaunchKernelGGL((paged_decode_kernel<D, KB, QM>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves),
+                     lds, st, q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv,
+                     page_size, num_pages, sm_scale, inv_scale, static_cast<const unsigned char*>(kv_scales), local,
+                     bias, v.hdr, v.descs, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
 
@@ -1867,6 +1908,73 @@ extern "C" int axk_paged_kv_write(const uint16_t* k, const uint16_t* v, uint16_t
   return axk_launch_status();
 }
 
+namespace {
+// The INT8 cache's KV write (q35_group.py kv_quant_row 197-205, kv_write_paged 250-255, KV8=1): per row and KV head
+// s = bf16(max(amax, bf16(1e-5)) * bf16(1 / 127)), codes int8(bf16(x * bf16(1 / s))) rounded to nearest even and
+// saturated, into cache[page, plane, slot, kvh, :]; s into scales[page, plane, slot, kvh]. Sixteen lanes per
+// (token, plane, KV head) row, D / 16 values each; the row's amax by shuffles within the 16 lanes.
+template <int D>
+__global__ __launch_bounds__(256) void paged_kv_write_i8_kernel(const uint16_t* __restrict__ k,
+                                                                const uint16_t* __restrict__ v,
+                                                                unsigned char* __restrict__ cache,
+                                                                uint16_t* __restrict__ scales,
+                                                                const int* __restrict__ loc, int batch, int hkv,
+                                                                int page_size, int64_t num_pages,
+                                                                int* __restrict__ status) {
+  constexpr int E = D / 16;  // values per lane (8 or 16)
+  const int64_t rows = (int64_t)batch * 2 * hkv;
+  const int sub = threadIdx.x & 15;
+  for (int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4; row < rows;
+       row += ((int64_t)gridDim.x * blockDim.x) >> 4) {
+    const int b = (int)(row / (2 * hkv)), rem = (int)(row - (int64_t)b * 2 * hkv);
+    const int plane = rem / hkv, kvh = rem - plane * hkv;
+    const int page = loc[2 * b], off = loc[2 * b + 1];
+    const bool bad = page < 0 || page >= num_pages || off < 0 || off >= page_size;  // uniform over the 16 lanes
+    if (bad) {
+      if (status && sub == 0) *status = 1;
+      continue;
+    }
+    const uint16_t* src = (plane ? v : k) + ((int64_t)b * hkv + kvh) * D + sub * E;
+    float x[E];
+#pragma unroll
+    for (int u = 0; u < E / 8; ++u) {
+      const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * u);
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[8 * u + e] = __uint_as_float(e & 1 ? (ww[e >> 1] & 0xffff0000u) : (ww[e >> 1] << 16));
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(x[e]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+    const float kFloor = __uint_as_float(0x3728u << 16);    // bf16(1e-5)
+    const float kInv127 = __uint_as_float(0x3c01u << 16);   // bf16(1 / 127)
+    const float s = round_bf16(fmaxf(amax, kFloor) * kInv127);
+    const float r = round_bf16(1.0f / s);
+    uint32_t codes[E / 4];
+#pragma unroll
+    for (int c4 = 0; c4 < E / 4; ++c4) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = fminf(fmaxf(rintf(round_bf16(x[4 * c4 + e] * r)), -128.0f), 127.0f);
+        word |= ((uint32_t)(int)y & 0xffu) << (8 * e);
+      }
+      codes[c4] = word;
+    }
+    const int64_t crow = ((int64_t)page * 2 + plane) * page_size + off;
+    unsigned char* dst = cache + (crow * hkv + kvh) * D + sub * E;
+    if constexpr (E == 16)
+      *reinterpret_cast<uint4*>(dst) = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+    else
+      *reinterpret_cast<uint2*>(dst) = make_uint2(codes[0], codes[1]);
+    if (sub == 0) scales[crow * hkv + kvh] = (uint16_t)f32_to_bf16_bits(s);
+  }
+}
+
+}  // namespace
+
 // ---- FP8 KV cache (E4M3 with one static power-of-two scale: the stored value is e4m3(bf16(x * kv_scale)), the
 // attended value stored / kv_scale, exact in bf16). q35_group.py:44-54, 244-247 (KV8=2).
 namespace {
@@ -1923,6 +2031,63 @@ extern "C" int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint
   hipLaunchKernelGGL(paged_kv_write_fp8_kernel, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v, kv_cache,
                      cache_location, (int)batch, (int)num_kv_heads, (int)head_dim, (int)page_size, num_pages, kv_scale,
                      status);
+  return axk_launch_status();
+}
+
+// ---- INT8 KV cache with a bf16 scale per row and KV head (q35_group.py:44-47, 197-221, 250-255, KV8=1) ----
+extern "C" int axk_paged_decode_i8(const uint16_t* q, const int8_t* kv_cache, const uint16_t* kv_scales,
+                                   const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                                   uint16_t* out, int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                                   int64_t head_dim, int64_t page_size, int64_t num_pages, float sm_scale,
+                                   void* workspace, size_t workspace_bytes, axk_stream_t stream) {
+  AXK_REQUIRE(q && kv_cache && kv_scales && indptr && indices && last_page_len && out, AXK_E_NULL);
+  int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
+  if (rc != AXK_OK) return rc;
+  AXK_REQUIRE(head_dim == 128 || head_dim == 256, AXK_E_SHAPE);  // whole 1 KiB load blocks split over the waves
+  AXK_REQUIRE(num_kv_heads <= 16, AXK_E_SHAPE);  // a tile's scales: one dword load per wave
+  AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16) && axk_aligned(kv_scales, 4), AXK_E_ALIGN);
+  const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
+  AXK_REQUIRE(workspace && workspace_bytes >= need && axk_aligned(workspace, 256), AXK_E_WORKSPACE);
+  const size_t qbytes = (size_t)batch * num_qo_heads * head_dim * 2;
+  AXK_REQUIRE(!axk_overlap(out, qbytes, q, qbytes), AXK_E_ALIAS);
+  AXK_REQUIRE(!axk_overlap(out, qbytes, workspace, workspace_bytes), AXK_E_ALIAS);
+  hipStream_t st = axk_stream(stream);
+  rc = decode_plan(indptr, last_page_len, batch, num_qo_heads, num_kv_heads, head_dim, page_size, 1, 0, workspace,
+                   workspace_bytes, st);
+  if (rc != AXK_OK) return rc;
+  const int B = (int)batch, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
+  rc = head_dim == 128 ? launch_split<128, 1, 1>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS,
+                                                 num_pages, sm_scale, workspace, st, 1.0f, 0, kv_scales)
+                       : launch_split<256, 1, 1>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS,
+                                                 num_pages, sm_scale, workspace, st, 1.0f, 0, kv_scales);
+  if (rc != AXK_OK) return rc;
+  return decode_merge(indptr, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim, page_size, 1, 0,
+                      workspace, st);
+}
+
+extern "C" int axk_paged_kv_write_i8(const uint16_t* k, const uint16_t* v, int8_t* kv_cache, uint16_t* kv_scales,
+                                     const int32_t* cache_location, int64_t batch, int64_t num_kv_heads,
+                                     int64_t head_dim, int64_t page_size, int64_t num_pages, int32_t* status,
+                                     axk_stream_t stream) {
+  AXK_REQUIRE(k && v && kv_cache && kv_scales && cache_location, AXK_E_NULL);
+  AXK_REQUIRE(batch >= 0 && num_kv_heads > 0 && (head_dim == 128 || head_dim == 256), AXK_E_SHAPE);
+  AXK_REQUIRE(page_size > 0 && num_pages > 0, AXK_E_SHAPE);
+  AXK_REQUIRE(axk_aligned(k, 16) && axk_aligned(v, 16) && axk_aligned(kv_cache, 16) && axk_aligned(kv_scales, 2),
+              AXK_E_ALIGN);
+  if (batch == 0) return AXK_OK;
+  const int64_t threads = 2 * batch * num_kv_heads * 16;
+  int64_t grid = (threads + 255) / 256;
+  if (grid > 4096) grid = 4096;
+  auto* c8 = reinterpret_cast<unsigned char*>(kv_cache);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(paged_kv_write_i8_kernel<128>, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v,
+                       c8, kv_scales, cache_location, (int)batch, (int)num_kv_heads, (int)page_size, num_pages,
+                       status);
+  else
+    hipLaunchKernelGGL(paged_kv_write_i8_kernel<256>, dim3((unsigned)grid), dim3(256), 0, axk_stream(stream), k, v,
+                       c8, kv_scales, cache_location, (int)batch, (int)num_kv_heads, (int)page_size, num_pages,
+                       status);
   return axk_launch_status();
 }
 

@@ -286,6 +286,22 @@ int axk_paged_kv_write_fp8(const uint16_t* k, const uint16_t* v, uint8_t* kv_cac
                            int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
                            int64_t num_pages, float kv_scale, int32_t* status, axk_stream_t stream);
 
+/* INT8 paged KV cache with a bf16 scale per row and KV head (models/qwen38_27b/decode/q35_group.py:44-47, KV8=1):
+ * kv_cache int8 [num_pages, 2, page_size, num_kv_heads, head_dim] and kv_scales bf16 [num_pages, 2, page_size,
+ * num_kv_heads], the layout of the reference's kv<j> / kvs<j> inputs. The write quantizes each row and head as
+ * kv_quant_row does (q35_group.py:197-205): s = bf16(max(amax, bf16(1e-5)) * bf16(1 / 127)), codes
+ * int8(bf16(x * bf16(1 / s))) rounded to nearest even and saturated; decode reads bf16(q * s) (kv_page, 208-221).
+ * Arguments otherwise as axk_paged_kv_write / axk_paged_decode; head_dim 128 or 256; decode takes num_kv_heads <= 16
+ * and 4-byte aligned scales. */
+int axk_paged_kv_write_i8(const uint16_t* k, const uint16_t* v, int8_t* kv_cache, uint16_t* kv_scales,
+                          const int32_t* cache_location, int64_t batch, int64_t num_kv_heads, int64_t head_dim,
+                          int64_t page_size, int64_t num_pages, int32_t* status, axk_stream_t stream);
+int axk_paged_decode_i8(const uint16_t* q, const int8_t* kv_cache, const uint16_t* kv_scales, const int32_t* indptr,
+                        const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,
+                        int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                        int64_t num_pages, float sm_scale, void* workspace, size_t workspace_bytes,
+                        axk_stream_t stream);
+
 /* Prefill / speculative-verify attention over the paged cache, causal (the history pages and the current block of
  * sgl_kernel_axera/attention/flash_attn.py:471-611 paged_flash_attention, flash_attn.py:1044 flash_attn_with_kvcache;
  * the G x P-row block attention of models/qwen35_35b_a3b/src/70b0fbc/q35_prefill.py:264-336). Sequence b's new tokens

@@ -7,10 +7,14 @@ Restates
   * the page-table semantics of sgl_kernel_axera/attention/flash_attn.py:1478-1495 (physical page =
     indices[indptr[b] + logical page]) and the tail mask of 87-104 (tokens past the valid length of the
     last page are excluded);
-  * store_paged_kv of flash_attn.py:53-84 (row = (page * 2 + plane) * page_size + offset).
+  * store_paged_kv of flash_attn.py:53-84 (row = (page * 2 + plane) * page_size + offset);
+  * the 8-bit caches of models/qwen38_27b/decode/q35_group.py: FP8 with a static scale (KV8=2, 244-247) and INT8
+    with a bf16 scale per row and head (KV8=1: kv_quant_row 197-205, kv_page 208-221, kv_write_paged 250-255).
 Pinned by tests/test_oracle_paged.py: torch SDPA (enable_gqa=True, the reference's golden call) on the
 same gathered rows, a brute-force per-token index computation of the gather, invariance under a
-consistent permutation of the page pool, and the one-page case against dense attention.
+consistent permutation of the page pool, and the one-page case against dense attention; the INT8 quantizer by its
+error bound (|x - bf16(q s)| <= s / 2 plus the bf16 roundings), the row maximum on +-127 (126 or 128 clipped only by
+the bf16 rounding of s and 1 / s), the 1e-5 floor for zero rows, and exactness where x is already a multiple of s.
 """
 from __future__ import annotations
 
@@ -110,3 +114,39 @@ def dequant_kv_fp8(codes: torch.Tensor, kv_scale: float) -> torch.Tensor:
     """The values attention reads from an FP8 cache: stored / kv_scale (q35_group.py:48-51: K through a constant
     E8M0 scale of 1 / KV8_SCALE, V with the probabilities carrying it), exact in bf16 for a power-of-two scale."""
     return (codes.view(torch.float8_e4m3fn).float() / kv_scale).to(torch.bfloat16)
+
+
+# ---- INT8 cache with a bf16 scale per row and KV head (models/qwen38_27b/decode/q35_group.py:44-47, KV8=1) ----
+_BF16_1E5 = float(torch.tensor(1e-5).to(torch.bfloat16))        # the floor of amax, a bf16 constant
+_BF16_INV127 = float(torch.tensor(1.0 / 127).to(torch.bfloat16))  # bf16(1 / 127)
+
+
+def quant_kv_i8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """kv_quant_row (q35_group.py:197-205) for rows x bf16 [..., D]: amax = max(max |x|, bf16(1e-5)); s = bf16(amax *
+    bf16(1 / 127)); codes = int8(bf16(x * bf16(1 / s))). Each product in fp32 then rounded to bf16 (the DSL's bf16
+    outputs); the int8 cast rounds to nearest even and saturates (the AX cast's rounding of ties and its saturation are
+    not stated in the reference: parity unpinned there). Returns (codes int8 [..., D], s bf16 [...])."""
+    xf = x.float()
+    amax = torch.clamp(xf.abs().amax(dim=-1), min=_BF16_1E5)
+    s = (amax * _BF16_INV127).to(torch.bfloat16)
+    r = (1.0 / s.float()).to(torch.bfloat16)
+    y = (xf * r.float()[..., None]).to(torch.bfloat16).float()
+    codes = torch.clamp(torch.round(y), -128, 127).to(torch.int8)
+    return codes, s
+
+
+def dequant_kv_i8(codes: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """kv_page's dequantization (q35_group.py:218-220): bf16(q * s) per row and head."""
+    return (codes.float() * s.float()[..., None]).to(torch.bfloat16)
+
+
+def store_paged_kv_i8(cache: torch.Tensor, scales: torch.Tensor, k: torch.Tensor, v: torch.Tensor, loc):
+    """kv_write_paged with kvs (q35_group.py:250-255): rows of k / v [B, HKV, D] quantized into cache int8
+    [P, 2, page, HKV, D] and scales bf16 [P, 2, page, HKV] at loc [B, 2] = (page, slot). Returns new tensors."""
+    cache, scales = cache.clone(), scales.clone()
+    for plane, x in ((0, k), (1, v)):
+        codes, s = quant_kv_i8(x)
+        for b, (pg, off) in enumerate(np.asarray(loc).reshape(-1, 2).tolist()):
+            cache[pg, plane, off] = codes[b]
+            scales[pg, plane, off] = s[b]
+    return cache, scales

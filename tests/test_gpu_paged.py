@@ -297,3 +297,83 @@ def test_paged_attention_decode_sgl_convention_matches_paged_decode(dev):
         ref = pa.paged_decode(c["q"], ref_cache, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
         torch.testing.assert_close(got.float(), ref.to(torch.bfloat16).float(), **TOL)
         assert torch.equal(cache.cpu().view(torch.int16), ref_cache.view(torch.int16))
+
+
+# ---- INT8 KV cache with a bf16 scale per row and KV head (q35_group.py:44-47, 197-221, 250-255; KV8=1) ----
+def _i8_case(c):
+    """c's cache quantized the reference's way (codes, scales), and the bf16 values attention reads from it."""
+    codes, scales = pa.quant_kv_i8(c["cache"])
+    return codes, scales, pa.dequant_kv_i8(codes, scales)
+
+
+@pytest.mark.parametrize(
+    "lens,hq,hkv,d,page",
+    [
+        ([1, 100, 1000], 16, 2, 256, 64),
+        ([500, 7, 129], 4, 4, 128, 64),
+        ([64, 0, 65], 8, 1, 256, 64),  # an empty sequence yields zeros
+        ([300, 2000], 16, 1, 128, 256),
+        ([40, 900], 16, 16, 128, 16),  # 16 KV heads: a tile's scales fill every lane of the four waves
+        ([(37 * i) % 700 for i in range(70)], 24, 8, 128, 32),  # the plan kernel's partition, 8 KV heads
+    ],
+)
+def test_paged_decode_i8(dev, lens, hq, hkv, d, page):
+    g = torch.Generator().manual_seed(sum(lens) + hq + d + hkv)
+    c = configs.paged_case(lens, hq, hkv, d, page, g)
+    print(f"i8 decode lens={lens[:4]} hq={hq} hkv={hkv} d={d} page={page}", flush=True)
+    codes, scales, deq = _i8_case(c)
+    got = axk.paged_decode_i8(c["q"].to(dev), codes.to(dev), scales.to(dev), c["indptr"].to(dev),
+                              c["indices"].to(dev), c["last_page_len"].to(dev), sm_scale=c["scale"]).cpu()
+    ref = pa.paged_decode(c["q"], deq, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not got[b].any()
+
+
+def test_paged_decode_i8_config1(dev):
+    c = configs.config1()
+    codes, scales, deq = _i8_case(c)
+    got = axk.paged_decode_i8(c["q"].to(dev), codes.to(dev), scales.to(dev), c["indptr"].to(dev),
+                              c["indices"].to(dev), c["last_page_len"].to(dev), sm_scale=c["scale"]).cpu()
+    ref = pa.paged_decode(c["q"], deq, c["indptr"], c["indices"], c["last_page_len"], c["scale"])
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)
+
+
+@pytest.mark.parametrize("d,hkv", [(128, 2), (256, 4)])
+def test_kv_write_i8_bytes(dev, d, hkv):
+    """The written codes and scales equal the reference quantization bit for bit (incl. a zero row, an outlier and
+    rows of mixed magnitude); every other cache and scale byte untouched."""
+    g = torch.Generator().manual_seed(7 + d)
+    b, page, pages = 6, 32, 9
+    k = (torch.randn(b, hkv, d, generator=g) * 4).bfloat16()
+    v = (torch.randn(b, hkv, d, generator=g) * torch.logspace(-3, 2, d)).bfloat16()
+    k[1, 0] = 0
+    k[2, hkv - 1, 5] = 1000.0
+    cache = torch.randint(-128, 128, (pages, 2, page, hkv, d), generator=g, dtype=torch.int8)
+    scales = torch.randn(pages, 2, page, hkv, generator=g).bfloat16()
+    loc = torch.tensor([[1, 0], [1, 31], [4, 7], [0, 0], [8, 16], [5, 3]], dtype=torch.int32)
+    gc, gs = cache.to(dev), scales.to(dev)
+    axk.store_paged_kv_i8(k.to(dev), v.to(dev), gc, gs, loc.to(dev))
+    rc, rs = pa.store_paged_kv_i8(cache, scales, k, v, loc)
+    assert torch.equal(gc.cpu(), rc)
+    assert torch.equal(gs.cpu().view(torch.int16), rs.view(torch.int16))
+
+
+def test_kv_write_then_decode_i8(dev):
+    """Write the new token of every sequence through axk, then decode over the INT8 cache: equal to the oracle's
+    write + decode (the bf16 cache's append case, quantized)."""
+    g = torch.Generator().manual_seed(12)
+    hq, hkv, d, page = 8, 2, 128, 64
+    c = configs.append_token_case([100, 63, 300], hq, hkv, d, page, g)
+    codes, scales = pa.quant_kv_i8(c["cache"])
+    k = torch.randn(3, hkv, d, generator=g).bfloat16()
+    v = torch.randn(3, hkv, d, generator=g).bfloat16()
+    q = torch.randn(3, hq, d, generator=g).bfloat16()
+    gc, gs = codes.to(dev), scales.to(dev)
+    axk.store_paged_kv_i8(k.to(dev), v.to(dev), gc, gs, c["loc"].to(dev))
+    got = axk.paged_decode_i8(q.to(dev), gc, gs, c["indptr"].to(dev), c["indices"].to(dev),
+                              c["last_page_len"].to(dev)).cpu()
+    rc, rs = pa.store_paged_kv_i8(codes, scales, k, v, c["loc"])
+    ref = pa.paged_decode(q, pa.dequant_kv_i8(rc, rs), c["indptr"], c["indices"], c["last_page_len"], d ** -0.5)
+    torch.testing.assert_close(got.float(), ref.float(), **TOL)

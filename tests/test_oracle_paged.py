@@ -169,3 +169,42 @@ def test_prefill_empty_and_short_cache():
     assert got.shape == (10, 8, 64)
     assert not got[4:7].any()  # sequence 2: qlen 6 > 3 cached tokens, its first 3 rows see nothing
     assert got[7:].abs().sum() > 0
+
+
+# ---- the INT8 cache's quantizer (kv_quant_row, q35_group.py:197-205; KV8=1) ----
+def test_int8_quantizer_error_bound_and_scale():
+    """|x - bf16(q s)| stays within s / 2 plus the bf16 roundings of 1 / s, x / s and q s; s tracks
+    amax / 127 to the two bf16 roundings (a 1 / 128 divisor or a truncating cast fails one of these); the row
+    maximum lands on 127 in magnitude up to those roundings (126, or -128 on the negative side)."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(64, 8, 128, generator=g) * torch.logspace(-3, 2, 64)[:, None, None]
+    x[5, 2, 17] = 400.0  # an outlier row
+    x = x.bfloat16()
+    q, s = pa.quant_kv_i8(x)
+    deq = pa.dequant_kv_i8(q, s).float()
+    sf = s.float()[..., None]
+    err = (x.float() - deq).abs()
+    # x / s carries the roundings of 1 / s and of the product (2^-8 relative each) into the code; bf16(q s) adds one
+    assert (err <= 0.5 * sf + x.float().abs() * 3 * 2.0 ** -8 + 1e-12).all(), float((err - 0.5 * sf).max())
+    amax = x.float().abs().amax(-1)
+    assert ((s.float() * 127 - amax).abs() <= amax * 2.0 ** -8 * 1.5).all()
+    top = q.int().abs().amax(-1)  # -128 is reachable: bf16(-amax * bf16(1 / s)) can round to -128
+    assert ((top >= 126) & (top <= 128)).all()
+    assert q.dtype == torch.int8 and s.dtype == torch.bfloat16
+
+
+def test_int8_quantizer_zero_rows_and_rounding_to_nearest():
+    """A zero row keeps the 1e-5 floor (codes 0, s = bf16(bf16(1e-5) / 127)); codes round to nearest (not toward
+    zero): x = (k + 0.4) s gives k, x = (k + 0.6) s gives k + 1 away from the row maximum."""
+    z = torch.zeros(1, 128).bfloat16()
+    q, s = pa.quant_kv_i8(z)
+    assert not q.any()
+    assert float(s) == float((torch.tensor(1e-5).bfloat16().float() * torch.tensor(1 / 127).bfloat16().float())
+                              .bfloat16())
+    # a row whose max is exactly 127 s (s a power of two: every product exact)
+    s0 = 2.0 ** -4
+    vals = torch.tensor([127.0, 10.4, 10.6, -20.4, -20.6, 0.4, 0.6, -3.0]) * s0
+    row = torch.zeros(1, 128)
+    row[0, :8] = vals
+    q, s = pa.quant_kv_i8(row.bfloat16())
+    assert q[0, :8].tolist() == [127, 10, 11, -20, -21, 0, 1, -3]
