@@ -390,6 +390,67 @@ class PagedDecodeFp8Workload(Workload):
                           f"median of {reps} runs"}
 
 
+class PagedDecodeI8Workload(PagedDecodeFp8Workload):
+    """Config 1's attention over an INT8 cache (SURVEY next row: KV8 = 1, q35_group.py:44-47, 197-221): the same
+    sequences, pages and queries, each row and KV head stored as int8 codes with a bf16 scale. One step =
+    axk_paged_decode_i8 (plan + split + merge); algorithmic bytes: the codes and scales of every valid token + q + out
+    + page table."""
+
+    name = "paged_decode_i8kv"
+    kernel = "paged_decode_kernel<256, 1, 1> (+ merge)"
+    traffic_profile = "paged_decode_i8kv_config1_pmc.txt"  # every kernel of the op, summed
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import attention, configs
+        from oracle import paged_attn
+
+        c = configs.config1()
+        self.host = c
+        tot = sum(c["lens"])
+        b, hq, d = c["q"].shape
+        pool, _, page, hkv, _ = c["cache"].shape
+        npages = int(c["indptr"][-1])
+        self.alg_bytes = tot * 2 * hkv * (d + 2) + 2 * b * hq * d * 2 + 4 * (npages + 2 * b + 1)
+        self.alg_flops = 4 * tot * hq * d
+        codes, scales = paged_attn.quant_kv_i8(c["cache"])
+        codes, scales = codes.to(dev), scales.to(dev)
+        self.copies = max(2, -(-ROTATE_BYTES // codes.numel()))
+        self.caches = [(codes, scales)] + [(codes.clone(), scales.clone()) for _ in range(self.copies - 1)]
+        self.q = c["q"].to(dev)
+        self.indptr, self.indices, self.last = (c[k].to(dev) for k in ("indptr", "indices", "last_page_len"))
+        self.out = torch.empty_like(self.q)
+        self.ws = attention.paged_decode_workspace(b, hq, hkv, d, dev)
+        self.scale = c["scale"]
+        self.config = {"workload": "config1 over an INT8 KV cache (bf16 scale per row and KV head): B=16 HQ=16 HKV=2 "
+                                   "D=256 page=64", "sum_context": tot, "rotating_copies": self.copies}
+        self.dtype = "int8 KV + bf16 row scales -> bf16 (fp32 softmax / accumulation)"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        codes, scales = self.caches[i % self.copies]
+        axk.paged_decode_i8(self.q, codes, scales, self.indptr, self.indices, self.last, sm_scale=self.scale,
+                            output=self.out, workspace=self.ws)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import paged_attn
+
+        c = self.host
+        deq = paged_attn.dequant_kv_i8(*paged_attn.quant_kv_i8(c["cache"]))
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: paged_attn.paged_decode(c["q"], deq, c["indptr"], c["indices"],
+                                                              c["last_page_len"], c["scale"]), budget_s=10.0,
+                              min_reps=2, max_reps=10)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"full config1 op on the dequantised INT8 cache (oracle/paged_attn.py, torch fp32 CPU), "
+                          f"median of {reps} runs"}
+
+
 class PagedPrefillWorkload(Workload):
     """Prefill attention (SURVEY next row: G x P-row causal block attention, q35_prefill.py:264-336; flash_attn.py:
     471-611): one sequence's 4096-token chunk over an empty history in the paged cache, config 1's attention shape
@@ -1075,7 +1136,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
-             LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload,
+             LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload, PagedDecodeI8Workload.name: PagedDecodeI8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
              MxLinearPrefillWorkload.name: MxLinearPrefillWorkload, MoeLayerPrefillWorkload.name: MoeLayerPrefillWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
