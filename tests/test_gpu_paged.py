@@ -235,6 +235,71 @@ def test_paged_decode_stream_k_partition(dev, lens, hq, hkv, d, page):
             assert not got[b].any()
 
 
+def test_stream_k_garbage_workspace_and_changing_partitions(dev):
+    """The stream-K split and merge keep nothing in the workspace from one call to the next: a workspace of random
+    bytes, then calls whose partitions differ (other lengths, so other pieces per pair) on that same workspace, each
+    against the oracle and bit-identical to the same call on a fresh zeroed workspace."""
+    g = torch.Generator().manual_seed(77)
+    ws = attention.paged_decode_workspace(6, 16, 2, 256, dev)
+    ws.copy_(torch.randint(0, 256, ws.shape, generator=g, dtype=torch.uint8).to(dev))
+    for trial, lens in enumerate([[3000, 17, 900, 4100, 64, 2500], [5, 9000, 1, 0, 700, 300],
+                                  [3000, 17, 900, 4100, 64, 2500]]):
+        c = configs.paged_case(lens, 16, 2, 256, 64, g)
+        print(f"trial {trial} lens={lens}", flush=True)
+        got = _run(c, dev, workspace=ws)
+        fresh = _run(c, dev, workspace=torch.zeros_like(ws))
+        assert torch.equal(got.view(torch.int16), fresh.view(torch.int16))
+        torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
+
+
+def test_stream_k_graph_replays_with_new_page_tables(dev):
+    """A captured decode (split + merge) replayed with the page table rewritten in place between replays (lengths
+    change, so the partition the kernels derive changes): every replay equals the eager call, with eager calls on the
+    same workspace in between."""
+    g = torch.Generator().manual_seed(78)
+    bsz, hq, hkv, d, page = 5, 16, 2, 256, 64
+    pool = 400
+    cache = (torch.randn(pool, 2, page, hkv, d, generator=g) * 0.5).bfloat16().to(dev)
+    q = torch.randn(bsz, hq, d, generator=g).bfloat16().to(dev)
+    ws = attention.paged_decode_workspace(bsz, hq, hkv, d, dev)
+    indptr = torch.zeros(bsz + 1, dtype=torch.int32, device=dev)
+    indices = torch.zeros(pool, dtype=torch.int32, device=dev)
+    last = torch.ones(bsz, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+
+    def set_table(lens):
+        npg = [(L + page - 1) // page for L in lens]
+        ptr = torch.tensor([0] + torch.tensor(npg).cumsum(0).tolist(), dtype=torch.int32)
+        perm = torch.randperm(pool, generator=g)[: int(ptr[-1])].to(torch.int32)
+        indptr.copy_(ptr.to(dev))
+        indices[: len(perm)].copy_(perm.to(dev))
+        last.copy_(torch.tensor([L - (n - 1) * page for L, n in zip(lens, npg)], dtype=torch.int32).to(dev))
+
+    tables = [[4000, 130, 6000, 64, 2000], [64, 64, 9000, 3000, 128], [7000, 1, 65, 4500, 2222]]
+    set_table(tables[0])
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            attention.paged_decode(q, cache, indptr, indices, last, sm_scale=d ** -0.5, output=out, workspace=ws)
+    torch.cuda.synchronize()
+    for rep in range(6):
+        set_table(tables[rep % 3])
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        eager = attention.paged_decode(q, cache, indptr, indices, last, sm_scale=d ** -0.5, workspace=ws)
+        torch.cuda.synchronize()
+        print(f"replay {rep} table {rep % 3}", flush=True)
+        assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+        if rep < 3:
+            ref = pa.paged_decode(q.cpu(), cache.cpu(), indptr.cpu(), indices.cpu(), last.cpu(), d ** -0.5)
+            torch.testing.assert_close(got.float().cpu(), ref.to(torch.bfloat16).float(), **TOL)
+
+
 # ---- the sgl decode convention (flash_attn.py:2335-2357): last_page_len counts history only, may be 0 ----
 def _sgl_reference_case(history, g, hq=8, hkv=2, d=256, page=256):
     """The metadata of the reference's own runtime test (test_qwen35_runtime.py:96-118): a 32-page pool of 256-token
