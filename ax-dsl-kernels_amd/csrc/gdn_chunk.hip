@@ -82,19 +82,22 @@ constexpr int kLdT = kC + 8;  // bf16 row stride of [D][C] and [C][C] tiles
 constexpr int kLdL = kC + 4;  // fp32 row stride of [C][C] tiles
 constexpr int kLdX = 32 + 1;  // fp32 scratch of the solve's block products
 
-constexpr int kOffK = 0;                  // k (bf16 [C][LdK])
+// Three regions, each reused as its contents die (52.7 KiB: three workgroups per CU):
+//   K: normalised k (bf16 [C][LdK]) until the K K^T products; then, in place, beta Gamma k for w.
+//   Q: normalised q (bf16 [C][LdK]) until the Q K^T products; P staging (bf16 [C][LdT]); the solve's fp32 scratch
+//      [32][LdX]; bf16 Tinv [C][LdT]; w staging (bf16 [C][LdK]).
+//   L: L (fp32 [C][LdL]), inverted in place into Tinv (each entry of Tinv overwrites the entry of L it replaces,
+//      after that entry was read); then beta v (bf16 [C][LdK]).
+constexpr int kOffK = 0;
 constexpr int kSzK = kC * kLdK * 2;
-constexpr int kOffQ = kOffK + kSzK;       // q (bf16 [C][LdK]); then (beta v)^T (bf16 [D][LdT]); later w staging
-constexpr int kSzQ = kD * kLdT * 2;
-constexpr int kOffL = kOffQ + kSzQ;       // L (fp32 [C][LdL]); then bf16 Tinv [C][LdT]
+constexpr int kOffQ = kOffK + kSzK;
+constexpr int kSzQ = kC * kLdK * 2;
+constexpr int kOffL = kOffQ + kSzQ;
 constexpr int kSzL = kC * kLdL * 4;
-constexpr int kOffT = kOffL + kSzL;       // P staging (bf16 [C][LdT]); Tinv (fp32 [C][LdL]); (beta Gamma k)^T
-constexpr int kSzT = kD * kLdT * 2;
-constexpr int kOffX = kOffT + kSzT;       // fp32 [32][LdX]
-constexpr int kSzX = 32 * kLdX * 4;
-constexpr int kOffG = kOffX + kSzX;       // G, beta: fp32 [C] each
+constexpr int kOffG = kOffL + kSzL;       // G, beta: fp32 [C] each
 constexpr int kPrepLds = kOffG + 2 * kC * 4;
-static_assert(kSzQ >= kC * kLdK * 2 && kSzT >= kC * kLdL * 4 && kSzL >= kC * kLdT * 2, "LDS carve");
+static_assert(kSzQ >= kC * kLdT * 2 && kSzQ >= 32 * kLdX * 4 && kSzL >= kC * kLdK * 2, "LDS carve");
+static_assert(3 * kPrepLds <= 160 * 1024, "three prep workgroups per CU");
 
 struct PrepArgs {
   const uint16_t *q, *k, *v, *a, *b;
@@ -109,9 +112,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* sK = reinterpret_cast<uint16_t*>(smem + kOffK);
   uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + kOffQ);
-  float* sL = reinterpret_cast<float*>(smem + kOffL);
-  float* sT = reinterpret_cast<float*>(smem + kOffT);
-  float* sX = reinterpret_cast<float*>(smem + kOffX);
+  float* sL = reinterpret_cast<float*>(smem + kOffL);  // L, then Tinv in place
+  float* sX = reinterpret_cast<float*>(smem + kOffQ);  // the solve's scratch (q is dead by then)
   float* sG = reinterpret_cast<float*>(smem + kOffG);
   float* sBeta = sG + kC;
 
@@ -123,6 +125,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   const int n = min(kC, p.T - t0);
   const int64_t vidx = ((int64_t)b * p.NV + h) * p.NC + c;   // (sequence, value head, chunk)
   const int64_t kidx = ((int64_t)b * p.NK + kh) * p.NC + c;  // (sequence, key head, chunk)
+
+  // the gate inputs of wave 0 (lane = token), issued with the q / k / v loads: one memory round trip
+  float a_in = 0.f, b_in = 0.f;
+  if (wave == 0 && lane < n) {
+    const int64_t vh = ((int64_t)b * p.T + t0 + lane) * p.NV + h;
+    a_in = bf16_bits_to_f32(p.a[vh]);
+    b_in = bf16_bits_to_f32(p.b[vh]);
+  }
+  const float dtb = p.dt_bias[h], alog = p.a_log[h];
 
   // ---- 1. q, k, v rows: thread = (token tt, 32-dim quarter qd); L2 norms over the 4 threads of a token ----
   const int tt = tid >> 2, qd = tid & 3;
@@ -180,11 +191,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   if (wave == 0) {
     float g = 0.f, beta = 0.f;
     if (lane < n) {
-      const int64_t vh = ((int64_t)b * p.T + t0 + lane) * p.NV + h;
-      const float x = bf16_bits_to_f32(p.a[vh]) + p.dt_bias[h];
+      const float x = a_in + dtb;
       const float sp = x > 20.f ? x : log1pf(expf(x));
-      g = -expf(p.a_log[h]) * sp;
-      beta = round_bf16(1.0f / (1.0f + expf(-bf16_bits_to_f32(p.b[vh]))));
+      g = -expf(alog) * sp;
+      beta = round_bf16(1.0f / (1.0f + expf(-b_in)));
     }
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -232,8 +242,9 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
     }
   }
 
-  // ---- 4. L (fp32, strictly lower), P = bf16((q k^T) * decay) staged for a coalesced write ----
-  uint16_t* sP = reinterpret_cast<uint16_t*>(sT);
+  // ---- 4. L (fp32, strictly lower), P = bf16((q k^T) * decay) staged (over q) for a coalesced write ----
+  uint16_t* sP = sQ;
+  __syncthreads();  // every wave's reads of q (and of k for the products) are done
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
@@ -258,8 +269,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   __syncthreads();
 
   // ---- 5. Tinv = (I + L)^-1 ----
-  // 5a. the four 16 x 16 diagonal blocks by forward substitution (wave 0: lane = 16 * block + column);
-  //     the other waves zero the blocks above the diagonal
+  // In place over L: L is zero on and above the diagonal (step 4 writes every entry), which is what Tinv holds
+  // above the diagonal, and every step writes a block of Tinv only after the block of L it replaces was read.
+  // 5a. the four 16 x 16 diagonal blocks by forward substitution (wave 0: lane = 16 * block + column; a lane
+  //     reads rows of its block, every read of the wave precedes its writes)
   if (wave == 0) {
     const int base = 16 * g4, col = l16;
     float t[16];
@@ -271,14 +284,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
       t[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sT[(base + i) * kLdL + base + col] = t[i];
-  } else {
-    for (int idx = tid - 64; idx < 6 * 256; idx += 192) {
-      const int pr = idx >> 8, e = idx & 255;  // block pairs (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-      const int rb = pr < 3 ? 0 : (pr < 5 ? 1 : 2);
-      const int cb = pr < 3 ? pr + 1 : (pr < 5 ? pr - 1 : 3);
-      sT[(16 * rb + (e >> 4)) * kLdL + 16 * cb + (e & 15)] = 0.f;
-    }
+    for (int i = 0; i < 16; ++i) sL[(base + i) * kLdL + base + col] = t[i];
   }
   __syncthreads();
   // 5b. 32 x 32 blocks: T21 = -T22 (L21 T11) with 16 x 16 parts (waves 0, 1: one 32-block each)
@@ -288,7 +294,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kq = 4 * st + g4;
-      x = mfma_f32_16x16x4(sL[(base + 16 + l16) * kLdL + base + kq], sT[(base + kq) * kLdL + base + l16], x);
+      x = mfma_f32_16x16x4(sL[(base + 16 + l16) * kLdL + base + kq], sL[(base + kq) * kLdL + base + l16], x);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) sX[wave * 16 * 17 + (4 * g4 + r) * 17 + l16] = x[r];
@@ -300,10 +306,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int kq = 4 * st + g4;
-      y = mfma_f32_16x16x4(sT[(base + 16 + l16) * kLdL + base + 16 + kq], sX[wave * 16 * 17 + kq * 17 + l16], y);
+      y = mfma_f32_16x16x4(sL[(base + 16 + l16) * kLdL + base + 16 + kq], sX[wave * 16 * 17 + kq * 17 + l16], y);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sT[(base + 16 + 4 * g4 + r) * kLdL + base + l16] = -y[r];
+    for (int r = 0; r < 4; ++r) sL[(base + 16 + 4 * g4 + r) * kLdL + base + l16] = -y[r];  // over L21 (read above)
   }
   __syncthreads();
   // 5c. the 64 x 64 level: T21 = -T22 (L21 T11) with 32 x 32 parts (wave w: output tile (w / 2, w % 2))
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const int kq = 4 * st + g4;
-      x = mfma_f32_16x16x4(sL[(32 + 16 * rt + l16) * kLdL + kq], sT[kq * kLdL + 16 * ct + l16], x);
+      x = mfma_f32_16x16x4(sL[(32 + 16 * rt + l16) * kLdL + kq], sL[kq * kLdL + 16 * ct + l16], x);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) sX[(16 * rt + 4 * g4 + r) * kLdX + 16 * ct + l16] = x[r];
@@ -322,23 +328,24 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const int kq = 4 * st + g4;
-      y = mfma_f32_16x16x4(sT[(32 + 16 * rt + l16) * kLdL + 32 + kq], sX[kq * kLdX + 16 * ct + l16], y);
+      y = mfma_f32_16x16x4(sL[(32 + 16 * rt + l16) * kLdL + 32 + kq], sX[kq * kLdX + 16 * ct + l16], y);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sT[(32 + 16 * rt + 4 * g4 + r) * kLdL + 16 * ct + l16] = -y[r];
+    for (int r = 0; r < 4; ++r) sL[(32 + 16 * rt + 4 * g4 + r) * kLdL + 16 * ct + l16] = -y[r];  // over L21 (read above)
   }
   __syncthreads();
 
-  // ---- 6. bf16 operands: Tinv [C][LdT] (over L), (beta v)^T (over q), (beta Gamma k)^T (over fp32 Tinv) ----
-  uint16_t* sTb = reinterpret_cast<uint16_t*>(sL);
+  // ---- 6. bf16 operands: Tinv [C][LdT] (over the scratch), beta v (over fp32 Tinv), beta Gamma k (over k) ----
+  uint16_t* sTb = sQ;
   for (int i = tid; i < kC * kC; i += 256) {
     const int r = i >> 6, cc = i & 63;
-    sTb[r * kLdT + cc] = (uint16_t)f32_to_bf16_bits(sT[r * kLdL + cc]);
+    sTb[r * kLdT + cc] = (uint16_t)f32_to_bf16_bits(sL[r * kLdL + cc]);
   }
   __syncthreads();
-  // beta v and beta Gamma k row-major [token][LdK] (16-byte writes); step 7 reads them transposed
-  uint16_t* sVB = sQ;
-  uint16_t* sKB = reinterpret_cast<uint16_t*>(sT);
+  // beta v and beta Gamma k row-major [token][LdK] (16-byte writes); step 7 reads them transposed. Each thread
+  // rewrites the k entries it reads (its own token and columns), so k -> beta Gamma k in place is safe.
+  uint16_t* sVB = reinterpret_cast<uint16_t*>(sL);
+  uint16_t* sKB = sK;
   {
     const float beta = sBeta[tt], gm = __expf(sG[tt]);
 #pragma unroll
@@ -384,7 +391,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(PrepArgs p) {
   }
   __syncthreads();
 
-  // ---- 8. u straight from the accumulators in the scan's order; w staged (over q) for row-major writes ----
+  // ---- 8. u straight from the accumulators in the scan's order; w staged (over Tinv) for row-major writes ----
   uint16_t* u_g = p.ws.u + vidx * kC * kD;
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
