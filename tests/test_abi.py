@@ -131,3 +131,29 @@ def test_entry_points_reach_the_launch_on_a_gpu_less_host():
     assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws, None) == launch
     assert lib.axk_gdn_layer_prefill(*bad, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws, None) == 3
     assert lib.axk_gdn_layer_prefill(*args, 1, 20, 256, 1, 2, 128, 4, 256, 1e-6, 0, 2, 1, p[150], pws - 1, None) == 6
+
+
+def test_int8_kv_contract_violations_return_before_launch():
+    """The INT8 cache entries reject bad shapes, NULL scales and misaligned scales before any launch; the Python
+    wrappers raise ValueError on mismatched scale tensors before touching a device."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every check below fails first
+    args = lambda scales, hkv, d: (fake, fake, scales, fake, fake, fake, fake, 2, 2 * hkv, hkv, d, 64, 8, 0.0625,
+                                   fake, 1 << 20, None)
+    assert lib.axk_paged_decode_i8(*args(None, 2, 128)) == 1               # NULL kv_scales
+    assert lib.axk_paged_decode_i8(*args(fake, 2, 64)) == 2                # head_dim 64
+    assert lib.axk_paged_decode_i8(*args(fake, 17, 128)) == 2              # more than 16 KV heads
+    assert lib.axk_paged_decode_i8(*args(ctypes.c_void_p(0x1002), 2, 128)) == 3  # scales not 4-byte aligned
+    assert lib.axk_paged_kv_write_i8(fake, fake, fake, None, fake, 2, 2, 128, 64, 8, None, None) == 1
+    assert lib.axk_paged_kv_write_i8(fake, fake, fake, fake, fake, 2, 2, 64, 64, 8, None, None) == 2
+    assert lib.axk_paged_kv_write_i8(ctypes.c_void_p(0x1008), fake, fake, fake, fake, 2, 2, 128, 64, 8, None,
+                                     None) == 3
+    q = torch.zeros(2, 4, 128, dtype=torch.bfloat16)
+    cache = torch.zeros(8, 2, 64, 2, 128, dtype=torch.int8)
+    ip, idx, last = torch.tensor([0, 1, 2], dtype=torch.int32), torch.zeros(2, dtype=torch.int32), \
+        torch.ones(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="kv_scales"):
+        axk.paged_decode_i8(q, cache, torch.zeros(8, 2, 64, 2, dtype=torch.float32), ip, idx, last)
+    with pytest.raises(ValueError, match="kv_scales"):
+        axk.store_paged_kv_i8(torch.zeros(2, 2, 128, dtype=torch.bfloat16), torch.zeros(2, 2, 128, dtype=torch.bfloat16),
+                              cache, torch.zeros(8, 2, 64, 3, dtype=torch.bfloat16), torch.zeros(2, 2, dtype=torch.int32))
