@@ -449,8 +449,9 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     // FP8: tiles land kAhead8 ahead in a ring of kAhead8 + 1 slots (an FP8 tile is half a bf16 one, so twice the
     // look-ahead keeps as many bytes in flight), and two bf16 staging tiles. Iteration ti: wait for tile ti + 1, one
     // fenced barrier (every wave's loads of ti + 1 landed, the conversion of ti done, the math of ti - 1 done), issue
-    // tile ti + kAhead8 into the slot of tile ti - 1, convert tile ti + 1 into the staging tile ti - 1 used, then
-    // the math of tile ti.
+    // tile ti + kAhead8 into the slot of tile ti - 1, the math of tile ti, then convert tile ti + 1 into the staging
+    // tile ti - 1 used (every wave finished that math before the barrier; issued behind the math, the conversion's
+    // latency overlaps it).
     constexpr int kAhead8 = 4, kNBuf8 = kAhead8 + 1;
     constexpr int IPWQ = L::IPW + (QM == 1 ? 1 : 0);  // this wave's loads of a tile
     unsigned char* stage = smem + kNBuf8 * L::BUF;
@@ -511,8 +512,8 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       wait_vmcnt<(kAhead8 - 2) * IPWQ>();  // tile ti + 1 has landed (later ones may not)
       __syncthreads();  // a fence with the barrier: LDS written by other waves is read after it
       const int nvn = issue(ti + kAhead8, (ti + kAhead8) % kNBuf8);  // into the slot of tile ti - 1 (converted)
-      if (nv[1] > 0) convert((ti + 1) % kNBuf8, stage + ((ti + 1) & 1) * C::BUF);
       if (nv[0] > 0) tile_math(stage + (ti & 1) * C::BUF, nv[0]);
+      if (nv[1] > 0) convert((ti + 1) % kNBuf8, stage + ((ti + 1) & 1) * C::BUF);
 #pragma unroll
       for (int j = 0; j + 1 < kAhead8; ++j) nv[j] = nv[j + 1];
       nv[kAhead8 - 1] = nvn;
