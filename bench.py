@@ -195,7 +195,7 @@ class MxLinearPrefillWorkload(Workload):
 
 
 class LmHeadWorkload(Workload):
-    """The MXFP4 LM head GEMV of decode (SURVEY next row): W [248320, 2048] (E2M1 + E8M0, config 0's encoding),
+    """The MXFP4 LM head GEMV of decode (a row next to the path): W [248320, 2048] (E2M1 + E8M0, config 0's encoding),
     x bf16 [1, 2048], fp32 logits (mul_mat_mx4_n248320_k2048, q35_layer_mc.py:705-724)."""
 
     name = "lm_head"
@@ -330,7 +330,7 @@ class PagedDecodeWorkload(Workload):
 
 
 class PagedDecodeFp8Workload(Workload):
-    """Config 1's attention over an FP8 E4M3 cache (SURVEY next row: KV8 = 2, q35_group.py:44-54): the same
+    """Config 1's attention over an FP8 E4M3 cache (the FP8 cache, KV8 = 2, q35_group.py:44-54): the same
     sequences, pages and queries, the cache stored as e4m3(bf16(x * 8)). One step = axk_paged_decode_fp8 (plan +
     split + merge); the roofline is the whole op's (so it includes the merge): K and V bytes of every valid token
     (half of bf16's) + q + out + page table."""
@@ -391,7 +391,7 @@ class PagedDecodeFp8Workload(Workload):
 
 
 class PagedDecodeI8Workload(PagedDecodeFp8Workload):
-    """Config 1's attention over an INT8 cache (SURVEY next row: KV8 = 1, q35_group.py:44-47, 197-221): the same
+    """Config 1's attention over an INT8 cache (the INT8 cache, KV8 = 1, q35_group.py:44-47, 197-221): the same
     sequences, pages and queries, each row and KV head stored as int8 codes with a bf16 scale. One step =
     axk_paged_decode_i8 (plan + split + merge); algorithmic bytes: the codes and scales of every valid token + q + out
     + page table."""
@@ -452,7 +452,7 @@ class PagedDecodeI8Workload(PagedDecodeFp8Workload):
 
 
 class PagedPrefillWorkload(Workload):
-    """Prefill attention (SURVEY next row: G x P-row causal block attention, q35_prefill.py:264-336; flash_attn.py:
+    """Prefill attention (G x P-row causal block attention, q35_prefill.py:264-336; flash_attn.py:
     471-611): one sequence's 4096-token chunk over an empty history in the paged cache, config 1's attention shape
     (HQ 16 / HKV 2, D 256, page 64). One step = axk_paged_prefill (one launch). MFMA-bound: the flops of the visible
     (query, key) pairs only, 4 D HQ sum_t (t + 1) (QK^T and PV), against dense bf16."""
