@@ -602,20 +602,24 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
     __syncthreads();
   };
 
-  // Three operand sets in rotation: chunk c + 2 is loaded while chunk c is processed. The loads are
-  // unconditional (past the end they repeat the last chunk, unused) so every path through the loop has the
-  // same loads in flight and the waits before each use stay two sets deep.
+  // Four operand sets in rotation: chunk c + 3 is loaded while chunk c is processed (the loads have three chunk
+  // steps to land; one wave per SIMD leaves the registers for it). The loads are unconditional (past the end they
+  // repeat the last chunk, unused) so every path through the loop has the same loads in flight and the waits
+  // before each use stay three sets deep.
   const int last = p.NC - 1;
-  ScanOps<CPW> o0, o1, o2;
+  ScanOps<CPW> o0, o1, o2, o3;
   scan_load(o0, sbase, 0);
   scan_load(o1, sbase, min(1, last));
-  for (int c = 0; c < p.NC; c += 3) {
-    scan_load(o2, sbase, min(c + 2, last));
+  scan_load(o2, sbase, min(2, last));
+  for (int c = 0; c < p.NC; c += 4) {
+    scan_load(o3, sbase, min(c + 3, last));
     process(o0, c);
-    scan_load(o0, sbase, min(c + 3, last));
+    scan_load(o0, sbase, min(c + 4, last));
     if (c + 1 < p.NC) process(o1, c + 1);
-    scan_load(o1, sbase, min(c + 4, last));
+    scan_load(o1, sbase, min(c + 5, last));
     if (c + 2 < p.NC) process(o2, c + 2);
+    scan_load(o2, sbase, min(c + 6, last));
+    if (c + 3 < p.NC) process(o3, c + 3);
   }
 
   float* sout = p.state_out + (int64_t)bh * kD * kD;
