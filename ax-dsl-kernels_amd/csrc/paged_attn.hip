@@ -1253,7 +1253,7 @@ constexpr int kPfWaves = 8;
 constexpr int kPfRowsPerWave = 16;
 constexpr int kPfNI = kPfRowsPerWave / 16;  // 16-row MFMA blocks per wave
 constexpr int kPfRows = kPfWaves * kPfRowsPerWave;
-constexpr int kPfAhead = 4;  // tiles in flight while two are computed (even: tiles are taken in pairs)
+constexpr int kPfAhead = 6;  // tiles in flight while two are computed (even: tiles are taken in pairs)
 constexpr int kPfBuf = kPfAhead + 2;
 
 template <int D>
