@@ -10,13 +10,15 @@
 // [E, 2F, H/32]; down e_dw [E, H, F/2], e_ds [E, H, F/32] (models/qwen35_35b_a3b/qwen35_35b_a3b.manifest.json).
 //
 // Router (axk_moe_decode; q35_layer_mc.py:820-829):
-//   router       — decode: split-K GEMV, workgroup = (16 experts, 16 tokens, K slice), partial logits per slice
+//   router_full  — decode: GEMV over the whole K, workgroup = (16 experts, 16 tokens), 16 waves summed in wave order;
+//                  final fp32 logits, and the shared gate's logit h2 . w_shg from one extra expert block
 //   router_tile  — prefill: 64 x 64 MFMA tiles of tokens x experts over two K halves
-//   route_part   — one wave per token: the slice partials summed in fixed order into the logits, softmax,
-//                  top-K by ballot rounds (ties: lower id), renormalised weights
+//   route_part   — one wave per token: the partials summed in fixed order into the logits (decode: the final
+//                  logits read in place), softmax, top-K by ballot rounds (ties: lower id), renormalised weights;
+//                  in decode the last workgroup to finish groups the pairs
 //   route        — the same selection from caller logits (axk_moe_route)
 // Experts, decode (tokens <= kDecodeTokens, tokens x top_k <= kMaxPairs):
-//   group   — one workgroup: per-expert token bitmasks, the (token, slot) pairs ranked by popcount (stable,
+//   group   — one workgroup (inside the routing launch when the router ran): per-expert token bitmasks, the (token, slot) pairs ranked by popcount (stable,
 //             deterministic), the active-expert records {rows, expert, first sorted row}
 //   gateup  — workgroup = (active expert or the shared expert, run of 16-row weight tiles): each wave streams its
 //             MXFP4 gate and up rows over the full K. For small row counts the weights pass through a
@@ -24,8 +26,8 @@
 //             in the MFMA layout; SwiGLU in the epilogue
 //   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the routing weight, written
 //             to y by pair
-//   combine — workgroup = (token, columns): shared gate once, residual, sum over the token's K pairs in slot
-//             order, one bf16 rounding
+//   combine — workgroup = (token, columns): shared gate (from the router's gate logit, or a dot here), residual,
+//             sum over the token's K pairs in slot order, one bf16 rounding
 // Every expert's weights are read once per call, whatever the number of its tokens.
 //
 // Prefill (tokens > kDecodeTokens; moe_slots_px + moe_combine of q35_moe_prefill.py:150-214):
@@ -48,8 +50,11 @@ using axk::WF_MXFP4;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxTopK = 32;  // <= 64: lane k of the routing wave keeps selection k
 constexpr int kMaxPairs = 8192;
-constexpr int kMaskWords = 4;  // token bitmask words per expert in the grouping kernel: tokens <= 256
-constexpr size_t kMaxStageLds = 160 * 1024;  // decode streaming: 16 staged activation rows of K + 8 bf16
+constexpr int kMaskWords = 4;  // token bitmask words per expert in a 256-token block of the prefill grouping
+constexpr size_t kMaxStageLds = 160 * 1024;  // dynamic LDS of the prefill GEMMs (the whole CU's LDS)
+// dynamic LDS of the decode streaming kernels (activation rows of K + 8 bf16, the wave tiles): the CU's LDS less
+// 4 KiB for their static grouping state
+constexpr size_t kMaxStreamLds = 156 * 1024;
 constexpr int kDecodeTokens = 64 * kMaskWords;  // above this the prefill path runs
 constexpr int64_t kMaxPrefillTokens = 1 << 16;
 constexpr int64_t kMaxPrefillPairs = 1 << 19;
@@ -73,7 +78,9 @@ struct MoeWs {
   int4* tiles;      // [max tiles] prefill GEMM tiles: {expert (-1: shared), first row, rows, 0}
   int* n_tiles;     // [1]
   int* row_pair;    // [P] pair t * K + k of sorted row (y is indexed by pair)
-  float* rpart;     // [S, T, E] decode router: partial logits of K slice s
+  float* rpart;     // [S, T, E] router partial logits of K slice s
+  float* gate_logit; // [T] decode: the shared expert's gate logit h2 . w_shg, summed from
+  float* gpart;      // [S, T] its slice partials
 };
 
 int64_t prefill_blocks(int64_t T) { return (T + kBlkTokens - 1) / kBlkTokens; }
@@ -83,26 +90,29 @@ int64_t prefill_max_tiles(int64_t T, int64_t E, int64_t K) {
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Decode router: K slices reduced in fixed order by the routing kernel (8 steps of 32 per slice, 1..16 slices).
+// Router partial logits, summed in slice order by the routing kernel. Decode: K slices of 8 steps of 32 (1..16 slices),
+// prefill: two K halves.
 constexpr int kMaxRouterSplits = 16;
-constexpr int kPrefillRouterSplits = 2;  // prefill router: K halves (two partial logits per token)
+constexpr int kPrefillRouterSplits = 2;
 int router_splits(int64_t H) {
   const int64_t s = (H / 32) / 8;
   return (int)(s < 1 ? 1 : (s > kMaxRouterSplits ? kMaxRouterSplits : s));
 }
 
-constexpr int kWsParts = 16;
+constexpr int kWsParts = 17;
 
 size_t moe_ws_layout(int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, int64_t Fs, size_t* off) {
   const int64_t P = T * K;
   const bool prefill = T > kDecodeTokens;
   const size_t nb = prefill ? (size_t)prefill_blocks(T) : 0, nt = prefill ? (size_t)prefill_max_tiles(T, E, K) : 0;
-  const size_t rp = (size_t)(prefill ? kPrefillRouterSplits : router_splits(H)) * T * E * 4;
+  const size_t S = prefill ? kPrefillRouterSplits : router_splits(H);
+  const size_t rp = S * T * E * 4;
   size_t o = 0;
   const size_t sizes[kWsParts] = {(size_t)E * 4,      (size_t)(E + 1) * 4, (size_t)E * 16,    8,
                                   (size_t)P * 4,      (size_t)P * 4,       (size_t)P * 4,     (size_t)P * F * 2,
                                   (size_t)T * Fs * 2, (size_t)P * H * 4,   (size_t)T * H * 4, nb * E * 4,
-                                  nt * 16,            4,                   (size_t)P * 4,     rp};
+                                  nt * 16,            4,                   (size_t)P * 4,     rp,
+                                  (S + 1) * T * 4};
   for (int i = 0; i < kWsParts; ++i) {
     off[i] = o;
     o = align256(o + sizes[i]);
@@ -121,7 +131,8 @@ MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, in
           reinterpret_cast<uint16_t*>(b + off[8]),  reinterpret_cast<float*>(b + off[9]),
           reinterpret_cast<float*>(b + off[10]),    reinterpret_cast<int*>(b + off[11]),
           reinterpret_cast<int4*>(b + off[12]),     reinterpret_cast<int*>(b + off[13]),
-          reinterpret_cast<int*>(b + off[14]),      reinterpret_cast<float*>(b + off[15])};
+          reinterpret_cast<int*>(b + off[14]),      reinterpret_cast<float*>(b + off[15]),
+          reinterpret_cast<float*>(b + off[16]),    reinterpret_cast<float*>(b + off[16]) + T};
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -195,60 +206,53 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
   route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
 }
 
-// The decode grouping (below, beside moe_group_kernel).
-template <bool COH = false>
-AXK_DEV void group_body(const int32_t* ids, const float* wts, int T, int E, int K, const MoeWs& w,
-                        unsigned long long* s_mask, int* s_off, int* s_tmp);
-
-// Decode routing from the router's partial logits: logit = sum of the S K-slice partials in slice order
-// (written out as the layer's logits), then route_select. GROUP (decode): the last workgroup to finish also groups
-// the pairs (moe_group_kernel's work), counted on `done`, which the router kernel zeroed earlier on the stream.
-template <int V, int MAXS, bool GROUP = false>  // MAXS: bound on the number of partials
-__global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part, int S, int T, int E,
+// Routing from the router's partial logits: logit = sum of the S K-slice partials in slice order (written out as the
+// layer's logits), then route_select. With gpart (decode), lane 0 of token t's wave also sums the shared gate's S
+// partial logits in slice order into gate_logit[t].
+template <int V, int MAXS>  // MAXS: bound on the number of partials
+__global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part,
+                                                             const float* __restrict__ gpart, int S, int T, int E,
                                                              int K, int norm_topk, float* __restrict__ logits,
-                                                             int32_t* __restrict__ ids, float* __restrict__ wts,
-                                                             MoeWs w, int* done) {
+                                                             float* __restrict__ gate_logit,
+                                                             int32_t* __restrict__ ids, float* __restrict__ wts) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t < T) {
-    // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
-    float pv[MAXS][V];
+  if (t >= T) return;
+  // all S x V partial loads unconditional (slices past S clamped, then dropped): one memory round trip
+  float pv[MAXS][V];
 #pragma unroll
-    for (int sl = 0; sl < MAXS; ++sl)
+  for (int sl = 0; sl < MAXS; ++sl)
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
-    float x[V];
+    for (int i = 0; i < V; ++i)
+      pv[sl][i] = part[((int64_t)min(sl, S - 1) * T + t) * E + min(i * 64 + lane, E - 1)];
+  float gp[MAXS];
+  if (gpart) {
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      float v = pv[0][i];
-#pragma unroll
-      for (int sl = 1; sl < MAXS; ++sl)
-        if (sl < S) v += pv[sl][i];
-      x[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const int e = i * 64 + lane;
-      if (e < E) logits[(int64_t)t * E + e] = x[i];
-      else x[i] = -INFINITY;
-    }
-    route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+    for (int sl = 0; sl < MAXS; ++sl) gp[sl] = gpart[(int64_t)min(sl, S - 1) * T + t];
   }
-  if constexpr (GROUP) {
-    __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
-    __shared__ int s_off[kMaxExperts + 1];
-    __shared__ int s_tmp[8];
-    __shared__ int s_last;
-    __threadfence();  // this workgroup's selections visible device-wide before it counts itself done
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(done, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (s_last) {
-      __threadfence();
-      group_body<true>(ids, wts, T, E, K, w, s_mask, s_off, s_tmp);
-    }
+  float x[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    float v = pv[0][i];
+#pragma unroll
+    for (int sl = 1; sl < MAXS; ++sl)
+      if (sl < S) v += pv[sl][i];
+    x[i] = v;
   }
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const int e = i * 64 + lane;
+    if (e < E) logits[(int64_t)t * E + e] = x[i];
+    else x[i] = -INFINITY;
+  }
+  if (gpart && lane == 0) {
+    float gv = gp[0];
+#pragma unroll
+    for (int sl = 1; sl < MAXS; ++sl)
+      if (sl < S) gv += gp[sl];
+    gate_logit[t] = gv;
+  }
+  route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
 }
 
 // Prefill router GEMM: workgroup (64 tokens, 64 experts, K slice s), waves 2 x 2 with 32 x 32 each; both operands
@@ -339,18 +343,20 @@ __global__ __launch_bounds__(256) void moe_router_tile_kernel(const uint16_t* __
 
 // Decode router GEMM, split over K: workgroup (16 experts, 16 tokens, K slice s); wave w multiplies the slice's
 // 32-wide K steps w, w + 4, ... on MFMA (h2 rows as A, router rows as B), the four waves are summed in LDS and
-// the partial logits written to part[s]. Rows past T or E are clamped for the loads and never stored.
+// the partial logits written to part[s]. With gpart, expert block ceil(E / 16) multiplies the shared expert's gate
+// vector w_shg instead and writes the partial gate logit (h2 . w_shg over the slice) to gpart[s, t]. Rows past T or
+// E are clamped for the loads and never stored.
 __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ h2,
-                                                         const uint16_t* __restrict__ wr, int T, int H, int E,
-                                                         int S, float* __restrict__ part, int* done) {
+                                                         const uint16_t* __restrict__ wr,
+                                                         const uint16_t* __restrict__ w_shg, int T, int H, int E,
+                                                         int S, float* __restrict__ part, float* __restrict__ gpart) {
   __shared__ float4 red[4][64];
-  // the routing kernel's finished-workgroup count, zeroed here (the router runs before it on the stream)
-  if (done && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *done = 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  const bool gate_blk = (int)blockIdx.x * 16 >= E;  // the extra block (launched only with gpart)
   const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16, sl = blockIdx.z;
   const int ns = H / 32, st0 = (int)((int64_t)sl * ns / S), st1 = (int)((int64_t)(sl + 1) * ns / S);
   const uint16_t* arow = h2 + (int64_t)min(t0 + nl, T - 1) * H + 8 * g;
-  const uint16_t* brow = wr + (int64_t)min(e0 + nl, E - 1) * H + 8 * g;
+  const uint16_t* brow = gate_blk ? w_shg + 8 * g : wr + (int64_t)min(e0 + nl, E - 1) * H + 8 * g;
   axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int i = st0 + wave; i < st1; i += 8) {
     const int j = min(i + 4, st1 - 1);
@@ -369,13 +375,15 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restr
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int t = t0 + 4 * g + r;
-    if (t < T && e < E) part[((int64_t)sl * T + t) * E + e] = v[r];
+    if (t >= T) continue;
+    if (gate_blk) {
+      if (nl == 0) gpart[(int64_t)sl * T + t] = v[r];
+    } else if (e < E) {
+      part[((int64_t)sl * T + t) * E + e] = v[r];
+    }
   }
 }
 
-// ---------------------------------------------------------------------------------------------
-// group: one workgroup; pairs grouped by expert, stable in (token, slot) order
-// ---------------------------------------------------------------------------------------------
 // Block-wide exclusive scan of one int per thread (256 threads); returns the exclusive prefix, *total the sum.
 __device__ __forceinline__ int block_exclusive_scan256(int v, int* s_tmp, int* total) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -394,106 +402,16 @@ __device__ __forceinline__ int block_exclusive_scan256(int v, int* s_tmp, int* t
   return base + incl - v;
 }
 
-// Expert e's tokens as a bitmask (a token's K experts are distinct, so a pair is (expert, token)): counts
-// are popcounts, and a pair's rank inside its expert is the popcount of the lower tokens' bits — the
-// grouping is stable in token order with no atomics on positions.
-// The grouping, for every thread of the workgroup (its barriers are unconditional); threads 0 .. 255 do the work.
-// COH: ids / wts were written by other workgroups of the same launch: read them at device scope (past this CU's L1).
-template <bool COH>
-AXK_DEV int load_id(const int32_t* p) {
-  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
-}
-template <bool COH>
-AXK_DEV float load_wt(const float* p) {
-  if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *p;
-}
-template <bool COH>
-AXK_DEV void group_body(const int32_t* ids, const float* wts, int T, int E, int K, const MoeWs& w,
-                        unsigned long long* s_mask, int* s_off, int* s_tmp) {
-  const int P = T * K, W = (T + 63) / 64;
-  const int tid = threadIdx.x;
-  const bool on = tid < 256;
-  if (on)
-    for (int i = tid; i < E * W; i += 256) s_mask[i] = 0ull;
-  __syncthreads();
-  if (on)
-    for (int p = tid; p < P; p += 256) {
-      const int e = load_id<COH>(ids + p), t = p / K;
-      if (e >= 0 && e < E) atomicOr(&s_mask[e * W + (t >> 6)], 1ull << (t & 63));
-    }
-  __syncthreads();
-  // expert e's count; 4 experts per thread (E <= 1024), then a block scan of the per-thread sums
-  constexpr int EPT = kMaxExperts / 256;
-  int cnt[EPT], sum = 0, nact = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid * EPT + j;
-    int c = 0;
-    if (on && e < E)
-      for (int i = 0; i < W; ++i) c += __popcll(s_mask[e * W + i]);
-    cnt[j] = c;
-    sum += c;
-    nact += c > 0;
-  }
-  int tot, tota;
-  int off = block_exclusive_scan256(sum, s_tmp, &tot);
-  int aoff = block_exclusive_scan256(nact, s_tmp + 4, &tota);
-  if (on) {
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const int e = tid * EPT + j;
-      if (e < E) {
-        s_off[e] = off;
-        w.counts[e] = cnt[j];
-        w.offsets[e] = off;
-        if (cnt[j] > 0) {
-          w.active[aoff] = make_int4(cnt[j], e, off, 0);
-          ++aoff;
-        }
-      }
-      off += cnt[j];
-    }
-    if (tid == 0) {
-      w.offsets[E] = tot;
-      *w.n_active = tota;
-    }
-    for (int j = tota + tid; j < E; j += 256) w.active[j] = make_int4(0, 0, 0, 0);  // streaming kernels exit
-  }
-  __syncthreads();
-  if (on)
-    for (int p = tid; p < P; p += 256) {
-      const int e = load_id<COH>(ids + p), t = p / K;
-      if (e < 0 || e >= E) {  // an id outside [0, E) selects no expert: the combine skips the pair
-        w.pair_pos[p] = -1;
-        continue;
-      }
-      int rank = __popcll(s_mask[e * W + (t >> 6)] & ((1ull << (t & 63)) - 1ull));
-      for (int i = 0; i < (t >> 6); ++i) rank += __popcll(s_mask[e * W + i]);
-      const int pos = s_off[e] + rank;
-      w.pair_pos[p] = pos;
-      w.row_tok[pos] = t;
-      w.row_w[pos] = load_wt<COH>(wts + p);
-      w.row_pair[pos] = p;
-    }
-}
-
-__global__ __launch_bounds__(256) void moe_group_kernel(const int32_t* __restrict__ ids,
-                                                        const float* __restrict__ wts, int T, int E, int K,
-                                                        MoeWs w) {
-  __shared__ unsigned long long s_mask[kMaxExperts * kMaskWords];
-  __shared__ int s_off[kMaxExperts + 1];
-  __shared__ int s_tmp[8];
-  group_body(ids, wts, T, E, K, w, s_mask, s_off, s_tmp);
-}
-
-
 // ---------------------------------------------------------------------------------------------
 // Decode expert streaming. A workgroup owns one slot (an active expert, or the shared expert) and a run of
-// 16-row weight tiles; the slot's gathered activation rows (16 per pass) are staged in LDS once, and every wave
+// 16-row weight tiles; the slot's gathered activation rows (8 or 16 per pass) are staged in LDS once, and every wave
 // then streams its own tiles over the full K with the next batch of 16-byte weight units in flight while the
 // current one feeds the MFMAs: no cross-wave reduction and no barrier inside the stream.
+//
+// The pairs are grouped by the streaming workgroups themselves (no grouping launch): each reads the T K top-K ids
+// once, marks the active experts in an LDS bitmap, takes the slot-th active expert in ascending id order, and ranks
+// that expert's pairs in pair order (token order: a token's K experts are distinct) by ballots. An id outside [0, E)
+// selects no expert. Activations and routed outputs are indexed by pair.
 // ---------------------------------------------------------------------------------------------
 #ifndef AXK_SW
 #define AXK_SW 4
@@ -520,19 +438,91 @@ constexpr int kWaveStageBytes = 32 * kStageLd;      // a wave's LDS tile: gate a
 constexpr int kStageLpr = 4 * kBatchChunks;         // staged loads: lanes per row segment,
 constexpr int kStageRpi = 64 / kStageLpr;           // rows per load instruction (kBatchChunks instructions a tile)
 constexpr int kSmallRows = 8;                       // activation rows per pass of the staged kernels
+constexpr int kStreamThreads = 64 * kStreamWaves;
 // byte offset of the wave tiles after the activation rows ([rows][K + 8] bf16), 16-byte aligned
 __host__ __device__ inline size_t stream_stage_off(int rows, int K) { return ((size_t)rows * (K + 8) * 2 + 15) & ~(size_t)15; }
 
-// Stage activation rows [m0, m0 + kStageRows) of the slot into LDS as [kStageRows][K + 8] bf16 (rows past cnt
-// are skipped).
-template <bool GATHER, int ROWS>
-__device__ void stage_rows(uint16_t* sA, const uint16_t* __restrict__ src, const int* __restrict__ row_tok,
-                           int row0, int m0, int cnt, int K) {
+// A routed slot's grouping in LDS.
+struct SlotLds {
+  unsigned long long act[kMaxExperts / 64];  // active experts
+  int pair[kDecodeTokens];                  // the expert's pairs in pair order (at most one per token)
+  int wcnt[kStreamWaves];
+};
+static_assert(sizeof(SlotLds) + kMaxStreamLds <= 160 * 1024, "streaming LDS over the CU's 160 KiB");
+
+// The slot-th active expert (ascending id), or -1 past the last. id0: the id of pair threadIdx.x (when < P), kept
+// for decode_rank_rows.
+AXK_DEV int decode_find_expert(const int32_t* __restrict__ ids, int P, int E, int slot, SlotLds& L, int& id0) {
+  const int tid = threadIdx.x;
+  id0 = ids[min(tid, P - 1)];
+  for (int i = tid; i < kMaxExperts / 64; i += kStreamThreads) L.act[i] = 0ull;
+  __syncthreads();
+  if (tid < P && id0 >= 0 && id0 < E) atomicOr(&L.act[id0 >> 6], 1ull << (id0 & 63));
+#pragma unroll 4
+  for (int p = tid + kStreamThreads; p < P; p += kStreamThreads) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) atomicOr(&L.act[e >> 6], 1ull << (e & 63));
+  }
+  __syncthreads();
+  int base = 0;
+  for (int wd = 0; wd < (E + 63) / 64; ++wd) {  // uniform
+    unsigned long long m = L.act[wd];
+    const int c = __popcll(m);
+    if (slot < base + c) {  // the r-th set bit of m, by halving
+      int r = slot - base, pos = 0;
+#pragma unroll
+      for (int h = 32; h >= 1; h >>= 1) {
+        const int cl = __popcll(m & ((1ull << h) - 1ull));
+        if (r >= cl) {
+          r -= cl;
+          m >>= h;
+          pos += h;
+        }
+      }
+      return wd * 64 + pos;
+    }
+    base += c;
+  }
+  return -1;
+}
+
+// Expert e's pairs in pair order into L.pair; returns their count. Past the first kStreamThreads pairs (id0) the ids
+// are read again (L2 hits). A token's K ids are distinct (top-K), so an expert has at most T <= kDecodeTokens pairs;
+// rows past that bound (repeated ids) are dropped. Ends with a barrier.
+AXK_DEV int decode_rank_rows(const int32_t* __restrict__ ids, int P, int e, int id0, SlotLds& L) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int cnt = 0;
+  for (int p0 = 0; p0 < P; p0 += kStreamThreads) {  // uniform
+    const int p = p0 + tid;
+    const bool hit = p < P && (p0 == 0 ? id0 : ids[min(p, P - 1)]) == e;
+    const unsigned long long b = __ballot(hit);
+    if (lane == 0) L.wcnt[wave] = __popcll(b);
+    __syncthreads();
+    int before = cnt, tot = cnt;
+#pragma unroll
+    for (int w = 0; w < kStreamWaves; ++w) {
+      const int c = L.wcnt[w];
+      before += w < wave ? c : 0;
+      tot += c;
+    }
+    const int r = before + __popcll(b & ((1ull << lane) - 1ull));
+    if (hit && r < kDecodeTokens) L.pair[r] = p;  // more rows than tokens needs repeated ids within a token
+    cnt = tot;
+    __syncthreads();
+  }
+  return min(cnt, kDecodeTokens);
+}
+
+// Stage activation rows [m0, m0 + ROWS) of the slot into LDS as [ROWS][K + 8] bf16 (rows past cnt are skipped).
+// Source row of row m: idx[m] / div (gathered), or m.
+template <int ROWS>
+__device__ void stage_rows(uint16_t* sA, const uint16_t* __restrict__ src, const int* idx, int div, int m0, int cnt,
+                           int K) {
   const int ld = K + 8, units = K / 8;
   const int rows = min(ROWS, cnt - m0);
   for (int i = threadIdx.x; i < rows * units; i += blockDim.x) {
     const int r = i / units, u = i - r * units;
-    const int64_t srow = GATHER ? row_tok[row0 + m0 + r] : (int64_t)(row0 + m0 + r);
+    const int64_t srow = idx ? idx[m0 + r] / div : (int64_t)(m0 + r);
     *reinterpret_cast<uint4*>(sA + r * ld + 8 * u) = *reinterpret_cast<const uint4*>(src + srow * K + 8 * u);
   }
 }
@@ -554,8 +544,9 @@ struct GateUpArgs {
   const uint16_t* h2;  // [T, H]
   const uint8_t *e_gw, *e_gs;
   const uint8_t *sg_w, *sg_s, *su_w, *su_s;  // shared gate / up (nullable: no shared expert)
-  int T, H, F, Fs, max_slots, ngrp, tpw;     // tpw: tiles per wave; ngrp: workgroups per slot
-  int nsp;                                   // grid slots of the shared expert (kStageRows tokens each)
+  const int32_t* ids;  // [T, K] top-K expert ids
+  int T, H, F, Fs, E, K, ngrp, tpw;          // tpw: tiles per wave; ngrp: workgroups per slot
+  int nsp;                                   // grid slots of the shared expert (ROWS tokens each)
   MoeWs w;
 };
 
@@ -568,41 +559,38 @@ struct GateUpArgs {
 // rows per load instruction, which keeps the address path's per-line work low), written to a wave-private LDS tile
 // and read back in the MFMA layout; ROWS activation rows per pass.
 template <bool WIDE, int ROWS, bool STAGE>
-__global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArgs a) {
+__global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a) {
   static_assert(!STAGE || WIDE, "staged weights need whole batches");
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ SlotLds L;
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
   unsigned char* sW = smem + stream_stage_off(ROWS, a.H) + (threadIdx.x >> 6) * kWaveStageBytes;
-  // grid slots [0, nsp): the shared expert, kStageRows tokens each (first, so the shared rows start early);
+  // grid slots [0, nsp): the shared expert, ROWS tokens each (first, so the shared rows start early);
   // slot s >= nsp: active expert s - nsp
   const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
   const bool shared = gslot < a.nsp;
-  const int slot = gslot - a.nsp;
-  int cnt, row0, Fo, mbeg = 0;
+  const int Fo = shared ? a.Fs : a.F;
+  const int ntiles = (Fo + 15) / 16;
+  const int tb = grp * kStreamWaves * a.tpw;
+  if (tb >= ntiles) return;
+  const int P = a.T * a.K;
+  int cnt, mbeg = 0, eid = -1, id0 = -1;
   const uint8_t *gw, *gs, *uw, *us;
   if (shared) {
     mbeg = gslot * ROWS;
     cnt = min(a.T, mbeg + ROWS);
-    row0 = 0;
-    Fo = a.Fs;
     gw = a.sg_w; gs = a.sg_s; uw = a.su_w; us = a.su_s;
   } else {
-    int4 am = a.w.active[slot];  // one 16-byte record; rows 0 past the active list
-    asm volatile("" : "+s"(am.x), "+s"(am.y), "+s"(am.z));  // keep the record's loads together, before the exit
-    cnt = am.x;
-    if (cnt == 0) return;
-    const int64_t e = am.y;
-    row0 = am.z;
-    Fo = a.F;
+    const int e = decode_find_expert(a.ids, P, a.E, gslot - a.nsp, L, id0);
+    if (e < 0) return;  // past the active experts (uniform)
+    eid = e;
+    cnt = -1;           // ranked in the first pass, behind the first weight loads
     const int64_t rows = 2 * (int64_t)a.F;
     gw = a.e_gw + e * rows * (a.H / 2);
     gs = a.e_gs + e * rows * (a.H / 32);
     uw = gw + (int64_t)a.F * (a.H / 2);
     us = gs + (int64_t)a.F * (a.H / 32);
   }
-  const int ntiles = (Fo + 15) / 16;
-  const int tb = grp * kStreamWaves * a.tpw;
-  if (tb >= ntiles) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
   const int H = a.H, ldA = H + 8;
   const int nc = (H + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;  // chunks, batches per tile
@@ -652,7 +640,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
     }
   };
 
-  for (int m0 = mbeg; m0 < cnt; m0 += ROWS) {
+  int m0 = mbeg;
+  do {
     axk_f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
       const int i = st / nb, bi = st - i * nb;
@@ -704,22 +693,23 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
             if (shared)
               a.w.act_sh[(int64_t)m * a.Fs + col] = act;
             else
-              a.w.act[(int64_t)(row0 + m) * a.F + col] = act;
+              a.w.act[(int64_t)L.pair[m] * a.F + col] = act;  // by pair
           }
         }
         accg = accu = axk_f32x4{0.f, 0.f, 0.f, 0.f};
       }
     };
     // three batches in rotation: batch st + 2 is loaded while batch st is used; the first two are issued
-    // before the activation rows are staged, so they overlap the expert's metadata and row gathers
+    // before the activation rows are ranked and staged, so they overlap the slot's grouping and row gathers
     Batch b0, b1, b2;
     __syncthreads();  // the previous pass's readers are done with sA
     load_batch(b0, 0);
     load_batch(b1, 1);
+    if (cnt < 0) cnt = decode_rank_rows(a.ids, P, eid, id0, L);
     if (shared)
-      stage_rows<false, ROWS>(sA, a.h2, nullptr, 0, m0, cnt, H);
+      stage_rows<ROWS>(sA, a.h2, nullptr, 1, m0, cnt, H);
     else
-      stage_rows<true, ROWS>(sA, a.h2, a.w.row_tok, row0, m0, cnt, H);
+      stage_rows<ROWS>(sA, a.h2, L.pair, a.K, m0, cnt, H);  // token = pair / K
     __syncthreads();
     for (int st = 0; st < steps; st += 3) {
       load_batch(b2, st + 2);
@@ -729,51 +719,52 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_gateup_kernel(GateUpArg
       load_batch(b1, st + 4);
       if (st + 2 < steps) proc(b2, st + 2);
     }
-  }
+    m0 += ROWS;
+  } while (m0 < cnt);
 }
 
 struct DownArgs {
   const uint8_t *e_dw, *e_ds;
   const uint8_t *sd_w, *sd_s;
-  int T, H, F, Fs, max_slots, ngrp, tpw, nsp;
+  const int32_t* ids;  // [T, K]
+  const float* wts;    // [T, K] routing weights
+  int T, H, F, Fs, E, K, ngrp, tpw, nsp;
   MoeWs w;
 };
 
 // down: workgroup (slot, run of kStreamWaves * tpw 16-row tiles of H); routed rows scaled by their routing weight.
 template <bool WIDE, int ROWS, bool STAGE>
-__global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a) {
+__global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
   static_assert(!STAGE || WIDE, "staged weights need whole batches");
   extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ SlotLds L;
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
   unsigned char* sW = smem + stream_stage_off(ROWS, a.Fs > a.F ? a.Fs : a.F) + (threadIdx.x >> 6) * kWaveStageBytes;
   const int gslot = blockIdx.x / a.ngrp, grp = blockIdx.x - gslot * a.ngrp;
   const bool shared = gslot < a.nsp;
-  const int slot = gslot - a.nsp;
-  int cnt, row0, K, mbeg = 0;
+  const int ntiles = (a.H + 15) / 16;
+  const int tb = grp * kStreamWaves * a.tpw;
+  if (tb >= ntiles) return;
+  const int P = a.T * a.K;
+  int cnt, K, mbeg = 0, eid = -1, id0 = -1;
   const uint8_t *dw, *ds;
   const uint16_t* act;
   if (shared) {
     mbeg = gslot * ROWS;
     cnt = min(a.T, mbeg + ROWS);
-    row0 = 0;
     K = a.Fs;
     dw = a.sd_w; ds = a.sd_s;
     act = a.w.act_sh;
   } else {
-    int4 am = a.w.active[slot];
-    asm volatile("" : "+s"(am.x), "+s"(am.y), "+s"(am.z));
-    cnt = am.x;
-    if (cnt == 0) return;
-    const int64_t e = am.y;
-    row0 = am.z;
+    const int e = decode_find_expert(a.ids, P, a.E, gslot - a.nsp, L, id0);
+    if (e < 0) return;
+    eid = e;
+    cnt = -1;
     K = a.F;
     dw = a.e_dw + e * (int64_t)a.H * (a.F / 2);
     ds = a.e_ds + e * (int64_t)a.H * (a.F / 32);
     act = a.w.act;
   }
-  const int ntiles = (a.H + 15) / 16;
-  const int tb = grp * kStreamWaves * a.tpw;
-  if (tb >= ntiles) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
   const int ldA = K + 8;
   const int nc = (K + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;
@@ -810,15 +801,26 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
     if (WIDE) load_scale_words(bt.s, ds + n * (K / 32) + 4 * kBatchChunks * bi);
   };
 
-  for (int m0 = mbeg; m0 < cnt; m0 += ROWS) {
+  int m0 = mbeg;
+  do {
+    Batch b0, b1, b2;
+    __syncthreads();
+    load_batch(b0, 0);
+    load_batch(b1, 1);
+    if (cnt < 0) cnt = decode_rank_rows(a.ids, P, eid, id0, L);
+    if (shared)
+      stage_rows<ROWS>(sA, act, nullptr, 1, m0, cnt, K);
+    else
+      stage_rows<ROWS>(sA, act, L.pair, 1, m0, cnt, K);  // activation rows by pair
     float rw[4];
-    int pr[4];  // the rows' pair indices (y is indexed by pair)
+    int pr[4];  // the rows' pair indices (y is indexed by pair); their routing weights are used after the stream
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 4 * g + r;
-      rw[r] = (!shared && m < cnt) ? a.w.row_w[row0 + m] : 1.0f;
-      pr[r] = (!shared && m < cnt) ? a.w.row_pair[row0 + m] : 0;
+      const int m = min(m0 + 4 * g + r, max(cnt - 1, 0));
+      pr[r] = shared ? 0 : L.pair[m];
+      rw[r] = shared ? 1.0f : a.wts[pr[r]];
     }
+    __syncthreads();
     axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
       const int i = st / nb, bi = st - i * nb;
@@ -864,12 +866,6 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
         acc = axk_f32x4{0.f, 0.f, 0.f, 0.f};
       }
     };
-    Batch b0, b1, b2;
-    __syncthreads();
-    load_batch(b0, 0);
-    load_batch(b1, 1);
-    stage_rows<false, ROWS>(sA, act, nullptr, row0, m0, cnt, K);
-    __syncthreads();
     for (int st = 0; st < steps; st += 3) {
       load_batch(b2, st + 2);
       proc(b0, st);
@@ -878,7 +874,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void moe_down_kernel(DownArgs a)
       load_batch(b1, st + 4);
       if (st + 2 < steps) proc(b2, st + 2);
     }
-  }
+    m0 += ROWS;
+  } while (m0 < cnt);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -888,22 +885,30 @@ struct CombineArgs {
   const uint16_t* h2;     // [T, H]
   const uint16_t* x_res;  // [T, H] or null
   const uint16_t* w_shg;  // [H] or null (gate = 1)
-  int has_shared, T, H, K;
+  const float* gate_logit;  // [T] h2 . w_shg from the decode router, or null (computed here)
+  const int32_t* ids;       // [T, K] top-K expert ids
+  int has_shared, T, H, E, K;
   MoeWs w;
   uint16_t* out;  // [T, H]
 };
 
 // Workgroup (token, block of columns), 4 columns per thread and pass: base = x_res + gate * y_sh, + the K routed
 // rows in slot order (y is indexed by pair t K + k; a pair whose id is outside [0, E) selected nothing), one bf16
-// rounding. The first pass's loads are unconditional (clamped) and issued before the shared-gate dot
-// (h2 . w_shg, reduced across the workgroup), so both share one memory round trip. Few tokens: one block per
-// 1024 columns; many tokens: one block per token (the gate is then computed once per token).
-// YB: the routed rows are bf16 (the prefill path's slot outputs), else fp32.
-template <bool YB>
+// rounding. A pass's loads (all KM routed rows, clamped to K) are issued together, before the shared-gate dot
+// (h2 . w_shg, reduced across the workgroup) where the router did not already form it, so they share one memory
+// round trip. Few tokens: one block per 1024 columns; many tokens: one block per token (the gate is then computed
+// once per token). YB: the routed rows are bf16 (the prefill path's slot outputs), else fp32. KM: a bound on K.
+template <bool YB, int KM>
 __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   __shared__ float s_part[4];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t row = (int64_t)t * a.H, pair0 = (int64_t)t * a.K;
+  bool sel[KM];  // pair k selected an expert (uniform over the workgroup)
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    const int e = a.ids[pair0 + min(k, a.K - 1)];
+    sel[k] = k < a.K && e >= 0 && e < a.E;
+  }
   auto gather = [&](int i, float4& acc, float4& ys) {
     acc = make_float4(0.f, 0.f, 0.f, 0.f);
     ys = acc;
@@ -913,18 +918,23 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
                         __uint_as_float(xv.y << 16), __uint_as_float(xv.y & 0xffff0000u));
     }
     if (a.has_shared) ys = *reinterpret_cast<const float4*>(a.w.y_sh + row + i);
-    for (int k = 0; k < a.K; ++k) {
-      float4 yv;
+    float4 yv[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+      const int64_t pr = pair0 + min(k, a.K - 1);
       if constexpr (YB) {
-        const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.w.y) + (pair0 + k) * a.H + i);
-        yv = make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u), __uint_as_float(b.y << 16),
-                         __uint_as_float(b.y & 0xffff0000u));
+        const uint2 b = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.w.y) + pr * a.H + i);
+        yv[k] = make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u),
+                            __uint_as_float(b.y << 16), __uint_as_float(b.y & 0xffff0000u));
       } else {
-        yv = *reinterpret_cast<const float4*>(a.w.y + (pair0 + k) * a.H + i);
+        yv[k] = *reinterpret_cast<const float4*>(a.w.y + pr * a.H + i);
       }
-      if (a.w.pair_pos[pair0 + k] < 0) continue;  // uniform: an id outside [0, E)
-      acc.x += yv.x; acc.y += yv.y; acc.z += yv.z; acc.w += yv.w;
     }
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+      if (sel[k]) {
+        acc.x += yv[k].x; acc.y += yv[k].y; acc.z += yv[k].z; acc.w += yv[k].w;
+      }
   };
   auto finish = [&](int i, float4 acc, const float4& ys, float gate) {
     acc.x += gate * ys.x; acc.y += gate * ys.y; acc.z += gate * ys.z; acc.w += gate * ys.w;
@@ -934,7 +944,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
   float4 acc0, ys0;
   gather(min(i0, a.H - 4), acc0, ys0);
   const bool gated = a.has_shared && a.w_shg;
-  if (gated) {
+  float gate = 1.0f;
+  if (gated && a.gate_logit) {
+    gate = sigmoid_f32(a.gate_logit[t]);
+  } else if (gated) {
     const uint16_t* hrow = a.h2 + row;
     float d = 0.f;
     for (int i = 8 * tid; i < a.H; i += 8 * blockDim.x) {
@@ -949,14 +962,24 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(CombineArgs a) {
     d = wave_sum(d);
     if (lane == 0) s_part[wave] = d;
     __syncthreads();
+    gate = sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]);
   }
-  const float gate = gated ? sigmoid_f32(s_part[0] + s_part[1] + s_part[2] + s_part[3]) : 1.0f;
   if (i0 < a.H) finish(i0, acc0, ys0, gate);
   for (int i = i0 + step; i < a.H; i += step) {
     float4 acc, ys;
     gather(i, acc, ys);
     finish(i, acc, ys, gate);
   }
+}
+
+// The combine launch: routed-row loads unrolled to a bound on K.
+template <bool YB>
+void launch_combine(const CombineArgs& ca, hipStream_t st) {
+  const dim3 grid((unsigned)ca.T, (unsigned)(ca.T >= 1024 ? 1 : (ca.H + 1023) / 1024)), block(256);
+  if (ca.K <= 8)
+    hipLaunchKernelGGL((moe_combine_kernel<YB, 8>), grid, block, 0, st, ca);
+  else
+    hipLaunchKernelGGL((moe_combine_kernel<YB, kMaxTopK>), grid, block, 0, st, ca);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1372,7 +1395,7 @@ extern "C" int axk_moe_route(const float* logits, int32_t* topk_ids, float* topk
 }
 
 namespace {
-// The experts half. grouped: the decode grouping already ran (in the routing launch's last workgroup); check_only: run the
+// The experts half. gate_given: the decode router formed the shared gate's logit in the workspace; check_only: run the
 // contract checks and return before any launch. y_sh_given (optional, with no MXFP4 shared expert): the shared
 // expert's fp32 output [T, H], computed by the caller; the combine gates and adds it as its own.
 int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w_shg, const uint8_t* sh_gate_w,
@@ -1380,7 +1403,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
                      const uint8_t* sh_down_w, const uint8_t* sh_down_s, const uint8_t* e_gw, const uint8_t* e_gs,
                      const uint8_t* e_dw, const uint8_t* e_ds, const int32_t* topk_ids, const float* topk_weights,
                      uint16_t* out, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
-                     int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream, bool grouped,
+                     int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream, bool gate_given,
                      bool check_only, const float* y_sh_given = nullptr) {
   AXK_REQUIRE(h2 && e_gw && e_gs && e_dw && e_ds && topk_ids && topk_weights && out, AXK_E_NULL);
   const bool has_shared = sh_gate_w != nullptr;
@@ -1394,6 +1417,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(!has_shared || shared_inter > 0, AXK_E_SHAPE);
   AXK_REQUIRE(axk_aligned(h2, 16) && axk_aligned(e_gw, 16) && axk_aligned(e_dw, 16), AXK_E_ALIGN);
+  AXK_REQUIRE((!w_shg || axk_aligned(w_shg, 16)) && (!x_res || axk_aligned(x_res, 8)), AXK_E_ALIGN);
   AXK_REQUIRE(!has_shared || (axk_aligned(sh_gate_w, 16) && axk_aligned(sh_up_w, 16) && axk_aligned(sh_down_w, 16)),
               AXK_E_ALIGN);
   const size_t need = axk_moe_workspace_size(tokens, hidden, num_experts, top_k, inter, d.Fs);
@@ -1442,12 +1466,10 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
       hipLaunchKernelGGL((moe_ggemm_kernel<1, true>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
     else
       hipLaunchKernelGGL((moe_ggemm_kernel<1, false>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
-    CombineArgs ca{h2, x_res, w_shg, combine_shared, T, H, K, w, out};
-    hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
-                       dim3(256), 0, st, ca);
+    CombineArgs ca{h2, x_res, w_shg, nullptr, topk_ids, combine_shared, T, H, E, K, w, out};
+    launch_combine<true>(ca, st);
     return axk_launch_status();
   }
-  if (!grouped) hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
   const int max_slots = E < T * K ? E : T * K;
   const int fmax = F > Fs ? F : Fs;
   // runs of 4 x tpw tiles per workgroup; activation rows staged in dynamic LDS ([rows][K + 8] bf16). Small batches
@@ -1463,7 +1485,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
   const int gu_rows = gu_stage ? kSmallRows : kStageRows, dn_rows = dn_stage ? kSmallRows : kStageRows;
   const size_t gu_lds = stream_stage_off(gu_rows, H) + (gu_stage ? kStreamWaves * kWaveStageBytes : 0);
   const size_t dn_lds = stream_stage_off(dn_rows, fmax) + (dn_stage ? kStreamWaves * kWaveStageBytes : 0);
-  AXK_REQUIRE(gu_lds <= kMaxStageLds && dn_lds <= kMaxStageLds, AXK_E_SHAPE);
+  AXK_REQUIRE(gu_lds <= kMaxStreamLds && dn_lds <= kMaxStreamLds, AXK_E_SHAPE);
   static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
   if (!lds_raised) {
     const void* fns[6] = {reinterpret_cast<const void*>(&moe_gateup_kernel<false, kStageRows, false>),
@@ -1473,12 +1495,12 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
                           reinterpret_cast<const void*>(&moe_down_kernel<true, kStageRows, false>),
                           reinterpret_cast<const void*>(&moe_down_kernel<true, kSmallRows, true>)};
     for (const void* f : fns)
-      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStreamLds) != hipSuccess)
         return AXK_E_LAUNCH;
     lds_raised = true;
   }
   const int gu_nsp = has_shared ? (T + gu_rows - 1) / gu_rows : 0, dn_nsp = has_shared ? (T + dn_rows - 1) / dn_rows : 0;
-  GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, T, H, F, Fs, max_slots, gu_grp, gu_tpw,
+  GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, topk_ids, T, H, F, Fs, E, K, gu_grp, gu_tpw,
                 gu_nsp, w};
   const dim3 gu_grid((unsigned)((max_slots + gu_nsp) * gu_grp)), dn_grid((unsigned)((max_slots + dn_nsp) * dn_grp));
   if (gu_stage)
@@ -1487,16 +1509,16 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     hipLaunchKernelGGL((moe_gateup_kernel<true, kStageRows, false>), gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
   else
     hipLaunchKernelGGL((moe_gateup_kernel<false, kStageRows, false>), gu_grid, dim3(64 * kStreamWaves), gu_lds, st, ga);
-  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, T, H, F, Fs, max_slots, dn_grp, dn_tpw, dn_nsp, w};
+  DownArgs da{e_dw, e_ds, sh_down_w, sh_down_s, topk_ids, topk_weights, T, H, F, Fs, E, K, dn_grp, dn_tpw, dn_nsp, w};
   if (dn_stage)
     hipLaunchKernelGGL((moe_down_kernel<true, kSmallRows, true>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   else if (dn_wide)
     hipLaunchKernelGGL((moe_down_kernel<true, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
   else
     hipLaunchKernelGGL((moe_down_kernel<false, kStageRows, false>), dn_grid, dim3(64 * kStreamWaves), dn_lds, st, da);
-  CombineArgs ca{h2, x_res, w_shg, combine_shared, T, H, K, w, out};
-  hipLaunchKernelGGL(moe_combine_kernel<false>, dim3((unsigned)T, (unsigned)(T >= 1024 ? 1 : (H + 1023) / 1024)),
-                     dim3(256), 0, st, ca);
+  // the decode router formed the shared gate's logit when the routing ran in this call (gate_given)
+  CombineArgs ca{h2, x_res, w_shg, gate_given ? w.gate_logit : nullptr, topk_ids, combine_shared, T, H, E, K, w, out};
+  launch_combine<false>(ca, st);
   return axk_launch_status();
 }
 }  // namespace
@@ -1537,26 +1559,22 @@ int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w
   const MoeWs w = moe_ws(workspace, tokens, hidden, num_experts, top_k, inter, sh_gate_w ? shared_inter : 0);
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k;
   const bool prefill = T > kDecodeTokens;
-  const bool grouped = !prefill;  // decode: the routing launch also groups the pairs
-  const int S = prefill ? (int)std::min<int64_t>(kPrefillRouterSplits, hidden / 64) : router_splits(hidden);
   hipStream_t st = axk_stream(stream);
-  // the router as K-slice partial logits in the workspace, summed in slice order by the routing kernel
+  // the router as K-slice partial logits in the workspace (decode: also the shared gate's), summed in slice order
+  // by the routing kernel, which writes the logits and the top-K
+  const int S = prefill ? (int)std::min<int64_t>(kPrefillRouterSplits, hidden / 64) : router_splits(hidden);
+  const bool gate = !prefill && w_shg != nullptr;
   if (prefill)
     hipLaunchKernelGGL(moe_router_tile_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64), (unsigned)S),
                        dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
   else
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16), (unsigned)((T + 15) / 16), (unsigned)S),
-                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart, w.n_active + 1);
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16 + (gate ? 1 : 0)), (unsigned)((T + 15) / 16),
+                       (unsigned)S), dim3(256), 0, st, h2, w_router, w_shg, T, H, E, S, w.rpart, w.gpart);
   const dim3 grid((unsigned)((T + 3) / 4)), block(256);
-#define AXK_ROUTE_PART(V, MS)                                                                                   \
-  do {                                                                                                          \
-    if (grouped)                                                                                                \
-      hipLaunchKernelGGL((moe_route_part_kernel<V, MS, true>), grid, block, 0, st, w.rpart, S, T, E, K,        \
-                         norm_topk_prob, logits, topk_ids, topk_weights, w, w.n_active + 1);                    \
-    else                                                                                                        \
-      hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, S, T, E, K, norm_topk_prob, \
-                         logits, topk_ids, topk_weights, w, nullptr);                                          \
-  } while (0)
+  float* const gp = gate ? w.gpart : nullptr;
+#define AXK_ROUTE_PART(V, MS)                                                                                     \
+  hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, gp, S, T, E, K, norm_topk_prob, \
+                     logits, w.gate_logit, topk_ids, topk_weights)
   if (prefill) {
     if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
     else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
@@ -1575,7 +1593,7 @@ int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w
   if (rc != AXK_OK) return rc;
   return moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
                           e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
-                          shared_inter, workspace, workspace_bytes, stream, grouped, false, y_sh_given);
+                          shared_inter, workspace, workspace_bytes, stream, gate, false, y_sh_given);
 }
 }  // namespace
 
