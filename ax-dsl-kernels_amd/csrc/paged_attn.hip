@@ -5,14 +5,13 @@
 // indices[indptr[b] .. indptr[b+1]); the last one holds last_page_len[b] valid tokens (1..page_size),
 // every other page is full (flash_attn.py:1421-1596 page-id lookup, tail mask 87-104).
 //
-// Up to kLocalPlanBatch sequences over a bf16 cache the split is stream-K (paged_decode_sk_kernel: every workgroup
-// streams the same number of 16-token tiles, its range crossing (sequence, KV head) pairs) and its own merge follows
-// (paged_merge_sk_kernel). Above that, and for the FP8 cache, three kernels partition by items:
+// Three kernels partition the work by items (a stream-K split, every workgroup taking the same number of tiles across
+// (sequence, KV head) pairs, measured slower on both config 1 and the 131,072-token config 4 and was removed):
 //  1. plan   — one wave: pages per split so that the number of (sequence, split, KV head) work items
 //              is about one per resident split workgroup, and one descriptor per item. Depends only on the
 //              page-table shape, so one plan serves every attention layer of a decode step (no host sync,
-//              no memset: graph-capturable). Up to kLocalPlanBatch sequences (the FP8 cache) the split and
-//              merge kernels compute the same partition themselves and no plan launch is needed.
+//              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
+//              compute the same partition themselves and no plan launch is needed.
 //  2. decode — persistent: a few workgroups per CU take the work items in turn. The 4 waves share every
 //              16-token K/V tile of the item's pages: the tile streams HBM -> LDS by direct loads into a
 //              3-deep ring (two tiles in flight while one is computed). Every wave computes the full scores
@@ -688,497 +687,6 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
   for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(o[j] * inv);
 }
 
-// ---- Stream-K split (bf16 cache, batch <= kLocalPlanBatch) ----
-constexpr int kSkBuf = 3;  // LDS ring of tiles of the stream-K split
-// Work units are (sequence, KV head, 16-token tile) triples, in that order. Split workgroup w of W takes the units
-// [w U / W, (w + 1) U / W) of the U in the batch, so every workgroup streams the same number of tiles (to one
-// tile), whatever the sequence lengths. Its range is a run of segments, one per (sequence, KV head) pair it
-// touches; the K / V tiles stream through the LDS ring across segment boundaries without a drain. A segment that
-// covers its whole pair writes the output directly; otherwise it writes an fp32 partial (m, l, O) into slot 2 w
-// (the pair began in an earlier workgroup) or 2 w + 1 (the pair continues in a later one). The merge kernel finds
-// a pair's pieces from the same arithmetic. Only the first and the last segment of a range can be pieces, so
-// 2 W slots suffice.
-
-AXK_DEV long long shfl_up64(long long v, int d) {
-  const int lo = __shfl_up((int)(unsigned)(unsigned long long)v, d, 64);
-  const int hi = __shfl_up((int)(v >> 32), d, 64);
-  return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
-}
-
-AXK_DEV long long readlane64(long long v, int src) {
-  const int lo = __builtin_amdgcn_readlane((int)(unsigned)(unsigned long long)v, src);
-  const int hi = __builtin_amdgcn_readlane((int)(v >> 32), src);
-  return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
-}
-
-// lane b (< batch) of every wave: sequence b
-struct SkTable {
-  int pbeg, np, len, nt;  // first index into `indices`, pages, tokens, 16-token tiles per KV head
-  long long u;            // the sequence's first unit
-  long long total;        // units of the batch (wave-uniform)
-};
-
-// The per-sequence facts from the page table. bias is added to last_page_len: 0 when it counts the valid tokens of
-// the last page (1 .. page_size), 1 when it counts the history only (0 .. page_size - 1) and the current token,
-// already written at the next slot, is attended too (the sgl decode convention, flash_attn.py:2353-2357).
-AXK_DEV SkTable sk_table(const int* __restrict__ indptr, const int* __restrict__ last_page_len, int bias, int batch,
-                         int hkv, int page_size) {
-  const int lane = threadIdx.x & 63;
-  SkTable t;
-  const int p0 = indptr[min(lane, batch)];
-  const int lv = lane < batch ? last_page_len[lane] + bias : 0;
-  const int p1 = __shfl(p0, min(lane + 1, 63), 64);
-  t.pbeg = p0;
-  t.np = lane < batch ? max(p1 - p0, 0) : 0;
-  t.len = t.np > 0 ? (t.np - 1) * page_size + min(max(lv, 0), page_size) : 0;
-  t.nt = (t.len + kTile - 1) / kTile;
-  const long long units = (long long)hkv * t.nt;
-  long long incl = units;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const long long v = shfl_up64(incl, o);
-    if (lane >= o) incl += v;
-  }
-  t.u = incl - units;
-  t.total = readlane64(incl, 63);  // a scalar: the workgroup's range and tile count are wave-uniform
-  return t;
-}
-
-// A position in the unit order. Every field is wave-uniform: sequence facts are read out of lane b with v_readlane
-// (no LDS permute) and the page / tile-in-page pair advances without a division, so the per-tile cursor work is scalar.
-struct SkCur {
-  int b, h, j;             // sequence, KV head, tile of the sequence
-  int p, tp;               // page of the sequence holding tile j, and the tile within that page
-  int nt, len, pbeg, np;   // sequence b's facts
-};
-
-AXK_DEV void sk_seq(SkCur& c, const SkTable& t) {
-  c.nt = __builtin_amdgcn_readlane(t.nt, c.b);
-  c.len = __builtin_amdgcn_readlane(t.len, c.b);
-  c.pbeg = __builtin_amdgcn_readlane(t.pbeg, c.b);
-  c.np = __builtin_amdgcn_readlane(t.np, c.b);
-}
-
-// The unit u (< total): the last sequence with tiles whose first unit is <= u.
-AXK_DEV SkCur sk_at(const SkTable& t, long long u, int batch, int tpp) {
-  const int lane = threadIdx.x & 63;
-  const unsigned long long m = __builtin_amdgcn_ballot_w64(lane < batch && t.nt > 0 && t.u <= u);
-  SkCur c;
-  c.b = 63 - __builtin_clzll(m);
-  sk_seq(c, t);
-  const long long r = u - readlane64(t.u, c.b);
-  c.h = (int)(r / c.nt);
-  c.j = (int)(r - (long long)c.h * c.nt);
-  c.p = c.j / tpp;
-  c.tp = c.j - c.p * tpp;
-  return c;
-}
-
-AXK_DEV void sk_next(SkCur& c, const SkTable& t, int batch, int hkv, int tpp) {
-  if (++c.j < c.nt) {
-    if (++c.tp == tpp) {
-      c.tp = 0;
-      ++c.p;
-    }
-    return;
-  }
-  c.j = 0;
-  c.p = 0;
-  c.tp = 0;
-  if (++c.h < hkv) return;
-  c.h = 0;
-  const int lane = threadIdx.x & 63;
-  const unsigned long long m = __builtin_amdgcn_ballot_w64(lane > c.b && lane < batch && t.nt > 0);
-  if (m) {
-    c.b = __builtin_ctzll(m);
-    sk_seq(c, t);
-  } else {
-    c.b = batch;  // past the last unit
-  }
-}
-
-// The workgroup holding unit u (the last w with w U / W <= u).
-AXK_DEV int sk_wg_of(long long u, long long total, int nwg) { return (int)(((u + 1) * nwg - 1) / total); }
-
-// Page ids of chunk c (256 pages) of sequence b: page 256 c + 64 k + lane in v[k] (0 past the sequence's pages).
-struct SkIds {
-  int v[4];
-  int b, c;
-};
-
-AXK_DEV void sk_load_ids(SkIds& ids, const int* __restrict__ indices, int pbeg, int np) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int p = (ids.c << 8) + 64 * k + lane;
-    const int x = indices[pbeg + min(p, np - 1)];  // np >= 1 for a sequence with tiles
-    ids.v[k] = p < np ? x : 0;
-  }
-}
-
-AXK_DEV int sk_page(const SkIds& ids, int p) {
-  const int k = (p >> 6) & 3, l = p & 63;
-  const int v0 = __builtin_amdgcn_readlane(ids.v[0], l), v1 = __builtin_amdgcn_readlane(ids.v[1], l);
-  const int v2 = __builtin_amdgcn_readlane(ids.v[2], l), v3 = __builtin_amdgcn_readlane(ids.v[3], l);
-  return k == 0 ? v0 : k == 1 ? v1 : k == 2 ? v2 : v3;
-}
-
-// Q of (sequence b, KV head kvh) as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8.
-template <int D>
-AXK_DEV void sk_load_q(axk_bf16x8 (&qb)[D / 32], const uint16_t* __restrict__ q, int b, int kvh, int hq,
-                       int group) {
-  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
-  const bool hv = l16 < group;
-  const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 8 * g;
-#pragma unroll
-  for (int s = 0; s < D / 32; ++s) qb[s] = hv ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void paged_decode_sk_kernel(
-    const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ indptr,
-    const int* __restrict__ last_page_len, const int* __restrict__ indices, int batch, int hq, int hkv,
-    int page_size, int64_t num_pages, float sm_scale, int bias, PlanHeader* __restrict__ hdr,
-    float* __restrict__ part_m, float* __restrict__ part_l, float* __restrict__ part_o, uint16_t* __restrict__ out) {
-  using C = PagedCfg<D>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const SkTable tab = sk_table(indptr, last_page_len, bias, batch, hkv, page_size);
-  const int nwg = gridDim.x, w = blockIdx.x;
-  const long long u0 = (long long)w * tab.total / nwg, u1 = (long long)(w + 1) * tab.total / nwg;
-  const int n = (int)(u1 - u0);  // units (tiles) of this workgroup
-  if (n <= 0) return;
-
-  const int group = hq / hkv;
-  const int tpp = page_size / kTile;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15, g = lane >> 4;
-  const float c = sm_scale * kLog2e;
-  const int64_t row_stride = (int64_t)hkv * D * 2;
-  const int64_t plane_stride = (int64_t)page_size * row_stride;
-  const uint32_t lds0 = lds_addr(smem);
-
-  SkCur ic = sk_at(tab, u0, batch, tpp);  // the next tile to issue
-  SkCur mc = ic;                     // the tile being computed
-  // Page-id chunks: A holds the first tile's; B the next different one in this range's tile order (both loaded
-  // here, so a range that crosses one chunk or pair boundary never waits for ids in the loop).
-  SkIds ida, idb;
-  ida.b = ic.b;
-  ida.c = ic.p >> 8;
-  idb.b = -1;
-  idb.c = -1;
-  int pb_b = 0, np_b = 1;
-  {
-    SkCur cc = ic;
-    int kc = ida.c;
-    long long x = 0;
-    for (int step = 0; step < 8; ++step) {
-      x += min(cc.nt, ((kc + 1) << 8) * tpp) - cc.j;  // to the end of this chunk's run of the pair
-      if (x >= n) break;
-      cc = sk_at(tab, u0 + x, batch, tpp);
-      kc = cc.p >> 8;
-      if (cc.b != ida.b || kc != ida.c) {
-        idb.b = cc.b;
-        idb.c = kc;
-        pb_b = cc.pbeg;
-        np_b = cc.np;
-        break;
-      }
-    }
-  }
-  sk_load_ids(ida, indices, ic.pbeg, ic.np);
-  if (idb.b >= 0) sk_load_ids(idb, indices, pb_b, np_b);
-  // Q of the first segment and of the next one
-  axk_bf16x8 qa[C::KSTEPS], qn[C::KSTEPS];
-  sk_load_q<D>(qa, q, ic.b, ic.h, hq, group);
-  {
-    const int x1 = min(ic.nt - ic.j, n);
-    if (x1 < n) {
-      const SkCur c1 = sk_at(tab, u0 + x1, batch, tpp);
-      sk_load_q<D>(qn, q, c1.b, c1.h, hq, group);
-    } else {
-#pragma unroll
-      for (int s = 0; s < C::KSTEPS; ++s) qn[s] = zero_bf16x8();
-    }
-  }
-  // the compiler takes its waits for these loads here, before the asm loads it cannot count
-#pragma unroll
-  for (int k = 0; k < 4; ++k) asm volatile("" : "+v"(ida.v[k]), "+v"(idb.v[k]));
-#pragma unroll
-  for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qa[s]), "+v"(qn[s]));
-
-  // per-lane byte offsets of this wave's loads inside a tile, and the same clamped to row 0
-  int lane_tok[C::IPW];
-  int64_t lane_off[C::IPW], lane_off0[C::IPW];
-#pragma unroll
-  for (int k = 0; k < C::IPW; ++k) {
-    const int j = wave * C::IPW + k;
-    const int plane = j / C::IPP, blk = j - plane * C::IPP;
-    lane_tok[k] = blk * C::RPI + lane / (C::RB / 16);
-    lane_off0[k] = plane * plane_stride + (lane % (C::RB / 16)) * 16;
-    lane_off[k] = lane_off0[k] + (int64_t)lane_tok[k] * row_stride;
-  }
-  const unsigned char* last_base = cache;
-  int ileft = n;
-  // this wave's share of the next tile's loads into ring buffer nb; returns its valid tokens. Past the range it
-  // re-issues the last tile's first row (in bounds, result unused), so every iteration waits on the same count.
-  auto issue = [&](int nb) -> int {
-    int nvalid = 0;
-    const unsigned char* kbase = last_base;
-    if (ileft > 0) {
-      const int p = ic.p, tp = ic.tp, ch = p >> 8;
-      if (ic.b != ida.b || ch != ida.c) {  // wave-uniform, rare
-        if (ic.b == idb.b && ch == idb.c) {
-          ida = idb;
-          idb.b = -1;
-        } else {
-          ida.b = ic.b;
-          ida.c = ch;
-          sk_load_ids(ida, indices, ic.pbeg, ic.np);
-#pragma unroll
-          for (int k = 0; k < 4; ++k) asm volatile("" : "+v"(ida.v[k]));  // waits inside this branch
-        }
-      }
-      int page = sk_page(ida, p);
-      nvalid = min(kTile, ic.len - ic.j * kTile);
-      if (page < 0 || page >= num_pages) {
-        if (lane == 0) hdr->bad_page = 1;
-        page = 0;
-        nvalid = 0;
-      }
-      kbase = cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)ic.h * D * 2;
-      last_base = kbase;
-      sk_next(ic, tab, batch, hkv, tpp);
-      --ileft;
-    }
-    const int nrow = nvalid > 0 ? nvalid : 1;
-#pragma unroll
-    for (int k = 0; k < C::IPW; ++k) {
-      const int j = wave * C::IPW + k;
-      const int plane = j / C::IPP, blk = j - plane * C::IPP;
-      lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
-                lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK);
-    }
-    return nvalid;
-  };
-
-  axk_f32x4 o[C::DT];
-#pragma unroll
-  for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-
-  auto tile_math = [&](const unsigned char* kt, int nvalid) {
-    const unsigned char* vt = kt + C::PLANE;
-    axk_f32x4 st = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-    const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
-    // every K fragment read first, then two independent MFMA chains (half the dependent chain length)
-    axk_bf16x8 kf[C::KSTEPS];
-#pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s) kf[s] = *reinterpret_cast<const axk_bf16x8*>(krow + 64 * s);
-#pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(kf[s]));  // one wait for all of them
-    axk_f32x4 st1 = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < C::KSTEPS; s += 2) {
-      st = mfma_bf16_16x16x32(kf[s], qa[s], st);
-      if (s + 1 < C::KSTEPS) st1 = mfma_bf16_16x16x32(kf[s + 1], qa[s + 1], st1);
-    }
-    st += st1;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float sv = (4 * g + rr < nvalid) ? st[rr] * c : -INFINITY;
-      st[rr] = sv;
-      mx = fmaxf(mx, sv);
-    }
-    mx = xor32_max(xor16_max(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float psum = 0.f;
-    axk_i16x4 pb;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float p = (4 * g + rr < nvalid) ? __builtin_amdgcn_exp2f(st[rr] - m_new) : 0.f;
-      psum += p;
-      pb[rr] = (short)f32_to_bf16_bits(p);
-    }
-    psum = xor32_sum(xor16_sum(psum));
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < C::DT; ++t) {
-      const axk_i16x4 va =
-          lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (wave * C::DW + 16 * t + 4 * (l16 & 3)) * 2);
-      if (moved) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
-      }
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
-    }
-  };
-
-  // the end of a segment: the pair's output (whole) or a partial in slot `slot`
-  auto finish = [&](int b, int kvh, bool whole, int slot) {
-    const bool hv = l16 < group;
-    if (whole) {
-      const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-      const int64_t ob = ((int64_t)b * hq + kvh * group + l16) * D + wave * C::DW + 4 * g;
-#pragma unroll
-      for (int t = 0; t < C::DT; ++t) {
-        if (!hv) continue;
-        uint2 v;
-        v.x = f32_to_bf16_bits(o[t][0] * inv) | (f32_to_bf16_bits(o[t][1] * inv) << 16);
-        v.y = f32_to_bf16_bits(o[t][2] * inv) | (f32_to_bf16_bits(o[t][3] * inv) << 16);
-        *reinterpret_cast<uint2*>(out + ob + 16 * t) = v;
-      }
-      return;
-    }
-#pragma unroll
-    for (int t = 0; t < C::DT; ++t)
-      if (hv)
-        *reinterpret_cast<float4*>(part_o + ((int64_t)slot * group + l16) * D + wave * C::DW + 16 * t + 4 * g) =
-            make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
-    if (wave == 0 && lane < group) {
-      part_m[(int64_t)slot * group + lane] = m_run;
-      part_l[(int64_t)slot * group + lane] = l_run;
-    }
-  };
-
-  int seg = 0, seg_j0 = mc.j;
-  constexpr int A = kSkBuf - 1;  // tiles in flight while one is computed
-  int nv[A];                     // valid tokens of tiles ti .. ti + A - 1
-#pragma unroll
-  for (int j = 0; j < A; ++j) nv[j] = issue(j);
-  for (int ti = 0; ti < n; ++ti) {
-    const int nb = ti % kSkBuf;
-    wait_vmcnt<(A - 1) * C::IPW>();  // this wave's loads of tile ti have landed (later tiles may not)
-    __builtin_amdgcn_s_barrier();    // ... and every other wave's; all are done with tile ti - 1
-    const int nvn = issue((ti + A) % kSkBuf);  // into the buffer of tile ti - 1
-    const int nvalid = nv[0];
-#pragma unroll
-    for (int j = 0; j + 1 < A; ++j) nv[j] = nv[j + 1];
-    nv[A - 1] = nvn;
-    if (ti > 0 && mc.j == 0) {  // the next pair begins: a new segment
-      ++seg;
-      seg_j0 = 0;
-      if (seg == 1) {
-#pragma unroll
-        for (int s = 0; s < C::KSTEPS; ++s) qa[s] = qn[s];
-      } else {  // a third segment or later (short sequences): load its Q now
-        sk_load_q<D>(qa, q, mc.b, mc.h, hq, group);
-#pragma unroll
-        for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qa[s]));
-      }
-#pragma unroll
-      for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-      m_run = -INFINITY;
-      l_run = 0.f;
-    }
-    if (nvalid > 0) tile_math(smem + nb * C::BUF, nvalid);
-    if (mc.j == mc.nt - 1 || ti == n - 1)
-      finish(mc.b, mc.h, seg_j0 == 0 && mc.j == mc.nt - 1, (seg == 0 && seg_j0 > 0) ? 2 * w : 2 * w + 1);
-    sk_next(mc, tab, batch, hkv, tpp);
-  }
-  wait_vmcnt<0>();  // the look-ahead loads land before the workgroup ends
-}
-
-// One workgroup per (sequence, query head): log-sum-exp merge of the pieces of a (sequence, KV head) pair that the
-// stream-K split spread over several workgroups (the split-KV merge of q35_layer_mc.py:330-349); zero output for a
-// sequence without tokens. Piece i of a pair whose units start at a lies in workgroup wf + i when there are at least as
-// many units as workgroups (every workgroup holds some), else in the workgroup of unit a + i (one unit each); piece 0
-// is in slot 2 wf + 1, the others in slot 2 w.
-template <int D>
-__global__ __launch_bounds__(256) void paged_merge_sk_kernel(const int* __restrict__ indptr,
-                                                             const int* __restrict__ last_page_len, int bias,
-                                                             int batch, int hq, int hkv, int page_size, int nwg,
-                                                             const float* __restrict__ part_m,
-                                                             const float* __restrict__ part_l,
-                                                             const float* __restrict__ part_o,
-                                                             uint16_t* __restrict__ out) {
-  constexpr int V = D / 64;  // output columns per lane
-  __shared__ float s_m[4], s_l[4];
-  __shared__ float s_acc[4][D];
-  const int b = blockIdx.x / hq, h = blockIdx.x - (blockIdx.x / hq) * hq;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int group = hq / hkv, kvh = h / group, hh = h - kvh * group;
-  const SkTable tab = sk_table(indptr, last_page_len, bias, batch, hkv, page_size);
-  const int nt = __builtin_amdgcn_readlane(tab.nt, b);
-  uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
-  if (nt == 0) {
-    if (wave == 0) {
-#pragma unroll
-      for (int j = 0; j < V; ++j) op[j] = 0;
-    }
-    return;
-  }
-  const long long total = tab.total;
-  const long long a = readlane64(tab.u, b) + (long long)kvh * nt;
-  const int wf = sk_wg_of(a, total, nwg), wl = sk_wg_of(a + nt - 1, total, nwg);
-  if (wf == wl) return;  // one workgroup held the whole pair and wrote its output
-  const bool dense = total >= nwg;
-  const int npieces = dense ? wl - wf + 1 : nt;
-  auto slot_of = [&](int i) -> int64_t {
-    const int wg = dense ? wf + i : sk_wg_of(a + i, total, nwg);
-    return i == 0 ? 2 * (int64_t)wg + 1 : 2 * (int64_t)wg;
-  };
-  constexpr int P = 16;
-  float mm = -INFINITY, ll = 0.f, acc[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) acc[j] = 0.f;
-  for (int c0 = wave; c0 < npieces; c0 += 4 * P) {
-    float mi[P], li[P], oi[P][V];
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-      const int64_t sl = slot_of(min(c0 + 4 * k, npieces - 1));  // clamped: in bounds, weight zeroed below
-      mi[k] = part_m[sl * group + hh];
-      li[k] = part_l[sl * group + hh];
-      const float* src = part_o + (sl * group + hh) * D + lane * V;
-#pragma unroll
-      for (int j = 0; j < V; ++j) oi[k][j] = src[j];
-    }
-    float cm = mm;
-#pragma unroll
-    for (int k = 0; k < P; ++k)
-      if (c0 + 4 * k < npieces) cm = fmaxf(cm, mi[k]);
-    const float sc = mm == -INFINITY ? 0.f : exp2f(mm - cm);
-    ll *= sc;
-#pragma unroll
-    for (int j = 0; j < V; ++j) acc[j] *= sc;
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-      const float wk = (c0 + 4 * k < npieces && mi[k] != -INFINITY) ? exp2f(mi[k] - cm) : 0.f;
-      ll += wk * li[k];
-#pragma unroll
-      for (int j = 0; j < V; ++j) acc[j] += wk * oi[k][j];
-    }
-    mm = cm;
-  }
-  if (lane == 0) {
-    s_m[wave] = mm;
-    s_l[wave] = ll;
-  }
-#pragma unroll
-  for (int j = 0; j < V; ++j) s_acc[wave][lane * V + j] = acc[j];
-  __syncthreads();
-  if (wave != 0) return;
-  float M = -INFINITY;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) M = fmaxf(M, s_m[k]);
-  float L = 0.f, o[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) o[j] = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float f = s_m[k] == -INFINITY ? 0.f : exp2f(s_m[k] - M);
-    L += f * s_l[k];
-#pragma unroll
-    for (int j = 0; j < V; ++j) o[j] += f * s_acc[k][lane * V + j];
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-#pragma unroll
-  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(o[j] * inv);
-}
-
 // cache[loc[b,0], 0, loc[b,1], kvh, :] = k[b, kvh, :]; plane 1 <- v (store_paged_kv, flash_attn.py:53-84).
 __global__ __launch_bounds__(256) void paged_kv_write_kernel(const uint16_t* __restrict__ k,
                                                              const uint16_t* __restrict__ v,
@@ -1591,43 +1099,10 @@ int split_grid(int batch, int hkv) {
   return (int)(items < slots ? items : slots);
 }
 
-// The stream-K split serves a bf16 cache up to kLocalPlanBatch sequences; larger batches and the FP8 cache take the
-// item partition of the plan.
-inline bool use_sk(int batch, int kb) { return kb == 2 && batch <= kLocalPlanBatch; }
-
-// Workgroups of the stream-K split: the split grid, bounded so its 2 W partial slots fit the workspace.
-int sk_grid(int batch, int hkv) {
-  const int half = (int)(ws_items_max(batch, hkv) / 2);
-  const int g = split_grid(batch, hkv);
-  return g < half ? g : half;
-}
-
-template <int D>
-int launch_split_sk(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
-                    uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                    int bias, void* ws, hipStream_t st) {
-  const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
-  const size_t lds = (size_t)kSkBuf * PagedCfg<D>::BUF;
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_sk_kernel<D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
-  hipLaunchKernelGGL((paged_decode_sk_kernel<D>), dim3((unsigned)sk_grid(batch, hkv)), dim3(64 * kWaves), lds, st,
-                     q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv, page_size,
-                     num_pages, sm_scale, bias, v.hdr, v.pm, v.pl, v.po, out);
-  return axk_launch_status();
-}
-
 template <int D, int KB = 2, int QM = 0>
 int launch_split(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
                  uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
                  void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr) {
-  if (use_sk(batch, KB))
-    return launch_split_sk<D>(q, cache, indptr, last, indices, out, batch, hq, hkv, page_size, num_pages, sm_scale,
-                              bias, ws, st);
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
   // the ring of landed tiles; an FP8 cache: a ring of 5 landing slots (kNBuf8) and two bf16 staging tiles
@@ -1652,11 +1127,6 @@ template <int D>
 int launch_merge(const int* indptr, const int* last, uint16_t* out, int batch, int hq, int hkv, int page_size,
                  void* ws, hipStream_t st, int kb = 2, int bias = 0) {
   const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
-  if (use_sk(batch, kb)) {
-    hipLaunchKernelGGL((paged_merge_sk_kernel<D>), dim3((unsigned)(batch * hq)), dim3(256), 0, st, indptr, last, bias,
-                       batch, hq, hkv, page_size, sk_grid(batch, hkv), v.pm, v.pl, v.po, out);
-    return axk_launch_status();
-  }
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
   hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)(batch * hq)), dim3(256), 0, st, indptr, last, v.hdr,
                      v.item_off, batch, hq, hkv, split_grid(batch, hkv), local, bias, v.pm, v.pl, v.po, out);
@@ -1690,7 +1160,8 @@ int check_ws(void* workspace, size_t workspace_bytes, int64_t batch, int64_t hq,
   return workspace && workspace_bytes >= need && axk_aligned(workspace, 256) ? AXK_OK : AXK_E_WORKSPACE;
 }
 
-// The plan (launched only for the item partition of large batches). bias as in sk_table.
+// The plan (launched only above kLocalPlanBatch sequences). bias: 0 when last_page_len counts the valid tokens of
+// the last page, 1 when it counts the history only and the current token (written at the next slot) is attended too.
 int decode_plan(const int32_t* indptr, const int32_t* last_page_len, int64_t batch, int64_t hq, int64_t hkv,
                 int64_t d, int64_t page_size, int kb, int bias, void* workspace, size_t workspace_bytes,
                 hipStream_t st) {

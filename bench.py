@@ -252,7 +252,7 @@ class PagedDecodeWorkload(Workload):
     """
 
     name = "paged_decode"
-    kernel = "paged_decode_sk_kernel<256>"  # launched by axk_paged_decode_split
+    kernel = "paged_decode_kernel<256, 2, 0>"  # launched by axk_paged_decode_split
     timing = "graph"       # value: K steps (plan + split + merge) replayed as one HIP graph
     traffic_profile = "paged_decode_config1_pmc.txt"
 

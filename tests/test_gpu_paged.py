@@ -211,8 +211,9 @@ def test_kv_write_fp8_bytes(dev):
     assert torch.equal(got.cpu(), ref)
 
 
-# ---- the stream-K partition's edge cases (batch <= 63): many segments per workgroup, fewer tiles than workgroups,
-# tails that are not whole tiles, page-id chunks of 256 pages crossed inside a sequence, odd KV-head counts ----
+# ---- the local item partition's edge cases (batch <= 63, the kernels derive the plan themselves): many items per
+# workgroup, fewer pages than workgroups, tails that are not whole tiles, long sequences split into many items, odd
+# KV-head counts ----
 @pytest.mark.parametrize(
     "lens,hq,hkv,d,page",
     [
@@ -224,7 +225,7 @@ def test_kv_write_fp8_bytes(dev):
         ([100000], 16, 2, 256, 64),                          # one long sequence over every workgroup
     ],
 )
-def test_paged_decode_stream_k_partition(dev, lens, hq, hkv, d, page):
+def test_paged_decode_local_partition(dev, lens, hq, hkv, d, page):
     g = torch.Generator().manual_seed(len(lens) * 7 + hkv)
     c = configs.paged_case(lens, hq, hkv, d, page, g, extra_pages=1)
     print(f"case lens={lens[:6]}.. hq={hq} hkv={hkv} d={d} page={page}", flush=True)
@@ -235,8 +236,8 @@ def test_paged_decode_stream_k_partition(dev, lens, hq, hkv, d, page):
             assert not got[b].any()
 
 
-def test_stream_k_garbage_workspace_and_changing_partitions(dev):
-    """The stream-K split and merge keep nothing in the workspace from one call to the next: a workspace of random
+def test_local_plan_garbage_workspace_and_changing_partitions(dev):
+    """The split and merge keep nothing in the workspace from one call to the next: a workspace of random
     bytes, then calls whose partitions differ (other lengths, so other pieces per pair) on that same workspace, each
     against the oracle and bit-identical to the same call on a fresh zeroed workspace."""
     g = torch.Generator().manual_seed(77)
@@ -252,7 +253,7 @@ def test_stream_k_garbage_workspace_and_changing_partitions(dev):
         torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
 
 
-def test_stream_k_graph_replays_with_new_page_tables(dev):
+def test_local_plan_graph_replays_with_new_page_tables(dev):
     """A captured decode (split + merge) replayed with the page table rewritten in place between replays (lengths
     change, so the partition the kernels derive changes): every replay equals the eager call, with eager calls on the
     same workspace in between."""
@@ -344,7 +345,7 @@ def test_paged_attention_decode_sgl_convention(dev, history):
 
 def test_paged_attention_decode_sgl_convention_matches_paged_decode(dev):
     """History-only last_page_len (+ the written current token) == axk_paged_decode with last_page_len + 1, for a
-    batch that takes the stream-K split (16) and one that takes the plan kernel's items (70)."""
+    batch whose kernels derive the partition themselves (16) and one that takes the plan kernel's items (70)."""
     for bsz in (16, 70):
         g = torch.Generator().manual_seed(bsz)
         hist = [int(x) for x in torch.randint(0, 3000, (bsz,), generator=g)]
