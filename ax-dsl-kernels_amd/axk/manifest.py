@@ -48,7 +48,15 @@ BANKS = {
 EXPERT_IO = ("e_gw", "e_gs", "e_dw", "e_ds")
 
 
-def storage_bytes(dtype: int, shape) -> int:
+def check_dtype(dtype: int, name: Optional[str] = None) -> None:
+    """Raise ValueError naming the IO for an AX dtype code axk does not take (0: the committed 35B manifest gives it to
+    its bf16 KV-cache outputs; the reference's ONNX table, tools/manifest/onnx_io.py:18-29, has no entry for it)."""
+    if dtype not in DT_TORCH:
+        raise ValueError(f"IO {name or '?'}: AX dtype code {dtype} is not one axk handles ({sorted(DT_TORCH)})")
+
+
+def storage_bytes(dtype: int, shape, name: Optional[str] = None) -> int:
+    check_dtype(dtype, name)
     n = 1
     for d in shape:
         n *= int(d)
@@ -224,8 +232,9 @@ def _u8(t: torch.Tensor) -> torch.Tensor:
     return t.reshape(-1).view(torch.uint8)
 
 
-def _typed(raw: torch.Tensor, dtype: int, shape) -> torch.Tensor:
+def _typed(raw: torch.Tensor, dtype: int, shape, name: Optional[str] = None) -> torch.Tensor:
     """u8 storage -> the tensor axk takes for an IO of AX dtype `dtype` and logical shape `shape`."""
+    check_dtype(dtype, name)
     return raw.view(DT_TORCH[dtype]).view(storage_shape(dtype, shape))
 
 
@@ -325,7 +334,7 @@ class Manifest:
             t = buffers[name]
             per = e.bytes // e.shape[0]
             raw = _u8(t)[block * per:(block + 1) * per]
-            out[param] = _typed(raw, e.dtype, e.shape[1:])
+            out[param] = _typed(raw, e.dtype, e.shape[1:], e.name)
         for part in ("w_", "s_"):  # the GDN's q / k / v row blocks -> w_qkv / s_qkv
             parts = [out.pop(part + g, None) for g in ("gq", "gk", "gv")]
             if all(p is not None for p in parts):
@@ -354,13 +363,13 @@ class Manifest:
             if p is None:
                 raise ValueError(f"{m.name}: no parameter {m.param!r} of kind {kind}")
             raw = _u8(buffers[m.pack])[m.offset:m.offset + m.bytes]
-            w[m.param] = _typed(m.to_row_major(raw).reshape(-1), p.dtype, p.shape)
+            w[m.param] = _typed(m.to_row_major(raw).reshape(-1), p.dtype, p.shape, m.param)
         w.update(self._banks(k, buffers, layer, kind))
         for base in EXPERT_IO:  # a MoE layer's routed experts: IO e_gw<j> .. of the group (mkmanifest.py:326-336)
             name = f"{base}{layer}"
             if any(e.name == name for e in k.inputs):
                 e = k.entry(name)
-                w[base] = _typed(_u8(buffers[name]), e.dtype, e.shape)
+                w[base] = _typed(_u8(buffers[name]), e.dtype, e.shape, name)
         missing = [n for n in params if n not in w]
         if missing:
             raise ValueError(f"{role} layer {layer} ({kind}): parameters not found in packs or banks: {missing}")

@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "axk.h"
 
 #define AXK_REQUIRE(cond, code) \
@@ -25,6 +28,29 @@ static inline bool axk_overlap(const void* a, size_t na, const void* b, size_t n
 }
 
 static inline hipStream_t axk_stream(axk_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// A one-time host step (raising a kernel's dynamic-LDS limit) that is retried until it succeeds once, safe when
+// several host threads make their first call together.
+struct AxkOnce {
+  std::atomic<bool> done{false};
+  std::mutex mu;
+};
+// Runs fn (returning hipError_t) unless an earlier call succeeded; AXK_OK, or AXK_E_LAUNCH when fn fails.
+template <class Fn>
+static inline int axk_once(AxkOnce& once, Fn&& fn) {
+  if (once.done.load(std::memory_order_acquire)) return AXK_OK;
+  std::lock_guard<std::mutex> lock(once.mu);
+  if (once.done.load(std::memory_order_relaxed)) return AXK_OK;
+  if (fn() != hipSuccess) return AXK_E_LAUNCH;
+  once.done.store(true, std::memory_order_release);
+  return AXK_OK;
+}
+// A kernel's dynamic-LDS limit raised to `bytes` once per process.
+static inline int axk_raise_lds(AxkOnce& once, const void* kernel, size_t bytes) {
+  return axk_once(once, [&] {
+    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  });
+}
 
 // Validate-only mode of the calling thread: while it is set, entry points run every argument check and return
 // AXK_OK just before their first launch. The composed layer entry points run their whole call sequence once this way

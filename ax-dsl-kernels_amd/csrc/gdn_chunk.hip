@@ -679,13 +679,9 @@ int chunk_prefill_impl(const uint16_t* q, const uint16_t* k, const uint16_t* v, 
   const ChunkWs ws = chunk_ws(workspace, batch, num_k_heads, num_v_heads, NC);
   AXK_LAUNCH_GATE();
   hipStream_t st = axk_stream(stream);
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gdn_chunk_prep_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kPrepLds) != hipSuccess)
-      return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
+  static AxkOnce lds_once;  // > 64 KiB of dynamic LDS must be allowed once
+  if (const int rc = axk_raise_lds(lds_once, reinterpret_cast<const void*>(&gdn_chunk_prep_kernel), kPrepLds))
+    return rc;
   const int kdiv = v_order == AXK_VORDER_TILED ? 1 : (int)(num_v_heads / num_k_heads);
   PrepArgs pa{q, k, v, a, b, a_log, dt_bias, ws, (int)batch, (int)tokens, (int)num_k_heads, (int)num_v_heads, NC,
               ldq, ldk, ldv, kdiv};

@@ -1444,17 +1444,19 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     const bool sdma0 = H % 128 == 0 && a4(e_gs) && a4(sh_gate_s) && a4(sh_up_s);
     const bool sdma1 = F % 128 == 0 && Fs % 128 == 0 && a4(e_ds) && a4(sh_down_s);
     const size_t lds0 = gemm_lds_bytes(H, sdma0), lds1 = gemm_lds_bytes(fmax, sdma1);
-    static bool gemm_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-    if (!gemm_raised) {
+    static AxkOnce gemm_once;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+    const int raised = axk_once(gemm_once, [] {
       const void* fns[4] = {reinterpret_cast<const void*>(&moe_ggemm_kernel<0, false>),
                             reinterpret_cast<const void*>(&moe_ggemm_kernel<1, false>),
                             reinterpret_cast<const void*>(&moe_ggemm_kernel<0, true>),
                             reinterpret_cast<const void*>(&moe_ggemm_kernel<1, true>)};
-      for (const void* f : fns)
-        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds) != hipSuccess)
-          return AXK_E_LAUNCH;
-      gemm_raised = true;
-    }
+      for (const void* f : fns) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStageLds);
+        if (e != hipSuccess) return e;
+      }
+      return hipSuccess;
+    });
+    if (raised != AXK_OK) return raised;
     const unsigned nb0 = (unsigned)((fmax + kG2Cols0 - 1) / kG2Cols0), nb1 = (unsigned)((H + kG2Cols1 - 1) / kG2Cols1);
     auto xgrid = [](unsigned n) { return dim3((n + kXcds - 1) / kXcds * kXcds); };  // whole rounds over the XCDs
     if (sdma0)
@@ -1486,19 +1488,21 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
   const size_t gu_lds = stream_stage_off(gu_rows, H) + (gu_stage ? kStreamWaves * kWaveStageBytes : 0);
   const size_t dn_lds = stream_stage_off(dn_rows, fmax) + (dn_stage ? kStreamWaves * kWaveStageBytes : 0);
   AXK_REQUIRE(gu_lds <= kMaxStreamLds && dn_lds <= kMaxStreamLds, AXK_E_SHAPE);
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-  if (!lds_raised) {
+  static AxkOnce lds_once;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  const int raised = axk_once(lds_once, [] {
     const void* fns[6] = {reinterpret_cast<const void*>(&moe_gateup_kernel<false, kStageRows, false>),
                           reinterpret_cast<const void*>(&moe_gateup_kernel<true, kStageRows, false>),
                           reinterpret_cast<const void*>(&moe_gateup_kernel<true, kSmallRows, true>),
                           reinterpret_cast<const void*>(&moe_down_kernel<false, kStageRows, false>),
                           reinterpret_cast<const void*>(&moe_down_kernel<true, kStageRows, false>),
                           reinterpret_cast<const void*>(&moe_down_kernel<true, kSmallRows, true>)};
-    for (const void* f : fns)
-      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStreamLds) != hipSuccess)
-        return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
+    for (const void* f : fns) {
+      const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxStreamLds);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  });
+  if (raised != AXK_OK) return raised;
   const int gu_nsp = has_shared ? (T + gu_rows - 1) / gu_rows : 0, dn_nsp = has_shared ? (T + dn_rows - 1) / dn_rows : 0;
   GateUpArgs ga{h2, e_gw, e_gs, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, topk_ids, T, H, F, Fs, E, K, gu_grp, gu_tpw,
                 gu_nsp, w};

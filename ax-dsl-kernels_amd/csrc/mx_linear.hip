@@ -625,13 +625,9 @@ bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv, const MxGroup& g) {
 
 template <int F, int EPI>
 int dg_launch(const DgArgs& d, hipStream_t st) {
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mx_gemm_kernel<F, EPI>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-      return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
+  static AxkOnce lds_once;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  if (const int rc = axk_raise_lds(lds_once, reinterpret_cast<const void*>(&mx_gemm_kernel<F, EPI>), 160 * 1024))
+    return rc;
   constexpr int COLS = EPI == EPI_SWIGLU ? kDgBN / 2 : kDgBN;
   const int64_t nb = EPI == EPI_PLAIN ? d.cb0[d.count] : ((int64_t)d.n[0] + COLS - 1) / COLS;
   const int64_t tiles = nb * (((int64_t)d.m + dg_bm<F>() - 1) / dg_bm<F>());

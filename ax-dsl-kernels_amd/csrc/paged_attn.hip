@@ -1046,13 +1046,8 @@ int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, c
   const int64_t grid = xph ? 8 * ((nblk + xph - 1) / xph) : nblk * hkv;
   if (grid > 0x7fffffff) return AXK_E_SHAPE;
   const size_t lds = (size_t)kPfBuf * PagedCfg<D>::BUF;
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_prefill_kernel<D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
+  static AxkOnce lds_once;  // > 64 KiB of dynamic LDS must be allowed once per kernel
+  if (const int rc = axk_raise_lds(lds_once, reinterpret_cast<const void*>(&paged_prefill_kernel<D>), lds)) return rc;
   AXK_LAUNCH_GATE();
   hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid), dim3(64 * kPfWaves), lds, st, q,
                      static_cast<const unsigned char*>(cache), qo_indptr, indptr, last, indices, batch, total_q, hq,
@@ -1099,22 +1094,29 @@ int split_grid(int batch, int hkv) {
   return (int)(items < slots ? items : slots);
 }
 
+// The split kernel's dynamic LDS: the ring of landed tiles; an FP8 / INT8 cache: a ring of 5 landing slots and two
+// bf16 staging tiles (INT8: and the scales' ring).
+template <int D, int KB, int QM>
+constexpr size_t split_lds() {
+  return KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF + (QM == 1 ? 5 * 1024 : 0)
+                 : (size_t)kNBuf * PagedCfg<D>::BUF;
+}
+
+// Allows the split kernel its dynamic LDS (above 64 KiB), once per process.
+template <int D, int KB, int QM>
+int raise_split_lds() {
+  static AxkOnce once;
+  return axk_raise_lds(once, reinterpret_cast<const void*>(&paged_decode_kernel<D, KB, QM>), split_lds<D, KB, QM>());
+}
+
 template <int D, int KB = 2, int QM = 0>
 int launch_split(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
                  uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
                  void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
-  // the ring of landed tiles; an FP8 cache: a ring of 5 landing slots (kNBuf8) and two bf16 staging tiles
-  const size_t lds = KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF + (QM == 1 ? 5 * 1024 : 0)
-                              : (size_t)kNBuf * PagedCfg<D>::BUF;
-  static bool lds_raised = false;  // > 64 KiB of dynamic LDS must be allowed once per kernel
-  if (!lds_raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&paged_decode_kernel<D, KB, QM>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return AXK_E_LAUNCH;
-    lds_raised = true;
-  }
+  constexpr size_t lds = split_lds<D, KB, QM>();
+  if (const int rc = raise_split_lds<D, KB, QM>()) return rc;
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
   hipLaunchKernelGGL((paged_decode_kernel<D, KB, QM>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves),
                      lds, st, q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv,
@@ -1329,12 +1331,32 @@ extern "C" int axk_paged_decode_noalloc(const uint16_t* q, const uint16_t* kv_ca
                                         const int32_t* indices, const int32_t* last_page_len, uint16_t* out,
                                         int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
                                         int64_t page_size, int64_t num_pages, float sm_scale, axk_stream_t stream) {
-  const int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
+  int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
   const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
   AXK_REQUIRE(need <= AXK_PAGED_NOALLOC_SCRATCH_BYTES, AXK_E_SCRATCH);
+  // The one-time set-up (this device's scratch address, the split kernel's LDS limit) is host work that must not
+  // happen inside a stream capture: a first call on a device while its stream is capturing returns AXK_E_LAUNCH and
+  // enqueues nothing (make one eager call first).
+  {
+    int dev = -1;
+    bool ready = hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices;
+    if (ready) {
+      std::lock_guard<std::mutex> lock(g_scratch_mu);
+      ready = g_scratch[dev] != nullptr;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    AXK_REQUIRE(hipStreamIsCapturing(axk_stream(stream), &cs) == hipSuccess, AXK_E_LAUNCH);
+    AXK_REQUIRE(ready || cs == hipStreamCaptureStatusNone, AXK_E_LAUNCH);
+  }
   void* ws = scratch_ptr();
   AXK_REQUIRE(ws, AXK_E_LAUNCH);
+  switch (head_dim) {  // the split kernel's LDS limit, raised here (outside any capture) rather than at its launch
+    case 64: rc = raise_split_lds<64, 2, 0>(); break;
+    case 128: rc = raise_split_lds<128, 2, 0>(); break;
+    default: rc = raise_split_lds<256, 2, 0>(); break;
+  }
+  if (rc != AXK_OK) return rc;
   return decode_all(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim,
                     page_size, num_pages, sm_scale, 0, ws, AXK_PAGED_NOALLOC_SCRATCH_BYTES, axk_stream(stream));
 }

@@ -22,7 +22,20 @@ for _p in (ROOT, os.path.join(ROOT, "ax-dsl-kernels_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFS = 2500.0  # dense bf16 MFMA
+BF16_PEAK_TFS = 2500.0  # dense MFMA peaks of MI355X: bf16, fp8, fp4 (the kernels compute in bf16)
+FP8_PEAK_TFS = 5000.0
+FP4_PEAK_TFS = 10100.0
+
+
+def mfma_fracs(tflops: float) -> dict:
+    """Achieved TFLOP/s as fractions of the dense bf16, fp8 and fp4 MFMA peaks."""
+    return {"bf16_mfma_frac": round(tflops / BF16_PEAK_TFS, 4), "fp8_mfma_frac": round(tflops / FP8_PEAK_TFS, 4),
+            "fp4_mfma_frac": round(tflops / FP4_PEAK_TFS, 4)}
+
+
+def tokens_per_s(wl, ms_per_step: float):
+    """Tokens per second through the path: the step's tokens over its time (None for a workload without tokens)."""
+    return round(wl.tokens / (ms_per_step * 1e-3), 1) if wl.tokens else None
 ROTATE_BYTES = 1 << 30
 METRIC = "µs/decode-layer + achieved HBM GB/s (% of 8 TB/s) for MXFP4 MoE + paged attn"
 
@@ -81,6 +94,7 @@ class Workload:
 
     in_suite = True
     traffic_profile = None  # profiles/ file holding the kernel's measured HBM bytes per launch
+    tokens = None  # tokens one step carries through the path (decode: one per sequence; prefill: the chunk)
 
     def pre(self, i: int) -> None:
         pass
@@ -96,6 +110,7 @@ class MxLinearWorkload(Workload):
     """Config 0: one MXFP4 linear, W 4096 x 4096 (E2M1 + E8M0), x bf16 [1, 4096], bf16 out."""
 
     name = "mxfp4_linear"
+    tokens = 1  # tokens one step carries through the path
     kernel = "mx_group_kernel"
     timing = "graph"
     traffic_profile = "mxfp4_linear_config0_pmc.txt"
@@ -144,6 +159,7 @@ class MxLinearPrefillWorkload(Workload):
     in registers, the activations are bf16)."""
 
     name = "mxfp4_linear_prefill"
+    tokens = 4096  # tokens one step carries through the path
     kernel = "mx_gemm_kernel<0, 0>"
     timing = "graph"
     mfma = True
@@ -199,6 +215,7 @@ class LmHeadWorkload(Workload):
     x bf16 [1, 2048], fp32 logits (mul_mat_mx4_n248320_k2048, q35_layer_mc.py:705-724)."""
 
     name = "lm_head"
+    tokens = 1  # tokens one step carries through the path
     kernel = "mx_group_kernel<0, 1, 4, 0, 4>"
     timing = "graph"
     traffic_profile = "lm_head_vocab248320_pmc.txt"
@@ -252,6 +269,7 @@ class PagedDecodeWorkload(Workload):
     """
 
     name = "paged_decode"
+    tokens = 16  # tokens one step carries through the path
     kernel = "paged_decode_kernel<256, 2, 0>"  # launched by axk_paged_decode_split
     timing = "graph"       # value: K steps (plan + split + merge) replayed as one HIP graph
     traffic_profile = "paged_decode_config1_pmc.txt"
@@ -329,6 +347,29 @@ class PagedDecodeWorkload(Workload):
                 "sample": f"full config1 op (oracle/paged_attn.py, torch fp32 CPU), median of {reps} runs"}
 
 
+def encode_cache(cache, dev, kind: str, kv_scale: float = 1.0):
+    """A bf16 paged cache [P, 2, page, HKV, D] written whole through the product's KV write kernels (every (page, slot)
+    row as one cache_location): the FP8 cache's codes, or the INT8 cache's (codes, scales)."""
+    import torch
+
+    from axk import attention
+
+    p, _, page, hkv, d = cache.shape
+    rows = p * page
+    k = cache[:, 0].reshape(rows, hkv, d).contiguous().to(dev)
+    v = cache[:, 1].reshape(rows, hkv, d).contiguous().to(dev)
+    loc = torch.stack([torch.arange(p).repeat_interleave(page), torch.arange(page).repeat(p)], 1)
+    loc = loc.to(torch.int32).contiguous().to(dev)
+    if kind == "fp8":
+        codes = torch.zeros(p, 2, page, hkv, d, dtype=torch.uint8, device=dev)
+        attention.store_paged_kv_fp8(k, v, codes, loc, kv_scale)
+        return codes
+    codes = torch.zeros(p, 2, page, hkv, d, dtype=torch.int8, device=dev)
+    scales = torch.zeros(p, 2, page, hkv, dtype=torch.bfloat16, device=dev)
+    attention.store_paged_kv_i8(k, v, codes, scales, loc)
+    return codes, scales
+
+
 class PagedDecodeFp8Workload(Workload):
     """Config 1's attention over an FP8 E4M3 cache (the FP8 cache, KV8 = 2, q35_group.py:44-54): the same
     sequences, pages and queries, the cache stored as e4m3(bf16(x * 8)). One step = axk_paged_decode_fp8 (plan +
@@ -336,6 +377,7 @@ class PagedDecodeFp8Workload(Workload):
     (half of bf16's) + q + out + page table."""
 
     name = "paged_decode_fp8kv"
+    tokens = 16  # tokens one step carries through the path
     kernel = "paged_decode_kernel<256, 1> (+ merge)"
     timing = "graph"
     traffic_profile = "paged_decode_fp8kv_config1_pmc.txt"  # every kernel of the op, summed
@@ -345,7 +387,6 @@ class PagedDecodeFp8Workload(Workload):
         import torch
 
         from axk import attention, configs
-        from oracle import paged_attn
 
         c = configs.config1()
         self.host = c
@@ -355,7 +396,7 @@ class PagedDecodeFp8Workload(Workload):
         npages = int(c["indptr"][-1])
         self.alg_bytes = tot * 2 * hkv * d + 2 * b * hq * d * 2 + 4 * (npages + 2 * b + 1)
         self.alg_flops = 4 * tot * hq * d
-        codes = paged_attn.quant_kv_fp8(c["cache"], self.KV_SCALE).to(dev)
+        codes = encode_cache(c["cache"], dev, "fp8", self.KV_SCALE)
         self.copies = max(2, -(-ROTATE_BYTES // codes.numel()))
         self.caches = [codes] + [codes.clone() for _ in range(self.copies - 1)]
         self.q = c["q"].to(dev)
@@ -397,6 +438,7 @@ class PagedDecodeI8Workload(PagedDecodeFp8Workload):
     + page table."""
 
     name = "paged_decode_i8kv"
+    tokens = 16  # tokens one step carries through the path
     kernel = "paged_decode_kernel<256, 1, 1> (+ merge)"
     traffic_profile = "paged_decode_i8kv_config1_pmc.txt"  # every kernel of the op, summed
 
@@ -404,7 +446,6 @@ class PagedDecodeI8Workload(PagedDecodeFp8Workload):
         import torch
 
         from axk import attention, configs
-        from oracle import paged_attn
 
         c = configs.config1()
         self.host = c
@@ -414,8 +455,7 @@ class PagedDecodeI8Workload(PagedDecodeFp8Workload):
         npages = int(c["indptr"][-1])
         self.alg_bytes = tot * 2 * hkv * (d + 2) + 2 * b * hq * d * 2 + 4 * (npages + 2 * b + 1)
         self.alg_flops = 4 * tot * hq * d
-        codes, scales = paged_attn.quant_kv_i8(c["cache"])
-        codes, scales = codes.to(dev), scales.to(dev)
+        codes, scales = encode_cache(c["cache"], dev, "i8")
         self.copies = max(2, -(-ROTATE_BYTES // codes.numel()))
         self.caches = [(codes, scales)] + [(codes.clone(), scales.clone()) for _ in range(self.copies - 1)]
         self.q = c["q"].to(dev)
@@ -458,6 +498,7 @@ class PagedPrefillWorkload(Workload):
     (query, key) pairs only, 4 D HQ sum_t (t + 1) (QK^T and PV), against dense bf16."""
 
     name = "paged_prefill"
+    tokens = 4096  # tokens one step carries through the path
     kernel = "paged_prefill_kernel<256>"
     timing = "graph"
     mfma = True
@@ -508,6 +549,7 @@ class GdnDecodeWorkload(Workload):
     """Config 2 decode: GDN recurrent step, B = 32, 32 value / 16 key heads, d = 128, fp32 state in place."""
 
     name = "gdn_decode"
+    tokens = 32  # tokens one step carries through the path
     kernel = "gdn_recurrent_kernel<false>"
     timing = "graph"
     traffic_profile = "gdn_decode_config2a_pmc.txt"
@@ -561,6 +603,7 @@ class GdnPrefillWorkload(Workload):
     output out, fp32 state in and out; algorithmic flops: the chunked form's products per (head, chunk)."""
 
     name = "gdn_prefill"
+    tokens = 4096  # tokens one step carries through the path
     kernel = "gdn chunk step (prep + scan)"
     timing = "graph"
     mfma = True
@@ -618,6 +661,7 @@ class MoeDecodeWorkload(Workload):
     activations in/out."""
 
     name = "moe_decode"
+    tokens = 32  # tokens one step carries through the path
     kernel = "moe step (router, route, group, gateup, down, combine)"
     timing = "graph"
     traffic_profile = "moe_decode_config3a_pmc.txt"
@@ -678,6 +722,7 @@ class MoeLayerDecodeWorkload(Workload):
     used (U distinct), the fp32 state read and written, the conv state, activations in and out."""
 
     name = "moe_layer_decode"
+    tokens = 32  # tokens one step carries through the path
     kernel = "35B MoE decode layer (GDN half + shared expert + routed experts)"
     timing = "graph"
     traffic_profile = "moe_layer_decode_b32_pmc.txt"  # every kernel of the step, summed
@@ -762,6 +807,7 @@ class MoeLayerPrefillWorkload(Workload):
     (every expert is routed at this size), the state read and written, activations in and out."""
 
     name = "moe_layer_prefill"
+    tokens = 4096  # tokens one step carries through the path
     kernel = "35B MoE prefill layer (GDN prefill + shared expert + grouped routed experts)"
     timing = "graph"
     mfma = True
@@ -861,6 +907,7 @@ class MoePrefillWorkload(Workload):
     experts."""
 
     name = "moe_prefill"
+    tokens = 4096  # tokens one step carries through the path
     kernel = "moe prefill step"
     timing = "graph"
     mfma = True
@@ -959,6 +1006,7 @@ class Fp8LinearWorkload(Workload):
     (the group's decode batch), bf16 out. Algorithmic bytes: weight + scales + x + out."""
 
     name = "fp8_linear"
+    tokens = 8  # tokens one step carries through the path
     kernel = "mx_group_kernel<FP8>"
     timing = "graph"
     traffic_profile = "fp8_linear_config4q_pmc.txt"
@@ -1007,6 +1055,7 @@ class KvWriteWorkload(Workload):
     paged cache in place. Algorithmic bytes: k, v and the locations read, the rows written."""
 
     name = "kv_write"
+    tokens = 16  # tokens one step carries through the path
     kernel = "paged_kv_write_kernel"
     timing = "graph"
     traffic_profile = "kv_write_config1_pmc.txt"
@@ -1050,6 +1099,7 @@ class GroupDecodeWorkload(Workload):
     The inputs (about 20 GB) are generated on the device by a seeded device generator."""
 
     name = "group_decode"
+    tokens = 8  # tokens one step carries through the path
     kernel = "hybrid decode group (16 layers)"
     timing = "graph"
     traffic_profile = "group_decode_config4_pmc.txt"
@@ -1214,7 +1264,7 @@ def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
         tf = wl.alg_flops / (kernel_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": wl.kernel, "achieved": round(tf, 2), "peak": BF16_PEAK_TFS,
                 "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFS, 4), "traffic": read_traffic(wl),
-                "alg_flops_per_launch": wl.alg_flops, "alg_bytes_per_launch": wl.alg_bytes}
+                "alg_flops_per_launch": wl.alg_flops, "alg_bytes_per_launch": wl.alg_bytes, **mfma_fracs(tf)}
     else:
         roof = {"bound": "hbm", "kernel": wl.kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(wl),
@@ -1237,6 +1287,7 @@ def report_line(wl, args, ms_per_step: float, kernel_ms: float) -> dict:
         "kernel_us": round(kernel_ms * 1e3, 3),
         "achieved_gbs": round(achieved, 1),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "tokens_per_s": tokens_per_s(wl, ms_per_step),
         "roofline": roof,
     }
 
@@ -1293,12 +1344,12 @@ def main() -> int:
             gbs = other.alg_bytes / (kms * 1e-3) / 1e9
             suite[name] = {"us_per_op": round(ms * 1e3, 3), "kernel_us": round(kms * 1e3, 3),
                            "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                           "config": other.config["workload"]}
+                           "tokens_per_s": tokens_per_s(other, ms), "config": other.config["workload"]}
             if getattr(other, "value_per", 1) > 1:
                 suite[name]["us_per_decode_layer"] = round(ms * 1e3 / other.value_per, 3)
             if getattr(other, "mfma", False):
                 tf = other.alg_flops / (kms * 1e-3) / 1e12
-                suite[name].update({"achieved_tflops": round(tf, 2), "bf16_mfma_frac": round(tf / BF16_PEAK_TFS, 4)})
+                suite[name].update({"achieved_tflops": round(tf, 2), **mfma_fracs(tf)})
             del other
             torch.cuda.empty_cache()
         line["suite"] = suite
@@ -1306,6 +1357,8 @@ def main() -> int:
         cpu = wl.cpu_baseline()
         if cpu is not None:
             cpu.update(cpu_machine())
+            if wl.tokens and cpu.get("value"):  # the same step on the host: value is per op (per layer for a group)
+                cpu["tokens_per_s"] = round(wl.tokens / (cpu["value"] * 1e-6 * getattr(wl, "value_per", 1)), 3)
             line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
     return 0

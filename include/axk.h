@@ -233,8 +233,10 @@ int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, const int32_t*
  * a static device array of the library (AXK_PAGED_NOALLOC_SCRATCH_BYTES, held by each GPU the library runs on until the
  * process ends); nothing is allocated or freed. A configuration whose axk_paged_decode_workspace_size exceeds it is
  * rejected with AXK_E_SCRATCH before anything is launched. Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (different streams, or host threads) race and must be serialised by the caller. Other arguments
- * and the result as axk_paged_decode. */
+ * overlap on one GPU (different streams, or host threads) race and must be serialised by the caller. The first call
+ * on a device does host set-up (the array's address on that device, the split kernel's LDS limit): made while its
+ * stream is capturing it returns AXK_E_LAUNCH and enqueues nothing, so make one eager call before capturing; later
+ * calls may be captured and the graph replayed. Other arguments and the result as axk_paged_decode. */
 #define AXK_PAGED_NOALLOC_SCRATCH_BYTES (24u << 20)
 int axk_paged_decode_noalloc(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr,
                              const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch,

@@ -225,6 +225,26 @@ def test_gdn_layer_prefill_moe(dev, b, t, h, nk, nv, e, fe, k, fmt):
     _conv_close(co, rc, 3)
 
 
+def test_gdn_layer_prefill_moe_bench_shape(dev):
+    """The bench's moe_layer_prefill itself: the 35B GDN MoE layer (hidden 2048, 16 / 32 heads, MXFP8 projections and
+    shared expert of 512, 256 MXFP4 experts of 512, top-8) over one 4096-token chunk from a random state."""
+    g = torch.Generator().manual_seed(4096)
+    b, t, h, nk, nv, e, fe, k, fmt = 1, 4096, 2048, 16, 32, 256, 512, 8, "mxfp8"
+    print("gdn prefill moe at the bench shape: t=4096 h=2048 e=256", flush=True)
+    w = configs.gdn_layer_weights(g, h, 512, nk, nv, proj_fmt="mxfp8", mlp_fmt=fmt)
+    blk = configs.moe_block(g, h, e, fe, k)
+    x = torch.randn(b, t, h, generator=g).bfloat16()
+    st = torch.randn(b, nv, 128, 128, generator=g) * 0.02
+    cv = torch.randn(b, 3, (2 * nk + nv) * 128, generator=g).bfloat16()
+    r = _routing_outputs(b * t, blk, dev)
+    out, so, co = layer.gdn_layer_prefill(x.to(dev), _dev(w, dev), st.to(dev), cv.to(dev), nk, nv, proj_fmt="mxfp8",
+                                          mlp_fmt=fmt, moe=dict(_dev_any(blk, dev), **r))
+    y, rs, rc, yslack = olayer.gdn_prefill_half(x, w, st, cv, nk, nv, proj_fmt="mxfp8")
+    _check_moe(out, r, x, y, w, blk, fmt, yslack)
+    torch.testing.assert_close(so.cpu(), rs, **STATE_TOL)
+    _conv_close(co, rc, 3)
+
+
 def test_attn_layer_prefill_moe(dev):
     """140 new tokens for each of 2 sequences (280 rows: the grouped prefill experts) over histories of 100 and 5."""
     g = torch.Generator().manual_seed(280)

@@ -426,6 +426,40 @@ def test_kv_write_i8_bytes(dev, d, hkv):
     assert torch.equal(gs.cpu().view(torch.int16), rs.view(torch.int16))
 
 
+def _i8_tie_rows(d):
+    """Rows whose scale is exactly 1 (amax 127 or 127.5: bf16(amax * bf16(1 / 127)) = 1), so every code is
+    round(x) of an exact product: half-integers x = n + 0.5 (ties), and +-127.5 (past 127: saturation)."""
+    rows = []
+    half = torch.arange(d, dtype=torch.float32) - d // 2 + 0.5       # ..., -1.5, -0.5, 0.5, 1.5, ... (every tie)
+    half = torch.where(half.abs() > 126, half.sign() * 126.5, half)  # inside (-127, 127)
+    r = half.clone(); r[0] = 127.0; rows.append(r)                    # amax 127: ties only
+    r = -half.clone(); r[1] = -127.0; rows.append(r)                  # negative amax
+    r = half.clone(); r[2] = 127.5; r[3] = -127.5; rows.append(r)     # 127.5 -> 128 (saturates to 127); -127.5 -> -128
+    return torch.stack(rows)
+
+
+def test_kv_write_i8_ties_and_saturation(dev):
+    """Ties and saturation of the int8 cast, pinned kernel == oracle (round half to even, clamp to [-128, 127]) on rows
+    where the products are exact half-integers and +-127.5, for both head dims."""
+    for d in (128, 256):
+        hkv, page = 3, 16
+        rows = _i8_tie_rows(d).bfloat16()
+        assert torch.equal(rows.float(), _i8_tie_rows(d))  # every value exactly representable
+        k = rows.reshape(1, 3, d)
+        v = (-rows).reshape(1, 3, d)
+        cache = torch.zeros(2, 2, page, hkv, d, dtype=torch.int8)
+        scales = torch.zeros(2, 2, page, hkv).bfloat16()
+        loc = torch.tensor([[1, 5]], dtype=torch.int32)
+        gc, gs = cache.to(dev), scales.to(dev)
+        axk.store_paged_kv_i8(k.to(dev), v.to(dev), gc, gs, loc.to(dev))
+        rc, rs = pa.store_paged_kv_i8(cache, scales, k, v, loc)
+        assert torch.equal(gc.cpu(), rc) and torch.equal(gs.cpu().view(torch.int16), rs.view(torch.int16))
+        assert (rs[1, :, 5].float() == 1.0).all()
+        codes = gc.cpu()[1, 0, 5]
+        assert codes[0, 0] == 127 and codes[2, 2] == 127 and codes[2, 3] == -128  # saturation
+        assert codes[0, d // 2] == 0 and codes[0, d // 2 + 1] == 2 and codes[0, d // 2 - 1] == 0  # 0.5, 1.5, -0.5
+
+
 def test_kv_write_then_decode_i8(dev):
     """Write the new token of every sequence through axk, then decode over the INT8 cache: equal to the oracle's
     write + decode (the bf16 cache's append case, quantized)."""

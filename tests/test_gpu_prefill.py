@@ -55,11 +55,23 @@ def test_paged_prefill_matches_oracle(dev, qlens, kv_lens, hq, hkv, d, page):
     assert not got[zero_rows].any()
 
 
-def test_paged_prefill_chunk_4096_and_determinism(dev):
-    # the bench workload's shape at a tenth of its length: one sequence, HQ 16 / HKV 2, D 256, page 64, no history
+def test_paged_prefill_chunk_512_and_determinism(dev):
+    # the bench workload's shape at an eighth of its length: one sequence, HQ 16 / HKV 2, D 256, page 64, no history
     g = torch.Generator().manual_seed(3)
     c = configs.prefill_case([512], [512], 16, 2, 256, 64, g)
     print("case prefill 512 tokens hq16 hkv2 d256", flush=True)
+    got = _run(c, dev)
+    torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
+    again = _run(c, dev)
+    assert torch.equal(got.view(torch.int16), again.view(torch.int16))
+
+
+def test_paged_prefill_chunk_4096_matches_oracle_and_determinism(dev):
+    """The bench workload itself (paged_prefill): one 4096-token chunk, HQ 16 / HKV 2, D 256, page 64, no history,
+    against the fp32 oracle, and bit-identical across launches."""
+    g = torch.Generator().manual_seed(4096)
+    c = configs.prefill_case([4096], [4096], 16, 2, 256, 64, g)
+    print("case prefill 4096 tokens hq16 hkv2 d256", flush=True)
     got = _run(c, dev)
     torch.testing.assert_close(got.float(), _ref(c).to(torch.bfloat16).float(), **TOL)
     again = _run(c, dev)

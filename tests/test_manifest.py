@@ -246,3 +246,39 @@ def test_state_views():
     kv = torch.zeros(4, 2, 256, 1024, dtype=torch.bfloat16)
     v = mf.paged_cache_view(kv, 4)
     assert v.shape == (4, 2, 256, 4, 256) and v.data_ptr() == kv.data_ptr()
+
+
+@pytest.mark.parametrize("path", [M9, M35])
+def test_every_manifest_dtype_is_handled_or_rejected_by_name(path):
+    """Every (name, dtype) of the committed manifests either has a storage size that matches its declared bytes, or
+    (the 35B's code 0 KV-cache outputs, absent from the reference's ONNX dtype table) is rejected with a ValueError that
+    names the IO, never a bare KeyError."""
+    import json
+
+    with open(path, encoding="utf-8") as f:
+        raw = json.load(f)
+    seen, rejected = set(), set()
+
+    def walk(o):
+        if isinstance(o, dict):
+            if "dtype" in o and "name" in o and "shape" in o:
+                name, dt, shape = o["name"], int(o["dtype"]), o["shape"]
+                seen.add(dt)
+                if dt in mf.DT_TORCH:
+                    assert mf.storage_bytes(dt, shape, name) == int(o["bytes"]), name
+                else:
+                    with pytest.raises(ValueError, match=name):
+                        mf.storage_bytes(dt, shape, name)
+                    with pytest.raises(ValueError, match=name):
+                        mf._typed(torch.zeros(int(o["bytes"]), dtype=torch.uint8), dt, shape, name)
+                    rejected.add(dt)
+            for v in o.values():
+                walk(v)
+        elif isinstance(o, list):
+            for v in o:
+                walk(v)
+
+    walk(raw)
+    assert seen
+    if path == M35:
+        assert rejected == {0}

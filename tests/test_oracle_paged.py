@@ -208,3 +208,17 @@ def test_int8_quantizer_zero_rows_and_rounding_to_nearest():
     row[0, :8] = vals
     q, s = pa.quant_kv_i8(row.bfloat16())
     assert q[0, :8].tolist() == [127, 10, 11, -20, -21, 0, 1, -3]
+
+
+def test_int8_quantizer_ties_and_saturation_choice():
+    """The oracle's stated choice where the reference is silent (parity unpinned against the AX cast): on rows whose
+    scale is exactly 1, every code equals Python's round-half-to-even of the exact half-integer, clamped to [-128, 127]
+    (so 127.5 saturates to 127 and -127.5 lands on -128)."""
+    d = 64
+    half = torch.arange(d, dtype=torch.float32) - d // 2 + 0.5
+    row = half.clone()
+    row[0], row[1] = 127.5, -127.5
+    q, s = pa.quant_kv_i8(row.bfloat16()[None])
+    assert float(s[0]) == 1.0
+    want = [max(-128, min(127, round(float(x)))) for x in row]
+    assert q[0].tolist() == want
