@@ -223,3 +223,38 @@ def test_mxfp8_linear_against_float64():
         got = mx.mxfp8_linear(a, codes, scales, fmt)
         ref = a.double() @ torch.from_numpy(mx.dequant_mxfp8(codes, scales, fmt)).double().T
         torch.testing.assert_close(got.double(), ref, rtol=1e-6, atol=1e-6)
+
+
+def _outside_bar(ref: torch.Tensor, got: torch.Tensor) -> float:
+    return float(((got - ref).abs() > 1e-2 + 2e-2 * ref.abs()).float().mean())
+
+
+def test_narrow_activations_break_the_parity_bar():
+    """Why the prefill GEMMs decode the MX weights to bf16 and run bf16 MFMA instead of gfx950's scaled FP8 / FP4 MFMA:
+    the scaled forms take both operands narrow, so the bf16 activations would be quantized (MXFP8 / MXFP4 with an E8M0
+    scale per 32, as the reference's own quant_mxfp8 / quant_mxfp4 do, q35_mx_build.py:60-72, mx4_common.py:11-49). On
+    config 3's draws (one expert's gate-up, activations ~ N(0, 1)) and config 0's linear, the product with quantized
+    activations leaves far more than the few-per-million flips the parity bar rel 2e-2 / abs 1e-2 tolerates (measured:
+    E4M3 about half of the outputs, E5M2 and E2M1 most of them), while bf16 activations stay inside it."""
+    from axk import configs
+
+    g = torch.Generator().manual_seed(0)
+    w = configs.moe_weights(g, hidden=2048, experts=2, inter=512, shared_inter=64)
+    wq = torch.from_numpy(mx.dequant_mxfp4(w["e_gw"][0].numpy(), w["e_gs"][0].numpy()))  # [1024, 2048] exact
+    x = torch.randn(32, 2048, generator=g).bfloat16().float()
+    ref = x @ wq.T
+    assert _outside_bar(ref, (x @ wq.T).bfloat16().float()) == 0.0  # bf16 outputs of bf16 activations: inside
+    fr = {}
+    for fmt in ("e4m3", "e5m2"):
+        codes, sc = mx.quant_mxfp8(x.numpy(), fmt)
+        xq = torch.from_numpy(mx.dequant_mxfp8(codes, sc, fmt))
+        fr[fmt] = _outside_bar(ref, (xq @ wq.T).bfloat16().float())
+    packed, sc = mx.quant_mxfp4(x.numpy())
+    fr["e2m1"] = _outside_bar(ref, (torch.from_numpy(mx.dequant_mxfp4(packed, sc)) @ wq.T).bfloat16().float())
+    assert fr["e4m3"] > 0.2 and fr["e5m2"] > 0.4 and fr["e2m1"] > 0.6, fr
+    c0 = configs.config0()
+    w0 = torch.from_numpy(mx.dequant_mxfp4(c0["w"].numpy(), c0["s"].numpy()))
+    x0 = c0["x"].float()
+    codes, sc = mx.quant_mxfp8(x0.numpy(), "e4m3")
+    got0 = (torch.from_numpy(mx.dequant_mxfp8(codes, sc, "e4m3")) @ w0.T).bfloat16().float()
+    assert _outside_bar(x0 @ w0.T, got0) > 0.2
