@@ -206,6 +206,21 @@ AXK_DEV float xor32_sum(float v) { const uint2 p = half_pair32(v); return __uint
 AXK_DEV float xor16_max(float v) { const uint2 p = row_pair16(v); return fmaxf(__uint_as_float(p.x), __uint_as_float(p.y)); }
 AXK_DEV float xor32_max(float v) { const uint2 p = half_pair32(v); return fmaxf(__uint_as_float(p.x), __uint_as_float(p.y)); }
 
+// Two 16x16 MFMA accumulator tiles a (rows 4 g + r) and b (rows 16 + 4 g + r) of one column (lane l16), rounded to
+// bf16, as the B operand of one 32-deep k-step (lane (column, g) holds k rows 8 g .. 8 g + 7). permlane32_swap gives
+// the lane groups {a@0, a@1, b@0, b@1} and {a@2, a@3, b@2, b@3}; permlane16_swap of those gives each group g the rows
+// of groups 2 (g & 1) (first four) and 2 (g & 1) + 1 (last four) of tile a (g < 2) or b (g >= 2).
+AXK_DEV axk_bf16x8 acc_pair_to_b(const axk_f32x4& a, const axk_f32x4& b) {
+  const unsigned a01 = pack_bf16x2(a[0], a[1]), a23 = pack_bf16x2(a[2], a[3]);
+  const unsigned b01 = pack_bf16x2(b[0], b[1]), b23 = pack_bf16x2(b[2], b[3]);
+  const auto s01 = __builtin_amdgcn_permlane32_swap(a01, b01, false, false);
+  const auto s23 = __builtin_amdgcn_permlane32_swap(a23, b23, false, false);
+  const auto t01 = __builtin_amdgcn_permlane16_swap(s01[0], s01[1], false, false);
+  const auto t23 = __builtin_amdgcn_permlane16_swap(s23[0], s23[1], false, false);
+  const axk_u32x4 f = {t01[0], t23[0], t01[1], t23[1]};
+  return __builtin_bit_cast(axk_bf16x8, f);
+}
+
 // Sum inside aligned groups of W lanes (W = 2, 4, 8 or 16), the same value in every lane of the group.
 template <int W>
 AXK_DEV float group_sum(float v) {

@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kTile = 16;  // tokens per tile = one 16x16x16 PV MFMA k-step
-constexpr int kNBuf = 3;   // LDS ring of tiles: two in flight while one is computed
+constexpr int kNBufPair = 4;  // bf16 LDS ring: two tile pairs, one landing while the other is computed
 constexpr int kTargetItems = 1024;
 constexpr int kMaxGroup = 16;  // query heads per KV head (MFMA N tile)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -294,7 +294,8 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int group = hq / hkv;
   const int b = desc.b, kvh = desc.kvh, nsplit = desc.nsplit;
   const int tpp = page_size / kTile;  // tiles per page
-  const int ntiles = desc.npg * tpp;
+  // tiles holding at least one valid token: the item's last page stops after its last valid token
+  const int ntiles = desc.npg > 0 ? (desc.npg - 1) * tpp + min(tpp, max(0, (desc.last_valid + kTile - 1) / kTile)) : 0;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
@@ -431,18 +432,82 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     }
   };
 
+  // the math of a tile pair (tokens 0 .. 15 from tile a at ka, 16 .. 31 from tile b at ka + BUF; nva / nvb valid, not
+  // both 0): the scores of both tiles, one online-softmax step over the 32 tokens, and O^T += V^T P^T as 32-deep
+  // MFMAs. P^T's B operand (lane (head, g): tokens 8 g .. 8 g + 7) comes from the score accumulators (tokens 4 g + r
+  // of each tile) by two lane swaps; V^T's A operand (lane (d, g): the same tokens) by two transposing LDS reads.
+  auto pair_math = [&](const unsigned char* ka, int nva, int nvb) {
+    const unsigned char* kb = ka + C::BUF;
+    // a tile with no valid token (a bad page) may hold any bytes: its zero weights take the other tile's finite V
+    if (nva <= 0) ka = kb;
+    if (nvb <= 0) kb = ka;
+    axk_f32x4 sa = axk_f32x4{0.f, 0.f, 0.f, 0.f}, sb = sa;
+    const unsigned char* kra = ka + C::row_off(l16) + 16 * g;
+    const unsigned char* krb = kb + C::row_off(l16) + 16 * g;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) {
+      sa = mfma_bf16_16x16x32(*reinterpret_cast<const axk_bf16x8*>(kra + 64 * s), qb[s], sa);
+      sb = mfma_bf16_16x16x32(*reinterpret_cast<const axk_bf16x8*>(krb + 64 * s), qb[s], sb);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      sa[rr] = (4 * g + rr < nva) ? sa[rr] * c : -INFINITY;
+      sb[rr] = (4 * g + rr < nvb) ? sb[rr] * c : -INFINITY;
+      mx = fmaxf(mx, fmaxf(sa[rr], sb[rr]));
+    }
+    mx = xor32_max(xor16_max(mx));
+    const float m_new = fmaxf(m_run, mx);  // finite: the pair holds at least one valid token
+    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first pair
+    float psum = 0.f;
+    axk_f32x4 pa, pb;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pa[rr] = (4 * g + rr < nva) ? __builtin_amdgcn_exp2f(sa[rr] - m_new) : 0.f;
+      pb[rr] = (4 * g + rr < nvb) ? __builtin_amdgcn_exp2f(sb[rr] - m_new) : 0.f;
+      psum += pa[rr] + pb[rr];
+    }
+    psum = xor32_sum(xor16_sum(psum));
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    const axk_bf16x8 pfrag = acc_pair_to_b(pa, pb);  // P rounded to bf16 as the MFMA operand
+    // V^T rows of this lane group: tokens 8 g .. 8 g + 7 = tile g / 2, rows 8 (g & 1) .. + 7
+    const unsigned char* vt = (g < 2 ? ka : kb) + C::PLANE;
+    const int vr = 8 * (g & 1) + (l16 >> 2);
+#pragma unroll
+    for (int t = 0; t < C::DT; ++t) {
+      const int vc = (wave * C::DW + 16 * t + 4 * (l16 & 3)) * 2;
+      const axk_i16x4 v0 = lds_read_tr16(vt + C::row_off(vr) + vc);
+      const axk_i16x4 v1 = lds_read_tr16(vt + C::row_off(vr + 4) + vc);
+      const axk_bf16x8 vfrag = __builtin_bit_cast(axk_bf16x8, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
+      if (moved) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+      }
+      o[t] = mfma_bf16_16x16x32(vfrag, pfrag, o[t]);
+    }
+  };
+
   if constexpr (KB == 2) {
-    int nv0 = issue(0, 0);  // valid tokens of tiles ti, ti + 1, ti + 2
-    int nv1 = issue(1, 1);
-    for (int ti = 0; ti < ntiles; ++ti) {
-      const int nb = ti % kNBuf;
-      wait_vmcnt<C::IPW>();              // this wave's loads of tile ti have landed (tile ti + 1 may not)
-      __builtin_amdgcn_s_barrier();      // ... and every other wave's; all are done with tile ti - 1
-      const int nv2 = issue(ti + 2, (ti + 2) % kNBuf);  // into the buffer of tile ti - 1
-      const int nvalid = nv0;
-      nv0 = nv1;
-      nv1 = nv2;
-      if (nvalid > 0) tile_math(smem + nb * C::BUF, nvalid);  // uniform over the workgroup
+    // Tile pairs: pair p = tiles 2 p, 2 p + 1 in ring slots 2 (p % 2), 2 (p % 2) + 1. Pair p + 1 is issued as pair p
+    // starts, into the slots of pair p - 1 (every wave finished it before the barrier), and lands while p computes:
+    // the same two tiles in flight as a single-tile ring, with one barrier, one softmax step and one set of page
+    // lookups per 32 tokens. A tile past the item re-reads its last tile and counts no tokens.
+    const int npairs = (ntiles + 1) / 2;
+    int nva = issue(0, 0), nvb = issue(1, 1);
+    for (int pp = 0; pp < npairs; ++pp) {
+      const int sl = 2 * (pp & 1);
+      wait_vmcnt<0>();                 // this wave's loads of pair pp have landed
+      __builtin_amdgcn_s_barrier();    // ... and every other wave's; all are done with pair pp - 1
+      int nna = 0, nnb = 0;
+      if (pp + 1 < npairs) {           // uniform
+        nna = issue(2 * pp + 2, 2 - sl);
+        nnb = issue(2 * pp + 3, 3 - sl);
+      }
+      if (nva > 0 || nvb > 0) pair_math(smem + sl * C::BUF, nva, nvb);  // uniform over the workgroup
+      nva = nna;
+      nvb = nnb;
     }
   } else {
     // FP8: tiles land kAhead8 ahead in a ring of kAhead8 + 1 slots (an FP8 tile is half a bf16 one, so twice the
@@ -1099,7 +1164,7 @@ int split_grid(int batch, int hkv) {
 template <int D, int KB, int QM>
 constexpr size_t split_lds() {
   return KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF + (QM == 1 ? 5 * 1024 : 0)
-                 : (size_t)kNBuf * PagedCfg<D>::BUF;
+                 : (size_t)kNBufPair * PagedCfg<D>::BUF;
 }
 
 // Allows the split kernel its dynamic LDS (above 64 KiB), once per process.
