@@ -105,6 +105,14 @@ AXK_DEV axk_s16x4 lds_read_tr16(const void* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) axk_s16x4*)(p));
 }
 
+// Transposing 8-byte LDS read of 8-bit elements: in each 16-lane group, lane i receives byte i % 8 of the 8-byte rows
+// read by source lanes i / 8 + 2j, j = 0 .. 7 (source lane 2j + a pointing at row j, bytes 8a .. 8a + 7 of a 16-column
+// block gives lane i column i of the eight rows).
+typedef int axk_i32x2 __attribute__((ext_vector_type(2)));
+AXK_DEV axk_i32x2 lds_read_tr8(const void* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) axk_i32x2*)(p));
+}
+
 // LDS byte address of a __shared__ pointer (for M0).
 AXK_DEV uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -151,6 +159,42 @@ AXK_DEV void lds_dma4_cached(const void* gptr, uint32_t lds_base_any) {
       "s_mov_b32 m0, %0"
       : "=&s"(save)
       : "s"(lds_base), "v"(gptr)
+      : "memory");
+}
+
+// A wave-uniform pointer in scalar registers (the value of the first active lane).
+AXK_DEV const void* uniform_ptr(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a), hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// As lds_dma16 / lds_dma4_cached, addressed as a wave-uniform 64-bit base (scalar registers) plus this lane's
+// 32-bit byte offset: no per-lane 64-bit address arithmetic.
+AXK_DEV void lds_dma16_so(const void* sbase_any, uint32_t voff, uint32_t lds_base_any) {
+  const void* sbase = uniform_ptr(sbase_any);
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(voff), "s"(sbase)
+      : "memory");
+}
+AXK_DEV void lds_dma4_so(const void* sbase_any, uint32_t voff, uint32_t lds_base_any) {
+  const void* sbase = uniform_ptr(sbase_any);
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "s"(lds_base), "v"(voff), "s"(sbase)
       : "memory");
 }
 

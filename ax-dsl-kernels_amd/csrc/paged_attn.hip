@@ -13,9 +13,9 @@
 //              no memset: graph-capturable). Up to kLocalPlanBatch sequences the split and merge kernels
 //              compute the same partition themselves and no plan launch is needed.
 //  2. decode — persistent: a few workgroups per CU take the work items in turn. The 4 waves share every
-//              16-token K/V tile of the item's pages: the tile streams HBM -> LDS by direct loads into a
-//              3-deep ring (two tiles in flight while one is computed). Every wave computes the full scores
-//              S^T = K Q^T of the tile on MFMA (Q in registers) and the online softmax in fp32 (exp2 domain),
+//              16-token K/V tile of the item's pages: tiles stream HBM -> LDS by direct loads into a ring
+//              and are computed in pairs (32 tokens per softmax step). Every wave computes the full scores
+//              S^T = K Q^T of the pair on MFMA (Q in registers) and the online softmax in fp32 (exp2 domain),
 //              then O^T += V^T P^T on MFMA for its own quarter of the head dim (V^T fragments by transposing
 //              LDS reads), so no cross-wave merge is needed. A sequence with one split writes its output
 //              directly; otherwise the item writes an fp32 partial (m, l, O).
@@ -34,6 +34,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kTile = 16;  // tokens per tile = one 16x16x16 PV MFMA k-step
 constexpr int kNBufPair = 4;  // bf16 LDS ring: two tile pairs, one landing while the other is computed
+constexpr int kAhead1 = 3;    // FP8 / INT8: tile pairs in flight ahead of the one computed (a ring of kAhead1 + 1)
 constexpr int kTargetItems = 1024;
 constexpr int kMaxGroup = 16;  // query heads per KV head (MFMA N tile)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -271,15 +272,16 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
 }
 
 // Attention of one work item. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
-// (each wave issues a quarter of its loads) into a ring of kNBuf buffers, two tiles ahead of the one being
-// computed. Every wave computes the full scores S^T = K Q^T of the tile (cheap on MFMA) and the online
-// softmax, then P x V for its own quarter of the head dim, so no cross-wave merge is needed.
-// KB = 1 (FP8 cache): each landed tile is converted by the four waves (a quarter of its 1 KiB blocks each, scaled by
-// inv_scale, exact for a power-of-two scale) into a bf16 staging tile of the bf16 layout, behind one more barrier;
-// the compute below then reads the staging tile.
+// (each wave issues a quarter of its loads) into a ring of tile pairs, computed a pair (32 tokens) at a time. Every
+// wave computes the full scores S^T = K Q^T of the pair (cheap on MFMA) and the online softmax, then P x V for its
+// own quarter of the head dim, so no cross-wave merge is needed.
+// KB = 1 (FP8 cache): the stored bytes land in LDS as they are, and each wave converts them to bf16 MFMA operands in
+// registers (scaled by inv_scale, exact for a power-of-two scale): K rows by 16-byte reads, V^T columns by
+// transposing 8-bit reads. Each row's 16-byte chunks are placed in LDS by an XOR swizzle (chunk c of row r at slot
+// c ^ r), so both read patterns spread over the banks.
 // QM = 1 (INT8 cache, KB = 1): each row and KV head carries a bf16 scale in kv_scales [pages, 2, page, hkv]; a
 // tile's scales (16 rows x hkv per plane, contiguous) land with the tile as one dword load per wave (256 dwords: up
-// to 16 KV heads), and the conversion writes bf16(q * s) (q35_group.py kv_page 208-221).
+// to 16 KV heads), and the conversion gives bf16(q * s) (q35_group.py kv_page 208-221).
 template <int D, int KB, int QM = 0>
 __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
                                             const unsigned char* __restrict__ cache, const int* __restrict__ indices,
@@ -292,10 +294,14 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   using C = PagedCfg<D>;      // the compute layout (bf16)
   using L = PagedCfg<D, KB>;  // the landing layout of the cached bytes
   const int group = hq / hkv;
-  const int b = desc.b, kvh = desc.kvh, nsplit = desc.nsplit;
+  const int b = __builtin_amdgcn_readfirstlane(desc.b), kvh = __builtin_amdgcn_readfirstlane(desc.kvh);
+  const int nsplit = __builtin_amdgcn_readfirstlane(desc.nsplit);
+  // the item's pages (wave-uniform: scalar registers)
+  const int npg = __builtin_amdgcn_readfirstlane(desc.npg), last_valid = __builtin_amdgcn_readfirstlane(desc.last_valid);
+  const int ibeg = __builtin_amdgcn_readfirstlane(desc.ibeg);
   const int tpp = page_size / kTile;  // tiles per page
   // tiles holding at least one valid token: the item's last page stops after its last valid token
-  const int ntiles = desc.npg > 0 ? (desc.npg - 1) * tpp + min(tpp, max(0, (desc.last_valid + kTile - 1) / kTile)) : 0;
+  const int ntiles = npg > 0 ? (npg - 1) * tpp + min(tpp, max(0, (last_valid + kTile - 1) / kTile)) : 0;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
@@ -303,39 +309,42 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int64_t row_stride = (int64_t)hkv * D * KB;  // bytes between consecutive tokens
   const int64_t plane_stride = (int64_t)page_size * row_stride;
   const uint32_t lds0 = lds_addr(smem);
-  // QM: the scale ring (kAhead8 + 1 slots of 1 KiB) after the landing ring and the two bf16 staging tiles
-  constexpr int scale_lds = 5 * L::BUF + 2 * C::BUF;
+  // QM: the scale ring (one 1 KiB slot per tile slot) after the landing ring
+  constexpr int scale_lds = 2 * (kAhead1 + 1) * L::BUF;
 
   // the item's page ids, 64 at a time: lane j holds page j of the current chunk
   int chunk = 0;
-  int pid = lane < desc.npg ? indices[desc.ibeg + lane] : 0;
+  int pid = lane < npg ? indices[ibeg + lane] : 0;
 
-  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s.
+  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s (bf16 cache);
+  // an 8-bit cache reads K as 16-byte row chunks (16 d), so steps 2s', 2s' + 1 take d = 64s' + 16g + 8e .. +8, e = 0, 1.
   axk_bf16x8 qb[C::KSTEPS];
   {
     const bool hv = l16 < group;
-    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 8 * g;
+    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D;
 #pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
+    for (int s = 0; s < C::KSTEPS; ++s) {
+      const int d0 = KB == 2 ? 32 * s + 8 * g : 64 * (s >> 1) + 16 * g + 8 * (s & 1);
+      qb[s] = hv ? load_bf16x8(qp + d0) : zero_bf16x8();
+    }
   }
   // make the compiler take its waits for Q and the page ids here, before the asm loads it cannot count
   asm volatile("" : "+v"(pid));
 #pragma unroll
   for (int s = 0; s < C::KSTEPS; ++s) asm volatile("" : "+v"(qb[s]));
 
-  // tile ti -> valid tokens and K base (both wave-uniform: scalar registers); a tile past the sequence end
-  // or on a page outside the pool gets nvalid = 0 and an in-bounds base
+  // tile (lp, tp) = tile tp of the item's page lp -> valid tokens and K base (both wave-uniform: scalar registers);
+  // a tile past the sequence end or on a page outside the pool gets nvalid = 0 and an in-bounds base
   const unsigned char* tile_scales = kv_scales;  // QM: the scales of the tile located last, plane 0
-  auto locate = [&](int ti, int& nvalid) -> const unsigned char* {
-    const int lp = ti / tpp, tp = ti - lp * tpp;
+  auto locate = [&](int lp, int tp, int& nvalid) -> const unsigned char* {
     if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
       chunk = lp >> 6;
       const int j = (chunk << 6) + lane;
-      pid = j < desc.npg ? indices[desc.ibeg + j] : 0;
+      pid = j < npg ? indices[ibeg + j] : 0;
       asm volatile("" : "+v"(pid));  // the compiler's wait for this load stays inside this rare branch
     }
-    int page = __builtin_amdgcn_readfirstlane(__shfl(pid, lp & 63, 64));
-    const int valid_in_page = (lp == desc.npg - 1) ? desc.last_valid : page_size;
+    int page = __builtin_amdgcn_readlane(pid, lp & 63);
+    const int valid_in_page = (lp == npg - 1) ? last_valid : page_size;
     nvalid = min(kTile, valid_in_page - tp * kTile);
     if (page < 0 || page >= num_pages) {
       if (lane == 0 && nvalid > 0) hdr->bad_page = 1;
@@ -349,34 +358,47 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   // QM: this lane's dword of a tile's scale spans (plane 0 dwords 0 .. 8 hkv - 1, then plane 1; past them dword 0
   // again, landing in the unused tail of the 1 KiB scale slot)
   const int sdw = wave * 64 + lane, sspan = 8 * hkv;
-  const int64_t s_off = sdw < 2 * sspan ? (sdw >= sspan ? (int64_t)page_size * hkv * 2 + 4 * (sdw - sspan) : 4 * sdw) : 0;
+  const uint32_t s_off = sdw < 2 * sspan ? (sdw >= sspan ? (uint32_t)(page_size * hkv * 2 + 4 * (sdw - sspan)) : 4u * sdw) : 0u;
   // per-lane element offsets of this wave's loads inside a tile (token row, plane, 16-byte chunk), and the
-  // same offsets clamped to row 0 for rows past nvalid
+  // same offsets clamped to row 0 for rows past nvalid. An 8-bit cache lands chunk c of row r at chunk slot
+  // c ^ (r mod NCH) of the row (lane slot q loads chunk q ^ (r mod NCH)).
+  constexpr int NCH = L::RB / 16;  // 16-byte chunks per row
+  // (32-bit: the launch checks that both planes of a page span less than 2^31 bytes)
   int lane_tok[L::IPW];
-  int64_t lane_off[L::IPW], lane_off0[L::IPW];  // bytes
+  uint32_t lane_off[L::IPW], lane_off0[L::IPW];  // bytes from the tile's K base
 #pragma unroll
   for (int k = 0; k < L::IPW; ++k) {
     const int j = wave * L::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
     const int plane = j / L::IPP, blk = j - plane * L::IPP;
-    lane_tok[k] = blk * L::RPI + lane / (L::RB / 16);
-    lane_off0[k] = plane * plane_stride + (lane % (L::RB / 16)) * 16;
-    lane_off[k] = lane_off0[k] + (int64_t)lane_tok[k] * row_stride;
+    lane_tok[k] = blk * L::RPI + lane / NCH;
+    const int chunk = KB == 1 ? (lane % NCH) ^ (lane_tok[k] % NCH) : lane % NCH;
+    lane_off0[k] = (uint32_t)(plane * plane_stride + chunk * 16);
+    lane_off[k] = lane_off0[k] + (uint32_t)(lane_tok[k] * row_stride);
   }
-  // this wave's share of tile ti's loads into ring buffer nb (rows past nvalid re-read row 0); returns the
+  // the tile cursor: issue() takes the item's tiles in order (tile cur_ti = tile cur_tp of page cur_lp); past the
+  // last tile it re-reads that tile and counts no tokens
+  int cur_ti = 0, cur_lp = 0, cur_tp = 0;
+  // this wave's share of the next tile's loads into ring buffer nb (rows past nvalid re-read row 0); returns the
   // tile's valid token count
-  auto issue = [&](int ti, int nb) -> int {
+  auto issue = [&](int nb) -> int {
     int nvalid;
-    const unsigned char* kbase = locate(ti < ntiles ? ti : ntiles - 1, nvalid);
+    const unsigned char* kbase = locate(cur_lp, cur_tp, nvalid);
     const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
 #pragma unroll
     for (int k = 0; k < L::IPW; ++k) {
       const int j = wave * L::IPW + k;
       const int plane = j / L::IPP, blk = j - plane * L::IPP;
-      lds_dma16(kbase + (lane_tok[k] < nrow ? lane_off[k] : lane_off0[k]),
-                lds0 + nb * L::BUF + plane * L::PLANE + blk * L::BLK);
+      lds_dma16_so(kbase, lane_tok[k] < nrow ? lane_off[k] : lane_off0[k],
+                   lds0 + nb * L::BUF + plane * L::PLANE + blk * L::BLK);
     }
-    if constexpr (QM == 1) lds_dma4_cached(tile_scales + s_off, lds0 + scale_lds + nb * 1024 + wave * 256);
-    return ti < ntiles ? nvalid : 0;
+    if constexpr (QM == 1) lds_dma4_so(tile_scales, s_off, lds0 + scale_lds + nb * 1024 + wave * 256);
+    const int r = cur_ti < ntiles ? nvalid : 0;
+    if (cur_ti + 1 < ntiles && ++cur_tp == tpp) {
+      cur_tp = 0;
+      ++cur_lp;
+    }
+    ++cur_ti;
+    return r;
   };
 
   // O^T tiles: lane holds O[head l16][d = wave*DW + 16t + 4g + r] (same head layout as the softmax state)
@@ -384,53 +406,6 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 #pragma unroll
   for (int t = 0; t < C::DT; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g and over the waves)
-
-  // the math of one tile from its bf16 K / V in LDS (kt: K plane; V plane at kt + PLANE), nvalid > 0 tokens
-  auto tile_math = [&](const unsigned char* kt, int nvalid) {
-    const unsigned char* vt = kt + C::PLANE;
-    // S^T (16 tokens x 16 heads): A = K rows (lane: token l16, d = 32s + 8g .. +8); lane holds
-    // S[token 4g + r][head l16]
-    axk_f32x4 st = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-    const unsigned char* krow = kt + C::row_off(l16) + 16 * g;
-#pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s)
-      st = mfma_bf16_16x16x32(*reinterpret_cast<const axk_bf16x8*>(krow + 64 * s), qb[s], st);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float sv = (4 * g + rr < nvalid) ? st[rr] * c : -INFINITY;
-      st[rr] = sv;
-      mx = fmaxf(mx, sv);
-    }
-    mx = xor32_max(xor16_max(mx));
-    const float m_new = fmaxf(m_run, mx);  // finite: the tile holds at least one valid token
-    // the running max rarely moves after the first tiles: rescale O only when it did (wave-uniform test)
-    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first tile
-    float psum = 0.f;
-    axk_i16x4 pb;  // B operand of O^T = V^T P^T: lane (head l16, group g) = P[head][tokens 4g .. 4g + 3]
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float p = (4 * g + rr < nvalid) ? __builtin_amdgcn_exp2f(st[rr] - m_new) : 0.f;
-      psum += p;
-      pb[rr] = (short)f32_to_bf16_bits(p);
-    }
-    psum = xor32_sum(xor16_sum(psum));
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < C::DT; ++t) {
-      // A operand V^T: lane (d = wave*DW + 16t + l16, group g) = V[tokens 4g .. 4g + 3][d], by one transposing
-      // LDS read: in each 16-lane group, source lane 4j + a points at V[4g + j][16t' + 4a .. +3] and lane i
-      // receives element i % 4 of source lanes i / 4 + 4j, i.e. V[4g + j][16t' + i]
-      const axk_i16x4 va = lds_read_tr16(vt + C::row_off(4 * g + (l16 >> 2)) + (wave * C::DW + 16 * t + 4 * (l16 & 3)) * 2);
-      if (moved) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
-      }
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
-    }
-  };
 
   // the math of a tile pair (tokens 0 .. 15 from tile a at ka, 16 .. 31 from tile b at ka + BUF; nva / nvb valid, not
   // both 0): the scores of both tiles, one online-softmax step over the 32 tokens, and O^T += V^T P^T as 32-deep
@@ -495,95 +470,163 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     // the same two tiles in flight as a single-tile ring, with one barrier, one softmax step and one set of page
     // lookups per 32 tokens. A tile past the item re-reads its last tile and counts no tokens.
     const int npairs = (ntiles + 1) / 2;
-    int nva = issue(0, 0), nvb = issue(1, 1);
+    int nva = issue(0), nvb = issue(1);
     for (int pp = 0; pp < npairs; ++pp) {
       const int sl = 2 * (pp & 1);
       wait_vmcnt<0>();                 // this wave's loads of pair pp have landed
       __builtin_amdgcn_s_barrier();    // ... and every other wave's; all are done with pair pp - 1
       int nna = 0, nnb = 0;
       if (pp + 1 < npairs) {           // uniform
-        nna = issue(2 * pp + 2, 2 - sl);
-        nnb = issue(2 * pp + 3, 3 - sl);
+        nna = issue(2 - sl);  // tiles 2 pp + 2, 2 pp + 3
+        nnb = issue(3 - sl);
       }
       if (nva > 0 || nvb > 0) pair_math(smem + sl * C::BUF, nva, nvb);  // uniform over the workgroup
       nva = nna;
       nvb = nnb;
     }
   } else {
-    // FP8: tiles land kAhead8 ahead in a ring of kAhead8 + 1 slots (an FP8 tile is half a bf16 one, so twice the
-    // look-ahead keeps as many bytes in flight), and two bf16 staging tiles. Iteration ti: wait for tile ti + 1, one
-    // fenced barrier (every wave's loads of ti + 1 landed, the conversion of ti done, the math of ti - 1 done), issue
-    // tile ti + kAhead8 into the slot of tile ti - 1, the math of tile ti, then convert tile ti + 1 into the staging
-    // tile ti - 1 used (every wave finished that math before the barrier; issued behind the math, the conversion's
-    // latency overlaps it).
-    constexpr int kAhead8 = 4, kNBuf8 = kAhead8 + 1;
+    // FP8 / INT8: the pair ring of the bf16 path, kAhead1 pairs ahead (an 8-bit tile is half a bf16 one, so the
+    // deeper look-ahead keeps as many bytes in flight) in a ring of kAhead1 + 1 pairs, and no staging tile: each wave
+    // converts the landed bytes to bf16 operands in registers. Pair pp + kAhead1 is issued as pair pp starts, into
+    // the slots of pair pp - 1 (every wave finished it before the barrier).
+    constexpr int NA = kAhead1;
+    static_assert(NA == 3, "the waits below count up to two pairs in flight behind the one computed");
     constexpr int IPWQ = L::IPW + (QM == 1 ? 1 : 0);  // this wave's loads of a tile
-    unsigned char* stage = smem + kNBuf8 * L::BUF;
-    auto convert = [&](int slot, unsigned char* dst_tile) {
-      // wave w converts 1 KiB blocks c = w, w + 4, ...: lane l's 16 stored bytes of row blk RPI + l / (RB / 16)
-#pragma unroll
-      for (int c = wave; c < 2 * L::IPP; c += kWaves) {
-        const int plane = c / L::IPP, blk = c - plane * L::IPP;
-        const int row = blk * L::RPI + lane / (L::RB / 16), col = (lane % (L::RB / 16)) * 16;
-        const axk_u32x4 f8 =
-            *reinterpret_cast<const axk_u32x4*>(smem + slot * L::BUF + plane * L::PLANE + blk * L::BLK + 16 * lane);
-        axk_u32x4 lo, hi;
-        if constexpr (QM == 1) {  // int8 codes of row `row`: bf16(q * s), s its row's scale for this KV head
-          const uint16_t sbits = *reinterpret_cast<const uint16_t*>(smem + scale_lds + slot * 1024 +
-                                                                    plane * 32 * hkv + (row * hkv + kvh) * 2);
-          const float sc = bf16_bits_to_f32(sbits), off = -128.0f * sc;
-          // q = (byte ^ 0x80) - 128 through the unsigned byte conversion; (u - 128) s = fma(u, s, -128 s) is exact
-          // (q s has at most 16 significant bits), so the bf16 rounding below sees fp32(q s)
-          uint32_t o16[8];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const uint32_t u = f8[w] ^ 0x80808080u;
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {
-              const float x0 = __builtin_fmaf((float)((u >> (16 * hb)) & 0xffu), sc, off);
-              const float x1 = __builtin_fmaf((float)((u >> (16 * hb + 8)) & 0xffu), sc, off);
-              o16[2 * w + hb] = f32_to_bf16_bits(x0) | (f32_to_bf16_bits(x1) << 16);
-            }
-          }
-          lo = axk_u32x4{o16[0], o16[1], o16[2], o16[3]};
-          hi = axk_u32x4{o16[4], o16[5], o16[6], o16[7]};
-        } else {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t b0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(f8[w], inv_scale, false));
-          const uint32_t b1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(f8[w], inv_scale, true));
-          if (w < 2) {
-            lo[2 * w] = b0;
-            lo[2 * w + 1] = b1;
-          } else {
-            hi[2 * w - 4] = b0;
-            hi[2 * w - 3] = b1;
-          }
-        }
-        }
-        unsigned char* dst = dst_tile + plane * C::PLANE + C::row_off(row) + 2 * col;
-        *reinterpret_cast<axk_u32x4*>(dst) = lo;
-        *reinterpret_cast<axk_u32x4*>(dst + 16) = hi;
+    auto row_scale = [&](int slot, int plane, int row) -> float {  // QM: the bf16 scale of a landed row
+      return bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(smem + scale_lds + slot * 1024 + plane * 32 * hkv +
+                                                                  (row * hkv + kvh) * 2));
+    };
+    // 4 stored bytes -> 4 bf16 (2 dwords): FP8 code * inv_scale; INT8: bf16(q * sc) with q = (byte ^ 0x80) - 128 by
+    // the unsigned byte conversion, (u - 128) sc = fma(u, sc, -128 sc) exact (q sc has at most 16 significant bits),
+    // so the bf16 rounding sees fp32(q sc). sc4: the scales of the four bytes.
+    auto cvt4 = [&](uint32_t w, const float* sc4, uint32_t& lo, uint32_t& hi) {
+      if constexpr (QM == 1) {
+        const uint32_t u = w ^ 0x80808080u;
+        lo = pack_bf16x2(__builtin_fmaf((float)(u & 0xffu), sc4[0], -128.0f * sc4[0]),
+                         __builtin_fmaf((float)((u >> 8) & 0xffu), sc4[1], -128.0f * sc4[1]));
+        hi = pack_bf16x2(__builtin_fmaf((float)((u >> 16) & 0xffu), sc4[2], -128.0f * sc4[2]),
+                         __builtin_fmaf((float)(u >> 24), sc4[3], -128.0f * sc4[3]));
+      } else {
+        lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, false));
+        hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, true));
       }
     };
-    int nv[kAhead8];  // valid tokens of tiles ti .. ti + kAhead8 - 1 (nv[j]: tile ti + j)
+    auto cvt8 = [&](uint32_t w0, uint32_t w1, const float* sc8) -> axk_bf16x8 {
+      uint32_t r0, r1, r2, r3;
+      cvt4(w0, sc8, r0, r1);
+      cvt4(w1, sc8 + 4, r2, r3);
+      const axk_u32x4 r = {r0, r1, r2, r3};
+      return __builtin_bit_cast(axk_bf16x8, r);
+    };
+    // the math of the pair in slots sa_slot, sa_slot + 1 (nva / nvb valid tokens, not both 0): as pair_math, with
+    // K's A operand (lane (token l16, g)) from 16-byte row chunks 4s' + g and V^T's (lane (d, g): tokens 8 g .. +7)
+    // from one transposing 8-bit read per 16 columns (source lane 2j + a: row 8 (g & 1) + j, bytes 8a .. 8a + 7 of the
+    // chunk; lane i receives column i of the eight rows).
+    auto pair_math8 = [&](int sa_slot, int nva, int nvb) {
+      int ta = sa_slot, tb = sa_slot + 1;
+      if (nva <= 0) ta = tb;  // a tile with no valid token (a bad page) may hold any bytes: use the other's
+      if (nvb <= 0) tb = ta;
+      const unsigned char* ka = smem + ta * L::BUF;
+      const unsigned char* kb = smem + tb * L::BUF;
+      float ksa[8], ksb[8];  // this lane's K row scales, replicated (QM)
+      if constexpr (QM == 1) {
+        const float xa = row_scale(ta, 0, l16), xb = row_scale(tb, 0, l16);
 #pragma unroll
-    for (int j = 0; j < kAhead8; ++j) nv[j] = issue(j, j);
-    wait_vmcnt<(kAhead8 - 1) * IPWQ>();  // tile 0 has landed
-    __syncthreads();
-    if (nv[0] > 0) convert(0, stage);
-    for (int ti = 0; ti < ntiles; ++ti) {
-      wait_vmcnt<(kAhead8 - 2) * IPWQ>();  // tile ti + 1 has landed (later ones may not)
-      __syncthreads();  // a fence with the barrier: LDS written by other waves is read after it
-      const int nvn = issue(ti + kAhead8, (ti + kAhead8) % kNBuf8);  // into the slot of tile ti - 1 (converted)
-      if (nv[0] > 0) tile_math(stage + (ti & 1) * C::BUF, nv[0]);
-      if (nv[1] > 0) convert((ti + 1) % kNBuf8, stage + ((ti + 1) & 1) * C::BUF);
+        for (int j = 0; j < 8; ++j) {
+          ksa[j] = xa;
+          ksb[j] = xb;
+        }
+      }
+      axk_f32x4 sa = axk_f32x4{0.f, 0.f, 0.f, 0.f}, sb = sa;
+      const int krow = l16 * L::RB, ksw = l16 % NCH;
 #pragma unroll
-      for (int j = 0; j + 1 < kAhead8; ++j) nv[j] = nv[j + 1];
-      nv[kAhead8 - 1] = nvn;
+      for (int s2 = 0; s2 < C::KSTEPS / 2; ++s2) {
+        const int off = krow + 16 * ((4 * s2 + g) ^ ksw);
+        const axk_u32x4 wa = *reinterpret_cast<const axk_u32x4*>(ka + off);
+        const axk_u32x4 wb = *reinterpret_cast<const axk_u32x4*>(kb + off);
+        sa = mfma_bf16_16x16x32(cvt8(wa[0], wa[1], ksa), qb[2 * s2], sa);
+        sa = mfma_bf16_16x16x32(cvt8(wa[2], wa[3], ksa), qb[2 * s2 + 1], sa);
+        sb = mfma_bf16_16x16x32(cvt8(wb[0], wb[1], ksb), qb[2 * s2], sb);
+        sb = mfma_bf16_16x16x32(cvt8(wb[2], wb[3], ksb), qb[2 * s2 + 1], sb);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        sa[rr] = (4 * g + rr < nva) ? sa[rr] * c : -INFINITY;
+        sb[rr] = (4 * g + rr < nvb) ? sb[rr] * c : -INFINITY;
+        mx = fmaxf(mx, fmaxf(sa[rr], sb[rr]));
+      }
+      mx = xor32_max(xor16_max(mx));
+      const float m_new = fmaxf(m_run, mx);  // finite: the pair holds at least one valid token
+      const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first pair
+      float psum = 0.f;
+      axk_f32x4 pa, pb;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        pa[rr] = (4 * g + rr < nva) ? __builtin_amdgcn_exp2f(sa[rr] - m_new) : 0.f;
+        pb[rr] = (4 * g + rr < nvb) ? __builtin_amdgcn_exp2f(sb[rr] - m_new) : 0.f;
+        psum += pa[rr] + pb[rr];
+      }
+      psum = xor32_sum(xor16_sum(psum));
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
+      const axk_bf16x8 pfrag = acc_pair_to_b(pa, pb);
+      const int tv = g < 2 ? ta : tb;
+      const unsigned char* vt = smem + tv * L::BUF + L::PLANE;
+      const int vr = 8 * (g & 1) + (l16 >> 1);
+      float vs[8];  // the scales of this lane group's eight V rows (QM)
+      if constexpr (QM == 1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vs[j] = row_scale(tv, 1, 8 * (g & 1) + j);
+      }
+#pragma unroll
+      for (int t = 0; t < C::DT; ++t) {
+        const int ch = wave * C::DT + t;  // the 16 columns of this O^T tile: chunk ch of the rows
+        const axk_i32x2 w = lds_read_tr8(vt + vr * L::RB + 16 * (ch ^ (vr % NCH)) + 8 * (l16 & 1));
+        const axk_bf16x8 vfrag = cvt8((uint32_t)w[0], (uint32_t)w[1], vs);
+        if (moved) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+        }
+        o[t] = mfma_bf16_16x16x32(vfrag, pfrag, o[t]);
+      }
+    };
+
+    const int npairs = (ntiles + 1) / 2;
+    int nv[NA][2];  // valid tokens of pairs pp .. pp + NA - 1
+#pragma unroll
+    for (int j = 0; j < NA; ++j) {
+      nv[j][0] = nv[j][1] = 0;
+      if (j < npairs) {  // uniform
+        nv[j][0] = issue(2 * j);  // tiles 2 j, 2 j + 1
+        nv[j][1] = issue(2 * j + 1);
+      }
+    }
+    for (int pp = 0; pp < npairs; ++pp) {
+      // this wave's loads of pair pp have landed: the pairs issued after it may still be in flight
+      const int later = min(NA - 1, npairs - 1 - pp);  // uniform
+      if (later >= 2) wait_vmcnt<4 * IPWQ>();
+      else if (later == 1) wait_vmcnt<2 * IPWQ>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();  // ... and every other wave's; all are done with pair pp - 1
+      int nn0 = 0, nn1 = 0;
+      if (pp + NA < npairs) {  // uniform
+        const int ns = 2 * ((pp + NA) % (NA + 1));
+        nn0 = issue(ns);  // tiles 2 (pp + NA), 2 (pp + NA) + 1
+        nn1 = issue(ns + 1);
+      }
+      if (nv[0][0] > 0 || nv[0][1] > 0) pair_math8(2 * (pp % (NA + 1)), nv[0][0], nv[0][1]);  // uniform
+#pragma unroll
+      for (int j = 0; j + 1 < NA; ++j) {
+        nv[j][0] = nv[j + 1][0];
+        nv[j][1] = nv[j + 1][1];
+      }
+      nv[NA - 1][0] = nn0;
+      nv[NA - 1][1] = nn1;
     }
   }
-  wait_vmcnt<0>();  // drain the two look-ahead tiles before the buffers are reused
+  wait_vmcnt<0>();  // every load has landed before the buffers are reused
   __builtin_amdgcn_s_barrier();
 
   // every wave holds the same (m, l) for head l16 and O^T for its own columns
@@ -1159,11 +1202,10 @@ int split_grid(int batch, int hkv) {
   return (int)(items < slots ? items : slots);
 }
 
-// The split kernel's dynamic LDS: the ring of landed tiles; an FP8 / INT8 cache: a ring of 5 landing slots and two
-// bf16 staging tiles (INT8: and the scales' ring).
+// The split kernel's dynamic LDS: the ring of landed tiles (an INT8 cache: and a 1 KiB scale slot per tile slot).
 template <int D, int KB, int QM>
 constexpr size_t split_lds() {
-  return KB == 1 ? (size_t)5 * PagedCfg<D, KB>::BUF + 2 * PagedCfg<D>::BUF + (QM == 1 ? 5 * 1024 : 0)
+  return KB == 1 ? (size_t)2 * (kAhead1 + 1) * (PagedCfg<D, KB>::BUF + (QM == 1 ? 1024 : 0))
                  : (size_t)kNBufPair * PagedCfg<D>::BUF;
 }
 
@@ -1180,6 +1222,8 @@ int launch_split(const uint16_t* q, const void* cache, const int* indptr, const 
                  void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
+  // the kernel's per-lane tile offsets are 32-bit: both planes of a page stay under 2^31 bytes
+  AXK_REQUIRE((int64_t)2 * page_size * hkv * D * KB < ((int64_t)1 << 31), AXK_E_SHAPE);
   constexpr size_t lds = split_lds<D, KB, QM>();
   if (const int rc = raise_split_lds<D, KB, QM>()) return rc;
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
