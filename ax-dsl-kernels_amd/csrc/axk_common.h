@@ -169,8 +169,8 @@ AXK_DEV const void* uniform_ptr(const void* p) {
   return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
 }
 
-// As lds_dma16 / lds_dma4_cached, addressed as a wave-uniform 64-bit base (scalar registers) plus this lane's
-// 32-bit byte offset: no per-lane 64-bit address arithmetic.
+// As lds_dma16, addressed as a wave-uniform 64-bit base (scalar registers) plus this lane's 32-bit byte offset: no
+// per-lane 64-bit address arithmetic.
 AXK_DEV void lds_dma16_so(const void* sbase_any, uint32_t voff, uint32_t lds_base_any) {
   const void* sbase = uniform_ptr(sbase_any);
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
@@ -179,19 +179,6 @@ AXK_DEV void lds_dma16_so(const void* sbase_any, uint32_t voff, uint32_t lds_bas
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %1\n\t"
       "global_load_lds_dwordx4 %2, %3 nt\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(save)
-      : "s"(lds_base), "v"(voff), "s"(sbase)
-      : "memory");
-}
-AXK_DEV void lds_dma4_so(const void* sbase_any, uint32_t voff, uint32_t lds_base_any) {
-  const void* sbase = uniform_ptr(sbase_any);
-  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_base_any);
-  uint32_t save;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dword %2, %3\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(save)
       : "s"(lds_base), "v"(voff), "s"(sbase)

@@ -34,7 +34,6 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kTile = 16;  // tokens per tile = one 16x16x16 PV MFMA k-step
 constexpr int kNBufPair = 4;  // bf16 LDS ring: two tile pairs, one landing while the other is computed
-constexpr int kAhead1 = 3;    // FP8 / INT8: tile pairs in flight ahead of the one computed (a ring of kAhead1 + 1)
 constexpr int kTargetItems = 1024;
 constexpr int kMaxGroup = 16;  // query heads per KV head (MFMA N tile)
 constexpr float kLog2e = 1.4426950408889634f;
@@ -166,25 +165,39 @@ __global__ __launch_bounds__(256) void paged_plan_kernel(const int* __restrict__
   }
 }
 
-// KB: bytes per cached K / V element (2: bf16; 1: FP8 E4M3 with a static scale, landed in LDS as stored and
-// converted to the bf16 layout before use).
-template <int D, int KB = 2>
+// The bf16 cache's tile layout in LDS (also the per-wave head-dim split of every decode path).
+template <int D>
 struct PagedCfg {
   static constexpr int KSTEPS = D / 32;       // 16x16x32 MFMA k-steps over the head dim (QK)
   static constexpr int DW = D / kWaves;       // head-dim columns of O owned by one wave
   static constexpr int DT = DW / 16;          // 16-wide O tiles per wave
-  static constexpr int RB = D * KB;           // bytes per cached row of one KV head
+  static constexpr int RB = D * 2;            // bytes per cached row of one KV head
   static constexpr int RPI = 1024 / RB;       // rows per direct-to-LDS instruction (64 lanes x 16 B)
   static constexpr int IPP = kTile / RPI;     // instructions per plane (K or V) of a tile
   static constexpr int IPW = 2 * IPP / kWaves;  // instructions per wave per tile
   static_assert(IPW >= 1 && IPW * kWaves == 2 * IPP, "a tile's loads split evenly over the waves");
-  // bytes after each 1 KiB block (bank spread for the transposing V reads of the bf16 layout; FP8 landing slots are
-  // only read row-wise)
-  static constexpr int PAD = KB == 1 ? 0 : (D == 256 ? 32 : 64);
+  // bytes after each 1 KiB block (bank spread for the transposing V reads)
+  static constexpr int PAD = D == 256 ? 32 : 64;
   static constexpr int BLK = 1024 + PAD;
   static constexpr int PLANE = IPP * BLK;     // one plane of a tile in LDS
   static constexpr int BUF = 2 * PLANE;       // one tile (K then V)
   static AXK_DEV int row_off(int tok) { return (tok / RPI) * BLK + (tok % RPI) * RB; }
+};
+
+// The 8-bit cache decode's step (a pair of 16-token tiles per wave step) and per-lane load counts.
+template <int D>
+struct WaveCfg {
+  static constexpr int NT = 2;                    // tiles per step
+  static constexpr int RB = D;                    // bytes per cached row of one KV head
+  static constexpr int NCH = RB / 16;             // 16-byte chunks per row
+  static constexpr int KLT = RB / 64;             // K loads (16 B) per lane per tile
+  static constexpr int KL = NT * KLT;             // ... per step (and 1 KiB V loads per tile)
+  static constexpr int DTF = D / 16;              // 16-wide O^T tiles of the full head dim
+  static constexpr int VPLANE = 16 * RB;          // one tile's V in a wave's slot
+  static constexpr int VSLOT = NT * VPLANE;       // one step's V: each wave has two slots
+  static constexpr int MERGE = kWaves * DTF * 64 * 16 + kWaves * 64 * 8;  // the end-of-item merge (over the slots)
+  static constexpr int LDS = 2 * kWaves * VSLOT > MERGE ? 2 * kWaves * VSLOT : MERGE;
+  static_assert(RB % 64 == 0 && 1024 % RB == 0, "a tile's V rows split evenly over 1 KiB loads");
 };
 
 // Software FP32 -> E4M3 (OCP e4m3fn) with round-to-nearest-even, as torch's float8_e4m3fn cast: |v| > 464
@@ -271,28 +284,20 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
   return d;
 }
 
-// Attention of one work item. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
+// Attention of one work item over a bf16 cache. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
 // (each wave issues a quarter of its loads) into a ring of tile pairs, computed a pair (32 tokens) at a time. Every
 // wave computes the full scores S^T = K Q^T of the pair (cheap on MFMA) and the online softmax, then P x V for its
-// own quarter of the head dim, so no cross-wave merge is needed.
-// KB = 1 (FP8 cache): the stored bytes land in LDS as they are, and each wave converts them to bf16 MFMA operands in
-// registers (scaled by inv_scale, exact for a power-of-two scale): K rows by 16-byte reads, V^T columns by
-// transposing 8-bit reads. Each row's 16-byte chunks are placed in LDS by an XOR swizzle (chunk c of row r at slot
-// c ^ r), so both read patterns spread over the banks.
-// QM = 1 (INT8 cache, KB = 1): each row and KV head carries a bf16 scale in kv_scales [pages, 2, page, hkv]; a
-// tile's scales (16 rows x hkv per plane, contiguous) land with the tile as one dword load per wave (256 dwords: up
-// to 16 KV heads), and the conversion gives bf16(q * s) (q35_group.py kv_page 208-221).
-template <int D, int KB, int QM = 0>
+// own quarter of the head dim, so no cross-wave merge is needed. (An 8-bit cache, half the bytes per token, takes
+// decode_item_8 below: there the conversions make the repeated score work too costly.)
+template <int D>
 __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
                                             const unsigned char* __restrict__ cache, const int* __restrict__ indices,
                                             int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                                            float inv_scale, const unsigned char* __restrict__ kv_scales,
                                             PlanHeader* __restrict__ hdr,
                                             float* __restrict__ part_m, float* __restrict__ part_l,
                                             float* __restrict__ part_o, uint16_t* __restrict__ out,
                                             unsigned char* smem) {
-  using C = PagedCfg<D>;      // the compute layout (bf16)
-  using L = PagedCfg<D, KB>;  // the landing layout of the cached bytes
+  using C = PagedCfg<D>;  // the bf16 tile layout
   const int group = hq / hkv;
   const int b = __builtin_amdgcn_readfirstlane(desc.b), kvh = __builtin_amdgcn_readfirstlane(desc.kvh);
   const int nsplit = __builtin_amdgcn_readfirstlane(desc.nsplit);
@@ -306,27 +311,21 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const float c = sm_scale * kLog2e;
-  const int64_t row_stride = (int64_t)hkv * D * KB;  // bytes between consecutive tokens
+  const int64_t row_stride = (int64_t)hkv * D * 2;  // bytes between consecutive tokens
   const int64_t plane_stride = (int64_t)page_size * row_stride;
   const uint32_t lds0 = lds_addr(smem);
-  // QM: the scale ring (one 1 KiB slot per tile slot) after the landing ring
-  constexpr int scale_lds = 2 * (kAhead1 + 1) * L::BUF;
 
   // the item's page ids, 64 at a time: lane j holds page j of the current chunk
   int chunk = 0;
   int pid = lane < npg ? indices[ibeg + lane] : 0;
 
-  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s (bf16 cache);
-  // an 8-bit cache reads K as 16-byte row chunks (16 d), so steps 2s', 2s' + 1 take d = 64s' + 16g + 8e .. +8, e = 0, 1.
+  // Q as the B operand of S^T = K Q^T: lane (head l16, group g) holds d = 32s + 8g .. +8 at step s
   axk_bf16x8 qb[C::KSTEPS];
   {
     const bool hv = l16 < group;
-    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D;
+    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 8 * g;
 #pragma unroll
-    for (int s = 0; s < C::KSTEPS; ++s) {
-      const int d0 = KB == 2 ? 32 * s + 8 * g : 64 * (s >> 1) + 16 * g + 8 * (s & 1);
-      qb[s] = hv ? load_bf16x8(qp + d0) : zero_bf16x8();
-    }
+    for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 32 * s) : zero_bf16x8();
   }
   // make the compiler take its waits for Q and the page ids here, before the asm loads it cannot count
   asm volatile("" : "+v"(pid));
@@ -335,7 +334,6 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
 
   // tile (lp, tp) = tile tp of the item's page lp -> valid tokens and K base (both wave-uniform: scalar registers);
   // a tile past the sequence end or on a page outside the pool gets nvalid = 0 and an in-bounds base
-  const unsigned char* tile_scales = kv_scales;  // QM: the scales of the tile located last, plane 0
   auto locate = [&](int lp, int tp, int& nvalid) -> const unsigned char* {
     if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
       chunk = lp >> 6;
@@ -351,28 +349,20 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       page = 0;
       nvalid = 0;
     }
-    if constexpr (QM == 1)
-      tile_scales = kv_scales + ((int64_t)page * 2 * page_size + tp * kTile) * hkv * 2;
-    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * D * KB;
+    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * D * 2;
   };
-  // QM: this lane's dword of a tile's scale spans (plane 0 dwords 0 .. 8 hkv - 1, then plane 1; past them dword 0
-  // again, landing in the unused tail of the 1 KiB scale slot)
-  const int sdw = wave * 64 + lane, sspan = 8 * hkv;
-  const uint32_t s_off = sdw < 2 * sspan ? (sdw >= sspan ? (uint32_t)(page_size * hkv * 2 + 4 * (sdw - sspan)) : 4u * sdw) : 0u;
   // per-lane element offsets of this wave's loads inside a tile (token row, plane, 16-byte chunk), and the
-  // same offsets clamped to row 0 for rows past nvalid. An 8-bit cache lands chunk c of row r at chunk slot
-  // c ^ (r mod NCH) of the row (lane slot q loads chunk q ^ (r mod NCH)).
-  constexpr int NCH = L::RB / 16;  // 16-byte chunks per row
+  // same offsets clamped to row 0 for rows past nvalid
+  constexpr int NCH = C::RB / 16;  // 16-byte chunks per row
   // (32-bit: the launch checks that both planes of a page span less than 2^31 bytes)
-  int lane_tok[L::IPW];
-  uint32_t lane_off[L::IPW], lane_off0[L::IPW];  // bytes from the tile's K base
+  int lane_tok[C::IPW];
+  uint32_t lane_off[C::IPW], lane_off0[C::IPW];  // bytes from the tile's K base
 #pragma unroll
-  for (int k = 0; k < L::IPW; ++k) {
-    const int j = wave * L::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
-    const int plane = j / L::IPP, blk = j - plane * L::IPP;
-    lane_tok[k] = blk * L::RPI + lane / NCH;
-    const int chunk = KB == 1 ? (lane % NCH) ^ (lane_tok[k] % NCH) : lane % NCH;
-    lane_off0[k] = (uint32_t)(plane * plane_stride + chunk * 16);
+  for (int k = 0; k < C::IPW; ++k) {
+    const int j = wave * C::IPW + k;  // instruction of the tile: plane j / IPP, block j % IPP
+    const int plane = j / C::IPP, blk = j - plane * C::IPP;
+    lane_tok[k] = blk * C::RPI + lane / NCH;
+    lane_off0[k] = (uint32_t)(plane * plane_stride + (lane % NCH) * 16);
     lane_off[k] = lane_off0[k] + (uint32_t)(lane_tok[k] * row_stride);
   }
   // the tile cursor: issue() takes the item's tiles in order (tile cur_ti = tile cur_tp of page cur_lp); past the
@@ -385,13 +375,12 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     const unsigned char* kbase = locate(cur_lp, cur_tp, nvalid);
     const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
 #pragma unroll
-    for (int k = 0; k < L::IPW; ++k) {
-      const int j = wave * L::IPW + k;
-      const int plane = j / L::IPP, blk = j - plane * L::IPP;
+    for (int k = 0; k < C::IPW; ++k) {
+      const int j = wave * C::IPW + k;
+      const int plane = j / C::IPP, blk = j - plane * C::IPP;
       lds_dma16_so(kbase, lane_tok[k] < nrow ? lane_off[k] : lane_off0[k],
-                   lds0 + nb * L::BUF + plane * L::PLANE + blk * L::BLK);
+                   lds0 + nb * C::BUF + plane * C::PLANE + blk * C::BLK);
     }
-    if constexpr (QM == 1) lds_dma4_so(tile_scales, s_off, lds0 + scale_lds + nb * 1024 + wave * 256);
     const int r = cur_ti < ntiles ? nvalid : 0;
     if (cur_ti + 1 < ntiles && ++cur_tp == tpp) {
       cur_tp = 0;
@@ -464,7 +453,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
     }
   };
 
-  if constexpr (KB == 2) {
+  {
     // Tile pairs: pair p = tiles 2 p, 2 p + 1 in ring slots 2 (p % 2), 2 (p % 2) + 1. Pair p + 1 is issued as pair p
     // starts, into the slots of pair p - 1 (every wave finished it before the barrier), and lands while p computes:
     // the same two tiles in flight as a single-tile ring, with one barrier, one softmax step and one set of page
@@ -483,147 +472,6 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
       if (nva > 0 || nvb > 0) pair_math(smem + sl * C::BUF, nva, nvb);  // uniform over the workgroup
       nva = nna;
       nvb = nnb;
-    }
-  } else {
-    // FP8 / INT8: the pair ring of the bf16 path, kAhead1 pairs ahead (an 8-bit tile is half a bf16 one, so the
-    // deeper look-ahead keeps as many bytes in flight) in a ring of kAhead1 + 1 pairs, and no staging tile: each wave
-    // converts the landed bytes to bf16 operands in registers. Pair pp + kAhead1 is issued as pair pp starts, into
-    // the slots of pair pp - 1 (every wave finished it before the barrier).
-    constexpr int NA = kAhead1;
-    static_assert(NA == 3, "the waits below count up to two pairs in flight behind the one computed");
-    constexpr int IPWQ = L::IPW + (QM == 1 ? 1 : 0);  // this wave's loads of a tile
-    auto row_scale = [&](int slot, int plane, int row) -> float {  // QM: the bf16 scale of a landed row
-      return bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(smem + scale_lds + slot * 1024 + plane * 32 * hkv +
-                                                                  (row * hkv + kvh) * 2));
-    };
-    // 4 stored bytes -> 4 bf16 (2 dwords): FP8 code * inv_scale; INT8: bf16(q * sc) with q = (byte ^ 0x80) - 128 by
-    // the unsigned byte conversion, (u - 128) sc = fma(u, sc, -128 sc) exact (q sc has at most 16 significant bits),
-    // so the bf16 rounding sees fp32(q sc). sc4: the scales of the four bytes.
-    auto cvt4 = [&](uint32_t w, const float* sc4, uint32_t& lo, uint32_t& hi) {
-      if constexpr (QM == 1) {
-        const uint32_t u = w ^ 0x80808080u;
-        lo = pack_bf16x2(__builtin_fmaf((float)(u & 0xffu), sc4[0], -128.0f * sc4[0]),
-                         __builtin_fmaf((float)((u >> 8) & 0xffu), sc4[1], -128.0f * sc4[1]));
-        hi = pack_bf16x2(__builtin_fmaf((float)((u >> 16) & 0xffu), sc4[2], -128.0f * sc4[2]),
-                         __builtin_fmaf((float)(u >> 24), sc4[3], -128.0f * sc4[3]));
-      } else {
-        lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, false));
-        hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, true));
-      }
-    };
-    auto cvt8 = [&](uint32_t w0, uint32_t w1, const float* sc8) -> axk_bf16x8 {
-      uint32_t r0, r1, r2, r3;
-      cvt4(w0, sc8, r0, r1);
-      cvt4(w1, sc8 + 4, r2, r3);
-      const axk_u32x4 r = {r0, r1, r2, r3};
-      return __builtin_bit_cast(axk_bf16x8, r);
-    };
-    // the math of the pair in slots sa_slot, sa_slot + 1 (nva / nvb valid tokens, not both 0): as pair_math, with
-    // K's A operand (lane (token l16, g)) from 16-byte row chunks 4s' + g and V^T's (lane (d, g): tokens 8 g .. +7)
-    // from one transposing 8-bit read per 16 columns (source lane 2j + a: row 8 (g & 1) + j, bytes 8a .. 8a + 7 of the
-    // chunk; lane i receives column i of the eight rows).
-    auto pair_math8 = [&](int sa_slot, int nva, int nvb) {
-      int ta = sa_slot, tb = sa_slot + 1;
-      if (nva <= 0) ta = tb;  // a tile with no valid token (a bad page) may hold any bytes: use the other's
-      if (nvb <= 0) tb = ta;
-      const unsigned char* ka = smem + ta * L::BUF;
-      const unsigned char* kb = smem + tb * L::BUF;
-      float ksa[8], ksb[8];  // this lane's K row scales, replicated (QM)
-      if constexpr (QM == 1) {
-        const float xa = row_scale(ta, 0, l16), xb = row_scale(tb, 0, l16);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          ksa[j] = xa;
-          ksb[j] = xb;
-        }
-      }
-      axk_f32x4 sa = axk_f32x4{0.f, 0.f, 0.f, 0.f}, sb = sa;
-      const int krow = l16 * L::RB, ksw = l16 % NCH;
-#pragma unroll
-      for (int s2 = 0; s2 < C::KSTEPS / 2; ++s2) {
-        const int off = krow + 16 * ((4 * s2 + g) ^ ksw);
-        const axk_u32x4 wa = *reinterpret_cast<const axk_u32x4*>(ka + off);
-        const axk_u32x4 wb = *reinterpret_cast<const axk_u32x4*>(kb + off);
-        sa = mfma_bf16_16x16x32(cvt8(wa[0], wa[1], ksa), qb[2 * s2], sa);
-        sa = mfma_bf16_16x16x32(cvt8(wa[2], wa[3], ksa), qb[2 * s2 + 1], sa);
-        sb = mfma_bf16_16x16x32(cvt8(wb[0], wb[1], ksb), qb[2 * s2], sb);
-        sb = mfma_bf16_16x16x32(cvt8(wb[2], wb[3], ksb), qb[2 * s2 + 1], sb);
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        sa[rr] = (4 * g + rr < nva) ? sa[rr] * c : -INFINITY;
-        sb[rr] = (4 * g + rr < nvb) ? sb[rr] * c : -INFINITY;
-        mx = fmaxf(mx, fmaxf(sa[rr], sb[rr]));
-      }
-      mx = xor32_max(xor16_max(mx));
-      const float m_new = fmaxf(m_run, mx);  // finite: the pair holds at least one valid token
-      const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first pair
-      float psum = 0.f;
-      axk_f32x4 pa, pb;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        pa[rr] = (4 * g + rr < nva) ? __builtin_amdgcn_exp2f(sa[rr] - m_new) : 0.f;
-        pb[rr] = (4 * g + rr < nvb) ? __builtin_amdgcn_exp2f(sb[rr] - m_new) : 0.f;
-        psum += pa[rr] + pb[rr];
-      }
-      psum = xor32_sum(xor16_sum(psum));
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      const axk_bf16x8 pfrag = acc_pair_to_b(pa, pb);
-      const int tv = g < 2 ? ta : tb;
-      const unsigned char* vt = smem + tv * L::BUF + L::PLANE;
-      const int vr = 8 * (g & 1) + (l16 >> 1);
-      float vs[8];  // the scales of this lane group's eight V rows (QM)
-      if constexpr (QM == 1) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) vs[j] = row_scale(tv, 1, 8 * (g & 1) + j);
-      }
-#pragma unroll
-      for (int t = 0; t < C::DT; ++t) {
-        const int ch = wave * C::DT + t;  // the 16 columns of this O^T tile: chunk ch of the rows
-        const axk_i32x2 w = lds_read_tr8(vt + vr * L::RB + 16 * (ch ^ (vr % NCH)) + 8 * (l16 & 1));
-        const axk_bf16x8 vfrag = cvt8((uint32_t)w[0], (uint32_t)w[1], vs);
-        if (moved) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
-        }
-        o[t] = mfma_bf16_16x16x32(vfrag, pfrag, o[t]);
-      }
-    };
-
-    const int npairs = (ntiles + 1) / 2;
-    int nv[NA][2];  // valid tokens of pairs pp .. pp + NA - 1
-#pragma unroll
-    for (int j = 0; j < NA; ++j) {
-      nv[j][0] = nv[j][1] = 0;
-      if (j < npairs) {  // uniform
-        nv[j][0] = issue(2 * j);  // tiles 2 j, 2 j + 1
-        nv[j][1] = issue(2 * j + 1);
-      }
-    }
-    for (int pp = 0; pp < npairs; ++pp) {
-      // this wave's loads of pair pp have landed: the pairs issued after it may still be in flight
-      const int later = min(NA - 1, npairs - 1 - pp);  // uniform
-      if (later >= 2) wait_vmcnt<4 * IPWQ>();
-      else if (later == 1) wait_vmcnt<2 * IPWQ>();
-      else wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();  // ... and every other wave's; all are done with pair pp - 1
-      int nn0 = 0, nn1 = 0;
-      if (pp + NA < npairs) {  // uniform
-        const int ns = 2 * ((pp + NA) % (NA + 1));
-        nn0 = issue(ns);  // tiles 2 (pp + NA), 2 (pp + NA) + 1
-        nn1 = issue(ns + 1);
-      }
-      if (nv[0][0] > 0 || nv[0][1] > 0) pair_math8(2 * (pp % (NA + 1)), nv[0][0], nv[0][1]);  // uniform
-#pragma unroll
-      for (int j = 0; j + 1 < NA; ++j) {
-        nv[j][0] = nv[j + 1][0];
-        nv[j][1] = nv[j + 1][1];
-      }
-      nv[NA - 1][0] = nn0;
-      nv[NA - 1][1] = nn1;
     }
   }
   wait_vmcnt<0>();  // every load has landed before the buffers are reused
@@ -655,11 +503,337 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   }
 }
 
+// Attention of one work item over an 8-bit cache (FP8 E4M3 codes * inv_scale, exact for a power-of-two scale; QM = 1:
+// INT8 codes q, bf16(q * s) with s the bf16 scale of the row and KV head in kv_scales [pages, 2, page, hkv],
+// q35_group.py kv_page 208-221), the item's tiles split between the 4 waves. A step is a pair of 16-token tiles
+// (16 KiB of K and V at D = 256); wave w streams steps [ns w / 4, ns (w + 1) / 4) of the item's ns steps with its own
+// online softmax, so every stored byte is converted once (no score or softmax work is repeated across waves): K
+// straight into registers (lane (token l16, g) loads the 16-byte row chunks 64 s' + 16 g of its MFMA A operand), V by
+// direct loads into the wave's LDS slot (chunk c of row r at chunk slot c ^ (r mod NCH), so the transposing 8-bit reads
+// spread over the banks), read back transposed as the A operand of O^T += V^T P^T. The next step's loads are issued
+// before the current step is computed; no barrier while streaming. At the end the four (m, l, O) are merged through
+// LDS and each wave finishes a quarter of the head dim.
+template <int D, int QM>
+__device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, const uint16_t* __restrict__ q,
+                                              const unsigned char* __restrict__ cache,
+                                              const int* __restrict__ indices, int hq, int hkv, int page_size,
+                                              int64_t num_pages, float sm_scale, float inv_scale,
+                                              const unsigned char* __restrict__ kv_scales,
+                                              PlanHeader* __restrict__ hdr, float* __restrict__ part_m,
+                                              float* __restrict__ part_l, float* __restrict__ part_o,
+                                              uint16_t* __restrict__ out, unsigned char* smem) {
+  using C = PagedCfg<D>;  // each wave's final quarter of the head dim
+  using W = WaveCfg<D>;
+  constexpr int NT = W::NT, RB = W::RB, NCH = W::NCH, KLT = W::KLT, KL = W::KL, DTF = W::DTF;
+  const int group = hq / hkv;
+  const int b = __builtin_amdgcn_readfirstlane(desc.b), kvh = __builtin_amdgcn_readfirstlane(desc.kvh);
+  const int nsplit = __builtin_amdgcn_readfirstlane(desc.nsplit);
+  const int npg = __builtin_amdgcn_readfirstlane(desc.npg), last_valid = __builtin_amdgcn_readfirstlane(desc.last_valid);
+  const int ibeg = __builtin_amdgcn_readfirstlane(desc.ibeg);
+  const int tpp = page_size / kTile;  // tiles per page
+  // tiles holding at least one valid token: the item's last page stops after its last valid token
+  const int ntiles = npg > 0 ? (npg - 1) * tpp + min(tpp, max(0, (last_valid + kTile - 1) / kTile)) : 0;
+  const int nsteps = (ntiles + NT - 1) / NT;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const float c = sm_scale * kLog2e;
+  const int64_t row_stride = (int64_t)hkv * RB;  // bytes between consecutive tokens
+  const int64_t plane_stride = (int64_t)page_size * row_stride;
+  const int s_beg = (nsteps * wave) >> 2, s_end = (nsteps * (wave + 1)) >> 2;
+
+  // Q as the B operand of S^T = K Q^T: K is read as 16-byte row chunks (16 d), so lane (head l16, group g) holds
+  // d = 64s' + 16g + 8e .. +8 at k-step 2s' + e, e = 0, 1
+  axk_bf16x8 qb[C::KSTEPS];
+  {
+    const bool hv = l16 < group;
+    const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 16 * g;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 64 * (s >> 1) + 8 * (s & 1)) : zero_bf16x8();
+  }
+
+  // the tile cursor: tiles are taken in order (tile cur_ti = tile cur_tp of the item's page cur_lp); past the item's
+  // last tile it re-reads that tile and counts no tokens
+  int cur_ti = s_beg * NT;
+  int cur_lp = cur_ti / tpp, cur_tp = cur_ti - cur_lp * tpp;
+  // the item's page ids, 64 at a time: lane j holds page j of the current chunk
+  int chunk = cur_lp >> 6;
+  int pid = (chunk << 6) + lane < npg ? indices[ibeg + (chunk << 6) + lane] : 0;
+  // tile (lp, tp) -> valid tokens and its K base (both wave-uniform); a tile on a page outside the pool gets
+  // nvalid = 0 and an in-bounds base (page 0); QM: sbase = the tile's row scales, plane 0
+  auto locate = [&](int lp, int tp, int& nvalid, const unsigned char*& sbase) -> const unsigned char* {
+    if ((lp >> 6) != chunk) {  // wave-uniform: next 64 page ids (every 64 pages)
+      chunk = lp >> 6;
+      const int j = (chunk << 6) + lane;
+      pid = j < npg ? indices[ibeg + j] : 0;
+    }
+    int page = __builtin_amdgcn_readlane(pid, lp & 63);
+    const int valid_in_page = (lp == npg - 1) ? last_valid : page_size;
+    nvalid = min(kTile, valid_in_page - tp * kTile);
+    if (page < 0 || page >= num_pages) {
+      if (lane == 0 && nvalid > 0) hdr->bad_page = 1;
+      page = 0;
+      nvalid = 0;
+    }
+    if constexpr (QM == 1) sbase = kv_scales + ((int64_t)page * 2 * page_size + tp * kTile) * hkv * 2;
+    return cache + (int64_t)page * 2 * plane_stride + (int64_t)(tp * kTile) * row_stride + (int64_t)kvh * RB;
+  };
+
+  // one step: K (tile j, chunk s': k[j KLT + s']) and (QM) the scales of this lane's K row (ks[j]) and of the eight V
+  // rows its transposing reads return (vs) into registers by ordinary loads; V by direct loads into the wave's LDS
+  // slot (asm: the compiler counts none of them; wait_step waits for everything)
+  struct Step {
+    axk_u32x4 k[KL];
+    int nv[NT];
+    float ks[NT];
+    float vs[8];
+  };
+  // per-lane V load offsets inside a tile (token row, 16-byte chunk: lane slot q of row r loads chunk q ^ (r mod NCH)),
+  // and the same clamped to row 0 for rows past nvalid
+  constexpr int VPT = KLT;  // V loads per tile (1 KiB each)
+  int vtok[VPT];
+  uint32_t voff[VPT], voff0[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    vtok[i] = i * (64 / NCH) + lane / NCH;
+    const int ch = (lane % NCH) ^ (vtok[i] % NCH);
+    voff0[i] = (uint32_t)(plane_stride + 16 * ch);
+    voff[i] = voff0[i] + (uint32_t)(vtok[i] * row_stride);
+  }
+  const uint32_t lds_slots = lds_addr(smem) + wave * 2 * W::VSLOT;
+  auto issue_step = [&](Step& st, int sl) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      int nvalid;
+      const unsigned char* sb = nullptr;
+      const unsigned char* base = locate(cur_lp, cur_tp, nvalid, sb);
+      st.nv[j] = cur_ti < ntiles ? nvalid : 0;
+      const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
+      if (cur_ti + 1 < ntiles && ++cur_tp == tpp) {
+        cur_tp = 0;
+        ++cur_lp;
+      }
+      ++cur_ti;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        lds_dma16_so(base, vtok[i] < nrow ? voff[i] : voff0[i],
+                     lds_slots + sl * W::VSLOT + j * W::VPLANE + i * 1024);
+      const int kr = l16 < nrow ? l16 : 0;
+      const unsigned char* kp = base + (uint32_t)(kr * row_stride + 16 * g);
+#pragma unroll
+      for (int s = 0; s < KLT; ++s)
+        st.k[j * KLT + s] = __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(kp + 64 * s));
+      if constexpr (QM == 1) {
+        st.ks[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sb + (kr * hkv + kvh) * 2));
+        // this lane's V^T rows: 8 (g & 1) + jj of tile g / 2; scale 0 for a tile without
+        // a valid token (its bytes may be anything: the math reads the other tile's V for it, with zero weights)
+        if (j == (g >= 2 ? 1 : 0)) {
+          const unsigned char* s1 = sb + (int64_t)page_size * hkv * 2;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const int r = 8 * (g & 1) + jj;
+            const float x = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(s1 + ((r < nrow ? r : 0) * hkv + kvh) * 2));
+            st.vs[jj] = st.nv[j] > 0 ? x : 0.f;
+          }
+        }
+      }
+    }
+  };
+  // every load of the step has landed (the register values pass through the wait, so the compiler adds none later)
+  auto wait_step = [&](Step& st) {
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int i = 0; i < KL; ++i) asm volatile("" : "+v"(st.k[i]));
+    if constexpr (QM == 1) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) asm volatile("" : "+v"(st.ks[j]));
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) asm volatile("" : "+v"(st.vs[jj]));
+    }
+  };
+
+  // 4 stored bytes -> 4 bf16 (2 dwords): FP8 code * inv_scale; INT8: bf16(q * sc) with q = (byte ^ 0x80) - 128 by
+  // the unsigned byte conversion, (u - 128) sc = fma(u, sc, -128 sc) exact (q sc has at most 16 significant bits),
+  // so the bf16 rounding sees fp32(q sc). sc4: the scales of the four bytes.
+  auto cvt4 = [&](uint32_t w, const float* sc4, uint32_t& lo, uint32_t& hi) {
+    if constexpr (QM == 1) {
+      const uint32_t u = w ^ 0x80808080u;
+      lo = pack_bf16x2(__builtin_fmaf((float)(u & 0xffu), sc4[0], -128.0f * sc4[0]),
+                       __builtin_fmaf((float)((u >> 8) & 0xffu), sc4[1], -128.0f * sc4[1]));
+      hi = pack_bf16x2(__builtin_fmaf((float)((u >> 16) & 0xffu), sc4[2], -128.0f * sc4[2]),
+                       __builtin_fmaf((float)(u >> 24), sc4[3], -128.0f * sc4[3]));
+    } else {
+      lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, false));
+      hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, true));
+    }
+  };
+  auto cvt8 = [&](uint32_t w0, uint32_t w1, const float* sc8) -> axk_bf16x8 {
+    uint32_t r0, r1, r2, r3;
+    cvt4(w0, sc8, r0, r1);
+    cvt4(w1, sc8 + 4, r2, r3);
+    const axk_u32x4 r = {r0, r1, r2, r3};
+    return __builtin_bit_cast(axk_bf16x8, r);
+  };
+
+  // O^T over the full head dim: lane holds O[head l16][d = 16t + 4g + r]
+  axk_f32x4 o[DTF];
+#pragma unroll
+  for (int t = 0; t < DTF; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g)
+
+  // the math of one step whose V is in the slot (at least one valid token)
+  auto compute = [&](const Step& st, int sl) {
+    const unsigned char* slot = smem + (wave * 2 + sl) * W::VSLOT;
+    axk_f32x4 sc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      sc[j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+      float ksc[8];
+      if constexpr (QM == 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ksc[e] = st.ks[j];
+      }
+#pragma unroll
+      for (int s = 0; s < KLT; ++s) {
+        const axk_u32x4 w = st.k[j * KLT + s];
+        sc[j] = mfma_bf16_16x16x32(cvt8(w[0], w[1], ksc), qb[2 * s], sc[j]);
+        sc[j] = mfma_bf16_16x16x32(cvt8(w[2], w[3], ksc), qb[2 * s + 1], sc[j]);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        sc[j][rr] = (4 * g + rr < st.nv[j]) ? sc[j][rr] * c : -INFINITY;
+        mx = fmaxf(mx, sc[j][rr]);
+      }
+    mx = xor32_max(xor16_max(mx));
+    const float m_new = fmaxf(m_run, mx);  // finite: the step holds at least one valid token
+    // the running max rarely moves after the first steps: rescale O only when it did (wave-uniform test)
+    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first step
+    float psum = 0.f;
+    axk_f32x4 p[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        p[j][rr] = (4 * g + rr < st.nv[j]) ? __builtin_amdgcn_exp2f(sc[j][rr] - m_new) : 0.f;
+        psum += p[j][rr];
+      }
+    psum = xor32_sum(xor16_sum(psum));
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    if (moved) {
+#pragma unroll
+      for (int t = 0; t < DTF; ++t)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+    }
+    // the 32-deep step: P^T's B operand from both score tiles by two lane swaps; V^T's A operand (lane (d, g):
+    // tokens 8 g .. 8 g + 7 = tile g / 2, rows 8 (g & 1) .. + 7) by one transposing 8-bit read per 16 columns
+    // (source lane 2j + a: row 8 (g & 1) + j, bytes 8a .. 8a + 7 of the chunk; lane i receives column i). A tile
+    // without a valid token (a bad page: any bytes) is read from the other tile, with zero weights.
+    const axk_bf16x8 pfrag = acc_pair_to_b(p[0], p[1]);
+    int tv = g >= 2 ? 1 : 0;
+    if (st.nv[tv] <= 0) tv = 1 - tv;
+    const int vr = 8 * (g & 1) + (l16 >> 1);
+    const unsigned char* vrow = slot + tv * W::VPLANE + vr * RB + 8 * (l16 & 1);
+    const int vsw = vr % NCH;
+#pragma unroll
+    for (int t = 0; t < DTF; ++t) {
+      const axk_i32x2 w = lds_read_tr8(vrow + 16 * (t ^ vsw));
+      o[t] = mfma_bf16_16x16x32(cvt8((uint32_t)w[0], (uint32_t)w[1], st.vs), pfrag, o[t]);
+    }
+  };
+
+  auto any_valid = [&](const Step& st) {
+    bool a = false;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) a = a || st.nv[j] > 0;
+    return a;
+  };
+  Step sa, sb;
+  if (s_beg < s_end) issue_step(sa, 0);
+  for (int s = s_beg; s < s_end; s += 2) {  // uniform
+    wait_step(sa);
+    if (s + 1 < s_end) issue_step(sb, 1);  // the next step's loads fly while this one is computed
+    if (any_valid(sa)) compute(sa, 0);
+    if (s + 1 >= s_end) break;
+    wait_step(sb);
+    if (s + 2 < s_end) issue_step(sa, 0);
+    if (any_valid(sb)) compute(sb, 1);
+  }
+
+  // merge the four waves' (m, l, O^T) through LDS (over the V slots): wave w takes the head-dim quarter
+  // [w D / 4, (w + 1) D / 4)
+  __syncthreads();  // every wave is done with its slot
+  float* mo = reinterpret_cast<float*>(smem);      // [wave][t][lane][4]
+  float* ml = mo + kWaves * DTF * 64 * 4;          // [wave][lane][2]
+#pragma unroll
+  for (int t = 0; t < DTF; ++t) *reinterpret_cast<axk_f32x4*>(mo + ((wave * DTF + t) * 64 + lane) * 4) = o[t];
+  ml[(wave * 64 + lane) * 2] = m_run;
+  ml[(wave * 64 + lane) * 2 + 1] = l_run;
+  __syncthreads();
+  float mw[kWaves], lw[kWaves];
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    mw[w] = ml[(w * 64 + lane) * 2];
+    lw[w] = ml[(w * 64 + lane) * 2 + 1];
+    M = fmaxf(M, mw[w]);
+  }
+  float fw[kWaves];
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    fw[w] = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);  // a wave without tokens: -inf, 0
+    L += fw[w] * lw[w];
+  }
+  axk_f32x4 of[C::DT];
+#pragma unroll
+  for (int t = 0; t < C::DT; ++t) {
+    of[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const axk_f32x4 x = *reinterpret_cast<const axk_f32x4*>(mo + ((w * DTF + wave * C::DT + t) * 64 + lane) * 4);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) of[t][rr] += fw[w] * x[rr];
+    }
+  }
+
+  // (M, L) for head l16 and O^T for this wave's columns d = wave DW + 16t + 4g + r
+  const int64_t out_base = ((int64_t)b * hq + kvh * group) * D;
+  const bool hv = l16 < group;
+  if (nsplit == 1) {  // the whole sequence in one item: normalise and store
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+    for (int t = 0; t < C::DT; ++t) {
+      if (!hv) continue;
+      uint2 w;
+      w.x = f32_to_bf16_bits(of[t][0] * inv) | (f32_to_bf16_bits(of[t][1] * inv) << 16);
+      w.y = f32_to_bf16_bits(of[t][2] * inv) | (f32_to_bf16_bits(of[t][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(out + out_base + (int64_t)l16 * D + wave * C::DW + 16 * t + 4 * g) = w;
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < C::DT; ++t)
+    if (hv)
+      *reinterpret_cast<float4*>(part_o + ((int64_t)it * group + l16) * D + wave * C::DW + 16 * t + 4 * g) =
+          make_float4(of[t][0], of[t][1], of[t][2], of[t][3]);
+  if (wave == 0 && lane < group) {
+    part_m[(int64_t)it * group + lane] = M;
+    part_l[(int64_t)it * group + lane] = L;
+  }
+}
+
 // Persistent split kernel: a few workgroups per CU; workgroup w takes items w, w + gridDim.x, ... (the plan
 // sizes the items to about one per workgroup). With local != 0 the descriptors come from the page table
 // directly (local_plan), otherwise from the plan in the workspace.
 template <int D, int KB, int QM = 0>
-__global__ __launch_bounds__(256) void paged_decode_kernel(
+__global__ __launch_bounds__(256, KB == 1 ? 2 : 1) void paged_decode_kernel(
     const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ indptr,
     const int* __restrict__ last_page_len, const int* __restrict__ indices, int batch, int hq, int hkv,
     int page_size, int64_t num_pages, float sm_scale, float inv_scale, const unsigned char* __restrict__ kv_scales,
@@ -671,9 +845,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
     const LocalPlan lp = local_plan(indptr, last_page_len, bias, batch, hkv, gridDim.x);
     for (int it = blockIdx.x; it < lp.n_items; it += gridDim.x) {
       const ItemDesc desc = local_item(lp, it, batch, page_size);
-      decode_item<D, KB, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
-                             kv_scales, hdr,
-                         part_m, part_l, part_o, out, smem);
+      if constexpr (KB == 2)
+        decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
+                       part_o, out, smem);
+      else
+        decode_item_8<D, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
+                             kv_scales, hdr, part_m, part_l, part_o, out, smem);
       __syncthreads();  // LDS is reused by the next item
     }
     return;
@@ -685,9 +862,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(
   if (h.batch != batch || h.hkv != hkv) return;
   for (int it = blockIdx.x; it < h.n_items; it += gridDim.x) {
     if (it != (int)blockIdx.x) desc = descs[it];
-    decode_item<D, KB, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
-                           kv_scales, hdr,
-                       part_m, part_l, part_o, out, smem);
+    if constexpr (KB == 2)
+      decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
+                     part_o, out, smem);
+    else
+      decode_item_8<D, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
+                           kv_scales, hdr, part_m, part_l, part_o, out, smem);
     __syncthreads();
   }
 }
@@ -1202,11 +1382,11 @@ int split_grid(int batch, int hkv) {
   return (int)(items < slots ? items : slots);
 }
 
-// The split kernel's dynamic LDS: the ring of landed tiles (an INT8 cache: and a 1 KiB scale slot per tile slot).
+// The split kernel's dynamic LDS: a bf16 cache: the ring of tile pairs; an 8-bit cache: the waves' V slots (the
+// end-of-item merge reuses them).
 template <int D, int KB, int QM>
 constexpr size_t split_lds() {
-  return KB == 1 ? (size_t)2 * (kAhead1 + 1) * (PagedCfg<D, KB>::BUF + (QM == 1 ? 1024 : 0))
-                 : (size_t)kNBufPair * PagedCfg<D>::BUF;
+  return KB == 1 ? (size_t)WaveCfg<D>::LDS : (size_t)kNBufPair * PagedCfg<D>::BUF;
 }
 
 // Allows the split kernel its dynamic LDS (above 64 KiB), once per process.
