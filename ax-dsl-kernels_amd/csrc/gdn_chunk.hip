@@ -495,6 +495,8 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
   __shared__ __align__(16) uint16_t sS[SW * kLdS];
   __shared__ __align__(16) uint16_t sV[SW * kLdV];
   __shared__ __align__(16) uint16_t sXd[SW * kLdV];
+  __shared__ __align__(16) uint16_t sO[NW][16 * SW];  // a wave's 16 output rows, staged for 16-byte stores
+  static_assert(Sh::CG == 1, "each wave holds all the slice's columns of its rows (the staged stores)");
   const int nbh = p.B * p.NV;
   const int slice = blockIdx.x / nbh, bh = blockIdx.x - slice * nbh;  // slices of a head share an XCD
   const int b = bh / p.NV, h = bh - b * p.NV, kh = (h / p.kdiv) % p.NK;
@@ -513,8 +515,10 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
   sbase.gam = p.ws.gam + vbase * kC + 16 * tt + 4 * g4;
   sbase.dec = p.ws.dec + vbase * kC + 16 * tt + 4 * g4;
   sbase.glast = p.ws.gam + vbase * kC + kC - 1;
-  // the wave's output column of token row 0; token t at + t * ostride
-  uint16_t* obase = p.out + ((int64_t)b * p.T * p.NV + h) * kD + col0 + l16;
+  // output rows leave as 16-byte stores: lane i < 2 SW of the wave writes 8 columns of token row 16 tt + i / (SW / 8)
+  constexpr int OL = 16 * SW / 8;  // lanes storing a wave's 16 rows
+  const int otok = lane / (SW / 8), ocol = 8 * (lane % (SW / 8));
+  uint16_t* obase = p.out + ((int64_t)b * p.T * p.NV + h) * kD + 16 * slice * Sh::CT + ocol;
   const int64_t ostride = (int64_t)p.NV * kD;
 
   // state rows 32 tt + 16 i + 4 g + r, columns col0 + 16 j + l16, in MFMA accumulator tiles
@@ -572,16 +576,15 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ScanArgs p) {
       axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 2; ++st) acc = mfma_bf16_16x16x32(o.pf[st], load_bf16x8(sV + lc * kLdV + 32 * st + 8 * g4), acc);
-      const int t0 = c * kC + 16 * tt + 4 * g4;
-      uint16_t* orow = obase + t0 * ostride + 16 * j;
-      if (c * kC + kC <= p.T) {  // a whole chunk (every one but possibly the last): no per-row test
 #pragma unroll
-        for (int r = 0; r < 4; ++r) orow[r * ostride] = (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (t0 + r < p.T) orow[r * ostride] = (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
-      }
+      for (int r = 0; r < 4; ++r)
+        sO[wave][(4 * g4 + r) * SW + 16 * (ct_l + j) + l16] = (uint16_t)f32_to_bf16_bits(base[j][r] * gmr[r] + acc[r]);
+    }
+    // the wave's rows out of its own staging (in order after its writes: no barrier)
+    if (lane < OL) {
+      const int t = c * kC + 16 * tt + otok;
+      const uint4 v = *reinterpret_cast<const uint4*>(&sO[wave][otok * SW + ocol]);
+      if (t < p.T) *reinterpret_cast<uint4*>(obase + t * ostride) = v;
     }
     // S <- Gamma_last S + k^T (v_new * decay_last)
 #pragma unroll
