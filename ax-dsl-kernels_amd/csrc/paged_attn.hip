@@ -872,9 +872,10 @@ __global__ __launch_bounds__(256, KB == 1 ? 2 : 1) void paged_decode_kernel(
   }
 }
 
-// One workgroup per (sequence, query head): log-sum-exp merge of the item partials of a sequence with more than
-// one split; zero output for a sequence without pages. Wave w merges splits w, w + 4, ... (16 per pass, every
-// load of a pass issued before any is used); the four running (m, l, O) are combined in LDS.
+// One wave per (sequence, query head), four per workgroup: log-sum-exp merge of the item partials of a sequence with
+// more than one split; zero output for a sequence without pages. Splits are taken 16 at a time: lane j loads split
+// j's (m, l) while every lane loads its D / 64 columns of the 16 splits' O (all of a pass issued before any is used,
+// the O loads independent of m), then one running (m, l, O) per wave; no LDS, no barrier.
 template <int D>
 __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict__ indptr,
                                                           const int* __restrict__ last_page_len,
@@ -886,10 +887,11 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
                                                           const float* __restrict__ part_o,
                                                           uint16_t* __restrict__ out) {
   constexpr int V = D / 64;  // output columns per lane
-  __shared__ float s_m[4], s_l[4];
-  __shared__ float s_acc[4][D];
-  const int b = blockIdx.x / hq, h = blockIdx.x - (blockIdx.x / hq) * hq;
+  constexpr int P = 16;      // splits per pass
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int bh = blockIdx.x * 4 + wave;
+  if (bh >= batch * hq) return;  // a whole wave
+  const int b = bh / hq, h = bh - b * hq;
   const int group = hq / hkv, kvh = h / group, hh = h - kvh * group;
   int np, nsplit, i0;
   if (local) {
@@ -909,70 +911,44 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
   }
   uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
   if (np == 0) {
-    if (wave == 0) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) op[j] = 0;
-    }
+    for (int j = 0; j < V; ++j) op[j] = 0;
     return;
   }
   if (nsplit <= 1) return;  // written by the decode kernel
-  constexpr int P = 16;
   float mm = -INFINITY, ll = 0.f, acc[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) acc[j] = 0.f;
-  for (int c0 = wave; c0 < nsplit; c0 += 4 * P) {
-    float mi[P], li[P], oi[P][V];
+  for (int c0 = 0; c0 < nsplit; c0 += P) {
+    // item of split i: i0 + i hkv (items are in (split, KV head) order); clamped: in-bounds, weight zeroed below
+    const int js = min(c0 + (lane & (P - 1)), nsplit - 1);
+    const int64_t ij = (int64_t)(i0 + js * hkv) * group + hh;
+    const float mj = part_m[ij], lj = part_l[ij];
+    float oi[P][V];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      // item of split i: i0 + i hkv (items are in (split, KV head) order); clamped: in-bounds, weight zeroed below
-      const int i = min(c0 + 4 * k, nsplit - 1) * hkv;
-      mi[k] = part_m[(int64_t)(i0 + i) * group + hh];
-      li[k] = part_l[(int64_t)(i0 + i) * group + hh];
-      const float* src = part_o + ((int64_t)(i0 + i) * group + hh) * D + lane * V;
+      const float* src = part_o + ((int64_t)(i0 + min(c0 + k, nsplit - 1) * hkv) * group + hh) * D + lane * V;
 #pragma unroll
       for (int j = 0; j < V; ++j) oi[k][j] = src[j];
     }
-    float cm = mm;
-#pragma unroll
-    for (int k = 0; k < P; ++k)
-      if (c0 + 4 * k < nsplit) cm = fmaxf(cm, mi[k]);
+    const bool jv = (lane < P) && (c0 + lane < nsplit) && mj != -INFINITY;
+    const float cm = fmaxf(mm, wave_max(jv ? mj : -INFINITY));
+    const float wj = jv ? exp2f(mj - cm) : 0.f;  // lane j < P: split c0 + j's weight
     const float sc = mm == -INFINITY ? 0.f : exp2f(mm - cm);
-    ll *= sc;
+    ll = ll * sc + wave_sum(wj * lj);
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] *= sc;
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      const float w = (c0 + 4 * k < nsplit && mi[k] != -INFINITY) ? exp2f(mi[k] - cm) : 0.f;
-      ll += w * li[k];
+      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), k));
 #pragma unroll
       for (int j = 0; j < V; ++j) acc[j] += w * oi[k][j];
     }
     mm = cm;
   }
-  if (lane == 0) {
-    s_m[wave] = mm;
-    s_l[wave] = ll;
-  }
+  const float inv = ll > 0.f ? 1.0f / ll : 0.f;
 #pragma unroll
-  for (int j = 0; j < V; ++j) s_acc[wave][lane * V + j] = acc[j];
-  __syncthreads();
-  if (wave != 0) return;
-  float M = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w]);
-  float L = 0.f, o[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) o[j] = 0.f;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float f = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - M);  // a wave without splits holds -inf, 0
-    L += f * s_l[w];
-#pragma unroll
-    for (int j = 0; j < V; ++j) o[j] += f * s_acc[w][lane * V + j];
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-#pragma unroll
-  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(o[j] * inv);
+  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
 }
 
 // cache[loc[b,0], 0, loc[b,1], kvh, :] = k[b, kvh, :]; plane 1 <- v (store_paged_kv, flash_attn.py:53-84).
@@ -1419,7 +1395,8 @@ int launch_merge(const int* indptr, const int* last, uint16_t* out, int batch, i
                  void* ws, hipStream_t st, int kb = 2, int bias = 0) {
   const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
-  hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)(batch * hq)), dim3(256), 0, st, indptr, last, v.hdr,
+  hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)((batch * hq + 3) / 4)), dim3(256), 0, st, indptr, last,
+                     v.hdr,
                      v.item_off, batch, hq, hkv, split_grid(batch, hkv), local, bias, v.pm, v.pl, v.po, out);
   return axk_launch_status();
 }
