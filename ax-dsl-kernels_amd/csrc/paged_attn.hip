@@ -601,7 +601,15 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     voff[i] = voff0[i] + (uint32_t)(vtok[i] * row_stride);
   }
   const uint32_t lds_slots = lds_addr(smem) + wave * 2 * W::VSLOT;
+  // this lane's K row offset (token l16, chunk g) and the same for row 0; QM: its K row's scale offset, and the V
+  // scales of rows 8 (g & 1) + jj at vs_off + jj hkv 2 (plane 1), row 0's at vs_off0
+  const uint32_t k_off = (uint32_t)(l16 * row_stride + 16 * g), k_off0 = (uint32_t)(16 * g);
+  const uint32_t ks_off = (uint32_t)((l16 * hkv + kvh) * 2), ks_off0 = (uint32_t)(kvh * 2);
+  const uint32_t vs_off0 = (uint32_t)(page_size * hkv * 2 + kvh * 2);
+  const uint32_t vs_off = vs_off0 + (uint32_t)(8 * (g & 1) * hkv * 2);
   auto issue_step = [&](Step& st, int sl) {
+    const unsigned char* sbs[NT];
+    int nrows[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       int nvalid;
@@ -609,6 +617,8 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
       const unsigned char* base = locate(cur_lp, cur_tp, nvalid, sb);
       st.nv[j] = cur_ti < ntiles ? nvalid : 0;
       const int nrow = nvalid > 0 ? nvalid : 1;  // every address stays inside the tile's valid rows
+      sbs[j] = sb;
+      nrows[j] = nrow;
       if (cur_ti + 1 < ntiles && ++cur_tp == tpp) {
         cur_tp = 0;
         ++cur_lp;
@@ -618,24 +628,27 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
       for (int i = 0; i < VPT; ++i)
         lds_dma16_so(base, vtok[i] < nrow ? voff[i] : voff0[i],
                      lds_slots + sl * W::VSLOT + j * W::VPLANE + i * 1024);
-      const int kr = l16 < nrow ? l16 : 0;
-      const unsigned char* kp = base + (uint32_t)(kr * row_stride + 16 * g);
+      const bool krow = l16 < nrow;
+      const unsigned char* kp = base + (krow ? k_off : k_off0);
 #pragma unroll
       for (int s = 0; s < KLT; ++s)
         st.k[j * KLT + s] = __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(kp + 64 * s));
-      if constexpr (QM == 1) {
-        st.ks[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sb + (kr * hkv + kvh) * 2));
-        // this lane's V^T rows: 8 (g & 1) + jj of tile g / 2; scale 0 for a tile without
-        // a valid token (its bytes may be anything: the math reads the other tile's V for it, with zero weights)
-        if (j == (g >= 2 ? 1 : 0)) {
-          const unsigned char* s1 = sb + (int64_t)page_size * hkv * 2;
+      if constexpr (QM == 1)
+        st.ks[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sb + (krow ? ks_off : ks_off0)));
+    }
+    if constexpr (QM == 1) {
+      // this lane's V^T rows: 8 (g & 1) + jj of tile g / 2; scale 0 for a tile without a valid token (its bytes may be
+      // anything: the math reads the other tile's V for it, with zero weights)
+      const int tv = g >= 2 ? 1 : 0;
+      const unsigned char* s1 = tv ? sbs[1] : sbs[0];
+      const int nr = tv ? nrows[1] : nrows[0];
+      const bool live = (tv ? st.nv[1] : st.nv[0]) > 0;
+      const uint32_t hs = (uint32_t)(hkv * 2);
 #pragma unroll
-          for (int jj = 0; jj < 8; ++jj) {
-            const int r = 8 * (g & 1) + jj;
-            const float x = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(s1 + ((r < nrow ? r : 0) * hkv + kvh) * 2));
-            st.vs[jj] = st.nv[j] > 0 ? x : 0.f;
-          }
-        }
+      for (int jj = 0; jj < 8; ++jj) {
+        const bool in = 8 * (g & 1) + jj < nr;
+        const float x = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(s1 + (in ? vs_off + jj * hs : vs_off0)));
+        st.vs[jj] = live ? x : 0.f;
       }
     }
   };
