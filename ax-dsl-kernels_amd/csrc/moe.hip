@@ -10,22 +10,21 @@
 // [E, 2F, H/32]; down e_dw [E, H, F/2], e_ds [E, H, F/32] (models/qwen35_35b_a3b/qwen35_35b_a3b.manifest.json).
 //
 // Router (axk_moe_decode; q35_layer_mc.py:820-829):
-//   router_full  — decode: GEMV over the whole K, workgroup = (16 experts, 16 tokens), 16 waves summed in wave order;
-//                  final fp32 logits, and the shared gate's logit h2 . w_shg from one extra expert block
+//   router       — decode: GEMV split over K, workgroup = (16 experts, 16 tokens, K slice), partial logits per
+//                  slice; one extra expert block forms the shared gate's partial logit h2 . w_shg per slice
 //   router_tile  — prefill: 64 x 64 MFMA tiles of tokens x experts over two K halves
-//   route_part   — one wave per token: the partials summed in fixed order into the logits (decode: the final
-//                  logits read in place), softmax, top-K by ballot rounds (ties: lower id), renormalised weights;
-//                  in decode the last workgroup to finish groups the pairs
+//   route_part   — one wave per token: the partials summed in slice order into the logits (and, in decode, the
+//                  gate logit), softmax, top-K by ballot rounds (ties: lower id), renormalised weights
 //   route        — the same selection from caller logits (axk_moe_route)
 // Experts, decode (tokens <= kDecodeTokens, tokens x top_k <= kMaxPairs):
-//   group   — one workgroup (inside the routing launch when the router ran): per-expert token bitmasks, the (token, slot) pairs ranked by popcount (stable,
-//             deterministic), the active-expert records {rows, expert, first sorted row}
-//   gateup  — workgroup = (active expert or the shared expert, run of 16-row weight tiles): each wave streams its
-//             MXFP4 gate and up rows over the full K. For small row counts the weights pass through a
-//             wave-private LDS tile in 128-byte row segments (whole cache lines per load) and are read back
-//             in the MFMA layout; SwiGLU in the epilogue
-//   down    — the same streaming over hidden-row tiles: act x Wd^T, scaled by the routing weight, written
-//             to y by pair
+//   gateup  — workgroup = (active expert or the shared expert, run of 16-row weight tiles). The workgroup groups
+//             the pairs itself: it reads the top-K ids once, finds the slot-th active expert in ascending id order
+//             from an LDS bitmap and ranks that expert's pairs by ballots (stable, deterministic, no grouping
+//             launch). Each wave streams its MXFP4 gate and up rows over the full K; for small row counts the
+//             weights pass through a wave-private LDS tile in 128-byte row segments (whole cache lines per
+//             load) and are read back in the MFMA layout; SwiGLU in the epilogue, activations by pair
+//   down    — the same grouping and streaming over hidden-row tiles: act x Wd^T, scaled by the routing weight,
+//             written to y by pair
 //   combine — workgroup = (token, columns): shared gate (from the router's gate logit, or a dot here), residual,
 //             sum over the token's K pairs in slot order, one bf16 rounding
 // Every expert's weights are read once per call, whatever the number of its tokens.
