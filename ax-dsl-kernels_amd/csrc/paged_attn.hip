@@ -1817,7 +1817,7 @@ extern "C" int axk_paged_decode_i8(const uint16_t* q, const int8_t* kv_cache, co
   int rc = check_heads(batch, num_qo_heads, num_kv_heads, head_dim);
   if (rc != AXK_OK) return rc;
   AXK_REQUIRE(head_dim == 128 || head_dim == 256, AXK_E_SHAPE);  // whole 1 KiB load blocks split over the waves
-  AXK_REQUIRE(num_kv_heads <= 16, AXK_E_SHAPE);  // a tile's scales: one dword load per wave
+  AXK_REQUIRE(num_kv_heads <= 16, AXK_E_SHAPE);  // the range the INT8 tests cover (HKV 1 .. 16)
   AXK_REQUIRE(page_size >= kTile && page_size % kTile == 0 && page_size <= 4096 && num_pages > 0, AXK_E_SHAPE);
   AXK_REQUIRE(axk_aligned(q, 16) && axk_aligned(kv_cache, 16) && axk_aligned(kv_scales, 4), AXK_E_ALIGN);
   const size_t need = axk_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim);
