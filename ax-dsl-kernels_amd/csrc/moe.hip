@@ -1310,41 +1310,66 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   }
   wait_vmcnt<0>();  // the look-ahead loads land before the workgroup's LDS is released
 
+  // Epilogue. The bf16 outputs (gate-up: act / act_sh; down, routed: bf16(rw * y) by pair) go through an LDS tile
+  // [64 rows][COLS + 8] over the ring, so that each row leaves as 16-byte stores of whole row segments instead of
+  // 2-byte stores of 16 lanes; the shared expert's fp32 down rows are stored directly.
+  constexpr int COLS = MODE == 0 ? kG2Cols0 : kG2Cols1, LDO = COLS + 8;
+  const bool staged = MODE == 0 || !shared;
+  uint16_t* so = reinterpret_cast<uint16_t*>(smem);
+  if (staged) __syncthreads();  // every wave is done with the ring
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * mt + 4 * g4 + r;
-      if (row >= rows) continue;
       const int64_t prow = row0 + row;
       if (MODE == 0) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const int col = col0 + 32 * wave + 16 * j + l16;
-          if (col >= No) continue;
           const float gv = round_bf16(acc[mt][j][r]), uv = round_bf16(acc[mt][j + 2][r]);
-          const uint16_t a = (uint16_t)f32_to_bf16_bits(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
-          if (shared)
-            g.ws.act_sh[prow * g.Fs + col] = a;
-          else
-            g.ws.act[prow * g.F + col] = a;
+          so[row * LDO + 32 * wave + 16 * j + l16] =
+              (uint16_t)f32_to_bf16_bits(gv * __builtin_amdgcn_rcpf(1.0f + __expf(-gv)) * uv);
         }
+      } else if (!shared) {
+        // a routed slot is stored as bf16(rw * y), as the reference's delivered slot kernels store it
+        // (qwen35moe_slots*_bo: SLOT_OUT=bf16, q35_moe_prefill.py:41, 100, 165) and its combine reads it
+        const float rw = row < rows ? g.ws.row_w[prow] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          so[row * LDO + 64 * wave + 16 * j + l16] = (uint16_t)f32_to_bf16_bits(acc[mt][j][r] * rw);
       } else {
-        const float rw = shared ? 1.0f : g.ws.row_w[prow];
-        const int64_t ypair = shared ? 0 : g.ws.row_pair[prow];
+        if (row >= rows) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int col = col0 + 64 * wave + 16 * j + l16;
-          if (col >= No) continue;
-          // a routed slot is stored as bf16(rw * y), as the reference's delivered slot kernels store it
-          // (qwen35moe_slots*_bo: SLOT_OUT=bf16, q35_moe_prefill.py:41, 100, 165) and its combine reads it
-          if (shared)
-            g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
-          else
-            reinterpret_cast<uint16_t*>(g.ws.y)[ypair * g.H + col] = (uint16_t)f32_to_bf16_bits(acc[mt][j][r] * rw);
+          if (col < No) g.ws.y_sh[prow * g.H + col] = acc[mt][j][r];
         }
       }
     }
+  if (!staged) return;
+  __syncthreads();
+  // row segments of 8 columns: thread t takes segments t, t + 256, ...; 16-byte stores where the output rows are
+  // 16-byte aligned (row lengths a multiple of 8)
+  constexpr int SPR = COLS / 8;  // segments per row
+  const bool vec = (MODE == 0 ? (shared ? g.Fs : g.F) : g.H) % 8 == 0;
+#pragma unroll
+  for (int i = 0; i < 64 * SPR / 256; ++i) {
+    const int sidx = tid + 256 * i, row = sidx / SPR, seg = sidx - row * SPR;
+    if (row >= rows) continue;
+    const int64_t prow = row0 + row;
+    const int col = col0 + 8 * seg;
+    uint16_t* dst;
+    if (MODE == 0)
+      dst = shared ? g.ws.act_sh + prow * g.Fs + col : g.ws.act + prow * g.F + col;
+    else
+      dst = reinterpret_cast<uint16_t*>(g.ws.y) + (int64_t)g.ws.row_pair[prow] * g.H + col;
+    const uint16_t* src = so + row * LDO + 8 * seg;
+    if (vec && col + 8 <= No) {
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    } else {
+      for (int e = 0; e < 8 && col + e < No; ++e) dst[e] = src[e];
+    }
+  }
 }
 
 struct MoeDims {
