@@ -573,35 +573,82 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
     if (g.bias[mi]) v += g.bias[mi][nn];
     return v;
   };
+  if (g.out_f32) {  // fp32 outputs (EPI_PLAIN): stored directly, 64-byte runs of 16 lanes
+#pragma unroll
+    for (int mt = 0; mt < kDgMT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * mt + 4 * g4 + r;
+        if (m >= g.m) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nn = col0 + 64 * wave + 16 * j + l16;
+          if (nn < N) reinterpret_cast<float*>(g.out[mat])[(int64_t)m * g.ldo[mat] + nn] = fin(mat, nn, m, acc[mt][j][r]);
+        }
+      }
+    return;
+  }
+  // bf16 outputs go through an LDS tile [BM rows][COLS + 8] over the ring, then leave as 16-byte row segments
+  // (EPI_RES: the residual read the same way and added as bf16(res + bf16(v)))
+  constexpr int LDO = COLS + 8;
+  static_assert(kDgBM * LDO * 2 <= kDgStages * STAGE, "the output tile fits in the ring");
+  uint16_t* so = reinterpret_cast<uint16_t*>(smem);
+  __syncthreads();  // every wave is done with the ring
 #pragma unroll
   for (int mt = 0; mt < kDgMT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 16 * mt + 4 * g4 + r;
-      if (m >= g.m) continue;
+      const int row = 16 * mt + 4 * g4 + r, m = min(m0 + row, g.m - 1);
       if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const int nn = col0 + 32 * wave + 16 * j + l16;
-          if (nn >= N) continue;
+          const int nn = min(col0 + 32 * wave + 16 * j + l16, N - 1);
           const float gv = fin(0, nn, m, acc[mt][j][r]), uv = fin(1, nn, m, acc[mt][j + 2][r]);
-          reinterpret_cast<uint16_t*>(g.out[0])[(int64_t)m * g.ldo[0] + nn] =
+          so[row * LDO + 32 * wave + 16 * j + l16] =
               (uint16_t)f32_to_bf16_bits(silu_f32(round_bf16(gv)) * round_bf16(uv));
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int nn = col0 + 64 * wave + 16 * j + l16;
-          if (nn >= N) continue;
-          float v = fin(mat, nn, m, acc[mt][j][r]);
-          if constexpr (EPI == EPI_RES) v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn]) + round_bf16(v);
-          if (g.out_f32)
-            reinterpret_cast<float*>(g.out[mat])[(int64_t)m * g.ldo[mat] + nn] = v;
-          else
-            reinterpret_cast<uint16_t*>(g.out[mat])[(int64_t)m * g.ldo[mat] + nn] = (uint16_t)f32_to_bf16_bits(v);
+          const int nn = min(col0 + 64 * wave + 16 * j + l16, N - 1);
+          so[row * LDO + 64 * wave + 16 * j + l16] = (uint16_t)f32_to_bf16_bits(fin(mat, nn, m, acc[mt][j][r]));
         }
       }
     }
+  __syncthreads();
+  constexpr int SPR = COLS / 8;  // 8-column segments per row
+  uint16_t* ob = reinterpret_cast<uint16_t*>(g.out[mat]);
+  const int64_t ldo = g.ldo[mat];
+  const bool vec = ldo % 8 == 0 && ((uintptr_t)ob & 15) == 0 &&
+                   (EPI != EPI_RES || (g.ldr % 8 == 0 && ((uintptr_t)g.res & 15) == 0));
+  for (int sidx = tid; sidx < kDgBM * SPR; sidx += 256) {
+    const int row = sidx / SPR, seg = sidx - row * SPR, m = m0 + row, nn = col0 + 8 * seg;
+    if (m >= g.m || nn >= N) continue;
+    const uint16_t* src = so + row * LDO + 8 * seg;
+    uint16_t* dst = ob + (int64_t)m * ldo + nn;
+    if (vec && nn + 8 <= N) {
+      uint4 v = *reinterpret_cast<const uint4*>(src);
+      if constexpr (EPI == EPI_RES) {
+        const uint4 rv = *reinterpret_cast<const uint4*>(g.res + (int64_t)m * g.ldr + nn);
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16_bits_to_f32(rw[i] & 0xffffu) + bf16_bits_to_f32(vw[i] & 0xffffu);
+          const float hi = bf16_bits_to_f32(rw[i] >> 16) + bf16_bits_to_f32(vw[i] >> 16);
+          ow[i] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+        }
+        v = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      }
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      for (int e = 0; e < 8 && nn + e < N; ++e) {
+        float v = bf16_bits_to_f32(src[e]);
+        if constexpr (EPI == EPI_RES) v = bf16_bits_to_f32(g.res[(int64_t)m * g.ldr + nn + e]) + v;
+        dst[e] = (uint16_t)f32_to_bf16_bits(v);
+      }
+    }
+  }
 }
 
 // The dense GEMM for a checked group: one launch for all of its matrices (their column blocks end to end; EPI_SWIGLU
