@@ -58,7 +58,7 @@ constexpr int kDecodeTokens = 64 * kMaskWords;  // above this the prefill path r
 constexpr int64_t kMaxPrefillTokens = 1 << 16;
 constexpr int64_t kMaxPrefillPairs = 1 << 19;
 constexpr int kBlkTokens = 256;  // tokens per block of the prefill grouping
-constexpr int kBM = 64, kBK = 64;  // prefill GEMM tile rows, K step
+constexpr int kBM = 128, kBK = 64;  // prefill GEMM tile rows, K step
 
 struct MoeWs {
   int* counts;      // [E]
@@ -1150,25 +1150,38 @@ constexpr int kG2Cols0 = kG2Rows / 2;  // gate-up: output (act) columns per work
 constexpr int kG2Cols1 = kG2Rows;      // down: output columns per workgroup
 constexpr int kXcds = 8;              // MI355X: consecutive workgroups go round-robin over 8 XCDs
 constexpr int kGStages = 3;
-constexpr int kGAStage = kBM * kBK * 2;      // 8 KiB
+// rows per workgroup: the gate-up GEMM takes a whole kBM-row tile (each decoded weight fragment feeds 8 MFMAs); the
+// down GEMM (K = F, a short reduction) a half tile, so twice the workgroups share its fixed costs
+template <int MODE>
+constexpr int g_bm() { return MODE == 0 ? kBM : kBM / 2; }
+template <int MODE>
+constexpr int g_astage() { return g_bm<MODE>() * kBK * 2; }
 constexpr int kGBStage = kG2Rows * kBK / 2;  // 8 KiB
-constexpr int kGStage = kGAStage + kGBStage;
+template <int MODE>
+constexpr int g_stage() { return g_astage<MODE>() + kGBStage; }
 constexpr int kGSStage = kG2Rows * 4;  // SDMA: one scale dword per weight row and step
+template <int MODE>
 size_t gemm_lds_bytes(int Kd, bool sdma) {
-  return sdma ? (size_t)kGStages * (kGStage + kGSStage) : (size_t)kGStages * kGStage + (size_t)kG2Rows * (Kd / 32 + 16);
+  return sdma ? (size_t)kGStages * (g_stage<MODE>() + kGSStage)
+              : (size_t)kGStages * g_stage<MODE>() + (size_t)kG2Rows * (Kd / 32 + 16);
 }
 
 template <int MODE, bool SDMA>
-__global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
+__global__ __launch_bounds__(256, 2) void moe_ggemm_kernel(GGemmArgs g) {
+  constexpr int BM = g_bm<MODE>(), SUB = kBM / BM;              // rows per workgroup, workgroups per tile
+  constexpr int kGAStage = g_astage<MODE>(), kGStage = g_stage<MODE>();
+  constexpr int kGAI = kGAStage / 1024 / 4;                        // A direct-load instructions per wave and step
+  constexpr int kGMT = BM / 16;                                    // 16-row MFMA tiles per wave (all rows of the tile)
   constexpr int STAGE = kGStage + (SDMA ? kGSStage : 0);
   extern __shared__ __align__(16) unsigned char smem[];
   const int nblk = MODE == 0 ? (g.Fmax + kG2Cols0 - 1) / kG2Cols0 : (g.H + kG2Cols1 - 1) / kG2Cols1;
-  const int total = *g.ws.n_tiles * nblk, per = (total + kXcds - 1) / kXcds;
+  const int total = *g.ws.n_tiles * SUB * nblk, per = (total + kXcds - 1) / kXcds;
   const int k = blockIdx.x / kXcds, lid = (blockIdx.x % kXcds) * per + k;
   if (k >= per || lid >= total) return;
-  const int tile = lid / nblk, cblk = lid - tile * nblk;
+  const int sub = lid / nblk, cblk = lid - sub * nblk, tile = sub / SUB, part = sub - tile * SUB;
   const int4 tl = g.ws.tiles[tile];
-  const int e = tl.x, row0 = tl.y, rows = tl.z;
+  const int e = tl.x, row0 = tl.y + part * BM, rows = min(BM, tl.z - part * BM);
+  if (rows <= 0) return;
   const bool shared = e < 0;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -1208,11 +1221,11 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   // per-lane sources of this wave's two A and two B load instructions of a step (instruction i = 2 wave + h):
   // A: row 8 i + lane / 8 (rows past the tile re-read its last row, never stored), chunk (lane % 8) ^ (row & 7);
   // B: weight row 32 i + lane / 2, half (lane % 2) ^ ((row >> 3) & 1)
-  const uint16_t* asrc[2];
+  const uint16_t* asrc[kGAI];
   const uint8_t* bsrc[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int i = 2 * wave + h;
+  for (int h = 0; h < kGAI; ++h) {
+    const int i = kGAI * wave + h;
     const int r = 8 * i + (lane >> 3), rr = min(r, rows - 1), ch = (lane & 7) ^ (r & 7);
     if (MODE == 0) {
       const int tok = shared ? row0 + rr : g.ws.row_tok[row0 + rr];
@@ -1220,7 +1233,10 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
     } else {
       asrc[h] = (shared ? g.a_sh + (int64_t)(row0 + rr) * g.Fs : g.a + (int64_t)(row0 + rr) * g.F) + 8 * ch;
     }
-    const int rho = 32 * i + (lane >> 1);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rho = 32 * (2 * wave + h) + (lane >> 1);
     bsrc[h] = wrow(rho, false) + 16 * ((lane & 1) ^ ((rho >> 3) & 1));
   }
   // SDMA: wave w loads the aligned dword holding blocks 4 (ks / 2) .. + 3 of weight rows 64 w + lane
@@ -1231,10 +1247,9 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
     const int kk = min(ks, nk - 1);
     const uint32_t base = lds0 + buf * STAGE;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      lds_dma16_cached(asrc[h] + kk * kBK, base + (2 * wave + h) * 1024);
-      lds_dma16_cached(bsrc[h] + kk * (kBK / 2), base + kGAStage + (2 * wave + h) * 1024);
-    }
+    for (int h = 0; h < kGAI; ++h) lds_dma16_cached(asrc[h] + kk * kBK, base + (kGAI * wave + h) * 1024);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) lds_dma16_cached(bsrc[h] + kk * (kBK / 2), base + kGAStage + (2 * wave + h) * 1024);
     if constexpr (SDMA) lds_dma4_cached(ssrc + 4 * (kk >> 1), base + kGStage + 256 * wave);
   };
   issue(0, 0);
@@ -1264,16 +1279,16 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   for (int j = 0; j < 4; ++j)
     brow[j] = MODE == 0 ? (j >> 1) * kG2Cols0 + 32 * wave + 16 * (j & 1) : 64 * wave + 16 * j;
 
-  axk_f32x4 acc[4][4];
+  axk_f32x4 acc[kGMT][4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kGMT; ++mt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[mt][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // step ks from ring slot BUF (a constant: the loop is unrolled over the ring, so every LDS offset is immediate)
   auto step = [&](int ks, auto buf_c) __attribute__((always_inline)) {
     constexpr int BUF = decltype(buf_c)::value;
-    wait_vmcnt<SDMA ? 5 : 4>();  // this wave's loads of step ks have landed (step ks + 1's may not have)
+    wait_vmcnt<kGAI + 2 + (SDMA ? 1 : 0)>();  // this wave's loads of step ks have landed (step ks + 1's may not)
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's reads of step ks - 1 are done
     __builtin_amdgcn_s_barrier();  // every wave's step-ks loads landed; every wave is done with step ks - 1
     asm volatile("" ::: "memory");
@@ -1282,7 +1297,7 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
     const unsigned char* sb = sa + kGAStage;
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
-      axk_bf16x8 af[4], bf[4];
+      axk_bf16x8 af[kGMT], bf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = brow[j] + l16;
@@ -1292,12 +1307,12 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
         bf[j] = fp4x8_to_bf16x8(w, e8m0_to_f32(sbyte));
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+      for (int mt = 0; mt < kGMT; ++mt) {
         const int r = 16 * mt + l16;
         af[mt] = *reinterpret_cast<const axk_bf16x8*>(sa + r * 128 + 16 * ((4 * kh + g4) ^ (r & 7)));
       }
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < kGMT; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mt][j] = mfma_bf16_16x16x32(af[mt], bf[j], acc[mt][j]);
     }
@@ -1311,14 +1326,14 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   wait_vmcnt<0>();  // the look-ahead loads land before the workgroup's LDS is released
 
   // Epilogue. The bf16 outputs (gate-up: act / act_sh; down, routed: bf16(rw * y) by pair) go through an LDS tile
-  // [64 rows][COLS + 8] over the ring, so that each row leaves as 16-byte stores of whole row segments instead of
+  // [BM rows][COLS + 8] over the ring, so that each row leaves as 16-byte stores of whole row segments instead of
   // 2-byte stores of 16 lanes; the shared expert's fp32 down rows are stored directly.
   constexpr int COLS = MODE == 0 ? kG2Cols0 : kG2Cols1, LDO = COLS + 8;
   const bool staged = MODE == 0 || !shared;
   uint16_t* so = reinterpret_cast<uint16_t*>(smem);
   if (staged) __syncthreads();  // every wave is done with the ring
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < kGMT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * mt + 4 * g4 + r;
@@ -1353,7 +1368,7 @@ __global__ __launch_bounds__(256) void moe_ggemm_kernel(GGemmArgs g) {
   constexpr int SPR = COLS / 8;  // segments per row
   const bool vec = (MODE == 0 ? (shared ? g.Fs : g.F) : g.H) % 8 == 0;
 #pragma unroll
-  for (int i = 0; i < 64 * SPR / 256; ++i) {
+  for (int i = 0; i < BM * SPR / 256; ++i) {
     const int sidx = tid + 256 * i, row = sidx / SPR, seg = sidx - row * SPR;
     if (row >= rows) continue;
     const int64_t prow = row0 + row;
@@ -1467,7 +1482,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     auto a4 = [](const void* p) { return p == nullptr || axk_aligned(p, 4); };
     const bool sdma0 = H % 128 == 0 && a4(e_gs) && a4(sh_gate_s) && a4(sh_up_s);
     const bool sdma1 = F % 128 == 0 && Fs % 128 == 0 && a4(e_ds) && a4(sh_down_s);
-    const size_t lds0 = gemm_lds_bytes(H, sdma0), lds1 = gemm_lds_bytes(fmax, sdma1);
+    const size_t lds0 = gemm_lds_bytes<0>(H, sdma0), lds1 = gemm_lds_bytes<1>(fmax, sdma1);
     static AxkOnce gemm_once;  // > 64 KiB of dynamic LDS must be allowed once per kernel
     const int raised = axk_once(gemm_once, [] {
       const void* fns[4] = {reinterpret_cast<const void*>(&moe_ggemm_kernel<0, false>),
@@ -1488,10 +1503,11 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
     else
       hipLaunchKernelGGL((moe_ggemm_kernel<0, false>), xgrid(tiles * nb0), dim3(256), lds0, st, gu);
     GGemmArgs dn{w.act, w.act_sh, e_dw, e_ds, sh_down_w, sh_down_s, nullptr, nullptr, T, H, F, Fs, fmax, w};
+    constexpr unsigned sub1 = kBM / g_bm<1>();  // down workgroups per tile
     if (sdma1)
-      hipLaunchKernelGGL((moe_ggemm_kernel<1, true>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
+      hipLaunchKernelGGL((moe_ggemm_kernel<1, true>), xgrid(tiles * sub1 * nb1), dim3(256), lds1, st, dn);
     else
-      hipLaunchKernelGGL((moe_ggemm_kernel<1, false>), xgrid(tiles * nb1), dim3(256), lds1, st, dn);
+      hipLaunchKernelGGL((moe_ggemm_kernel<1, false>), xgrid(tiles * sub1 * nb1), dim3(256), lds1, st, dn);
     CombineArgs ca{h2, x_res, w_shg, nullptr, topk_ids, combine_shared, T, H, E, K, w, out};
     launch_combine<true>(ca, st);
     return axk_launch_status();
