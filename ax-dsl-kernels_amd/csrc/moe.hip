@@ -425,13 +425,21 @@ constexpr int kStreamWaves = AXK_SW;
 constexpr int kBatchChunks = AXK_BC;  // 128-wide K chunks per streamed batch (each lane: one unit per chunk)
 constexpr int kStageRows = AXK_ROWS;  // activation rows staged per pass (MFMA rows past it are zero)
 #ifndef AXK_GU_TPW
-#define AXK_GU_TPW 2
+#define AXK_GU_TPW 1
 #endif
 #ifndef AXK_DN_TPW
 #define AXK_DN_TPW 4
 #endif
+#ifndef AXK_GU_NB
+#define AXK_GU_NB 3
+#endif
+#ifndef AXK_DN_NB
+#define AXK_DN_NB 3
+#endif
 constexpr int kGateUpTilesPerWave = AXK_GU_TPW;  // 16-row tiles each wave streams (gate-up / down)
 constexpr int kDownTilesPerWave = AXK_DN_TPW;
+constexpr int kGateUpBufs = AXK_GU_NB;  // weight batches in rotation per wave (NB - 1 in flight while one is used)
+constexpr int kDownBufs = AXK_DN_NB;
 constexpr int kStageLd = 64 * kBatchChunks + 16;    // bytes per staged weight row segment of a batch (+16 pad)
 constexpr int kWaveStageBytes = 32 * kStageLd;      // a wave's LDS tile: gate and up, 16 rows each
 constexpr int kStageLpr = 4 * kBatchChunks;         // staged loads: lanes per row segment,
@@ -590,7 +598,10 @@ __global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a
     uw = gw + (int64_t)a.F * (a.H / 2);
     us = gs + (int64_t)a.F * (a.H / 32);
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  // the wave index as a scalar: the step count and the past-the-end test derived from it stay uniform, so the
+  // look-ahead loads select their address instead of branching around the load
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nl = lane & 15,
+            g = lane >> 4;
   const int H = a.H, ldA = H + 8;
   const int nc = (H + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;  // chunks, batches per tile
   // this wave's tiles: tb + wave + kStreamWaves i, i < nmine
@@ -603,9 +614,10 @@ __global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a
   };
   // Loads are unconditional, from addresses clamped into the weights (a row past Fo is never stored, a unit past
   // K is zeroed where it is used): a branch around a load would make every later wait drain the queue. Steps past
-  // the wave's last (the look-ahead at the end of its stream) load the first 16 bytes of h2, already in L2 from the
+  // the wave's last (the look-ahead at the end of its stream) load the first bytes of h2, already in L2 from the
   // row staging, instead of repeating the last weight batch: those non-temporal re-reads missed L2 and came from
-  // HBM again.
+  // HBM again. Each such load takes its own 16-byte unit: two loads of one address are merged by the compiler
+  // into one load and a register copy, and the copy waits for the whole load queue.
   const uint8_t* idle = reinterpret_cast<const uint8_t*>(a.h2);
   auto load_batch = [&](Batch& bt, int step) {
     const bool past = step >= steps;  // wave-uniform
@@ -618,15 +630,15 @@ __global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)Fo - 1);
         const int64_t off = (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr);
-        bt.qg[h] = load_nt(past ? idle : gw + r * (H / 2) + off);  // expert weights: read once per step
-        bt.qu[h] = load_nt(past ? idle : uw + r * (H / 2) + off);
+        bt.qg[h] = load_nt(past ? idle + 32 * h : gw + r * (H / 2) + off);  // expert weights: read once per step
+        bt.qu[h] = load_nt(past ? idle + 32 * h + 16 : uw + r * (H / 2) + off);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)H - 32);
-        bt.qg[j] = load_nt(past ? idle : gw + n * (H / 2) + kb / 2);
-        bt.qu[j] = load_nt(past ? idle : uw + n * (H / 2) + kb / 2);
+        bt.qg[j] = load_nt(past ? idle + 32 * j : gw + n * (H / 2) + kb / 2);
+        bt.qu[j] = load_nt(past ? idle + 32 * j + 16 : uw + n * (H / 2) + kb / 2);
         if (!WIDE) {
           bt.sg[j] = gs[n * (H / 32) + kb / 32];
           bt.su[j] = us[n * (H / 32) + kb / 32];
@@ -667,15 +679,16 @@ __global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int c = bi * kBatchChunks + j;
-        if (c * 128 >= H) continue;  // whole chunk past K (uniform)
+        if (!WIDE && c * 128 >= H) continue;  // whole chunk past K (uniform)
         const int kb = c * 128 + 32 * g;
-        const bool kv = kb < H;      // this lane's unit (a chunk can straddle the end of K)
+        const bool kv = WIDE || kb < H;       // this lane's unit (a chunk can straddle the end of K)
         const int kc = kv ? kb : H - 32;
         const uint32_t bg = WIDE ? (cur.sg[j] >> (8 * g)) & 0xffu : cur.sg[j];
         const uint32_t bu = WIDE ? (cur.su[j] >> (8 * g)) & 0xffu : cur.su[j];
         const float scg = kv ? e8m0_to_f32(bg) : 0.f, scu = kv ? e8m0_to_f32(bu) : 0.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+          // only lanes of staged rows read (LDS bandwidth); the other MFMA rows are zero and never stored
           const axk_bf16x8 af = (kv && nl < ROWS) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8();
           accg = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wg[j]), s, scg), accg);
           accu = mfma_bf16_16x16x32(af, axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wu[j]), s, scu), accu);
@@ -698,25 +711,28 @@ __global__ __launch_bounds__(kStreamThreads) void moe_gateup_kernel(GateUpArgs a
         accg = accu = axk_f32x4{0.f, 0.f, 0.f, 0.f};
       }
     };
-    // three batches in rotation: batch st + 2 is loaded while batch st is used; the first two are issued
-    // before the activation rows are ranked and staged, so they overlap the slot's grouping and row gathers
-    Batch b0, b1, b2;
+    // NB batches in rotation: batch st + NB - 1 is loaded while batch st is used. The first two are issued
+    // before the activation rows are ranked and staged, so they overlap the slot's grouping and row gathers; the
+    // rest after the gathers (whose in-order wait would otherwise take them all)
+    constexpr int NB = kGateUpBufs, NPRE = NB - 1 < 2 ? NB - 1 : 2;
+    Batch bt[NB];
     __syncthreads();  // the previous pass's readers are done with sA
-    load_batch(b0, 0);
-    load_batch(b1, 1);
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) load_batch(bt[j], j);
     if (cnt < 0) cnt = decode_rank_rows(a.ids, P, eid, id0, L);
     if (shared)
       stage_rows<ROWS>(sA, a.h2, nullptr, 1, m0, cnt, H);
     else
       stage_rows<ROWS>(sA, a.h2, L.pair, a.K, m0, cnt, H);  // token = pair / K
+#pragma unroll
+    for (int j = NPRE; j < NB - 1; ++j) load_batch(bt[j], j);
     __syncthreads();
-    for (int st = 0; st < steps; st += 3) {
-      load_batch(b2, st + 2);
-      proc(b0, st);
-      load_batch(b0, st + 3);
-      if (st + 1 < steps) proc(b1, st + 1);
-      load_batch(b1, st + 4);
-      if (st + 2 < steps) proc(b2, st + 2);
+    for (int st = 0; st < steps; st += NB) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        load_batch(bt[(j + NB - 1) % NB], st + j + NB - 1);
+        if (st + j < steps) proc(bt[j], st + j);
+      }
     }
     m0 += ROWS;
   } while (m0 < cnt);
@@ -764,7 +780,10 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
     ds = a.e_ds + e * (int64_t)a.H * (a.F / 32);
     act = a.w.act;
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nl = lane & 15, g = lane >> 4;
+  // the wave index as a scalar: the step count and the past-the-end test derived from it stay uniform, so the
+  // look-ahead loads select their address instead of branching around the load
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nl = lane & 15,
+            g = lane >> 4;
   const int ldA = K + 8;
   const int nc = (K + 127) / 128, nb = (nc + kBatchChunks - 1) / kBatchChunks;
   const int nmine = max(0, min(a.tpw, (ntiles - tb - wave + kStreamWaves - 1) / kStreamWaves));
@@ -787,13 +806,14 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
       for (int h = 0; h < kBatchChunks; ++h) {
         const int64_t r = min((int64_t)(tb + wave + kStreamWaves * i) * 16 + kStageRpi * h + lane / kStageLpr,
                               (int64_t)a.H - 1);
-        bt.q[h] = load_nt(past ? idle : dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr));
+        bt.q[h] = load_nt(past ? idle + 16 * h
+                                : dw + r * (K / 2) + (int64_t)bi * (64 * kBatchChunks) + 16 * (lane % kStageLpr));
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int64_t kb = min((int64_t)(bi * kBatchChunks + j) * 128 + 32 * g, (int64_t)K - 32);
-        bt.q[j] = load_nt(past ? idle : dw + n * (K / 2) + kb / 2);
+        bt.q[j] = load_nt(past ? idle + 16 * j : dw + n * (K / 2) + kb / 2);
         if (!WIDE) bt.s[j] = ds[n * (K / 32) + kb / 32];
       }
     }
@@ -802,10 +822,11 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
 
   int m0 = mbeg;
   do {
-    Batch b0, b1, b2;
+    constexpr int NB = kDownBufs, NPRE = NB - 1 < 2 ? NB - 1 : 2;  // as in the gate-up kernel
+    Batch bt[NB];
     __syncthreads();
-    load_batch(b0, 0);
-    load_batch(b1, 1);
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) load_batch(bt[j], j);
     if (cnt < 0) cnt = decode_rank_rows(a.ids, P, eid, id0, L);
     if (shared)
       stage_rows<ROWS>(sA, act, nullptr, 1, m0, cnt, K);
@@ -819,6 +840,8 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
       pr[r] = shared ? 0 : L.pair[m];
       rw[r] = shared ? 1.0f : a.wts[pr[r]];
     }
+#pragma unroll
+    for (int j = NPRE; j < NB - 1; ++j) load_batch(bt[j], j);
     __syncthreads();
     axk_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     auto proc = [&](const Batch& cur, int st) {
@@ -839,16 +862,17 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
 #pragma unroll
       for (int j = 0; j < kBatchChunks; ++j) {
         const int c = bi * kBatchChunks + j;
-        if (c * 128 >= K) continue;
+        if (!WIDE && c * 128 >= K) continue;
         const int kb = c * 128 + 32 * g;
-        const bool kv = kb < K;
+        const bool kv = WIDE || kb < K;
         const int kc = kv ? kb : K - 32;
         const uint32_t sb = WIDE ? (cur.s[j] >> (8 * g)) & 0xffu : cur.s[j];
         const float sc = kv ? e8m0_to_f32(sb) : 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < 4; ++s) {
           acc = mfma_bf16_16x16x32((kv && nl < ROWS) ? load_bf16x8(sA + nl * ldA + kc + 8 * s) : zero_bf16x8(),
                                    axk::WUnit<WF_MXFP4>::conv(__builtin_bit_cast(uint4, wq[j]), s, sc), acc);
+        }
       }
       if (bi == nb - 1) {
         const int64_t col = (int64_t)(tb + wave + kStreamWaves * i) * 16 + nl;
@@ -865,13 +889,12 @@ __global__ __launch_bounds__(kStreamThreads) void moe_down_kernel(DownArgs a) {
         acc = axk_f32x4{0.f, 0.f, 0.f, 0.f};
       }
     };
-    for (int st = 0; st < steps; st += 3) {
-      load_batch(b2, st + 2);
-      proc(b0, st);
-      load_batch(b0, st + 3);
-      if (st + 1 < steps) proc(b1, st + 1);
-      load_batch(b1, st + 4);
-      if (st + 2 < steps) proc(b2, st + 2);
+    for (int st = 0; st < steps; st += NB) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        load_batch(bt[(j + NB - 1) % NB], st + j + NB - 1);
+        if (st + j < steps) proc(bt[j], st + j);
+      }
     }
     m0 += ROWS;
   } while (m0 < cnt);
