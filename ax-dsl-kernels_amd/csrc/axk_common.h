@@ -252,6 +252,40 @@ AXK_DEV axk_bf16x8 acc_pair_to_b(const axk_f32x4& a, const axk_f32x4& b) {
   return __builtin_bit_cast(axk_bf16x8, f);
 }
 
+// fp16 operands (the INT8 cache decode)
+typedef _Float16 axk_f16x8 __attribute__((ext_vector_type(8)));
+AXK_DEV axk_f32x4 mfma_f16_16x16x32(axk_f16x8 a, axk_f16x8 b, axk_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// Eight int8 codes (two dwords, bytes in order) as the fp16 values 1152 + code, exactly: the byte with its sign bit
+// flipped (code + 128, 0 .. 255) is the low mantissa byte under the exponent of 1024 (fp16 bits 0x6400 | byte), one
+// byte permute per two values (selector bytes 0 .. 3 take the flipped codes, 4 the 0x64 of the first operand).
+AXK_DEV axk_f16x8 i8x8_to_f16x8_off(uint32_t w0, uint32_t w1) {
+  const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+  const axk_u32x4 r = {__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u),
+                       __builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u),
+                       __builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u),
+                       __builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)};
+  return __builtin_bit_cast(axk_f16x8, r);
+}
+// Two floats -> fp16 pair, round to nearest even.
+AXK_DEV uint32_t pack_f16x2(float lo, float hi) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+// acc_pair_to_b with fp16 rounding (the same lane swaps).
+AXK_DEV axk_f16x8 acc_pair_to_b_f16(const axk_f32x4& a, const axk_f32x4& b) {
+  const unsigned a01 = pack_f16x2(a[0], a[1]), a23 = pack_f16x2(a[2], a[3]);
+  const unsigned b01 = pack_f16x2(b[0], b[1]), b23 = pack_f16x2(b[2], b[3]);
+  const auto s01 = __builtin_amdgcn_permlane32_swap(a01, b01, false, false);
+  const auto s23 = __builtin_amdgcn_permlane32_swap(a23, b23, false, false);
+  const auto t01 = __builtin_amdgcn_permlane16_swap(s01[0], s01[1], false, false);
+  const auto t23 = __builtin_amdgcn_permlane16_swap(s23[0], s23[1], false, false);
+  const axk_u32x4 f = {t01[0], t23[0], t01[1], t23[1]};
+  return __builtin_bit_cast(axk_f16x8, f);
+}
+
 // Sum inside aligned groups of W lanes (W = 2, 4, 8 or 16), the same value in every lane of the group.
 template <int W>
 AXK_DEV float group_sum(float v) {

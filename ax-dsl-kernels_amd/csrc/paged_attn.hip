@@ -503,9 +503,12 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   }
 }
 
-// Attention of one work item over an 8-bit cache (FP8 E4M3 codes * inv_scale, exact for a power-of-two scale; QM = 1:
-// INT8 codes q, bf16(q * s) with s the bf16 scale of the row and KV head in kv_scales [pages, 2, page, hkv],
-// q35_group.py kv_page 208-221), the item's tiles split between the 4 waves. A step is a pair of 16-token tiles
+// Attention of one work item over an 8-bit cache (FP8 E4M3 codes * inv_scale, exact for a power-of-two scale, on bf16
+// MFMAs; QM = 1: INT8 codes q times s, the bf16 scale of the row and KV head in kv_scales [pages, 2, page, hkv],
+// q35_group.py kv_page 208-221, on fp16 MFMAs: the codes enter exactly as 1152 + q by one byte permute per two codes,
+// the row scales multiply the scores (K) and the probabilities (V) instead of every element, and the constant
+// offsets come off the sums; the reference rounds bf16(q * s) per element, this rounds only the products' fp32
+// sums and the fp16 probabilities), the item's tiles split between the 4 waves. A step is a pair of 16-token tiles
 // (16 KiB of K and V at D = 256); wave w streams steps [ns w / 4, ns (w + 1) / 4) of the item's ns steps with its own
 // online softmax, so every stored byte is converted once (no score or softmax work is repeated across waves): K
 // straight into registers (lane (token l16, g) loads the 16-byte row chunks 64 s' + 16 g of its MFMA A operand), V by
@@ -550,6 +553,33 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     const uint16_t* qp = q + ((int64_t)b * hq + kvh * group + (hv ? l16 : 0)) * D + 16 * g;
 #pragma unroll
     for (int s = 0; s < C::KSTEPS; ++s) qb[s] = hv ? load_bf16x8(qp + 64 * (s >> 1) + 8 * (s & 1)) : zero_bf16x8();
+  }
+  // INT8 (QM = 1) runs its MFMAs on fp16: Q scaled per head by a power of two qs that puts its largest magnitude in
+  // [2^14, 2^15) (bf16 -> fp16 then keeps every bit of each element down to 2^-10 of that magnitude), the codes as
+  // exact fp16 1152 + code (i8x8_to_f16x8_off), so a score accumulates S' = sum q (1152 + code) and its code part is
+  // S' - qoff with qoff = 1152 * (the head's fp16 Q summed); the K row scale and cq = the softmax scale / qs follow
+  float qoff = 0.f, cq = c;
+  axk_f16x8 qh[QM == 1 ? C::KSTEPS : 1];
+  if constexpr (QM == 1) {
+    float amax = 0.f;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)qb[s][e]));
+    amax = xor32_max(xor16_max(amax));  // the head's (lanes l16, l16 + 16, + 32, + 48)
+    const int ex = amax > 0.f ? max(-120, min(120, ilogbf(amax))) : 0;
+    const float qs = ldexpf(1.0f, 14 - ex);
+    float qsum = 0.f;
+#pragma unroll
+    for (int s = 0; s < C::KSTEPS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 h = (_Float16)((float)qb[s][e] * qs);
+        qh[s][e] = h;
+        qsum += (float)h;
+      }
+    qoff = 1152.0f * xor32_sum(xor16_sum(qsum));
+    cq = c * ldexpf(1.0f, ex - 14);
   }
 
   // the tile cursor: tiles are taken in order (tile cur_ti = tile cur_tp of the item's page cur_lp); past the item's
@@ -601,12 +631,31 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     voff[i] = voff0[i] + (uint32_t)(vtok[i] * row_stride);
   }
   const uint32_t lds_slots = lds_addr(smem) + wave * 2 * W::VSLOT;
-  // this lane's K row offset (token l16, chunk g) and the same for row 0; QM: its K row's scale offset, and the V
-  // scales of rows 8 (g & 1) + jj at vs_off + jj hkv 2 (plane 1), row 0's at vs_off0
+  // this lane's K row offset (token l16, chunk g) and the same for row 0; QM: the V scales' plane (plane 1, head kvh)
   const uint32_t k_off = (uint32_t)(l16 * row_stride + 16 * g), k_off0 = (uint32_t)(16 * g);
   const uint32_t ks_off = (uint32_t)((l16 * hkv + kvh) * 2), ks_off0 = (uint32_t)(kvh * 2);
   const uint32_t vs_off0 = (uint32_t)(page_size * hkv * 2 + kvh * 2);
-  const uint32_t vs_off = vs_off0 + (uint32_t)(8 * (g & 1) * hkv * 2);
+  // QM: the scales of KV head kvh in rows 4 g .. 4 g + 3 from p = their row 4 g, head 0: one 8- or 16-byte load for
+  // one or two KV heads (rows at hkv * 2 bytes) when the scale array is that aligned, four 2-byte loads otherwise;
+  // packed (rows 4 g, + 1), (+ 2, + 3)
+  const uint32_t row4_off = (uint32_t)(4 * g * hkv * 2);
+  const bool svec = (reinterpret_cast<uintptr_t>(kv_scales) & (hkv == 1 ? 7u : 15u)) == 0;
+  auto load_scales4 = [&](const unsigned char* p, uint32_t& lo, uint32_t& hi) {
+    if (svec && hkv == 1) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      lo = v.x;
+      hi = v.y;
+    } else if (svec && hkv == 2) {  // dword i = (row i, head 0) | (row i, head 1) << 16
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      const uint32_t sel = kvh ? 0x07060302u : 0x05040100u;
+      lo = __builtin_amdgcn_perm(v.y, v.x, sel);
+      hi = __builtin_amdgcn_perm(v.w, v.z, sel);
+    } else {
+      const uint16_t* q2 = reinterpret_cast<const uint16_t*>(p) + kvh;
+      lo = (uint32_t)q2[0] | ((uint32_t)q2[hkv] << 16);
+      hi = (uint32_t)q2[2 * hkv] | ((uint32_t)q2[3 * hkv] << 16);
+    }
+  };
   auto issue_step = [&](Step& st, int sl) {
     const unsigned char* sbs[NT];
     int nrows[NT];
@@ -637,18 +686,14 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
         st.ks[j] = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sb + (krow ? ks_off : ks_off0)));
     }
     if constexpr (QM == 1) {
-      // this lane's V^T rows: 8 (g & 1) + jj of tile g / 2; scale 0 for a tile without a valid token (its bytes may be
-      // anything: the math reads the other tile's V for it, with zero weights)
-      const int tv = g >= 2 ? 1 : 0;
-      const unsigned char* s1 = tv ? sbs[1] : sbs[0];
-      const int nr = tv ? nrows[1] : nrows[0];
-      const bool live = (tv ? st.nv[1] : st.nv[0]) > 0;
       const uint32_t hs = (uint32_t)(hkv * 2);
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
-        const bool in = 8 * (g & 1) + jj < nr;
-        const float x = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(s1 + (in ? vs_off + jj * hs : vs_off0)));
-        st.vs[jj] = live ? x : 0.f;
+        const int tl = jj >> 2, row = 4 * g + (jj & 3);
+        const unsigned char* sbt = tl ? sbs[1] : sbs[0];
+        const bool in = row < (tl ? nrows[1] : nrows[0]);
+        const float x = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sbt + vs_off0 + (in ? row * hs : 0u)));
+        st.vs[jj] = (tl ? st.nv[1] : st.nv[0]) > 0 ? x : 0.f;
       }
     }
   };
@@ -665,26 +710,12 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     }
   };
 
-  // 4 stored bytes -> 4 bf16 (2 dwords): FP8 code * inv_scale; INT8: bf16(q * sc) with q = (byte ^ 0x80) - 128 by
-  // the unsigned byte conversion, (u - 128) sc = fma(u, sc, -128 sc) exact (q sc has at most 16 significant bits),
-  // so the bf16 rounding sees fp32(q sc). sc4: the scales of the four bytes.
-  auto cvt4 = [&](uint32_t w, const float* sc4, uint32_t& lo, uint32_t& hi) {
-    if constexpr (QM == 1) {
-      const uint32_t u = w ^ 0x80808080u;
-      lo = pack_bf16x2(__builtin_fmaf((float)(u & 0xffu), sc4[0], -128.0f * sc4[0]),
-                       __builtin_fmaf((float)((u >> 8) & 0xffu), sc4[1], -128.0f * sc4[1]));
-      hi = pack_bf16x2(__builtin_fmaf((float)((u >> 16) & 0xffu), sc4[2], -128.0f * sc4[2]),
-                       __builtin_fmaf((float)(u >> 24), sc4[3], -128.0f * sc4[3]));
-    } else {
-      lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, false));
-      hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, inv_scale, true));
-    }
-  };
-  auto cvt8 = [&](uint32_t w0, uint32_t w1, const float* sc8) -> axk_bf16x8 {
-    uint32_t r0, r1, r2, r3;
-    cvt4(w0, sc8, r0, r1);
-    cvt4(w1, sc8 + 4, r2, r3);
-    const axk_u32x4 r = {r0, r1, r2, r3};
+  // FP8: 8 stored bytes -> 8 bf16 (4 dwords), code * inv_scale
+  auto cvt8 = [&](uint32_t w0, uint32_t w1) -> axk_bf16x8 {
+    const axk_u32x4 r = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, inv_scale, false)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, inv_scale, true)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, inv_scale, false)),
+                         __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, inv_scale, true))};
     return __builtin_bit_cast(axk_bf16x8, r);
   };
 
@@ -693,6 +724,11 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
 #pragma unroll
   for (int t = 0; t < DTF; ++t) o[t] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;  // for head l16 (replicated over g)
+  // INT8: P'^T = P^T times the V-row scales times 2^-e_run (e_run: the largest scale exponent seen by the wave, so
+  // P' <= 2 in fp16), against the codes as 1152 + code; o_one accumulates sum P' (an all-ones A operand: exactly the
+  // P' the MFMAs saw), so O = (O' - 1152 sum P') 2^e_run at the end
+  axk_f32x4 o_one = {0.f, 0.f, 0.f, 0.f};
+  int e_run = -1000;
 
   // the math of one step whose V is in the slot (at least one valid token)
   auto compute = [&](const Step& st, int sl) {
@@ -701,16 +737,16 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       sc[j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
-      float ksc[8];
-      if constexpr (QM == 1) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ksc[e] = st.ks[j];
-      }
 #pragma unroll
       for (int s = 0; s < KLT; ++s) {
         const axk_u32x4 w = st.k[j * KLT + s];
-        sc[j] = mfma_bf16_16x16x32(cvt8(w[0], w[1], ksc), qb[2 * s], sc[j]);
-        sc[j] = mfma_bf16_16x16x32(cvt8(w[2], w[3], ksc), qb[2 * s + 1], sc[j]);
+        if constexpr (QM == 1) {
+          sc[j] = mfma_f16_16x16x32(i8x8_to_f16x8_off(w[0], w[1]), qh[2 * s], sc[j]);
+          sc[j] = mfma_f16_16x16x32(i8x8_to_f16x8_off(w[2], w[3]), qh[2 * s + 1], sc[j]);
+        } else {
+          sc[j] = mfma_bf16_16x16x32(cvt8(w[0], w[1]), qb[2 * s], sc[j]);
+          sc[j] = mfma_bf16_16x16x32(cvt8(w[2], w[3]), qb[2 * s + 1], sc[j]);
+        }
       }
     }
     float mx = -INFINITY;
@@ -718,13 +754,31 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        sc[j][rr] = (4 * g + rr < st.nv[j]) ? sc[j][rr] * c : -INFINITY;
+        float v;
+        if constexpr (QM == 1) {
+          v = (sc[j][rr] - qoff) * (__shfl(st.ks[j], 4 * g + rr, 64) * cq);
+        } else
+          v = sc[j][rr] * c;
+        sc[j][rr] = (4 * g + rr < st.nv[j]) ? v : -INFINITY;
         mx = fmaxf(mx, sc[j][rr]);
       }
     mx = xor32_max(xor16_max(mx));
     const float m_new = fmaxf(m_run, mx);  // finite: the step holds at least one valid token
+    int e_new = e_run;
+    float vs[8];  // QM: the V row scales of this lane's score rows (jj < 4: tile 0 row 4 g + jj, else tile 1), 0 past
+                  // a tile's valid rows (whatever bytes lie there)
+    if constexpr (QM == 1) {  // the step's largest V-row scale exponent (a valid tile's scales are > 0)
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) vs[jj] = st.vs[jj];
+      float vm = 0.f;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) vm = fmaxf(vm, vs[jj]);
+      vm = wave_max(vm);
+      if (vm > 0.f) e_new = max(e_run, ilogbf(vm));
+      e_new = __builtin_amdgcn_readfirstlane(e_new);
+    }
     // the running max rarely moves after the first steps: rescale O only when it did (wave-uniform test)
-    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0;
+    const bool moved = __builtin_amdgcn_ballot_w64(m_new > m_run) != 0 || e_new != e_run;
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // exp2(-inf) = 0 on the first step
     float psum = 0.f;
     axk_f32x4 p[NT];
@@ -739,25 +793,49 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     l_run = l_run * alpha + psum;
     m_run = m_new;
     if (moved) {
+      const float f = QM == 1 ? alpha * ldexpf(1.0f, e_run - e_new) : alpha;  // 2^(e_run - e_new): 0 at the start
 #pragma unroll
       for (int t = 0; t < DTF; ++t)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= alpha;
+        for (int rr = 0; rr < 4; ++rr) o[t][rr] *= f;
+      if constexpr (QM == 1) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o_one[rr] *= f;
+      }
     }
+    e_run = e_new;
     // the 32-deep step: P^T's B operand from both score tiles by two lane swaps; V^T's A operand (lane (d, g):
     // tokens 8 g .. 8 g + 7 = tile g / 2, rows 8 (g & 1) .. + 7) by one transposing 8-bit read per 16 columns
     // (source lane 2j + a: row 8 (g & 1) + j, bytes 8a .. 8a + 7 of the chunk; lane i receives column i). A tile
     // without a valid token (a bad page: any bytes) is read from the other tile, with zero weights.
-    const axk_bf16x8 pfrag = acc_pair_to_b(p[0], p[1]);
     int tv = g >= 2 ? 1 : 0;
     if (st.nv[tv] <= 0) tv = 1 - tv;
     const int vr = 8 * (g & 1) + (l16 >> 1);
     const unsigned char* vrow = slot + tv * W::VPLANE + vr * RB + 8 * (l16 & 1);
     const int vsw = vr % NCH;
+    if constexpr (QM == 1) {
+      const float ef = ldexpf(1.0f, -e_run);
+      axk_f32x4 pa, pb;
 #pragma unroll
-    for (int t = 0; t < DTF; ++t) {
-      const axk_i32x2 w = lds_read_tr8(vrow + 16 * (t ^ vsw));
-      o[t] = mfma_bf16_16x16x32(cvt8((uint32_t)w[0], (uint32_t)w[1], st.vs), pfrag, o[t]);
+      for (int rr = 0; rr < 4; ++rr) {
+        pa[rr] = p[0][rr] * (vs[rr] * ef);
+        pb[rr] = p[1][rr] * (vs[4 + rr] * ef);
+      }
+      const axk_f16x8 pfh = acc_pair_to_b_f16(pa, pb);
+#pragma unroll
+      for (int t = 0; t < DTF; ++t) {
+        const axk_i32x2 w = lds_read_tr8(vrow + 16 * (t ^ vsw));
+        o[t] = mfma_f16_16x16x32(i8x8_to_f16x8_off((uint32_t)w[0], (uint32_t)w[1]), pfh, o[t]);
+      }
+      const axk_u32x4 ones = {0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};  // fp16 1.0 x 8
+      o_one = mfma_f16_16x16x32(__builtin_bit_cast(axk_f16x8, ones), pfh, o_one);
+    } else {
+      const axk_bf16x8 pfrag = acc_pair_to_b(p[0], p[1]);
+#pragma unroll
+      for (int t = 0; t < DTF; ++t) {
+        const axk_i32x2 w = lds_read_tr8(vrow + 16 * (t ^ vsw));
+        o[t] = mfma_bf16_16x16x32(cvt8((uint32_t)w[0], (uint32_t)w[1]), pfrag, o[t]);
+      }
     }
   };
 
@@ -777,6 +855,14 @@ __device__ __forceinline__ void decode_item_8(const ItemDesc& desc, int it, cons
     wait_step(sb);
     if (s + 2 < s_end) issue_step(sa, 0);
     if (any_valid(sb)) compute(sb, 1);
+  }
+
+  if constexpr (QM == 1) {  // O = (O' - 1152 sum P') 2^e_run (a wave without tokens: all zero)
+    const float r = 1152.0f * o_one[0], ef = e_run > -1000 ? ldexpf(1.0f, e_run) : 0.f;
+#pragma unroll
+    for (int t = 0; t < DTF; ++t)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) o[t][rr] = (o[t][rr] - r) * ef;
   }
 
   // merge the four waves' (m, l, O^T) through LDS (over the V slots): wave w takes the head-dim quarter

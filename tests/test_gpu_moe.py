@@ -56,7 +56,12 @@ def _check_layer(c, dev, norm=True):
                                           (2, 64, 1000, 32, 0, 32), (130, 64, 16, 32, 32, 4),
                                           (256, 64, 8, 32, 0, 2),
                                           # K multiples of 256 with <= 64 tokens: the staged-weight streaming kernels
-                                          (20, 512, 32, 256, 256, 4), (64, 256, 64, 256, 0, 8), (65, 256, 16, 256, 256, 2)])
+                                          (20, 512, 32, 256, 256, 4), (64, 256, 64, 256, 0, 8), (65, 256, 16, 256, 256, 2),
+                                          # the staged-weight kernels at H 1024 / 2048: one token; experts over several
+                                          # 8-row passes with F != Fs; no shared expert and 2-tile slots; E > 256;
+                                          # 6-tile routed and 2-tile shared slots
+                                          (1, 1024, 16, 64, 64, 4), (64, 1024, 8, 96, 160, 2), (33, 2048, 128, 32, 0, 8),
+                                          (40, 1024, 300, 32, 32, 6), (9, 1024, 64, 96, 32, 3)])
 def test_moe_small_shapes(dev, t, h, e, f, fs, k):
     g = torch.Generator().manual_seed(t + h + e)
     w = configs.moe_weights(g, hidden=h, experts=e, inter=f, shared_inter=max(fs, 32), router_std=0.5)
