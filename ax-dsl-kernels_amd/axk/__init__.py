@@ -50,6 +50,11 @@ from . import layer  # noqa: E402
 
 __all__ += ["layer"]
 
+from . import group  # noqa: E402
+from .group import DecodeGroup  # noqa: E402
+
+__all__ += ["group", "DecodeGroup"]
+
 from . import manifest  # noqa: E402
 from .manifest import Manifest, io_table  # noqa: E402
 

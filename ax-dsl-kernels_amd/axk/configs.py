@@ -370,3 +370,100 @@ def config4_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None 
     x = torch.randn(b, h, generator=g, device=dev).to(torch.bfloat16)
     return {"cfg": c4, "layers": layers, "indptr": indptr, "indices": perm, "last_page_len": last, "loc": loc,
             "cos": cos, "sin": sin, "x": x}
+
+
+# The 35B's MoE decode group (qwen35moe_group8_gggaggga_mx8_kvc_c16384 of the 35B manifest, built by
+# models/qwen35_35b_a3b/src/70b0fbc/q35_moe_group.py): 8 layers (GDN, GDN, GDN, attention) x 2, hidden 2048,
+# MXFP8 projections and shared expert (inter 512), 256 MXFP4 routed experts of 512, top-8, GDN 16 / 32 heads,
+# attention HQ 16 / HKV 2 / D 256 (the manifest's w_q [8192, 2048] = 16 heads of [q | gate], kc [16384, 512]),
+# rot 64; the reference's 16,384-token cache, here per sequence at a batch of 32 (config 3a's decode batch).
+MOE_GROUP = dict(batch=32, ctx=16383, hidden=2048, inter=512, experts=256, expert_inter=512, top_k=8, hq=16, hkv=2,
+                 d=256, rot=64, nk=16, nv=32, conv=4, page=64, theta=10_000_000.0, eps=1e-6, pattern="gggaggga")
+
+
+def moe_group(dev, seed: int = 0, ctx: int | None = None, batch: int | None = None,
+              pattern: str | None = None) -> dict:
+    """The MoE group's weights, states, paged KV caches and page table, generated ON THE DEVICE by a seeded device
+    generator. Distributions as the small-shape generators: MXFP8 projections and shared expert as proj_weight
+    ("mxfp8": E4M3 codes of N(0, 3^2), E8M0 bytes uniform in 119..123), routed experts as moe_block (MXFP4 nibbles
+    uniform, E8M0 bytes 119..123), bf16 router and shared-expert gate N(0, 0.02), norms 1 + N(0, 0.1), conv taps
+    N(0, 0.5^2) bf16, A_log and dt_bias N(0, 0.5^2), KV ~ N(0, 1) bf16, GDN state ~ N(0, 0.02^2), x ~ N(0, 1).
+    Every sequence holds ctx tokens before the step; the step's token is position ctx, in the page that holds it
+    (a fresh page when ctx is a multiple of the page size). Returns {"cfg", "layers" (DecodeGroup's layer dicts),
+    "attn" (cos, sin, indptr, indices, last_page_len, loc), "x"}."""
+    cg = dict(MOE_GROUP)
+    for k, v in (("ctx", ctx), ("batch", batch), ("pattern", pattern)):
+        if v is not None:
+            cg[k] = v
+    b, h, f, fe, ne = cg["batch"], cg["hidden"], cg["inter"], cg["expert_inter"], cg["experts"]
+    d, hkv, hq, page, nk, nv = cg["d"], cg["hkv"], cg["hq"], cg["page"], cg["nk"], cg["nv"]
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def mx8(n, k):
+        codes = (torch.randn(n, k, generator=g, device=dev) * 3).to(torch.float8_e4m3fn).view(torch.uint8)
+        return codes.contiguous(), torch.randint(119, 124, (n, k // 32), generator=g, device=dev, dtype=torch.uint8)
+
+    def mx4(lead, n, k):
+        codes = torch.randint(0, 256, (lead, n, k // 2), generator=g, device=dev, dtype=torch.uint8)
+        return codes, torch.randint(119, 124, (lead, n, k // 32), generator=g, device=dev, dtype=torch.uint8)
+
+    def norm(n):
+        return 1.0 + 0.1 * torch.randn(n, generator=g, device=dev)
+
+    def bf16(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16)
+
+    def mlp_and_moe(w):
+        w["w_gate"], w["s_gate"] = mx8(f, h)
+        w["w_up"], w["s_up"] = mx8(f, h)
+        w["w_down"], w["s_down"] = mx8(h, f)
+        m = {"w_router": bf16(ne, h, std=0.02), "w_shg": bf16(h, std=0.02)}
+        m["e_gw"], m["e_gs"] = mx4(ne, 2 * fe, h)
+        m["e_dw"], m["e_ds"] = mx4(ne, h, fe)
+        m["top_k"] = cg["top_k"]
+        return m
+
+    kd, vd = nk * 128, nv * 128
+    pages_per_seq = cg["ctx"] // page + 1  # the pages up to and including the one holding position ctx
+    pool = b * pages_per_seq
+    perm = torch.randperm(pool, generator=g, device=dev).to(torch.int32)
+    indptr = (torch.arange(b + 1, device=dev, dtype=torch.int32) * pages_per_seq).contiguous()
+    last = torch.full((b,), cg["ctx"] % page + 1, dtype=torch.int32, device=dev)
+    loc = torch.stack([perm[indptr[1:].long() - 1], torch.full((b,), cg["ctx"] % page, dtype=torch.int32,
+                                                               device=dev)], 1).to(torch.int32).contiguous()
+    layers = []
+    for kind in cg["pattern"]:
+        w = {"ln1": norm(h)}
+        if kind == "g":
+            w["w_qkv"], w["s_qkv"] = mx8(2 * kd + vd, h)
+            w["w_z"], w["s_z"] = mx8(vd, h)
+            w["w_b"], w["s_b"] = mx8(nv, h)
+            w["w_a"], w["s_a"] = mx8(nv, h)
+            w["conv_w"] = bf16(2 * kd + vd, cg["conv"], std=0.5)
+            w["a_log"] = torch.randn(nv, generator=g, device=dev) * 0.5
+            w["dt_bias"] = torch.randn(nv, generator=g, device=dev) * 0.5
+            w["norm_w"] = norm(128)
+            w["w_out"], w["s_out"] = mx8(h, vd)
+            w["ln2"] = norm(h)
+            m = mlp_and_moe(w)
+            st = torch.randn(b, nv, 128, 128, generator=g, device=dev) * 0.02
+            cv = bf16(b, cg["conv"] - 1, 2 * kd + vd)
+            layers.append({"kind": "g", "w": w, "moe": m, "state": st, "conv": cv})
+        else:
+            w["w_q"], w["s_q"] = mx8(hq * 2 * d, h)
+            w["w_k"], w["s_k"] = mx8(hkv * d, h)
+            w["w_v"], w["s_v"] = mx8(hkv * d, h)
+            w["q_norm"] = norm(d)
+            w["k_norm"] = norm(d)
+            w["w_o"], w["s_o"] = mx8(h, hq * d)
+            w["ln2"] = norm(h)
+            m = mlp_and_moe(w)
+            cache = torch.randn(pool, 2, page, hkv, d, generator=g, device=dev, dtype=torch.bfloat16)
+            layers.append({"kind": "a", "w": w, "moe": m, "cache": cache})
+    inv = 1.0 / (cg["theta"] ** (torch.arange(0, cg["rot"], 2, dtype=torch.int64).float() / cg["rot"]))
+    fpos = float(cg["ctx"]) * inv
+    cos = fpos.cos().bfloat16().reshape(1, -1).repeat(b, 1).to(dev).contiguous()
+    sin = fpos.sin().bfloat16().reshape(1, -1).repeat(b, 1).to(dev).contiguous()
+    x = bf16(b, h)
+    attn = {"cos": cos, "sin": sin, "indptr": indptr, "indices": perm, "last_page_len": last, "loc": loc}
+    return {"cfg": cg, "layers": layers, "attn": attn, "x": x}

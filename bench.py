@@ -1181,6 +1181,111 @@ class GroupDecodeWorkload(Workload):
                           f"CPU), scaled to {n_g} GDN + {n_a} attention layers x {c4['batch']} sequences, per layer"}
 
 
+class MoeGroupDecodeWorkload(Workload):
+    """The 35B's MoE decode group (qwen35moe_group8_gggaggga_mx8_kvc_c16384, q35_moe_group.py:90-123): 8 layers
+    ((GDN, GDN, GDN, attention) x 2) at the 35B's widths, every MLP the MoE block (shared expert MXFP8 inter 512,
+    256 MXFP4 experts of 512, top-8), MXFP8 projections, GDN 16 / 32 heads, attention HQ 16 / HKV 2 / D 256; 32
+    sequences, each at 16,383 cached tokens of paged bf16 KV (the step's token fills the reference's 16,384-token
+    cache). One step = the 8 layers for one new token per sequence (axk.DecodeGroup.step), captured with the other
+    steps in one HIP graph. value: µs per decode layer (step / 8). Algorithmic bytes: every dense weight, norm,
+    router and shared-expert gate read once, the routed experts each layer actually uses (its distinct experts over
+    the 32 tokens), the GDN and conv states read and written, every sequence's K and V read by each attention layer,
+    the new rows written, each layer's activations in and out. The inputs (about 6 GB) are generated on the device."""
+
+    name = "moe_group_decode"
+    tokens = 32  # tokens one step carries through the path
+    kernel = "35B MoE decode group (8 layers)"
+    timing = "graph"
+    traffic_profile = "moe_group_decode_b32_pmc.txt"  # every kernel of the step, summed
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs, group
+
+        c = configs.moe_group(dev)
+        cg = c["cfg"]
+        self.c, self.cg = c, cg
+        b, h = cg["batch"], cg["hidden"]
+        args = (c["layers"], b, h, dev, cg["nk"], cg["nv"], cg["hq"], cg["rot"], cg["eps"], "mxfp8", "mxfp8")
+        # one eager step with the routing outputs kept: the distinct experts each layer reads
+        probe = group.DecodeGroup(*args, attn=c["attn"], routing=True)
+        probe.step(c["x"])
+        self.active = [int(torch.unique(r["topk_ids"]).numel()) for r in probe.routing]
+        del probe
+        self.grp = group.DecodeGroup(*args, attn=c["attn"])
+        self.grp.x.copy_(c["x"])
+        per_expert = sum(c["layers"][0]["moe"][n][0].numel() for n in ("e_gw", "e_gs", "e_dw", "e_ds"))
+        wbytes = sum(t.numel() * t.element_size() for L in c["layers"] for t in L["w"].values())
+        wbytes += sum(L["moe"][n].numel() * L["moe"][n].element_size() for L in c["layers"]
+                      for n in ("w_router", "w_shg"))
+        sbytes = sum(2 * (L["state"].numel() * 4 + L["conv"].numel() * 2) for L in c["layers"] if L["kind"] == "g")
+        tokens = b * (cg["ctx"] + 1)
+        n_attn = sum(1 for L in c["layers"] if L["kind"] == "a")
+        kv_row = 2 * cg["hkv"] * cg["d"] * 2  # K and V of one token, bytes
+        self.alg_bytes = wbytes + sum(self.active) * per_expert + sbytes + \
+            n_attn * (tokens * kv_row + b * kv_row) + 2 * len(c["layers"]) * b * h * 2
+        self.layers_per_step = len(c["layers"])
+        self.value_per = self.layers_per_step
+        self.unit = "µs/decode-layer"
+        self.config = {"workload": "35B MoE decode group (gggaggga), B=32, ctx 16384, H=2048, MXFP8 projections, "
+                                   "GDN 16/32 heads, HQ=16 HKV=2 D=256, MoE 256 MXFP4 experts F=512 top-8 + shared "
+                                   "MXFP8 F=512",
+                       "layers": self.layers_per_step, "distinct_experts_per_layer": self.active,
+                       "kv_bytes_per_attention_layer": tokens * kv_row}
+        self.dtype = "bf16 activations, mxfp8 / mxfp4 weights, fp32 accumulation and state"
+
+    def step(self, i: int) -> None:
+        self.grp.step()
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import layer as olayer
+
+        c, cg = self.c, self.cg
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        n = 4  # a bounded sample: 4 of the 32 sequences through one GDN layer, scaled by sequences
+        gl = next(L for L in c["layers"] if L["kind"] == "g")
+        al = next(L for L in c["layers"] if L["kind"] == "a")
+        wg = {k: v.cpu() for k, v in gl["w"].items()}
+        wa = {k: v.cpu() for k, v in al["w"].items()}
+        mg = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in gl["moe"].items()}
+        ma = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in al["moe"].items()}
+        x = c["x"].cpu()
+        st, cv = gl["state"][:n].cpu(), gl["conv"][:n].cpu()
+
+        def run_g():
+            y, _, _ = olayer.gdn_layer_half(x[:n], wg, st, cv, cg["nk"], cg["nv"], cg["eps"], proj_fmt="mxfp8")
+            return olayer.moe_block_parts(x[:n], y, wg, mg, cg["eps"], fmt="mxfp8")
+
+        t_g, reps_g = _time_cpu(run_g, budget_s=8.0, min_reps=1, max_reps=3)
+        # sequence 0 of one attention layer at the full context: its pages gathered into a compact host cache
+        a = c["attn"]
+        n0 = int(a["indptr"][1].item())
+        cache0 = al["cache"][a["indices"][:n0].long()].cpu()
+        ptr0 = torch.tensor([0, n0], dtype=torch.int32)
+        ind0 = torch.arange(n0, dtype=torch.int32)
+        loc0 = torch.tensor([[n0 - 1, int(a["loc"][0, 1].item())]], dtype=torch.int32)
+        cos, sin, last = a["cos"][:1].cpu(), a["sin"][:1].cpu(), a["last_page_len"][:1].cpu()
+
+        def run_a():
+            y, _ = olayer.attn_layer_half(x[:1], wa, cos, sin, cache0, ptr0, ind0, last, loc0, cg["hq"], cg["rot"],
+                                          cg["eps"], proj_fmt="mxfp8")
+            return olayer.moe_block_parts(x[:1], y, wa, ma, cg["eps"], fmt="mxfp8")
+
+        t_a, reps_a = _time_cpu(run_a, budget_s=8.0, min_reps=1, max_reps=3)
+        n_g = sum(1 for L in c["layers"] if L["kind"] == "g")
+        n_a = len(c["layers"]) - n_g
+        step = n_g * t_g * cg["batch"] / n + n_a * cg["batch"] * t_a
+        return {"value": step / len(c["layers"]) * 1e6, "unit": "µs/decode-layer", "cores": nt, "kind": "port",
+                "sample": f"one GDN MoE layer on {n} of the {cg['batch']} sequences (median of {reps_g}) and one "
+                          f"attention MoE layer for one sequence at the full context (median of {reps_a}) with the "
+                          f"oracle (oracle/layer.py, torch CPU), scaled to {n_g} GDN + {n_a} attention layers x "
+                          f"{cg['batch']} sequences, per layer"}
+
+
 WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: PagedDecodeWorkload,
              GdnDecodeWorkload.name: GdnDecodeWorkload, GdnPrefillWorkload.name: GdnPrefillWorkload,
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
@@ -1189,6 +1294,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload, PagedDecodeI8Workload.name: PagedDecodeI8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
              MxLinearPrefillWorkload.name: MxLinearPrefillWorkload, MoeLayerPrefillWorkload.name: MoeLayerPrefillWorkload,
+             MoeGroupDecodeWorkload.name: MoeGroupDecodeWorkload,
              CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
