@@ -12,6 +12,8 @@ The role of the reference's group kernels, one call per group of G layers instea
   * models/qwen38_27b/decode/q35_group.py:413-437 (the dense group of config 4).
 The attention layers of a group share the step's rope rows and page table (cos / sin / pos / nblk / mask of
 q35_moe_group.py:97-99, 155-156: the same token positions in every attention layer of the step).
+A group that ends the model also carries the LM head (LMHEAD=1 of models/qwen38_27b/decode/q35_group.py:55-57,
+442-452): the final RMSNorm of the last layer's output and the output projection into fp32 logits, inside the step.
 """
 from __future__ import annotations
 
@@ -19,7 +21,7 @@ from typing import Optional
 
 import torch
 
-from . import layer
+from . import gemm, glue, layer
 
 _ATTN_KEYS = ("cos", "sin", "indptr", "indices", "last_page_len", "loc")
 
@@ -36,7 +38,9 @@ class DecodeGroup:
     updated in place by every step). attn: the page table of the step shared by the attention layers, {"cos", "sin"
     bf16 [B, rot/2], "indptr", "indices", "last_page_len" int32, "loc" int32 [B, 2]} (layer.attn_layer_decode's
     arguments). routing=True gives every MoE layer its routing outputs (logits, topk_ids, topk_weights) in
-    self.routing[j].
+    self.routing[j]. lm_head (optional): {"norm": f32 [H] (the final norm's 1 + weight), "w", "s": the output
+    projection [V, H] in "fmt" ("mxfp4": E2M1 pairs [V, H/2]; "mxfp8": E4M3 bytes [V, H]; E8M0 scales [V, H/32])};
+    every step then also writes self.logits f32 [B, V] = rmsnorm(out, norm) W^T (self.hn holds the normalised rows).
 
     Workspaces are allocated here, once per layer kind, and shared by the layers of that kind (the layers run one
     after another on one stream); a step allocates nothing. step() runs the layers eagerly; capture() records one
@@ -45,7 +49,8 @@ class DecodeGroup:
 
     def __init__(self, layers: list, batch: int, hidden: int, device, num_k_heads: int = 16, num_v_heads: int = 32,
                  num_qo_heads: int = 0, rot: int = 0, eps: float = 1e-6, proj_fmt: str = "fp8",
-                 mlp_fmt: str = "mxfp4", attn: Optional[dict] = None, routing: bool = False):
+                 mlp_fmt: str = "mxfp4", attn: Optional[dict] = None, routing: bool = False,
+                 lm_head: Optional[dict] = None):
         _check(len(layers) > 0, "a decode group needs at least one layer")
         self.layers, self.b, self.h = layers, batch, hidden
         self.nk, self.nv, self.hq, self.rot, self.eps = num_k_heads, num_v_heads, num_qo_heads, rot, eps
@@ -92,6 +97,18 @@ class DecodeGroup:
         self.out = torch.empty_like(self.x)
         self._bufs = [torch.empty_like(self.x), torch.empty_like(self.x)]
         self.inputs = None  # set by step(record=True): each layer's input, cloned
+        self.lm_head, self.hn, self.logits = None, None, None
+        if lm_head is not None:
+            fmt = lm_head.get("fmt", "mxfp4")
+            _check(fmt in ("mxfp4", "mxfp8"), f"the LM head's fmt must be 'mxfp4' or 'mxfp8', got {fmt!r}")
+            nw, w, sc = lm_head["norm"], lm_head["w"], lm_head["s"]
+            _check(nw.dtype == torch.float32 and nw.numel() == hidden, f"the LM head's norm must be float32 [{hidden}]")
+            _check(w.dim() == 2 and w.shape[1] == (hidden // 2 if fmt == "mxfp4" else hidden) and
+                   tuple(sc.shape) == (w.shape[0], hidden // 32),
+                   f"the LM head's w / s must be [V, {hidden // 2 if fmt == 'mxfp4' else hidden}] / [V, {hidden // 32}]")
+            self.lm_head = dict(norm=nw, w=w, s=sc, fmt=fmt)
+            self.hn = torch.empty_like(self.x)
+            self.logits = torch.empty(batch, w.shape[0], dtype=torch.float32, device=device)
         self.graph = None
         self._stream = None
 
@@ -123,6 +140,13 @@ class DecodeGroup:
                 self.inputs.append(src.clone())
             self._layer(j, src, dst)
             src = dst
+        if self.lm_head is not None:
+            lm = self.lm_head
+            glue.rmsnorm(self.out, lm["norm"], self.eps, out=self.hn)
+            if lm["fmt"] == "mxfp4":
+                gemm.mxfp4_gemm(self.hn, lm["w"], lm["s"], out_dtype=torch.float32, output=self.logits)
+            else:
+                gemm.mxfp8_gemm(self.hn, lm["w"], lm["s"], out_dtype=torch.float32, output=self.logits, fmt="e4m3")
         return self.out
 
     def capture(self) -> None:

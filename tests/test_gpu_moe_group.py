@@ -11,6 +11,8 @@ attention HQ 16 / HKV 2 / D 256), 32 sequences at 16,383 cached tokens each.
   * the group bound from the 35B manifest's decode.group (its packs filled by Manifest.store_layer, the routed
     experts in e_gw<j> .. e_ds<j>) through group.manifest_layers runs like the same weights as loose tensors, bit for
     bit (a small batch and context);
+  * the group carrying the LM head (final norm + the 35B's MXFP4 output projection) gives the separate calls'
+    logits bit for bit, eager and replayed, and the oracle's on a slice;
   * the first GDN layer (4 sequences) and the first attention layer (sequence 0 over its full context) of the eager
     step against the oracle at the MoE layer bars: the routing from the kernel's own logits (ids bit-exact against a
     stable descending sort of them, weights at fp32 tolerance), the output within the reference's fused-layer bar
@@ -24,6 +26,7 @@ import pytest
 import torch
 
 from axk import configs, group
+from axk import gemm as axk_gemm
 from axk import manifest as mf
 from oracle import layer as olayer
 from oracle import moe as omoe
@@ -199,3 +202,44 @@ def test_moe_group_bound_from_the_manifest_runs_like_loose_tensors(dev):
         for n in ("state", "conv", "cache"):
             if n in L:
                 assert _same(Lb[n], L[n])
+
+
+def test_moe_group_with_lm_head(dev):
+    """The group that ends the model carries the LM head (q35_group.py:442-452 with LMHEAD=1): the final norm and
+    the 35B's MXFP4 output projection (248320 x 2048, mul_mat_mx4_n248320_k2048) inside the step. The logits equal
+    the separate norm and GEMM calls on the step's output bit for bit, eager and graph-replayed; the normalised rows
+    and a slice of the logits against the oracle at the per-op bar."""
+    from axk import glue
+    from oracle import mx
+
+    c = configs.moe_group(dev, batch=4, ctx=100, seed=7)
+    cg = c["cfg"]
+    lm = configs.lm_head_case(dev, seed=8)
+    norm = 1.0 + 0.1 * torch.randn(cg["hidden"], generator=torch.Generator(device=dev).manual_seed(9), device=dev)
+    print(f"35B MoE group + LM head {lm['w'].shape[0]} x {cg['hidden']}, batch 4", flush=True)
+    grp = group.DecodeGroup(c["layers"], cg["batch"], cg["hidden"], dev, cg["nk"], cg["nv"], cg["hq"], cg["rot"],
+                            cg["eps"], "mxfp8", "mxfp8", attn=c["attn"],
+                            lm_head=dict(norm=norm, w=lm["w"], s=lm["s"], fmt="mxfp4"))
+    wm = torch.zeros(c["layers"][3]["cache"].shape[0], c["layers"][3]["cache"].shape[2], dtype=torch.bool,
+                     device=dev)
+    wm[c["attn"]["loc"][:, 0].long(), c["attn"]["loc"][:, 1].long()] = True
+    s0 = _snapshot(c, wm)
+    out = grp.step(c["x"]).clone()
+    logits = grp.logits.clone()
+    hn = glue.rmsnorm(out, norm, cg["eps"])
+    sep = axk_gemm.mxfp4_gemm(hn, lm["w"], lm["s"], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert _same(grp.hn, hn) and _same(logits, sep)
+    assert torch.isfinite(logits).all()
+    ref_h = olayer.rmsnorm(out.cpu(), norm.cpu(), cg["eps"])
+    torch.testing.assert_close(hn.float().cpu(), ref_h.float(), **TOL)
+    rows = 3000
+    ref = mx.mx_linear(hn.cpu(), lm["w"][:rows].cpu().numpy(), lm["s"][:rows].cpu().numpy())
+    torch.testing.assert_close(logits[:, :rows].cpu(), ref.float(), **TOL)
+    # graph-replayed from the same states: the same logits bit for bit
+    grp.capture()
+    _restore(c, s0, wm)
+    torch.cuda.synchronize()
+    grp.replay(c["x"])
+    torch.cuda.synchronize()
+    assert _same(grp.out, out) and _same(grp.logits, logits)
