@@ -42,6 +42,18 @@ def lm_head_case(dev, seed: int = 0, n: int = LM_HEAD["vocab"], k: int = LM_HEAD
     return {"x": x, "w": pack_codes(codes).contiguous(), "s": scales.contiguous()}
 
 
+def lm_head_nvfp4_case(dev, seed: int = 0, n: int = LM_HEAD["vocab"], k: int = LM_HEAD["hidden"], m: int = 1):
+    """The LM head in NVFP4 (the reference's NVFP4 head, test_nvfp4_lm_head.py): uniform nibbles, E4M3 block scale
+    bytes uniform in 0x28 .. 0x37 (0.25 .. 0.47), scale2 = 0.05 (a weight RMS of about 0.05 as the MXFP4 head's), x
+    bf16 [m, k] ~ N(0,1), fp32 logits. Generated on `dev`."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    codes = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8, device=dev)
+    scales = torch.randint(0x28, 0x38, (n, k // 16), generator=g, dtype=torch.uint8, device=dev)
+    x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+    return {"x": x, "w": pack_codes(codes).contiguous(), "s": scales.contiguous(),
+            "s2": torch.tensor([0.05], dtype=torch.float32, device=dev)}
+
+
 def paged_case(lens, hq: int, hkv: int, d: int, page: int, g: torch.Generator, extra_pages: int = 0):
     """A paged KV pool holding sequences of the given lengths, pages placed by a random permutation."""
     npages = [(L + page - 1) // page for L in lens]

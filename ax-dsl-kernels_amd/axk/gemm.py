@@ -1,4 +1,4 @@
-"""Runtime-weight linear operators (MXFP4 / FP8 E4M3 / bf16 weights) on gfx950.
+"""Runtime-weight linear operators (MXFP4 / NVFP4 / MXFP8 / FP8 E4M3 / bf16 weights) on gfx950.
 
 Mirrors the operator API of sgl_kernel_axera.gemm
 (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/gemm.py): the same names, argument meaning and
@@ -106,6 +106,42 @@ def mxfp4_gemm(
     _lib.call(
         "axk_mxfp4_gemm", a.data_ptr(), a.stride(0), codes.data_ptr(), scales.data_ptr(), _lib.ptr(bias),
         output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output
+
+
+def nvfp4_gemm(
+    a: torch.Tensor,
+    b_fp4: torch.Tensor,
+    b_scale: torch.Tensor,
+    b_scale2: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """NVFP4 GEMM: output = a @ dequant(b_fp4, b_scale, b_scale2).T + bias (gemm.py:495-561).
+
+    a        : (m, k) bf16 activation
+    b_fp4    : (n, k/2) packed E2M1 codes, low nibble = even column (u8 or float4_e2m1fn_x2 view), as
+               quantize_nvfp4 packs them
+    b_scale  : (n, k/16) E4M3 per-16 block scale (u8 or float8_e4m3fn view)
+    b_scale2 : (1,) float32 global scale on the device (a runtime input: rescaling it needs no repacking)
+    """
+    m, k = _check_a(a)
+    codes, scales = _as_u8(b_fp4, "b_fp4"), _as_u8(b_scale, "b_scale")
+    n = codes.shape[0]
+    if codes.dim() != 2 or codes.shape[1] * 2 != k:
+        raise ValueError(f"b_fp4 shape {tuple(b_fp4.shape)} is incompatible with a having k={k}")
+    if tuple(scales.shape) != (n, k // 16):
+        raise ValueError(f"b_scale shape {tuple(b_scale.shape)} is incompatible with (n, k/16)={(n, k // 16)}")
+    if b_scale2.dtype != torch.float32 or b_scale2.numel() != 1:
+        raise ValueError("b_scale2 must be a float32 tensor of one element")
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    codes, scales = codes.contiguous(), scales.contiguous()
+    _lib.require_device(a, codes, scales, b_scale2, output)
+    _lib.call(
+        "axk_nvfp4_gemm", a.data_ptr(), a.stride(0), codes.data_ptr(), scales.data_ptr(), b_scale2.data_ptr(),
+        _lib.ptr(bias), output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
     )
     return output
 

@@ -39,7 +39,9 @@ class DecodeGroup:
     bf16 [B, rot/2], "indptr", "indices", "last_page_len" int32, "loc" int32 [B, 2]} (layer.attn_layer_decode's
     arguments). routing=True gives every MoE layer its routing outputs (logits, topk_ids, topk_weights) in
     self.routing[j]. lm_head (optional): {"norm": f32 [H] (the final norm's 1 + weight), "w", "s": the output
-    projection [V, H] in "fmt" ("mxfp4": E2M1 pairs [V, H/2]; "mxfp8": E4M3 bytes [V, H]; E8M0 scales [V, H/32])};
+    projection [V, H] in "fmt" ("mxfp4": E2M1 pairs [V, H/2] with E8M0 scales [V, H/32]; "mxfp8": E4M3 bytes
+    [V, H] with E8M0 scales [V, H/32]; "nvfp4": E2M1 pairs [V, H/2] with E4M3 scales [V, H/16] and "s2", the fp32
+    scale2 [1] on the device)};
     every step then also writes self.logits f32 [B, V] = rmsnorm(out, norm) W^T (self.hn holds the normalised rows).
 
     Workspaces are allocated here, once per layer kind, and shared by the layers of that kind (the layers run one
@@ -100,13 +102,15 @@ class DecodeGroup:
         self.lm_head, self.hn, self.logits = None, None, None
         if lm_head is not None:
             fmt = lm_head.get("fmt", "mxfp4")
-            _check(fmt in ("mxfp4", "mxfp8"), f"the LM head's fmt must be 'mxfp4' or 'mxfp8', got {fmt!r}")
+            _check(fmt in ("mxfp4", "mxfp8", "nvfp4"), f"the LM head's fmt must be mxfp4, mxfp8 or nvfp4, got {fmt!r}")
             nw, w, sc = lm_head["norm"], lm_head["w"], lm_head["s"]
             _check(nw.dtype == torch.float32 and nw.numel() == hidden, f"the LM head's norm must be float32 [{hidden}]")
-            _check(w.dim() == 2 and w.shape[1] == (hidden // 2 if fmt == "mxfp4" else hidden) and
-                   tuple(sc.shape) == (w.shape[0], hidden // 32),
-                   f"the LM head's w / s must be [V, {hidden // 2 if fmt == 'mxfp4' else hidden}] / [V, {hidden // 32}]")
-            self.lm_head = dict(norm=nw, w=w, s=sc, fmt=fmt)
+            kw = hidden if fmt == "mxfp8" else hidden // 2
+            ks = hidden // (16 if fmt == "nvfp4" else 32)
+            _check(w.dim() == 2 and w.shape[1] == kw and tuple(sc.shape) == (w.shape[0], ks),
+                   f"the LM head's w / s must be [V, {kw}] / [V, {ks}]")
+            _check(fmt != "nvfp4" or lm_head.get("s2") is not None, "an NVFP4 LM head needs its scale2 s2")
+            self.lm_head = dict(norm=nw, w=w, s=sc, fmt=fmt, s2=lm_head.get("s2"))
             self.hn = torch.empty_like(self.x)
             self.logits = torch.empty(batch, w.shape[0], dtype=torch.float32, device=device)
         self.graph = None
@@ -145,6 +149,8 @@ class DecodeGroup:
             glue.rmsnorm(self.out, lm["norm"], self.eps, out=self.hn)
             if lm["fmt"] == "mxfp4":
                 gemm.mxfp4_gemm(self.hn, lm["w"], lm["s"], out_dtype=torch.float32, output=self.logits)
+            elif lm["fmt"] == "nvfp4":
+                gemm.nvfp4_gemm(self.hn, lm["w"], lm["s"], lm["s2"], out_dtype=torch.float32, output=self.logits)
             else:
                 gemm.mxfp8_gemm(self.hn, lm["w"], lm["s"], out_dtype=torch.float32, output=self.logits, fmt="e4m3")
         return self.out

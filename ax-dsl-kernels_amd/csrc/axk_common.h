@@ -84,6 +84,22 @@ AXK_DEV float e4m3_to_f32(uint32_t b) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
+// Eight E2M1 codes times an arbitrary fp32 scale s (an NVFP4 block's E4M3 scale) -> bf16. gfx950's scaled converts
+// apply only the exponent of their scale operand (a power of two, as MX scales are), so the codes are decoded
+// exactly at scale 1 and multiplied by s in fp32: the product of an E2M1 value (at most 2 significant bits) and an
+// E4M3 value (at most 4) is exact in fp32 and again in bf16.
+AXK_DEV axk_bf16x8 fp4x8_to_bf16x8_mul(uint32_t w, float s) {
+  const axk_f32x2 f0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+  const axk_f32x2 f1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+  const axk_f32x2 f2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+  const axk_f32x2 f3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  axk_bf16x8 r;
+  r[0] = (__bf16)(f0[0] * s); r[1] = (__bf16)(f0[1] * s); r[2] = (__bf16)(f1[0] * s); r[3] = (__bf16)(f1[1] * s);
+  r[4] = (__bf16)(f2[0] * s); r[5] = (__bf16)(f2[1] * s); r[6] = (__bf16)(f3[0] * s); r[7] = (__bf16)(f3[1] * s);
+  return r;
+}
+
+
 // Four E4M3 bytes -> four bf16 (exact: E4M3 values fit bf16's 8-bit exponent and 7-bit mantissa).
 AXK_DEV void fp8x4_to_bf16(uint32_t w, __bf16* dst) {
 #pragma unroll

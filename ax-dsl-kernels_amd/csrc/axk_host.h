@@ -112,7 +112,7 @@ __attribute__((visibility("hidden"))) int axk_fill_iota_i32(int32_t* out, int64_
 // leading dimension ldr). Rows must be whole 128-byte segments. Returns an AXK status.
 #define AXK_MX_GROUP_MAX 4
 enum { AXK_MX_EPI_PLAIN = 0, AXK_MX_EPI_SWIGLU = 1, AXK_MX_EPI_RES = 2 };
-enum { AXK_MX_MXFP4 = 0, AXK_MX_FP8 = 1, AXK_MX_MXFP8 = 2 };
+enum { AXK_MX_MXFP4 = 0, AXK_MX_FP8 = 1, AXK_MX_MXFP8 = 2, AXK_MX_NVFP4 = 3 };
 struct AxkMxMat {
   const uint8_t* w;
   const uint8_t* ws;
@@ -121,6 +121,7 @@ struct AxkMxMat {
   void* out;
   int64_t ldo;
   int64_t n;
+  const float* gscale;  // NVFP4 (AXK_MX_NVFP4): the fp32 scale2 [1] in device memory; E4M3 ws [n, k/16]
 };
 // Optional conv epilogue on mats[0] (plain bf16): each row is one token of its sequence; the output is
 // silu(causal_conv1d) over the projection's bf16 output with taps w [n, kernel] (tap 0 = the current token) and

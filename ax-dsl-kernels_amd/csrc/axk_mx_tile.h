@@ -9,10 +9,15 @@
 
 namespace axk {
 
-enum WeightFmt { WF_MXFP4 = 0, WF_FP8 = 1, WF_BF16 = 2, WF_MXFP8 = 3, WF_MXBF8 = 4 };
+enum WeightFmt { WF_MXFP4 = 0, WF_FP8 = 1, WF_BF16 = 2, WF_MXFP8 = 3, WF_MXBF8 = 4, WF_NVFP4 = 5 };
 
 // Formats whose E8M0 scales (one per 32 values along K, [N, K/32]) are applied inside the unit decode.
 __host__ __device__ constexpr bool is_mx(int F) { return F == WF_MXFP4 || F == WF_MXFP8 || F == WF_MXBF8; }
+// NVFP4: E2M1 codes as MXFP4's with E4M3 scales, one per 16 values along K ([N, K/16]), applied inside the unit
+// decode; the per-matrix fp32 scale2 multiplies the sums in the epilogue.
+__host__ __device__ constexpr bool is_nv(int F) { return F == WF_NVFP4; }
+__host__ __device__ constexpr bool has_block_scales(int F) { return is_mx(F) || is_nv(F); }
+__host__ __device__ constexpr bool is_fp4(int F) { return F == WF_MXFP4 || F == WF_NVFP4; }
 
 template <int F>
 struct WUnit;
@@ -31,6 +36,27 @@ struct WUnit<WF_MXFP4> {
   static AXK_DEV axk_bf16x8 conv(const uint4& q, int step, float sc) {
     const uint32_t word = step == 0 ? q.x : step == 1 ? q.y : step == 2 ? q.z : q.w;
     return fp4x8_to_bf16x8(word, sc);
+  }
+};
+
+// NVFP4: codes [N, K/2] (low nibble = even k), E4M3 scales [N, K/16]. A 16-byte unit (32 values) spans two scale
+// blocks: steps 0-1 the first, 2-3 the second; its scale is the two E4M3 bytes (first block low).
+template <>
+struct WUnit<WF_NVFP4> {
+  static constexpr int V = 32;
+  static constexpr int STEPS = 4;
+  static AXK_DEV uint4 load(const uint8_t* w, int64_t n, int64_t K, int64_t kb) {
+    return *reinterpret_cast<const uint4*>(w + n * (K >> 1) + (kb >> 1));
+  }
+  static AXK_DEV uint32_t scale(const uint8_t* s, int64_t n, int64_t K, int64_t kb) {
+    const uint8_t* p = s + n * (K >> 4) + (kb >> 4);
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+  }
+  static AXK_DEV axk_bf16x8 conv(const uint4& q, int step, uint32_t sc2) {
+    const uint32_t word = step == 0 ? q.x : step == 1 ? q.y : step == 2 ? q.z : q.w;
+    // both E4M3 scales of the unit in one convert (scale 1: exact), shared by the four steps
+    const axk_f32x2 s = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(sc2, 1.0f, false);
+    return fp4x8_to_bf16x8_mul(word, step >= 2 ? s[1] : s[0]);
   }
 };
 
@@ -116,8 +142,9 @@ __device__ __forceinline__ void mx_tile_accum(const uint16_t* const (&xrow)[MT],
   const int lane = threadIdx.x & 63, g = lane >> 4;
   const int64_t NC = (K + CH - 1) / CH;
   for (int64_t c0 = c_begin; c0 < NC; c0 += c_step * UNROLL) {
+    using S = decltype(U::scale(wscale, n, K, 0));  // float, or NVFP4's pair of E4M3 bytes
     uint4 q[UNROLL];
-    float sc[UNROLL];
+    S sc[UNROLL];
     int64_t kb[UNROLL];
     bool kv[UNROLL];
 #pragma unroll
@@ -126,7 +153,7 @@ __device__ __forceinline__ void mx_tile_accum(const uint16_t* const (&xrow)[MT],
       kb[u] = c * CH + g * U::V;
       kv[u] = c < NC && kb[u] < K;
       q[u] = make_uint4(0u, 0u, 0u, 0u);
-      sc[u] = 1.0f;
+      sc[u] = S(1);
       if (nvalid && kv[u]) {
         q[u] = U::load(w, n, K, kb[u]);
         sc[u] = U::scale(wscale, n, K, kb[u]);
@@ -155,7 +182,7 @@ constexpr int kSegLd = kSegBytes + 16;
 
 template <int F>
 __host__ __device__ constexpr int64_t row_bytes(int64_t K) {
-  return F == WF_MXFP4 ? K / 2 : (F == WF_BF16 ? 2 * K : K);
+  return is_fp4(F) ? K / 2 : (F == WF_BF16 ? 2 * K : K);
 }
 
 }  // namespace axk

@@ -44,7 +44,8 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
                                                           const uint8_t* __restrict__ wscale,
                                                           const float* __restrict__ row_scale,
                                                           const float* __restrict__ col_scale,
-                                                          const float* __restrict__ bias, void* __restrict__ out,
+                                                          const float* __restrict__ bias,
+                                                          const float* __restrict__ gscale, void* __restrict__ out,
                                                           int out_f32, int M, int N, int64_t K) {
   __shared__ __align__(16) float red[kMaxWaves * MT * 4 * 64];
 
@@ -83,6 +84,7 @@ __global__ __launch_bounds__(1024) void mx_linear_kernel(const uint16_t* __restr
     if (m < M && nn < N) {
       if (row_scale) v *= row_scale[m];
       if (col_scale) v *= col_scale[nn];
+      if (gscale) v *= *gscale;
       if (bias) v += bias[nn];
       if (out_f32)
         reinterpret_cast<float*>(out)[(int64_t)m * N + nn] = v;
@@ -100,6 +102,7 @@ struct MxGroup {
   const uint8_t* ws[AXK_MX_GROUP_MAX];
   const float* col_scale[AXK_MX_GROUP_MAX];
   const float* bias[AXK_MX_GROUP_MAX];
+  const float* gscale[AXK_MX_GROUP_MAX];  // NVFP4: the matrix's fp32 scale2 (one value, device memory)
   void* out[AXK_MX_GROUP_MAX];
   int64_t ldo[AXK_MX_GROUP_MAX];
   int n[AXK_MX_GROUP_MAX];
@@ -181,7 +184,8 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
       const int64_t r = n0 + 8 * h + lr;
       src[t][h] = g.w[mi] + (r < nmax ? r : nmax) * rb + 16 * lc;
     }
-    srow[t] = axk::is_mx(F) ? g.ws[mi] + (n0 + nl < nmax ? n0 + nl : nmax) * (K / 32) : nullptr;
+    srow[t] = axk::has_block_scales(F) ? g.ws[mi] + (n0 + nl < nmax ? n0 + nl : nmax) * (K / (axk::is_nv(F) ? 16 : 32))
+                                       : nullptr;
   }
 
   axk_f32x4 acc[NT][MT];
@@ -193,12 +197,14 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
   for (int64_t d = wave; d < ND; d += nwaves) {
     axk_u32x4 q[NT][2];
     uint2 sw[NT];  // the segment's E8M0 scales: 8 bytes (MXFP4: 256 values) or 4 (MXFP8: 128 values)
+    uint4 sv[NT];  // NVFP4: the segment's 16 E4M3 scales (256 values)
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)  // weights are read once: non-temporal
         q[t][h] = __builtin_nontemporal_load(reinterpret_cast<const axk_u32x4*>(src[t][h] + d * axk::kSegBytes));
       if (F == axk::WF_MXFP4) sw[t] = *reinterpret_cast<const uint2*>(srow[t] + 8 * d);
+      if (F == axk::WF_NVFP4) sv[t] = *reinterpret_cast<const uint4*>(srow[t] + 16 * d);
       if (F == axk::WF_MXFP8 || F == axk::WF_MXBF8) sw[t].x = *reinterpret_cast<const uint32_t*>(srow[t] + 4 * d);
     }
     axk_bf16x8 a[MT][2][U::STEPS];
@@ -220,10 +226,17 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
       for (int j = 0; j < 2; ++j) {
         const uint4 unit = __builtin_bit_cast(
             uint4, *reinterpret_cast<const axk_u32x4*>(tile + (t * 16 + nl) * axk::kSegLd + 64 * j + 16 * kg));
-        // unit (j, kg) of the segment: values 64 j + V kg .. + V, in scale block (64 j + V kg) / 32
-        const float sc = F == axk::WF_MXFP4 ? e8m0_to_f32(((j ? sw[t].y : sw[t].x) >> (8 * kg)) & 0xffu)
-                         : axk::is_mx(F)    ? e8m0_to_f32((sw[t].x >> (8 * (2 * j + (kg >> 1)))) & 0xffu)
-                                            : 1.0f;
+        // unit (j, kg) of the segment: values 64 j + V kg .. + V, in scale block (64 j + V kg) / 32 (NVFP4: the two
+        // 16-value blocks 4 j + 2 kg and the next, bytes 2 (kg % 2) .. + 1 of dword 2 j + kg / 2)
+        decltype(U::scale(nullptr, 0, 0, 0)) sc;
+        if constexpr (F == axk::WF_NVFP4) {
+          const uint32_t dw = (kg >> 1) ? (j ? sv[t].w : sv[t].y) : (j ? sv[t].z : sv[t].x);
+          sc = (dw >> (16 * (kg & 1))) & 0xffffu;
+        } else {
+          sc = F == axk::WF_MXFP4 ? e8m0_to_f32(((j ? sw[t].y : sw[t].x) >> (8 * kg)) & 0xffu)
+               : axk::is_mx(F)    ? e8m0_to_f32((sw[t].x >> (8 * (2 * j + (kg >> 1)))) & 0xffu)
+                                  : 1.0f;
+        }
 #pragma unroll
         for (int s = 0; s < U::STEPS; ++s) {
           const axk_bf16x8 b = U::conv(unit, s, sc);
@@ -256,11 +269,13 @@ __global__ __launch_bounds__(64 * WMAX) __attribute__((amdgpu_waves_per_eu(WMAX 
     float v = total(t, u, r, l);
     if (g.row_scale) v *= g.row_scale[m];
     if (g.col_scale[mi]) v *= g.col_scale[mi][nn];
+    if (g.gscale[mi]) v *= *g.gscale[mi];
     if (g.bias[mi]) v += g.bias[mi][nn];
     if (EPI == EPI_SWIGLU) {
       float up = total(t + 1, u, r, l);
       if (g.row_scale) up *= g.row_scale[m];
       if (g.col_scale[1]) up *= g.col_scale[1][nn];
+      if (g.gscale[1]) up *= *g.gscale[1];
       if (g.bias[1]) up += g.bias[1][nn];
       v = silu_f32(round_bf16(v)) * round_bf16(up);
     } else if (EPI == EPI_RES) {
@@ -393,7 +408,7 @@ constexpr int kDgBN = 256, kDgBK = 64, kDgStages = 3, kDgXcds = 8, kDgGroupRows 
 // activation rows per workgroup: 128 for MXFP4 (each decoded weight fragment feeds eight MFMAs; a 75 KiB ring, two
 // workgroups a CU), 64 for the 8-bit formats (whose 64-byte weight rows would make a 128-row ring 99 KiB: one a CU)
 template <int F>
-constexpr int dg_bm() { return F == WF_MXFP4 ? 128 : 64; }
+constexpr int dg_bm() { return axk::is_fp4(F) ? 128 : 64; }
 template <int F>
 constexpr int dg_mt() { return dg_bm<F>() / 16; }  // 16-row MFMA tiles per wave (a wave spans every row of the tile)
 template <int F>
@@ -402,10 +417,12 @@ template <int F>
 constexpr int dg_astage() { return dg_bm<F>() * kDgBK * 2; }
 constexpr int64_t kDgMinRows = 128;  // below this the group kernel (weights streamed once per 16 / 32 rows) is faster
 template <int F>
-constexpr int dg_row_bytes() { return F == WF_MXFP4 ? kDgBK / 2 : kDgBK; }  // weight bytes per row and step
+constexpr int dg_row_bytes() { return axk::is_fp4(F) ? kDgBK / 2 : kDgBK; }  // weight bytes per row and step
 constexpr int kDgSStage = kDgBN * 4;  // MX formats: one scale dword per weight row and step
 template <int F>
-constexpr int dg_stage() { return dg_astage<F>() + kDgBN * dg_row_bytes<F>() + (axk::is_mx(F) ? kDgSStage : 0); }
+constexpr int dg_stage() {
+  return dg_astage<F>() + kDgBN * dg_row_bytes<F>() + (axk::has_block_scales(F) ? kDgSStage : 0);
+}
 template <int F>
 size_t dg_lds_bytes(int64_t) {
   return (size_t)kDgStages * dg_stage<F>();
@@ -418,6 +435,7 @@ struct DgArgs {
   const uint8_t* ws[AXK_MX_GROUP_MAX];  // E8M0 scales [n, k/32] (MX formats)
   const float* col_scale[AXK_MX_GROUP_MAX];
   const float* bias[AXK_MX_GROUP_MAX];
+  const float* gscale[AXK_MX_GROUP_MAX];  // NVFP4 scale2
   void* out[AXK_MX_GROUP_MAX];
   int64_t ldo[AXK_MX_GROUP_MAX];
   int n[AXK_MX_GROUP_MAX];
@@ -432,9 +450,10 @@ struct DgArgs {
 
 template <int F>
 AXK_DEV axk_bf16x8 dg_decode(const unsigned char* row, int kh, int g4, int r, float sc) {
-  if constexpr (F == WF_MXFP4) {
+  if constexpr (axk::is_fp4(F)) {
     const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 16 * (kh ^ ((r >> 3) & 1)) + 4 * g4);
-    return fp4x8_to_bf16x8(w, sc);
+    if constexpr (F == axk::WF_NVFP4) return fp4x8_to_bf16x8_mul(w, sc);
+    else return fp4x8_to_bf16x8(w, sc);
   } else {
     // 8 bytes (k = 32 kh + 8 g4 ..) of the 64-byte row: chunk 2 kh + g4 / 2, half g4 % 2
     const int c = (2 * kh + (g4 >> 1)) ^ ((r >> 2) & 3);
@@ -473,7 +492,8 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
   auto wrow = [&](int rho, bool scale) -> const uint8_t* {
     const int mi = EPI == EPI_SWIGLU ? (rho >= COLS ? 1 : 0) : mat;
     const int c = min(col0 + (EPI == EPI_SWIGLU ? (rho & (COLS - 1)) : rho), N - 1);
-    return scale ? g.ws[mi] + (int64_t)c * (K / 32) : g.w[mi] + (int64_t)c * axk::row_bytes<F>(K);
+    return scale ? g.ws[mi] + (int64_t)c * (K / (axk::is_nv(F) ? 16 : 32))
+                 : g.w[mi] + (int64_t)c * axk::row_bytes<F>(K);
   };
   // per-lane sources of this wave's direct loads of a step: A instructions i = kDgAI wave + h (rows 8 i + lane / 8,
   // chunk (lane % 8) ^ (row & 7)); B instructions (RB == 32: 2 per wave, 32 rows each; RB == 64: 4 per wave,
@@ -506,7 +526,8 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
   // the E8M0 bytes of a step (MX formats) join the direct loads: wave w loads the aligned dword holding blocks
   // 4 (ks / 2) .. + 3 of weight rows 64 w + lane into the slot's scale table [256 rows][4 B], so no whole-K scale
   // table takes LDS (which then fits several workgroups a CU) and the loop has no load the compiler waits on
-  const uint8_t* ssrc = axk::is_mx(F) ? wrow(64 * wave + lane, true) : nullptr;
+  // (NVFP4: the dword holding the step's four 16-value blocks)
+  const uint8_t* ssrc = axk::has_block_scales(F) ? wrow(64 * wave + lane, true) : nullptr;
   // step ks into ring slot BUF (past the last step the last one again: in bounds, unused), so every iteration
   // waits on the same count
   auto issue = [&](int ks, auto buf_c) __attribute__((always_inline)) {
@@ -519,8 +540,9 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
     for (int h = 0; h < BI; ++h) lds_dma16_cached(bsrc[h] + kk * RB, base + kDgAStage + (BI * wave + h) * 1024);
     if constexpr (axk::is_mx(F))
       lds_dma4_cached(ssrc + 4 * (kk >> 1), base + kDgAStage + kDgBN * RB + 256 * wave);
+    if constexpr (axk::is_nv(F)) lds_dma4_cached(ssrc + 4 * kk, base + kDgAStage + kDgBN * RB + 256 * wave);
   };
-  constexpr int LPS = kDgAI + BI + (axk::is_mx(F) ? 1 : 0);  // vector-memory instructions per step
+  constexpr int LPS = kDgAI + BI + (axk::has_block_scales(F) ? 1 : 0);  // vector-memory instructions per step
   issue(0, std::integral_constant<int, 0>{});
   issue(1, std::integral_constant<int, 1>{});
   axk_f32x4 acc[kDgMT][4];
@@ -544,7 +566,9 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = brow[j] + l16;
-        const float sc = axk::is_mx(F) ? e8m0_to_f32(sb[kDgBN * RB + 4 * r + 2 * (ks & 1) + kh]) : 1.0f;
+        const float sc = axk::is_mx(F)   ? e8m0_to_f32(sb[kDgBN * RB + 4 * r + 2 * (ks & 1) + kh])
+                         : axk::is_nv(F) ? e4m3_to_f32(sb[kDgBN * RB + 4 * r + 2 * kh + (g4 >> 1)])
+                                         : 1.0f;
         bf[j] = dg_decode<F>(sb + r * RB, kh, g4, r, sc);
       }
 #pragma unroll
@@ -570,6 +594,7 @@ __global__ __launch_bounds__(256, 2) void mx_gemm_kernel(DgArgs g) {
   auto fin = [&](int mi, int nn, int m, float v) {
     if (g.row_scale) v *= g.row_scale[m];
     if (g.col_scale[mi]) v *= g.col_scale[mi][nn];
+    if (g.gscale[mi]) v *= *g.gscale[mi];
     if (g.bias[mi]) v += g.bias[mi][nn];
     return v;
   };
@@ -666,6 +691,10 @@ bool dg_fits(int64_t m, int64_t k, const AxkConvEpi* conv, const MxGroup& g) {
       for (int i = 0; i < g.count; ++i)
         if (!axk_aligned(g.ws[i], 4)) return false;
     }
+    if constexpr (axk::is_nv(F)) {  // each step's scales one aligned dword of the row (K / 16 bytes, K % 64 == 0)
+      for (int i = 0; i < g.count; ++i)
+        if (!axk_aligned(g.ws[i], 4)) return false;
+    }
     return true;
   }
 }
@@ -693,6 +722,7 @@ int dg_group(const uint16_t* a, int64_t lda, const MxGroup& g, int epi, int64_t 
   d.cb0[0] = 0;
   for (int i = 0; i < g.count; ++i) {
     d.w[i] = g.w[i], d.ws[i] = g.ws[i], d.col_scale[i] = g.col_scale[i], d.bias[i] = g.bias[i];
+    d.gscale[i] = g.gscale[i];
     d.out[i] = g.out[i], d.ldo[i] = g.ldo[i], d.n[i] = g.n[i];
     d.cb0[i + 1] = d.cb0[i] + (g.n[i] + kDgBN - 1) / kDgBN;
   }
@@ -745,9 +775,12 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i) {
     const AxkMxMat& p = mats[i];
-    AXK_REQUIRE(p.w && p.out && (!axk::is_mx(F) || p.ws), AXK_E_NULL);
+    AXK_REQUIRE(p.w && p.out && (!axk::has_block_scales(F) || p.ws) && (!axk::is_nv(F) || p.gscale), AXK_E_NULL);
     AXK_REQUIRE(p.n > 0 && p.n <= INT32_MAX && p.ldo >= p.n, AXK_E_SHAPE);
-    AXK_REQUIRE(axk_aligned(p.w, 16) && (!axk::is_mx(F) || axk_aligned(p.ws, F == axk::WF_MXFP4 ? 8 : 4)),
+    AXK_REQUIRE(axk_aligned(p.w, 16) &&
+                    (!axk::has_block_scales(F) ||
+                     axk_aligned(p.ws, axk::is_nv(F) ? 16 : F == axk::WF_MXFP4 ? 8 : 4)) &&
+                    (!axk::is_nv(F) || axk_aligned(p.gscale, 4)),
                 AXK_E_ALIGN);
     const size_t o_bytes = m > 0 ? (size_t)((m - 1) * p.ldo + p.n) * esz : 0;
     AXK_REQUIRE(!axk_overlap(p.out, o_bytes, a, a_bytes), AXK_E_ALIAS);
@@ -760,6 +793,7 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
     g.ws[i] = p.ws;
     g.col_scale[i] = p.col_scale;
     g.bias[i] = p.bias;
+    g.gscale[i] = p.gscale;
     g.out[i] = p.out;
     g.ldo[i] = p.ldo;
     g.n[i] = (int)p.n;
@@ -779,9 +813,10 @@ int mx_group(const uint16_t* a, int64_t lda, const AxkMxMat* mats, int count, in
 template <int F>
 int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_t* ws, const float* row_scale,
                   const float* col_scale, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
-                  int64_t k, axk_stream_t stream) {
+                  int64_t k, axk_stream_t stream, const float* gscale = nullptr) {
   AXK_REQUIRE(a && w && out, AXK_E_NULL);
-  AXK_REQUIRE(!axk::is_mx(F) || ws, AXK_E_NULL);
+  AXK_REQUIRE(!axk::has_block_scales(F) || ws, AXK_E_NULL);
+  AXK_REQUIRE(!axk::is_nv(F) || gscale, AXK_E_NULL);
   AXK_REQUIRE(m >= 0 && n >= 0 && k > 0 && k % 32 == 0, AXK_E_SHAPE);
   AXK_REQUIRE(m <= INT32_MAX && n <= INT32_MAX, AXK_E_SHAPE);
   AXK_REQUIRE(lda >= k && lda % 8 == 0, AXK_E_ALIGN);
@@ -795,8 +830,9 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   hipStream_t st = axk_stream(stream);
   // staged group kernel when rows are whole 128-byte segments (and scale rows 8-byte (MXFP4) / 4-byte (MXFP8)
   // aligned)
-  if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 && (!axk::is_mx(F) || axk_aligned(ws, F == WF_MXFP4 ? 8 : 4))) {
-    const AxkMxMat mat{w, ws, col_scale, bias, out, n, n};
+  if (axk::row_bytes<F>(k) % axk::kSegBytes == 0 &&
+      (!axk::has_block_scales(F) || axk_aligned(ws, axk::is_nv(F) ? 16 : F == WF_MXFP4 ? 8 : 4))) {
+    const AxkMxMat mat{w, ws, col_scale, bias, out, n, n, gscale};
     return mx_group<F>(a, lda, &mat, 1, EPI_PLAIN, nullptr, 0, row_scale, out_dtype, m, k, nullptr, st);
   }
   constexpr int CH = 4 * WUnit<F>::V;
@@ -807,11 +843,11 @@ int launch_linear(const uint16_t* a, int64_t lda, const uint8_t* w, const uint8_
   dim3 block(64 * waves);
   const int of32 = out_dtype == AXK_DT_F32;
   if (mt == 1)
-    hipLaunchKernelGGL((mx_linear_kernel<F, 1>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, out,
-                       of32, (int)m, (int)n, k);
+    hipLaunchKernelGGL((mx_linear_kernel<F, 1>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, gscale,
+                       out, of32, (int)m, (int)n, k);
   else
-    hipLaunchKernelGGL((mx_linear_kernel<F, 2>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, out,
-                       of32, (int)m, (int)n, k);
+    hipLaunchKernelGGL((mx_linear_kernel<F, 2>), grid, block, 0, st, a, lda, w, ws, row_scale, col_scale, bias, gscale,
+                       out, of32, (int)m, (int)n, k);
   return axk_launch_status();
 }
 
@@ -826,6 +862,8 @@ int axk_mx_group(int fmt, const uint16_t* a, int64_t lda, const AxkMxMat* mats, 
     return mx_group<WF_MXFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   if (fmt == AXK_MX_MXFP8)
     return mx_group<axk::WF_MXFP8>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
+  if (fmt == AXK_MX_NVFP4)
+    return mx_group<axk::WF_NVFP4>(a, lda, mats, count, epi, res, ldr, row_scale, out_dtype, m, k, conv, stream);
   return AXK_E_DTYPE;
 }
 
@@ -848,6 +886,15 @@ extern "C" int axk_mxfp4_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_f
                               const float* bias, void* out, int out_dtype, int64_t m, int64_t n, int64_t k,
                               axk_stream_t stream) {
   return launch_linear<WF_MXFP4>(a, lda, b_fp4, b_scale, nullptr, nullptr, bias, out, out_dtype, m, n, k, stream);
+}
+
+extern "C" int axk_nvfp4_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp4, const uint8_t* b_scale,
+                              const float* b_scale2, const float* bias, void* out, int out_dtype, int64_t m,
+                              int64_t n, int64_t k, axk_stream_t stream) {
+  AXK_REQUIRE(b_scale2, AXK_E_NULL);
+  AXK_REQUIRE(axk_aligned(b_scale2, 4), AXK_E_ALIGN);
+  return launch_linear<axk::WF_NVFP4>(a, lda, b_fp4, b_scale, nullptr, nullptr, bias, out, out_dtype, m, n, k, stream,
+                                      b_scale2);
 }
 
 extern "C" int axk_fp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const float* scale_a,

@@ -259,6 +259,60 @@ class LmHeadWorkload(Workload):
                           f"scaled by rows"}
 
 
+class LmHeadNvfp4Workload(Workload):
+    """The LM head in NVFP4 (the reference's NVFP4 head, test_nvfp4_lm_head.py; nvfp4_gemm, gemm.py:495-561):
+    W [248320, 2048] E2M1 pairs with E4M3 scales per 16 along K and an fp32 scale2, x bf16 [1, 2048], fp32 logits.
+    Each code is decoded at scale 1 and multiplied by its block's E4M3 scale in fp32 (gfx950's scaled converts take
+    only a power of two), so the decode costs more VALU than the MXFP4 head's."""
+
+    name = "lm_head_nvfp4"
+    tokens = 1  # tokens one step carries through the path
+    kernel = "mx_group_kernel<5, 1, 4, 0, 4>"
+    timing = "graph"
+    traffic_profile = "lm_head_nvfp4_vocab248320_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        from axk import configs
+
+        self.m, self.n, self.k = 1, configs.LM_HEAD["vocab"], configs.LM_HEAD["hidden"]
+        per_copy = self.n * self.k // 2 + self.n * self.k // 16
+        # algorithmic bytes per launch: codes + E4M3 scales + scale2 + x + fp32 logits
+        self.alg_bytes = per_copy + 4 + 2 * self.m * self.k + 4 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        self.copies = max(2, -(-ROTATE_BYTES // per_copy))
+        c = [configs.lm_head_nvfp4_case(dev, seed=i) for i in range(self.copies)]
+        self.w, self.s, self.s2, self.x = [ci["w"] for ci in c], [ci["s"] for ci in c], c[0]["s2"], c[0]["x"]
+        self.out = torch.empty(self.m, self.n, dtype=torch.float32, device=dev)
+        self.config = {"workload": f"NVFP4 LM head GEMV N={self.n} K={self.k} M=1, fp32 logits",
+                       "rotating_copies": self.copies}
+        self.dtype = "nvfp4 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import torch
+
+        import axk
+
+        j = i % self.copies
+        axk.nvfp4_gemm(self.x, self.w[j], self.s[j], self.s2, out_dtype=torch.float32, output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import mx
+
+        rows = 4096  # a bounded sample of the vocabulary's rows, scaled to the whole head
+        x = self.x.cpu()
+        w, s, s2 = self.w[0][:rows].cpu().numpy(), self.s[0][:rows].cpu().numpy(), self.s2.item()
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        sec, reps = _time_cpu(lambda: mx.nvfp4_linear(x, w, s, s2))
+        return {"value": sec * 1e6 * self.n / rows, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"{rows} of the {self.n} rows (oracle/mx.py: numpy dequant + torch fp32 matmul), median of "
+                          f"{reps} runs, scaled by rows"}
+
+
 class PagedDecodeWorkload(Workload):
     """Config 1: paged decode attention, batch 16, 16 q / 2 KV heads, D 256, page 64, L_b ~ U[1024, 16384].
 
@@ -1291,7 +1345,7 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              MoeDecodeWorkload.name: MoeDecodeWorkload, MoePrefillWorkload.name: MoePrefillWorkload,
              MxDequantWorkload.name: MxDequantWorkload, Fp8LinearWorkload.name: Fp8LinearWorkload,
              KvWriteWorkload.name: KvWriteWorkload, GroupDecodeWorkload.name: GroupDecodeWorkload,
-             LmHeadWorkload.name: LmHeadWorkload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload, PagedDecodeI8Workload.name: PagedDecodeI8Workload,
+             LmHeadWorkload.name: LmHeadWorkload, LmHeadNvfp4Workload.name: LmHeadNvfp4Workload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload, PagedDecodeI8Workload.name: PagedDecodeI8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
              MxLinearPrefillWorkload.name: MxLinearPrefillWorkload, MoeLayerPrefillWorkload.name: MoeLayerPrefillWorkload,
              MoeGroupDecodeWorkload.name: MoeGroupDecodeWorkload,

@@ -159,6 +159,20 @@ int axk_fp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const flo
 int axk_mxfp8_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp8, const uint8_t* b_scale, int fp8_dtype,
                    const float* bias, void* out, int out_dtype, int64_t m, int64_t n, int64_t k, axk_stream_t stream);
 
+/* NVFP4 GEMM: output = a @ dequant(b_fp4, b_scale, b_scale2).T + bias, fp32 accumulation, where
+ * dequant(w)[n, k] = E2M1(code[n, k]) * E4M3(b_scale[n, k / 16]) * b_scale2[0]. Replaces sgl_kernel_axera.gemm.nvfp4_gemm
+ * (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/gemm.py:495-561) on weights packed by quantize_nvfp4
+ * (sgl_kernel_axera/quantization.py:8-37), the NVFP4 projections of q35_mx_build.py:168-200.
+ *   a         bf16 [m, k] (row stride lda elements, lda % 8 == 0)
+ *   b_fp4     u8   [n, k/2]: E2M1 pairs, low nibble = even k (the reference's packed layout)
+ *   b_scale   u8   [n, k/16]: E4M3 block scales
+ *   b_scale2  f32  [1] in device memory (a runtime input, as the reference keeps it)
+ *   bias f32 [n] or NULL; out bf16 / f32 [m, n]; k % 32 == 0; a, b_fp4 16-byte aligned.
+ * Each code times its block scale is exact in bf16; b_scale2 multiplies the fp32 sums. */
+int axk_nvfp4_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp4, const uint8_t* b_scale,
+                   const float* b_scale2, const float* bias, void* out, int out_dtype, int64_t m, int64_t n,
+                   int64_t k, axk_stream_t stream);
+
 /* Dense bf16-weight linear (router logits and other small bf16 projections):
  * output = a @ b.T + bias, fp32 accumulation. Replaces sgl_kernel_axera.gemm.fp16_gemm / bf16_gemm
  * (gemm.py:81-116, 469-476). a bf16 [m, k]; b bf16 [n, k]; k % 32 == 0. */

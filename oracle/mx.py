@@ -12,11 +12,19 @@ Restates
   * quant_mxfp8 / dequant    models/qwen35_35b_a3b/src/70b0fbc/q35_mx_build.py:60-72 (E4M3 codes, one E8M0 per 32
                              along K, e = ceil(log2(amax / 448)) so nothing saturates); E5M2 codes as the other
                              MXFP8 element type sgl's mxfp8_gemm accepts (gemm.py:644-659)
+  * quantize_nvfp4 / dequant  models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/quantization.py:8-37 (scale2 =
+                             amax / (448 * 6) or 1; E4M3 block scales per 16 along K = clamp(block amax / (6 scale2),
+                             448) rounded to nearest even; codes = E2M1 of value / (scale * scale2), nearest with ties
+                             to the even code, saturating at 6, the sign kept for values that round to zero);
+                             the decode of models/qwen35_35b_a3b/sgl/tests/test_nvfp4_lm_head.py:11-16
+  * NVFP4 linear             sgl_kernel_axera/gemm.py:495-561 (a @ dequant(w).T + bias, fp32 acc)
 Pinned by tests/test_oracle_mx.py: exhaustive 16 x 256 code/scale table against the closed form and
 torch's float8_e8m0fnu / exp2, E4M3 and E5M2 tables against torch.float8_e4m3fn / float8_e5m2, the
 MXFP8 dequant against a float64 bit-field decode for every (code, scale) pair, the MXFP8 quantiser's
 scale rule and nearest-code choice against a brute-force search over all 256 codes, the C restatement
-(oracle/mx_codec.c) against this module, quantiser brute force + round trip, and the linears
+(oracle/mx_codec.c) against this module, quantiser brute force + round trip, the NVFP4 codec against the reference
+test's vectors (its midpoint row, zero blocks, an all-zero matrix) and its E2M1 choice against a brute-force
+nearest-value search, the NVFP4 dequant against a float64 decode of every (code, scale) pair, and the linears
 against float64 dot products.
 """
 from __future__ import annotations
@@ -175,6 +183,63 @@ def fp8_linear(a: torch.Tensor, w_fp8: np.ndarray, scale_a, scale_b, bias=None) 
     if scale_a is not None:
         x = x * torch.as_tensor(scale_a, dtype=torch.float32).reshape(-1, 1)
     out = x @ w.T
+    if bias is not None:
+        out = out + bias.float().cpu()
+    return out
+
+
+NV_GROUP = 16  # NVFP4 block size along K
+
+
+def e2m1_code(x: np.ndarray) -> np.ndarray:
+    """fp32 values -> E2M1 codes (u8): the magnitude to the nearest of 0, 0.5, 1, 1.5, 2, 3, 4, 6 (beyond 6: 6), a
+    tie between two neighbours to the even code; bit 3 the sign of x, kept for values that round to zero (the
+    reference's expected codes turn -0.25 into 8, test_nvfp4_lm_head.py:21-31)."""
+    x = np.asarray(x, dtype=np.float32)
+    mag = np.abs(x).astype(np.float64)
+    d = np.abs(mag[..., None] - E2M1.astype(np.float64))
+    best = d.min(-1, keepdims=True)
+    tied = d == best
+    idx = np.arange(8)
+    even = np.where(tied & (idx % 2 == 0), idx, 8).min(-1)
+    code = np.where(even < 8, even, np.argmax(tied, -1))
+    return (code | (np.signbit(x).astype(np.int64) << 3)).astype(np.uint8)
+
+
+def quantize_nvfp4(w) -> tuple[np.ndarray, np.ndarray, np.float32]:
+    """[N, K] (K % 16 == 0) -> (packed E2M1 u8 [N, K/2] (even k in the low nibble), E4M3 scale bytes u8 [N, K/16],
+    fp32 scale2) by the rule of quantization.py:8-37: scale2 = fp32(amax / 2688) (1 for an all-zero matrix); each
+    block's scale = E4M3(min(fp32(block amax / fp32(6 scale2)), 448)) by torch's round-to-nearest-even cast; the
+    values divided by fp32(scale * scale2) (by 1 where that is 0) and coded by e2m1_code."""
+    t = torch.as_tensor(np.asarray(w, dtype=np.float32))
+    n, k = t.shape
+    assert k % NV_GROUP == 0
+    amax = float(t.abs().max()) if t.numel() else 0.0
+    s2 = np.float32(amax / (448 * 6) if amax else 1.0)
+    blocks = t.reshape(n, k // NV_GROUP, NV_GROUP)
+    six_s2 = np.float32(6.0) * s2
+    sc = torch.clamp(blocks.abs().amax(-1) / torch.tensor(six_s2), max=448.0).to(torch.float8_e4m3fn)
+    dec = sc.float() * torch.tensor(s2)
+    scaled = blocks / torch.where(dec > 0, dec, torch.ones_like(dec)).unsqueeze(-1)
+    codes = e2m1_code(scaled.reshape(n, k).numpy())
+    return pack_fp4_codes(codes), sc.view(torch.uint8).numpy(), s2
+
+
+def dequant_nvfp4(packed: np.ndarray, scales: np.ndarray, scale2) -> np.ndarray:
+    """packed u8 [N, K/2] + E4M3 scale bytes u8 [N, K/16] + fp32 scale2 -> fp32 [N, K]: value(code) * scale * scale2
+    in that order (test_nvfp4_lm_head.py:11-16)."""
+    codes = unpack_fp4_codes(np.asarray(packed, dtype=np.uint8))
+    n, k = codes.shape
+    v = FP4_LUT[codes].reshape(n, k // NV_GROUP, NV_GROUP)
+    s = e4m3_table()[np.asarray(scales, dtype=np.uint8)].reshape(n, k // NV_GROUP, 1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return ((v * s) * np.float32(scale2)).reshape(n, k).astype(np.float32)
+
+
+def nvfp4_linear(a: torch.Tensor, packed: np.ndarray, scales: np.ndarray, scale2, bias=None) -> torch.Tensor:
+    """a[M, K] @ dequant_nvfp4(packed, scales, scale2).T (+ bias) in fp32 (sgl nvfp4_gemm, gemm.py:495-561)."""
+    w = torch.from_numpy(dequant_nvfp4(packed, scales, scale2))
+    out = a.float().cpu() @ w.T
     if bias is not None:
         out = out + bias.float().cpu()
     return out

@@ -220,3 +220,90 @@ def test_mxfp8_config4_projections(dev, n, k):
     got = axk.mxfp8_gemm(a.to(dev), torch.from_numpy(codes).to(dev), torch.from_numpy(scales).to(dev), fmt="e4m3")
     ref = mx.mxfp8_linear(a, codes, scales, "e4m3")
     torch.testing.assert_close(got.float().cpu(), ref.to(torch.bfloat16).float(), **BF16_TOL)
+
+
+# ---- NVFP4 (E2M1 pairs + E4M3 per 16 along K + an fp32 scale2): sgl nvfp4_gemm (gemm.py:495-561) ----
+def _nvfp4_weight(n, k, g, lo=0x20, hi=0x50):
+    """Uniform nibbles and E4M3 scale bytes in lo .. hi - 1 (normal positive scales 2^-3 .. 2^2)."""
+    codes = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8).numpy()
+    scales = torch.randint(lo, hi, (n, k // 16), generator=g, dtype=torch.uint8).numpy()
+    return mx.pack_fp4_codes(codes), scales
+
+
+def test_nvfp4_decode_bit_exact_through_identity(dev):
+    """out = I @ dequant(W)^T = dequant(W)^T exactly (one product per output, fp32 out, scale2 1): every code at every
+    finite positive E4M3 scale byte (0x01 .. 0x7e) through the decode and the scale multiply, on the staged group
+    kernel (k = 256) and the unstaged one (k = 160: rows of 80 bytes); gfx950's scaled converts would apply only the
+    scale's exponent, so a non-power-of-two scale exposes that mistake."""
+    for k in (256, 160):
+        n = 126
+        codes = np.resize(np.arange(16, dtype=np.uint8), (n, k))
+        codes = np.roll(codes, 5, axis=1)
+        scales = (1 + (np.arange(n * k // 16).reshape(n, k // 16) * 37) % 126).astype(np.uint8)
+        packed = mx.pack_fp4_codes(codes)
+        eye = torch.eye(k, dtype=torch.bfloat16)
+        one = torch.ones(1, device=dev)
+        got = axk.nvfp4_gemm(eye.to(dev), torch.from_numpy(packed).to(dev), torch.from_numpy(scales).to(dev), one,
+                             out_dtype=torch.float32).cpu().numpy()
+        want = mx.dequant_nvfp4(packed, scales, np.float32(1)).T
+        zero = want == 0
+        assert (got[zero] == 0).all()
+        assert _bits_equal(got[~zero], want[~zero]), f"k={k}"
+
+
+# decode shapes on the staged group kernel (k a multiple of 256), rows of 80 / 48 bytes on the unstaged kernel, and
+# m >= 128 on the prefill GEMM (k a multiple of 64)
+@pytest.mark.parametrize("m,n,k", [(1, 16, 256), (1, 4096, 2048), (4, 1000, 2048), (16, 512, 512), (33, 300, 1024),
+                                   (1, 100, 160), (5, 64, 96), (128, 512, 1024), (300, 1000, 2048), (200, 64, 320)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_nvfp4_gemm_matches_oracle(dev, m, n, k, out_dtype):
+    g = torch.Generator().manual_seed(9000 * m + n + k)
+    packed, scales = _nvfp4_weight(n, k, g)
+    s2 = np.float32(0.0371)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g) / 8
+    print(f"nvfp4 m={m} n={n} k={k} {out_dtype}", flush=True)
+    got = axk.nvfp4_gemm(a.to(dev), torch.from_numpy(packed).to(dev), torch.from_numpy(scales).to(dev),
+                         torch.tensor([s2], device=dev), out_dtype=out_dtype, bias=bias.to(dev)).cpu()
+    ref = mx.nvfp4_linear(a, packed, scales, s2, bias=bias.to(out_dtype).float())
+    torch.testing.assert_close(got.float(), ref.to(out_dtype).float(), **(BF16_TOL if out_dtype == torch.bfloat16 else F32_TOL))
+
+
+def test_nvfp4_gemm_runtime_scale2_and_quantized_weights(dev):
+    """Weights from the host codec (axk.quantize_nvfp4): the product within the bf16 bar of the oracle on the same
+    codes; scale2 is a runtime input: doubling it doubles every fp32 output exactly (as the reference's test rescales
+    it without repacking, test_nvfp4_lm_head.py:55-60)."""
+    g = torch.Generator().manual_seed(93)
+    w = torch.randn(513, 1024, generator=g) * 0.1
+    packed, scales, s2 = axk.quantize_nvfp4(w)
+    a = torch.randn(17, 1024, generator=g).bfloat16()
+    pd, sd, s2d = packed.to(dev), scales.to(dev), s2.to(dev)
+    got = axk.nvfp4_gemm(a.to(dev), pd, sd, s2d, out_dtype=torch.float32)
+    ref = mx.nvfp4_linear(a, packed.view(torch.uint8).numpy(), scales.view(torch.uint8).numpy(), s2.item())
+    torch.testing.assert_close(got.cpu(), ref, **F32_TOL)
+    twice = axk.nvfp4_gemm(a.to(dev), pd, sd, s2d * 2, out_dtype=torch.float32)
+    assert torch.equal(twice, got * 2)
+
+
+def test_nvfp4_lm_head_vocab_gemv(dev):
+    """The NVFP4 LM head at the full vocabulary (248320 x 2048, fp32 logits), M = 1 and 4, against an fp32 matmul
+    on the GPU over the dequantised weight (torch ops on the codes, scales and scale2), and a slice of rows against
+    the CPU oracle."""
+    c = configs.lm_head_nvfp4_case(dev, seed=5, m=4)
+    lut = torch.tensor(mx.FP4_LUT, device=dev)
+    p = c["w"]
+    codes = torch.stack([p & 15, p >> 4], -1).reshape(p.shape[0], -1).long()
+    sc = c["s"].view(torch.float8_e4m3fn).float().repeat_interleave(16, -1)
+    wf = (lut[codes] * sc) * c["s2"]
+    del codes, sc
+    for m in (1, 4):
+        x = c["x"][:m].contiguous()
+        got = axk.nvfp4_gemm(x, c["w"], c["s"], c["s2"], out_dtype=torch.float32)
+        ref = (wf @ x.float().t().contiguous()).t()
+        torch.testing.assert_close(got, ref, **BF16_TOL)
+    del wf
+    rows = 3000
+    got = axk.nvfp4_gemm(c["x"][:1].contiguous(), c["w"][:rows], c["s"][:rows], c["s2"], out_dtype=torch.float32)
+    ref = mx.nvfp4_linear(c["x"][:1].cpu(), c["w"][:rows].cpu().numpy(), c["s"][:rows].cpu().numpy(),
+                          c["s2"].item())
+    torch.testing.assert_close(got.cpu(), ref, **F32_TOL)

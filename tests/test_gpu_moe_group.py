@@ -204,22 +204,23 @@ def test_moe_group_bound_from_the_manifest_runs_like_loose_tensors(dev):
                 assert _same(Lb[n], L[n])
 
 
-def test_moe_group_with_lm_head(dev):
+@pytest.mark.parametrize("fmt", ["mxfp4", "nvfp4"])
+def test_moe_group_with_lm_head(dev, fmt):
     """The group that ends the model carries the LM head (q35_group.py:442-452 with LMHEAD=1): the final norm and
-    the 35B's MXFP4 output projection (248320 x 2048, mul_mat_mx4_n248320_k2048) inside the step. The logits equal
-    the separate norm and GEMM calls on the step's output bit for bit, eager and graph-replayed; the normalised rows
-    and a slice of the logits against the oracle at the per-op bar."""
+    the 35B's output projection (248320 x 2048: MXFP4 as mul_mat_mx4_n248320_k2048, or NVFP4 as the reference's
+    NVFP4 head) inside the step. The logits equal the separate norm and GEMM calls on the step's output bit for bit,
+    eager and graph-replayed; the normalised rows and a slice of the logits against the oracle at the per-op bar."""
     from axk import glue
     from oracle import mx
 
     c = configs.moe_group(dev, batch=4, ctx=100, seed=7)
     cg = c["cfg"]
-    lm = configs.lm_head_case(dev, seed=8)
+    lm = configs.lm_head_case(dev, seed=8) if fmt == "mxfp4" else configs.lm_head_nvfp4_case(dev, seed=8)
     norm = 1.0 + 0.1 * torch.randn(cg["hidden"], generator=torch.Generator(device=dev).manual_seed(9), device=dev)
-    print(f"35B MoE group + LM head {lm['w'].shape[0]} x {cg['hidden']}, batch 4", flush=True)
+    print(f"35B MoE group + {fmt} LM head {lm['w'].shape[0]} x {cg['hidden']}, batch 4", flush=True)
     grp = group.DecodeGroup(c["layers"], cg["batch"], cg["hidden"], dev, cg["nk"], cg["nv"], cg["hq"], cg["rot"],
                             cg["eps"], "mxfp8", "mxfp8", attn=c["attn"],
-                            lm_head=dict(norm=norm, w=lm["w"], s=lm["s"], fmt="mxfp4"))
+                            lm_head=dict(norm=norm, w=lm["w"], s=lm["s"], s2=lm.get("s2"), fmt=fmt))
     wm = torch.zeros(c["layers"][3]["cache"].shape[0], c["layers"][3]["cache"].shape[2], dtype=torch.bool,
                      device=dev)
     wm[c["attn"]["loc"][:, 0].long(), c["attn"]["loc"][:, 1].long()] = True
@@ -227,14 +228,20 @@ def test_moe_group_with_lm_head(dev):
     out = grp.step(c["x"]).clone()
     logits = grp.logits.clone()
     hn = glue.rmsnorm(out, norm, cg["eps"])
-    sep = axk_gemm.mxfp4_gemm(hn, lm["w"], lm["s"], out_dtype=torch.float32)
+    if fmt == "mxfp4":
+        sep = axk_gemm.mxfp4_gemm(hn, lm["w"], lm["s"], out_dtype=torch.float32)
+    else:
+        sep = axk_gemm.nvfp4_gemm(hn, lm["w"], lm["s"], lm["s2"], out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert _same(grp.hn, hn) and _same(logits, sep)
     assert torch.isfinite(logits).all()
     ref_h = olayer.rmsnorm(out.cpu(), norm.cpu(), cg["eps"])
     torch.testing.assert_close(hn.float().cpu(), ref_h.float(), **TOL)
     rows = 3000
-    ref = mx.mx_linear(hn.cpu(), lm["w"][:rows].cpu().numpy(), lm["s"][:rows].cpu().numpy())
+    if fmt == "mxfp4":
+        ref = mx.mx_linear(hn.cpu(), lm["w"][:rows].cpu().numpy(), lm["s"][:rows].cpu().numpy())
+    else:
+        ref = mx.nvfp4_linear(hn.cpu(), lm["w"][:rows].cpu().numpy(), lm["s"][:rows].cpu().numpy(), lm["s2"].item())
     torch.testing.assert_close(logits[:, :rows].cpu(), ref.float(), **TOL)
     # graph-replayed from the same states: the same logits bit for bit
     grp.capture()

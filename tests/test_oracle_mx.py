@@ -258,3 +258,78 @@ def test_narrow_activations_break_the_parity_bar():
     codes, sc = mx.quant_mxfp8(x0.numpy(), "e4m3")
     got0 = (torch.from_numpy(mx.dequant_mxfp8(codes, sc, "e4m3")) @ w0.T).bfloat16().float()
     assert _outside_bar(x0 @ w0.T, got0) > 0.2
+
+
+# ---- NVFP4 (E2M1 codes, E4M3 scales per 16 along K, an fp32 scale2): quantization.py:8-37 ----
+def _e2m1_by_binade(x):
+    """E2M1 rounding restated per binade: the grid spacing is 0.5 below 2, 1 in [2, 4), 2 in [4, 6]; numpy's
+    round-half-even on the multiple of the spacing makes a tie go to the even mantissa, which is the even code;
+    past 6 the value saturates. Returns (code, value)."""
+    x = np.asarray(x, dtype=np.float64)
+    mag = np.abs(x)
+    step = np.where(mag < 2, 0.5, np.where(mag < 4, 1.0, 2.0))
+    val = np.minimum(np.round(mag / step) * step, 6.0)
+    code = np.searchsorted(mx.E2M1.astype(np.float64), val)
+    return (code | (np.signbit(x) << 3)).astype(np.uint8), np.where(np.signbit(x), -val, val)
+
+
+def test_nvfp4_reference_vectors():
+    """The reference test's own vectors (test_nvfp4_lm_head.py:19-39): a midpoint row, zero blocks, scale2 = 1."""
+    src = torch.zeros(3, 32, dtype=torch.bfloat16)
+    src[0, 0] = 448 * 6  # makes the global decode scale exactly one
+    src[1, :16] = torch.tensor([0, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, 6, -0.25, -0.75, -1.25, -1.75, -2.5, -3.5, -5])
+    packed, scales, s2 = mx.quantize_nvfp4(src.float().numpy())
+    assert packed.shape == (3, 16) and scales.shape == (3, 2) and s2 == np.float32(1)
+    expected = np.array([0, 0, 2, 2, 4, 4, 6, 6, 7, 8, 10, 10, 12, 12, 14, 14], dtype=np.uint8)
+    assert np.array_equal(packed[1, :8], expected[::2] | (expected[1::2] << 4))
+    assert not packed[2].any()
+    assert mx.e4m3_table()[scales[1, 0]] == 1 and not mx.e4m3_table()[scales[2]].any()
+    assert np.isfinite(mx.dequant_nvfp4(packed, scales, s2)).all()
+    zp, zs, z2 = mx.quantize_nvfp4(np.zeros((2, 16), np.float32))
+    assert z2 == np.float32(1) and not mx.dequant_nvfp4(zp, zs, z2).any()
+
+
+def test_e2m1_code_against_binade_rounding():
+    grid = mx.E2M1.astype(np.float64)
+    mids = (grid[:-1] + grid[1:]) / 2
+    g = np.random.default_rng(5)
+    x = np.concatenate([grid, mids, -grid, -mids, mids + 1e-6, mids - 1e-6, [6.5, 7.0, 1e6, -9.0],
+                        g.uniform(-7, 7, 4000)]).astype(np.float32)
+    code, val = _e2m1_by_binade(x)
+    assert np.array_equal(mx.e2m1_code(x), code)
+    assert np.array_equal(mx.FP4_LUT[code], val.astype(np.float32))
+
+
+def test_dequant_nvfp4_every_code_and_scale():
+    """Every (code, E4M3 scale byte) pair against a float64 decode of the two fields, times an fp32 scale2."""
+    codes = np.tile(np.arange(16, dtype=np.uint8), 256 * 2)  # 32 values per row: two 16-blocks
+    codes = np.tile(codes[:32], (256, 1))
+    packed = mx.pack_fp4_codes(codes)
+    scales = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 2, axis=1)
+    for s2 in (np.float32(1.0), np.float32(2.0 ** -9), np.float32(0.0371)):
+        got = mx.dequant_nvfp4(packed, scales, s2).astype(np.float64)
+        e4 = np.array([_fp8_closed_form(b, "e4m3") for b in range(256)])
+        v = np.array(REF_FP4_LUT, dtype=np.float64)[codes]
+        with np.errstate(invalid="ignore"):
+            want = ((v * e4[:, None]).astype(np.float32).astype(np.float64) * np.float64(s2)).astype(np.float32)
+        both_nan = np.isnan(got) & np.isnan(want)
+        assert np.array_equal(got[~both_nan], want.astype(np.float64)[~both_nan])
+
+
+def test_quantize_nvfp4_block_rule():
+    """Every block with a normal E4M3 scale codes its largest magnitude to 6 (the scale rounds within E4M3's relative
+    step of amax / 6, so the quotient lands above the 4 / 6 midpoint; blocks far below the matrix's amax get
+    subnormal or zero scales, the format's range limit), and each code is the nearest E2M1 value of the block's
+    quotient."""
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(8, 256, generator=g) * torch.logspace(-4, 2, 8)[:, None]).numpy()
+    packed, scales, s2 = mx.quantize_nvfp4(w)
+    codes = mx.unpack_fp4_codes(packed).reshape(8, 16, 16)
+    blocks = w.reshape(8, 16, 16)
+    top = np.abs(blocks).argmax(-1)
+    normal = ((scales >> 3) & 15) >= 1
+    assert normal.sum() >= 64 and (~normal).sum() >= 8  # both kinds of block occur
+    assert np.all((np.take_along_axis(codes, top[..., None], -1)[..., 0] & 7)[normal] == 7)
+    dec = (mx.e4m3_table()[scales].astype(np.float32) * s2).astype(np.float32)
+    q = (blocks / np.where(dec > 0, dec, np.float32(1))[..., None]).astype(np.float32)  # a zero scale divides by 1
+    assert np.array_equal(codes, _e2m1_by_binade(q)[0])
