@@ -146,6 +146,12 @@ _RESTYPES = {
 }
 
 
+class Nvfp4Scales(ctypes.Structure):
+    """axk_nvfp4_scales of include/axk.h: an NVFP4 weight's E4M3 block scales and fp32 scale2 (device pointers)."""
+
+    _fields_ = [("block_scales", ctypes.c_void_p), ("scale2", ctypes.c_void_p)]
+
+
 class MoeBlock(ctypes.Structure):
     """axk_moe_block of include/axk.h: the MoE block of the MoE decode layers (device pointers and sizes)."""
 

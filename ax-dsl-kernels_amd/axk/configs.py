@@ -195,6 +195,19 @@ def proj_weight(fmt: str, n: int, k: int, g: torch.Generator):
     return codes, torch.randint(119, 124, (n, k // 32), generator=g, dtype=torch.uint8)
 
 
+def _put(w: dict, name: str, fmt: str, n: int, k: int, g: torch.Generator) -> None:
+    """w_<name>, s_<name> (and t_<name> for "nvfp4") of an [n, k] weight in format fmt: proj_weight's draws, or for
+    NVFP4 uniform nibbles with E4M3 scale bytes uniform in 0x28 .. 0x37 (0.25 .. 0.47) and scale2 0.05, a weight RMS
+    of about 0.05 as the MXFP8 draws."""
+    if fmt == "nvfp4":
+        codes = torch.randint(0, 16, (n, k), generator=g, dtype=torch.uint8)
+        w["w_" + name] = pack_codes(codes).contiguous()
+        w["s_" + name] = torch.randint(0x28, 0x38, (n, k // 16), generator=g, dtype=torch.uint8)
+        w["t_" + name] = torch.tensor([0.05], dtype=torch.float32)
+    else:
+        w["w_" + name], w["s_" + name] = proj_weight(fmt, n, k, g)
+
+
 def _norm_w(n: int, g: torch.Generator):
     """A norm's run-time weight as the reference passes it: 1 + N(0, 0.1) (f32)."""
     return 1.0 + 0.1 * torch.randn(n, generator=g)
@@ -204,9 +217,9 @@ def mlp_weights(g: torch.Generator, hidden: int, inter: int, fmt: str = "mxfp4")
     """The dense MLP of a layer: gate / up [inter, hidden], down [hidden, inter] (MXFP4 by default, as config 0's
     draws)."""
     w = {}
-    w["w_gate"], w["s_gate"] = proj_weight(fmt, inter, hidden, g)
-    w["w_up"], w["s_up"] = proj_weight(fmt, inter, hidden, g)
-    w["w_down"], w["s_down"] = proj_weight(fmt, hidden, inter, g)
+    _put(w, "gate", fmt, inter, hidden, g)
+    _put(w, "up", fmt, inter, hidden, g)
+    _put(w, "down", fmt, hidden, inter, g)
     return w
 
 
@@ -217,15 +230,15 @@ def gdn_layer_weights(g: torch.Generator, hidden: int, inter: int, nk: int, nv: 
     mlp_fmt (MXFP4 by default)."""
     kd, vd = nk * 128, nv * 128
     w = {"ln1": _norm_w(hidden, g)}
-    w["w_qkv"], w["s_qkv"] = proj_weight(proj_fmt, 2 * kd + vd, hidden, g)
-    w["w_z"], w["s_z"] = proj_weight(proj_fmt, vd, hidden, g)
-    w["w_b"], w["s_b"] = proj_weight(proj_fmt, nv, hidden, g)
-    w["w_a"], w["s_a"] = proj_weight(proj_fmt, nv, hidden, g)
+    _put(w, "qkv", proj_fmt, 2 * kd + vd, hidden, g)
+    _put(w, "z", proj_fmt, vd, hidden, g)
+    _put(w, "b", proj_fmt, nv, hidden, g)
+    _put(w, "a", proj_fmt, nv, hidden, g)
     w["conv_w"] = (torch.randn(2 * kd + vd, conv_kernel, generator=g) * 0.5).to(torch.bfloat16)
     w["a_log"] = torch.randn(nv, generator=g) * 0.5
     w["dt_bias"] = torch.randn(nv, generator=g) * 0.5
     w["norm_w"] = _norm_w(128, g)
-    w["w_out"], w["s_out"] = proj_weight(proj_fmt, hidden, vd, g)
+    _put(w, "out", proj_fmt, hidden, vd, g)
     w["ln2"] = _norm_w(hidden, g)
     w.update(mlp_weights(g, hidden, inter, mlp_fmt))
     return w
@@ -236,12 +249,12 @@ def attn_layer_weights(g: torch.Generator, hidden: int, inter: int, hq: int, hkv
     """An attention decode layer's weights (names of q35_step.py attn_args): q (per head [q | gate]), k, v, o in
     proj_fmt (FP8 by default); f32 norms 1 + N(0, 0.1); the MLP in mlp_fmt (MXFP4 by default)."""
     w = {"ln1": _norm_w(hidden, g)}
-    w["w_q"], w["s_q"] = proj_weight(proj_fmt, hq * 2 * d, hidden, g)
-    w["w_k"], w["s_k"] = proj_weight(proj_fmt, hkv * d, hidden, g)
-    w["w_v"], w["s_v"] = proj_weight(proj_fmt, hkv * d, hidden, g)
+    _put(w, "q", proj_fmt, hq * 2 * d, hidden, g)
+    _put(w, "k", proj_fmt, hkv * d, hidden, g)
+    _put(w, "v", proj_fmt, hkv * d, hidden, g)
     w["q_norm"] = _norm_w(d, g)
     w["k_norm"] = _norm_w(d, g)
-    w["w_o"], w["s_o"] = proj_weight(proj_fmt, hidden, hq * d, g)
+    _put(w, "o", proj_fmt, hidden, hq * d, g)
     w["ln2"] = _norm_w(hidden, g)
     w.update(mlp_weights(g, hidden, inter, mlp_fmt))
     return w

@@ -7,6 +7,8 @@ s_<name>, in the format given by proj_fmt / mlp_fmt:
   "fp8"   (w u8 E4M3 [N, K], s f32 [N] per output channel)  - config 4's projections (sgl gemm.py:119-181)
   "mxfp8" (w u8 E4M3 [N, K], s u8 E8M0 [N, K/32])            - the 35B manifest (q35_mx_build.py:60-72)
   "mxfp4" (w u8 E2M1 pairs [N, K/2], s u8 E8M0 [N, K/32])    - the 9B / 27B manifests and config 4's MLP
+  "nvfp4" (w u8 E2M1 pairs [N, K/2], s u8 E4M3 [N, K/16], t_<name> f32 [1] scale2) - the WFMT=nv4 projections
+          (q35_mx_build.py:168-200; sgl quantize_nvfp4), passed to the C-ABI as an axk_nvfp4_scales per weight
 norms f32 (ln1, ln2, q_norm, k_norm as 1 + weight; norm_w raw). The workspace is allocated once by the caller
 (layer_workspace) and reused; a layer call allocates nothing.
 
@@ -27,7 +29,9 @@ GDN_WEIGHTS = ("ln1", "w_qkv", "s_qkv", "w_z", "s_z", "w_b", "s_b", "w_a", "s_a"
                "norm_w", "w_out", "s_out", "ln2")
 ATTN_WEIGHTS = ("ln1", "w_q", "s_q", "w_k", "s_k", "w_v", "s_v", "q_norm", "k_norm", "w_o", "s_o", "ln2")
 MLP_WEIGHTS = ("w_gate", "s_gate", "w_up", "s_up", "w_down", "s_down")
-WFMT = {"fp8": 0, "mxfp8": 1, "mxfp4": 2}  # AXK_WFMT_FP8_CHANNEL, AXK_WFMT_MXFP8, AXK_WFMT_MXFP4
+WFMT = {"fp8": 0, "mxfp8": 1, "mxfp4": 2, "nvfp4": 3}  # AXK_WFMT_FP8_CHANNEL, _MXFP8, _MXFP4, _NVFP4
+_PROJ_SCALES = {"s_qkv", "s_z", "s_b", "s_a", "s_out", "s_q", "s_k", "s_v", "s_o"}
+_MLP_SCALES = {"s_gate", "s_up", "s_down"}
 VORDER = {"grouped": 0, "tiled": 1}  # AXK_VORDER_GROUPED, AXK_VORDER_TILED
 
 
@@ -70,15 +74,48 @@ def tile_value_heads(w: dict, num_k_heads: int, num_v_heads: int, proj_fmt: str 
     rows("dt_bias", 1)
     for name, unit, start in (("s_qkv", 128, kd), ("s_z", 128, 0), ("s_b", 1, 0), ("s_a", 1, 0)):
         rows(name, unit, start)  # per-row scales: f32 [N] or E8M0 [N, K/32], rows as their weight's
-    out["w_out"] = v_tiled(w["w_out"], 1, nk, nv, 64 if proj_fmt == "mxfp4" else 128)
-    if proj_fmt != "fp8":  # E8M0 [H, VD / 32]: 4 scale columns per value head
-        out["s_out"] = v_tiled(w["s_out"], 1, nk, nv, 4)
+    out["w_out"] = v_tiled(w["w_out"], 1, nk, nv, 64 if proj_fmt in ("mxfp4", "nvfp4") else 128)
+    if proj_fmt != "fp8":  # E8M0 [H, VD / 32]: 4 scale columns per value head (NVFP4's E4M3 [H, VD / 16]: 8)
+        out["s_out"] = v_tiled(w["s_out"], 1, nk, nv, 8 if proj_fmt == "nvfp4" else 4)
     return out
 
 
 def _check(cond: bool, msg: str) -> None:
     if not cond:
         raise ValueError(msg)
+
+
+class _Nvfp4Scales:
+    """An NVFP4 weight's scales as the C-ABI takes them: an axk_nvfp4_scales (host memory) naming the E4M3 block scales
+    s_<name> [N, K/16] and the fp32 scale2 t_<name> [1]; it stands in the weight lists for the tensor s_<name>."""
+
+    def __init__(self, name: str, s: torch.Tensor, t: torch.Tensor):
+        _check(s.dtype in (torch.uint8, torch.float8_e4m3fn) and s.is_contiguous(),
+               f"{name} must be contiguous E4M3 bytes [N, K/16]")
+        _check(t.dtype == torch.float32 and t.numel() == 1 and t.device == s.device,
+               f"t_{name[2:]} must be one float32 on {s.device}")
+        self.s, self.t, self.device = s, t, s.device
+        self.st = _lib.Nvfp4Scales(s.data_ptr(), t.data_ptr())
+
+    def data_ptr(self) -> int:
+        return ctypes.addressof(self.st)
+
+    def is_contiguous(self) -> bool:
+        return True
+
+
+def _nv_weights(w: dict, proj_fmt: str, mlp_fmt: str) -> dict:
+    """w with each NVFP4 weight's s_<name> replaced by its _Nvfp4Scales (s_<name> and t_<name> together)."""
+    if "nvfp4" not in (proj_fmt, mlp_fmt):
+        return w
+    out = dict(w)
+    for n in w:
+        fmt = proj_fmt if n in _PROJ_SCALES else mlp_fmt if n in _MLP_SCALES else None
+        if fmt == "nvfp4":
+            t = w.get("t_" + n[2:])
+            _check(t is not None, f"the NVFP4 weight w_{n[2:]} needs its scale2 t_{n[2:]}")
+            out[n] = _Nvfp4Scales(n, w[n], t)
+    return out
 
 
 def _weights(w: dict, names) -> list:
@@ -169,6 +206,7 @@ def gdn_layer_decode(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     moe (optional, see moe_block): the MLP is the MoE block, whose shared expert is the MLP weights
     (gdn_layer_full_mx, q35_layer_mc.py:855-866)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, h = x.shape
     inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
@@ -203,6 +241,7 @@ def attn_layer_decode(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
     the page table describes each sequence including the new token; cos, sin bf16 [B, rot/2].
     moe (optional, see moe_block): the MLP is the MoE block (attn_layer_full_mx, q35_layer_mc.py:867-880)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous(), "x must be contiguous bf16 [B, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
     inter = w["w_gate"].shape[0]
@@ -258,6 +297,7 @@ def gdn_layer_verify(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in: 
     snapshots state_snap f32 [T, B, NV, 128, 128] and conv_snap bf16 [T, B, K-1, C] receive the states after
     each row."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, t, h = x.shape
     inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
@@ -289,6 +329,7 @@ def attn_layer_verify(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.Te
     [B, T, 2] (page, slot) of each new row; cos, sin bf16 [B, T, rot / 2]. kv_cache bf16 [P, 2, page, HKV, D] is
     written in place. Returns out bf16 [B, T, hidden]."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, t, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
     inter = w["w_gate"].shape[0]
@@ -351,6 +392,7 @@ def gdn_layer_prefill(x: torch.Tensor, w: dict, state_in: torch.Tensor, conv_in:
     moe_block; routing outputs [B T, ...]): the MLP is the MoE block (qwen35moe_gdn_prefill,
     q35_moe_prefill.py:47-52)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, t, h = x.shape
     inter = w["w_gate"].shape[0]
     kconv = w["conv_w"].shape[1]
@@ -384,6 +426,7 @@ def attn_layer_prefill(x: torch.Tensor, w: dict, cos: torch.Tensor, sin: torch.T
     [P, 2, page, HKV, D] is written in place. Returns out bf16 [B, T, hidden]. moe (optional): the MLP is the MoE
     block (qwen35moe_attn_prefill, q35_moe_prefill.py:55-60)."""
     _check(x.dtype == torch.bfloat16 and x.dim() == 3 and x.is_contiguous(), "x must be contiguous bf16 [B, T, H]")
+    w = _nv_weights(w, proj_fmt, mlp_fmt)
     b, t, h = x.shape
     pages, two, page, hkv, d = kv_cache.shape
     inter = w["w_gate"].shape[0]

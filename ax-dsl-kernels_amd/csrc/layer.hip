@@ -39,6 +39,7 @@ int mx_fmt_of(int wfmt) {
     case AXK_WFMT_FP8_CHANNEL: return AXK_MX_FP8;
     case AXK_WFMT_MXFP8: return AXK_MX_MXFP8;
     case AXK_WFMT_MXFP4: return AXK_MX_MXFP4;
+    case AXK_WFMT_NVFP4: return AXK_MX_NVFP4;
     default: return -1;
   }
 }
@@ -46,6 +47,10 @@ int mx_fmt_of(int wfmt) {
 // One projection of the group: per-channel f32 scales [N] (FP8) or E8M0 block scales [N, K/32] (MX formats).
 AxkMxMat proj_mat(int wfmt, const uint8_t* w, const void* s, void* out, int64_t n) {
   if (wfmt == AXK_WFMT_FP8_CHANNEL) return AxkMxMat{w, nullptr, static_cast<const float*>(s), nullptr, out, n, n};
+  if (wfmt == AXK_WFMT_NVFP4) {  // s: the host descriptor of the E4M3 block scales and the fp32 scale2
+    const axk_nvfp4_scales* ns = static_cast<const axk_nvfp4_scales*>(s);
+    return AxkMxMat{w, ns ? ns->block_scales : nullptr, nullptr, nullptr, out, n, n, ns ? ns->scale2 : nullptr};
+  }
   return AxkMxMat{w, static_cast<const uint8_t*>(s), nullptr, nullptr, out, n, n};
 }
 

@@ -56,10 +56,20 @@ typedef void* axk_stream_t; /* hipStream_t */
 /* Weight formats of the decode layers' projections and MLP (proj_fmt / mlp_fmt):
  *   AXK_WFMT_FP8_CHANNEL  E4M3 bytes [N, K] + f32 per-output-channel scale [N]   (sgl gemm.py:119-181)
  *   AXK_WFMT_MXFP8        E4M3 bytes [N, K] + E8M0 bytes [N, K/32]              (q35_mx_build.py:60-72; the 35B manifest)
- *   AXK_WFMT_MXFP4        E2M1 pairs [N, K/2] + E8M0 bytes [N, K/32]            (q35_moe.py:46-63; the 9B / 27B manifests) */
+ *   AXK_WFMT_MXFP4        E2M1 pairs [N, K/2] + E8M0 bytes [N, K/32]            (q35_moe.py:46-63; the 9B / 27B manifests)
+ *   AXK_WFMT_NVFP4        E2M1 pairs [N, K/2] + E4M3 bytes [N, K/16] + f32 scale2 [1] (q35_mx_build.py:168-200, the
+ *                         WFMT=nv4 projections; sgl quantize_nvfp4): the s_<name> argument of a layer entry then points
+ *                         to an axk_nvfp4_scales in host memory naming both device arrays (the reference's s_<name> and
+ *                         t_<name> inputs), read while the call is made */
 #define AXK_WFMT_FP8_CHANNEL 0
 #define AXK_WFMT_MXFP8 1
 #define AXK_WFMT_MXFP4 2
+#define AXK_WFMT_NVFP4 3
+
+typedef struct axk_nvfp4_scales {
+  const uint8_t* block_scales; /* E4M3 [N, K/16], 16-byte aligned */
+  const float* scale2;         /* f32 [1] */
+} axk_nvfp4_scales;
 
 /* Value-head order of the GDN layers when num_v_heads > num_k_heads: which key head value head vh reads
  * (models/qwen35_35b_a3b/src/70b0fbc/q35_step.py:82-85; the weights of the value heads, w_qkv's v rows, conv_w's

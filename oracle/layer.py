@@ -95,7 +95,8 @@ def add(x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
 # ---------------------------------------------------------------------------------------------
 def proj(a: torch.Tensor, w: dict, name: str, fmt: str = "fp8") -> torch.Tensor:
     """bf16(a @ W_name^T) in fp32 for the weight w_<name> / s_<name> in format fmt: "fp8" (E4M3 with a per-channel
-    scale, gemm.py:119-181), "mxfp8" (E4M3 + E8M0 per 32, q35_mx_build.py:60-72) or "mxfp4" (q35_moe.py:46-63)."""
+    scale, gemm.py:119-181), "mxfp8" (E4M3 + E8M0 per 32, q35_mx_build.py:60-72), "mxfp4" (q35_moe.py:46-63) or
+    "nvfp4" (E2M1 + E4M3 per 16 + the scale2 t_<name>, q35_mx_build.py:168-200)."""
     from oracle import mx
 
     wt, s = w["w_" + name], w["s_" + name]
@@ -103,6 +104,8 @@ def proj(a: torch.Tensor, w: dict, name: str, fmt: str = "fp8") -> torch.Tensor:
         y = mx.fp8_linear(a, wt.numpy(), None, s)
     elif fmt == "mxfp8":
         y = mx.mxfp8_linear(a, wt.numpy(), s.numpy(), "e4m3")
+    elif fmt == "nvfp4":  # E2M1 + E4M3 per 16 + scale2 t_<name> (q35_mx_build.py:168-200)
+        y = mx.nvfp4_linear(a, wt.numpy(), s.view(torch.uint8).numpy(), float(w["t_" + name].reshape(-1)[0]))
     else:
         y = mx.mx_linear(a, wt.numpy(), s.numpy())
     return _bf(y)
@@ -126,6 +129,8 @@ def dequant_weight(w: dict, name: str, fmt: str) -> torch.Tensor:
         return torch.from_numpy(mx.e4m3_table()[wt]) * s.float().reshape(-1, 1)
     if fmt == "mxfp8":
         return torch.from_numpy(mx.dequant_mxfp8(wt, s.numpy(), "e4m3"))
+    if fmt == "nvfp4":
+        return torch.from_numpy(mx.dequant_nvfp4(wt, s.view(torch.uint8).numpy(), float(w["t_" + name].reshape(-1)[0])))
     return torch.from_numpy(mx.dequant_mxfp4(wt, s.numpy()))
 
 

@@ -195,7 +195,8 @@ def test_layer_late_contract_error_enqueues_nothing(dev):
 
 # ---- the manifests' weight formats: MXFP8 layer weights (the 35B manifest, q35_mx_build.py:60-72) and MXFP4 layer
 # weights (the 9B / 27B manifests), for the projections and the MLP ----
-@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4"), ("mxfp8", "mxfp4")])
+@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4"), ("mxfp8", "mxfp4"),
+                                              ("nvfp4", "nvfp4"), ("mxfp8", "nvfp4")])
 def test_gdn_layer_decode_weight_formats(dev, proj_fmt, mlp_fmt):
     b, nk, nv = 3, 2, 4
     g = torch.Generator().manual_seed(31)
@@ -212,7 +213,7 @@ def test_gdn_layer_decode_weight_formats(dev, proj_fmt, mlp_fmt):
     _check_conv(co, rc)
 
 
-@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4")])
+@pytest.mark.parametrize("proj_fmt,mlp_fmt", [("mxfp8", "mxfp8"), ("mxfp4", "mxfp4"), ("nvfp4", "nvfp4")])
 def test_attn_layer_decode_weight_formats(dev, proj_fmt, mlp_fmt):
     lens, hq, hkv, rot, d = [100, 64, 300], 4, 2, 64, 256
     g = torch.Generator().manual_seed(37)

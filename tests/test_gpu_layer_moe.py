@@ -51,6 +51,7 @@ def _check_moe(out, r, x, y, w, blk, fmt):
 @pytest.mark.parametrize("b,h,f,nk,nv,e,fe,k,fmt", [
     (3, 256, 256, 2, 4, 16, 256, 4, "mxfp8"),
     (5, 256, 512, 2, 4, 40, 256, 8, "mxfp4"),
+    (3, 256, 256, 2, 4, 16, 256, 4, "nvfp4"),  # an NVFP4 shared expert
     (2, 2048, 512, 16, 32, 256, 512, 8, "mxfp8"),  # the 35B's widths (hidden 2048, 256 experts of 512, top-8)
     (32, 2048, 512, 16, 32, 256, 512, 8, "mxfp8"),  # the bench's moe_layer_decode: the 35B's widths at 32 sequences
 ])

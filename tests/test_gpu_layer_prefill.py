@@ -57,11 +57,14 @@ def _fused_close(got, ref, slack):
     assert (d <= tol + slack).all(), f"max excess {(d - tol - slack).max().item()}"
 
 
-# ragged chunks (100 = 64 + 36), one token, exactly one chunk, rows >= 128 in the dense GEMM path, the 35B's heads
+# ragged chunks (100 = 64 + 36), one token, exactly one chunk, rows >= 128 in the dense GEMM path, the 35B's heads,
+# NVFP4 weights
 @pytest.mark.parametrize("b,t,nk,nv,proj_fmt,mlp_fmt", [(2, 100, 2, 4, "fp8", "mxfp4"), (3, 1, 2, 4, "fp8", "mxfp4"),
                                                        (1, 64, 2, 2, "mxfp8", "mxfp8"),
                                                        (2, 130, 1, 2, "mxfp4", "mxfp8"),
-                                                       (1, 40, 16, 32, "mxfp8", "mxfp4")])
+                                                       (1, 40, 16, 32, "mxfp8", "mxfp4"),
+                                                       # NVFP4 projections and MLP, rows >= 128 (the prefill GEMM)
+                                                       (2, 100, 2, 4, "nvfp4", "nvfp4")])
 def test_gdn_layer_prefill_matches_oracle(dev, b, t, nk, nv, proj_fmt, mlp_fmt):
     w, x, st, cv = _gdn_case(b * 1000 + t + nk, b, t, nk, nv, proj_fmt, mlp_fmt)
     print(f"gdn prefill b={b} t={t} nk={nk} nv={nv} {proj_fmt}/{mlp_fmt}", flush=True)
