@@ -4,11 +4,11 @@ Python host layer over libaxk.so (include/axk.h). Operator names and contracts m
 sgl_kernel_axera operator API; tensors are torch device tensors used only as memory and streams.
 """
 from . import _lib
-from .gemm import bf16_gemm, fp8_gemm, mxfp4_dequant, mxfp4_gemm, mxfp8_gemm, nvfp4_gemm
+from .gemm import bf16_gemm, fp8_gemm, int4_gemm, int8_gemm, mxfp4_dequant, mxfp4_gemm, mxfp8_gemm, nvfp4_gemm
 from .quantization import quantize_nvfp4
 
-__all__ = ["bf16_gemm", "fp8_gemm", "mxfp4_dequant", "mxfp4_gemm", "mxfp8_gemm", "nvfp4_gemm", "quantize_nvfp4",
-           "load_library"]
+__all__ = ["bf16_gemm", "fp8_gemm", "int4_gemm", "int8_gemm", "mxfp4_dequant", "mxfp4_gemm", "mxfp8_gemm",
+           "nvfp4_gemm", "quantize_nvfp4", "load_library"]
 
 
 def load_library():

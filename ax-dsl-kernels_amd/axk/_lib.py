@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "axk_mxfp8_gemm": [_vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_nvfp4_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_bf16_gemm": [_vp, _i64, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "axk_int8_gemm": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
+    "axk_int4_gemm": [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i32, _i64, _i64, _i64, _vp],
     "axk_paged_decode_workspace_size": [_i64, _i64, _i64, _i64],
     "axk_paged_decode_plan": [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp],
     "axk_paged_decode_split": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,

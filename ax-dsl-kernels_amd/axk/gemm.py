@@ -1,4 +1,4 @@
-"""Runtime-weight linear operators (MXFP4 / NVFP4 / MXFP8 / FP8 E4M3 / bf16 weights) on gfx950.
+"""Runtime-weight linear operators (MXFP4 / NVFP4 / MXFP8 / FP8 E4M3 / INT8 / INT4 / bf16 weights) on gfx950.
 
 Mirrors the operator API of sgl_kernel_axera.gemm
 (models/qwen35_35b_a3b/sgl/python/sgl_kernel_axera/gemm.py): the same names, argument meaning and
@@ -242,5 +242,78 @@ def bf16_gemm(
     _lib.call(
         "axk_bf16_gemm", a.data_ptr(), a.stride(0), b_t.data_ptr(), _lib.ptr(bias), output.data_ptr(),
         _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
+    )
+    return output
+
+
+def int8_gemm(
+    a_int8: torch.Tensor,
+    b_int8_t: torch.Tensor,
+    scale_a: torch.Tensor,
+    scale_b: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """INT8 scaled GEMM (gemm.py:479-492 over _scaled_gemm 119-181).
+
+    output = (a_int8 * scale_a[:, None]) @ (b_int8_t * scale_b[:, None]).T + bias
+    a_int8 int8 [m, k] (unit stride along K, k % 16 == 0); b_int8_t int8 [n, k]; scale_a [m] or a scalar,
+    scale_b [n] or a scalar. The int8 products are summed exactly in int32; each sum is scaled once in fp32.
+    """
+    if a_int8.dim() != 2 or b_int8_t.dim() != 2:
+        raise ValueError("a and b_t must be 2D tensors")
+    if a_int8.dtype != torch.int8 or b_int8_t.dtype != torch.int8:
+        raise ValueError(f"a_int8 and b_int8_t must be int8, got {a_int8.dtype} / {b_int8_t.dtype}")
+    m, k = a_int8.shape
+    if b_int8_t.shape[1] != k:
+        raise ValueError(f"b_t must have shape [N, K], got {tuple(b_int8_t.shape)} for K={k}")
+    n = b_int8_t.shape[0]
+    sa = _normalize_scale(scale_a, m, "scale_a", a_int8.device)
+    sb = _normalize_scale(scale_b, n, "scale_b", a_int8.device)
+    bias, output = _prepare_bias_output(n, m, a_int8.device, out_dtype, bias, output)
+    if a_int8.stride(1) != 1 or a_int8.stride(0) % 16:
+        a_int8 = a_int8.contiguous()
+    w = b_int8_t.contiguous()
+    _lib.require_device(a_int8, w, sa, sb, output)
+    _lib.call(
+        "axk_int8_gemm", a_int8.data_ptr(), a_int8.stride(0), w.data_ptr(), sa.data_ptr(), sb.data_ptr(),
+        _lib.ptr(bias), output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a_int8),
+    )
+    return output
+
+
+def int4_gemm(
+    a: torch.Tensor,
+    b_int4: torch.Tensor,
+    b_scale: torch.Tensor,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    output: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """INT4 GEMM: output = a @ dequant(b_int4, b_scale).T + bias (gemm.py:662-677).
+
+    a       : (m, k) bf16 activation
+    b_int4  : (n, k) int8 tensor holding one signed int4 value (-8..7) per byte
+    b_scale : (n, k // group) float32 per-group scale; group = k // b_scale.shape[1], a multiple of 32
+    """
+    m, k = _check_a(a)
+    if b_int4.dim() != 2 or b_int4.shape[1] != k:
+        raise ValueError(f"b_w shape {tuple(b_int4.shape)} is incompatible with a having k={k}")
+    if b_int4.dtype != torch.int8:
+        raise ValueError(f"b_int4 must be an int8 tensor (one int4 per byte), got {b_int4.dtype}")
+    n = b_int4.shape[0]
+    if b_scale.dim() != 2 or b_scale.shape[0] != n or b_scale.shape[1] == 0 or k % b_scale.shape[1]:
+        raise ValueError(f"b_scale shape {tuple(b_scale.shape)} is incompatible with (n, k/group) for n={n}, k={k}")
+    group = k // b_scale.shape[1]
+    if group % 32:
+        raise ValueError(f"group size {group} must be a multiple of 32")
+    bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    w = b_int4.contiguous()
+    scales = b_scale.to(torch.float32).contiguous()
+    _lib.require_device(a, w, scales, output)
+    _lib.call(
+        "axk_int4_gemm", a.data_ptr(), a.stride(0), w.data_ptr(), scales.data_ptr(), group, _lib.ptr(bias),
+        output.data_ptr(), _OUT_DT[out_dtype], m, n, k, _lib.stream_of(a),
     )
     return output

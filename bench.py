@@ -1104,6 +1104,107 @@ class Fp8LinearWorkload(Workload):
                 "sample": f"full config4 q projection (oracle/mx.py fp8_linear, torch CPU), median of {reps} runs"}
 
 
+class Int8LinearWorkload(Workload):
+    """sgl int8_gemm (gemm.py:479-492) at config 4's q-projection shape: int8 weight [16384, 4096] with an fp32 scale
+    per channel, int8 activations [8, 4096] with a scale per row, bf16 out. Algorithmic bytes: weight + both scale
+    vectors + activations + out."""
+
+    name = "int8_linear"
+    tokens = 8  # tokens one step carries through the path
+    kernel = "int8_skinny_kernel<1>"
+    timing = "graph"
+    traffic_profile = "int8_linear_n16384_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        self.m, self.n, self.k = 8, 16384, 4096
+        g = torch.Generator().manual_seed(8)
+        self.alg_bytes = self.n * self.k + 4 * self.n + self.m * self.k + 4 * self.m + 2 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        self.copies = max(2, -(-ROTATE_BYTES // (self.n * self.k)))
+        self.host_w = torch.randint(-128, 128, (self.n, self.k), generator=g, dtype=torch.int8)
+        self.host_x = torch.randint(-128, 128, (self.m, self.k), generator=g, dtype=torch.int8)
+        self.host_sa = torch.rand(self.m, generator=g) / 127
+        self.host_sb = torch.rand(self.n, generator=g) / (127 * 64)
+        w = self.host_w.to(dev)
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.x, self.sa, self.sb = self.host_x.to(dev), self.host_sa.to(dev), self.host_sb.to(dev)
+        self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
+        self.config = {"workload": "int8_gemm N=16384 K=4096 M=8 (per-row and per-channel scales, bf16 out)",
+                       "rotating_copies": self.copies}
+        self.dtype = "int8 x int8 -> int32 acc"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        axk.int8_gemm(self.x, self.w[i % self.copies], self.sa, self.sb, output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import mx as omx
+
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        w, x, sa, sb = self.host_w.numpy(), self.host_x.numpy(), self.host_sa.numpy(), self.host_sb.numpy()
+        sec, reps = _time_cpu(lambda: omx.int8_linear(x, w, sa, sb), budget_s=10.0, min_reps=2)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"the full op (oracle/mx.py int8_linear, torch CPU), median of {reps} runs"}
+
+
+class Int4LinearWorkload(Workload):
+    """sgl int4_gemm (gemm.py:662-677) at config 4's q-projection shape: int4 weight [16384, 4096] one value per byte
+    with an fp32 scale per 128 along K, bf16 activations [8, 4096], bf16 out. Algorithmic bytes: weight + group scales
+    + activations + out."""
+
+    name = "int4_linear"
+    tokens = 8  # tokens one step carries through the path
+    kernel = "int4_skinny_kernel<1, 64>"
+    timing = "graph"
+    traffic_profile = "int4_linear_n16384_pmc.txt"
+
+    def __init__(self, dev):
+        import torch
+
+        self.m, self.n, self.k, self.group = 8, 16384, 4096, 128
+        g = torch.Generator().manual_seed(4)
+        ng = self.k // self.group
+        self.alg_bytes = self.n * self.k + 4 * self.n * ng + 2 * self.m * self.k + 2 * self.m * self.n
+        self.alg_flops = 2 * self.m * self.n * self.k
+        per_copy = self.n * self.k + 4 * self.n * ng
+        self.copies = max(2, -(-ROTATE_BYTES // per_copy))
+        self.host_w = torch.randint(-8, 8, (self.n, self.k), generator=g, dtype=torch.int8)
+        self.host_s = torch.rand(self.n, ng, generator=g) / 512
+        self.host_x = torch.randn(self.m, self.k, generator=g).to(torch.bfloat16)
+        w, s = self.host_w.to(dev), self.host_s.to(dev)
+        self.w = [w.clone() for _ in range(self.copies)]
+        self.s = [s.clone() for _ in range(self.copies)]
+        self.x = self.host_x.to(dev)
+        self.out = torch.empty(self.m, self.n, dtype=torch.bfloat16, device=dev)
+        self.config = {"workload": "int4_gemm N=16384 K=4096 M=8 (one int4 per byte, fp32 scale per 128, bf16 out)",
+                       "rotating_copies": self.copies}
+        self.dtype = "int4 x bf16 -> fp32 acc"
+
+    def step(self, i: int) -> None:
+        import axk
+
+        j = i % self.copies
+        axk.int4_gemm(self.x, self.w[j], self.s[j], output=self.out)
+
+    def cpu_baseline(self) -> dict:
+        import torch
+
+        from oracle import mx as omx
+
+        nt = _cpu_threads()
+        torch.set_num_threads(nt)
+        w, s = self.host_w.numpy(), self.host_s.numpy()
+        sec, reps = _time_cpu(lambda: omx.int4_linear(self.host_x, w, s), budget_s=10.0, min_reps=2)
+        return {"value": sec * 1e6, "unit": "µs/op", "cores": nt, "kind": "port",
+                "sample": f"the full op (oracle/mx.py int4_linear, torch CPU), median of {reps} runs"}
+
+
 class KvWriteWorkload(Workload):
     """Config 1's KV write: the current token's K and V rows (16 sequences x 2 KV heads x 256) scattered into the
     paged cache in place. Algorithmic bytes: k, v and the locations read, the rows written."""
@@ -1348,8 +1449,8 @@ WORKLOADS = {MxLinearWorkload.name: MxLinearWorkload, PagedDecodeWorkload.name: 
              LmHeadWorkload.name: LmHeadWorkload, LmHeadNvfp4Workload.name: LmHeadNvfp4Workload, PagedDecodeFp8Workload.name: PagedDecodeFp8Workload, PagedDecodeI8Workload.name: PagedDecodeI8Workload,
              PagedPrefillWorkload.name: PagedPrefillWorkload, MoeLayerDecodeWorkload.name: MoeLayerDecodeWorkload,
              MxLinearPrefillWorkload.name: MxLinearPrefillWorkload, MoeLayerPrefillWorkload.name: MoeLayerPrefillWorkload,
-             MoeGroupDecodeWorkload.name: MoeGroupDecodeWorkload,
-             CopyCalibWorkload.name: CopyCalibWorkload}
+             MoeGroupDecodeWorkload.name: MoeGroupDecodeWorkload, Int8LinearWorkload.name: Int8LinearWorkload,
+             Int4LinearWorkload.name: Int4LinearWorkload, CopyCalibWorkload.name: CopyCalibWorkload}
 DEFAULT_WORKLOAD = PagedDecodeWorkload.name
 
 

@@ -189,6 +189,25 @@ int axk_nvfp4_gemm(const uint16_t* a, int64_t lda, const uint8_t* b_fp4, const u
 int axk_bf16_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, const float* bias, void* out,
                   int out_dtype, int64_t m, int64_t n, int64_t k, axk_stream_t stream);
 
+/* INT8 scaled GEMM: output = (a * scale_a[:, None]) @ (b_int8 * scale_b[:, None]).T + bias. Replaces
+ * sgl_kernel_axera.gemm.int8_gemm (gemm.py:479-492 over _scaled_gemm 119-181); int32 MFMA accumulation, the
+ * scales applied to each exact int32 sum in fp32.
+ *   a       int8 [m, k], row stride lda bytes (lda % 16 == 0, 16-byte aligned)
+ *   b_int8  int8 [n, k] contiguous (16-byte aligned); k % 16 == 0
+ *   scale_a f32 [m], scale_b f32 [n] (a scalar scale is broadcast by the caller, as _normalize_scale does) */
+int axk_int8_gemm(const int8_t* a, int64_t lda, const int8_t* b_int8, const float* scale_a, const float* scale_b,
+                  const float* bias, void* out, int out_dtype, int64_t m, int64_t n, int64_t k,
+                  axk_stream_t stream);
+
+/* INT4-weight GEMM: output = a @ (b_int4 * b_scale[:, k / group]).T + bias. Replaces
+ * sgl_kernel_axera.gemm.int4_gemm (gemm.py:662-677 over _mx_gemm 564-623); fp32 accumulation.
+ *   a       bf16 [m, k], row stride lda elements (lda % 8 == 0, 16-byte aligned)
+ *   b_int4  int8 [n, k] contiguous: one signed int4 value (-8..7) per byte, as the reference stores it
+ *   b_scale f32 [n, k / group]: one scale per `group` consecutive K of a channel; group % 32 == 0, k % group == 0 */
+int axk_int4_gemm(const uint16_t* a, int64_t lda, const int8_t* b_int4, const float* b_scale, int64_t group,
+                  const float* bias, void* out, int out_dtype, int64_t m, int64_t n, int64_t k,
+                  axk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Paged flash-attention decode and the paged KV write
  * ------------------------------------------------------------------------------------------- */

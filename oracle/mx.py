@@ -18,14 +18,19 @@ Restates
                              to the even code, saturating at 6, the sign kept for values that round to zero);
                              the decode of models/qwen35_35b_a3b/sgl/tests/test_nvfp4_lm_head.py:11-16
   * NVFP4 linear             sgl_kernel_axera/gemm.py:495-561 (a @ dequant(w).T + bias, fp32 acc)
+  * INT8 scaled linear       sgl_kernel_axera/gemm.py:479-492 over 119-181 (each int8 operand times its scale,
+                             rounded to the output dtype; fp32 matmul; bias rounded to the output dtype)
+  * INT4 dequant / linear    sgl_kernel_axera/gemm.py:662-677 over 564-623 (one int4 per byte times its fp32 group
+                             scale, group = K / scale columns; a @ w.T + bias, fp32 acc)
 Pinned by tests/test_oracle_mx.py: exhaustive 16 x 256 code/scale table against the closed form and
 torch's float8_e8m0fnu / exp2, E4M3 and E5M2 tables against torch.float8_e4m3fn / float8_e5m2, the
 MXFP8 dequant against a float64 bit-field decode for every (code, scale) pair, the MXFP8 quantiser's
 scale rule and nearest-code choice against a brute-force search over all 256 codes, the C restatement
 (oracle/mx_codec.c) against this module, quantiser brute force + round trip, the NVFP4 codec against the reference
 test's vectors (its midpoint row, zero blocks, an all-zero matrix) and its E2M1 choice against a brute-force
-nearest-value search, the NVFP4 dequant against a float64 decode of every (code, scale) pair, and the linears
-against float64 dot products.
+nearest-value search, the NVFP4 dequant against a float64 decode of every (code, scale) pair, the INT8 linear
+against exact int64 dot products under power-of-two scales and against single-element cases of its operand and bias
+rounding, the INT4 linear against float64 loops over each group, and the linears against float64 dot products.
 """
 from __future__ import annotations
 
@@ -239,6 +244,43 @@ def dequant_nvfp4(packed: np.ndarray, scales: np.ndarray, scale2) -> np.ndarray:
 def nvfp4_linear(a: torch.Tensor, packed: np.ndarray, scales: np.ndarray, scale2, bias=None) -> torch.Tensor:
     """a[M, K] @ dequant_nvfp4(packed, scales, scale2).T (+ bias) in fp32 (sgl nvfp4_gemm, gemm.py:495-561)."""
     w = torch.from_numpy(dequant_nvfp4(packed, scales, scale2))
+    out = a.float().cpu() @ w.T
+    if bias is not None:
+        out = out + bias.float().cpu()
+    return out
+
+
+def int8_linear(a_int8, b_int8, scale_a, scale_b, out_dtype=torch.bfloat16, bias=None) -> torch.Tensor:
+    """sgl int8_gemm (gemm.py:479-492 -> scaled_gemm_kernel 123-153): each operand times its per-row / per-channel
+    scale (a scalar broadcasts, _normalize_scale 17-23) rounded to out_dtype, an fp32 matmul, plus the bias rounded
+    to out_dtype (_prepare_bias_output 34-39). Returns fp32; the caller rounds to out_dtype."""
+    a = torch.as_tensor(np.asarray(a_int8, dtype=np.int8)).float()
+    b = torch.as_tensor(np.asarray(b_int8, dtype=np.int8)).float()
+    sa = torch.as_tensor(np.asarray(scale_a, dtype=np.float32)).reshape(-1)
+    sb = torch.as_tensor(np.asarray(scale_b, dtype=np.float32)).reshape(-1)
+    sa = sa.expand(a.shape[0]) if sa.numel() == 1 else sa
+    sb = sb.expand(b.shape[0]) if sb.numel() == 1 else sb
+    x = (a * sa[:, None]).to(out_dtype).float()
+    w = (b * sb[:, None]).to(out_dtype).float()
+    out = x @ w.T
+    if bias is not None:
+        out = out + torch.as_tensor(bias).float().to(out_dtype).float()
+    return out
+
+
+def dequant_int4(b_int4, b_scale) -> np.ndarray:
+    """int4 values (one signed value per byte) [N, K] times the fp32 scale of their group of K / G along K
+    (G = K / b_scale.shape[1]): the hardware dequantisation w = w_int * scale of gemm.py:580-589."""
+    w = np.asarray(b_int4, dtype=np.int8).astype(np.float32)
+    s = np.asarray(b_scale, dtype=np.float32)
+    n, k = w.shape
+    g = k // s.shape[1]
+    return (w.reshape(n, k // g, g) * s[:, :, None]).reshape(n, k)
+
+
+def int4_linear(a: torch.Tensor, b_int4, b_scale, bias=None) -> torch.Tensor:
+    """a[M, K] @ dequant_int4(b_int4, b_scale).T (+ bias) in fp32 (sgl int4_gemm, gemm.py:662-677 -> _mx_gemm)."""
+    w = torch.from_numpy(dequant_int4(b_int4, b_scale))
     out = a.float().cpu() @ w.T
     if bias is not None:
         out = out + bias.float().cpu()

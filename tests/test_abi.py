@@ -54,6 +54,16 @@ def test_contract_violations_return_before_launch():
     assert lib.axk_mxfp4_gemm(fake, 64, ctypes.c_void_p(0x9000), fake, None, fake, 9, 1, 16, 64, None) == 5
     # fp8 without its channel scales
     assert lib.axk_fp8_gemm(fake, 64, fake, None, None, None, fake, 9, 1, 16, 64, None) == 1
+    # int8: k not a multiple of 16; misaligned leading dimension; bad dtype; missing scale_a
+    assert lib.axk_int8_gemm(fake, 64, fake, fake, fake, None, fake, 9, 1, 16, 40, None) == 2
+    assert lib.axk_int8_gemm(fake, 72, fake, fake, fake, None, fake, 9, 1, 16, 64, None) == 3
+    assert lib.axk_int8_gemm(fake, 64, fake, fake, fake, None, fake, 6, 1, 16, 64, None) == 4
+    assert lib.axk_int8_gemm(fake, 64, fake, None, fake, None, fake, 9, 1, 16, 64, None) == 1
+    # int4: a group that is not a multiple of 32 or does not divide k; output over the weights
+    assert lib.axk_int4_gemm(fake, 64, fake, fake, 16, None, fake, 9, 1, 16, 64, None) == 2
+    assert lib.axk_int4_gemm(fake, 96, fake, fake, 64, None, fake, 9, 1, 16, 96, None) == 2
+    assert lib.axk_int4_gemm(fake, 64, ctypes.c_void_p(0x9000), fake, 32, None, ctypes.c_void_p(0x9100), 9, 1, 16, 64,
+                             None) == 5
 
 
 def test_python_layer_raises_value_error_on_contract():
@@ -68,6 +78,19 @@ def test_python_layer_raises_value_error_on_contract():
         axk.mxfp4_gemm(a.float(), torch.zeros(16, 32, dtype=torch.uint8), s)  # fp32 activation
     with pytest.raises(ValueError):
         axk.mxfp4_gemm(a, torch.zeros(16, 32, dtype=torch.uint8), torch.zeros(16, 3, dtype=torch.uint8))
+    i8 = torch.zeros(2, 64, dtype=torch.int8)
+    with pytest.raises(ValueError):
+        axk.int8_gemm(i8, torch.zeros(16, 48, dtype=torch.int8), torch.ones(1), torch.ones(1))  # k mismatch
+    with pytest.raises(ValueError):
+        axk.int8_gemm(i8, torch.zeros(16, 64, dtype=torch.int8), torch.ones(3), torch.ones(1))  # scale_a size
+    with pytest.raises(ValueError):
+        axk.int8_gemm(a, torch.zeros(16, 64, dtype=torch.int8), torch.ones(1), torch.ones(1))  # bf16 activation
+    with pytest.raises(ValueError):
+        axk.int4_gemm(a, torch.zeros(16, 64, dtype=torch.int8), torch.ones(16, 4))  # group 16
+    with pytest.raises(ValueError):
+        axk.int4_gemm(a, torch.zeros(16, 64, dtype=torch.int8), torch.ones(15, 2))  # scale rows
+    with pytest.raises(ValueError):
+        axk.int4_gemm(a, torch.zeros(16, 64, dtype=torch.uint8), torch.ones(16, 2))  # unsigned storage
 
 
 def test_moe_workspace_size_limits():
@@ -109,6 +132,8 @@ def test_entry_points_reach_the_launch_on_a_gpu_less_host():
     p = [base + 65536 * i for i in range(200)]
     launch = 7  # AXK_E_LAUNCH
     assert lib.axk_rmsnorm(p[0], 64, p[1], p[2], 64, 1, 64, 1e-6, None) == launch
+    assert lib.axk_int8_gemm(p[0], 64, p[1], p[2], p[3], None, p[4], 9, 3, 70, 64, None) == launch
+    assert lib.axk_int4_gemm(p[0], 64, p[1], p[2], 32, p[3], p[4], 3, 3, 70, 64, None) == launch
     ws = lib.axk_paged_decode_workspace_size(2, 8, 2, 128)
     assert lib.axk_paged_decode(p[0], p[1], p[2], p[3], p[4], p[5], 2, 8, 2, 128, 32, 4, 0.1, p[100], ws,
                                 None) == launch

@@ -333,3 +333,59 @@ def test_quantize_nvfp4_block_rule():
     dec = (mx.e4m3_table()[scales].astype(np.float32) * s2).astype(np.float32)
     q = (blocks / np.where(dec > 0, dec, np.float32(1))[..., None]).astype(np.float32)  # a zero scale divides by 1
     assert np.array_equal(codes, _e2m1_by_binade(q)[0])
+
+
+def test_int8_linear_exact_under_power_of_two_scales():
+    """With power-of-two scales every scaled operand, product and sum up to 2^24 is exact in fp32 and bf16 holds
+    int8 * 2^e exactly, so the linear equals the int64 dot product times 2^(ea[m] + eb[n]) bit for bit; distinct m
+    and n sizes and scales make a transposed operand or swapped scale fail."""
+    rng = np.random.default_rng(5)
+    m, n, k = 5, 7, 96
+    a = rng.integers(-128, 128, (m, k), dtype=np.int8)
+    b = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    ea, eb = rng.integers(-6, 4, m), rng.integers(-5, 5, n)
+    exact = np.zeros((m, n), dtype=np.int64)
+    for i in range(m):
+        for j in range(n):
+            exact[i, j] = sum(int(a[i, t]) * int(b[j, t]) for t in range(k))
+    want = exact.astype(np.float64) * np.exp2(ea)[:, None] * np.exp2(eb)[None, :]
+    for dt in (torch.float32, torch.bfloat16):
+        got = mx.int8_linear(a, b, np.exp2(ea).astype(np.float32), np.exp2(eb).astype(np.float32), dt)
+        assert np.array_equal(got.numpy().astype(np.float64), want)
+    # a scalar scale broadcasts like a vector of one value
+    one = mx.int8_linear(a, b, np.float32(0.25), np.float32(2.0), torch.float32)
+    vec = mx.int8_linear(a, b, np.full(m, 0.25, np.float32), np.full(n, 2.0, np.float32), torch.float32)
+    assert torch.equal(one, vec) and np.array_equal(one.numpy().astype(np.float64), exact * 0.5)
+
+
+def test_int8_linear_rounds_operands_and_bias_to_the_output_dtype():
+    """1 x 1 x 1 cases: 127 * (1/3) is rounded to bf16 (42.25, not fp32's 42.333332) before the matmul when the
+    output is bf16 and kept in fp32 otherwise; a bias of 1 + 2^-10 adds 1 at bf16."""
+    a, b = np.array([[127]], np.int8), np.array([[1]], np.int8)
+    third = np.float32(1.0 / 3.0)
+    assert mx.int8_linear(a, b, third, np.float32(1), torch.bfloat16).item() == 42.25
+    assert mx.int8_linear(a, b, third, np.float32(1), torch.float32).item() == float(np.float32(127) * third)
+    bias = torch.tensor([1.0 + 2.0 ** -10])
+    assert mx.int8_linear(a, b, np.float32(1), np.float32(1), torch.bfloat16, bias).item() == 128.0
+    assert mx.int8_linear(a, b, np.float32(1), np.float32(1), torch.float32, bias).item() == 128.0 + 2.0 ** -10
+
+
+def test_int4_linear_against_group_loops():
+    """The int4 linear equals float64 loops that scale each group's partial dot product by its own scale (group = K /
+    scale columns): a scale indexed by k % G, by the wrong channel, or a transposed weight fails."""
+    rng = np.random.default_rng(6)
+    for m, n, k, g in ((3, 5, 128, 32), (2, 4, 192, 64)):
+        a = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+        w = rng.integers(-8, 8, (n, k), dtype=np.int8)
+        s = (rng.random((n, k // g)) + 0.25).astype(np.float32)
+        af = a.double().numpy()
+        want = np.zeros((m, n))
+        for i in range(m):
+            for j in range(n):
+                for q in range(k // g):
+                    want[i, j] += float(s[j, q]) * sum(af[i, t] * int(w[j, t]) for t in range(q * g, (q + 1) * g))
+        got = mx.int4_linear(a, w, s).numpy().astype(np.float64)
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+        # unit scales: the plain integer-weight product
+        ones = mx.int4_linear(a, w, np.ones_like(s)).numpy().astype(np.float64)
+        np.testing.assert_allclose(ones, af @ w.T.astype(np.float64), rtol=1e-6, atol=1e-5)
