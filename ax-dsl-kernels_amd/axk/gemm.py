@@ -272,6 +272,8 @@ def int8_gemm(
     sa = _normalize_scale(scale_a, m, "scale_a", a_int8.device)
     sb = _normalize_scale(scale_b, n, "scale_b", a_int8.device)
     bias, output = _prepare_bias_output(n, m, a_int8.device, out_dtype, bias, output)
+    if m == 0 or n == 0:  # nothing to compute (an empty tensor may have no device address)
+        return output
     if a_int8.stride(1) != 1 or a_int8.stride(0) % 16:
         a_int8 = a_int8.contiguous()
     w = b_int8_t.contiguous()
@@ -309,6 +311,8 @@ def int4_gemm(
     if group % 32:
         raise ValueError(f"group size {group} must be a multiple of 32")
     bias, output = _prepare_bias_output(n, m, a.device, out_dtype, bias, output)
+    if m == 0 or n == 0:  # nothing to compute (an empty tensor may have no device address)
+        return output
     w = b_int4.contiguous()
     scales = b_scale.to(torch.float32).contiguous()
     _lib.require_device(a, w, scales, output)

@@ -100,3 +100,55 @@ def test_int4_gemm_matches_oracle(dev, m, n, k, g, out_dtype):
     got = axk.int4_gemm(a.to(dev), w.to(dev), s.to(dev), out_dtype=out_dtype, bias=bias.to(dev))
     want = mx.int4_linear(a, w.numpy(), s.numpy(), bias)
     torch.testing.assert_close(got.float().cpu(), want, **(BF16_TOL if out_dtype == torch.bfloat16 else F32_TOL))
+
+
+def test_int_gemm_edge_shapes(dev):
+    """Empty m returns the empty output; the smallest K (16 for int8, 32 for int4); one output channel; a weight given
+    as a transposed view (made contiguous by the wrapper); bias None against an explicit zero bias."""
+    a0 = torch.empty(0, 64, dtype=torch.int8, device=dev)
+    out = axk.int8_gemm(a0, _i8((8, 64), 1).to(dev), torch.ones(1, device=dev), torch.ones(8, device=dev))
+    assert out.shape == (0, 8)
+    a, b = _i8((5, 16), 2), _i8((3, 16), 3)
+    got = axk.int8_gemm(a.to(dev), b.to(dev), torch.tensor(1.0), torch.tensor(1.0), out_dtype=torch.float32).cpu()
+    assert torch.equal(got.double(), (a.long() @ b.long().T).double())
+    bt = _i8((96, 1), 4).to(dev).T  # [1, 96] view of a [96, 1] tensor
+    a = _i8((4, 96), 5).to(dev)
+    got = axk.int8_gemm(a, bt, torch.tensor(0.5), torch.tensor(2.0), out_dtype=torch.float32).cpu()
+    assert torch.equal(got.double(), (a.cpu().long() @ bt.cpu().long().T).double())
+    x = torch.randn(3, 32, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(dev)
+    w, s = _i4(2, 32, 7).to(dev), torch.full((2, 1), 0.25, device=dev)
+    z = torch.zeros(2, device=dev)
+    assert torch.equal(axk.int4_gemm(x, w, s, out_dtype=torch.float32),
+                       axk.int4_gemm(x, w, s, out_dtype=torch.float32, bias=z))
+
+
+def test_int_gemm_graph_replays(dev):
+    """Both entry points captured in one HIP graph: every replay, with eager calls and new inputs copied in between,
+    equals the eager result (no memset or allocation inside the calls)."""
+    m, n, k = 8, 512, 1024
+    a8, b8 = _i8((m, k), 8).to(dev), _i8((n, k), 9).to(dev)
+    sa, sb = torch.rand(m, device=dev), torch.rand(n, device=dev)
+    xa = torch.randn(m, k, device=dev).to(torch.bfloat16)
+    w4, s4 = _i4(n, k, 10).to(dev), torch.rand(n, k // 64, device=dev)
+    o8 = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    o4 = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+    axk.int8_gemm(a8, b8, sa, sb, output=o8)
+    axk.int4_gemm(xa, w4, s4, output=o4)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            axk.int8_gemm(a8, b8, sa, sb, output=o8)
+            axk.int4_gemm(xa, w4, s4, output=o4)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        a8.copy_(_i8((m, k), 20 + rep).to(dev))
+        xa.copy_(torch.randn(m, k, generator=torch.Generator().manual_seed(rep)).to(torch.bfloat16).to(dev))
+        want8 = axk.int8_gemm(a8, b8, sa, sb).clone()
+        want4 = axk.int4_gemm(xa, w4, s4).clone()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"int gemm replay {rep}", flush=True)
+        assert torch.equal(o8, want8) and torch.equal(o4, want4)
