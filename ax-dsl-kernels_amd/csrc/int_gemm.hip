@@ -13,8 +13,9 @@
 // fp32 sums), and its 16 x 16 partial is scaled by the slice's group scale (one per output channel = one per lane)
 // into the fp32 accumulator: group % 32 == 0.
 //
-// m <= 64 (decode batches) takes the skinny kernels below; larger m the tiled ones: workgroup = 64 output rows x 64
-// output channels, 4 waves as 2 x 2 blocks of 32 x 32 (2 x 2 MFMA tiles). Each
+// m <= 64 (decode batches) takes the skinny kernels below; m and n of at least 128 the 128 x 128 tiles; the rest the
+// 64 x 64 tiles: workgroup = 64 output rows x 64 output channels, 4 waves as 2 x 2 blocks of 32 x 32 (2 x 2 MFMA
+// tiles). Each
 // 64-wide K step of A and B is loaded one step ahead into registers (16 or 32 bytes a thread, 4 lanes per row),
 // written to one of two LDS buffers (rows padded by 16 bytes: the 16-byte fragment reads of a wave spread over the
 // banks) and read back in the MFMA layout: lane (row l % 16, K group l / 16) takes its row's K slice of group l / 16
@@ -90,6 +91,87 @@ __global__ __launch_bounds__(256) void int8_gemm_kernel(const int8_t* __restrict
         else
           reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
       }
+}
+
+// The large-tile int8 form (m and n of at least 128): workgroup = 128 x 128 outputs, 4 waves as 2 x 2 blocks of
+// 64 x 64 (4 x 4 MFMA tiles each, 64 accumulator registers), so each 16-byte fragment read from LDS feeds 4 MFMAs
+// instead of 2; the same 64-K steps double-buffered in LDS, each thread moving 2 + 2 16-byte pieces a step.
+constexpr int kI8Big = 128;
+
+__global__ __launch_bounds__(256) void int8_gemm_big_kernel(const int8_t* __restrict__ a, int64_t lda,
+                                                            const int8_t* __restrict__ b, const float* __restrict__ sa,
+                                                            const float* __restrict__ sb,
+                                                            const float* __restrict__ bias, void* __restrict__ out,
+                                                            int out_f32, int M, int N, int K) {
+  __shared__ __align__(16) int8_t sA[2][kI8Big * kI8Ld];
+  __shared__ __align__(16) int8_t sB[2][kI8Big * kI8Ld];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
+  const int n0 = blockIdx.x * kI8Big, m0 = blockIdx.y * kI8Big;
+  const int wm = wave >> 1, wn = wave & 1;
+  // this thread's pieces of a step: rows r and r + 64 of each tile, bytes 16 c .. 16 c + 15 of the step
+  const int r = tid >> 2, c = tid & 3;
+  const int8_t* ap0 = a + (int64_t)min(m0 + r, M - 1) * lda + 16 * c;
+  const int8_t* ap1 = a + (int64_t)min(m0 + r + 64, M - 1) * lda + 16 * c;
+  const int8_t* bp0 = b + (int64_t)min(n0 + r, N - 1) * K + 16 * c;
+  const int8_t* bp1 = b + (int64_t)min(n0 + r + 64, N - 1) * K + 16 * c;
+  const int nk = (K + kI8Bk - 1) / kI8Bk;
+  const axk_i32x4 z = {0, 0, 0, 0};
+  // K % 16 == 0: a piece is wholly inside K or wholly past it
+  auto load = [&](const int8_t* p, int ks) -> axk_i32x4 {
+    const int kb = ks * kI8Bk;
+    return kb + 16 * c < K ? *reinterpret_cast<const axk_i32x4*>(p + kb) : z;
+  };
+  axk_i32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = z;
+
+  axk_i32x4 ra0 = load(ap0, 0), ra1 = load(ap1, 0), rb0 = load(bp0, 0), rb1 = load(bp1, 0);
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+    *reinterpret_cast<axk_i32x4*>(&sA[buf][r * kI8Ld + 16 * c]) = ra0;
+    *reinterpret_cast<axk_i32x4*>(&sA[buf][(r + 64) * kI8Ld + 16 * c]) = ra1;
+    *reinterpret_cast<axk_i32x4*>(&sB[buf][r * kI8Ld + 16 * c]) = rb0;
+    *reinterpret_cast<axk_i32x4*>(&sB[buf][(r + 64) * kI8Ld + 16 * c]) = rb1;
+    __syncthreads();  // the step's tiles are in LDS; every wave is done with the buffer written two steps ago
+    if (ks + 1 < nk) {  // uniform: the next step lands while this one is computed
+      ra0 = load(ap0, ks + 1);
+      ra1 = load(ap1, ks + 1);
+      rb0 = load(bp0, ks + 1);
+      rb1 = load(bp1, ks + 1);
+    }
+    axk_i32x4 af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      af[i] = *reinterpret_cast<const axk_i32x4*>(&sA[buf][(64 * wm + 16 * i + l16) * kI8Ld + 16 * g4]);
+      bf[i] = *reinterpret_cast<const axk_i32x4*>(&sB[buf][(64 * wn + 16 * i + l16) * kI8Ld + 16 * g4]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
+  // element (i, j, q): row m0 + 64 wm + 16 i + 4 g4 + q, channel n0 + 64 wn + 16 j + l16
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 64 * wn + 16 * j + l16;
+    if (n >= N) continue;
+    const float sbn = sb[n], bn = bias ? bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = m0 + 64 * wm + 16 * i + 4 * g4 + q;
+        if (m >= M) continue;
+        float v = (float)acc[i][j][q] * sa[m] * sbn;
+        if (bias) v += bn;
+        if (out_f32)
+          reinterpret_cast<float*>(out)[(int64_t)m * N + n] = v;
+        else
+          reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
+      }
+  }
 }
 
 // 8 signed bytes -> 8 bf16 (exact: |v| <= 128 needs 8 significant bits).
@@ -185,6 +267,101 @@ __global__ __launch_bounds__(256) void int4_gemm_kernel(const uint16_t* __restri
         else
           reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
       }
+}
+
+// The large-tile int4 form (m and n of at least 128): 128 x 128 outputs per workgroup, 4 waves of 64 x 64 (4 x 4
+// MFMA tiles), 64-K steps double-buffered in LDS (each thread moving 4 16-byte activation pieces and 2 weight pieces a
+// step); each 32-wide K slice's 16 x 16 partial scaled by its group scale as in the 64 x 64 form.
+__global__ __launch_bounds__(256) void int4_gemm_big_kernel(const uint16_t* __restrict__ a, int64_t lda,
+                                                            const int8_t* __restrict__ b, const float* __restrict__ bs,
+                                                            int group, const float* __restrict__ bias,
+                                                            void* __restrict__ out, int out_f32, int M, int N, int K) {
+  __shared__ __align__(16) uint8_t sA[2][kI8Big * kI4LdA];
+  __shared__ __align__(16) int8_t sB[2][kI8Big * kI8Ld];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g4 = lane >> 4;
+  const int n0 = blockIdx.x * kI8Big, m0 = blockIdx.y * kI8Big;
+  const int wm = wave >> 1, wn = wave & 1;
+  // this thread's share of a step: rows r and r + 64 of each tile, K 16 c .. 16 c + 15 of the step
+  const int r = tid >> 2, c = tid & 3;
+  const uint16_t* ap0 = a + (int64_t)min(m0 + r, M - 1) * lda + 16 * c;
+  const uint16_t* ap1 = a + (int64_t)min(m0 + r + 64, M - 1) * lda + 16 * c;
+  const int8_t* bp0 = b + (int64_t)min(n0 + r, N - 1) * K + 16 * c;
+  const int8_t* bp1 = b + (int64_t)min(n0 + r + 64, N - 1) * K + 16 * c;
+  const int nk = (K + kI8Bk - 1) / kI8Bk, ngroups = K / group;
+  const float* srow[4];  // group scales of the four output channels this lane's accumulators hold (tile column j)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) srow[j] = bs + (int64_t)min(n0 + 64 * wn + 16 * j + l16, N - 1) * ngroups;
+  const axk_u32x4 z = {0u, 0u, 0u, 0u};
+  axk_f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = axk_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // K % 32 == 0: a 16-wide chunk is wholly inside K or wholly past it
+  axk_u32x4 ra[4], rb[2];
+  auto load = [&](int kb) {
+    const bool in = kb + 16 * c < K;
+    ra[0] = in ? *reinterpret_cast<const axk_u32x4*>(ap0 + kb) : z;
+    ra[1] = in ? *reinterpret_cast<const axk_u32x4*>(ap0 + kb + 8) : z;
+    ra[2] = in ? *reinterpret_cast<const axk_u32x4*>(ap1 + kb) : z;
+    ra[3] = in ? *reinterpret_cast<const axk_u32x4*>(ap1 + kb + 8) : z;
+    rb[0] = in ? *reinterpret_cast<const axk_u32x4*>(bp0 + kb) : z;
+    rb[1] = in ? *reinterpret_cast<const axk_u32x4*>(bp1 + kb) : z;
+  };
+  load(0);
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+    *reinterpret_cast<axk_u32x4*>(&sA[buf][r * kI4LdA + 32 * c]) = ra[0];
+    *reinterpret_cast<axk_u32x4*>(&sA[buf][r * kI4LdA + 32 * c + 16]) = ra[1];
+    *reinterpret_cast<axk_u32x4*>(&sA[buf][(r + 64) * kI4LdA + 32 * c]) = ra[2];
+    *reinterpret_cast<axk_u32x4*>(&sA[buf][(r + 64) * kI4LdA + 32 * c + 16]) = ra[3];
+    *reinterpret_cast<axk_u32x4*>(&sB[buf][r * kI8Ld + 16 * c]) = rb[0];
+    *reinterpret_cast<axk_u32x4*>(&sB[buf][(r + 64) * kI8Ld + 16 * c]) = rb[1];
+    __syncthreads();  // the step's tiles are in LDS; every wave is done with the buffer written two steps ago
+    if (ks + 1 < nk) load((ks + 1) * kI8Bk);  // uniform
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k32 = ks * kI8Bk + 32 * h;
+      if (k32 >= K) break;  // uniform
+      axk_bf16x8 af[4], bf[4];
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        af[i] = *reinterpret_cast<const axk_bf16x8*>(&sA[buf][(64 * wm + 16 * i + l16) * kI4LdA + 64 * h + 16 * g4]);
+        bf[i] = i8x8_to_bf16x8(
+            *reinterpret_cast<const uint2*>(&sB[buf][(64 * wn + 16 * i + l16) * kI8Ld + 32 * h + 8 * g4]));
+        sc[i] = srow[i][k32 / group];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const axk_f32x4 p = mfma_bf16_16x16x32(af[i], bf[j], axk_f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[i][j][q] = __builtin_fmaf(p[q], sc[j], acc[i][j][q]);
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 64 * wn + 16 * j + l16;
+    if (n >= N) continue;
+    const float bn = bias ? bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = m0 + 64 * wm + 16 * i + 4 * g4 + q;
+        if (m >= M) continue;
+        float v = acc[i][j][q];
+        if (bias) v += bn;
+        if (out_f32)
+          reinterpret_cast<float*>(out)[(int64_t)m * N + n] = v;
+        else
+          reinterpret_cast<uint16_t*>(out)[(int64_t)m * N + n] = (uint16_t)f32_to_bf16_bits(v);
+      }
+  }
 }
 
 // Skinny forms (m <= 64, decode batches): a workgroup per 16 output channels, so n / 16 workgroups stream the
@@ -368,6 +545,12 @@ extern "C" int axk_int8_gemm(const int8_t* a, int64_t lda, const int8_t* b_int8,
                          f32, (int)m, (int)n, (int)k);
     return axk_launch_status();
   }
+  if (m >= kI8Big && n >= kI8Big) {
+    const dim3 bg((unsigned)((n + kI8Big - 1) / kI8Big), (unsigned)((m + kI8Big - 1) / kI8Big));
+    hipLaunchKernelGGL(int8_gemm_big_kernel, bg, dim3(256), 0, axk_stream(stream), a, lda, b_int8, scale_a, scale_b,
+                       bias, out, f32, (int)m, (int)n, (int)k);
+    return axk_launch_status();
+  }
   hipLaunchKernelGGL(int8_gemm_kernel, grid, dim3(256), 0, axk_stream(stream), a, lda, b_int8, scale_a, scale_b, bias,
                      out, out_dtype == AXK_DT_F32 ? 1 : 0, (int)m, (int)n, (int)k);
   return axk_launch_status();
@@ -407,6 +590,12 @@ extern "C" int axk_int4_gemm(const uint16_t* a, int64_t lda, const int8_t* b_int
       wide ? go(int4_skinny_kernel<2, 64>) : go(int4_skinny_kernel<2, 32>);
     else
       wide ? go(int4_skinny_kernel<4, 64>) : go(int4_skinny_kernel<4, 32>);
+    return axk_launch_status();
+  }
+  if (m >= kI8Big && n >= kI8Big) {
+    const dim3 bg((unsigned)((n + kI8Big - 1) / kI8Big), (unsigned)((m + kI8Big - 1) / kI8Big));
+    hipLaunchKernelGGL(int4_gemm_big_kernel, bg, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale,
+                       (int)group, bias, out, f32, (int)m, (int)n, (int)k);
     return axk_launch_status();
   }
   hipLaunchKernelGGL(int4_gemm_kernel, grid, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale, (int)group,

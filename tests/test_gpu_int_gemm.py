@@ -17,9 +17,10 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = dict(rtol=2e-2, atol=1e-2)
 F32_TOL = dict(rtol=1e-4, atol=1e-4)
 
-# m <= 64 takes the skinny kernels (row tiles 1, 2, 4: m = 1, 20, 33, 64), larger m the 64 x 64 tiles
+# m <= 64 takes the skinny kernels (row tiles 1, 2, 4: m = 1, 20, 33, 64); m and n >= 128 the 128 x 128 tiles
+# (exact, ragged, a K tail); the rest the 64 x 64 tiles
 I8_SHAPES = [(1, 64, 64), (1, 4096, 2048), (20, 1000, 4096), (33, 100, 272), (64, 128, 1024), (65, 96, 128),
-             (200, 300, 4096)]
+             (128, 128, 64), (300, 200, 272), (200, 300, 4096), (130, 100, 512)]
 
 
 def _i8(shape, seed):
@@ -67,9 +68,11 @@ def test_int8_gemm_scalar_scales_and_strided_activation(dev):
     assert torch.equal(out.cpu(), exact.float().to(torch.bfloat16))
 
 
-# skinny (m <= 64) in both step widths (group 32: 32 K a step; group % 64 == 0: 64) and all row tiles; then tiled
+# skinny (m <= 64) in both step widths (group 32: 32 K a step; group % 64 == 0: 64) and all row tiles; then the
+# 64 x 64 tiles (n < 128) and the 128 x 128 tiles (exact, ragged, a half step of K at the end)
 I4_SHAPES = [(1, 64, 64, 32), (7, 130, 96, 32), (20, 64, 256, 32), (40, 80, 512, 32), (32, 256, 2048, 128),
-             (48, 512, 4096, 64), (1, 4096, 2048, 128), (65, 96, 96, 32), (130, 200, 2048, 256)]
+             (48, 512, 4096, 64), (1, 4096, 2048, 128), (65, 96, 96, 32), (130, 200, 2048, 256), (128, 128, 64, 32),
+             (256, 300, 96, 32), (200, 512, 1024, 64)]
 
 
 def _i4(n, k, seed):
