@@ -271,7 +271,9 @@ __global__ __launch_bounds__(256) void int4_gemm_kernel(const uint16_t* __restri
 
 // The large-tile int4 form (m and n of at least 128): 128 x 128 outputs per workgroup, 4 waves of 64 x 64 (4 x 4
 // MFMA tiles), 64-K steps double-buffered in LDS (each thread moving 4 16-byte activation pieces and 2 weight pieces a
-// step); each 32-wide K slice's 16 x 16 partial scaled by its group scale as in the 64 x 64 form.
+// step); each 32-wide K slice's 16 x 16 partial scaled by its group scale as in the 64 x 64 form, or with CH (group %
+// 64 == 0: a step lies in one group) the step's two slices chained into one partial, scaled once.
+template <bool CH>
 __global__ __launch_bounds__(256) void int4_gemm_big_kernel(const uint16_t* __restrict__ a, int64_t lda,
                                                             const int8_t* __restrict__ b, const float* __restrict__ bs,
                                                             int group, const float* __restrict__ bias,
@@ -320,27 +322,53 @@ __global__ __launch_bounds__(256) void int4_gemm_big_kernel(const uint16_t* __re
     *reinterpret_cast<axk_u32x4*>(&sB[buf][(r + 64) * kI8Ld + 16 * c]) = rb[1];
     __syncthreads();  // the step's tiles are in LDS; every wave is done with the buffer written two steps ago
     if (ks + 1 < nk) load((ks + 1) * kI8Bk);  // uniform
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k32 = ks * kI8Bk + 32 * h;
-      if (k32 >= K) break;  // uniform
-      axk_bf16x8 af[4], bf[4];
+    if constexpr (CH) {  // K % 64 == 0: the whole step, one group
+      axk_bf16x8 af[2][4], bf[2][4];
       float sc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        af[i] = *reinterpret_cast<const axk_bf16x8*>(&sA[buf][(64 * wm + 16 * i + l16) * kI4LdA + 64 * h + 16 * g4]);
-        bf[i] = i8x8_to_bf16x8(
-            *reinterpret_cast<const uint2*>(&sB[buf][(64 * wn + 16 * i + l16) * kI8Ld + 32 * h + 8 * g4]));
-        sc[i] = srow[i][k32 / group];
-      }
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          af[h][i] =
+              *reinterpret_cast<const axk_bf16x8*>(&sA[buf][(64 * wm + 16 * i + l16) * kI4LdA + 64 * h + 16 * g4]);
+          bf[h][i] = i8x8_to_bf16x8(
+              *reinterpret_cast<const uint2*>(&sB[buf][(64 * wn + 16 * i + l16) * kI8Ld + 32 * h + 8 * g4]));
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[j] = srow[j][ks * kI8Bk / group];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const axk_f32x4 p = mfma_bf16_16x16x32(af[i], bf[j], axk_f32x4{0.f, 0.f, 0.f, 0.f});
+          axk_f32x4 p = mfma_bf16_16x16x32(af[0][i], bf[0][j], axk_f32x4{0.f, 0.f, 0.f, 0.f});
+          p = mfma_bf16_16x16x32(af[1][i], bf[1][j], p);
 #pragma unroll
           for (int q = 0; q < 4; ++q) acc[i][j][q] = __builtin_fmaf(p[q], sc[j], acc[i][j][q]);
         }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k32 = ks * kI8Bk + 32 * h;
+        if (k32 >= K) break;  // uniform
+        axk_bf16x8 af[4], bf[4];
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          af[i] =
+              *reinterpret_cast<const axk_bf16x8*>(&sA[buf][(64 * wm + 16 * i + l16) * kI4LdA + 64 * h + 16 * g4]);
+          bf[i] = i8x8_to_bf16x8(
+              *reinterpret_cast<const uint2*>(&sB[buf][(64 * wn + 16 * i + l16) * kI8Ld + 32 * h + 8 * g4]));
+          sc[i] = srow[i][k32 / group];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const axk_f32x4 p = mfma_bf16_16x16x32(af[i], bf[j], axk_f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[i][j][q] = __builtin_fmaf(p[q], sc[j], acc[i][j][q]);
+          }
+      }
     }
   }
 #pragma unroll
@@ -594,8 +622,12 @@ extern "C" int axk_int4_gemm(const uint16_t* a, int64_t lda, const int8_t* b_int
   }
   if (m >= kI8Big && n >= kI8Big) {
     const dim3 bg((unsigned)((n + kI8Big - 1) / kI8Big), (unsigned)((m + kI8Big - 1) / kI8Big));
-    hipLaunchKernelGGL(int4_gemm_big_kernel, bg, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale,
-                       (int)group, bias, out, f32, (int)m, (int)n, (int)k);
+    if (group % 64 == 0)
+      hipLaunchKernelGGL(int4_gemm_big_kernel<true>, bg, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale,
+                         (int)group, bias, out, f32, (int)m, (int)n, (int)k);
+    else
+      hipLaunchKernelGGL(int4_gemm_big_kernel<false>, bg, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale,
+                         (int)group, bias, out, f32, (int)m, (int)n, (int)k);
     return axk_launch_status();
   }
   hipLaunchKernelGGL(int4_gemm_kernel, grid, dim3(256), 0, axk_stream(stream), a, lda, b_int4, b_scale, (int)group,
