@@ -22,7 +22,7 @@ for _p in (ROOT, os.path.join(ROOT, "ax-dsl-kernels_amd")):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFS = 2500.0  # dense MFMA peaks of MI355X: bf16, fp8, fp4 (the kernels compute in bf16)
+BF16_PEAK_TFS = 2500.0  # dense MFMA peaks of MI355X: bf16, fp8, fp4 (the prefill kernels' MFMAs are bf16, fp32 acc)
 FP8_PEAK_TFS = 5000.0
 FP4_PEAK_TFS = 10100.0
 
