@@ -284,6 +284,13 @@ AXK_DEV ItemDesc local_item(const LocalPlan& lp, int it, int batch, int page_siz
   return d;
 }
 
+// The optional attention output gate on one output value: bf16(v * sigmoid(g)) for the already bf16-rounded v (the
+// elementwise sigmoid-mul of the decode layer, applied where the row is written); v as is without a gate.
+AXK_DEV uint32_t gated_bf16(float v, const uint16_t* gate, int64_t gi) {
+  const uint32_t vb = f32_to_bf16_bits(v);
+  return gate ? f32_to_bf16_bits(bf16_bits_to_f32(vb) * sigmoid_f32(bf16_bits_to_f32(gate[gi]))) : vb;
+}
+
 // Attention of one work item over a bf16 cache. The 4 waves share every 16-token K/V tile: the tile streams HBM -> LDS
 // (each wave issues a quarter of its loads) into a ring of tile pairs, computed a pair (32 tokens) at a time. Every
 // wave computes the full scores S^T = K Q^T of the pair (cheap on MFMA) and the online softmax, then P x V for its
@@ -296,7 +303,7 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
                                             PlanHeader* __restrict__ hdr,
                                             float* __restrict__ part_m, float* __restrict__ part_l,
                                             float* __restrict__ part_o, uint16_t* __restrict__ out,
-                                            unsigned char* smem) {
+                                            unsigned char* smem, const uint16_t* __restrict__ gate, int64_t ldg) {
   using C = PagedCfg<D>;  // the bf16 tile layout
   const int group = hq / hkv;
   const int b = __builtin_amdgcn_readfirstlane(desc.b), kvh = __builtin_amdgcn_readfirstlane(desc.kvh);
@@ -482,13 +489,15 @@ __device__ __forceinline__ void decode_item(const ItemDesc& desc, int it, const 
   const bool hv = l16 < group;
   if (nsplit == 1) {  // the whole sequence in one item: normalise and store
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    const int64_t gi0 = ((int64_t)b * hq + kvh * group + l16) * ldg;  // this lane's head's gate row
 #pragma unroll
     for (int t = 0; t < C::DT; ++t) {
       if (!hv) continue;
+      const int col = wave * C::DW + 16 * t + 4 * g;
       uint2 w;
-      w.x = f32_to_bf16_bits(o[t][0] * inv) | (f32_to_bf16_bits(o[t][1] * inv) << 16);
-      w.y = f32_to_bf16_bits(o[t][2] * inv) | (f32_to_bf16_bits(o[t][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(out + out_base + (int64_t)l16 * D + wave * C::DW + 16 * t + 4 * g) = w;
+      w.x = gated_bf16(o[t][0] * inv, gate, gi0 + col) | (gated_bf16(o[t][1] * inv, gate, gi0 + col + 1) << 16);
+      w.y = gated_bf16(o[t][2] * inv, gate, gi0 + col + 2) | (gated_bf16(o[t][3] * inv, gate, gi0 + col + 3) << 16);
+      *reinterpret_cast<uint2*>(out + out_base + (int64_t)l16 * D + col) = w;
     }
     return;
   }
@@ -938,7 +947,8 @@ __global__ __launch_bounds__(256, KB == 1 ? 2 : 1) void paged_decode_kernel(
     int page_size, int64_t num_pages, float sm_scale, float inv_scale, const unsigned char* __restrict__ kv_scales,
     int local, int bias,
     PlanHeader* __restrict__ hdr, const ItemDesc* __restrict__ descs, float* __restrict__ part_m,
-    float* __restrict__ part_l, float* __restrict__ part_o, uint16_t* __restrict__ out) {
+    float* __restrict__ part_l, float* __restrict__ part_o, uint16_t* __restrict__ out,
+    const uint16_t* __restrict__ gate, int64_t ldg) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (local) {
     const LocalPlan lp = local_plan(indptr, last_page_len, bias, batch, hkv, gridDim.x);
@@ -946,7 +956,7 @@ __global__ __launch_bounds__(256, KB == 1 ? 2 : 1) void paged_decode_kernel(
       const ItemDesc desc = local_item(lp, it, batch, page_size);
       if constexpr (KB == 2)
         decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
-                       part_o, out, smem);
+                       part_o, out, smem, gate, ldg);
       else
         decode_item_8<D, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
                              kv_scales, hdr, part_m, part_l, part_o, out, smem);
@@ -963,7 +973,7 @@ __global__ __launch_bounds__(256, KB == 1 ? 2 : 1) void paged_decode_kernel(
     if (it != (int)blockIdx.x) desc = descs[it];
     if constexpr (KB == 2)
       decode_item<D>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, hdr, part_m, part_l,
-                     part_o, out, smem);
+                     part_o, out, smem, gate, ldg);
     else
       decode_item_8<D, QM>(desc, it, q, cache, indices, hq, hkv, page_size, num_pages, sm_scale, inv_scale,
                            kv_scales, hdr, part_m, part_l, part_o, out, smem);
@@ -984,7 +994,8 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
                                                           const float* __restrict__ part_m,
                                                           const float* __restrict__ part_l,
                                                           const float* __restrict__ part_o,
-                                                          uint16_t* __restrict__ out) {
+                                                          uint16_t* __restrict__ out,
+                                                          const uint16_t* __restrict__ gate, int64_t ldg) {
   constexpr int V = D / 64;  // output columns per lane
   constexpr int P = 16;      // splits per pass
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1009,9 +1020,10 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
     i0 = io0 + kvh;
   }
   uint16_t* op = out + ((int64_t)b * hq + h) * D + lane * V;
+  const int64_t gi = ((int64_t)b * hq + h) * ldg + lane * V;  // the gate row's columns (with a gate)
   if (np == 0) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) op[j] = 0;
+    for (int j = 0; j < V; ++j) op[j] = (uint16_t)gated_bf16(0.f, gate, gi + j);
     return;
   }
   if (nsplit <= 1) return;  // written by the decode kernel
@@ -1047,7 +1059,7 @@ __global__ __launch_bounds__(256) void paged_merge_kernel(const int* __restrict_
   }
   const float inv = ll > 0.f ? 1.0f / ll : 0.f;
 #pragma unroll
-  for (int j = 0; j < V; ++j) op[j] = (uint16_t)f32_to_bf16_bits(acc[j] * inv);
+  for (int j = 0; j < V; ++j) op[j] = (uint16_t)gated_bf16(acc[j] * inv, gate, gi + j);
 }
 
 // cache[loc[b,0], 0, loc[b,1], kvh, :] = k[b, kvh, :]; plane 1 <- v (store_paged_kv, flash_attn.py:53-84).
@@ -1474,7 +1486,8 @@ int raise_split_lds() {
 template <int D, int KB = 2, int QM = 0>
 int launch_split(const uint16_t* q, const void* cache, const int* indptr, const int* last, const int* indices,
                  uint16_t* out, int batch, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale,
-                 void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr) {
+                 void* ws, hipStream_t st, float inv_scale = 1.0f, int bias = 0, const void* kv_scales = nullptr,
+                 const uint16_t* gate = nullptr, int64_t ldg = 0) {
   const int group = hq / hkv;
   const WsView v = ws_view(ws, batch, hkv, group, D);
   // the kernel's per-lane tile offsets are 32-bit: both planes of a page stay under 2^31 bytes
@@ -1485,18 +1498,18 @@ int launch_split(const uint16_t* q, const void* cache, const int* indptr, const 
   hipLaunchKernelGGL((paged_decode_kernel<D, KB, QM>), dim3((unsigned)split_grid(batch, hkv)), dim3(64 * kWaves),
                      lds, st, q, static_cast<const unsigned char*>(cache), indptr, last, indices, batch, hq, hkv,
                      page_size, num_pages, sm_scale, inv_scale, static_cast<const unsigned char*>(kv_scales), local,
-                     bias, v.hdr, v.descs, v.pm, v.pl, v.po, out);
+                     bias, v.hdr, v.descs, v.pm, v.pl, v.po, out, gate, ldg);
   return axk_launch_status();
 }
 
 template <int D>
 int launch_merge(const int* indptr, const int* last, uint16_t* out, int batch, int hq, int hkv, int page_size,
-                 void* ws, hipStream_t st, int kb = 2, int bias = 0) {
+                 void* ws, hipStream_t st, int kb = 2, int bias = 0, const uint16_t* gate = nullptr, int64_t ldg = 0) {
   const WsView v = ws_view(ws, batch, hkv, hq / hkv, D);
   const int local = batch <= kLocalPlanBatch ? 1 : 0;
   hipLaunchKernelGGL((paged_merge_kernel<D>), dim3((unsigned)((batch * hq + 3) / 4)), dim3(256), 0, st, indptr, last,
                      v.hdr,
-                     v.item_off, batch, hq, hkv, split_grid(batch, hkv), local, bias, v.pm, v.pl, v.po, out);
+                     v.item_off, batch, hq, hkv, split_grid(batch, hkv), local, bias, v.pm, v.pl, v.po, out, gate, ldg);
   return axk_launch_status();
 }
 
@@ -1566,28 +1579,29 @@ int check_split(const void* q, const void* kv_cache, const int32_t* indptr, cons
 int decode_split(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
                  const int32_t* last_page_len, uint16_t* out, int64_t batch, int64_t hq, int64_t hkv, int64_t d,
                  int64_t page_size, int64_t num_pages, float sm_scale, int bias, void* workspace,
-                 hipStream_t st) {
+                 hipStream_t st, const uint16_t* gate = nullptr, int64_t ldg = 0) {
   const int B = (int)batch, HQ = (int)hq, HKV = (int)hkv, PS = (int)page_size;
   switch (d) {
     case 64:
       return launch_split<64>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                              workspace, st, 1.0f, bias);
+                              workspace, st, 1.0f, bias, nullptr, gate, ldg);
     case 128:
       return launch_split<128>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                               workspace, st, 1.0f, bias);
+                               workspace, st, 1.0f, bias, nullptr, gate, ldg);
     default:
       return launch_split<256>(q, kv_cache, indptr, last_page_len, indices, out, B, HQ, HKV, PS, num_pages, sm_scale,
-                               workspace, st, 1.0f, bias);
+                               workspace, st, 1.0f, bias, nullptr, gate, ldg);
   }
 }
 
 int decode_merge(const int32_t* indptr, const int32_t* last_page_len, uint16_t* out, int64_t batch, int64_t hq,
-                 int64_t hkv, int64_t d, int64_t page_size, int kb, int bias, void* workspace, hipStream_t st) {
+                 int64_t hkv, int64_t d, int64_t page_size, int kb, int bias, void* workspace, hipStream_t st,
+                 const uint16_t* gate = nullptr, int64_t ldg = 0) {
   const int B = (int)batch, HQ = (int)hq, HKV = (int)hkv, PS = (int)page_size;
   switch (d) {
-    case 64: return launch_merge<64>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias);
-    case 128: return launch_merge<128>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias);
-    default: return launch_merge<256>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias);
+    case 64: return launch_merge<64>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias, gate, ldg);
+    case 128: return launch_merge<128>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias, gate, ldg);
+    default: return launch_merge<256>(indptr, last_page_len, out, B, HQ, HKV, PS, workspace, st, kb, bias, gate, ldg);
   }
 }
 
@@ -1595,7 +1609,7 @@ int decode_merge(const int32_t* indptr, const int32_t* last_page_len, uint16_t* 
 int decode_all(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
                const int32_t* last_page_len, uint16_t* out, int64_t batch, int64_t hq, int64_t hkv, int64_t d,
                int64_t page_size, int64_t num_pages, float sm_scale, int bias, void* workspace, size_t workspace_bytes,
-               hipStream_t st) {
+               hipStream_t st, const uint16_t* gate = nullptr, int64_t ldg = 0) {
   int rc = check_split(q, kv_cache, indptr, indices, last_page_len, out, batch, hq, hkv, d, page_size, num_pages,
                        workspace, workspace_bytes);
   if (rc != AXK_OK) return rc;
@@ -1604,9 +1618,9 @@ int decode_all(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indpt
     return rc;
   AXK_LAUNCH_GATE();
   if ((rc = decode_split(q, kv_cache, indptr, indices, last_page_len, out, batch, hq, hkv, d, page_size, num_pages,
-                         sm_scale, bias, workspace, st)) != AXK_OK)
+                         sm_scale, bias, workspace, st, gate, ldg)) != AXK_OK)
     return rc;
-  return decode_merge(indptr, last_page_len, out, batch, hq, hkv, d, page_size, 2, bias, workspace, st);
+  return decode_merge(indptr, last_page_len, out, batch, hq, hkv, d, page_size, 2, bias, workspace, st, gate, ldg);
 }
 
 }  // namespace
@@ -1666,6 +1680,19 @@ extern "C" int axk_paged_decode(const uint16_t* q, const uint16_t* kv_cache, con
                                 axk_stream_t stream) {
   return decode_all(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim,
                     page_size, num_pages, sm_scale, 0, workspace, workspace_bytes, axk_stream(stream));
+}
+
+int axk_paged_decode_gated(const uint16_t* q, const uint16_t* kv_cache, const int32_t* indptr, const int32_t* indices,
+                           const int32_t* last_page_len, const uint16_t* gate, int64_t ldg, uint16_t* out,
+                           int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim,
+                           int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream) {
+  AXK_REQUIRE(gate, AXK_E_NULL);
+  AXK_REQUIRE(ldg >= head_dim, AXK_E_SHAPE);
+  const size_t gbytes = (size_t)((batch * num_qo_heads - 1) * ldg + head_dim) * 2;
+  AXK_REQUIRE(!axk_overlap(out, (size_t)batch * num_qo_heads * head_dim * 2, gate, gbytes), AXK_E_ALIAS);
+  return decode_all(q, kv_cache, indptr, indices, last_page_len, out, batch, num_qo_heads, num_kv_heads, head_dim,
+                    page_size, num_pages, sm_scale, 0, workspace, workspace_bytes, stream, gate, ldg);
 }
 
 // ---- No-allocation variant: the workspace is a static device array of the library ----
