@@ -141,8 +141,8 @@ MoeWs moe_ws(void* ws, int64_t T, int64_t H, int64_t E, int64_t K, int64_t F, in
 // the largest remaining logit (the softmax is monotonic), ties to the lower expert id: a DPP wave maximum, then
 // one ballot per register finds the lowest id holding it. Lane k keeps selection k.
 template <int V>
-AXK_DEV void route_select(const float (&x)[V], int lane, int E, int K, int norm_topk, int32_t* __restrict__ ids,
-                          float* __restrict__ wts) {
+AXK_DEV int route_select(const float (&x)[V], int lane, int E, int K, int norm_topk, int32_t* __restrict__ ids,
+                         float* __restrict__ wts) {
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < V; ++i) mx = fmaxf(mx, x[i]);
@@ -185,6 +185,7 @@ AXK_DEV void route_select(const float (&x)[V], int lane, int E, int K, int norm_
     ids[lane] = myid;
     wts[lane] = norm_topk ? myp / psum : myp;
   }
+  return lane < K ? myid : -1;  // lane k: selection k
 }
 
 template <int V>  // expert logits per lane (num_experts <= 64 V)
@@ -207,13 +208,16 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 
 // Routing from the router's partial logits: logit = sum of the S K-slice partials in slice order (written out as the
 // layer's logits), then route_select. With gpart (decode), lane 0 of token t's wave also sums the shared gate's S
-// partial logits in slice order into gate_logit[t].
+// partial logits in slice order into gate_logit[t]. With blk (prefill), each selection is counted into its
+// (256-token block, expert) count blk[block E + e], zeroed by the router launch: the counts the prefill grouping
+// scans (a token's K selections are distinct experts, so this is each block's per-expert token count).
 template <int V, int MAXS>  // MAXS: bound on the number of partials
 __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __restrict__ part,
                                                              const float* __restrict__ gpart, int S, int T, int E,
                                                              int K, int norm_topk, float* __restrict__ logits,
                                                              float* __restrict__ gate_logit,
-                                                             int32_t* __restrict__ ids, float* __restrict__ wts) {
+                                                             int32_t* __restrict__ ids, float* __restrict__ wts,
+                                                             int* __restrict__ blk) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -251,7 +255,8 @@ __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __rest
       if (sl < S) gv += gp[sl];
     gate_logit[t] = gv;
   }
-  route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+  const int id = route_select<V>(x, lane, E, K, norm_topk, ids + (int64_t)t * K, wts + (int64_t)t * K);
+  if (blk && id >= 0 && id < E) atomicAdd(blk + (int64_t)(t / kBlkTokens) * E + id, 1);
 }
 
 // Prefill router GEMM: workgroup (64 tokens, 64 experts, K slice s), waves 2 x 2 with 32 x 32 each; both operands
@@ -259,7 +264,13 @@ __global__ __launch_bounds__(256) void moe_route_part_kernel(const float* __rest
 // steps ahead in register stages. Writes the slice's partial logits like the decode router.
 __global__ __launch_bounds__(256) void moe_router_tile_kernel(const uint16_t* __restrict__ h2,
                                                               const uint16_t* __restrict__ wr, int T, int H, int E,
-                                                              int S, float* __restrict__ part) {
+                                                              int S, float* __restrict__ part, int* __restrict__ blk,
+                                                              int nblk) {
+  {  // the routing launch's (block, expert) counts to zero, spread over the grid
+    const int64_t wg = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+    const int64_t nth = (int64_t)gridDim.x * gridDim.y * gridDim.z * blockDim.x;
+    for (int64_t i = wg * blockDim.x + threadIdx.x; i < nblk; i += nth) blk[i] = 0;
+  }
   constexpr int kLd = 72;
   __shared__ __align__(16) uint16_t sA[2][64 * kLd];
   __shared__ __align__(16) uint16_t sB[2][64 * kLd];
@@ -1466,7 +1477,7 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
                      const uint8_t* e_dw, const uint8_t* e_ds, const int32_t* topk_ids, const float* topk_weights,
                      uint16_t* out, int64_t tokens, int64_t hidden, int64_t num_experts, int64_t top_k, int64_t inter,
                      int64_t shared_inter, void* workspace, size_t workspace_bytes, axk_stream_t stream, bool gate_given,
-                     bool check_only, const float* y_sh_given = nullptr) {
+                     bool check_only, const float* y_sh_given = nullptr, bool counted = false) {
   AXK_REQUIRE(h2 && e_gw && e_gs && e_dw && e_ds && topk_ids && topk_weights && out, AXK_E_NULL);
   const bool has_shared = sh_gate_w != nullptr;
   AXK_REQUIRE(!has_shared || (sh_gate_s && sh_up_w && sh_up_s && sh_down_w && sh_down_s), AXK_E_NULL);
@@ -1495,7 +1506,8 @@ int moe_experts_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* 
   const int T = (int)tokens, H = (int)hidden, E = (int)num_experts, K = (int)top_k, F = (int)inter, Fs = (int)d.Fs;
   if (T > kDecodeTokens) {
     const int NB = (int)prefill_blocks(T);
-    hipLaunchKernelGGL(moe_pcount_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, T, E, K, w);
+    // the (block, expert) counts: counted by the routing launch when it ran in this call, else from the ids
+    if (!counted) hipLaunchKernelGGL(moe_pcount_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, T, E, K, w);
     hipLaunchKernelGGL(moe_pscan_kernel, dim3(1), dim3(256), 0, st, T, E, NB, has_shared ? 1 : 0, w);
     hipLaunchKernelGGL(moe_pscatter_kernel, dim3((unsigned)NB), dim3(256), 0, st, topk_ids, topk_weights, T, E, K, w);
     const unsigned tiles = (unsigned)prefill_max_tiles(T, E, K);
@@ -1633,7 +1645,7 @@ int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w
   const bool gate = !prefill && w_shg != nullptr;
   if (prefill)
     hipLaunchKernelGGL(moe_router_tile_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64), (unsigned)S),
-                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart);
+                       dim3(256), 0, st, h2, w_router, T, H, E, S, w.rpart, w.blk, (int)(prefill_blocks(T) * E));
   else
     hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 15) / 16 + (gate ? 1 : 0)), (unsigned)((T + 15) / 16),
                        (unsigned)S), dim3(256), 0, st, h2, w_router, w_shg, T, H, E, S, w.rpart, w.gpart);
@@ -1641,7 +1653,7 @@ int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w
   float* const gp = gate ? w.gpart : nullptr;
 #define AXK_ROUTE_PART(V, MS)                                                                                     \
   hipLaunchKernelGGL((moe_route_part_kernel<V, MS>), grid, block, 0, st, w.rpart, gp, S, T, E, K, norm_topk_prob, \
-                     logits, w.gate_logit, topk_ids, topk_weights)
+                     logits, w.gate_logit, topk_ids, topk_weights, prefill ? w.blk : nullptr)
   if (prefill) {
     if (E <= 64) AXK_ROUTE_PART(1, kPrefillRouterSplits);
     else if (E <= 256) AXK_ROUTE_PART(4, kPrefillRouterSplits);
@@ -1660,7 +1672,7 @@ int moe_decode_impl(const uint16_t* h2, const uint16_t* x_res, const uint16_t* w
   if (rc != AXK_OK) return rc;
   return moe_experts_impl(h2, x_res, w_shg, sh_gate_w, sh_gate_s, sh_up_w, sh_up_s, sh_down_w, sh_down_s, e_gw, e_gs,
                           e_dw, e_ds, topk_ids, topk_weights, out, tokens, hidden, num_experts, top_k, inter,
-                          shared_inter, workspace, workspace_bytes, stream, gate, false, y_sh_given);
+                          shared_inter, workspace, workspace_bytes, stream, gate, false, y_sh_given, prefill);
 }
 }  // namespace
 
