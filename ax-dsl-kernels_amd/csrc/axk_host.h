@@ -156,6 +156,15 @@ __attribute__((visibility("hidden"))) int axk_paged_decode_gated(
     int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages, float sm_scale, void* workspace,
     size_t workspace_bytes, hipStream_t stream);
 
+// Internal (not exported): axk_paged_prefill with the attention output gate applied where each output row is
+// written, as axk_paged_decode_gated (gate rows ldg elements apart, one per (token, query head) row). Returns an
+// AXK status.
+__attribute__((visibility("hidden"))) int axk_paged_prefill_gated(
+    const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr, const int32_t* indptr,
+    const int32_t* indices, const int32_t* last_page_len, const uint16_t* gate, int64_t ldg, uint16_t* out,
+    int64_t batch, int64_t total_q, int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+    int64_t num_pages, float sm_scale, hipStream_t stream);
+
 // Internal (not exported): axk_moe_decode with the shared expert computed by the caller: y_sh [tokens, hidden] fp32
 // is its down projection (any weight format), gated by sigmoid(h2 . w_shg) in the combine as the library's own
 // shared expert is; the routed experts and routing as axk_moe_decode. Size the workspace with

@@ -513,9 +513,9 @@ int attn_rows_impl(const uint16_t* x, const float* ln1, const uint8_t* w_q, cons
     AXK_TRY(axk_attn_qkv_prep(a.qg, a.kk, a.vv, q_norm, k_norm, cos, sin, a.q, kv_cache, cache_location, R, HQ, HKV,
                               D, rot, page_size, num_pages, eps, axk_stream(stream)));
     AXK_TRY(axk_fill_iota_i32(a.qo_indptr, B, T, axk_stream(stream)));
-    AXK_TRY(axk_paged_prefill(a.q, kv_cache, a.qo_indptr, indptr, indices, last_page_len, a.attn, B, R, HQ, HKV, D,
-                              page_size, num_pages, sm_scale, nullptr, stream));
-    AXK_TRY(axk_sigmoid_mul(a.attn, a.qg + D, 2 * D, a.gated, R * HQ, D, stream));
+    // the attention with its output gate applied as each row is written: gated = bf16(attn * sigmoid(gate))
+    AXK_TRY(axk_paged_prefill_gated(a.q, kv_cache, a.qo_indptr, indptr, indices, last_page_len, a.qg + D, 2 * D,
+                                    a.gated, B, R, HQ, HKV, D, page_size, num_pages, sm_scale, axk_stream(stream)));
     const AxkMxMat o = proj_mat(proj_fmt, w_o, s_o, a.y, H);
     AXK_TRY(projs(proj_fmt, a.gated, HQ * D, &o, 1, R, HQ * D, stream));
     if (moe) return moe_residual(x, a.y, ln2, mw, mlp_fmt, *moe, out, a.mlp, eb, R, H, F, eps, stream);

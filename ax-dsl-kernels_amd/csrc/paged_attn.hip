@@ -1144,7 +1144,7 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, const unsigned char* __restrict__ cache, const int* __restrict__ qo_indptr,
     const int* __restrict__ indptr, const int* __restrict__ last_page_len, const int* __restrict__ indices,
     int batch, int total_q, int hq, int hkv, int page_size, int64_t num_pages, float sm_scale, int xcd_per_head,
-    int* __restrict__ status, uint16_t* __restrict__ out) {
+    int* __restrict__ status, uint16_t* __restrict__ out, const uint16_t* __restrict__ gate, int64_t ldg) {
   using C = PagedCfg<D>;
   extern __shared__ __align__(16) unsigned char smem[];
   const int group = hq / hkv;
@@ -1401,12 +1401,14 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
     const int r = r_first + kPfRowsPerWave * wave + 16 * i + l16;
     if (r > r_last) continue;
     const float inv = l_run[i] > 0.f ? 1.0f / l_run[i] : 0.f;
+    const int64_t gi0 = qoff[i] / D * ldg;  // the row's gate (with a gate)
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
+      const int col = 16 * t + 4 * g;
       uint2 w;
-      w.x = f32_to_bf16_bits(o[i][t][0] * inv) | (f32_to_bf16_bits(o[i][t][1] * inv) << 16);
-      w.y = f32_to_bf16_bits(o[i][t][2] * inv) | (f32_to_bf16_bits(o[i][t][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(out + qoff[i] + 16 * t + 4 * g) = w;
+      w.x = gated_bf16(o[i][t][0] * inv, gate, gi0 + col) | (gated_bf16(o[i][t][1] * inv, gate, gi0 + col + 1) << 16);
+      w.y = gated_bf16(o[i][t][2] * inv, gate, gi0 + col + 2) | (gated_bf16(o[i][t][3] * inv, gate, gi0 + col + 3) << 16);
+      *reinterpret_cast<uint2*>(out + qoff[i] + col) = w;
     }
   }
 }
@@ -1414,7 +1416,8 @@ __global__ __launch_bounds__(64 * kPfWaves) void paged_prefill_kernel(
 template <int D>
 int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, const int* indptr, const int* last,
                    const int* indices, uint16_t* out, int batch, int total_q, int hq, int hkv, int page_size,
-                   int64_t num_pages, float sm_scale, int* status, hipStream_t st) {
+                   int64_t num_pages, float sm_scale, int* status, hipStream_t st, const uint16_t* gate = nullptr,
+                   int64_t ldg = 0) {
   const int64_t rows = (int64_t)total_q * (hq / hkv);
   const int64_t nblk = (rows + kPfRows - 1) / kPfRows + batch;  // >= the sum over sequences of their row blocks
   const int xph = hkv <= 8 && 8 % hkv == 0 ? 8 / hkv : 0;      // XCDs per KV head
@@ -1426,7 +1429,7 @@ int launch_prefill(const uint16_t* q, const void* cache, const int* qo_indptr, c
   AXK_LAUNCH_GATE();
   hipLaunchKernelGGL((paged_prefill_kernel<D>), dim3((unsigned)grid), dim3(64 * kPfWaves), lds, st, q,
                      static_cast<const unsigned char*>(cache), qo_indptr, indptr, last, indices, batch, total_q, hq,
-                     hkv, page_size, num_pages, sm_scale, xph, status, out);
+                     hkv, page_size, num_pages, sm_scale, xph, status, out, gate, ldg);
   return axk_launch_status();
 }
 
@@ -1981,11 +1984,12 @@ extern "C" int axk_paged_kv_write_i8(const uint16_t* k, const uint16_t* v, int8_
 // already written into the cache as the sequence's last tokens) attend causally over its paged history and
 // themselves. flash_attn.py:471-611 (paged_flash_attention: history pages, then the causal current block),
 // q35_prefill.py:264-336 (the G x P-row block attention per KV head).
-extern "C" int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr,
-                                 const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
-                                 uint16_t* out, int64_t batch, int64_t total_q, int64_t num_qo_heads,
-                                 int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
-                                 float sm_scale, int32_t* status, axk_stream_t stream) {
+namespace {
+// axk_paged_prefill, with the optional attention output gate applied as each row is written (gate rows ldg apart).
+int prefill_impl(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr, const int32_t* indptr,
+                 const int32_t* indices, const int32_t* last_page_len, uint16_t* out, int64_t batch, int64_t total_q,
+                 int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                 float sm_scale, int32_t* status, hipStream_t st, const uint16_t* gate, int64_t ldg) {
   AXK_REQUIRE(q && kv_cache && qo_indptr && indptr && indices && last_page_len && out, AXK_E_NULL);
   AXK_REQUIRE(batch > 0 && batch <= (1 << 20) && total_q >= 0 && total_q <= (1 << 24), AXK_E_SHAPE);
   AXK_REQUIRE(num_kv_heads > 0 && num_qo_heads > 0 && num_qo_heads % num_kv_heads == 0, AXK_E_SHAPE);
@@ -1996,17 +2000,41 @@ extern "C" int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, co
   if (total_q == 0) return AXK_OK;
   const size_t qbytes = (size_t)total_q * num_qo_heads * head_dim * 2;
   AXK_REQUIRE(!axk_overlap(out, qbytes, q, qbytes), AXK_E_ALIAS);
-  hipStream_t st = axk_stream(stream);
   const int B = (int)batch, T = (int)total_q, HQ = (int)num_qo_heads, HKV = (int)num_kv_heads, PS = (int)page_size;
   switch (head_dim) {
     case 64:
       return launch_prefill<64>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
-                                num_pages, sm_scale, status, st);
+                                num_pages, sm_scale, status, st, gate, ldg);
     case 128:
       return launch_prefill<128>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
-                                 num_pages, sm_scale, status, st);
+                                 num_pages, sm_scale, status, st, gate, ldg);
     default:
       return launch_prefill<256>(q, kv_cache, qo_indptr, indptr, last_page_len, indices, out, B, T, HQ, HKV, PS,
-                                 num_pages, sm_scale, status, st);
+                                 num_pages, sm_scale, status, st, gate, ldg);
   }
+}
+}  // namespace
+
+extern "C" int axk_paged_prefill(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr,
+                                 const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                                 uint16_t* out, int64_t batch, int64_t total_q, int64_t num_qo_heads,
+                                 int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+                                 float sm_scale, int32_t* status, axk_stream_t stream) {
+  return prefill_impl(q, kv_cache, qo_indptr, indptr, indices, last_page_len, out, batch, total_q, num_qo_heads,
+                      num_kv_heads, head_dim, page_size, num_pages, sm_scale, status, axk_stream(stream), nullptr, 0);
+}
+
+int axk_paged_prefill_gated(const uint16_t* q, const uint16_t* kv_cache, const int32_t* qo_indptr,
+                            const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                            const uint16_t* gate, int64_t ldg, uint16_t* out, int64_t batch, int64_t total_q,
+                            int64_t num_qo_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                            int64_t num_pages, float sm_scale, hipStream_t stream) {
+  AXK_REQUIRE(gate, AXK_E_NULL);
+  AXK_REQUIRE(ldg >= head_dim, AXK_E_SHAPE);
+  if (total_q > 0) {
+    const size_t gbytes = (size_t)((total_q * num_qo_heads - 1) * ldg + head_dim) * 2;
+    AXK_REQUIRE(!axk_overlap(out, (size_t)total_q * num_qo_heads * head_dim * 2, gate, gbytes), AXK_E_ALIAS);
+  }
+  return prefill_impl(q, kv_cache, qo_indptr, indptr, indices, last_page_len, out, batch, total_q, num_qo_heads,
+                      num_kv_heads, head_dim, page_size, num_pages, sm_scale, nullptr, stream, gate, ldg);
 }
